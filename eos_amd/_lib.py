@@ -1,0 +1,115 @@
+"""ctypes binding of libeoship.so (declared in include/eoship.h).
+
+The library is the only compute path: when it is missing or fails to load,
+every call raises; there is no host fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG_DIR, "libeoship.so")
+
+c_err = C.POINTER(C.c_char_p)
+
+
+class EosHipTQDesc(C.Structure):
+    _fields_ = [
+        ("dim", C.c_int32),
+        ("bits", C.c_int32),
+        ("codebook_scale", C.c_float),
+        ("codebook", C.POINTER(C.c_int8)),
+        ("rotation", C.POINTER(C.c_float)),
+    ]
+
+
+class EosHipTQStats(C.Structure):
+    _fields_ = [
+        ("candidate_count", C.c_int64),
+        ("candidates_kept", C.c_int64),
+        ("fallback_queries", C.c_int32),
+        ("batches", C.c_int32),
+    ]
+
+
+# name -> (argtypes) ; every function returns int except where noted
+_SIGNATURES = {
+    "eoship_abi_version": ([], C.c_int),
+    "eoship_free_cstring": ([C.c_void_p], None),
+    "eoship_runtime_create": ([C.c_int, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_runtime_destroy": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_device_info": ([C.c_void_p, C.c_char_p, C.c_size_t, C.POINTER(C.c_int), C.c_char_p,
+                            C.c_size_t, C.c_void_p], C.c_int),
+    "eoship_malloc": ([C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_free": ([C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_h2d": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "eoship_d2h": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "eoship_d2d": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "eoship_sync": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_module_load": ([C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p), C.c_void_p],
+                           C.c_int),
+    "eoship_module_unload": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_function": ([C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_launch": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                       C.c_uint32, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_profile_enable": ([C.c_void_p, C.c_int, C.c_void_p], C.c_int),
+    "eoship_profile_read": ([C.c_void_p, C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_double),
+                             C.c_void_p], C.c_int),
+    "eoship_profile_reset": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_timer_mark": ([C.c_void_p, C.c_int, C.c_void_p], C.c_int),
+    "eoship_timer_elapsed": ([C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_double), C.c_void_p],
+                             C.c_int),
+    "eoship_tq_bind_corpus": ([C.c_void_p, C.POINTER(EosHipTQDesc), C.c_void_p, C.c_void_p,
+                               C.c_int64, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_tq_release": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_topk": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
+                        C.c_void_p, C.POINTER(EosHipTQStats), C.c_void_p], C.c_int),
+    "eoship_tq_topk_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                               C.c_void_p, C.c_void_p, C.POINTER(EosHipTQStats), C.c_void_p],
+                              C.c_int),
+    "eoship_tq_scores": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int64, C.c_int64,
+                          C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_prepare": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
+                           C.c_void_p], C.c_int),
+}
+
+_lib = None
+
+
+class EosHipError(RuntimeError):
+    """Error reported by libeoship (the char** err message)."""
+
+
+def load() -> C.CDLL:
+    """Load libeoship.so and declare its prototypes; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise EosHipError(
+            f"{LIB_PATH} is not built; run `python -m eos_amd.build` (the HIP library is the only "
+            "compute path)")
+    lib = C.CDLL(LIB_PATH)
+    for name, (argtypes, restype) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = restype
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> list[str]:
+    return sorted(_SIGNATURES)
+
+
+def call(name: str, *args) -> None:
+    """Call an int-returning entry point with a trailing char** err; raise on failure."""
+    lib = load()
+    err = C.c_char_p()
+    rc = getattr(lib, name)(*args, C.byref(err))
+    if rc != 0:
+        msg = err.value.decode("utf-8", "replace") if err.value else f"{name} failed"
+        if err.value:
+            lib.eoship_free_cstring(C.cast(err, C.c_void_p))
+        raise EosHipError(msg)

@@ -1,0 +1,95 @@
+"""Build recipe for the eoship library (gfx950 only).
+
+1. Each device source under ``csrc/kernels`` is compiled offline into a gfx950
+   code object with ``hipcc --genco`` (no run-time compiler, the counterpart of
+   the reference's NVRTC step in runtime/backends/cuda/native_linux.go:500-588).
+2. The code objects are linked into the shared library as read-only data
+   (``.incbin``) and loaded at runtime creation with ``hipModuleLoadData``.
+3. The host shim (plain C++ over the HIP runtime API) is compiled with g++ into
+   ``eos_amd/libeoship.so``.
+
+Run ``python -m eos_amd.build`` or call :func:`build`.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+CSRC = os.path.join(PKG_DIR, "csrc")
+BUILD_DIR = os.path.join(PKG_DIR, "_build")
+LIB_PATH = os.path.join(PKG_DIR, "libeoship.so")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+ARCH = "gfx950"
+
+# (code object symbol stem, device source)
+DEVICE_SOURCES = [
+    ("tq", os.path.join(CSRC, "kernels", "tq_kernels.hip")),
+]
+HOST_SOURCES = [
+    os.path.join(CSRC, "eoship_runtime.cpp"),
+    os.path.join(CSRC, "eoship_tq.cpp"),
+]
+
+# Packed-FP32 instructions are disabled for every device build.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print("+", " ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(
+            f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{proc.stdout}\n{proc.stderr}")
+
+
+def build(verbose: bool = False) -> str:
+    """Compile every gfx950 code object and the host shim; return the .so path."""
+    hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    blobs = []
+    for stem, src in DEVICE_SOURCES:
+        out = os.path.join(BUILD_DIR, f"{stem}.hsaco")
+        _run([hipcc, *HIPCC_FLAGS, "--genco", "-I", os.path.join(CSRC, "kernels"), "-o", out, src],
+             verbose)
+        blobs.append((stem, out))
+    asm = [".section .note.GNU-stack,\"\",@progbits"]
+    for stem, path in blobs:
+        asm += [
+            f".section .rodata.eoship_{stem},\"a\",@progbits",
+            ".balign 4096",
+            f".globl eoship_{stem}_co_begin",
+            f"eoship_{stem}_co_begin:",
+            f".incbin \"{path}\"",
+            f".globl eoship_{stem}_co_end",
+            f"eoship_{stem}_co_end:",
+            ".byte 0",
+        ]
+    asm_path = os.path.join(BUILD_DIR, "eoship_blobs.S")
+    with open(asm_path, "w") as f:
+        f.write("\n".join(asm) + "\n")
+    tmp = LIB_PATH + ".tmp"
+    _run([
+        "g++", "-O2", "-g", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
+        "-Wno-unused-parameter", "-D__HIP_PLATFORM_AMD__",
+        "-I", os.path.join(REPO_DIR, "include"), "-I", CSRC, "-I", os.path.join(ROCM, "include"),
+        *HOST_SOURCES, asm_path,
+        "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
+        "-Wl,--no-undefined", "-o", tmp,
+    ], verbose)
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,57 @@
+// Internal declarations shared by the eoship host translation units.
+#ifndef EOSHIP_INTERNAL_H
+#define EOSHIP_INTERNAL_H
+
+#include <hip/hip_runtime_api.h>
+
+#include <map>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "eoship.h"
+
+#define EOSHIP_ABI_VERSION 1
+
+namespace eoship {
+
+constexpr int kTimerSlots = 16;
+
+struct ProfileRecord {
+  std::string name;
+  hipEvent_t begin;
+  hipEvent_t end;
+};
+
+int set_err(char** err, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_err(char** err, const char* what, hipError_t e);
+
+struct Runtime {
+  int device = 0;
+  int compute_units = 0;
+  std::string name;
+  std::string arch;
+  hipStream_t stream = nullptr;
+  hipModule_t builtin = nullptr;
+  std::unordered_map<std::string, hipFunction_t> fns;
+  bool profiling = false;
+  std::vector<ProfileRecord> records;
+  std::map<std::string, std::pair<int64_t, double>> totals;
+  hipEvent_t timer[kTimerSlots];
+
+  int function(const char* name, hipFunction_t* out, char** err);
+  // Launches builtin kernel `name` whose single by-value argument is *args.
+  // `label` names the launch in profiles (defaults to the kernel name).
+  int launch(const char* name, dim3 grid, dim3 block, size_t lds, void* args, char** err,
+             const char* label = nullptr);
+  int alloc(size_t bytes, void** p, char** err);
+  void release(void* p);
+  int sync(char** err);
+  int flush_profile(char** err);
+};
+
+}  // namespace eoship
+
+struct EosHipRuntime : eoship::Runtime {};
+
+#endif  // EOSHIP_INTERNAL_H

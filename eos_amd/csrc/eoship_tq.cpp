@@ -1,0 +1,591 @@
+// TurboQuant half of the eoship C ABI: corpus binding and top-k scoring.
+//
+// Replaces the host loop topTurboQuantRetrievalScoresWithStats
+// (runtime/retrieval_turboquant.go:1853-1887) and its per-document
+// q.InnerProductPrepared calls with a device pipeline per batch of <= 64
+// queries:
+//   1. eos_tq_prepare   rotate (f64), quantize to int16, split hi/lo fragments
+//   2. sample scan      exact scores of every 32nd tile of 32 vectors
+//   3. eos_tq_row_select  per query, the r-th best sample score -> threshold
+//   4. filter scan      one pass over the corpus, keep score >= threshold
+//   5. eos_tq_finalize  sort kept candidates (score desc, id asc), emit top-k
+//   6. exact fallback   for any query whose kept set is too small or
+//                       overflowed: exhaustive scores + exact radix select.
+// Step 6 makes the result exact whatever the data; steps 2-3 only decide how
+// much work step 4 saves.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "eoship_internal.h"
+#include "kernels/tq_args.h"
+
+using eoship::hip_err;
+using eoship::set_err;
+
+namespace {
+
+constexpr int kBatch = 64;          // queries per scan (two 32-column groups)
+constexpr int kCap = 8192;          // kept candidates per query
+constexpr int kSortCap = 8192;      // largest k the device sort handles
+constexpr int kSampleStride = 32;   // sample every 32nd tile
+constexpr int kTile = 32;
+constexpr int kQmaxLimit = 127 * 256 + 127;  // largest int16 with int8 hi/lo halves
+const int kSupportedKs[] = {1, 2, 4, 8, 12, 16, 24, 32};
+
+int ks_for_dim(int d) {
+  for (int ks : kSupportedKs)
+    if (ks * 32 >= d) return ks;
+  return 0;
+}
+
+inline uint8_t sext(uint8_t b) { return (b & 0x80) ? 0xff : 0x00; }
+
+// Emulates v_perm_b32 (byte select with sign-replicate/zero/0xFF selectors).
+uint32_t perm_emul(uint32_t s0, uint32_t s1, uint32_t sel) {
+  const uint64_t in = ((uint64_t)s0 << 32) | s1;
+  uint32_t out = 0;
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t s = (sel >> (8 * b)) & 0xff;
+    uint32_t v;
+    if (s >= 13) v = 0xff;
+    else if (s == 12) v = 0x00;
+    else if (s == 11) v = ((in >> 63) & 1) ? 0xff : 0;
+    else if (s == 10) v = ((in >> 47) & 1) ? 0xff : 0;
+    else if (s == 9) v = ((in >> 31) & 1) ? 0xff : 0;
+    else if (s == 8) v = ((in >> 15) & 1) ? 0xff : 0;
+    else v = (uint32_t)((in >> (8 * s)) & 0xff);
+    out |= v << (8 * b);
+  }
+  return out;
+}
+
+// Solves the two XOR-combined 8-byte tables of the 4-bit decode so that
+// perm(A, x) ^ perm(B, x ^ 8) == C[x] for every 4-bit x.
+int solve_lut4(const int8_t* cb, uint32_t lut[4], char** err) {
+  uint8_t c[16];
+  for (int i = 0; i < 16; ++i) c[i] = (uint8_t)cb[i];
+  uint8_t kb[8] = {0}, ka[16] = {0};
+  kb[4] = 0x00;
+  kb[5] = kb[6] = kb[7] = 0xff;
+  ka[12] = 0x00;
+  ka[13] = ka[14] = ka[15] = 0xff;
+  kb[2] = sext((uint8_t)~c[13]);
+  kb[3] = sext((uint8_t)~c[15]);
+  ka[10] = sext((uint8_t)~c[5]);
+  ka[11] = sext((uint8_t)~c[7]);
+  ka[9] = sext(c[3] ^ kb[3]);
+  kb[1] = sext(c[11] ^ ka[11]);
+  kb[0] = sext(c[9] ^ ka[9]);
+  ka[8] = sext(c[1] ^ kb[1]);
+  uint8_t ta[8], tb[8];
+  for (int u = 0; u < 8; ++u) {
+    ta[u] = c[u] ^ kb[u];
+    tb[u] = c[u + 8] ^ ka[u + 8];
+  }
+  lut[0] = ta[0] | (ta[1] << 8) | (ta[2] << 16) | ((uint32_t)ta[3] << 24);
+  lut[1] = ta[4] | (ta[5] << 8) | (ta[6] << 16) | ((uint32_t)ta[7] << 24);
+  lut[2] = tb[0] | (tb[1] << 8) | (tb[2] << 16) | ((uint32_t)tb[3] << 24);
+  lut[3] = tb[4] | (tb[5] << 8) | (tb[6] << 16) | ((uint32_t)tb[7] << 24);
+  for (uint32_t x = 0; x < 16; ++x) {
+    const uint32_t sel = x * 0x01010101u;
+    const uint32_t r = perm_emul(lut[1], lut[0], sel) ^ perm_emul(lut[3], lut[2], sel ^ 0x08080808u);
+    if (r != (uint32_t)c[x] * 0x01010101u)
+      return set_err(err, "eoship: 4-bit codebook lookup table self-check failed at code %u", x);
+  }
+  return 0;
+}
+
+}  // namespace
+
+struct EosHipTQ {
+  EosHipRuntime* rt = nullptr;
+  int d = 0, bits = 0, ks = 0, nload = 0, row_bytes = 0, qmax = 0;
+  int64_t n = 0, ntiles = 0;
+  float cb_scale = 0.f;
+  int8_t codebook[16] = {0};
+  uint32_t lut[4] = {0, 0, 0, 0};
+  void* packed = nullptr;
+  float* norms = nullptr;
+  float* rot_t = nullptr;
+  // per-batch device scratch
+  int8_t* bfrag = nullptr;
+  float* alpha = nullptr;
+  float* tau = nullptr;
+  unsigned long long* cand = nullptr;
+  uint32_t* cand_count = nullptr;
+  int* status = nullptr;
+  float* samp = nullptr;
+  int64_t samp_tiles = 0;
+  float* dense = nullptr;
+  size_t dense_bytes = 0;
+  int32_t* dense_dots = nullptr;
+  size_t dense_dots_bytes = 0;
+  int16_t* qs_buf = nullptr;
+  // host-API staging
+  void* io = nullptr;
+  size_t io_bytes = 0;
+
+  void free_all() {
+    void* ptrs[] = {packed, norms, rot_t, bfrag, alpha, tau, cand, cand_count,
+                    status, samp, dense, dense_dots, qs_buf, io};
+    for (void* p : ptrs)
+      if (p) hipFree(p);
+  }
+
+  int ensure(void** p, size_t* have, size_t need, char** err) {
+    if (*have >= need && *p != nullptr) return 0;
+    if (*p) hipFree(*p);
+    *p = nullptr;
+    *have = 0;
+    if (rt->alloc(need, p, err) != 0) return 1;
+    *have = need;
+    return 0;
+  }
+
+  int nqg_for(int qb) const { return (qb <= 32 || ks > 24) ? 1 : 2; }
+  int batch_cap() const { return ks > 24 ? 32 : kBatch; }
+
+  void scan_base(TqScanArgs* s, int qb) const {
+    memset(s, 0, sizeof(*s));
+    s->packed = static_cast<const int32_t*>(packed);
+    s->norms = norms;
+    s->bfrag = bfrag;
+    s->alpha = alpha;
+    s->tau = tau;
+    s->cand = cand;
+    s->cand_count = cand_count;
+    s->n = n;
+    s->tile_step = 1;
+    s->q = qb;
+    s->cap = kCap;
+    s->lut0 = lut[0];
+    s->lut1 = lut[1];
+    s->lut2 = lut[2];
+    s->lut3 = lut[3];
+  }
+
+  int launch_scan(TqScanArgs* s, int qb, char** err) {
+    static const char* const labels[3] = {"tq_scan_dense", "tq_scan_filter", "tq_scan_sample"};
+    const int nqg = nqg_for(qb);
+    char name[64];
+    snprintf(name, sizeof(name), "eos_tq_scan_b%d_k%d_g%d", bits, ks, nqg);
+    const int waves = 4;
+    int64_t blocks = (s->ntiles + waves - 1) / waves;
+    const int64_t maxb = (int64_t)rt->compute_units * 2;
+    if (blocks > maxb) blocks = maxb;
+    if (blocks < 1) blocks = 1;
+    return rt->launch(name, dim3((unsigned)blocks), dim3(256), 0, s, err, labels[s->mode]);
+  }
+
+  int prepare(const float* d_queries, int qb, int16_t* qs_out, char** err) {
+    const int nqg = nqg_for(qb);
+    TqPrepArgs p;
+    memset(&p, 0, sizeof(p));
+    p.queries = d_queries;
+    p.rot_t = rot_t;
+    p.bfrag = bfrag;
+    p.alpha = alpha;
+    p.tau = tau;
+    p.cand_count = cand_count;
+    p.qs_out = qs_out;
+    p.q = qb;
+    p.d = d;
+    p.ks = ks;
+    p.ncb = 2 * nqg;
+    p.qmax = qmax;
+    p.cb_scale = cb_scale;
+    return rt->launch("eos_tq_prepare", dim3(32 * nqg), dim3(256), 0, &p, err);
+  }
+
+  // Exhaustive scores of all queries of the batch into dense [qb][count].
+  int dense_scores(int qb, int64_t begin, int64_t count, bool want_dots, char** err) {
+    const size_t need = (size_t)qb * (size_t)count * sizeof(float);
+    if (ensure(reinterpret_cast<void**>(&dense), &dense_bytes, need, err) != 0) return 1;
+    if (want_dots &&
+        ensure(reinterpret_cast<void**>(&dense_dots), &dense_dots_bytes,
+               (size_t)qb * (size_t)count * sizeof(int32_t), err) != 0)
+      return 1;
+    TqScanArgs s;
+    scan_base(&s, qb);
+    s.mode = 0;
+    s.out_scores = dense;
+    s.out_dots = want_dots ? dense_dots : nullptr;
+    s.out_begin = begin;
+    s.out_count = count;
+    s.out_stride = count;
+    s.tile_begin = begin / kTile;
+    const int64_t tile_end = (begin + count + kTile - 1) / kTile;
+    s.ntiles = (int)(tile_end - s.tile_begin);
+    return launch_scan(&s, qb, err);
+  }
+
+  int topk_batch(const float* d_queries, int qb, int kk, int64_t* d_ids, float* d_scores,
+                 EosHipTQStats* st, char** err) {
+    if (prepare(d_queries, qb, nullptr, err) != 0) return 1;
+    if (n > kCap) {
+      const int64_t ns = (ntiles + kSampleStride - 1) / kSampleStride;
+      int64_t nsv = 0;
+      for (int64_t j = 0; j < ns; ++j) nsv += std::min<int64_t>(kTile, n - j * kSampleStride * kTile);
+      const double target = std::min<double>(8.0 * kk, kCap / 4.0);
+      int64_t r = (int64_t)std::ceil(target * (double)nsv / (double)n);
+      r = std::max<int64_t>(1, std::min<int64_t>(r, nsv));
+      TqScanArgs s;
+      scan_base(&s, qb);
+      s.mode = 2;
+      s.out_scores = samp;
+      s.out_stride = ns * kTile;
+      s.tile_begin = 0;
+      s.tile_step = kSampleStride;
+      s.ntiles = (int)ns;
+      if (launch_scan(&s, qb, err) != 0) return 1;
+      TqSelectArgs sel;
+      memset(&sel, 0, sizeof(sel));
+      sel.rows = samp;
+      sel.tau = tau;
+      sel.n = ns * kTile;
+      sel.stride = ns * kTile;
+      sel.kk = (int)r;
+      sel.mode = 0;
+      sel.nrows = qb;
+      if (rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err) != 0) return 1;
+    }
+    TqScanArgs s;
+    scan_base(&s, qb);
+    s.mode = 1;
+    s.tile_begin = 0;
+    s.ntiles = (int)ntiles;
+    if (launch_scan(&s, qb, err) != 0) return 1;
+    TqFinalizeArgs f;
+    memset(&f, 0, sizeof(f));
+    f.cand = cand;
+    f.cand_count = cand_count;
+    f.ids = reinterpret_cast<long long*>(d_ids);
+    f.scores = d_scores;
+    f.status = status;
+    f.cap = kCap;
+    f.kk = kk;
+    f.q = qb;
+    if (rt->launch("eos_tq_finalize", dim3(qb), dim3(1024), 0, &f, err) != 0) return 1;
+    int hstatus[kBatch];
+    uint32_t hcount[kBatch];
+    hipError_t e = hipMemcpyAsync(hstatus, status, sizeof(int) * qb, hipMemcpyDeviceToHost, rt->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(hcount, cand_count, sizeof(uint32_t) * qb, hipMemcpyDeviceToHost, rt->stream);
+    if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
+    if (rt->sync(err) != 0) return 1;
+    int flagged = 0;
+    for (int i = 0; i < qb; ++i) {
+      if (hstatus[i] != 0) ++flagged;
+      if (st) st->candidates_kept += std::min<uint32_t>(hcount[i], (uint32_t)kCap);
+    }
+    if (flagged > 0) {
+      if (dense_scores(qb, 0, n, false, err) != 0) return 1;
+      TqSelectArgs sel;
+      memset(&sel, 0, sizeof(sel));
+      sel.rows = dense;
+      sel.status = status;
+      sel.ids = reinterpret_cast<long long*>(d_ids);
+      sel.scores = d_scores;
+      sel.n = n;
+      sel.stride = n;
+      sel.kk = kk;
+      sel.mode = 1;
+      sel.nrows = qb;
+      if (rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err) != 0) return 1;
+      if (rt->sync(err) != 0) return 1;
+    }
+    if (st) {
+      st->fallback_queries += flagged;
+      st->candidate_count += (int64_t)qb * n;
+      st->batches += 1;
+    }
+    return 0;
+  }
+};
+
+extern "C" {
+
+int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uint8_t* codes,
+                          const float* norms, int64_t n, EosHipTQ** out, char** err) {
+  if (rt == nullptr || desc == nullptr || out == nullptr)
+    return set_err(err, "eoship_tq_bind_corpus: NULL argument");
+  *out = nullptr;
+  if (desc->bits != 2 && desc->bits != 4)
+    return set_err(err, "eoship_tq_bind_corpus: bits must be 2 or 4 (got %d)", desc->bits);
+  const int ks = ks_for_dim(desc->dim);
+  if (desc->dim < 1 || ks == 0)
+    return set_err(err, "eoship_tq_bind_corpus: dim must be in [1, 1024] (got %d)", desc->dim);
+  if (!(desc->codebook_scale > 0.f) || !std::isfinite(desc->codebook_scale))
+    return set_err(err, "eoship_tq_bind_corpus: codebook_scale must be finite and > 0");
+  if (desc->codebook == nullptr) return set_err(err, "eoship_tq_bind_corpus: codebook is NULL");
+  if (n < 0 || n >= (int64_t)0xffffffffLL)
+    return set_err(err, "eoship_tq_bind_corpus: n must be in [0, 2^32-1) (got %lld)", (long long)n);
+  if (n > 0 && (codes == nullptr || norms == nullptr))
+    return set_err(err, "eoship_tq_bind_corpus: codes/norms are NULL");
+  for (int64_t i = 0; i < n; ++i) {
+    if (!(norms[i] >= 0.f) || !std::isfinite(norms[i]))
+      return set_err(err,
+                     "eoship_tq_bind_corpus: vector %lld has Norm %g; Norm must be finite and >= 0",
+                     (long long)i, (double)norms[i]);
+  }
+  auto* tq = new EosHipTQ();
+  tq->rt = rt;
+  tq->d = desc->dim;
+  tq->bits = desc->bits;
+  tq->ks = ks;
+  const int spl = 8 / desc->bits;
+  tq->nload = (ks + spl - 1) / spl;
+  tq->row_bytes = (desc->dim * desc->bits + 7) / 8;
+  tq->n = n;
+  tq->ntiles = (n + kTile - 1) / kTile;
+  tq->cb_scale = desc->codebook_scale;
+  const int levels = 1 << desc->bits;
+  int cmax = 0;
+  for (int v = 0; v < levels; ++v) {
+    tq->codebook[v] = desc->codebook[v];
+    cmax = std::max(cmax, std::abs((int)desc->codebook[v]));
+  }
+  if (cmax == 0) {
+    tq->qmax = kQmaxLimit;
+  } else {
+    const int64_t lim = (int64_t)2147483647 / ((int64_t)cmax * desc->dim) - 128;
+    tq->qmax = (int)std::min<int64_t>(kQmaxLimit, lim);
+  }
+  if (tq->qmax < 1) {
+    delete tq;
+    return set_err(err, "eoship_tq_bind_corpus: dim too large for exact int32 dots");
+  }
+  if (desc->bits == 4) {
+    if (solve_lut4(tq->codebook, tq->lut, err) != 0) {
+      delete tq;
+      return 1;
+    }
+  } else {
+    tq->lut[0] = (uint8_t)tq->codebook[0] | ((uint8_t)tq->codebook[1] << 8) |
+                 ((uint8_t)tq->codebook[2] << 16) | ((uint32_t)(uint8_t)tq->codebook[3] << 24);
+  }
+  auto fail = [&](void) {
+    tq->free_all();
+    delete tq;
+    return 1;
+  };
+  hipError_t e = hipSetDevice(rt->device);
+  if (e != hipSuccess) {
+    hip_err(err, "hipSetDevice", e);
+    return fail();
+  }
+  const int64_t padded = tq->ntiles * kTile;
+  const size_t packed_bytes = (size_t)tq->ntiles * tq->nload * 64 * 16;
+  if (rt->alloc(packed_bytes, &tq->packed, err) != 0) return fail();
+  if (rt->alloc((size_t)std::max<int64_t>(padded, 1) * sizeof(float),
+                reinterpret_cast<void**>(&tq->norms), err) != 0)
+    return fail();
+  e = hipMemsetAsync(tq->norms, 0, (size_t)std::max<int64_t>(padded, 1) * sizeof(float), rt->stream);
+  if (e != hipSuccess) {
+    hip_err(err, "hipMemsetAsync(norms)", e);
+    return fail();
+  }
+  if (n > 0) {
+    e = hipMemcpyAsync(tq->norms, norms, (size_t)n * sizeof(float), hipMemcpyHostToDevice, rt->stream);
+    if (e != hipSuccess) {
+      hip_err(err, "hipMemcpyAsync(norms)", e);
+      return fail();
+    }
+    void* dcodes = nullptr;
+    const size_t code_bytes = (size_t)n * tq->row_bytes;
+    if (rt->alloc(code_bytes, &dcodes, err) != 0) return fail();
+    e = hipMemcpyAsync(dcodes, codes, code_bytes, hipMemcpyHostToDevice, rt->stream);
+    if (e != hipSuccess) {
+      hipFree(dcodes);
+      hip_err(err, "hipMemcpyAsync(codes)", e);
+      return fail();
+    }
+    TqPackArgs p;
+    memset(&p, 0, sizeof(p));
+    p.codes = static_cast<const uint8_t*>(dcodes);
+    p.packed = static_cast<uint32_t*>(tq->packed);
+    p.n = n;
+    p.total_dwords = (long long)(packed_bytes / 4);
+    p.d = tq->d;
+    p.bits = tq->bits;
+    p.row_bytes = tq->row_bytes;
+    p.ks = tq->ks;
+    p.nload = tq->nload;
+    const int64_t blocks = (p.total_dwords + 255) / 256;
+    if (rt->launch("eos_tq_pack", dim3((unsigned)blocks), dim3(256), 0, &p, err) != 0) {
+      rt->sync(nullptr);
+      hipFree(dcodes);
+      return fail();
+    }
+    const int rc = rt->sync(err);
+    hipFree(dcodes);
+    if (rc != 0) return fail();
+  }
+  if (desc->rotation != nullptr) {
+    std::vector<float> rt_host((size_t)tq->d * tq->d);
+    for (int j = 0; j < tq->d; ++j)
+      for (int k = 0; k < tq->d; ++k) rt_host[(size_t)k * tq->d + j] = desc->rotation[(size_t)j * tq->d + k];
+    if (rt->alloc(rt_host.size() * sizeof(float), reinterpret_cast<void**>(&tq->rot_t), err) != 0)
+      return fail();
+    e = hipMemcpy(tq->rot_t, rt_host.data(), rt_host.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      hip_err(err, "hipMemcpy(rotation)", e);
+      return fail();
+    }
+  }
+  const size_t bfrag_bytes = (size_t)tq->ks * 4 * 64 * 16;
+  tq->samp_tiles = (tq->ntiles + kSampleStride - 1) / kSampleStride;
+  if (rt->alloc(bfrag_bytes, reinterpret_cast<void**>(&tq->bfrag), err) != 0 ||
+      rt->alloc(kBatch * sizeof(float), reinterpret_cast<void**>(&tq->alpha), err) != 0 ||
+      rt->alloc(kBatch * sizeof(float), reinterpret_cast<void**>(&tq->tau), err) != 0 ||
+      rt->alloc(kBatch * sizeof(uint32_t), reinterpret_cast<void**>(&tq->cand_count), err) != 0 ||
+      rt->alloc(kBatch * sizeof(int), reinterpret_cast<void**>(&tq->status), err) != 0 ||
+      rt->alloc((size_t)kBatch * kCap * sizeof(unsigned long long),
+                reinterpret_cast<void**>(&tq->cand), err) != 0 ||
+      rt->alloc((size_t)kBatch * std::max<int64_t>(tq->samp_tiles, 1) * kTile * sizeof(float),
+                reinterpret_cast<void**>(&tq->samp), err) != 0)
+    return fail();
+  *out = tq;
+  return 0;
+}
+
+int eoship_tq_release(EosHipTQ* tq, char** err) {
+  (void)err;
+  if (tq == nullptr) return 0;
+  hipStreamSynchronize(tq->rt->stream);
+  tq->free_all();
+  delete tq;
+  return 0;
+}
+
+static int topk_device_impl(EosHipRuntime* rt, EosHipTQ* tq, const float* d_queries, int32_t q,
+                            int32_t k, int64_t* d_ids, float* d_scores, EosHipTQStats* stats,
+                            char** err) {
+  if (stats) memset(stats, 0, sizeof(*stats));
+  const int64_t kk64 = (k <= 0 || (int64_t)k > tq->n) ? tq->n : k;
+  if (q == 0 || kk64 == 0) return 0;
+  if (kk64 > kSortCap)
+    return set_err(err, "eoship_tq_topk: k=%lld exceeds the device top-k limit of %d",
+                   (long long)kk64, kSortCap);
+  const int kk = (int)kk64;
+  const int cap = tq->batch_cap();
+  for (int q0 = 0; q0 < q; q0 += cap) {
+    const int qb = std::min(cap, q - q0);
+    if (tq->topk_batch(d_queries + (size_t)q0 * tq->d, qb, kk, d_ids + (size_t)q0 * kk,
+                       d_scores + (size_t)q0 * kk, stats, err) != 0)
+      return 1;
+  }
+  return 0;
+}
+
+static int check_common(EosHipRuntime* rt, EosHipTQ* tq, int32_t q, const char* what, char** err) {
+  if (rt == nullptr || tq == nullptr) return set_err(err, "%s: NULL runtime or corpus", what);
+  if (tq->rt != rt) return set_err(err, "%s: corpus was bound on another runtime", what);
+  if (q < 0) return set_err(err, "%s: negative query count", what);
+  return 0;
+}
+
+int eoship_tq_topk_device(EosHipRuntime* rt, EosHipTQ* tq, const float* d_queries, int32_t q,
+                          int32_t k, int64_t* d_ids, float* d_scores, EosHipTQStats* stats,
+                          char** err) {
+  if (check_common(rt, tq, q, "eoship_tq_topk_device", err) != 0) return 1;
+  if (q > 0 && (d_queries == nullptr || d_ids == nullptr || d_scores == nullptr))
+    return set_err(err, "eoship_tq_topk_device: NULL buffer");
+  return topk_device_impl(rt, tq, d_queries, q, k, d_ids, d_scores, stats, err);
+}
+
+int eoship_tq_topk(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int32_t q, int32_t k,
+                   int64_t* ids, float* scores, EosHipTQStats* stats, char** err) {
+  if (check_common(rt, tq, q, "eoship_tq_topk", err) != 0) return 1;
+  const int64_t kk = (k <= 0 || (int64_t)k > tq->n) ? tq->n : k;
+  if (stats) memset(stats, 0, sizeof(*stats));
+  if (q == 0 || kk == 0) return 0;
+  if (queries == nullptr || ids == nullptr || scores == nullptr)
+    return set_err(err, "eoship_tq_topk: NULL buffer");
+  const size_t qbytes = (size_t)q * tq->d * sizeof(float);
+  const size_t ibytes = (size_t)q * kk * sizeof(int64_t);
+  const size_t sbytes = (size_t)q * kk * sizeof(float);
+  if (tq->ensure(&tq->io, &tq->io_bytes, qbytes + ibytes + sbytes + 256, err) != 0) return 1;
+  char* base = static_cast<char*>(tq->io);
+  float* dq = reinterpret_cast<float*>(base);
+  int64_t* di = reinterpret_cast<int64_t*>(base + ((qbytes + 15) & ~(size_t)15));
+  float* ds = reinterpret_cast<float*>(reinterpret_cast<char*>(di) + ibytes);
+  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
+  if (topk_device_impl(rt, tq, dq, q, k, di, ds, stats, err) != 0) return 1;
+  e = hipMemcpyAsync(ids, di, ibytes, hipMemcpyDeviceToHost, rt->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(scores, ds, sbytes, hipMemcpyDeviceToHost, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(results)", e);
+  return rt->sync(err);
+}
+
+int eoship_tq_scores(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int32_t q,
+                     int64_t begin, int64_t count, int32_t* dots, float* scores, char** err) {
+  if (check_common(rt, tq, q, "eoship_tq_scores", err) != 0) return 1;
+  if (begin < 0 || count < 0 || begin + count > tq->n)
+    return set_err(err, "eoship_tq_scores: range [%lld, %lld) outside [0, %lld)", (long long)begin,
+                   (long long)(begin + count), (long long)tq->n);
+  if (q == 0 || count == 0) return 0;
+  if (queries == nullptr) return set_err(err, "eoship_tq_scores: queries is NULL");
+  const size_t qbytes = (size_t)q * tq->d * sizeof(float);
+  if (tq->ensure(&tq->io, &tq->io_bytes, qbytes, err) != 0) return 1;
+  float* dq = static_cast<float*>(tq->io);
+  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
+  const int cap = tq->batch_cap();
+  for (int q0 = 0; q0 < q; q0 += cap) {
+    const int qb = std::min(cap, q - q0);
+    if (tq->prepare(dq + (size_t)q0 * tq->d, qb, nullptr, err) != 0) return 1;
+    if (tq->dense_scores(qb, begin, count, dots != nullptr, err) != 0) return 1;
+    const size_t rows = (size_t)qb * count;
+    if (scores) {
+      e = hipMemcpyAsync(scores + (size_t)q0 * count, tq->dense, rows * sizeof(float),
+                         hipMemcpyDeviceToHost, rt->stream);
+      if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(scores)", e);
+    }
+    if (dots) {
+      e = hipMemcpyAsync(dots + (size_t)q0 * count, tq->dense_dots, rows * sizeof(int32_t),
+                         hipMemcpyDeviceToHost, rt->stream);
+      if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(dots)", e);
+    }
+    if (rt->sync(err) != 0) return 1;
+  }
+  return 0;
+}
+
+int eoship_tq_prepare(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int32_t q,
+                      int16_t* qs, float* alpha, char** err) {
+  if (check_common(rt, tq, q, "eoship_tq_prepare", err) != 0) return 1;
+  if (q == 0) return 0;
+  if (queries == nullptr) return set_err(err, "eoship_tq_prepare: queries is NULL");
+  const size_t qbytes = (size_t)q * tq->d * sizeof(float);
+  if (tq->ensure(&tq->io, &tq->io_bytes, qbytes, err) != 0) return 1;
+  if (tq->qs_buf == nullptr &&
+      tq->rt->alloc((size_t)kBatch * tq->d * sizeof(int16_t), reinterpret_cast<void**>(&tq->qs_buf),
+                    err) != 0)
+    return 1;
+  float* dq = static_cast<float*>(tq->io);
+  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
+  const int cap = tq->batch_cap();
+  for (int q0 = 0; q0 < q; q0 += cap) {
+    const int qb = std::min(cap, q - q0);
+    if (tq->prepare(dq + (size_t)q0 * tq->d, qb, tq->qs_buf, err) != 0) return 1;
+    if (qs) {
+      e = hipMemcpyAsync(qs + (size_t)q0 * tq->d, tq->qs_buf, (size_t)qb * tq->d * sizeof(int16_t),
+                         hipMemcpyDeviceToHost, rt->stream);
+      if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(qs)", e);
+    }
+    if (alpha) {
+      e = hipMemcpyAsync(alpha + q0, tq->alpha, (size_t)qb * sizeof(float), hipMemcpyDeviceToHost,
+                         rt->stream);
+      if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(alpha)", e);
+    }
+    if (rt->sync(err) != 0) return 1;
+  }
+  return 0;
+}
+
+}  // extern "C"

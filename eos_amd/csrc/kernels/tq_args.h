@@ -1,0 +1,74 @@
+// Kernel argument blocks shared by the gfx950 code objects and the host shim.
+// Each kernel takes one of these by value; keep field order and types in sync
+// on both sides (this header is the only definition).
+#ifndef EOSHIP_TQ_ARGS_H
+#define EOSHIP_TQ_ARGS_H
+
+#include <stdint.h>
+
+struct TqPrepArgs {
+  const float* queries;  // [q][d]
+  const float* rot_t;    // [d][d], rot_t[k*d + j] = R[j][k]; NULL = identity
+  int8_t* bfrag;         // [ks][ncb][64][16] query fragments
+  float* alpha;          // [32*ncb/2]
+  float* tau;            // [32*ncb/2] reset to -inf
+  uint32_t* cand_count;  // [32*ncb/2] reset to 0
+  int16_t* qs_out;       // optional [q][d]
+  int q, d, ks, ncb, qmax;
+  float cb_scale;
+};
+
+struct TqPackArgs {
+  const uint8_t* codes;  // [n][row_bytes] reference layout
+  uint32_t* packed;      // [ntiles][nload][64][4] dwords
+  long long n;
+  long long total_dwords;
+  int d, bits, row_bytes, ks, nload;
+};
+
+struct TqScanArgs {
+  const int32_t* packed;   // [ntiles][nload][64][4] dwords
+  const float* norms;      // [ntiles*32], zero past n
+  const int8_t* bfrag;     // [ks][ncb][64][16]
+  const float* alpha;      // [32*nqg]
+  const float* tau;        // [32*nqg] filter thresholds
+  unsigned long long* cand;               // [32*nqg][cap] rank keys
+  uint32_t* cand_count;    // [32*nqg]
+  float* out_scores;       // dense/sample output [q][out_stride]
+  int32_t* out_dots;       // dense output (optional)
+  long long n;             // valid vectors
+  long long out_begin;     // dense: vector index of column 0
+  long long out_count;     // dense: columns
+  long long out_stride;
+  long long tile_begin;    // first physical tile
+  long long tile_step;     // logical tile j -> tile_begin + j * tile_step
+  int ntiles;              // logical tiles in this launch
+  int q;                   // live query columns
+  int cap;                 // candidate capacity per query
+  int mode;                // 0 dense, 1 filter, 2 sample
+  uint32_t lut0, lut1, lut2, lut3;
+};
+
+struct TqSelectArgs {
+  const float* rows;       // [nrows][stride] scores
+  const int* status;       // mode 1: rows with status 0 are skipped (NULL = all)
+  float* tau;              // mode 0 output [nrows]
+  long long* ids;          // mode 1 output [nrows][kk]
+  float* scores;           // mode 1 output [nrows][kk]
+  long long n;             // elements per row
+  long long stride;
+  int kk;                  // rank
+  int mode;                // 0: tau = score of the kk-th best; 1: sorted top-kk
+  int nrows;
+};
+
+struct TqFinalizeArgs {
+  const unsigned long long* cand;
+  const uint32_t* cand_count;
+  long long* ids;     // [q][kk]
+  float* scores;      // [q][kk]
+  int* status;        // [q]: 0 ok, 1 too few candidates, 2 overflow
+  int cap, kk, q;
+};
+
+#endif  // EOSHIP_TQ_ARGS_H

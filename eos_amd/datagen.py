@@ -1,0 +1,161 @@
+"""Seeded synthetic inputs for the BASELINE configurations.
+
+Every generator is counter-based (splitmix64 over the element index), so a
+(seed, shape) pair always yields the same array on any machine and in any
+process; tests, the smoke check and the benchmark all draw from here.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+_GAMMA = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+
+
+def splitmix64(seed: int, count: int, offset: int = 0) -> np.ndarray:
+    """Element i is splitmix64's output for state seed + (offset + i + 1) * golden gamma."""
+    with np.errstate(over="ignore"):
+        idx = np.arange(offset + 1, offset + count + 1, dtype=np.uint64)
+        z = np.uint64(seed & 0xFFFFFFFFFFFFFFFF) + idx * _GAMMA
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        return z ^ (z >> np.uint64(31))
+
+
+def uniform(seed: int, count: int) -> np.ndarray:
+    """Uniform doubles in [0, 1) from the top 53 bits."""
+    return (splitmix64(seed, count) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+
+
+def normal(seed: int, count: int) -> np.ndarray:
+    """Standard normal doubles (Box-Muller; u1 in (0, 1])."""
+    half = (count + 1) // 2
+    u = uniform(seed, 2 * half)
+    u1 = 1.0 - u[0::2]
+    u2 = u[1::2]
+    r = np.sqrt(-2.0 * np.log(u1))
+    z = np.empty(2 * half, dtype=np.float64)
+    z[0::2] = r * np.cos(2.0 * math.pi * u2)
+    z[1::2] = r * np.sin(2.0 * math.pi * u2)
+    return z[:count]
+
+
+def uniform_int(seed: int, count: int, lo: int, hi: int) -> np.ndarray:
+    """Integers uniform in [lo, hi) (multiply-shift on the top 32 bits)."""
+    top = (splitmix64(seed, count) >> np.uint64(32)).astype(np.uint64)
+    span = np.uint64(hi - lo)
+    return ((top * span) >> np.uint64(32)).astype(np.int64) + lo
+
+
+def random_bytes(seed: int, count: int) -> np.ndarray:
+    words = splitmix64(seed, (count + 7) // 8)
+    return words.view(np.uint8)[:count].copy()
+
+
+def lognormal(seed: int, count: int, sigma: float) -> np.ndarray:
+    return np.exp(sigma * normal(seed, count))
+
+
+def orthogonal(seed: int, d: int) -> np.ndarray:
+    """Seeded random orthogonal d x d matrix (QR of a Gaussian, R's diagonal made positive)."""
+    g = normal(seed, d * d).reshape(d, d)
+    q, r = np.linalg.qr(g)
+    q = q * np.sign(np.diag(r))[None, :]
+    return q
+
+
+def unit_rows(x: np.ndarray) -> np.ndarray:
+    n = np.sqrt(np.sum(x.astype(np.float64) ** 2, axis=-1, keepdims=True))
+    n[n == 0] = 1.0
+    return x / n
+
+
+def lloyd_max_normal(levels: int, iters: int = 500) -> np.ndarray:
+    """Lloyd-Max reconstruction points of N(0, 1) (ascending)."""
+    def phi(x):
+        return math.exp(-0.5 * x * x) / math.sqrt(2.0 * math.pi)
+
+    def cdf(x):
+        return 0.5 * (1.0 + math.erf(x / math.sqrt(2.0)))
+
+    c = [(-3.0 + 6.0 * (i + 0.5) / levels) for i in range(levels)]
+    for _ in range(iters):
+        b = [-math.inf] + [(c[i] + c[i + 1]) / 2.0 for i in range(levels - 1)] + [math.inf]
+        nc = []
+        for i in range(levels):
+            lo, hi = b[i], b[i + 1]
+            plo = 0.0 if lo == -math.inf else phi(lo)
+            phi_hi = 0.0 if hi == math.inf else phi(hi)
+            mass = (1.0 if hi == math.inf else cdf(hi)) - (0.0 if lo == -math.inf else cdf(lo))
+            nc.append((plo - phi_hi) / mass)
+        c = nc
+    return np.array(c, dtype=np.float64)
+
+
+def turboquant_codebook(bits: int, dim: int) -> tuple[np.ndarray, float]:
+    """Build-defined TurboQuant codebook on an int8 grid.
+
+    Centroids are the Lloyd-Max points of N(0, 1/dim) (the coordinate law of a
+    rotated unit vector), scale s_c = max|c| / 127, grid values round(c / s_c).
+    Returns (int8 codes [2^bits], s_c)."""
+    c = lloyd_max_normal(1 << bits) / math.sqrt(dim)
+    s = float(np.float32(np.max(np.abs(c)) / 127.0))
+    grid = np.clip(np.rint(c / s), -127, 127).astype(np.int8)
+    return grid, s
+
+
+def pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """[n, d] integer codes -> [n, ceil(d*bits/8)] bytes, coordinate j at bit
+    (j*bits) % 8 of byte (j*bits) // 8 (low bits first)."""
+    n, d = codes.shape
+    row_bytes = (d * bits + 7) // 8
+    per = 8 // bits
+    pad = row_bytes * per - d
+    c = np.concatenate([codes.astype(np.uint8), np.zeros((n, pad), np.uint8)], axis=1)
+    c = c.reshape(n, row_bytes, per)
+    out = np.zeros((n, row_bytes), np.uint8)
+    for e in range(per):
+        out |= (c[:, :, e] & ((1 << bits) - 1)) << (e * bits)
+    return out
+
+
+def unpack_codes(packed: np.ndarray, bits: int, d: int) -> np.ndarray:
+    per = 8 // bits
+    n, row_bytes = packed.shape
+    out = np.zeros((n, row_bytes, per), np.uint8)
+    for e in range(per):
+        out[:, :, e] = (packed >> (e * bits)) & ((1 << bits) - 1)
+    return out.reshape(n, row_bytes * per)[:, :d]
+
+
+class TurboQuantCorpus:
+    """Synthetic TurboQuant corpus of the BASELINE flat / multivector configs."""
+
+    def __init__(self, n: int, dim: int, bits: int, seed_codes: int, seed_norms: int,
+                 seed_rot: int, norm_sigma: float = 0.25, rotation: bool = True):
+        self.n, self.dim, self.bits = n, dim, bits
+        row_bytes = (dim * bits + 7) // 8
+        if bits == 4 or bits == 2:
+            # Uniform codes: every packed byte is uniform over [0, 256).
+            self.codes = random_bytes(seed_codes, n * row_bytes).reshape(n, row_bytes)
+            if (dim * bits) % 8:
+                keep = (dim * bits) % 8
+                self.codes[:, -1] &= np.uint8((1 << keep) - 1)
+        else:
+            raise ValueError("bits must be 2 or 4")
+        self.norms = lognormal(seed_norms, n, norm_sigma).astype(np.float32)
+        self.rotation = orthogonal(seed_rot, dim).astype(np.float32) if rotation else None
+        self.codebook, self.codebook_scale = turboquant_codebook(bits, dim)
+
+
+def baseline_flat_corpus(n: int = 1_000_000, dim: int = 384) -> TurboQuantCorpus:
+    """4-bit codes (seed 3), lognormal(0, 0.25) norms (seed 4), rotation seed 5."""
+    return TurboQuantCorpus(n, dim, 4, seed_codes=3, seed_norms=4, seed_rot=5)
+
+
+def baseline_queries(q: int, dim: int, seed: int = 6) -> np.ndarray:
+    """Gaussian queries, unit-normalized in f64, stored f32."""
+    return unit_rows(normal(seed, q * dim).reshape(q, dim)).astype(np.float32)

@@ -1,0 +1,154 @@
+"""TurboQuant retrieval scoring on the MI355X backend.
+
+Host-side mirror of the reference's scoring entry points, with the same names,
+argument meaning and error behaviour:
+
+* ``TurboQuantIndex``  -- the bound corpus; the device-resident counterpart of
+  ``[]turboQuantRetrievalDoc`` + ``*turboquant.IPQuantizer``
+  (runtime/retrieval_turboquant.go:699-711).
+* ``top_turboquant_retrieval_scores_with_stats`` --
+  ``topTurboQuantRetrievalScoresWithStats`` (runtime/retrieval_turboquant.go:1853-1887):
+  top-k by score descending, ties by id ascending (runtime/retrieval_eval.go:1153-1161);
+  ``top_k <= 0`` or ``top_k > len(docs)`` means all documents (:1854-1856).
+* ``TurboQuantIndex.inner_product_prepared`` -- ``InnerProductPrepared`` over a
+  slice of documents (runtime/retrieval_turboquant.go:1874), with the exact
+  integer code dot products.
+
+All arithmetic runs in libeoship's gfx950 kernels; nothing here computes scores.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from .runtime import DeviceBuffer, Runtime
+
+
+@dataclass
+class RetrievalScoredDoc:
+    """One ranked result (runtime/retrieval_eval.go retrievalScoredDoc): ID is the vector index."""
+    id: int
+    score: float
+
+
+@dataclass
+class TurboQuantRetrievalScoreStats:
+    """Counterpart of turboQuantRetrievalScoreStats (runtime/retrieval_turboquant.go:1857-1887)."""
+    candidate_count: int = 0
+    candidates_scored: int = 0
+    candidates_kept: int = 0
+    fallback_queries: int = 0
+    batches: int = 0
+    pruning_supported: bool = False
+    pruning_used: bool = False
+
+
+class TurboQuantIndex:
+    """A TurboQuant corpus bound on the device.
+
+    codes: uint8 [n, ceil(dim*bits/8)] (coordinate j at bit (j*bits)%8 of byte
+    (j*bits)//8, low bits first); norms: float32 [n], finite and >= 0;
+    codebook: int8 [2^bits] grid values with f32 scale; rotation: float32
+    [dim, dim] orthogonal (None = identity).
+    """
+
+    def __init__(self, rt: Runtime, codes: np.ndarray, norms: np.ndarray, dim: int, bits: int,
+                 codebook: np.ndarray, codebook_scale: float, rotation: np.ndarray | None = None):
+        codes = np.ascontiguousarray(codes, dtype=np.uint8)
+        norms = np.ascontiguousarray(norms, dtype=np.float32)
+        n = int(norms.shape[0])
+        row_bytes = (dim * bits + 7) // 8
+        if codes.shape != (n, row_bytes):
+            raise ValueError(f"codes must have shape ({n}, {row_bytes}), got {codes.shape}")
+        cb = np.ascontiguousarray(codebook, dtype=np.int8)
+        if cb.shape != (1 << bits,):
+            raise ValueError(f"codebook must have {1 << bits} entries")
+        rot = None if rotation is None else np.ascontiguousarray(rotation, dtype=np.float32)
+        if rot is not None and rot.shape != (dim, dim):
+            raise ValueError("rotation must be dim x dim")
+        self.rt, self.n, self.dim, self.bits = rt, n, dim, bits
+        desc = _lib.EosHipTQDesc(
+            dim=dim, bits=bits, codebook_scale=float(codebook_scale),
+            codebook=cb.ctypes.data_as(C.POINTER(C.c_int8)),
+            rotation=rot.ctypes.data_as(C.POINTER(C.c_float)) if rot is not None else None)
+        self.handle = C.c_void_p()
+        _lib.call("eoship_tq_bind_corpus", rt.handle, C.byref(desc), codes.ctypes.data_as(C.c_void_p),
+                  norms.ctypes.data_as(C.c_void_p), C.c_int64(n), C.byref(self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            _lib.call("eoship_tq_release", self.handle)
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    def _queries(self, queries: np.ndarray) -> np.ndarray:
+        q = np.ascontiguousarray(queries, dtype=np.float32)
+        if q.ndim == 1:
+            q = q[None, :]
+        if q.ndim != 2 or q.shape[1] != self.dim:
+            raise ValueError(f"queries must be [Q, {self.dim}]")
+        return q
+
+    def effective_k(self, top_k: int) -> int:
+        return self.n if (top_k <= 0 or top_k > self.n) else int(top_k)
+
+    def top_k(self, queries: np.ndarray, top_k: int):
+        """Returns (ids int64 [Q, kk], scores float32 [Q, kk], stats)."""
+        q = self._queries(queries)
+        kk = self.effective_k(top_k)
+        ids = np.zeros((q.shape[0], kk), np.int64)
+        scores = np.zeros((q.shape[0], kk), np.float32)
+        st = _lib.EosHipTQStats()
+        _lib.call("eoship_tq_topk", self.rt.handle, self.handle, q.ctypes.data_as(C.c_void_p),
+                  C.c_int32(q.shape[0]), C.c_int32(int(top_k)), ids.ctypes.data_as(C.c_void_p),
+                  scores.ctypes.data_as(C.c_void_p), C.byref(st))
+        stats = TurboQuantRetrievalScoreStats(
+            candidate_count=st.candidate_count, candidates_scored=st.candidate_count,
+            candidates_kept=st.candidates_kept, fallback_queries=st.fallback_queries,
+            batches=st.batches)
+        return ids, scores, stats
+
+    def top_k_device(self, d_queries: DeviceBuffer, nq: int, top_k: int, d_ids: DeviceBuffer,
+                     d_scores: DeviceBuffer) -> _lib.EosHipTQStats:
+        st = _lib.EosHipTQStats()
+        _lib.call("eoship_tq_topk_device", self.rt.handle, self.handle, d_queries.ptr,
+                  C.c_int32(nq), C.c_int32(int(top_k)), d_ids.ptr, d_scores.ptr, C.byref(st))
+        return st
+
+    def inner_product_prepared(self, queries: np.ndarray, begin: int = 0, count: int | None = None):
+        """Exhaustive (dots int32 [Q, count], scores float32 [Q, count]) for vectors [begin, begin+count)."""
+        q = self._queries(queries)
+        count = self.n - begin if count is None else int(count)
+        dots = np.zeros((q.shape[0], count), np.int32)
+        scores = np.zeros((q.shape[0], count), np.float32)
+        _lib.call("eoship_tq_scores", self.rt.handle, self.handle, q.ctypes.data_as(C.c_void_p),
+                  C.c_int32(q.shape[0]), C.c_int64(begin), C.c_int64(count),
+                  dots.ctypes.data_as(C.c_void_p), scores.ctypes.data_as(C.c_void_p))
+        return dots, scores
+
+    def prepare_query(self, queries: np.ndarray):
+        """Device PrepareQuery: (int16 [Q, dim] rotated-rounded query, float32 [Q] alpha)."""
+        q = self._queries(queries)
+        qs = np.zeros((q.shape[0], self.dim), np.int16)
+        alpha = np.zeros(q.shape[0], np.float32)
+        _lib.call("eoship_tq_prepare", self.rt.handle, self.handle, q.ctypes.data_as(C.c_void_p),
+                  C.c_int32(q.shape[0]), qs.ctypes.data_as(C.c_void_p),
+                  alpha.ctypes.data_as(C.c_void_p))
+        return qs, alpha
+
+
+def top_turboquant_retrieval_scores_with_stats(index: TurboQuantIndex, queries: np.ndarray,
+                                               top_k: int):
+    """Per query, the ranked [RetrievalScoredDoc] list and the run's stats."""
+    ids, scores, stats = index.top_k(queries, top_k)
+    out = [[RetrievalScoredDoc(int(i), float(s)) for i, s in zip(ids[r], scores[r])]
+           for r in range(ids.shape[0])]
+    return out, stats

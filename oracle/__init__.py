@@ -1,0 +1,134 @@
+"""TEST INFRASTRUCTURE ONLY: the CPU oracle (plain C restatement of the
+reference's host path, see the headers of the C sources for the file:line each
+function follows). Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this package; the product path never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_DIR, "liboracle.so")
+_lib = None
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", _DIR], check=True)
+    return LIB_PATH
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        build()
+    lib = C.CDLL(LIB_PATH)
+    P = C.c_void_p
+    lib.tq_qmax.argtypes = [P, C.c_int, C.c_int]
+    lib.tq_qmax.restype = C.c_int
+    lib.tq_prepare.argtypes = [P, P, C.c_int, C.c_int, C.c_float, P, P]
+    lib.tq_prepare.restype = None
+    lib.tq_dots.argtypes = [P, C.c_int, P, C.c_int64, C.c_int, P, P]
+    lib.tq_dots.restype = None
+    lib.tq_scores.argtypes = [P, C.c_int, P, C.c_int, C.c_int, P, C.c_float, P, P, C.c_int64,
+                              C.c_int64, P, P]
+    lib.tq_scores.restype = None
+    lib.tq_scores_f64.argtypes = [P, C.c_int, P, C.c_int, C.c_int, P, C.c_float, P, P, C.c_int64, P]
+    lib.tq_scores_f64.restype = None
+    lib.tq_topk.argtypes = [P, C.c_int, P, C.c_int, C.c_int, P, C.c_float, P, P, C.c_int64, C.c_int,
+                            P, P]
+    lib.tq_topk.restype = C.c_int64
+    lib.topk_scores.argtypes = [P, C.c_int64, C.c_int, P, P]
+    lib.topk_scores.restype = C.c_int64
+    _lib = lib
+    return lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def tq_qmax(codebook: np.ndarray, dim: int) -> int:
+    cb = np.ascontiguousarray(codebook, dtype=np.int8)
+    return load().tq_qmax(_p(cb), int(cb.shape[0]), int(dim))
+
+
+def tq_prepare(query: np.ndarray, rotation, codebook, codebook_scale: float):
+    q = _f32(query)
+    d = q.shape[0]
+    rot = None if rotation is None else _f32(rotation)
+    qs = np.zeros(d, np.int16)
+    alpha = C.c_float()
+    load().tq_prepare(_p(q), _p(rot), d, tq_qmax(codebook, d), C.c_float(codebook_scale), _p(qs),
+                      C.byref(alpha))
+    return qs, np.float32(alpha.value)
+
+
+def tq_dots(qs: np.ndarray, codes: np.ndarray, bits: int, codebook: np.ndarray) -> np.ndarray:
+    qs = np.ascontiguousarray(qs, dtype=np.int16)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    cb = np.ascontiguousarray(codebook, dtype=np.int8)
+    out = np.zeros(codes.shape[0], np.int32)
+    load().tq_dots(_p(qs), qs.shape[0], _p(codes), codes.shape[0], bits, _p(cb), _p(out))
+    return out
+
+
+def tq_scores(queries, rotation, dim, bits, codebook, codebook_scale, codes, norms, begin=0,
+              count=None):
+    q = _f32(queries).reshape(-1, dim)
+    rot = None if rotation is None else _f32(rotation)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    norms = _f32(norms)
+    cb = np.ascontiguousarray(codebook, dtype=np.int8)
+    count = codes.shape[0] - begin if count is None else count
+    dots = np.zeros((q.shape[0], count), np.int32)
+    scores = np.zeros((q.shape[0], count), np.float32)
+    load().tq_scores(_p(q), q.shape[0], _p(rot), dim, bits, _p(cb), C.c_float(codebook_scale),
+                     _p(codes), _p(norms), begin, count, _p(dots), _p(scores))
+    return dots, scores
+
+
+def tq_scores_f64(queries, rotation, dim, bits, codebook, codebook_scale, codes, norms):
+    q = _f32(queries).reshape(-1, dim)
+    rot = None if rotation is None else _f32(rotation)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    norms = _f32(norms)
+    cb = np.ascontiguousarray(codebook, dtype=np.int8)
+    out = np.zeros((q.shape[0], codes.shape[0]), np.float64)
+    load().tq_scores_f64(_p(q), q.shape[0], _p(rot), dim, bits, _p(cb), C.c_float(codebook_scale),
+                         _p(codes), _p(norms), codes.shape[0], _p(out))
+    return out
+
+
+def tq_topk(queries, rotation, dim, bits, codebook, codebook_scale, codes, norms, k):
+    q = _f32(queries).reshape(-1, dim)
+    rot = None if rotation is None else _f32(rotation)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    norms = _f32(norms)
+    cb = np.ascontiguousarray(codebook, dtype=np.int8)
+    n = codes.shape[0]
+    kk = n if (k <= 0 or k > n) else k
+    ids = np.zeros((q.shape[0], kk), np.int64)
+    scores = np.zeros((q.shape[0], kk), np.float32)
+    load().tq_topk(_p(q), q.shape[0], _p(rot), dim, bits, _p(cb), C.c_float(codebook_scale),
+                   _p(codes), _p(norms), n, int(k), _p(ids), _p(scores))
+    return ids, scores
+
+
+def topk_scores(scores: np.ndarray, k: int):
+    s = _f32(scores)
+    n = s.shape[0]
+    kk = n if (k <= 0 or k > n) else k
+    ids = np.zeros(kk, np.int64)
+    out = np.zeros(kk, np.float32)
+    load().topk_scores(_p(s), n, int(k), _p(ids), _p(out))
+    return ids, out

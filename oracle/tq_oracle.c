@@ -1,0 +1,265 @@
+/*
+ * TEST INFRASTRUCTURE ONLY -- the CPU oracle for TurboQuant scoring.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load this; the product path never does.
+ *
+ * Restates, in plain C:
+ *  - topTurboQuantRetrievalScoresWithStats / ...Exhaustive
+ *    (runtime/retrieval_turboquant.go:1853-1908): per query, score every
+ *    document, keep a size-k heap ordered by retrievalScoreBetter
+ *    (runtime/retrieval_eval.go:1153-1187: score desc, then id asc), then the
+ *    insertion sort slicesSortRetrievalScores (retrieval_turboquant.go:1910-1916);
+ *    k <= 0 or k > n means n (:1854-1856);
+ *  - the build-defined PrepareQuery / InnerProductPrepared arithmetic of the
+ *    scan (the reference's is inside m31labs.dev/turboquant v0.2.1, not vendored):
+ *      q' = R q (f64, fma in k order), Qs = rint(q' * (qmax / max|q'|)),
+ *      D = sum_j Qs_j C[code_j] (exact int32),
+ *      score = ((float)D * alpha) * norm + 0.0f, alpha = (float)((max|q'|/qmax) * s_c);
+ *  - the f64 float estimator norm * <R q, s_c C[code]> the integer path
+ *    approximates (checked within the stated tolerance, not bit-exact).
+ * Built with -ffp-contract=off so that no multiply-add is fused implicitly.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define QMAX_LIMIT (127 * 256 + 127)
+
+static inline unsigned code_at(const uint8_t* row, int j, int bits) {
+  const int bit = j * bits;
+  return (row[bit >> 3] >> (bit & 7)) & ((1u << bits) - 1u);
+}
+
+int tq_qmax(const int8_t* cb, int levels, int d) {
+  int cmax = 0;
+  for (int v = 0; v < levels; ++v) {
+    const int a = abs((int)cb[v]);
+    if (a > cmax) cmax = a;
+  }
+  if (cmax == 0) return QMAX_LIMIT;
+  long long lim = 2147483647LL / ((long long)cmax * d) - 128;
+  return (int)(lim < QMAX_LIMIT ? lim : QMAX_LIMIT);
+}
+
+/* rot: d x d row-major R (NULL = identity). */
+void tq_prepare(const float* q, const float* rot, int d, int qmax, float cb_scale, int16_t* qs,
+                float* alpha) {
+  double* qr = (double*)malloc(sizeof(double) * (size_t)d);
+  double maxabs = 0.0;
+  for (int j = 0; j < d; ++j) {
+    double acc = 0.0;
+    if (rot != NULL) {
+      for (int k = 0; k < d; ++k) acc = fma((double)rot[(size_t)j * d + k], (double)q[k], acc);
+    } else {
+      acc = (double)q[j];
+    }
+    qr[j] = acc;
+    if (fabs(acc) > maxabs) maxabs = fabs(acc);
+  }
+  const double inv = maxabs > 0.0 ? (double)qmax / maxabs : 0.0;
+  for (int j = 0; j < d; ++j) {
+    double v = rint(qr[j] * inv);
+    if (v > qmax) v = qmax;
+    if (v < -qmax) v = -qmax;
+    qs[j] = (int16_t)v;
+  }
+  *alpha = maxabs > 0.0 ? (float)((maxabs / (double)qmax) * (double)cb_scale) : 0.0f;
+  free(qr);
+}
+
+static inline float tq_score(int32_t dot, float alpha, float norm) {
+  const float a = (float)dot * alpha;
+  const float s = a * norm;
+  return s + 0.0f;
+}
+
+/* Exact integer dots of one prepared query against n vectors. */
+void tq_dots(const int16_t* qs, int d, const uint8_t* codes, int64_t n, int bits,
+             const int8_t* cb, int32_t* out) {
+  const int row_bytes = (d * bits + 7) / 8;
+  for (int64_t i = 0; i < n; ++i) {
+    const uint8_t* row = codes + (size_t)i * row_bytes;
+    int64_t acc = 0;
+    for (int j = 0; j < d; ++j) acc += (int64_t)qs[j] * cb[code_at(row, j, bits)];
+    out[i] = (int32_t)acc;
+  }
+}
+
+/* Scores of nq raw queries against vectors [begin, begin+count). */
+void tq_scores(const float* queries, int nq, const float* rot, int d, int bits, const int8_t* cb,
+               float cb_scale, const uint8_t* codes, const float* norms, int64_t begin,
+               int64_t count, int32_t* dots_out, float* scores_out) {
+  const int qmax = tq_qmax(cb, 1 << bits, d);
+  const int row_bytes = (d * bits + 7) / 8;
+  int16_t* qs = (int16_t*)malloc(sizeof(int16_t) * (size_t)d);
+  int32_t* dots = (int32_t*)malloc(sizeof(int32_t) * (size_t)(count > 0 ? count : 1));
+  for (int q = 0; q < nq; ++q) {
+    float alpha;
+    tq_prepare(queries + (size_t)q * d, rot, d, qmax, cb_scale, qs, &alpha);
+    tq_dots(qs, d, codes + (size_t)begin * row_bytes, count, bits, cb, dots);
+    for (int64_t i = 0; i < count; ++i) {
+      if (dots_out) dots_out[(size_t)q * count + i] = dots[i];
+      if (scores_out) scores_out[(size_t)q * count + i] = tq_score(dots[i], alpha, norms[begin + i]);
+    }
+  }
+  free(qs);
+  free(dots);
+}
+
+/* f64 float estimator norm * sum_j (R q)_j * s_c * C[code_j] (no query rounding). */
+void tq_scores_f64(const float* queries, int nq, const float* rot, int d, int bits,
+                   const int8_t* cb, float cb_scale, const uint8_t* codes, const float* norms,
+                   int64_t n, double* out) {
+  const int row_bytes = (d * bits + 7) / 8;
+  double* qr = (double*)malloc(sizeof(double) * (size_t)d);
+  for (int q = 0; q < nq; ++q) {
+    const float* x = queries + (size_t)q * d;
+    for (int j = 0; j < d; ++j) {
+      double acc = 0.0;
+      if (rot) {
+        for (int k = 0; k < d; ++k) acc += (double)rot[(size_t)j * d + k] * (double)x[k];
+      } else {
+        acc = x[j];
+      }
+      qr[j] = acc;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+      const uint8_t* row = codes + (size_t)i * row_bytes;
+      double acc = 0.0;
+      for (int j = 0; j < d; ++j) acc += qr[j] * (double)cb_scale * (double)cb[code_at(row, j, bits)];
+      out[(size_t)q * n + i] = (double)norms[i] * acc;
+    }
+  }
+  free(qr);
+}
+
+/* ---------------------------------------------------------------- heap */
+
+typedef struct {
+  int64_t id;
+  float score;
+} scored_t;
+
+/* retrievalScoreBetter (runtime/retrieval_eval.go:1153-1161) on integer ids. */
+static inline int better(scored_t a, scored_t b) {
+  if (a.score > b.score) return 1;
+  if (a.score < b.score) return 0;
+  return a.id < b.id;
+}
+
+/* Min-heap on "better": the root is the worst kept element (retrieval_eval.go:1163-1187). */
+static void sift_down(scored_t* h, int n, int i) {
+  for (;;) {
+    int w = i;
+    const int l = 2 * i + 1, r = l + 1;
+    if (l < n && better(h[w], h[l])) w = l;
+    if (r < n && better(h[w], h[r])) w = r;
+    if (w == i) return;
+    scored_t t = h[i];
+    h[i] = h[w];
+    h[w] = t;
+    i = w;
+  }
+}
+
+static void sift_up(scored_t* h, int i) {
+  while (i > 0) {
+    const int p = (i - 1) / 2;
+    if (!better(h[p], h[i])) return;
+    scored_t t = h[i];
+    h[i] = h[p];
+    h[p] = t;
+    i = p;
+  }
+}
+
+static void heap_offer(scored_t* h, int* len, int k, scored_t s) {
+  if (*len < k) {
+    h[*len] = s;
+    sift_up(h, *len);
+    *len += 1;
+    return;
+  }
+  if (better(s, h[0])) {
+    h[0] = s;
+    sift_down(h, k, 0);
+  }
+}
+
+/* slicesSortRetrievalScores (retrieval_turboquant.go:1910-1916). */
+static void insertion_sort(scored_t* s, int n) {
+  for (int i = 1; i < n; ++i)
+    for (int j = i; j > 0 && better(s[j], s[j - 1]); --j) {
+      scored_t t = s[j];
+      s[j] = s[j - 1];
+      s[j - 1] = t;
+    }
+}
+
+/* Per query: prepare, score every document through a per-query byte lookup
+ * table (exact: same int32 dots as tq_dots), heap top-k, sort.
+ * ids/scores are [nq][kk] with kk = (k <= 0 || k > n) ? n : k; returns kk. */
+int64_t tq_topk(const float* queries, int nq, const float* rot, int d, int bits, const int8_t* cb,
+                float cb_scale, const uint8_t* codes, const float* norms, int64_t n, int k,
+                int64_t* ids, float* scores) {
+  const int64_t kk = (k <= 0 || (int64_t)k > n) ? n : k;
+  if (kk == 0) return 0;
+  const int qmax = tq_qmax(cb, 1 << bits, d);
+  const int row_bytes = (d * bits + 7) / 8;
+  const int per = 8 / bits;
+  int16_t* qs = (int16_t*)malloc(sizeof(int16_t) * (size_t)d);
+  int32_t* lut = (int32_t*)malloc(sizeof(int32_t) * (size_t)row_bytes * 256);
+  scored_t* heap = (scored_t*)malloc(sizeof(scored_t) * (size_t)kk);
+  for (int q = 0; q < nq; ++q) {
+    float alpha;
+    tq_prepare(queries + (size_t)q * d, rot, d, qmax, cb_scale, qs, &alpha);
+    for (int b = 0; b < row_bytes; ++b) {
+      for (int byte = 0; byte < 256; ++byte) {
+        int32_t acc = 0;
+        for (int e = 0; e < per; ++e) {
+          const int j = b * per + e;
+          if (j < d) acc += (int32_t)qs[j] * cb[(byte >> (e * bits)) & ((1 << bits) - 1)];
+        }
+        lut[(size_t)b * 256 + byte] = acc;
+      }
+    }
+    int len = 0;
+    for (int64_t i = 0; i < n; ++i) {
+      const uint8_t* row = codes + (size_t)i * row_bytes;
+      int32_t dot = 0;
+      for (int b = 0; b < row_bytes; ++b) dot += lut[(size_t)b * 256 + row[b]];
+      scored_t s = {i, tq_score(dot, alpha, norms[i])};
+      heap_offer(heap, &len, (int)kk, s);
+    }
+    insertion_sort(heap, len);
+    for (int64_t i = 0; i < kk; ++i) {
+      ids[(size_t)q * kk + i] = heap[i].id;
+      scores[(size_t)q * kk + i] = heap[i].score;
+    }
+  }
+  free(qs);
+  free(lut);
+  free(heap);
+  return kk;
+}
+
+/* Reference top-k over an arbitrary score array (exhaustive heap + sort), used
+ * to pin the selection itself on hand-built ties. */
+int64_t topk_scores(const float* s, int64_t n, int k, int64_t* ids, float* out) {
+  const int64_t kk = (k <= 0 || (int64_t)k > n) ? n : k;
+  if (kk == 0) return 0;
+  scored_t* heap = (scored_t*)malloc(sizeof(scored_t) * (size_t)kk);
+  int len = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    scored_t e = {i, s[i]};
+    heap_offer(heap, &len, (int)kk, e);
+  }
+  insertion_sort(heap, len);
+  for (int64_t i = 0; i < kk; ++i) {
+    ids[i] = heap[i].id;
+    out[i] = heap[i].score;
+  }
+  free(heap);
+  return kk;
+}

@@ -1,0 +1,181 @@
+"""GPU parity of the TurboQuant scan (libeoship on gfx950) against the CPU oracle.
+
+Bar: prepared queries, integer code dot products, scores and top-k ids are
+bit-exact against oracle/tq_oracle.c on the same seeded inputs; at the
+BASELINE size (1M x 384, 4-bit, 64 queries, k = 100) the filtered top-k must
+equal the exhaustive device scores sorted by (score desc, id asc), and the
+exhaustive scores must equal the oracle's on a sampled subset."""
+import numpy as np
+import pytest
+
+import oracle
+from eos_amd import datagen
+from eos_amd.turboquant import TurboQuantIndex, top_turboquant_retrieval_scores_with_stats
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(name):
+    print(f"[case] {name}", flush=True)
+
+
+def _corpus(n, d, bits, seed=21, rotation=True):
+    return datagen.TurboQuantCorpus(n, d, bits, seed, seed + 1, seed + 2, rotation=rotation)
+
+
+def _index(rt, c, norms=None, codes=None):
+    return TurboQuantIndex(rt, c.codes if codes is None else codes,
+                           c.norms if norms is None else norms, c.dim, c.bits, c.codebook,
+                           c.codebook_scale, c.rotation)
+
+
+def _oracle_scores(c, q, norms=None, codes=None, begin=0, count=None):
+    return oracle.tq_scores(q, c.rotation, c.dim, c.bits, c.codebook, c.codebook_scale,
+                            c.codes if codes is None else codes,
+                            c.norms if norms is None else norms, begin, count)
+
+
+def test_prepare_bit_exact(rt):
+    _case("prepare d=384 Q=70")
+    c = _corpus(64, 384, 4)
+    q = datagen.baseline_queries(70, 384, 7)
+    idx = _index(rt, c)
+    qs, alpha = idx.prepare_query(q)
+    for i in range(70):
+        oqs, oal = oracle.tq_prepare(q[i], c.rotation, c.codebook, c.codebook_scale)
+        np.testing.assert_array_equal(qs[i], oqs)
+        assert alpha[i] == oal
+
+
+@pytest.mark.parametrize("bits,d,n,nq", [(4, 384, 1000, 64), (4, 384, 517, 33), (2, 128, 1000, 64),
+                                         (4, 64, 300, 1), (4, 100, 333, 40), (2, 40, 95, 70),
+                                         (4, 768, 200, 16), (2, 1024, 100, 5)])
+def test_scores_and_dots_bit_exact(rt, bits, d, n, nq):
+    _case(f"scores bits={bits} d={d} n={n} Q={nq}")
+    c = _corpus(n, d, bits, seed=d + bits)
+    q = datagen.baseline_queries(nq, d, 8)
+    idx = _index(rt, c)
+    dots, sc = idx.inner_product_prepared(q)
+    odots, osc = _oracle_scores(c, q)
+    np.testing.assert_array_equal(dots, odots)
+    np.testing.assert_array_equal(sc, osc)
+    # an unaligned slice
+    b, cnt = n // 3 + 1, n // 2
+    dots2, sc2 = idx.inner_product_prepared(q, b, cnt)
+    np.testing.assert_array_equal(dots2, odots[:, b:b + cnt])
+    np.testing.assert_array_equal(sc2, osc[:, b:b + cnt])
+
+
+@pytest.mark.parametrize("n", [1000, 8192, 8193, 20000, 100000])
+@pytest.mark.parametrize("bits,d", [(4, 384), (2, 128)])
+def test_topk_matches_oracle(rt, n, bits, d):
+    _case(f"topk n={n} bits={bits} d={d}")
+    c = _corpus(n, d, bits, seed=n % 97 + bits)
+    q = datagen.baseline_queries(64, d, 9)
+    idx = _index(rt, c)
+    for k in (1, 7, 100, 255):
+        ids, sc, stats = idx.top_k(q, k)
+        oids, osc = oracle.tq_topk(q, c.rotation, d, bits, c.codebook, c.codebook_scale, c.codes,
+                                   c.norms, k)
+        np.testing.assert_array_equal(ids, oids)
+        np.testing.assert_array_equal(sc, osc)
+        assert stats.candidate_count == 64 * n
+
+
+def test_topk_multiple_batches(rt):
+    _case("topk Q=130 n=30000")
+    c = _corpus(30000, 384, 4, seed=5)
+    q = datagen.baseline_queries(130, 384, 10)
+    idx = _index(rt, c)
+    ids, sc, stats = idx.top_k(q, 50)
+    oids, osc = oracle.tq_topk(q, c.rotation, 384, 4, c.codebook, c.codebook_scale, c.codes,
+                               c.norms, 50)
+    np.testing.assert_array_equal(ids, oids)
+    np.testing.assert_array_equal(sc, osc)
+    assert stats.batches == 3
+
+
+def test_topk_all_ties_uses_exact_fallback(rt):
+    """Every vector scores the same: the filter overflows, the exhaustive path
+    must return ids 0..k-1 (ties to the lower id)."""
+    _case("topk all ties n=20000")
+    c = _corpus(20000, 384, 4, seed=6)
+    codes = np.full_like(c.codes, 0x55)
+    norms = np.ones(20000, np.float32)
+    q = datagen.baseline_queries(8, 384, 11)
+    idx = _index(rt, c, norms=norms, codes=codes)
+    ids, sc, stats = idx.top_k(q, 100)
+    np.testing.assert_array_equal(ids, np.tile(np.arange(100), (8, 1)))
+    oids, osc = oracle.tq_topk(q, c.rotation, 384, 4, c.codebook, c.codebook_scale, codes, norms, 100)
+    np.testing.assert_array_equal(ids, oids)
+    np.testing.assert_array_equal(sc, osc)
+    assert stats.fallback_queries == 8
+
+
+def test_topk_zero_norms_zero_query_and_k_semantics(rt):
+    _case("topk edge cases")
+    c = _corpus(500, 384, 4, seed=7)
+    norms = c.norms.copy()
+    norms[::3] = 0.0
+    idx = _index(rt, c, norms=norms)
+    q = datagen.baseline_queries(3, 384, 12)
+    q[1] = 0.0
+    for k in (0, -5, 500, 10_000, 1):
+        ids, sc, _ = idx.top_k(q, k)
+        oids, osc = oracle.tq_topk(q, c.rotation, 384, 4, c.codebook, c.codebook_scale, c.codes,
+                                   norms, k)
+        assert ids.shape == oids.shape
+        np.testing.assert_array_equal(ids, oids)
+        np.testing.assert_array_equal(sc, osc)
+    ids, sc, _ = idx.top_k(q[1:2], 10)
+    np.testing.assert_array_equal(ids[0], np.arange(10))
+    assert np.all(sc == 0.0) and not np.any(np.signbit(sc))
+
+
+def test_reference_tie_case(rt):
+    """runtime/turboquant_retrieval_pruning_test.go:80-99 with integer ids."""
+    _case("reference tie case")
+    c = _corpus(2, 32, 4, seed=8)
+    idx = _index(rt, c, norms=np.zeros(2, np.float32))
+    q = np.zeros((1, 32), np.float32)
+    q[0, 0] = 1.0
+    docs, _ = top_turboquant_retrieval_scores_with_stats(idx, q, 1)
+    assert len(docs[0]) == 1 and docs[0][0].id == 0 and docs[0][0].score == 0.0
+
+
+def test_bind_rejects_bad_norms(rt):
+    _case("bind validation")
+    from eos_amd._lib import EosHipError
+    c = _corpus(10, 32, 4, seed=9)
+    bad = c.norms.copy()
+    bad[4] = -1.0
+    with pytest.raises(EosHipError, match="Norm"):
+        _index(rt, c, norms=bad)
+    bad[4] = np.nan
+    with pytest.raises(EosHipError, match="Norm"):
+        _index(rt, c, norms=bad)
+
+
+def test_baseline_c2_full_size(rt):
+    """BASELINE config 2 at full size: 1M x 384 4-bit, 64 queries, k = 100."""
+    _case("c2 full size 1M x 384")
+    c = datagen.baseline_flat_corpus()
+    q = datagen.baseline_queries(64, 384)
+    idx = _index(rt, c)
+    ids, sc, stats = idx.top_k(q, 100)
+    assert stats.fallback_queries == 0
+    dots, dense = idx.inner_product_prepared(q)
+    for i in range(64):
+        order = np.argsort(-dense[i], kind="stable")[:100]
+        np.testing.assert_array_equal(ids[i], order)
+        np.testing.assert_array_equal(sc[i], dense[i][order])
+    rng = np.random.default_rng(0)
+    sub = np.sort(rng.choice(c.n, 2048, replace=False))
+    odots, osc = oracle.tq_scores(q, c.rotation, 384, 4, c.codebook, c.codebook_scale,
+                                  c.codes[sub], c.norms[sub])
+    np.testing.assert_array_equal(dots[:, sub], odots)
+    np.testing.assert_array_equal(dense[:, sub], osc)
+    oids, osc2 = oracle.tq_topk(q[:2], c.rotation, 384, 4, c.codebook, c.codebook_scale, c.codes,
+                                c.norms, 100)
+    np.testing.assert_array_equal(ids[:2], oids)
+    np.testing.assert_array_equal(sc[:2], osc2)
