@@ -103,17 +103,21 @@ def main() -> int:
     rt.profile_reset()
     rt.profile(True)
     log(f"timing {args.steps} steps")
-    fallbacks = 0
     rt.mark(0)
     for _ in range(args.steps):
-        st = idx.top_k_device(dq, args.queries, args.k, dids, dsc)
-        fallbacks += st.fallback_queries
+        idx.top_k_device(dq, args.queries, args.k, dids, dsc, with_stats=False)
     rt.mark(1)
     total_ms = rt.elapsed_ms(0, 1)
     rt.sync()
     n_filter, ms_filter = rt.profile_read("tq_scan_filter")
-    n_sample, ms_sample = rt.profile_read("tq_scan_sample")
+    breakdown = {}
+    for name in ("eos_tq_prepare", "tq_scan_sample", "eos_tq_threshold", "tq_scan_filter",
+                 "eos_tq_finalize", "tq_scan_dense", "tq_fallback_select"):
+        breakdown[name] = rt.profile_read(name)[1] / args.steps
     rt.profile(False)
+    st = idx.top_k_device(dq, args.queries, args.k, dids, dsc, with_stats=True)
+    fallbacks = st.fallback_queries
+    kept = st.candidates_kept
     ms_per_step = total_ms / args.steps
     value = args.queries * corpus.n / (ms_per_step / 1e3)
     bytes_per_launch = corpus.n * (corpus.dim * corpus.bits // 8 + 4)
@@ -146,9 +150,9 @@ def main() -> int:
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel": "tq_scan_filter", "avg_launch_ms": avg_filter_ms,
                      "bytes_per_launch": bytes_per_launch},
-        "breakdown_ms_per_step": {"tq_scan_filter": ms_filter / args.steps,
-                                  "tq_scan_sample": ms_sample / args.steps},
+        "breakdown_ms_per_step": breakdown,
         "fallback_queries": fallbacks,
+        "candidates_kept_per_query": kept / args.queries,
         "device": info,
     }
     if not args.no_cpu_baseline:

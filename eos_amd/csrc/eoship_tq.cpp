@@ -29,7 +29,8 @@ namespace {
 constexpr int kBatch = 64;          // queries per scan (two 32-column groups)
 constexpr int kCap = 8192;          // kept candidates per query
 constexpr int kSortCap = 8192;      // largest k the device sort handles
-constexpr int kSampleStride = 32;   // sample every 32nd tile
+constexpr int kSampleStride = 32;   // sample every 32nd tile (at least)
+constexpr int kMaxSampleTiles = 1024;  // the threshold kernel holds <= 32768 samples
 constexpr int kTile = 32;
 constexpr int kQmaxLimit = 127 * 256 + 127;  // largest int16 with int8 hi/lo halves
 const int kSupportedKs[] = {1, 2, 4, 8, 12, 16, 24, 32};
@@ -170,7 +171,7 @@ struct EosHipTQ {
     static const char* const labels[3] = {"tq_scan_dense", "tq_scan_filter", "tq_scan_sample"};
     const int nqg = nqg_for(qb);
     char name[64];
-    snprintf(name, sizeof(name), "eos_tq_scan_b%d_k%d_g%d", bits, ks, nqg);
+    snprintf(name, sizeof(name), "eos_tq_scan_b%d_k%d_g%d_%c", bits, ks, nqg, s->mode == 1 ? 'f' : 'w');
     const int waves = 4;
     int64_t blocks = (s->ntiles + waves - 1) / waves;
     const int64_t maxb = (int64_t)rt->compute_units * 2;
@@ -221,13 +222,18 @@ struct EosHipTQ {
     return launch_scan(&s, qb, err);
   }
 
+  // Enqueues one batch on the runtime stream; no host synchronisation unless
+  // stats are requested. The exact fallback is launched unconditionally and
+  // gated on the device by the finalize status, so results are exact without a
+  // host round trip.
   int topk_batch(const float* d_queries, int qb, int kk, int64_t* d_ids, float* d_scores,
                  EosHipTQStats* st, char** err) {
     if (prepare(d_queries, qb, nullptr, err) != 0) return 1;
     if (n > kCap) {
-      const int64_t ns = (ntiles + kSampleStride - 1) / kSampleStride;
+      const int64_t stride = std::max<int64_t>(kSampleStride, (ntiles + kMaxSampleTiles - 1) / kMaxSampleTiles);
+      const int64_t ns = (ntiles + stride - 1) / stride;
       int64_t nsv = 0;
-      for (int64_t j = 0; j < ns; ++j) nsv += std::min<int64_t>(kTile, n - j * kSampleStride * kTile);
+      for (int64_t j = 0; j < ns; ++j) nsv += std::min<int64_t>(kTile, n - j * stride * kTile);
       const double target = std::min<double>(8.0 * kk, kCap / 4.0);
       int64_t r = (int64_t)std::ceil(target * (double)nsv / (double)n);
       r = std::max<int64_t>(1, std::min<int64_t>(r, nsv));
@@ -237,7 +243,7 @@ struct EosHipTQ {
       s.out_scores = samp;
       s.out_stride = ns * kTile;
       s.tile_begin = 0;
-      s.tile_step = kSampleStride;
+      s.tile_step = stride;
       s.ntiles = (int)ns;
       if (launch_scan(&s, qb, err) != 0) return 1;
       TqSelectArgs sel;
@@ -247,9 +253,8 @@ struct EosHipTQ {
       sel.n = ns * kTile;
       sel.stride = ns * kTile;
       sel.kk = (int)r;
-      sel.mode = 0;
       sel.nrows = qb;
-      if (rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err) != 0) return 1;
+      if (rt->launch("eos_tq_threshold", dim3(qb), dim3(1024), 0, &sel, err) != 0) return 1;
     }
     TqScanArgs s;
     scan_base(&s, qb);
@@ -267,37 +272,44 @@ struct EosHipTQ {
     f.cap = kCap;
     f.kk = kk;
     f.q = qb;
-    if (rt->launch("eos_tq_finalize", dim3(qb), dim3(1024), 0, &f, err) != 0) return 1;
-    int hstatus[kBatch];
-    uint32_t hcount[kBatch];
-    hipError_t e = hipMemcpyAsync(hstatus, status, sizeof(int) * qb, hipMemcpyDeviceToHost, rt->stream);
-    if (e == hipSuccess)
-      e = hipMemcpyAsync(hcount, cand_count, sizeof(uint32_t) * qb, hipMemcpyDeviceToHost, rt->stream);
-    if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
-    if (rt->sync(err) != 0) return 1;
-    int flagged = 0;
-    for (int i = 0; i < qb; ++i) {
-      if (hstatus[i] != 0) ++flagged;
-      if (st) st->candidates_kept += std::min<uint32_t>(hcount[i], (uint32_t)kCap);
-    }
-    if (flagged > 0) {
-      if (dense_scores(qb, 0, n, false, err) != 0) return 1;
-      TqSelectArgs sel;
-      memset(&sel, 0, sizeof(sel));
-      sel.rows = dense;
-      sel.status = status;
-      sel.ids = reinterpret_cast<long long*>(d_ids);
-      sel.scores = d_scores;
-      sel.n = n;
-      sel.stride = n;
-      sel.kk = kk;
-      sel.mode = 1;
-      sel.nrows = qb;
-      if (rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err) != 0) return 1;
-      if (rt->sync(err) != 0) return 1;
-    }
+    if (rt->launch("eos_tq_finalize", dim3(qb), dim3(256), 0, &f, err) != 0) return 1;
+    // Exact fallback, gated on status: exhaustive scores + radix selection.
+    TqScanArgs ds;
+    scan_base(&ds, qb);
+    ds.mode = 0;
+    ds.gate = status;
+    ds.out_scores = dense;
+    ds.out_begin = 0;
+    ds.out_count = n;
+    ds.out_stride = n;
+    ds.tile_begin = 0;
+    ds.ntiles = (int)ntiles;
+    if (launch_scan(&ds, qb, err) != 0) return 1;
+    TqSelectArgs sel;
+    memset(&sel, 0, sizeof(sel));
+    sel.rows = dense;
+    sel.status = status;
+    sel.ids = reinterpret_cast<long long*>(d_ids);
+    sel.scores = d_scores;
+    sel.n = n;
+    sel.stride = n;
+    sel.kk = kk;
+    sel.mode = 1;
+    sel.nrows = qb;
+    if (rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err, "tq_fallback_select") != 0)
+      return 1;
     if (st) {
-      st->fallback_queries += flagged;
+      int hstatus[kBatch];
+      uint32_t hcount[kBatch];
+      hipError_t e = hipMemcpyAsync(hstatus, status, sizeof(int) * qb, hipMemcpyDeviceToHost, rt->stream);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(hcount, cand_count, sizeof(uint32_t) * qb, hipMemcpyDeviceToHost, rt->stream);
+      if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
+      if (rt->sync(err) != 0) return 1;
+      for (int i = 0; i < qb; ++i) {
+        if (hstatus[i] != 0) st->fallback_queries += 1;
+        st->candidates_kept += std::min<uint32_t>(hcount[i], (uint32_t)kCap);
+      }
       st->candidate_count += (int64_t)qb * n;
       st->batches += 1;
     }
@@ -436,7 +448,7 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
     }
   }
   const size_t bfrag_bytes = (size_t)tq->ks * 4 * 64 * 16;
-  tq->samp_tiles = (tq->ntiles + kSampleStride - 1) / kSampleStride;
+  tq->samp_tiles = std::min<int64_t>((tq->ntiles + kSampleStride - 1) / kSampleStride, kMaxSampleTiles);
   if (rt->alloc(bfrag_bytes, reinterpret_cast<void**>(&tq->bfrag), err) != 0 ||
       rt->alloc(kBatch * sizeof(float), reinterpret_cast<void**>(&tq->alpha), err) != 0 ||
       rt->alloc(kBatch * sizeof(float), reinterpret_cast<void**>(&tq->tau), err) != 0 ||
@@ -471,6 +483,9 @@ static int topk_device_impl(EosHipRuntime* rt, EosHipTQ* tq, const float* d_quer
                    (long long)kk64, kSortCap);
   const int kk = (int)kk64;
   const int cap = tq->batch_cap();
+  if (tq->ensure(reinterpret_cast<void**>(&tq->dense), &tq->dense_bytes,
+                 (size_t)std::min(cap, (int)q) * (size_t)tq->n * sizeof(float), err) != 0)
+    return 1;
   for (int q0 = 0; q0 < q; q0 += cap) {
     const int qb = std::min(cap, q - q0);
     if (tq->topk_batch(d_queries + (size_t)q0 * tq->d, qb, kk, d_ids + (size_t)q0 * kk,

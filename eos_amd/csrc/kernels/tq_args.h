@@ -36,6 +36,7 @@ struct TqScanArgs {
   uint32_t* cand_count;    // [32*nqg]
   float* out_scores;       // dense/sample output [q][out_stride]
   int32_t* out_dots;       // dense output (optional)
+  const int* gate;         // non-NULL: run only if some gate[i] != 0, i < q
   long long n;             // valid vectors
   long long out_begin;     // dense: vector index of column 0
   long long out_count;     // dense: columns

@@ -68,7 +68,15 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_prepare(TqPrepArgs a) {
     double acc = 0.0;
     if (j < a.d) {
       if (a.rot_t != nullptr) {
-        for (int k = 0; k < a.d; ++k) acc = fma((double)a.rot_t[(size_t)k * a.d + j], sq[k], acc);
+        for (int k0 = 0; k0 < a.d; k0 += 16) {
+          float rv[16];
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            rv[u] = (k0 + u < a.d) ? a.rot_t[(size_t)(k0 + u) * a.d + j] : 0.0f;
+#pragma unroll
+          for (int u = 0; u < 16; ++u)
+            if (k0 + u < a.d) acc = fma((double)rv[u], sq[k0 + u], acc);
+        }
       } else {
         acc = sq[j];
       }
@@ -192,12 +200,20 @@ EOS_DEV v4i decode_step<2>(const v4i& raw, int h, const TqScanArgs& a) {
   return f;
 }
 
-template <int BITS, int KS, int NQG>
+// FILTER = true: keep (score >= tau) rank keys (mode 1). FILTER = false: write
+// every score (mode 0 dense slice, mode 2 sampled tiles).
+template <int BITS, int KS, int NQG, bool FILTER>
 EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   constexpr int NCB = 2 * NQG;
   constexpr int SPL = 8 / BITS;
   constexpr int NLOAD = (KS + SPL - 1) / SPL;
   __shared__ v4i sb[KS * NCB * 64];
+  if (a.gate != nullptr) {
+    // Exhaustive pass of the exact fallback: run only when a query was flagged.
+    bool any = false;
+    for (int i = 0; i < a.q; ++i) any |= a.gate[i] != 0;
+    if (!any) return;
+  }
   {
     const v4i* src = reinterpret_cast<const v4i*>(a.bfrag);
     for (int i = threadIdx.x; i < KS * NCB * 64; i += kScanThreads) sb[i] = src[i];
@@ -207,12 +223,39 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   const int wave = threadIdx.x >> 6;
   const int nw = gridDim.x * (kScanThreads / 64);
   const int half = lane >> 5;
-  for (int j = blockIdx.x * (kScanThreads / 64) + wave; j < a.ntiles; j += nw) {
+  const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
+  // Software pipeline: the codes and norms of the wave's next tile are in
+  // flight while the current tile is decoded, multiplied and filtered.
+  int j = blockIdx.x * (kScanThreads / 64) + wave;
+  v4i raw[NLOAD];
+  float4 nrm4[4];
+  if (j < a.ntiles) {
     const long long tile = a.tile_begin + (long long)j * a.tile_step;
-    const v4i* src = reinterpret_cast<const v4i*>(a.packed) + (size_t)tile * NLOAD * 64 + lane;
-    v4i raw[NLOAD];
+    const v4i* src = packed + (size_t)tile * NLOAD * 64 + lane;
 #pragma unroll
     for (int c = 0; c < NLOAD; ++c) raw[c] = __builtin_nontemporal_load(src + c * 64);
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4)
+      nrm4[i4] = *reinterpret_cast<const float4*>(a.norms + tile * kTile + 8 * i4 + 4 * half);
+  }
+  for (; j < a.ntiles; j += nw) {
+    const long long tile = a.tile_begin + (long long)j * a.tile_step;
+    v4i nraw[NLOAD];
+    float4 nnrm4[4];
+    const int jn = j + nw;
+    if (jn < a.ntiles) {
+      const long long ntile = a.tile_begin + (long long)jn * a.tile_step;
+      const v4i* src = packed + (size_t)ntile * NLOAD * 64 + lane;
+#pragma unroll
+      for (int c = 0; c < NLOAD; ++c) nraw[c] = __builtin_nontemporal_load(src + c * 64);
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4)
+        nnrm4[i4] = *reinterpret_cast<const float4*>(a.norms + ntile * kTile + 8 * i4 + 4 * half);
+    }
+    // Opaque per-tile LDS offset: keeps the query fragments in LDS rather than
+    // letting them be hoisted into registers across the tile loop.
+    int boff = lane;
+    asm volatile("" : "+v"(boff));
     v16i acc[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
@@ -225,7 +268,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
           const v4i af = decode_step<BITS>(raw[c], h, a);
 #pragma unroll
           for (int cb = 0; cb < NCB; ++cb) {
-            const v4i bf = sb[(s * NCB + cb) * 64 + lane];
+            const v4i bf = sb[(s * NCB + cb) * 64 + boff];
             acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, acc[cb], 0, 0, 0);
           }
         }
@@ -237,50 +280,92 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     float nrm[16];
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
-      const float4 n4 = *reinterpret_cast<const float4*>(a.norms + vbase + 8 * i4 + 4 * half);
-      nrm[4 * i4 + 0] = n4.x;
-      nrm[4 * i4 + 1] = n4.y;
-      nrm[4 * i4 + 2] = n4.z;
-      nrm[4 * i4 + 3] = n4.w;
+      nrm[4 * i4 + 0] = nrm4[i4].x;
+      nrm[4 * i4 + 1] = nrm4[i4].y;
+      nrm[4 * i4 + 2] = nrm4[i4].z;
+      nrm[4 * i4 + 3] = nrm4[i4].w;
     }
 #pragma unroll
     for (int g = 0; g < NQG; ++g) {
       const int qi = g * 32 + (lane & 31);
-      if (qi >= a.q) continue;
-      const float al = a.alpha[qi];
-      const float ta = a.mode == 1 ? a.tau[qi] : 0.0f;
+      const bool live = qi < a.q;
+      const float al = live ? a.alpha[qi] : 0.0f;
+      float sc[16];
+      int dots[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int r = 8 * (i >> 2) + 4 * half + (i & 3);
-        const long long v = vbase + r;
-        const int dot = acc[2 * g][i] * 256 + acc[2 * g + 1][i];
-        const float score = ((float)dot * al) * nrm[i] + 0.0f;
-        if (a.mode == 1) {
-          if (v < a.n && score >= ta) {
-            const uint32_t pos = atomicAdd(&a.cand_count[qi], 1u);
-            if ((int)pos < a.cap) a.cand[(size_t)qi * a.cap + pos] = rank_key(score, (uint32_t)v);
+        dots[i] = acc[2 * g][i] * 256 + acc[2 * g + 1][i];
+        sc[i] = ((float)dots[i] * al) * nrm[i] + 0.0f;
+      }
+      // Rows of this tile that are real vectors (the last tile may be partial).
+      const long long rem64 = a.n - vbase;
+      const int rem = rem64 >= kTile ? kTile : (int)rem64;
+      if constexpr (FILTER) {
+        const float ta = live ? a.tau[qi] : __builtin_inff();
+        bool hit = false;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) hit |= sc[i] >= ta;
+        if (hit) {
+          // Rare path: count this lane's kept rows, reserve slots with one
+          // atomic, then write the rank keys.
+          uint32_t cnt = 0;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = 8 * (i >> 2) + 4 * half + (i & 3);
+            cnt += (r < rem && sc[i] >= ta) ? 1u : 0u;
           }
-        } else if (a.mode == 0) {
-          const long long colx = v - a.out_begin;
-          if (v < a.n && colx >= 0 && colx < a.out_count) {
-            a.out_scores[(size_t)qi * a.out_stride + colx] = score;
-            if (a.out_dots != nullptr) a.out_dots[(size_t)qi * a.out_stride + colx] = dot;
+          uint32_t pos = cnt ? atomicAdd(&a.cand_count[qi], cnt) : 0u;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = 8 * (i >> 2) + 4 * half + (i & 3);
+            if (r < rem && sc[i] >= ta) {
+              if ((int)pos < a.cap)
+                a.cand[(size_t)qi * a.cap + pos] = rank_key(sc[i], (uint32_t)(vbase + r));
+              ++pos;
+            }
+          }
+        }
+      } else if (live) {
+        if (a.mode == 0) {
+          float* orow = a.out_scores + (size_t)qi * a.out_stride;
+          int32_t* drow = a.out_dots != nullptr ? a.out_dots + (size_t)qi * a.out_stride : nullptr;
+          const long long c0 = vbase - a.out_begin;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = 8 * (i >> 2) + 4 * half + (i & 3);
+            const long long colx = c0 + r;
+            if (r < rem && colx >= 0 && colx < a.out_count) {
+              orow[colx] = sc[i];
+              if (drow != nullptr) drow[colx] = dots[i];
+            }
           }
         } else {
-          const long long colx = (long long)j * kTile + r;
-          a.out_scores[(size_t)qi * a.out_stride + colx] = v < a.n ? score : -__builtin_inff();
+          float* orow = a.out_scores + (size_t)qi * a.out_stride + (size_t)j * kTile;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = 8 * (i >> 2) + 4 * half + (i & 3);
+            orow[r] = r < rem ? sc[i] : -__builtin_inff();
+          }
         }
       }
     }
+#pragma unroll
+    for (int c = 0; c < NLOAD; ++c) raw[c] = nraw[c];
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) nrm4[i4] = nnrm4[i4];
   }
 }
 
 }  // namespace
 
 #define EOS_TQ_SCAN(BITS, KS, NQG)                                                        \
-  extern "C" __global__ __launch_bounds__(kScanThreads) void eos_tq_scan_b##BITS##_k##KS##_g##NQG( \
-      TqScanArgs a) {                                                                     \
-    tq_scan_body<BITS, KS, NQG>(a);                                                       \
+  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) \
+  void eos_tq_scan_b##BITS##_k##KS##_g##NQG##_f(TqScanArgs a) {                           \
+    tq_scan_body<BITS, KS, NQG, true>(a);                                                 \
+  }                                                                                       \
+  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) \
+  void eos_tq_scan_b##BITS##_k##KS##_g##NQG##_w(TqScanArgs a) {                           \
+    tq_scan_body<BITS, KS, NQG, false>(a);                                                \
   }
 
 #define EOS_TQ_SCAN_KS(BITS, NQG) \
@@ -407,35 +492,118 @@ extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_row_select(TqSe
   }
 }
 
+// --------------------------------------------------------------- threshold
+
+namespace {
+
+constexpr int kThrThreads = 1024;
+constexpr int kThrPer = 32;            // sample scores held per thread
+constexpr int kFinThreads = 256;
+constexpr int kFinPer = kSortCap / kFinThreads;
+
+// Block-wide sum of per-wave counts (each wave passes a uniform value).
+template <int NT>
+EOS_DEV uint32_t block_sum(uint32_t wave_count, uint32_t* slots) {
+  if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = wave_count;
+  __syncthreads();
+  uint32_t t = 0;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) t += slots[i];
+  __syncthreads();
+  return t;
+}
+
+}  // namespace
+
+// Per query: tau = the r-th best score of the sampled rows, found by bisection
+// on the order-preserving key with the row held in registers (count of keys
+// >= mid via wave ballots). Any tau <= the true k-th best score is valid; the
+// finalize kernel proves it after the fact. One workgroup per row.
+extern "C" __global__ __launch_bounds__(kThrThreads) void eos_tq_threshold(TqSelectArgs a) {
+  __shared__ uint32_t slots[kThrThreads / 64];
+  const int row = blockIdx.x;
+  if (row >= a.nrows) return;
+  const int tid = threadIdx.x;
+  if ((long long)a.kk > a.n || a.kk <= 0 || a.n > (long long)kThrThreads * kThrPer) {
+    if (tid == 0) a.tau[row] = -__builtin_inff();
+    return;
+  }
+  const float* x = a.rows + (size_t)row * a.stride;
+  uint32_t key[kThrPer];
+#pragma unroll
+  for (int v = 0; v < kThrPer; ++v) {
+    const long long i = tid + (long long)v * kThrThreads;
+    key[v] = i < a.n ? score_key(x[i]) : 0u;
+  }
+  uint32_t lo = 0u, hi = 0xffffffffu;
+  while (lo < hi) {
+    const uint32_t mid = lo + ((hi - lo) >> 1) + 1u;
+    uint32_t c = 0;
+#pragma unroll
+    for (int v = 0; v < kThrPer; ++v) c += (uint32_t)__popcll(__ballot(key[v] >= mid));
+    if (block_sum<kThrThreads>(c, slots) >= (uint32_t)a.kk) lo = mid;
+    else hi = mid - 1u;
+  }
+  if (tid == 0) a.tau[row] = key_score(lo);
+}
+
 // --------------------------------------------------------------- finalize
 
-
-// Sorts each query's filtered candidates (score desc, id asc) and emits the
-// first kk. A query whose candidate set cannot be proven to hold its top-kk is
-// flagged for the exhaustive path.
-extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_finalize(TqFinalizeArgs a) {
-  __shared__ u64 list[kSortCap];
+// Orders each query's kept candidates (score desc, id asc) and emits the first
+// kk: bisection on the 64-bit rank key finds the kk-th best (rank keys are
+// unique, so exactly kk candidates are >= it), then each selected candidate's
+// output slot is its count of better selected candidates. A query whose kept
+// set is smaller than kk or overflowed is flagged (status 1 / 2) for the
+// exhaustive path; status 0 means its output row is final.
+extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFinalizeArgs a) {
+  __shared__ uint32_t slots[kFinThreads / 64];
+  __shared__ u64 sel[kSortCap];
+  __shared__ uint32_t sel_n;
   const int row = blockIdx.x;
   if (row >= a.q) return;
+  const int tid = threadIdx.x;
   const uint32_t cnt = a.cand_count[row];
   if (cnt > (uint32_t)a.cap || cnt > (uint32_t)kSortCap) {
-    if (threadIdx.x == 0) a.status[row] = 2;
+    if (tid == 0) a.status[row] = 2;
     return;
   }
   if (cnt < (uint32_t)a.kk) {
-    if (threadIdx.x == 0) a.status[row] = 1;
+    if (tid == 0) a.status[row] = 1;
     return;
   }
-  int npow = 1;
-  while (npow < (int)cnt) npow <<= 1;
-  for (int i = threadIdx.x; i < npow; i += blockDim.x)
-    list[i] = i < (int)cnt ? a.cand[(size_t)row * a.cap + i] : 0ull;
-  __syncthreads();
-  bitonic_sort_desc(list, npow);
-  for (int i = threadIdx.x; i < a.kk; i += blockDim.x) {
-    const u64 c = list[i];
-    a.ids[(size_t)row * a.kk + i] = (long long)rank_id(c);
-    a.scores[(size_t)row * a.kk + i] = key_score((uint32_t)(c >> 32));
+  const int nv = (int)((cnt + kFinThreads - 1) / kFinThreads);
+  u64 c[kFinPer];
+#pragma unroll
+  for (int v = 0; v < kFinPer; ++v) {
+    const uint32_t i = tid + v * kFinThreads;
+    c[v] = (v < nv && i < cnt) ? a.cand[(size_t)row * a.cap + i] : 0ull;
   }
-  if (threadIdx.x == 0) a.status[row] = 0;
+  u64 lo = 0ull, hi = ~0ull;
+  while (lo < hi) {
+    const u64 mid = lo + ((hi - lo) >> 1) + 1ull;
+    uint32_t n = 0;
+#pragma unroll
+    for (int v = 0; v < kFinPer; ++v)
+      if (v < nv) n += (uint32_t)__popcll(__ballot(c[v] >= mid));
+    if (block_sum<kFinThreads>(n, slots) >= (uint32_t)a.kk) lo = mid;
+    else hi = mid - 1ull;
+  }
+  if (tid == 0) sel_n = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < kFinPer; ++v) {
+    if (v < nv && c[v] >= lo && c[v] != 0ull) {
+      const uint32_t pos = atomicAdd(&sel_n, 1u);
+      if (pos < (uint32_t)kSortCap) sel[pos] = c[v];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < a.kk; i += kFinThreads) {
+    const u64 x = sel[i];
+    int rank = 0;
+    for (int j = 0; j < a.kk; ++j) rank += sel[j] > x ? 1 : 0;
+    a.ids[(size_t)row * a.kk + rank] = (long long)rank_id(x);
+    a.scores[(size_t)row * a.kk + rank] = key_score((uint32_t)(x >> 32));
+  }
+  if (tid == 0) a.status[row] = 0;
 }

@@ -117,10 +117,13 @@ class TurboQuantIndex:
         return ids, scores, stats
 
     def top_k_device(self, d_queries: DeviceBuffer, nq: int, top_k: int, d_ids: DeviceBuffer,
-                     d_scores: DeviceBuffer) -> _lib.EosHipTQStats:
-        st = _lib.EosHipTQStats()
+                     d_scores: DeviceBuffer, with_stats: bool = True):
+        """Enqueue a top-k on device buffers. Without stats the call does not
+        wait for the device; results are complete after Runtime.sync()."""
+        st = _lib.EosHipTQStats() if with_stats else None
         _lib.call("eoship_tq_topk_device", self.rt.handle, self.handle, d_queries.ptr,
-                  C.c_int32(nq), C.c_int32(int(top_k)), d_ids.ptr, d_scores.ptr, C.byref(st))
+                  C.c_int32(nq), C.c_int32(int(top_k)), d_ids.ptr, d_scores.ptr,
+                  C.byref(st) if st is not None else None)
         return st
 
     def inner_product_prepared(self, queries: np.ndarray, begin: int = 0, count: int | None = None):
