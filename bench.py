@@ -111,7 +111,8 @@ def main() -> int:
     rt.sync()
     n_filter, ms_filter = rt.profile_read("tq_scan_filter")
     breakdown = {}
-    for name in ("eos_tq_prepare", "tq_scan_sample", "eos_tq_threshold", "tq_scan_filter",
+    for name in ("eos_tq_rotate", "eos_tq_quantize", "tq_scan_sample", "eos_tq_threshold",
+                 "tq_scan_filter",
                  "eos_tq_finalize", "tq_scan_dense", "tq_fallback_select"):
         breakdown[name] = rt.profile_read(name)[1] / args.steps
     rt.profile(False)

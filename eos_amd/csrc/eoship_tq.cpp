@@ -3,14 +3,17 @@
 // Replaces the host loop topTurboQuantRetrievalScoresWithStats
 // (runtime/retrieval_turboquant.go:1853-1887) and its per-document
 // q.InnerProductPrepared calls with a device pipeline per batch of <= 64
-// queries:
-//   1. eos_tq_prepare   rotate (f64), quantize to int16, split hi/lo fragments
-//   2. sample scan      exact scores of every 32nd tile of 32 vectors
-//   3. eos_tq_row_select  per query, the r-th best sample score -> threshold
+// queries, enqueued on the runtime stream without host synchronisation:
+//   1. eos_tq_rotate / eos_tq_quantize  rotate (f64), round to int16, split
+//                       into int8 hi/lo MFMA fragments (PrepareQuery)
+//   2. sample scan      exact scores of every s-th tile of 32 vectors
+//   3. eos_tq_threshold per query, a score below the r-th best sample
 //   4. filter scan      one pass over the corpus, keep score >= threshold
-//   5. eos_tq_finalize  sort kept candidates (score desc, id asc), emit top-k
-//   6. exact fallback   for any query whose kept set is too small or
-//                       overflowed: exhaustive scores + exact radix select.
+//   5. eos_tq_finalize  select + order the kept candidates (score desc,
+//                       id asc), emit top-k, or flag the query
+//   6. exact fallback   gated on the flags: exhaustive scores + exact radix
+//                       selection for any query whose kept set is too small
+//                       or overflowed.
 // Step 6 makes the result exact whatever the data; steps 2-3 only decide how
 // much work step 4 saves.
 #include <algorithm>
@@ -110,6 +113,7 @@ struct EosHipTQ {
   void* packed = nullptr;
   float* norms = nullptr;
   float* rot_t = nullptr;
+  double* qrot = nullptr;  // [64][d] rotated queries
   // per-batch device scratch
   int8_t* bfrag = nullptr;
   float* alpha = nullptr;
@@ -129,7 +133,7 @@ struct EosHipTQ {
   size_t io_bytes = 0;
 
   void free_all() {
-    void* ptrs[] = {packed, norms, rot_t, bfrag, alpha, tau, cand, cand_count,
+    void* ptrs[] = {packed, norms, rot_t, qrot, bfrag, alpha, tau, cand, cand_count,
                     status, samp, dense, dense_dots, qs_buf, io};
     for (void* p : ptrs)
       if (p) hipFree(p);
@@ -197,7 +201,13 @@ struct EosHipTQ {
     p.ncb = 2 * nqg;
     p.qmax = qmax;
     p.cb_scale = cb_scale;
-    return rt->launch("eos_tq_prepare", dim3(32 * nqg), dim3(256), 0, &p, err);
+    p.qrot = qrot;
+    if (rot_t != nullptr) {
+      const unsigned jblocks = (unsigned)((d + 63) / 64);
+      const unsigned qblocks = (unsigned)((qb + 3) / 4);
+      if (rt->launch("eos_tq_rotate", dim3(jblocks, qblocks), dim3(256), 0, &p, err) != 0) return 1;
+    }
+    return rt->launch("eos_tq_quantize", dim3(32 * nqg), dim3(256), 0, &p, err);
   }
 
   // Exhaustive scores of all queries of the batch into dense [qb][count].
@@ -450,6 +460,7 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
   const size_t bfrag_bytes = (size_t)tq->ks * 4 * 64 * 16;
   tq->samp_tiles = std::min<int64_t>((tq->ntiles + kSampleStride - 1) / kSampleStride, kMaxSampleTiles);
   if (rt->alloc(bfrag_bytes, reinterpret_cast<void**>(&tq->bfrag), err) != 0 ||
+      rt->alloc((size_t)kBatch * tq->d * sizeof(double), reinterpret_cast<void**>(&tq->qrot), err) != 0 ||
       rt->alloc(kBatch * sizeof(float), reinterpret_cast<void**>(&tq->alpha), err) != 0 ||
       rt->alloc(kBatch * sizeof(float), reinterpret_cast<void**>(&tq->tau), err) != 0 ||
       rt->alloc(kBatch * sizeof(uint32_t), reinterpret_cast<void**>(&tq->cand_count), err) != 0 ||

@@ -49,40 +49,68 @@ EOS_DEV uint32_t rank_id(u64 c) { return ~(uint32_t)(c & 0xffffffffu); }
 
 // ------------------------------------------------------------------ prepare
 
+namespace {
+constexpr int kRotJ = 64;    // rotated coordinates per workgroup
+constexpr int kRotQ = 4;     // queries per workgroup
+constexpr int kRotK = 128;   // rotation rows staged per LDS chunk
+constexpr int kMaxDim = 1024;
+}  // namespace
 
-// One workgroup per query column (padded to a multiple of 32 queries).
-extern "C" __global__ __launch_bounds__(256) void eos_tq_prepare(TqPrepArgs a) {
-  __shared__ double sq[2048];
+// q'[q][j] = sum_k R[j][k] q[k] in f64: one fma chain per (q, j), k ascending.
+// Workgroup (x, y) computes j in [64x, 64x + 64) for queries [4y, 4y + 4);
+// R^T streams through LDS 128 rows of k at a time (all loads of a chunk are
+// issued before any is consumed).
+extern "C" __global__ __launch_bounds__(256) void eos_tq_rotate(TqPrepArgs a) {
+  __shared__ float rs[kRotK * kRotJ];
+  __shared__ double qsh[kRotQ * kMaxDim];
+  const int tid = threadIdx.x;
+  const int j0 = blockIdx.x * kRotJ, q0 = blockIdx.y * kRotQ;
+  const int jj = tid & 63, ql = tid >> 6;
+  for (int i = tid; i < kRotQ * a.d; i += 256) {
+    const int qq = i / a.d, k = i - qq * a.d;
+    const int qi = q0 + qq;
+    qsh[qq * kMaxDim + k] = qi < a.q ? (double)a.queries[(size_t)qi * a.d + k] : 0.0;
+  }
+  double acc = 0.0;
+  for (int k0 = 0; k0 < a.d; k0 += kRotK) {
+    const int kn = min(kRotK, a.d - k0);
+    float tmp[kRotK * kRotJ / 256];
+#pragma unroll
+    for (int r = 0; r < kRotK * kRotJ / 256; ++r) {
+      const int i = tid + 256 * r;
+      const int kk = i >> 6, jc = i & 63;
+      tmp[r] = (kk < kn && j0 + jc < a.d) ? a.rot_t[(size_t)(k0 + kk) * a.d + j0 + jc] : 0.0f;
+    }
+    __syncthreads();  // previous chunk consumed; qsh visible
+#pragma unroll
+    for (int r = 0; r < kRotK * kRotJ / 256; ++r) rs[tid + 256 * r] = tmp[r];
+    __syncthreads();
+    for (int kk = 0; kk < kn; ++kk)
+      acc = fma((double)rs[kk * kRotJ + jj], qsh[ql * kMaxDim + k0 + kk], acc);
+  }
+  const int j = j0 + jj, qi = q0 + ql;
+  if (j < a.d && qi < a.q) a.qrot[(size_t)qi * a.d + j] = acc;
+}
+
+// One workgroup per query column (padded to a multiple of 32 queries):
+// max |q'|, int16 rounding, hi/lo fragments, alpha; resets the query's
+// threshold and candidate count for the scan that follows.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) {
   __shared__ double red[256];
   const int qi = blockIdx.x;
   const int tid = threadIdx.x;
   const bool live = qi < a.q;
   const int dpad = a.ks * 32;
-  for (int j = tid; j < a.d; j += 256) sq[j] = live ? (double)a.queries[(size_t)qi * a.d + j] : 0.0;
-  __syncthreads();
-  double qr[8];
+  double qr[kMaxDim / 256];
   double mx = 0.0;
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
+  for (int r = 0; r < kMaxDim / 256; ++r) {
     const int j = tid + 256 * r;
-    double acc = 0.0;
-    if (j < a.d) {
-      if (a.rot_t != nullptr) {
-        for (int k0 = 0; k0 < a.d; k0 += 16) {
-          float rv[16];
-#pragma unroll
-          for (int u = 0; u < 16; ++u)
-            rv[u] = (k0 + u < a.d) ? a.rot_t[(size_t)(k0 + u) * a.d + j] : 0.0f;
-#pragma unroll
-          for (int u = 0; u < 16; ++u)
-            if (k0 + u < a.d) acc = fma((double)rv[u], sq[k0 + u], acc);
-        }
-      } else {
-        acc = sq[j];
-      }
-    }
-    qr[r] = acc;
-    mx = fmax(mx, fabs(acc));
+    double v = 0.0;
+    if (live && j < a.d)
+      v = a.rot_t != nullptr ? a.qrot[(size_t)qi * a.d + j] : (double)a.queries[(size_t)qi * a.d + j];
+    qr[r] = v;
+    mx = fmax(mx, fabs(v));
   }
   red[tid] = mx;
   __syncthreads();
@@ -95,7 +123,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_prepare(TqPrepArgs a) {
   const int cb_hi = 2 * (qi >> 5);
   const int col = qi & 31;
 #pragma unroll
-  for (int r = 0; r < 8; ++r) {
+  for (int r = 0; r < kMaxDim / 256; ++r) {
     const int j = tid + 256 * r;
     if (j >= dpad) continue;
     int qs = 0;
@@ -200,6 +228,24 @@ EOS_DEV v4i decode_step<2>(const v4i& raw, int h, const TqScanArgs& a) {
   return f;
 }
 
+// Per-workgroup candidate stage of the filter scan: kept rank keys are
+// appended with LDS atomics and flushed to the global list once per query at
+// the end, so the scan never waits on a global atomic.
+constexpr int kLdsSlots = 16;
+
+template <int NLOAD>
+EOS_DEV void load_tile_codes(v4i (&r)[NLOAD], const v4i* packed, long long tile, int lane) {
+  const v4i* src = packed + (size_t)tile * NLOAD * 64 + lane;
+#pragma unroll
+  for (int c = 0; c < NLOAD; ++c) r[c] = __builtin_nontemporal_load(src + c * 64);
+}
+
+EOS_DEV void load_tile_norms(float4 (&n)[4], const float* norms, long long tile, int half) {
+#pragma unroll
+  for (int i4 = 0; i4 < 4; ++i4)
+    n[i4] = *reinterpret_cast<const float4*>(norms + tile * kTile + 8 * i4 + 4 * half);
+}
+
 // FILTER = true: keep (score >= tau) rank keys (mode 1). FILTER = false: write
 // every score (mode 0 dense slice, mode 2 sampled tiles).
 template <int BITS, int KS, int NQG, bool FILTER>
@@ -207,7 +253,10 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   constexpr int NCB = 2 * NQG;
   constexpr int SPL = 8 / BITS;
   constexpr int NLOAD = (KS + SPL - 1) / SPL;
+  constexpr int NQ = 32 * NQG;
   __shared__ v4i sb[KS * NCB * 64];
+  __shared__ uint32_t lc_cnt[FILTER ? NQ : 1];
+  __shared__ u64 lc_buf[FILTER ? NQ * kLdsSlots : 1];
   if (a.gate != nullptr) {
     // Exhaustive pass of the exact fallback: run only when a query was flagged.
     bool any = false;
@@ -217,6 +266,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   {
     const v4i* src = reinterpret_cast<const v4i*>(a.bfrag);
     for (int i = threadIdx.x; i < KS * NCB * 64; i += kScanThreads) sb[i] = src[i];
+    if (FILTER && threadIdx.x < NQ) lc_cnt[threadIdx.x] = 0u;
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
@@ -224,34 +274,25 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   const int nw = gridDim.x * (kScanThreads / 64);
   const int half = lane >> 5;
   const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
-  // Software pipeline: the codes and norms of the wave's next tile are in
-  // flight while the current tile is decoded, multiplied and filtered.
+  // Software pipeline: codes are in flight two tiles ahead and norms one tile
+  // ahead of the tile being decoded, multiplied and filtered.
   int j = blockIdx.x * (kScanThreads / 64) + wave;
-  v4i raw[NLOAD];
-  float4 nrm4[4];
+  v4i raw0[NLOAD], raw1[NLOAD];
+  float4 nrm0[4];
   if (j < a.ntiles) {
-    const long long tile = a.tile_begin + (long long)j * a.tile_step;
-    const v4i* src = packed + (size_t)tile * NLOAD * 64 + lane;
-#pragma unroll
-    for (int c = 0; c < NLOAD; ++c) raw[c] = __builtin_nontemporal_load(src + c * 64);
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4)
-      nrm4[i4] = *reinterpret_cast<const float4*>(a.norms + tile * kTile + 8 * i4 + 4 * half);
+    const long long t0 = a.tile_begin + (long long)j * a.tile_step;
+    load_tile_codes<NLOAD>(raw0, packed, t0, lane);
+    load_tile_norms(nrm0, a.norms, t0, half);
   }
+  if (j + nw < a.ntiles) load_tile_codes<NLOAD>(raw1, packed, a.tile_begin + (long long)(j + nw) * a.tile_step, lane);
   for (; j < a.ntiles; j += nw) {
     const long long tile = a.tile_begin + (long long)j * a.tile_step;
-    v4i nraw[NLOAD];
-    float4 nnrm4[4];
-    const int jn = j + nw;
-    if (jn < a.ntiles) {
-      const long long ntile = a.tile_begin + (long long)jn * a.tile_step;
-      const v4i* src = packed + (size_t)ntile * NLOAD * 64 + lane;
-#pragma unroll
-      for (int c = 0; c < NLOAD; ++c) nraw[c] = __builtin_nontemporal_load(src + c * 64);
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4)
-        nnrm4[i4] = *reinterpret_cast<const float4*>(a.norms + ntile * kTile + 8 * i4 + 4 * half);
-    }
+    v4i raw2[NLOAD];
+    float4 nrm1[4];
+    if (j + 2 * nw < a.ntiles)
+      load_tile_codes<NLOAD>(raw2, packed, a.tile_begin + (long long)(j + 2 * nw) * a.tile_step, lane);
+    if (j + nw < a.ntiles)
+      load_tile_norms(nrm1, a.norms, a.tile_begin + (long long)(j + nw) * a.tile_step, half);
     // Opaque per-tile LDS offset: keeps the query fragments in LDS rather than
     // letting them be hoisted into registers across the tile loop.
     int boff = lane;
@@ -265,7 +306,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
       for (int h = 0; h < SPL; ++h) {
         const int s = c * SPL + h;
         if (s < KS) {
-          const v4i af = decode_step<BITS>(raw[c], h, a);
+          const v4i af = decode_step<BITS>(raw0[c], h, a);
 #pragma unroll
           for (int cb = 0; cb < NCB; ++cb) {
             const v4i bf = sb[(s * NCB + cb) * 64 + boff];
@@ -280,11 +321,14 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     float nrm[16];
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
-      nrm[4 * i4 + 0] = nrm4[i4].x;
-      nrm[4 * i4 + 1] = nrm4[i4].y;
-      nrm[4 * i4 + 2] = nrm4[i4].z;
-      nrm[4 * i4 + 3] = nrm4[i4].w;
+      nrm[4 * i4 + 0] = nrm0[i4].x;
+      nrm[4 * i4 + 1] = nrm0[i4].y;
+      nrm[4 * i4 + 2] = nrm0[i4].z;
+      nrm[4 * i4 + 3] = nrm0[i4].w;
     }
+    // Rows of this tile that are real vectors (the last tile may be partial).
+    const long long rem64 = a.n - vbase;
+    const int rem = rem64 >= kTile ? kTile : (int)rem64;
 #pragma unroll
     for (int g = 0; g < NQG; ++g) {
       const int qi = g * 32 + (lane & 31);
@@ -297,30 +341,32 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
         dots[i] = acc[2 * g][i] * 256 + acc[2 * g + 1][i];
         sc[i] = ((float)dots[i] * al) * nrm[i] + 0.0f;
       }
-      // Rows of this tile that are real vectors (the last tile may be partial).
-      const long long rem64 = a.n - vbase;
-      const int rem = rem64 >= kTile ? kTile : (int)rem64;
       if constexpr (FILTER) {
         const float ta = live ? a.tau[qi] : __builtin_inff();
         bool hit = false;
 #pragma unroll
         for (int i = 0; i < 16; ++i) hit |= sc[i] >= ta;
         if (hit) {
-          // Rare path: count this lane's kept rows, reserve slots with one
-          // atomic, then write the rank keys.
+          // Rare path: count this lane's kept rows, reserve LDS slots with one
+          // LDS atomic; keys past the stage's capacity go to the global list.
           uint32_t cnt = 0;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int r = 8 * (i >> 2) + 4 * half + (i & 3);
             cnt += (r < rem && sc[i] >= ta) ? 1u : 0u;
           }
-          uint32_t pos = cnt ? atomicAdd(&a.cand_count[qi], cnt) : 0u;
+          uint32_t pos = atomicAdd(&lc_cnt[qi], cnt);
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int r = 8 * (i >> 2) + 4 * half + (i & 3);
             if (r < rem && sc[i] >= ta) {
-              if ((int)pos < a.cap)
-                a.cand[(size_t)qi * a.cap + pos] = rank_key(sc[i], (uint32_t)(vbase + r));
+              const u64 key = rank_key(sc[i], (uint32_t)(vbase + r));
+              if (pos < (uint32_t)kLdsSlots) {
+                lc_buf[qi * kLdsSlots + pos] = key;
+              } else {
+                const uint32_t gpos = atomicAdd(&a.cand_count[qi], 1u);
+                if ((int)gpos < a.cap) a.cand[(size_t)qi * a.cap + gpos] = key;
+              }
               ++pos;
             }
           }
@@ -350,9 +396,25 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
       }
     }
 #pragma unroll
-    for (int c = 0; c < NLOAD; ++c) raw[c] = nraw[c];
+    for (int c = 0; c < NLOAD; ++c) {
+      raw0[c] = raw1[c];
+      raw1[c] = raw2[c];
+    }
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) nrm4[i4] = nnrm4[i4];
+    for (int i4 = 0; i4 < 4; ++i4) nrm0[i4] = nrm1[i4];
+  }
+  if constexpr (FILTER) {
+    // Flush the stage: one global atomic per query per workgroup.
+    __syncthreads();
+    if (threadIdx.x < NQ && threadIdx.x < a.q) {
+      const int qi = threadIdx.x;
+      const uint32_t nk = lc_cnt[qi] < (uint32_t)kLdsSlots ? lc_cnt[qi] : (uint32_t)kLdsSlots;
+      if (nk > 0) {
+        const uint32_t base = atomicAdd(&a.cand_count[qi], nk);
+        for (uint32_t i = 0; i < nk; ++i)
+          if ((int)(base + i) < a.cap) a.cand[(size_t)qi * a.cap + base + i] = lc_buf[qi * kLdsSlots + i];
+      }
+    }
   }
 }
 
@@ -513,14 +575,38 @@ EOS_DEV uint32_t block_sum(uint32_t wave_count, uint32_t* slots) {
   return t;
 }
 
+// Block-wide min and max of per-thread values.
+template <int NT>
+EOS_DEV void block_minmax(uint32_t& vmin, uint32_t& vmax, uint32_t* smin, uint32_t* smax) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    vmin = min(vmin, (uint32_t)__shfl_xor((int)vmin, o));
+    vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, o));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    smin[threadIdx.x >> 6] = vmin;
+    smax[threadIdx.x >> 6] = vmax;
+  }
+  __syncthreads();
+  vmin = 0xffffffffu;
+  vmax = 0u;
+#pragma unroll
+  for (int i = 0; i < NT / 64; ++i) {
+    vmin = min(vmin, smin[i]);
+    vmax = max(vmax, smax[i]);
+  }
+  __syncthreads();
+}
+
 }  // namespace
 
-// Per query: tau = the r-th best score of the sampled rows, found by bisection
-// on the order-preserving key with the row held in registers (count of keys
-// >= mid via wave ballots). Any tau <= the true k-th best score is valid; the
-// finalize kernel proves it after the fact. One workgroup per row.
+// Per query: tau = the lower edge of the 16-bit key bucket that holds the
+// r-th best sampled score (bisection over bucket prefixes, the row held in
+// registers, counts by wave ballots). Any tau <= the true k-th best score is
+// valid; the finalize kernel proves it after the fact. One workgroup per row.
 extern "C" __global__ __launch_bounds__(kThrThreads) void eos_tq_threshold(TqSelectArgs a) {
   __shared__ uint32_t slots[kThrThreads / 64];
+  __shared__ uint32_t smin[kThrThreads / 64], smax[kThrThreads / 64];
   const int row = blockIdx.x;
   if (row >= a.nrows) return;
   const int tid = threadIdx.x;
@@ -530,33 +616,46 @@ extern "C" __global__ __launch_bounds__(kThrThreads) void eos_tq_threshold(TqSel
   }
   const float* x = a.rows + (size_t)row * a.stride;
   uint32_t key[kThrPer];
+  uint32_t pmin = 0xffffu, pmax = 0u;
 #pragma unroll
   for (int v = 0; v < kThrPer; ++v) {
     const long long i = tid + (long long)v * kThrThreads;
     key[v] = i < a.n ? score_key(x[i]) : 0u;
+    if (i < a.n) {
+      pmin = min(pmin, key[v] >> 16);
+      pmax = max(pmax, key[v] >> 16);
+    }
   }
-  uint32_t lo = 0u, hi = 0xffffffffu;
+  block_minmax<kThrThreads>(pmin, pmax, smin, smax);
+  uint32_t lo = pmin, hi = pmax;
   while (lo < hi) {
-    const uint32_t mid = lo + ((hi - lo) >> 1) + 1u;
+    const uint32_t mid = lo + ((hi - lo + 1u) >> 1);
+    const uint32_t t = mid << 16;
     uint32_t c = 0;
 #pragma unroll
-    for (int v = 0; v < kThrPer; ++v) c += (uint32_t)__popcll(__ballot(key[v] >= mid));
+    for (int v = 0; v < kThrPer; ++v) c += (uint32_t)__popcll(__ballot(key[v] >= t));
     if (block_sum<kThrThreads>(c, slots) >= (uint32_t)a.kk) lo = mid;
     else hi = mid - 1u;
   }
-  if (tid == 0) a.tau[row] = key_score(lo);
+  if (tid == 0) {
+    const uint32_t t = lo << 16;
+    a.tau[row] = t < 0x00800000u ? -__builtin_inff() : key_score(t);
+  }
 }
 
 // --------------------------------------------------------------- finalize
 
 // Orders each query's kept candidates (score desc, id asc) and emits the first
-// kk: bisection on the 64-bit rank key finds the kk-th best (rank keys are
-// unique, so exactly kk candidates are >= it), then each selected candidate's
-// output slot is its count of better selected candidates. A query whose kept
-// set is smaller than kk or overflowed is flagged (status 1 / 2) for the
-// exhaustive path; status 0 means its output row is final.
+// kk. Bisection on the 32-bit score key (over the kept range) finds the kk-th
+// best score K; if K is tied across the cut, a second bisection over the tied
+// ids picks the lowest ones. Rank keys are unique, so exactly kk candidates
+// are >= the resulting composite threshold; each one's output slot is its
+// count of better selected candidates. A query whose kept set is smaller than
+// kk or overflowed is flagged (status 1 / 2) for the exhaustive path; status 0
+// means its output row is final.
 extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFinalizeArgs a) {
   __shared__ uint32_t slots[kFinThreads / 64];
+  __shared__ uint32_t smin[kFinThreads / 64], smax[kFinThreads / 64];
   __shared__ u64 sel[kSortCap];
   __shared__ uint32_t sel_n;
   const int row = blockIdx.x;
@@ -573,26 +672,64 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
   }
   const int nv = (int)((cnt + kFinThreads - 1) / kFinThreads);
   u64 c[kFinPer];
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
   for (int v = 0; v < kFinPer; ++v) {
     const uint32_t i = tid + v * kFinThreads;
     c[v] = (v < nv && i < cnt) ? a.cand[(size_t)row * a.cap + i] : 0ull;
+    if (c[v] != 0ull) {
+      kmin = min(kmin, (uint32_t)(c[v] >> 32));
+      kmax = max(kmax, (uint32_t)(c[v] >> 32));
+    }
   }
-  u64 lo = 0ull, hi = ~0ull;
+  block_minmax<kFinThreads>(kmin, kmax, smin, smax);
+  // K = the kk-th best score key.
+  uint32_t lo = kmin, hi = kmax;
   while (lo < hi) {
-    const u64 mid = lo + ((hi - lo) >> 1) + 1ull;
+    const uint32_t mid = lo + ((hi - lo) >> 1) + 1u;
     uint32_t n = 0;
 #pragma unroll
     for (int v = 0; v < kFinPer; ++v)
-      if (v < nv) n += (uint32_t)__popcll(__ballot(c[v] >= mid));
+      if (v < nv) n += (uint32_t)__popcll(__ballot(c[v] != 0ull && (uint32_t)(c[v] >> 32) >= mid));
     if (block_sum<kFinThreads>(n, slots) >= (uint32_t)a.kk) lo = mid;
-    else hi = mid - 1ull;
+    else hi = mid - 1u;
+  }
+  const uint32_t K = lo;
+  uint32_t ng = 0, ne = 0;
+#pragma unroll
+  for (int v = 0; v < kFinPer; ++v) {
+    if (v < nv) {
+      const uint32_t k = (uint32_t)(c[v] >> 32);
+      ng += (uint32_t)__popcll(__ballot(c[v] != 0ull && k > K));
+      ne += (uint32_t)__popcll(__ballot(c[v] != 0ull && k == K));
+    }
+  }
+  ng = block_sum<kFinThreads>(ng, slots);
+  ne = block_sum<kFinThreads>(ne, slots);
+  u64 thr = (u64)K << 32;
+  if (ng + ne > (uint32_t)a.kk) {
+    // Tie at the cut: keep the (kk - ng) tied candidates with the lowest ids,
+    // i.e. the largest low words (~id).
+    const uint32_t need = (uint32_t)a.kk - ng;
+    uint32_t l = 0u, h = 0xffffffffu;
+    while (l < h) {
+      const uint32_t mid = l + ((h - l) >> 1) + 1u;
+      uint32_t n = 0;
+#pragma unroll
+      for (int v = 0; v < kFinPer; ++v)
+        if (v < nv)
+          n += (uint32_t)__popcll(__ballot(c[v] != 0ull && (uint32_t)(c[v] >> 32) == K &&
+                                           (uint32_t)c[v] >= mid));
+      if (block_sum<kFinThreads>(n, slots) >= need) l = mid;
+      else h = mid - 1u;
+    }
+    thr |= l;
   }
   if (tid == 0) sel_n = 0u;
   __syncthreads();
 #pragma unroll
   for (int v = 0; v < kFinPer; ++v) {
-    if (v < nv && c[v] >= lo && c[v] != 0ull) {
+    if (v < nv && c[v] != 0ull && c[v] >= thr) {
       const uint32_t pos = atomicAdd(&sel_n, 1u);
       if (pos < (uint32_t)kSortCap) sel[pos] = c[v];
     }
