@@ -33,7 +33,7 @@ constexpr int kBatch = 64;          // queries per scan (two 32-column groups)
 constexpr int kCap = 8192;          // kept candidates per query
 constexpr int kSortCap = 8192;      // largest k the device sort handles
 constexpr int kSampleStride = 32;   // sample every 32nd tile (at least)
-constexpr int kMaxSampleTiles = 1024;  // the threshold kernel holds <= 32768 samples
+constexpr int kMaxSampleTiles = 1024;  // the threshold kernel holds <= 1024 tile maxima
 constexpr int kTile = 32;
 constexpr int kQmaxLimit = 127 * 256 + 127;  // largest int16 with int8 hi/lo halves
 const int kSupportedKs[] = {1, 2, 4, 8, 12, 16, 24, 32};
@@ -246,12 +246,12 @@ struct EosHipTQ {
       for (int64_t j = 0; j < ns; ++j) nsv += std::min<int64_t>(kTile, n - j * stride * kTile);
       const double target = std::min<double>(8.0 * kk, kCap / 4.0);
       int64_t r = (int64_t)std::ceil(target * (double)nsv / (double)n);
-      r = std::max<int64_t>(1, std::min<int64_t>(r, nsv));
+      r = std::max<int64_t>(1, std::min<int64_t>(r, ns));  // r-th best of ns tile maxima
       TqScanArgs s;
       scan_base(&s, qb);
       s.mode = 2;
       s.out_scores = samp;
-      s.out_stride = ns * kTile;
+      s.out_stride = ns;
       s.tile_begin = 0;
       s.tile_step = stride;
       s.ntiles = (int)ns;
@@ -260,11 +260,11 @@ struct EosHipTQ {
       memset(&sel, 0, sizeof(sel));
       sel.rows = samp;
       sel.tau = tau;
-      sel.n = ns * kTile;
-      sel.stride = ns * kTile;
+      sel.n = ns;
+      sel.stride = ns;
       sel.kk = (int)r;
       sel.nrows = qb;
-      if (rt->launch("eos_tq_threshold", dim3(qb), dim3(1024), 0, &sel, err) != 0) return 1;
+      if (rt->launch("eos_tq_threshold", dim3(qb), dim3(64), 0, &sel, err) != 0) return 1;
     }
     TqScanArgs s;
     scan_base(&s, qb);
@@ -467,7 +467,7 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
       rt->alloc(kBatch * sizeof(int), reinterpret_cast<void**>(&tq->status), err) != 0 ||
       rt->alloc((size_t)kBatch * kCap * sizeof(unsigned long long),
                 reinterpret_cast<void**>(&tq->cand), err) != 0 ||
-      rt->alloc((size_t)kBatch * std::max<int64_t>(tq->samp_tiles, 1) * kTile * sizeof(float),
+      rt->alloc((size_t)kBatch * std::max<int64_t>(tq->samp_tiles, 1) * sizeof(float),
                 reinterpret_cast<void**>(&tq->samp), err) != 0)
     return fail();
   *out = tq;

@@ -85,8 +85,14 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_rotate(TqPrepArgs a) {
 #pragma unroll
     for (int r = 0; r < kRotK * kRotJ / 256; ++r) rs[tid + 256 * r] = tmp[r];
     __syncthreads();
-    for (int kk = 0; kk < kn; ++kk)
-      acc = fma((double)rs[kk * kRotJ + jj], qsh[ql * kMaxDim + k0 + kk], acc);
+    if (kn == kRotK) {
+#pragma unroll 16
+      for (int kk = 0; kk < kRotK; ++kk)
+        acc = fma((double)rs[kk * kRotJ + jj], qsh[ql * kMaxDim + k0 + kk], acc);
+    } else {
+      for (int kk = 0; kk < kn; ++kk)
+        acc = fma((double)rs[kk * kRotJ + jj], qsh[ql * kMaxDim + k0 + kk], acc);
+    }
   }
   const int j = j0 + jj, qi = q0 + ql;
   if (j < a.d && qi < a.q) a.qrot[(size_t)qi * a.d + j] = acc;
@@ -386,12 +392,16 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
             }
           }
         } else {
-          float* orow = a.out_scores + (size_t)qi * a.out_stride + (size_t)j * kTile;
+          // Sample mode: the best score of the tile's real rows for this query
+          // (lanes l and l^32 hold the two halves of the tile's rows).
+          float m = -__builtin_inff();
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int r = 8 * (i >> 2) + 4 * half + (i & 3);
-            orow[r] = r < rem ? sc[i] : -__builtin_inff();
+            if (r < rem) m = fmaxf(m, sc[i]);
           }
+          m = fmaxf(m, __shfl_xor(m, 32));
+          if (half == 0) a.out_scores[(size_t)qi * a.out_stride + j] = m;
         }
       }
     }
@@ -558,31 +568,37 @@ extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_row_select(TqSe
 
 namespace {
 
-constexpr int kThrThreads = 1024;
-constexpr int kThrPer = 32;            // sample scores held per thread
+constexpr int kThrPer = 16;            // tile maxima held per lane (<= 1024 per row)
 constexpr int kFinThreads = 256;
 constexpr int kFinPer = kSortCap / kFinThreads;
 
-// Block-wide sum of per-wave counts (each wave passes a uniform value).
+// Block-wide sum of per-wave counts (each wave passes a uniform value). The
+// two slot sets alternate, so one barrier per call suffices: a set is
+// rewritten only after a later barrier that every reader of it has passed.
 template <int NT>
-EOS_DEV uint32_t block_sum(uint32_t wave_count, uint32_t* slots) {
-  if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = wave_count;
+EOS_DEV uint32_t block_sum(uint32_t wave_count, uint32_t* slots, int& parity) {
+  uint32_t* set = slots + parity * (NT / 64);
+  if ((threadIdx.x & 63) == 0) set[threadIdx.x >> 6] = wave_count;
   __syncthreads();
   uint32_t t = 0;
 #pragma unroll
-  for (int i = 0; i < NT / 64; ++i) t += slots[i];
-  __syncthreads();
+  for (int i = 0; i < NT / 64; ++i) t += set[i];
+  parity ^= 1;
   return t;
 }
 
-// Block-wide min and max of per-thread values.
-template <int NT>
-EOS_DEV void block_minmax(uint32_t& vmin, uint32_t& vmax, uint32_t* smin, uint32_t* smax) {
+EOS_DEV void wave_minmax(uint32_t& vmin, uint32_t& vmax) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     vmin = min(vmin, (uint32_t)__shfl_xor((int)vmin, o));
     vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, o));
   }
+}
+
+// Block-wide min and max of per-thread values.
+template <int NT>
+EOS_DEV void block_minmax(uint32_t& vmin, uint32_t& vmax, uint32_t* smin, uint32_t* smax) {
+  wave_minmax(vmin, vmax);
   if ((threadIdx.x & 63) == 0) {
     smin[threadIdx.x >> 6] = vmin;
     smax[threadIdx.x >> 6] = vmax;
@@ -600,47 +616,42 @@ EOS_DEV void block_minmax(uint32_t& vmin, uint32_t& vmax, uint32_t* smin, uint32
 
 }  // namespace
 
-// Per query: tau = the lower edge of the 16-bit key bucket that holds the
-// r-th best sampled score (bisection over bucket prefixes, the row held in
-// registers, counts by wave ballots). Any tau <= the true k-th best score is
-// valid; the finalize kernel proves it after the fact. One workgroup per row.
-extern "C" __global__ __launch_bounds__(kThrThreads) void eos_tq_threshold(TqSelectArgs a) {
-  __shared__ uint32_t slots[kThrThreads / 64];
-  __shared__ uint32_t smin[kThrThreads / 64], smax[kThrThreads / 64];
+// Per query: tau = the r-th best of the sampled tiles' best scores, by
+// bisection on the order-preserving key (one wavefront per query, the row in
+// registers, counts by ballots; no barriers). The r-th best tile maximum is
+// <= the r-th best sampled score, and any tau <= the true k-th best score is
+// valid: the finalize kernel proves the kept set after the fact.
+extern "C" __global__ __launch_bounds__(64) void eos_tq_threshold(TqSelectArgs a) {
   const int row = blockIdx.x;
   if (row >= a.nrows) return;
-  const int tid = threadIdx.x;
-  if ((long long)a.kk > a.n || a.kk <= 0 || a.n > (long long)kThrThreads * kThrPer) {
-    if (tid == 0) a.tau[row] = -__builtin_inff();
+  const int lane = threadIdx.x;
+  if ((long long)a.kk > a.n || a.kk <= 0 || a.n > 64LL * kThrPer) {
+    if (lane == 0) a.tau[row] = -__builtin_inff();
     return;
   }
   const float* x = a.rows + (size_t)row * a.stride;
   uint32_t key[kThrPer];
-  uint32_t pmin = 0xffffu, pmax = 0u;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
 #pragma unroll
   for (int v = 0; v < kThrPer; ++v) {
-    const long long i = tid + (long long)v * kThrThreads;
+    const long long i = lane + 64LL * v;
     key[v] = i < a.n ? score_key(x[i]) : 0u;
     if (i < a.n) {
-      pmin = min(pmin, key[v] >> 16);
-      pmax = max(pmax, key[v] >> 16);
+      kmin = min(kmin, key[v]);
+      kmax = max(kmax, key[v]);
     }
   }
-  block_minmax<kThrThreads>(pmin, pmax, smin, smax);
-  uint32_t lo = pmin, hi = pmax;
+  wave_minmax(kmin, kmax);
+  uint32_t lo = kmin, hi = kmax;
   while (lo < hi) {
-    const uint32_t mid = lo + ((hi - lo + 1u) >> 1);
-    const uint32_t t = mid << 16;
+    const uint32_t mid = lo + ((hi - lo) >> 1) + 1u;
     uint32_t c = 0;
 #pragma unroll
-    for (int v = 0; v < kThrPer; ++v) c += (uint32_t)__popcll(__ballot(key[v] >= t));
-    if (block_sum<kThrThreads>(c, slots) >= (uint32_t)a.kk) lo = mid;
+    for (int v = 0; v < kThrPer; ++v) c += (uint32_t)__popcll(__ballot(key[v] >= mid));
+    if (c >= (uint32_t)a.kk) lo = mid;
     else hi = mid - 1u;
   }
-  if (tid == 0) {
-    const uint32_t t = lo << 16;
-    a.tau[row] = t < 0x00800000u ? -__builtin_inff() : key_score(t);
-  }
+  if (lane == 0) a.tau[row] = lo < 0x00800000u ? -__builtin_inff() : key_score(lo);
 }
 
 // --------------------------------------------------------------- finalize
@@ -654,7 +665,8 @@ extern "C" __global__ __launch_bounds__(kThrThreads) void eos_tq_threshold(TqSel
 // kk or overflowed is flagged (status 1 / 2) for the exhaustive path; status 0
 // means its output row is final.
 extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFinalizeArgs a) {
-  __shared__ uint32_t slots[kFinThreads / 64];
+  __shared__ uint32_t slots[2 * (kFinThreads / 64)];
+  int parity = 0;
   __shared__ uint32_t smin[kFinThreads / 64], smax[kFinThreads / 64];
   __shared__ u64 sel[kSortCap];
   __shared__ uint32_t sel_n;
@@ -691,7 +703,7 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
 #pragma unroll
     for (int v = 0; v < kFinPer; ++v)
       if (v < nv) n += (uint32_t)__popcll(__ballot(c[v] != 0ull && (uint32_t)(c[v] >> 32) >= mid));
-    if (block_sum<kFinThreads>(n, slots) >= (uint32_t)a.kk) lo = mid;
+    if (block_sum<kFinThreads>(n, slots, parity) >= (uint32_t)a.kk) lo = mid;
     else hi = mid - 1u;
   }
   const uint32_t K = lo;
@@ -704,8 +716,8 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
       ne += (uint32_t)__popcll(__ballot(c[v] != 0ull && k == K));
     }
   }
-  ng = block_sum<kFinThreads>(ng, slots);
-  ne = block_sum<kFinThreads>(ne, slots);
+  ng = block_sum<kFinThreads>(ng, slots, parity);
+  ne = block_sum<kFinThreads>(ne, slots, parity);
   u64 thr = (u64)K << 32;
   if (ng + ne > (uint32_t)a.kk) {
     // Tie at the cut: keep the (kk - ng) tied candidates with the lowest ids,
@@ -720,7 +732,7 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
         if (v < nv)
           n += (uint32_t)__popcll(__ballot(c[v] != 0ull && (uint32_t)(c[v] >> 32) == K &&
                                            (uint32_t)c[v] >= mid));
-      if (block_sum<kFinThreads>(n, slots) >= need) l = mid;
+      if (block_sum<kFinThreads>(n, slots, parity) >= need) l = mid;
       else h = mid - 1u;
     }
     thr |= l;
@@ -738,6 +750,7 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
   for (int i = tid; i < a.kk; i += kFinThreads) {
     const u64 x = sel[i];
     int rank = 0;
+#pragma unroll 8
     for (int j = 0; j < a.kk; ++j) rank += sel[j] > x ? 1 : 0;
     a.ids[(size_t)row * a.kk + rank] = (long long)rank_id(x);
     a.scores[(size_t)row * a.kk + rank] = key_score((uint32_t)(x >> 32));
