@@ -33,6 +33,35 @@ class EosHipTQStats(C.Structure):
     ]
 
 
+class EosHipEncoderDesc(C.Structure):
+    _fields_ = [
+        ("layers", C.c_int32),
+        ("hidden", C.c_int32),
+        ("heads", C.c_int32),
+        ("intermediate", C.c_int32),
+        ("vocab", C.c_int32),
+        ("max_positions", C.c_int32),
+        ("type_vocab", C.c_int32),
+        ("ln_eps", C.c_float),
+        ("gelu", C.c_int32),
+    ]
+
+
+_I8P = C.POINTER(C.c_int8)
+_F32P = C.POINTER(C.c_float)
+
+
+class EosHipEncoderLayer(C.Structure):
+    _fields_ = [
+        ("w_qkv", _I8P), ("s_qkv", _F32P), ("b_qkv", _F32P),
+        ("w_o", _I8P), ("s_o", _F32P), ("b_o", _F32P),
+        ("ln1_gamma", _F32P), ("ln1_beta", _F32P),
+        ("w_1", _I8P), ("s_1", _F32P), ("b_1", _F32P),
+        ("w_2", _I8P), ("s_2", _F32P), ("b_2", _F32P),
+        ("ln2_gamma", _F32P), ("ln2_beta", _F32P),
+    ]
+
+
 # name -> (argtypes) ; every function returns int except where noted
 _SIGNATURES = {
     "eoship_abi_version": ([], C.c_int),
@@ -72,6 +101,15 @@ _SIGNATURES = {
                           C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_tq_prepare": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,
                            C.c_void_p], C.c_int),
+    "eoship_encoder_bind": ([C.c_void_p, C.POINTER(EosHipEncoderDesc), _F32P, _F32P, _F32P, _F32P,
+                             _F32P, C.POINTER(EosHipEncoderLayer), C.POINTER(C.c_void_p),
+                             C.c_void_p], C.c_int),
+    "eoship_encoder_release": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_encoder_forward": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_encoder_forward_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_encoder_status": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_int32), C.c_void_p], C.c_int),
 }
 
 _lib = None

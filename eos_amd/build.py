@@ -28,10 +28,12 @@ ARCH = "gfx950"
 # (code object symbol stem, device source)
 DEVICE_SOURCES = [
     ("tq", os.path.join(CSRC, "kernels", "tq_kernels.hip")),
+    ("enc", os.path.join(CSRC, "kernels", "enc_kernels.hip")),
 ]
 HOST_SOURCES = [
     os.path.join(CSRC, "eoship_runtime.cpp"),
     os.path.join(CSRC, "eoship_tq.cpp"),
+    os.path.join(CSRC, "eoship_encoder.cpp"),
 ]
 
 # Packed-FP32 instructions are disabled for every device build.
@@ -81,7 +83,7 @@ def build(verbose: bool = False) -> str:
     tmp = LIB_PATH + ".tmp"
     _run([
         "g++", "-O2", "-g", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
-        "-Wno-unused-parameter", "-D__HIP_PLATFORM_AMD__",
+        "-Wno-unused-parameter", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
         "-I", os.path.join(REPO_DIR, "include"), "-I", CSRC, "-I", os.path.join(ROCM, "include"),
         *HOST_SOURCES, asm_path,
         "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",

@@ -1,0 +1,324 @@
+// Encoder half of the eoship C ABI: binds a BERT-style q8 encoder and runs its
+// forward pass (the bert_embedder step, runtime/backend/bert_embedder_ops.go:
+// 101-197) on the runtime stream:
+//   eos_enc_pack        active positions -> contiguous rows per sequence
+//   eos_enc_embed       token + position + type, affine LayerNorm
+//   per layer:  eos_enc_gemm (QKV) -> eos_enc_attn_hd* -> eos_enc_gemm_ln_h*
+//               (O + residual + LN) -> eos_enc_gemm (FFN up + GELU) ->
+//               eos_enc_gemm_ln_h* (FFN down + residual + LN)
+//   eos_enc_pool        masked mean pool + L2 normalize
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "eoship_internal.h"
+#include "kernels/enc_args.h"
+
+using eoship::hip_err;
+using eoship::set_err;
+
+namespace {
+
+// IEEE binary16 bits of an int8 code (every value in [-128, 127] is exact).
+uint16_t int8_to_f16_bits(int8_t x) {
+  if (x == 0) return 0;
+  const uint16_t sign = x < 0 ? 0x8000 : 0;
+  unsigned v = (unsigned)(x < 0 ? -(int)x : (int)x);
+  int e = 0;
+  while ((v >> (e + 1)) != 0) ++e;
+  const unsigned mant = (v << (10 - e)) & 0x3ffu;
+  return (uint16_t)(sign | ((unsigned)(e + 15) << 10) | mant);
+}
+
+struct DevLayer {
+  uint16_t* w_qkv = nullptr;
+  float* s_qkv = nullptr;
+  float* b_qkv = nullptr;
+  uint16_t* w_o = nullptr;
+  float* s_o = nullptr;
+  float* b_o = nullptr;
+  float* g1 = nullptr;
+  float* be1 = nullptr;
+  uint16_t* w_1 = nullptr;
+  float* s_1 = nullptr;
+  float* b_1 = nullptr;
+  uint16_t* w_2 = nullptr;
+  float* s_2 = nullptr;
+  float* b_2 = nullptr;
+  float* g2 = nullptr;
+  float* be2 = nullptr;
+};
+
+}  // namespace
+
+struct EosHipEncoder {
+  EosHipRuntime* rt = nullptr;
+  EosHipEncoderDesc desc{};
+  std::vector<void*> owned;
+  float *tok = nullptr, *pos = nullptr, *typ = nullptr, *eg = nullptr, *eb = nullptr;
+  std::vector<DevLayer> layers;
+  // activations, sized for cap_rows = batch * tokens
+  size_t cap_rows = 0;
+  int cap_batch = 0;
+  uint16_t *h = nullptr, *qkv = nullptr, *ctx = nullptr, *mid = nullptr;
+  int32_t *row_b = nullptr, *row_t = nullptr, *seq_off = nullptr, *seq_cnt = nullptr;
+  int32_t *total = nullptr, *status = nullptr;
+  // host-API staging
+  void* io = nullptr;
+  size_t io_bytes = 0;
+
+  ~EosHipEncoder() {
+    for (void* p : owned)
+      if (p) hipFree(p);
+    void* act[] = {h, qkv, ctx, mid, row_b, row_t, seq_off, seq_cnt, total, status, io};
+    for (void* p : act)
+      if (p) hipFree(p);
+  }
+
+  template <typename T>
+  int upload(T** dst, const T* src, size_t count, char** err) {
+    void* p = nullptr;
+    if (rt->alloc(count * sizeof(T), &p, err) != 0) return 1;
+    owned.push_back(p);
+    hipError_t e = hipMemcpy(p, src, count * sizeof(T), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_err(err, "hipMemcpy(encoder weights)", e);
+    *dst = static_cast<T*>(p);
+    return 0;
+  }
+
+  int upload_codes(uint16_t** dst, const int8_t* src, size_t count, char** err) {
+    std::vector<uint16_t> h16(count);
+    for (size_t i = 0; i < count; ++i) h16[i] = int8_to_f16_bits(src[i]);
+    return upload(dst, h16.data(), count, err);
+  }
+
+  int ensure_activations(int batch, int tokens, char** err) {
+    const size_t rows = (size_t)batch * tokens;
+    if (rows <= cap_rows && batch <= cap_batch) return 0;
+    void* act[] = {h, qkv, ctx, mid, row_b, row_t, seq_off, seq_cnt, total, status};
+    for (void* p : act)
+      if (p) hipFree(p);
+    h = qkv = ctx = mid = nullptr;
+    row_b = row_t = seq_off = seq_cnt = total = status = nullptr;
+    cap_rows = 0;
+    cap_batch = 0;
+    const size_t H = desc.hidden, F = desc.intermediate;
+    if (rt->alloc(rows * H * 2, reinterpret_cast<void**>(&h), err) ||
+        rt->alloc(rows * 3 * H * 2, reinterpret_cast<void**>(&qkv), err) ||
+        rt->alloc(rows * H * 2, reinterpret_cast<void**>(&ctx), err) ||
+        rt->alloc(rows * F * 2, reinterpret_cast<void**>(&mid), err) ||
+        rt->alloc(rows * 4, reinterpret_cast<void**>(&row_b), err) ||
+        rt->alloc(rows * 4, reinterpret_cast<void**>(&row_t), err) ||
+        rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_off), err) ||
+        rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_cnt), err) ||
+        rt->alloc(4, reinterpret_cast<void**>(&total), err) ||
+        rt->alloc(4, reinterpret_cast<void**>(&status), err))
+      return 1;
+    cap_rows = rows;
+    cap_batch = batch;
+    return 0;
+  }
+
+  int forward(const int32_t* d_ids, const int32_t* d_types, const int32_t* d_mask, int batch,
+              int tokens, float* d_out, char** err) {
+    if (ensure_activations(batch, tokens, err) != 0) return 1;
+    const int H = desc.hidden, F = desc.intermediate, nh = desc.heads, hd = H / nh;
+    const int max_rows = batch * tokens;
+    hipError_t e = hipMemsetAsync(status, 0, 4, rt->stream);
+    if (e != hipSuccess) return hip_err(err, "hipMemsetAsync(status)", e);
+    EncPackArgs pk{d_mask, row_b, row_t, seq_off, seq_cnt, total, batch, tokens};
+    if (rt->launch("eos_enc_pack", dim3(batch), dim3(256), 0, &pk, err) != 0) return 1;
+    EncEmbedArgs em;
+    memset(&em, 0, sizeof(em));
+    em.ids = d_ids;
+    em.type_ids = d_types;
+    em.row_b = row_b;
+    em.row_t = row_t;
+    em.total = total;
+    em.tok = tok;
+    em.pos = pos;
+    em.typ = typ;
+    em.gamma = eg;
+    em.beta = eb;
+    em.out = h;
+    em.status = status;
+    em.tokens = tokens;
+    em.hidden = H;
+    em.vocab = desc.vocab;
+    em.npos = desc.max_positions;
+    em.ntype = desc.type_vocab;
+    em.eps = desc.ln_eps;
+    if (rt->launch("eos_enc_embed", dim3((max_rows + 3) / 4), dim3(256), 0, &em, err) != 0) return 1;
+    char ln_name[48];
+    snprintf(ln_name, sizeof(ln_name), "eos_enc_gemm_ln_h%d", H);
+    char attn_name[48];
+    snprintf(attn_name, sizeof(attn_name), "eos_enc_attn_hd%d", hd);
+    const unsigned mblocks = (unsigned)((max_rows + 127) / 128);
+    const unsigned lnblocks = (unsigned)((max_rows + 31) / 32);
+    for (const DevLayer& L : layers) {
+      EncGemmArgs g{h, L.w_qkv, L.s_qkv, L.b_qkv, qkv, total, max_rows, 3 * H, H, 0};
+      if (rt->launch("eos_enc_gemm", dim3(3 * H / 128, mblocks), dim3(256), 0, &g, err, "enc_gemm_qkv") != 0)
+        return 1;
+      EncAttnArgs at{qkv, ctx, seq_off, seq_cnt, batch, nh, H, tokens,
+                     (float)(1.4426950408889634 / std::sqrt((double)hd))};
+      if (rt->launch(attn_name, dim3((tokens + 127) / 128, nh, batch), dim3(256), 0, &at, err) != 0)
+        return 1;
+      EncGemmLnArgs o{ctx, L.w_o, L.s_o, L.b_o, h, L.g1, L.be1, h, total, max_rows, H, desc.ln_eps};
+      if (rt->launch(ln_name, dim3(lnblocks), dim3(256), 0, &o, err, "enc_gemm_o_ln") != 0) return 1;
+      EncGemmArgs up{h, L.w_1, L.s_1, L.b_1, mid, total, max_rows, F, H, desc.gelu};
+      if (rt->launch("eos_enc_gemm", dim3(F / 128, mblocks), dim3(256), 0, &up, err, "enc_gemm_ffn_up") != 0)
+        return 1;
+      EncGemmLnArgs dn{mid, L.w_2, L.s_2, L.b_2, h, L.g2, L.be2, h, total, max_rows, F, desc.ln_eps};
+      if (rt->launch(ln_name, dim3(lnblocks), dim3(256), 0, &dn, err, "enc_gemm_ffn_down_ln") != 0)
+        return 1;
+    }
+    EncPoolArgs pl{h, seq_off, seq_cnt, d_out, batch, H};
+    return rt->launch("eos_enc_pool", dim3(batch), dim3(1024), 0, &pl, err);
+  }
+};
+
+extern "C" {
+
+int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const float* tok_emb,
+                        const float* pos_emb, const float* type_emb, const float* emb_ln_gamma,
+                        const float* emb_ln_beta, const EosHipEncoderLayer* layers,
+                        EosHipEncoder** out, char** err) {
+  if (rt == nullptr || desc == nullptr || out == nullptr || tok_emb == nullptr ||
+      pos_emb == nullptr || type_emb == nullptr || emb_ln_gamma == nullptr ||
+      emb_ln_beta == nullptr || (desc->layers > 0 && layers == nullptr))
+    return set_err(err, "eoship_encoder_bind: NULL argument");
+  *out = nullptr;
+  const int H = desc->hidden, F = desc->intermediate;
+  if (H != 384 && H != 512 && H != 768)
+    return set_err(err, "eoship_encoder_bind: hidden must be 384, 512 or 768 (got %d)", H);
+  if (desc->heads <= 0 || H % desc->heads != 0 || (H / desc->heads != 32 && H / desc->heads != 64))
+    return set_err(err, "eoship_encoder_bind: head dim must be 32 or 64 (hidden %d, heads %d)", H,
+                   desc->heads);
+  if (F <= 0 || F % 128 != 0)
+    return set_err(err, "eoship_encoder_bind: intermediate must be a positive multiple of 128");
+  if (desc->layers < 0 || desc->vocab <= 0 || desc->max_positions <= 0 || desc->type_vocab <= 0)
+    return set_err(err, "eoship_encoder_bind: layers/vocab/positions/type_vocab out of range");
+  if (!(desc->ln_eps >= 0.f)) return set_err(err, "eoship_encoder_bind: ln_eps must be >= 0");
+  if (desc->gelu != 1 && desc->gelu != 2)
+    return set_err(err, "eoship_encoder_bind: gelu must be 1 (erf) or 2 (tanh)");
+  auto* enc = new EosHipEncoder();
+  enc->rt = rt;
+  enc->desc = *desc;
+  auto fail = [&]() {
+    delete enc;
+    return 1;
+  };
+  if (enc->upload(&enc->tok, tok_emb, (size_t)desc->vocab * H, err) ||
+      enc->upload(&enc->pos, pos_emb, (size_t)desc->max_positions * H, err) ||
+      enc->upload(&enc->typ, type_emb, (size_t)desc->type_vocab * H, err) ||
+      enc->upload(&enc->eg, emb_ln_gamma, (size_t)H, err) ||
+      enc->upload(&enc->eb, emb_ln_beta, (size_t)H, err))
+    return fail();
+  for (int l = 0; l < desc->layers; ++l) {
+    const EosHipEncoderLayer& s = layers[l];
+    const void* req[] = {s.w_qkv, s.s_qkv, s.b_qkv, s.w_o, s.s_o, s.b_o, s.ln1_gamma, s.ln1_beta,
+                         s.w_1, s.s_1, s.b_1, s.w_2, s.s_2, s.b_2, s.ln2_gamma, s.ln2_beta};
+    for (const void* p : req)
+      if (p == nullptr) {
+        set_err(err, "eoship_encoder_bind: layer %d has a NULL tensor", l);
+        return fail();
+      }
+    DevLayer d;
+    if (enc->upload_codes(&d.w_qkv, s.w_qkv, (size_t)3 * H * H, err) ||
+        enc->upload(&d.s_qkv, s.s_qkv, (size_t)3 * H, err) ||
+        enc->upload(&d.b_qkv, s.b_qkv, (size_t)3 * H, err) ||
+        enc->upload_codes(&d.w_o, s.w_o, (size_t)H * H, err) ||
+        enc->upload(&d.s_o, s.s_o, (size_t)H, err) || enc->upload(&d.b_o, s.b_o, (size_t)H, err) ||
+        enc->upload(&d.g1, s.ln1_gamma, (size_t)H, err) ||
+        enc->upload(&d.be1, s.ln1_beta, (size_t)H, err) ||
+        enc->upload_codes(&d.w_1, s.w_1, (size_t)F * H, err) ||
+        enc->upload(&d.s_1, s.s_1, (size_t)F, err) || enc->upload(&d.b_1, s.b_1, (size_t)F, err) ||
+        enc->upload_codes(&d.w_2, s.w_2, (size_t)H * F, err) ||
+        enc->upload(&d.s_2, s.s_2, (size_t)H, err) || enc->upload(&d.b_2, s.b_2, (size_t)H, err) ||
+        enc->upload(&d.g2, s.ln2_gamma, (size_t)H, err) ||
+        enc->upload(&d.be2, s.ln2_beta, (size_t)H, err))
+      return fail();
+    enc->layers.push_back(d);
+  }
+  *out = enc;
+  return 0;
+}
+
+int eoship_encoder_release(EosHipEncoder* enc, char** err) {
+  (void)err;
+  if (enc == nullptr) return 0;
+  hipStreamSynchronize(enc->rt->stream);
+  delete enc;
+  return 0;
+}
+
+static int check_shape(EosHipEncoder* enc, int32_t batch, int32_t tokens, const char* what,
+                       char** err) {
+  if (batch <= 0 || tokens <= 0)
+    return set_err(err, "%s: batch and tokens must be positive (got %d, %d)", what, batch, tokens);
+  if (tokens > enc->desc.max_positions)
+    return set_err(err, "%s: tokens %d exceed the position table (%d rows)", what, tokens,
+                   enc->desc.max_positions);
+  if ((int64_t)batch * tokens > (int64_t)1 << 30)
+    return set_err(err, "%s: batch * tokens too large", what);
+  return 0;
+}
+
+int eoship_encoder_forward_device(EosHipRuntime* rt, EosHipEncoder* enc, const int32_t* d_ids,
+                                  const int32_t* d_type_ids, const int32_t* d_mask, int32_t batch,
+                                  int32_t tokens, float* d_out, char** err) {
+  if (rt == nullptr || enc == nullptr || d_ids == nullptr || d_mask == nullptr || d_out == nullptr)
+    return set_err(err, "eoship_encoder_forward_device: NULL argument");
+  if (enc->rt != rt) return set_err(err, "eoship_encoder_forward_device: encoder bound on another runtime");
+  if (check_shape(enc, batch, tokens, "eoship_encoder_forward_device", err) != 0) return 1;
+  return enc->forward(d_ids, d_type_ids, d_mask, batch, tokens, d_out, err);
+}
+
+int eoship_encoder_status(EosHipRuntime* rt, EosHipEncoder* enc, int32_t* status, char** err) {
+  if (rt == nullptr || enc == nullptr || status == nullptr)
+    return set_err(err, "eoship_encoder_status: NULL argument");
+  *status = 0;
+  if (enc->status == nullptr) return 0;
+  hipError_t e = hipMemcpyAsync(status, enc->status, 4, hipMemcpyDeviceToHost, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
+  return rt->sync(err);
+}
+
+int eoship_encoder_forward(EosHipRuntime* rt, EosHipEncoder* enc, const int32_t* ids,
+                           const int32_t* type_ids, const int32_t* mask, int32_t batch,
+                           int32_t tokens, float* out, char** err) {
+  if (rt == nullptr || enc == nullptr || ids == nullptr || mask == nullptr || out == nullptr)
+    return set_err(err, "eoship_encoder_forward: NULL argument");
+  if (enc->rt != rt) return set_err(err, "eoship_encoder_forward: encoder bound on another runtime");
+  if (check_shape(enc, batch, tokens, "eoship_encoder_forward", err) != 0) return 1;
+  const size_t n = (size_t)batch * tokens;
+  const size_t H = enc->desc.hidden;
+  const size_t need = n * 4 * 3 + (size_t)batch * H * 4 + 64;
+  if (enc->io_bytes < need) {
+    if (enc->io) hipFree(enc->io);
+    enc->io = nullptr;
+    enc->io_bytes = 0;
+    if (rt->alloc(need, &enc->io, err) != 0) return 1;
+    enc->io_bytes = need;
+  }
+  int32_t* d_ids = static_cast<int32_t*>(enc->io);
+  int32_t* d_types = d_ids + n;
+  int32_t* d_mask = d_types + n;
+  float* d_out = reinterpret_cast<float*>(d_mask + n);
+  hipError_t e = hipMemcpyAsync(d_ids, ids, n * 4, hipMemcpyHostToDevice, rt->stream);
+  if (e == hipSuccess && type_ids != nullptr)
+    e = hipMemcpyAsync(d_types, type_ids, n * 4, hipMemcpyHostToDevice, rt->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(d_mask, mask, n * 4, hipMemcpyHostToDevice, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(encoder inputs)", e);
+  if (enc->forward(d_ids, type_ids ? d_types : nullptr, d_mask, batch, tokens, d_out, err) != 0)
+    return 1;
+  e = hipMemcpyAsync(out, d_out, (size_t)batch * H * 4, hipMemcpyDeviceToHost, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(embeddings)", e);
+  int32_t st = 0;
+  if (eoship_encoder_status(rt, enc, &st, err) != 0) return 1;
+  if (st != 0)
+    return set_err(err, "eoship_encoder_forward: input id out of range (token, token type or position)");
+  return 0;
+}
+
+}  // extern "C"

@@ -11,7 +11,7 @@
 
 #include "eoship.h"
 
-#define EOSHIP_ABI_VERSION 1
+#define EOSHIP_ABI_VERSION 2
 
 namespace eoship {
 
@@ -32,7 +32,7 @@ struct Runtime {
   std::string name;
   std::string arch;
   hipStream_t stream = nullptr;
-  hipModule_t builtin = nullptr;
+  std::vector<hipModule_t> builtin;  // built-in code objects, searched in order
   std::unordered_map<std::string, hipFunction_t> fns;
   bool profiling = false;
   std::vector<ProfileRecord> records;

@@ -13,6 +13,8 @@ extern "C" {
 // Code objects built offline for gfx950 and linked in by eoship_blobs.S.
 extern const unsigned char eoship_tq_co_begin[];
 extern const unsigned char eoship_tq_co_end[];
+extern const unsigned char eoship_enc_co_begin[];
+extern const unsigned char eoship_enc_co_end[];
 }
 
 namespace eoship {
@@ -43,7 +45,11 @@ int Runtime::function(const char* name, hipFunction_t* out, char** err) {
     return 0;
   }
   hipFunction_t f = nullptr;
-  hipError_t e = hipModuleGetFunction(&f, builtin, name);
+  hipError_t e = hipErrorNotFound;
+  for (hipModule_t m : builtin) {
+    e = hipModuleGetFunction(&f, m, name);
+    if (e == hipSuccess) break;
+  }
   if (e != hipSuccess) return hip_err(err, name, e);
   fns.emplace(name, f);
   *out = f;
@@ -154,12 +160,18 @@ int eoship_runtime_create(int device, EosHipRuntime** out, char** err) {
     delete rt;
     return hip_err(err, "hipStreamCreateWithFlags", e);
   }
-  const size_t co_bytes = static_cast<size_t>(eoship_tq_co_end - eoship_tq_co_begin);
-  e = hipModuleLoadData(&rt->builtin, eoship_tq_co_begin);
-  if (e != hipSuccess || co_bytes == 0) {
-    hipStreamDestroy(rt->stream);
-    delete rt;
-    return hip_err(err, "hipModuleLoadData(builtin gfx950 code object)", e);
+  const unsigned char* images[2][2] = {{eoship_tq_co_begin, eoship_tq_co_end},
+                                       {eoship_enc_co_begin, eoship_enc_co_end}};
+  for (auto& im : images) {
+    hipModule_t m = nullptr;
+    e = im[1] > im[0] ? hipModuleLoadData(&m, im[0]) : hipErrorInvalidImage;
+    if (e != hipSuccess) {
+      for (hipModule_t mm : rt->builtin) hipModuleUnload(mm);
+      hipStreamDestroy(rt->stream);
+      delete rt;
+      return hip_err(err, "hipModuleLoadData(built-in gfx950 code object)", e);
+    }
+    rt->builtin.push_back(m);
   }
   for (auto& ev : rt->timer) ev = nullptr;
   *out = rt;
@@ -176,7 +188,7 @@ int eoship_runtime_destroy(EosHipRuntime* rt, char** err) {
   }
   for (auto& ev : rt->timer)
     if (ev) hipEventDestroy(ev);
-  if (rt->builtin) hipModuleUnload(rt->builtin);
+  for (hipModule_t m : rt->builtin) hipModuleUnload(m);
   hipError_t e = hipStreamDestroy(rt->stream);
   delete rt;
   if (e != hipSuccess) return hip_err(err, "hipStreamDestroy", e);

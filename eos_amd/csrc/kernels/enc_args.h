@@ -1,0 +1,87 @@
+// Kernel argument blocks of the encoder code object, shared with the host
+// shim. f16 tensors are passed as uint16_t pointers (bit patterns).
+#ifndef EOSHIP_ENC_ARGS_H
+#define EOSHIP_ENC_ARGS_H
+
+#include <stdint.h>
+
+// Packs the active (mask != 0) positions of a [batch][tokens] mask into rows:
+// row r holds sequence row_b[r], position row_t[r]; sequence b owns rows
+// [seq_off[b], seq_off[b] + seq_cnt[b]).
+struct EncPackArgs {
+  const int32_t* mask;   // [batch][tokens]
+  int32_t* row_b;        // [batch*tokens]
+  int32_t* row_t;        // [batch*tokens]
+  int32_t* seq_off;      // [batch]
+  int32_t* seq_cnt;      // [batch]
+  int32_t* total;        // [1] active rows
+  int batch, tokens;
+};
+
+// Embeddings (token + position + type) followed by affine LayerNorm.
+struct EncEmbedArgs {
+  const int32_t* ids;       // [batch][tokens]
+  const int32_t* type_ids;  // [batch][tokens] or NULL (all 0)
+  const int32_t* row_b;
+  const int32_t* row_t;
+  const int32_t* total;
+  const float* tok;         // [vocab][hidden]
+  const float* pos;         // [npos][hidden]
+  const float* typ;         // [ntype][hidden]
+  const float* gamma;
+  const float* beta;
+  uint16_t* out;            // [rows][hidden] f16
+  int32_t* status;          // set to 1 on an out-of-range id
+  int tokens, hidden, vocab, npos, ntype;
+  float eps;
+};
+
+// out[m][n] = epi(scale[n] * sum_k a[m][k] w[n][k] + bias[n]) for m < *rows.
+// w holds int8 codes stored as f16 (exact), [n][k] (HF [out, in] layout).
+// epi: 0 identity, 1 erf GELU, 2 tanh GELU. Rows past *rows are skipped.
+struct EncGemmArgs {
+  const uint16_t* a;       // [rows][k] f16
+  const uint16_t* w;       // [n][k] f16 codes
+  const float* wscale;     // [n]
+  const float* bias;       // [n]
+  uint16_t* out;           // [rows][n] f16
+  const int32_t* rows;     // device row count
+  int max_rows, n, k, epi;
+};
+
+// out[m] = LayerNorm(scale * (a[m] w^T) + bias + residual[m]) (n == hidden).
+struct EncGemmLnArgs {
+  const uint16_t* a;       // [rows][k] f16
+  const uint16_t* w;       // [hidden][k] f16 codes
+  const float* wscale;
+  const float* bias;
+  const uint16_t* residual;  // [rows][hidden] f16
+  const float* gamma;
+  const float* beta;
+  uint16_t* out;           // [rows][hidden] f16 (may alias residual)
+  const int32_t* rows;
+  int max_rows, k;
+  float eps;
+};
+
+// Masked multi-head attention over packed rows: every active row of a
+// sequence attends to every active row of the same sequence.
+struct EncAttnArgs {
+  const uint16_t* qkv;     // [rows][3*hidden] f16: q | k | v, head-major
+  uint16_t* ctx;           // [rows][hidden] f16
+  const int32_t* seq_off;
+  const int32_t* seq_cnt;
+  int batch, heads, hidden, max_len;
+  float scale_log2;        // log2(e) / sqrt(head_dim)
+};
+
+// Masked mean pool + L2 normalize per sequence.
+struct EncPoolArgs {
+  const uint16_t* h;       // [rows][hidden] f16
+  const int32_t* seq_off;
+  const int32_t* seq_cnt;
+  float* out;              // [batch][hidden]
+  int batch, hidden;
+};
+
+#endif  // EOSHIP_ENC_ARGS_H

@@ -1,0 +1,515 @@
+// q8 BERT-style encoder forward on gfx950 (CDNA4).
+//
+// Semantics follow the reference host path of the imported BERT embedder
+// (runtime/backend/bert_embedder_ops.go:101-197): embeddings + affine LN
+// (tensor_ops.go:1451-1512), per layer QKV -> masked attention -> O proj ->
+// residual + LN -> FFN (erf GELU) -> residual + LN
+// (bert_encoder_layer_ops.go:80-225), masked mean pool then L2 normalize.
+//
+// Layout: only active (mask != 0) positions are computed, packed into rows
+// [0, total); a sequence's rows are contiguous. Activations are f16, every
+// GEMM accumulates in f32 on v_mfma_f32_32x32x16_f16, weights are int8 codes
+// (stored as exact f16) with a per-output-channel f32 scale applied in the
+// epilogue together with the bias, the activation or the residual + LN.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "enc_args.h"
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+#define EOS_DEV __device__ __forceinline__
+
+namespace {
+
+EOS_DEV float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+EOS_DEV uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+EOS_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+EOS_DEV float gelu(float x, int kind) {
+  if (kind == 1) return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+  const float u = 0.7978845608f * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(u));
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------- pack
+
+// One workgroup per sequence: its offset is the number of active positions
+// of the sequences before it; positions are compacted in increasing order.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
+  __shared__ int wsum[4];
+  __shared__ int base_sh;
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int before = 0;
+  for (long long i = tid; i < (long long)b * a.tokens; i += 256) before += a.mask[i] != 0;
+  for (int o = 32; o > 0; o >>= 1) before += __shfl_xor(before, o);
+  if (lane == 0) wsum[w] = before;
+  __syncthreads();
+  if (tid == 0) base_sh = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  __syncthreads();
+  int base = base_sh;
+  const int32_t* m = a.mask + (size_t)b * a.tokens;
+  for (int t0 = 0; t0 < a.tokens; t0 += 256) {
+    const int t = t0 + tid;
+    const bool on = t < a.tokens && m[t] != 0;
+    const unsigned long long bal = __ballot(on);
+    const int below = __popcll(bal & ((1ull << lane) - 1ull));
+    __syncthreads();
+    if (lane == 0) wsum[w] = __popcll(bal);
+    __syncthreads();
+    int woff = 0;
+    for (int i = 0; i < w; ++i) woff += wsum[i];
+    if (on) {
+      const int r = base + woff + below;
+      a.row_b[r] = b;
+      a.row_t[r] = t;
+    }
+    base += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  }
+  if (tid == 0) {
+    a.seq_off[b] = base_sh;
+    a.seq_cnt[b] = base - base_sh;
+    if (b == a.batch - 1) *a.total = base;
+  }
+}
+
+// -------------------------------------------------------------- embedding
+
+// One wavefront per active row: token + position + type in f32 (that order),
+// then affine LayerNorm (two-pass statistics), f16 out.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= *a.total) return;
+  const int b = a.row_b[row], t = a.row_t[row];
+  int id = a.ids[(size_t)b * a.tokens + t];
+  int ty = a.type_ids ? a.type_ids[(size_t)b * a.tokens + t] : 0;
+  const int pos = t;
+  if (id < 0 || id >= a.vocab || ty < 0 || ty >= a.ntype || pos >= a.npos) {
+    if (lane == 0) *a.status = 1;
+    id = id < 0 || id >= a.vocab ? 0 : id;
+    ty = ty < 0 || ty >= a.ntype ? 0 : ty;
+  }
+  const int p = pos < a.npos ? pos : a.npos - 1;
+  constexpr int kMaxPer = 16;  // hidden <= 1024
+  float v[kMaxPer];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    const int c = lane + 64 * j;
+    v[j] = 0.f;
+    if (c < a.hidden) {
+      v[j] = a.tok[(size_t)id * a.hidden + c] + a.pos[(size_t)p * a.hidden + c] +
+             a.typ[(size_t)ty * a.hidden + c];
+      s += v[j];
+    }
+  }
+  const float mean = wave_sum(s) / (float)a.hidden;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    const int c = lane + 64 * j;
+    if (c < a.hidden) q += (v[j] - mean) * (v[j] - mean);
+  }
+  const float inv = 1.0f / sqrtf(wave_sum(q) / (float)a.hidden + a.eps);
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    const int c = lane + 64 * j;
+    if (c < a.hidden) a.out[(size_t)row * a.hidden + c] = f2h((v[j] - mean) * inv * a.gamma[c] + a.beta[c]);
+  }
+}
+
+// ------------------------------------------------------------------- GEMM
+
+namespace {
+constexpr int kBM = 128, kBN = 128, kBK = 32, kPadK = kBK + 8;  // halves per LDS row
+}
+
+// 128 x 128 output tile per workgroup (4 wavefronts, 64 x 64 each = 2 x 2
+// MFMA 32x32 blocks), K in chunks of 32 staged through LDS with the next
+// chunk's global loads in flight during the current chunk's MFMAs.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm(EncGemmArgs a) {
+  __shared__ uint16_t as[2][kBM * kPadK];
+  __shared__ uint16_t ws[2][kBN * kPadK];
+  const int rows = *a.rows;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  if (m0 >= rows) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int g = lane >> 5, l32 = lane & 31;
+  // global -> register staging: 2 x 16 B of A and of W per thread
+  v4i ra[2], rw[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = tid + 256 * u;          // 512 chunks of 16 B
+      const int r = idx >> 2, c = (idx & 3) * 8;
+      const int am = min(m0 + r, a.max_rows - 1);
+      ra[u] = *reinterpret_cast<const v4i*>(a.a + (size_t)am * a.k + k0 + c);
+      rw[u] = *reinterpret_cast<const v4i*>(a.w + (size_t)(n0 + r) * a.k + k0 + c);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = tid + 256 * u;
+      const int r = idx >> 2, c = (idx & 3) * 8;
+      *reinterpret_cast<v4i*>(&as[buf][r * kPadK + c]) = ra[u];
+      *reinterpret_cast<v4i*>(&ws[buf][r * kPadK + c]) = rw[u];
+    }
+  };
+  v16f acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16f{0};
+  const int nk = a.k / kBK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kc = 0; kc < nk; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < nk) gload((kc + 1) * kBK);
+#pragma unroll
+    for (int s = 0; s < kBK / 16; ++s) {
+      v8h af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        af[i] = *reinterpret_cast<const v8h*>(&as[buf][(wm * 64 + i * 32 + l32) * kPadK + s * 16 + g * 8]);
+        bf[i] = *reinterpret_cast<const v8h*>(&ws[buf][(wn * 64 + i * 32 + l32) * kPadK + s * 16 + g * 8]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kc + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+  // Epilogue: element e of lane (l32, g) is row 8(e/4) + 4g + e%4, column l32.
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + wn * 64 + j * 32 + l32;
+    const float sc = a.wscale[col], bi = a.bias[col];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+        if (row < rows) {
+          float v = acc[i][j][e] * sc + bi;
+          if (a.epi != 0) v = gelu(v, a.epi);
+          a.out[(size_t)row * a.n + col] = f2h(v);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------ GEMM + residual + LN
+
+namespace {
+constexpr int kLnBM = 32;
+}
+
+// 32 full rows per workgroup (4 wavefronts, each NT x 32 columns), then
+// bias + residual and a two-pass f32 LayerNorm over the row in LDS.
+template <int NT>
+EOS_DEV void gemm_ln_body(const EncGemmLnArgs& a) {
+  constexpr int H = 4 * NT * 32;
+  constexpr int kOutPad = H + 4;
+  constexpr int kStage = 2 * (kLnBM + H) * kPadK;  // halves
+  constexpr int kEpi = kLnBM * kOutPad * 2;         // halves (f32 tile)
+  __shared__ uint16_t smem[kStage > kEpi ? kStage : kEpi];
+  uint16_t* as0 = smem;
+  uint16_t* ws0 = smem + 2 * kLnBM * kPadK;
+  const int rows = *a.rows;
+  const int m0 = blockIdx.x * kLnBM;
+  if (m0 >= rows) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  // chunks of 16 B: A 32 rows x 4 = 128, W H rows x 4
+  constexpr int kWChunks = H * 4;
+  constexpr int kWPer = (kWChunks + 255) / 256;
+  v4i ra, rw[kWPer];
+  auto gload = [&](int k0) {
+    if (tid < 128) {
+      const int r = tid >> 2, c = (tid & 3) * 8;
+      const int am = min(m0 + r, a.max_rows - 1);
+      ra = *reinterpret_cast<const v4i*>(a.a + (size_t)am * a.k + k0 + c);
+    }
+#pragma unroll
+    for (int u = 0; u < kWPer; ++u) {
+      const int idx = tid + 256 * u;
+      if (idx < kWChunks) {
+        const int r = idx >> 2, c = (idx & 3) * 8;
+        rw[u] = *reinterpret_cast<const v4i*>(a.w + (size_t)r * a.k + k0 + c);
+      }
+    }
+  };
+  auto lstore = [&](int buf) {
+    if (tid < 128) {
+      const int r = tid >> 2, c = (tid & 3) * 8;
+      *reinterpret_cast<v4i*>(&as0[buf * kLnBM * kPadK + r * kPadK + c]) = ra;
+    }
+#pragma unroll
+    for (int u = 0; u < kWPer; ++u) {
+      const int idx = tid + 256 * u;
+      if (idx < kWChunks) {
+        const int r = idx >> 2, c = (idx & 3) * 8;
+        *reinterpret_cast<v4i*>(&ws0[buf * H * kPadK + r * kPadK + c]) = rw[u];
+      }
+    }
+  };
+  v16f acc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) acc[j] = v16f{0};
+  const int nk = a.k / kBK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kc = 0; kc < nk; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < nk) gload((kc + 1) * kBK);
+#pragma unroll
+    for (int s = 0; s < kBK / 16; ++s) {
+      const v8h af = *reinterpret_cast<const v8h*>(&as0[buf * kLnBM * kPadK + l32 * kPadK + s * 16 + g * 8]);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int ncol = wave * NT * 32 + j * 32 + l32;
+        const v8h bf = *reinterpret_cast<const v8h*>(&ws0[buf * H * kPadK + ncol * kPadK + s * 16 + g * 8]);
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[j], 0, 0, 0);
+      }
+    }
+    if (kc + 1 < nk) lstore(buf ^ 1);
+    __syncthreads();
+  }
+  // bias + residual into an f32 row tile in LDS (the staging space is free).
+  float* tile = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int col = wave * NT * 32 + j * 32 + l32;
+    const float sc = a.wscale[col], bi = a.bias[col];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int r = 8 * (e >> 2) + 4 * g + (e & 3);
+      const int row = min(m0 + r, rows - 1);
+      tile[r * kOutPad + col] = acc[j][e] * sc + bi + h2f(a.residual[(size_t)row * H + col]);
+    }
+  }
+  __syncthreads();
+  // LayerNorm: each wavefront normalizes 8 rows.
+  constexpr int PER = H / 64;
+  for (int rr = 0; rr < kLnBM / 4; ++rr) {
+    const int r = wave * (kLnBM / 4) + rr;
+    const int row = m0 + r;
+    float v[PER];
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      v[j] = tile[r * kOutPad + lane + 64 * j];
+      s += v[j];
+    }
+    const float mean = wave_sum(s) / (float)H;
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) q += (v[j] - mean) * (v[j] - mean);
+    const float inv = 1.0f / sqrtf(wave_sum(q) / (float)H + a.eps);
+    if (row < rows) {
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int c = lane + 64 * j;
+        a.out[(size_t)row * H + c] = f2h((v[j] - mean) * inv * a.gamma[c] + a.beta[c]);
+      }
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h384(EncGemmLnArgs a) {
+  gemm_ln_body<3>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h512(EncGemmLnArgs a) {
+  gemm_ln_body<4>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h768(EncGemmLnArgs a) {
+  gemm_ln_body<6>(a);
+}
+
+// --------------------------------------------------------------- attention
+
+// Flash-style attention in transposed form: each wavefront owns 32 queries of
+// one (sequence, head); per block of 32 keys it computes S^T = K Q^T (keys x
+// queries, so each lane owns one query column and its softmax state), masks
+// keys past the sequence, updates the running max / sum in f32 (exp2 domain),
+// and accumulates O^T += V^T P^T on MFMA. P^T is fed straight from the S^T
+// registers: the K order of that MFMA is the row order the S^T accumulator
+// already has, and the V^T fragment is gathered in the same order.
+template <int HD>
+EOS_DEV void attn_body(const EncAttnArgs& a) {
+  constexpr int KB = 32;                 // keys per block
+  constexpr int QW = 32;                 // queries per wavefront
+  __shared__ uint16_t ks[KB * (HD + 8)];
+  __shared__ uint16_t vt[HD * (KB + 8)];
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int cnt = a.seq_cnt[b];
+  const int q0 = blockIdx.x * (4 * QW);
+  if (q0 >= cnt) return;
+  const int off = a.seq_off[b];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int ld = 3 * a.hidden;
+  const int qi = q0 + wave * QW + l32;           // this lane's query (column)
+  const bool qlive = qi < cnt;
+  // Q^T fragments (B operand): lane (query l32, group g) holds q[16s + 8g .. +7].
+  v8h qf[HD / 16];
+  {
+    const uint16_t* qrow = a.qkv + (size_t)(off + (qlive ? qi : 0)) * ld + h * HD;
+#pragma unroll
+    for (int s = 0; s < HD / 16; ++s) qf[s] = *reinterpret_cast<const v8h*>(qrow + s * 16 + g * 8);
+  }
+  v16f o[HD / 32];
+#pragma unroll
+  for (int t = 0; t < HD / 32; ++t) o[t] = v16f{0};
+  float mrun = -__builtin_inff(), lrun = 0.f;
+  for (int k0 = 0; k0 < cnt; k0 += KB) {
+    __syncthreads();
+    // stage K [key][HD] and V^T [HD][key] for keys k0..k0+31
+    for (int idx = tid; idx < KB * HD / 8; idx += 256) {
+      const int kr = idx / (HD / 8), c = (idx % (HD / 8)) * 8;
+      const int key = min(k0 + kr, cnt - 1);
+      const uint16_t* base = a.qkv + (size_t)(off + key) * ld + h * HD + c;
+      const v4i kv = *reinterpret_cast<const v4i*>(base + a.hidden);
+      const v4i vv = *reinterpret_cast<const v4i*>(base + 2 * a.hidden);
+      *reinterpret_cast<v4i*>(&ks[kr * (HD + 8) + c]) = kv;
+      const uint16_t* vh = reinterpret_cast<const uint16_t*>(&vv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[(c + e) * (KB + 8) + kr] = vh[e];
+    }
+    __syncthreads();
+    // S^T (32 keys x 32 queries)
+    v16f s = v16f{0};
+#pragma unroll
+    for (int st = 0; st < HD / 16; ++st) {
+      const v8h kf = *reinterpret_cast<const v8h*>(&ks[l32 * (HD + 8) + st * 16 + g * 8]);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s, 0, 0, 0);
+    }
+    // element e is key k0 + 8(e/4) + 4g + e%4
+    float mloc = -__builtin_inff();
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
+      s[e] = key < cnt ? s[e] * a.scale_log2 : -__builtin_inff();
+      mloc = fmaxf(mloc, s[e]);
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    const float mnew = fmaxf(mrun, mloc);
+    const float corr = exp2f(mrun - mnew);
+    float psum = 0.f;
+    v8h pf[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float p = exp2f(s[e] - mnew);
+      psum += p;
+      pf[e >> 3][e & 7] = (_Float16)p;
+    }
+    psum += __shfl_xor(psum, 32);
+    lrun = lrun * corr + psum;
+    mrun = mnew;
+#pragma unroll
+    for (int t = 0; t < HD / 32; ++t) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[t][e] *= corr;
+    }
+    // O^T += V^T P^T. K step st covers the keys this lane's P holds for
+    // e in [8 st, 8 st + 8): 16 st + {4g..4g+3} and 16 st + 8 + {4g..4g+3}.
+#pragma unroll
+    for (int t = 0; t < HD / 32; ++t) {
+      const int d = t * 32 + l32;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const uint16_t* vr = &vt[d * (KB + 8) + 16 * st + 4 * g];
+        v8h vf;
+        const v4h lo = *reinterpret_cast<const v4h*>(vr);
+        const v4h hi = *reinterpret_cast<const v4h*>(vr + 8);
+        vf[0] = lo[0]; vf[1] = lo[1]; vf[2] = lo[2]; vf[3] = lo[3];
+        vf[4] = hi[0]; vf[5] = hi[1]; vf[6] = hi[2]; vf[7] = hi[3];
+        o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[st], o[t], 0, 0, 0);
+      }
+    }
+  }
+  if (!qlive) return;
+  const float inv = lrun > 0.f ? 1.0f / lrun : 0.f;
+  uint16_t* orow = a.ctx + (size_t)(off + qi) * a.hidden + h * HD;
+#pragma unroll
+  for (int t = 0; t < HD / 32; ++t) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int d = t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
+      orow[d] = f2h(o[t][e] * inv);
+    }
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd32(EncAttnArgs a) {
+  attn_body<32>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd64(EncAttnArgs a) {
+  attn_body<64>(a);
+}
+
+// ------------------------------------------------------------------- pool
+
+// Masked mean pool then L2 normalize (rows of norm 0 unchanged). One
+// workgroup of 16 wavefronts per sequence: wavefront w sums rows w, w+16, ...
+// in f32 (lane owns columns lane + 64 j), the 16 partial sums are added in
+// wavefront order, times 1/count.
+extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
+  constexpr int kWaves = 16, kPer = 16;  // hidden <= 1024
+  __shared__ float part[kWaves * 1024];
+  __shared__ float red[kWaves];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int off = a.seq_off[b], cnt = a.seq_cnt[b];
+  float s[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) s[j] = 0.f;
+  for (int r = w; r < cnt; r += kWaves) {
+    const uint16_t* row = a.h + (size_t)(off + r) * a.hidden;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int c = lane + 64 * j;
+      if (c < a.hidden) s[j] += h2f(row[c]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int c = lane + 64 * j;
+    if (c < a.hidden) part[w * 1024 + c] = s[j];
+  }
+  __syncthreads();
+  float v = 0.f;
+  const int c = tid;
+  if (c < a.hidden) {
+    for (int i = 0; i < kWaves; ++i) v += part[i * 1024 + c];
+    v = cnt > 0 ? v * (1.0f / (float)cnt) : 0.f;
+  }
+  const float ss = wave_sum(c < a.hidden ? v * v : 0.f);
+  if (lane == 0) red[w] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  for (int i = 0; i < kWaves; ++i) tot += red[i];
+  const float norm = sqrtf(tot);
+  if (c < a.hidden) a.out[(size_t)b * a.hidden + c] = norm > 0.f ? v / norm : v;
+}

@@ -159,3 +159,52 @@ def baseline_flat_corpus(n: int = 1_000_000, dim: int = 384) -> TurboQuantCorpus
 def baseline_queries(q: int, dim: int, seed: int = 6) -> np.ndarray:
     """Gaussian queries, unit-normalized in f64, stored f32."""
     return unit_rows(normal(seed, q * dim).reshape(q, dim)).astype(np.float32)
+
+
+def bert_q8_weights(layers: int, hidden: int, heads: int, inter: int, vocab: int, npos: int,
+                    ntype: int = 2, seed: int = 7, eps: float = 1e-12, gelu: int = 1,
+                    random_affine: bool = False):
+    """Random-init BERT-style encoder (weights N(0, 0.02)) quantized to int8
+    per output channel. With random_affine, biases, LayerNorm gamma/beta are
+    drawn too (otherwise biases 0, gamma 1, beta 0)."""
+    from .encoder import EncoderLayerWeights, EncoderWeights, quantize_per_channel
+
+    counter = [seed * 1000003]
+
+    def draw(shape, std=0.02):
+        counter[0] += 1
+        n = int(np.prod(shape))
+        return (std * normal(counter[0], n)).astype(np.float32).reshape(shape)
+
+    def vec(n, base=0.0, std=0.02):
+        if not random_affine:
+            return np.full(n, base, np.float32)
+        return (base + draw((n,), std)).astype(np.float32)
+
+    H, F = hidden, inter
+    tok = draw((vocab, H))
+    pos = draw((npos, H))
+    typ = draw((ntype, H))
+    w = EncoderWeights(hidden=H, heads=heads, intermediate=F, ln_eps=eps, gelu=gelu, tok=tok,
+                       pos=pos, typ=typ, emb_gamma=vec(H, 1.0, 0.1), emb_beta=vec(H, 0.0, 0.05))
+    for _ in range(layers):
+        qkv, sq = quantize_per_channel(draw((3 * H, H)))
+        wo, so = quantize_per_channel(draw((H, H)))
+        w1, s1 = quantize_per_channel(draw((F, H)))
+        w2, s2 = quantize_per_channel(draw((H, F)))
+        w.layers.append(EncoderLayerWeights(
+            w_qkv=qkv, s_qkv=sq, b_qkv=vec(3 * H), w_o=wo, s_o=so, b_o=vec(H),
+            ln1_gamma=vec(H, 1.0, 0.1), ln1_beta=vec(H, 0.0, 0.05), w_1=w1, s_1=s1, b_1=vec(F),
+            w_2=w2, s_2=s2, b_2=vec(H), ln2_gamma=vec(H, 1.0, 0.1), ln2_beta=vec(H, 0.0, 0.05)))
+    return w
+
+
+def encoder_batch(batch: int, tokens: int, vocab: int, lo: int, hi: int, seed_ids: int,
+                  seed_len: int):
+    """Token ids uniform over [0, vocab), valid lengths uniform in [lo, hi];
+    mask[b, t] = t < len_b (right padding, runtime/embedding_model.go:1457-1495)."""
+    ids = uniform_int(seed_ids, batch * tokens, 0, vocab).astype(np.int32).reshape(batch, tokens)
+    lens = uniform_int(seed_len, batch, lo, hi + 1).astype(np.int32)
+    mask = (np.arange(tokens)[None, :] < lens[:, None]).astype(np.int32)
+    ids = np.where(mask == 1, ids, 0).astype(np.int32)
+    return ids, mask, lens

@@ -1,0 +1,183 @@
+"""q8 BERT-style encoder on the MI355X backend.
+
+Host-side mirror of the reference's bert_embedder step
+(runtime/backend/bert_embedder_ops.go:101-197, BERTEmbedderReferenceWithPooling):
+``Encoder.embed(input_ids, attention_mask, token_type_ids)`` returns the masked
+mean-pooled, L2-normalized sentence embeddings [batch, hidden]. Errors follow
+the reference: ids outside their tables are rejected
+(runtime/backend/tensor_ops.go:1484-1492). All arithmetic runs in libeoship's
+gfx950 kernels.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+from .runtime import DeviceBuffer, Runtime
+
+
+@dataclass
+class EncoderLayerWeights:
+    """One post-LN layer: int8 codes in HF [out, in] layout + per-output-channel scales."""
+    w_qkv: np.ndarray  # int8 [3H, H]
+    s_qkv: np.ndarray  # f32 [3H]
+    b_qkv: np.ndarray  # f32 [3H]
+    w_o: np.ndarray
+    s_o: np.ndarray
+    b_o: np.ndarray
+    ln1_gamma: np.ndarray
+    ln1_beta: np.ndarray
+    w_1: np.ndarray    # int8 [F, H]
+    s_1: np.ndarray
+    b_1: np.ndarray
+    w_2: np.ndarray    # int8 [H, F]
+    s_2: np.ndarray
+    b_2: np.ndarray
+    ln2_gamma: np.ndarray
+    ln2_beta: np.ndarray
+
+    def dequantized(self):
+        """The 16 f32 tensors in the reference order (q,k,v split), code * scale."""
+        H = self.w_o.shape[0]
+        wq = self.w_qkv.astype(np.float32) * self.s_qkv[:, None]
+        wo = self.w_o.astype(np.float32) * self.s_o[:, None]
+        w1 = self.w_1.astype(np.float32) * self.s_1[:, None]
+        w2 = self.w_2.astype(np.float32) * self.s_2[:, None]
+        b = self.b_qkv
+        return [wq[:H], b[:H], wq[H:2 * H], b[H:2 * H], wq[2 * H:], b[2 * H:], wo, self.b_o,
+                self.ln1_gamma, self.ln1_beta, w1, self.b_1, w2, self.b_2, self.ln2_gamma,
+                self.ln2_beta]
+
+
+@dataclass
+class EncoderWeights:
+    hidden: int
+    heads: int
+    intermediate: int
+    ln_eps: float
+    gelu: int  # 1 erf, 2 tanh
+    tok: np.ndarray     # f32 [V, H]
+    pos: np.ndarray     # f32 [P, H]
+    typ: np.ndarray     # f32 [T, H]
+    emb_gamma: np.ndarray
+    emb_beta: np.ndarray
+    layers: list = field(default_factory=list)
+
+
+def quantize_per_channel(w: np.ndarray):
+    """Symmetric absmax int8 per output channel (rows): scale = max|w|/127,
+    code = clamp(round(w/scale), +-127) -- the reference's q8 grid
+    (runtime/mll_export.go:918-942) applied per row."""
+    w = np.asarray(w, dtype=np.float32)
+    mx = np.max(np.abs(w), axis=1)
+    scale = np.where(mx > 0, mx / np.float32(127.0), np.float32(0.0)).astype(np.float32)
+    safe = np.where(scale > 0, scale, np.float32(1.0))
+    codes = np.clip(np.rint(w / safe[:, None]), -127, 127).astype(np.int8)
+    codes[scale == 0] = 0
+    return codes, scale
+
+
+def _p(a, t):
+    return a.ctypes.data_as(C.POINTER(t))
+
+
+class Encoder:
+    """An encoder bound on the device."""
+
+    def __init__(self, rt: Runtime, w: EncoderWeights):
+        self.rt, self.w = rt, w
+        H, F = w.hidden, w.intermediate
+        self._keep = []
+
+        def f32(x, shape):
+            a = np.ascontiguousarray(x, dtype=np.float32)
+            if a.shape != shape:
+                raise ValueError(f"expected {shape}, got {a.shape}")
+            self._keep.append(a)
+            return a
+
+        def i8(x, shape):
+            a = np.ascontiguousarray(x, dtype=np.int8)
+            if a.shape != shape:
+                raise ValueError(f"expected {shape}, got {a.shape}")
+            self._keep.append(a)
+            return a
+
+        layers = (_lib.EosHipEncoderLayer * max(len(w.layers), 1))()
+        for i, L in enumerate(w.layers):
+            x = layers[i]
+            x.w_qkv = _p(i8(L.w_qkv, (3 * H, H)), C.c_int8)
+            x.s_qkv = _p(f32(L.s_qkv, (3 * H,)), C.c_float)
+            x.b_qkv = _p(f32(L.b_qkv, (3 * H,)), C.c_float)
+            x.w_o = _p(i8(L.w_o, (H, H)), C.c_int8)
+            x.s_o = _p(f32(L.s_o, (H,)), C.c_float)
+            x.b_o = _p(f32(L.b_o, (H,)), C.c_float)
+            x.ln1_gamma = _p(f32(L.ln1_gamma, (H,)), C.c_float)
+            x.ln1_beta = _p(f32(L.ln1_beta, (H,)), C.c_float)
+            x.w_1 = _p(i8(L.w_1, (F, H)), C.c_int8)
+            x.s_1 = _p(f32(L.s_1, (F,)), C.c_float)
+            x.b_1 = _p(f32(L.b_1, (F,)), C.c_float)
+            x.w_2 = _p(i8(L.w_2, (H, F)), C.c_int8)
+            x.s_2 = _p(f32(L.s_2, (H,)), C.c_float)
+            x.b_2 = _p(f32(L.b_2, (H,)), C.c_float)
+            x.ln2_gamma = _p(f32(L.ln2_gamma, (H,)), C.c_float)
+            x.ln2_beta = _p(f32(L.ln2_beta, (H,)), C.c_float)
+        desc = _lib.EosHipEncoderDesc(
+            layers=len(w.layers), hidden=H, heads=w.heads, intermediate=F,
+            vocab=w.tok.shape[0], max_positions=w.pos.shape[0], type_vocab=w.typ.shape[0],
+            ln_eps=w.ln_eps, gelu=w.gelu)
+        tok = f32(w.tok, (w.tok.shape[0], H))
+        pos = f32(w.pos, (w.pos.shape[0], H))
+        typ = f32(w.typ, (w.typ.shape[0], H))
+        eg = f32(w.emb_gamma, (H,))
+        eb = f32(w.emb_beta, (H,))
+        self.handle = C.c_void_p()
+        _lib.call("eoship_encoder_bind", rt.handle, C.byref(desc), _p(tok, C.c_float),
+                  _p(pos, C.c_float), _p(typ, C.c_float), _p(eg, C.c_float), _p(eb, C.c_float),
+                  layers, C.byref(self.handle))
+        self._keep = []
+
+    def release(self) -> None:
+        if self.handle:
+            _lib.call("eoship_encoder_release", self.handle)
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    def embed(self, input_ids: np.ndarray, attention_mask: np.ndarray,
+              token_type_ids: np.ndarray | None = None) -> np.ndarray:
+        ids = np.ascontiguousarray(input_ids, dtype=np.int32)
+        mask = np.ascontiguousarray(attention_mask, dtype=np.int32)
+        if ids.ndim != 2 or mask.shape != ids.shape:
+            raise ValueError("input_ids and attention_mask must both be [batch, tokens]")
+        types = None
+        if token_type_ids is not None:
+            types = np.ascontiguousarray(token_type_ids, dtype=np.int32)
+            if types.shape != ids.shape:
+                raise ValueError("token_type_ids must match input_ids")
+        out = np.zeros((ids.shape[0], self.w.hidden), np.float32)
+        _lib.call("eoship_encoder_forward", self.rt.handle, self.handle,
+                  ids.ctypes.data_as(C.c_void_p),
+                  types.ctypes.data_as(C.c_void_p) if types is not None else None,
+                  mask.ctypes.data_as(C.c_void_p), C.c_int32(ids.shape[0]),
+                  C.c_int32(ids.shape[1]), out.ctypes.data_as(C.c_void_p))
+        return out
+
+    def embed_device(self, d_ids: DeviceBuffer, d_mask: DeviceBuffer, batch: int, tokens: int,
+                     d_out: DeviceBuffer, d_types: DeviceBuffer | None = None) -> None:
+        """Enqueue a forward on device buffers (no wait)."""
+        _lib.call("eoship_encoder_forward_device", self.rt.handle, self.handle, d_ids.ptr,
+                  d_types.ptr if d_types is not None else None, d_mask.ptr, C.c_int32(batch),
+                  C.c_int32(tokens), d_out.ptr)
+
+    def status(self) -> int:
+        st = C.c_int32()
+        _lib.call("eoship_encoder_status", self.rt.handle, self.handle, C.byref(st))
+        return st.value

@@ -130,6 +130,64 @@ int eoship_tq_scores(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int3
 int eoship_tq_prepare(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int32_t q,
                       int16_t* qs, float* alpha, char** err);
 
+/* ---------------------------------------------------------------- encoder */
+
+typedef struct EosHipEncoder EosHipEncoder;
+
+/* BERT-style post-LN encoder (the imported bert_embedder step): the
+ * architecture fields of BERTEmbedderReferenceWithPooling
+ * (runtime/backend/bert_embedder_ops.go:101-197). */
+typedef struct {
+  int32_t layers;        /* num_hidden_layers */
+  int32_t hidden;        /* 384, 512 or 768 */
+  int32_t heads;         /* hidden / heads in {32, 64} */
+  int32_t intermediate;  /* FFN width, multiple of 128 */
+  int32_t vocab;         /* token table rows */
+  int32_t max_positions; /* position table rows (>= tokens) */
+  int32_t type_vocab;    /* token-type table rows */
+  float ln_eps;          /* LayerNorm epsilon (BERT: 1e-12) */
+  int32_t gelu;          /* 1 = erf GELU (exactGELU), 2 = tanh GELU */
+} EosHipEncoderDesc;
+
+/* One layer's weights (host). Dense weights are int8 codes in HF [out][in]
+ * layout with one f32 scale per output channel (dequantized weight =
+ * code * scale; one equal scale per tensor reproduces the reference's
+ * per-tensor q8 grid, runtime/mll_export.go:897-975). w_qkv stacks the query,
+ * key and value projections ([3*hidden][hidden]). */
+typedef struct {
+  const int8_t* w_qkv; const float* s_qkv; const float* b_qkv;
+  const int8_t* w_o;   const float* s_o;   const float* b_o;
+  const float* ln1_gamma; const float* ln1_beta;
+  const int8_t* w_1;   const float* s_1;   const float* b_1;   /* [intermediate][hidden] */
+  const int8_t* w_2;   const float* s_2;   const float* b_2;   /* [hidden][intermediate] */
+  const float* ln2_gamma; const float* ln2_beta;
+} EosHipEncoderLayer;
+
+/* Uploads embedding tables (f32) and layer weights. Replaces loading the
+ * bert_embedder step's weights (runtime/backend/bert_embedder_ops.go:101-197;
+ * q8 dequantization at load, runtime/weight_file.go:315-333). */
+int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const float* tok_emb,
+                        const float* pos_emb, const float* type_emb, const float* emb_ln_gamma,
+                        const float* emb_ln_beta, const EosHipEncoderLayer* layers,
+                        EosHipEncoder** out, char** err);
+int eoship_encoder_release(EosHipEncoder* enc, char** err);
+/* Embeds a [batch][tokens] batch (host buffers): embeddings, all layers,
+ * masked mean pool, L2 normalize -> out [batch][hidden] f32. type_ids may be
+ * NULL (all 0). Fails with an error for a token, type or position id outside
+ * its table (the reference rejects these, runtime/backend/tensor_ops.go:1484-1492).
+ * Replaces Program.Run of a bert_embedder plan / EmbeddingModel.EmbedBatch
+ * (runtime/inference.go:57-101; runtime/embedding_model.go:669-761). */
+int eoship_encoder_forward(EosHipRuntime* rt, EosHipEncoder* enc, const int32_t* ids,
+                           const int32_t* type_ids, const int32_t* mask, int32_t batch,
+                           int32_t tokens, float* out, char** err);
+/* Same on device buffers; enqueued on the runtime stream (no wait). The id
+ * check result is readable with eoship_encoder_status after a sync. */
+int eoship_encoder_forward_device(EosHipRuntime* rt, EosHipEncoder* enc, const int32_t* d_ids,
+                                  const int32_t* d_type_ids, const int32_t* d_mask, int32_t batch,
+                                  int32_t tokens, float* d_out, char** err);
+/* 0 when every id of the last forward was in range; synchronises. */
+int eoship_encoder_status(EosHipRuntime* rt, EosHipEncoder* enc, int32_t* status, char** err);
+
 #ifdef __cplusplus
 }
 #endif

@@ -132,3 +132,92 @@ def topk_scores(scores: np.ndarray, k: int):
     out = np.zeros(kk, np.float32)
     load().topk_scores(_p(s), n, int(k), _p(ids), _p(out))
     return ids, out
+
+
+# ------------------------------------------------------------------ encoder
+
+def _enc():
+    lib = load()
+    if getattr(lib, "_enc_ready", False):
+        return lib
+    P = C.c_void_p
+    lib.dense_hf.argtypes = [P, C.c_int, C.c_int, P, P, C.c_int, P]
+    lib.dense_hf.restype = None
+    lib.bert_attention.argtypes = [P, P, P, P, C.c_int, C.c_int, C.c_int, C.c_int, P]
+    lib.bert_attention.restype = None
+    lib.bert_embed.argtypes = [P, C.c_int, P, C.c_int, P, C.c_int, P, P, P, C.c_int, P, P, P,
+                               C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, P]
+    lib.bert_embed.restype = None
+    lib.mean_pool_masked.argtypes = [P, P, C.c_int, C.c_int, C.c_int, P]
+    lib.mean_pool_masked.restype = None
+    lib.normalize_rows.argtypes = [P, C.c_int, C.c_int]
+    lib.normalize_rows.restype = None
+    lib.tiny_embed.argtypes = [P, C.c_int, C.c_int, P, C.c_int, P, C.c_int, P]
+    lib.tiny_embed.restype = None
+    lib._enc_ready = True
+    return lib
+
+
+def bert_embed(tok, pos, typ, emb_gamma, emb_beta, layers, ids, mask, type_ids, heads, eps):
+    """layers: list of 16-tensor lists (reference order, f32, HF [out, in])."""
+    lib = _enc()
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    mask = np.ascontiguousarray(mask, dtype=np.int32)
+    types = np.zeros_like(ids) if type_ids is None else np.ascontiguousarray(type_ids, np.int32)
+    batch, tokens = ids.shape
+    hidden = tok.shape[1]
+    inter = layers[0][10].shape[0] if layers else hidden
+    keep = [_f32(x) for L in layers for x in L]
+    ptrs = (C.c_void_p * max(len(keep), 1))(*[k.ctypes.data for k in keep])
+    tok, pos, typ = _f32(tok), _f32(pos), _f32(typ)
+    g, b = _f32(emb_gamma), _f32(emb_beta)
+    out = np.zeros((batch, hidden), np.float32)
+    lib.bert_embed(_p(tok), tok.shape[0], _p(pos), pos.shape[0], _p(typ), typ.shape[0], _p(g),
+                   _p(b), ptrs, len(layers), _p(ids), _p(types), _p(mask), batch, tokens, hidden,
+                   heads, inter, C.c_double(eps), _p(out))
+    return out
+
+
+def dense_hf(x, w, b):
+    lib = _enc()
+    x, w, b = _f32(x), _f32(w), _f32(b)
+    y = np.zeros((x.shape[0], w.shape[0]), np.float32)
+    lib.dense_hf(_p(x), x.shape[0], x.shape[1], _p(w), _p(b), w.shape[0], _p(y))
+    return y
+
+
+def bert_attention(q, k, v, mask, heads):
+    lib = _enc()
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    mask = np.ascontiguousarray(mask, dtype=np.int32)
+    batch, tokens = mask.shape
+    ctx = np.zeros_like(q)
+    lib.bert_attention(_p(q), _p(k), _p(v), _p(mask), batch, tokens, q.shape[1], heads, _p(ctx))
+    return ctx
+
+
+def mean_pool_masked(h, mask):
+    lib = _enc()
+    h = _f32(h)
+    mask = np.ascontiguousarray(mask, dtype=np.int32)
+    batch, tokens, hidden = h.shape
+    out = np.zeros((batch, hidden), np.float32)
+    lib.mean_pool_masked(_p(h), _p(mask), batch, tokens, hidden, _p(out))
+    return out
+
+
+def normalize_rows(x):
+    lib = _enc()
+    x = _f32(x).copy()
+    lib.normalize_rows(_p(x), x.shape[0], x.shape[1])
+    return x
+
+
+def tiny_embed(table, proj, ids):
+    lib = _enc()
+    table, proj = _f32(table), _f32(proj)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    out = np.zeros((ids.shape[0], proj.shape[1]), np.float32)
+    lib.tiny_embed(_p(table), table.shape[0], table.shape[1], _p(proj), proj.shape[1], _p(ids),
+                   ids.shape[0], _p(out))
+    return out

@@ -1,0 +1,110 @@
+"""GPU parity of the q8 encoder (libeoship on gfx950) against the CPU oracle.
+
+Bar: per sequence, cosine >= 0.9999 and max-abs error
+<= 2e-2 between the GPU embedding and the oracle's, both using the same
+dequantized int8 per-channel weights; the oracle follows the reference's f32/f64
+host path (oracle/encoder_oracle.c)."""
+import numpy as np
+import pytest
+
+import oracle
+from eos_amd import datagen
+from eos_amd.encoder import Encoder
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.9999
+ABS_MAX = 2e-2
+
+
+def _case(name):
+    print(f"[case] {name}", flush=True)
+
+
+def _oracle(w, ids, mask, types=None):
+    return oracle.bert_embed(w.tok, w.pos, w.typ, w.emb_gamma, w.emb_beta,
+                             [L.dequantized() for L in w.layers], ids, mask, types, w.heads,
+                             w.ln_eps)
+
+
+def _check(got, want):
+    n = np.linalg.norm(got, axis=1) * np.linalg.norm(want, axis=1)
+    live = n > 0
+    cos = np.sum(got * want, axis=1)[live] / n[live]
+    err = np.max(np.abs(got - want))
+    print(f"  min cos {cos.min() if live.any() else 1.0:.8f}  max abs {err:.3e}", flush=True)
+    if live.any():
+        assert cos.min() >= COS_MIN
+    assert err <= ABS_MAX
+    np.testing.assert_array_equal(got[~live], want[~live])
+
+
+@pytest.mark.parametrize("hidden,heads,inter,tokens", [(384, 12, 1536, 256), (512, 8, 2048, 300),
+                                                       (768, 12, 3072, 96)])
+def test_encoder_matches_oracle(rt, hidden, heads, inter, tokens):
+    _case(f"encoder H={hidden} heads={heads} F={inter} T={tokens}")
+    w = datagen.bert_q8_weights(2, hidden, heads, inter, 2000, 512, seed=hidden,
+                                random_affine=True)
+    ids, mask, lens = datagen.encoder_batch(6, tokens, 2000, 1, tokens, hidden + 1, hidden + 2)
+    mask[0, :] = (np.arange(tokens) < 1)      # a single active token
+    mask[1, :] = 1                            # full length
+    types = (np.arange(tokens)[None, :] % 2 * mask).astype(np.int32)
+    enc = Encoder(rt, w)
+    got = enc.embed(ids, mask, types)
+    _check(got, _oracle(w, ids, mask, types))
+
+
+def test_encoder_mask_holes_and_empty_sequence(rt):
+    _case("encoder mask holes / empty")
+    w = datagen.bert_q8_weights(1, 384, 12, 1536, 500, 128, seed=3, random_affine=True)
+    ids, mask, _ = datagen.encoder_batch(4, 128, 500, 64, 128, 5, 6)
+    rng = np.random.default_rng(2)
+    mask[2] = (rng.random(128) < 0.5).astype(np.int32)   # holes keep absolute positions
+    mask[3] = 0                                           # no active token -> zeros
+    enc = Encoder(rt, w)
+    got = enc.embed(ids, mask)
+    want = _oracle(w, ids, mask)
+    assert np.all(got[3] == 0) and np.all(want[3] == 0)
+    _check(got, want)
+
+
+def test_encoder_sequences_are_independent(rt):
+    """A sequence's embedding does not depend on the rest of the batch."""
+    _case("encoder batch independence")
+    w = datagen.bert_q8_weights(2, 384, 12, 1536, 1000, 256, seed=4, random_affine=True)
+    ids, mask, _ = datagen.encoder_batch(5, 200, 1000, 10, 200, 7, 8)
+    enc = Encoder(rt, w)
+    full = enc.embed(ids, mask)
+    for b in (0, 3):
+        one = enc.embed(ids[b:b + 1], mask[b:b + 1])
+        np.testing.assert_allclose(one[0], full[b], rtol=0, atol=2e-6)
+
+
+def test_encoder_rejects_out_of_range_ids(rt):
+    _case("encoder id validation")
+    from eos_amd._lib import EosHipError
+    w = datagen.bert_q8_weights(1, 384, 12, 1536, 100, 64, seed=5)
+    enc = Encoder(rt, w)
+    ids = np.zeros((2, 16), np.int32)
+    mask = np.ones((2, 16), np.int32)
+    ids[1, 3] = 100
+    with pytest.raises(EosHipError, match="out of range"):
+        enc.embed(ids, mask)
+    ids[1, 3] = 99
+    enc.embed(ids, mask)
+    with pytest.raises(EosHipError, match="position"):
+        enc.embed(np.zeros((1, 65), np.int32), np.ones((1, 65), np.int32))
+
+
+def test_baseline_c3_full_size(rt):
+    """BASELINE config 3 at full size: 6 layers, hidden 384, 12 heads, FFN
+    1536, batch 64 x 512, lengths U[32, 512]; four sequences checked against
+    the oracle (sequences are independent), all 64 unit-norm."""
+    _case("c3 full size 64 x 512")
+    w = datagen.bert_q8_weights(6, 384, 12, 1536, 30522, 512, seed=7)
+    ids, mask, lens = datagen.encoder_batch(64, 512, 30522, 32, 512, 8, 9)
+    enc = Encoder(rt, w)
+    got = enc.embed(ids, mask)
+    np.testing.assert_allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
+    pick = np.array([0, int(np.argmin(lens)), int(np.argmax(lens)), 37])
+    _check(got[pick], _oracle(w, ids[pick], mask[pick]))
