@@ -53,6 +53,60 @@ def cpu_baseline(corpus, queries, nq_sample: int) -> dict:
     }
 
 
+def encoder_leg(rt, steps: int) -> dict:
+    """q8 BERT-style encoder, 6 layers, hidden 384, 12 heads,
+    FFN 1536, batch 64 x seq 512, lengths U[32, 512]; inputs resident on device."""
+    from eos_amd import datagen
+    from eos_amd.encoder import Encoder
+    from eos_amd.runtime import DeviceBuffer
+
+    L, H, NH, F, B, T = 6, 384, 12, 1536, 64, 512
+    w = datagen.bert_q8_weights(L, H, NH, F, 30522, T, seed=7)
+    ids, mask, lens = datagen.encoder_batch(B, T, 30522, 32, 512, 8, 9)
+    enc = Encoder(rt, w)
+    d_ids = DeviceBuffer.from_array(rt, ids)
+    d_mask = DeviceBuffer.from_array(rt, mask)
+    d_out = DeviceBuffer(rt, B * H * 4)
+    for _ in range(2):
+        enc.embed_device(d_ids, d_mask, B, T, d_out)
+    rt.sync()
+    rt.profile_reset()
+    rt.profile(True)
+    rt.mark(2)
+    for _ in range(steps):
+        enc.embed_device(d_ids, d_mask, B, T, d_out)
+    rt.mark(3)
+    ms = rt.elapsed_ms(2, 3) / steps
+    rt.sync()
+    kernels = {}
+    for name in ("eos_enc_pack", "eos_enc_embed", "enc_gemm_qkv", "eos_enc_attn", "enc_gemm_o_ln",
+                 "enc_gemm_ffn_up", "enc_gemm_ffn_down_ln", "eos_enc_pool"):
+        n, t = rt.profile_read(name)
+        kernels[name] = t / steps
+    rt.profile(False)
+    valid = int(lens.sum())
+    lin = 2.0 * valid * L * (3 * H * H + H * H + 2 * H * F)
+    att = 2.0 * 2.0 * float(np.sum(lens.astype(np.float64) ** 2)) * H * L
+    flops = lin + att
+    achieved = flops / (ms / 1e3) / 1e12
+    enc.release()
+    return {
+        "metric": "q8 encoder tokens/s @seq512",
+        "value": B * T / (ms / 1e3),
+        "unit": "tokens/s (batch x 512 per forward)",
+        "valid_tokens_per_s": valid / (ms / 1e3),
+        "ms_per_forward": ms,
+        "config": {"layers": L, "hidden": H, "heads": NH, "ffn": F, "batch": B, "seq": T,
+                   "valid_tokens": valid},
+        "dtype": "int8 weights (per-channel scales) x f16 activations on f16 MFMA, f32 accumulate",
+        "roofline": {"bound": "mfma", "achieved": achieved, "unit": "TFLOP/s",
+                     "peak_f16": 2500.0, "frac_f16": achieved / 2500.0,
+                     "peak_int8": 5000.0, "frac_int8": achieved / 5000.0,
+                     "flops_per_forward_valid": flops},
+        "breakdown_ms": kernels,
+    }
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -73,6 +127,8 @@ def main() -> int:
     ap.add_argument("--k", type=int, default=100)
     ap.add_argument("--cpu-sample-queries", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-encoder", action="store_true")
+    ap.add_argument("--encoder-steps", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -161,6 +217,11 @@ def main() -> int:
         out["cpu_baseline"] = cpu_baseline(corpus, queries, args.cpu_sample_queries)
     else:
         out["cpu_baseline"] = None
+    idx.release()
+    del corpus
+    if not args.skip_encoder:
+        log("encoder c3")
+        out["encoder_c3"] = encoder_leg(rt, args.encoder_steps)
     rt.close()
     print(json.dumps(out), flush=True)
     return 0
