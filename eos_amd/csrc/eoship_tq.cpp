@@ -30,6 +30,7 @@ using eoship::set_err;
 namespace {
 
 constexpr int kBatch = 64;          // queries per scan (two 32-column groups)
+constexpr int kMaxCols = 128;       // MFMA query columns per pass (MaxSim: four 32-token groups)
 constexpr int kCap = 8192;          // kept candidates per query
 constexpr int kSortCap = 8192;      // largest k the device sort handles
 constexpr int kSampleStride = 32;   // sample every 32nd tile (at least)
@@ -184,30 +185,72 @@ struct EosHipTQ {
     return rt->launch(name, dim3((unsigned)blocks), dim3(256), 0, s, err, labels[s->mode]);
   }
 
-  int prepare(const float* d_queries, int qb, int16_t* qs_out, char** err) {
-    const int nqg = nqg_for(qb);
+  // Rotates and quantizes nsrc source rows into ncols = 32 * nqg MFMA columns:
+  // column c reads source row (c / group) * group_live + c % group when
+  // c % group < group_live, else it is a zero column.
+  int prepare_cols(const float* d_src, int nsrc, int nqg, int group, int group_live,
+                   int16_t* qs_out, char** err) {
     TqPrepArgs p;
     memset(&p, 0, sizeof(p));
-    p.queries = d_queries;
+    p.queries = d_src;
     p.rot_t = rot_t;
     p.bfrag = bfrag;
     p.alpha = alpha;
     p.tau = tau;
     p.cand_count = cand_count;
     p.qs_out = qs_out;
-    p.q = qb;
+    p.q = nsrc;
     p.d = d;
     p.ks = ks;
     p.ncb = 2 * nqg;
     p.qmax = qmax;
     p.cb_scale = cb_scale;
     p.qrot = qrot;
+    p.group = group;
+    p.group_live = group_live;
     if (rot_t != nullptr) {
       const unsigned jblocks = (unsigned)((d + 63) / 64);
-      const unsigned qblocks = (unsigned)((qb + 3) / 4);
+      const unsigned qblocks = (unsigned)((nsrc + 3) / 4);
       if (rt->launch("eos_tq_rotate", dim3(jblocks, qblocks), dim3(256), 0, &p, err) != 0) return 1;
     }
     return rt->launch("eos_tq_quantize", dim3(32 * nqg), dim3(256), 0, &p, err);
+  }
+
+  int prepare(const float* d_queries, int qb, int16_t* qs_out, char** err) {
+    return prepare_cols(d_queries, qb, nqg_for(qb), 1, 1, qs_out, err);
+  }
+
+  int maxsim_nqg() const { return ks <= 8 ? 4 : ks <= 24 ? 2 : 1; }
+
+  // Doc scores of qp queries (tq tokens each, source rows [qp * tq][d]) for
+  // documents [doc_begin, doc_begin + ndocs) into out [qp][ndocs].
+  int maxsim_pass(const float* d_src, int qp, int tq, int doc_len, int64_t doc_begin,
+                  int64_t ndocs, float* out, char** err) {
+    const int nqg = maxsim_nqg();
+    if (prepare_cols(d_src, qp * tq, nqg, 32, tq, nullptr, err) != 0) return 1;
+    TqMaxsimArgs m;
+    memset(&m, 0, sizeof(m));
+    m.packed = static_cast<const int32_t*>(packed);
+    m.norms = norms;
+    m.bfrag = bfrag;
+    m.alpha = alpha;
+    m.out = out;
+    m.doc_begin = doc_begin;
+    m.ndocs = ndocs;
+    m.out_stride = ndocs;
+    m.tiles_per_doc = doc_len / kTile;
+    m.groups = qp;
+    m.lut0 = lut[0];
+    m.lut1 = lut[1];
+    m.lut2 = lut[2];
+    m.lut3 = lut[3];
+    char name[64];
+    snprintf(name, sizeof(name), "eos_tq_maxsim_b%d_k%d_g%d", bits, ks, nqg);
+    int64_t blocks = (ndocs + 3) / 4;
+    const int64_t maxb = (int64_t)rt->compute_units * 2;
+    if (blocks > maxb) blocks = maxb;
+    if (blocks < 1) blocks = 1;
+    return rt->launch(name, dim3((unsigned)blocks), dim3(256), 0, &m, err, "tq_maxsim");
   }
 
   // Exhaustive scores of all queries of the batch into dense [qb][count].
@@ -457,14 +500,14 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
       return fail();
     }
   }
-  const size_t bfrag_bytes = (size_t)tq->ks * 4 * 64 * 16;
+  const size_t bfrag_bytes = (size_t)tq->ks * 8 * 64 * 16;
   tq->samp_tiles = std::min<int64_t>((tq->ntiles + kSampleStride - 1) / kSampleStride, kMaxSampleTiles);
   if (rt->alloc(bfrag_bytes, reinterpret_cast<void**>(&tq->bfrag), err) != 0 ||
-      rt->alloc((size_t)kBatch * tq->d * sizeof(double), reinterpret_cast<void**>(&tq->qrot), err) != 0 ||
-      rt->alloc(kBatch * sizeof(float), reinterpret_cast<void**>(&tq->alpha), err) != 0 ||
-      rt->alloc(kBatch * sizeof(float), reinterpret_cast<void**>(&tq->tau), err) != 0 ||
-      rt->alloc(kBatch * sizeof(uint32_t), reinterpret_cast<void**>(&tq->cand_count), err) != 0 ||
-      rt->alloc(kBatch * sizeof(int), reinterpret_cast<void**>(&tq->status), err) != 0 ||
+      rt->alloc((size_t)kMaxCols * tq->d * sizeof(double), reinterpret_cast<void**>(&tq->qrot), err) != 0 ||
+      rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&tq->alpha), err) != 0 ||
+      rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&tq->tau), err) != 0 ||
+      rt->alloc(kMaxCols * sizeof(uint32_t), reinterpret_cast<void**>(&tq->cand_count), err) != 0 ||
+      rt->alloc(kMaxCols * sizeof(int), reinterpret_cast<void**>(&tq->status), err) != 0 ||
       rt->alloc((size_t)kBatch * kCap * sizeof(unsigned long long),
                 reinterpret_cast<void**>(&tq->cand), err) != 0 ||
       rt->alloc((size_t)kBatch * std::max<int64_t>(tq->samp_tiles, 1) * sizeof(float),
@@ -609,6 +652,131 @@ int eoship_tq_prepare(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int
                          rt->stream);
       if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(alpha)", e);
     }
+    if (rt->sync(err) != 0) return 1;
+  }
+  return 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+int maxsim_check(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, int32_t q, int32_t tq_tokens,
+                 const char* what, char** err) {
+  if (rt == nullptr || tq == nullptr) return set_err(err, "%s: NULL runtime or corpus", what);
+  if (tq->rt != rt) return set_err(err, "%s: corpus was bound on another runtime", what);
+  if (q < 0) return set_err(err, "%s: negative query count", what);
+  if (doc_len <= 0 || doc_len % kTile != 0)
+    return set_err(err, "%s: doc_len must be a positive multiple of %d (got %d)", what, kTile, doc_len);
+  if (tq->n % doc_len != 0)
+    return set_err(err, "%s: corpus size %lld is not a whole number of %d-vector documents", what,
+                   (long long)tq->n, doc_len);
+  if (tq_tokens < 1 || tq_tokens > 32)
+    return set_err(err, "%s: query tokens must be in [1, 32] (got %d)", what, tq_tokens);
+  return 0;
+}
+
+int maxsim_topk_impl(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const float* d_queries,
+                     int32_t q, int32_t tq_tokens, int32_t k, int64_t* d_ids, float* d_scores,
+                     char** err) {
+  const int64_t ndocs = tq->n / doc_len;
+  const int64_t kk64 = (k <= 0 || (int64_t)k > ndocs) ? ndocs : k;
+  if (q == 0 || kk64 == 0) return 0;
+  if (kk64 > kSortCap)
+    return set_err(err, "eoship_tq_maxsim_topk: k=%lld exceeds the device top-k limit of %d",
+                   (long long)kk64, kSortCap);
+  const int kk = (int)kk64;
+  const int per = tq->maxsim_nqg();
+  if (tq->ensure(reinterpret_cast<void**>(&tq->dense), &tq->dense_bytes,
+                 (size_t)per * (size_t)ndocs * sizeof(float), err) != 0)
+    return 1;
+  for (int q0 = 0; q0 < q; q0 += per) {
+    const int qp = std::min(per, q - q0);
+    if (tq->maxsim_pass(d_queries + (size_t)q0 * tq_tokens * tq->d, qp, tq_tokens, doc_len, 0, ndocs,
+                        tq->dense, err) != 0)
+      return 1;
+    TqSelectArgs sel;
+    memset(&sel, 0, sizeof(sel));
+    sel.rows = tq->dense;
+    sel.ids = reinterpret_cast<long long*>(d_ids + (size_t)q0 * kk);
+    sel.scores = d_scores + (size_t)q0 * kk;
+    sel.n = ndocs;
+    sel.stride = ndocs;
+    sel.kk = kk;
+    sel.mode = 1;
+    sel.nrows = qp;
+    if (rt->launch("eos_tq_row_select", dim3(qp), dim3(1024), 0, &sel, err, "tq_maxsim_select") != 0)
+      return 1;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int eoship_tq_maxsim_topk_device(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len,
+                                 const float* d_queries, int32_t q, int32_t tq_tokens, int32_t k,
+                                 int64_t* d_ids, float* d_scores, char** err) {
+  if (maxsim_check(rt, tq, doc_len, q, tq_tokens, "eoship_tq_maxsim_topk_device", err) != 0) return 1;
+  if (q > 0 && (d_queries == nullptr || d_ids == nullptr || d_scores == nullptr))
+    return set_err(err, "eoship_tq_maxsim_topk_device: NULL buffer");
+  return maxsim_topk_impl(rt, tq, doc_len, d_queries, q, tq_tokens, k, d_ids, d_scores, err);
+}
+
+int eoship_tq_maxsim_topk(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const float* queries,
+                          int32_t q, int32_t tq_tokens, int32_t k, int64_t* ids, float* scores,
+                          char** err) {
+  if (maxsim_check(rt, tq, doc_len, q, tq_tokens, "eoship_tq_maxsim_topk", err) != 0) return 1;
+  const int64_t ndocs = tq->n / doc_len;
+  const int64_t kk = (k <= 0 || (int64_t)k > ndocs) ? ndocs : k;
+  if (q == 0 || kk == 0) return 0;
+  if (queries == nullptr || ids == nullptr || scores == nullptr)
+    return set_err(err, "eoship_tq_maxsim_topk: NULL buffer");
+  const size_t qbytes = (size_t)q * tq_tokens * tq->d * sizeof(float);
+  const size_t ibytes = (size_t)q * kk * sizeof(int64_t);
+  const size_t sbytes = (size_t)q * kk * sizeof(float);
+  if (tq->ensure(&tq->io, &tq->io_bytes, qbytes + ibytes + sbytes + 256, err) != 0) return 1;
+  char* base = static_cast<char*>(tq->io);
+  float* dq = reinterpret_cast<float*>(base);
+  int64_t* di = reinterpret_cast<int64_t*>(base + ((qbytes + 15) & ~(size_t)15));
+  float* ds = reinterpret_cast<float*>(reinterpret_cast<char*>(di) + ibytes);
+  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
+  if (maxsim_topk_impl(rt, tq, doc_len, dq, q, tq_tokens, k, di, ds, err) != 0) return 1;
+  e = hipMemcpyAsync(ids, di, ibytes, hipMemcpyDeviceToHost, rt->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(scores, ds, sbytes, hipMemcpyDeviceToHost, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(results)", e);
+  return rt->sync(err);
+}
+
+int eoship_tq_maxsim_scores(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const float* queries,
+                            int32_t q, int32_t tq_tokens, int64_t doc_begin, int64_t doc_count,
+                            float* scores, char** err) {
+  if (maxsim_check(rt, tq, doc_len, q, tq_tokens, "eoship_tq_maxsim_scores", err) != 0) return 1;
+  const int64_t ndocs = tq->n / doc_len;
+  if (doc_begin < 0 || doc_count < 0 || doc_begin + doc_count > ndocs)
+    return set_err(err, "eoship_tq_maxsim_scores: documents [%lld, %lld) outside [0, %lld)",
+                   (long long)doc_begin, (long long)(doc_begin + doc_count), (long long)ndocs);
+  if (q == 0 || doc_count == 0) return 0;
+  if (queries == nullptr || scores == nullptr) return set_err(err, "eoship_tq_maxsim_scores: NULL buffer");
+  const size_t qbytes = (size_t)q * tq_tokens * tq->d * sizeof(float);
+  if (tq->ensure(&tq->io, &tq->io_bytes, qbytes, err) != 0) return 1;
+  float* dq = static_cast<float*>(tq->io);
+  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
+  const int per = tq->maxsim_nqg();
+  if (tq->ensure(reinterpret_cast<void**>(&tq->dense), &tq->dense_bytes,
+                 (size_t)per * (size_t)doc_count * sizeof(float), err) != 0)
+    return 1;
+  for (int q0 = 0; q0 < q; q0 += per) {
+    const int qp = std::min(per, q - q0);
+    if (tq->maxsim_pass(dq + (size_t)q0 * tq_tokens * tq->d, qp, tq_tokens, doc_len, doc_begin,
+                        doc_count, tq->dense, err) != 0)
+      return 1;
+    e = hipMemcpyAsync(scores + (size_t)q0 * doc_count, tq->dense,
+                       (size_t)qp * doc_count * sizeof(float), hipMemcpyDeviceToHost, rt->stream);
+    if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(scores)", e);
     if (rt->sync(err) != 0) return 1;
   }
   return 0;

@@ -17,6 +17,10 @@ struct TqPrepArgs {
   double* qrot;          // [32*ncb/2][d] rotated queries (written by eos_tq_rotate)
   int q, d, ks, ncb, qmax;
   float cb_scale;
+  // Column -> source row: column c belongs to group c / group (a query of the
+  // pass) and slot c % group; slots >= group_live are zero columns. The flat
+  // scan uses group = group_live = 1 (column c = query c).
+  int group, group_live;
 };
 
 struct TqPackArgs {
@@ -71,6 +75,23 @@ struct TqFinalizeArgs {
   float* scores;      // [q][kk]
   int* status;        // [q]: 0 ok, 1 too few candidates, 2 overflow
   int cap, kk, q;
+};
+
+// MaxSim over documents of tiles_per_doc consecutive tiles: per query group
+// g (32 token columns) and document, the pairwise-tree sum over the 32 token
+// slots of each token's best score in the document.
+struct TqMaxsimArgs {
+  const int32_t* packed;
+  const float* norms;
+  const int8_t* bfrag;
+  const float* alpha;      // [32*nqg] per token column
+  float* out;              // [groups][out_stride]
+  long long doc_begin;     // first document
+  long long ndocs;         // documents in this launch
+  long long out_stride;
+  int tiles_per_doc;
+  int groups;              // live query groups (<= nqg)
+  uint32_t lut0, lut1, lut2, lut3;
 };
 
 #endif  // EOSHIP_TQ_ARGS_H

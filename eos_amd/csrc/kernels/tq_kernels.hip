@@ -103,9 +103,11 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_rotate(TqPrepArgs a) {
 // threshold and candidate count for the scan that follows.
 extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) {
   __shared__ double red[256];
-  const int qi = blockIdx.x;
+  const int qi = blockIdx.x;  // column
   const int tid = threadIdx.x;
-  const bool live = qi < a.q;
+  const int grp = qi / a.group, slot = qi - grp * a.group;
+  const int src = grp * a.group_live + slot;  // source row
+  const bool live = src < a.q && slot < a.group_live;
   const int dpad = a.ks * 32;
   double qr[kMaxDim / 256];
   double mx = 0.0;
@@ -114,7 +116,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) 
     const int j = tid + 256 * r;
     double v = 0.0;
     if (live && j < a.d)
-      v = a.rot_t != nullptr ? a.qrot[(size_t)qi * a.d + j] : (double)a.queries[(size_t)qi * a.d + j];
+      v = a.rot_t != nullptr ? a.qrot[(size_t)src * a.d + j] : (double)a.queries[(size_t)src * a.d + j];
     qr[r] = v;
     mx = fmax(mx, fabs(v));
   }
@@ -137,7 +139,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) 
       double v = rint(qr[r] * inv);
       v = fmin(fmax(v, (double)-a.qmax), (double)a.qmax);
       qs = (int)v;
-      if (live && a.qs_out != nullptr) a.qs_out[(size_t)qi * a.d + j] = (int16_t)qs;
+      if (live && a.qs_out != nullptr) a.qs_out[(size_t)src * a.d + j] = (int16_t)qs;
     }
     const int lo = ((qs + 128) & 255) - 128;
     const int hi = (qs - lo) >> 8;
@@ -757,3 +759,123 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
   }
   if (tid == 0) a.status[row] = 0;
 }
+
+// ------------------------------------------------------------------ maxsim
+
+namespace {
+
+template <int BITS, int KS, int NQG>
+EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
+  constexpr int NCB = 2 * NQG;
+  constexpr int SPL = 8 / BITS;
+  constexpr int NLOAD = (KS + SPL - 1) / SPL;
+  __shared__ v4i sb[KS * NCB * 64];
+  {
+    const v4i* src = reinterpret_cast<const v4i*>(a.bfrag);
+    for (int i = threadIdx.x; i < KS * NCB * 64; i += kScanThreads) sb[i] = src[i];
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = gridDim.x * (kScanThreads / 64);
+  const int half = lane >> 5;
+  const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
+  TqScanArgs la;  // lookup tables for decode_step
+  la.lut0 = a.lut0;
+  la.lut1 = a.lut1;
+  la.lut2 = a.lut2;
+  la.lut3 = a.lut3;
+  float al[NQG];
+#pragma unroll
+  for (int g = 0; g < NQG; ++g) al[g] = a.alpha[g * 32 + (lane & 31)];
+  for (long long doc = blockIdx.x * (kScanThreads / 64) + wave; doc < a.ndocs; doc += nw) {
+    float mx[NQG];
+#pragma unroll
+    for (int g = 0; g < NQG; ++g) mx[g] = -__builtin_inff();
+    const long long t0 = (a.doc_begin + doc) * a.tiles_per_doc;
+    v4i raw[NLOAD];
+    float4 nrm4[4];
+    load_tile_codes<NLOAD>(raw, packed, t0, lane);
+    load_tile_norms(nrm4, a.norms, t0, half);
+    for (int t = 0; t < a.tiles_per_doc; ++t) {
+      v4i nraw[NLOAD];
+      float4 nnrm4[4];
+      if (t + 1 < a.tiles_per_doc) {
+        load_tile_codes<NLOAD>(nraw, packed, t0 + t + 1, lane);
+        load_tile_norms(nnrm4, a.norms, t0 + t + 1, half);
+      }
+      int boff = lane;
+      asm volatile("" : "+v"(boff));
+      v16i acc[NCB];
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
+#pragma unroll
+      for (int c = 0; c < NLOAD; ++c) {
+#pragma unroll
+        for (int h = 0; h < SPL; ++h) {
+          const int s = c * SPL + h;
+          if (s < KS) {
+            const v4i af = decode_step<BITS>(raw[c], h, la);
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+              const v4i bf = sb[(s * NCB + cb) * 64 + boff];
+              acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, acc[cb], 0, 0, 0);
+            }
+          }
+        }
+      }
+      float nrm[16];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        nrm[4 * i4 + 0] = nrm4[i4].x;
+        nrm[4 * i4 + 1] = nrm4[i4].y;
+        nrm[4 * i4 + 2] = nrm4[i4].z;
+        nrm[4 * i4 + 3] = nrm4[i4].w;
+      }
+#pragma unroll
+      for (int g = 0; g < NQG; ++g) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int dot = acc[2 * g][i] * 256 + acc[2 * g + 1][i];
+          mx[g] = fmaxf(mx[g], ((float)dot * al[g]) * nrm[i] + 0.0f);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < NLOAD; ++c) raw[c] = nraw[c];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) nrm4[i4] = nnrm4[i4];
+    }
+#pragma unroll
+    for (int g = 0; g < NQG; ++g) {
+      float v = fmaxf(mx[g], __shfl_xor(mx[g], 32));  // token max over the document
+#pragma unroll
+      for (int o = 1; o < 32; o <<= 1) v = v + __shfl_xor(v, o);
+      if (lane == 0 && g < a.groups) a.out[(size_t)g * a.out_stride + doc] = v;
+    }
+  }
+}
+
+}  // namespace
+
+#define EOS_TQ_MAXSIM(BITS, KS, NQG)                                                        \
+  extern "C" __global__ __launch_bounds__(kScanThreads) void eos_tq_maxsim_b##BITS##_k##KS##_g##NQG( \
+      TqMaxsimArgs a) {                                                                     \
+    tq_maxsim_body<BITS, KS, NQG>(a);                                                       \
+  }
+
+EOS_TQ_MAXSIM(2, 1, 4)
+EOS_TQ_MAXSIM(2, 2, 4)
+EOS_TQ_MAXSIM(2, 4, 4)
+EOS_TQ_MAXSIM(2, 8, 4)
+EOS_TQ_MAXSIM(2, 12, 2)
+EOS_TQ_MAXSIM(2, 16, 2)
+EOS_TQ_MAXSIM(2, 24, 2)
+EOS_TQ_MAXSIM(2, 32, 1)
+EOS_TQ_MAXSIM(4, 1, 4)
+EOS_TQ_MAXSIM(4, 2, 4)
+EOS_TQ_MAXSIM(4, 4, 4)
+EOS_TQ_MAXSIM(4, 8, 4)
+EOS_TQ_MAXSIM(4, 12, 2)
+EOS_TQ_MAXSIM(4, 16, 2)
+EOS_TQ_MAXSIM(4, 24, 2)
+EOS_TQ_MAXSIM(4, 32, 1)

@@ -148,6 +148,53 @@ class TurboQuantIndex:
         return qs, alpha
 
 
+class TurboQuantMultiVectorIndex:
+    """A bound corpus viewed as documents of doc_len consecutive vectors
+    (the multivector children of runtime/retrieval_multivector_turboquant.go:
+    546-605), scored by MaxSim: sum over query tokens of the best child score."""
+
+    def __init__(self, index: TurboQuantIndex, doc_len: int):
+        if doc_len <= 0 or doc_len % 32 or index.n % doc_len:
+            raise ValueError("doc_len must be a multiple of 32 dividing the corpus size")
+        self.index, self.doc_len = index, doc_len
+        self.ndocs = index.n // doc_len
+
+    def _queries(self, queries: np.ndarray) -> np.ndarray:
+        q = np.ascontiguousarray(queries, dtype=np.float32)
+        if q.ndim == 2:
+            q = q[:, None, :]
+        if q.ndim != 3 or q.shape[2] != self.index.dim or not 1 <= q.shape[1] <= 32:
+            raise ValueError(f"queries must be [Q, tokens<=32, {self.index.dim}]")
+        return q
+
+    def top_k(self, queries: np.ndarray, top_k: int):
+        q = self._queries(queries)
+        kk = self.ndocs if (top_k <= 0 or top_k > self.ndocs) else int(top_k)
+        ids = np.zeros((q.shape[0], kk), np.int64)
+        scores = np.zeros((q.shape[0], kk), np.float32)
+        _lib.call("eoship_tq_maxsim_topk", self.index.rt.handle, self.index.handle,
+                  C.c_int32(self.doc_len), q.ctypes.data_as(C.c_void_p), C.c_int32(q.shape[0]),
+                  C.c_int32(q.shape[1]), C.c_int32(int(top_k)), ids.ctypes.data_as(C.c_void_p),
+                  scores.ctypes.data_as(C.c_void_p))
+        return ids, scores
+
+    def top_k_device(self, d_queries: DeviceBuffer, nq: int, tokens: int, top_k: int,
+                     d_ids: DeviceBuffer, d_scores: DeviceBuffer) -> None:
+        _lib.call("eoship_tq_maxsim_topk_device", self.index.rt.handle, self.index.handle,
+                  C.c_int32(self.doc_len), d_queries.ptr, C.c_int32(nq), C.c_int32(tokens),
+                  C.c_int32(int(top_k)), d_ids.ptr, d_scores.ptr)
+
+    def scores(self, queries: np.ndarray, doc_begin: int = 0, doc_count: int | None = None):
+        q = self._queries(queries)
+        doc_count = self.ndocs - doc_begin if doc_count is None else int(doc_count)
+        out = np.zeros((q.shape[0], doc_count), np.float32)
+        _lib.call("eoship_tq_maxsim_scores", self.index.rt.handle, self.index.handle,
+                  C.c_int32(self.doc_len), q.ctypes.data_as(C.c_void_p), C.c_int32(q.shape[0]),
+                  C.c_int32(q.shape[1]), C.c_int64(doc_begin), C.c_int64(doc_count),
+                  out.ctypes.data_as(C.c_void_p))
+        return out
+
+
 def top_turboquant_retrieval_scores_with_stats(index: TurboQuantIndex, queries: np.ndarray,
                                                top_k: int):
     """Per query, the ranked [RetrievalScoredDoc] list and the run's stats."""

@@ -130,6 +130,28 @@ int eoship_tq_scores(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int3
 int eoship_tq_prepare(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int32_t q,
                       int16_t* qs, float* alpha, char** err);
 
+/* Multivector late interaction (MaxSim) over a bound corpus grouped into
+ * documents of doc_len consecutive vectors (doc_len a multiple of 32, corpus
+ * size a whole number of documents). A query is tq_tokens (1..32) token
+ * vectors; its score for a document is the sum, as a pairwise tree over 32
+ * token slots (slot i += slot i^o for o = 1, 2, 4, 8, 16; missing tokens
+ * contribute +0), of each token's best per-vector TurboQuant score in the
+ * document. With one token this is the reference child-max
+ * (runtime/retrieval_multivector_turboquant.go:746-783, 785-810 with "max"
+ * aggregation); parents rank by score desc, id asc (:890-908).
+ * queries [Q][tq_tokens][d]; ids/scores [Q][min(k, ndocs)]. */
+int eoship_tq_maxsim_topk(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const float* queries,
+                          int32_t q, int32_t tq_tokens, int32_t k, int64_t* ids, float* scores,
+                          char** err);
+int eoship_tq_maxsim_topk_device(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len,
+                                 const float* d_queries, int32_t q, int32_t tq_tokens, int32_t k,
+                                 int64_t* d_ids, float* d_scores, char** err);
+/* Exhaustive MaxSim document scores for documents [doc_begin, doc_begin +
+ * doc_count) (host output [Q][doc_count]). */
+int eoship_tq_maxsim_scores(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const float* queries,
+                            int32_t q, int32_t tq_tokens, int64_t doc_begin, int64_t doc_count,
+                            float* scores, char** err);
+
 /* ---------------------------------------------------------------- encoder */
 
 typedef struct EosHipEncoder EosHipEncoder;

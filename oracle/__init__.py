@@ -45,6 +45,9 @@ def load() -> C.CDLL:
     lib.tq_topk.restype = C.c_int64
     lib.topk_scores.argtypes = [P, C.c_int64, C.c_int, P, P]
     lib.topk_scores.restype = C.c_int64
+    lib.tq_maxsim_scores.argtypes = [P, C.c_int, C.c_int, P, C.c_int, C.c_int, P, C.c_float, P, P,
+                                     C.c_int64, C.c_int, P]
+    lib.tq_maxsim_scores.restype = None
     _lib = lib
     return lib
 
@@ -132,6 +135,24 @@ def topk_scores(scores: np.ndarray, k: int):
     out = np.zeros(kk, np.float32)
     load().topk_scores(_p(s), n, int(k), _p(ids), _p(out))
     return ids, out
+
+
+def tq_maxsim_scores(queries, rotation, dim, bits, codebook, codebook_scale, codes, norms,
+                     doc_len):
+    """queries [Q, tokens, dim] -> doc scores [Q, ndocs]."""
+    q = _f32(queries)
+    if q.ndim == 2:
+        q = q[:, None, :]
+    rot = None if rotation is None else _f32(rotation)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    norms = _f32(norms)
+    cb = np.ascontiguousarray(codebook, dtype=np.int8)
+    ndocs = codes.shape[0] // doc_len
+    out = np.zeros((q.shape[0], ndocs), np.float32)
+    load().tq_maxsim_scores(_p(q), q.shape[0], q.shape[1], _p(rot), dim, bits, _p(cb),
+                            C.c_float(codebook_scale), _p(codes), _p(norms), ndocs, doc_len,
+                            _p(out))
+    return out
 
 
 # ------------------------------------------------------------------ encoder

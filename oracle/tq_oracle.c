@@ -263,3 +263,51 @@ int64_t topk_scores(const float* s, int64_t n, int k, int64_t* ids, float* out) 
   free(heap);
   return kk;
 }
+
+/* ------------------------------------------------------------- MaxSim
+ * Build-defined late interaction over the same per-pair score as the flat
+ * scan: for query token i and document vector v, s_iv = tq score; the token's
+ * document score is max_v s_iv (the reference child-max,
+ * runtime/retrieval_multivector_turboquant.go:746-783 with "max"
+ * aggregation, :785-810), and the document score is the sum over the 32
+ * token slots (tokens past tq_tokens are zero vectors and contribute +0) as
+ * a pairwise tree: at step o = 1, 2, 4, 8, 16 slot i becomes s_i + s_(i^o);
+ * slot 0 is the result. With one token this is exactly the child max. */
+void tq_maxsim_scores(const float* queries, int nq, int tq_tokens, const float* rot, int d,
+                      int bits, const int8_t* cb, float cb_scale, const uint8_t* codes,
+                      const float* norms, int64_t ndocs, int doc_len, float* out) {
+  const int qmax = tq_qmax(cb, 1 << bits, d);
+  const int row_bytes = (d * bits + 7) / 8;
+  int16_t* qs = (int16_t*)malloc(sizeof(int16_t) * (size_t)d * 32);
+  float alpha[32];
+  int32_t* dots = (int32_t*)malloc(sizeof(int32_t) * (size_t)doc_len);
+  float* zero = (float*)calloc((size_t)d, sizeof(float));
+  for (int q = 0; q < nq; ++q) {
+    for (int t = 0; t < 32; ++t) {
+      const float* src = t < tq_tokens ? queries + ((size_t)q * tq_tokens + t) * d : zero;
+      tq_prepare(src, rot, d, qmax, cb_scale, qs + (size_t)t * d, &alpha[t]);
+    }
+    for (int64_t doc = 0; doc < ndocs; ++doc) {
+      float slot[32];
+      for (int t = 0; t < 32; ++t) {
+        tq_dots(qs + (size_t)t * d, d, codes + (size_t)doc * doc_len * row_bytes, doc_len, bits, cb,
+                dots);
+        float m = -INFINITY;
+        for (int v = 0; v < doc_len; ++v) {
+          const float s = tq_score(dots[v], alpha[t], norms[doc * doc_len + v]);
+          if (s > m) m = s;
+        }
+        slot[t] = m;
+      }
+      for (int o = 1; o < 32; o <<= 1) {
+        float nxt[32];
+        for (int t = 0; t < 32; ++t) nxt[t] = slot[t] + slot[t ^ o];
+        memcpy(slot, nxt, sizeof(slot));
+      }
+      out[(size_t)q * ndocs + doc] = slot[0];
+    }
+  }
+  free(qs);
+  free(dots);
+  free(zero);
+}

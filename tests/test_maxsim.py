@@ -1,0 +1,118 @@
+"""MaxSim (multivector late interaction) on the TurboQuant scan.
+
+CPU: the oracle's MaxSim is pinned to the flat scorer -- with one query token
+it equals the reference child-max (per document, the best child score,
+runtime/retrieval_multivector_turboquant.go:746-783), and the token sum is
+the stated pairwise tree. GPU: document scores and top-k ids are bit-exact
+against the oracle; at BASELINE config 5 size (100k docs x 128 vectors,
+d = 128, 2-bit, 32 queries x 32 tokens) the device top-k must equal the sort
+of the device's exhaustive document scores, and those equal the oracle's on a
+sampled subset of documents."""
+import numpy as np
+import pytest
+
+import oracle
+from eos_amd import datagen
+
+
+def _corpus(ndocs, doc_len, d, bits, seed=31):
+    return datagen.TurboQuantCorpus(ndocs * doc_len, d, bits, seed, seed + 1, seed + 2)
+
+
+def _tokens(q, t, d, seed):
+    return datagen.unit_rows(datagen.normal(seed, q * t * d).reshape(q, t, d)).astype(np.float32)
+
+
+def test_one_token_is_child_max():
+    c = _corpus(20, 64, 64, 2)
+    q = _tokens(3, 1, 64, 5)
+    ms = oracle.tq_maxsim_scores(q, c.rotation, 64, 2, c.codebook, c.codebook_scale, c.codes,
+                                 c.norms, 64)
+    _, flat = oracle.tq_scores(q[:, 0], c.rotation, 64, 2, c.codebook, c.codebook_scale, c.codes,
+                               c.norms)
+    np.testing.assert_array_equal(ms, flat.reshape(3, 20, 64).max(axis=2))
+
+
+def test_token_sum_is_pairwise_tree():
+    c = _corpus(10, 32, 32, 4)
+    q = _tokens(2, 7, 32, 6)
+    ms = oracle.tq_maxsim_scores(q, c.rotation, 32, 4, c.codebook, c.codebook_scale, c.codes,
+                                 c.norms, 32)
+    per_tok = np.stack([oracle.tq_scores(q[:, t], c.rotation, 32, 4, c.codebook,
+                                         c.codebook_scale, c.codes, c.norms)[1]
+                        .reshape(2, 10, 32).max(axis=2) for t in range(7)], axis=2)
+    slots = np.zeros((2, 10, 32), np.float32)
+    slots[:, :, :7] = per_tok
+    for o in (1, 2, 4, 8, 16):
+        slots = (slots + slots[:, :, np.arange(32) ^ o]).astype(np.float32)
+    np.testing.assert_array_equal(ms, slots[:, :, 0])
+    # and it is the plain sum up to f32 rounding
+    np.testing.assert_allclose(ms, per_tok.astype(np.float64).sum(axis=2), rtol=1e-5, atol=1e-6)
+
+
+def _dev_index(rt, c):
+    from eos_amd.turboquant import TurboQuantIndex
+    return TurboQuantIndex(rt, c.codes, c.norms, c.dim, c.bits, c.codebook, c.codebook_scale,
+                           c.rotation)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("bits,d,doc_len,ntok,nq", [(2, 128, 128, 32, 9), (4, 384, 64, 5, 4),
+                                                    (2, 64, 32, 1, 6), (4, 128, 96, 32, 1)])
+def test_maxsim_matches_oracle(rt, bits, d, doc_len, ntok, nq):
+    print(f"[case] maxsim bits={bits} d={d} doc_len={doc_len} tokens={ntok} Q={nq}", flush=True)
+    from eos_amd.turboquant import TurboQuantMultiVectorIndex
+    c = _corpus(300, doc_len, d, bits, seed=d + bits)
+    q = _tokens(nq, ntok, d, 7)
+    mv = TurboQuantMultiVectorIndex(_dev_index(rt, c), doc_len)
+    got = mv.scores(q)
+    want = oracle.tq_maxsim_scores(q, c.rotation, d, bits, c.codebook, c.codebook_scale, c.codes,
+                                   c.norms, doc_len)
+    np.testing.assert_array_equal(got, want)
+    sub = mv.scores(q, 17, 100)
+    np.testing.assert_array_equal(sub, want[:, 17:117])
+    for k in (1, 10, 100, 0):
+        ids, sc = mv.top_k(q, k)
+        kk = 300 if k <= 0 else k
+        for i in range(nq):
+            order = np.lexsort((np.arange(300), -want[i]))[:kk]
+            np.testing.assert_array_equal(ids[i], order)
+            np.testing.assert_array_equal(sc[i], want[i][order])
+
+
+@pytest.mark.gpu
+def test_maxsim_rejects_bad_shapes(rt):
+    print("[case] maxsim validation", flush=True)
+    from eos_amd._lib import EosHipError
+    from eos_amd.turboquant import TurboQuantMultiVectorIndex
+    c = _corpus(4, 64, 64, 2)
+    idx = _dev_index(rt, c)
+    with pytest.raises(ValueError):
+        TurboQuantMultiVectorIndex(idx, 48)
+    mv = TurboQuantMultiVectorIndex(idx, 64)
+    with pytest.raises(ValueError):
+        mv.top_k(np.zeros((1, 33, 64), np.float32), 1)
+    mv.doc_len = 96  # bypass the host check: the library must refuse too
+    with pytest.raises(EosHipError):
+        mv.scores(np.zeros((1, 2, 64), np.float32), 0, 1)
+
+
+@pytest.mark.gpu
+def test_baseline_c5_full_size(rt):
+    print("[case] c5 full size 100k x 128 x 128", flush=True)
+    from eos_amd.turboquant import TurboQuantMultiVectorIndex
+    c = datagen.TurboQuantCorpus(100_000 * 128, 128, 2, 11, 12, 13)
+    q = _tokens(32, 32, 128, 14)
+    mv = TurboQuantMultiVectorIndex(_dev_index(rt, c), 128)
+    ids, sc = mv.top_k(q, 100)
+    dense = mv.scores(q)
+    for i in range(32):
+        order = np.argsort(-dense[i], kind="stable")[:100]
+        np.testing.assert_array_equal(ids[i], order)
+        np.testing.assert_array_equal(sc[i], dense[i][order])
+    docs = np.unique(np.concatenate([ids[:2].ravel(), np.arange(0, 100_000, 1000)]))
+    sub_codes = c.codes.reshape(100_000, 128, -1)[docs].reshape(-1, c.codes.shape[1])
+    sub_norms = c.norms.reshape(100_000, 128)[docs].reshape(-1)
+    want = oracle.tq_maxsim_scores(q[:2], c.rotation, 128, 2, c.codebook, c.codebook_scale,
+                                   sub_codes, sub_norms, 128)
+    np.testing.assert_array_equal(dense[:2, docs], want)
