@@ -108,6 +108,13 @@ _SIGNATURES = {
                                      C.c_int),
     "eoship_tq_maxsim_scores": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int32,
                                  C.c_int64, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_embed_bind": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_int32,
+                           C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_embed_release": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_embed_run": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p],
+                         C.c_int),
+    "eoship_embed_run_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p,
+                                 C.c_void_p], C.c_int),
     "eoship_encoder_bind": ([C.c_void_p, C.POINTER(EosHipEncoderDesc), _F32P, _F32P, _F32P, _F32P,
                              _F32P, C.POINTER(EosHipEncoderLayer), C.POINTER(C.c_void_p),
                              C.c_void_p], C.c_int),

@@ -34,6 +34,7 @@ HOST_SOURCES = [
     os.path.join(CSRC, "eoship_runtime.cpp"),
     os.path.join(CSRC, "eoship_tq.cpp"),
     os.path.join(CSRC, "eoship_encoder.cpp"),
+    os.path.join(CSRC, "eoship_embed.cpp"),
 ]
 
 # Packed-FP32 instructions are disabled for every device build.

@@ -84,4 +84,16 @@ struct EncPoolArgs {
   int batch, hidden;
 };
 
+// Tiny embed pipeline (examples/embed.eos): gather f16 table rows, multiply by
+// an f16 [dim][edim] projection (f32, k ascending), L2-normalize each row,
+// f16 out.
+struct EmbedTinyArgs {
+  const uint16_t* table;   // [vocab][dim] f16
+  const uint16_t* proj;    // [dim][edim] f16
+  const int32_t* tokens;   // [n]
+  uint16_t* out;           // [n][edim] f16
+  int32_t* status;         // set to 1 on an out-of-range token
+  int n, vocab, dim, edim;
+};
+
 #endif  // EOSHIP_ENC_ARGS_H

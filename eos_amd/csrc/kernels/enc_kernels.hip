@@ -513,3 +513,50 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
   const float norm = sqrtf(tot);
   if (c < a.hidden) a.out[(size_t)b * a.hidden + c] = norm > 0.f ? v / norm : v;
 }
+
+// ------------------------------------------------------------- tiny embed
+
+// examples/embed.eos on one wavefront per token: gather (tensor_ops.go:
+// 938-1166), f32 matmul with k ascending and separate multiply / add
+// (matmulTensor, tensor_ops.go:1168-1249), then normalizeRows
+// (tensor_ops.go:1367-1391): f64 sum of squares in column order, f32 norm,
+// rows of norm 0 unchanged; stored as f16.
+extern "C" __global__ __launch_bounds__(256) void eos_embed_tiny(EmbedTinyArgs a) {
+  __shared__ float xs[4][1024];
+  __shared__ float ys[4][1024];
+  __shared__ float nrm[4];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + w;
+  const bool live = row < a.n;
+  int tok = live ? a.tokens[row] : 0;
+  if (tok < 0 || tok >= a.vocab) {
+    if (lane == 0) *a.status = 1;
+    tok = 0;
+  }
+  for (int k = lane; k < a.dim; k += 64) xs[w][k] = h2f(a.table[(size_t)tok * a.dim + k]);
+  __syncthreads();
+  for (int e = lane; e < a.edim; e += 64) {
+    float acc = 0.0f;
+    for (int k = 0; k < a.dim; ++k) {
+      const float p = xs[w][k] * h2f(a.proj[(size_t)k * a.edim + e]);
+      acc = acc + p;
+    }
+    ys[w][e] = acc;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    double ss = 0.0;
+    for (int e = 0; e < a.edim; ++e) {
+      const double v = (double)ys[w][e];
+      ss = ss + v * v;
+    }
+    nrm[w] = (float)sqrt(ss);
+  }
+  __syncthreads();
+  if (!live) return;
+  const float nv = nrm[w];
+  for (int e = lane; e < a.edim; e += 64) {
+    const float v = ys[w][e];
+    a.out[(size_t)row * a.edim + e] = f2h(nv == 0.0f ? v : v / nv);
+  }
+}

@@ -181,3 +181,41 @@ class Encoder:
         st = C.c_int32()
         _lib.call("eoship_encoder_status", self.rt.handle, self.handle, C.byref(st))
         return st.value
+
+
+class TinyEmbed:
+    """The examples/embed.eos pipeline (gather -> matmul -> l2_normalize) with
+    f16 weights resident on the device; ``embed(tokens)`` returns f16 [T, E]."""
+
+    def __init__(self, rt: Runtime, token_embedding: np.ndarray, projection: np.ndarray):
+        table = np.ascontiguousarray(token_embedding, dtype=np.float16)
+        proj = np.ascontiguousarray(projection, dtype=np.float16)
+        if table.ndim != 2 or proj.ndim != 2 or proj.shape[0] != table.shape[1]:
+            raise ValueError("token_embedding [V, D] and projection [D, E] required")
+        self.rt, self.edim = rt, proj.shape[1]
+        self.handle = C.c_void_p()
+        _lib.call("eoship_embed_bind", rt.handle, table.ctypes.data_as(C.c_void_p),
+                  C.c_int32(table.shape[0]), C.c_int32(table.shape[1]),
+                  proj.ctypes.data_as(C.c_void_p), C.c_int32(proj.shape[1]), C.byref(self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            _lib.call("eoship_embed_release", self.handle)
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    def embed(self, tokens: np.ndarray) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32).reshape(-1)
+        out = np.zeros((t.shape[0], self.edim), np.float16)
+        _lib.call("eoship_embed_run", self.rt.handle, self.handle, t.ctypes.data_as(C.c_void_p),
+                  C.c_int32(t.shape[0]), out.ctypes.data_as(C.c_void_p))
+        return out
+
+    def embed_device(self, d_tokens: DeviceBuffer, n: int, d_out: DeviceBuffer) -> None:
+        _lib.call("eoship_embed_run_device", self.rt.handle, self.handle, d_tokens.ptr,
+                  C.c_int32(n), d_out.ptr)

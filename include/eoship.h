@@ -152,6 +152,26 @@ int eoship_tq_maxsim_scores(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, co
                             int32_t q, int32_t tq_tokens, int64_t doc_begin, int64_t doc_count,
                             float* scores, char** err);
 
+/* ------------------------------------------------------------- tiny embed */
+
+typedef struct EosHipEmbed EosHipEmbed;
+
+/* The examples/embed.eos pipeline -- gather(token_embedding f16 [V][D]),
+ * @matmul(projection f16 [D][E]), l2_normalize -- with resident weights.
+ * Replaces the host gather + cuBLAS matmul + l2_normalize kernel steps that
+ * Program.Run executes for it (runtime/backend/tensor_ops.go:938-1166,
+ * 1168-1249, 1367-1391; runtime/runtime.go:222). f16 tensors are IEEE
+ * binary16 bit patterns. */
+int eoship_embed_bind(EosHipRuntime* rt, const uint16_t* table_f16, int32_t vocab, int32_t dim,
+                      const uint16_t* proj_f16, int32_t edim, EosHipEmbed** out, char** err);
+int eoship_embed_release(EosHipEmbed* emb, char** err);
+/* tokens [n] -> out [n][E] f16 (host); token ids outside [0, V) are an error
+ * (gatherTensor rejects them, runtime/backend/tensor_ops.go:938-1166). */
+int eoship_embed_run(EosHipRuntime* rt, EosHipEmbed* emb, const int32_t* tokens, int32_t n,
+                     uint16_t* out_f16, char** err);
+int eoship_embed_run_device(EosHipRuntime* rt, EosHipEmbed* emb, const int32_t* d_tokens,
+                            int32_t n, uint16_t* d_out_f16, char** err);
+
 /* ---------------------------------------------------------------- encoder */
 
 typedef struct EosHipEncoder EosHipEncoder;
