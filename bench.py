@@ -117,35 +117,15 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--n", type=int, default=1_000_000)
-    ap.add_argument("--queries", type=int, default=64)
-    ap.add_argument("--k", type=int, default=100)
-    ap.add_argument("--cpu-sample-queries", type=int, default=32)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--skip-encoder", action="store_true")
-    ap.add_argument("--encoder-steps", type=int, default=5)
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the scan would shard by corpus rows with one top-k merge; see DESIGN.md)",
-              file=sys.stderr)
-        return 2
-
+def tq_leg(rt, args) -> dict:
+    """BASELINE config 2 (the bench line's workload)."""
     from eos_amd import datagen
-    from eos_amd.runtime import DeviceBuffer, Runtime
+    from eos_amd.runtime import DeviceBuffer
     from eos_amd.turboquant import TurboQuantIndex
 
     log("generating corpus")
     corpus = datagen.baseline_flat_corpus(n=args.n)
     queries = datagen.baseline_queries(args.queries, corpus.dim)
-    rt = Runtime(0)
-    info = rt.info()
-    log(f"device {info}")
     idx = TurboQuantIndex(rt, corpus.codes, corpus.norms, corpus.dim, corpus.bits, corpus.codebook,
                           corpus.codebook_scale, corpus.rotation)
     kk = idx.effective_k(args.k)
@@ -168,15 +148,11 @@ def main() -> int:
     n_filter, ms_filter = rt.profile_read("tq_scan_filter")
     breakdown = {}
     for name in ("eos_tq_rotate", "eos_tq_quantize", "tq_scan_sample", "eos_tq_threshold",
-                 "tq_scan_filter",
-                 "eos_tq_finalize", "tq_scan_dense", "tq_fallback_select"):
+                 "tq_scan_filter", "eos_tq_finalize", "tq_scan_dense", "tq_fallback_select"):
         breakdown[name] = rt.profile_read(name)[1] / args.steps
     rt.profile(False)
     st = idx.top_k_device(dq, args.queries, args.k, dids, dsc, with_stats=True)
-    fallbacks = st.fallback_queries
-    kept = st.candidates_kept
     ms_per_step = total_ms / args.steps
-    value = args.queries * corpus.n / (ms_per_step / 1e3)
     bytes_per_launch = corpus.n * (corpus.dim * corpus.bits // 8 + 4)
     avg_filter_ms = ms_filter / max(n_filter, 1)
     achieved = bytes_per_launch / (avg_filter_ms / 1e3) / 1e9
@@ -187,19 +163,8 @@ def main() -> int:
         except (OSError, ValueError):
             traffic = None
     out = {
-        "metric": METRIC,
-        "value": value,
-        "unit": "vectors scored/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "value": args.queries * corpus.n / (ms_per_step / 1e3),
         "ms_per_step": ms_per_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "u4 codes x int16 query (int8 MFMA, exact i32), f32 scores",
-        "data": "synthetic (seeded splitmix64: uniform 4-bit codes, lognormal(0,0.25) norms, "
-                "QR rotation, unit Gaussian queries)",
         "config": {"workload": "turboquant_flat_c2", "n": corpus.n, "dim": corpus.dim,
                    "bits": corpus.bits, "queries": args.queries, "k": args.k,
                    "parallelism": "single GPU"},
@@ -208,9 +173,8 @@ def main() -> int:
                      "kernel": "tq_scan_filter", "avg_launch_ms": avg_filter_ms,
                      "bytes_per_launch": bytes_per_launch},
         "breakdown_ms_per_step": breakdown,
-        "fallback_queries": fallbacks,
-        "candidates_kept_per_query": kept / args.queries,
-        "device": info,
+        "fallback_queries": st.fallback_queries,
+        "candidates_kept_per_query": st.candidates_kept / args.queries,
     }
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -218,10 +182,74 @@ def main() -> int:
     else:
         out["cpu_baseline"] = None
     idx.release()
-    del corpus
+    return out
+
+
+def copy_calibration(rt, mb: int, reps: int = 5) -> dict:
+    """Device-to-device copies of a known size: the reference kernel whose
+    FETCH_SIZE / WRITE_SIZE counters scale the scan's in a --pmc run."""
+    from eos_amd.runtime import DeviceBuffer
+    from eos_amd import _lib
+    import ctypes as C
+    nbytes = mb * 1_000_000
+    src = DeviceBuffer(rt, nbytes)
+    dst = DeviceBuffer(rt, nbytes)
+    rt.sync()
+    rt.mark(4)
+    for _ in range(reps):
+        _lib.call("eoship_d2d", rt.handle, dst.ptr, src.ptr, C.c_size_t(nbytes))
+    rt.mark(5)
+    ms = rt.elapsed_ms(4, 5) / reps
+    return {"bytes": nbytes, "ms": ms, "read_plus_write_GBps": 2 * nbytes / (ms / 1e3) / 1e9}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--n", type=int, default=1_000_000)
+    ap.add_argument("--queries", type=int, default=64)
+    ap.add_argument("--k", type=int, default=100)
+    ap.add_argument("--cpu-sample-queries", type=int, default=32)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--skip-encoder", action="store_true")
+    ap.add_argument("--skip-tq", action="store_true", help="profiling runs of the encoder only")
+    ap.add_argument("--encoder-steps", type=int, default=5)
+    ap.add_argument("--copy-calibration-mb", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the scan would shard by corpus rows with one top-k merge; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    from eos_amd.runtime import Runtime
+
+    rt = Runtime(0)
+    info = rt.info()
+    log(f"device {info}")
+    out = {
+        "metric": METRIC,
+        "unit": "vectors scored/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 codes x int16 query (int8 MFMA, exact i32), f32 scores",
+        "data": "synthetic (seeded splitmix64: uniform 4-bit codes, lognormal(0,0.25) norms, "
+                "QR rotation, unit Gaussian queries)",
+    }
+    if not args.skip_tq:
+        out.update(tq_leg(rt, args))
     if not args.skip_encoder:
         log("encoder c3")
         out["encoder_c3"] = encoder_leg(rt, args.encoder_steps)
+    if args.copy_calibration_mb > 0:
+        out["copy_calibration"] = copy_calibration(rt, args.copy_calibration_mb)
+    out["device"] = info
     rt.close()
     print(json.dumps(out), flush=True)
     return 0
