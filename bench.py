@@ -70,13 +70,17 @@ def encoder_leg(rt, steps: int) -> dict:
     for _ in range(2):
         enc.embed_device(d_ids, d_mask, B, T, d_out)
     rt.sync()
-    rt.profile_reset()
-    rt.profile(True)
     rt.mark(2)
     for _ in range(steps):
         enc.embed_device(d_ids, d_mask, B, T, d_out)
     rt.mark(3)
     ms = rt.elapsed_ms(2, 3) / steps
+    # Per-kernel breakdown from a separate pass with every launch bracketed.
+    rt.profile_reset()
+    rt.profile_select(None)
+    rt.profile(True)
+    for _ in range(steps):
+        enc.embed_device(d_ids, d_mask, B, T, d_out)
     rt.sync()
     kernels = {}
     for name in ("eos_enc_pack", "eos_enc_embed", "enc_gemm_qkv", "eos_enc_attn", "enc_gemm_o_ln",
@@ -136,16 +140,31 @@ def tq_leg(rt, args) -> dict:
     for _ in range(args.warmup):
         idx.top_k_device(dq, args.queries, args.k, dids, dsc)
     rt.sync()
-    rt.profile_reset()
-    rt.profile(True)
+    # Timed region: every launch runs bare (an event pair around a launch
+    # costs ~5 us of stream time on each side).
     log(f"timing {args.steps} steps")
     rt.mark(0)
     for _ in range(args.steps):
         idx.top_k_device(dq, args.queries, args.k, dids, dsc, with_stats=False)
     rt.mark(1)
     total_ms = rt.elapsed_ms(0, 1)
+    # Roofline: the same steps again with only the filter scan bracketed by
+    # events on the library stream; its average launch time is the figure.
+    rt.profile_reset()
+    rt.profile_select("tq_scan_filter")
+    rt.profile(True)
+    for _ in range(args.steps):
+        idx.top_k_device(dq, args.queries, args.k, dids, dsc, with_stats=False)
     rt.sync()
     n_filter, ms_filter = rt.profile_read("tq_scan_filter")
+    rt.profile(False)
+    # Per-kernel breakdown from a separate pass with every launch bracketed.
+    rt.profile_reset()
+    rt.profile_select(None)
+    rt.profile(True)
+    for _ in range(args.steps):
+        idx.top_k_device(dq, args.queries, args.k, dids, dsc, with_stats=False)
+    rt.sync()
     breakdown = {}
     for name in ("eos_tq_rotate", "eos_tq_quantize", "tq_scan_sample", "eos_tq_threshold",
                  "tq_scan_filter", "eos_tq_finalize", "tq_scan_dense", "tq_fallback_select"):

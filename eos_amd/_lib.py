@@ -83,6 +83,7 @@ _SIGNATURES = {
     "eoship_launch": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
                        C.c_uint32, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
     "eoship_profile_enable": ([C.c_void_p, C.c_int, C.c_void_p], C.c_int),
+    "eoship_profile_select": ([C.c_void_p, C.c_char_p, C.c_void_p], C.c_int),
     "eoship_profile_read": ([C.c_void_p, C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_double),
                              C.c_void_p], C.c_int),
     "eoship_profile_reset": ([C.c_void_p, C.c_void_p], C.c_int),

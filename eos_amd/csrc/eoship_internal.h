@@ -35,7 +35,9 @@ struct Runtime {
   std::vector<hipModule_t> builtin;  // built-in code objects, searched in order
   std::unordered_map<std::string, hipFunction_t> fns;
   bool profiling = false;
+  std::string profile_prefix;  // record only labels starting with this (empty = all)
   std::vector<ProfileRecord> records;
+  std::vector<hipEvent_t> event_pool;  // recycled profiling events
   std::map<std::string, std::pair<int64_t, double>> totals;
   hipEvent_t timer[kTimerSlots];
 
@@ -48,6 +50,7 @@ struct Runtime {
   void release(void* p);
   int sync(char** err);
   int flush_profile(char** err);
+  int take_event(hipEvent_t* ev, char** err);
 };
 
 }  // namespace eoship

@@ -61,23 +61,36 @@ int Runtime::launch(const char* name, dim3 grid, dim3 block, size_t lds, void* a
   hipFunction_t f = nullptr;
   if (function(name, &f, err) != 0) return 1;
   void* params[1] = {args};
+  const char* tag = label ? label : name;
+  const bool rec = profiling && (profile_prefix.empty() ||
+                                 strncmp(tag, profile_prefix.c_str(), profile_prefix.size()) == 0);
   hipEvent_t e0 = nullptr, e1 = nullptr;
-  if (profiling) {
-    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)
-      return set_err(err, "hipEventCreate failed");
+  if (rec) {
+    if (take_event(&e0, err) != 0 || take_event(&e1, err) != 0) return 1;
     hipEventRecord(e0, stream);
   }
   hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
                                        static_cast<unsigned>(lds), stream, params, nullptr);
   if (e != hipSuccess) {
-    if (e0) hipEventDestroy(e0);
-    if (e1) hipEventDestroy(e1);
+    if (e0) event_pool.push_back(e0);
+    if (e1) event_pool.push_back(e1);
     return hip_err(err, name, e);
   }
-  if (profiling) {
+  if (rec) {
     hipEventRecord(e1, stream);
-    records.push_back(ProfileRecord{label ? label : name, e0, e1});
+    records.push_back(ProfileRecord{tag, e0, e1});
   }
+  return 0;
+}
+
+int Runtime::take_event(hipEvent_t* ev, char** err) {
+  if (!event_pool.empty()) {
+    *ev = event_pool.back();
+    event_pool.pop_back();
+    return 0;
+  }
+  hipError_t e = hipEventCreate(ev);
+  if (e != hipSuccess) return hip_err(err, "hipEventCreate", e);
   return 0;
 }
 
@@ -108,8 +121,8 @@ int Runtime::flush_profile(char** err) {
     auto& acc = totals[r.name];
     acc.first += 1;
     acc.second += ms;
-    hipEventDestroy(r.begin);
-    hipEventDestroy(r.end);
+    event_pool.push_back(r.begin);
+    event_pool.push_back(r.end);
   }
   records.clear();
   return 0;
@@ -186,6 +199,7 @@ int eoship_runtime_destroy(EosHipRuntime* rt, char** err) {
     hipEventDestroy(r.begin);
     hipEventDestroy(r.end);
   }
+  for (hipEvent_t ev : rt->event_pool) hipEventDestroy(ev);
   for (auto& ev : rt->timer)
     if (ev) hipEventDestroy(ev);
   for (hipModule_t m : rt->builtin) hipModuleUnload(m);
@@ -286,6 +300,12 @@ int eoship_profile_enable(EosHipRuntime* rt, int enabled, char** err) {
   if (rt == nullptr) return set_err(err, "eoship_profile_enable: runtime is NULL");
   if (!enabled && rt->flush_profile(err) != 0) return 1;
   rt->profiling = enabled != 0;
+  return 0;
+}
+
+int eoship_profile_select(EosHipRuntime* rt, const char* prefix, char** err) {
+  if (rt == nullptr) return set_err(err, "eoship_profile_select: runtime is NULL");
+  rt->profile_prefix = prefix ? prefix : "";
   return 0;
 }
 

@@ -4,8 +4,8 @@
 // (runtime/retrieval_turboquant.go:1853-1887) and its per-document
 // q.InnerProductPrepared calls with a device pipeline per batch of <= 64
 // queries, enqueued on the runtime stream without host synchronisation:
-//   1. eos_tq_rotate / eos_tq_quantize  rotate (f64), round to int16, split
-//                       into int8 hi/lo MFMA fragments (PrepareQuery)
+//   1. eos_tq_rotate /  rotate (f64), round to int16, split into int8 hi/lo
+//      eos_tq_quantize  MFMA fragments (PrepareQuery)
 //   2. sample scan      exact scores of every s-th tile of 32 vectors
 //   3. eos_tq_threshold per query, a score below the r-th best sample
 //   4. filter scan      one pass over the corpus, keep score >= threshold
@@ -33,8 +33,13 @@ constexpr int kBatch = 64;          // queries per scan (two 32-column groups)
 constexpr int kMaxCols = 128;       // MFMA query columns per pass (MaxSim: four 32-token groups)
 constexpr int kCap = 8192;          // kept candidates per query
 constexpr int kSortCap = 8192;      // largest k the device sort handles
-constexpr int kSampleStride = 32;   // sample every 32nd tile (at least)
-constexpr int kMaxSampleTiles = 1024;  // the threshold kernel holds <= 1024 tile maxima
+constexpr int kSampleStride = 16;     // sample every 16th tile (at least)
+constexpr int kMaxSampleTiles = 2048;  // tile maxima per query (the threshold kernel holds 4096)
+// Candidates the sample threshold aims to keep per query, as a multiple of k:
+// on the BASELINE corpus a 1/16 sample at 3 k keeps ~320 for k = 100, with the
+// fewest kept over 256 queries still ~1.8 k (fewer than k triggers the exact
+// fallback, which stays correct but costs a dense pass).
+constexpr double kKeepFactor = 3.0;
 constexpr int kTile = 32;
 constexpr int kQmaxLimit = 127 * 256 + 127;  // largest int16 with int8 hi/lo halves
 const int kSupportedKs[] = {1, 2, 4, 8, 12, 16, 24, 32};
@@ -114,7 +119,7 @@ struct EosHipTQ {
   void* packed = nullptr;
   float* norms = nullptr;
   float* rot_t = nullptr;
-  double* qrot = nullptr;  // [64][d] rotated queries
+  double* qrot = nullptr;  // [kMaxCols][d] rotated query columns
   // per-batch device scratch
   int8_t* bfrag = nullptr;
   float* alpha = nullptr;
@@ -208,12 +213,12 @@ struct EosHipTQ {
     p.qrot = qrot;
     p.group = group;
     p.group_live = group_live;
+    const unsigned cblocks = (unsigned)(32 * nqg / 8);  // 8 columns per workgroup
     if (rot_t != nullptr) {
-      const unsigned jblocks = (unsigned)((d + 63) / 64);
-      const unsigned qblocks = (unsigned)((nsrc + 3) / 4);
-      if (rt->launch("eos_tq_rotate", dim3(jblocks, qblocks), dim3(256), 0, &p, err) != 0) return 1;
+      const unsigned jblocks = (unsigned)((d + 31) / 32);
+      if (rt->launch("eos_tq_rotate", dim3(jblocks, cblocks), dim3(256), 0, &p, err) != 0) return 1;
     }
-    return rt->launch("eos_tq_quantize", dim3(32 * nqg), dim3(256), 0, &p, err);
+    return rt->launch("eos_tq_quantize", dim3(cblocks), dim3(256), 0, &p, err);
   }
 
   int prepare(const float* d_queries, int qb, int16_t* qs_out, char** err) {
@@ -287,7 +292,7 @@ struct EosHipTQ {
       const int64_t ns = (ntiles + stride - 1) / stride;
       int64_t nsv = 0;
       for (int64_t j = 0; j < ns; ++j) nsv += std::min<int64_t>(kTile, n - j * stride * kTile);
-      const double target = std::min<double>(8.0 * kk, kCap / 4.0);
+      const double target = std::min<double>(kKeepFactor * kk, kCap / 4.0);
       int64_t r = (int64_t)std::ceil(target * (double)nsv / (double)n);
       r = std::max<int64_t>(1, std::min<int64_t>(r, ns));  // r-th best of ns tile maxima
       TqScanArgs s;
@@ -307,7 +312,7 @@ struct EosHipTQ {
       sel.stride = ns;
       sel.kk = (int)r;
       sel.nrows = qb;
-      if (rt->launch("eos_tq_threshold", dim3(qb), dim3(64), 0, &sel, err) != 0) return 1;
+      if (rt->launch("eos_tq_threshold", dim3(qb), dim3(256), 0, &sel, err) != 0) return 1;
     }
     TqScanArgs s;
     scan_base(&s, qb);

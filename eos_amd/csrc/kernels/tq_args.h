@@ -14,7 +14,7 @@ struct TqPrepArgs {
   float* tau;            // [32*ncb/2] reset to -inf
   uint32_t* cand_count;  // [32*ncb/2] reset to 0
   int16_t* qs_out;       // optional [q][d]
-  double* qrot;          // [32*ncb/2][d] rotated queries (written by eos_tq_rotate)
+  double* qrot;          // [32*ncb/2][d] rotated columns (written by eos_tq_rotate)
   int q, d, ks, ncb, qmax;
   float cb_scale;
   // Column -> source row: column c belongs to group c / group (a query of the

@@ -50,96 +50,50 @@ EOS_DEV uint32_t rank_id(u64 c) { return ~(uint32_t)(c & 0xffffffffu); }
 // ------------------------------------------------------------------ prepare
 
 namespace {
-constexpr int kRotJ = 64;    // rotated coordinates per workgroup
-constexpr int kRotQ = 4;     // queries per workgroup
-constexpr int kRotK = 128;   // rotation rows staged per LDS chunk
 constexpr int kMaxDim = 1024;
-}  // namespace
 
-// q'[q][j] = sum_k R[j][k] q[k] in f64: one fma chain per (q, j), k ascending.
-// Workgroup (x, y) computes j in [64x, 64x + 64) for queries [4y, 4y + 4);
-// R^T streams through LDS 128 rows of k at a time (all loads of a chunk are
-// issued before any is consumed).
-extern "C" __global__ __launch_bounds__(256) void eos_tq_rotate(TqPrepArgs a) {
-  __shared__ float rs[kRotK * kRotJ];
-  __shared__ double qsh[kRotQ * kMaxDim];
-  const int tid = threadIdx.x;
-  const int j0 = blockIdx.x * kRotJ, q0 = blockIdx.y * kRotQ;
-  const int jj = tid & 63, ql = tid >> 6;
-  for (int i = tid; i < kRotQ * a.d; i += 256) {
-    const int qq = i / a.d, k = i - qq * a.d;
-    const int qi = q0 + qq;
-    qsh[qq * kMaxDim + k] = qi < a.q ? (double)a.queries[(size_t)qi * a.d + k] : 0.0;
-  }
-  double acc = 0.0;
-  for (int k0 = 0; k0 < a.d; k0 += kRotK) {
-    const int kn = min(kRotK, a.d - k0);
-    float tmp[kRotK * kRotJ / 256];
-#pragma unroll
-    for (int r = 0; r < kRotK * kRotJ / 256; ++r) {
-      const int i = tid + 256 * r;
-      const int kk = i >> 6, jc = i & 63;
-      tmp[r] = (kk < kn && j0 + jc < a.d) ? a.rot_t[(size_t)(k0 + kk) * a.d + j0 + jc] : 0.0f;
-    }
-    __syncthreads();  // previous chunk consumed; qsh visible
-#pragma unroll
-    for (int r = 0; r < kRotK * kRotJ / 256; ++r) rs[tid + 256 * r] = tmp[r];
-    __syncthreads();
-    if (kn == kRotK) {
-#pragma unroll 16
-      for (int kk = 0; kk < kRotK; ++kk)
-        acc = fma((double)rs[kk * kRotJ + jj], qsh[ql * kMaxDim + k0 + kk], acc);
-    } else {
-      for (int kk = 0; kk < kn; ++kk)
-        acc = fma((double)rs[kk * kRotJ + jj], qsh[ql * kMaxDim + k0 + kk], acc);
-    }
-  }
-  const int j = j0 + jj, qi = q0 + ql;
-  if (j < a.d && qi < a.q) a.qrot[(size_t)qi * a.d + j] = acc;
+// Column c of the MFMA query block reads source row (c / group) * group_live
+// + c % group when c % group < group_live; other columns are zero.
+EOS_DEV int prep_source(const TqPrepArgs& a, int c) {
+  const int grp = c / a.group, slot = c - grp * a.group;
+  const int src = grp * a.group_live + slot;
+  return (slot < a.group_live && src < a.q) ? src : -1;
 }
 
-// One workgroup per query column (padded to a multiple of 32 queries):
-// max |q'|, int16 rounding, hi/lo fragments, alpha; resets the query's
-// threshold and candidate count for the scan that follows.
-extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) {
-  __shared__ double red[256];
-  const int qi = blockIdx.x;  // column
-  const int tid = threadIdx.x;
-  const int grp = qi / a.group, slot = qi - grp * a.group;
-  const int src = grp * a.group_live + slot;  // source row
-  const bool live = src < a.q && slot < a.group_live;
-  const int dpad = a.ks * 32;
-  double qr[kMaxDim / 256];
+// Quantizes column c of the query block from its rotated (or raw) values:
+// max |q'|, Qs = rint(q' qmax / max|q'|) clamped, hi/lo int8 fragments,
+// alpha; resets the column's threshold and candidate count. Called by the 32
+// lanes of one half-wave (t = lane & 31), values fetched by get(j).
+template <typename Get>
+EOS_DEV void prep_quantize_column(const TqPrepArgs& a, int c, int t, Get get) {
+  constexpr int M = kMaxDim / 32;  // values per lane
+  const int src = prep_source(a, c);
+  // All of the lane's values are fetched before any is used, so the loads
+  // overlap instead of costing one round trip each.
+  double v[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int j = t + 32 * m;
+    v[m] = (src >= 0 && j < a.d) ? get(src, j) : 0.0;
+  }
   double mx = 0.0;
 #pragma unroll
-  for (int r = 0; r < kMaxDim / 256; ++r) {
-    const int j = tid + 256 * r;
-    double v = 0.0;
-    if (live && j < a.d)
-      v = a.rot_t != nullptr ? a.qrot[(size_t)src * a.d + j] : (double)a.queries[(size_t)src * a.d + j];
-    qr[r] = v;
-    mx = fmax(mx, fabs(v));
-  }
-  red[tid] = mx;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (tid < s) red[tid] = fmax(red[tid], red[tid + s]);
-    __syncthreads();
-  }
-  const double maxabs = red[0];
-  const double inv = maxabs > 0.0 ? (double)a.qmax / maxabs : 0.0;
-  const int cb_hi = 2 * (qi >> 5);
-  const int col = qi & 31;
+  for (int m = 0; m < M; ++m) mx = fmax(mx, fabs(v[m]));
 #pragma unroll
-  for (int r = 0; r < kMaxDim / 256; ++r) {
-    const int j = tid + 256 * r;
-    if (j >= dpad) continue;
+  for (int o = 16; o > 0; o >>= 1) mx = fmax(mx, __shfl_xor(mx, o));
+  const double inv = mx > 0.0 ? (double)a.qmax / mx : 0.0;
+  const int cb_hi = 2 * (c >> 5), col = c & 31;
+  const int dpad = a.ks * 32;
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    const int j = t + 32 * m;
+    if (j >= dpad) break;
     int qs = 0;
-    if (j < a.d) {
-      double v = rint(qr[r] * inv);
-      v = fmin(fmax(v, (double)-a.qmax), (double)a.qmax);
-      qs = (int)v;
-      if (live && a.qs_out != nullptr) a.qs_out[(size_t)src * a.d + j] = (int16_t)qs;
+    if (src >= 0 && j < a.d) {
+      double x = rint(v[m] * inv);
+      x = fmin(fmax(x, (double)-a.qmax), (double)a.qmax);
+      qs = (int)x;
+      if (a.qs_out != nullptr) a.qs_out[(size_t)src * a.d + j] = (int16_t)qs;
     }
     const int lo = ((qs + 128) & 255) - 128;
     const int hi = (qs - lo) >> 8;
@@ -148,10 +102,85 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) 
     a.bfrag[((size_t)(s * a.ncb + cb_hi) * 64 + lane) * 16 + i] = (int8_t)hi;
     a.bfrag[((size_t)(s * a.ncb + cb_hi + 1) * 64 + lane) * 16 + i] = (int8_t)lo;
   }
-  if (tid == 0) {
-    a.alpha[qi] = maxabs > 0.0 ? (float)((maxabs / (double)a.qmax) * (double)a.cb_scale) : 0.0f;
-    a.tau[qi] = -__builtin_inff();
-    a.cand_count[qi] = 0u;
+  if (t == 0) {
+    a.alpha[c] = mx > 0.0 ? (float)((mx / (double)a.qmax) * (double)a.cb_scale) : 0.0f;
+    a.tau[c] = -__builtin_inff();
+    a.cand_count[c] = 0u;
+  }
+}
+
+constexpr int kPrepJ = 32;     // rotated coordinates per workgroup
+constexpr int kPrepC = 8;      // query columns per workgroup
+constexpr int kPrepK = 512;    // rotation rows staged in LDS per chunk
+
+}  // namespace
+
+// Rotation of the query block: workgroup (x, y) computes
+// q'[c][j] = sum_k R[j][k] q_src(c)[k] in f64 (one fma chain per (c, j), k
+// ascending) for j in [32x, 32x + 32) and the 8 columns [8y, 8y + 8). The
+// query rows and the R^T slice are staged in LDS with every load of a stage in
+// flight at once. eos_tq_quantize runs next on the same stream: the kernel
+// boundary orders the two (a device-scope fence inside one launch costs more
+// than the second launch).
+extern "C" __global__ __launch_bounds__(256) void eos_tq_rotate(TqPrepArgs a) {
+  __shared__ float rs[kPrepK * kPrepJ];
+  __shared__ float qsh[kPrepC * kMaxDim];
+  const int tid = threadIdx.x;
+  const int j0 = blockIdx.x * kPrepJ, c0 = blockIdx.y * kPrepC;
+  const int jj = tid & 31, cl = tid >> 5;
+  {
+    // Every query value of the 8 columns is loaded before any is stored, so
+    // the staging costs one memory round trip.
+    constexpr int R = kMaxDim / 256;
+    float qv[kPrepC][R];
+#pragma unroll
+    for (int cc = 0; cc < kPrepC; ++cc) {
+      const int src = prep_source(a, c0 + cc);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int k = tid + 256 * r;
+        qv[cc][r] = (src >= 0 && k < a.d) ? a.queries[(size_t)src * a.d + k] : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < kPrepC; ++cc)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (tid + 256 * r < a.d) qsh[cc * kMaxDim + tid + 256 * r] = qv[cc][r];
+  }
+  const int j = j0 + jj;
+  double acc = 0.0;
+  for (int k0 = 0; k0 < a.d; k0 += kPrepK) {
+    const int kn = min(kPrepK, a.d - k0);
+    float tmp[kPrepK * kPrepJ / 256];
+#pragma unroll
+    for (int r = 0; r < kPrepK * kPrepJ / 256; ++r) {
+      const int kk = (tid >> 5) + 8 * r;
+      tmp[r] = (kk < kn && j < a.d) ? a.rot_t[(size_t)(k0 + kk) * a.d + j] : 0.0f;
+    }
+    __syncthreads();  // previous chunk consumed; qsh visible
+#pragma unroll
+    for (int r = 0; r < kPrepK * kPrepJ / 256; ++r) rs[tid + 256 * r] = tmp[r];
+    __syncthreads();
+    const float* qc = qsh + cl * kMaxDim + k0;
+#pragma unroll 16
+    for (int kk = 0; kk < kn; ++kk) acc = fma((double)rs[kk * kPrepJ + jj], (double)qc[kk], acc);
+  }
+  const int c = c0 + cl;
+  if (j < a.d) a.qrot[(size_t)c * a.d + j] = acc;
+}
+
+// Quantization of the query block, one half-wave per column: from the
+// rotated columns eos_tq_rotate wrote, or from the raw queries when the
+// corpus has no rotation.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) {
+  const int c = blockIdx.x * kPrepC + (threadIdx.x >> 5);
+  if (a.rot_t != nullptr) {
+    prep_quantize_column(a, c, threadIdx.x & 31,
+                         [&](int, int jx) { return a.qrot[(size_t)c * a.d + jx]; });
+  } else {
+    prep_quantize_column(a, c, threadIdx.x & 31,
+                         [&](int src, int jx) { return (double)a.queries[(size_t)src * a.d + jx]; });
   }
 }
 
@@ -265,6 +294,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   __shared__ v4i sb[KS * NCB * 64];
   __shared__ uint32_t lc_cnt[FILTER ? NQ : 1];
   __shared__ u64 lc_buf[FILTER ? NQ * kLdsSlots : 1];
+  __shared__ float4 nstage[kScanThreads / 64][8];
   if (a.gate != nullptr) {
     // Exhaustive pass of the exact fallback: run only when a query was flagged.
     bool any = false;
@@ -278,29 +308,62 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform tile indices keep the tile addressing in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = gridDim.x * (kScanThreads / 64);
   const int half = lane >> 5;
   const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
-  // Software pipeline: codes are in flight two tiles ahead and norms one tile
-  // ahead of the tile being decoded, multiplied and filtered.
-  int j = blockIdx.x * (kScanThreads / 64) + wave;
-  v4i raw0[NLOAD], raw1[NLOAD];
-  float4 nrm0[4];
-  if (j < a.ntiles) {
-    const long long t0 = a.tile_begin + (long long)j * a.tile_step;
-    load_tile_codes<NLOAD>(raw0, packed, t0, lane);
-    load_tile_norms(nrm0, a.norms, t0, half);
+  // Per-column constants live in registers for the whole scan: a global load
+  // inside the tile loop would make every tile wait for the code prefetch
+  // issued ahead of it (loads retire in order).
+  float al_r[NQG], ta_r[NQG];
+  bool live_r[NQG];
+#pragma unroll
+  for (int g = 0; g < NQG; ++g) {
+    const int qi = g * 32 + (lane & 31);
+    live_r[g] = qi < a.q;
+    al_r[g] = live_r[g] ? a.alpha[qi] : 0.0f;
+    ta_r[g] = (FILTER && live_r[g]) ? a.tau[qi] : __builtin_inff();
   }
-  if (j + nw < a.ntiles) load_tile_codes<NLOAD>(raw1, packed, a.tile_begin + (long long)(j + nw) * a.tile_step, lane);
-  for (; j < a.ntiles; j += nw) {
+  // Pre-test thresholds of the filter. For tau > 0 and alpha > 0 a kept score
+  // s = fl(fl(fl(D) a) n) >= tau implies D > 0, n > 0 and, with u = 2^-24,
+  // p = fl(fl(D) n) >= (tau / a)(1 - u) / (1 + u)^2 > (tau / a)(1 - 2^-16)
+  // rounded, which is pt. Other cases test every row exactly (pt = -inf) or
+  // none (alpha = 0: every score is 0 < tau).
+  float pt_r[NQG];
+#pragma unroll
+  for (int g = 0; g < NQG; ++g) {
+    const float ta = ta_r[g], al = al_r[g];
+    float pt = -__builtin_inff();
+    if (ta > 0.0f) {
+      if (!(al > 0.0f)) {
+        pt = __builtin_inff();
+      } else {
+        pt = (ta / al) * 0.9999847412109375f;
+        if (!(pt <= 3.402823466e38f)) pt = -__builtin_inff();
+      }
+    }
+    pt_r[g] = pt;
+  }
+  // Software pipeline over three register stages (a ring, unrolled so that no
+  // stage is ever copied: a copy of a register still being loaded would wait
+  // for every load issued before it). Codes are in flight two tiles ahead of
+  // the tile being decoded, norms one tile ahead. A stage holds one norm per
+  // lane (row lane % 32 of its tile); the epilogue redistributes them to the
+  // accumulator layout through a 128-byte LDS slot of the wave.
+  struct Stage {
+    v4i raw[NLOAD];
+    float nv;
+  };
+  auto load_codes = [&](Stage& st, int jj) {
+    load_tile_codes<NLOAD>(st.raw, packed, a.tile_begin + (long long)jj * a.tile_step, lane);
+  };
+  auto load_norms = [&](Stage& st, int jj) {
+    st.nv = a.norms[(a.tile_begin + (long long)jj * a.tile_step) * kTile + (lane & 31)];
+  };
+  auto process = [&](const Stage& st, int j) {
+    const v4i(&raw)[NLOAD] = st.raw;
     const long long tile = a.tile_begin + (long long)j * a.tile_step;
-    v4i raw2[NLOAD];
-    float4 nrm1[4];
-    if (j + 2 * nw < a.ntiles)
-      load_tile_codes<NLOAD>(raw2, packed, a.tile_begin + (long long)(j + 2 * nw) * a.tile_step, lane);
-    if (j + nw < a.ntiles)
-      load_tile_norms(nrm1, a.norms, a.tile_begin + (long long)(j + nw) * a.tile_step, half);
     // Opaque per-tile LDS offset: keeps the query fragments in LDS rather than
     // letting them be hoisted into registers across the tile loop.
     int boff = lane;
@@ -314,7 +377,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
       for (int h = 0; h < SPL; ++h) {
         const int s = c * SPL + h;
         if (s < KS) {
-          const v4i af = decode_step<BITS>(raw0[c], h, a);
+          const v4i af = decode_step<BITS>(raw[c], h, a);
 #pragma unroll
           for (int cb = 0; cb < NCB; ++cb) {
             const v4i bf = sb[(s * NCB + cb) * 64 + boff];
@@ -326,13 +389,22 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     // Epilogue. Accumulator element i of lane l is row 8(i/4) + 4(l/32) + i%4
     // (a corpus vector of the tile) and column l%32 (a query of the group).
     const long long vbase = tile * kTile;
+    // Row r's norm sits at float r of the wave's slot; lane l needs rows
+    // 8 i4 + 4 (l / 32) + {0..3}, i.e. float4 2 i4 + l / 32. LDS operations of
+    // one wave complete in order, so no barrier is needed around the slot.
+    if (lane < 32) reinterpret_cast<float*>(nstage[wave])[lane] = st.nv;
+    __builtin_amdgcn_wave_barrier();
+    float4 nrm4[4];
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) nrm4[i4] = nstage[wave][2 * i4 + half];
+    __builtin_amdgcn_wave_barrier();
     float nrm[16];
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
-      nrm[4 * i4 + 0] = nrm0[i4].x;
-      nrm[4 * i4 + 1] = nrm0[i4].y;
-      nrm[4 * i4 + 2] = nrm0[i4].z;
-      nrm[4 * i4 + 3] = nrm0[i4].w;
+      nrm[4 * i4 + 0] = nrm4[i4].x;
+      nrm[4 * i4 + 1] = nrm4[i4].y;
+      nrm[4 * i4 + 2] = nrm4[i4].z;
+      nrm[4 * i4 + 3] = nrm4[i4].w;
     }
     // Rows of this tile that are real vectors (the last tile may be partial).
     const long long rem64 = a.n - vbase;
@@ -340,21 +412,22 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
 #pragma unroll
     for (int g = 0; g < NQG; ++g) {
       const int qi = g * 32 + (lane & 31);
-      const bool live = qi < a.q;
-      const float al = live ? a.alpha[qi] : 0.0f;
-      float sc[16];
+      const bool live = live_r[g];
+      const float al = al_r[g];
       int dots[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        dots[i] = acc[2 * g][i] * 256 + acc[2 * g + 1][i];
-        sc[i] = ((float)dots[i] * al) * nrm[i] + 0.0f;
-      }
+      for (int i = 0; i < 16; ++i) dots[i] = acc[2 * g][i] * 256 + acc[2 * g + 1][i];
       if constexpr (FILTER) {
-        const float ta = live ? a.tau[qi] : __builtin_inff();
-        bool hit = false;
+        const float ta = ta_r[g];
+        // Conservative pre-test: max_i fl(fl(D_i) * norm_i) >= pt_r whenever
+        // some exact score of the lane reaches tau (pt_r carries the slack).
+        float m = -__builtin_inff();
 #pragma unroll
-        for (int i = 0; i < 16; ++i) hit |= sc[i] >= ta;
-        if (hit) {
+        for (int i = 0; i < 16; ++i) m = fmaxf(m, (float)dots[i] * nrm[i]);
+        if (m >= pt_r[g]) {
+          float sc[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sc[i] = ((float)dots[i] * al) * nrm[i] + 0.0f;
           // Rare path: count this lane's kept rows, reserve LDS slots with one
           // LDS atomic; keys past the stage's capacity go to the global list.
           uint32_t cnt = 0;
@@ -380,6 +453,9 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
           }
         }
       } else if (live) {
+        float sc[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) sc[i] = ((float)dots[i] * al) * nrm[i] + 0.0f;
         if (a.mode == 0) {
           float* orow = a.out_scores + (size_t)qi * a.out_stride;
           int32_t* drow = a.out_dots != nullptr ? a.out_dots + (size_t)qi * a.out_stride : nullptr;
@@ -407,13 +483,52 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
         }
       }
     }
-#pragma unroll
-    for (int c = 0; c < NLOAD; ++c) {
-      raw0[c] = raw1[c];
-      raw1[c] = raw2[c];
+  };
+  const int nt = a.ntiles;
+  int j = blockIdx.x * (kScanThreads / 64) + wave;
+  // Loads past the last tile are clamped to it rather than skipped, so every
+  // path issues the same loads and each wait covers only the stage it needs.
+  auto cl = [&](int jj) { return jj < nt ? jj : nt - 1; };
+  // Three stages (codes two tiles ahead) when the ring and the accumulators
+  // fit the 256 registers of two waves per SIMD; two stages otherwise.
+  constexpr bool kRing3 = NLOAD * 12 + NCB * 16 <= 168;
+  if (j < nt) {
+    if constexpr (kRing3) {
+      Stage s0, s1, s2;
+      load_codes(s0, j);
+      load_norms(s0, j);
+      load_codes(s1, cl(j + nw));
+      for (;;) {
+        load_codes(s2, cl(j + 2 * nw));
+        load_norms(s1, cl(j + nw));
+        process(s0, j);
+        if (j + nw >= nt) break;
+        load_codes(s0, cl(j + 3 * nw));
+        load_norms(s2, cl(j + 2 * nw));
+        process(s1, j + nw);
+        if (j + 2 * nw >= nt) break;
+        load_codes(s1, cl(j + 4 * nw));
+        load_norms(s0, cl(j + 3 * nw));
+        process(s2, j + 2 * nw);
+        j += 3 * nw;
+        if (j >= nt) break;
+      }
+    } else {
+      Stage s0, s1;
+      load_codes(s0, j);
+      load_norms(s0, j);
+      for (;;) {
+        load_codes(s1, cl(j + nw));
+        load_norms(s1, cl(j + nw));
+        process(s0, j);
+        if (j + nw >= nt) break;
+        load_codes(s0, cl(j + 2 * nw));
+        load_norms(s0, cl(j + 2 * nw));
+        process(s1, j + nw);
+        j += 2 * nw;
+        if (j >= nt) break;
+      }
     }
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) nrm0[i4] = nrm1[i4];
   }
   if constexpr (FILTER) {
     // Flush the stage: one global atomic per query per workgroup.
@@ -570,107 +685,192 @@ extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_row_select(TqSe
 
 namespace {
 
-constexpr int kThrPer = 16;            // tile maxima held per lane (<= 1024 per row)
 constexpr int kFinThreads = 256;
-constexpr int kFinPer = kSortCap / kFinThreads;
+constexpr int kThrMax = 4096;         // tile maxima per row the threshold accepts
+constexpr int kThrThreads = 256;
+constexpr int kRankSortMax = 1024;    // finalize orders up to this many by rank counting
 
-// Block-wide sum of per-wave counts (each wave passes a uniform value). The
-// two slot sets alternate, so one barrier per call suffices: a set is
-// rewritten only after a later barrier that every reader of it has passed.
+// Block-wide exclusive suffix sum: thread t gets the sum of v over threads
+// t' > t. `scr` holds NT / 64 words.
 template <int NT>
-EOS_DEV uint32_t block_sum(uint32_t wave_count, uint32_t* slots, int& parity) {
-  uint32_t* set = slots + parity * (NT / 64);
-  if ((threadIdx.x & 63) == 0) set[threadIdx.x >> 6] = wave_count;
-  __syncthreads();
-  uint32_t t = 0;
+EOS_DEV uint32_t block_suffix_excl(uint32_t v, uint32_t* scr) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t s = v;
 #pragma unroll
-  for (int i = 0; i < NT / 64; ++i) t += set[i];
-  parity ^= 1;
-  return t;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t t = (uint32_t)__shfl_down((int)s, o);
+    if (lane + o < 64) s += t;
+  }
+  if constexpr (NT > 64) {
+    if (lane == 0) scr[wave] = s;  // wave total
+    __syncthreads();
+    uint32_t above = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w)
+      if (w > wave) above += scr[w];
+    __syncthreads();
+    return s - v + above;
+  } else {
+    return s - v;
+  }
 }
 
-EOS_DEV void wave_minmax(uint32_t& vmin, uint32_t& vmax) {
+// Block-wide min and max of per-thread values (`scr` holds 2 * NT / 64 words).
+template <int NT>
+EOS_DEV void block_minmax(uint32_t& vmin, uint32_t& vmax, uint32_t* scr) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     vmin = min(vmin, (uint32_t)__shfl_xor((int)vmin, o));
     vmax = max(vmax, (uint32_t)__shfl_xor((int)vmax, o));
   }
+  if constexpr (NT > 64) {
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+      scr[wave] = vmin;
+      scr[NT / 64 + wave] = vmax;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+      vmin = min(vmin, scr[w]);
+      vmax = max(vmax, scr[NT / 64 + w]);
+    }
+    __syncthreads();
+  }
 }
 
-// Block-wide min and max of per-thread values.
-template <int NT>
-EOS_DEV void block_minmax(uint32_t& vmin, uint32_t& vmax, uint32_t* smin, uint32_t* smax) {
-  wave_minmax(vmin, vmax);
-  if ((threadIdx.x & 63) == 0) {
-    smin[threadIdx.x >> 6] = vmin;
-    smax[threadIdx.x >> 6] = vmax;
+// The r-th largest (1-based, with multiplicity) of the 32-bit keys
+// key_at(i).second over the members (key_at(i).first) of i in [0, count).
+// Bits shared by the members' minimum and maximum are skipped; the remaining
+// bits are resolved by radix passes of up to 8 bits over per-wave LDS
+// histograms (`hist` holds NT / 64 * 256 words; per-wave copies keep the
+// atomics of clustered keys from serialising on one bin). Requires
+// 1 <= r <= the member count. On return *rank_in_bin is r's rank among the
+// members equal to the result and *bin_count their number. Every thread of
+// the block calls it.
+template <int NT, typename KeyAt>
+EOS_DEV uint32_t block_select_desc(int count, KeyAt key_at, uint32_t r, uint32_t* hist,
+                                   uint32_t* scr, uint32_t* rank_in_bin, uint32_t* bin_count) {
+  constexpr int NW = NT / 64;
+  constexpr int BPT = 256 / NT;  // histogram bins per thread
+  const int wave = threadIdx.x >> 6;
+  uint32_t kmin = 0xffffffffu, kmax = 0u, nmem = 0u;
+  for (int i = threadIdx.x; i < count; i += NT) {
+    const auto m = key_at(i);
+    if (m.first) {
+      kmin = min(kmin, m.second);
+      kmax = max(kmax, m.second);
+      ++nmem;
+    }
   }
-  __syncthreads();
-  vmin = 0xffffffffu;
-  vmax = 0u;
+  block_minmax<NT>(kmin, kmax, scr + 8);
+  if (kmin == kmax) {
+    // Every member holds the same key.
+    const uint32_t tot = nmem + block_suffix_excl<NT>(nmem, scr + 8);  // thread 0: all members
+    if (threadIdx.x == 0) scr[2] = tot;
+    __syncthreads();
+    *rank_in_bin = r;
+    *bin_count = scr[2];
+    __syncthreads();
+    return kmin;
+  }
+  int bits = 32 - __clz(kmin ^ kmax);  // bits still to resolve: [bits - 1, 0]
+  uint32_t mask = bits >= 32 ? 0u : ~((1u << bits) - 1u);
+  uint32_t prefix = kmin & mask, nbin = 0u;
+  while (bits > 0) {
+    const int w = bits < 8 ? bits : 8;
+    const int shift = bits - w;
+    const uint32_t dmask = (1u << w) - 1u;
+    for (int b = threadIdx.x; b < NW * 256; b += NT) hist[b] = 0u;
+    __syncthreads();
+    uint32_t* wh = hist + wave * 256;
+    for (int i = threadIdx.x; i < count; i += NT) {
+      const auto m = key_at(i);
+      if (m.first && (m.second & mask) == prefix) atomicAdd(&wh[(m.second >> shift) & dmask], 1u);
+    }
+    __syncthreads();
+    uint32_t h[BPT], tot = 0;
 #pragma unroll
-  for (int i = 0; i < NT / 64; ++i) {
-    vmin = min(vmin, smin[i]);
-    vmax = max(vmax, smax[i]);
+    for (int k = 0; k < BPT; ++k) {
+      uint32_t c = 0;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) c += hist[v * 256 + threadIdx.x * BPT + k];
+      h[k] = c;
+      tot += c;
+    }
+    // Members in bins above this thread's, then walk its bins downwards.
+    uint32_t above = block_suffix_excl<NT>(tot, scr + 8);
+#pragma unroll
+    for (int k = BPT - 1; k >= 0; --k) {
+      if (above < r && above + h[k] >= r) {
+        scr[0] = (uint32_t)(threadIdx.x * BPT + k);
+        scr[1] = r - above;
+        scr[2] = h[k];
+      }
+      above += h[k];
+    }
+    __syncthreads();
+    const uint32_t digit = scr[0];
+    r = scr[1];
+    nbin = scr[2];
+    __syncthreads();
+    prefix |= digit << shift;
+    mask |= dmask << shift;
+    bits = shift;
   }
-  __syncthreads();
+  *rank_in_bin = r;
+  *bin_count = nbin;
+  return prefix;
 }
+
+struct KeyPair {
+  bool first;
+  uint32_t second;
+};
 
 }  // namespace
 
-// Per query: tau = the r-th best of the sampled tiles' best scores, by
-// bisection on the order-preserving key (one wavefront per query, the row in
-// registers, counts by ballots; no barriers). The r-th best tile maximum is
-// <= the r-th best sampled score, and any tau <= the true k-th best score is
-// valid: the finalize kernel proves the kept set after the fact.
-extern "C" __global__ __launch_bounds__(64) void eos_tq_threshold(TqSelectArgs a) {
+// Per query: tau = the r-th best of the sampled tiles' best scores (radix
+// selection on the order-preserving key; one wavefront per query). The r-th
+// best tile maximum is <= the r-th best sampled score, and any tau <= the true
+// k-th best score is valid: the finalize kernel proves the kept set after the
+// fact.
+extern "C" __global__ __launch_bounds__(kThrThreads) void eos_tq_threshold(TqSelectArgs a) {
+  __shared__ uint32_t keys[kThrMax];
+  __shared__ uint32_t hist[kThrThreads / 64 * 256];
+  __shared__ uint32_t scr[16];
   const int row = blockIdx.x;
   if (row >= a.nrows) return;
-  const int lane = threadIdx.x;
-  if ((long long)a.kk > a.n || a.kk <= 0 || a.n > 64LL * kThrPer) {
-    if (lane == 0) a.tau[row] = -__builtin_inff();
+  const int tid = threadIdx.x;
+  if ((long long)a.kk > a.n || a.kk <= 0 || a.n > kThrMax) {
+    if (tid == 0) a.tau[row] = -__builtin_inff();
     return;
   }
+  const int n = (int)a.n;
   const float* x = a.rows + (size_t)row * a.stride;
-  uint32_t key[kThrPer];
-  uint32_t kmin = 0xffffffffu, kmax = 0u;
-#pragma unroll
-  for (int v = 0; v < kThrPer; ++v) {
-    const long long i = lane + 64LL * v;
-    key[v] = i < a.n ? score_key(x[i]) : 0u;
-    if (i < a.n) {
-      kmin = min(kmin, key[v]);
-      kmax = max(kmax, key[v]);
-    }
-  }
-  wave_minmax(kmin, kmax);
-  uint32_t lo = kmin, hi = kmax;
-  while (lo < hi) {
-    const uint32_t mid = lo + ((hi - lo) >> 1) + 1u;
-    uint32_t c = 0;
-#pragma unroll
-    for (int v = 0; v < kThrPer; ++v) c += (uint32_t)__popcll(__ballot(key[v] >= mid));
-    if (c >= (uint32_t)a.kk) lo = mid;
-    else hi = mid - 1u;
-  }
-  if (lane == 0) a.tau[row] = lo < 0x00800000u ? -__builtin_inff() : key_score(lo);
+  for (int i = tid; i < n; i += kThrThreads) keys[i] = score_key(x[i]);
+  __syncthreads();
+  uint32_t rib, nb;
+  const uint32_t k = block_select_desc<kThrThreads>(
+      n, [&](int i) { return KeyPair{true, keys[i]}; }, (uint32_t)a.kk, hist, scr, &rib, &nb);
+  if (tid == 0) a.tau[row] = k < 0x00800000u ? -__builtin_inff() : key_score(k);
 }
 
 // --------------------------------------------------------------- finalize
 
 // Orders each query's kept candidates (score desc, id asc) and emits the first
-// kk. Bisection on the 32-bit score key (over the kept range) finds the kk-th
-// best score K; if K is tied across the cut, a second bisection over the tied
-// ids picks the lowest ones. Rank keys are unique, so exactly kk candidates
-// are >= the resulting composite threshold; each one's output slot is its
-// count of better selected candidates. A query whose kept set is smaller than
-// kk or overflowed is flagged (status 1 / 2) for the exhaustive path; status 0
-// means its output row is final.
+// kk. A radix selection on the 32-bit score key finds the kk-th best score K;
+// if K is tied across the cut, a second selection over the tied candidates'
+// low words (~id) picks the lowest ids. Rank keys are unique, so exactly kk
+// candidates are >= the resulting composite threshold; they are ordered by
+// rank counting (or a bitonic sort when kk is large). A query whose kept set
+// is smaller than kk or overflowed is flagged (status 1 / 2) for the
+// exhaustive path; status 0 means its output row is final.
 extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFinalizeArgs a) {
-  __shared__ uint32_t slots[2 * (kFinThreads / 64)];
-  int parity = 0;
-  __shared__ uint32_t smin[kFinThreads / 64], smax[kFinThreads / 64];
+  __shared__ u64 cbuf[kSortCap];
   __shared__ u64 sel[kSortCap];
+  __shared__ uint32_t hist[kFinThreads / 64 * 256];
+  __shared__ uint32_t scr[16];
   __shared__ uint32_t sel_n;
   const int row = blockIdx.x;
   if (row >= a.q) return;
@@ -680,82 +880,61 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
     if (tid == 0) a.status[row] = 2;
     return;
   }
-  if (cnt < (uint32_t)a.kk) {
-    if (tid == 0) a.status[row] = 1;
+  if (cnt < (uint32_t)a.kk || a.kk <= 0) {
+    if (tid == 0) a.status[row] = a.kk <= 0 ? 0 : 1;
     return;
   }
-  const int nv = (int)((cnt + kFinThreads - 1) / kFinThreads);
-  u64 c[kFinPer];
-  uint32_t kmin = 0xffffffffu, kmax = 0u;
-#pragma unroll
-  for (int v = 0; v < kFinPer; ++v) {
-    const uint32_t i = tid + v * kFinThreads;
-    c[v] = (v < nv && i < cnt) ? a.cand[(size_t)row * a.cap + i] : 0ull;
-    if (c[v] != 0ull) {
-      kmin = min(kmin, (uint32_t)(c[v] >> 32));
-      kmax = max(kmax, (uint32_t)(c[v] >> 32));
-    }
-  }
-  block_minmax<kFinThreads>(kmin, kmax, smin, smax);
-  // K = the kk-th best score key.
-  uint32_t lo = kmin, hi = kmax;
-  while (lo < hi) {
-    const uint32_t mid = lo + ((hi - lo) >> 1) + 1u;
-    uint32_t n = 0;
-#pragma unroll
-    for (int v = 0; v < kFinPer; ++v)
-      if (v < nv) n += (uint32_t)__popcll(__ballot(c[v] != 0ull && (uint32_t)(c[v] >> 32) >= mid));
-    if (block_sum<kFinThreads>(n, slots, parity) >= (uint32_t)a.kk) lo = mid;
-    else hi = mid - 1u;
-  }
-  const uint32_t K = lo;
-  uint32_t ng = 0, ne = 0;
-#pragma unroll
-  for (int v = 0; v < kFinPer; ++v) {
-    if (v < nv) {
-      const uint32_t k = (uint32_t)(c[v] >> 32);
-      ng += (uint32_t)__popcll(__ballot(c[v] != 0ull && k > K));
-      ne += (uint32_t)__popcll(__ballot(c[v] != 0ull && k == K));
-    }
-  }
-  ng = block_sum<kFinThreads>(ng, slots, parity);
-  ne = block_sum<kFinThreads>(ne, slots, parity);
-  u64 thr = (u64)K << 32;
-  if (ng + ne > (uint32_t)a.kk) {
-    // Tie at the cut: keep the (kk - ng) tied candidates with the lowest ids,
-    // i.e. the largest low words (~id).
-    const uint32_t need = (uint32_t)a.kk - ng;
-    uint32_t l = 0u, h = 0xffffffffu;
-    while (l < h) {
-      const uint32_t mid = l + ((h - l) >> 1) + 1u;
-      uint32_t n = 0;
-#pragma unroll
-      for (int v = 0; v < kFinPer; ++v)
-        if (v < nv)
-          n += (uint32_t)__popcll(__ballot(c[v] != 0ull && (uint32_t)(c[v] >> 32) == K &&
-                                           (uint32_t)c[v] >= mid));
-      if (block_sum<kFinThreads>(n, slots, parity) >= need) l = mid;
-      else h = mid - 1u;
-    }
-    thr |= l;
-  }
+  const int n = (int)cnt;
+  const u64* src = a.cand + (size_t)row * a.cap;
+  for (int i = tid; i < n; i += kFinThreads) cbuf[i] = src[i];
   if (tid == 0) sel_n = 0u;
   __syncthreads();
-#pragma unroll
-  for (int v = 0; v < kFinPer; ++v) {
-    if (v < nv && c[v] != 0ull && c[v] >= thr) {
+  const uint32_t kk = (uint32_t)a.kk;
+  uint32_t need, ne;
+  const uint32_t K = block_select_desc<kFinThreads>(
+      n, [&](int i) { return KeyPair{true, (uint32_t)(cbuf[i] >> 32)}; }, kk, hist, scr, &need, &ne);
+  u64 thr = (u64)K << 32;
+  if (ne > need) {
+    // Tie at the cut: of the ne candidates scoring K keep the `need` with the
+    // lowest ids, i.e. the largest low words (~id).
+    uint32_t r2, n2;
+    const uint32_t L = block_select_desc<kFinThreads>(
+        n,
+        [&](int i) {
+          const u64 c = cbuf[i];
+          return KeyPair{(uint32_t)(c >> 32) == K, (uint32_t)c};
+        },
+        need, hist, scr, &r2, &n2);
+    thr |= L;
+  }
+  for (int i = tid; i < n; i += kFinThreads) {
+    const u64 c = cbuf[i];
+    if (c >= thr) {
       const uint32_t pos = atomicAdd(&sel_n, 1u);
-      if (pos < (uint32_t)kSortCap) sel[pos] = c[v];
+      if (pos < kk) sel[pos] = c;
     }
   }
   __syncthreads();
-  for (int i = tid; i < a.kk; i += kFinThreads) {
-    const u64 x = sel[i];
-    int rank = 0;
+  if (kk <= (uint32_t)kRankSortMax) {
+    for (uint32_t i = tid; i < kk; i += kFinThreads) {
+      const u64 x = sel[i];
+      uint32_t rank = 0;
 #pragma unroll 8
-    for (int j = 0; j < a.kk; ++j) rank += sel[j] > x ? 1 : 0;
-    a.ids[(size_t)row * a.kk + rank] = (long long)rank_id(x);
-    a.scores[(size_t)row * a.kk + rank] = key_score((uint32_t)(x >> 32));
+      for (uint32_t j = 0; j < kk; ++j) rank += sel[j] > x ? 1u : 0u;
+      a.ids[(size_t)row * kk + rank] = (long long)rank_id(x);
+      a.scores[(size_t)row * kk + rank] = key_score((uint32_t)(x >> 32));
+    }
+  } else {
+    int npow = 1;
+    while (npow < (int)kk) npow <<= 1;
+    for (int i = (int)kk + tid; i < npow; i += kFinThreads) sel[i] = 0ull;
+    __syncthreads();
+    bitonic_sort_desc(sel, npow);
+    for (uint32_t i = tid; i < kk; i += kFinThreads) {
+      const u64 x = sel[i];
+      a.ids[(size_t)row * kk + i] = (long long)rank_id(x);
+      a.scores[(size_t)row * kk + i] = key_score((uint32_t)(x >> 32));
+    }
   }
   if (tid == 0) a.status[row] = 0;
 }
@@ -776,7 +955,8 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Wave-uniform tile indices keep the tile addressing in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = gridDim.x * (kScanThreads / 64);
   const int half = lane >> 5;
   const v4i* packed = reinterpret_cast<const v4i*>(a.packed);

@@ -89,6 +89,10 @@ class Runtime:
     def profile(self, enabled: bool) -> None:
         _lib.call("eoship_profile_enable", self.handle, int(bool(enabled)))
 
+    def profile_select(self, prefix: str | None) -> None:
+        """Record only launches whose label starts with ``prefix`` (None = all)."""
+        _lib.call("eoship_profile_select", self.handle, prefix.encode() if prefix else None)
+
     def profile_reset(self) -> None:
         _lib.call("eoship_profile_reset", self.handle)
 

@@ -68,6 +68,10 @@ int eoship_launch(EosHipRuntime* rt, EosHipFunction* fn, const uint32_t grid[3],
  * (native_linux.go:285-500). When enabled, every launch of a library kernel is
  * bracketed by two events on the runtime stream. */
 int eoship_profile_enable(EosHipRuntime* rt, int enabled, char** err);
+/* Restricts profiling to launches whose label starts with prefix (NULL or ""
+ * records every launch), so that a timed loop can bracket one kernel without
+ * paying two events for every other launch. */
+int eoship_profile_select(EosHipRuntime* rt, const char* prefix, char** err);
 /* Sums the recorded launches of kernels whose name starts with prefix. */
 int eoship_profile_read(EosHipRuntime* rt, const char* prefix, int64_t* launches, double* total_ms,
                         char** err);

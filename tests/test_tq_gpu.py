@@ -95,6 +95,41 @@ def test_topk_multiple_batches(rt):
     assert stats.batches == 3
 
 
+def test_topk_ties_at_the_cut_filter_path(rt):
+    """Every vector appears 8 times (copies 5000 ids apart), so the k-th best
+    score is tied across the cut; the filtered path (no fallback) must keep the
+    lowest ids of the tied group, as the oracle's heap does."""
+    _case("topk ties at the cut n=40000")
+    c = _corpus(5000, 384, 4, seed=13)
+    codes = np.tile(c.codes, (8, 1))
+    norms = np.tile(c.norms, 8)
+    q = datagen.baseline_queries(64, 384, 14)
+    idx = _index(rt, c, norms=norms, codes=codes)
+    for k in (1, 7, 100, 255):
+        ids, sc, stats = idx.top_k(q, k)
+        oids, osc = oracle.tq_topk(q, c.rotation, 384, 4, c.codebook, c.codebook_scale, codes,
+                                   norms, k)
+        np.testing.assert_array_equal(ids, oids)
+        np.testing.assert_array_equal(sc, osc)
+        assert stats.fallback_queries == 0
+
+
+@pytest.mark.parametrize("k", [1024, 1025, 3000, 8192])
+def test_topk_large_k_sorted_on_device(rt, k):
+    """n <= the candidate capacity keeps every vector; large k orders the kept
+    set with the bitonic sort instead of rank counting."""
+    _case(f"topk n=8192 k={k}")
+    c = _corpus(8192, 128, 2, seed=15)
+    q = datagen.baseline_queries(5, 128, 16)
+    idx = _index(rt, c)
+    ids, sc, stats = idx.top_k(q, k)
+    oids, osc = oracle.tq_topk(q, c.rotation, 128, 2, c.codebook, c.codebook_scale, c.codes,
+                               c.norms, k)
+    np.testing.assert_array_equal(ids, oids)
+    np.testing.assert_array_equal(sc, osc)
+    assert stats.fallback_queries == 0
+
+
 def test_topk_all_ties_uses_exact_fallback(rt):
     """Every vector scores the same: the filter overflows, the exhaustive path
     must return ids 0..k-1 (ties to the lower id)."""
