@@ -98,6 +98,10 @@ _SIGNATURES = {
     "eoship_tq_topk_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                                C.c_void_p, C.c_void_p, C.POINTER(EosHipTQStats), C.c_void_p],
                               C.c_int),
+    "eoship_tq_topk_device_deferred": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_topk_repair_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_tq_scores": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int64, C.c_int64,
                           C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_tq_prepare": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p,

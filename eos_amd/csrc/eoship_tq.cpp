@@ -280,12 +280,14 @@ struct EosHipTQ {
     return launch_scan(&s, qb, err);
   }
 
-  // Enqueues one batch on the runtime stream; no host synchronisation unless
-  // stats are requested. The exact fallback is launched unconditionally and
-  // gated on the device by the finalize status, so results are exact without a
-  // host round trip.
+  // Enqueues one batch on the runtime stream (no host synchronisation):
+  // prepare, sample + threshold, filter scan, finalize. Finalize writes each
+  // query's status to d_status (0: its row is final; 1: fewer than k kept;
+  // 2: the kept set overflowed). With `gated` the exact fallback follows on
+  // the device, gated by those flags, so the rows are exact when the stream
+  // reaches that point; otherwise flagged rows wait for fallback_batch.
   int topk_batch(const float* d_queries, int qb, int kk, int64_t* d_ids, float* d_scores,
-                 EosHipTQStats* st, char** err) {
+                 int* d_status, bool gated, char** err) {
     if (prepare(d_queries, qb, nullptr, err) != 0) return 1;
     if (n > kCap) {
       const int64_t stride = std::max<int64_t>(kSampleStride, (ntiles + kMaxSampleTiles - 1) / kMaxSampleTiles);
@@ -326,16 +328,29 @@ struct EosHipTQ {
     f.cand_count = cand_count;
     f.ids = reinterpret_cast<long long*>(d_ids);
     f.scores = d_scores;
-    f.status = status;
+    f.status = d_status;
     f.cap = kCap;
     f.kk = kk;
     f.q = qb;
     if (rt->launch("eos_tq_finalize", dim3(qb), dim3(256), 0, &f, err) != 0) return 1;
-    // Exact fallback, gated on status: exhaustive scores + radix selection.
+    if (gated) return fallback_batch(d_queries, qb, kk, d_ids, d_scores, d_status, false, err);
+    return 0;
+  }
+
+  // Exact fallback of one batch, gated on the device by d_status: exhaustive
+  // scores of the batch (skipped by every workgroup when no query is
+  // flagged) and an exact radix selection for each flagged row. `reprepare`
+  // rebuilds the query fragments first (another batch may have used them).
+  int fallback_batch(const float* d_queries, int qb, int kk, int64_t* d_ids, float* d_scores,
+                     const int* d_status, bool reprepare, char** err) {
+    if (ensure(reinterpret_cast<void**>(&dense), &dense_bytes, (size_t)qb * (size_t)n * sizeof(float),
+               err) != 0)
+      return 1;
+    if (reprepare && prepare(d_queries, qb, nullptr, err) != 0) return 1;
     TqScanArgs ds;
     scan_base(&ds, qb);
     ds.mode = 0;
-    ds.gate = status;
+    ds.gate = d_status;
     ds.out_scores = dense;
     ds.out_begin = 0;
     ds.out_count = n;
@@ -346,7 +361,7 @@ struct EosHipTQ {
     TqSelectArgs sel;
     memset(&sel, 0, sizeof(sel));
     sel.rows = dense;
-    sel.status = status;
+    sel.status = d_status;
     sel.ids = reinterpret_cast<long long*>(d_ids);
     sel.scores = d_scores;
     sel.n = n;
@@ -354,23 +369,30 @@ struct EosHipTQ {
     sel.kk = kk;
     sel.mode = 1;
     sel.nrows = qb;
-    if (rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err, "tq_fallback_select") != 0)
-      return 1;
+    return rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err, "tq_fallback_select");
+  }
+
+  // Waits for the batch and reads its per-query status (and kept counts for
+  // the statistics); returns the number of flagged queries in *flagged.
+  int batch_status(int qb, const int* d_status, EosHipTQStats* st, int* flagged, char** err) {
+    int hstatus[kBatch];
+    uint32_t hcount[kBatch];
+    hipError_t e = hipMemcpyAsync(hstatus, d_status, sizeof(int) * qb, hipMemcpyDeviceToHost, rt->stream);
+    if (e == hipSuccess && st)
+      e = hipMemcpyAsync(hcount, cand_count, sizeof(uint32_t) * qb, hipMemcpyDeviceToHost, rt->stream);
+    if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
+    if (rt->sync(err) != 0) return 1;
+    int nf = 0;
+    for (int i = 0; i < qb; ++i) {
+      if (hstatus[i] != 0) ++nf;
+      if (st) st->candidates_kept += std::min<uint32_t>(hcount[i], (uint32_t)kCap);
+    }
     if (st) {
-      int hstatus[kBatch];
-      uint32_t hcount[kBatch];
-      hipError_t e = hipMemcpyAsync(hstatus, status, sizeof(int) * qb, hipMemcpyDeviceToHost, rt->stream);
-      if (e == hipSuccess)
-        e = hipMemcpyAsync(hcount, cand_count, sizeof(uint32_t) * qb, hipMemcpyDeviceToHost, rt->stream);
-      if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
-      if (rt->sync(err) != 0) return 1;
-      for (int i = 0; i < qb; ++i) {
-        if (hstatus[i] != 0) st->fallback_queries += 1;
-        st->candidates_kept += std::min<uint32_t>(hcount[i], (uint32_t)kCap);
-      }
+      st->fallback_queries += nf;
       st->candidate_count += (int64_t)qb * n;
       st->batches += 1;
     }
+    *flagged = nf;
     return 0;
   }
 };
@@ -531,9 +553,21 @@ int eoship_tq_release(EosHipTQ* tq, char** err) {
   return 0;
 }
 
+static int check_common(EosHipRuntime* rt, EosHipTQ* tq, int32_t q, const char* what, char** err) {
+  if (rt == nullptr || tq == nullptr) return set_err(err, "%s: NULL runtime or corpus", what);
+  if (tq->rt != rt) return set_err(err, "%s: corpus was bound on another runtime", what);
+  if (q < 0) return set_err(err, "%s: negative query count", what);
+  return 0;
+}
+
+// Batches of <= 64 queries through the pipeline. mode 0: the device-gated
+// exact fallback follows every batch (no host wait). mode 1: statuses go to
+// d_status_out and flagged rows are left for eoship_tq_topk_repair_device.
+// mode 2 (host API): each batch is awaited and the fallback runs only for a
+// batch with a flagged query.
 static int topk_device_impl(EosHipRuntime* rt, EosHipTQ* tq, const float* d_queries, int32_t q,
                             int32_t k, int64_t* d_ids, float* d_scores, EosHipTQStats* stats,
-                            char** err) {
+                            int mode, int32_t* d_status_out, char** err) {
   if (stats) memset(stats, 0, sizeof(*stats));
   const int64_t kk64 = (k <= 0 || (int64_t)k > tq->n) ? tq->n : k;
   if (q == 0 || kk64 == 0) return 0;
@@ -542,22 +576,20 @@ static int topk_device_impl(EosHipRuntime* rt, EosHipTQ* tq, const float* d_quer
                    (long long)kk64, kSortCap);
   const int kk = (int)kk64;
   const int cap = tq->batch_cap();
-  if (tq->ensure(reinterpret_cast<void**>(&tq->dense), &tq->dense_bytes,
-                 (size_t)std::min(cap, (int)q) * (size_t)tq->n * sizeof(float), err) != 0)
-    return 1;
   for (int q0 = 0; q0 < q; q0 += cap) {
     const int qb = std::min(cap, q - q0);
-    if (tq->topk_batch(d_queries + (size_t)q0 * tq->d, qb, kk, d_ids + (size_t)q0 * kk,
-                       d_scores + (size_t)q0 * kk, stats, err) != 0)
-      return 1;
+    const float* dq = d_queries + (size_t)q0 * tq->d;
+    int64_t* di = d_ids + (size_t)q0 * kk;
+    float* ds = d_scores + (size_t)q0 * kk;
+    int* st = mode == 1 ? d_status_out + q0 : tq->status;
+    if (tq->topk_batch(dq, qb, kk, di, ds, st, mode == 0, err) != 0) return 1;
+    if (mode == 2 || stats) {
+      int flagged = 0;
+      if (tq->batch_status(qb, st, stats, &flagged, err) != 0) return 1;
+      if (mode == 2 && flagged > 0 && tq->fallback_batch(dq, qb, kk, di, ds, st, false, err) != 0)
+        return 1;
+    }
   }
-  return 0;
-}
-
-static int check_common(EosHipRuntime* rt, EosHipTQ* tq, int32_t q, const char* what, char** err) {
-  if (rt == nullptr || tq == nullptr) return set_err(err, "%s: NULL runtime or corpus", what);
-  if (tq->rt != rt) return set_err(err, "%s: corpus was bound on another runtime", what);
-  if (q < 0) return set_err(err, "%s: negative query count", what);
   return 0;
 }
 
@@ -567,7 +599,38 @@ int eoship_tq_topk_device(EosHipRuntime* rt, EosHipTQ* tq, const float* d_querie
   if (check_common(rt, tq, q, "eoship_tq_topk_device", err) != 0) return 1;
   if (q > 0 && (d_queries == nullptr || d_ids == nullptr || d_scores == nullptr))
     return set_err(err, "eoship_tq_topk_device: NULL buffer");
-  return topk_device_impl(rt, tq, d_queries, q, k, d_ids, d_scores, stats, err);
+  return topk_device_impl(rt, tq, d_queries, q, k, d_ids, d_scores, stats, 0, nullptr, err);
+}
+
+int eoship_tq_topk_device_deferred(EosHipRuntime* rt, EosHipTQ* tq, const float* d_queries,
+                                   int32_t q, int32_t k, int64_t* d_ids, float* d_scores,
+                                   int32_t* d_status, char** err) {
+  if (check_common(rt, tq, q, "eoship_tq_topk_device_deferred", err) != 0) return 1;
+  if (q > 0 && (d_queries == nullptr || d_ids == nullptr || d_scores == nullptr || d_status == nullptr))
+    return set_err(err, "eoship_tq_topk_device_deferred: NULL buffer");
+  return topk_device_impl(rt, tq, d_queries, q, k, d_ids, d_scores, nullptr, 1, d_status, err);
+}
+
+int eoship_tq_topk_repair_device(EosHipRuntime* rt, EosHipTQ* tq, const float* d_queries, int32_t q,
+                                 int32_t k, int64_t* d_ids, float* d_scores,
+                                 const int32_t* d_status, char** err) {
+  if (check_common(rt, tq, q, "eoship_tq_topk_repair_device", err) != 0) return 1;
+  const int64_t kk64 = (k <= 0 || (int64_t)k > tq->n) ? tq->n : k;
+  if (q == 0 || kk64 == 0) return 0;
+  if (d_queries == nullptr || d_ids == nullptr || d_scores == nullptr || d_status == nullptr)
+    return set_err(err, "eoship_tq_topk_repair_device: NULL buffer");
+  if (kk64 > kSortCap)
+    return set_err(err, "eoship_tq_topk_repair_device: k=%lld exceeds the device top-k limit of %d",
+                   (long long)kk64, kSortCap);
+  const int kk = (int)kk64;
+  const int cap = tq->batch_cap();
+  for (int q0 = 0; q0 < q; q0 += cap) {
+    const int qb = std::min(cap, q - q0);
+    if (tq->fallback_batch(d_queries + (size_t)q0 * tq->d, qb, kk, d_ids + (size_t)q0 * kk,
+                           d_scores + (size_t)q0 * kk, d_status + q0, true, err) != 0)
+      return 1;
+  }
+  return 0;
 }
 
 int eoship_tq_topk(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int32_t q, int32_t k,
@@ -588,7 +651,7 @@ int eoship_tq_topk(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int32_
   float* ds = reinterpret_cast<float*>(reinterpret_cast<char*>(di) + ibytes);
   hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
-  if (topk_device_impl(rt, tq, dq, q, k, di, ds, stats, err) != 0) return 1;
+  if (topk_device_impl(rt, tq, dq, q, k, di, ds, stats, 2, nullptr, err) != 0) return 1;
   e = hipMemcpyAsync(ids, di, ibytes, hipMemcpyDeviceToHost, rt->stream);
   if (e == hipSuccess) e = hipMemcpyAsync(scores, ds, sbytes, hipMemcpyDeviceToHost, rt->stream);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(results)", e);

@@ -45,6 +45,45 @@ EOS_DEV u64 rank_key(float s, uint32_t id) {
 }
 EOS_DEV uint32_t rank_id(u64 c) { return ~(uint32_t)(c & 0xffffffffu); }
 
+// Calls f(i, src[i]) for i = threadIdx.x, threadIdx.x + NT, ... < n with U
+// loads of each thread in flight before any value is used (a loop whose
+// every iteration uses its own load would wait one memory round trip per
+// iteration). Indices past n are clamped for the load and skipped for f.
+template <int NT, int U, typename T, typename F>
+EOS_DEV void for_each_batched(const T* src, long long n, F f) {
+  for (long long base = threadIdx.x; base < n; base += (long long)NT * U) {
+    T v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long i = base + (long long)u * NT;
+      v[u] = src[i < n ? i : n - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long i = base + (long long)u * NT;
+      if (i < n) f(i, v[u]);
+    }
+  }
+}
+
+// Copies the query fragments [KS*NCB*64] into LDS with every load issued
+// before the first store.
+template <int NT, int COUNT>
+EOS_DEV void stage_fragments(v4i* dst, const v4i* src) {
+  constexpr int PER = (COUNT + NT - 1) / NT;
+  v4i v[PER];
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int i = threadIdx.x + r * NT;
+    if (i < COUNT) v[r] = src[i];
+  }
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int i = threadIdx.x + r * NT;
+    if (i < COUNT) dst[i] = v[r];
+  }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ prepare
@@ -301,12 +340,6 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     for (int i = 0; i < a.q; ++i) any |= a.gate[i] != 0;
     if (!any) return;
   }
-  {
-    const v4i* src = reinterpret_cast<const v4i*>(a.bfrag);
-    for (int i = threadIdx.x; i < KS * NCB * 64; i += kScanThreads) sb[i] = src[i];
-    if (FILTER && threadIdx.x < NQ) lc_cnt[threadIdx.x] = 0u;
-  }
-  __syncthreads();
   const int lane = threadIdx.x & 63;
   // Wave-uniform tile indices keep the tile addressing in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -492,12 +525,19 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   // Three stages (codes two tiles ahead) when the ring and the accumulators
   // fit the 256 registers of two waves per SIMD; two stages otherwise.
   constexpr bool kRing3 = NLOAD * 12 + NCB * 16 <= 168;
+  // The first tiles are requested before the query fragments are staged, so
+  // the two round trips overlap. Every wave reaches the barrier.
+  Stage s0, s1, s2;
+  if (j < nt) {
+    load_codes(s0, j);
+    load_norms(s0, j);
+    if constexpr (kRing3) load_codes(s1, cl(j + nw));
+  }
+  stage_fragments<kScanThreads, KS * NCB * 64>(sb, reinterpret_cast<const v4i*>(a.bfrag));
+  if (FILTER && threadIdx.x < NQ) lc_cnt[threadIdx.x] = 0u;
+  __syncthreads();
   if (j < nt) {
     if constexpr (kRing3) {
-      Stage s0, s1, s2;
-      load_codes(s0, j);
-      load_norms(s0, j);
-      load_codes(s1, cl(j + nw));
       for (;;) {
         load_codes(s2, cl(j + 2 * nw));
         load_norms(s1, cl(j + nw));
@@ -514,9 +554,6 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
         if (j >= nt) break;
       }
     } else {
-      Stage s0, s1;
-      load_codes(s0, j);
-      load_norms(s0, j);
       for (;;) {
         load_codes(s1, cl(j + nw));
         load_norms(s1, cl(j + nw));
@@ -632,10 +669,10 @@ extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_row_select(TqSe
     __syncthreads();
     const u64 pfx = sel_prefix;
     const u64 hmask = p == 0 ? 0ull : ~((1ull << (shift + 8)) - 1ull);
-    for (long long i = tid; i < a.n; i += kSelThreads) {
-      const u64 c = rank_key(x[i], (uint32_t)i);
+    for_each_batched<kSelThreads, 8>(x, a.n, [&](long long i, float v) {
+      const u64 c = rank_key(v, (uint32_t)i);
       if (((c ^ pfx) & hmask) == 0ull) atomicAdd(&hist[(c >> shift) & 255u], 1u);
-    }
+    });
     __syncthreads();
     if (tid == 0) {
       int rem = sel_rem;
@@ -665,13 +702,13 @@ extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_row_select(TqSe
   if (tid == 0) list_n = 0;
   for (int i = tid; i < npow; i += kSelThreads) list[i] = 0ull;
   __syncthreads();
-  for (long long i = tid; i < a.n; i += kSelThreads) {
-    const u64 c = rank_key(x[i], (uint32_t)i);
+  for_each_batched<kSelThreads, 8>(x, a.n, [&](long long i, float v) {
+    const u64 c = rank_key(v, (uint32_t)i);
     if (c >= thr) {
       const int pos = atomicAdd(&list_n, 1);
       if (pos < kSortCap) list[pos] = c;
     }
-  }
+  });
   __syncthreads();
   bitonic_sort_desc(list, npow);
   for (int i = tid; i < a.kk; i += kSelThreads) {
@@ -848,7 +885,7 @@ extern "C" __global__ __launch_bounds__(kThrThreads) void eos_tq_threshold(TqSel
   }
   const int n = (int)a.n;
   const float* x = a.rows + (size_t)row * a.stride;
-  for (int i = tid; i < n; i += kThrThreads) keys[i] = score_key(x[i]);
+  for_each_batched<kThrThreads, 8>(x, n, [&](long long i, float v) { keys[i] = score_key(v); });
   __syncthreads();
   uint32_t rib, nb;
   const uint32_t k = block_select_desc<kThrThreads>(
@@ -886,7 +923,7 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
   }
   const int n = (int)cnt;
   const u64* src = a.cand + (size_t)row * a.cap;
-  for (int i = tid; i < n; i += kFinThreads) cbuf[i] = src[i];
+  for_each_batched<kFinThreads, 8>(src, n, [&](long long i, u64 v) { cbuf[i] = v; });
   if (tid == 0) sel_n = 0u;
   __syncthreads();
   const uint32_t kk = (uint32_t)a.kk;
@@ -950,8 +987,7 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
   constexpr int NLOAD = (KS + SPL - 1) / SPL;
   __shared__ v4i sb[KS * NCB * 64];
   {
-    const v4i* src = reinterpret_cast<const v4i*>(a.bfrag);
-    for (int i = threadIdx.x; i < KS * NCB * 64; i += kScanThreads) sb[i] = src[i];
+    stage_fragments<kScanThreads, KS * NCB * 64>(sb, reinterpret_cast<const v4i*>(a.bfrag));
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;

@@ -44,7 +44,18 @@ class DeviceBuffer:
                   C.c_size_t(out.nbytes))
         return out
 
+    def view(self, offset: int, nbytes: int) -> "DeviceBuffer":
+        """A non-owning window [offset, offset + nbytes) of this allocation."""
+        if offset < 0 or nbytes < 0 or offset + nbytes > self.nbytes:
+            raise ValueError("view outside the buffer")
+        v = DeviceBuffer.__new__(DeviceBuffer)
+        v.rt, v.nbytes, v._owner = self.rt, int(nbytes), self
+        v.ptr = C.c_void_p(self.ptr.value + int(offset))
+        return v
+
     def free(self) -> None:
+        if getattr(self, "_owner", None) is not None:
+            return  # a view owns nothing
         if self.ptr:
             _lib.call("eoship_free", self.rt.handle, self.ptr)
             self.ptr = C.c_void_p()

@@ -126,6 +126,20 @@ class TurboQuantIndex:
                   C.byref(st) if st is not None else None)
         return st
 
+    def top_k_device_deferred(self, d_queries: DeviceBuffer, nq: int, top_k: int,
+                              d_ids: DeviceBuffer, d_scores: DeviceBuffer,
+                              d_status: DeviceBuffer) -> None:
+        """Enqueue a top-k without the exhaustive fallback: int32 d_status[nq]
+        receives 0 for final rows, nonzero for rows repair_device must redo."""
+        _lib.call("eoship_tq_topk_device_deferred", self.rt.handle, self.handle, d_queries.ptr,
+                  C.c_int32(nq), C.c_int32(int(top_k)), d_ids.ptr, d_scores.ptr, d_status.ptr)
+
+    def repair_device(self, d_queries: DeviceBuffer, nq: int, top_k: int, d_ids: DeviceBuffer,
+                      d_scores: DeviceBuffer, d_status: DeviceBuffer) -> None:
+        """Exhaustively recompute the rows a deferred top-k flagged."""
+        _lib.call("eoship_tq_topk_repair_device", self.rt.handle, self.handle, d_queries.ptr,
+                  C.c_int32(nq), C.c_int32(int(top_k)), d_ids.ptr, d_scores.ptr, d_status.ptr)
+
     def inner_product_prepared(self, queries: np.ndarray, begin: int = 0, count: int | None = None):
         """Exhaustive (dots int32 [Q, count], scores float32 [Q, count]) for vectors [begin, begin+count)."""
         q = self._queries(queries)

@@ -89,7 +89,7 @@ int eoship_timer_elapsed(EosHipRuntime* rt, int slot_begin, int slot_end, double
  * plus one f32 Norm. Codebook centroid v is codebook_scale * codebook[v]
  * (int8 grid). Scores estimate <q, x> = Norm * <R q, c[code]>. */
 typedef struct {
-  int32_t dim;              /* vector dimension d (1..2048) */
+  int32_t dim;              /* vector dimension d (1..1024) */
   int32_t bits;             /* code width: 2 or 4 */
   float codebook_scale;     /* s_c > 0 */
   const int8_t* codebook;   /* 2^bits int8 centroids (host) */
@@ -123,6 +123,20 @@ int eoship_tq_topk(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int32_
 int eoship_tq_topk_device(EosHipRuntime* rt, EosHipTQ* tq, const float* d_queries, int32_t q,
                           int32_t k, int64_t* d_ids, float* d_scores, EosHipTQStats* stats,
                           char** err);
+/* The same top-k with the exactness check left to the caller, for callers that
+ * synchronise once per many calls (also topTurboQuantRetrievalScoresWithStats,
+ * runtime/retrieval_turboquant.go:1853-1887). Enqueues no exhaustive fallback;
+ * writes d_status[Q] instead: 0 means the query's row is final, nonzero means
+ * the filtered pass could not prove it and eoship_tq_topk_repair_device must
+ * be called for it (with the same queries and k) before the row is used. */
+int eoship_tq_topk_device_deferred(EosHipRuntime* rt, EosHipTQ* tq, const float* d_queries,
+                                   int32_t q, int32_t k, int64_t* d_ids, float* d_scores,
+                                   int32_t* d_status, char** err);
+/* Recomputes, exhaustively and exactly, the rows whose d_status is nonzero
+ * (the rest are left as they are). */
+int eoship_tq_topk_repair_device(EosHipRuntime* rt, EosHipTQ* tq, const float* d_queries, int32_t q,
+                                 int32_t k, int64_t* d_ids, float* d_scores,
+                                 const int32_t* d_status, char** err);
 /* Exhaustive scores and exact integer code dot products for vectors
  * [begin, begin+count) (host outputs [Q][count]; either may be NULL). The
  * counterpart of InnerProductPrepared over a slice of documents

@@ -147,6 +147,37 @@ def test_topk_all_ties_uses_exact_fallback(rt):
     assert stats.fallback_queries == 8
 
 
+def test_topk_deferred_status_and_repair(rt):
+    """The deferred device path flags exactly the rows the filter cannot prove;
+    after repair_device every row equals the oracle's (clean corpus: no flags,
+    same rows as the gated device path; all-ties corpus: every row flagged)."""
+    from eos_amd.runtime import DeviceBuffer
+    _case("topk deferred + repair")
+    c = _corpus(30000, 384, 4, seed=17)
+    q = datagen.baseline_queries(70, 384, 18)
+    for codes, norms, expect_flags in ((c.codes, c.norms, False),
+                                       (np.full_like(c.codes, 0x55), np.ones(c.n, np.float32), True)):
+        idx = _index(rt, c, norms=norms, codes=codes)
+        k = 100
+        dq = DeviceBuffer.from_array(rt, q)
+        dids = DeviceBuffer(rt, 70 * k * 8)
+        dsc = DeviceBuffer(rt, 70 * k * 4)
+        dst = DeviceBuffer(rt, 70 * 4)
+        idx.top_k_device_deferred(dq, 70, k, dids, dsc, dst)
+        status = dst.download(np.int32, (70,))
+        assert bool(np.any(status != 0)) == expect_flags
+        if expect_flags:
+            assert np.all(status != 0)
+        idx.repair_device(dq, 70, k, dids, dsc, dst)
+        ids = dids.download(np.int64, (70, k))
+        sc = dsc.download(np.float32, (70, k))
+        oids, osc = oracle.tq_topk(q, c.rotation, 384, 4, c.codebook, c.codebook_scale, codes,
+                                   norms, k)
+        np.testing.assert_array_equal(ids, oids)
+        np.testing.assert_array_equal(sc, osc)
+        idx.release()
+
+
 def test_topk_zero_norms_zero_query_and_k_semantics(rt):
     _case("topk edge cases")
     c = _corpus(500, 384, 4, seed=7)
