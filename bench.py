@@ -54,16 +54,25 @@ def cpu_baseline(corpus, queries, nq_sample: int) -> dict:
     }
 
 
-def encoder_leg(rt, steps: int) -> dict:
-    """q8 BERT-style encoder, 6 layers, hidden 384, 12 heads,
-    FFN 1536, batch 64 x seq 512, lengths U[32, 512]; inputs resident on device."""
+ENCODER_CONFIGS = {
+    # name: layers, hidden, heads, ffn, batch, seq, len_lo, len_hi, weight seed, ids seed, len seed
+    "c3": (6, 384, 12, 1536, 64, 512, 32, 512, 7, 8, 9),
+    "c4": (4, 512, 8, 2048, 4, 8192, 4096, 8192, 10, 11, 10),
+}
+
+
+def encoder_leg(rt, steps: int, name: str = "c3") -> dict:
+    """BASELINE config 3 (q8 BERT-style encoder, 6 layers, hidden 384, 12
+    heads, FFN 1536, batch 64 x seq 512, lengths U[32, 512]) or config 4 (long
+    context: 4 layers, hidden 512, 8 heads, FFN 2048, batch 4 x 8192, lengths
+    U[4096, 8192]); inputs resident on device."""
     from eos_amd import datagen
     from eos_amd.encoder import Encoder
     from eos_amd.runtime import DeviceBuffer
 
-    L, H, NH, F, B, T = 6, 384, 12, 1536, 64, 512
-    w = datagen.bert_q8_weights(L, H, NH, F, 30522, T, seed=7)
-    ids, mask, lens = datagen.encoder_batch(B, T, 30522, 32, 512, 8, 9)
+    L, H, NH, F, B, T, lo, hi, sw, si, sl = ENCODER_CONFIGS[name]
+    w = datagen.bert_q8_weights(L, H, NH, F, 30522, T, seed=sw)
+    ids, mask, lens = datagen.encoder_batch(B, T, 30522, lo, hi, si, sl)
     enc = Encoder(rt, w)
     d_ids = DeviceBuffer.from_array(rt, ids)
     d_mask = DeviceBuffer.from_array(rt, mask)
@@ -84,10 +93,10 @@ def encoder_leg(rt, steps: int) -> dict:
         enc.embed_device(d_ids, d_mask, B, T, d_out)
     rt.sync()
     kernels = {}
-    for name in ("eos_enc_pack", "eos_enc_embed", "enc_gemm_qkv", "eos_enc_attn", "enc_gemm_o_ln",
-                 "enc_gemm_ffn_up", "enc_gemm_ffn_down_ln", "eos_enc_pool"):
-        n, t = rt.profile_read(name)
-        kernels[name] = t / steps
+    for kname in ("eos_enc_pack", "eos_enc_embed", "enc_gemm_qkv", "eos_enc_attn", "enc_gemm_o_ln",
+                  "enc_gemm_ffn_up", "enc_gemm_ffn_down_ln", "eos_enc_pool"):
+        n, t = rt.profile_read(kname)
+        kernels[kname] = t / steps
     rt.profile(False)
     valid = int(lens.sum())
     lin = 2.0 * valid * L * (3 * H * H + H * H + 2 * H * F)
@@ -96,9 +105,9 @@ def encoder_leg(rt, steps: int) -> dict:
     achieved = flops / (ms / 1e3) / 1e12
     enc.release()
     return {
-        "metric": "q8 encoder tokens/s @seq512",
+        "metric": f"q8 encoder tokens/s @seq{T}",
         "value": B * T / (ms / 1e3),
-        "unit": "tokens/s (batch x 512 per forward)",
+        "unit": f"tokens/s (batch x {T} per forward)",
         "valid_tokens_per_s": valid / (ms / 1e3),
         "ms_per_forward": ms,
         "config": {"layers": L, "hidden": H, "heads": NH, "ffn": F, "batch": B, "seq": T,
@@ -254,6 +263,7 @@ def main() -> int:
     ap.add_argument("--skip-encoder", action="store_true")
     ap.add_argument("--skip-tq", action="store_true", help="profiling runs of the encoder only")
     ap.add_argument("--encoder-steps", type=int, default=5)
+    ap.add_argument("--encoder-configs", default="c3,c4", help="comma list of c3, c4")
     ap.add_argument("--copy-calibration-mb", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -283,8 +293,9 @@ def main() -> int:
     if not args.skip_tq:
         out.update(tq_leg(rt, args))
     if not args.skip_encoder:
-        log("encoder c3")
-        out["encoder_c3"] = encoder_leg(rt, args.encoder_steps)
+        for name in args.encoder_configs.split(","):
+            log(f"encoder {name}")
+            out[f"encoder_{name}"] = encoder_leg(rt, args.encoder_steps, name)
     if args.copy_calibration_mb > 0:
         out["copy_calibration"] = copy_calibration(rt, args.copy_calibration_mb)
     out["device"] = info

@@ -44,43 +44,93 @@ EOS_DEV float gelu(float x, int kind) {
 
 // ------------------------------------------------------------------- pack
 
+namespace {
+
+// Block-wide exclusive prefix sum of one int per thread (256 threads);
+// *total receives the sum over the block. `scr` holds 4 ints.
+EOS_DEV int block_exclusive_scan256(int v, int* scr, int* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(inc, o);
+    if (lane >= o) inc += t;
+  }
+  if (lane == 63) scr[w] = inc;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    before += i < w ? scr[i] : 0;
+    all += scr[i];
+  }
+  __syncthreads();
+  *total = all;
+  return before + inc - v;
+}
+
+}  // namespace
+
 // One workgroup per sequence: its offset is the number of active positions
 // of the sequences before it; positions are compacted in increasing order.
+// Thread i owns the contiguous positions [i * per, (i + 1) * per); mask
+// values are read 8 per thread at a time so the loads overlap.
 extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
-  __shared__ int wsum[4];
-  __shared__ int base_sh;
+  __shared__ int scr[4];
   const int b = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x;
+  // Active positions of the sequences before b.
+  const long long nb = (long long)b * a.tokens;
   int before = 0;
-  for (long long i = tid; i < (long long)b * a.tokens; i += 256) before += a.mask[i] != 0;
-  for (int o = 32; o > 0; o >>= 1) before += __shfl_xor(before, o);
-  if (lane == 0) wsum[w] = before;
-  __syncthreads();
-  if (tid == 0) base_sh = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-  __syncthreads();
-  int base = base_sh;
-  const int32_t* m = a.mask + (size_t)b * a.tokens;
-  for (int t0 = 0; t0 < a.tokens; t0 += 256) {
-    const int t = t0 + tid;
-    const bool on = t < a.tokens && m[t] != 0;
-    const unsigned long long bal = __ballot(on);
-    const int below = __popcll(bal & ((1ull << lane) - 1ull));
-    __syncthreads();
-    if (lane == 0) wsum[w] = __popcll(bal);
-    __syncthreads();
-    int woff = 0;
-    for (int i = 0; i < w; ++i) woff += wsum[i];
-    if (on) {
-      const int r = base + woff + below;
-      a.row_b[r] = b;
-      a.row_t[r] = t;
+  for (long long base = tid; base < nb; base += 256LL * 8) {
+    int v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const long long i = base + 256LL * u;
+      v[u] = a.mask[i < nb ? i : 0];
     }
-    base += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) before += (base + 256LL * u < nb && v[u] != 0) ? 1 : 0;
+  }
+  int seq_base = 0;
+  (void)block_exclusive_scan256(before, scr, &seq_base);
+  // This sequence: count per thread, scan, then write rows in order.
+  const int32_t* m = a.mask + nb;
+  const int per = (a.tokens + 255) / 256;
+  const int t0 = tid * per;
+  int mine = 0;
+  for (int k0 = 0; k0 < per; k0 += 8) {
+    int v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = t0 + k0 + u;
+      v[u] = (k0 + u < per && t < a.tokens) ? m[t] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mine += v[u] != 0 ? 1 : 0;
+  }
+  int seq_cnt = 0;
+  int r = seq_base + block_exclusive_scan256(mine, scr, &seq_cnt);
+  for (int k0 = 0; k0 < per; k0 += 8) {
+    int v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = t0 + k0 + u;
+      v[u] = (k0 + u < per && t < a.tokens) ? m[t] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (v[u] != 0) {
+        a.row_b[r] = b;
+        a.row_t[r] = t0 + k0 + u;
+        ++r;
+      }
+    }
   }
   if (tid == 0) {
-    a.seq_off[b] = base_sh;
-    a.seq_cnt[b] = base - base_sh;
-    if (b == a.batch - 1) *a.total = base;
+    a.seq_off[b] = seq_base;
+    a.seq_cnt[b] = seq_cnt;
+    if (b == a.batch - 1) *a.total = seq_base + seq_cnt;
   }
 }
 
@@ -476,27 +526,51 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd64(EncAttnArgs 
 // in f32 (lane owns columns lane + 64 j), the 16 partial sums are added in
 // wavefront order, times 1/count.
 extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
-  constexpr int kWaves = 16, kPer = 16;  // hidden <= 1024
+  // One workgroup per sequence; each lane sums 8 consecutive columns of a row
+  // per 16-byte load (hidden <= 1024: up to two 512-column segments), and
+  // each wave keeps 8 rows' loads in flight before accumulating them.
+  constexpr int kWaves = 16, kRows = 8;
   __shared__ float part[kWaves * 1024];
   __shared__ float red[kWaves];
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int off = a.seq_off[b], cnt = a.seq_cnt[b];
-  float s[kPer];
+  float s[2][8];
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) s[j] = 0.f;
-  for (int r = w; r < cnt; r += kWaves) {
-    const uint16_t* row = a.h + (size_t)(off + r) * a.hidden;
+  for (int g = 0; g < 2; ++g)
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int c = lane + 64 * j;
-      if (c < a.hidden) s[j] += h2f(row[c]);
+    for (int e = 0; e < 8; ++e) s[g][e] = 0.f;
+  for (int r0 = w * kRows; r0 < cnt; r0 += kWaves * kRows) {
+    v4i v[kRows][2];
+#pragma unroll
+    for (int u = 0; u < kRows; ++u) {
+      const int r = min(r0 + u, cnt - 1);
+      const uint16_t* row = a.h + (size_t)(off + r) * a.hidden;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int c = g * 512 + lane * 8;
+        v[u][g] = c < a.hidden ? *reinterpret_cast<const v4i*>(row + c) : v4i{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRows; ++u) {
+      if (r0 + u < cnt) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const v8h hv = __builtin_bit_cast(v8h, v[u][g]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s[g][e] += (float)hv[e];
+        }
+      }
     }
   }
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int c = lane + 64 * j;
-    if (c < a.hidden) part[w * 1024 + c] = s[j];
+  for (int g = 0; g < 2; ++g) {
+    const int c = g * 512 + lane * 8;
+    if (c < a.hidden) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part[w * 1024 + c + e] = s[g][e];
+    }
   }
   __syncthreads();
   float v = 0.f;

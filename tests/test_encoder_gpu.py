@@ -108,3 +108,20 @@ def test_baseline_c3_full_size(rt):
     np.testing.assert_allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
     pick = np.array([0, int(np.argmin(lens)), int(np.argmax(lens)), 37])
     _check(got[pick], _oracle(w, ids[pick], mask[pick]))
+
+
+def test_baseline_c4_long_context(rt):
+    """BASELINE config 4 at full size: 4 layers, hidden 512, 8 heads (hd 64),
+    FFN 2048, batch 4 x 8192, lengths U[4096, 8192] (seed 10). The shortest
+    sequence is checked against the oracle on its own valid tokens (sequences
+    are independent and padding never reaches a valid token)."""
+    _case("c4 full size 4 x 8192")
+    w = datagen.bert_q8_weights(4, 512, 8, 2048, 30522, 8192, seed=10)
+    ids, mask, lens = datagen.encoder_batch(4, 8192, 30522, 4096, 8192, 11, 10)
+    enc = Encoder(rt, w)
+    got = enc.embed(ids, mask)
+    np.testing.assert_allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
+    b = int(np.argmin(lens))
+    n = int(lens[b])
+    want = _oracle(w, ids[b:b + 1, :n], np.ones((1, n), np.int32))
+    _check(got[b:b + 1], want)
