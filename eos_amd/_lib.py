@@ -62,6 +62,29 @@ class EosHipEncoderLayer(C.Structure):
     ]
 
 
+class EosHipCompactDesc(C.Structure):
+    _fields_ = [
+        ("layers", C.c_int32),
+        ("model_dim", C.c_int32),
+        ("heads", C.c_int32),
+        ("hidden_dim", C.c_int32),
+        ("vocab", C.c_int32),
+        ("max_sequence", C.c_int32),
+        ("output_dim", C.c_int32),
+    ]
+
+
+class EosHipCompactLayer(C.Structure):
+    _fields_ = [
+        ("attn_q", _I8P), ("s_q", C.c_float),
+        ("attn_k", _I8P), ("s_k", C.c_float),
+        ("attn_v", _I8P), ("s_v", C.c_float),
+        ("attn_o", _I8P), ("s_o", C.c_float),
+        ("ffn_up", _I8P), ("s_up", C.c_float),
+        ("ffn_down", _I8P), ("s_down", C.c_float),
+    ]
+
+
 # name -> (argtypes) ; every function returns int except where noted
 _SIGNATURES = {
     "eoship_abi_version": ([], C.c_int),
@@ -123,6 +146,9 @@ _SIGNATURES = {
     "eoship_encoder_bind": ([C.c_void_p, C.POINTER(EosHipEncoderDesc), _F32P, _F32P, _F32P, _F32P,
                              _F32P, C.POINTER(EosHipEncoderLayer), C.POINTER(C.c_void_p),
                              C.c_void_p], C.c_int),
+    "eoship_encoder_bind_compact": ([C.c_void_p, C.POINTER(EosHipCompactDesc), _I8P, C.c_float,
+                                     _I8P, C.c_float, C.POINTER(EosHipCompactLayer), _I8P,
+                                     C.c_float, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
     "eoship_encoder_release": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_forward": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                 C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),

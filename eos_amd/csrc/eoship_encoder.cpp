@@ -7,6 +7,7 @@
 //               (O + residual + LN) -> eos_enc_gemm (FFN up + GELU) ->
 //               eos_enc_gemm_ln_h* (FFN down + residual + LN)
 //   eos_enc_pool        masked mean pool + L2 normalize
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <vector>
@@ -54,6 +55,12 @@ struct DevLayer {
 struct EosHipEncoder {
   EosHipRuntime* rt = nullptr;
   EosHipEncoderDesc desc{};
+  // 0: BERT family (affine LN embeddings, pool then normalize); 1: compact
+  // family (token + role with RoPE, normalize per row then pool, optional
+  // output projection `proj` [hidden][odim] f32).
+  int family = 0;
+  int odim = 0;
+  float* proj = nullptr;
   std::vector<void*> owned;
   float *tok = nullptr, *pos = nullptr, *typ = nullptr, *eg = nullptr, *eb = nullptr;
   std::vector<DevLayer> layers;
@@ -91,6 +98,28 @@ struct EosHipEncoder {
     for (size_t i = 0; i < count; ++i) h16[i] = int8_to_f16_bits(src[i]);
     return upload(dst, h16.data(), count, err);
   }
+
+  // Stacks [in][out] code matrices (reference layout) into one [sum out][in]
+  // f16 code matrix (the kernels' layout) and its per-output-channel scales.
+  int upload_codes_t(uint16_t** dst, float** scale, const int8_t* const* src, const float* s,
+                     const int* outs, int parts, int in, char** err) {
+    size_t total = 0;
+    for (int p = 0; p < parts; ++p) total += (size_t)outs[p];
+    std::vector<uint16_t> h16(total * (size_t)in);
+    std::vector<float> sc(total);
+    size_t o0 = 0;
+    for (int p = 0; p < parts; ++p) {
+      for (int o = 0; o < outs[p]; ++o) {
+        sc[o0 + o] = s[p];
+        for (int i = 0; i < in; ++i)
+          h16[(o0 + o) * (size_t)in + i] = int8_to_f16_bits(src[p][(size_t)i * outs[p] + o]);
+      }
+      o0 += (size_t)outs[p];
+    }
+    return upload(dst, h16.data(), h16.size(), err) || upload(scale, sc.data(), sc.size(), err);
+  }
+
+  int out_dim() const { return family == 1 ? odim : desc.hidden; }
 
   int ensure_activations(int batch, int tokens, char** err) {
     const size_t rows = (size_t)batch * tokens;
@@ -148,6 +177,7 @@ struct EosHipEncoder {
     em.npos = desc.max_positions;
     em.ntype = desc.type_vocab;
     em.eps = desc.ln_eps;
+    em.mode = family;
     if (rt->launch("eos_enc_embed", dim3((max_rows + 3) / 4), dim3(256), 0, &em, err) != 0) return 1;
     char ln_name[48];
     snprintf(ln_name, sizeof(ln_name), "eos_enc_gemm_ln_h%d", H);
@@ -172,10 +202,24 @@ struct EosHipEncoder {
       if (rt->launch(ln_name, dim3(lnblocks), dim3(256), 0, &dn, err, "enc_gemm_ffn_down_ln") != 0)
         return 1;
     }
-    EncPoolArgs pl{h, seq_off, seq_cnt, d_out, batch, H};
+    EncPoolArgs pl{h, seq_off, seq_cnt, d_out, proj, batch, H, family, out_dim()};
     return rt->launch("eos_enc_pool", dim3(batch), dim3(1024), 0, &pl, err);
   }
 };
+
+// Shapes the kernels are instantiated for: LN-GEMM row widths 128..768,
+// attention head dims 32/64/128, GEMM N tiles of 128.
+static int check_dims(int H, int heads, int F, const char* what, char** err) {
+  if (H != 128 && H != 256 && H != 384 && H != 512 && H != 768)
+    return set_err(err, "%s: hidden must be 128, 256, 384, 512 or 768 (got %d)", what, H);
+  if (heads <= 0 || H % heads != 0 ||
+      (H / heads != 32 && H / heads != 64 && H / heads != 128))
+    return set_err(err, "%s: head dim must be 32, 64 or 128 (hidden %d, heads %d)", what, H,
+                   heads);
+  if (F <= 0 || F % 128 != 0)
+    return set_err(err, "%s: intermediate width must be a positive multiple of 128", what);
+  return 0;
+}
 
 extern "C" {
 
@@ -189,13 +233,7 @@ int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const 
     return set_err(err, "eoship_encoder_bind: NULL argument");
   *out = nullptr;
   const int H = desc->hidden, F = desc->intermediate;
-  if (H != 384 && H != 512 && H != 768)
-    return set_err(err, "eoship_encoder_bind: hidden must be 384, 512 or 768 (got %d)", H);
-  if (desc->heads <= 0 || H % desc->heads != 0 || (H / desc->heads != 32 && H / desc->heads != 64))
-    return set_err(err, "eoship_encoder_bind: head dim must be 32 or 64 (hidden %d, heads %d)", H,
-                   desc->heads);
-  if (F <= 0 || F % 128 != 0)
-    return set_err(err, "eoship_encoder_bind: intermediate must be a positive multiple of 128");
+  if (check_dims(H, desc->heads, F, "eoship_encoder_bind", err) != 0) return 1;
   if (desc->layers < 0 || desc->vocab <= 0 || desc->max_positions <= 0 || desc->type_vocab <= 0)
     return set_err(err, "eoship_encoder_bind: layers/vocab/positions/type_vocab out of range");
   if (!(desc->ln_eps >= 0.f)) return set_err(err, "eoship_encoder_bind: ln_eps must be >= 0");
@@ -239,6 +277,107 @@ int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const 
         enc->upload(&d.be2, s.ln2_beta, (size_t)H, err))
       return fail();
     enc->layers.push_back(d);
+  }
+  *out = enc;
+  return 0;
+}
+
+int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc,
+                                const int8_t* token_embedding, float s_token,
+                                const int8_t* role_embedding, float s_role,
+                                const EosHipCompactLayer* layers, const int8_t* output_projection,
+                                float s_output, EosHipEncoder** out, char** err) {
+  const char* what = "eoship_encoder_bind_compact";
+  if (rt == nullptr || desc == nullptr || out == nullptr || token_embedding == nullptr ||
+      role_embedding == nullptr || (desc->layers > 0 && layers == nullptr))
+    return set_err(err, "%s: NULL argument", what);
+  *out = nullptr;
+  const int D = desc->model_dim, F = desc->hidden_dim, O = desc->output_dim;
+  if (check_dims(D, desc->heads, F, what, err) != 0) return 1;
+  if (desc->layers < 0 || desc->vocab <= 0 || desc->max_sequence <= 0)
+    return set_err(err, "%s: layers/vocab/max_sequence out of range", what);
+  if (O <= 0 || O > 8192) return set_err(err, "%s: output_dim must be in 1..8192 (got %d)", what, O);
+  if ((O != D) != (output_projection != nullptr))
+    return set_err(err, "%s: output_projection must be given exactly when output_dim != model_dim",
+                   what);
+  auto bad_scale = [](float sc) { return !(sc >= 0.f) || std::isinf(sc); };
+  if (bad_scale(s_token) || bad_scale(s_role) || (output_projection && bad_scale(s_output)))
+    return set_err(err, "%s: scales must be finite and >= 0", what);
+  for (int l = 0; l < desc->layers; ++l) {
+    const EosHipCompactLayer& s = layers[l];
+    if (!s.attn_q || !s.attn_k || !s.attn_v || !s.attn_o || !s.ffn_up || !s.ffn_down)
+      return set_err(err, "%s: layer %d has a NULL tensor", what, l);
+    if (bad_scale(s.s_q) || bad_scale(s.s_k) || bad_scale(s.s_v) || bad_scale(s.s_o) ||
+        bad_scale(s.s_up) || bad_scale(s.s_down))
+      return set_err(err, "%s: layer %d has a negative or non-finite scale", what, l);
+  }
+  auto* enc = new EosHipEncoder();
+  enc->rt = rt;
+  enc->family = 1;
+  enc->odim = O;
+  EosHipEncoderDesc& d = enc->desc;
+  d.layers = desc->layers;
+  d.hidden = D;
+  d.heads = desc->heads;
+  d.intermediate = F;
+  d.vocab = desc->vocab;
+  d.max_positions = desc->max_sequence;
+  d.type_vocab = 3;
+  d.ln_eps = 1e-5f;
+  d.gelu = 2;
+  auto fail = [&]() {
+    delete enc;
+    return 1;
+  };
+  // Dequantized tables (code * scale in f32, as the reference's q8/q4 decode).
+  auto dequant = [](const int8_t* c, float sc, size_t n) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; ++i) v[i] = (float)c[i] * sc;
+    return v;
+  };
+  const std::vector<float> tok = dequant(token_embedding, s_token, (size_t)desc->vocab * D);
+  const std::vector<float> role = dequant(role_embedding, s_role, (size_t)3 * D);
+  // RoPE table: per position, (cos, sin) of theta = pos / 10000^(c / D) for
+  // each even column c, computed in f64 and rounded to f32 (ropeRows,
+  // runtime/backend/tensor_ops.go:1936-1965).
+  std::vector<float> rope((size_t)desc->max_sequence * D);
+  for (int pos = 0; pos < desc->max_sequence; ++pos)
+    for (int c = 0; c + 1 < D; c += 2) {
+      const double theta = (double)pos / std::pow(10000.0, (double)c / (double)D);
+      rope[(size_t)pos * D + c] = (float)std::cos(theta);
+      rope[(size_t)pos * D + c + 1] = (float)std::sin(theta);
+    }
+  const std::vector<float> ones((size_t)D, 1.0f);
+  const std::vector<float> zeros((size_t)std::max(3 * D, F), 0.0f);
+  float *g1 = nullptr, *b0 = nullptr;
+  if (enc->upload(&enc->tok, tok.data(), tok.size(), err) ||
+      enc->upload(&enc->typ, role.data(), role.size(), err) ||
+      enc->upload(&enc->pos, rope.data(), rope.size(), err) ||
+      enc->upload(&g1, ones.data(), ones.size(), err) ||
+      enc->upload(&b0, zeros.data(), zeros.size(), err))
+    return fail();
+  enc->eg = g1;
+  enc->eb = b0;
+  if (output_projection != nullptr) {
+    const std::vector<float> pr = dequant(output_projection, s_output, (size_t)D * O);
+    if (enc->upload(&enc->proj, pr.data(), pr.size(), err)) return fail();
+  }
+  for (int l = 0; l < desc->layers; ++l) {
+    const EosHipCompactLayer& s = layers[l];
+    DevLayer dl;
+    const int8_t* qkv[] = {s.attn_q, s.attn_k, s.attn_v};
+    const float sqkv[] = {s.s_q, s.s_k, s.s_v};
+    const int oqkv[] = {D, D, D};
+    const int oD[] = {D}, oF[] = {F};
+    if (enc->upload_codes_t(&dl.w_qkv, &dl.s_qkv, qkv, sqkv, oqkv, 3, D, err) ||
+        enc->upload_codes_t(&dl.w_o, &dl.s_o, &s.attn_o, &s.s_o, oD, 1, D, err) ||
+        enc->upload_codes_t(&dl.w_1, &dl.s_1, &s.ffn_up, &s.s_up, oF, 1, D, err) ||
+        enc->upload_codes_t(&dl.w_2, &dl.s_2, &s.ffn_down, &s.s_down, oD, 1, F, err))
+      return fail();
+    dl.b_qkv = dl.b_o = dl.b_1 = dl.b_2 = b0;
+    dl.g1 = dl.g2 = g1;
+    dl.be1 = dl.be2 = b0;
+    enc->layers.push_back(dl);
   }
   *out = enc;
   return 0;
@@ -292,8 +431,7 @@ int eoship_encoder_forward(EosHipRuntime* rt, EosHipEncoder* enc, const int32_t*
   if (enc->rt != rt) return set_err(err, "eoship_encoder_forward: encoder bound on another runtime");
   if (check_shape(enc, batch, tokens, "eoship_encoder_forward", err) != 0) return 1;
   const size_t n = (size_t)batch * tokens;
-  const size_t H = enc->desc.hidden;
-  const size_t need = n * 4 * 3 + (size_t)batch * H * 4 + 64;
+  const size_t need = n * 4 * 3 + (size_t)batch * enc->out_dim() * 4 + 64;
   if (enc->io_bytes < need) {
     if (enc->io) hipFree(enc->io);
     enc->io = nullptr;
@@ -312,7 +450,8 @@ int eoship_encoder_forward(EosHipRuntime* rt, EosHipEncoder* enc, const int32_t*
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(encoder inputs)", e);
   if (enc->forward(d_ids, type_ids ? d_types : nullptr, d_mask, batch, tokens, d_out, err) != 0)
     return 1;
-  e = hipMemcpyAsync(out, d_out, (size_t)batch * H * 4, hipMemcpyDeviceToHost, rt->stream);
+  e = hipMemcpyAsync(out, d_out, (size_t)batch * enc->out_dim() * 4, hipMemcpyDeviceToHost,
+                     rt->stream);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(embeddings)", e);
   int32_t st = 0;
   if (eoship_encoder_status(rt, enc, &st, err) != 0) return 1;

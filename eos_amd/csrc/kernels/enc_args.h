@@ -18,22 +18,25 @@ struct EncPackArgs {
   int batch, tokens;
 };
 
-// Embeddings (token + position + type) followed by affine LayerNorm.
+// mode 0 (BERT): token + position + type, then affine LayerNorm.
+// mode 1 (compact): token + role, then RoPE with the rotation table `pos`
+//   ([npos][hidden] f32: cos, sin of each column pair); gamma/beta unused.
 struct EncEmbedArgs {
   const int32_t* ids;       // [batch][tokens]
-  const int32_t* type_ids;  // [batch][tokens] or NULL (all 0)
+  const int32_t* type_ids;  // [batch][tokens] or NULL (all 0): type or role ids
   const int32_t* row_b;
   const int32_t* row_t;
   const int32_t* total;
   const float* tok;         // [vocab][hidden]
-  const float* pos;         // [npos][hidden]
-  const float* typ;         // [ntype][hidden]
+  const float* pos;         // mode 0: [npos][hidden]; mode 1: rotation table
+  const float* typ;         // [ntype][hidden] type or role table
   const float* gamma;
   const float* beta;
   uint16_t* out;            // [rows][hidden] f16
   int32_t* status;          // set to 1 on an out-of-range id
   int tokens, hidden, vocab, npos, ntype;
   float eps;
+  int mode;
 };
 
 // out[m][n] = epi(scale[n] * sum_k a[m][k] w[n][k] + bias[n]) for m < *rows.
@@ -75,13 +78,16 @@ struct EncAttnArgs {
   float scale_log2;        // log2(e) / sqrt(head_dim)
 };
 
-// Masked mean pool + L2 normalize per sequence.
+// mode 0: masked mean pool, then L2 normalize -> out [batch][hidden].
+// mode 1: L2 normalize every row, masked mean pool, then (proj != NULL)
+//   times proj [hidden][odim] -> out [batch][odim] (odim = hidden without).
 struct EncPoolArgs {
   const uint16_t* h;       // [rows][hidden] f16
   const int32_t* seq_off;
   const int32_t* seq_cnt;
-  float* out;              // [batch][hidden]
-  int batch, hidden;
+  float* out;
+  const float* proj;       // mode 1 only, [hidden][odim] f32, or NULL
+  int batch, hidden, mode, odim;
 };
 
 // Tiny embed pipeline (examples/embed.eos): gather f16 table rows, multiply by

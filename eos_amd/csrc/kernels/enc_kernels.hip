@@ -6,6 +6,10 @@
 // residual + LN -> FFN (erf GELU) -> residual + LN
 // (bert_encoder_layer_ops.go:80-225), masked mean pool then L2 normalize.
 //
+// The compact transformer family (models/default_embedding.go:419-505) runs
+// on the same kernels: embed mode 1 (token + role, RoPE), non-affine LN
+// (gamma 1, beta 0, eps 1e-5), tanh GELU, bias-free GEMMs, pool mode 1.
+//
 // Layout: only active (mask != 0) positions are computed, packed into rows
 // [0, total); a sequence's rows are contiguous. Activations are f16, every
 // GEMM accumulates in f32 on v_mfma_f32_32x32x16_f16, weights are int8 codes
@@ -152,6 +156,35 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
     ty = ty < 0 || ty >= a.ntype ? 0 : ty;
   }
   const int p = pos < a.npos ? pos : a.npos - 1;
+  if (a.mode == 1) {
+    // Compact family: lane owns column pairs (2i, 2i + 1), i = lane + 64 j;
+    // x = tok + role in f32, then the pair is rotated by the position's
+    // (cos, sin) as ropeRows does: (x0 c - x1 s, x0 s + x1 c).
+    const float2* te = reinterpret_cast<const float2*>(a.tok + (size_t)id * a.hidden);
+    const float2* re = reinterpret_cast<const float2*>(a.typ + (size_t)ty * a.hidden);
+    const float2* rt = reinterpret_cast<const float2*>(a.pos + (size_t)p * a.hidden);
+    const int pairs = a.hidden >> 1;
+    float2 tv[8], rv[8], cs[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = min(lane + 64 * j, pairs - 1);
+      tv[j] = te[i];
+      rv[j] = re[i];
+      cs[j] = rt[i];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = lane + 64 * j;
+      if (i < pairs) {
+        const float x0 = tv[j].x + rv[j].x, x1 = tv[j].y + rv[j].y;
+        const float y0 = __fsub_rn(__fmul_rn(x0, cs[j].x), __fmul_rn(x1, cs[j].y));
+        const float y1 = __fadd_rn(__fmul_rn(x0, cs[j].y), __fmul_rn(x1, cs[j].x));
+        const uint32_t packed = (uint32_t)f2h(y0) | ((uint32_t)f2h(y1) << 16);
+        *reinterpret_cast<uint32_t*>(a.out + (size_t)row * a.hidden + 2 * i) = packed;
+      }
+    }
+    return;
+  }
   constexpr int kMaxPer = 16;  // hidden <= 1024
   float v[kMaxPer];
   float s = 0.f;
@@ -387,6 +420,12 @@ EOS_DEV void gemm_ln_body(const EncGemmLnArgs& a) {
   }
 }
 
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h128(EncGemmLnArgs a) {
+  gemm_ln_body<1>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h256(EncGemmLnArgs a) {
+  gemm_ln_body<2>(a);
+}
 extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h384(EncGemmLnArgs a) {
   gemm_ln_body<3>(a);
 }
@@ -518,10 +557,16 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd32(EncAttnArgs 
 extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd64(EncAttnArgs a) {
   attn_body<64>(a);
 }
+extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd128(EncAttnArgs a) {
+  attn_body<128>(a);
+}
 
 // ------------------------------------------------------------------- pool
 
-// Masked mean pool then L2 normalize (rows of norm 0 unchanged). One
+// mode 0 (BERT, bert_embedder_ops.go:179-192): masked mean pool then L2
+// normalize (rows of norm 0 unchanged). mode 1 (compact family,
+// models/default_embedding.go:496-505): L2 normalize every row, masked mean
+// pool, then the optional output projection. One
 // workgroup of 16 wavefronts per sequence: wavefront w sums rows w, w+16, ...
 // in f32 (lane owns columns lane + 64 j), the 16 partial sums are added in
 // wavefront order, times 1/count.
@@ -552,6 +597,31 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
         v[u][g] = c < a.hidden ? *reinterpret_cast<const v4i*>(row + c) : v4i{0, 0, 0, 0};
       }
     }
+    if (a.mode == 1) {
+      // Each row is L2-normalized first (x / ||x||, rows of norm 0 kept).
+#pragma unroll
+      for (int u = 0; u < kRows; ++u) {
+        float x[2][8];
+        float q = 0.f;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const v8h hv = __builtin_bit_cast(v8h, v[u][g]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            x[g][e] = (float)hv[e];
+            q += x[g][e] * x[g][e];
+          }
+        }
+        const float norm = sqrtf(wave_sum(q));
+        if (r0 + u < cnt) {
+#pragma unroll
+          for (int g = 0; g < 2; ++g)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[g][e] += norm > 0.f ? x[g][e] / norm : x[g][e];
+        }
+      }
+      continue;
+    }
 #pragma unroll
     for (int u = 0; u < kRows; ++u) {
       if (r0 + u < cnt) {
@@ -578,6 +648,23 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
   if (c < a.hidden) {
     for (int i = 0; i < kWaves; ++i) v += part[i * 1024 + c];
     v = cnt > 0 ? v * (1.0f / (float)cnt) : 0.f;
+  }
+  if (a.mode == 1) {
+    if (a.proj == nullptr) {
+      if (c < a.hidden) a.out[(size_t)b * a.hidden + c] = v;
+      return;
+    }
+    // Output projection of the pooled row: pool(X) P equals pool(X P) up to
+    // f32 rounding, at 1/count of the work.
+    __syncthreads();
+    if (c < a.hidden) part[c] = v;
+    __syncthreads();
+    for (int o = tid; o < a.odim; o += 1024) {
+      float acc = 0.f;
+      for (int d = 0; d < a.hidden; ++d) acc += part[d] * a.proj[(size_t)d * a.odim + o];
+      a.out[(size_t)b * a.odim + o] = acc;
+    }
+    return;
   }
   const float ss = wave_sum(c < a.hidden ? v * v : 0.f);
   if (lane == 0) red[w] = ss;

@@ -199,6 +199,41 @@ def bert_q8_weights(layers: int, hidden: int, heads: int, inter: int, vocab: int
     return w
 
 
+def compact_q8_weights(layers: int, dim: int, heads: int, ffn: int, vocab: int, max_seq: int,
+                       out_dim: int | None = None, seed: int = 7, bits: int = 8):
+    """Random-init compact (family (a)) embedder, quantized per tensor on the
+    reference's q8/q4 grid. Embedding tables are N(0, 0.02); dense weights are
+    N(0, 1/fan_in) so attention logits are O(1) once LayerNorm has run."""
+    from .encoder import CompactLayerWeights, CompactWeights, quantize_per_tensor
+
+    counter = [seed * 1000033]
+
+    def draw(shape, std):
+        counter[0] += 1
+        n = int(np.prod(shape))
+        w = (std * normal(counter[0], n)).astype(np.float32).reshape(shape)
+        return quantize_per_tensor(w, bits)
+
+    D, F = dim, ffn
+    tok, st = draw((vocab, D), 0.02)
+    role, sr = draw((3, D), 0.02)
+    w = CompactWeights(model_dim=D, heads=heads, hidden_dim=F, max_sequence=max_seq,
+                       token_embedding=tok, s_token=st, role_embedding=role, s_role=sr)
+    for _ in range(layers):
+        q, sq = draw((D, D), D ** -0.5)
+        k, sk = draw((D, D), D ** -0.5)
+        v, sv = draw((D, D), D ** -0.5)
+        o, so = draw((D, D), D ** -0.5)
+        up, su = draw((D, F), D ** -0.5)
+        dn, sd = draw((F, D), F ** -0.5)
+        w.layers.append(CompactLayerWeights(attn_q=q, s_q=sq, attn_k=k, s_k=sk, attn_v=v, s_v=sv,
+                                            attn_o=o, s_o=so, ffn_up=up, s_up=su, ffn_down=dn,
+                                            s_down=sd))
+    if out_dim is not None and out_dim != D:
+        w.output_projection, w.s_output = draw((D, out_dim), D ** -0.5)
+    return w
+
+
 def encoder_batch(batch: int, tokens: int, vocab: int, lo: int, hi: int, seed_ids: int,
                   seed_len: int):
     """Token ids uniform over [0, vocab), valid lengths uniform in [lo, hi];

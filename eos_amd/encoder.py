@@ -1,10 +1,15 @@
-"""q8 BERT-style encoder on the MI355X backend.
+"""q8 encoders on the MI355X backend.
 
-Host-side mirror of the reference's bert_embedder step
-(runtime/backend/bert_embedder_ops.go:101-197, BERTEmbedderReferenceWithPooling):
-``Encoder.embed(input_ids, attention_mask, token_type_ids)`` returns the masked
-mean-pooled, L2-normalized sentence embeddings [batch, hidden]. Errors follow
-the reference: ids outside their tables are rejected
+Host-side mirrors of the reference's two embedder families:
+- ``Encoder``: the bert_embedder step (runtime/backend/bert_embedder_ops.go:
+  101-197, BERTEmbedderReferenceWithPooling). ``embed(input_ids,
+  attention_mask, token_type_ids)`` returns the masked mean-pooled,
+  L2-normalized sentence embeddings [batch, hidden].
+- ``CompactEncoder``: the compact transformer graph of the default embedder
+  (models/default_embedding.go:419-505). ``embed(tokens, attention_mask,
+  role_ids)`` returns the masked mean of the per-token normalized (and
+  optionally projected) states [batch, output_dim].
+Errors follow the reference: ids outside their tables are rejected
 (runtime/backend/tensor_ops.go:1484-1492). All arithmetic runs in libeoship's
 gfx950 kernels.
 """
@@ -80,6 +85,71 @@ def quantize_per_channel(w: np.ndarray):
     return codes, scale
 
 
+def quantize_per_tensor(w: np.ndarray, bits: int = 8):
+    """The reference's per-tensor grid (packQuantizedTensorStorage,
+    runtime/mll_export.go:897-942): levels = 2^(bits-1) - 1, scale =
+    float32(max|w|) / levels, code = clamp(round-half-away(float32(w / scale)),
+    +-levels). q4 codes are passed unpacked (the payload nibble is code + 8,
+    runtime/weight_file.go:334-350). Returns int8 codes and the f32 scale (0
+    for an all-zero tensor)."""
+    w = np.asarray(w, dtype=np.float32)
+    levels = np.float32((1 << (bits - 1)) - 1)
+    mx = np.float32(np.max(np.abs(w))) if w.size else np.float32(0.0)
+    if mx == 0:
+        return np.zeros(w.shape, np.int8), np.float32(0.0)
+    scale = np.float32(mx / levels)
+    q = (w / scale).astype(np.float32)
+    q = np.sign(q) * np.floor(np.abs(q).astype(np.float64) + 0.5)  # exact in f64
+    codes = np.clip(q, -levels, levels).astype(np.int8)
+    return codes, scale
+
+
+@dataclass
+class CompactLayerWeights:
+    """One compact layer: int8 codes in the reference's [in, out] layout, one
+    scale per tensor (models/default_embedding.go:425-431)."""
+    attn_q: np.ndarray   # int8 [D, D]
+    s_q: float
+    attn_k: np.ndarray
+    s_k: float
+    attn_v: np.ndarray
+    s_v: float
+    attn_o: np.ndarray
+    s_o: float
+    ffn_up: np.ndarray   # int8 [D, H]
+    s_up: float
+    ffn_down: np.ndarray  # int8 [H, D]
+    s_down: float
+
+    def dequantized(self):
+        """(wq, wk, wv, wo, wup, wdown) f32 = code * scale, [in, out]."""
+        f = lambda c, s: c.astype(np.float32) * np.float32(s)
+        return (f(self.attn_q, self.s_q), f(self.attn_k, self.s_k), f(self.attn_v, self.s_v),
+                f(self.attn_o, self.s_o), f(self.ffn_up, self.s_up),
+                f(self.ffn_down, self.s_down))
+
+
+@dataclass
+class CompactWeights:
+    """DefaultEmbeddingPackageConfig-shaped weights (models/default_embedding.go:264-300)."""
+    model_dim: int
+    heads: int
+    hidden_dim: int
+    max_sequence: int
+    token_embedding: np.ndarray  # int8 [V, D]
+    s_token: float
+    role_embedding: np.ndarray   # int8 [3, D]
+    s_role: float
+    layers: list = field(default_factory=list)
+    output_projection: np.ndarray | None = None  # int8 [D, O]
+    s_output: float = 0.0
+
+    @property
+    def output_dim(self) -> int:
+        p = self.output_projection
+        return self.model_dim if p is None else int(p.shape[1])
+
+
 def _p(a, t):
     return a.ctypes.data_as(C.POINTER(t))
 
@@ -134,6 +204,7 @@ class Encoder:
         typ = f32(w.typ, (w.typ.shape[0], H))
         eg = f32(w.emb_gamma, (H,))
         eb = f32(w.emb_beta, (H,))
+        self.out_dim = H
         self.handle = C.c_void_p()
         _lib.call("eoship_encoder_bind", rt.handle, C.byref(desc), _p(tok, C.c_float),
                   _p(pos, C.c_float), _p(typ, C.c_float), _p(eg, C.c_float), _p(eb, C.c_float),
@@ -162,7 +233,7 @@ class Encoder:
             types = np.ascontiguousarray(token_type_ids, dtype=np.int32)
             if types.shape != ids.shape:
                 raise ValueError("token_type_ids must match input_ids")
-        out = np.zeros((ids.shape[0], self.w.hidden), np.float32)
+        out = np.zeros((ids.shape[0], self.out_dim), np.float32)
         _lib.call("eoship_encoder_forward", self.rt.handle, self.handle,
                   ids.ctypes.data_as(C.c_void_p),
                   types.ctypes.data_as(C.c_void_p) if types is not None else None,
@@ -181,6 +252,52 @@ class Encoder:
         st = C.c_int32()
         _lib.call("eoship_encoder_status", self.rt.handle, self.handle, C.byref(st))
         return st.value
+
+
+class CompactEncoder(Encoder):
+    """A compact (family (a)) embedder bound on the device; ``embed`` takes
+    (tokens, attention_mask, role_ids) and returns [batch, output_dim]."""
+
+    def __init__(self, rt: Runtime, w: CompactWeights):
+        self.rt, self.w = rt, w
+        D, F = w.model_dim, w.hidden_dim
+        keep = []
+
+        def i8(x, shape):
+            a = np.ascontiguousarray(x, dtype=np.int8)
+            if a.shape != shape:
+                raise ValueError(f"expected {shape}, got {a.shape}")
+            keep.append(a)
+            return _p(a, C.c_int8)
+
+        layers = (_lib.EosHipCompactLayer * max(len(w.layers), 1))()
+        for i, L in enumerate(w.layers):
+            x = layers[i]
+            x.attn_q, x.s_q = i8(L.attn_q, (D, D)), L.s_q
+            x.attn_k, x.s_k = i8(L.attn_k, (D, D)), L.s_k
+            x.attn_v, x.s_v = i8(L.attn_v, (D, D)), L.s_v
+            x.attn_o, x.s_o = i8(L.attn_o, (D, D)), L.s_o
+            x.ffn_up, x.s_up = i8(L.ffn_up, (D, F)), L.s_up
+            x.ffn_down, x.s_down = i8(L.ffn_down, (F, D)), L.s_down
+        vocab = int(np.asarray(w.token_embedding).shape[0])
+        tok = i8(w.token_embedding, (vocab, D))
+        role = i8(w.role_embedding, (3, D))
+        proj = None
+        if w.output_projection is not None:
+            proj = i8(w.output_projection, (D, w.output_dim))
+        desc = _lib.EosHipCompactDesc(layers=len(w.layers), model_dim=D, heads=w.heads,
+                                      hidden_dim=F, vocab=vocab, max_sequence=w.max_sequence,
+                                      output_dim=w.output_dim)
+        self.out_dim = w.output_dim
+        self.handle = C.c_void_p()
+        _lib.call("eoship_encoder_bind_compact", rt.handle, C.byref(desc), tok,
+                  C.c_float(w.s_token), role, C.c_float(w.s_role), layers, proj,
+                  C.c_float(w.s_output), C.byref(self.handle))
+        del keep
+
+    def embed(self, tokens: np.ndarray, attention_mask: np.ndarray,
+              role_ids: np.ndarray | None = None) -> np.ndarray:
+        return super().embed(tokens, attention_mask, role_ids)
 
 
 class TinyEmbed:

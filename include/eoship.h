@@ -199,8 +199,8 @@ typedef struct EosHipEncoder EosHipEncoder;
  * (runtime/backend/bert_embedder_ops.go:101-197). */
 typedef struct {
   int32_t layers;        /* num_hidden_layers */
-  int32_t hidden;        /* 384, 512 or 768 */
-  int32_t heads;         /* hidden / heads in {32, 64} */
+  int32_t hidden;        /* 128, 256, 384, 512 or 768 */
+  int32_t heads;         /* hidden / heads in {32, 64, 128} */
   int32_t intermediate;  /* FFN width, multiple of 128 */
   int32_t vocab;         /* token table rows */
   int32_t max_positions; /* position table rows (>= tokens) */
@@ -232,7 +232,8 @@ int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const 
                         EosHipEncoder** out, char** err);
 int eoship_encoder_release(EosHipEncoder* enc, char** err);
 /* Embeds a [batch][tokens] batch (host buffers): embeddings, all layers,
- * masked mean pool, L2 normalize -> out [batch][hidden] f32. type_ids may be
+ * masked mean pool, L2 normalize -> out [batch][hidden] f32 (an encoder bound
+ * with eoship_encoder_bind_compact: out [batch][output_dim]). type_ids may be
  * NULL (all 0). Fails with an error for a token, type or position id outside
  * its table (the reference rejects these, runtime/backend/tensor_ops.go:1484-1492).
  * Replaces Program.Run of a bert_embedder plan / EmbeddingModel.EmbedBatch
@@ -247,6 +248,48 @@ int eoship_encoder_forward_device(EosHipRuntime* rt, EosHipEncoder* enc, const i
                                   int32_t tokens, float* d_out, char** err);
 /* 0 when every id of the last forward was in range; synchronises. */
 int eoship_encoder_status(EosHipRuntime* rt, EosHipEncoder* enc, int32_t* status, char** err);
+
+/* Compact transformer embedder (family (a): the graph that
+ * compactTransformerSource emits, models/default_embedding.go:419-505, with
+ * the DefaultEmbeddingPackageConfig fields of :264-300). */
+typedef struct {
+  int32_t layers;        /* EncoderRepeats (each layer has its own weights) */
+  int32_t model_dim;     /* D: 128, 256, 384, 512 or 768 */
+  int32_t heads;         /* AttentionHeads; D / heads in {32, 64, 128} */
+  int32_t hidden_dim;    /* FFN width H, positive multiple of 128 */
+  int32_t vocab;         /* token_embedding rows */
+  int32_t max_sequence;  /* longest accepted tokens (RoPE table rows) */
+  int32_t output_dim;    /* O; equal to model_dim when there is no output_projection */
+} EosHipCompactDesc;
+
+/* One layer's q8 (or unpacked q4) codes in the reference's [in][out] layout,
+ * each tensor with its per-tensor scale (dequantized = code * scale,
+ * runtime/weight_file.go:315-350; a scale of 0 means an all-zero tensor). */
+typedef struct {
+  const int8_t* attn_q; float s_q;       /* [D][D] */
+  const int8_t* attn_k; float s_k;       /* [D][D] */
+  const int8_t* attn_v; float s_v;       /* [D][D] */
+  const int8_t* attn_o; float s_o;       /* [D][D] */
+  const int8_t* ffn_up; float s_up;      /* [D][H] */
+  const int8_t* ffn_down; float s_down;  /* [H][D] */
+} EosHipCompactLayer;
+
+/* Uploads a compact embedder: token_embedding [V][D] and role_embedding
+ * [3][D] codes, per-layer weights, and output_projection [D][O] (NULL when
+ * output_dim == model_dim). The forward calls above then run its graph:
+ * rope(dequant(tok) + dequant(role)), per layer q/k/v = x W, masked
+ * attention (one head: scaled_attention_scores + masked_softmax; several:
+ * compact_multihead_attention_hN), layernorm(x W_o + x), tanh-GELU FFN,
+ * layernorm(ffn + h), then normalize per token, the optional projection and
+ * the masked mean (out [batch][output_dim]); their type_ids argument carries
+ * the role_ids (0..2). Replaces loading and running that graph through
+ * ExecuteSymbolic (runtime/backend/symbolic.go:17-172) or the CUDA compact
+ * forward (runtime/backends/cuda/compact_forward_accel_linux.go:106-305). */
+int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc,
+                                const int8_t* token_embedding, float s_token,
+                                const int8_t* role_embedding, float s_role,
+                                const EosHipCompactLayer* layers, const int8_t* output_projection,
+                                float s_output, EosHipEncoder** out, char** err);
 
 #ifdef __cplusplus
 }

@@ -175,6 +175,19 @@ def _enc():
     lib.normalize_rows.restype = None
     lib.tiny_embed.argtypes = [P, C.c_int, C.c_int, P, C.c_int, P, C.c_int, P]
     lib.tiny_embed.restype = None
+    lib.rope_rows.argtypes = [P, C.c_int, C.c_int, C.c_int]
+    lib.rope_rows.restype = None
+    lib.matmul_f32.argtypes = [P, C.c_int, C.c_int, P, C.c_int, P]
+    lib.matmul_f32.restype = None
+    lib.layer_norm_rows.argtypes = [P, C.c_int, C.c_int]
+    lib.layer_norm_rows.restype = None
+    lib.compact_single_head_attention.argtypes = [P, P, P, P, C.c_int, C.c_int, C.c_int, P]
+    lib.compact_single_head_attention.restype = None
+    lib.compact_embed.argtypes = [P, C.c_int, P, C.c_int, P, C.c_int, P, C.c_int, P, P, P,
+                                  C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P]
+    lib.compact_embed.restype = None
+    lib.gelu_tanh_inplace.argtypes = [P, C.c_long]
+    lib.gelu_tanh_inplace.restype = None
     lib._enc_ready = True
     return lib
 
@@ -241,4 +254,72 @@ def tiny_embed(table, proj, ids):
     out = np.zeros((ids.shape[0], proj.shape[1]), np.float32)
     lib.tiny_embed(_p(table), table.shape[0], table.shape[1], _p(proj), proj.shape[1], _p(ids),
                    ids.shape[0], _p(out))
+    return out
+
+
+# ------------------------------------------------- compact (family (a)) embedder
+
+def rope_rows(x, seq):
+    """ropeRows on [rows][cols] with pos = row % seq."""
+    lib = _enc()
+    x = _f32(x).copy()
+    lib.rope_rows(_p(x), x.shape[0], seq, x.shape[1])
+    return x
+
+
+def matmul_f32(x, w):
+    """matmulTensor: x [rows][in] @ w [in][out], f32 in k order."""
+    lib = _enc()
+    x, w = _f32(x), _f32(w)
+    y = np.zeros((x.shape[0], w.shape[1]), np.float32)
+    lib.matmul_f32(_p(x), x.shape[0], x.shape[1], _p(w), w.shape[1], _p(y))
+    return y
+
+
+def layer_norm_rows(x):
+    lib = _enc()
+    x = _f32(x).copy()
+    lib.layer_norm_rows(_p(x), x.shape[0], x.shape[1])
+    return x
+
+
+def gelu_tanh(x):
+    """geluTensor (tanh form) elementwise."""
+    lib = _enc()
+    x = _f32(x).copy()
+    lib.gelu_tanh_inplace(_p(x), x.size)
+    return x
+
+
+def compact_single_head_attention(q, k, v, mask):
+    """q, k, v: [batch*tokens][dim]; mask [batch][tokens]."""
+    lib = _enc()
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    mask = np.ascontiguousarray(mask, dtype=np.int32)
+    batch, tokens = mask.shape
+    out = np.zeros_like(q)
+    lib.compact_single_head_attention(_p(q), _p(k), _p(v), _p(mask), batch, tokens, q.shape[1],
+                                      _p(out))
+    return out
+
+
+def compact_embed(tok, role, layers, ids, mask, role_ids, heads, wout=None):
+    """Family (a) embedder. tok [V][D], role [R][D] dequantized f32; layers: list
+    of (wq, wk, wv, wo, wup, wdown) in [in, out] layout; wout [D][O] or None."""
+    lib = _enc()
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    mask = np.ascontiguousarray(mask, dtype=np.int32)
+    roles = np.zeros_like(ids) if role_ids is None else np.ascontiguousarray(role_ids, np.int32)
+    batch, tokens = ids.shape
+    dim = tok.shape[1]
+    ffn = layers[0][4].shape[1] if layers else dim
+    keep = [_f32(x) for L in layers for x in L]
+    ptrs = (C.c_void_p * max(len(keep), 1))(*[k.ctypes.data for k in keep])
+    tok, role = _f32(tok), _f32(role)
+    wo = None if wout is None else _f32(wout)
+    odim = dim if wo is None else wo.shape[1]
+    out = np.zeros((batch, odim), np.float32)
+    lib.compact_embed(_p(tok), tok.shape[0], _p(role), role.shape[0], ptrs, len(layers),
+                      None if wo is None else _p(wo), odim, _p(ids), _p(roles), _p(mask), batch,
+                      tokens, dim, heads, ffn, _p(out))
     return out

@@ -228,3 +228,192 @@ void tiny_embed(const float* table, int vocab, int dim, const float* proj, int e
   }
   normalize_rows(out, n, edim);
 }
+
+/* ------------------------------------------------------------------------
+ * Compact transformer embedder (family (a): the shipped default embedder's
+ * graph, models/default_embedding.go:419-505), restated step by step in the
+ * reference's precisions:
+ *  - gather + dequant of q8/q4 token and role rows, summed in f32;
+ *  - ropeRows (tensor_ops.go:1936-1965): pairs (c, c+1), theta =
+ *    pos / 10000^(c/cols) in f64, cos/sin rounded to f32, f32 rotation,
+ *    pos = the row's position inside its padded sequence;
+ *  - matmulTensor (tensor_ops.go:1168-1249): [in, out] weights, f32 sum in
+ *    k order;
+ *  - one head: scaled_attention_scores = (q kT) * float32(1/sqrt(D))
+ *    (matmulScale "rsqrt_rhs_rows", tensor_ops.go:1291-1315), then
+ *    maskedSoftmaxRowsF32 (tensor_ops.go:1825-1865: f32 max over active
+ *    keys, f64 exp and sum, f32 probabilities times float32(1/sum)), then
+ *    probs @ v in f32; several heads: compactMultiheadAttentionTensor
+ *    (tensor_ops.go:1867-1924) = the BERT f64 attention above;
+ *  - layerNormRows (tensor_ops.go:1393-1421): non-affine, f32 mean/variance,
+ *    invStd = float32(1/sqrt(f64(var) + 1e-5));
+ *  - geluTensor (tensor_ops.go:1926-1934): tanh form, f64 tanh;
+ *  - normalizeRows per token, the optional output projection per token,
+ *    then meanPoolMaskedTensor.
+ * ------------------------------------------------------------------------ */
+
+void rope_rows(float* x, int rows, int seq, int cols) {
+  for (int r = 0; r < rows; ++r) {
+    const int pos = r % seq;
+    for (int c = 0; c + 1 < cols; c += 2) {
+      const double theta = (double)pos / pow(10000.0, (double)c / (double)cols);
+      const float ct = (float)cos(theta), st = (float)sin(theta);
+      const float x0 = x[(size_t)r * cols + c], x1 = x[(size_t)r * cols + c + 1];
+      x[(size_t)r * cols + c] = x0 * ct - x1 * st;
+      x[(size_t)r * cols + c + 1] = x0 * st + x1 * ct;
+    }
+  }
+}
+
+/* y[r][j] = sum_k x[r][k] w[k][j] (f32, k ascending); W is [in][out]. */
+void matmul_f32(const float* x, int rows, int in, const float* w, int out, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int r = 0; r < rows; ++r) {
+    const float* xr = x + (size_t)r * in;
+    for (int j = 0; j < out; ++j) {
+      float sum = 0.0f;
+      for (int k = 0; k < in; ++k) sum += xr[k] * w[(size_t)k * out + j];
+      y[(size_t)r * out + j] = sum;
+    }
+  }
+}
+
+void layer_norm_rows(float* x, int rows, int cols) {
+  for (int r = 0; r < rows; ++r) {
+    float* row = x + (size_t)r * cols;
+    float mean = 0.0f;
+    for (int c = 0; c < cols; ++c) mean += row[c];
+    mean /= (float)cols;
+    float var = 0.0f;
+    for (int c = 0; c < cols; ++c) {
+      const float d = row[c] - mean;
+      var += d * d;
+    }
+    var /= (float)cols;
+    const float inv = (float)(1.0 / sqrt((double)var + 1e-5));
+    for (int c = 0; c < cols; ++c) row[c] = (row[c] - mean) * inv;
+  }
+}
+
+static inline float tanh_gelu(float x) {
+  const float cubic = x * x * x;
+  const float inner = 0.7978845608f * (x + 0.044715f * cubic);
+  return 0.5f * x * (1.0f + (float)tanh((double)inner));
+}
+
+void gelu_tanh_inplace(float* x, long n) {
+  for (long i = 0; i < n; ++i) x[i] = tanh_gelu(x[i]);
+}
+
+/* Single-head attention of the compact graph on [batch][tokens][dim]. */
+void compact_single_head_attention(const float* q, const float* k, const float* v,
+                                   const int32_t* mask, int batch, int tokens, int dim,
+                                   float* mixed) {
+  const float scale = (float)(1.0 / sqrt((double)dim));
+#pragma omp parallel for schedule(dynamic, 8)
+  for (long job = 0; job < (long)batch * tokens; ++job) {
+    const int b = (int)(job / tokens);
+    const float* qr = q + (size_t)job * dim;
+    const int32_t* mb = mask + (size_t)b * tokens;
+    float* p = (float*)malloc(sizeof(float) * (size_t)tokens);
+    for (int kt = 0; kt < tokens; ++kt) {
+      const float* kr = k + ((size_t)b * tokens + kt) * dim;
+      float sum = 0.0f;
+      for (int d = 0; d < dim; ++d) sum += qr[d] * kr[d];
+      p[kt] = sum * scale;
+    }
+    float mx = -INFINITY;
+    int any = 0;
+    for (int kt = 0; kt < tokens; ++kt) {
+      if (mb[kt] == 0) continue;
+      if (!any || p[kt] > mx) mx = p[kt];
+      any = 1;
+    }
+    if (!any) {
+      for (int kt = 0; kt < tokens; ++kt) p[kt] = 0.0f;
+    } else {
+      double s = 0.0;
+      for (int kt = 0; kt < tokens; ++kt) {
+        if (mb[kt] == 0) {
+          p[kt] = 0.0f;
+          continue;
+        }
+        const double ev = exp((double)(p[kt] - mx));
+        p[kt] = (float)ev;
+        s += ev;
+      }
+      if (s != 0.0) {
+        const float inv = (float)(1.0 / s);
+        for (int kt = 0; kt < tokens; ++kt)
+          if (mb[kt] != 0) p[kt] *= inv;
+      }
+    }
+    float* out = mixed + (size_t)job * dim;
+    for (int d = 0; d < dim; ++d) {
+      float sum = 0.0f;
+      for (int kt = 0; kt < tokens; ++kt) sum += p[kt] * v[((size_t)b * tokens + kt) * dim + d];
+      out[d] = sum;
+    }
+    free(p);
+  }
+}
+
+/* tok [vocab][dim], role [nrole][dim] (dequantized); layer_w: 6 pointers per
+ * layer, wq wk wv wo [dim][dim], wup [dim][ffn], wdown [ffn][dim], all
+ * [in][out]; wout [dim][odim] or NULL. out: [batch][wout ? odim : dim]. */
+void compact_embed(const float* tok, int vocab, const float* role, int nrole,
+                   const float* const* layer_w, int layers, const float* wout, int odim,
+                   const int32_t* ids, const int32_t* role_ids, const int32_t* mask, int batch,
+                   int tokens, int dim, int heads, int ffn, float* out) {
+  (void)vocab;
+  (void)nrole;
+  const int rows = batch * tokens;
+  const size_t rd = (size_t)rows * dim;
+  float* x = (float*)malloc(sizeof(float) * rd);
+  float* q = (float*)malloc(sizeof(float) * rd);
+  float* k = (float*)malloc(sizeof(float) * rd);
+  float* v = (float*)malloc(sizeof(float) * rd);
+  float* mixed = (float*)malloc(sizeof(float) * rd);
+  float* t = (float*)malloc(sizeof(float) * rd);
+  float* mid = (float*)malloc(sizeof(float) * (size_t)rows * ffn);
+  for (int r = 0; r < rows; ++r) {
+    const float* te = tok + (size_t)ids[r] * dim;
+    const float* re = role + (size_t)(role_ids ? role_ids[r] : 0) * dim;
+    for (int c = 0; c < dim; ++c) x[(size_t)r * dim + c] = te[c] + re[c];
+  }
+  rope_rows(x, rows, tokens, dim);
+  for (int l = 0; l < layers; ++l) {
+    const float* const* w = layer_w + (size_t)l * 6;
+    matmul_f32(x, rows, dim, w[0], dim, q);
+    matmul_f32(x, rows, dim, w[1], dim, k);
+    matmul_f32(x, rows, dim, w[2], dim, v);
+    if (heads > 1)
+      bert_attention(q, k, v, mask, batch, tokens, dim, heads, mixed);
+    else
+      compact_single_head_attention(q, k, v, mask, batch, tokens, dim, mixed);
+    matmul_f32(mixed, rows, dim, w[3], dim, t);
+    for (size_t i = 0; i < rd; ++i) t[i] = t[i] + x[i];
+    layer_norm_rows(t, rows, dim);
+    matmul_f32(t, rows, dim, w[4], ffn, mid);
+    for (size_t i = 0; i < (size_t)rows * ffn; ++i) mid[i] = tanh_gelu(mid[i]);
+    matmul_f32(mid, rows, ffn, w[5], dim, q);
+    for (size_t i = 0; i < rd; ++i) x[i] = q[i] + t[i];
+    layer_norm_rows(x, rows, dim);
+  }
+  normalize_rows(x, rows, dim);
+  if (wout != NULL) {
+    float* y = (float*)malloc(sizeof(float) * (size_t)rows * odim);
+    matmul_f32(x, rows, dim, wout, odim, y);
+    mean_pool_masked(y, mask, batch, tokens, odim, out);
+    free(y);
+  } else {
+    mean_pool_masked(x, mask, batch, tokens, dim, out);
+  }
+  free(x);
+  free(q);
+  free(k);
+  free(v);
+  free(mixed);
+  free(t);
+  free(mid);
+}
