@@ -851,3 +851,211 @@ int eoship_tq_maxsim_scores(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, co
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------ parent aggregation
+
+// A parent layout over a bound corpus: parent p owns the corpus vectors
+// [off[p], off[p+1]) -- the children of topTurboQuantMultiVectorParentScores
+// (runtime/retrieval_multivector_turboquant.go:746-758), grouped by parent.
+struct EosHipTQParents {
+  EosHipTQ* tq = nullptr;
+  int64_t np = 0, live = 0;
+  long long* off = nullptr;   // [np + 1]
+  double* l1p = nullptr;      // [np] log1p(child count)
+  float* pscores = nullptr;   // [per][np]
+  size_t pscores_bytes = 0;
+  void* io = nullptr;         // host-API staging
+  size_t io_bytes = 0;
+  ~EosHipTQParents() {
+    void* ptrs[] = {off, l1p, pscores, io};
+    for (void* p : ptrs)
+      if (p) hipFree(p);
+  }
+};
+
+namespace {
+
+// Queries per pass: the dense child-score block [per][n] stays under 4 GiB.
+int parent_batch(const EosHipTQParents* P) {
+  const int64_t by_mem = ((int64_t)1 << 32) / std::max<int64_t>(1, P->tq->n * 4);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(P->tq->batch_cap(), by_mem));
+}
+
+int parent_check(EosHipRuntime* rt, EosHipTQParents* P, int32_t q, int32_t top_n, double penalty,
+                 const char* what, char** err) {
+  if (rt == nullptr || P == nullptr) return set_err(err, "%s: NULL runtime or parents", what);
+  if (P->tq->rt != rt) return set_err(err, "%s: parents were bound on another runtime", what);
+  if (q < 0) return set_err(err, "%s: negative query count", what);
+  if (top_n != 1 && top_n != 2 && top_n != 3 && top_n != 5)
+    return set_err(err, "%s: aggregation must be max (1), top2-mean, top3-mean or top5-mean (got top_n %d)",
+                   what, top_n);
+  if (!(penalty >= 0.0) || std::isinf(penalty))
+    return set_err(err, "%s: child-count-penalty must be non-negative and finite", what);
+  return 0;
+}
+
+int parent_topk_impl(EosHipRuntime* rt, EosHipTQParents* P, const float* d_queries, int32_t q,
+                     int32_t k, int32_t top_n, double penalty, int64_t* d_ids, float* d_scores,
+                     int64_t* d_best, float* d_best_score, char** err) {
+  EosHipTQ* tq = P->tq;
+  const int64_t kk64 = (k <= 0 || (int64_t)k > P->live) ? P->live : k;
+  if (q == 0 || kk64 == 0) return 0;
+  if (kk64 > kSortCap)
+    return set_err(err, "eoship_tq_parent_topk: k=%lld exceeds the device top-k limit of %d",
+                   (long long)kk64, kSortCap);
+  const int kk = (int)kk64;
+  const int per = parent_batch(P);
+  if (tq->ensure(reinterpret_cast<void**>(&P->pscores), &P->pscores_bytes,
+                 (size_t)per * (size_t)P->np * sizeof(float), err) != 0)
+    return 1;
+  for (int q0 = 0; q0 < q; q0 += per) {
+    const int qb = std::min(per, q - q0);
+    if (tq->prepare(d_queries + (size_t)q0 * tq->d, qb, nullptr, err) != 0) return 1;
+    if (tq->dense_scores(qb, 0, tq->n, false, err) != 0) return 1;
+    TqParentArgs ag;
+    memset(&ag, 0, sizeof(ag));
+    ag.scores = tq->dense;
+    ag.off = P->off;
+    ag.l1p = P->l1p;
+    ag.out = P->pscores;
+    ag.np = P->np;
+    ag.stride = tq->n;
+    ag.penalty = penalty;
+    ag.top_n = top_n;
+    ag.qb = qb;
+    if (rt->launch("eos_tq_parent_agg", dim3((unsigned)((P->np + 3) / 4), qb), dim3(256), 0, &ag,
+                   err, "tq_parent_agg") != 0)
+      return 1;
+    TqSelectArgs sel;
+    memset(&sel, 0, sizeof(sel));
+    sel.rows = P->pscores;
+    sel.ids = reinterpret_cast<long long*>(d_ids + (size_t)q0 * kk);
+    sel.scores = d_scores + (size_t)q0 * kk;
+    sel.n = P->np;
+    sel.stride = P->np;
+    sel.kk = kk;
+    sel.mode = 1;
+    sel.nrows = qb;
+    if (rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err, "tq_parent_select") != 0)
+      return 1;
+    TqParentBestArgs bb;
+    memset(&bb, 0, sizeof(bb));
+    bb.scores = tq->dense;
+    bb.off = P->off;
+    bb.parents = reinterpret_cast<const long long*>(d_ids + (size_t)q0 * kk);
+    bb.best_child = reinterpret_cast<long long*>(d_best + (size_t)q0 * kk);
+    bb.best_score = d_best_score + (size_t)q0 * kk;
+    bb.stride = tq->n;
+    bb.kk = kk;
+    bb.qb = qb;
+    if (rt->launch("eos_tq_parent_best", dim3((unsigned)((kk + 3) / 4), qb), dim3(256), 0, &bb, err,
+                   "tq_parent_best") != 0)
+      return 1;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int eoship_tq_parents_bind(EosHipRuntime* rt, EosHipTQ* tq, const int64_t* offsets,
+                           int64_t nparents, EosHipTQParents** out, char** err) {
+  const char* what = "eoship_tq_parents_bind";
+  if (rt == nullptr || tq == nullptr || offsets == nullptr || out == nullptr)
+    return set_err(err, "%s: NULL argument", what);
+  *out = nullptr;
+  if (tq->rt != rt) return set_err(err, "%s: corpus was bound on another runtime", what);
+  if (nparents <= 0 || nparents > ((int64_t)1 << 31))
+    return set_err(err, "%s: parent count must be in 1..2^31 (got %lld)", what, (long long)nparents);
+  if (offsets[0] != 0 || offsets[nparents] != tq->n)
+    return set_err(err, "%s: offsets must start at 0 and end at the corpus size %lld", what,
+                   (long long)tq->n);
+  std::vector<double> l1p((size_t)nparents);
+  int64_t live = 0;
+  for (int64_t p = 0; p < nparents; ++p) {
+    const int64_t c = offsets[p + 1] - offsets[p];
+    if (c < 0) return set_err(err, "%s: offsets decrease at parent %lld", what, (long long)p);
+    live += c > 0 ? 1 : 0;
+    l1p[(size_t)p] = std::log1p((double)c);
+  }
+  auto* P = new EosHipTQParents();
+  P->tq = tq;
+  P->np = nparents;
+  P->live = live;
+  const size_t ob = (size_t)(nparents + 1) * sizeof(long long), lb = (size_t)nparents * sizeof(double);
+  hipError_t e = hipSuccess;
+  if (rt->alloc(ob, reinterpret_cast<void**>(&P->off), err) ||
+      rt->alloc(lb, reinterpret_cast<void**>(&P->l1p), err)) {
+    delete P;
+    return 1;
+  }
+  e = hipMemcpy(P->off, offsets, ob, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(P->l1p, l1p.data(), lb, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    delete P;
+    return hip_err(err, "hipMemcpy(parent offsets)", e);
+  }
+  *out = P;
+  return 0;
+}
+
+int eoship_tq_parents_release(EosHipTQParents* parents, char** err) {
+  (void)err;
+  if (parents == nullptr) return 0;
+  hipStreamSynchronize(parents->tq->rt->stream);
+  delete parents;
+  return 0;
+}
+
+int eoship_tq_parent_topk_device(EosHipRuntime* rt, EosHipTQParents* parents,
+                                 const float* d_queries, int32_t q, int32_t k, int32_t top_n,
+                                 double child_count_penalty, int64_t* d_parent_ids,
+                                 float* d_scores, int64_t* d_best_child, float* d_best_child_score,
+                                 char** err) {
+  const char* what = "eoship_tq_parent_topk_device";
+  if (parent_check(rt, parents, q, top_n, child_count_penalty, what, err) != 0) return 1;
+  if (q > 0 && (d_queries == nullptr || d_parent_ids == nullptr || d_scores == nullptr ||
+                d_best_child == nullptr || d_best_child_score == nullptr))
+    return set_err(err, "%s: NULL buffer", what);
+  return parent_topk_impl(rt, parents, d_queries, q, k, top_n, child_count_penalty, d_parent_ids,
+                          d_scores, d_best_child, d_best_child_score, err);
+}
+
+int eoship_tq_parent_topk(EosHipRuntime* rt, EosHipTQParents* parents, const float* queries,
+                          int32_t q, int32_t k, int32_t top_n, double child_count_penalty,
+                          int64_t* parent_ids, float* scores, int64_t* best_child,
+                          float* best_child_score, char** err) {
+  const char* what = "eoship_tq_parent_topk";
+  if (parent_check(rt, parents, q, top_n, child_count_penalty, what, err) != 0) return 1;
+  const int64_t kk = (k <= 0 || (int64_t)k > parents->live) ? parents->live : k;
+  if (q == 0 || kk == 0) return 0;
+  if (queries == nullptr || parent_ids == nullptr || scores == nullptr || best_child == nullptr ||
+      best_child_score == nullptr)
+    return set_err(err, "%s: NULL buffer", what);
+  const int d = parents->tq->d;
+  const size_t qbytes = ((size_t)q * d * sizeof(float) + 15) & ~(size_t)15;
+  const size_t rows = (size_t)q * (size_t)kk;
+  const size_t need = qbytes + rows * (8 + 4 + 8 + 4) + 64;
+  if (parents->tq->ensure(&parents->io, &parents->io_bytes, need, err) != 0) return 1;
+  char* base = static_cast<char*>(parents->io);
+  float* dq = reinterpret_cast<float*>(base);
+  int64_t* di = reinterpret_cast<int64_t*>(base + qbytes);
+  int64_t* db = di + rows;
+  float* ds = reinterpret_cast<float*>(db + rows);
+  float* dbs = ds + rows;
+  hipError_t e = hipMemcpyAsync(dq, queries, (size_t)q * d * sizeof(float), hipMemcpyHostToDevice,
+                                rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
+  if (parent_topk_impl(rt, parents, dq, q, k, top_n, child_count_penalty, di, ds, db, dbs, err) != 0)
+    return 1;
+  e = hipMemcpyAsync(parent_ids, di, rows * 8, hipMemcpyDeviceToHost, rt->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(scores, ds, rows * 4, hipMemcpyDeviceToHost, rt->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(best_child, db, rows * 8, hipMemcpyDeviceToHost, rt->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(best_child_score, dbs, rows * 4, hipMemcpyDeviceToHost, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(results)", e);
+  return rt->sync(err);
+}
+
+}  // extern "C"

@@ -94,4 +94,30 @@ struct TqMaxsimArgs {
   uint32_t lut0, lut1, lut2, lut3;
 };
 
+// Parent (multivector) aggregation over child scores: parent p owns children
+// [off[p], off[p+1]) of each score row; out[q][p] = f32(mean of its best
+// min(top_n, 5, count) child scores (f64 sum in descending order) -
+// penalty * l1p[p]); parents without children get -inf.
+struct TqParentArgs {
+  const float* scores;      // [qb][stride] child scores
+  const long long* off;     // [np + 1]
+  const double* l1p;        // [np] log1p(child count)
+  float* out;               // [qb][np]
+  long long np, stride;
+  double penalty;
+  int top_n, qb;
+};
+
+// Best child of each selected parent: the highest child score, ties to the
+// lower child index.
+struct TqParentBestArgs {
+  const float* scores;        // [qb][stride] child scores
+  const long long* off;       // [np + 1]
+  const long long* parents;   // [qb][kk] selected parent ids
+  long long* best_child;      // [qb][kk]
+  float* best_score;          // [qb][kk]
+  long long stride;
+  int kk, qb;
+};
+
 #endif  // EOSHIP_TQ_ARGS_H

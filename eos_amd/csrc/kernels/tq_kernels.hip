@@ -1095,3 +1095,113 @@ EOS_TQ_MAXSIM(4, 12, 2)
 EOS_TQ_MAXSIM(4, 16, 2)
 EOS_TQ_MAXSIM(4, 24, 2)
 EOS_TQ_MAXSIM(4, 32, 1)
+
+// ------------------------------------------------------- parent aggregation
+
+// One wavefront per (query, parent): each lane keeps the 5 best of the child
+// scores it reads (sorted descending in registers, 8 loads in flight), then
+// the wave pops the best min(top_n, count) values in descending order --
+// the order aggregateMultiVectorParentScores sums the accumulator's list in
+// (runtime/retrieval_multivector_turboquant.go:769-810) -- and forms the
+// parent score in f64 with explicitly rounded operations.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_parent_agg(TqParentArgs a) {
+  const int lane = threadIdx.x & 63;
+  const long long p = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int q = blockIdx.y;
+  if (p >= a.np || q >= a.qb) return;
+  const long long c0 = a.off[p], c1 = a.off[p + 1];
+  const long long cnt = c1 - c0;
+  float* out = a.out + (size_t)q * a.np + p;
+  if (cnt <= 0) {
+    if (lane == 0) *out = -__builtin_inff();
+    return;
+  }
+  const float* row = a.scores + (size_t)q * a.stride;
+  float t[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) t[i] = -__builtin_inff();
+  constexpr int U = 8;
+  for (long long base = c0 + lane; base < c1; base += 64LL * U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long c = base + 64LL * u;
+      v[u] = row[c < c1 ? c : c1 - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (base + 64LL * u < c1) {
+        float x = v[u];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+          const float hi = fmaxf(x, t[i]), lo = fminf(x, t[i]);
+          t[i] = hi;
+          x = lo;
+        }
+      }
+    }
+  }
+  const int avail = (a.top_n <= 0 || (long long)a.top_n > cnt || a.top_n > 5)
+                        ? (int)(cnt < 5 ? cnt : 5)
+                        : a.top_n;
+  double sum = 0.0;
+  for (int r = 0; r < avail; ++r) {
+    float m = t[0];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const unsigned long long owners = __ballot(t[0] == m);
+    if (lane == __builtin_ctzll(owners)) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] = t[i + 1];
+      t[4] = -__builtin_inff();
+    }
+    sum = __dadd_rn(sum, (double)m);
+  }
+  double sc = __ddiv_rn(sum, (double)avail);
+  if (a.penalty != 0.0) sc = __dsub_rn(sc, __dmul_rn(a.penalty, a.l1p[p]));
+  if (lane == 0) *out = (float)sc;
+}
+
+// One wavefront per (query, selected parent): argmax over its children,
+// ties to the lower child index (the accumulator's best child, :769-776).
+extern "C" __global__ __launch_bounds__(256) void eos_tq_parent_best(TqParentBestArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int q = blockIdx.y;
+  if (i >= a.kk || q >= a.qb) return;
+  const long long p = a.parents[(size_t)q * a.kk + i];
+  const long long c0 = a.off[p], c1 = a.off[p + 1];
+  const float* row = a.scores + (size_t)q * a.stride;
+  float bv = -__builtin_inff();
+  long long bi = c1;
+  constexpr int U = 8;
+  for (long long base = c0 + lane; base < c1; base += 64LL * U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long c = base + 64LL * u;
+      v[u] = row[c < c1 ? c : c1 - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long c = base + 64LL * u;
+      if (c < c1 && (v[u] > bv || (v[u] == bv && c < bi))) {
+        bv = v[u];
+        bi = c;
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const long long oi = __shfl_xor(bi, o);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    a.best_child[(size_t)q * a.kk + i] = bi;
+    a.best_score[(size_t)q * a.kk + i] = bv;
+  }
+}

@@ -13,6 +13,11 @@ argument meaning and error behaviour:
 * ``TurboQuantIndex.inner_product_prepared`` -- ``InnerProductPrepared`` over a
   slice of documents (runtime/retrieval_turboquant.go:1874), with the exact
   integer code dot products.
+* ``TurboQuantMultiVectorIndex`` -- MaxSim over fixed-size documents.
+* ``TurboQuantParents`` / ``top_turboquant_multivector_parent_scores`` --
+  ``topTurboQuantMultiVectorParentScores`` over ragged parents with the
+  max / topN-mean aggregations and the child-count penalty
+  (runtime/retrieval_multivector_turboquant.go:746-908).
 
 All arithmetic runs in libeoship's gfx950 kernels; nothing here computes scores.
 """
@@ -207,6 +212,91 @@ class TurboQuantMultiVectorIndex:
                   C.c_int32(q.shape[1]), C.c_int64(doc_begin), C.c_int64(doc_count),
                   out.ctypes.data_as(C.c_void_p))
         return out
+
+
+_AGGREGATION_TOP_N = {"max": 1, "top2-mean": 2, "top3-mean": 3, "top5-mean": 5}
+
+
+@dataclass
+class ParentScoredDoc:
+    """A ranked parent with its best child (retrievalScoredDoc's ID, Score,
+    ChildID and ChildScore, runtime/retrieval_multivector_turboquant.go:
+    800-806); ids are integer parent and corpus-vector indices."""
+    id: int
+    score: float
+    child_id: int
+    child_score: float
+
+
+class TurboQuantParents:
+    """Children grouped by parent over a bound corpus: parent p owns vectors
+    [offsets[p], offsets[p+1]). ``top_k`` is topTurboQuantMultiVectorParentScores
+    (runtime/retrieval_multivector_turboquant.go:746-758) for each query vector,
+    with aggregation "max" | "top2-mean" | "top3-mean" | "top5-mean" and a
+    non-negative child_count_penalty (validated as :826-837 does)."""
+
+    def __init__(self, index: TurboQuantIndex, offsets: np.ndarray):
+        off = np.ascontiguousarray(offsets, dtype=np.int64)
+        if off.ndim != 1 or off.shape[0] < 2:
+            raise ValueError("offsets must be [nparents + 1]")
+        self.index, self.offsets = index, off
+        self.nparents = off.shape[0] - 1
+        self.live = int(np.sum(off[1:] > off[:-1]))
+        self.handle = C.c_void_p()
+        _lib.call("eoship_tq_parents_bind", index.rt.handle, index.handle,
+                  off.ctypes.data_as(C.c_void_p), C.c_int64(self.nparents), C.byref(self.handle))
+
+    def release(self) -> None:
+        if self.handle:
+            _lib.call("eoship_tq_parents_release", self.handle)
+            self.handle = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _top_n(aggregation: str) -> int:
+        if aggregation not in _AGGREGATION_TOP_N:
+            raise ValueError("aggregation must be one of max, top2-mean, top3-mean, top5-mean")
+        return _AGGREGATION_TOP_N[aggregation]
+
+    def top_k(self, queries: np.ndarray, top_k: int, aggregation: str = "max",
+              child_count_penalty: float = 0.0):
+        """Returns (parent_ids, scores, best_child, best_child_score), each [Q, kk]."""
+        q = np.ascontiguousarray(queries, dtype=np.float32).reshape(-1, self.index.dim)
+        kk = self.live if (top_k <= 0 or top_k > self.live) else int(top_k)
+        ids = np.zeros((q.shape[0], kk), np.int64)
+        sc = np.zeros((q.shape[0], kk), np.float32)
+        bc = np.zeros((q.shape[0], kk), np.int64)
+        bs = np.zeros((q.shape[0], kk), np.float32)
+        _lib.call("eoship_tq_parent_topk", self.index.rt.handle, self.handle,
+                  q.ctypes.data_as(C.c_void_p), C.c_int32(q.shape[0]), C.c_int32(int(top_k)),
+                  C.c_int32(self._top_n(aggregation)), C.c_double(child_count_penalty),
+                  ids.ctypes.data_as(C.c_void_p), sc.ctypes.data_as(C.c_void_p),
+                  bc.ctypes.data_as(C.c_void_p), bs.ctypes.data_as(C.c_void_p))
+        return ids, sc, bc, bs
+
+    def top_k_device(self, d_queries: DeviceBuffer, nq: int, top_k: int, d_ids: DeviceBuffer,
+                     d_scores: DeviceBuffer, d_best: DeviceBuffer, d_best_scores: DeviceBuffer,
+                     aggregation: str = "max", child_count_penalty: float = 0.0) -> None:
+        _lib.call("eoship_tq_parent_topk_device", self.index.rt.handle, self.handle, d_queries.ptr,
+                  C.c_int32(nq), C.c_int32(int(top_k)), C.c_int32(self._top_n(aggregation)),
+                  C.c_double(child_count_penalty), d_ids.ptr, d_scores.ptr, d_best.ptr,
+                  d_best_scores.ptr)
+
+
+def top_turboquant_multivector_parent_scores(parents: TurboQuantParents, query: np.ndarray,
+                                             top_k: int, aggregation: str = "max",
+                                             child_count_penalty: float = 0.0):
+    """topTurboQuantMultiVectorParentScores for one query vector: the ranked
+    [ParentScoredDoc] list."""
+    ids, sc, bc, bs = parents.top_k(np.asarray(query)[None, :], top_k, aggregation,
+                                    child_count_penalty)
+    return [ParentScoredDoc(int(i), float(s), int(c), float(cs))
+            for i, s, c, cs in zip(ids[0], sc[0], bc[0], bs[0])]
 
 
 def top_turboquant_retrieval_scores_with_stats(index: TurboQuantIndex, queries: np.ndarray,

@@ -170,6 +170,37 @@ int eoship_tq_maxsim_scores(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, co
                             int32_t q, int32_t tq_tokens, int64_t doc_begin, int64_t doc_count,
                             float* scores, char** err);
 
+/* Parent aggregation over children (one query vector per query): the
+ * corpus vectors [offsets[p], offsets[p+1]) are the children of parent p
+ * (offsets ascending, offsets[0] = 0, offsets[nparents] = corpus size; a
+ * parent may have no children). Replaces topTurboQuantMultiVectorParentScores
+ * (runtime/retrieval_multivector_turboquant.go:746-758) with its
+ * accumulator and aggregation (:769-810) and topParentScoresFromMap
+ * (:890-908), ids being integer parent and child indices. Release the
+ * parents before their corpus. */
+typedef struct EosHipTQParents EosHipTQParents;
+int eoship_tq_parents_bind(EosHipRuntime* rt, EosHipTQ* tq, const int64_t* offsets,
+                           int64_t nparents, EosHipTQParents** out, char** err);
+int eoship_tq_parents_release(EosHipTQParents* parents, char** err);
+/* Per query: every child's TurboQuant score; per parent the mean of its
+ * best min(top_n, count) child scores (f64 sum in descending order; top_n 1
+ * = "max", 2/3/5 = "top2/3/5-mean", validateTurboQuantMultiVectorAggregation-
+ * Config :826-837) minus child_count_penalty * log1p(count) when the penalty
+ * is nonzero (>= 0, else an error), rounded to f32; the best min(k,
+ * parents with children) parents (k <= 0: all of them) by score desc, parent
+ * id asc, each with its best child (highest score, then lowest index) and
+ * that child's score. Outputs [q][kk] (host buffers). */
+int eoship_tq_parent_topk(EosHipRuntime* rt, EosHipTQParents* parents, const float* queries,
+                          int32_t q, int32_t k, int32_t top_n, double child_count_penalty,
+                          int64_t* parent_ids, float* scores, int64_t* best_child,
+                          float* best_child_score, char** err);
+/* Same on device buffers, enqueued on the runtime stream (no wait). */
+int eoship_tq_parent_topk_device(EosHipRuntime* rt, EosHipTQParents* parents,
+                                 const float* d_queries, int32_t q, int32_t k, int32_t top_n,
+                                 double child_count_penalty, int64_t* d_parent_ids,
+                                 float* d_scores, int64_t* d_best_child, float* d_best_child_score,
+                                 char** err);
+
 /* ------------------------------------------------------------- tiny embed */
 
 typedef struct EosHipEmbed EosHipEmbed;

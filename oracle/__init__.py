@@ -48,6 +48,9 @@ def load() -> C.CDLL:
     lib.tq_maxsim_scores.argtypes = [P, C.c_int, C.c_int, P, C.c_int, C.c_int, P, C.c_float, P, P,
                                      C.c_int64, C.c_int, P]
     lib.tq_maxsim_scores.restype = None
+    lib.tq_parent_topk.argtypes = [P, C.c_int, P, C.c_int, C.c_int, P, C.c_float, P, P, P,
+                                   C.c_int64, C.c_int, C.c_double, C.c_int, P, P, P, P]
+    lib.tq_parent_topk.restype = C.c_int64
     _lib = lib
     return lib
 
@@ -153,6 +156,31 @@ def tq_maxsim_scores(queries, rotation, dim, bits, codebook, codebook_scale, cod
                             C.c_float(codebook_scale), _p(codes), _p(norms), ndocs, doc_len,
                             _p(out))
     return out
+
+
+def tq_parent_topk(queries, rotation, dim, bits, codebook, codebook_scale, codes, norms,
+                   offsets, k, top_n=1, penalty=0.0):
+    """Parent (multivector child) aggregation top-k, one query vector each.
+    offsets [nparents + 1] (parent p owns vectors [off[p], off[p+1])).
+    Returns (ids, scores, best_child, best_child_score), each [Q, kk]."""
+    q = _f32(queries).reshape(-1, dim)
+    rot = None if rotation is None else _f32(rotation)
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    norms = _f32(norms)
+    cb = np.ascontiguousarray(codebook, dtype=np.int8)
+    off = np.ascontiguousarray(offsets, dtype=np.int64)
+    npar = off.shape[0] - 1
+    live = int(np.sum(off[1:] > off[:-1]))
+    kk = live if (k <= 0 or k > live) else k
+    ids = np.zeros((q.shape[0], kk), np.int64)
+    sc = np.zeros((q.shape[0], kk), np.float32)
+    bc = np.zeros((q.shape[0], kk), np.int64)
+    bs = np.zeros((q.shape[0], kk), np.float32)
+    got = load().tq_parent_topk(_p(q), q.shape[0], _p(rot), dim, bits, _p(cb),
+                                C.c_float(codebook_scale), _p(codes), _p(norms), _p(off), npar,
+                                top_n, C.c_double(penalty), k, _p(ids), _p(sc), _p(bc), _p(bs))
+    assert got == kk
+    return ids, sc, bc, bs
 
 
 # ------------------------------------------------------------------ encoder

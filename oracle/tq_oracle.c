@@ -311,3 +311,80 @@ void tq_maxsim_scores(const float* queries, int nq, int tq_tokens, const float* 
   free(dots);
   free(zero);
 }
+
+/* ------------------------------------------------------ parent aggregation
+ * topTurboQuantMultiVectorParentScores (runtime/retrieval_multivector_
+ * turboquant.go:746-758) for one query vector at a time, on integer ids:
+ * parent p owns the corpus vectors [off[p], off[p+1]) (its children). Per
+ * parent, the accumulator's add (:769-783) keeps the count, the best child
+ * (higher score, then the lower child id) and the 5 best scores in
+ * descending order; aggregateMultiVectorParentScores (:785-810) sums the
+ * first min(top_n, kept) of them in f64 in that order, divides, subtracts
+ * penalty * log1p(count) when the penalty is nonzero, and rounds to f32;
+ * topParentScoresFromMap (:890-908) keeps the best k parents under
+ * retrievalScoreBetter. Parents without children never enter the map, so
+ * kk = min(k, parents with children) (k <= 0 means all of them). Returns kk;
+ * ids/scores/best_child/best_child_score are [nq][kk]. */
+int64_t tq_parent_topk(const float* queries, int nq, const float* rot, int d, int bits,
+                       const int8_t* cb, float cb_scale, const uint8_t* codes, const float* norms,
+                       const int64_t* off, int64_t np, int top_n, double penalty, int k,
+                       int64_t* ids, float* scores, int64_t* best_child, float* best_child_score) {
+  int64_t live = 0;
+  for (int64_t p = 0; p < np; ++p) live += off[p + 1] > off[p] ? 1 : 0;
+  const int64_t kk = (k <= 0 || (int64_t)k > live) ? live : k;
+  if (kk == 0) return 0;
+  const int64_t n = off[np];
+  float* s = (float*)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+  float* pscore = (float*)malloc(sizeof(float) * (size_t)np);
+  int64_t* pbest = (int64_t*)malloc(sizeof(int64_t) * (size_t)np);
+  scored_t* heap = (scored_t*)malloc(sizeof(scored_t) * (size_t)kk);
+  for (int q = 0; q < nq; ++q) {
+    tq_scores(queries + (size_t)q * d, 1, rot, d, bits, cb, cb_scale, codes, norms, 0, n, NULL, s);
+    int len = 0;
+    for (int64_t p = 0; p < np; ++p) {
+      const int64_t c0 = off[p], c1 = off[p + 1];
+      if (c1 <= c0) continue;
+      float top[6];
+      int kept = 0;
+      int64_t bid = -1;
+      float bsc = 0.0f;
+      for (int64_t c = c0; c < c1; ++c) {
+        const float v = s[c];
+        if (bid < 0 || v > bsc || (v == bsc && c < bid)) {
+          bid = c;
+          bsc = v;
+        }
+        top[kept++] = v;
+        for (int i = kept - 1; i > 0 && top[i] > top[i - 1]; --i) {
+          const float t = top[i];
+          top[i] = top[i - 1];
+          top[i - 1] = t;
+        }
+        if (kept > 5) kept = 5;
+      }
+      int avail = top_n;
+      if (avail <= 0 || avail > kept) avail = kept;
+      double sum = 0.0;
+      for (int i = 0; i < avail; ++i) sum += (double)top[i];
+      double sc = sum / (double)avail;
+      if (penalty != 0.0) sc -= penalty * log1p((double)(c1 - c0));
+      pscore[p] = (float)sc;
+      pbest[p] = bid;
+      scored_t e = {p, (float)sc};
+      heap_offer(heap, &len, (int)kk, e);
+    }
+    insertion_sort(heap, len);
+    for (int64_t i = 0; i < kk; ++i) {
+      const int64_t p = heap[i].id;
+      ids[(size_t)q * kk + i] = p;
+      scores[(size_t)q * kk + i] = heap[i].score;
+      best_child[(size_t)q * kk + i] = pbest[p];
+      best_child_score[(size_t)q * kk + i] = s[pbest[p]];
+    }
+  }
+  free(s);
+  free(pscore);
+  free(pbest);
+  free(heap);
+  return kk;
+}
