@@ -192,7 +192,8 @@ def tq_leg(rt, args) -> dict:
     rt.sync()
     breakdown = {}
     for name in ("eos_tq_rotate", "eos_tq_quantize", "tq_scan_sample", "eos_tq_threshold",
-                 "tq_scan_filter", "eos_tq_finalize", "tq_scan_dense", "tq_fallback_select"):
+                 "tq_scan_filter", "tq_rescore", "eos_tq_finalize", "tq_scan_dense",
+                 "tq_fallback_select"):
         breakdown[name] = rt.profile_read(name)[1] / args.steps
     rt.profile(False)
     st = idx.top_k_device(dq, args.queries, args.k, dids, dsc, with_stats=True)

@@ -32,6 +32,7 @@ namespace {
 constexpr int kBatch = 64;          // queries per scan (two 32-column groups)
 constexpr int kMaxCols = 128;       // MFMA query columns per pass (MaxSim: four 32-token groups)
 constexpr int kCap = 8192;          // kept candidates per query
+constexpr int kRescoreBlocks = 16;  // workgroups per query rescoring kept ids (64 ids each)
 constexpr int kSortCap = 8192;      // largest k the device sort handles
 constexpr int kSampleStride = 16;     // sample every 16th tile (at least)
 constexpr int kMaxSampleTiles = 2048;  // tile maxima per query (the threshold kernel holds 4096)
@@ -134,13 +135,19 @@ struct EosHipTQ {
   int32_t* dense_dots = nullptr;
   size_t dense_dots_bytes = 0;
   int16_t* qs_buf = nullptr;
+  // high-half filter bounds: per query column ||lo||_2, per tile max ||C||_2
+  float* lonorm = nullptr;
+  float* tile_cn = nullptr;
+  // reference-layout code rows padded to rs16 16-byte chunks (rescoring)
+  uint8_t* codes_rm = nullptr;
+  int rs16 = 0;
   // host-API staging
   void* io = nullptr;
   size_t io_bytes = 0;
 
   void free_all() {
     void* ptrs[] = {packed, norms, rot_t, qrot, bfrag, alpha, tau, cand, cand_count,
-                    status, samp, dense, dense_dots, qs_buf, io};
+                    status, samp, dense, dense_dots, qs_buf, lonorm, tile_cn, codes_rm, io};
     for (void* p : ptrs)
       if (p) hipFree(p);
   }
@@ -175,13 +182,17 @@ struct EosHipTQ {
     s->lut1 = lut[1];
     s->lut2 = lut[2];
     s->lut3 = lut[3];
+    s->lonorm = lonorm;
+    s->tile_cn = tile_cn;
   }
 
   int launch_scan(TqScanArgs* s, int qb, char** err) {
-    static const char* const labels[3] = {"tq_scan_dense", "tq_scan_filter", "tq_scan_sample"};
+    static const char* const labels[4] = {"tq_scan_dense", "tq_scan_filter", "tq_scan_sample",
+                                          "tq_scan_filter"};
     const int nqg = nqg_for(qb);
     char name[64];
-    snprintf(name, sizeof(name), "eos_tq_scan_b%d_k%d_g%d_%c", bits, ks, nqg, s->mode == 1 ? 'f' : 'w');
+    const char kind = s->mode == 1 ? 'f' : s->mode == 3 ? 'h' : 'w';
+    snprintf(name, sizeof(name), "eos_tq_scan_b%d_k%d_g%d_%c", bits, ks, nqg, kind);
     const int waves = 4;
     int64_t blocks = (s->ntiles + waves - 1) / waves;
     const int64_t maxb = (int64_t)rt->compute_units * 2;
@@ -213,6 +224,7 @@ struct EosHipTQ {
     p.qrot = qrot;
     p.group = group;
     p.group_live = group_live;
+    p.lonorm = lonorm;
     const unsigned cblocks = (unsigned)(32 * nqg / 8);  // 8 columns per workgroup
     if (rot_t != nullptr) {
       const unsigned jblocks = (unsigned)((d + 31) / 32);
@@ -288,7 +300,7 @@ struct EosHipTQ {
   // reaches that point; otherwise flagged rows wait for fallback_batch.
   int topk_batch(const float* d_queries, int qb, int kk, int64_t* d_ids, float* d_scores,
                  int* d_status, bool gated, char** err) {
-    if (prepare(d_queries, qb, nullptr, err) != 0) return 1;
+    if (prepare(d_queries, qb, qs_buf, err) != 0) return 1;
     if (n > kCap) {
       const int64_t stride = std::max<int64_t>(kSampleStride, (ntiles + kMaxSampleTiles - 1) / kMaxSampleTiles);
       const int64_t ns = (ntiles + stride - 1) / stride;
@@ -316,12 +328,35 @@ struct EosHipTQ {
       sel.nrows = qb;
       if (rt->launch("eos_tq_threshold", dim3(qb), dim3(256), 0, &sel, err) != 0) return 1;
     }
+    // High-half filter (ids whose score bound reaches tau), then their exact
+    // scores: the kept set equals the exact filter's.
     TqScanArgs s;
     scan_base(&s, qb);
-    s.mode = 1;
+    s.mode = 3;
     s.tile_begin = 0;
     s.ntiles = (int)ntiles;
     if (launch_scan(&s, qb, err) != 0) return 1;
+    TqRescoreArgs rs;
+    memset(&rs, 0, sizeof(rs));
+    rs.codes = codes_rm;
+    rs.norms = norms;
+    rs.qs = qs_buf;
+    rs.alpha = alpha;
+    rs.tau = tau;
+    rs.cand = cand;
+    rs.cand_count = cand_count;
+    rs.n = n;
+    rs.q = qb;
+    rs.d = d;
+    rs.rs = rs16;
+    rs.cap = kCap;
+    rs.lut0 = lut[0];
+    rs.lut1 = lut[1];
+    rs.lut2 = lut[2];
+    rs.lut3 = lut[3];
+    if (rt->launch(bits == 4 ? "eos_tq_rescore_b4" : "eos_tq_rescore_b2", dim3(qb, kRescoreBlocks),
+                   dim3(256), 0, &rs, err, "tq_rescore") != 0)
+      return 1;
     TqFinalizeArgs f;
     memset(&f, 0, sizeof(f));
     f.cand = cand;
@@ -494,6 +529,24 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
       hip_err(err, "hipMemcpyAsync(codes)", e);
       return fail();
     }
+    if (rt->alloc((size_t)tq->ntiles * sizeof(float), reinterpret_cast<void**>(&tq->tile_cn), err) != 0) {
+      hipFree(dcodes);
+      return fail();
+    }
+    TqTileNormArgs tn;
+    memset(&tn, 0, sizeof(tn));
+    tn.codes = static_cast<const uint8_t*>(dcodes);
+    tn.tile_cn = tq->tile_cn;
+    tn.n = n;
+    tn.d = tq->d;
+    tn.bits = tq->bits;
+    tn.row_bytes = tq->row_bytes;
+    for (int v = 0; v < levels; ++v) tn.cb[v] = tq->codebook[v];
+    if (rt->launch("eos_tq_tile_cnorm", dim3((unsigned)((n + 255) / 256)), dim3(256), 0, &tn, err) != 0) {
+      rt->sync(nullptr);
+      hipFree(dcodes);
+      return fail();
+    }
     TqPackArgs p;
     memset(&p, 0, sizeof(p));
     p.codes = static_cast<const uint8_t*>(dcodes);
@@ -512,8 +565,33 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
       return fail();
     }
     const int rc = rt->sync(err);
-    hipFree(dcodes);
-    if (rc != 0) return fail();
+    if (rc != 0) {
+      hipFree(dcodes);
+      return fail();
+    }
+    // The reference-layout rows stay resident for the exact rescoring of
+    // kept ids, padded to whole 16-byte chunks (at most 32: 1024 dims at 4
+    // bits); rows that already are whole chunks are kept as uploaded.
+    tq->rs16 = (tq->row_bytes + 15) / 16;
+    const size_t pitch = (size_t)tq->rs16 * 16;
+    if (pitch == (size_t)tq->row_bytes) {
+      tq->codes_rm = static_cast<uint8_t*>(dcodes);
+    } else {
+      if (rt->alloc((size_t)n * pitch, reinterpret_cast<void**>(&tq->codes_rm), err) != 0) {
+        hipFree(dcodes);
+        return fail();
+      }
+      e = hipMemsetAsync(tq->codes_rm, 0, (size_t)n * pitch, rt->stream);
+      if (e == hipSuccess)
+        e = hipMemcpy2DAsync(tq->codes_rm, pitch, dcodes, tq->row_bytes, tq->row_bytes, (size_t)n,
+                             hipMemcpyDeviceToDevice, rt->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+      hipFree(dcodes);
+      if (e != hipSuccess) {
+        hip_err(err, "hipMemcpy2DAsync(code rows)", e);
+        return fail();
+      }
+    }
   }
   if (desc->rotation != nullptr) {
     std::vector<float> rt_host((size_t)tq->d * tq->d);
@@ -532,11 +610,15 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
   if (rt->alloc(bfrag_bytes, reinterpret_cast<void**>(&tq->bfrag), err) != 0 ||
       rt->alloc((size_t)kMaxCols * tq->d * sizeof(double), reinterpret_cast<void**>(&tq->qrot), err) != 0 ||
       rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&tq->alpha), err) != 0 ||
+      rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&tq->lonorm), err) != 0 ||
+      rt->alloc((size_t)kBatch * tq->d * sizeof(int16_t), reinterpret_cast<void**>(&tq->qs_buf),
+                err) != 0 ||
       rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&tq->tau), err) != 0 ||
       rt->alloc(kMaxCols * sizeof(uint32_t), reinterpret_cast<void**>(&tq->cand_count), err) != 0 ||
       rt->alloc(kMaxCols * sizeof(int), reinterpret_cast<void**>(&tq->status), err) != 0 ||
       rt->alloc((size_t)kBatch * kCap * sizeof(unsigned long long),
                 reinterpret_cast<void**>(&tq->cand), err) != 0 ||
+
       rt->alloc((size_t)kBatch * std::max<int64_t>(tq->samp_tiles, 1) * sizeof(float),
                 reinterpret_cast<void**>(&tq->samp), err) != 0)
     return fail();

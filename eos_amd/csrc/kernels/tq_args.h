@@ -15,6 +15,7 @@ struct TqPrepArgs {
   uint32_t* cand_count;  // [32*ncb/2] reset to 0
   int16_t* qs_out;       // optional [q][d]
   double* qrot;          // [32*ncb/2][d] rotated columns (written by eos_tq_rotate)
+  float* lonorm;         // optional [32*ncb/2]: ||lo||_2 of the column, rounded up
   int q, d, ks, ncb, qmax;
   float cb_scale;
   // Column -> source row: column c belongs to group c / group (a query of the
@@ -42,6 +43,8 @@ struct TqScanArgs {
   float* out_scores;       // dense/sample output [q][out_stride]
   int32_t* out_dots;       // dense output (optional)
   const int* gate;         // non-NULL: run only if some gate[i] != 0, i < q
+  const float* lonorm;     // high-half filter: [32*nqg] ||lo||_2 per column (rounded up)
+  const float* tile_cn;    // high-half filter: [ntiles] max ||C[codes]||_2 of the tile (rounded up)
   long long n;             // valid vectors
   long long out_begin;     // dense: vector index of column 0
   long long out_count;     // dense: columns
@@ -51,7 +54,7 @@ struct TqScanArgs {
   int ntiles;              // logical tiles in this launch
   int q;                   // live query columns
   int cap;                 // candidate capacity per query
-  int mode;                // 0 dense, 1 filter, 2 sample
+  int mode;                // 0 dense, 1 filter, 2 sample (3: high-half filter, kernels _h)
   uint32_t lut0, lut1, lut2, lut3;
 };
 
@@ -70,7 +73,7 @@ struct TqSelectArgs {
 
 struct TqFinalizeArgs {
   const unsigned long long* cand;
-  const uint32_t* cand_count;
+  uint32_t* cand_count;   // rewritten with the live (nonzero) entry count
   long long* ids;     // [q][kk]
   float* scores;      // [q][kk]
   int* status;        // [q]: 0 ok, 1 too few candidates, 2 overflow
@@ -118,6 +121,31 @@ struct TqParentBestArgs {
   float* best_score;          // [qb][kk]
   long long stride;
   int kk, qb;
+};
+
+// Exact rescoring of the high-half filter's kept ids, in place: each entry of
+// cand[q] (a list that did not overflow) becomes the exact rank key when the
+// exact score reaches tau, else 0.
+struct TqRescoreArgs {
+  const uint8_t* codes;    // [n][16 * rs] reference-layout code rows, zero-padded
+  const float* norms;
+  const int16_t* qs;       // [q][d] int16 queries
+  const float* alpha;
+  const float* tau;
+  unsigned long long* cand;
+  const uint32_t* cand_count;
+  long long n;               // corpus vectors (ids >= n are dropped)
+  int q, d, rs, cap;         // rs: 16-byte chunks per code row (<= 32)
+  uint32_t lut0, lut1, lut2, lut3;
+};
+
+// Per tile of 32 vectors, the largest ||C[codes]||_2 (rounded up to f32).
+struct TqTileNormArgs {
+  const uint8_t* codes;    // [n][row_bytes] reference layout
+  float* tile_cn;          // [ntiles]
+  long long n;
+  int d, bits, row_bytes;
+  int cb[16];              // codebook grid values
 };
 
 #endif  // EOSHIP_TQ_ARGS_H

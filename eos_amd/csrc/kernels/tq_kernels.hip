@@ -91,6 +91,15 @@ EOS_DEV void stage_fragments(v4i* dst, const v4i* src) {
 namespace {
 constexpr int kMaxDim = 1024;
 
+// sqrt(v) rounded up to f32 (v >= 0 an exact integer < 2^53): the f32 result
+// squared is exact in f64, so one comparison settles the direction.
+EOS_DEV float sqrt_up(long long v) {
+  const double dv = (double)v;
+  float f = (float)sqrt(dv);
+  if ((double)f * (double)f < dv) f = __uint_as_float(__float_as_uint(f) + 1u);
+  return f;
+}
+
 // Column c of the MFMA query block reads source row (c / group) * group_live
 // + c % group when c % group < group_live; other columns are zero.
 EOS_DEV int prep_source(const TqPrepArgs& a, int c) {
@@ -123,6 +132,7 @@ EOS_DEV void prep_quantize_column(const TqPrepArgs& a, int c, int t, Get get) {
   const double inv = mx > 0.0 ? (double)a.qmax / mx : 0.0;
   const int cb_hi = 2 * (c >> 5), col = c & 31;
   const int dpad = a.ks * 32;
+  int lo2 = 0;  // sum of lo^2 over the lane's coordinates (<= 1024 * 128^2)
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     const int j = t + 32 * m;
@@ -136,12 +146,16 @@ EOS_DEV void prep_quantize_column(const TqPrepArgs& a, int c, int t, Get get) {
     }
     const int lo = ((qs + 128) & 255) - 128;
     const int hi = (qs - lo) >> 8;
+    lo2 += lo * lo;
     const int s = j >> 5, g = (j >> 4) & 1, i = j & 15;
     const int lane = col + 32 * g;
     a.bfrag[((size_t)(s * a.ncb + cb_hi) * 64 + lane) * 16 + i] = (int8_t)hi;
     a.bfrag[((size_t)(s * a.ncb + cb_hi + 1) * 64 + lane) * 16 + i] = (int8_t)lo;
   }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) lo2 += __shfl_xor(lo2, o);
   if (t == 0) {
+    if (a.lonorm != nullptr) a.lonorm[c] = sqrt_up(lo2);
     a.alpha[c] = mx > 0.0 ? (float)((mx / (double)a.qmax) * (double)a.cb_scale) : 0.0f;
     a.tau[c] = -__builtin_inff();
     a.cand_count[c] = 0u;
@@ -265,6 +279,29 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_pack(TqPackArgs a) {
   a.packed[o] = out;
 }
 
+// Per tile, the largest ||C[codes_v]||_2 over its vectors (exact integer
+// sums of squares, rounded up): one thread per vector, a half-wave per tile.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_tile_cnorm(TqTileNormArgs a) {
+  const long long v = (long long)blockIdx.x * 256 + threadIdx.x;
+  long long ss = 0;
+  if (v < a.n) {
+    const uint8_t* row = a.codes + (size_t)v * a.row_bytes;
+    const uint32_t mask = (1u << a.bits) - 1u;
+    for (int k = 0; k < a.d; ++k) {
+      const int bit = k * a.bits;
+      const int c = a.cb[(row[bit >> 3] >> (bit & 7)) & mask];
+      ss += (long long)(c * c);
+    }
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) {
+    const long long t = __shfl_xor(ss, o);
+    ss = t > ss ? t : ss;
+  }
+  const long long tile = v >> 5;
+  if ((threadIdx.x & 31) == 0 && tile * kTile < a.n) a.tile_cn[tile] = sqrt_up(ss);
+}
+
 // --------------------------------------------------------------------- scan
 
 
@@ -324,13 +361,21 @@ EOS_DEV void load_tile_norms(float4 (&n)[4], const float* norms, long long tile,
 
 // FILTER = true: keep (score >= tau) rank keys (mode 1). FILTER = false: write
 // every score (mode 0 dense slice, mode 2 sampled tiles).
-template <int BITS, int KS, int NQG, bool FILTER>
+// HI (with FILTER): only the high int8 half of the query enters the MFMAs.
+// With Qs = 256 hi + lo, D = 256 D_hi + sum_j lo_j C_j and, by Cauchy-Schwarz,
+// |sum_j lo_j C_j| <= ||lo||_2 ||C[codes]||_2 <= L = lonorm * tile_cn (both
+// rounded up, the product bumped by 2^-22). Rounding to nearest is monotone,
+// so fl(fl(256 D_hi + L) n) >= fl(fl(D) n): every row whose exact score could
+// reach tau passes the exact filter's pre-test on this bound. Such rows are
+// kept as ids only; eos_tq_rescore computes their exact scores.
+template <int BITS, int KS, int NQG, bool FILTER, bool HI = false>
 EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   constexpr int NCB = 2 * NQG;
+  constexpr int NCBU = HI ? NQG : NCB;  // column blocks the MFMAs use
   constexpr int SPL = 8 / BITS;
   constexpr int NLOAD = (KS + SPL - 1) / SPL;
   constexpr int NQ = 32 * NQG;
-  __shared__ v4i sb[KS * NCB * 64];
+  __shared__ v4i sb[KS * NCBU * 64];
   __shared__ uint32_t lc_cnt[FILTER ? NQ : 1];
   __shared__ u64 lc_buf[FILTER ? NQ * kLdsSlots : 1];
   __shared__ float4 nstage[kScanThreads / 64][8];
@@ -349,7 +394,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   // Per-column constants live in registers for the whole scan: a global load
   // inside the tile loop would make every tile wait for the code prefetch
   // issued ahead of it (loads retire in order).
-  float al_r[NQG], ta_r[NQG];
+  float al_r[NQG], ta_r[NQG], lo_r[NQG];
   bool live_r[NQG];
 #pragma unroll
   for (int g = 0; g < NQG; ++g) {
@@ -357,6 +402,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     live_r[g] = qi < a.q;
     al_r[g] = live_r[g] ? a.alpha[qi] : 0.0f;
     ta_r[g] = (FILTER && live_r[g]) ? a.tau[qi] : __builtin_inff();
+    lo_r[g] = (HI && live_r[g]) ? a.lonorm[qi] : 0.0f;
   }
   // Pre-test thresholds of the filter. For tau > 0 and alpha > 0 a kept score
   // s = fl(fl(fl(D) a) n) >= tau implies D > 0, n > 0 and, with u = 2^-24,
@@ -391,8 +437,13 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   auto load_codes = [&](Stage& st, int jj) {
     load_tile_codes<NLOAD>(st.raw, packed, a.tile_begin + (long long)jj * a.tile_step, lane);
   };
+  // Lanes 0-31 load the tile's norms; with HI, lanes 32-63 load its tile_cn.
   auto load_norms = [&](Stage& st, int jj) {
-    st.nv = a.norms[(a.tile_begin + (long long)jj * a.tile_step) * kTile + (lane & 31)];
+    const long long t = a.tile_begin + (long long)jj * a.tile_step;
+    if constexpr (HI)
+      st.nv = lane < 32 ? a.norms[t * kTile + lane] : a.tile_cn[t];
+    else
+      st.nv = a.norms[t * kTile + (lane & 31)];
   };
   auto process = [&](const Stage& st, int j) {
     const v4i(&raw)[NLOAD] = st.raw;
@@ -401,9 +452,9 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     // letting them be hoisted into registers across the tile loop.
     int boff = lane;
     asm volatile("" : "+v"(boff));
-    v16i acc[NCB];
+    v16i acc[NCBU];
 #pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
+    for (int cb = 0; cb < NCBU; ++cb) acc[cb] = v16i{0};
 #pragma unroll
     for (int c = 0; c < NLOAD; ++c) {
 #pragma unroll
@@ -412,8 +463,8 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
         if (s < KS) {
           const v4i af = decode_step<BITS>(raw[c], h, a);
 #pragma unroll
-          for (int cb = 0; cb < NCB; ++cb) {
-            const v4i bf = sb[(s * NCB + cb) * 64 + boff];
+          for (int cb = 0; cb < NCBU; ++cb) {
+            const v4i bf = sb[(s * NCBU + cb) * 64 + boff];
             acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, acc[cb], 0, 0, 0);
           }
         }
@@ -442,6 +493,44 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     // Rows of this tile that are real vectors (the last tile may be partial).
     const long long rem64 = a.n - vbase;
     const int rem = rem64 >= kTile ? kTile : (int)rem64;
+    if constexpr (HI) {
+      const float cn = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(st.nv), 32));
+#pragma unroll
+      for (int g = 0; g < NQG; ++g) {
+        const int qi = g * 32 + (lane & 31);
+        const float lb = (lo_r[g] * cn) * 1.0000002f;  // >= lonorm * cn exactly
+        float p[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) p[i] = ((float)acc[g][i] * 256.0f + lb) * nrm[i];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = fmaxf(m, p[i]);
+        if (m >= pt_r[g]) {
+          uint32_t cnt = 0;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = 8 * (i >> 2) + 4 * half + (i & 3);
+            cnt += (r < rem && p[i] >= pt_r[g]) ? 1u : 0u;
+          }
+          uint32_t pos = atomicAdd(&lc_cnt[qi], cnt);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int r = 8 * (i >> 2) + 4 * half + (i & 3);
+            if (r < rem && p[i] >= pt_r[g]) {
+              const u64 key = (u64)(~(uint32_t)(vbase + r));  // id only; rescored later
+              if (pos < (uint32_t)kLdsSlots) {
+                lc_buf[qi * kLdsSlots + pos] = key;
+              } else {
+                const uint32_t gpos = atomicAdd(&a.cand_count[qi], 1u);
+                if ((int)gpos < a.cap) a.cand[(size_t)qi * a.cap + gpos] = key;
+              }
+              ++pos;
+            }
+          }
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int g = 0; g < NQG; ++g) {
       const int qi = g * 32 + (lane & 31);
@@ -524,7 +613,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   auto cl = [&](int jj) { return jj < nt ? jj : nt - 1; };
   // Three stages (codes two tiles ahead) when the ring and the accumulators
   // fit the 256 registers of two waves per SIMD; two stages otherwise.
-  constexpr bool kRing3 = NLOAD * 12 + NCB * 16 <= 168;
+  constexpr bool kRing3 = NLOAD * 12 + NCBU * 16 <= 168;
   // The first tiles are requested before the query fragments are staged, so
   // the two round trips overlap. Every wave reaches the barrier.
   Stage s0, s1, s2;
@@ -533,7 +622,28 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     load_norms(s0, j);
     if constexpr (kRing3) load_codes(s1, cl(j + nw));
   }
-  stage_fragments<kScanThreads, KS * NCB * 64>(sb, reinterpret_cast<const v4i*>(a.bfrag));
+  if constexpr (HI) {
+    // The high-half blocks only: block cb = 2 g of each K-step.
+    constexpr int COUNT = KS * NQG * 64;
+    constexpr int PER = (COUNT + kScanThreads - 1) / kScanThreads;
+    const v4i* src = reinterpret_cast<const v4i*>(a.bfrag);
+    v4i v[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int i = threadIdx.x + r * kScanThreads;
+      if (i < COUNT) {
+        const int st = i / (NQG * 64), g = (i / 64) % NQG, l = i % 64;
+        v[r] = src[(st * NCB + 2 * g) * 64 + l];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int i = threadIdx.x + r * kScanThreads;
+      if (i < COUNT) sb[i] = v[r];
+    }
+  } else {
+    stage_fragments<kScanThreads, KS * NCB * 64>(sb, reinterpret_cast<const v4i*>(a.bfrag));
+  }
   if (FILTER && threadIdx.x < NQ) lc_cnt[threadIdx.x] = 0u;
   __syncthreads();
   if (j < nt) {
@@ -592,6 +702,10 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) \
   void eos_tq_scan_b##BITS##_k##KS##_g##NQG##_w(TqScanArgs a) {                           \
     tq_scan_body<BITS, KS, NQG, false>(a);                                                \
+  }                                                                                       \
+  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) \
+  void eos_tq_scan_b##BITS##_k##KS##_g##NQG##_h(TqScanArgs a) {                           \
+    tq_scan_body<BITS, KS, NQG, true, true>(a);                                           \
   }
 
 #define EOS_TQ_SCAN_KS(BITS, NQG) \
@@ -609,6 +723,111 @@ EOS_TQ_SCAN_KS(2, 1)
 EOS_TQ_SCAN_KS(2, 2)
 EOS_TQ_SCAN(4, 32, 1)
 EOS_TQ_SCAN(2, 32, 1)
+
+// ----------------------------------------------------------------- rescore
+
+namespace {
+
+
+// Candidates of query blockIdx.x spread over gridDim.y workgroups, four
+// threads per id: thread s of the four decodes chunks s, s + 4, ... of the
+// id's code row (reference layout, rs 16-byte chunks). The list entry is read
+// first, then the code row, the norm and the query are requested together,
+// so the kernel waits two memory round trips. The partial dots are summed
+// over the four; the entry is rewritten in place with the exact rank key
+// when the exact score ((float)D * alpha) * norm + 0 reaches tau, else with 0
+// (below every rank key: finalize skips it). Dimension k of a row is at bit
+// k * BITS, low bits first.
+template <int BITS>
+EOS_DEV void rescore_body(const TqRescoreArgs& a) {
+  constexpr int kSlots = 8;                 // chunks per thread: rs <= 32
+  constexpr int kDims = 32 * 128 / BITS;    // dims of the longest row
+  constexpr int kQPer = kDims / 256;        // query values staged per thread
+  __shared__ int qsh[kDims];
+  const int q = blockIdx.x;
+  if (q >= a.q) return;
+  const int tid = threadIdx.x, sub = tid & 3;
+  const uint32_t cnt = a.cand_count[q];
+  if (cnt > (uint32_t)a.cap) return;  // overflowed: finalize flags it
+  const uint32_t first = blockIdx.y * 64u;
+  if (first >= cnt) return;
+  const int dims = a.rs * 128 / BITS;
+  const float al = a.alpha[q], ta = a.tau[q];
+  u64* list = a.cand + (size_t)q * a.cap;
+  for (uint32_t base = first; base < cnt; base += 64u * gridDim.y) {
+    // Entries are rewritten in place, so a lane past the end must not read
+    // another entry (it may already be 0): it scores vector 0 and writes
+    // nothing. An id outside the corpus is dropped without reading its row.
+    const uint32_t i = base + (uint32_t)(tid >> 2);
+    const bool in_list = i < cnt;
+    const uint32_t lid = in_list ? rank_id(list[i]) : 0u;
+    const bool live = in_list && (long long)lid < a.n;
+    const uint32_t id = live ? lid : 0u;
+    const v4i* row = reinterpret_cast<const v4i*>(a.codes + (size_t)id * a.rs * 16);
+    v4i r[kSlots];
+#pragma unroll
+    for (int u = 0; u < kSlots; ++u) {
+      const int c = sub + 4 * u;
+      r[u] = c < a.rs ? row[c] : v4i{0, 0, 0, 0};
+    }
+    const float nv = a.norms[id];
+    if (base == first) {
+      int qv[kQPer];
+#pragma unroll
+      for (int u = 0; u < kQPer; ++u) {
+        const int j = tid + 256 * u;
+        qv[u] = (j < dims && j < a.d) ? (int)a.qs[(size_t)q * a.d + j] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kQPer; ++u)
+        if (tid + 256 * u < dims) qsh[tid + 256 * u] = qv[u];
+      __syncthreads();
+    }
+    int D = 0;
+#pragma unroll
+    for (int u = 0; u < kSlots; ++u) {
+      const int c = sub + 4 * u;
+      if (c < a.rs) {
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {
+          const uint32_t w = (uint32_t)r[u][wi];
+          const int* qp = &qsh[(16 * c + 4 * wi) * (8 / BITS)];  // first dim of the dword
+          if constexpr (BITS == 4) {
+            // byte b holds dims 2b (low nibble) and 2b + 1
+            const uint32_t ev = lut16(w & 0x0f0f0f0fu, a.lut0, a.lut1, a.lut2, a.lut3);
+            const uint32_t od = lut16((w >> 4) & 0x0f0f0f0fu, a.lut0, a.lut1, a.lut2, a.lut3);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+              D += qp[2 * b] * (int)(int8_t)(ev >> (8 * b));
+              D += qp[2 * b + 1] * (int)(int8_t)(od >> (8 * b));
+            }
+          } else {
+            // byte b holds dims 4b + e, e = 0..3
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t v = __builtin_amdgcn_perm(0u, a.lut0, (w >> (2 * e)) & 0x03030303u);
+#pragma unroll
+              for (int b = 0; b < 4; ++b) D += qp[4 * b + e] * (int)(int8_t)(v >> (8 * b));
+            }
+          }
+        }
+      }
+    }
+    D += __shfl_xor(D, 1);
+    D += __shfl_xor(D, 2);
+    const float sc = ((float)D * al) * nv + 0.0f;
+    if (in_list && sub == 0) list[i] = (live && sc >= ta) ? rank_key(sc, id) : 0ull;
+  }
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void eos_tq_rescore_b4(TqRescoreArgs a) {
+  rescore_body<4>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void eos_tq_rescore_b2(TqRescoreArgs a) {
+  rescore_body<2>(a);
+}
 
 // ------------------------------------------------------------ row select
 
@@ -923,9 +1142,27 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
   }
   const int n = (int)cnt;
   const u64* src = a.cand + (size_t)row * a.cap;
-  for_each_batched<kFinThreads, 8>(src, n, [&](long long i, u64 v) { cbuf[i] = v; });
+  // Entries equal to 0 were dropped by the rescoring (below every rank key);
+  // the row is final only if at least kk entries remain.
+  uint32_t live = 0;
+  for_each_batched<kFinThreads, 8>(src, n, [&](long long i, u64 v) {
+    cbuf[i] = v;
+    live += v != 0ull ? 1u : 0u;
+  });
   if (tid == 0) sel_n = 0u;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) live += (uint32_t)__shfl_xor((int)live, o);
+  if ((tid & 63) == 0) scr[tid >> 6] = live;
   __syncthreads();
+  live = 0;
+#pragma unroll
+  for (int w = 0; w < kFinThreads / 64; ++w) live += scr[w];
+  __syncthreads();  // scr is reused by the selection
+  if (tid == 0) a.cand_count[row] = live;
+  if (live < (uint32_t)a.kk) {
+    if (tid == 0) a.status[row] = 1;
+    return;
+  }
   const uint32_t kk = (uint32_t)a.kk;
   uint32_t need, ne;
   const uint32_t K = block_select_desc<kFinThreads>(
