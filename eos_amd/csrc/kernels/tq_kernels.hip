@@ -287,7 +287,20 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_tile_cnorm(TqTileNormAr
   if (v < a.n) {
     const uint8_t* row = a.codes + (size_t)v * a.row_bytes;
     const uint32_t mask = (1u << a.bits) - 1u;
-    for (int k = 0; k < a.d; ++k) {
+    const int per = 32 / a.bits;  // codes per dword
+    int k = 0;
+    if ((a.row_bytes & 3) == 0) {
+      // Whole dwords: 8 (4-bit) or 16 (2-bit) codes per load.
+      const uint32_t* rw = reinterpret_cast<const uint32_t*>(row);
+      for (int w = 0; w < a.row_bytes / 4; ++w) {
+        const uint32_t x = rw[w];
+        for (int e = 0; e < per && k < a.d; ++e, ++k) {
+          const int c = a.cb[(x >> (e * a.bits)) & mask];
+          ss += (long long)(c * c);
+        }
+      }
+    }
+    for (; k < a.d; ++k) {
       const int bit = k * a.bits;
       const int c = a.cb[(row[bit >> 3] >> (bit & 7)) & mask];
       ss += (long long)(c * c);
