@@ -3,9 +3,9 @@
 // 101-197) on the runtime stream:
 //   eos_enc_pack        active positions -> contiguous rows per sequence
 //   eos_enc_embed       token + position + type, affine LayerNorm
-//   per layer:  eos_enc_gemm (QKV) -> eos_enc_attn_hd* -> eos_enc_gemm_ln_h*
-//               (O + residual + LN) -> eos_enc_gemm (FFN up + GELU) ->
-//               eos_enc_gemm_ln_h* (FFN down + residual + LN)
+//   per layer:  eos_enc_gemm_t* (QKV) -> eos_enc_attn_hd* -> eos_enc_gemm_t*
+//               (O + residual) -> eos_enc_ln -> eos_enc_gemm_t* (FFN up + GELU)
+//               -> eos_enc_gemm_t* (FFN down + residual) -> eos_enc_ln
 //   eos_enc_pool        masked mean pool + L2 normalize
 #include <algorithm>
 #include <cmath>
@@ -179,27 +179,39 @@ struct EosHipEncoder {
     em.eps = desc.ln_eps;
     em.mode = family;
     if (rt->launch("eos_enc_embed", dim3((max_rows + 3) / 4), dim3(256), 0, &em, err) != 0) return 1;
-    char ln_name[48];
-    snprintf(ln_name, sizeof(ln_name), "eos_enc_gemm_ln_h%d", H);
     char attn_name[48];
     snprintf(attn_name, sizeof(attn_name), "eos_enc_attn_hd%d", hd);
-    const unsigned mblocks = (unsigned)((max_rows + 127) / 128);
-    const unsigned lnblocks = (unsigned)((max_rows + 31) / 32);
+    // GEMM tiles: 256 x 128 for wide outputs, 128 x 128 for hidden-width ones
+    // (more workgroups for the smaller N).
+    auto gemm = [&](const uint16_t* A, const uint16_t* W, const float* sc, const float* b,
+                    uint16_t* out, const uint16_t* res, int n, int k, int epi, const char* label) {
+      const bool wide = n >= 1024;
+      const int bm = wide ? 256 : 128;
+      EncGemmArgs g{A, W, sc, b, out, total, res, max_rows, n, k, epi};
+      // One-dimensional grid: n / 128 column tiles for each row block, row
+      // blocks rounded up to a multiple of 8 (the kernel maps workgroups to
+      // tiles per XCD; tiles past the rows exit at once).
+      const unsigned mblk = (unsigned)(((max_rows + bm - 1) / bm + 7) / 8 * 8);
+      return rt->launch(wide ? "eos_enc_gemm_t256" : "eos_enc_gemm_t128",
+                        dim3((unsigned)(n / 128) * mblk), dim3(256), 0, &g, err, label);
+    };
+    auto layer_norm = [&](const float* gm, const float* bt) {
+      EncLnArgs l{h, gm, bt, total, max_rows, H, desc.ln_eps};
+      return rt->launch("eos_enc_ln", dim3((unsigned)((max_rows + 3) / 4)), dim3(256), 0, &l, err,
+                        "enc_ln");
+    };
     for (const DevLayer& L : layers) {
-      EncGemmArgs g{h, L.w_qkv, L.s_qkv, L.b_qkv, qkv, total, max_rows, 3 * H, H, 0};
-      if (rt->launch("eos_enc_gemm", dim3(3 * H / 128, mblocks), dim3(256), 0, &g, err, "enc_gemm_qkv") != 0)
+      if (gemm(h, L.w_qkv, L.s_qkv, L.b_qkv, qkv, nullptr, 3 * H, H, 0, "enc_gemm_qkv") != 0)
         return 1;
       EncAttnArgs at{qkv, ctx, seq_off, seq_cnt, batch, nh, H, tokens,
                      (float)(1.4426950408889634 / std::sqrt((double)hd))};
       if (rt->launch(attn_name, dim3((tokens + 127) / 128, nh, batch), dim3(256), 0, &at, err) != 0)
         return 1;
-      EncGemmLnArgs o{ctx, L.w_o, L.s_o, L.b_o, h, L.g1, L.be1, h, total, max_rows, H, desc.ln_eps};
-      if (rt->launch(ln_name, dim3(lnblocks), dim3(256), 0, &o, err, "enc_gemm_o_ln") != 0) return 1;
-      EncGemmArgs up{h, L.w_1, L.s_1, L.b_1, mid, total, max_rows, F, H, desc.gelu};
-      if (rt->launch("eos_enc_gemm", dim3(F / 128, mblocks), dim3(256), 0, &up, err, "enc_gemm_ffn_up") != 0)
-        return 1;
-      EncGemmLnArgs dn{mid, L.w_2, L.s_2, L.b_2, h, L.g2, L.be2, h, total, max_rows, F, desc.ln_eps};
-      if (rt->launch(ln_name, dim3(lnblocks), dim3(256), 0, &dn, err, "enc_gemm_ffn_down_ln") != 0)
+      if (gemm(ctx, L.w_o, L.s_o, L.b_o, h, h, H, H, 3, "enc_gemm_o") != 0 ||
+          layer_norm(L.g1, L.be1) != 0 ||
+          gemm(h, L.w_1, L.s_1, L.b_1, mid, nullptr, F, H, desc.gelu, "enc_gemm_ffn_up") != 0 ||
+          gemm(mid, L.w_2, L.s_2, L.b_2, h, h, H, F, 3, "enc_gemm_ffn_down") != 0 ||
+          layer_norm(L.g2, L.be2) != 0)
         return 1;
     }
     EncPoolArgs pl{h, seq_off, seq_cnt, d_out, proj, batch, H, family, out_dim()};

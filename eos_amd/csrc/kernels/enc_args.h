@@ -41,7 +41,8 @@ struct EncEmbedArgs {
 
 // out[m][n] = epi(scale[n] * sum_k a[m][k] w[n][k] + bias[n]) for m < *rows.
 // w holds int8 codes stored as f16 (exact), [n][k] (HF [out, in] layout).
-// epi: 0 identity, 1 erf GELU, 2 tanh GELU. Rows past *rows are skipped.
+// epi: 0 identity, 1 erf GELU, 2 tanh GELU, 3 + residual[m][n] (residual may
+// alias out). Rows past *rows are skipped.
 struct EncGemmArgs {
   const uint16_t* a;       // [rows][k] f16
   const uint16_t* w;       // [n][k] f16 codes
@@ -49,21 +50,17 @@ struct EncGemmArgs {
   const float* bias;       // [n]
   uint16_t* out;           // [rows][n] f16
   const int32_t* rows;     // device row count
+  const uint16_t* residual;  // epi 3: [rows][n] f16
   int max_rows, n, k, epi;
 };
 
-// out[m] = LayerNorm(scale * (a[m] w^T) + bias + residual[m]) (n == hidden).
-struct EncGemmLnArgs {
-  const uint16_t* a;       // [rows][k] f16
-  const uint16_t* w;       // [hidden][k] f16 codes
-  const float* wscale;
-  const float* bias;
-  const uint16_t* residual;  // [rows][hidden] f16
+// In-place affine LayerNorm of h [rows][hidden] f16 (hidden % 8 == 0, <= 1024).
+struct EncLnArgs {
+  uint16_t* h;
   const float* gamma;
   const float* beta;
-  uint16_t* out;           // [rows][hidden] f16 (may alias residual)
   const int32_t* rows;
-  int max_rows, k;
+  int max_rows, hidden;
   float eps;
 };
 

@@ -216,224 +216,223 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
 // ------------------------------------------------------------------- GEMM
 
 namespace {
-constexpr int kBM = 128, kBN = 128, kBK = 32, kPadK = kBK + 8;  // halves per LDS row
-}
+constexpr int kBK = 32, kPadK = kBK + 8;  // K chunk; halves per LDS row (padded)
 
-// 128 x 128 output tile per workgroup (4 wavefronts, 64 x 64 each = 2 x 2
-// MFMA 32x32 blocks), K in chunks of 32 staged through LDS with the next
-// chunk's global loads in flight during the current chunk's MFMAs.
-extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm(EncGemmArgs a) {
-  __shared__ uint16_t as[2][kBM * kPadK];
-  __shared__ uint16_t ws[2][kBN * kPadK];
+// Workgroup tile (64 WM) x (64 WN) over 4 wavefronts in a 2 x 2 grid, each
+// wavefront (32 WM) x (32 WN) = WM x WN MFMA 32x32 blocks. K advances in
+// chunks of 32 through a double-buffered LDS stage fed from two register
+// sets: chunk j is requested three chunk-steps before it is computed, so two
+// chunks of MFMAs cover each load. Per 16-wide K step a wavefront reads
+// WM + WN fragments from LDS for WM * WN MFMAs.
+// Epilogue: v = scale[n] * acc + bias[n]; mode 1 erf GELU, 2 tanh GELU,
+// 3 + residual[m][n] (out may alias residual: each element is read and
+// written by the same lane).
+template <int WM, int WN>
+EOS_DEV void gemm_body(const EncGemmArgs& a) {
+  constexpr int BM = 64 * WM, BN = 64 * WN;
+  constexpr int ACH = BM * kBK / 8 / 256;  // 16-byte chunks per thread
+  constexpr int WCH = BN * kBK / 8 / 256;
+  __shared__ uint16_t as[2][BM * kPadK];
+  __shared__ uint16_t ws[2][BN * kPadK];
   const int rows = *a.rows;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  // XCD-aware tile order: workgroup w runs on XCD w % 8 (round-robin
+  // dispatch), so XCD x takes row blocks x, x + 8, ... and walks all column
+  // tiles of a row block back to back: the block's A rows are fetched into
+  // that XCD's L2 once instead of once per column tile.
+  const int ntn = a.n / BN;
+  const int w = blockIdx.x, xcd = w & 7, l = w >> 3;
+  const int mb = xcd + 8 * (l / ntn), nb = l % ntn;
+  const int m0 = mb * BM, n0 = nb * BN;
   if (m0 >= rows) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int g = lane >> 5, l32 = lane & 31;
-  // global -> register staging: 2 x 16 B of A and of W per thread
-  v4i ra[2], rw[2];
-  auto gload = [&](int k0) {
+  // Per-thread source rows and columns of its 16-byte chunks (fixed over K).
+  const uint16_t* asrc[ACH];
+  const uint16_t* wsrc[WCH];
+  int aoff[ACH], woff[WCH];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int idx = tid + 256 * u;          // 512 chunks of 16 B
-      const int r = idx >> 2, c = (idx & 3) * 8;
-      const int am = min(m0 + r, a.max_rows - 1);
-      ra[u] = *reinterpret_cast<const v4i*>(a.a + (size_t)am * a.k + k0 + c);
-      rw[u] = *reinterpret_cast<const v4i*>(a.w + (size_t)(n0 + r) * a.k + k0 + c);
-    }
+  for (int u = 0; u < ACH; ++u) {
+    const int idx = tid + 256 * u;
+    const int r = idx >> 2, c = (idx & 3) * 8;
+    asrc[u] = a.a + (size_t)min(m0 + r, a.max_rows - 1) * a.k + c;
+    aoff[u] = r * kPadK + c;
+  }
+#pragma unroll
+  for (int u = 0; u < WCH; ++u) {
+    const int idx = tid + 256 * u;
+    const int r = idx >> 2, c = (idx & 3) * 8;
+    wsrc[u] = a.w + (size_t)(n0 + r) * a.k + c;
+    woff[u] = r * kPadK + c;
+  }
+  struct Set {
+    v4i ra[ACH], rw[WCH];
   };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int idx = tid + 256 * u;
-      const int r = idx >> 2, c = (idx & 3) * 8;
-      *reinterpret_cast<v4i*>(&as[buf][r * kPadK + c]) = ra[u];
-      *reinterpret_cast<v4i*>(&ws[buf][r * kPadK + c]) = rw[u];
-    }
-  };
-  v16f acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v16f{0};
   const int nk = a.k / kBK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kc = 0; kc < nk; ++kc) {
-    const int buf = kc & 1;
-    if (kc + 1 < nk) gload((kc + 1) * kBK);
+  // Chunks past the end are clamped to the last one (loaded, never stored).
+  auto gload = [&](Set& st, int kc) {
+    const int k0 = min(kc, nk - 1) * kBK;
+#pragma unroll
+    for (int u = 0; u < ACH; ++u) st.ra[u] = *reinterpret_cast<const v4i*>(asrc[u] + k0);
+#pragma unroll
+    for (int u = 0; u < WCH; ++u) st.rw[u] = *reinterpret_cast<const v4i*>(wsrc[u] + k0);
+  };
+  auto lstore = [&](const Set& st, int buf) {
+#pragma unroll
+    for (int u = 0; u < ACH; ++u) *reinterpret_cast<v4i*>(&as[buf][aoff[u]]) = st.ra[u];
+#pragma unroll
+    for (int u = 0; u < WCH; ++u) *reinterpret_cast<v4i*>(&ws[buf][woff[u]]) = st.rw[u];
+  };
+  v16f acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[i][j] = v16f{0};
+  auto compute = [&](int buf) {
 #pragma unroll
     for (int s = 0; s < kBK / 16; ++s) {
-      v8h af[2], bf[2];
+      v8h af[WM], bf[WN];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        af[i] = *reinterpret_cast<const v8h*>(&as[buf][(wm * 64 + i * 32 + l32) * kPadK + s * 16 + g * 8]);
-        bf[i] = *reinterpret_cast<const v8h*>(&ws[buf][(wn * 64 + i * 32 + l32) * kPadK + s * 16 + g * 8]);
-      }
+      for (int i = 0; i < WM; ++i)
+        af[i] = *reinterpret_cast<const v8h*>(
+            &as[buf][(wm * 32 * WM + i * 32 + l32) * kPadK + s * 16 + g * 8]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < WN; ++j)
+        bf[j] = *reinterpret_cast<const v8h*>(
+            &ws[buf][(wn * 32 * WN + j * 32 + l32) * kPadK + s * 16 + g * 8]);
+      // Operands swapped (W as the MFMA's first operand) so that a lane's
+      // results lie along an output row: see the epilogue.
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
     }
-    if (kc + 1 < nk) lstore(buf ^ 1);
+  };
+  // Set s0 carries chunks 0, 2, 4, ...; s1 chunks 1, 3, 5, ...
+  Set s0, s1;
+  gload(s0, 0);
+  gload(s1, 1);
+  lstore(s0, 0);
+  gload(s0, 2);
+  __syncthreads();
+  // nk is even (K is a multiple of 64): one back-edge, no exit in the body.
+  // The last pass stores clamped chunks that nothing reads.
+  for (int kc = 0; kc < nk; kc += 2) {
+    // chunk kc in LDS[0]; s1 holds chunk kc + 1; s0 receives chunk kc + 2.
+    compute(0);
+    lstore(s1, 1);
+    gload(s1, kc + 3);
+    __syncthreads();
+    compute(1);
+    lstore(s0, 0);
+    gload(s0, kc + 4);
     __syncthreads();
   }
-  // Epilogue: element e of lane (l32, g) is row 8(e/4) + 4g + e%4, column l32.
+  // With W as the first operand, element e of lane (l32, g) is output row
+  // l32 of the block and column 8(e/4) + 4g + e%4: each group of 4
+  // elements is 4 consecutive columns of one row, written as one 8-byte
+  // store (and the residual read as one 8-byte load).
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + wn * 64 + j * 32 + l32;
-    const float sc = a.wscale[col], bi = a.bias[col];
+  for (int i = 0; i < WM; ++i) {
+    const int row = m0 + wm * 32 * WM + i * 32 + l32;
+    if (row >= rows) continue;
+    uint16_t* orow = a.out + (size_t)row * a.n;
+    const uint16_t* rrow = a.residual != nullptr ? a.residual + (size_t)row * a.n : nullptr;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int j = 0; j < WN; ++j) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-        if (row < rows) {
-          float v = acc[i][j][e] * sc + bi;
-          if (a.epi != 0) v = gelu(v, a.epi);
-          a.out[(size_t)row * a.n + col] = f2h(v);
+      for (int q = 0; q < 4; ++q) {
+        const int col = n0 + wn * 32 * WN + j * 32 + 8 * q + 4 * g;
+        const float4 sc = *reinterpret_cast<const float4*>(a.wscale + col);
+        const float4 bi = *reinterpret_cast<const float4*>(a.bias + col);
+        float v[4] = {acc[i][j][4 * q] * sc.x + bi.x, acc[i][j][4 * q + 1] * sc.y + bi.y,
+                      acc[i][j][4 * q + 2] * sc.z + bi.z, acc[i][j][4 * q + 3] * sc.w + bi.w};
+        if (a.epi == 3) {
+          const v4h r = *reinterpret_cast<const v4h*>(rrow + col);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] += (float)r[t];
+        } else if (a.epi != 0) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = gelu(v[t], a.epi);
         }
+        v4h o;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t] = (_Float16)v[t];
+        *reinterpret_cast<v4h*>(orow + col) = o;
       }
     }
   }
 }
 
-// ------------------------------------------------------ GEMM + residual + LN
+}  // namespace
 
-namespace {
-constexpr int kLnBM = 32;
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_t128(EncGemmArgs a) {
+  gemm_body<2, 2>(a);
 }
-
-// 32 full rows per workgroup (4 wavefronts, each NT x 32 columns), then
-// bias + residual and a two-pass f32 LayerNorm over the row in LDS.
-template <int NT>
-EOS_DEV void gemm_ln_body(const EncGemmLnArgs& a) {
-  constexpr int H = 4 * NT * 32;
-  constexpr int kOutPad = H + 4;
-  constexpr int kStage = 2 * (kLnBM + H) * kPadK;  // halves
-  constexpr int kEpi = kLnBM * kOutPad * 2;         // halves (f32 tile)
-  __shared__ uint16_t smem[kStage > kEpi ? kStage : kEpi];
-  uint16_t* as0 = smem;
-  uint16_t* ws0 = smem + 2 * kLnBM * kPadK;
-  const int rows = *a.rows;
-  const int m0 = blockIdx.x * kLnBM;
-  if (m0 >= rows) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 5, l32 = lane & 31;
-  // chunks of 16 B: A 32 rows x 4 = 128, W H rows x 4
-  constexpr int kWChunks = H * 4;
-  constexpr int kWPer = (kWChunks + 255) / 256;
-  v4i ra, rw[kWPer];
-  auto gload = [&](int k0) {
-    if (tid < 128) {
-      const int r = tid >> 2, c = (tid & 3) * 8;
-      const int am = min(m0 + r, a.max_rows - 1);
-      ra = *reinterpret_cast<const v4i*>(a.a + (size_t)am * a.k + k0 + c);
-    }
-#pragma unroll
-    for (int u = 0; u < kWPer; ++u) {
-      const int idx = tid + 256 * u;
-      if (idx < kWChunks) {
-        const int r = idx >> 2, c = (idx & 3) * 8;
-        rw[u] = *reinterpret_cast<const v4i*>(a.w + (size_t)r * a.k + k0 + c);
-      }
-    }
-  };
-  auto lstore = [&](int buf) {
-    if (tid < 128) {
-      const int r = tid >> 2, c = (tid & 3) * 8;
-      *reinterpret_cast<v4i*>(&as0[buf * kLnBM * kPadK + r * kPadK + c]) = ra;
-    }
-#pragma unroll
-    for (int u = 0; u < kWPer; ++u) {
-      const int idx = tid + 256 * u;
-      if (idx < kWChunks) {
-        const int r = idx >> 2, c = (idx & 3) * 8;
-        *reinterpret_cast<v4i*>(&ws0[buf * H * kPadK + r * kPadK + c]) = rw[u];
-      }
-    }
-  };
-  v16f acc[NT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j) acc[j] = v16f{0};
-  const int nk = a.k / kBK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  for (int kc = 0; kc < nk; ++kc) {
-    const int buf = kc & 1;
-    if (kc + 1 < nk) gload((kc + 1) * kBK);
-#pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      const v8h af = *reinterpret_cast<const v8h*>(&as0[buf * kLnBM * kPadK + l32 * kPadK + s * 16 + g * 8]);
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const int ncol = wave * NT * 32 + j * 32 + l32;
-        const v8h bf = *reinterpret_cast<const v8h*>(&ws0[buf * H * kPadK + ncol * kPadK + s * 16 + g * 8]);
-        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[j], 0, 0, 0);
-      }
-    }
-    if (kc + 1 < nk) lstore(buf ^ 1);
-    __syncthreads();
-  }
-  // bias + residual into an f32 row tile in LDS (the staging space is free).
-  float* tile = reinterpret_cast<float*>(smem);
-#pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    const int col = wave * NT * 32 + j * 32 + l32;
-    const float sc = a.wscale[col], bi = a.bias[col];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int r = 8 * (e >> 2) + 4 * g + (e & 3);
-      const int row = min(m0 + r, rows - 1);
-      tile[r * kOutPad + col] = acc[j][e] * sc + bi + h2f(a.residual[(size_t)row * H + col]);
-    }
-  }
-  __syncthreads();
-  // LayerNorm: each wavefront normalizes 8 rows.
-  constexpr int PER = H / 64;
-  for (int rr = 0; rr < kLnBM / 4; ++rr) {
-    const int r = wave * (kLnBM / 4) + rr;
-    const int row = m0 + r;
-    float v[PER];
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      v[j] = tile[r * kOutPad + lane + 64 * j];
-      s += v[j];
-    }
-    const float mean = wave_sum(s) / (float)H;
-    float q = 0.f;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) q += (v[j] - mean) * (v[j] - mean);
-    const float inv = 1.0f / sqrtf(wave_sum(q) / (float)H + a.eps);
-    if (row < rows) {
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        const int c = lane + 64 * j;
-        a.out[(size_t)row * H + c] = f2h((v[j] - mean) * inv * a.gamma[c] + a.beta[c]);
-      }
-    }
-  }
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void eos_enc_gemm_t256(EncGemmArgs a) {
+  gemm_body<4, 2>(a);
 }
 
-extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h128(EncGemmLnArgs a) {
-  gemm_ln_body<1>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h256(EncGemmLnArgs a) {
-  gemm_ln_body<2>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h384(EncGemmLnArgs a) {
-  gemm_ln_body<3>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h512(EncGemmLnArgs a) {
-  gemm_ln_body<4>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_ln_h768(EncGemmLnArgs a) {
-  gemm_ln_body<6>(a);
+// ------------------------------------------------------------ LayerNorm
+
+// In-place affine LayerNorm of rows [0, *rows) of h [rows][hidden] (f16),
+// one wavefront per row: each lane holds up to two 8-column chunks in f32,
+// two-pass mean / variance over the row, out = (x - mean) / sqrt(var + eps)
+// * gamma + beta.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_ln(EncLnArgs a) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= *a.rows) return;
+  const int nch = a.hidden >> 3;  // 8-column chunks (hidden <= 1024)
+  uint16_t* rp = a.h + (size_t)row * a.hidden;
+  float x[2][8];
+  v4i raw[2];
+  float4 gb[2][4];  // gamma and beta of the lane's chunks, requested with the row
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int c = lane + 64 * t;
+    const int cc = c < nch ? c : 0;
+    raw[t] = c < nch ? *reinterpret_cast<const v4i*>(rp + 8 * c) : v4i{0, 0, 0, 0};
+    gb[t][0] = *reinterpret_cast<const float4*>(a.gamma + 8 * cc);
+    gb[t][1] = *reinterpret_cast<const float4*>(a.gamma + 8 * cc + 4);
+    gb[t][2] = *reinterpret_cast<const float4*>(a.beta + 8 * cc);
+    gb[t][3] = *reinterpret_cast<const float4*>(a.beta + 8 * cc + 4);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const v8h hv = __builtin_bit_cast(v8h, raw[t]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[t][e] = (float)hv[e];
+      s += x[t][e];
+    }
+  }
+  const float mean = wave_sum(s) / (float)a.hidden;
+  float q = 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (lane + 64 * t < nch) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q += (x[t][e] - mean) * (x[t][e] - mean);
+    }
+  }
+  const float inv = 1.0f / sqrtf(wave_sum(q) / (float)a.hidden + a.eps);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int c = lane + 64 * t;
+    if (c < nch) {
+      const float4 g0 = gb[t][0], g1 = gb[t][1], b0 = gb[t][2], b1 = gb[t][3];
+      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+      const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+      v8h o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (_Float16)((x[t][e] - mean) * inv * gg[e] + bb[e]);
+      *reinterpret_cast<v8h*>(rp + 8 * c) = o;
+    }
+  }
 }
 
 // --------------------------------------------------------------- attention
