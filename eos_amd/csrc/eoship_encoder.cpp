@@ -68,6 +68,7 @@ struct EosHipEncoder {
   size_t cap_rows = 0;
   int cap_batch = 0;
   uint16_t *h = nullptr, *qkv = nullptr, *ctx = nullptr, *mid = nullptr;
+  float* pool_part = nullptr;  // [batch][chunks][hidden] pool partial sums
   int32_t *row_b = nullptr, *row_t = nullptr, *seq_off = nullptr, *seq_cnt = nullptr;
   int32_t *total = nullptr, *status = nullptr;
   // host-API staging
@@ -77,7 +78,7 @@ struct EosHipEncoder {
   ~EosHipEncoder() {
     for (void* p : owned)
       if (p) hipFree(p);
-    void* act[] = {h, qkv, ctx, mid, row_b, row_t, seq_off, seq_cnt, total, status, io};
+    void* act[] = {h, qkv, ctx, mid, pool_part, row_b, row_t, seq_off, seq_cnt, total, status, io};
     for (void* p : act)
       if (p) hipFree(p);
   }
@@ -124,10 +125,11 @@ struct EosHipEncoder {
   int ensure_activations(int batch, int tokens, char** err) {
     const size_t rows = (size_t)batch * tokens;
     if (rows <= cap_rows && batch <= cap_batch) return 0;
-    void* act[] = {h, qkv, ctx, mid, row_b, row_t, seq_off, seq_cnt, total, status};
+    void* act[] = {h, qkv, ctx, mid, pool_part, row_b, row_t, seq_off, seq_cnt, total, status};
     for (void* p : act)
       if (p) hipFree(p);
     h = qkv = ctx = mid = nullptr;
+    pool_part = nullptr;
     row_b = row_t = seq_off = seq_cnt = total = status = nullptr;
     cap_rows = 0;
     cap_batch = 0;
@@ -136,6 +138,10 @@ struct EosHipEncoder {
         rt->alloc(rows * 3 * H * 2, reinterpret_cast<void**>(&qkv), err) ||
         rt->alloc(rows * H * 2, reinterpret_cast<void**>(&ctx), err) ||
         rt->alloc(rows * F * 2, reinterpret_cast<void**>(&mid), err) ||
+        // chunks of any later shape within the caps: batch' * ceil(tokens' /
+        // 256) <= rows / 256 + batch
+        rt->alloc((rows / kPoolChunk + (size_t)batch) * H * 4,
+                  reinterpret_cast<void**>(&pool_part), err) ||
         rt->alloc(rows * 4, reinterpret_cast<void**>(&row_b), err) ||
         rt->alloc(rows * 4, reinterpret_cast<void**>(&row_t), err) ||
         rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_off), err) ||
@@ -214,7 +220,11 @@ struct EosHipEncoder {
           layer_norm(L.g2, L.be2) != 0)
         return 1;
     }
-    EncPoolArgs pl{h, seq_off, seq_cnt, d_out, proj, batch, H, family, out_dim()};
+    const int nchunk = (tokens + kPoolChunk - 1) / kPoolChunk;
+    EncPoolArgs pl{h, seq_off, seq_cnt, d_out, proj, pool_part, batch, H, family, out_dim(), nchunk};
+    if (rt->launch("eos_enc_pool_part", dim3((unsigned)nchunk, (unsigned)batch), dim3(256), 0, &pl,
+                   err) != 0)
+      return 1;
     return rt->launch("eos_enc_pool", dim3(batch), dim3(1024), 0, &pl, err);
   }
 };

@@ -78,13 +78,17 @@ struct EncAttnArgs {
 // mode 0: masked mean pool, then L2 normalize -> out [batch][hidden].
 // mode 1: L2 normalize every row, masked mean pool, then (proj != NULL)
 //   times proj [hidden][odim] -> out [batch][odim] (odim = hidden without).
+// Two launches: eos_enc_pool_part (chunk partial sums into part) and
+// eos_enc_pool (chunk sums in order, mean, normalize or projection).
+constexpr int kPoolChunk = 64;   // rows per partial sum
 struct EncPoolArgs {
   const uint16_t* h;       // [rows][hidden] f16
   const int32_t* seq_off;
   const int32_t* seq_cnt;
   float* out;
   const float* proj;       // mode 1 only, [hidden][odim] f32, or NULL
-  int batch, hidden, mode, odim;
+  float* part;             // [batch][nchunk][hidden] f32 partial sums
+  int batch, hidden, mode, odim, nchunk;
 };
 
 // Tiny embed pipeline (examples/embed.eos): gather f16 table rows, multiply by

@@ -232,8 +232,8 @@ EOS_DEV void gemm_body(const EncGemmArgs& a) {
   constexpr int BM = 64 * WM, BN = 64 * WN;
   constexpr int ACH = BM * kBK / 8 / 256;  // 16-byte chunks per thread
   constexpr int WCH = BN * kBK / 8 / 256;
-  __shared__ uint16_t as[2][BM * kPadK];
-  __shared__ uint16_t ws[2][BN * kPadK];
+  __shared__ __attribute__((aligned(16))) uint16_t as[2][BM * kPadK];
+  __shared__ __attribute__((aligned(16))) uint16_t ws[2][BN * kPadK];
   const int rows = *a.rows;
   // XCD-aware tile order: workgroup w runs on XCD w % 8 (round-robin
   // dispatch), so XCD x takes row blocks x, x + 8, ... and walks all column
@@ -448,8 +448,10 @@ template <int HD>
 EOS_DEV void attn_body(const EncAttnArgs& a) {
   constexpr int KB = 32;                 // keys per block
   constexpr int QW = 32;                 // queries per wavefront
-  __shared__ uint16_t ks[KB * (HD + 8)];
-  __shared__ uint16_t vt[HD * (KB + 8)];
+  constexpr int NCH = KB * HD / 8;       // 8-half chunks of K (and of V) per block
+  constexpr int CPT = (NCH + 255) / 256; // chunks per thread
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][KB * (HD + 8)];
+  __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * (KB + 8)];
   const int b = blockIdx.z, h = blockIdx.y;
   const int cnt = a.seq_cnt[b];
   const int q0 = blockIdx.x * (4 * QW);
@@ -461,65 +463,106 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   const int qi = q0 + wave * QW + l32;           // this lane's query (column)
   const bool qlive = qi < cnt;
   // Q^T fragments (B operand): lane (query l32, group g) holds q[16s + 8g .. +7].
+  // Q is pre-scaled by log2(e) / sqrt(hd) (in f32, rounded once to f16), so
+  // the scores come out in the exp2 domain.
   v8h qf[HD / 16];
   {
     const uint16_t* qrow = a.qkv + (size_t)(off + (qlive ? qi : 0)) * ld + h * HD;
 #pragma unroll
-    for (int s = 0; s < HD / 16; ++s) qf[s] = *reinterpret_cast<const v8h*>(qrow + s * 16 + g * 8);
+    for (int s = 0; s < HD / 16; ++s) {
+      const v8h raw = *reinterpret_cast<const v8h*>(qrow + s * 16 + g * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] = (_Float16)((float)raw[e] * a.scale_log2);
+    }
   }
   v16f o[HD / 32];
 #pragma unroll
   for (int t = 0; t < HD / 32; ++t) o[t] = v16f{0};
   float mrun = -__builtin_inff(), lrun = 0.f;
-  for (int k0 = 0; k0 < cnt; k0 += KB) {
-    __syncthreads();
-    // stage K [key][HD] and V^T [HD][key] for keys k0..k0+31
-    for (int idx = tid; idx < KB * HD / 8; idx += 256) {
-      const int kr = idx / (HD / 8), c = (idx % (HD / 8)) * 8;
-      const int key = min(k0 + kr, cnt - 1);
-      const uint16_t* base = a.qkv + (size_t)(off + key) * ld + h * HD + c;
-      const v4i kv = *reinterpret_cast<const v4i*>(base + a.hidden);
-      const v4i vv = *reinterpret_cast<const v4i*>(base + 2 * a.hidden);
-      *reinterpret_cast<v4i*>(&ks[kr * (HD + 8) + c]) = kv;
-      const uint16_t* vh = reinterpret_cast<const uint16_t*>(&vv);
+  // K [key][HD] and V^T [HD][key] of a 32-key block are staged in LDS from
+  // registers; the next block's rows are requested before the current
+  // block's MFMAs (double-buffered, one barrier per block).
+  v4i kreg[CPT], vreg[CPT];
+  auto kv_load = [&](int k0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) vt[(c + e) * (KB + 8) + kr] = vh[e];
+    for (int u = 0; u < CPT; ++u) {
+      const int idx = tid + 256 * u;
+      if (idx < NCH) {
+        const int kr = idx / (HD / 8), c = (idx % (HD / 8)) * 8;
+        const int key = min(k0 + kr, cnt - 1);
+        const uint16_t* base = a.qkv + (size_t)(off + key) * ld + h * HD + c;
+        kreg[u] = *reinterpret_cast<const v4i*>(base + a.hidden);
+        vreg[u] = *reinterpret_cast<const v4i*>(base + 2 * a.hidden);
+      }
     }
-    __syncthreads();
+  };
+  auto kv_store = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int idx = tid + 256 * u;
+      if (idx < NCH) {
+        const int kr = idx / (HD / 8), c = (idx % (HD / 8)) * 8;
+        *reinterpret_cast<v4i*>(&ks[buf][kr * (HD + 8) + c]) = kreg[u];
+        // Key kr = 16 st + 8 hh + 4 gg + j is stored at 16 st + 8 gg + 4 hh + j,
+        // so the 8 keys a lane's P fragment covers are 16 contiguous bytes.
+        const int pos = (kr & 16) | ((kr & 4) << 1) | ((kr & 8) >> 1) | (kr & 3);
+        const uint16_t* vh = reinterpret_cast<const uint16_t*>(&vreg[u]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vt[buf][(c + e) * (KB + 8) + pos] = vh[e];
+      }
+    }
+  };
+  kv_load(0);
+  kv_store(0);
+  __syncthreads();
+  int buf = 0;
+  for (int k0 = 0; k0 < cnt; k0 += KB, buf ^= 1) {
+    const bool more = k0 + KB < cnt;
+    if (more) kv_load(k0 + KB);
     // S^T (32 keys x 32 queries)
     v16f s = v16f{0};
 #pragma unroll
     for (int st = 0; st < HD / 16; ++st) {
-      const v8h kf = *reinterpret_cast<const v8h*>(&ks[l32 * (HD + 8) + st * 16 + g * 8]);
+      const v8h kf = *reinterpret_cast<const v8h*>(&ks[buf][l32 * (HD + 8) + st * 16 + g * 8]);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s, 0, 0, 0);
     }
-    // element e is key k0 + 8(e/4) + 4g + e%4
+    // element e is key k0 + 8(e/4) + 4g + e%4; only the last block of the
+    // sequence has keys past its end (masked to -inf).
     float mloc = -__builtin_inff();
+    if (k0 + KB <= cnt) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
-      s[e] = key < cnt ? s[e] * a.scale_log2 : -__builtin_inff();
-      mloc = fmaxf(mloc, s[e]);
+      for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
+        s[e] = key < cnt ? s[e] : -__builtin_inff();
+        mloc = fmaxf(mloc, s[e]);
+      }
     }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
     const float mnew = fmaxf(mrun, mloc);
-    const float corr = exp2f(mrun - mnew);
+    // v_exp_f32 directly: every argument is <= 0 or -inf (exp2 -> 0).
+    const float corr = __builtin_amdgcn_exp2f(mrun - mnew);
     float psum = 0.f;
     v8h pf[2];
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float p = exp2f(s[e] - mnew);
+      const float p = __builtin_amdgcn_exp2f(s[e] - mnew);
       psum += p;
       pf[e >> 3][e & 7] = (_Float16)p;
     }
     psum += __shfl_xor(psum, 32);
     lrun = lrun * corr + psum;
-    mrun = mnew;
+    // The running output needs rescaling only when some lane's maximum grew.
+    if (__ballot(mnew != mrun) != 0ull) {
 #pragma unroll
-    for (int t = 0; t < HD / 32; ++t) {
+      for (int t = 0; t < HD / 32; ++t) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[t][e] *= corr;
+        for (int e = 0; e < 16; ++e) o[t][e] *= corr;
+      }
     }
+    mrun = mnew;
     // O^T += V^T P^T. K step st covers the keys this lane's P holds for
     // e in [8 st, 8 st + 8): 16 st + {4g..4g+3} and 16 st + 8 + {4g..4g+3}.
 #pragma unroll
@@ -527,15 +570,13 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
       const int d = t * 32 + l32;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
-        const uint16_t* vr = &vt[d * (KB + 8) + 16 * st + 4 * g];
-        v8h vf;
-        const v4h lo = *reinterpret_cast<const v4h*>(vr);
-        const v4h hi = *reinterpret_cast<const v4h*>(vr + 8);
-        vf[0] = lo[0]; vf[1] = lo[1]; vf[2] = lo[2]; vf[3] = lo[3];
-        vf[4] = hi[0]; vf[5] = hi[1]; vf[6] = hi[2]; vf[7] = hi[3];
+        const v8h vf = *reinterpret_cast<const v8h*>(&vt[buf][d * (KB + 8) + 16 * st + 8 * g]);
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[st], o[t], 0, 0, 0);
       }
     }
+    // The other buffer was last read before the previous barrier.
+    if (more) kv_store(buf ^ 1);
+    __syncthreads();
   }
   if (!qlive) return;
   const float inv = lrun > 0.f ? 1.0f / lrun : 0.f;
@@ -562,116 +603,118 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd128(EncAttnArgs
 
 // ------------------------------------------------------------------- pool
 
-// mode 0 (BERT, bert_embedder_ops.go:179-192): masked mean pool then L2
-// normalize (rows of norm 0 unchanged). mode 1 (compact family,
-// models/default_embedding.go:496-505): L2 normalize every row, masked mean
-// pool, then the optional output projection. One
-// workgroup of 16 wavefronts per sequence: wavefront w sums rows w, w+16, ...
-// in f32 (lane owns columns lane + 64 j), the 16 partial sums are added in
-// wavefront order, times 1/count.
-extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
-  // One workgroup per sequence; each lane sums 8 consecutive columns of a row
-  // per 16-byte load (hidden <= 1024: up to two 512-column segments), and
-  // each wave keeps 8 rows' loads in flight before accumulating them.
-  constexpr int kWaves = 16, kRows = 8;
-  __shared__ float part[kWaves * 1024];
-  __shared__ float red[kWaves];
-  const int b = blockIdx.x;
+// Partial sums of the masked mean pool: workgroup (c, b) sums rows
+// [64 c, 64 c + 64) of sequence b (mode 1 normalizes each row first:
+// x / ||x||, rows of norm 0 kept) into part[b][c][hidden] (f32). Each lane
+// covers 8 consecutive columns per 16-byte load (hidden <= 1024: up to two
+// 512-column segments); wavefront w sums rows w, w + 4, ... with 8 rows'
+// loads in flight, and the 4 wavefront sums are added in wavefront order.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_pool_part(EncPoolArgs a) {
+  constexpr int kRows = 8;
+  __shared__ float wsum[4][1024];
+  const int c = blockIdx.x, b = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int off = a.seq_off[b], cnt = a.seq_cnt[b];
+  const int r_begin = c * kPoolChunk;
+  if (r_begin >= cnt && c > 0) return;
+  const int r_end = min(r_begin + kPoolChunk, cnt);
   float s[2][8];
 #pragma unroll
-  for (int g = 0; g < 2; ++g)
+  for (int gg = 0; gg < 2; ++gg)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s[g][e] = 0.f;
-  for (int r0 = w * kRows; r0 < cnt; r0 += kWaves * kRows) {
+    for (int e = 0; e < 8; ++e) s[gg][e] = 0.f;
+  for (int r0 = r_begin + w * kRows; r0 < r_end; r0 += 4 * kRows) {
     v4i v[kRows][2];
 #pragma unroll
     for (int u = 0; u < kRows; ++u) {
-      const int r = min(r0 + u, cnt - 1);
+      const int r = min(r0 + u, r_end - 1);
       const uint16_t* row = a.h + (size_t)(off + r) * a.hidden;
 #pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const int c = g * 512 + lane * 8;
-        v[u][g] = c < a.hidden ? *reinterpret_cast<const v4i*>(row + c) : v4i{0, 0, 0, 0};
+      for (int gg = 0; gg < 2; ++gg) {
+        const int col = gg * 512 + lane * 8;
+        v[u][gg] = col < a.hidden ? *reinterpret_cast<const v4i*>(row + col) : v4i{0, 0, 0, 0};
       }
-    }
-    if (a.mode == 1) {
-      // Each row is L2-normalized first (x / ||x||, rows of norm 0 kept).
-#pragma unroll
-      for (int u = 0; u < kRows; ++u) {
-        float x[2][8];
-        float q = 0.f;
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          const v8h hv = __builtin_bit_cast(v8h, v[u][g]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            x[g][e] = (float)hv[e];
-            q += x[g][e] * x[g][e];
-          }
-        }
-        const float norm = sqrtf(wave_sum(q));
-        if (r0 + u < cnt) {
-#pragma unroll
-          for (int g = 0; g < 2; ++g)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) s[g][e] += norm > 0.f ? x[g][e] / norm : x[g][e];
-        }
-      }
-      continue;
     }
 #pragma unroll
     for (int u = 0; u < kRows; ++u) {
-      if (r0 + u < cnt) {
+      float x[2][8];
+      float q = 0.f;
 #pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          const v8h hv = __builtin_bit_cast(v8h, v[u][g]);
+      for (int gg = 0; gg < 2; ++gg) {
+        const v8h hv = __builtin_bit_cast(v8h, v[u][gg]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) s[g][e] += (float)hv[e];
+        for (int e = 0; e < 8; ++e) {
+          x[gg][e] = (float)hv[e];
+          q += x[gg][e] * x[gg][e];
         }
+      }
+      float scale = 1.0f;
+      if (a.mode == 1) {
+        const float norm = sqrtf(wave_sum(q));
+        scale = norm > 0.f ? norm : 1.0f;
+      }
+      if (r0 + u < r_end) {
+#pragma unroll
+        for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s[gg][e] += a.mode == 1 ? x[gg][e] / scale : x[gg][e];
       }
     }
   }
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const int c = g * 512 + lane * 8;
-    if (c < a.hidden) {
+  for (int gg = 0; gg < 2; ++gg) {
+    const int col = gg * 512 + lane * 8;
+    if (col < a.hidden) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part[w * 1024 + c + e] = s[g][e];
+      for (int e = 0; e < 8; ++e) wsum[w][col + e] = s[gg][e];
     }
   }
   __syncthreads();
+  float* dst = a.part + ((size_t)b * a.nchunk + c) * a.hidden;
+  for (int col = tid; col < a.hidden; col += 256)
+    dst[col] = ((wsum[0][col] + wsum[1][col]) + wsum[2][col]) + wsum[3][col];
+}
+
+// Pool finalize, one workgroup per sequence: the chunk partials added in
+// chunk order, times 1/count (count 0 -> zeros). mode 0 (BERT,
+// bert_embedder_ops.go:179-192): then L2 normalize (norm 0 kept). mode 1
+// (compact family, models/default_embedding.go:496-505): the rows were
+// normalized before pooling; then the optional output projection
+// (pool(X) P equals pool(X P) up to f32 rounding, at 1/count of the work).
+extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
+  __shared__ float pooled[1024];
+  __shared__ float red[16];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int cnt = a.seq_cnt[b];
+  const int nc = cnt > 0 ? (cnt + kPoolChunk - 1) / kPoolChunk : 0;
   float v = 0.f;
-  const int c = tid;
-  if (c < a.hidden) {
-    for (int i = 0; i < kWaves; ++i) v += part[i * 1024 + c];
+  if (tid < a.hidden) {
+    const float* src = a.part + (size_t)b * a.nchunk * a.hidden + tid;
+    for (int c = 0; c < nc; ++c) v += src[(size_t)c * a.hidden];
     v = cnt > 0 ? v * (1.0f / (float)cnt) : 0.f;
   }
   if (a.mode == 1) {
     if (a.proj == nullptr) {
-      if (c < a.hidden) a.out[(size_t)b * a.hidden + c] = v;
+      if (tid < a.hidden) a.out[(size_t)b * a.hidden + tid] = v;
       return;
     }
-    // Output projection of the pooled row: pool(X) P equals pool(X P) up to
-    // f32 rounding, at 1/count of the work.
-    __syncthreads();
-    if (c < a.hidden) part[c] = v;
+    if (tid < a.hidden) pooled[tid] = v;
     __syncthreads();
     for (int o = tid; o < a.odim; o += 1024) {
       float acc = 0.f;
-      for (int d = 0; d < a.hidden; ++d) acc += part[d] * a.proj[(size_t)d * a.odim + o];
+      for (int d = 0; d < a.hidden; ++d) acc += pooled[d] * a.proj[(size_t)d * a.odim + o];
       a.out[(size_t)b * a.odim + o] = acc;
     }
     return;
   }
-  const float ss = wave_sum(c < a.hidden ? v * v : 0.f);
+  const float ss = wave_sum(tid < a.hidden ? v * v : 0.f);
   if (lane == 0) red[w] = ss;
   __syncthreads();
   float tot = 0.f;
-  for (int i = 0; i < kWaves; ++i) tot += red[i];
+  for (int i = 0; i < 16; ++i) tot += red[i];
   const float norm = sqrtf(tot);
-  if (c < a.hidden) a.out[(size_t)b * a.hidden + c] = norm > 0.f ? v / norm : v;
+  if (tid < a.hidden) a.out[(size_t)b * a.hidden + tid] = norm > 0.f ? v / norm : v;
 }
 
 // ------------------------------------------------------------- tiny embed
