@@ -69,6 +69,10 @@ struct EosHipEncoder {
   int cap_batch = 0;
   uint16_t *h = nullptr, *qkv = nullptr, *ctx = nullptr, *mid = nullptr;
   float* pool_part = nullptr;  // [batch][chunks][hidden] pool partial sums
+  // V of the QKV projection, feature-major [hidden][vt_ld] (zeroed padding
+  // past the rows, so attention may read whole 16-byte key groups)
+  uint16_t* vt = nullptr;
+  int vt_ld = 0;
   int32_t *row_b = nullptr, *row_t = nullptr, *seq_off = nullptr, *seq_cnt = nullptr;
   int32_t *total = nullptr, *status = nullptr;
   // host-API staging
@@ -78,7 +82,7 @@ struct EosHipEncoder {
   ~EosHipEncoder() {
     for (void* p : owned)
       if (p) hipFree(p);
-    void* act[] = {h, qkv, ctx, mid, pool_part, row_b, row_t, seq_off, seq_cnt, total, status, io};
+    void* act[] = {h, qkv, ctx, mid, pool_part, vt, row_b, row_t, seq_off, seq_cnt, total, status, io};
     for (void* p : act)
       if (p) hipFree(p);
   }
@@ -122,14 +126,19 @@ struct EosHipEncoder {
 
   int out_dim() const { return family == 1 ? odim : desc.hidden; }
 
+  // Packed rows: each sequence starts at a multiple of 8, so a batch needs up
+  // to batch * (tokens + 7) rows.
+  static size_t row_capacity(int batch, int tokens) { return (size_t)batch * (tokens + 7); }
+
   int ensure_activations(int batch, int tokens, char** err) {
-    const size_t rows = (size_t)batch * tokens;
+    const size_t rows = row_capacity(batch, tokens);
     if (rows <= cap_rows && batch <= cap_batch) return 0;
-    void* act[] = {h, qkv, ctx, mid, pool_part, row_b, row_t, seq_off, seq_cnt, total, status};
+    void* act[] = {h, qkv, ctx, mid, pool_part, vt, row_b, row_t, seq_off, seq_cnt, total, status};
     for (void* p : act)
       if (p) hipFree(p);
     h = qkv = ctx = mid = nullptr;
     pool_part = nullptr;
+    vt = nullptr;
     row_b = row_t = seq_off = seq_cnt = total = status = nullptr;
     cap_rows = 0;
     cap_batch = 0;
@@ -149,6 +158,10 @@ struct EosHipEncoder {
         rt->alloc(4, reinterpret_cast<void**>(&total), err) ||
         rt->alloc(4, reinterpret_cast<void**>(&status), err))
       return 1;
+    vt_ld = (int)((rows + 7) / 8 * 8 + 32);
+    if (rt->alloc((size_t)H * vt_ld * 2, reinterpret_cast<void**>(&vt), err)) return 1;
+    hipError_t e = hipMemset(vt, 0, (size_t)H * vt_ld * 2);
+    if (e != hipSuccess) return hip_err(err, "hipMemset(vt)", e);
     cap_rows = rows;
     cap_batch = batch;
     return 0;
@@ -158,11 +171,13 @@ struct EosHipEncoder {
               int tokens, float* d_out, char** err) {
     if (ensure_activations(batch, tokens, err) != 0) return 1;
     const int H = desc.hidden, F = desc.intermediate, nh = desc.heads, hd = H / nh;
-    const int max_rows = batch * tokens;
+    const int max_rows = (int)row_capacity(batch, tokens);
     hipError_t e = hipMemsetAsync(status, 0, 4, rt->stream);
     if (e != hipSuccess) return hip_err(err, "hipMemsetAsync(status)", e);
     EncPackArgs pk{d_mask, row_b, row_t, seq_off, seq_cnt, total, batch, tokens};
-    if (rt->launch("eos_enc_pack", dim3(batch), dim3(256), 0, &pk, err) != 0) return 1;
+    if (rt->launch("eos_enc_count", dim3(batch), dim3(256), 0, &pk, err) != 0 ||
+        rt->launch("eos_enc_pack", dim3(batch), dim3(256), 0, &pk, err) != 0)
+      return 1;
     EncEmbedArgs em;
     memset(&em, 0, sizeof(em));
     em.ids = d_ids;
@@ -190,10 +205,11 @@ struct EosHipEncoder {
     // GEMM tiles: 256 x 128 for wide outputs, 128 x 128 for hidden-width ones
     // (more workgroups for the smaller N).
     auto gemm = [&](const uint16_t* A, const uint16_t* W, const float* sc, const float* b,
-                    uint16_t* out, const uint16_t* res, int n, int k, int epi, const char* label) {
+                    uint16_t* out, const uint16_t* res, int n, int k, int epi, const char* label,
+                    uint16_t* vt_out = nullptr) {
       const bool wide = n >= 1024;
       const int bm = wide ? 256 : 128;
-      EncGemmArgs g{A, W, sc, b, out, total, res, max_rows, n, k, epi};
+      EncGemmArgs g{A, W, sc, b, out, total, res, max_rows, n, k, epi, vt_out, 2 * H, vt_ld};
       // One-dimensional grid: n / 128 column tiles for each row block, row
       // blocks rounded up to a multiple of 8 (the kernel maps workgroups to
       // tiles per XCD; tiles past the rows exit at once).
@@ -207,9 +223,10 @@ struct EosHipEncoder {
                         "enc_ln");
     };
     for (const DevLayer& L : layers) {
-      if (gemm(h, L.w_qkv, L.s_qkv, L.b_qkv, qkv, nullptr, 3 * H, H, 0, "enc_gemm_qkv") != 0)
+      // Q and K rows into qkv, V feature-major into vt.
+      if (gemm(h, L.w_qkv, L.s_qkv, L.b_qkv, qkv, nullptr, 3 * H, H, 0, "enc_gemm_qkv", vt) != 0)
         return 1;
-      EncAttnArgs at{qkv, ctx, seq_off, seq_cnt, batch, nh, H, tokens,
+      EncAttnArgs at{qkv, vt, ctx, seq_off, seq_cnt, batch, nh, H, tokens, vt_ld,
                      (float)(1.4426950408889634 / std::sqrt((double)hd))};
       if (rt->launch(attn_name, dim3((tokens + 127) / 128, nh, batch), dim3(256), 0, &at, err) != 0)
         return 1;

@@ -52,6 +52,8 @@ struct EncGemmArgs {
   const int32_t* rows;     // device row count
   const uint16_t* residual;  // epi 3: [rows][n] f16
   int max_rows, n, k, epi;
+  uint16_t* vt;            // optional: columns >= vt_col0 go to vt[col - vt_col0][row]
+  int vt_col0, vt_ld;      // (vt rows hold vt_ld entries, the first max_rows rounded up to 4 + 32 padding)
 };
 
 // In-place affine LayerNorm of h [rows][hidden] f16 (hidden % 8 == 0, <= 1024).
@@ -67,11 +69,12 @@ struct EncLnArgs {
 // Masked multi-head attention over packed rows: every active row of a
 // sequence attends to every active row of the same sequence.
 struct EncAttnArgs {
-  const uint16_t* qkv;     // [rows][3*hidden] f16: q | k | v, head-major
+  const uint16_t* qkv;     // [rows][3*hidden] f16: q | k (| v unused), head-major
+  const uint16_t* vt;      // [hidden][vt_ld] f16: V transposed (feature-major)
   uint16_t* ctx;           // [rows][hidden] f16
   const int32_t* seq_off;
   const int32_t* seq_cnt;
-  int batch, heads, hidden, max_len;
+  int batch, heads, hidden, max_len, vt_ld;
   float scale_log2;        // log2(e) / sqrt(head_dim)
 };
 

@@ -75,31 +75,43 @@ EOS_DEV int block_exclusive_scan256(int v, int* scr, int* total) {
 
 }  // namespace
 
-// One workgroup per sequence: its offset is the number of active positions
-// of the sequences before it; positions are compacted in increasing order.
-// Thread i owns the contiguous positions [i * per, (i + 1) * per); mask
-// values are read 8 per thread at a time so the loads overlap.
+// Active positions per sequence: one workgroup per sequence, mask values
+// read 8 per thread at a time so the loads overlap.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_count(EncPackArgs a) {
+  __shared__ int scr[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int32_t* m = a.mask + (size_t)b * a.tokens;
+  int mine = 0;
+  for (int base = tid; base < a.tokens; base += 256 * 8) {
+    int v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int t = base + 256 * u;
+      v[u] = t < a.tokens ? m[t] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mine += v[u] != 0 ? 1 : 0;
+  }
+  int total = 0;
+  (void)block_exclusive_scan256(mine, scr, &total);
+  if (tid == 0) a.seq_cnt[b] = total;
+}
+
+// One workgroup per sequence: rows of sequence b start at the sum of the
+// earlier sequences' counts, each rounded up to a multiple of 8 (so every
+// sequence starts 16-byte aligned in feature-major copies); its positions
+// are compacted in increasing order, and the rows up to the next multiple
+// of 8 are pad rows (position -1). Thread i owns the contiguous positions
+// [i * per, (i + 1) * per). The last workgroup writes the row total.
 extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
   __shared__ int scr[4];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
-  // Active positions of the sequences before b.
-  const long long nb = (long long)b * a.tokens;
   int before = 0;
-  for (long long base = tid; base < nb; base += 256LL * 8) {
-    int v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const long long i = base + 256LL * u;
-      v[u] = a.mask[i < nb ? i : 0];
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) before += (base + 256LL * u < nb && v[u] != 0) ? 1 : 0;
-  }
+  for (int i = tid; i < b; i += 256) before += (a.seq_cnt[i] + 7) & ~7;
   int seq_base = 0;
   (void)block_exclusive_scan256(before, scr, &seq_base);
-  // This sequence: count per thread, scan, then write rows in order.
-  const int32_t* m = a.mask + nb;
+  const int32_t* m = a.mask + (size_t)b * a.tokens;
   const int per = (a.tokens + 255) / 256;
   const int t0 = tid * per;
   int mine = 0;
@@ -131,10 +143,14 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
       }
     }
   }
+  const int padded = (seq_cnt + 7) & ~7;
+  if (tid < padded - seq_cnt) {
+    a.row_b[seq_base + seq_cnt + tid] = b;
+    a.row_t[seq_base + seq_cnt + tid] = -1;
+  }
   if (tid == 0) {
     a.seq_off[b] = seq_base;
-    a.seq_cnt[b] = seq_cnt;
-    if (b == a.batch - 1) *a.total = seq_base + seq_cnt;
+    if (b == a.batch - 1) *a.total = seq_base + padded;
   }
 }
 
@@ -147,6 +163,11 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
   const int lane = threadIdx.x & 63;
   if (row >= *a.total) return;
   const int b = a.row_b[row], t = a.row_t[row];
+  if (t < 0) {
+    // Pad row (sequence alignment): zeros, never pooled or attended to.
+    for (int c = lane; c < a.hidden; c += 64) a.out[(size_t)row * a.hidden + c] = 0;
+    return;
+  }
   int id = a.ids[(size_t)b * a.tokens + t];
   int ty = a.type_ids ? a.type_ids[(size_t)b * a.tokens + t] : 0;
   const int pos = t;
@@ -227,23 +248,18 @@ constexpr int kBK = 32, kPadK = kBK + 8;  // K chunk; halves per LDS row (padded
 // Epilogue: v = scale[n] * acc + bias[n]; mode 1 erf GELU, 2 tanh GELU,
 // 3 + residual[m][n] (out may alias residual: each element is read and
 // written by the same lane).
-template <int WM, int WN>
-EOS_DEV void gemm_body(const EncGemmArgs& a) {
+// TR = false: W is the MFMA's first operand, a lane's results lie along an
+// output row (row-major out). TR = true (columns from vt_col0 on, when vt is
+// given): A first, a lane's results lie along an output column, stored
+// transposed into vt[col - vt_col0][row].
+template <int WM, int WN, bool TR>
+EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t* as0,
+                       uint16_t* ws0) {
   constexpr int BM = 64 * WM, BN = 64 * WN;
   constexpr int ACH = BM * kBK / 8 / 256;  // 16-byte chunks per thread
   constexpr int WCH = BN * kBK / 8 / 256;
-  __shared__ __attribute__((aligned(16))) uint16_t as[2][BM * kPadK];
-  __shared__ __attribute__((aligned(16))) uint16_t ws[2][BN * kPadK];
-  const int rows = *a.rows;
-  // XCD-aware tile order: workgroup w runs on XCD w % 8 (round-robin
-  // dispatch), so XCD x takes row blocks x, x + 8, ... and walks all column
-  // tiles of a row block back to back: the block's A rows are fetched into
-  // that XCD's L2 once instead of once per column tile.
-  const int ntn = a.n / BN;
-  const int w = blockIdx.x, xcd = w & 7, l = w >> 3;
-  const int mb = xcd + 8 * (l / ntn), nb = l % ntn;
-  const int m0 = mb * BM, n0 = nb * BN;
-  if (m0 >= rows) return;
+  auto as = [&](int buf) { return as0 + buf * BM * kPadK; };
+  auto ws = [&](int buf) { return ws0 + buf * BN * kPadK; };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int g = lane >> 5, l32 = lane & 31;
@@ -279,9 +295,9 @@ EOS_DEV void gemm_body(const EncGemmArgs& a) {
   };
   auto lstore = [&](const Set& st, int buf) {
 #pragma unroll
-    for (int u = 0; u < ACH; ++u) *reinterpret_cast<v4i*>(&as[buf][aoff[u]]) = st.ra[u];
+    for (int u = 0; u < ACH; ++u) *reinterpret_cast<v4i*>(as(buf) + aoff[u]) = st.ra[u];
 #pragma unroll
-    for (int u = 0; u < WCH; ++u) *reinterpret_cast<v4i*>(&ws[buf][woff[u]]) = st.rw[u];
+    for (int u = 0; u < WCH; ++u) *reinterpret_cast<v4i*>(ws(buf) + woff[u]) = st.rw[u];
   };
   v16f acc[WM][WN];
 #pragma unroll
@@ -295,18 +311,20 @@ EOS_DEV void gemm_body(const EncGemmArgs& a) {
 #pragma unroll
       for (int i = 0; i < WM; ++i)
         af[i] = *reinterpret_cast<const v8h*>(
-            &as[buf][(wm * 32 * WM + i * 32 + l32) * kPadK + s * 16 + g * 8]);
+            as(buf) + (wm * 32 * WM + i * 32 + l32) * kPadK + s * 16 + g * 8);
 #pragma unroll
       for (int j = 0; j < WN; ++j)
         bf[j] = *reinterpret_cast<const v8h*>(
-            &ws[buf][(wn * 32 * WN + j * 32 + l32) * kPadK + s * 16 + g * 8]);
-      // Operands swapped (W as the MFMA's first operand) so that a lane's
-      // results lie along an output row: see the epilogue.
+            ws(buf) + (wn * 32 * WN + j * 32 + l32) * kPadK + s * 16 + g * 8);
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < WN; ++j) {
+          if constexpr (TR)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
+        }
     }
   };
   // Set s0 carries chunks 0, 2, 4, ...; s1 chunks 1, 3, 5, ...
@@ -328,6 +346,32 @@ EOS_DEV void gemm_body(const EncGemmArgs& a) {
     lstore(s0, 0);
     gload(s0, kc + 4);
     __syncthreads();
+  }
+  if constexpr (TR) {
+    // Element e of lane (l32, g) is row 8(e/4) + 4g + e%4 of the block and
+    // column l32: each group of 4 is 4 consecutive rows of one column, one
+    // 8-byte store into vt. Row groups start below rows; their tail past
+    // rows lands in vt's padding.
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int col = n0 + wn * 32 * WN + j * 32 + l32;
+      const float sc = a.wscale[col], bi = a.bias[col];
+      uint16_t* vrow = a.vt + (size_t)(col - a.vt_col0) * a.vt_ld;
+#pragma unroll
+      for (int i = 0; i < WM; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = m0 + wm * 32 * WM + i * 32 + 8 * q + 4 * g;
+          if (row < rows) {
+            v4h o;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) o[t] = (_Float16)(acc[i][j][4 * q + t] * sc + bi);
+            *reinterpret_cast<v4h*>(vrow + row) = o;
+          }
+        }
+      }
+    }
+    return;
   }
   // With W as the first operand, element e of lane (l32, g) is output row
   // l32 of the block and column 8(e/4) + 4g + e%4: each group of 4
@@ -363,6 +407,27 @@ EOS_DEV void gemm_body(const EncGemmArgs& a) {
       }
     }
   }
+}
+
+template <int WM, int WN>
+EOS_DEV void gemm_body(const EncGemmArgs& a) {
+  constexpr int BM = 64 * WM, BN = 64 * WN;
+  __shared__ __attribute__((aligned(16))) uint16_t as[2 * BM * kPadK];
+  __shared__ __attribute__((aligned(16))) uint16_t ws[2 * BN * kPadK];
+  const int rows = *a.rows;
+  // XCD-aware tile order: workgroup w runs on XCD w % 8 (round-robin
+  // dispatch), so XCD x takes row blocks x, x + 8, ... and walks all column
+  // tiles of a row block back to back: the block's A rows are fetched into
+  // that XCD's L2 once instead of once per column tile.
+  const int ntn = a.n / BN;
+  const int w = blockIdx.x, xcd = w & 7, l = w >> 3;
+  const int mb = xcd + 8 * (l / ntn), nb = l % ntn;
+  const int m0 = mb * BM, n0 = nb * BN;
+  if (m0 >= rows) return;
+  if (a.vt != nullptr && n0 >= a.vt_col0)
+    gemm_tile<WM, WN, true>(a, m0, n0, rows, as, ws);
+  else
+    gemm_tile<WM, WN, false>(a, m0, n0, rows, as, ws);
 }
 
 }  // namespace
@@ -448,7 +513,7 @@ template <int HD>
 EOS_DEV void attn_body(const EncAttnArgs& a) {
   constexpr int KB = 32;                 // keys per block
   constexpr int QW = 32;                 // queries per wavefront
-  constexpr int NCH = KB * HD / 8;       // 8-half chunks of K (and of V) per block
+  constexpr int NCH = KB * HD / 8;       // 8-half chunks of K (and of V^T) per block
   constexpr int CPT = (NCH + 255) / 256; // chunks per thread
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][KB * (HD + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * (KB + 8)];
@@ -482,6 +547,10 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   // K [key][HD] and V^T [HD][key] of a 32-key block are staged in LDS from
   // registers; the next block's rows are requested before the current
   // block's MFMAs (double-buffered, one barrier per block).
+  // V^T comes from the feature-major copy the QKV GEMM wrote: chunk idx of a
+  // block is feature d = idx / 4, keys 8 (idx % 4) .. + 7 (16 bytes; keys
+  // past the sequence read the next rows or the zeroed padding, and their
+  // probabilities are 0).
   v4i kreg[CPT], vreg[CPT];
   auto kv_load = [&](int k0) {
 #pragma unroll
@@ -490,9 +559,10 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
       if (idx < NCH) {
         const int kr = idx / (HD / 8), c = (idx % (HD / 8)) * 8;
         const int key = min(k0 + kr, cnt - 1);
-        const uint16_t* base = a.qkv + (size_t)(off + key) * ld + h * HD + c;
-        kreg[u] = *reinterpret_cast<const v4i*>(base + a.hidden);
-        vreg[u] = *reinterpret_cast<const v4i*>(base + 2 * a.hidden);
+        kreg[u] = *reinterpret_cast<const v4i*>(a.qkv + (size_t)(off + key) * ld + a.hidden +
+                                                h * HD + c);
+        const int d = idx >> 2, k8 = (idx & 3) * 8;
+        vreg[u] = *reinterpret_cast<const v4i*>(a.vt + (size_t)(h * HD + d) * a.vt_ld + off + k0 + k8);
       }
     }
   };
@@ -503,12 +573,15 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
       if (idx < NCH) {
         const int kr = idx / (HD / 8), c = (idx % (HD / 8)) * 8;
         *reinterpret_cast<v4i*>(&ks[buf][kr * (HD + 8) + c]) = kreg[u];
-        // Key kr = 16 st + 8 hh + 4 gg + j is stored at 16 st + 8 gg + 4 hh + j,
-        // so the 8 keys a lane's P fragment covers are 16 contiguous bytes.
-        const int pos = (kr & 16) | ((kr & 4) << 1) | ((kr & 8) >> 1) | (kr & 3);
-        const uint16_t* vh = reinterpret_cast<const uint16_t*>(&vreg[u]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vt[buf][(c + e) * (KB + 8) + pos] = vh[e];
+        // Key k = 16 st + 8 hh + 4 gg + j is stored at 16 st + 8 gg + 4 hh + j,
+        // so the 8 keys a lane's P fragment covers are 16 contiguous bytes:
+        // the two 4-key halves of this chunk go to positions 8 and 4 apart.
+        const int d = idx >> 2, k8 = (idx & 3) * 8;
+        const int p0 = (k8 & 16) | ((k8 & 8) >> 1);   // keys k8 .. k8 + 3
+        uint16_t* vrow = &vt[buf][d * (KB + 8)];
+        const v4i v = vreg[u];
+        *reinterpret_cast<uint2*>(vrow + p0) = make_uint2((uint32_t)v.x, (uint32_t)v.y);
+        *reinterpret_cast<uint2*>(vrow + p0 + 8) = make_uint2((uint32_t)v.z, (uint32_t)v.w);
       }
     }
   };
