@@ -136,6 +136,10 @@ _SIGNATURES = {
                                      C.c_int),
     "eoship_tq_maxsim_scores": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int32,
                                  C.c_int64, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_encode": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+                          C.c_void_p], C.c_int),
+    "eoship_tq_encode_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p,
+                                 C.c_void_p, C.c_void_p], C.c_int),
     "eoship_tq_parents_bind": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                 C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
     "eoship_tq_parents_release": ([C.c_void_p, C.c_void_p], C.c_int),

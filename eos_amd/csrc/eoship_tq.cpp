@@ -1141,3 +1141,86 @@ int eoship_tq_parent_topk(EosHipRuntime* rt, EosHipTQParents* parents, const flo
 }
 
 }  // extern "C"
+
+// ----------------------------------------------------------------- encode
+
+namespace {
+
+int encode_impl(EosHipRuntime* rt, EosHipTQ* tq, const float* d_x, int64_t n, uint8_t* d_codes,
+                float* d_norms, char** err) {
+  if (n == 0) return 0;
+  TqEncodeArgs a;
+  memset(&a, 0, sizeof(a));
+  a.rot_t = tq->rot_t;
+  a.d = tq->d;
+  a.bits = tq->bits;
+  a.row_bytes = tq->row_bytes;
+  a.cb_scale = tq->cb_scale;
+  for (int v = 0; v < (1 << tq->bits); ++v) a.cb[v] = tq->codebook[v];
+  const bool small = tq->d <= 512;
+  const int per_wg = small ? 32 : 16;
+  // At most 2^24 vectors per launch (grid size).
+  const int64_t step = (int64_t)1 << 24;
+  for (int64_t i0 = 0; i0 < n; i0 += step) {
+    const int64_t cnt = std::min(step, n - i0);
+    a.x = d_x + (size_t)i0 * tq->d;
+    a.codes = d_codes + (size_t)i0 * tq->row_bytes;
+    a.norms = d_norms + i0;
+    a.n = cnt;
+    if (rt->launch(small ? "eos_tq_encode_d512" : "eos_tq_encode_d1024",
+                   dim3((unsigned)((cnt + per_wg - 1) / per_wg)), dim3(256), 0, &a, err,
+                   "tq_encode") != 0)
+      return 1;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int eoship_tq_encode_device(EosHipRuntime* rt, EosHipTQ* tq, const float* d_x, int64_t n,
+                            uint8_t* d_codes, float* d_norms, char** err) {
+  if (rt == nullptr || tq == nullptr) return set_err(err, "eoship_tq_encode_device: NULL argument");
+  if (tq->rt != rt) return set_err(err, "eoship_tq_encode_device: quantizer bound on another runtime");
+  if (n < 0) return set_err(err, "eoship_tq_encode_device: negative vector count");
+  if (n > 0 && (d_x == nullptr || d_codes == nullptr || d_norms == nullptr))
+    return set_err(err, "eoship_tq_encode_device: NULL buffer");
+  return encode_impl(rt, tq, d_x, n, d_codes, d_norms, err);
+}
+
+int eoship_tq_encode(EosHipRuntime* rt, EosHipTQ* tq, const float* x, int64_t n, uint8_t* codes,
+                     float* norms, char** err) {
+  if (rt == nullptr || tq == nullptr) return set_err(err, "eoship_tq_encode: NULL argument");
+  if (tq->rt != rt) return set_err(err, "eoship_tq_encode: quantizer bound on another runtime");
+  if (n < 0) return set_err(err, "eoship_tq_encode: negative vector count");
+  if (n == 0) return 0;
+  if (x == nullptr || codes == nullptr || norms == nullptr)
+    return set_err(err, "eoship_tq_encode: NULL buffer");
+  // Host rows go through the staging buffer in chunks of at most 2^18 vectors.
+  const int64_t chunk = std::min<int64_t>(n, (int64_t)1 << 18);
+  const size_t xb = ((size_t)chunk * tq->d * sizeof(float) + 255) & ~(size_t)255;
+  const size_t cb = ((size_t)chunk * tq->row_bytes + 255) & ~(size_t)255;
+  const size_t nb = (size_t)chunk * sizeof(float);
+  if (tq->ensure(&tq->io, &tq->io_bytes, xb + cb + nb, err) != 0) return 1;
+  char* base = static_cast<char*>(tq->io);
+  float* dx = reinterpret_cast<float*>(base);
+  uint8_t* dc = reinterpret_cast<uint8_t*>(base + xb);
+  float* dn = reinterpret_cast<float*>(base + xb + cb);
+  for (int64_t i0 = 0; i0 < n; i0 += chunk) {
+    const int64_t cnt = std::min(chunk, n - i0);
+    hipError_t e = hipMemcpyAsync(dx, x + (size_t)i0 * tq->d, (size_t)cnt * tq->d * sizeof(float),
+                                  hipMemcpyHostToDevice, rt->stream);
+    if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(vectors)", e);
+    if (encode_impl(rt, tq, dx, cnt, dc, dn, err) != 0) return 1;
+    e = hipMemcpyAsync(codes + (size_t)i0 * tq->row_bytes, dc, (size_t)cnt * tq->row_bytes,
+                       hipMemcpyDeviceToHost, rt->stream);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(norms + i0, dn, (size_t)cnt * sizeof(float), hipMemcpyDeviceToHost, rt->stream);
+    if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(codes)", e);
+    if (rt->sync(err) != 0) return 1;
+  }
+  return 0;
+}
+
+}  // extern "C"

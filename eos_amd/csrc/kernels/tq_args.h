@@ -148,4 +148,17 @@ struct TqTileNormArgs {
   int cb[16];              // codebook grid values
 };
 
+// Corpus encoder (MSE stage): rows of x -> reference-layout codes + norms,
+// 32 vectors per workgroup (d <= 1024).
+struct TqEncodeArgs {
+  const float* x;          // [n][d]
+  const float* rot_t;      // [d][d], rot_t[k*d + j] = R[j][k]; NULL = identity
+  uint8_t* codes;          // [n][row_bytes]
+  float* norms;            // [n]
+  long long n;
+  int d, bits, row_bytes;
+  float cb_scale;
+  int cb[16];
+};
+
 #endif  // EOSHIP_TQ_ARGS_H

@@ -315,6 +315,105 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_tile_cnorm(TqTileNormAr
   if ((threadIdx.x & 31) == 0 && tile * kTile < a.n) a.tile_cn[tile] = sqrt_up(ss);
 }
 
+// ----------------------------------------------------------------- encode
+
+
+// Build-defined MSE-stage encoder, one workgroup per V vectors (d <= DMAX):
+//   u_j = sum_k R[j][k] x_k (f64, one fma chain per coordinate, k ascending),
+//   ss = sum_k x_k^2 (f64 fma chain), nrm = sqrt(ss), norm = (float)nrm,
+//   code_j = argmin_v |u_j - nrm c_v| (ties to the lower v), c_v = s_c C_v
+// in f64, each product and difference rounded once (nrm c_v is formed before
+// the differences and read back from LDS, so nothing is contracted). The
+// vectors are staged in LDS ([k][v], f32); thread t runs the chains of
+// coordinates t, t + 256, ... for all V vectors, reading R^T rows
+// coalesced. Codes go through LDS and are packed low bits first.
+namespace {
+template <int kEncV, int DMAX>
+EOS_DEV void encode_body(const TqEncodeArgs& a) {
+  __shared__ float xs[DMAX * kEncV];
+  __shared__ double ncs[kEncV * 16];
+  __shared__ uint8_t cs[kEncV * DMAX];
+  const int tid = threadIdx.x;
+  const long long v0 = (long long)blockIdx.x * kEncV;
+  const int nv = (int)min((long long)kEncV, a.n - v0);
+  if (nv <= 0) return;
+  const int d = a.d, levels = 1 << a.bits;
+  // Stage x (rows past n are zero).
+  for (int i = tid; i < kEncV * d; i += 256) {
+    const int v = i / d, k = i - v * d;
+    xs[k * kEncV + v] = v < nv ? a.x[(size_t)(v0 + v) * d + k] : 0.0f;
+  }
+  __syncthreads();
+  if (tid < kEncV) {
+    double ss = 0.0;
+    for (int k = 0; k < d; ++k) {
+      const double xk = (double)xs[k * kEncV + tid];
+      ss = fma(xk, xk, ss);
+    }
+    const double nrm = __builtin_sqrt(ss);
+    if (tid < nv) a.norms[v0 + tid] = (float)nrm;
+    for (int l = 0; l < levels; ++l) ncs[tid * 16 + l] = nrm * ((double)a.cb_scale * (double)a.cb[l]);
+  }
+  __syncthreads();
+  for (int j = tid; j < d; j += 256) {
+    double acc[kEncV];
+#pragma unroll
+    for (int v = 0; v < kEncV; ++v) acc[v] = 0.0;
+    if (a.rot_t != nullptr) {
+      for (int k = 0; k < d; ++k) {
+        const double r = (double)a.rot_t[(size_t)k * d + j];
+        const float4* xr = reinterpret_cast<const float4*>(&xs[k * kEncV]);
+#pragma unroll
+        for (int q = 0; q < kEncV / 4; ++q) {
+          const float4 xv = xr[q];
+          acc[4 * q + 0] = fma(r, (double)xv.x, acc[4 * q + 0]);
+          acc[4 * q + 1] = fma(r, (double)xv.y, acc[4 * q + 1]);
+          acc[4 * q + 2] = fma(r, (double)xv.z, acc[4 * q + 2]);
+          acc[4 * q + 3] = fma(r, (double)xv.w, acc[4 * q + 3]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < kEncV; ++v) acc[v] = (double)xs[j * kEncV + v];
+    }
+#pragma unroll 4
+    for (int v = 0; v < kEncV; ++v) {
+      const double u = acc[v];
+      int best = 0;
+      double bd = fabs(u - ncs[v * 16]);
+      for (int l = 1; l < levels; ++l) {
+        const double dv = fabs(u - ncs[v * 16 + l]);
+        if (dv < bd) {
+          bd = dv;
+          best = l;
+        }
+      }
+      cs[v * DMAX + j] = (uint8_t)best;
+    }
+  }
+  __syncthreads();
+  // Pack: byte b of vector v holds codes of coordinates 8b/bits ... (low bits first).
+  const int per = 8 / a.bits;
+  for (int i = tid; i < nv * a.row_bytes; i += 256) {
+    const int v = i / a.row_bytes, b = i - v * a.row_bytes;
+    uint32_t byte = 0;
+    for (int e = 0; e < per; ++e) {
+      const int j = b * per + e;
+      if (j < d) byte |= (uint32_t)cs[v * DMAX + j] << (e * a.bits);
+    }
+    a.codes[(size_t)(v0 + v) * a.row_bytes + b] = (uint8_t)byte;
+  }
+}
+}  // namespace
+
+// 32 vectors per workgroup for d <= 512, 16 for d <= 1024 (LDS).
+extern "C" __global__ __launch_bounds__(256) void eos_tq_encode_d512(TqEncodeArgs a) {
+  encode_body<32, 512>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void eos_tq_encode_d1024(TqEncodeArgs a) {
+  encode_body<16, 1024>(a);
+}
+
 // --------------------------------------------------------------------- scan
 
 

@@ -94,6 +94,30 @@ class TurboQuantIndex:
         except Exception:
             pass
 
+    def encode(self, vectors: np.ndarray):
+        """Quantizes rows of vectors [n, dim] on the device with this index's
+        rotation, codebook and bits: (codes uint8 [n, row_bytes], norms f32 [n]),
+        ready to bind as a TurboQuantIndex corpus (the corpus-side Quantize of
+        runtime/retrieval_turboquant.go:700,708). An index bound with no vectors
+        serves as a pure quantizer."""
+        x = np.ascontiguousarray(vectors, dtype=np.float32)
+        if x.ndim != 2 or x.shape[1] != self.dim:
+            raise ValueError(f"vectors must be [n, {self.dim}]")
+        row_bytes = (self.dim * self.bits + 7) // 8
+        codes = np.zeros((x.shape[0], row_bytes), np.uint8)
+        norms = np.zeros(x.shape[0], np.float32)
+        _lib.call("eoship_tq_encode", self.rt.handle, self.handle, x.ctypes.data_as(C.c_void_p),
+                  C.c_int64(x.shape[0]), codes.ctypes.data_as(C.c_void_p),
+                  norms.ctypes.data_as(C.c_void_p))
+        return codes, norms
+
+    def encode_device(self, d_x: DeviceBuffer, n: int, d_codes: DeviceBuffer,
+                      d_norms: DeviceBuffer) -> None:
+        """Enqueues encode on device buffers (x f32 [n, dim] -> codes
+        [n, row_bytes], norms f32 [n]); no wait."""
+        _lib.call("eoship_tq_encode_device", self.rt.handle, self.handle, d_x.ptr, C.c_int64(n),
+                  d_codes.ptr, d_norms.ptr)
+
     def _queries(self, queries: np.ndarray) -> np.ndarray:
         q = np.ascontiguousarray(queries, dtype=np.float32)
         if q.ndim == 1:

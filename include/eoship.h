@@ -170,6 +170,21 @@ int eoship_tq_maxsim_scores(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, co
                             int32_t q, int32_t tq_tokens, int64_t doc_begin, int64_t doc_count,
                             float* scores, char** err);
 
+/* Corpus encoder with a bound corpus's quantizer (rotation, codebook, bits;
+ * a corpus bound with n = 0 serves as a pure quantizer): rows of x [n][dim]
+ * f32 -> codes [n][ceil(dim*bits/8)] in the reference layout (coordinate j
+ * at bit j*bits, low bits first) and norms [n]. The MSE stage of the
+ * corpus-side quantizer (turboquant.NewIPWithSeed / IPQuantizer.Quantize,
+ * called at runtime/retrieval_turboquant.go:700,708; build-defined
+ * arithmetic: u = R x in f64 fma chains, norm = (float)sqrt(sum x^2),
+ * code_j = argmin_v |u_j - norm_f64 * s_c C_v|, ties to the lower v). The
+ * outputs bind directly with eoship_tq_bind_corpus; the device form takes
+ * embeddings already on the device (an encoder's output). */
+int eoship_tq_encode(EosHipRuntime* rt, EosHipTQ* tq, const float* x, int64_t n, uint8_t* codes,
+                     float* norms, char** err);
+int eoship_tq_encode_device(EosHipRuntime* rt, EosHipTQ* tq, const float* d_x, int64_t n,
+                            uint8_t* d_codes, float* d_norms, char** err);
+
 /* Parent aggregation over children (one query vector per query): the
  * corpus vectors [offsets[p], offsets[p+1]) are the children of parent p
  * (offsets ascending, offsets[0] = 0, offsets[nparents] = corpus size; a

@@ -51,6 +51,8 @@ def load() -> C.CDLL:
     lib.tq_parent_topk.argtypes = [P, C.c_int, P, C.c_int, C.c_int, P, C.c_float, P, P, P,
                                    C.c_int64, C.c_int, C.c_double, C.c_int, P, P, P, P]
     lib.tq_parent_topk.restype = C.c_int64
+    lib.tq_encode.argtypes = [P, C.c_int64, P, C.c_int, C.c_int, P, C.c_float, P, P]
+    lib.tq_encode.restype = None
     _lib = lib
     return lib
 
@@ -156,6 +158,19 @@ def tq_maxsim_scores(queries, rotation, dim, bits, codebook, codebook_scale, cod
                             C.c_float(codebook_scale), _p(codes), _p(norms), ndocs, doc_len,
                             _p(out))
     return out
+
+
+def tq_encode(vectors, rotation, dim, bits, codebook, codebook_scale):
+    """Build-defined MSE-stage encoder: (codes uint8 [n, row_bytes], norms f32 [n])."""
+    x = _f32(vectors).reshape(-1, dim)
+    rot = None if rotation is None else _f32(rotation)
+    cb = np.ascontiguousarray(codebook, dtype=np.int8)
+    row_bytes = (dim * bits + 7) // 8
+    codes = np.zeros((x.shape[0], row_bytes), np.uint8)
+    norms = np.zeros(x.shape[0], np.float32)
+    load().tq_encode(_p(x), x.shape[0], _p(rot), dim, bits, _p(cb), C.c_float(codebook_scale),
+                     _p(codes), _p(norms))
+    return codes, norms
 
 
 def tq_parent_topk(queries, rotation, dim, bits, codebook, codebook_scale, codes, norms,

@@ -388,3 +388,56 @@ int64_t tq_parent_topk(const float* queries, int nq, const float* rot, int d, in
   free(heap);
   return kk;
 }
+
+/* ------------------------------------------------------------- encode
+ * Build-defined corpus encoder of the MSE stage (the reference's quantizer,
+ * turboquant.IPQuantizer.Quantize, lives in the un-vendored module and is
+ * called at runtime/retrieval_turboquant.go:700,708): for each vector x,
+ *   u_j  = sum_k R[j][k] x_k          f64, one fma chain in k order (R = I without rotation)
+ *   ss   = sum_k x_k^2                f64 fma chain in k order
+ *   nrm  = sqrt(ss) (f64), norm = (float)nrm
+ *   code_j = argmin_v |u_j - nrm * c_v|, c_v = (double)s_c * (double)C_v,
+ *            ties to the lower v (each product and difference rounded once)
+ * and the codes are packed low bits first (coordinate j at bit j * bits). */
+void tq_encode(const float* x, int64_t n, const float* rot, int d, int bits, const int8_t* cb,
+               float cb_scale, uint8_t* codes, float* norms) {
+  const int levels = 1 << bits;
+  const int row_bytes = (d * bits + 7) / 8;
+  double c[16];
+  for (int v = 0; v < levels; ++v) c[v] = (double)cb_scale * (double)cb[v];
+  double* u = (double*)malloc(sizeof(double) * (size_t)d);
+  double nc[16];
+  for (int64_t i = 0; i < n; ++i) {
+    const float* xi = x + (size_t)i * d;
+    double ss = 0.0;
+    for (int k = 0; k < d; ++k) ss = fma((double)xi[k], (double)xi[k], ss);
+    for (int j = 0; j < d; ++j) {
+      if (rot == NULL) {
+        u[j] = (double)xi[j];
+        continue;
+      }
+      double acc = 0.0;
+      for (int k = 0; k < d; ++k) acc = fma((double)rot[(size_t)j * d + k], (double)xi[k], acc);
+      u[j] = acc;
+    }
+    const double nrm = sqrt(ss);
+    norms[i] = (float)nrm;
+    for (int v = 0; v < levels; ++v) nc[v] = nrm * c[v];
+    uint8_t* row = codes + (size_t)i * row_bytes;
+    memset(row, 0, (size_t)row_bytes);
+    for (int j = 0; j < d; ++j) {
+      int best = 0;
+      double bd = fabs(u[j] - nc[0]);
+      for (int v = 1; v < levels; ++v) {
+        const double dv = fabs(u[j] - nc[v]);
+        if (dv < bd) {
+          bd = dv;
+          best = v;
+        }
+      }
+      const int bit = j * bits;
+      row[bit >> 3] |= (uint8_t)(best << (bit & 7));
+    }
+  }
+  free(u);
+}
