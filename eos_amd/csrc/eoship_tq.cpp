@@ -187,18 +187,24 @@ struct EosHipTQ {
   }
 
   int launch_scan(TqScanArgs* s, int qb, char** err) {
+    // The scan kernels assume at least one tile (their first loads are clamped
+    // to the last tile); with none there is nothing to scan or keep.
+    if (s->ntiles <= 0) return 0;
     static const char* const labels[4] = {"tq_scan_dense", "tq_scan_filter", "tq_scan_sample",
                                           "tq_scan_filter"};
     const int nqg = nqg_for(qb);
     char name[64];
     const char kind = s->mode == 1 ? 'f' : s->mode == 3 ? 'h' : 'w';
     snprintf(name, sizeof(name), "eos_tq_scan_b%d_k%d_g%d_%c", bits, ks, nqg, kind);
-    const int waves = 4;
-    int64_t blocks = (s->ntiles + waves - 1) / waves;
-    const int64_t maxb = (int64_t)rt->compute_units * 2;
-    if (blocks > maxb) blocks = maxb;
+    // One workgroup per CU (eight waves; twelve for the high-half filter up to
+    // 16 K-steps, matching the kernels' launch bounds),
+    // each owning a contiguous tile range of at least one tile (the kernel
+    // clamps its loads to the range).
+    const int threads = s->mode == 3 && ks <= 16 ? 768 : 512;
+    int64_t blocks = (s->ntiles + threads / 64 - 1) / (threads / 64);
+    if (blocks > rt->compute_units) blocks = rt->compute_units;
     if (blocks < 1) blocks = 1;
-    return rt->launch(name, dim3((unsigned)blocks), dim3(256), 0, s, err, labels[s->mode]);
+    return rt->launch(name, dim3((unsigned)blocks), dim3(threads), 0, s, err, labels[s->mode]);
   }
 
   // Rotates and quantizes nsrc source rows into ncols = 32 * nqg MFMA columns:

@@ -30,6 +30,10 @@ namespace {
 
 constexpr int kTile = 32;        // corpus vectors per MFMA row block
 constexpr int kScanThreads = 256;
+// The corpus scans run one workgroup per CU: eight waves (two per SIMD), or
+// twelve (three per SIMD) for the high-half filter up to 16 K-steps, whose
+// registers fit the 168 of three waves.
+constexpr int scan_threads(bool hi, int ks) { return hi && ks <= 16 ? 768 : 512; }
 
 EOS_DEV uint32_t score_key(float s) {
   uint32_t u = __float_as_uint(s);
@@ -458,6 +462,14 @@ EOS_DEV v4i decode_step<2>(const v4i& raw, int h, const TqScanArgs& a) {
 // the end, so the scan never waits on a global atomic.
 constexpr int kLdsSlots = 16;
 
+// Register budget of the scan's stage ring and accumulators (the rest of the
+// 256 registers of two waves per SIMD hold decode temporaries, per-query
+// constants, addresses and, without HI, the exact-score epilogue), and the
+// deepest ring used.
+constexpr int kRingRegsHi = 176;
+constexpr int kRingRegsExact = 150;
+constexpr int kRingCap = 2;
+
 template <int NLOAD>
 EOS_DEV void load_tile_codes(v4i (&r)[NLOAD], const v4i* packed, long long tile, int lane) {
   const v4i* src = packed + (size_t)tile * NLOAD * 64 + lane;
@@ -487,10 +499,12 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   constexpr int SPL = 8 / BITS;
   constexpr int NLOAD = (KS + SPL - 1) / SPL;
   constexpr int NQ = 32 * NQG;
+  constexpr int NTH = scan_threads(HI, KS);
   __shared__ v4i sb[KS * NCBU * 64];
   __shared__ uint32_t lc_cnt[FILTER ? NQ : 1];
   __shared__ u64 lc_buf[FILTER ? NQ * kLdsSlots : 1];
-  __shared__ float4 nstage[kScanThreads / 64][8];
+  __shared__ float4 nstage[NTH / 64][8];
+  __shared__ int tile_next;
   if (a.gate != nullptr) {
     // Exhaustive pass of the exact fallback: run only when a query was flagged.
     bool any = false;
@@ -500,7 +514,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   const int lane = threadIdx.x & 63;
   // Wave-uniform tile indices keep the tile addressing in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = gridDim.x * (kScanThreads / 64);
+  constexpr int NWV = NTH / 64;
   const int half = lane >> 5;
   const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
   // Per-column constants live in registers for the whole scan: a global load
@@ -516,42 +530,22 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     ta_r[g] = (FILTER && live_r[g]) ? a.tau[qi] : __builtin_inff();
     lo_r[g] = (HI && live_r[g]) ? a.lonorm[qi] : 0.0f;
   }
-  // Pre-test thresholds of the filter. For tau > 0 and alpha > 0 a kept score
-  // s = fl(fl(fl(D) a) n) >= tau implies D > 0, n > 0 and, with u = 2^-24,
-  // p = fl(fl(D) n) >= (tau / a)(1 - u) / (1 + u)^2 > (tau / a)(1 - 2^-16)
-  // rounded, which is pt. Other cases test every row exactly (pt = -inf) or
-  // none (alpha = 0: every score is 0 < tau).
-  float pt_r[NQG];
-#pragma unroll
-  for (int g = 0; g < NQG; ++g) {
-    const float ta = ta_r[g], al = al_r[g];
-    float pt = -__builtin_inff();
-    if (ta > 0.0f) {
-      if (!(al > 0.0f)) {
-        pt = __builtin_inff();
-      } else {
-        pt = (ta / al) * 0.9999847412109375f;
-        if (!(pt <= 3.402823466e38f)) pt = -__builtin_inff();
-      }
-    }
-    pt_r[g] = pt;
-  }
-  // Software pipeline over three register stages (a ring, unrolled so that no
+  float pt_r[NQG];  // filled once the first tile loads are issued
+  // Software pipeline over a ring of register stages (unrolled so that no
   // stage is ever copied: a copy of a register still being loaded would wait
-  // for every load issued before it). Codes are in flight two tiles ahead of
-  // the tile being decoded, norms one tile ahead. A stage holds one norm per
-  // lane (row lane % 32 of its tile); the epilogue redistributes them to the
-  // accumulator layout through a 128-byte LDS slot of the wave.
+  // for every load issued before it). A stage holds a tile's codes and one
+  // norm per lane (row lane % 32 of its tile); the epilogue redistributes the
+  // norms to the accumulator layout through a 128-byte LDS slot of the wave.
   struct Stage {
     v4i raw[NLOAD];
     float nv;
+    int t;  // tile index in [0, ntiles); >= the range end: none
   };
-  auto load_codes = [&](Stage& st, int jj) {
-    load_tile_codes<NLOAD>(st.raw, packed, a.tile_begin + (long long)jj * a.tile_step, lane);
-  };
-  // Lanes 0-31 load the tile's norms; with HI, lanes 32-63 load its tile_cn.
-  auto load_norms = [&](Stage& st, int jj) {
+  // Codes first, then norms: lanes 0-31 load the tile's norms; with HI, lanes
+  // 32-63 load its tile_cn.
+  auto load_stage = [&](Stage& st, int jj) {
     const long long t = a.tile_begin + (long long)jj * a.tile_step;
+    load_tile_codes<NLOAD>(st.raw, packed, t, lane);
     if constexpr (HI)
       st.nv = lane < 32 ? a.norms[t * kTile + lane] : a.tile_cn[t];
     else
@@ -613,30 +607,29 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
         const float lb = (lo_r[g] * cn) * 1.0000002f;  // >= lonorm * cn exactly
         float p[16];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) p[i] = ((float)acc[g][i] * 256.0f + lb) * nrm[i];
+        for (int i = 0; i < 16; ++i) {
+          // fl(D) * 256 is exact, so one fma gives fl(fl(D) * 256 + lb).
+          p[i] = __builtin_fmaf((float)acc[g][i], 256.0f, lb) * nrm[i];
+        }
         float m = -__builtin_inff();
 #pragma unroll
         for (int i = 0; i < 16; ++i) m = fmaxf(m, p[i]);
         if (m >= pt_r[g]) {
-          uint32_t cnt = 0;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int r = 8 * (i >> 2) + 4 * half + (i & 3);
-            cnt += (r < rem && p[i] >= pt_r[g]) ? 1u : 0u;
-          }
-          uint32_t pos = atomicAdd(&lc_cnt[qi], cnt);
+          // Rare path (about one kept row per wave and group): one LDS atomic
+          // per kept row reserves its slot; rows past the stage's capacity go
+          // to the global list.
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int r = 8 * (i >> 2) + 4 * half + (i & 3);
             if (r < rem && p[i] >= pt_r[g]) {
               const u64 key = (u64)(~(uint32_t)(vbase + r));  // id only; rescored later
+              const uint32_t pos = atomicAdd(&lc_cnt[qi], 1u);
               if (pos < (uint32_t)kLdsSlots) {
                 lc_buf[qi * kLdsSlots + pos] = key;
               } else {
                 const uint32_t gpos = atomicAdd(&a.cand_count[qi], 1u);
                 if ((int)gpos < a.cap) a.cand[(size_t)qi * a.cap + gpos] = key;
               }
-              ++pos;
             }
           }
         }
@@ -718,76 +711,113 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
       }
     }
   };
+  // Work distribution: workgroup b (one per CU) owns the contiguous tile
+  // range [rb, re). Its waves take their first R - 1 tiles statically and
+  // then claim tiles one at a time from an LDS counter, so the two waves that
+  // share a SIMD finish together however the SIMD arbitrates between them
+  // (with a fixed share per wave, one of them ran its last quarter alone).
   const int nt = a.ntiles;
-  int j = blockIdx.x * (kScanThreads / 64) + wave;
-  // Loads past the last tile are clamped to it rather than skipped, so every
-  // path issues the same loads and each wait covers only the stage it needs.
-  auto cl = [&](int jj) { return jj < nt ? jj : nt - 1; };
-  // Three stages (codes two tiles ahead) when the ring and the accumulators
-  // fit the 256 registers of two waves per SIMD; two stages otherwise.
-  constexpr bool kRing3 = NLOAD * 12 + NCBU * 16 <= 168;
-  // The first tiles are requested before the query fragments are staged, so
-  // the two round trips overlap. Every wave reaches the barrier.
-  Stage s0, s1, s2;
-  if (j < nt) {
-    load_codes(s0, j);
-    load_norms(s0, j);
-    if constexpr (kRing3) load_codes(s1, cl(j + nw));
-  }
-  if constexpr (HI) {
-    // The high-half blocks only: block cb = 2 g of each K-step.
-    constexpr int COUNT = KS * NQG * 64;
-    constexpr int PER = (COUNT + kScanThreads - 1) / kScanThreads;
-    const v4i* src = reinterpret_cast<const v4i*>(a.bfrag);
-    v4i v[PER];
-#pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      const int i = threadIdx.x + r * kScanThreads;
-      if (i < COUNT) {
-        const int st = i / (NQG * 64), g = (i / 64) % NQG, l = i % 64;
-        v[r] = src[(st * NCB + 2 * g) * 64 + l];
-      }
+  const int rb = (int)((long long)blockIdx.x * nt / gridDim.x);
+  const int re = (int)((long long)(blockIdx.x + 1) * nt / gridDim.x);
+  // Loads past the range are clamped to its last tile rather than skipped, so
+  // every path issues the same loads and each wait covers only the stage it
+  // needs (the host launches no more workgroups than tiles).
+  auto cl = [&](int jj) { return jj < re ? jj : re - 1; };
+  auto claim = [&]() {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&tile_next, 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+  // Ring depth R: a stage holds one tile's codes and norms; R - 1 stages are in
+  // flight while one is processed. Deeper rings keep more bytes in flight per
+  // wave (bandwidth = bytes in flight / latency), as many as fit next to the
+  // accumulators in the 256 registers of two waves per SIMD.
+  constexpr int kStageRegs = NLOAD * 4 + 1;
+  constexpr int kRingFit = ((HI ? kRingRegsHi : kRingRegsExact) - NCBU * 16) / kStageRegs;
+  constexpr int R = kRingFit > kRingCap ? kRingCap : kRingFit < 2 ? 2 : kRingFit;
+  Stage st[R];
+  // Query fragments (HI: the high-half blocks only, block cb = 2 g of each
+  // K-step) are staged in LDS once per workgroup. Loads retire in order, so
+  // the fragments are requested before the first tiles whenever their
+  // registers fit beside the ring: no wave then waits for R - 1 tiles before
+  // it can start. Every wave reaches the barrier.
+  constexpr int FCOUNT = KS * NCBU * 64;
+  constexpr int FPER = (FCOUNT + NTH - 1) / NTH;
+  constexpr bool kFragFirst = FPER * 4 + (R - 1) * kStageRegs <= 200;
+  const v4i* fsrc = reinterpret_cast<const v4i*>(a.bfrag);
+  auto frag_index = [&](int i) {
+    if constexpr (HI) {
+      const int stp = i / (NQG * 64), g = (i / 64) % NQG, l = i % 64;
+      return (stp * NCB + 2 * g) * 64 + l;
+    } else {
+      return i;
     }
+  };
+  // Unconditional (indices are clamped; the host launches no scan without a
+  // tile): a branch here would make the wait before the fragment writes cover
+  // the tile loads as well.
+  auto prologue = [&]() {
 #pragma unroll
-    for (int r = 0; r < PER; ++r) {
-      const int i = threadIdx.x + r * kScanThreads;
-      if (i < COUNT) sb[i] = v[r];
+    for (int p = 0; p < R - 1; ++p) {
+      st[p].t = rb + wave + p * NWV;
+      load_stage(st[p], cl(st[p].t));
     }
-  } else {
-    stage_fragments<kScanThreads, KS * NCB * 64>(sb, reinterpret_cast<const v4i*>(a.bfrag));
+  };
+  if constexpr (!kFragFirst) prologue();
+  {
+    v4i fv[FPER];
+#pragma unroll
+    for (int r = 0; r < FPER; ++r) {
+      const int i = threadIdx.x + r * NTH;
+      if (i < FCOUNT) fv[r] = fsrc[frag_index(i)];
+    }
+    if constexpr (kFragFirst) prologue();
+#pragma unroll
+    for (int r = 0; r < FPER; ++r) {
+      const int i = threadIdx.x + r * NTH;
+      if (i < FCOUNT) sb[i] = fv[r];
+    }
   }
   if (FILTER && threadIdx.x < NQ) lc_cnt[threadIdx.x] = 0u;
+  if (threadIdx.x == 0) tile_next = rb + (R - 1) * NWV;
   __syncthreads();
-  if (j < nt) {
-    if constexpr (kRing3) {
-      for (;;) {
-        load_codes(s2, cl(j + 2 * nw));
-        load_norms(s1, cl(j + nw));
-        process(s0, j);
-        if (j + nw >= nt) break;
-        load_codes(s0, cl(j + 3 * nw));
-        load_norms(s2, cl(j + 2 * nw));
-        process(s1, j + nw);
-        if (j + 2 * nw >= nt) break;
-        load_codes(s1, cl(j + 4 * nw));
-        load_norms(s0, cl(j + 3 * nw));
-        process(s2, j + 2 * nw);
-        j += 3 * nw;
-        if (j >= nt) break;
-      }
-    } else {
-      for (;;) {
-        load_codes(s1, cl(j + nw));
-        load_norms(s1, cl(j + nw));
-        process(s0, j);
-        if (j + nw >= nt) break;
-        load_codes(s0, cl(j + 2 * nw));
-        load_norms(s0, cl(j + 2 * nw));
-        process(s1, j + nw);
-        j += 2 * nw;
-        if (j >= nt) break;
+  // Pre-test thresholds of the filter (computed after the first loads are
+  // issued, so their wait covers only the per-query values). For tau > 0 and alpha > 0 a kept score
+  // s = fl(fl(fl(D) a) n) >= tau implies D > 0, n > 0 and, with u = 2^-24,
+  // p = fl(fl(D) n) >= (tau / a)(1 - u) / (1 + u)^2 > (tau / a)(1 - 2^-16)
+  // rounded, which is pt. Other cases test every row exactly (pt = -inf) or
+  // none (alpha = 0: every score is 0 < tau).
+#pragma unroll
+  for (int g = 0; g < NQG; ++g) {
+    const float ta = ta_r[g], al = al_r[g];
+    float pt = -__builtin_inff();
+    if (ta > 0.0f) {
+      if (!(al > 0.0f)) {
+        pt = __builtin_inff();
+      } else {
+        pt = (ta / al) * 0.9999847412109375f;
+        if (!(pt <= 3.402823466e38f)) pt = -__builtin_inff();
       }
     }
+    pt_r[g] = pt;
+  }
+  if (st[0].t < re) {
+    // Phase p of a pass refills the stage processed in phase p - 1 with a
+    // newly claimed tile, then processes stage p; stages past the range only
+    // load (a wave-uniform branch). A wave's claims increase, so once the next
+    // stage to process is past the range every later one is too. The loop has
+    // a single exit at its end: exits between phases make the compiler's wait
+    // analysis merge every phase at the loop head and wait for all but the
+    // newest stage.
+    do {
+#pragma unroll
+      for (int p = 0; p < R; ++p) {
+        Stage& nx = st[(p + R - 1) % R];
+        nx.t = claim();
+        load_stage(nx, cl(nx.t));
+        if (st[p].t < re) process(st[p], st[p].t);
+      }
+    } while (st[0].t < re);
   }
   if constexpr (FILTER) {
     // Flush the stage: one global atomic per query per workgroup.
@@ -807,15 +837,16 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
 }  // namespace
 
 #define EOS_TQ_SCAN(BITS, KS, NQG)                                                        \
-  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) \
+  extern "C" __global__ __launch_bounds__(scan_threads(false, KS)) __attribute__((amdgpu_waves_per_eu(2, 8))) \
   void eos_tq_scan_b##BITS##_k##KS##_g##NQG##_f(TqScanArgs a) {                           \
     tq_scan_body<BITS, KS, NQG, true>(a);                                                 \
   }                                                                                       \
-  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) \
+  extern "C" __global__ __launch_bounds__(scan_threads(false, KS)) __attribute__((amdgpu_waves_per_eu(2, 8))) \
   void eos_tq_scan_b##BITS##_k##KS##_g##NQG##_w(TqScanArgs a) {                           \
     tq_scan_body<BITS, KS, NQG, false>(a);                                                \
   }                                                                                       \
-  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2, 8))) \
+  extern "C" __global__ __launch_bounds__(scan_threads(true, KS))                         \
+      __attribute__((amdgpu_waves_per_eu(scan_threads(true, KS) / 256, 8)))               \
   void eos_tq_scan_b##BITS##_k##KS##_g##NQG##_h(TqScanArgs a) {                           \
     tq_scan_body<BITS, KS, NQG, true, true>(a);                                           \
   }
