@@ -134,7 +134,7 @@ def _cpu_model() -> str:
 def tq_leg(rt, args) -> dict:
     """BASELINE config 2 (the bench line's workload)."""
     from eos_amd import datagen
-    from eos_amd.runtime import DeviceBuffer
+    from eos_amd.runtime import DeviceBuffer, Runtime
     from eos_amd.turboquant import TurboQuantIndex
 
     log("generating corpus")
@@ -155,24 +155,53 @@ def tq_leg(rt, args) -> dict:
     for i in range(args.warmup):
         idx.top_k_device_deferred(dq, args.queries, args.k, dids, dsc, dstat.view(i * srow, srow))
     rt.sync()
-    # Timed region: every launch runs bare (an event pair around a launch
-    # costs ~5 us of stream time on each side).
-    log(f"timing {args.steps} steps")
     views = [dstat.view(i * srow, srow) for i in range(args.steps)]
-    gc.disable()
-    t0 = time.perf_counter()
-    rt.mark(0)
-    for i in range(args.steps):
-        idx.top_k_device_deferred(dq, args.queries, args.k, dids, dsc, views[i])
-    enqueue_ms = (time.perf_counter() - t0) * 1e3
-    flags = dstat.download(np.int32, (args.steps, args.queries))  # waits for the stream
-    repaired = int(np.count_nonzero(np.any(flags != 0, axis=1)))
-    for i in np.nonzero(np.any(flags != 0, axis=1))[0]:
-        idx.repair_device(dq, args.queries, args.k, dids, dsc, dstat.view(int(i) * srow, srow))
-    rt.mark(1)
-    total_ms = rt.elapsed_ms(0, 1)
-    wall_ms = (time.perf_counter() - t0) * 1e3
-    gc.enable()
+
+    def timed(handles, outs):
+        """K steps, step i on handle i % len(handles) (its own stream and
+        output buffers), bracketed by events on the first runtime, which waits
+        for the others before its closing event. Flagged steps are repaired
+        inside the region. Returns (ms, enqueue_ms, wall_ms, repaired)."""
+        for h in handles:
+            h.rt.sync()
+        gc.disable()
+        t0 = time.perf_counter()
+        rt.mark(0)
+        for h in handles[1:]:
+            h.rt.wait_for(rt)
+        for i in range(args.steps):
+            j = i % len(handles)
+            handles[j].top_k_device_deferred(dq, args.queries, args.k, outs[j][0], outs[j][1], views[i])
+        enqueue_ms = (time.perf_counter() - t0) * 1e3
+        for h in handles[1:]:
+            rt.wait_for(h.rt)
+        flags = dstat.download(np.int32, (args.steps, args.queries))  # waits for rt's stream
+        repaired = int(np.count_nonzero(np.any(flags != 0, axis=1)))
+        for i in np.nonzero(np.any(flags != 0, axis=1))[0]:
+            idx.repair_device(dq, args.queries, args.k, dids, dsc, dstat.view(int(i) * srow, srow))
+        rt.mark(1)
+        ms = rt.elapsed_ms(0, 1)
+        wall_ms = (time.perf_counter() - t0) * 1e3
+        gc.enable()
+        return ms, enqueue_ms, wall_ms, repaired
+
+    # Timed regions: every launch runs bare (an event pair around a launch
+    # costs ~5 us of stream time on each side). The one-stream region gives the
+    # latency of a batch; with two streams, consecutive batches alternate
+    # between two handles on the same resident corpus and overlap on the GPU.
+    log(f"timing {args.steps} steps on one stream")
+    lat_ms, _, _, _ = timed([idx], [(dids, dsc)])
+    idx2 = rt2 = None
+    handles, outs = [idx], [(dids, dsc)]
+    if args.streams == 2:
+        rt2 = Runtime(0)
+        idx2 = idx.share(rt2)
+        outs.append((DeviceBuffer(rt2, args.queries * kk * 8), DeviceBuffer(rt2, args.queries * kk * 4)))
+        handles.append(idx2)
+        for i in range(args.warmup):
+            idx2.top_k_device_deferred(dq, args.queries, args.k, outs[1][0], outs[1][1], views[0])
+        log(f"timing {args.steps} steps on two streams")
+    total_ms, enqueue_ms, wall_ms, repaired = timed(handles, outs)
     # Roofline: the same steps again with only the filter scan bracketed by
     # events on the library stream; its average launch time is the figure.
     rt.profile_reset()
@@ -198,6 +227,11 @@ def tq_leg(rt, args) -> dict:
     rt.profile(False)
     st = idx.top_k_device(dq, args.queries, args.k, dids, dsc, with_stats=True)
     ms_per_step = total_ms / args.steps
+    if idx2 is not None:
+        for b in outs[1]:
+            b.free()
+        idx2.release()
+        rt2.close()
     bytes_per_launch = corpus.n * (corpus.dim * corpus.bits // 8 + 4)
     avg_filter_ms = ms_filter / max(n_filter, 1)
     achieved = bytes_per_launch / (avg_filter_ms / 1e3) / 1e9
@@ -210,9 +244,10 @@ def tq_leg(rt, args) -> dict:
     out = {
         "value": args.queries * corpus.n / (ms_per_step / 1e3),
         "ms_per_step": ms_per_step,
+        "ms_per_batch_one_stream": lat_ms / args.steps,
         "config": {"workload": "turboquant_flat_c2", "n": corpus.n, "dim": corpus.dim,
                    "bits": corpus.bits, "queries": args.queries, "k": args.k,
-                   "parallelism": "single GPU"},
+                   "batches_in_flight": args.streams, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "kernel": "tq_scan_filter", "avg_launch_ms": avg_filter_ms,
@@ -259,6 +294,8 @@ def main() -> int:
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--queries", type=int, default=64)
     ap.add_argument("--k", type=int, default=100)
+    ap.add_argument("--streams", type=int, default=2, choices=(1, 2),
+                    help="query batches in flight (one stream each) in the timed region")
     ap.add_argument("--cpu-sample-queries", type=int, default=32)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-encoder", action="store_true")

@@ -99,6 +99,7 @@ _SIGNATURES = {
     "eoship_d2h": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
     "eoship_d2d": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
     "eoship_sync": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_runtime_wait": ([C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_module_load": ([C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p), C.c_void_p],
                            C.c_int),
     "eoship_module_unload": ([C.c_void_p, C.c_void_p], C.c_int),
@@ -116,6 +117,7 @@ _SIGNATURES = {
     "eoship_tq_bind_corpus": ([C.c_void_p, C.POINTER(EosHipTQDesc), C.c_void_p, C.c_void_p,
                                C.c_int64, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
     "eoship_tq_release": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_share": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
     "eoship_tq_topk": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
                         C.c_void_p, C.POINTER(EosHipTQStats), C.c_void_p], C.c_int),
     "eoship_tq_topk_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,

@@ -11,7 +11,7 @@
 
 #include "eoship.h"
 
-#define EOSHIP_ABI_VERSION 3
+#define EOSHIP_ABI_VERSION 4
 
 namespace eoship {
 

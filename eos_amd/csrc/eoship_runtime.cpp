@@ -257,6 +257,23 @@ int eoship_sync(EosHipRuntime* rt, char** err) {
   return rt->sync(err);
 }
 
+int eoship_runtime_wait(EosHipRuntime* rt, EosHipRuntime* other, char** err) {
+  if (rt == nullptr || other == nullptr) return set_err(err, "eoship_runtime_wait: NULL runtime");
+  if (rt == other) return 0;
+  if (rt->device != other->device)
+    return set_err(err, "eoship_runtime_wait: runtimes are on devices %d and %d", rt->device,
+                   other->device);
+  hipEvent_t ev = nullptr;
+  hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e != hipSuccess) return hip_err(err, "hipEventCreateWithFlags", e);
+  e = hipEventRecord(ev, other->stream);
+  if (e == hipSuccess) e = hipStreamWaitEvent(rt->stream, ev, 0);
+  // Destroying a recorded event is deferred by the runtime until it completes.
+  hipEventDestroy(ev);
+  if (e != hipSuccess) return hip_err(err, "eoship_runtime_wait", e);
+  return 0;
+}
+
 int eoship_module_load(EosHipRuntime* rt, const void* image, size_t bytes, EosHipModule** out,
                        char** err) {
   if (rt == nullptr || image == nullptr || out == nullptr || bytes == 0)

@@ -144,12 +144,41 @@ struct EosHipTQ {
   // host-API staging
   void* io = nullptr;
   size_t io_bytes = 0;
+  // Handles sharing the corpus arrays (packed, norms, rot_t, tile_cn,
+  // codes_rm) through eoship_tq_share; nullptr while this is the only one.
+  int* corpus_refs = nullptr;
 
   void free_all() {
-    void* ptrs[] = {packed, norms, rot_t, qrot, bfrag, alpha, tau, cand, cand_count,
-                    status, samp, dense, dense_dots, qs_buf, lonorm, tile_cn, codes_rm, io};
-    for (void* p : ptrs)
+    void* scratch[] = {qrot, bfrag, alpha, tau, cand, cand_count, status,
+                       samp, dense, dense_dots, qs_buf, lonorm, io};
+    for (void* p : scratch)
       if (p) hipFree(p);
+    if (corpus_refs != nullptr && --*corpus_refs > 0) return;
+    delete corpus_refs;
+    corpus_refs = nullptr;
+    void* corpus[] = {packed, norms, rot_t, tile_cn, codes_rm};
+    for (void* p : corpus)
+      if (p) hipFree(p);
+  }
+
+  // Per-call device scratch (the corpus arrays are allocated by the bind).
+  int alloc_scratch(char** err) {
+    const size_t bfrag_bytes = (size_t)ks * 8 * 64 * 16;
+    samp_tiles = std::min<int64_t>((ntiles + kSampleStride - 1) / kSampleStride, kMaxSampleTiles);
+    if (rt->alloc(bfrag_bytes, reinterpret_cast<void**>(&bfrag), err) != 0 ||
+        rt->alloc((size_t)kMaxCols * d * sizeof(double), reinterpret_cast<void**>(&qrot), err) != 0 ||
+        rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&alpha), err) != 0 ||
+        rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&lonorm), err) != 0 ||
+        rt->alloc((size_t)kBatch * d * sizeof(int16_t), reinterpret_cast<void**>(&qs_buf), err) != 0 ||
+        rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&tau), err) != 0 ||
+        rt->alloc(kMaxCols * sizeof(uint32_t), reinterpret_cast<void**>(&cand_count), err) != 0 ||
+        rt->alloc(kMaxCols * sizeof(int), reinterpret_cast<void**>(&status), err) != 0 ||
+        rt->alloc((size_t)kBatch * kCap * sizeof(unsigned long long), reinterpret_cast<void**>(&cand),
+                  err) != 0 ||
+        rt->alloc((size_t)kBatch * std::max<int64_t>(samp_tiles, 1) * sizeof(float),
+                  reinterpret_cast<void**>(&samp), err) != 0)
+      return 1;
+    return 0;
   }
 
   int ensure(void** p, size_t* have, size_t need, char** err) {
@@ -611,23 +640,46 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
       return fail();
     }
   }
-  const size_t bfrag_bytes = (size_t)tq->ks * 8 * 64 * 16;
-  tq->samp_tiles = std::min<int64_t>((tq->ntiles + kSampleStride - 1) / kSampleStride, kMaxSampleTiles);
-  if (rt->alloc(bfrag_bytes, reinterpret_cast<void**>(&tq->bfrag), err) != 0 ||
-      rt->alloc((size_t)kMaxCols * tq->d * sizeof(double), reinterpret_cast<void**>(&tq->qrot), err) != 0 ||
-      rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&tq->alpha), err) != 0 ||
-      rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&tq->lonorm), err) != 0 ||
-      rt->alloc((size_t)kBatch * tq->d * sizeof(int16_t), reinterpret_cast<void**>(&tq->qs_buf),
-                err) != 0 ||
-      rt->alloc(kMaxCols * sizeof(float), reinterpret_cast<void**>(&tq->tau), err) != 0 ||
-      rt->alloc(kMaxCols * sizeof(uint32_t), reinterpret_cast<void**>(&tq->cand_count), err) != 0 ||
-      rt->alloc(kMaxCols * sizeof(int), reinterpret_cast<void**>(&tq->status), err) != 0 ||
-      rt->alloc((size_t)kBatch * kCap * sizeof(unsigned long long),
-                reinterpret_cast<void**>(&tq->cand), err) != 0 ||
+  if (tq->alloc_scratch(err) != 0) return fail();
+  *out = tq;
+  return 0;
+}
 
-      rt->alloc((size_t)kBatch * std::max<int64_t>(tq->samp_tiles, 1) * sizeof(float),
-                reinterpret_cast<void**>(&tq->samp), err) != 0)
-    return fail();
+int eoship_tq_share(EosHipRuntime* rt, EosHipTQ* src, EosHipTQ** out, char** err) {
+  if (rt == nullptr || src == nullptr || out == nullptr)
+    return set_err(err, "eoship_tq_share: NULL argument");
+  *out = nullptr;
+  if (rt->device != src->rt->device)
+    return set_err(err, "eoship_tq_share: runtime is on device %d, the corpus on device %d",
+                   rt->device, src->rt->device);
+  // The corpus arrays are complete: the bind synchronised its stream.
+  auto* tq = new EosHipTQ();
+  tq->rt = rt;
+  tq->d = src->d;
+  tq->bits = src->bits;
+  tq->ks = src->ks;
+  tq->nload = src->nload;
+  tq->row_bytes = src->row_bytes;
+  tq->qmax = src->qmax;
+  tq->n = src->n;
+  tq->ntiles = src->ntiles;
+  tq->cb_scale = src->cb_scale;
+  memcpy(tq->codebook, src->codebook, sizeof(tq->codebook));
+  memcpy(tq->lut, src->lut, sizeof(tq->lut));
+  tq->rs16 = src->rs16;
+  if (tq->alloc_scratch(err) != 0) {
+    tq->free_all();  // scratch only: the corpus arrays are not attached yet
+    delete tq;
+    return 1;
+  }
+  if (src->corpus_refs == nullptr) src->corpus_refs = new int(1);
+  tq->corpus_refs = src->corpus_refs;
+  ++*tq->corpus_refs;
+  tq->packed = src->packed;
+  tq->norms = src->norms;
+  tq->rot_t = src->rot_t;
+  tq->tile_cn = src->tile_cn;
+  tq->codes_rm = src->codes_rm;
   *out = tq;
   return 0;
 }

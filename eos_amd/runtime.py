@@ -94,6 +94,11 @@ class Runtime:
                   C.c_size_t(64))
         return {"name": name.value.decode(), "arch": arch.value.decode(), "compute_units": cus.value}
 
+    def wait_for(self, other: "Runtime") -> None:
+        """Work enqueued here after this call starts after everything enqueued
+        on ``other`` so far (no host wait)."""
+        _lib.call("eoship_runtime_wait", self.handle, other.handle)
+
     def sync(self) -> None:
         _lib.call("eoship_sync", self.handle)
 

@@ -83,6 +83,16 @@ class TurboQuantIndex:
         _lib.call("eoship_tq_bind_corpus", rt.handle, C.byref(desc), codes.ctypes.data_as(C.c_void_p),
                   norms.ctypes.data_as(C.c_void_p), C.c_int64(n), C.byref(self.handle))
 
+    def share(self, rt: Runtime) -> "TurboQuantIndex":
+        """A handle on the same resident corpus for another runtime (stream)
+        of the device, with its own scratch: batches on the two runtimes may
+        run concurrently."""
+        h = C.c_void_p()
+        _lib.call("eoship_tq_share", rt.handle, self.handle, C.byref(h))
+        other = TurboQuantIndex.__new__(TurboQuantIndex)
+        other.rt, other.n, other.dim, other.bits, other.handle = rt, self.n, self.dim, self.bits, h
+        return other
+
     def release(self) -> None:
         if self.handle:
             _lib.call("eoship_tq_release", self.handle)

@@ -54,6 +54,12 @@ int eoship_h2d(EosHipRuntime* rt, void* dst, const void* src, size_t bytes, char
 int eoship_d2h(EosHipRuntime* rt, void* dst, const void* src, size_t bytes, char** err);
 int eoship_d2d(EosHipRuntime* rt, void* dst, const void* src, size_t bytes, char** err);
 int eoship_sync(EosHipRuntime* rt, char** err);
+/* Orders two runtimes on one device: work enqueued on rt after this call
+ * starts only after all work enqueued on other so far has finished (an event
+ * on other's stream that rt's stream waits for; the host does not wait). No
+ * counterpart in the reference, whose runtime has one stream per device; it
+ * joins concurrent query batches on separate streams. */
+int eoship_runtime_wait(EosHipRuntime* rt, EosHipRuntime* other, char** err);
 
 /* Generic code-object path; replaces the NVRTC compile + cuModuleLoadData +
  * cuLaunchKernel bridge (native_linux.go:500-632, :3548-3563). */
@@ -110,6 +116,14 @@ typedef struct {
 int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uint8_t* codes,
                           const float* norms, int64_t n, EosHipTQ** out, char** err);
 int eoship_tq_release(EosHipTQ* tq, char** err);
+/* A second handle on a bound corpus for another runtime (stream) of the same
+ * device: it shares the resident corpus arrays and owns its own per-call
+ * scratch, so batches on the two streams may run concurrently. Handles may be
+ * released in any order; the corpus is freed with the last. Handles are not
+ * thread-safe: create and release them from one host thread. No counterpart
+ * in the reference (one query loop per corpus); it serves concurrent query
+ * batches. */
+int eoship_tq_share(EosHipRuntime* rt, EosHipTQ* src, EosHipTQ** out, char** err);
 
 /* Top-k by inner-product estimate for Q queries (host buffers).
  * Replaces PrepareQuery + topTurboQuantRetrievalScoresWithStats

@@ -178,6 +178,49 @@ def test_topk_deferred_status_and_repair(rt):
         idx.release()
 
 
+def test_shared_handle_concurrent_batches(rt):
+    """eoship_tq_share: a second handle on another runtime (stream) shares the
+    resident corpus; batches enqueued on both streams at once give the
+    oracle's rows, and the second handle keeps working after the original is
+    released (the corpus is freed with the last handle)."""
+    from eos_amd.runtime import DeviceBuffer, Runtime
+    _case("shared handle, two streams")
+    c = _corpus(50000, 384, 4, seed=23)
+    qa = datagen.baseline_queries(64, 384, 24)
+    qb = datagen.baseline_queries(40, 384, 25)
+    k = 50
+    idx = _index(rt, c)
+    rt2 = Runtime(0)
+    idx2 = idx.share(rt2)
+    bufs = []
+    for r, q in ((rt, qa), (rt2, qb)):
+        bufs.append((DeviceBuffer.from_array(r, q), DeviceBuffer(r, len(q) * k * 8),
+                     DeviceBuffer(r, len(q) * k * 4)))
+    for rep in range(3):
+        idx.top_k_device(bufs[0][0], 64, k, bufs[0][1], bufs[0][2], with_stats=False)
+        idx2.top_k_device(bufs[1][0], 40, k, bufs[1][1], bufs[1][2], with_stats=False)
+    rt.wait_for(rt2)
+    rt.sync()
+    for (dq, dids, dsc), q in zip(bufs, (qa, qb)):
+        ids = dids.download(np.int64, (len(q), k))
+        sc = dsc.download(np.float32, (len(q), k))
+        oids, osc = oracle.tq_topk(q, c.rotation, 384, 4, c.codebook, c.codebook_scale, c.codes,
+                                   c.norms, k)
+        np.testing.assert_array_equal(ids, oids)
+        np.testing.assert_array_equal(sc, osc)
+    idx.release()
+    ids, sc, _ = idx2.top_k(qb, k)
+    oids, osc = oracle.tq_topk(qb, c.rotation, 384, 4, c.codebook, c.codebook_scale, c.codes,
+                               c.norms, k)
+    np.testing.assert_array_equal(ids, oids)
+    np.testing.assert_array_equal(sc, osc)
+    for b in bufs:
+        for x in b:
+            x.free()
+    idx2.release()
+    rt2.close()
+
+
 def test_topk_zero_norms_zero_query_and_k_semantics(rt):
     _case("topk edge cases")
     c = _corpus(500, 384, 4, seed=7)
