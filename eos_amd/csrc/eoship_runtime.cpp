@@ -4,6 +4,16 @@
 // on HIP: one stream per runtime, int return codes, malloc'd error strings.
 #include "eoship_internal.h"
 
+// HIP's launch with dispatch-recorded start/stop events (a C entry point of
+// libamdhip64; its header also holds templates only hipcc compiles).
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX,
+                                               uint32_t globalWorkSizeY, uint32_t globalWorkSizeZ,
+                                               uint32_t localWorkSizeX, uint32_t localWorkSizeY,
+                                               uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void** kernelParams,
+                                               void** extra, hipEvent_t startEvent,
+                                               hipEvent_t stopEvent, uint32_t flags);
+
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -65,21 +75,23 @@ int Runtime::launch(const char* name, dim3 grid, dim3 block, size_t lds, void* a
   const bool rec = profiling && (profile_prefix.empty() ||
                                  strncmp(tag, profile_prefix.c_str(), profile_prefix.size()) == 0);
   hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t e;
   if (rec) {
     if (take_event(&e0, err) != 0 || take_event(&e1, err) != 0) return 1;
-    hipEventRecord(e0, stream);
+    // The dispatch itself records the two events at the kernel's start and
+    // end, so a profiled duration excludes the gaps around the launch.
+    e = hipExtModuleLaunchKernel(f, grid.x * block.x, grid.y * block.y, grid.z * block.z, block.x,
+                                 block.y, block.z, lds, stream, params, nullptr, e0, e1, 0);
+  } else {
+    e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                              static_cast<unsigned>(lds), stream, params, nullptr);
   }
-  hipError_t e = hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
-                                       static_cast<unsigned>(lds), stream, params, nullptr);
   if (e != hipSuccess) {
     if (e0) event_pool.push_back(e0);
     if (e1) event_pool.push_back(e1);
     return hip_err(err, name, e);
   }
-  if (rec) {
-    hipEventRecord(e1, stream);
-    records.push_back(ProfileRecord{tag, e0, e1});
-  }
+  if (rec) records.push_back(ProfileRecord{tag, e0, e1});
   return 0;
 }
 
