@@ -548,9 +548,8 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   // registers; the next block's rows are requested before the current
   // block's MFMAs (double-buffered, one barrier per block).
   // V^T comes from the feature-major copy the QKV GEMM wrote: chunk idx of a
-  // block is feature d = idx / 4, keys 8 (idx % 4) .. + 7 (16 bytes; keys
-  // past the sequence read the next rows or the zeroed padding, and their
-  // probabilities are 0).
+  // block is feature d = idx / 4, keys 8 (idx % 4) .. + 7 (16 bytes; values
+  // of keys past the sequence are zeroed after the load).
   v4i kreg[CPT], vreg[CPT];
   auto kv_load = [&](int k0) {
 #pragma unroll
@@ -562,7 +561,20 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
         kreg[u] = *reinterpret_cast<const v4i*>(a.qkv + (size_t)(off + key) * ld + a.hidden +
                                                 h * HD + c);
         const int d = idx >> 2, k8 = (idx & 3) * 8;
-        vreg[u] = *reinterpret_cast<const v4i*>(a.vt + (size_t)(h * HD + d) * a.vt_ld + off + k0 + k8);
+        v4i vv = *reinterpret_cast<const v4i*>(a.vt + (size_t)(h * HD + d) * a.vt_ld + off + k0 + k8);
+        const int kb = k0 + k8;
+        if (k0 + 32 > cnt && kb + 8 > cnt) {  // only a sequence's last block
+          // Keys at or past the sequence length: their probabilities are 0,
+          // but the rows there (pad rows, another sequence, or memory no
+          // kernel wrote) may hold anything, and 0 * NaN is NaN. Zero them.
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t keep = (kb + 2 * j < cnt ? 0x0000ffffu : 0u) |
+                                  (kb + 2 * j + 1 < cnt ? 0xffff0000u : 0u);
+            vv[j] = (int)((uint32_t)vv[j] & keep);
+          }
+        }
+        vreg[u] = vv;
       }
     }
   };

@@ -212,9 +212,11 @@ class Encoder:
         self._keep = []
 
     def release(self) -> None:
-        if self.handle:
+        # After the runtime is closed the object cannot be released any more
+        # (its stream is gone); the handle is only dropped.
+        if self.handle and self.rt.handle:
             _lib.call("eoship_encoder_release", self.handle)
-            self.handle = C.c_void_p()
+        self.handle = C.c_void_p()
 
     def __del__(self):
         try:
@@ -316,9 +318,11 @@ class TinyEmbed:
                   proj.ctypes.data_as(C.c_void_p), C.c_int32(proj.shape[1]), C.byref(self.handle))
 
     def release(self) -> None:
-        if self.handle:
+        # After the runtime is closed the object cannot be released any more
+        # (its stream is gone); the handle is only dropped.
+        if self.handle and self.rt.handle:
             _lib.call("eoship_embed_release", self.handle)
-            self.handle = C.c_void_p()
+        self.handle = C.c_void_p()
 
     def __del__(self):
         try:

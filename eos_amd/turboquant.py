@@ -94,9 +94,11 @@ class TurboQuantIndex:
         return other
 
     def release(self) -> None:
-        if self.handle:
+        # After the runtime is closed the object cannot be released any more
+        # (its stream is gone); the handle is only dropped.
+        if self.handle and self.rt.handle:
             _lib.call("eoship_tq_release", self.handle)
-            self.handle = C.c_void_p()
+        self.handle = C.c_void_p()
 
     def __del__(self):
         try:
@@ -281,9 +283,11 @@ class TurboQuantParents:
                   off.ctypes.data_as(C.c_void_p), C.c_int64(self.nparents), C.byref(self.handle))
 
     def release(self) -> None:
-        if self.handle:
+        # After the runtime is closed the object cannot be released any more
+        # (its stream is gone); the handle is only dropped.
+        if self.handle and self.index.rt.handle:
             _lib.call("eoship_tq_parents_release", self.handle)
-            self.handle = C.c_void_p()
+        self.handle = C.c_void_p()
 
     def __del__(self):
         try:

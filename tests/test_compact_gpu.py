@@ -69,6 +69,27 @@ def test_compact_matches_oracle(rt, D, heads, F, L, O, T):
     enc.release()
 
 
+def test_stale_memory_does_not_leak_into_embeddings(rt):
+    """Activation rows no kernel writes (pad rows between packed sequences,
+    rows past a sequence that attention's V blocks cover) may hold anything
+    a freed buffer left behind: a freed block filled with f16 NaN is reused
+    by the encoder's buffers, and the embeddings must still match."""
+    from eos_amd.runtime import DeviceBuffer
+    _case("compact on reused NaN-filled memory")
+    poison = DeviceBuffer(rt, 256 << 20)
+    poison.upload(np.full(128 << 20, 0xFFFF, np.uint16))
+    poison.free()
+    w = datagen.compact_q8_weights(2, 128, 1, 256, vocab=3000, max_seq=256, out_dim=64, seed=61)
+    ids, mask, _ = datagen.encoder_batch(6, 200, 3000, 1, 200, 62, 63)
+    mask[3, :] = 0
+    roles = datagen.uniform_int(64, ids.size, 0, 3).astype(np.int32).reshape(ids.shape)
+    enc = CompactEncoder(rt, w)
+    got = enc.embed(ids, mask, roles)
+    assert np.isfinite(got).all()
+    _check(got, _oracle(w, ids, mask, roles))
+    enc.release()
+
+
 def test_compact_q4_weights_and_no_roles(rt):
     _case("compact q4 weights, role ids omitted")
     w = datagen.compact_q8_weights(2, 128, 1, 256, vocab=500, max_seq=64, seed=9, bits=4)
