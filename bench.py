@@ -269,6 +269,65 @@ def tq_leg(rt, args) -> dict:
     return out
 
 
+def maxsim_leg(rt, steps: int) -> dict:
+    """100,000 documents x 128 token vectors of dim 128,
+    2-bit codes, lognormal(0, 0.25) norms, seeded rotation; 32 queries x 32
+    unit Gaussian tokens; MaxSim top-100 documents per query."""
+    from eos_amd import datagen
+    from eos_amd.runtime import DeviceBuffer
+    from eos_amd.turboquant import TurboQuantIndex, TurboQuantMultiVectorIndex
+
+    ndocs, doc_len, dim, bits, nq, tokens, k = 100_000, 128, 128, 2, 32, 32, 100
+    log("maxsim c5: generating corpus")
+    corpus = datagen.TurboQuantCorpus(ndocs * doc_len, dim, bits, 21, 22, 23)
+    q = datagen.baseline_queries(nq * tokens, dim, 24).reshape(nq, tokens, dim)
+    idx = TurboQuantIndex(rt, corpus.codes, corpus.norms, dim, bits, corpus.codebook,
+                          corpus.codebook_scale, corpus.rotation)
+    mv = TurboQuantMultiVectorIndex(idx, doc_len)
+    dq = DeviceBuffer.from_array(rt, q)
+    dids = DeviceBuffer(rt, nq * k * 8)
+    dsc = DeviceBuffer(rt, nq * k * 4)
+    mv.top_k_device(dq, nq, tokens, k, dids, dsc)
+    rt.sync()
+    rt.mark(6)
+    for _ in range(steps):
+        mv.top_k_device(dq, nq, tokens, k, dids, dsc)
+    rt.mark(7)
+    ms = rt.elapsed_ms(6, 7) / steps
+    # Per-launch time of the MaxSim scan (dispatch-recorded events): each
+    # launch streams the whole corpus once for a group of queries.
+    rt.profile_reset()
+    rt.profile_select("tq_maxsim")
+    rt.profile(True)
+    mv.top_k_device(dq, nq, tokens, k, dids, dsc)
+    rt.sync()
+    n_scan, ms_scan = rt.profile_read("tq_maxsim")
+    n_sel, ms_sel = rt.profile_read("tq_maxsim_select")
+    rt.profile(False)
+    n_scan -= n_sel
+    ms_scan -= ms_sel
+    bytes_per_pass = corpus.n * (dim * bits // 8 + 4)
+    avg = ms_scan / max(n_scan, 1)
+    achieved = bytes_per_pass / (avg / 1e3) / 1e9
+    out = {
+        "metric": "MaxSim query-document pairs scored/s",
+        "value": nq * ndocs / (ms / 1e3),
+        "unit": "query-document pairs/s",
+        "ms_per_batch": ms,
+        "config": {"workload": "turboquant_maxsim_c5", "docs": ndocs, "doc_len": doc_len,
+                   "dim": dim, "bits": bits, "queries": nq, "tokens": tokens, "k": k},
+        "token_vector_pairs_per_s": nq * tokens * corpus.n / (ms / 1e3),
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "kernel": "tq_maxsim",
+                     "avg_launch_ms": avg, "launches_per_batch": n_scan,
+                     "bytes_per_launch": bytes_per_pass},
+    }
+    for b in (dq, dids, dsc):
+        b.free()
+    idx.release()
+    return out
+
+
 def copy_calibration(rt, mb: int, reps: int = 5) -> dict:
     """Device-to-device copies of a known size: the reference kernel whose
     FETCH_SIZE / WRITE_SIZE counters scale the scan's in a --pmc run."""
@@ -302,6 +361,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--skip-encoder", action="store_true")
     ap.add_argument("--skip-tq", action="store_true", help="profiling runs of the encoder only")
+    ap.add_argument("--skip-maxsim", action="store_true")
+    ap.add_argument("--maxsim-steps", type=int, default=5)
     ap.add_argument("--encoder-steps", type=int, default=5)
     ap.add_argument("--encoder-configs", default="c3,c4", help="comma list of c3, c4")
     ap.add_argument("--copy-calibration-mb", type=int, default=0)
@@ -336,6 +397,8 @@ def main() -> int:
         for name in args.encoder_configs.split(","):
             log(f"encoder {name}")
             out[f"encoder_{name}"] = encoder_leg(rt, args.encoder_steps, name)
+    if not args.skip_maxsim:
+        out["maxsim_c5"] = maxsim_leg(rt, args.maxsim_steps)
     if args.copy_calibration_mb > 0:
         out["copy_calibration"] = copy_calibration(rt, args.copy_calibration_mb)
     out["device"] = info
