@@ -895,25 +895,35 @@ int maxsim_topk_impl(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const flo
                    (long long)kk64, kSortCap);
   const int kk = (int)kk64;
   const int per = tq->maxsim_nqg();
+  // The document scores of a chunk of queries (all of its scan passes) are
+  // kept, so one select launch ranks every row of the chunk in parallel (one
+  // workgroup per row; a select per pass ran only `per` workgroups at once).
+  // Chunks are whole passes, and their score block stays under 1 GiB.
+  const int64_t by_mem = std::max<int64_t>(1, ((int64_t)1 << 30) / (ndocs * 4));
+  const int chunk = (int)std::max<int64_t>(per, std::min<int64_t>(256, by_mem) / per * per);
+  const int rows = std::min(chunk, q);
   if (tq->ensure(reinterpret_cast<void**>(&tq->dense), &tq->dense_bytes,
-                 (size_t)per * (size_t)ndocs * sizeof(float), err) != 0)
+                 (size_t)rows * (size_t)ndocs * sizeof(float), err) != 0)
     return 1;
-  for (int q0 = 0; q0 < q; q0 += per) {
-    const int qp = std::min(per, q - q0);
-    if (tq->maxsim_pass(d_queries + (size_t)q0 * tq_tokens * tq->d, qp, tq_tokens, doc_len, 0, ndocs,
-                        tq->dense, err) != 0)
-      return 1;
+  for (int c0 = 0; c0 < q; c0 += chunk) {
+    const int cq = std::min(chunk, q - c0);
+    for (int q0 = c0; q0 < c0 + cq; q0 += per) {
+      const int qp = std::min(per, c0 + cq - q0);
+      if (tq->maxsim_pass(d_queries + (size_t)q0 * tq_tokens * tq->d, qp, tq_tokens, doc_len, 0,
+                          ndocs, tq->dense + (size_t)(q0 - c0) * ndocs, err) != 0)
+        return 1;
+    }
     TqSelectArgs sel;
     memset(&sel, 0, sizeof(sel));
     sel.rows = tq->dense;
-    sel.ids = reinterpret_cast<long long*>(d_ids + (size_t)q0 * kk);
-    sel.scores = d_scores + (size_t)q0 * kk;
+    sel.ids = reinterpret_cast<long long*>(d_ids + (size_t)c0 * kk);
+    sel.scores = d_scores + (size_t)c0 * kk;
     sel.n = ndocs;
     sel.stride = ndocs;
     sel.kk = kk;
     sel.mode = 1;
-    sel.nrows = qp;
-    if (rt->launch("eos_tq_row_select", dim3(qp), dim3(1024), 0, &sel, err, "tq_maxsim_select") != 0)
+    sel.nrows = cq;
+    if (rt->launch("eos_tq_row_select", dim3(cq), dim3(1024), 0, &sel, err, "tq_maxsim_select") != 0)
       return 1;
   }
   return 0;

@@ -1428,12 +1428,14 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
         nrm[4 * i4 + 2] = nrm4[i4].z;
         nrm[4 * i4 + 3] = nrm4[i4].w;
       }
+      // The score's "+ 0.0f" (-0 -> +0) commutes with the maximum (fmaxf
+      // treats the zeros as equal), so it is applied once to the token max.
 #pragma unroll
       for (int g = 0; g < NQG; ++g) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int dot = acc[2 * g][i] * 256 + acc[2 * g + 1][i];
-          mx[g] = fmaxf(mx[g], ((float)dot * al[g]) * nrm[i] + 0.0f);
+          mx[g] = fmaxf(mx[g], ((float)dot * al[g]) * nrm[i]);
         }
       }
 #pragma unroll
@@ -1443,7 +1445,7 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
     }
 #pragma unroll
     for (int g = 0; g < NQG; ++g) {
-      float v = fmaxf(mx[g], __shfl_xor(mx[g], 32));  // token max over the document
+      float v = fmaxf(mx[g], __shfl_xor(mx[g], 32)) + 0.0f;  // token max over the document
 #pragma unroll
       for (int o = 1; o < 32; o <<= 1) v = v + __shfl_xor(v, o);
       if (lane == 0 && g < a.groups) a.out[(size_t)g * a.out_stride + doc] = v;

@@ -81,6 +81,31 @@ def test_maxsim_matches_oracle(rt, bits, d, doc_len, ntok, nq):
 
 
 @pytest.mark.gpu
+def test_maxsim_zero_scores_keep_the_oracle_sign(rt):
+    """Documents whose vectors all have norm 0 score (D * alpha) * 0, which is
+    -0 for a negative dot; the score's + 0.0f makes it +0 before the token
+    maximum. The device sums must carry the oracle's bits, sign of zero
+    included (a float comparison would take -0 == +0)."""
+    print("[case] maxsim zero-norm documents", flush=True)
+    from eos_amd.turboquant import TurboQuantIndex, TurboQuantMultiVectorIndex
+    d, bits, doc_len = 64, 2, 32
+    c = _corpus(40, doc_len, d, bits, seed=29)
+    norms = c.norms.copy()
+    norms[: 10 * doc_len] = 0.0           # documents 0..9: every vector of norm 0
+    norms[20 * doc_len: 21 * doc_len] = 0.0
+    q = _tokens(3, 4, d, 31)
+    idx = TurboQuantIndex(rt, c.codes, norms, c.dim, c.bits, c.codebook, c.codebook_scale,
+                          c.rotation)
+    mv = TurboQuantMultiVectorIndex(idx, doc_len)
+    got = mv.scores(q)
+    want = oracle.tq_maxsim_scores(q, c.rotation, d, bits, c.codebook, c.codebook_scale, c.codes,
+                                   norms, doc_len)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.all(got[:, :10].view(np.uint32) == 0)  # +0, not -0
+    idx.release()
+
+
+@pytest.mark.gpu
 def test_maxsim_rejects_bad_shapes(rt):
     print("[case] maxsim validation", flush=True)
     from eos_amd._lib import EosHipError
