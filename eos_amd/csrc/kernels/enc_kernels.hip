@@ -38,10 +38,33 @@ EOS_DEV float wave_sum(float v) {
   return v;
 }
 
+// erf(z) by Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26
+// (|error| <= 1.5e-7): one reciprocal, one exp2 and a degree-5 polynomial,
+// branch-free (the library erff evaluates two polynomials in divergent
+// branches). The GELU output is rounded to f16, far coarser than either.
+EOS_DEV float erf_as(float z) {
+  const float a = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.3275911f, a, 1.0f));
+  float p = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  p = __builtin_fmaf(p, t, 1.421413741f);
+  p = __builtin_fmaf(p, t, -0.284496736f);
+  p = __builtin_fmaf(p, t, 0.254829592f);
+  p *= t;
+  const float e = __builtin_amdgcn_exp2f(-(a * a) * 1.4426950408889634f);  // exp(-a^2)
+  return __builtin_copysignf(1.0f - p * e, z);
+}
+
+// tanh(u) = 1 - 2 / (exp(2u) + 1): one exp2 and one reciprocal; saturates to
+// +-1 (exp2 -> inf or 0), absolute error ~1e-7.
+EOS_DEV float tanh_exp(float u) {
+  const float e = __builtin_amdgcn_exp2f(2.8853900817779268f * u);  // exp(2u)
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
+
 EOS_DEV float gelu(float x, int kind) {
-  if (kind == 1) return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+  if (kind == 1) return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
   const float u = 0.7978845608f * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(u));
+  return 0.5f * x * (1.0f + tanh_exp(u));
 }
 
 }  // namespace
