@@ -571,8 +571,10 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   // registers; the next block's rows are requested before the current
   // block's MFMAs (double-buffered, one barrier per block).
   // V^T comes from the feature-major copy the QKV GEMM wrote: chunk idx of a
-  // block is feature d = idx / 4, keys 8 (idx % 4) .. + 7 (16 bytes; values
-  // of keys past the sequence are zeroed after the load).
+  // block is feature d = idx / 4, keys 8 (idx % 4) .. + 7 (16 bytes). Keys
+  // past the sequence (probability 0) read its pad rows, the next sequence or
+  // vt's zeroed tail: all finite, since every row the GEMMs read was written
+  // in this forward (pad rows of ctx included, below), and 0 * finite = 0.
   v4i kreg[CPT], vreg[CPT];
   auto kv_load = [&](int k0) {
 #pragma unroll
@@ -584,20 +586,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
         kreg[u] = *reinterpret_cast<const v4i*>(a.qkv + (size_t)(off + key) * ld + a.hidden +
                                                 h * HD + c);
         const int d = idx >> 2, k8 = (idx & 3) * 8;
-        v4i vv = *reinterpret_cast<const v4i*>(a.vt + (size_t)(h * HD + d) * a.vt_ld + off + k0 + k8);
-        const int kb = k0 + k8;
-        if (k0 + 32 > cnt && kb + 8 > cnt) {  // only a sequence's last block
-          // Keys at or past the sequence length: their probabilities are 0,
-          // but the rows there (pad rows, another sequence, or memory no
-          // kernel wrote) may hold anything, and 0 * NaN is NaN. Zero them.
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t keep = (kb + 2 * j < cnt ? 0x0000ffffu : 0u) |
-                                  (kb + 2 * j + 1 < cnt ? 0xffff0000u : 0u);
-            vv[j] = (int)((uint32_t)vv[j] & keep);
-          }
-        }
-        vreg[u] = vv;
+        vreg[u] = *reinterpret_cast<const v4i*>(a.vt + (size_t)(h * HD + d) * a.vt_ld + off + k0 + k8);
       }
     }
   };
@@ -686,7 +675,19 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     if (more) kv_store(buf ^ 1);
     __syncthreads();
   }
-  if (!qlive) return;
+  if (!qlive) {
+    // Pad rows of the sequence's 8-row slot get zeros: no kernel writes them
+    // otherwise, and the memory may hold anything a freed buffer left (a NaN
+    // there would reach the next layer's V rows past the sequence).
+    if (qi < ((cnt + 7) & ~7)) {
+      uint16_t* prow = a.ctx + (size_t)(off + qi) * a.hidden + h * HD;
+#pragma unroll
+      for (int t = 0; t < HD / 32; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) prow[t * 32 + 8 * (e >> 2) + 4 * g + (e & 3)] = 0;
+    }
+    return;
+  }
   const float inv = lrun > 0.f ? 1.0f / lrun : 0.f;
   uint16_t* orow = a.ctx + (size_t)(off + qi) * a.hidden + h * HD;
 #pragma unroll
