@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "enc_args.h"
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
@@ -260,14 +262,65 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
 // ------------------------------------------------------------------- GEMM
 
 namespace {
-constexpr int kBK = 32, kPadK = kBK + 8;  // K chunk; halves per LDS row (padded)
+constexpr int kBK = 32;  // K chunk: 32 halves = one 64-byte segment of each operand row
+
+// Stage layout: BM rows of A then BN rows of W, 64 bytes (four 16-byte slots)
+// per row, no padding. Chunk c of row r sits in slot c ^ ((r >> 2) & 3): the 16
+// rows that a quarter-wavefront's 16-byte fragment reads touch cover all 64
+// banks once, and each load instruction still fills 1 KB of LDS contiguously.
+EOS_DEV int swz(int r, int c) { return c ^ ((r >> 2) & 3); }
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+EOS_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS byte address of a pointer into a __shared__ array.
+typedef __attribute__((address_space(3))) const uint16_t lds_u16;
+EOS_DEV uint32_t lds_addr(const uint16_t* p) { return (uint32_t)(uintptr_t)(lds_u16*)p; }
+
+// 16-byte LDS read at addr + OFF. Issued as inline assembly: the compiler's
+// wait analysis treats every compiler-visible LDS read as possibly reading
+// memory an outstanding direct-to-LDS load writes and waits for all of them
+// (vmcnt(0)), which would drain the load pipeline at each step. Completion
+// is awaited with lgkm_wait below; stage contents with wait_vmcnt + barrier.
+template <int OFF>
+EOS_DEV v8h lds_read16(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset range");
+  v8h r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+
+// s_waitcnt lgkmcnt(0) that the fragments pass through, so no consumer of
+// them can be scheduled above the wait.
+template <int N>
+EOS_DEV void lgkm_wait(v8h (&f)[N]) {
+  static_assert(N <= 6, "fragment count");
+  if constexpr (N == 2)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]));
+  else if constexpr (N == 3)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]));
+  else if constexpr (N == 4)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]));
+  else if constexpr (N == 6)
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]));
+  else
+    static_assert(N == 2 || N == 3 || N == 4 || N == 6, "fragment count");
+}
 
 // Workgroup tile (64 WM) x (64 WN) over 4 wavefronts in a 2 x 2 grid, each
 // wavefront (32 WM) x (32 WN) = WM x WN MFMA 32x32 blocks. K advances in
-// chunks of 32 through a double-buffered LDS stage fed from two register
-// sets: chunk j is requested three chunk-steps before it is computed, so two
-// chunks of MFMAs cover each load. Per 16-wide K step a wavefront reads
-// WM + WN fragments from LDS for WM * WN MFMAs.
+// chunks of 32 through three LDS stages filled by direct global -> LDS loads
+// (16 bytes per lane, no staging registers): chunk kc + 2 is requested while
+// chunk kc is computed, so each load has two chunks of MFMAs to land. Per
+// chunk a wavefront issues WM + WN loads (16 rows each) and waits with
+// vmcnt(WM + WN), i.e. for everything but the newest chunk, then one barrier
+// makes the whole stage visible.
 // Epilogue: v = scale[n] * acc + bias[n]; mode 1 erf GELU, 2 tanh GELU,
 // 3 + residual[m][n] (out may alias residual: each element is read and
 // written by the same lane).
@@ -276,100 +329,110 @@ constexpr int kBK = 32, kPadK = kBK + 8;  // K chunk; halves per LDS row (padded
 // given): A first, a lane's results lie along an output column, stored
 // transposed into vt[col - vt_col0][row].
 template <int WM, int WN, bool TR>
-EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t* as0,
-                       uint16_t* ws0) {
-  constexpr int BM = 64 * WM, BN = 64 * WN;
-  constexpr int ACH = BM * kBK / 8 / 256;  // 16-byte chunks per thread
-  constexpr int WCH = BN * kBK / 8 / 256;
-  auto as = [&](int buf) { return as0 + buf * BM * kPadK; };
-  auto ws = [&](int buf) { return ws0 + buf * BN * kPadK; };
+EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t* st) {
+  constexpr int BM = 64 * WM, BN = 64 * WN, ST = (BM + BN) * kBK;  // halves per stage
+  constexpr int NLD = WM + WN;  // 16-row loads per wavefront per chunk
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int g = lane >> 5, l32 = lane & 31;
-  // Per-thread source rows and columns of its 16-byte chunks (fixed over K).
-  const uint16_t* asrc[ACH];
-  const uint16_t* wsrc[WCH];
-  int aoff[ACH], woff[WCH];
+  // Load u of this wavefront fills stage rows 16 (wave + 4u) .. + 15 (A rows
+  // for u < WM, W rows after): lane i writes slot i % 4 of row
+  // 16 (wave + 4u) + i / 4 and so reads chunk swz(row, i % 4) of that row.
+  // Rows past the matrix are clamped to its last row (computed, never stored).
+  const uint16_t* src[NLD];
 #pragma unroll
-  for (int u = 0; u < ACH; ++u) {
-    const int idx = tid + 256 * u;
-    const int r = idx >> 2, c = (idx & 3) * 8;
-    asrc[u] = a.a + (size_t)min(m0 + r, a.max_rows - 1) * a.k + c;
-    aoff[u] = r * kPadK + c;
+  for (int u = 0; u < NLD; ++u) {
+    const int r = 16 * (wave + 4 * u) + (lane >> 2);
+    const int c = swz(r, lane & 3);
+    if (u < WM)
+      src[u] = a.a + (size_t)min(m0 + r, a.max_rows - 1) * a.k + c * 8;
+    else
+      src[u] = a.w + (size_t)(n0 + r - BM) * a.k + c * 8;
   }
-#pragma unroll
-  for (int u = 0; u < WCH; ++u) {
-    const int idx = tid + 256 * u;
-    const int r = idx >> 2, c = (idx & 3) * 8;
-    wsrc[u] = a.w + (size_t)(n0 + r) * a.k + c;
-    woff[u] = r * kPadK + c;
-  }
-  struct Set {
-    v4i ra[ACH], rw[WCH];
-  };
   const int nk = a.k / kBK;
-  // Chunks past the end are clamped to the last one (loaded, never stored).
-  auto gload = [&](Set& st, int kc) {
+  // Chunks past the end are clamped to the last one (loaded, never computed).
+  auto issue = [&](uint16_t* st, int kc) {
     const int k0 = min(kc, nk - 1) * kBK;
 #pragma unroll
-    for (int u = 0; u < ACH; ++u) st.ra[u] = *reinterpret_cast<const v4i*>(asrc[u] + k0);
-#pragma unroll
-    for (int u = 0; u < WCH; ++u) st.rw[u] = *reinterpret_cast<const v4i*>(wsrc[u] + k0);
+    for (int u = 0; u < NLD; ++u)
+      __builtin_amdgcn_global_load_lds(src[u] + k0, st + 16 * 32 * (wave + 4 * u), 16, 0, 0);
   };
-  auto lstore = [&](const Set& st, int buf) {
+  // Fragment of lane (l32, g) at K step s: row base + l32, chunk 2s + g (base
+  // is a multiple of 32, so the swizzle depends on l32 only). Byte addresses
+  // of this lane's first A and B fragments in stage 0, per K step.
+  const uint32_t st_b = lds_addr(st);
+  uint32_t abase[2], bbase[2];
 #pragma unroll
-    for (int u = 0; u < ACH; ++u) *reinterpret_cast<v4i*>(as(buf) + aoff[u]) = st.ra[u];
-#pragma unroll
-    for (int u = 0; u < WCH; ++u) *reinterpret_cast<v4i*>(ws(buf) + woff[u]) = st.rw[u];
-  };
+  for (int s = 0; s < 2; ++s) {
+    const int fo = l32 * kBK + swz(l32, 2 * s + g) * 8;
+    abase[s] = st_b + 2 * (wm * 32 * WM * kBK + fo);
+    bbase[s] = st_b + 2 * ((BM + wn * 32 * WN) * kBK + fo);
+  }
   v16f acc[WM][WN];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = v16f{0};
-  auto compute = [&](int buf) {
+  // Fragments of K step S of stage STG (read, then awaited).
+  auto frags = [&](auto stg_c, auto s_c, v8h (&f)[WM + WN]) {
+    constexpr int STG = decltype(stg_c)::value, S = decltype(s_c)::value;
 #pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      v8h af[WM], bf[WN];
-#pragma unroll
-      for (int i = 0; i < WM; ++i)
-        af[i] = *reinterpret_cast<const v8h*>(
-            as(buf) + (wm * 32 * WM + i * 32 + l32) * kPadK + s * 16 + g * 8);
-#pragma unroll
-      for (int j = 0; j < WN; ++j)
-        bf[j] = *reinterpret_cast<const v8h*>(
-            ws(buf) + (wn * 32 * WN + j * 32 + l32) * kPadK + s * 16 + g * 8);
-#pragma unroll
-      for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-          if constexpr (TR)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-          else
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
-        }
+    for (int i = 0; i < WM; ++i) {
+      constexpr int kStage = 2 * STG * ST;
+      f[i] = lds_read16<kStage>(abase[S] + 2 * i * 32 * kBK);
     }
+#pragma unroll
+    for (int j = 0; j < WN; ++j) f[WM + j] = lds_read16<2 * STG * ST>(bbase[S] + 2 * j * 32 * kBK);
   };
-  // Set s0 carries chunks 0, 2, 4, ...; s1 chunks 1, 3, 5, ...
-  Set s0, s1;
-  gload(s0, 0);
-  gload(s1, 1);
-  lstore(s0, 0);
-  gload(s0, 2);
-  __syncthreads();
-  // nk is even (K is a multiple of 64): one back-edge, no exit in the body.
-  // The last pass stores clamped chunks that nothing reads.
-  for (int kc = 0; kc < nk; kc += 2) {
-    // chunk kc in LDS[0]; s1 holds chunk kc + 1; s0 receives chunk kc + 2.
-    compute(0);
-    lstore(s1, 1);
-    gload(s1, kc + 3);
-    __syncthreads();
-    compute(1);
-    lstore(s0, 0);
-    gload(s0, kc + 4);
-    __syncthreads();
-  }
+  auto mma = [&](v8h (&f)[WM + WN]) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        if constexpr (TR)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], f[WM + j], acc[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[WM + j], f[i], acc[i][j], 0, 0, 0);
+      }
+  };
+  auto compute = [&](auto stg_c) {
+    v8h f0[WM + WN], f1[WM + WN];
+    frags(stg_c, std::integral_constant<int, 0>{}, f0);
+    lgkm_wait(f0);
+    frags(stg_c, std::integral_constant<int, 1>{}, f1);
+    mma(f0);
+    lgkm_wait(f1);
+    mma(f1);
+  };
+  uint16_t* const st0 = st;
+  uint16_t* const st1 = st + ST;
+  uint16_t* const st2 = st + 2 * ST;
+  issue(st0, 0);
+  issue(st1, 1);
+  // Three chunks per pass, one stage each; one back-edge and no exit in the
+  // body. The stage refilled at a step was last read in the step before, and
+  // the step's barrier orders that read before the refill. The barrier is the
+  // bare s_barrier: a fenced one (__syncthreads) must wait for every
+  // outstanding direct-to-LDS load, including the chunk just requested, and
+  // vmcnt(NLD) has already made this wavefront's part of the stage land.
+  int kc = 0;
+  do {
+    wait_vmcnt<NLD>();
+    __builtin_amdgcn_s_barrier();
+    issue(st2, kc + 2);
+    compute(std::integral_constant<int, 0>{});
+    wait_vmcnt<NLD>();
+    __builtin_amdgcn_s_barrier();
+    issue(st0, kc + 3);
+    if (kc + 1 < nk) compute(std::integral_constant<int, 1>{});
+    wait_vmcnt<NLD>();
+    __builtin_amdgcn_s_barrier();
+    issue(st1, kc + 4);
+    if (kc + 2 < nk) compute(std::integral_constant<int, 2>{});
+    kc += 3;
+  } while (kc < nk);
+  // No LDS write may land after the workgroup exits.
+  wait_vmcnt<0>();
   if constexpr (TR) {
     // Element e of lane (l32, g) is row 8(e/4) + 4g + e%4 of the block and
     // column l32: each group of 4 is 4 consecutive rows of one column, one
@@ -434,9 +497,8 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
 
 template <int WM, int WN>
 EOS_DEV void gemm_body(const EncGemmArgs& a) {
-  constexpr int BM = 64 * WM, BN = 64 * WN;
-  __shared__ __attribute__((aligned(16))) uint16_t as[2 * BM * kPadK];
-  __shared__ __attribute__((aligned(16))) uint16_t ws[2 * BN * kPadK];
+  constexpr int BM = 64 * WM, BN = 64 * WN, ST = (BM + BN) * kBK;
+  __shared__ __attribute__((aligned(16))) uint16_t st[3 * ST];
   const int rows = *a.rows;
   // XCD-aware tile order: workgroup w runs on XCD w % 8 (round-robin
   // dispatch), so XCD x takes row blocks x, x + 8, ... and walks all column
@@ -448,9 +510,9 @@ EOS_DEV void gemm_body(const EncGemmArgs& a) {
   const int m0 = mb * BM, n0 = nb * BN;
   if (m0 >= rows) return;
   if (a.vt != nullptr && n0 >= a.vt_col0)
-    gemm_tile<WM, WN, true>(a, m0, n0, rows, as, ws);
+    gemm_tile<WM, WN, true>(a, m0, n0, rows, st);
   else
-    gemm_tile<WM, WN, false>(a, m0, n0, rows, as, ws);
+    gemm_tile<WM, WN, false>(a, m0, n0, rows, st);
 }
 
 }  // namespace
