@@ -700,28 +700,38 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
       }
     }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float mnew = fmaxf(mrun, mloc);
-    // v_exp_f32 directly: every argument is <= 0 or -inf (exp2 -> 0).
-    const float corr = __builtin_amdgcn_exp2f(mrun - mnew);
-    float psum = 0.f;
-    v8h pf[2];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float p = __builtin_amdgcn_exp2f(s[e] - mnew);
-      psum += p;
-      pf[e >> 3][e & 7] = (_Float16)p;
-    }
-    psum += __shfl_xor(psum, 32);
-    lrun = lrun * corr + psum;
-    // The running output needs rescaling only when some lane's maximum grew.
-    if (__ballot(mnew != mrun) != 0ull) {
+    // Lazy rescaling: the exponentials are taken against a per-query reference
+    // mrun that moves only when a score exceeds it by more than kLazy (log2
+    // units), so p <= 2^kLazy (exact in f16's range, no f32 overflow over any
+    // sequence) and o, lrun are rescaled only then. The quotient o / lrun is
+    // the same for any reference; with the first block's maximum as reference
+    // later blocks almost never move it, where an exact running maximum grows
+    // in a large share of the blocks of a long sequence.
+    constexpr float kLazy = 8.0f;
+    const bool grow = mloc > mrun + kLazy;  // always true in the first block
+    if (__ballot(grow) != 0ull) {
+      const float mnew = grow ? mloc : mrun;
+      // v_exp_f32 directly: the argument is <= 0 or -inf (exp2 -> 0).
+      const float corr = __builtin_amdgcn_exp2f(mrun - mnew);
+      lrun *= corr;
 #pragma unroll
       for (int t = 0; t < HD / 32; ++t) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) o[t][e] *= corr;
       }
+      mrun = mnew;
     }
-    mrun = mnew;
+    float psum = 0.f;
+    v8h pf[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      // s - mrun <= kLazy, or -inf for masked keys (exp2 -> 0).
+      const float p = __builtin_amdgcn_exp2f(s[e] - mrun);
+      psum += p;
+      pf[e >> 3][e & 7] = (_Float16)p;
+    }
+    psum += __shfl_xor(psum, 32);
+    lrun += psum;
     // O^T += V^T P^T. K step st covers the keys this lane's P holds for
     // e in [8 st, 8 st + 8): 16 st + {4g..4g+3} and 16 st + 8 + {4g..4g+3}.
 #pragma unroll
@@ -762,13 +772,21 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd32(EncAttnArgs a) {
+// A register budget of at most 256 VGPRs (here: at least 3 or 2 waves per
+// SIMD) makes the compiler use the MFMA forms that accumulate in ordinary
+// VGPRs. With the 512-register budget of one wave per SIMD it picks the
+// accumulation-register forms and copies S and O between the two register
+// files in every key block (about 110 extra VALU moves per block at hd 64).
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void eos_enc_attn_hd32(EncAttnArgs a) {
   attn_body<32>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd64(EncAttnArgs a) {
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void eos_enc_attn_hd64(EncAttnArgs a) {
   attn_body<64>(a);
 }
-extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd128(EncAttnArgs a) {
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void eos_enc_attn_hd128(EncAttnArgs a) {
   attn_body<128>(a);
 }
 
