@@ -19,6 +19,7 @@
 #include <stdint.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "enc_args.h"
 
@@ -278,6 +279,16 @@ EOS_DEV void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{}).
+template <typename F, int... I>
+EOS_DEV void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+EOS_DEV void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // LDS byte address of a pointer into a __shared__ array.
 typedef __attribute__((address_space(3))) const uint16_t lds_u16;
 EOS_DEV uint32_t lds_addr(const uint16_t* p) { return (uint32_t)(uintptr_t)(lds_u16*)p; }
@@ -315,12 +326,12 @@ EOS_DEV void lgkm_wait(v8h (&f)[N]) {
 
 // Workgroup tile (64 WM) x (64 WN) over 4 wavefronts in a 2 x 2 grid, each
 // wavefront (32 WM) x (32 WN) = WM x WN MFMA 32x32 blocks. K advances in
-// chunks of 32 through three LDS stages filled by direct global -> LDS loads
-// (16 bytes per lane, no staging registers): chunk kc + 2 is requested while
-// chunk kc is computed, so each load has two chunks of MFMAs to land. Per
-// chunk a wavefront issues WM + WN loads (16 rows each) and waits with
-// vmcnt(WM + WN), i.e. for everything but the newest chunk, then one barrier
-// makes the whole stage visible.
+// chunks of 32 through NS LDS stages filled by direct global -> LDS loads
+// (16 bytes per lane, no staging registers): chunk kc + NS - 1 is requested
+// while chunk kc is computed, so each load has NS - 1 chunks of MFMAs to
+// land. Per chunk a wavefront issues WM + WN loads (16 rows each) and waits
+// with vmcnt((NS - 2)(WM + WN)), i.e. for everything but the newer chunks,
+// then one barrier makes the whole stage visible.
 // Epilogue: v = scale[n] * acc + bias[n]; mode 1 erf GELU, 2 tanh GELU,
 // 3 + residual[m][n] (out may alias residual: each element is read and
 // written by the same lane).
@@ -328,7 +339,7 @@ EOS_DEV void lgkm_wait(v8h (&f)[N]) {
 // output row (row-major out). TR = true (columns from vt_col0 on, when vt is
 // given): A first, a lane's results lie along an output column, stored
 // transposed into vt[col - vt_col0][row].
-template <int WM, int WN, bool TR>
+template <int WM, int WN, int NS, bool TR>
 EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t* st) {
   constexpr int BM = 64 * WM, BN = 64 * WN, ST = (BM + BN) * kBK;  // halves per stage
   constexpr int NLD = WM + WN;  // 16-row loads per wavefront per chunk
@@ -404,32 +415,27 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
     lgkm_wait(f1);
     mma(f1);
   };
-  uint16_t* const st0 = st;
-  uint16_t* const st1 = st + ST;
-  uint16_t* const st2 = st + 2 * ST;
-  issue(st0, 0);
-  issue(st1, 1);
-  // Three chunks per pass, one stage each; one back-edge and no exit in the
-  // body. The stage refilled at a step was last read in the step before, and
-  // the step's barrier orders that read before the refill. The barrier is the
-  // bare s_barrier: a fenced one (__syncthreads) must wait for every
-  // outstanding direct-to-LDS load, including the chunk just requested, and
-  // vmcnt(NLD) has already made this wavefront's part of the stage land.
+  // Chunks 0 .. NS - 2 are requested up front; at the step of chunk c the
+  // stage of chunk c - 1 (read at the step before, ordered by this step's
+  // barrier) receives chunk c + NS - 1, so NS - 1 chunks are in flight.
+#pragma unroll
+  for (int c = 0; c < NS - 1; ++c) issue(st + c * ST, c);
+  // NS chunks per pass, one stage each, stage indices static (the fragment
+  // reads address stages by immediate offsets); one back-edge and no exit in
+  // the body. The barrier is the bare s_barrier: a fenced one
+  // (__syncthreads) must wait for every outstanding direct-to-LDS load,
+  // including the chunks just requested, and vmcnt has already made this
+  // wavefront's part of the stage land.
   int kc = 0;
   do {
-    wait_vmcnt<NLD>();
-    __builtin_amdgcn_s_barrier();
-    issue(st2, kc + 2);
-    compute(std::integral_constant<int, 0>{});
-    wait_vmcnt<NLD>();
-    __builtin_amdgcn_s_barrier();
-    issue(st0, kc + 3);
-    if (kc + 1 < nk) compute(std::integral_constant<int, 1>{});
-    wait_vmcnt<NLD>();
-    __builtin_amdgcn_s_barrier();
-    issue(st1, kc + 4);
-    if (kc + 2 < nk) compute(std::integral_constant<int, 2>{});
-    kc += 3;
+    static_for<NS>([&](auto sc) {
+      constexpr int S = decltype(sc)::value;
+      wait_vmcnt<(NS - 2) * NLD>();
+      __builtin_amdgcn_s_barrier();
+      issue(st + ((S + NS - 1) % NS) * ST, kc + S + NS - 1);
+      if (S == 0 || kc + S < nk) compute(sc);
+    });
+    kc += NS;
   } while (kc < nk);
   // No LDS write may land after the workgroup exits.
   wait_vmcnt<0>();
@@ -495,10 +501,10 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
   }
 }
 
-template <int WM, int WN>
+template <int WM, int WN, int NS>
 EOS_DEV void gemm_body(const EncGemmArgs& a) {
   constexpr int BM = 64 * WM, BN = 64 * WN, ST = (BM + BN) * kBK;
-  __shared__ __attribute__((aligned(16))) uint16_t st[3 * ST];
+  __shared__ __attribute__((aligned(16))) uint16_t st[NS * ST];
   const int rows = *a.rows;
   // XCD-aware tile order: workgroup w runs on XCD w % 8 (round-robin
   // dispatch), so XCD x takes row blocks x, x + 8, ... and walks all column
@@ -510,19 +516,19 @@ EOS_DEV void gemm_body(const EncGemmArgs& a) {
   const int m0 = mb * BM, n0 = nb * BN;
   if (m0 >= rows) return;
   if (a.vt != nullptr && n0 >= a.vt_col0)
-    gemm_tile<WM, WN, true>(a, m0, n0, rows, st);
+    gemm_tile<WM, WN, NS, true>(a, m0, n0, rows, st);
   else
-    gemm_tile<WM, WN, false>(a, m0, n0, rows, st);
+    gemm_tile<WM, WN, NS, false>(a, m0, n0, rows, st);
 }
 
 }  // namespace
 
 extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_t128(EncGemmArgs a) {
-  gemm_body<2, 2>(a);
+  gemm_body<2, 2, 3>(a);
 }
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void eos_enc_gemm_t256(EncGemmArgs a) {
-  gemm_body<4, 2>(a);
+  gemm_body<4, 2, 3>(a);
 }
 
 // ------------------------------------------------------------ LayerNorm
