@@ -41,6 +41,28 @@ EOS_DEV float wave_sum(float v) {
   return v;
 }
 
+// Sum over the wavefront without LDS round trips: DPP adds within each row of
+// 16 lanes (quad swaps, then half-row and row mirrors, so every lane of a row
+// holds the row's sum), then the four row sums read into scalars. Uniform
+// result; a different summation order from wave_sum.
+template <int CTRL>
+EOS_DEV float dpp_shuffled(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+EOS_DEV float wave_sum_dpp(float v) {
+  v += dpp_shuffled<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_shuffled<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_shuffled<0x141>(v);  // row_half_mirror
+  v += dpp_shuffled<0x140>(v);  // row_mirror
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // erf(z) by Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26
 // (|error| <= 1.5e-7): one reciprocal, one exp2 and a degree-5 polynomial,
 // branch-free (the library erff evaluates two polynomials in divergent
@@ -68,6 +90,24 @@ EOS_DEV float gelu(float x, int kind) {
   if (kind == 1) return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
   const float u = 0.7978845608f * (x + 0.044715f * x * x * x);
   return 0.5f * x * (1.0f + tanh_exp(u));
+}
+
+// erf GELU x Phi(x) for the GEMM epilogue, the same Abramowitz & Stegun
+// 7.1.26 approximation as erf_as rearranged: with h(a) = erfc(a / sqrt 2) / 2
+// ~ t (c1 + t (c2 + ...)) exp(-a^2 / 2), t = 1 / (1 + (p / sqrt 2) a), the
+// c_i half the A&S coefficients, Phi(x) = 1 - h(x) for x >= 0 and h(-x)
+// otherwise, so GELU(x) = max(x, 0) - |x| h(|x|): no sign fix-up, and the
+// 1 / sqrt 2 and 1 / 2 folded into the constants.
+EOS_DEV float gelu_erf_fast(float x) {
+  const float a = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.2316418883f, a, 1.0f));
+  float p = __builtin_fmaf(0.5307027145f, t, -0.7265760135f);
+  p = __builtin_fmaf(p, t, 0.7107068705f);
+  p = __builtin_fmaf(p, t, -0.142248368f);
+  p = __builtin_fmaf(p, t, 0.127414796f);
+  p *= t;
+  const float e = __builtin_amdgcn_exp2f((x * -0.72134752044448170f) * x);  // exp(-x^2 / 2)
+  return __builtin_fmaf(-a, p * e, fmaxf(x, 0.0f));
 }
 
 }  // namespace
@@ -245,14 +285,14 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
       s += v[j];
     }
   }
-  const float mean = wave_sum(s) / (float)a.hidden;
+  const float mean = wave_sum_dpp(s) / (float)a.hidden;
   float q = 0.f;
 #pragma unroll
   for (int j = 0; j < kMaxPer; ++j) {
     const int c = lane + 64 * j;
     if (c < a.hidden) q += (v[j] - mean) * (v[j] - mean);
   }
-  const float inv = 1.0f / sqrtf(wave_sum(q) / (float)a.hidden + a.eps);
+  const float inv = 1.0f / sqrtf(wave_sum_dpp(q) / (float)a.hidden + a.eps);
 #pragma unroll
   for (int j = 0; j < kMaxPer; ++j) {
     const int c = lane + 64 * j;
@@ -469,35 +509,48 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
   // l32 of the block and column 8(e/4) + 4g + e%4: each group of 4
   // elements is 4 consecutive columns of one row, written as one 8-byte
   // store (and the residual read as one 8-byte load).
+  // One straight-line epilogue per mode (the mode is uniform).
+  auto epilogue = [&](auto epi_c) {
+    constexpr int EPI = decltype(epi_c)::value;
 #pragma unroll
-  for (int i = 0; i < WM; ++i) {
-    const int row = m0 + wm * 32 * WM + i * 32 + l32;
-    if (row >= rows) continue;
-    uint16_t* orow = a.out + (size_t)row * a.n;
-    const uint16_t* rrow = a.residual != nullptr ? a.residual + (size_t)row * a.n : nullptr;
+    for (int i = 0; i < WM; ++i) {
+      const int row = m0 + wm * 32 * WM + i * 32 + l32;
+      if (row >= rows) continue;
+      uint16_t* orow = a.out + (size_t)row * a.n;
+      const uint16_t* rrow = EPI == 3 ? a.residual + (size_t)row * a.n : nullptr;
 #pragma unroll
-    for (int j = 0; j < WN; ++j) {
+      for (int j = 0; j < WN; ++j) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int col = n0 + wn * 32 * WN + j * 32 + 8 * q + 4 * g;
-        const float4 sc = *reinterpret_cast<const float4*>(a.wscale + col);
-        const float4 bi = *reinterpret_cast<const float4*>(a.bias + col);
-        float v[4] = {acc[i][j][4 * q] * sc.x + bi.x, acc[i][j][4 * q + 1] * sc.y + bi.y,
-                      acc[i][j][4 * q + 2] * sc.z + bi.z, acc[i][j][4 * q + 3] * sc.w + bi.w};
-        if (a.epi == 3) {
-          const v4h r = *reinterpret_cast<const v4h*>(rrow + col);
+        for (int q = 0; q < 4; ++q) {
+          const int col = n0 + wn * 32 * WN + j * 32 + 8 * q + 4 * g;
+          const float4 sc = *reinterpret_cast<const float4*>(a.wscale + col);
+          const float4 bi = *reinterpret_cast<const float4*>(a.bias + col);
+          float v[4] = {acc[i][j][4 * q] * sc.x + bi.x, acc[i][j][4 * q + 1] * sc.y + bi.y,
+                        acc[i][j][4 * q + 2] * sc.z + bi.z, acc[i][j][4 * q + 3] * sc.w + bi.w};
+          if constexpr (EPI == 3) {
+            const v4h r = *reinterpret_cast<const v4h*>(rrow + col);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) v[t] += (float)r[t];
-        } else if (a.epi != 0) {
+            for (int t = 0; t < 4; ++t) v[t] += (float)r[t];
+          } else if constexpr (EPI == 1) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) v[t] = gelu(v[t], a.epi);
+            for (int t = 0; t < 4; ++t) v[t] = gelu_erf_fast(v[t]);
+          } else if constexpr (EPI == 2) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[t] = gelu(v[t], 2);
+          }
+          v4h o;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) o[t] = (_Float16)v[t];
+          *reinterpret_cast<v4h*>(orow + col) = o;
         }
-        v4h o;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) o[t] = (_Float16)v[t];
-        *reinterpret_cast<v4h*>(orow + col) = o;
       }
     }
+  };
+  switch (a.epi) {
+    case 1: epilogue(std::integral_constant<int, 1>{}); break;
+    case 2: epilogue(std::integral_constant<int, 2>{}); break;
+    case 3: epilogue(std::integral_constant<int, 3>{}); break;
+    default: epilogue(std::integral_constant<int, 0>{}); break;
   }
 }
 
@@ -566,7 +619,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_ln(EncLnArgs a) {
       s += x[t][e];
     }
   }
-  const float mean = wave_sum(s) / (float)a.hidden;
+  const float mean = wave_sum_dpp(s) / (float)a.hidden;
   float q = 0.f;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -575,7 +628,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_ln(EncLnArgs a) {
       for (int e = 0; e < 8; ++e) q += (x[t][e] - mean) * (x[t][e] - mean);
     }
   }
-  const float inv = 1.0f / sqrtf(wave_sum(q) / (float)a.hidden + a.eps);
+  const float inv = 1.0f / sqrtf(wave_sum_dpp(q) / (float)a.hidden + a.eps);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int c = lane + 64 * t;
