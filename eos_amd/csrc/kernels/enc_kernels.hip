@@ -758,18 +758,21 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
         mloc = fmaxf(mloc, s[e]);
       }
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
     // Lazy rescaling: the exponentials are taken against a per-query reference
     // mrun that moves only when a score exceeds it by more than kLazy (log2
     // units), so p <= 2^kLazy (exact in f16's range, no f32 overflow over any
     // sequence) and o, lrun are rescaled only then. The quotient o / lrun is
     // the same for any reference; with the first block's maximum as reference
     // later blocks almost never move it, where an exact running maximum grows
-    // in a large share of the blocks of a long sequence.
+    // in a large share of the blocks of a long sequence. The two lanes of a
+    // query (g = 0, 1) hold different keys: only the rare rescale combines
+    // their maxima, so both keep the same reference; lrun is each lane's own
+    // partial sum (both are rescaled alike), added at the end.
     constexpr float kLazy = 8.0f;
-    const bool grow = mloc > mrun + kLazy;  // always true in the first block
+    const bool grow = mloc > mrun + kLazy;  // true in the first block
     if (__ballot(grow) != 0ull) {
-      const float mnew = grow ? mloc : mrun;
+      const float mpair = fmaxf(mloc, __shfl_xor(mloc, 32));
+      const float mnew = mpair > mrun + kLazy ? mpair : mrun;
       // v_exp_f32 directly: the argument is <= 0 or -inf (exp2 -> 0).
       const float corr = __builtin_amdgcn_exp2f(mrun - mnew);
       lrun *= corr;
@@ -789,7 +792,6 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
       psum += p;
       pf[e >> 3][e & 7] = (_Float16)p;
     }
-    psum += __shfl_xor(psum, 32);
     lrun += psum;
     // O^T += V^T P^T. K step st covers the keys this lane's P holds for
     // e in [8 st, 8 st + 8): 16 st + {4g..4g+3} and 16 st + 8 + {4g..4g+3}.
@@ -806,6 +808,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     if (more) kv_store(buf ^ 1);
     __syncthreads();
   }
+  const float lsum = lrun + __shfl_xor(lrun, 32);  // before any lane leaves
   if (!qlive) {
     // Pad rows of the sequence's 8-row slot get zeros: no kernel writes them
     // otherwise, and the memory may hold anything a freed buffer left (a NaN
@@ -819,7 +822,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     }
     return;
   }
-  const float inv = lrun > 0.f ? 1.0f / lrun : 0.f;
+  const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
   uint16_t* orow = a.ctx + (size_t)(off + qi) * a.hidden + h * HD;
 #pragma unroll
   for (int t = 0; t < HD / 32; ++t) {
