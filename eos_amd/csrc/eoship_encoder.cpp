@@ -246,8 +246,9 @@ struct EosHipEncoder {
   }
 };
 
-// Shapes the kernels are instantiated for: LN-GEMM row widths 128..768,
-// attention head dims 32/64/128, GEMM N tiles of 128.
+// Shapes the kernels support: hidden widths 128..768 (embed and LayerNorm
+// hold a row in one wavefront; every GEMM N a multiple of the 128-column
+// tile), attention head dims 32/64/128, FFN widths in multiples of 128.
 static int check_dims(int H, int heads, int F, const char* what, char** err) {
   if (H != 128 && H != 256 && H != 384 && H != 512 && H != 768)
     return set_err(err, "%s: hidden must be 128, 256, 384, 512 or 768 (got %d)", what, H);
