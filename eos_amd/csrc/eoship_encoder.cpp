@@ -48,6 +48,10 @@ struct DevLayer {
   float* b_2 = nullptr;
   float* g2 = nullptr;
   float* be2 = nullptr;
+  // BERT family: int8 copies of the QKV and FFN-up codes for the W8A8 GEMMs
+  // (their inputs are LayerNorm / embedding outputs, which carry int8 rows).
+  int8_t* w_qkv8 = nullptr;
+  int8_t* w_18 = nullptr;
 };
 
 }  // namespace
@@ -68,6 +72,10 @@ struct EosHipEncoder {
   size_t cap_rows = 0;
   int cap_batch = 0;
   uint16_t *h = nullptr, *qkv = nullptr, *ctx = nullptr, *mid = nullptr;
+  // int8 copy of h with one scale per row (BERT family: QKV and FFN-up run on
+  // int8 MFMA with these as activations)
+  int8_t* h8 = nullptr;
+  float* hs = nullptr;
   float* pool_part = nullptr;  // [batch][chunks][hidden] pool partial sums
   // V of the QKV projection, feature-major [hidden][vt_ld] (zeroed padding
   // past the rows, so attention may read whole 16-byte key groups)
@@ -82,7 +90,8 @@ struct EosHipEncoder {
   ~EosHipEncoder() {
     for (void* p : owned)
       if (p) hipFree(p);
-    void* act[] = {h, qkv, ctx, mid, pool_part, vt, row_b, row_t, seq_off, seq_cnt, total, status, io};
+    void* act[] = {h, qkv, ctx, mid, h8, hs, pool_part, vt, row_b, row_t, seq_off, seq_cnt, total,
+                   status, io};
     for (void* p : act)
       if (p) hipFree(p);
   }
@@ -133,10 +142,13 @@ struct EosHipEncoder {
   int ensure_activations(int batch, int tokens, char** err) {
     const size_t rows = row_capacity(batch, tokens);
     if (rows <= cap_rows && batch <= cap_batch) return 0;
-    void* act[] = {h, qkv, ctx, mid, pool_part, vt, row_b, row_t, seq_off, seq_cnt, total, status};
+    void* act[] = {h, qkv, ctx, mid, h8, hs, pool_part, vt, row_b, row_t, seq_off, seq_cnt, total,
+                   status};
     for (void* p : act)
       if (p) hipFree(p);
     h = qkv = ctx = mid = nullptr;
+    h8 = nullptr;
+    hs = nullptr;
     pool_part = nullptr;
     vt = nullptr;
     row_b = row_t = seq_off = seq_cnt = total = status = nullptr;
@@ -147,6 +159,8 @@ struct EosHipEncoder {
         rt->alloc(rows * 3 * H * 2, reinterpret_cast<void**>(&qkv), err) ||
         rt->alloc(rows * H * 2, reinterpret_cast<void**>(&ctx), err) ||
         rt->alloc(rows * F * 2, reinterpret_cast<void**>(&mid), err) ||
+        rt->alloc(rows * H, reinterpret_cast<void**>(&h8), err) ||
+        rt->alloc(rows * 4, reinterpret_cast<void**>(&hs), err) ||
         // chunks of any later shape within the caps: batch' * ceil(tokens' /
         // 256) <= rows / 256 + batch
         rt->alloc((rows / kPoolChunk + (size_t)batch) * H * 4,
@@ -199,41 +213,51 @@ struct EosHipEncoder {
     em.ntype = desc.type_vocab;
     em.eps = desc.ln_eps;
     em.mode = family;
+    // BERT family: QKV and FFN-up run W8A8, so the embedding and every
+    // LayerNorm also write their rows as int8 codes with per-row scales.
+    const bool a8 = family == 0;
+    em.q8 = a8 ? h8 : nullptr;
+    em.qscale = a8 ? hs : nullptr;
     if (rt->launch("eos_enc_embed", dim3((max_rows + 3) / 4), dim3(256), 0, &em, err) != 0) return 1;
     char attn_name[48];
     snprintf(attn_name, sizeof(attn_name), "eos_enc_attn_hd%d", hd);
     // GEMM tiles: 256 x 128 for wide outputs, 128 x 128 for hidden-width ones
     // (more workgroups for the smaller N).
-    auto gemm = [&](const uint16_t* A, const uint16_t* W, const float* sc, const float* b,
-                    uint16_t* out, const uint16_t* res, int n, int k, int epi, const char* label,
-                    uint16_t* vt_out = nullptr) {
+    // W8 != NULL: int8 codes of W; A is then h8 with the row scales hs.
+    auto gemm = [&](const uint16_t* A, const uint16_t* W, const int8_t* W8, const float* sc,
+                    const float* b, uint16_t* out, const uint16_t* res, int n, int k, int epi,
+                    const char* label, uint16_t* vt_out = nullptr) {
       const bool wide = n >= 1024;
       const int bm = wide ? 256 : 128;
-      EncGemmArgs g{A, W, sc, b, out, total, res, max_rows, n, k, epi, vt_out, 2 * H, vt_ld};
+      EncGemmArgs g{A, W, sc, b, out, total, res, max_rows, n, k, epi, vt_out, 2 * H, vt_ld,
+                    W8 != nullptr ? h8 : nullptr, W8 != nullptr ? hs : nullptr, W8};
+      const char* name = W8 != nullptr ? (wide ? "eos_enc_gemm8_t256" : "eos_enc_gemm8_t128")
+                                       : (wide ? "eos_enc_gemm_t256" : "eos_enc_gemm_t128");
       // One-dimensional grid: n / 128 column tiles for each row block, row
       // blocks rounded up to a multiple of 8 (the kernel maps workgroups to
       // tiles per XCD; tiles past the rows exit at once).
       const unsigned mblk = (unsigned)(((max_rows + bm - 1) / bm + 7) / 8 * 8);
-      return rt->launch(wide ? "eos_enc_gemm_t256" : "eos_enc_gemm_t128",
-                        dim3((unsigned)(n / 128) * mblk), dim3(256), 0, &g, err, label);
+      return rt->launch(name, dim3((unsigned)(n / 128) * mblk), dim3(256), 0, &g, err, label);
     };
     auto layer_norm = [&](const float* gm, const float* bt) {
-      EncLnArgs l{h, gm, bt, total, max_rows, H, desc.ln_eps};
+      EncLnArgs l{h, gm, bt, total, max_rows, H, desc.ln_eps, a8 ? h8 : nullptr, a8 ? hs : nullptr};
       return rt->launch("eos_enc_ln", dim3((unsigned)((max_rows + 3) / 4)), dim3(256), 0, &l, err,
                         "enc_ln");
     };
     for (const DevLayer& L : layers) {
       // Q and K rows into qkv, V feature-major into vt.
-      if (gemm(h, L.w_qkv, L.s_qkv, L.b_qkv, qkv, nullptr, 3 * H, H, 0, "enc_gemm_qkv", vt) != 0)
+      if (gemm(h, L.w_qkv, a8 ? L.w_qkv8 : nullptr, L.s_qkv, L.b_qkv, qkv, nullptr, 3 * H, H, 0,
+               "enc_gemm_qkv", vt) != 0)
         return 1;
       EncAttnArgs at{qkv, vt, ctx, seq_off, seq_cnt, batch, nh, H, tokens, vt_ld,
                      (float)(1.4426950408889634 / std::sqrt((double)hd))};
       if (rt->launch(attn_name, dim3((tokens + 127) / 128, nh, batch), dim3(256), 0, &at, err) != 0)
         return 1;
-      if (gemm(ctx, L.w_o, L.s_o, L.b_o, h, h, H, H, 3, "enc_gemm_o") != 0 ||
+      if (gemm(ctx, L.w_o, nullptr, L.s_o, L.b_o, h, h, H, H, 3, "enc_gemm_o") != 0 ||
           layer_norm(L.g1, L.be1) != 0 ||
-          gemm(h, L.w_1, L.s_1, L.b_1, mid, nullptr, F, H, desc.gelu, "enc_gemm_ffn_up") != 0 ||
-          gemm(mid, L.w_2, L.s_2, L.b_2, h, h, H, F, 3, "enc_gemm_ffn_down") != 0 ||
+          gemm(h, L.w_1, a8 ? L.w_18 : nullptr, L.s_1, L.b_1, mid, nullptr, F, H, desc.gelu,
+               "enc_gemm_ffn_up") != 0 ||
+          gemm(mid, L.w_2, nullptr, L.s_2, L.b_2, h, h, H, F, 3, "enc_gemm_ffn_down") != 0 ||
           layer_norm(L.g2, L.be2) != 0)
         return 1;
     }
@@ -314,7 +338,9 @@ int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const 
         enc->upload_codes(&d.w_2, s.w_2, (size_t)H * F, err) ||
         enc->upload(&d.s_2, s.s_2, (size_t)H, err) || enc->upload(&d.b_2, s.b_2, (size_t)H, err) ||
         enc->upload(&d.g2, s.ln2_gamma, (size_t)H, err) ||
-        enc->upload(&d.be2, s.ln2_beta, (size_t)H, err))
+        enc->upload(&d.be2, s.ln2_beta, (size_t)H, err) ||
+        enc->upload(&d.w_qkv8, s.w_qkv, (size_t)3 * H * H, err) ||
+        enc->upload(&d.w_18, s.w_1, (size_t)F * H, err))
       return fail();
     enc->layers.push_back(d);
   }

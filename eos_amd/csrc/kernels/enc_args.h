@@ -37,6 +37,8 @@ struct EncEmbedArgs {
   int tokens, hidden, vocab, npos, ntype;
   float eps;
   int mode;
+  int8_t* q8;               // optional int8 copy of out, as for EncLnArgs
+  float* qscale;
 };
 
 // out[m][n] = epi(scale[n] * sum_k a[m][k] w[n][k] + bias[n]) for m < *rows.
@@ -54,6 +56,11 @@ struct EncGemmArgs {
   int max_rows, n, k, epi;
   uint16_t* vt;            // optional: columns >= vt_col0 go to vt[col - vt_col0][row]
   int vt_col0, vt_ld;      // (vt rows hold vt_ld entries, the first max_rows rounded up to 4 + 32 padding)
+  // int8 kernels (eos_enc_gemm8_*): A as int8 codes with one f32 scale per
+  // row (a = a8 * ascale[row]) and W as int8 codes; a and w are unused.
+  const int8_t* a8;        // [rows][k]
+  const float* ascale;     // [rows]
+  const int8_t* w8;        // [n][k]
 };
 
 // In-place affine LayerNorm of h [rows][hidden] f16 (hidden % 8 == 0, <= 1024).
@@ -64,6 +71,10 @@ struct EncLnArgs {
   const int32_t* rows;
   int max_rows, hidden;
   float eps;
+  // Optional (q8 != NULL): each output row also as int8 codes, q8 = rint(y /
+  // qscale) with qscale = max|y| / 127 (0 for a zero row), y the f32 result.
+  int8_t* q8;              // [rows][hidden]
+  float* qscale;           // [rows]
 };
 
 // Masked multi-head attention over packed rows: every active row of a

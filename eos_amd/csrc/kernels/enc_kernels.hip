@@ -27,6 +27,7 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 #define EOS_DEV __device__ __forceinline__
 
@@ -61,6 +62,27 @@ EOS_DEV float wave_sum_dpp(float v) {
   const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
   const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
   return (r0 + r1) + (r2 + r3);
+}
+
+// Maximum over the wavefront, the same pattern as wave_sum_dpp.
+EOS_DEV float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_shuffled<0xb1>(v));
+  v = fmaxf(v, dpp_shuffled<0x4e>(v));
+  v = fmaxf(v, dpp_shuffled<0x141>(v));
+  v = fmaxf(v, dpp_shuffled<0x140>(v));
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// Symmetric per-row int8 quantization: scale = max|y| / 127 (0 for a zero
+// row), code = rint(y * 127 / max|y|), |code| <= 127.
+EOS_DEV float q8_inv(float amax) { return amax > 0.0f ? 127.0f / amax : 0.0f; }
+EOS_DEV int8_t q8_code(float y, float inv) {
+  return (int8_t)fminf(fmaxf(rintf(y * inv), -127.0f), 127.0f);
 }
 
 // erf(z) by Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26
@@ -232,6 +254,10 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
   if (t < 0) {
     // Pad row (sequence alignment): zeros, never pooled or attended to.
     for (int c = lane; c < a.hidden; c += 64) a.out[(size_t)row * a.hidden + c] = 0;
+    if (a.q8 != nullptr) {
+      for (int c = lane; c < a.hidden; c += 64) a.q8[(size_t)row * a.hidden + c] = 0;
+      if (lane == 0) a.qscale[row] = 0.0f;
+    }
     return;
   }
   int id = a.ids[(size_t)b * a.tokens + t];
@@ -293,10 +319,25 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
     if (c < a.hidden) q += (v[j] - mean) * (v[j] - mean);
   }
   const float inv = 1.0f / sqrtf(wave_sum_dpp(q) / (float)a.hidden + a.eps);
+  float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < kMaxPer; ++j) {
     const int c = lane + 64 * j;
-    if (c < a.hidden) a.out[(size_t)row * a.hidden + c] = f2h((v[j] - mean) * inv * a.gamma[c] + a.beta[c]);
+    if (c < a.hidden) {
+      v[j] = (v[j] - mean) * inv * a.gamma[c] + a.beta[c];
+      a.out[(size_t)row * a.hidden + c] = f2h(v[j]);
+      amax = fmaxf(amax, fabsf(v[j]));
+    }
+  }
+  if (a.q8 != nullptr) {
+    amax = wave_max_dpp(amax);
+    const float qi = q8_inv(amax);
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j) {
+      const int c = lane + 64 * j;
+      if (c < a.hidden) a.q8[(size_t)row * a.hidden + c] = q8_code(v[j], qi);
+    }
+    if (lane == 0) a.qscale[row] = amax / 127.0f;
   }
 }
 
@@ -379,9 +420,10 @@ EOS_DEV void lgkm_wait(v8h (&f)[N]) {
 // output row (row-major out). TR = true (columns from vt_col0 on, when vt is
 // given): A first, a lane's results lie along an output column, stored
 // transposed into vt[col - vt_col0][row].
-template <int WM, int WN, int NS, bool TR>
+template <int WM, int WN, int NS, bool TR, bool I8>
 EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t* st) {
   constexpr int BM = 64 * WM, BN = 64 * WN, ST = (BM + BN) * kBK;  // halves per stage
+  constexpr int ESZ = I8 ? 1 : 2;  // operand bytes: a 64-byte chunk is 32 halves or 64 int8
   constexpr int NLD = WM + WN;  // 16-row loads per wavefront per chunk
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -390,20 +432,23 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
   // for u < WM, W rows after): lane i writes slot i % 4 of row
   // 16 (wave + 4u) + i / 4 and so reads chunk swz(row, i % 4) of that row.
   // Rows past the matrix are clamped to its last row (computed, never stored).
-  const uint16_t* src[NLD];
+  const char* const abytes = I8 ? (const char*)a.a8 : (const char*)a.a;
+  const char* const wbytes = I8 ? (const char*)a.w8 : (const char*)a.w;
+  const size_t rowb = (size_t)a.k * ESZ;
+  const char* src[NLD];
 #pragma unroll
   for (int u = 0; u < NLD; ++u) {
     const int r = 16 * (wave + 4 * u) + (lane >> 2);
     const int c = swz(r, lane & 3);
     if (u < WM)
-      src[u] = a.a + (size_t)min(m0 + r, a.max_rows - 1) * a.k + c * 8;
+      src[u] = abytes + (size_t)min(m0 + r, a.max_rows - 1) * rowb + c * 16;
     else
-      src[u] = a.w + (size_t)(n0 + r - BM) * a.k + c * 8;
+      src[u] = wbytes + (size_t)(n0 + r - BM) * rowb + c * 16;
   }
-  const int nk = a.k / kBK;
+  const int nk = (int)(rowb / 64);
   // Chunks past the end are clamped to the last one (loaded, never computed).
   auto issue = [&](uint16_t* st, int kc) {
-    const int k0 = min(kc, nk - 1) * kBK;
+    const int k0 = min(kc, nk - 1) * 64;
 #pragma unroll
     for (int u = 0; u < NLD; ++u)
       __builtin_amdgcn_global_load_lds(src[u] + k0, st + 16 * 32 * (wave + 4 * u), 16, 0, 0);
@@ -419,11 +464,12 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
     abase[s] = st_b + 2 * (wm * 32 * WM * kBK + fo);
     bbase[s] = st_b + 2 * ((BM + wn * 32 * WN) * kBK + fo);
   }
-  v16f acc[WM][WN];
+  using Acc = std::conditional_t<I8, v16i, v16f>;
+  Acc acc[WM][WN];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < WN; ++j) acc[i][j] = v16f{0};
+    for (int j = 0; j < WN; ++j) acc[i][j] = Acc{0};
   // Fragments of K step S of stage STG (read, then awaited).
   auto frags = [&](auto stg_c, auto s_c, v8h (&f)[WM + WN]) {
     constexpr int STG = decltype(stg_c)::value, S = decltype(s_c)::value;
@@ -440,10 +486,16 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
     for (int i = 0; i < WM; ++i)
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
-        if constexpr (TR)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], f[WM + j], acc[i][j], 0, 0, 0);
+        // int8: 32 K values (16 bytes) per lane, the same bytes of the stage
+        // as 16 halves, so addressing and layout are shared.
+        const v8h& x = TR ? f[i] : f[WM + j];
+        const v8h& y = TR ? f[WM + j] : f[i];
+        if constexpr (I8)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(v4i, x),
+                                                            __builtin_bit_cast(v4i, y), acc[i][j],
+                                                            0, 0, 0);
         else
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[WM + j], f[i], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x, y, acc[i][j], 0, 0, 0);
       }
   };
   auto compute = [&](auto stg_c) {
@@ -495,9 +547,21 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
         for (int q = 0; q < 4; ++q) {
           const int row = m0 + wm * 32 * WM + i * 32 + 8 * q + 4 * g;
           if (row < rows) {
+            // int8: the row scales of the 4 rows (row is a multiple of 4 and
+            // rows of 8, so all 4 are below rows).
+            float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+            if constexpr (I8) {
+              const float4 r4 = *reinterpret_cast<const float4*>(a.ascale + row);
+              rs[0] = r4.x, rs[1] = r4.y, rs[2] = r4.z, rs[3] = r4.w;
+            }
             v4h o;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) o[t] = (_Float16)(acc[i][j][4 * q + t] * sc + bi);
+            for (int t = 0; t < 4; ++t) {
+              if constexpr (I8)
+                o[t] = (_Float16)((float)acc[i][j][4 * q + t] * (sc * rs[t]) + bi);
+              else
+                o[t] = (_Float16)(acc[i][j][4 * q + t] * sc + bi);
+            }
             *reinterpret_cast<v4h*>(vrow + row) = o;
           }
         }
@@ -518,15 +582,19 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
       if (row >= rows) continue;
       uint16_t* orow = a.out + (size_t)row * a.n;
       const uint16_t* rrow = EPI == 3 ? a.residual + (size_t)row * a.n : nullptr;
+      const float rs = I8 ? a.ascale[row] : 1.0f;  // int8: the row's activation scale
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int col = n0 + wn * 32 * WN + j * 32 + 8 * q + 4 * g;
-          const float4 sc = *reinterpret_cast<const float4*>(a.wscale + col);
+          float4 sc = *reinterpret_cast<const float4*>(a.wscale + col);
           const float4 bi = *reinterpret_cast<const float4*>(a.bias + col);
-          float v[4] = {acc[i][j][4 * q] * sc.x + bi.x, acc[i][j][4 * q + 1] * sc.y + bi.y,
-                        acc[i][j][4 * q + 2] * sc.z + bi.z, acc[i][j][4 * q + 3] * sc.w + bi.w};
+          if constexpr (I8) sc = make_float4(sc.x * rs, sc.y * rs, sc.z * rs, sc.w * rs);
+          float v[4] = {(float)acc[i][j][4 * q] * sc.x + bi.x,
+                        (float)acc[i][j][4 * q + 1] * sc.y + bi.y,
+                        (float)acc[i][j][4 * q + 2] * sc.z + bi.z,
+                        (float)acc[i][j][4 * q + 3] * sc.w + bi.w};
           if constexpr (EPI == 3) {
             const v4h r = *reinterpret_cast<const v4h*>(rrow + col);
 #pragma unroll
@@ -554,7 +622,7 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
   }
 }
 
-template <int WM, int WN, int NS>
+template <int WM, int WN, int NS, bool I8 = false>
 EOS_DEV void gemm_body(const EncGemmArgs& a) {
   constexpr int BM = 64 * WM, BN = 64 * WN, ST = (BM + BN) * kBK;
   __shared__ __attribute__((aligned(16))) uint16_t st[NS * ST];
@@ -569,9 +637,9 @@ EOS_DEV void gemm_body(const EncGemmArgs& a) {
   const int m0 = mb * BM, n0 = nb * BN;
   if (m0 >= rows) return;
   if (a.vt != nullptr && n0 >= a.vt_col0)
-    gemm_tile<WM, WN, NS, true>(a, m0, n0, rows, st);
+    gemm_tile<WM, WN, NS, true, I8>(a, m0, n0, rows, st);
   else
-    gemm_tile<WM, WN, NS, false>(a, m0, n0, rows, st);
+    gemm_tile<WM, WN, NS, false, I8>(a, m0, n0, rows, st);
 }
 
 }  // namespace
@@ -582,6 +650,17 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm_t128(EncGemmArgs 
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void eos_enc_gemm_t256(EncGemmArgs a) {
   gemm_body<4, 2, 3>(a);
+}
+// W8A8 variant: int8 activation codes with per-row scales (written by the
+// LayerNorm / embedding kernels) times int8 weight codes on
+// v_mfma_i32_32x32x32_i8 (exact int32 sums), scaled by weight scale x row
+// scale in the epilogue.
+extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void eos_enc_gemm8_t256(EncGemmArgs a) {
+  gemm_body<4, 2, 3, true>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm8_t128(EncGemmArgs a) {
+  gemm_body<2, 2, 3, true>(a);
 }
 
 // ------------------------------------------------------------ LayerNorm
@@ -629,6 +708,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_ln(EncLnArgs a) {
     }
   }
   const float inv = 1.0f / sqrtf(wave_sum_dpp(q) / (float)a.hidden + a.eps);
+  float amax = 0.0f;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int c = lane + 64 * t;
@@ -638,9 +718,31 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_ln(EncLnArgs a) {
       const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
       v8h o;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (_Float16)((x[t][e] - mean) * inv * gg[e] + bb[e]);
+      for (int e = 0; e < 8; ++e) {
+        x[t][e] = (x[t][e] - mean) * inv * gg[e] + bb[e];
+        o[e] = (_Float16)x[t][e];
+        amax = fmaxf(amax, fabsf(x[t][e]));
+      }
       *reinterpret_cast<v8h*>(rp + 8 * c) = o;
     }
+  }
+  if (a.q8 != nullptr) {
+    amax = wave_max_dpp(amax);
+    const float qi = q8_inv(amax);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int c = lane + 64 * t;
+      if (c < nch) {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          lo |= (uint32_t)(uint8_t)q8_code(x[t][e], qi) << (8 * e);
+          hi |= (uint32_t)(uint8_t)q8_code(x[t][4 + e], qi) << (8 * e);
+        }
+        *reinterpret_cast<uint2*>(a.q8 + (size_t)row * a.hidden + 8 * c) = make_uint2(lo, hi);
+      }
+    }
+    if (lane == 0) a.qscale[row] = amax / 127.0f;
   }
 }
 
