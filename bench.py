@@ -112,11 +112,14 @@ def encoder_leg(rt, steps: int, name: str = "c3") -> dict:
         "ms_per_forward": ms,
         "config": {"layers": L, "hidden": H, "heads": NH, "ffn": F, "batch": B, "seq": T,
                    "valid_tokens": valid},
-        "dtype": "int8 weights (per-channel scales) x f16 activations on f16 MFMA, f32 accumulate",
+        "dtype": ("QKV and FFN-up: int8 activations (per-row scales) x int8 weights "
+                  "(per-channel scales) on int8 MFMA, exact i32; O, FFN-down: f16 activations x "
+                  "int8 weight codes on f16 MFMA, f32 accumulate; attention f16 MFMA, f32 softmax"),
         "roofline": {"bound": "mfma", "achieved": achieved, "unit": "TFLOP/s",
                      "peak_f16": 2500.0, "frac_f16": achieved / 2500.0,
                      "peak_int8": 5000.0, "frac_int8": achieved / 5000.0,
-                     "flops_per_forward_valid": flops},
+                     "flops_per_forward_valid": flops,
+                     "int8_share_of_gemm_flops": (3 * H * H + H * F) / (4 * H * H + 2 * H * F)},
         "breakdown_ms": kernels,
     }
 
