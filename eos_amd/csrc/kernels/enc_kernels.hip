@@ -255,7 +255,8 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
     // Pad row (sequence alignment): zeros, never pooled or attended to.
     for (int c = lane; c < a.hidden; c += 64) a.out[(size_t)row * a.hidden + c] = 0;
     if (a.q8 != nullptr) {
-      for (int c = lane; c < a.hidden; c += 64) a.q8[(size_t)row * a.hidden + c] = 0;
+      for (int c = lane; c < a.hidden / 16; c += 64)
+        *reinterpret_cast<uint4*>(a.q8 + (size_t)row * a.hidden + 16 * c) = make_uint4(0, 0, 0, 0);
       if (lane == 0) a.qscale[row] = 0.0f;
     }
     return;
@@ -298,7 +299,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
     }
     return;
   }
-  constexpr int kMaxPer = 16;  // hidden <= 1024
+  constexpr int kMaxPer = 12;  // hidden <= 768
   float v[kMaxPer];
   float s = 0.f;
 #pragma unroll
@@ -319,24 +320,39 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
     if (c < a.hidden) q += (v[j] - mean) * (v[j] - mean);
   }
   const float inv = 1.0f / sqrtf(wave_sum_dpp(q) / (float)a.hidden + a.eps);
+  // The f16 outputs are kept (not the f32 values, which would stay live
+  // across the row maximum and cost occupancy); the int8 codes are taken
+  // from them, with the row maximum of the f32 values as the scale.
+  _Float16 y16[kMaxPer];
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < kMaxPer; ++j) {
     const int c = lane + 64 * j;
+    y16[j] = (_Float16)0.0f;
     if (c < a.hidden) {
-      v[j] = (v[j] - mean) * inv * a.gamma[c] + a.beta[c];
-      a.out[(size_t)row * a.hidden + c] = f2h(v[j]);
-      amax = fmaxf(amax, fabsf(v[j]));
+      const float y = (v[j] - mean) * inv * a.gamma[c] + a.beta[c];
+      y16[j] = (_Float16)y;
+      a.out[(size_t)row * a.hidden + c] = __builtin_bit_cast(uint16_t, y16[j]);
+      amax = fmaxf(amax, fabsf(y));
     }
   }
   if (a.q8 != nullptr) {
+    // The codes are staged in this wavefront's LDS row and written with
+    // 16-byte stores. One wavefront writes and reads its own row: LDS
+    // operations of a wavefront complete in order.
+    __shared__ __attribute__((aligned(16))) int8_t qrow[4][1024];
+    int8_t* qr = qrow[threadIdx.x >> 6];
     amax = wave_max_dpp(amax);
     const float qi = q8_inv(amax);
 #pragma unroll
     for (int j = 0; j < kMaxPer; ++j) {
       const int c = lane + 64 * j;
-      if (c < a.hidden) a.q8[(size_t)row * a.hidden + c] = q8_code(v[j], qi);
+      if (c < a.hidden) qr[c] = q8_code((float)y16[j], qi);
     }
+    __builtin_amdgcn_wave_barrier();
+    for (int c = lane; c < a.hidden / 16; c += 64)
+      *reinterpret_cast<uint4*>(a.q8 + (size_t)row * a.hidden + 16 * c) =
+          *reinterpret_cast<const uint4*>(qr + 16 * c);
     if (lane == 0) a.qscale[row] = amax / 127.0f;
   }
 }
