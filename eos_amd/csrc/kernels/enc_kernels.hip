@@ -864,33 +864,48 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     }
     // element e is key k0 + 8(e/4) + 4g + e%4; only the last block of the
     // sequence has keys past its end (masked to -inf).
-    float mloc = -__builtin_inff();
-    if (k0 + KB <= cnt) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
-    } else {
+    if (k0 + KB > cnt) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
         s[e] = key < cnt ? s[e] : -__builtin_inff();
-        mloc = fmaxf(mloc, s[e]);
       }
     }
     // Lazy rescaling: the exponentials are taken against a per-query reference
-    // mrun that moves only when a score exceeds it by more than kLazy (log2
-    // units), so p <= 2^kLazy (exact in f16's range, no f32 overflow over any
-    // sequence) and o, lrun are rescaled only then. The quotient o / lrun is
-    // the same for any reference; with the first block's maximum as reference
-    // later blocks almost never move it, where an exact running maximum grows
-    // in a large share of the blocks of a long sequence. The two lanes of a
-    // query (g = 0, 1) hold different keys: only the rare rescale combines
-    // their maxima, so both keep the same reference; lrun is each lane's own
-    // partial sum (both are rescaled alike), added at the end.
-    constexpr float kLazy = 8.0f;
-    const bool grow = mloc > mrun + kLazy;  // true in the first block
-    if (__ballot(grow) != 0ull) {
+    // mrun that moves only when needed, and o, lrun are rescaled only then (the
+    // quotient o / lrun is the same for any reference). A block is accepted
+    // when every lane's sum of its 16 p stays <= kSafe, so every p fits f16 and
+    // no f32 sum can overflow; otherwise (the first block, where mrun = -inf
+    // gives inf or NaN, or a score above mrun + 12) the reference of that
+    // query moves to the block's maximum, o and lrun are rescaled and the p
+    // recomputed. With the first block's maximum as reference later blocks
+    // almost never move it, where an exact running maximum grows in a large
+    // share of the blocks of a long sequence, and the common path needs no
+    // maximum at all. The two lanes of a query (g = 0, 1) hold different keys
+    // and move their reference together; lrun is each lane's own partial sum
+    // (both are rescaled alike), added at the end.
+    constexpr float kSafe = 4096.0f;
+    float psum;
+    v8h pf[2];
+    auto exps = [&]() {
+      psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        // v_exp_f32 directly: masked keys give exp2(-inf) = 0.
+        const float p = __builtin_amdgcn_exp2f(s[e] - mrun);
+        psum += p;
+        pf[e >> 3][e & 7] = (_Float16)p;
+      }
+    };
+    exps();
+    const bool over = !(psum <= kSafe);  // also true for inf and NaN
+    if (__ballot(over) != 0ull) {
+      float mloc = -__builtin_inff();
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
       const float mpair = fmaxf(mloc, __shfl_xor(mloc, 32));
-      const float mnew = mpair > mrun + kLazy ? mpair : mrun;
+      const bool pover = over || __shfl_xor((int)over, 32) != 0;
+      const float mnew = pover ? fmaxf(mpair, mrun) : mrun;
       // v_exp_f32 directly: the argument is <= 0 or -inf (exp2 -> 0).
       const float corr = __builtin_amdgcn_exp2f(mrun - mnew);
       lrun *= corr;
@@ -900,15 +915,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
         for (int e = 0; e < 16; ++e) o[t][e] *= corr;
       }
       mrun = mnew;
-    }
-    float psum = 0.f;
-    v8h pf[2];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      // s - mrun <= kLazy, or -inf for masked keys (exp2 -> 0).
-      const float p = __builtin_amdgcn_exp2f(s[e] - mrun);
-      psum += p;
-      pf[e >> 3][e & 7] = (_Float16)p;
+      exps();  // now every s - mrun <= 0 for the moved queries
     }
     lrun += psum;
     // O^T += V^T P^T. K step st covers the keys this lane's P holds for
@@ -936,18 +943,23 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
 #pragma unroll
       for (int t = 0; t < HD / 32; ++t)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) prow[t * 32 + 8 * (e >> 2) + 4 * g + (e & 3)] = 0;
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<v4h*>(prow + t * 32 + 8 * q + 4 * g) = v4h{0, 0, 0, 0};
     }
     return;
   }
   const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
   uint16_t* orow = a.ctx + (size_t)(off + qi) * a.hidden + h * HD;
+  // Elements 4q .. 4q + 3 are the 4 consecutive features 8q + 4g .. + 3: one
+  // 8-byte store each.
 #pragma unroll
   for (int t = 0; t < HD / 32; ++t) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int d = t * 32 + 8 * (e >> 2) + 4 * g + (e & 3);
-      orow[d] = f2h(o[t][e] * inv);
+    for (int q = 0; q < 4; ++q) {
+      v4h v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = (_Float16)(o[t][4 * q + j] * inv);
+      *reinterpret_cast<v4h*>(orow + t * 32 + 8 * q + 4 * g) = v;
     }
   }
 }
