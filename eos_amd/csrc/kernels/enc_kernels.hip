@@ -697,12 +697,17 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_ln(EncLnArgs a) {
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int c = lane + 64 * t;
-    const int cc = c < nch ? c : 0;
-    raw[t] = c < nch ? *reinterpret_cast<const v4i*>(rp + 8 * c) : v4i{0, 0, 0, 0};
-    gb[t][0] = *reinterpret_cast<const float4*>(a.gamma + 8 * cc);
-    gb[t][1] = *reinterpret_cast<const float4*>(a.gamma + 8 * cc + 4);
-    gb[t][2] = *reinterpret_cast<const float4*>(a.beta + 8 * cc);
-    gb[t][3] = *reinterpret_cast<const float4*>(a.beta + 8 * cc + 4);
+    raw[t] = v4i{0, 0, 0, 0};
+    gb[t][0] = gb[t][1] = gb[t][2] = gb[t][3] = make_float4(0.f, 0.f, 0.f, 0.f);
+    // Only lanes with a chunk load (at hidden <= 512 the second chunk exists
+    // for no lane, and the wavefront skips those loads).
+    if (c < nch) {
+      raw[t] = *reinterpret_cast<const v4i*>(rp + 8 * c);
+      gb[t][0] = *reinterpret_cast<const float4*>(a.gamma + 8 * c);
+      gb[t][1] = *reinterpret_cast<const float4*>(a.gamma + 8 * c + 4);
+      gb[t][2] = *reinterpret_cast<const float4*>(a.beta + 8 * c);
+      gb[t][3] = *reinterpret_cast<const float4*>(a.beta + 8 * c + 4);
+    }
   }
   float s = 0.f;
 #pragma unroll
