@@ -172,7 +172,11 @@ struct EosHipEncoder {
         rt->alloc(4, reinterpret_cast<void**>(&total), err) ||
         rt->alloc(4, reinterpret_cast<void**>(&status), err))
       return 1;
-    vt_ld = (int)((rows + 7) / 8 * 8 + 32);
+    // At least 64 zeroed entries past the rows (attention reads whole 64-key
+    // blocks); 72, so that the row stride is no multiple of 1 KiB (with +64
+    // at c3 it was exactly 65 KiB and the transposed V stores of the QKV
+    // GEMM ran 3 % slower).
+    vt_ld = (int)((rows + 7) / 8 * 8 + 72);
     if (rt->alloc((size_t)H * vt_ld * 2, reinterpret_cast<void**>(&vt), err)) return 1;
     hipError_t e = hipMemset(vt, 0, (size_t)H * vt_ld * 2);
     if (e != hipSuccess) return hip_err(err, "hipMemset(vt)", e);

@@ -55,7 +55,7 @@ struct EncGemmArgs {
   const uint16_t* residual;  // epi 3: [rows][n] f16
   int max_rows, n, k, epi;
   uint16_t* vt;            // optional: columns >= vt_col0 go to vt[col - vt_col0][row]
-  int vt_col0, vt_ld;      // (vt rows hold vt_ld entries, the first max_rows rounded up to 4 + 32 padding)
+  int vt_col0, vt_ld;      // (vt rows hold vt_ld entries, the first max_rows rounded up to 8 + 72 padding)
   // int8 kernels (eos_enc_gemm8_*): A as int8 codes with one f32 scale per
   // row (a = a8 * ascale[row]) and W as int8 codes; a and w are unused.
   const int8_t* a8;        // [rows][k]

@@ -776,9 +776,11 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_ln(EncLnArgs a) {
 // and accumulates O^T += V^T P^T on MFMA. P^T is fed straight from the S^T
 // registers: the K order of that MFMA is the row order the S^T accumulator
 // already has, and the V^T fragment is gathered in the same order.
-template <int HD>
+template <int HD, int KB>
 EOS_DEV void attn_body(const EncAttnArgs& a) {
-  constexpr int KB = 32;                 // keys per block
+  static_assert(KB == 32 || KB == 64, "keys per block");
+  constexpr int KC = KB / 8;             // 8-key chunks of a V^T row per block
+  constexpr int NT = KB / 32;            // 32-key S^T tiles per block
   constexpr int QW = 32;                 // queries per wavefront
   constexpr int NCH = KB * HD / 8;       // 8-half chunks of K (and of V^T) per block
   constexpr int CPT = (NCH + 255) / 256; // chunks per thread
@@ -815,7 +817,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   // registers; the next block's rows are requested before the current
   // block's MFMAs (double-buffered, one barrier per block).
   // V^T comes from the feature-major copy the QKV GEMM wrote: chunk idx of a
-  // block is feature d = idx / 4, keys 8 (idx % 4) .. + 7 (16 bytes). Keys
+  // block is feature d = idx / KC, keys 8 (idx % KC) .. + 7 (16 bytes). Keys
   // past the sequence (probability 0) read its pad rows, the next sequence or
   // vt's zeroed tail: all finite, since every row the GEMMs read was written
   // in this forward (pad rows of ctx included, below), and 0 * finite = 0.
@@ -829,7 +831,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
         const int key = min(k0 + kr, cnt - 1);
         kreg[u] = *reinterpret_cast<const v4i*>(a.qkv + (size_t)(off + key) * ld + a.hidden +
                                                 h * HD + c);
-        const int d = idx >> 2, k8 = (idx & 3) * 8;
+        const int d = idx / KC, k8 = (idx % KC) * 8;
         vreg[u] = *reinterpret_cast<const v4i*>(a.vt + (size_t)(h * HD + d) * a.vt_ld + off + k0 + k8);
       }
     }
@@ -844,8 +846,8 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
         // Key k = 16 st + 8 hh + 4 gg + j is stored at 16 st + 8 gg + 4 hh + j,
         // so the 8 keys a lane's P fragment covers are 16 contiguous bytes:
         // the two 4-key halves of this chunk go to positions 8 and 4 apart.
-        const int d = idx >> 2, k8 = (idx & 3) * 8;
-        const int p0 = (k8 & 16) | ((k8 & 8) >> 1);   // keys k8 .. k8 + 3
+        const int d = idx / KC, k8 = (idx % KC) * 8;
+        const int p0 = (k8 & ~15) | ((k8 & 8) >> 1);  // keys k8 .. k8 + 3
         uint16_t* vrow = &vt[buf][d * (KB + 8)];
         const v4i v = vreg[u];
         *reinterpret_cast<uint2*>(vrow + p0) = make_uint2((uint32_t)v.x, (uint32_t)v.y);
@@ -860,26 +862,33 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   for (int k0 = 0; k0 < cnt; k0 += KB, buf ^= 1) {
     const bool more = k0 + KB < cnt;
     if (more) kv_load(k0 + KB);
-    // S^T (32 keys x 32 queries)
-    v16f s = v16f{0};
+    // S^T, NT tiles of 32 keys x 32 queries
+    v16f s[NT];
 #pragma unroll
-    for (int st = 0; st < HD / 16; ++st) {
-      const v8h kf = *reinterpret_cast<const v8h*>(&ks[buf][l32 * (HD + 8) + st * 16 + g * 8]);
-      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s, 0, 0, 0);
+    for (int hh = 0; hh < NT; ++hh) {
+      s[hh] = v16f{0};
+#pragma unroll
+      for (int st = 0; st < HD / 16; ++st) {
+        const v8h kf = *reinterpret_cast<const v8h*>(
+            &ks[buf][(32 * hh + l32) * (HD + 8) + st * 16 + g * 8]);
+        s[hh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s[hh], 0, 0, 0);
+      }
     }
-    // element e is key k0 + 8(e/4) + 4g + e%4; only the last block of the
-    // sequence has keys past its end (masked to -inf).
+    // element e of tile hh is key k0 + 32 hh + 8(e/4) + 4g + e%4; only the
+    // last block of the sequence has keys past its end (masked to -inf).
     if (k0 + KB > cnt) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int key = k0 + 8 * (e >> 2) + 4 * g + (e & 3);
-        s[e] = key < cnt ? s[e] : -__builtin_inff();
-      }
+      for (int hh = 0; hh < NT; ++hh)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = k0 + 32 * hh + 8 * (e >> 2) + 4 * g + (e & 3);
+          s[hh][e] = key < cnt ? s[hh][e] : -__builtin_inff();
+        }
     }
     // Lazy rescaling: the exponentials are taken against a per-query reference
     // mrun that moves only when needed, and o, lrun are rescaled only then (the
     // quotient o / lrun is the same for any reference). A block is accepted
-    // when every lane's sum of its 16 p stays <= kSafe, so every p fits f16 and
+    // when every lane's sum of its 16 NT p stays <= kSafe, so every p fits f16 and
     // no f32 sum can overflow; otherwise (the first block, where mrun = -inf
     // gives inf or NaN, or a score above mrun + 12) the reference of that
     // query moves to the block's maximum, o and lrun are rescaled and the p
@@ -891,23 +900,27 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     // (both are rescaled alike), added at the end.
     constexpr float kSafe = 4096.0f;
     float psum;
-    v8h pf[2];
+    v8h pf[2 * NT];
     auto exps = [&]() {
       psum = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        // v_exp_f32 directly: masked keys give exp2(-inf) = 0.
-        const float p = __builtin_amdgcn_exp2f(s[e] - mrun);
-        psum += p;
-        pf[e >> 3][e & 7] = (_Float16)p;
-      }
+      for (int hh = 0; hh < NT; ++hh)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          // v_exp_f32 directly: masked keys give exp2(-inf) = 0.
+          const float p = __builtin_amdgcn_exp2f(s[hh][e] - mrun);
+          psum += p;
+          pf[2 * hh + (e >> 3)][e & 7] = (_Float16)p;
+        }
     };
     exps();
     const bool over = !(psum <= kSafe);  // also true for inf and NaN
     if (__ballot(over) != 0ull) {
       float mloc = -__builtin_inff();
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[e]);
+      for (int hh = 0; hh < NT; ++hh)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[hh][e]);
       const float mpair = fmaxf(mloc, __shfl_xor(mloc, 32));
       const bool pover = over || __shfl_xor((int)over, 32) != 0;
       const float mnew = pover ? fmaxf(mpair, mrun) : mrun;
@@ -924,12 +937,13 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     }
     lrun += psum;
     // O^T += V^T P^T. K step st covers the keys this lane's P holds for
-    // e in [8 st, 8 st + 8): 16 st + {4g..4g+3} and 16 st + 8 + {4g..4g+3}.
+    // tile st / 2, e in [8 (st % 2), + 8): keys 16 st + {4g..4g+3} and
+    // 16 st + 8 + {4g..4g+3} of the block.
 #pragma unroll
     for (int t = 0; t < HD / 32; ++t) {
       const int d = t * 32 + l32;
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
+      for (int st = 0; st < 2 * NT; ++st) {
         const v8h vf = *reinterpret_cast<const v8h*>(&vt[buf][d * (KB + 8) + 16 * st + 8 * g]);
         o[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[st], o[t], 0, 0, 0);
       }
@@ -976,15 +990,15 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
 // files in every key block (about 110 extra VALU moves per block at hd 64).
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void eos_enc_attn_hd32(EncAttnArgs a) {
-  attn_body<32>(a);
+  attn_body<32, 32>(a);
 }
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void eos_enc_attn_hd64(EncAttnArgs a) {
-  attn_body<64>(a);
+  attn_body<64, 64>(a);
 }
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void eos_enc_attn_hd128(EncAttnArgs a) {
-  attn_body<128>(a);
+  attn_body<128, 32>(a);
 }
 
 // ------------------------------------------------------------------- pool
