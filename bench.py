@@ -349,6 +349,73 @@ def copy_calibration(rt, mb: int, reps: int = 5) -> dict:
     return {"bytes": nbytes, "ms": ms, "read_plus_write_GBps": 2 * nbytes / (ms / 1e3) / 1e9}
 
 
+
+def two_stage_leg(rt, steps: int, n: int) -> dict:
+    """Two-stage retrieval on the c2 corpus shape (the promoted serving profile
+    turboquant_ip_b4_overfetch200_fp16_rerank): TurboQuant top-200 over n x 384
+    4-bit vectors, then the f16 rerank of those 200 to the top 100 with the
+    rank-100 rescue. Document rows: seeded unit Gaussian f32 vectors converted
+    to f16 on the device at bind."""
+    from eos_amd import datagen
+    from eos_amd.runtime import DeviceBuffer
+    from eos_amd.turboquant import F16Sidecar, TurboQuantIndex, top_fp16_rerank_scores_device
+
+    dim, bits, nq, k, over = 384, 4, 64, 100, 200
+    log("two-stage c2: generating corpus and f16 rows")
+    corpus = datagen.TurboQuantCorpus(n, dim, bits, 31, 32, 33)
+    rng = np.random.default_rng(35)
+    docs = rng.standard_normal((n, dim), dtype=np.float32)
+    docs /= np.linalg.norm(docs, axis=1, keepdims=True)
+    idx = TurboQuantIndex(rt, corpus.codes, corpus.norms, dim, bits, corpus.codebook,
+                          corpus.codebook_scale, corpus.rotation)
+    side = F16Sidecar(rt, docs)
+    del docs
+    q = datagen.baseline_queries(nq, dim, 34)
+    dq = DeviceBuffer.from_array(rt, q)
+    dcid, dcs = DeviceBuffer(rt, nq * over * 8), DeviceBuffer(rt, nq * over * 4)
+    dids, dsc = DeviceBuffer(rt, nq * k * 8), DeviceBuffer(rt, nq * k * 4)
+
+    def step():
+        idx.top_k_device(dq, nq, over, dcid, dcs, with_stats=False)
+        top_fp16_rerank_scores_device(side, dq, nq, dcid, dcs, over, k, bits, over, dids, dsc)
+
+    for _ in range(3):
+        step()
+    rt.sync()
+    rt.mark(6)
+    for _ in range(steps):
+        step()
+    rt.mark(7)
+    ms = rt.elapsed_ms(6, 7) / steps
+    rt.profile_reset()
+    rt.profile_select("tq_fp16_rerank")
+    rt.profile(True)
+    for _ in range(10):
+        step()
+    rt.sync()
+    n_rr, ms_rr = rt.profile_read("tq_fp16_rerank")
+    rt.profile(False)
+    avg = ms_rr / max(n_rr, 1)
+    rr_bytes = nq * over * (dim * 2 + 12) + nq * dim * 4 + nq * k * 12
+    out = {
+        "metric": "two-stage retrieval queries/s (TurboQuant top-200 + f16 rerank top-100)",
+        "value": nq / (ms / 1e3),
+        "unit": "queries/s",
+        "ms_per_batch": ms,
+        "vectors_scored_per_s": n * nq / (ms / 1e3),
+        "config": {"workload": "turboquant_two_stage_c2", "n": n, "dim": dim, "bits": bits,
+                   "queries": nq, "overfetch": over, "k": k,
+                   "profile": "turboquant_ip_b4_overfetch200_fp16_rerank"},
+        "rerank": {"kernel": "tq_fp16_rerank", "bound": "latency", "avg_launch_ms": avg,
+                   "launches": n_rr, "bytes_per_launch": rr_bytes,
+                   "achieved_gbs": rr_bytes / (avg / 1e3) / 1e9 if avg > 0 else None},
+    }
+    for b in (dq, dcid, dcs, dids, dsc):
+        b.free()
+    side.buf.free()
+    idx.release()
+    return out
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -365,6 +432,7 @@ def main() -> int:
     ap.add_argument("--skip-encoder", action="store_true")
     ap.add_argument("--skip-tq", action="store_true", help="profiling runs of the encoder only")
     ap.add_argument("--skip-maxsim", action="store_true")
+    ap.add_argument("--skip-two-stage", action="store_true")
     ap.add_argument("--maxsim-steps", type=int, default=5)
     ap.add_argument("--encoder-steps", type=int, default=5)
     ap.add_argument("--encoder-configs", default="c3,c4", help="comma list of c3, c4")
@@ -402,6 +470,9 @@ def main() -> int:
             out[f"encoder_{name}"] = encoder_leg(rt, args.encoder_steps, name)
     if not args.skip_maxsim:
         out["maxsim_c5"] = maxsim_leg(rt, args.maxsim_steps)
+    if not args.skip_two_stage:
+        log("two-stage c2")
+        out["two_stage_c2"] = two_stage_leg(rt, args.maxsim_steps * 4, args.n)
     if args.copy_calibration_mb > 0:
         out["copy_calibration"] = copy_calibration(rt, args.copy_calibration_mb)
     out["device"] = info

@@ -138,6 +138,11 @@ _SIGNATURES = {
                                      C.c_int),
     "eoship_tq_maxsim_scores": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p, C.c_int32, C.c_int32,
                                  C.c_int64, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_f16_sidecar_device": ([C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_fp16_rerank_device": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
+                                      C.c_int64, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                      C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p],
+                                     C.c_int),
     "eoship_tq_encode": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
                           C.c_void_p], C.c_int),
     "eoship_tq_encode_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p,

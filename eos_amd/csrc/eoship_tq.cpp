@@ -1292,3 +1292,55 @@ int eoship_tq_encode(EosHipRuntime* rt, EosHipTQ* tq, const float* x, int64_t n,
 }
 
 }  // extern "C"
+
+// ------------------------------------------------- two-stage retrieval (f16)
+
+extern "C" {
+
+int eoship_f16_sidecar_device(EosHipRuntime* rt, const float* d_x, int64_t count, uint16_t* d_half,
+                              char** err) {
+  if (rt == nullptr) return set_err(err, "eoship_f16_sidecar_device: NULL runtime");
+  if (count < 0) return set_err(err, "eoship_f16_sidecar_device: negative count");
+  if (count == 0) return 0;
+  if (d_x == nullptr || d_half == nullptr) return set_err(err, "eoship_f16_sidecar_device: NULL buffer");
+  TqHalfArgs a;
+  a.x = d_x;
+  a.h = reinterpret_cast<unsigned short*>(d_half);
+  a.count = count;
+  const int64_t blocks = std::min<int64_t>((count + 1023) / 1024, 8192);
+  return rt->launch("eos_tq_f16_sidecar", dim3((unsigned)blocks), dim3(256), 0, &a, err,
+                    "f16_sidecar");
+}
+
+int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int32_t q, int32_t d,
+                                 const uint16_t* d_rows, int64_t n, const int64_t* d_cand_ids,
+                                 const float* d_cand_scores, int32_t c, int32_t k,
+                                 int32_t bit_width, int32_t overfetch, int64_t* d_ids,
+                                 float* d_scores, char** err) {
+  if (rt == nullptr) return set_err(err, "eoship_tq_fp16_rerank_device: NULL runtime");
+  if (q < 0 || c < 0 || n < 0) return set_err(err, "eoship_tq_fp16_rerank_device: negative size");
+  if (d < 1 || d > 4096) return set_err(err, "eoship_tq_fp16_rerank_device: dim must be in [1, 4096]");
+  if (c > 1024) return set_err(err, "eoship_tq_fp16_rerank_device: at most 1024 candidates per query");
+  if (n >= ((int64_t)1 << 32) - 1)
+    return set_err(err, "eoship_tq_fp16_rerank_device: corpus must hold fewer than 2^32 - 1 rows");
+  if (q == 0 || c == 0) return 0;
+  if (d_queries == nullptr || d_rows == nullptr || d_cand_ids == nullptr || d_cand_scores == nullptr ||
+      d_ids == nullptr || d_scores == nullptr)
+    return set_err(err, "eoship_tq_fp16_rerank_device: NULL buffer");
+  TqRerankArgs a;
+  a.queries = d_queries;
+  a.rows = reinterpret_cast<const unsigned short*>(d_rows);
+  a.cand_ids = reinterpret_cast<const long long*>(d_cand_ids);
+  a.cand_scores = d_cand_scores;
+  a.out_ids = reinterpret_cast<long long*>(d_ids);
+  a.out_scores = d_scores;
+  a.n = n;
+  a.d = d;
+  a.c = c;
+  a.kk = (k <= 0 || k > c) ? c : k;
+  // shouldApplyTurboQuantFP16RerankRescue (runtime/retrieval_turboquant.go:1664-1669).
+  a.rescue = (bit_width == 4 && k == 100 && overfetch == 200 && c >= 120) ? 1 : 0;
+  return rt->launch("eos_tq_fp16_rerank", dim3((unsigned)q), dim3(256), 0, &a, err, "tq_fp16_rerank");
+}
+
+}  // extern "C"

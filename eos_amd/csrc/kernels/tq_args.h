@@ -161,4 +161,24 @@ struct TqEncodeArgs {
   int cb[16];
 };
 
+// f16 rerank sidecar: f32 rows -> the reference's half encoding.
+struct TqHalfArgs {
+  const float* x;          // [count]
+  unsigned short* h;       // [count]
+  long long count;
+};
+
+// Second stage of two-stage retrieval: exact f16-row rerank of the overfetched
+// candidates of each query (one workgroup per query).
+struct TqRerankArgs {
+  const float* queries;          // [q][d]
+  const unsigned short* rows;    // [n][d] halves
+  const long long* cand_ids;     // [q][c] first-stage order (score desc, id asc)
+  const float* cand_scores;      // [q][c] first-stage scores
+  long long* out_ids;            // [q][kk]
+  float* out_scores;             // [q][kk]
+  long long n;
+  int d, c, kk, rescue;
+};
+
 #endif  // EOSHIP_TQ_ARGS_H

@@ -1587,3 +1587,208 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_parent_best(TqParentBes
     a.best_score[(size_t)q * a.kk + i] = bv;
   }
 }
+
+// ------------------------------------------------- two-stage retrieval (f16)
+// f32 -> half exactly as float32ToHalf (runtime/mll_export.go:1007-1041):
+// ties round away from zero (bit 12 of the f32 mantissa, not to even), and a
+// finite value at or above 2^16 with a nonzero mantissa keeps its top mantissa
+// bits under the all-ones exponent (a NaN pattern).
+__device__ inline unsigned short ref_f32_to_half(float v) {
+  const unsigned bits = __float_as_uint(v);
+  const unsigned sign = (bits >> 16) & 0x8000u;
+  const int e = (int)((bits >> 23) & 0xffu) - 127 + 15;
+  unsigned mant = bits & 0x7fffffu;
+  if (e <= 0) {
+    if (e < -10) return (unsigned short)sign;
+    mant |= 0x800000u;
+    const unsigned shift = (unsigned)(14 - e);
+    unsigned half = mant >> shift;
+    if ((mant >> (shift - 1)) & 1u) half++;
+    return (unsigned short)(sign | half);
+  }
+  if (e >= 0x1f) return (unsigned short)(sign | 0x7c00u | (mant == 0 ? 0u : (mant >> 13)));
+  unsigned hexp = (unsigned)e << 10, hmant = mant >> 13;
+  if (mant & 0x1000u) {
+    hmant++;
+    if (hmant & 0x400u) {
+      hmant = 0;
+      hexp += 0x400u;
+      if (hexp >= 0x7c00u) hexp = 0x7c00u;
+    }
+  }
+  return (unsigned short)(sign | hexp | hmant);
+}
+
+// halfToFloat32 (runtime/weight_file.go:461-483); a subnormal half is m * 2^-24
+// exactly.
+__device__ inline float ref_half_to_f32(unsigned h) {
+  const unsigned sign = (h & 0x8000u) << 16;
+  const unsigned e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0) return __uint_as_float(sign | __float_as_uint((float)m * 5.9604644775390625e-8f));
+  if (e == 31) return __uint_as_float(sign | 0x7f800000u | (m << 13));
+  return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+extern "C" __global__ __launch_bounds__(256) void eos_tq_f16_sidecar(TqHalfArgs a) {
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < a.count; i += stride)
+    a.h[i] = ref_f32_to_half(a.x[i]);
+}
+
+constexpr int kRrThreads = 256;
+constexpr int kRrMaxCand = 1024;
+constexpr int kRrMaxDim = 4096;
+constexpr int kRescueTopK = 100, kRescueLo = 100, kRescueHi = 120, kRescuePromote = 5;
+
+// Order key of a score for a descending sort (-0 and +0 compare equal, as Go's
+// float comparisons do).
+__device__ inline unsigned rr_desc(float s) {
+  unsigned u = __float_as_uint(s);
+  if (u == 0x80000000u) u = 0;
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ~u;
+}
+
+// One candidate's score: scoreValue += query[i] * halfToFloat32(half) in
+// order, each product and sum rounded to f32 (no fused multiply-add), as
+// topFP16RerankScores computes it (runtime/retrieval_turboquant.go:1646-1649).
+__device__ __attribute__((noinline)) float rr_dot(const float* qv, const unsigned short* row, int d) {
+#pragma clang fp contract(off)
+  float s = 0.0f;
+  int i = 0;
+  if ((d & 7) == 0) {
+    const uint4* r4 = reinterpret_cast<const uint4*>(row);
+    for (; i < d; i += 8) {
+      const uint4 w = r4[i >> 3];
+      const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float p0 = qv[i + 2 * t] * ref_half_to_f32(ws[t] & 0xffffu);
+        s = s + p0;
+        const float p1 = qv[i + 2 * t + 1] * ref_half_to_f32(ws[t] >> 16);
+        s = s + p1;
+      }
+    }
+  }
+  for (; i < d; ++i) {
+    const float p = qv[i] * ref_half_to_f32(row[i]);
+    s = s + p;
+  }
+  return s;
+}
+
+// Scores every candidate of one query from its f16 row, sorts them in LDS by
+// (score desc, id asc) -- the heap + insertion sort of topFP16RerankScores
+// (runtime/retrieval_turboquant.go:1635-1662) -- or, with rescue, by (score
+// desc, first-stage rank asc) (sortTurboQuantFP16RankedScores, :1698-1719;
+// ranks are distinct, so its id tie-break never decides) and then applies
+// applyTurboQuantFP16RerankRescue (:1721-1786). Candidates whose id is outside
+// [0, n) have no row and are skipped (`if !ok { continue }`).
+extern "C" __global__ __launch_bounds__(kRrThreads) void eos_tq_fp16_rerank(TqRerankArgs a) {
+  __shared__ float qv[kRrMaxDim];
+  __shared__ unsigned long long key[kRrMaxCand];
+  __shared__ int pos[kRrMaxCand];
+  __shared__ float fscore[kRrMaxCand];
+  __shared__ int outpos[kRrMaxCand];
+  __shared__ unsigned char seen[kRrMaxCand];
+  __shared__ int valid_n;
+  const int qi = blockIdx.x, tid = threadIdx.x;
+  const long long* cid = a.cand_ids + (size_t)qi * a.c;
+  for (int i = tid; i < a.d; i += kRrThreads) qv[i] = a.queries[(size_t)qi * a.d + i];
+  if (tid == 0) valid_n = 0;
+  int P = 1;
+  while (P < a.c) P <<= 1;
+  __syncthreads();
+  int my_valid = 0;
+  for (int j = tid; j < P; j += kRrThreads) {
+    unsigned long long k = ~0ull;
+    if (j < a.c) {
+      const long long id = cid[j];
+      seen[j] = 0;
+      if (id >= 0 && id < a.n) {
+        const float s = rr_dot(qv, a.rows + (size_t)id * a.d, a.d);
+        fscore[j] = s;
+        const unsigned tie = a.rescue ? (unsigned)(j + 1) : (unsigned)id;
+        k = ((unsigned long long)rr_desc(s) << 32) | tie;
+        ++my_valid;
+      }
+    }
+    key[j] = k;
+    pos[j] = j;
+  }
+  if (my_valid) atomicAdd(&valid_n, my_valid);
+  for (int size = 2; size <= P; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      __syncthreads();
+      for (int t = tid; t < (P >> 1); t += kRrThreads) {
+        const int lo = 2 * t - (t & (stride - 1)), hi = lo + stride;
+        const bool asc = (lo & size) == 0;
+        const unsigned long long kl = key[lo], kh = key[hi];
+        if ((kl > kh) == asc) {
+          key[lo] = kh;
+          key[hi] = kl;
+          const int pl = pos[lo];
+          pos[lo] = pos[hi];
+          pos[hi] = pl;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int m = valid_n;
+  const int nout = a.kk < m ? a.kk : m;
+  if (a.rescue && m >= kRescueHi && m > kRescueTopK) {
+    if (tid == 0) {
+      // Ranks kRescueLo..kRescueHi (1-based) by (first-stage score desc,
+      // first-stage rank asc); the first kRescuePromote are promoted.
+      int promoted[kRescuePromote];
+      unsigned long long taken = 0;
+      const int pool = kRescueHi - kRescueLo + 1;
+      for (int r = 0; r < kRescuePromote; ++r) {
+        int best = -1;
+        unsigned long long bk = ~0ull;
+        for (int i = 0; i < pool; ++i) {
+          if (taken >> i & 1ull) continue;
+          const int p = pos[kRescueLo - 1 + i];
+          const unsigned long long ck = ((unsigned long long)rr_desc(a.cand_scores[(size_t)qi * a.c + p]) << 32) | (unsigned)(p + 1);
+          if (best < 0 || ck < bk) { best = i; bk = ck; }
+        }
+        taken |= 1ull << best;
+        promoted[r] = pos[kRescueLo - 1 + best];
+      }
+      int o = 0;
+      for (int i = 0; i < kRescueTopK && o < nout; ++i) {
+        const int p = pos[i];
+        bool pr = false;
+        for (int r = 0; r < kRescuePromote; ++r) pr |= promoted[r] == p;
+        if (pr) continue;
+        outpos[o++] = p;
+        seen[p] = 1;
+      }
+      for (int r = 0; r < kRescuePromote && o < nout; ++r) {
+        if (seen[promoted[r]]) continue;
+        outpos[o++] = promoted[r];
+        seen[promoted[r]] = 1;
+      }
+      for (int i = 0; i < m && o < nout; ++i) {
+        if (seen[pos[i]]) continue;
+        outpos[o++] = pos[i];
+        seen[pos[i]] = 1;
+      }
+    }
+  } else {
+    for (int i = tid; i < nout; i += kRrThreads) outpos[i] = pos[i];
+  }
+  __syncthreads();
+  for (int i = tid; i < a.kk; i += kRrThreads) {
+    long long id = -1;
+    float s = 0.0f;
+    if (i < nout) {
+      const int p = outpos[i];
+      id = cid[p];
+      s = fscore[p];
+    }
+    a.out_ids[(size_t)qi * a.kk + i] = id;
+    a.out_scores[(size_t)qi * a.kk + i] = s;
+  }
+}

@@ -344,3 +344,70 @@ def top_turboquant_retrieval_scores_with_stats(index: TurboQuantIndex, queries: 
     out = [[RetrievalScoredDoc(int(i), float(s)) for i, s in zip(ids[r], scores[r])]
            for r in range(ids.shape[0])]
     return out, stats
+
+
+class F16Sidecar:
+    """f16 rerank rows on the device: the counterpart of halfByID in
+    computeTurboQuantFP16RerankRetrievalQuality (runtime/retrieval_turboquant.go:1503-1511),
+    each f32 converted by float32ToHalf (runtime/mll_export.go:1007-1041) in a
+    gfx950 kernel. vectors: float32 [n, dim]; row i is the document with id i."""
+
+    def __init__(self, rt: Runtime, vectors: np.ndarray):
+        v = np.ascontiguousarray(vectors, np.float32)
+        if v.ndim != 2:
+            raise ValueError("sidecar vectors must be [n, dim]")
+        self.rt, self.n, self.dim = rt, int(v.shape[0]), int(v.shape[1])
+        self.buf = DeviceBuffer(rt, max(2, v.size * 2))
+        src = DeviceBuffer.from_array(rt, v) if v.size else None
+        if src is not None:
+            _lib.call("eoship_f16_sidecar_device", rt.handle, src.ptr, C.c_int64(v.size),
+                      self.buf.ptr)
+            src.free()
+
+    def halves(self) -> np.ndarray:
+        return self.buf.download(np.uint16, (self.n, self.dim))
+
+
+def top_fp16_rerank_scores_device(sidecar: F16Sidecar, d_queries: DeviceBuffer, nq: int,
+                                  d_cand_ids: DeviceBuffer, d_cand_scores: DeviceBuffer, c: int,
+                                  top_k: int, bit_width: int, overfetch: int,
+                                  d_ids: DeviceBuffer, d_scores: DeviceBuffer) -> int:
+    """topFP16RerankScores / topFP16RerankRescueScores for nq queries on device
+    buffers (runtime/retrieval_turboquant.go:1551-1556, :1635-1786). Returns kk."""
+    _lib.call("eoship_tq_fp16_rerank_device", sidecar.rt.handle, d_queries.ptr, C.c_int32(nq),
+              C.c_int32(sidecar.dim), sidecar.buf.ptr, C.c_int64(sidecar.n), d_cand_ids.ptr,
+              d_cand_scores.ptr, C.c_int32(c), C.c_int32(int(top_k)), C.c_int32(int(bit_width)),
+              C.c_int32(int(overfetch)), d_ids.ptr, d_scores.ptr)
+    return c if (top_k <= 0 or top_k > c) else int(top_k)
+
+
+def turboquant_fp16_rerank_top_k(index: "TurboQuantIndex", sidecar: F16Sidecar,
+                                 queries: np.ndarray, top_k: int, overfetch: int):
+    """Two-stage retrieval per query as computeTurboQuantFP16RerankRetrievalQuality
+    runs it (runtime/retrieval_turboquant.go:1512-1556): top_k < 100 -> 100,
+    overfetch < top_k -> top_k, TurboQuant top-overfetch candidates, then the f16
+    rerank (with the rank-100 rescue for the b4 / overfetch 200 / top 100 profile).
+    Returns (ids int64 [Q, kk], scores float32 [Q, kk], candidate ids [Q, c])."""
+    top_k = max(int(top_k), 100)
+    overfetch = max(int(overfetch), top_k)
+    if sidecar.n != index.n or sidecar.dim != index.dim:
+        raise ValueError("sidecar rows must match the bound corpus")
+    q = index._queries(queries)
+    nq = q.shape[0]
+    c = index.effective_k(overfetch)
+    rt = index.rt
+    d_q = DeviceBuffer.from_array(rt, q)
+    d_cid = DeviceBuffer(rt, max(8, nq * c * 8))
+    d_cs = DeviceBuffer(rt, max(4, nq * c * 4))
+    index.top_k_device(d_q, nq, overfetch, d_cid, d_cs)
+    kk = c if top_k > c else top_k
+    d_ids = DeviceBuffer(rt, max(8, nq * kk * 8))
+    d_sc = DeviceBuffer(rt, max(4, nq * kk * 4))
+    top_fp16_rerank_scores_device(sidecar, d_q, nq, d_cid, d_cs, c, top_k, index.bits, overfetch,
+                                  d_ids, d_sc)
+    ids = d_ids.download(np.int64, (nq, kk))
+    scores = d_sc.download(np.float32, (nq, kk))
+    cand = d_cid.download(np.int64, (nq, c))
+    for b in (d_q, d_cid, d_cs, d_ids, d_sc):
+        b.free()
+    return ids, scores, cand

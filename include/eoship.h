@@ -351,6 +351,28 @@ int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc
                                 const EosHipCompactLayer* layers, const int8_t* output_projection,
                                 float s_output, EosHipEncoder** out, char** err);
 
+/* Two-stage retrieval, second stage (the promoted serving profile
+ * turboquant_ip_b4_overfetch200_fp16_rerank). eoship_f16_sidecar_device turns
+ * f32 document vectors into the f16 rerank rows exactly as the halfByID loop of
+ * computeTurboQuantFP16RerankRetrievalQuality does
+ * (runtime/retrieval_turboquant.go:1503-1511, float32ToHalf in
+ * runtime/mll_export.go:1007-1041: ties round away from zero). */
+int eoship_f16_sidecar_device(EosHipRuntime* rt, const float* d_x, int64_t count, uint16_t* d_half,
+                              char** err);
+/* Reranks each query's first-stage candidates (d_cand_ids/d_cand_scores
+ * [Q][c], c <= 1024, in first-stage order as eoship_tq_topk_device writes them)
+ * by the f16 rows d_rows [n][d]: topFP16RerankScores, or
+ * topFP16RerankRescueScores when shouldApplyTurboQuantFP16RerankRescue(bit_width,
+ * k, overfetch, c) holds (runtime/retrieval_turboquant.go:1551-1556,
+ * :1635-1786). Scores are sequential f32 sums of f32 products. k <= 0 or k > c
+ * means k = c; outputs [Q][kk]; a query with fewer than kk candidates in
+ * [0, n) pads its row with id -1 and score 0. Enqueued on the runtime stream. */
+int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int32_t q, int32_t d,
+                                 const uint16_t* d_rows, int64_t n, const int64_t* d_cand_ids,
+                                 const float* d_cand_scores, int32_t c, int32_t k,
+                                 int32_t bit_width, int32_t overfetch, int64_t* d_ids,
+                                 float* d_scores, char** err);
+
 #ifdef __cplusplus
 }
 #endif

@@ -366,3 +366,65 @@ def compact_embed(tok, role, layers, ids, mask, role_ids, heads, wout=None):
                       None if wo is None else _p(wo), odim, _p(ids), _p(roles), _p(mask), batch,
                       tokens, dim, heads, ffn, _p(out))
     return out
+
+
+# ------------------------------------------------ two-stage retrieval (f16)
+class _Scored(C.Structure):
+    _fields_ = [("id", C.c_int64), ("score", C.c_float), ("rank", C.c_int), ("compact", C.c_float)]
+
+
+def f32_to_half(x) -> np.ndarray:
+    """float32ToHalf (runtime/mll_export.go:1007-1041) elementwise -> uint16."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    load().oracle_f32_to_half_n(x.ctypes.data_as(C.c_void_p), C.c_int64(x.size),
+                                out.ctypes.data_as(C.c_void_p))
+    return out
+
+
+def half_to_f32(h) -> np.ndarray:
+    """halfToFloat32 (runtime/weight_file.go:461-483) elementwise."""
+    fn = load().oracle_half_to_f32
+    fn.restype, fn.argtypes = C.c_float, [C.c_uint16]
+    h = np.asarray(h, np.uint16)
+    return np.array([fn(int(v)) for v in h.ravel()], np.float32).reshape(h.shape)
+
+
+def fp16_rerank_should_rescue(bit_width: int, k: int, overfetch: int, c: int) -> bool:
+    """shouldApplyTurboQuantFP16RerankRescue (runtime/retrieval_turboquant.go:1664-1669)."""
+    return bit_width == 4 and k == 100 and overfetch == 200 and c >= 120
+
+
+def apply_rescue(ids, scores, ranks, compact) -> np.ndarray:
+    """applyTurboQuantFP16RerankRescue over an already fp16-ranked list; returns the ids."""
+    m = len(ids)
+    arr = (_Scored * max(m, 1))()
+    for i in range(m):
+        arr[i] = _Scored(int(ids[i]), float(scores[i]), int(ranks[i]), float(compact[i]))
+    out = (_Scored * max(m, 1))()
+    load().oracle_apply_rescue(arr, C.c_int(m), out)
+    return np.array([out[i].id for i in range(m)], np.int64)
+
+
+def fp16_rerank(queries, rows, cand_ids, cand_scores, k, bit_width=0, overfetch=0, rescue=None):
+    """Second stage for each query: (ids int64 [Q, kk], scores float32 [Q, kk]),
+    rows past a query's result count hold id -1 and score 0."""
+    q = np.ascontiguousarray(queries, np.float32)
+    rows = np.ascontiguousarray(rows, np.uint16)
+    cid = np.ascontiguousarray(cand_ids, np.int64)
+    cs = np.ascontiguousarray(cand_scores, np.float32)
+    nq, d = q.shape
+    c = cid.shape[1]
+    kk = c if (k <= 0 or k > c) else k
+    if rescue is None:
+        rescue = fp16_rerank_should_rescue(bit_width, k, overfetch, c)
+    ids = np.full((nq, kk), -1, np.int64)
+    scores = np.zeros((nq, kk), np.float32)
+    lib = load()
+    for i in range(nq):
+        lib.oracle_fp16_rerank(q[i].ctypes.data_as(C.c_void_p), C.c_int(d),
+                               rows.ctypes.data_as(C.c_void_p), C.c_int64(rows.shape[0]),
+                               cid[i].ctypes.data_as(C.c_void_p), cs[i].ctypes.data_as(C.c_void_p),
+                               C.c_int(c), C.c_int(int(k)), C.c_int(1 if rescue else 0),
+                               ids[i].ctypes.data_as(C.c_void_p), scores[i].ctypes.data_as(C.c_void_p))
+    return ids, scores

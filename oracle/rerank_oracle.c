@@ -1,0 +1,198 @@
+/* TEST INFRASTRUCTURE ONLY: CPU restatement of the reference's second retrieval
+ * stage (f16 rerank of TurboQuant-overfetched candidates), the checker for
+ * eos_tq_f16_sidecar / eos_tq_fp16_rerank. Never linked into the product.
+ *
+ *   oracle_f32_to_half   float32ToHalf        runtime/mll_export.go:1007-1041
+ *   oracle_half_to_f32   halfToFloat32        runtime/weight_file.go:461-483
+ *   oracle_fp16_rerank   topFP16RerankScores  runtime/retrieval_turboquant.go:1635-1662
+ *                        topFP16RerankRescueScores + sortTurboQuantFP16RankedScores
+ *                        + applyTurboQuantFP16RerankRescue  :1671-1786
+ * Built with -ffp-contract=off: each product and sum is rounded to f32, as Go
+ * compiles `s += a * b` for amd64 at its default GOAMD64=v1 (no fused
+ * multiply-add). Ids are vector indices; "ID asc/desc" compares them as
+ * integers (the reference's string IDs order the same way when they are
+ * fixed-width, e.g. d%03d in its rescue fixtures). */
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+uint16_t oracle_f32_to_half(float value) {
+  uint32_t bits;
+  memcpy(&bits, &value, 4);
+  const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+  const int exp = (int)((bits >> 23) & 0xffu) - 127 + 15;
+  uint32_t mant = bits & 0x7fffffu;
+  if (exp <= 0) {
+    if (exp < -10) return sign;
+    mant |= 0x800000u;
+    const uint32_t shift = (uint32_t)(14 - exp);
+    uint16_t half = (uint16_t)(mant >> shift);
+    if ((mant >> (shift - 1)) & 1u) half++;
+    return (uint16_t)(sign | half);
+  }
+  if (exp >= 0x1f) {
+    if (mant == 0) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | 0x7c00u | (uint16_t)(mant >> 13));
+  }
+  uint16_t half_exp = (uint16_t)((uint16_t)exp << 10);
+  uint16_t half_mant = (uint16_t)(mant >> 13);
+  if (mant & 0x00001000u) {
+    half_mant++;
+    if (half_mant & 0x0400u) {
+      half_mant = 0;
+      half_exp = (uint16_t)(half_exp + 0x0400u);
+      if (half_exp >= 0x7c00u) half_exp = 0x7c00u;
+    }
+  }
+  return (uint16_t)(sign | half_exp | half_mant);
+}
+
+float oracle_half_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu;
+  uint32_t mant = h & 0x03ffu, out;
+  if (exp == 0) {
+    if (mant == 0) {
+      out = sign;
+    } else {
+      uint32_t exp32 = 127 - 15 + 1;
+      while ((mant & 0x0400u) == 0) {
+        mant <<= 1;
+        exp32--;
+      }
+      mant &= 0x03ffu;
+      out = sign | (exp32 << 23) | (mant << 13);
+    }
+  } else if (exp == 0x1f) {
+    out = sign | 0x7f800000u | (mant << 13);
+  } else {
+    out = sign | ((exp + 127 - 15) << 23) | (mant << 13);
+  }
+  float f;
+  memcpy(&f, &out, 4);
+  return f;
+}
+
+void oracle_f32_to_half_n(const float* x, int64_t n, uint16_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = oracle_f32_to_half(x[i]);
+}
+
+typedef struct {
+  int64_t id;
+  float score;
+  int rank;          /* first-stage rank, 1-based */
+  float compact;     /* first-stage score */
+} scored_t;
+
+/* retrievalScoreBetter (runtime/retrieval_eval.go:1153-1161). */
+static int better(const scored_t* a, const scored_t* b) {
+  if (a->score > b->score) return 1;
+  if (a->score < b->score) return 0;
+  return a->id < b->id;
+}
+
+/* sortTurboQuantFP16RankedScores's less (retrieval_turboquant.go:1699-1718). */
+static int cmp_fp16_ranked(const void* pa, const void* pb) {
+  const scored_t* a = (const scored_t*)pa;
+  const scored_t* b = (const scored_t*)pb;
+  if (a->score > b->score) return -1;
+  if (a->score < b->score) return 1;
+  if (a->rank != b->rank) return a->rank < b->rank ? -1 : 1;
+  return a->id > b->id ? -1 : (a->id < b->id ? 1 : 0);
+}
+
+/* The rescue pool's less (retrieval_turboquant.go:1732-1751). */
+static int cmp_rescue_pool(const void* pa, const void* pb) {
+  const scored_t* a = (const scored_t*)pa;
+  const scored_t* b = (const scored_t*)pb;
+  if (a->compact > b->compact) return -1;
+  if (a->compact < b->compact) return 1;
+  if (a->rank != b->rank) return a->rank < b->rank ? -1 : 1;
+  return a->id > b->id ? -1 : (a->id < b->id ? 1 : 0);
+}
+
+enum { RESCUE_TOPK = 100, RESCUE_LO = 100, RESCUE_HI = 120, RESCUE_PROMOTE = 5 };
+
+/* applyTurboQuantFP16RerankRescue over ranked[0..m); writes the reordered
+ * list to out (m entries). */
+void oracle_apply_rescue(const scored_t* ranked, int m, scored_t* out) {
+  if (m < RESCUE_HI || m <= RESCUE_TOPK) {
+    memcpy(out, ranked, (size_t)m * sizeof(scored_t));
+    return;
+  }
+  scored_t pool[RESCUE_HI - RESCUE_LO + 1];
+  int np = 0;
+  for (int i = 0; i < m; ++i) {
+    const int rank = i + 1;
+    if (rank >= RESCUE_LO && rank <= RESCUE_HI) pool[np++] = ranked[i];
+  }
+  qsort(pool, (size_t)np, sizeof(scored_t), cmp_rescue_pool);
+  if (np > RESCUE_PROMOTE) np = RESCUE_PROMOTE;
+  unsigned char* seen = (unsigned char*)calloc((size_t)m, 1);
+  int o = 0;
+  for (int i = 0; i < RESCUE_TOPK; ++i) {
+    int promoted = 0;
+    for (int r = 0; r < np; ++r) promoted |= pool[r].id == ranked[i].id;
+    if (promoted) continue;
+    out[o++] = ranked[i];
+    seen[i] = 1;
+  }
+  for (int r = 0; r < np; ++r) {
+    int idx = -1;
+    for (int i = 0; i < m; ++i)
+      if (ranked[i].id == pool[r].id) idx = i;
+    if (seen[idx]) continue;
+    out[o++] = ranked[idx];
+    seen[idx] = 1;
+  }
+  for (int i = 0; i < m; ++i) {
+    if (seen[i]) continue;
+    out[o++] = ranked[i];
+    seen[i] = 1;
+  }
+  free(seen);
+}
+
+/* One query. Returns the number of results written (<= kk, the k rule of
+ * :1636-1638). */
+int oracle_fp16_rerank(const float* query, int d, const uint16_t* rows, int64_t n,
+                       const int64_t* cand_ids, const float* cand_scores, int c, int k,
+                       int rescue, int64_t* out_ids, float* out_scores) {
+  int topk = (k <= 0 || k > c) ? c : k;
+  scored_t* ranked = (scored_t*)malloc((size_t)(c > 0 ? c : 1) * sizeof(scored_t));
+  int m = 0;
+  for (int j = 0; j < c; ++j) {
+    const int64_t id = cand_ids[j];
+    if (id < 0 || id >= n) continue; /* docs[candidate.ID] missing */
+    const uint16_t* vec = rows + (size_t)id * (size_t)d;
+    float score = 0.0f;
+    for (int i = 0; i < d; ++i) score += query[i] * oracle_half_to_f32(vec[i]);
+    ranked[m].id = id;
+    ranked[m].score = score;
+    ranked[m].rank = j + 1;
+    ranked[m].compact = cand_scores[j];
+    ++m;
+  }
+  if (rescue) {
+    qsort(ranked, (size_t)m, sizeof(scored_t), cmp_fp16_ranked);
+    scored_t* out = (scored_t*)malloc((size_t)(m > 0 ? m : 1) * sizeof(scored_t));
+    oracle_apply_rescue(ranked, m, out);
+    memcpy(ranked, out, (size_t)m * sizeof(scored_t));
+    free(out);
+  } else {
+    /* slicesSortRetrievalScores: insertion sort by retrievalScoreBetter. */
+    for (int i = 1; i < m; ++i)
+      for (int j = i; j > 0 && better(&ranked[j], &ranked[j - 1]); --j) {
+        scored_t t = ranked[j];
+        ranked[j] = ranked[j - 1];
+        ranked[j - 1] = t;
+      }
+  }
+  if (topk > m) topk = m;
+  for (int i = 0; i < topk; ++i) {
+    out_ids[i] = ranked[i].id;
+    out_scores[i] = ranked[i].score;
+  }
+  free(ranked);
+  return topk;
+}

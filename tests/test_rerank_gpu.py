@@ -1,0 +1,112 @@
+"""GPU parity of the two-stage retrieval's second stage (eos_tq_f16_sidecar,
+eos_tq_fp16_rerank through the C ABI) against the CPU oracle. Bar: halves,
+rerank ids and f32 scores bit-exact, including the rank-100 rescue of the
+b4 / overfetch 200 / top 100 profile and the reference's own rescue fixture."""
+import numpy as np
+import pytest
+
+import oracle
+from eos_amd import datagen
+from eos_amd.runtime import DeviceBuffer
+from eos_amd.turboquant import (F16Sidecar, TurboQuantIndex, top_fp16_rerank_scores_device,
+                                turboquant_fp16_rerank_top_k)
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(name):
+    print(f"[case] {name}", flush=True)
+
+
+def _rerank(rt, side, q, cid, cs, k, bits, overfetch):
+    nq, c = cid.shape
+    d_q = DeviceBuffer.from_array(rt, np.ascontiguousarray(q, np.float32))
+    d_cid = DeviceBuffer.from_array(rt, np.ascontiguousarray(cid, np.int64))
+    d_cs = DeviceBuffer.from_array(rt, np.ascontiguousarray(cs, np.float32))
+    kk = c if (k <= 0 or k > c) else k
+    d_ids, d_sc = DeviceBuffer(rt, nq * kk * 8), DeviceBuffer(rt, nq * kk * 4)
+    top_fp16_rerank_scores_device(side, d_q, nq, d_cid, d_cs, c, k, bits, overfetch, d_ids, d_sc)
+    return d_ids.download(np.int64, (nq, kk)), d_sc.download(np.float32, (nq, kk))
+
+
+def test_sidecar_bit_exact(rt):
+    _case("f16 sidecar 4096 x 37 incl. ties, subnormals, overflow")
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((4096, 37)) * np.exp(rng.uniform(-18, 12, (4096, 37)))).astype(np.float32)
+    special = np.array([1.0, np.uint32(0x3F801000).view(np.float32), 65519.0, 65520.0, 70000.0,
+                        np.inf, -np.inf, 2.0 ** -25, 2.0 ** -24, -0.0, 0.0], np.float32)
+    x.ravel()[:special.size] = special
+    side = F16Sidecar(rt, x)
+    assert np.array_equal(side.halves(), oracle.f32_to_half(x))
+
+
+def test_rerank_known_answer_sums(rt):
+    _case("rerank sequential-sum and no-FMA known answers")
+    third = np.float32(1.0) / np.float32(3.0)
+    for q, row, want in (([1, 1, 1, 1], [1.0, 2.0 ** -24, 2.0 ** -24, 2.0 ** -24], 1.0),
+                         ([1.0, third], [-1.0, 3.0], 0.0)):
+        side = F16Sidecar(rt, np.array([row], np.float32))
+        ids, sc = _rerank(rt, side, np.array([q], np.float32), np.array([[0]], np.int64),
+                          np.zeros((1, 1), np.float32), 1, 4, 200)
+        assert ids[0, 0] == 0 and sc[0, 0].view(np.uint32) == np.float32(want).view(np.uint32)
+
+
+@pytest.mark.parametrize("n", [119, 121])
+def test_reference_rescue_fixture(rt, n):
+    _case(f"rescue fixture n={n}")
+    d = 8
+    x = np.zeros((n + 1, d), np.float32)
+    x[1:, 0] = (n - np.arange(n)).astype(np.float32)   # doc i+1 scores n-i
+    side = F16Sidecar(rt, x)
+    q = np.zeros((1, d), np.float32)
+    q[0, 0] = 1
+    order = list(range(1, n + 1))
+    comp = [float(n - i) for i in range(n)]
+    if n == 121:   # d120 strongest at the first stage (rank 1)
+        order = [120] + [i for i in order if i != 120]
+        comp = [10000.0] + [float(n - i + 1) for i in order[1:]]
+    cid = np.array([order], np.int64)
+    cs = np.array([comp], np.float32)
+    ids, sc = _rerank(rt, side, q, cid, cs, 100, 4, 200)
+    wids, wsc = oracle.fp16_rerank(q, side.halves(), cid, cs, 100, 4, 200)
+    assert np.array_equal(ids, wids) and np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))
+    if n == 121:
+        assert ids[0, 99] == 120 and 100 not in ids[0, :100].tolist()
+    else:
+        assert ids[0].tolist() == list(range(1, 101))
+
+
+def test_rerank_edges(rt):
+    _case("rerank edges: missing ids, k=0, k>c, odd dim")
+    rng = np.random.default_rng(9)
+    n, d = 500, 13
+    side = F16Sidecar(rt, rng.standard_normal((n, d)).astype(np.float32))
+    q = rng.standard_normal((3, d)).astype(np.float32)
+    cid = np.stack([rng.permutation(n)[:64] for _ in range(3)]).astype(np.int64)
+    cid[0, 3], cid[1, 10], cid[2, :] = -1, n + 7, -1
+    cs = rng.standard_normal(cid.shape).astype(np.float32)
+    for k in (0, 10, 64, 100):
+        ids, sc = _rerank(rt, side, q, cid, cs, k, 4, 200)
+        wids, wsc = oracle.fp16_rerank(q, side.halves(), cid, cs, k, 4, 200)
+        assert np.array_equal(ids, wids) and np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))
+    assert (ids[2] == -1).all()
+
+
+@pytest.mark.parametrize("k,overfetch", [(100, 200), (100, 300), (150, 200)])
+def test_two_stage_end_to_end(rt, k, overfetch):
+    _case(f"two-stage 20000 x 384 b4 Q=16 k={k} overfetch={overfetch}")
+    c = datagen.TurboQuantCorpus(20000, 384, 4, 41, 42, 43, rotation=True)
+    rng = np.random.default_rng(44)
+    docs = rng.standard_normal((c.n, c.dim)).astype(np.float32)
+    docs /= np.linalg.norm(docs, axis=1, keepdims=True)
+    q = rng.standard_normal((16, c.dim)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    idx = TurboQuantIndex(rt, c.codes, c.norms, c.dim, c.bits, c.codebook, c.codebook_scale,
+                          c.rotation)
+    side = F16Sidecar(rt, docs)
+    ids, sc, cand = turboquant_fp16_rerank_top_k(idx, side, q, k, overfetch)
+    wc_ids, wc_sc = oracle.tq_topk(q, c.rotation, c.dim, c.bits, c.codebook, c.codebook_scale,
+                                   c.codes, c.norms, overfetch)
+    assert np.array_equal(cand, wc_ids)
+    wids, wsc = oracle.fp16_rerank(q, oracle.f32_to_half(docs), wc_ids, wc_sc, k, 4, overfetch)
+    assert np.array_equal(ids, wids) and np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))

@@ -1,0 +1,140 @@
+"""Pins the CPU oracle of the two-stage retrieval's second stage (f16 rerank).
+
+* float32ToHalf (runtime/mll_export.go:1007-1041): known answers where it
+  departs from round-to-nearest-even (ties round away from zero; finite values
+  >= 2^16 keep mantissa bits under the all-ones exponent), agreement with
+  numpy's float16 cast everywhere else, and the exact round trip of all 63,488
+  finite halves.
+* halfToFloat32 (runtime/weight_file.go:461-483): equals numpy's exact
+  float16 -> float32 widening for every non-NaN half.
+* The rerank score is a sequential f32 sum of f32 products: known answers that
+  an f64 accumulator, another summation order or a fused multiply-add fail.
+* applyTurboQuantFP16RerankRescue: the reference's three rescue tests
+  (runtime/retrieval_eval_test.go:1336-1380, fixture :1434-1445) restated.
+* topFP16RerankScores: brute force (Python sort by (score desc, id asc)).
+"""
+import numpy as np
+import pytest
+
+import oracle
+
+
+def _bits(x):
+    return int(np.float32(x).view(np.uint32))
+
+
+def _f(u):
+    return np.uint32(u).view(np.float32)
+
+
+@pytest.mark.parametrize("value,want", [
+    (1.0, 0x3C00),
+    (_f(0x3F801000), 0x3C01),        # 1 + 2^-11: tie, away from zero (RNE gives 0x3C00)
+    (_f(0xBF801000), 0xBC01),        # negative tie
+    (_f(0x3F803000), 0x3C02),        # 1 + 3*2^-11: tie to 0x3C02 either way
+    (65504.0, 0x7BFF),
+    (65519.0, 0x7BFF),
+    (65520.0, 0x7C00),               # tie at the top rounds up to infinity
+    (70000.0, 0x7C45),               # finite >= 2^16 keeps mantissa bits: NaN pattern
+    (float("inf"), 0x7C00),
+    (2.0 ** -24, 0x0001),
+    (2.0 ** -25, 0x0001),            # subnormal tie rounds up (RNE gives 0)
+    (2.0 ** -26, 0x0000),
+    (-0.0, 0x8000),
+])
+def test_f32_to_half_known_answers(value, want):
+    assert int(oracle.f32_to_half(np.array([value], np.float32))[0]) == want
+
+
+def test_f32_to_half_matches_rne_off_ties():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(200000) * np.exp(rng.uniform(-12, 10, 200000))).astype(np.float32)
+    u = x.view(np.uint32)
+    ex = ((u >> 23) & 0xFF).astype(np.int64) - 127
+    normal = (ex >= -14) & (ex <= 15)
+    tie = (u & 0x1FFF) == 0x1000
+    sel = normal & ~tie
+    got = oracle.f32_to_half(x[sel])
+    want = x[sel].astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_half_round_trip_and_widening_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    finite = (h & 0x7C00) != 0x7C00
+    wide = oracle.half_to_f32(h)
+    ref = h.view(np.float16).astype(np.float32)
+    notnan = ~np.isnan(ref)
+    assert np.array_equal(wide[notnan].view(np.uint32), ref[notnan].view(np.uint32))
+    assert np.array_equal(oracle.f32_to_half(ref[finite]), h[finite])
+
+
+def _one(q, row_halves, k=1):
+    rows = np.array([row_halves], np.uint16)
+    ids, scores = oracle.fp16_rerank(np.array([q], np.float32), rows, np.array([[0]], np.int64),
+                                     np.array([[0.0]], np.float32), k)
+    return scores[0, 0]
+
+
+def test_score_is_sequential_f32():
+    # 1 + 2^-24 + 2^-24 + 2^-24 in order stays 1 in f32; f64 or a reversed
+    # order gives a larger value.
+    s = _one([1, 1, 1, 1], [0x3C00, 0x0001, 0x0001, 0x0001])
+    assert _bits(s) == _bits(1.0)
+
+
+def test_score_has_no_fused_multiply_add():
+    # -1 + fl(fl(1/3) * 3) = -1 + 1 = 0; with a fused multiply-add it is 2^-25-ish.
+    third = np.float32(1.0) / np.float32(3.0)
+    s = _one([1.0, third], [0xBC00, 0x4200])
+    assert _bits(s) == 0
+
+
+def _rescue_fixture(n):
+    ids = np.arange(1, n + 1, dtype=np.int64)
+    scores = (n - np.arange(n)).astype(np.float32)
+    return ids, scores, np.arange(1, n + 1), scores.copy()
+
+
+def test_rescue_leaves_incomplete_window_unchanged():
+    ids, s, ranks, comp = _rescue_fixture(119)
+    assert np.array_equal(oracle.apply_rescue(ids, s, ranks, comp), ids)
+
+
+def test_rescue_promotes_strong_compact_boundary_candidate():
+    ids, s, ranks, comp = _rescue_fixture(121)
+    comp[119], ranks[119] = 10000, 1          # d120
+    got = oracle.apply_rescue(ids, s, ranks, comp)
+    assert 120 in got[:100] and 100 not in got[:100]
+    assert got[99] == 120
+
+
+def test_rescue_compact_tie_break():
+    ids, s, ranks, comp = _rescue_fixture(121)
+    comp[109] = comp[110] = 10000             # d110, d111
+    ranks[109] = ranks[110] = 7
+    assert oracle.apply_rescue(ids, s, ranks, comp)[99] == 111
+
+
+def test_rerank_brute_force_no_rescue():
+    rng = np.random.default_rng(11)
+    n, d, c = 300, 24, 150
+    rows = oracle.f32_to_half(rng.standard_normal((n, d)).astype(np.float32) * 0.2)
+    rows[7] = rows[8]                           # a score tie: id order decides
+    q = rng.standard_normal((2, d)).astype(np.float32)
+    cid = np.stack([rng.permutation(n)[:c] for _ in range(2)]).astype(np.int64)
+    cid[0, :2] = [8, 7]
+    cid[1, 5] = n + 3                           # no row: skipped
+    ids, scores = oracle.fp16_rerank(q, rows, cid, np.zeros_like(cid, np.float32), 40)
+    for i in range(2):
+        sc = []
+        for j in cid[i]:
+            if j >= n:
+                continue
+            acc = np.float32(0)
+            for t in range(d):
+                acc = np.float32(acc + np.float32(q[i, t] * np.float32(rows[j, t].view(np.float16))))
+            sc.append((-float(acc), int(j), acc))
+        sc.sort()
+        assert [j for _, j, _ in sc[:40]] == ids[i].tolist()
+        assert np.array_equal(np.array([a for _, _, a in sc[:40]], np.float32), scores[i])
