@@ -1657,18 +1657,30 @@ __device__ __attribute__((noinline)) float rr_dot(const float* qv, const unsigne
   float s = 0.0f;
   int i = 0;
   if ((d & 7) == 0) {
+    // 16 row loads in flight per chunk; the sum still runs in index order.
     const uint4* r4 = reinterpret_cast<const uint4*>(row);
-    for (; i < d; i += 8) {
-      const uint4 w = r4[i >> 3];
-      const unsigned ws[4] = {w.x, w.y, w.z, w.w};
+    const int nch = d >> 3;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+      uint4 buf[16];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float p0 = qv[i + 2 * t] * ref_half_to_f32(ws[t] & 0xffffu);
-        s = s + p0;
-        const float p1 = qv[i + 2 * t + 1] * ref_half_to_f32(ws[t] >> 16);
-        s = s + p1;
+      for (int u = 0; u < 16; ++u)
+        if (c0 + u < nch) buf[u] = r4[c0 + u];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        if (c0 + u < nch) {
+          const unsigned ws[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
+          const int b = (c0 + u) * 8;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float p0 = qv[b + 2 * t] * ref_half_to_f32(ws[t] & 0xffffu);
+            s = s + p0;
+            const float p1 = qv[b + 2 * t + 1] * ref_half_to_f32(ws[t] >> 16);
+            s = s + p1;
+          }
+        }
       }
     }
+    i = d;
   }
   for (; i < d; ++i) {
     const float p = qv[i] * ref_half_to_f32(row[i]);
@@ -1691,6 +1703,7 @@ extern "C" __global__ __launch_bounds__(kRrThreads) void eos_tq_fp16_rerank(TqRe
   __shared__ float fscore[kRrMaxCand];
   __shared__ int outpos[kRrMaxCand];
   __shared__ unsigned char seen[kRrMaxCand];
+  __shared__ unsigned long long pool_key[kRescueHi - kRescueLo + 1];
   __shared__ int valid_n;
   const int qi = blockIdx.x, tid = threadIdx.x;
   const long long* cid = a.cand_ids + (size_t)qi * a.c;
@@ -1738,26 +1751,37 @@ extern "C" __global__ __launch_bounds__(kRrThreads) void eos_tq_fp16_rerank(TqRe
   const int m = valid_n;
   const int nout = a.kk < m ? a.kk : m;
   if (a.rescue && m >= kRescueHi && m > kRescueTopK) {
+    // The pool is ranks kRescueLo..kRescueHi (1-based), so ranks below
+    // kRescueLo are never promoted and keep their places.
+    constexpr int pool = kRescueHi - kRescueLo + 1;
+    if (tid < pool) {
+      const int p = pos[kRescueLo - 1 + tid];
+      pool_key[tid] = ((unsigned long long)rr_desc(a.cand_scores[(size_t)qi * a.c + p]) << 32) |
+                      (unsigned)(p + 1);
+    }
+    for (int i = tid; i < kRescueLo - 1 && i < nout; i += kRrThreads) {
+      outpos[i] = pos[i];
+      seen[pos[i]] = 1;
+    }
+    __syncthreads();
     if (tid == 0) {
-      // Ranks kRescueLo..kRescueHi (1-based) by (first-stage score desc,
-      // first-stage rank asc); the first kRescuePromote are promoted.
+      // Pool order: first-stage score desc, first-stage rank asc; the first
+      // kRescuePromote are promoted.
       int promoted[kRescuePromote];
       unsigned long long taken = 0;
-      const int pool = kRescueHi - kRescueLo + 1;
       for (int r = 0; r < kRescuePromote; ++r) {
         int best = -1;
         unsigned long long bk = ~0ull;
         for (int i = 0; i < pool; ++i) {
           if (taken >> i & 1ull) continue;
-          const int p = pos[kRescueLo - 1 + i];
-          const unsigned long long ck = ((unsigned long long)rr_desc(a.cand_scores[(size_t)qi * a.c + p]) << 32) | (unsigned)(p + 1);
+          const unsigned long long ck = pool_key[i];
           if (best < 0 || ck < bk) { best = i; bk = ck; }
         }
         taken |= 1ull << best;
         promoted[r] = pos[kRescueLo - 1 + best];
       }
-      int o = 0;
-      for (int i = 0; i < kRescueTopK && o < nout; ++i) {
+      int o = nout < kRescueLo - 1 ? nout : kRescueLo - 1;
+      for (int i = kRescueLo - 1; i < kRescueTopK && o < nout; ++i) {
         const int p = pos[i];
         bool pr = false;
         for (int r = 0; r < kRescuePromote; ++r) pr |= promoted[r] == p;
@@ -1770,7 +1794,7 @@ extern "C" __global__ __launch_bounds__(kRrThreads) void eos_tq_fp16_rerank(TqRe
         outpos[o++] = promoted[r];
         seen[promoted[r]] = 1;
       }
-      for (int i = 0; i < m && o < nout; ++i) {
+      for (int i = kRescueLo - 1; i < m && o < nout; ++i) {
         if (seen[pos[i]]) continue;
         outpos[o++] = pos[i];
         seen[pos[i]] = 1;
