@@ -24,6 +24,13 @@ class EosHipTQDesc(C.Structure):
     ]
 
 
+class EosHipTQBindOptions(C.Structure):
+    _fields_ = [
+        ("zero_vector_allowed", C.POINTER(C.c_uint8)),
+        ("id_rank", C.POINTER(C.c_int64)),
+    ]
+
+
 class EosHipTQStats(C.Structure):
     _fields_ = [
         ("candidate_count", C.c_int64),
@@ -116,6 +123,12 @@ _SIGNATURES = {
                              C.c_int),
     "eoship_tq_bind_corpus": ([C.c_void_p, C.POINTER(EosHipTQDesc), C.c_void_p, C.c_void_p,
                                C.c_int64, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_tq_bind_corpus_opts": ([C.c_void_p, C.POINTER(EosHipTQDesc), C.c_void_p, C.c_void_p,
+                                    C.c_int64, C.POINTER(EosHipTQBindOptions),
+                                    C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_tq_vector_bytes": ([C.c_int32, C.c_int32, C.POINTER(C.c_int64), C.c_void_p], C.c_int),
+    "eoship_tq_mse_vector_bytes": ([C.c_int32, C.c_int32, C.POINTER(C.c_int64), C.c_void_p],
+                                   C.c_int),
     "eoship_tq_release": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_tq_share": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
     "eoship_tq_topk": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
@@ -141,8 +154,8 @@ _SIGNATURES = {
     "eoship_f16_sidecar_device": ([C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_tq_fp16_rerank_device": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
                                       C.c_int64, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
-                                      C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p],
-                                     C.c_int),
+                                      C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.c_void_p], C.c_int),
     "eoship_tq_encode": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
                           C.c_void_p], C.c_int),
     "eoship_tq_encode_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p,
@@ -175,6 +188,8 @@ _SIGNATURES = {
     "eoship_encoder_forward_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_status": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_int32), C.c_void_p], C.c_int),
+    "eoship_encoder_attention_moves": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_int64), C.c_void_p],
+                                       C.c_int),
 }
 
 _lib = None

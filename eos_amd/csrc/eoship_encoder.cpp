@@ -170,7 +170,7 @@ struct EosHipEncoder {
         rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_off), err) ||
         rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_cnt), err) ||
         rt->alloc(4, reinterpret_cast<void**>(&total), err) ||
-        rt->alloc(4, reinterpret_cast<void**>(&status), err))
+        rt->alloc(8, reinterpret_cast<void**>(&status), err))
       return 1;
     // At least 64 zeroed entries past the rows (attention reads whole 64-key
     // blocks); 72, so that the row stride is no multiple of 1 KiB (with +64
@@ -190,7 +190,8 @@ struct EosHipEncoder {
     if (ensure_activations(batch, tokens, err) != 0) return 1;
     const int H = desc.hidden, F = desc.intermediate, nh = desc.heads, hd = H / nh;
     const int max_rows = (int)row_capacity(batch, tokens);
-    hipError_t e = hipMemsetAsync(status, 0, 4, rt->stream);
+    // status[0]: an id out of range; status[1]: attention reference moves.
+    hipError_t e = hipMemsetAsync(status, 0, 8, rt->stream);
     if (e != hipSuccess) return hip_err(err, "hipMemsetAsync(status)", e);
     EncPackArgs pk{d_mask, row_b, row_t, seq_off, seq_cnt, total, batch, tokens};
     if (rt->launch("eos_enc_count", dim3(batch), dim3(256), 0, &pk, err) != 0 ||
@@ -254,7 +255,7 @@ struct EosHipEncoder {
                "enc_gemm_qkv", vt) != 0)
         return 1;
       EncAttnArgs at{qkv, vt, ctx, seq_off, seq_cnt, batch, nh, H, tokens, vt_ld,
-                     (float)(1.4426950408889634 / std::sqrt((double)hd))};
+                     (float)(1.4426950408889634 / std::sqrt((double)hd)), status + 1};
       if (rt->launch(attn_name, dim3((tokens + 127) / 128, nh, batch), dim3(256), 0, &at, err) != 0)
         return 1;
       if (gemm(ctx, L.w_o, nullptr, L.s_o, L.b_o, h, h, H, H, 3, "enc_gemm_o") != 0 ||
@@ -491,6 +492,20 @@ int eoship_encoder_status(EosHipRuntime* rt, EosHipEncoder* enc, int32_t* status
   hipError_t e = hipMemcpyAsync(status, enc->status, 4, hipMemcpyDeviceToHost, rt->stream);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
   return rt->sync(err);
+}
+
+int eoship_encoder_attention_moves(EosHipRuntime* rt, EosHipEncoder* enc, int64_t* moves,
+                                   char** err) {
+  if (rt == nullptr || enc == nullptr || moves == nullptr)
+    return set_err(err, "eoship_encoder_attention_moves: NULL argument");
+  *moves = 0;
+  if (enc->status == nullptr) return 0;
+  int32_t v = 0;
+  hipError_t e = hipMemcpyAsync(&v, enc->status + 1, 4, hipMemcpyDeviceToHost, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(moves)", e);
+  if (rt->sync(err) != 0) return 1;
+  *moves = v;
+  return 0;
 }
 
 int eoship_encoder_forward(EosHipRuntime* rt, EosHipEncoder* enc, const int32_t* ids,

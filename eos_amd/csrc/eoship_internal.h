@@ -11,7 +11,7 @@
 
 #include "eoship.h"
 
-#define EOSHIP_ABI_VERSION 4
+#define EOSHIP_ABI_VERSION 5
 
 namespace eoship {
 
@@ -47,11 +47,28 @@ struct Runtime {
   int launch(const char* name, dim3 grid, dim3 block, size_t lds, void* args, char** err,
              const char* label = nullptr);
   int alloc(size_t bytes, void** p, char** err);
+  // A device workspace owned by the runtime, grown (never shrunk) on demand
+  // and reused by later calls on the same stream; freed with the runtime.
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  int workspace(size_t bytes, void** p, char** err);
   void release(void* p);
   int sync(char** err);
   int flush_profile(char** err);
   int take_event(hipEvent_t* ev, char** err);
 };
+
+// Two-stage rerank on a caller-chosen scratch buffer of at least
+// q * c * 4 bytes (the candidates' f32 scores between its two kernels).
+int tq_fp16_rerank_launch(Runtime* rt, const float* d_queries, int32_t q, int32_t d,
+                          const uint16_t* d_rows, int64_t n, const int64_t* d_cand_ids,
+                          const float* d_cand_scores, int32_t c, int32_t k, int32_t bit_width,
+                          int32_t overfetch, const int64_t* d_id_rank, int64_t* d_ids,
+                          float* d_scores, float* scratch, const char* what, char** err);
+int tq_fp16_rerank_check(const Runtime* rt, const float* d_queries, int32_t q, int32_t d,
+                         const uint16_t* d_rows, int64_t n, const int64_t* d_cand_ids,
+                         const float* d_cand_scores, int32_t c, int64_t* d_ids, float* d_scores,
+                         const char* what, char** err);
 
 }  // namespace eoship
 

@@ -114,6 +114,22 @@ int Runtime::alloc(size_t bytes, void** p, char** err) {
   return 0;
 }
 
+int Runtime::workspace(size_t bytes, void** p, char** err) {
+  if (bytes > ws_bytes) {
+    if (ws != nullptr) {
+      // Earlier launches on this stream may still read the old block.
+      if (sync(err) != 0) return 1;
+      hipFree(ws);
+      ws = nullptr;
+      ws_bytes = 0;
+    }
+    if (alloc(bytes, &ws, err) != 0) return 1;
+    ws_bytes = bytes;
+  }
+  *p = ws;
+  return 0;
+}
+
 void Runtime::release(void* p) {
   if (p != nullptr) hipFree(p);
 }
@@ -215,6 +231,7 @@ int eoship_runtime_destroy(EosHipRuntime* rt, char** err) {
   for (auto& ev : rt->timer)
     if (ev) hipEventDestroy(ev);
   for (hipModule_t m : rt->builtin) hipModuleUnload(m);
+  if (rt->ws != nullptr) hipFree(rt->ws);
   hipError_t e = hipStreamDestroy(rt->stream);
   delete rt;
   if (e != hipSuccess) return hip_err(err, "hipStreamDestroy", e);

@@ -144,8 +144,14 @@ struct EosHipTQ {
   // host-API staging
   void* io = nullptr;
   size_t io_bytes = 0;
+  // Corpus bound with an ID order (EosHipTQBindOptions::id_rank): vector i
+  // sits at position rank[i], so position order is the string-ID order the
+  // ties follow; id_map[p] (device) is the vector index at position p,
+  // reported in its place. Empty / nullptr for index order.
+  long long* id_map = nullptr;
+  std::vector<int64_t> rank_host;
   // Handles sharing the corpus arrays (packed, norms, rot_t, tile_cn,
-  // codes_rm) through eoship_tq_share; nullptr while this is the only one.
+  // codes_rm, id_map) through eoship_tq_share; nullptr while this is the only one.
   int* corpus_refs = nullptr;
 
   void free_all() {
@@ -156,7 +162,7 @@ struct EosHipTQ {
     if (corpus_refs != nullptr && --*corpus_refs > 0) return;
     delete corpus_refs;
     corpus_refs = nullptr;
-    void* corpus[] = {packed, norms, rot_t, tile_cn, codes_rm};
+    void* corpus[] = {packed, norms, rot_t, tile_cn, codes_rm, id_map};
     for (void* p : corpus)
       if (p) hipFree(p);
   }
@@ -402,6 +408,7 @@ struct EosHipTQ {
     f.cap = kCap;
     f.kk = kk;
     f.q = qb;
+    f.id_map = id_map;
     if (rt->launch("eos_tq_finalize", dim3(qb), dim3(256), 0, &f, err) != 0) return 1;
     if (gated) return fallback_batch(d_queries, qb, kk, d_ids, d_scores, d_status, false, err);
     return 0;
@@ -439,6 +446,7 @@ struct EosHipTQ {
     sel.kk = kk;
     sel.mode = 1;
     sel.nrows = qb;
+    sel.id_map = id_map;
     return rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err, "tq_fallback_select");
   }
 
@@ -471,6 +479,12 @@ extern "C" {
 
 int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uint8_t* codes,
                           const float* norms, int64_t n, EosHipTQ** out, char** err) {
+  return eoship_tq_bind_corpus_opts(rt, desc, codes, norms, n, nullptr, out, err);
+}
+
+int eoship_tq_bind_corpus_opts(EosHipRuntime* rt, const EosHipTQDesc* desc, const uint8_t* codes,
+                               const float* norms, int64_t n, const EosHipTQBindOptions* opts,
+                               EosHipTQ** out, char** err) {
   if (rt == nullptr || desc == nullptr || out == nullptr)
     return set_err(err, "eoship_tq_bind_corpus: NULL argument");
   *out = nullptr;
@@ -486,13 +500,55 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
     return set_err(err, "eoship_tq_bind_corpus: n must be in [0, 2^32-1) (got %lld)", (long long)n);
   if (n > 0 && (codes == nullptr || norms == nullptr))
     return set_err(err, "eoship_tq_bind_corpus: codes/norms are NULL");
+  // validateEosQuantizedVectorNorm (runtime/turboquant_quantized_vector.go:
+  // 25-34): Norm > 0 is accepted, Norm == 0 only for a vector the caller
+  // confirms as the genuine zero vector, anything else is refused. Infinite
+  // norms are refused too (the reference would score them as +-inf or NaN).
+  const uint8_t* zero_ok = opts != nullptr ? opts->zero_vector_allowed : nullptr;
   for (int64_t i = 0; i < n; ++i) {
-    if (!(norms[i] >= 0.f) || !std::isfinite(norms[i]))
+    const float nv = norms[i];
+    if (nv > 0.f && std::isfinite(nv)) continue;
+    if (nv == 0.f && zero_ok != nullptr && zero_ok[i] != 0) continue;
+    if (nv == 0.f)
       return set_err(err,
-                     "eoship_tq_bind_corpus: vector %lld has Norm %g; Norm must be finite and >= 0",
-                     (long long)i, (double)norms[i]);
+                     "eoship_tq_bind_corpus: vector %lld has Norm 0; refusing to score a vector that "
+                     "dropped its input-norm field (set zero_vector_allowed only for a confirmed "
+                     "genuine zero-vector input)",
+                     (long long)i);
+    return set_err(err,
+                   "eoship_tq_bind_corpus: vector %lld has non-positive or non-finite Norm %g",
+                   (long long)i, (double)nv);
+  }
+  // Optional ID order: a permutation of 0..n-1, checked before anything is
+  // allocated; codes and norms are laid out in that order.
+  const int64_t* id_rank = opts != nullptr ? opts->id_rank : nullptr;
+  std::vector<uint8_t> codes_perm;
+  std::vector<float> norms_perm;
+  std::vector<long long> map_host;
+  const size_t row_bytes_in = (size_t)(desc->dim * desc->bits + 7) / 8;
+  if (id_rank != nullptr && n > 0) {
+    std::vector<uint8_t> seen((size_t)n, 0);
+    map_host.resize((size_t)n);
+    for (int64_t i = 0; i < n; ++i) {
+      const int64_t r = id_rank[i];
+      if (r < 0 || r >= n || seen[(size_t)r])
+        return set_err(err, "eoship_tq_bind_corpus: id_rank is not a permutation of 0..n-1 (entry %lld = %lld)",
+                       (long long)i, (long long)r);
+      seen[(size_t)r] = 1;
+      map_host[(size_t)r] = (long long)i;
+    }
+    codes_perm.resize((size_t)n * row_bytes_in);
+    norms_perm.resize((size_t)n);
+    for (int64_t i = 0; i < n; ++i) {
+      const size_t r = (size_t)id_rank[i];
+      memcpy(&codes_perm[r * row_bytes_in], codes + (size_t)i * row_bytes_in, row_bytes_in);
+      norms_perm[r] = norms[i];
+    }
+    codes = codes_perm.data();
+    norms = norms_perm.data();
   }
   auto* tq = new EosHipTQ();
+  if (id_rank != nullptr && n > 0) tq->rank_host.assign(id_rank, id_rank + n);
   tq->rt = rt;
   tq->d = desc->dim;
   tq->bits = desc->bits;
@@ -640,8 +696,36 @@ int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uin
       return fail();
     }
   }
+  if (!map_host.empty()) {
+    if (rt->alloc(map_host.size() * sizeof(long long), reinterpret_cast<void**>(&tq->id_map), err) != 0)
+      return fail();
+    e = hipMemcpy(tq->id_map, map_host.data(), map_host.size() * sizeof(long long),
+                  hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      hip_err(err, "hipMemcpy(id_map)", e);
+      return fail();
+    }
+  }
   if (tq->alloc_scratch(err) != 0) return fail();
   *out = tq;
+  return 0;
+}
+
+int eoship_tq_vector_bytes(int32_t dim, int32_t bit_width, int64_t* bytes, char** err) {
+  if (bytes == nullptr) return set_err(err, "eoship_tq_vector_bytes: NULL output");
+  if (dim < 1 || bit_width < 1 || bit_width > 8)
+    return set_err(err, "eoship_tq_vector_bytes: dim must be >= 1 and bit_width in [1, 8]");
+  const int64_t mse = ((int64_t)dim * (bit_width - 1) + 7) / 8;
+  const int64_t signs = ((int64_t)dim + 7) / 8;
+  *bytes = mse + signs + 8;
+  return 0;
+}
+
+int eoship_tq_mse_vector_bytes(int32_t dim, int32_t bits, int64_t* bytes, char** err) {
+  if (bytes == nullptr) return set_err(err, "eoship_tq_mse_vector_bytes: NULL output");
+  if (dim < 1 || bits < 1 || bits > 8)
+    return set_err(err, "eoship_tq_mse_vector_bytes: dim must be >= 1 and bits in [1, 8]");
+  *bytes = ((int64_t)dim * bits + 7) / 8 + 4;
   return 0;
 }
 
@@ -667,6 +751,7 @@ int eoship_tq_share(EosHipRuntime* rt, EosHipTQ* src, EosHipTQ** out, char** err
   memcpy(tq->codebook, src->codebook, sizeof(tq->codebook));
   memcpy(tq->lut, src->lut, sizeof(tq->lut));
   tq->rs16 = src->rs16;
+  tq->rank_host = src->rank_host;
   if (tq->alloc_scratch(err) != 0) {
     tq->free_all();  // scratch only: the corpus arrays are not attached yet
     delete tq;
@@ -680,6 +765,7 @@ int eoship_tq_share(EosHipRuntime* rt, EosHipTQ* src, EosHipTQ** out, char** err
   tq->rot_t = src->rot_t;
   tq->tile_cn = src->tile_cn;
   tq->codes_rm = src->codes_rm;
+  tq->id_map = src->id_map;
   *out = tq;
   return 0;
 }
@@ -812,6 +898,33 @@ int eoship_tq_scores(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int3
   hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
   const int cap = tq->batch_cap();
+  if (tq->id_map != nullptr) {
+    // Ranked corpus: vector i sits at position rank[i]; every position is
+    // scored and the requested vectors are picked out on the host.
+    const int64_t n = tq->n;
+    std::vector<float> hs(scores ? (size_t)cap * n : 0);
+    std::vector<int32_t> hd(dots ? (size_t)cap * n : 0);
+    for (int q0 = 0; q0 < q; q0 += cap) {
+      const int qb = std::min(cap, q - q0);
+      if (tq->prepare(dq + (size_t)q0 * tq->d, qb, nullptr, err) != 0) return 1;
+      if (tq->dense_scores(qb, 0, n, dots != nullptr, err) != 0) return 1;
+      if (scores) e = hipMemcpyAsync(hs.data(), tq->dense, (size_t)qb * n * sizeof(float),
+                                     hipMemcpyDeviceToHost, rt->stream);
+      if (e == hipSuccess && dots)
+        e = hipMemcpyAsync(hd.data(), tq->dense_dots, (size_t)qb * n * sizeof(int32_t),
+                           hipMemcpyDeviceToHost, rt->stream);
+      if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(scores)", e);
+      if (rt->sync(err) != 0) return 1;
+      for (int r = 0; r < qb; ++r)
+        for (int64_t j = 0; j < count; ++j) {
+          const size_t src = (size_t)r * n + (size_t)tq->rank_host[(size_t)(begin + j)];
+          const size_t dst = (size_t)(q0 + r) * count + (size_t)j;
+          if (scores) scores[dst] = hs[src];
+          if (dots) dots[dst] = hd[src];
+        }
+    }
+    return 0;
+  }
   for (int q0 = 0; q0 < q; q0 += cap) {
     const int qb = std::min(cap, q - q0);
     if (tq->prepare(dq + (size_t)q0 * tq->d, qb, nullptr, err) != 0) return 1;
@@ -874,6 +987,9 @@ int maxsim_check(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, int32_t q, in
   if (rt == nullptr || tq == nullptr) return set_err(err, "%s: NULL runtime or corpus", what);
   if (tq->rt != rt) return set_err(err, "%s: corpus was bound on another runtime", what);
   if (q < 0) return set_err(err, "%s: negative query count", what);
+  if (tq->id_map != nullptr)
+    return set_err(err, "%s: documents need their vectors in index order (corpus bound with id_rank)",
+                   what);
   if (doc_len <= 0 || doc_len % kTile != 0)
     return set_err(err, "%s: doc_len must be a positive multiple of %d (got %d)", what, kTile, doc_len);
   if (tq->n % doc_len != 0)
@@ -1116,6 +1232,9 @@ int eoship_tq_parents_bind(EosHipRuntime* rt, EosHipTQ* tq, const int64_t* offse
     return set_err(err, "%s: NULL argument", what);
   *out = nullptr;
   if (tq->rt != rt) return set_err(err, "%s: corpus was bound on another runtime", what);
+  if (tq->id_map != nullptr)
+    return set_err(err, "%s: parents need their children in index order (corpus bound with id_rank)",
+                   what);
   if (nparents <= 0 || nparents > ((int64_t)1 << 31))
     return set_err(err, "%s: parent count must be in 1..2^31 (got %lld)", what, (long long)nparents);
   if (offsets[0] != 0 || offsets[nparents] != tq->n)
@@ -1295,6 +1414,58 @@ int eoship_tq_encode(EosHipRuntime* rt, EosHipTQ* tq, const float* x, int64_t n,
 
 // ------------------------------------------------- two-stage retrieval (f16)
 
+namespace eoship {
+
+int tq_fp16_rerank_check(const Runtime* rt, const float* d_queries, int32_t q, int32_t d,
+                         const uint16_t* d_rows, int64_t n, const int64_t* d_cand_ids,
+                         const float* d_cand_scores, int32_t c, int64_t* d_ids, float* d_scores,
+                         const char* what, char** err) {
+  if (rt == nullptr) return set_err(err, "%s: NULL runtime", what);
+  if (q < 0 || c < 0 || n < 0) return set_err(err, "%s: negative size", what);
+  if (d < 1 || d > 4096) return set_err(err, "%s: dim must be in [1, 4096]", what);
+  if (c > 4096)
+    return set_err(err, "%s: at most 4096 candidates per query (got %d; the reference takes any overfetch)",
+                   what, c);
+  if (q > 65535) return set_err(err, "%s: at most 65535 queries per call", what);
+  if (n >= ((int64_t)1 << 32) - 1)
+    return set_err(err, "%s: corpus must hold fewer than 2^32 - 1 rows", what);
+  if (q == 0 || c == 0) return 0;
+  if (d_queries == nullptr || d_rows == nullptr || d_cand_ids == nullptr || d_cand_scores == nullptr ||
+      d_ids == nullptr || d_scores == nullptr)
+    return set_err(err, "%s: NULL buffer", what);
+  return 0;
+}
+
+int tq_fp16_rerank_launch(Runtime* rt, const float* d_queries, int32_t q, int32_t d,
+                          const uint16_t* d_rows, int64_t n, const int64_t* d_cand_ids,
+                          const float* d_cand_scores, int32_t c, int32_t k, int32_t bit_width,
+                          int32_t overfetch, const int64_t* d_id_rank, int64_t* d_ids,
+                          float* d_scores, float* scratch, const char* what, char** err) {
+  (void)what;
+  TqRerankArgs a;
+  memset(&a, 0, sizeof(a));
+  a.queries = d_queries;
+  a.rows = reinterpret_cast<const unsigned short*>(d_rows);
+  a.cand_ids = reinterpret_cast<const long long*>(d_cand_ids);
+  a.cand_scores = d_cand_scores;
+  a.out_ids = reinterpret_cast<long long*>(d_ids);
+  a.out_scores = d_scores;
+  a.dots = scratch;
+  a.n = n;
+  a.d = d;
+  a.c = c;
+  a.kk = (k <= 0 || k > c) ? c : k;
+  a.id_rank = reinterpret_cast<const long long*>(d_id_rank);
+  // shouldApplyTurboQuantFP16RerankRescue (runtime/retrieval_turboquant.go:1664-1669).
+  a.rescue = (bit_width == 4 && k == 100 && overfetch == 200 && c >= 120) ? 1 : 0;
+  if (rt->launch("eos_tq_rr_dots", dim3((unsigned)((c + 63) / 64), (unsigned)q), dim3(64), 0, &a,
+                 err, "tq_fp16_rerank_dots") != 0)
+    return 1;
+  return rt->launch("eos_tq_rr_sort", dim3((unsigned)q), dim3(256), 0, &a, err, "tq_fp16_rerank_sort");
+}
+
+}  // namespace eoship
+
 extern "C" {
 
 int eoship_f16_sidecar_device(EosHipRuntime* rt, const float* d_x, int64_t count, uint16_t* d_half,
@@ -1315,32 +1486,18 @@ int eoship_f16_sidecar_device(EosHipRuntime* rt, const float* d_x, int64_t count
 int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int32_t q, int32_t d,
                                  const uint16_t* d_rows, int64_t n, const int64_t* d_cand_ids,
                                  const float* d_cand_scores, int32_t c, int32_t k,
-                                 int32_t bit_width, int32_t overfetch, int64_t* d_ids,
-                                 float* d_scores, char** err) {
-  if (rt == nullptr) return set_err(err, "eoship_tq_fp16_rerank_device: NULL runtime");
-  if (q < 0 || c < 0 || n < 0) return set_err(err, "eoship_tq_fp16_rerank_device: negative size");
-  if (d < 1 || d > 4096) return set_err(err, "eoship_tq_fp16_rerank_device: dim must be in [1, 4096]");
-  if (c > 1024) return set_err(err, "eoship_tq_fp16_rerank_device: at most 1024 candidates per query");
-  if (n >= ((int64_t)1 << 32) - 1)
-    return set_err(err, "eoship_tq_fp16_rerank_device: corpus must hold fewer than 2^32 - 1 rows");
+                                 int32_t bit_width, int32_t overfetch, const int64_t* d_id_rank,
+                                 int64_t* d_ids, float* d_scores, char** err) {
+  const char* what = "eoship_tq_fp16_rerank_device";
+  if (eoship::tq_fp16_rerank_check(rt, d_queries, q, d, d_rows, n, d_cand_ids, d_cand_scores, c,
+                                   d_ids, d_scores, what, err) != 0)
+    return 1;
   if (q == 0 || c == 0) return 0;
-  if (d_queries == nullptr || d_rows == nullptr || d_cand_ids == nullptr || d_cand_scores == nullptr ||
-      d_ids == nullptr || d_scores == nullptr)
-    return set_err(err, "eoship_tq_fp16_rerank_device: NULL buffer");
-  TqRerankArgs a;
-  a.queries = d_queries;
-  a.rows = reinterpret_cast<const unsigned short*>(d_rows);
-  a.cand_ids = reinterpret_cast<const long long*>(d_cand_ids);
-  a.cand_scores = d_cand_scores;
-  a.out_ids = reinterpret_cast<long long*>(d_ids);
-  a.out_scores = d_scores;
-  a.n = n;
-  a.d = d;
-  a.c = c;
-  a.kk = (k <= 0 || k > c) ? c : k;
-  // shouldApplyTurboQuantFP16RerankRescue (runtime/retrieval_turboquant.go:1664-1669).
-  a.rescue = (bit_width == 4 && k == 100 && overfetch == 200 && c >= 120) ? 1 : 0;
-  return rt->launch("eos_tq_fp16_rerank", dim3((unsigned)q), dim3(256), 0, &a, err, "tq_fp16_rerank");
+  void* ws = nullptr;
+  if (rt->workspace((size_t)q * (size_t)c * sizeof(float), &ws, err) != 0) return 1;
+  return eoship::tq_fp16_rerank_launch(rt, d_queries, q, d, d_rows, n, d_cand_ids, d_cand_scores,
+                                       c, k, bit_width, overfetch, d_id_rank, d_ids, d_scores,
+                                       static_cast<float*>(ws), what, err);
 }
 
 }  // extern "C"

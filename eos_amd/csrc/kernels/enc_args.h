@@ -87,6 +87,9 @@ struct EncAttnArgs {
   const int32_t* seq_cnt;
   int batch, heads, hidden, max_len, vt_ld;
   float scale_log2;        // log2(e) / sqrt(head_dim)
+  // Optional: counts (per wavefront) the exponent-reference moves after a
+  // sequence's first key block, the lazy-rescale path trained models reach.
+  int32_t* moves;
 };
 
 // mode 0: masked mean pool, then L2 normalize -> out [batch][hidden].

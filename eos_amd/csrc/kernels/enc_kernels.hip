@@ -916,13 +916,19 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     exps();
     const bool over = !(psum <= kSafe);  // also true for inf and NaN
     if (__ballot(over) != 0ull) {
+      if (a.moves != nullptr && k0 > 0 && lane == 0) atomicAdd(a.moves, 1);
       float mloc = -__builtin_inff();
 #pragma unroll
       for (int hh = 0; hh < NT; ++hh)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[hh][e]);
       const float mpair = fmaxf(mloc, __shfl_xor(mloc, 32));
-      const bool pover = over || __shfl_xor((int)over, 32) != 0;
+      // Both shuffles run with every lane active: a shuffle inside the
+      // short-circuit of `over || ...` would run only in the lanes that are
+      // not over and read 0 from the disabled partner, so a pair where only
+      // one lane overflows would move one lane and not the other.
+      const int over_pair = (over ? 1 : 0) | __shfl_xor(over ? 1 : 0, 32);
+      const bool pover = over_pair != 0;
       const float mnew = pover ? fmaxf(mpair, mrun) : mrun;
       // v_exp_f32 directly: the argument is <= 0 or -inf (exp2 -> 0).
       const float corr = __builtin_amdgcn_exp2f(mrun - mnew);

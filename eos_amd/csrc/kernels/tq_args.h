@@ -69,6 +69,7 @@ struct TqSelectArgs {
   int kk;                  // rank
   int mode;                // 0: tau = score of the kk-th best; 1: sorted top-kk
   int nrows;
+  const long long* id_map; // mode 1, optional [n]: element i is reported as id id_map[i]
 };
 
 struct TqFinalizeArgs {
@@ -78,6 +79,7 @@ struct TqFinalizeArgs {
   float* scores;      // [q][kk]
   int* status;        // [q]: 0 ok, 1 too few candidates, 2 overflow
   int cap, kk, q;
+  const long long* id_map;  // optional [n]: corpus position p is reported as id id_map[p]
 };
 
 // MaxSim over documents of tiles_per_doc consecutive tiles: per query group
@@ -169,7 +171,8 @@ struct TqHalfArgs {
 };
 
 // Second stage of two-stage retrieval: exact f16-row rerank of the overfetched
-// candidates of each query (one workgroup per query).
+// candidates of each query (eos_tq_rr_dots: one lane per candidate;
+// eos_tq_rr_sort: one workgroup per query).
 struct TqRerankArgs {
   const float* queries;          // [q][d]
   const unsigned short* rows;    // [n][d] halves
@@ -177,8 +180,12 @@ struct TqRerankArgs {
   const float* cand_scores;      // [q][c] first-stage scores
   long long* out_ids;            // [q][kk]
   float* out_scores;             // [q][kk]
+  float* dots;                   // [q][c] f32 rerank scores (scratch between the two kernels)
   long long n;
   int d, c, kk, rescue;
+  // Optional [n]: the order of id's string ID among the corpus IDs; equal
+  // rerank scores then rank by it instead of by the integer id.
+  const long long* id_rank;
 };
 
 #endif  // EOSHIP_TQ_ARGS_H

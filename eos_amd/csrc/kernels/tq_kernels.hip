@@ -1075,7 +1075,8 @@ extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_row_select(TqSe
   bitonic_sort_desc(list, npow);
   for (int i = tid; i < a.kk; i += kSelThreads) {
     const u64 c = list[i];
-    a.ids[(size_t)row * a.kk + i] = (long long)rank_id(c);
+    const uint32_t p = rank_id(c);
+    a.ids[(size_t)row * a.kk + i] = a.id_map != nullptr ? a.id_map[p] : (long long)p;
     a.scores[(size_t)row * a.kk + i] = key_score((uint32_t)(c >> 32));
   }
 }
@@ -1338,7 +1339,8 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
       uint32_t rank = 0;
 #pragma unroll 8
       for (uint32_t j = 0; j < kk; ++j) rank += sel[j] > x ? 1u : 0u;
-      a.ids[(size_t)row * kk + rank] = (long long)rank_id(x);
+      const uint32_t p = rank_id(x);
+      a.ids[(size_t)row * kk + rank] = a.id_map != nullptr ? a.id_map[p] : (long long)p;
       a.scores[(size_t)row * kk + rank] = key_score((uint32_t)(x >> 32));
     }
   } else {
@@ -1349,7 +1351,8 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
     bitonic_sort_desc(sel, npow);
     for (uint32_t i = tid; i < kk; i += kFinThreads) {
       const u64 x = sel[i];
-      a.ids[(size_t)row * kk + i] = (long long)rank_id(x);
+      const uint32_t p = rank_id(x);
+      a.ids[(size_t)row * kk + i] = a.id_map != nullptr ? a.id_map[p] : (long long)p;
       a.scores[(size_t)row * kk + i] = key_score((uint32_t)(x >> 32));
     }
   }
@@ -1636,7 +1639,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_f16_sidecar(TqHalfArgs 
 }
 
 constexpr int kRrThreads = 256;
-constexpr int kRrMaxCand = 1024;
+constexpr int kRrMaxCand = 4096;
 constexpr int kRrMaxDim = 4096;
 constexpr int kRescueTopK = 100, kRescueLo = 100, kRescueHi = 120, kRescuePromote = 5;
 
@@ -1652,19 +1655,23 @@ __device__ inline unsigned rr_desc(float s) {
 // One candidate's score: scoreValue += query[i] * halfToFloat32(half) in
 // order, each product and sum rounded to f32 (no fused multiply-add), as
 // topFP16RerankScores computes it (runtime/retrieval_turboquant.go:1646-1649).
-__device__ __attribute__((noinline)) float rr_dot(const float* qv, const unsigned short* row, int d) {
+// halfToFloat32 is exact for every finite half and for the infinities, where
+// it equals the hardware conversion; a NaN row element gives a NaN score
+// either way (NaN payloads are outside the ranking contract).
+__device__ inline float rr_dot(const float* qv, const unsigned short* row, int d) {
 #pragma clang fp contract(off)
   float s = 0.0f;
   int i = 0;
   if ((d & 7) == 0) {
     // 16 row loads in flight per chunk; the sum still runs in index order.
-    const uint4* r4 = reinterpret_cast<const uint4*>(row);
+    typedef unsigned v4u __attribute__((ext_vector_type(4)));
+    const v4u* r4 = reinterpret_cast<const v4u*>(row);
     const int nch = d >> 3;
     for (int c0 = 0; c0 < nch; c0 += 16) {
-      uint4 buf[16];
+      v4u buf[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u)
-        if (c0 + u < nch) buf[u] = r4[c0 + u];
+        if (c0 + u < nch) buf[u] = __builtin_nontemporal_load(r4 + c0 + u);
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         if (c0 + u < nch) {
@@ -1672,9 +1679,9 @@ __device__ __attribute__((noinline)) float rr_dot(const float* qv, const unsigne
           const int b = (c0 + u) * 8;
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const float p0 = qv[b + 2 * t] * ref_half_to_f32(ws[t] & 0xffffu);
+            const float p0 = qv[b + 2 * t] * (float)__builtin_bit_cast(_Float16, (unsigned short)(ws[t] & 0xffffu));
             s = s + p0;
-            const float p1 = qv[b + 2 * t + 1] * ref_half_to_f32(ws[t] >> 16);
+            const float p1 = qv[b + 2 * t + 1] * (float)__builtin_bit_cast(_Float16, (unsigned short)(ws[t] >> 16));
             s = s + p1;
           }
         }
@@ -1689,25 +1696,38 @@ __device__ __attribute__((noinline)) float rr_dot(const float* qv, const unsigne
   return s;
 }
 
-// Scores every candidate of one query from its f16 row, sorts them in LDS by
+// First rerank kernel: one lane per (query, candidate), spread over the whole
+// device (grid: candidate blocks of 64 x queries). The f32 score of candidate
+// j of query qi goes to a.dots[qi * c + j]; candidates whose id is outside
+// [0, n) have no row and are left unscored (the sort kernel skips them).
+extern "C" __global__ __launch_bounds__(64) void eos_tq_rr_dots(TqRerankArgs a) {
+  __shared__ float qv[kRrMaxDim];
+  const int qi = blockIdx.y, j = blockIdx.x * 64 + threadIdx.x;
+  for (int i = threadIdx.x; i < a.d; i += 64) qv[i] = a.queries[(size_t)qi * a.d + i];
+  __syncthreads();
+  if (j >= a.c) return;
+  const long long id = a.cand_ids[(size_t)qi * a.c + j];
+  if (id < 0 || id >= a.n) return;
+  a.dots[(size_t)qi * a.c + j] = rr_dot(qv, a.rows + (size_t)id * a.d, a.d);
+}
+
+// Second rerank kernel, one workgroup per query: sorts the candidates in LDS by
 // (score desc, id asc) -- the heap + insertion sort of topFP16RerankScores
 // (runtime/retrieval_turboquant.go:1635-1662) -- or, with rescue, by (score
 // desc, first-stage rank asc) (sortTurboQuantFP16RankedScores, :1698-1719;
 // ranks are distinct, so its id tie-break never decides) and then applies
 // applyTurboQuantFP16RerankRescue (:1721-1786). Candidates whose id is outside
 // [0, n) have no row and are skipped (`if !ok { continue }`).
-extern "C" __global__ __launch_bounds__(kRrThreads) void eos_tq_fp16_rerank(TqRerankArgs a) {
-  __shared__ float qv[kRrMaxDim];
+extern "C" __global__ __launch_bounds__(kRrThreads) void eos_tq_rr_sort(TqRerankArgs a) {
   __shared__ unsigned long long key[kRrMaxCand];
   __shared__ int pos[kRrMaxCand];
-  __shared__ float fscore[kRrMaxCand];
   __shared__ int outpos[kRrMaxCand];
   __shared__ unsigned char seen[kRrMaxCand];
   __shared__ unsigned long long pool_key[kRescueHi - kRescueLo + 1];
   __shared__ int valid_n;
   const int qi = blockIdx.x, tid = threadIdx.x;
   const long long* cid = a.cand_ids + (size_t)qi * a.c;
-  for (int i = tid; i < a.d; i += kRrThreads) qv[i] = a.queries[(size_t)qi * a.d + i];
+  const float* fscore = a.dots + (size_t)qi * a.c;
   if (tid == 0) valid_n = 0;
   int P = 1;
   while (P < a.c) P <<= 1;
@@ -1719,9 +1739,10 @@ extern "C" __global__ __launch_bounds__(kRrThreads) void eos_tq_fp16_rerank(TqRe
       const long long id = cid[j];
       seen[j] = 0;
       if (id >= 0 && id < a.n) {
-        const float s = rr_dot(qv, a.rows + (size_t)id * a.d, a.d);
-        fscore[j] = s;
-        const unsigned tie = a.rescue ? (unsigned)(j + 1) : (unsigned)id;
+        const float s = fscore[j];
+        const unsigned tie = a.rescue            ? (unsigned)(j + 1)
+                             : a.id_rank != nullptr ? (unsigned)a.id_rank[id]
+                                                    : (unsigned)id;
         k = ((unsigned long long)rr_desc(s) << 32) | tie;
         ++my_valid;
       }

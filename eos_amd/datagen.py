@@ -163,10 +163,19 @@ def baseline_queries(q: int, dim: int, seed: int = 6) -> np.ndarray:
 
 def bert_q8_weights(layers: int, hidden: int, heads: int, inter: int, vocab: int, npos: int,
                     ntype: int = 2, seed: int = 7, eps: float = 1e-12, gelu: int = 1,
-                    random_affine: bool = False):
+                    random_affine: bool = False, peaked: dict | None = None):
     """Random-init BERT-style encoder (weights N(0, 0.02)) quantized to int8
     per output channel. With random_affine, biases, LayerNorm gamma/beta are
-    drawn too (otherwise biases 0, gamma 1, beta 0)."""
+    drawn too (otherwise biases 0, gamma 1, beta 0).
+
+    peaked = {"alpha": a, "beta": b, "tokens": {id: mix}} plants peaked
+    attention: with u = (+1, -1, ...) / sqrt(H) and w = (+1, +1, -1, -1, ...)
+    / sqrt(H), token `id`'s embedding row becomes 3 (mix u + sqrt(1 - mix^2)
+    w), every layer's query bias gets b and its key weights a u^T on the first
+    feature of each head. Every query then scores such a key about
+    a b mix sqrt(H) / sqrt(hd) above the others (40 nats at a = 4, b = 3, mix
+    1, H = 384, hd = 32), so the key's position decides in which key block the
+    softmax maximum appears."""
     from .encoder import EncoderLayerWeights, EncoderWeights, quantize_per_channel
 
     counter = [seed * 1000003]
@@ -185,15 +194,28 @@ def bert_q8_weights(layers: int, hidden: int, heads: int, inter: int, vocab: int
     tok = draw((vocab, H))
     pos = draw((npos, H))
     typ = draw((ntype, H))
+    hd = H // heads
+    if peaked is not None:
+        u = np.where(np.arange(H) % 2 == 0, 1.0, -1.0) / np.sqrt(H)
+        wdir = np.where((np.arange(H) // 2) % 2 == 0, 1.0, -1.0) / np.sqrt(H)
+        for tid, mix in peaked["tokens"].items():
+            tok[tid] = (3.0 * (mix * u + np.sqrt(max(0.0, 1.0 - mix * mix)) * wdir)).astype(np.float32)
     w = EncoderWeights(hidden=H, heads=heads, intermediate=F, ln_eps=eps, gelu=gelu, tok=tok,
                        pos=pos, typ=typ, emb_gamma=vec(H, 1.0, 0.1), emb_beta=vec(H, 0.0, 0.05))
     for _ in range(layers):
-        qkv, sq = quantize_per_channel(draw((3 * H, H)))
+        # Draw order as before the peaked option (same weights for every seed).
+        wqkv = draw((3 * H, H))
         wo, so = quantize_per_channel(draw((H, H)))
         w1, s1 = quantize_per_channel(draw((F, H)))
         w2, s2 = quantize_per_channel(draw((H, F)))
+        bqkv = vec(3 * H)
+        if peaked is not None:
+            for h in range(heads):
+                wqkv[H + h * hd] += np.float32(peaked["alpha"]) * u.astype(np.float32)
+                bqkv[h * hd] = np.float32(peaked["beta"])
+        qkv, sq = quantize_per_channel(wqkv)
         w.layers.append(EncoderLayerWeights(
-            w_qkv=qkv, s_qkv=sq, b_qkv=vec(3 * H), w_o=wo, s_o=so, b_o=vec(H),
+            w_qkv=qkv, s_qkv=sq, b_qkv=bqkv, w_o=wo, s_o=so, b_o=vec(H),
             ln1_gamma=vec(H, 1.0, 0.1), ln1_beta=vec(H, 0.0, 0.05), w_1=w1, s_1=s1, b_1=vec(F),
             w_2=w2, s_2=s2, b_2=vec(H), ln2_gamma=vec(H, 1.0, 0.1), ln2_beta=vec(H, 0.0, 0.05)))
     return w

@@ -255,6 +255,13 @@ class Encoder:
         _lib.call("eoship_encoder_status", self.rt.handle, self.handle, C.byref(st))
         return st.value
 
+    def attention_moves(self) -> int:
+        """Diagnostic of the last forward: attention wavefronts that moved their
+        softmax exponent reference after a sequence's first key block."""
+        mv = C.c_int64()
+        _lib.call("eoship_encoder_attention_moves", self.rt.handle, self.handle, C.byref(mv))
+        return int(mv.value)
+
 
 class CompactEncoder(Encoder):
     """A compact (family (a)) embedder bound on the device; ``embed`` takes

@@ -32,6 +32,34 @@ from . import _lib
 from .runtime import DeviceBuffer, Runtime
 
 
+def string_id_rank(ids) -> np.ndarray:
+    """Position of each ID among the IDs sorted ascending by Go string order
+    (bytewise UTF-8), as int64 [n]; IDs must be distinct."""
+    keys = [str(x).encode("utf-8") for x in ids]
+    order = sorted(range(len(keys)), key=lambda i: keys[i])
+    rank = np.empty(len(keys), np.int64)
+    rank[np.asarray(order, dtype=np.int64)] = np.arange(len(keys), dtype=np.int64)
+    if len(set(keys)) != len(keys):
+        raise ValueError("document IDs must be distinct")
+    return rank
+
+
+def turboquant_vector_bytes(dim: int, bit_width: int) -> int:
+    """turboquantVectorBytes (runtime/turboquant_bytes.go:14-25): MSE codes at
+    bit_width - 1 bits, QJL signs at one bit per coordinate, plus Norm and
+    ResNorm (8 bytes)."""
+    out = C.c_int64()
+    _lib.call("eoship_tq_vector_bytes", C.c_int32(dim), C.c_int32(bit_width), C.byref(out))
+    return int(out.value)
+
+
+def turboquant_mse_vector_bytes(dim: int, bits: int) -> int:
+    """Bytes per vector of the MSE-stage layout bound here: codes + one f32 Norm."""
+    out = C.c_int64()
+    _lib.call("eoship_tq_mse_vector_bytes", C.c_int32(dim), C.c_int32(bits), C.byref(out))
+    return int(out.value)
+
+
 @dataclass
 class RetrievalScoredDoc:
     """One ranked result (runtime/retrieval_eval.go retrievalScoredDoc): ID is the vector index."""
@@ -55,13 +83,22 @@ class TurboQuantIndex:
     """A TurboQuant corpus bound on the device.
 
     codes: uint8 [n, ceil(dim*bits/8)] (coordinate j at bit (j*bits)%8 of byte
-    (j*bits)//8, low bits first); norms: float32 [n], finite and >= 0;
-    codebook: int8 [2^bits] grid values with f32 scale; rotation: float32
-    [dim, dim] orthogonal (None = identity).
+    (j*bits)//8, low bits first); norms: float32 [n], finite and > 0 (the
+    Norm policy of validateEosQuantizedVectorNorm,
+    runtime/turboquant_quantized_vector.go:25-34); codebook: int8 [2^bits]
+    grid values with f32 scale; rotation: float32 [dim, dim] orthogonal (None =
+    identity).
+
+    zero_vector_allowed: None, True (every vector of Norm 0 is a confirmed
+    genuine zero vector) or a bool array [n] (zeroVectorAllowed per vector).
+    ids: None (IDs order like the indices) or the documents' string IDs [n];
+    equal scores then rank by string ID ascending (retrievalScoreBetter,
+    runtime/retrieval_eval.go:1153-1161), and results still report indices.
     """
 
     def __init__(self, rt: Runtime, codes: np.ndarray, norms: np.ndarray, dim: int, bits: int,
-                 codebook: np.ndarray, codebook_scale: float, rotation: np.ndarray | None = None):
+                 codebook: np.ndarray, codebook_scale: float, rotation: np.ndarray | None = None,
+                 zero_vector_allowed=None, ids=None):
         codes = np.ascontiguousarray(codes, dtype=np.uint8)
         norms = np.ascontiguousarray(norms, dtype=np.float32)
         n = int(norms.shape[0])
@@ -80,8 +117,23 @@ class TurboQuantIndex:
             codebook=cb.ctypes.data_as(C.POINTER(C.c_int8)),
             rotation=rot.ctypes.data_as(C.POINTER(C.c_float)) if rot is not None else None)
         self.handle = C.c_void_p()
-        _lib.call("eoship_tq_bind_corpus", rt.handle, C.byref(desc), codes.ctypes.data_as(C.c_void_p),
-                  norms.ctypes.data_as(C.c_void_p), C.c_int64(n), C.byref(self.handle))
+        self.id_rank = None
+        opts = _lib.EosHipTQBindOptions()
+        keep = []
+        if zero_vector_allowed is not None:
+            z = np.broadcast_to(np.asarray(zero_vector_allowed, dtype=bool), (n,))
+            z = np.ascontiguousarray(z, dtype=np.uint8)
+            keep.append(z)
+            opts.zero_vector_allowed = z.ctypes.data_as(C.POINTER(C.c_uint8))
+        if ids is not None:
+            self.id_rank = string_id_rank(ids)
+            if self.id_rank.shape != (n,):
+                raise ValueError(f"ids must hold {n} entries")
+            opts.id_rank = self.id_rank.ctypes.data_as(C.POINTER(C.c_int64))
+        _lib.call("eoship_tq_bind_corpus_opts", rt.handle, C.byref(desc),
+                  codes.ctypes.data_as(C.c_void_p), norms.ctypes.data_as(C.c_void_p), C.c_int64(n),
+                  C.byref(opts), C.byref(self.handle))
+        del keep
 
     def share(self, rt: Runtime) -> "TurboQuantIndex":
         """A handle on the same resident corpus for another runtime (stream)
@@ -91,6 +143,7 @@ class TurboQuantIndex:
         _lib.call("eoship_tq_share", rt.handle, self.handle, C.byref(h))
         other = TurboQuantIndex.__new__(TurboQuantIndex)
         other.rt, other.n, other.dim, other.bits, other.handle = rt, self.n, self.dim, self.bits, h
+        other.id_rank = self.id_rank
         return other
 
     def release(self) -> None:
@@ -371,13 +424,17 @@ class F16Sidecar:
 def top_fp16_rerank_scores_device(sidecar: F16Sidecar, d_queries: DeviceBuffer, nq: int,
                                   d_cand_ids: DeviceBuffer, d_cand_scores: DeviceBuffer, c: int,
                                   top_k: int, bit_width: int, overfetch: int,
-                                  d_ids: DeviceBuffer, d_scores: DeviceBuffer) -> int:
+                                  d_ids: DeviceBuffer, d_scores: DeviceBuffer,
+                                  d_id_rank: DeviceBuffer | None = None) -> int:
     """topFP16RerankScores / topFP16RerankRescueScores for nq queries on device
-    buffers (runtime/retrieval_turboquant.go:1551-1556, :1635-1786). Returns kk."""
+    buffers (runtime/retrieval_turboquant.go:1551-1556, :1635-1786). c is the
+    first stage's output width, min(overfetch, n). d_id_rank (int64 [n], the
+    string-ID order) breaks equal scores by string ID. Returns kk."""
     _lib.call("eoship_tq_fp16_rerank_device", sidecar.rt.handle, d_queries.ptr, C.c_int32(nq),
               C.c_int32(sidecar.dim), sidecar.buf.ptr, C.c_int64(sidecar.n), d_cand_ids.ptr,
               d_cand_scores.ptr, C.c_int32(c), C.c_int32(int(top_k)), C.c_int32(int(bit_width)),
-              C.c_int32(int(overfetch)), d_ids.ptr, d_scores.ptr)
+              C.c_int32(int(overfetch)), d_id_rank.ptr if d_id_rank is not None else None,
+              d_ids.ptr, d_scores.ptr)
     return c if (top_k <= 0 or top_k > c) else int(top_k)
 
 
@@ -403,11 +460,12 @@ def turboquant_fp16_rerank_top_k(index: "TurboQuantIndex", sidecar: F16Sidecar,
     kk = c if top_k > c else top_k
     d_ids = DeviceBuffer(rt, max(8, nq * kk * 8))
     d_sc = DeviceBuffer(rt, max(4, nq * kk * 4))
+    d_rank = DeviceBuffer.from_array(rt, index.id_rank) if index.id_rank is not None else None
     top_fp16_rerank_scores_device(sidecar, d_q, nq, d_cid, d_cs, c, top_k, index.bits, overfetch,
-                                  d_ids, d_sc)
+                                  d_ids, d_sc, d_rank)
     ids = d_ids.download(np.int64, (nq, kk))
     scores = d_sc.download(np.float32, (nq, kk))
     cand = d_cid.download(np.int64, (nq, c))
-    for b in (d_q, d_cid, d_cs, d_ids, d_sc):
+    for b in (d_q, d_cid, d_cs, d_ids, d_sc) + ((d_rank,) if d_rank is not None else ()):
         b.free()
     return ids, scores, cand

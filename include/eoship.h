@@ -111,10 +111,45 @@ typedef struct {
 
 /* Binds a corpus: uploads codes and norms and repacks the codes into the
  * MFMA tile layout. Replaces the per-document turboquant.IPQuantized slice
- * the host loop walks (runtime/retrieval_turboquant.go:704-711). Norms must be
- * finite and >= 0 (runtime/turboquant_quantized_vector.go:25-34). */
+ * the host loop walks (runtime/retrieval_turboquant.go:704-711). The Norm
+ * policy is validateEosQuantizedVectorNorm's
+ * (runtime/turboquant_quantized_vector.go:25-34): Norm > 0 is accepted;
+ * Norm == 0 is refused here (a vector that dropped its norm field) and
+ * accepted only through eoship_tq_bind_corpus_opts for a vector the caller
+ * confirms as a genuine zero vector; negative, NaN and infinite norms are
+ * refused. */
 int eoship_tq_bind_corpus(EosHipRuntime* rt, const EosHipTQDesc* desc, const uint8_t* codes,
                           const float* norms, int64_t n, EosHipTQ** out, char** err);
+
+typedef struct {
+  /* [n] or NULL: nonzero when the caller confirms that vector i was the
+   * genuine zero vector, so its Norm == 0 is accepted (zeroVectorAllowed of
+   * validateEosQuantizedVectorNorm / newEosQuantizedVector,
+   * runtime/turboquant_quantized_vector.go:25-49). */
+  const uint8_t* zero_vector_allowed;
+  /* [n] or NULL: the position of vector i's string ID among the corpus IDs
+   * sorted ascending (Go string order), a permutation of 0..n-1. Equal
+   * scores then rank by string ID as retrievalScoreBetter does
+   * (runtime/retrieval_eval.go:1153-1161; e.g. "d1" < "d10" < "d2"); results
+   * still report vector indices. NULL: IDs order like their indices. A ranked
+   * corpus serves flat top-k and eoship_tq_scores; MaxSim documents and
+   * parents need index order and refuse it. */
+  const int64_t* id_rank;
+} EosHipTQBindOptions;
+
+/* eoship_tq_bind_corpus with options (opts may be NULL: no options). */
+int eoship_tq_bind_corpus_opts(EosHipRuntime* rt, const EosHipTQDesc* desc, const uint8_t* codes,
+                               const float* norms, int64_t n, const EosHipTQBindOptions* opts,
+                               EosHipTQ** out, char** err);
+
+/* Stored bytes of one turboquant.IPQuantized vector: (bit_width - 1)-bit MSE
+ * codes and one QJL sign bit per coordinate, each packed to whole bytes, plus
+ * the Norm and ResNorm f32 fields (turboquantVectorBytes,
+ * runtime/turboquant_bytes.go:14-25: 136 B at dim 256, bit width 4). */
+int eoship_tq_vector_bytes(int32_t dim, int32_t bit_width, int64_t* bytes, char** err);
+/* Bytes of one vector of the MSE-stage layout this library binds:
+ * ceil(dim * bits / 8) code bytes plus one f32 Norm (196 B at dim 384, 4 bits). */
+int eoship_tq_mse_vector_bytes(int32_t dim, int32_t bits, int64_t* bytes, char** err);
 int eoship_tq_release(EosHipTQ* tq, char** err);
 /* A second handle on a bound corpus for another runtime (stream) of the same
  * device: it shares the resident corpus arrays and owns its own per-call
@@ -308,6 +343,13 @@ int eoship_encoder_forward_device(EosHipRuntime* rt, EosHipEncoder* enc, const i
                                   int32_t tokens, float* d_out, char** err);
 /* 0 when every id of the last forward was in range; synchronises. */
 int eoship_encoder_status(EosHipRuntime* rt, EosHipEncoder* enc, int32_t* status, char** err);
+/* Diagnostic of the last forward (synchronises): how many times a wavefront
+ * of the attention kernels moved its softmax exponent reference after a
+ * sequence's first key block (a score far above every earlier one, as peaked
+ * late-maximum attention gives). No counterpart in the reference, whose host
+ * softmax subtracts the exact maximum (bert_encoder_layer_ops.go:272-324). */
+int eoship_encoder_attention_moves(EosHipRuntime* rt, EosHipEncoder* enc, int64_t* moves,
+                                   char** err);
 
 /* Compact transformer embedder (family (a): the graph that
  * compactTransformerSource emits, models/default_embedding.go:419-505, with
@@ -360,18 +402,23 @@ int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc
 int eoship_f16_sidecar_device(EosHipRuntime* rt, const float* d_x, int64_t count, uint16_t* d_half,
                               char** err);
 /* Reranks each query's first-stage candidates (d_cand_ids/d_cand_scores
- * [Q][c], c <= 1024, in first-stage order as eoship_tq_topk_device writes them)
- * by the f16 rows d_rows [n][d]: topFP16RerankScores, or
- * topFP16RerankRescueScores when shouldApplyTurboQuantFP16RerankRescue(bit_width,
- * k, overfetch, c) holds (runtime/retrieval_turboquant.go:1551-1556,
- * :1635-1786). Scores are sequential f32 sums of f32 products. k <= 0 or k > c
- * means k = c; outputs [Q][kk]; a query with fewer than kk candidates in
- * [0, n) pads its row with id -1 and score 0. Enqueued on the runtime stream. */
+ * [Q][c], in first-stage order as eoship_tq_topk_device writes them) by the
+ * f16 rows d_rows [n][d]: topFP16RerankScores, or topFP16RerankRescueScores
+ * when shouldApplyTurboQuantFP16RerankRescue(bit_width, k, overfetch, c)
+ * holds (runtime/retrieval_turboquant.go:1551-1556, :1635-1786). c must be
+ * the first stage's output width, min(overfetch, n), and at most 4096 (the
+ * reference takes any overfetch; larger c is refused). Scores are sequential
+ * f32 sums of f32 products. Equal scores rank by id ascending, or by
+ * d_id_rank[id] ([n], the string-ID order of EosHipTQBindOptions::id_rank)
+ * when it is not NULL. k <= 0 or k > c means k = c; outputs [Q][kk]; a query
+ * with fewer than kk candidates in [0, n) pads its row with id -1 and score 0.
+ * Enqueued on the runtime stream; uses a workspace of Q * c * 4 bytes that the
+ * runtime allocates on first use and keeps. */
 int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int32_t q, int32_t d,
                                  const uint16_t* d_rows, int64_t n, const int64_t* d_cand_ids,
                                  const float* d_cand_scores, int32_t c, int32_t k,
-                                 int32_t bit_width, int32_t overfetch, int64_t* d_ids,
-                                 float* d_scores, char** err);
+                                 int32_t bit_width, int32_t overfetch, const int64_t* d_id_rank,
+                                 int64_t* d_ids, float* d_scores, char** err);
 
 #ifdef __cplusplus
 }

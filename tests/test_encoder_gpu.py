@@ -125,3 +125,66 @@ def test_baseline_c4_long_context(rt):
     n = int(lens[b])
     want = _oracle(w, ids[b:b + 1, :n], np.ones((1, n), np.int32))
     _check(got[b:b + 1], want)
+
+
+def _peaked_batch(tokens, vocab, special):
+    """Sequences with the planted high-scoring tokens at chosen positions:
+    (ids, mask); `special` maps sequence -> [(position, token id)], every
+    other token is drawn from ids >= 3."""
+    rng = np.random.default_rng(77)
+    b = len(special)
+    ids = rng.integers(3, vocab, size=(b, tokens)).astype(np.int32)
+    mask = np.ones((b, tokens), np.int32)
+    for s, plants in special.items():
+        for p, t in plants:
+            ids[s, p] = t
+    mask[4, 40:] = 0
+    ids[4, 40:] = 0
+    return ids, mask
+
+
+@pytest.mark.parametrize("hidden,heads,inter", [(384, 12, 1536), (512, 8, 2048), (512, 4, 1024)])
+def test_attention_late_maximum_moves_reference(rt, hidden, heads, inter):
+    """Peaked, late-maximum attention (trained-model regime): a key far above
+    every earlier one (about 25-40 nats) appears after the first key block,
+    so the lazy-rescale branch moves the exponent reference, rescales O and
+    the partial sums and recomputes the block (enc_kernels.hip attention).
+    Sequence 0 moves twice (a weaker key in block 1..2, the strongest later),
+    sequence 1 has its maximum in block 0 (no move), sequence 2 only at its
+    end, sequence 3 has no planted key, sequence 4 is short with the key at
+    its last positions. Only one lane of a query's pair holds the key."""
+    hd = hidden // heads
+    _case(f"peaked attention hd={hd}")
+    peaked = {"alpha": 4.0, "beta": 3.0, "tokens": {1: 1.0, 2: 0.6}}
+    w = datagen.bert_q8_weights(2, hidden, heads, inter, 2000, 512, seed=hidden + heads,
+                                random_affine=True, peaked=peaked)
+    special = {0: [(80, 2), (200, 1)], 1: [(5, 1), (150, 2)], 2: [(300, 1)], 3: [],
+               4: [(35, 1), (38, 2)]}
+    ids, mask = _peaked_batch(320, 2000, special)
+    enc = Encoder(rt, w)
+    got = enc.embed(ids, mask)
+    moves = enc.attention_moves()
+    print(f"  later-block reference moves: {moves}", flush=True)
+    assert moves > 0
+    _check(got, _oracle(w, ids, mask))
+
+
+def test_w8a8_outlier_channels(rt):
+    """LayerNorm outputs with a few channels 30-50x the others (as trained
+    BERT models have): the per-row int8 activations of the QKV and FFN-up
+    GEMMs then leave the other channels a few levels, and the contract must
+    still hold (a float64 simulation of this case gives min cos 0.9999987)."""
+    _case("W8A8 with outlier channels")
+    w = datagen.bert_q8_weights(3, 384, 12, 1536, 2000, 512, seed=31, random_affine=True)
+    rng = np.random.default_rng(32)
+    for nch, factor in ((3, 50.0), (8, 30.0)):
+        ch = rng.choice(384, nch, replace=False)
+        gammas = [w.emb_gamma] + [L.ln1_gamma for L in w.layers] + [L.ln2_gamma for L in w.layers]
+        for g in gammas:
+            g[ch] *= np.float32(factor)
+        for L in w.layers:
+            L.ln1_beta[ch[:1]] += np.float32(0.5 * factor)
+        ids, mask, _ = datagen.encoder_batch(8, 256, 2000, 16, 256, 33 + nch, 34 + nch)
+        enc = Encoder(rt, w)
+        _check(enc.embed(ids, mask), _oracle(w, ids, mask))
+        enc.release()

@@ -95,7 +95,7 @@ def test_maxsim_zero_scores_keep_the_oracle_sign(rt):
     norms[20 * doc_len: 21 * doc_len] = 0.0
     q = _tokens(3, 4, d, 31)
     idx = TurboQuantIndex(rt, c.codes, norms, c.dim, c.bits, c.codebook, c.codebook_scale,
-                          c.rotation)
+                          c.rotation, zero_vector_allowed=True)
     mv = TurboQuantMultiVectorIndex(idx, doc_len)
     got = mv.scores(q)
     want = oracle.tq_maxsim_scores(q, c.rotation, d, bits, c.codebook, c.codebook_scale, c.codes,

@@ -110,3 +110,78 @@ def test_two_stage_end_to_end(rt, k, overfetch):
     assert np.array_equal(cand, wc_ids)
     wids, wsc = oracle.fp16_rerank(q, oracle.f32_to_half(docs), wc_ids, wc_sc, k, 4, overfetch)
     assert np.array_equal(ids, wids) and np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))
+
+
+def test_rerank_subnormal_and_infinite_rows(rt):
+    """Rows holding subnormal halves, signed zeros and infinities (d a multiple
+    of 8, the vectorised path): scores equal the oracle's bit for bit."""
+    _case("rerank subnormal / inf rows")
+    rng = np.random.default_rng(12)
+    n, d = 64, 16
+    x = (rng.standard_normal((n, d)) * 2.0 ** rng.integers(-26, -12, (n, d))).astype(np.float32)
+    x[5, 3], x[6, 0], x[7, 7] = np.inf, -np.inf, -0.0
+    side = F16Sidecar(rt, x)
+    h = side.halves()
+    assert np.any((h & 0x7c00) == 0) and np.any(((h & 0x7c00) == 0) & ((h & 0x3ff) != 0))
+    q = rng.standard_normal((4, d)).astype(np.float32)
+    q[3] = np.abs(q[3])
+    cid = np.stack([rng.permutation(n)[:40] for _ in range(4)]).astype(np.int64)
+    cs = np.zeros(cid.shape, np.float32)
+    ids, sc = _rerank(rt, side, q, cid, cs, 40, 4, 200)
+    wids, wsc = oracle.fp16_rerank(q, h, cid, cs, 40, 4, 200)
+    assert np.array_equal(ids, wids) and np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))
+
+
+def test_rerank_large_candidate_lists(rt):
+    """c above the old 1024 limit (the reference takes any overfetch), up to the
+    4096 this kernel holds; 4097 is refused with a message."""
+    _case("rerank c=3000 and c=4096; c=4097 refused")
+    from eos_amd._lib import EosHipError
+    rng = np.random.default_rng(13)
+    n, d = 6000, 64
+    side = F16Sidecar(rt, rng.standard_normal((n, d)).astype(np.float32))
+    q = rng.standard_normal((3, d)).astype(np.float32)
+    for c in (3000, 4096):
+        cid = np.stack([rng.permutation(n)[:c] for _ in range(3)]).astype(np.int64)
+        cs = np.sort(rng.standard_normal(cid.shape).astype(np.float32), axis=1)[:, ::-1].copy()
+        for k in (100, 0):
+            ids, sc = _rerank(rt, side, q, cid, cs, k, 4, c)
+            wids, wsc = oracle.fp16_rerank(q, side.halves(), cid, cs, k, 4, c)
+            assert np.array_equal(ids, wids)
+            assert np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))
+    cid = np.zeros((1, 4097), np.int64)
+    with pytest.raises(EosHipError, match="4096"):
+        _rerank(rt, side, q[:1], cid, np.zeros((1, 4097), np.float32), 100, 4, 4097)
+
+
+def test_rerank_string_id_ties(rt):
+    """Equal rerank scores rank by string ID when the ID order is given
+    (retrievalScoreBetter, runtime/retrieval_eval.go:1153-1161)."""
+    _case("rerank string-id ties")
+    from eos_amd.turboquant import string_id_rank
+    rng = np.random.default_rng(14)
+    n, d = 300, 24
+    x = rng.standard_normal((n, d)).astype(np.float32)
+    x[rng.integers(0, n, 200)] = x[7]          # many exact duplicates of row 7
+    side = F16Sidecar(rt, x)
+    names = [f"p{int(i)}" for i in rng.permutation(n)]
+    rank = string_id_rank(names)
+    q = rng.standard_normal((2, d)).astype(np.float32)
+    cid = np.stack([rng.permutation(n)[:150] for _ in range(2)]).astype(np.int64)
+    cs = np.zeros(cid.shape, np.float32)
+    d_q = DeviceBuffer.from_array(rt, q)
+    d_cid = DeviceBuffer.from_array(rt, cid)
+    d_cs = DeviceBuffer.from_array(rt, cs)
+    d_rank = DeviceBuffer.from_array(rt, rank)
+    d_ids, d_sc = DeviceBuffer(rt, 2 * 150 * 8), DeviceBuffer(rt, 2 * 150 * 4)
+    top_fp16_rerank_scores_device(side, d_q, 2, d_cid, d_cs, 150, 0, 4, 200, d_ids, d_sc, d_rank)
+    ids = d_ids.download(np.int64, (2, 150))
+    sc = d_sc.download(np.float32, (2, 150))
+    # the oracle over rows laid out in ID order ranks ties by position = ID order
+    inv = np.empty_like(rank)
+    inv[rank] = np.arange(n)
+    wpos, wsc = oracle.fp16_rerank(q, side.halves()[inv], rank[cid], cs, 0, 4, 200)
+    assert np.array_equal(ids, inv[wpos])
+    assert np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))
+    plain, _ = oracle.fp16_rerank(q, side.halves(), cid, cs, 0, 4, 200)
+    assert not np.array_equal(plain, ids)

@@ -23,10 +23,10 @@ def _corpus(n, d, bits, seed=21, rotation=True):
     return datagen.TurboQuantCorpus(n, d, bits, seed, seed + 1, seed + 2, rotation=rotation)
 
 
-def _index(rt, c, norms=None, codes=None):
+def _index(rt, c, norms=None, codes=None, **kw):
     return TurboQuantIndex(rt, c.codes if codes is None else codes,
                            c.norms if norms is None else norms, c.dim, c.bits, c.codebook,
-                           c.codebook_scale, c.rotation)
+                           c.codebook_scale, c.rotation, **kw)
 
 
 def _oracle_scores(c, q, norms=None, codes=None, begin=0, count=None):
@@ -226,7 +226,7 @@ def test_topk_zero_norms_zero_query_and_k_semantics(rt):
     c = _corpus(500, 384, 4, seed=7)
     norms = c.norms.copy()
     norms[::3] = 0.0
-    idx = _index(rt, c, norms=norms)
+    idx = _index(rt, c, norms=norms, zero_vector_allowed=True)
     q = datagen.baseline_queries(3, 384, 12)
     q[1] = 0.0
     for k in (0, -5, 500, 10_000, 1):
@@ -245,7 +245,7 @@ def test_reference_tie_case(rt):
     """runtime/turboquant_retrieval_pruning_test.go:80-99 with integer ids."""
     _case("reference tie case")
     c = _corpus(2, 32, 4, seed=8)
-    idx = _index(rt, c, norms=np.zeros(2, np.float32))
+    idx = _index(rt, c, norms=np.zeros(2, np.float32), zero_vector_allowed=True)
     q = np.zeros((1, 32), np.float32)
     q[0, 0] = 1.0
     docs, _ = top_turboquant_retrieval_scores_with_stats(idx, q, 1)
@@ -263,6 +263,123 @@ def test_bind_rejects_bad_norms(rt):
     bad[4] = np.nan
     with pytest.raises(EosHipError, match="Norm"):
         _index(rt, c, norms=bad)
+    bad[4] = np.inf
+    with pytest.raises(EosHipError, match="Norm"):
+        _index(rt, c, norms=bad)
+    with pytest.raises(EosHipError, match="Norm"):   # -1 even when zero vectors are allowed
+        bad[4] = -1.0
+        _index(rt, c, norms=bad, zero_vector_allowed=True)
+
+
+def test_zero_norm_needs_zero_vector_allowed(rt):
+    """validateEosQuantizedVectorNorm (runtime/turboquant_quantized_vector.go:
+    25-34): Norm == 0 is the dropped-norm footgun unless the caller confirms a
+    genuine zero vector, per vector."""
+    _case("bind zero-norm policy")
+    from eos_amd._lib import EosHipError
+    c = _corpus(10, 32, 4, seed=9)
+    z = c.norms.copy()
+    z[6] = 0.0
+    with pytest.raises(EosHipError, match="vector 6 has Norm 0"):
+        _index(rt, c, norms=z)
+    allow = np.zeros(10, bool)
+    allow[5] = True                                  # another vector: still refused
+    with pytest.raises(EosHipError, match="vector 6 has Norm 0"):
+        _index(rt, c, norms=z, zero_vector_allowed=allow)
+    allow[6] = True
+    idx = _index(rt, c, norms=z, zero_vector_allowed=allow)
+    q = datagen.baseline_queries(2, 32, 3)
+    _, sc = idx.inner_product_prepared(q)
+    assert np.all(sc[:, 6] == 0.0)
+    idx.release()
+    _index(rt, c, zero_vector_allowed=allow).release()   # positive norms need no flag
+
+
+def _ranked_oracle(c, codes, norms, q, k, rank):
+    """The oracle on the corpus laid out in string-ID order, mapped back: its
+    index tie order is then the string-ID order."""
+    inv = np.empty_like(rank)
+    inv[rank] = np.arange(rank.size)
+    pids, psc = oracle.tq_topk(q, c.rotation, c.dim, c.bits, c.codebook, c.codebook_scale,
+                               codes[inv], norms[inv], k)
+    return inv[pids], psc
+
+
+def test_string_id_tie_order(rt):
+    """Equal scores rank by string ID (retrievalScoreBetter,
+    runtime/retrieval_eval.go:1153-1161): with IDs "d0".."d11" and all scores
+    equal the order is d0, d1, d10, d11, d2, ..., not the index order."""
+    _case("string id ties (small)")
+    from eos_amd.turboquant import string_id_rank
+    c = _corpus(12, 64, 4, seed=41)
+    codes = np.repeat(c.codes[:1], 12, axis=0)
+    norms = np.ones(12, np.float32)
+    names = [f"d{i}" for i in range(12)]
+    idx = _index(rt, c, norms=norms, codes=codes, ids=names)
+    q = datagen.baseline_queries(2, 64, 5)
+    ids, sc, _ = idx.top_k(q, 5)
+    want = [0, 1, 10, 11, 2]
+    np.testing.assert_array_equal(ids, [want, want])
+    assert np.all(sc == sc[:, :1])
+    rank = string_id_rank(names)
+    np.testing.assert_array_equal(rank, [0, 1, 4, 5, 6, 7, 8, 9, 10, 11, 2, 3])
+    # scores are still addressed by vector index
+    _, dense = idx.inner_product_prepared(q, 3, 6)
+    np.testing.assert_array_equal(dense, np.repeat(sc[:, :1], 6, axis=1))
+    idx.release()
+
+
+def test_string_id_ties_at_the_cut_filter_path(rt):
+    """Filter path (n > 8192) with heavy exact ties at the top-k cut: 20000
+    vectors drawn from 40 distinct code rows, IDs with mixed widths."""
+    _case("string id ties (filter path)")
+    c = _corpus(20000, 128, 4, seed=43)
+    rng = np.random.default_rng(44)
+    pick = rng.integers(0, 40, size=20000)
+    codes = np.ascontiguousarray(c.codes[pick])
+    norms = np.ones(20000, np.float32)
+    names = [f"doc-{int(i)}" for i in rng.permutation(20000)]
+    idx = _index(rt, c, norms=norms, codes=codes, ids=names)
+    q = datagen.baseline_queries(8, 128, 45)
+    for k in (100, 700):
+        ids, sc, _ = idx.top_k(q, k)
+        wids, wsc = _ranked_oracle(c, codes, norms, q, k, idx.id_rank)
+        np.testing.assert_array_equal(ids, wids)
+        np.testing.assert_array_equal(sc, wsc)
+        plain, _ = oracle.tq_topk(q, c.rotation, 128, 4, c.codebook, c.codebook_scale, codes,
+                                  norms, k)
+        assert not np.array_equal(plain, wids)   # the two tie orders differ here
+    idx.release()
+
+
+def test_ranked_corpus_refuses_documents_and_parents(rt):
+    _case("ranked corpus: documents / parents refused")
+    from eos_amd._lib import EosHipError
+    from eos_amd.turboquant import TurboQuantMultiVectorIndex, TurboQuantParents
+    c = _corpus(64, 32, 4, seed=46)
+    idx = _index(rt, c, ids=[str(i) for i in range(64)])
+    with pytest.raises(EosHipError, match="index order"):
+        TurboQuantMultiVectorIndex(idx, 32).scores(datagen.baseline_queries(1, 32, 1))
+    with pytest.raises(EosHipError, match="index order"):
+        TurboQuantParents(idx, np.array([0, 10, 64]))
+    with pytest.raises(EosHipError, match="permutation"):
+        _lib_bind_bad_rank(rt, c)
+    idx.release()
+
+
+def _lib_bind_bad_rank(rt, c):
+    import ctypes as C
+    from eos_amd import _lib
+    rank = np.zeros(c.n, np.int64)   # not a permutation
+    cb = np.ascontiguousarray(c.codebook, np.int8)
+    desc = _lib.EosHipTQDesc(dim=c.dim, bits=c.bits, codebook_scale=float(c.codebook_scale),
+                             codebook=cb.ctypes.data_as(C.POINTER(C.c_int8)), rotation=None)
+    opts = _lib.EosHipTQBindOptions()
+    opts.id_rank = rank.ctypes.data_as(C.POINTER(C.c_int64))
+    h = C.c_void_p()
+    _lib.call("eoship_tq_bind_corpus_opts", rt.handle, C.byref(desc),
+              c.codes.ctypes.data_as(C.c_void_p), c.norms.ctypes.data_as(C.c_void_p),
+              C.c_int64(c.n), C.byref(opts), C.byref(h))
 
 
 def test_baseline_c2_full_size(rt):
