@@ -156,6 +156,11 @@ _SIGNATURES = {
                                       C.c_int64, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
                                       C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_void_p], C.c_int),
+    "eoship_tq_fp16_rerank_device_noalloc": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                              C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+                                              C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                              C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
+                                             C.c_int),
     "eoship_tq_encode": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
                           C.c_void_p], C.c_int),
     "eoship_tq_encode_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p,

@@ -6,7 +6,9 @@
 2. The code objects are linked into the shared library as read-only data
    (``.incbin``) and loaded at runtime creation with ``hipModuleLoadData``.
 3. The host shim (plain C++ over the HIP runtime API) is compiled with g++ into
-   ``eos_amd/libeoship.so``.
+   ``eos_amd/libeoship.so``, together with the objects hipcc builds from the
+   host sources that declare device variables (the static scratch of the
+   no-allocation entry points).
 
 Run ``python -m eos_amd.build`` or call :func:`build`.
 """
@@ -29,6 +31,10 @@ ARCH = "gfx950"
 DEVICE_SOURCES = [
     ("tq", os.path.join(CSRC, "kernels", "tq_kernels.hip")),
     ("enc", os.path.join(CSRC, "kernels", "enc_kernels.hip")),
+]
+# Host translation units that hold device variables (hipcc, host + device).
+HIP_HOST_SOURCES = [
+    os.path.join(CSRC, "eoship_noalloc.hip"),
 ]
 HOST_SOURCES = [
     os.path.join(CSRC, "eoship_runtime.cpp"),
@@ -78,6 +84,12 @@ def build(verbose: bool = False) -> str:
             f"eoship_{stem}_co_end:",
             ".byte 0",
         ]
+    hip_objs = []
+    for src in HIP_HOST_SOURCES:
+        obj = os.path.join(BUILD_DIR, os.path.splitext(os.path.basename(src))[0] + ".o")
+        _run([hipcc, *HIPCC_FLAGS, "-fPIC", "-c", "-I", os.path.join(REPO_DIR, "include"), "-I", CSRC,
+              "-o", obj, src], verbose)
+        hip_objs.append(obj)
     asm_path = os.path.join(BUILD_DIR, "eoship_blobs.S")
     with open(asm_path, "w") as f:
         f.write("\n".join(asm) + "\n")
@@ -86,7 +98,7 @@ def build(verbose: bool = False) -> str:
         "g++", "-O2", "-g", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
         "-Wno-unused-parameter", "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
         "-I", os.path.join(REPO_DIR, "include"), "-I", CSRC, "-I", os.path.join(ROCM, "include"),
-        *HOST_SOURCES, asm_path,
+        *HOST_SOURCES, *hip_objs, asm_path,
         "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
         "-Wl,--no-undefined", "-o", tmp,
     ], verbose)

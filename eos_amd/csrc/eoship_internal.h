@@ -65,6 +65,11 @@ int tq_fp16_rerank_launch(Runtime* rt, const float* d_queries, int32_t q, int32_
                           const float* d_cand_scores, int32_t c, int32_t k, int32_t bit_width,
                           int32_t overfetch, const int64_t* d_id_rank, int64_t* d_ids,
                           float* d_scores, float* scratch, const char* what, char** err);
+// Resolves the no-allocation entry points' static scratch on `device` (which
+// must be current); called once per runtime creation, failures are reported
+// by those entry points.
+void noalloc_init(int device);
+
 int tq_fp16_rerank_check(const Runtime* rt, const float* d_queries, int32_t q, int32_t d,
                          const uint16_t* d_rows, int64_t n, const int64_t* d_cand_ids,
                          const float* d_cand_scores, int32_t c, int64_t* d_ids, float* d_scores,

@@ -215,6 +215,7 @@ int eoship_runtime_create(int device, EosHipRuntime** out, char** err) {
     rt->builtin.push_back(m);
   }
   for (auto& ev : rt->timer) ev = nullptr;
+  eoship::noalloc_init(device);
   *out = rt;
   return 0;
 }

@@ -425,12 +425,15 @@ def top_fp16_rerank_scores_device(sidecar: F16Sidecar, d_queries: DeviceBuffer, 
                                   d_cand_ids: DeviceBuffer, d_cand_scores: DeviceBuffer, c: int,
                                   top_k: int, bit_width: int, overfetch: int,
                                   d_ids: DeviceBuffer, d_scores: DeviceBuffer,
-                                  d_id_rank: DeviceBuffer | None = None) -> int:
+                                  d_id_rank: DeviceBuffer | None = None,
+                                  noalloc: bool = False) -> int:
     """topFP16RerankScores / topFP16RerankRescueScores for nq queries on device
     buffers (runtime/retrieval_turboquant.go:1551-1556, :1635-1786). c is the
     first stage's output width, min(overfetch, n). d_id_rank (int64 [n], the
-    string-ID order) breaks equal scores by string ID. Returns kk."""
-    _lib.call("eoship_tq_fp16_rerank_device", sidecar.rt.handle, d_queries.ptr, C.c_int32(nq),
+    string-ID order) breaks equal scores by string ID. noalloc selects the entry
+    point that allocates no device memory (nq * c <= 2^20). Returns kk."""
+    entry = "eoship_tq_fp16_rerank_device_noalloc" if noalloc else "eoship_tq_fp16_rerank_device"
+    _lib.call(entry, sidecar.rt.handle, d_queries.ptr, C.c_int32(nq),
               C.c_int32(sidecar.dim), sidecar.buf.ptr, C.c_int64(sidecar.n), d_cand_ids.ptr,
               d_cand_scores.ptr, C.c_int32(c), C.c_int32(int(top_k)), C.c_int32(int(bit_width)),
               C.c_int32(int(overfetch)), d_id_rank.ptr if d_id_rank is not None else None,

@@ -419,6 +419,21 @@ int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int3
                                  const float* d_cand_scores, int32_t c, int32_t k,
                                  int32_t bit_width, int32_t overfetch, const int64_t* d_id_rank,
                                  int64_t* d_ids, float* d_scores, char** err);
+/* eoship_tq_fp16_rerank_device without any device allocation: no counterpart
+ * in the reference; for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The scores
+ * between its two kernels go to a static device array of 2^20 floats per GPU
+ * (4 MiB, held until the process ends), so q * c must be <= 2^20 (larger is
+ * refused with an error). Arguments, limits and results are those of
+ * eoship_tq_fp16_rerank_device. Every call on one GPU shares that array:
+ * calls that overlap on one GPU (two runtimes' streams running at once)
+ * race; calls ordered on one stream do not. */
+int eoship_tq_fp16_rerank_device_noalloc(EosHipRuntime* rt, const float* d_queries, int32_t q,
+                                         int32_t d, const uint16_t* d_rows, int64_t n,
+                                         const int64_t* d_cand_ids, const float* d_cand_scores,
+                                         int32_t c, int32_t k, int32_t bit_width,
+                                         int32_t overfetch, const int64_t* d_id_rank,
+                                         int64_t* d_ids, float* d_scores, char** err);
 
 #ifdef __cplusplus
 }
