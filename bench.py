@@ -28,6 +28,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "q8 encoder tokens/s @seq512; TurboQuant vectors scored/s; % of roofline"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "tq_scan_filter_c2_traffic.json")
 
 
@@ -35,20 +36,51 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def _cpu_threads() -> int:
+    """Host threads for the all-core CPU variants: the job's CPU share
+    (OMP_NUM_THREADS, 16 on the GPU box), else every core."""
+    try:
+        return max(1, int(os.environ.get("OMP_NUM_THREADS", "") or os.cpu_count() or 1))
+    except ValueError:
+        return os.cpu_count() or 1
+
+
+def _threaded(fn, chunks, threads: int) -> float:
+    """Runs fn over chunks on `threads` host threads (the oracle's ctypes calls
+    release the GIL); returns the wall seconds."""
+    from concurrent.futures import ThreadPoolExecutor
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(fn, chunks))
+    return time.perf_counter() - t0
+
+
 def cpu_baseline(corpus, queries, nq_sample: int) -> dict:
     import oracle  # the checker/baseline only; never the measured path
     q = queries[:nq_sample]
+    args = (corpus.rotation, corpus.dim, corpus.bits, corpus.codebook, corpus.codebook_scale,
+            corpus.codes, corpus.norms, 100)
     t0 = time.perf_counter()
-    oracle.tq_topk(q, corpus.rotation, corpus.dim, corpus.bits, corpus.codebook,
-                   corpus.codebook_scale, corpus.codes, corpus.norms, 100)
+    oracle.tq_topk(q, *args)
     dt = time.perf_counter() - t0
+    # All-core variant: queries split over the host threads.
+    threads = _cpu_threads()
+    nq_all = max(threads * 4, nq_sample)
+    qa = np.concatenate([queries] * (-(-nq_all // len(queries))))[:nq_all]
+    chunks = np.array_split(qa, threads)
+    dt_all = _threaded(lambda c: oracle.tq_topk(c, *args), chunks, threads)
     return {
         "value": nq_sample * corpus.n / dt,
         "unit": "vectors scored/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{nq_sample} queries x {corpus.n} vectors, top-100, single-threaded C port of "
-                  f"topTurboQuantRetrievalScoresWithStats ({dt:.2f} s)",
+        "sample": f"{nq_sample} queries x {corpus.n} vectors, top-100 ({dt:.2f} s): single-threaded C "
+                  "restatement of the loop of topTurboQuantRetrievalScoresWithStats (score every "
+                  "vector, size-k heap, final sort) scoring with this build's exact integer "
+                  "estimator (int16 query x int8-grid codebook through a byte LUT), not the "
+                  "reference module's f32 estimator",
+        "all_core": {"value": nq_all * corpus.n / dt_all, "cores": threads,
+                     "sample": f"{nq_all} queries split over {threads} threads ({dt_all:.2f} s)"},
         "cpu_model": _cpu_model(),
         "host_cores": os.cpu_count(),
     }
@@ -61,7 +93,47 @@ ENCODER_CONFIGS = {
 }
 
 
-def encoder_leg(rt, steps: int, name: str = "c3") -> dict:
+def encoder_cpu_baseline(w, ids, mask, lens, name: str) -> dict:
+    """The oracle's restatement of BERTEncoderLayerReference
+    (bert_encoder_layer_ops.go:80-495: f64 dense over every padded row,
+    per-(query, head) f64 attention over active keys), OpenMP over rows and
+    query heads like the reference's goroutines, timed on a sample and
+    extrapolated to the whole batch with its work model: per sequence and
+    layer, T rows x (4 H^2 + 2 H F) dense MAC + 2 T len H attention MAC."""
+    import oracle
+    B, T = ids.shape
+    H, F, L = w.hidden, w.intermediate, len(w.layers)
+    if name == "c3":
+        nseq, nlay = 16, L              # 16 whole sequences, every layer
+    else:
+        nseq, nlay = 1, 1               # c4: one sequence through one layer
+    layers = [Ly.dequantized() for Ly in w.layers[:nlay]]
+
+    def work(blens, nl):
+        return float(sum(nl * T * (4 * H * H + 2 * H * F) + 2.0 * nl * T * int(n) * H
+                         for n in blens))
+
+    t0 = time.perf_counter()
+    oracle.bert_embed(w.tok, w.pos, w.typ, w.emb_gamma, w.emb_beta, layers, ids[:nseq],
+                      mask[:nseq], None, w.heads, w.ln_eps)
+    dt = time.perf_counter() - t0
+    full_s = dt * work(lens, L) / work(lens[:nseq], nlay)
+    threads = _cpu_threads()
+    return {
+        "value": B * T / full_s,
+        "unit": f"tokens/s (batch x {T} per forward)",
+        "valid_tokens_per_s": float(lens.sum()) / full_s,
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{nseq} of {B} sequences through {nlay} of {L} layers in {dt:.2f} s "
+                   f"(f64 C restatement of BERTEncoderLayerReference, OpenMP on {threads} "
+                   f"threads), extrapolated by the dense + attention MAC count to the whole "
+                   f"batch: {full_s:.1f} s per forward"),
+        "cpu_model": _cpu_model(),
+    }
+
+
+def encoder_leg(rt, steps: int, name: str = "c3", cpu: bool = True) -> dict:
     """BASELINE config 3 (q8 BERT-style encoder, 6 layers, hidden 384, 12
     heads, FFN 1536, batch 64 x seq 512, lengths U[32, 512]) or config 4 (long
     context: 4 layers, hidden 512, 8 heads, FFN 2048, batch 4 x 8192, lengths
@@ -104,6 +176,10 @@ def encoder_leg(rt, steps: int, name: str = "c3") -> dict:
     flops = lin + att
     achieved = flops / (ms / 1e3) / 1e12
     enc.release()
+    base = None
+    if cpu:
+        log(f"encoder {name}: cpu baseline")
+        base = encoder_cpu_baseline(w, ids, mask, lens, name)
     return {
         "metric": f"q8 encoder tokens/s @seq{T}",
         "value": B * T / (ms / 1e3),
@@ -121,6 +197,7 @@ def encoder_leg(rt, steps: int, name: str = "c3") -> dict:
                      "flops_per_forward_valid": flops,
                      "int8_share_of_gemm_flops": (3 * H * H + H * F) / (4 * H * H + 2 * H * F)},
         "breakdown_ms": kernels,
+        "cpu_baseline": base,
     }
 
 
@@ -272,7 +349,7 @@ def tq_leg(rt, args) -> dict:
     return out
 
 
-def maxsim_leg(rt, steps: int) -> dict:
+def maxsim_leg(rt, steps: int, cpu: bool = True) -> dict:
     """100,000 documents x 128 token vectors of dim 128,
     2-bit codes, lognormal(0, 0.25) norms, seeded rotation; 32 queries x 32
     unit Gaussian tokens; MaxSim top-100 documents per query."""
@@ -311,7 +388,13 @@ def maxsim_leg(rt, steps: int) -> dict:
     ms_scan -= ms_sel
     bytes_per_pass = corpus.n * (dim * bits // 8 + 4)
     avg = ms_scan / max(n_scan, 1)
-    achieved = bytes_per_pass / (avg / 1e3) / 1e9
+    hbm_gbs = bytes_per_pass / (avg / 1e3) / 1e9
+    # MFMA bound: 2 x MAC per (query token, vector, dim), twice over for the
+    # int16 query split into two int8 halves = 6.7 T int8 ops per batch,
+    # spread over the batch's scan launches.
+    ops_per_batch = 2.0 * 2.0 * nq * tokens * corpus.n * dim
+    ops_per_launch = ops_per_batch / max(n_scan, 1)
+    achieved = ops_per_launch / (avg / 1e3) / 1e12
     out = {
         "metric": "MaxSim query-document pairs scored/s",
         "value": nq * ndocs / (ms / 1e3),
@@ -320,15 +403,47 @@ def maxsim_leg(rt, steps: int) -> dict:
         "config": {"workload": "turboquant_maxsim_c5", "docs": ndocs, "doc_len": doc_len,
                    "dim": dim, "bits": bits, "queries": nq, "tokens": tokens, "k": k},
         "token_vector_pairs_per_s": nq * tokens * corpus.n / (ms / 1e3),
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "kernel": "tq_maxsim",
-                     "avg_launch_ms": avg, "launches_per_batch": n_scan,
-                     "bytes_per_launch": bytes_per_pass},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS,
+                     "unit": "TOP/s (int8)", "frac": achieved / INT8_PEAK_TOPS,
+                     "kernel": "tq_maxsim", "avg_launch_ms": avg, "launches_per_batch": n_scan,
+                     "int8_ops_per_launch": ops_per_launch, "bytes_per_launch": bytes_per_pass,
+                     "hbm_gbs": hbm_gbs, "hbm_frac": hbm_gbs / HBM_PEAK_GBS},
     }
+    if cpu:
+        out["cpu_baseline"] = maxsim_cpu_baseline(corpus, q, doc_len, ndocs)
     for b in (dq, dids, dsc):
         b.free()
     idx.release()
     return out
+
+
+def maxsim_cpu_baseline(corpus, q, doc_len: int, ndocs: int) -> dict:
+    """The oracle's MaxSim (per query token the reference child-max over a
+    document's vectors, summed over tokens) on the first 2000 documents:
+    4 queries single-threaded, and all 32 queries over the host threads."""
+    import oracle
+    nd = 2000
+    rows = nd * doc_len
+    args = (corpus.rotation, corpus.dim, corpus.bits, corpus.codebook, corpus.codebook_scale,
+            corpus.codes[:rows], corpus.norms[:rows], doc_len)
+    t0 = time.perf_counter()
+    oracle.tq_maxsim_scores(q[:4], *args)
+    dt = time.perf_counter() - t0
+    threads = _cpu_threads()
+    chunks = [c for c in np.array_split(q, threads) if len(c)]
+    dt_all = _threaded(lambda c: oracle.tq_maxsim_scores(c, *args), chunks, threads)
+    return {
+        "value": 4 * nd / dt,
+        "unit": "query-document pairs/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"4 queries x {q.shape[1]} tokens against the first {nd} of {ndocs} documents "
+                  f"({dt:.2f} s, single-threaded C restatement of the child-max loop, "
+                  "retrieval_multivector_turboquant.go:746-808, summed over query tokens)",
+        "all_core": {"value": q.shape[0] * nd / dt_all, "cores": threads,
+                     "sample": f"{q.shape[0]} queries split over {threads} threads ({dt_all:.2f} s)"},
+        "cpu_model": _cpu_model(),
+    }
 
 
 def copy_calibration(rt, mb: int, reps: int = 5) -> dict:
@@ -348,6 +463,78 @@ def copy_calibration(rt, mb: int, reps: int = 5) -> dict:
     ms = rt.elapsed_ms(4, 5) / reps
     return {"bytes": nbytes, "ms": ms, "read_plus_write_GBps": 2 * nbytes / (ms / 1e3) / 1e9}
 
+
+
+def tiny_leg(rt, reps: int, cpu: bool = True) -> dict:
+    """BASELINE config 1 (examples/embed.eos): f16 token_embedding [30522, 256]
+    and projection [256, 128], N(0, 0.02); 128 tokens; gather -> matmul ->
+    row L2 normalize -> f16 [128, 128]. Latency-bound: one launch per call."""
+    from eos_amd import datagen
+    from eos_amd.encoder import TinyEmbed
+    from eos_amd.runtime import DeviceBuffer
+
+    V, D, E, T = 30522, 256, 128, 128
+    table = (0.02 * datagen.normal(1, V * D)).astype(np.float16).reshape(V, D)
+    proj = (0.02 * datagen.normal(101, D * E)).astype(np.float16).reshape(D, E)
+    tokens = datagen.uniform_int(2, T, 0, V).astype(np.int32)
+    m = TinyEmbed(rt, table, proj)
+    d_tok = DeviceBuffer.from_array(rt, tokens)
+    d_out = DeviceBuffer(rt, T * E * 2)
+    for _ in range(20):
+        m.embed_device(d_tok, T, d_out)
+    rt.sync()
+    rt.mark(8)
+    for _ in range(reps):
+        m.embed_device(d_tok, T, d_out)
+    rt.mark(9)
+    us = rt.elapsed_ms(8, 9) / reps * 1e3
+    rt.profile_reset()
+    rt.profile_select(None)
+    rt.profile(True)
+    for _ in range(reps):
+        m.embed_device(d_tok, T, d_out)
+    rt.sync()
+    n_k, ms_k = rt.profile_read("eos_embed_tiny")
+    rt.profile(False)
+    kern_us = ms_k / max(n_k, 1) * 1e3
+    # One call end to end from the host (tokens up, embeddings down).
+    t0 = time.perf_counter()
+    for _ in range(50):
+        m.embed(tokens)
+    host_us = (time.perf_counter() - t0) / 50 * 1e6
+    touched = T * D * 2 + D * E * 2 + T * E * 2 + T * 4
+    out = {
+        "metric": "tiny embed calls/s (T = 128)",
+        "value": 1e6 / us,
+        "unit": "calls/s",
+        "us_per_call": us,
+        "tokens_per_s": T * 1e6 / us,
+        "kernel_us": kern_us,
+        "host_roundtrip_us_per_call": host_us,
+        "config": {"workload": "tiny_embed_c1", "vocab": V, "dim": D, "out_dim": E, "tokens": T},
+        "roofline": {"bound": "latency", "kernel": "eos_embed_tiny", "avg_launch_ms": kern_us / 1e3,
+                     "bytes_per_launch": touched, "flops_per_launch": 2.0 * T * D * E,
+                     "achieved_gbs": touched / (kern_us / 1e6) / 1e9 if kern_us > 0 else None},
+    }
+    if cpu:
+        import oracle
+        tf, pf = table.astype(np.float32), proj.astype(np.float32)
+        n = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < 2.0:
+            oracle.tiny_embed(tf, pf, tokens)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        out["cpu_baseline"] = {
+            "value": 1.0 / dt, "unit": "calls/s", "us_per_call": dt * 1e6,
+            "tokens_per_s": T / dt, "cores": 1, "kind": "port",
+            "sample": f"{n} calls in 2 s: single-threaded C restatement of gather + f32 "
+                      "matmulTensor (k order) + normalizeRows",
+            "cpu_model": _cpu_model()}
+    for b in (d_tok, d_out):
+        b.free()
+    m.release()
+    return out
 
 
 def two_stage_leg(rt, steps: int, n: int) -> dict:
@@ -436,7 +623,9 @@ def main() -> int:
     ap.add_argument("--maxsim-steps", type=int, default=5)
     ap.add_argument("--encoder-steps", type=int, default=5)
     ap.add_argument("--encoder-configs", default="c3,c4", help="comma list of c3, c4")
-    ap.add_argument("--copy-calibration-mb", type=int, default=0)
+    ap.add_argument("--copy-calibration-mb", type=int, default=1024)
+    ap.add_argument("--skip-tiny", action="store_true")
+    ap.add_argument("--tiny-reps", type=int, default=2000)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -464,17 +653,26 @@ def main() -> int:
     }
     if not args.skip_tq:
         out.update(tq_leg(rt, args))
+        if args.copy_calibration_mb > 0:
+            # Achievable HBM: a device-to-device copy of a known size beside
+            # the vendor peak.
+            cal = copy_calibration(rt, args.copy_calibration_mb)
+            out["copy_calibration"] = cal
+            out["roofline"]["peak_measured"] = cal["read_plus_write_GBps"]
+            out["roofline"]["frac_measured"] = out["roofline"]["achieved"] / cal["read_plus_write_GBps"]
+    if not args.skip_tiny:
+        log("tiny c1")
+        out["tiny_c1"] = tiny_leg(rt, args.tiny_reps, cpu=not args.no_cpu_baseline)
     if not args.skip_encoder:
         for name in args.encoder_configs.split(","):
             log(f"encoder {name}")
-            out[f"encoder_{name}"] = encoder_leg(rt, args.encoder_steps, name)
+            out[f"encoder_{name}"] = encoder_leg(rt, args.encoder_steps, name,
+                                                 cpu=not args.no_cpu_baseline)
     if not args.skip_maxsim:
-        out["maxsim_c5"] = maxsim_leg(rt, args.maxsim_steps)
+        out["maxsim_c5"] = maxsim_leg(rt, args.maxsim_steps, cpu=not args.no_cpu_baseline)
     if not args.skip_two_stage:
         log("two-stage c2")
         out["two_stage_c2"] = two_stage_leg(rt, args.maxsim_steps * 4, args.n)
-    if args.copy_calibration_mb > 0:
-        out["copy_calibration"] = copy_calibration(rt, args.copy_calibration_mb)
     out["device"] = info
     rt.close()
     print(json.dumps(out), flush=True)

@@ -307,3 +307,20 @@ def test_qmax_keeps_int32_exact():
         qmax = oracle.tq_qmax(cb, d)
         assert (qmax + 128) * 127 * d <= 2**31 - 1
         assert qmax <= 127 * 256 + 127
+
+
+@pytest.mark.parametrize("bits,d,n", [(4, 384, 20000), (2, 128, 20000), (4, 64, 5000)])
+def test_topk_scores_relative_to_their_own_magnitude(bits, d, n):
+    """The returned top-100 scores against the f64 estimator of the same
+    vectors, relative to |score| itself (the north-star's 1e-4 relative
+    contract), at the c2 / c5 shapes on a 20k-vector sample."""
+    corpus = datagen.TurboQuantCorpus(n, d, bits, 61, 62, 63)
+    q = datagen.baseline_queries(64, d, 64)
+    ids, sc = oracle.tq_topk(q, corpus.rotation, d, bits, corpus.codebook, corpus.codebook_scale,
+                             corpus.codes, corpus.norms, 100)
+    ref = oracle.tq_scores_f64(q, corpus.rotation, d, bits, corpus.codebook,
+                               corpus.codebook_scale, corpus.codes, corpus.norms)
+    want = np.take_along_axis(ref, ids, axis=1)
+    rel = np.abs(sc.astype(np.float64) - want) / np.abs(want)
+    print(f"max relative error of the top-100 scores: {rel.max():.3e}")
+    assert rel.max() <= 1e-4
