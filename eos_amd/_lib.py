@@ -193,6 +193,7 @@ _SIGNATURES = {
     "eoship_encoder_forward_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_status": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_int32), C.c_void_p], C.c_int),
+    "eoship_encoder_set_fused_tail": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p], C.c_int),
     "eoship_encoder_attention_moves": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_int64), C.c_void_p],
                                        C.c_int),
 }

@@ -52,6 +52,12 @@ struct DevLayer {
   // (their inputs are LayerNorm / embedding outputs, which carry int8 rows).
   int8_t* w_qkv8 = nullptr;
   int8_t* w_18 = nullptr;
+  // Fused layer tail: the O, FFN-up and FFN-down codes in MFMA fragment order
+  // (one 1 KB block per 32 output rows x one K step, lane-major), so that every
+  // weight load of a wavefront reads 1 KB contiguously.
+  uint16_t* w_of = nullptr;
+  int8_t* w_1f = nullptr;
+  uint16_t* w_2f = nullptr;
 };
 
 }  // namespace
@@ -63,6 +69,10 @@ struct EosHipEncoder {
   // family (token + role with RoPE, normalize per row then pool, optional
   // output projection `proj` [hidden][odim] f32).
   int family = 0;
+  // BERT family at hidden 384 / 512 / 768: O projection through the second
+  // LayerNorm as one kernel per row block (eos_enc_tail_*); otherwise, or
+  // when switched off, the unfused GEMM + LayerNorm launches.
+  bool fused_tail = true;
   int odim = 0;
   float* proj = nullptr;
   std::vector<void*> owned;
@@ -111,6 +121,32 @@ struct EosHipEncoder {
     std::vector<uint16_t> h16(count);
     for (size_t i = 0; i < count; ++i) h16[i] = int8_to_f16_bits(src[i]);
     return upload(dst, h16.data(), count, err);
+  }
+
+  // Fragment order of an [n][k] code matrix (n % 32 == 0): block (nt, ks) is
+  // the 64 lanes' operands of rows 32 nt .. + 31 at K step ks, lane (l, g)
+  // holding row 32 nt + l, K values ks * KS + g * KS / 2 .. + KS / 2 - 1.
+  // f16 (KS = 16, 8 halves per lane) for the f16 MFMAs, int8 (KS = 32, 16
+  // codes per lane) for the int8 ones.
+  int upload_frag16(uint16_t** dst, const int8_t* src, int n, int k, char** err) {
+    std::vector<uint16_t> f((size_t)n * k);
+    size_t o = 0;
+    for (int nt = 0; nt < n / 32; ++nt)
+      for (int ks = 0; ks < k / 16; ++ks)
+        for (int lane = 0; lane < 64; ++lane)
+          for (int e = 0; e < 8; ++e)
+            f[o++] = int8_to_f16_bits(src[(size_t)(32 * nt + (lane & 31)) * k + 16 * ks + 8 * (lane >> 5) + e]);
+    return upload(dst, f.data(), f.size(), err);
+  }
+  int upload_frag8(int8_t** dst, const int8_t* src, int n, int k, char** err) {
+    std::vector<int8_t> f((size_t)n * k);
+    size_t o = 0;
+    for (int nt = 0; nt < n / 32; ++nt)
+      for (int ks = 0; ks < k / 32; ++ks)
+        for (int lane = 0; lane < 64; ++lane)
+          for (int e = 0; e < 16; ++e)
+            f[o++] = src[(size_t)(32 * nt + (lane & 31)) * k + 32 * ks + 16 * (lane >> 5) + e];
+    return upload(dst, f.data(), f.size(), err);
   }
 
   // Stacks [in][out] code matrices (reference layout) into one [sum out][in]
@@ -249,6 +285,15 @@ struct EosHipEncoder {
       return rt->launch("eos_enc_ln", dim3((unsigned)((max_rows + 3) / 4)), dim3(256), 0, &l, err,
                         "enc_ln");
     };
+    // Fused tail: the largest row block whose LDS fits the hidden width.
+    const char* tail_name = nullptr;
+    char tail_buf[48];
+    int tail_bm = 0;
+    if (a8 && fused_tail && (H == 384 || H == 512 || H == 768) && F <= 4 * H) {
+      tail_bm = H == 384 ? 96 : H == 512 ? 64 : 32;
+      snprintf(tail_buf, sizeof(tail_buf), "eos_enc_tail_r%d_h%d_g%d", tail_bm / 32, H, desc.gelu);
+      tail_name = tail_buf;
+    }
     for (const DevLayer& L : layers) {
       // Q and K rows into qkv, V feature-major into vt.
       if (gemm(h, L.w_qkv, a8 ? L.w_qkv8 : nullptr, L.s_qkv, L.b_qkv, qkv, nullptr, 3 * H, H, 0,
@@ -258,6 +303,16 @@ struct EosHipEncoder {
                      (float)(1.4426950408889634 / std::sqrt((double)hd)), status + 1};
       if (rt->launch(attn_name, dim3((tokens + 127) / 128, nh, batch), dim3(256), 0, &at, err) != 0)
         return 1;
+      if (tail_name != nullptr) {
+        EncTailArgs tl{ctx,    h,      mid,    h8,     hs,     L.w_of, L.s_o,    L.b_o,     L.g1,
+                       L.be1,  L.w_1f, L.s_1,  L.b_1,  L.w_2f, L.s_2,    L.b_2,     L.g2,
+                       L.be2,  total,  max_rows, F,    desc.ln_eps, desc.gelu};
+        if (rt->launch(tail_name, dim3((unsigned)((max_rows + tail_bm - 1) / tail_bm)),
+                       dim3(EOS_TAIL_THREADS),
+                       0, &tl, err, "enc_tail") != 0)
+          return 1;
+        continue;
+      }
       if (gemm(ctx, L.w_o, nullptr, L.s_o, L.b_o, h, h, H, H, 3, "enc_gemm_o") != 0 ||
           layer_norm(L.g1, L.be1) != 0 ||
           gemm(h, L.w_1, a8 ? L.w_18 : nullptr, L.s_1, L.b_1, mid, nullptr, F, H, desc.gelu,
@@ -346,6 +401,11 @@ int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const 
         enc->upload(&d.be2, s.ln2_beta, (size_t)H, err) ||
         enc->upload(&d.w_qkv8, s.w_qkv, (size_t)3 * H * H, err) ||
         enc->upload(&d.w_18, s.w_1, (size_t)F * H, err))
+      return fail();
+    if ((H == 384 || H == 512 || H == 768) &&
+        (enc->upload_frag16(&d.w_of, s.w_o, H, H, err) ||
+         enc->upload_frag8(&d.w_1f, s.w_1, F, H, err) ||
+         enc->upload_frag16(&d.w_2f, s.w_2, H, F, err)))
       return fail();
     enc->layers.push_back(d);
   }
@@ -492,6 +552,13 @@ int eoship_encoder_status(EosHipRuntime* rt, EosHipEncoder* enc, int32_t* status
   hipError_t e = hipMemcpyAsync(status, enc->status, 4, hipMemcpyDeviceToHost, rt->stream);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
   return rt->sync(err);
+}
+
+int eoship_encoder_set_fused_tail(EosHipRuntime* rt, EosHipEncoder* enc, int32_t fused,
+                                   char** err) {
+  if (rt == nullptr || enc == nullptr) return set_err(err, "eoship_encoder_set_fused_tail: NULL argument");
+  enc->fused_tail = fused != 0;
+  return 0;
 }
 
 int eoship_encoder_attention_moves(EosHipRuntime* rt, EosHipEncoder* enc, int64_t* moves,

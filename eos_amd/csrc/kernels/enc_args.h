@@ -63,6 +63,45 @@ struct EncGemmArgs {
   const int8_t* w8;        // [n][k]
 };
 
+// Fused layer tail of the BERT family for one block of rows: O projection +
+// bias + residual, affine LayerNorm, FFN up (W8A8 on int8 MFMA) + bias +
+// GELU, FFN down + bias + residual, affine LayerNorm. The same rounding
+// points as the unfused kernels (f16 after each residual add, after each
+// LayerNorm and after the GELU; int8 codes of the first LayerNorm's f32
+// output), with the intermediate kept in LDS. h is read as the residual and
+// overwritten with the layer output (rows below *rows), together with its
+// int8 codes h8 / scales hs; h1 receives the first LayerNorm's f16 output
+// (the FFN's residual).
+// Workgroup size of the fused tail kernels (4 down + 4 up wavefronts).
+#define EOS_TAIL_THREADS 512
+struct EncTailArgs {
+  const uint16_t* ctx;     // [rows][hidden] f16 attention context
+  uint16_t* h;             // [rows][hidden] f16 layer input -> layer output
+  uint16_t* h1;            // [rows][hidden] f16 scratch
+  int8_t* h8;              // [rows][hidden] int8 codes of the output
+  float* hs;               // [rows] their scales
+  // Weights in MFMA fragment order: block (nt, ks) = the 64 lanes' operands
+  // of output rows 32 nt .. + 31 at K step ks (f16: 16 K values, 8 per lane
+  // half; int8: 32 K values, 16 per lane half), 1 KB per block.
+  const uint16_t* w_o;     // [hidden][hidden] codes as f16, fragment order
+  const float* s_o;
+  const float* b_o;
+  const float* g1;
+  const float* be1;
+  const int8_t* w_1;       // [inter][hidden] int8 codes, fragment order
+  const float* s_1;
+  const float* b_1;
+  const uint16_t* w_2;     // [hidden][inter] codes as f16, fragment order
+  const float* s_2;
+  const float* b_2;
+  const float* g2;
+  const float* be2;
+  const int32_t* rows;     // device row count
+  int max_rows, inter;
+  float eps;
+  int gelu;                // 1 erf, 2 tanh
+};
+
 // In-place affine LayerNorm of h [rows][hidden] f16 (hidden % 8 == 0, <= 1024).
 struct EncLnArgs {
   uint16_t* h;

@@ -574,9 +574,9 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
               if constexpr (I8)
-                o[t] = (_Float16)((float)acc[i][j][4 * q + t] * (sc * rs[t]) + bi);
+                o[t] = (_Float16)__builtin_fmaf((float)acc[i][j][4 * q + t], sc * rs[t], bi);
               else
-                o[t] = (_Float16)(acc[i][j][4 * q + t] * sc + bi);
+                o[t] = (_Float16)__builtin_fmaf(acc[i][j][4 * q + t], sc, bi);
             }
             *reinterpret_cast<v4h*>(vrow + row) = o;
           }
@@ -607,10 +607,10 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
           float4 sc = *reinterpret_cast<const float4*>(a.wscale + col);
           const float4 bi = *reinterpret_cast<const float4*>(a.bias + col);
           if constexpr (I8) sc = make_float4(sc.x * rs, sc.y * rs, sc.z * rs, sc.w * rs);
-          float v[4] = {(float)acc[i][j][4 * q] * sc.x + bi.x,
-                        (float)acc[i][j][4 * q + 1] * sc.y + bi.y,
-                        (float)acc[i][j][4 * q + 2] * sc.z + bi.z,
-                        (float)acc[i][j][4 * q + 3] * sc.w + bi.w};
+          float v[4] = {__builtin_fmaf((float)acc[i][j][4 * q], sc.x, bi.x),
+                        __builtin_fmaf((float)acc[i][j][4 * q + 1], sc.y, bi.y),
+                        __builtin_fmaf((float)acc[i][j][4 * q + 2], sc.z, bi.z),
+                        __builtin_fmaf((float)acc[i][j][4 * q + 3], sc.w, bi.w)};
           if constexpr (EPI == 3) {
             const v4h r = *reinterpret_cast<const v4h*>(rrow + col);
 #pragma unroll
@@ -681,91 +681,521 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_gemm8_t128(EncGemmArgs
 
 // ------------------------------------------------------------ LayerNorm
 
-// In-place affine LayerNorm of rows [0, *rows) of h [rows][hidden] (f16),
-// one wavefront per row: each lane holds up to two 8-column chunks in f32,
-// two-pass mean / variance over the row, out = (x - mean) / sqrt(var + eps)
-// * gamma + beta.
+namespace {
+
+// gamma / beta of the column pairs 2 lane + 128 t (t < H / 128) of a row.
+template <int H>
+struct LnParams {
+  float2 g[H / 128], b[H / 128];
+};
+template <int H>
+EOS_DEV void ln_params(const float* gamma, const float* beta, int lane, LnParams<H>& p) {
+#pragma unroll
+  for (int t = 0; t < H / 128; ++t) {
+    p.g[t] = *reinterpret_cast<const float2*>(gamma + 2 * lane + 128 * t);
+    p.b[t] = *reinterpret_cast<const float2*>(beta + 2 * lane + 128 * t);
+  }
+}
+
+// One wavefront: affine LayerNorm of NR f16 rows y[r] (LDS or global memory;
+// yout[r] may alias y[r]), processed together so that their wavefront
+// reductions overlap. Every lane holds the column pairs 2 lane + 128 t.
+// Two-pass mean / variance in f32 (wavefront sums by DPP), then
+// out = (x - mean) * (rsq(var + eps) * gamma) + beta as one fma, rounded to
+// f16 into yout[r]. With q8[r], also the int8 codes rint(out * 127 / max|out|)
+// of the f32 result (|code| <= 127 since the reciprocal is within 1 ulp) and
+// the scale max|out| / 127 (0 for a zero row) into *qscale[r].
+template <int H, int NR>
+EOS_DEV void ln_rows(const uint16_t* const (&y)[NR], const LnParams<H>& p, float eps, int lane,
+                     uint16_t* const (&yout)[NR], int8_t* const (&q8)[NR],
+                     float* const (&qscale)[NR]) {
+  constexpr int P = H / 128;
+  float x[NR][P][2];
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(y[r] + 2 * lane + 128 * t);
+      x[r][t][0] = h2f((uint16_t)(w & 0xffffu));
+      x[r][t][1] = h2f((uint16_t)(w >> 16));
+    }
+  float mean[NR], inv[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < P; ++t) s += x[r][t][0] + x[r][t][1];
+    mean[r] = wave_sum_dpp(s) * (1.0f / (float)H);
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    float q = 0.f;
+#pragma unroll
+    for (int t = 0; t < P; ++t)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        x[r][t][e] -= mean[r];
+        q = __builtin_fmaf(x[r][t][e], x[r][t][e], q);
+      }
+    inv[r] = __builtin_amdgcn_rsqf(wave_sum_dpp(q) * (1.0f / (float)H) + eps);
+  }
+  float amax[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    amax[r] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+      x[r][t][0] = __builtin_fmaf(x[r][t][0], inv[r] * p.g[t].x, p.b[t].x);
+      x[r][t][1] = __builtin_fmaf(x[r][t][1], inv[r] * p.g[t].y, p.b[t].y);
+      amax[r] = fmaxf(amax[r], fmaxf(fabsf(x[r][t][0]), fabsf(x[r][t][1])));
+      *reinterpret_cast<uint32_t*>(yout[r] + 2 * lane + 128 * t) =
+          (uint32_t)f2h(x[r][t][0]) | ((uint32_t)f2h(x[r][t][1]) << 16);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    if (q8[r] == nullptr) continue;
+    const float am = wave_max_dpp(amax[r]);
+    const float qi = am > 0.0f ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f;
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+      const uint32_t c0 = (uint32_t)(uint8_t)(int8_t)(int)rintf(x[r][t][0] * qi);
+      const uint32_t c1 = (uint32_t)(uint8_t)(int8_t)(int)rintf(x[r][t][1] * qi);
+      *reinterpret_cast<uint16_t*>(q8[r] + 2 * lane + 128 * t) = (uint16_t)(c0 | (c1 << 8));
+    }
+    if (lane == 0) *qscale[r] = am * (1.0f / 127.0f);
+  }
+}
+
+template <int H>
+EOS_DEV void ln_global_row(const EncLnArgs& a, int row, int lane) {
+  LnParams<H> p;
+  ln_params<H>(a.gamma, a.beta, lane, p);
+  uint16_t* rp = a.h + (size_t)row * H;
+  const uint16_t* const yin[1] = {rp};
+  uint16_t* const yout[1] = {rp};
+  int8_t* const q8[1] = {a.q8 != nullptr ? a.q8 + (size_t)row * H : nullptr};
+  float* const qs[1] = {a.qscale != nullptr ? a.qscale + row : nullptr};
+  ln_rows<H, 1>(yin, p, a.eps, lane, yout, q8, qs);
+}
+
+}  // namespace
+
+// In-place affine LayerNorm of rows [0, *rows) of h [rows][hidden] (f16,
+// hidden 128 / 256 / 384 / 512 / 768), one wavefront per row (ln_row).
 extern "C" __global__ __launch_bounds__(256) void eos_enc_ln(EncLnArgs a) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= *a.rows) return;
-  const int nch = a.hidden >> 3;  // 8-column chunks (hidden <= 1024)
-  uint16_t* rp = a.h + (size_t)row * a.hidden;
-  float x[2][8];
-  v4i raw[2];
-  float4 gb[2][4];  // gamma and beta of the lane's chunks, requested with the row
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int c = lane + 64 * t;
-    raw[t] = v4i{0, 0, 0, 0};
-    gb[t][0] = gb[t][1] = gb[t][2] = gb[t][3] = make_float4(0.f, 0.f, 0.f, 0.f);
-    // Only lanes with a chunk load (at hidden <= 512 the second chunk exists
-    // for no lane, and the wavefront skips those loads).
-    if (c < nch) {
-      raw[t] = *reinterpret_cast<const v4i*>(rp + 8 * c);
-      gb[t][0] = *reinterpret_cast<const float4*>(a.gamma + 8 * c);
-      gb[t][1] = *reinterpret_cast<const float4*>(a.gamma + 8 * c + 4);
-      gb[t][2] = *reinterpret_cast<const float4*>(a.beta + 8 * c);
-      gb[t][3] = *reinterpret_cast<const float4*>(a.beta + 8 * c + 4);
-    }
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const v8h hv = __builtin_bit_cast(v8h, raw[t]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      x[t][e] = (float)hv[e];
-      s += x[t][e];
-    }
-  }
-  const float mean = wave_sum_dpp(s) / (float)a.hidden;
-  float q = 0.f;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    if (lane + 64 * t < nch) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) q += (x[t][e] - mean) * (x[t][e] - mean);
-    }
-  }
-  const float inv = 1.0f / sqrtf(wave_sum_dpp(q) / (float)a.hidden + a.eps);
-  float amax = 0.0f;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int c = lane + 64 * t;
-    if (c < nch) {
-      const float4 g0 = gb[t][0], g1 = gb[t][1], b0 = gb[t][2], b1 = gb[t][3];
-      const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-      const float bb[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-      v8h o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x[t][e] = (x[t][e] - mean) * inv * gg[e] + bb[e];
-        o[e] = (_Float16)x[t][e];
-        amax = fmaxf(amax, fabsf(x[t][e]));
-      }
-      *reinterpret_cast<v8h*>(rp + 8 * c) = o;
-    }
-  }
-  if (a.q8 != nullptr) {
-    amax = wave_max_dpp(amax);
-    const float qi = q8_inv(amax);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int c = lane + 64 * t;
-      if (c < nch) {
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          lo |= (uint32_t)(uint8_t)q8_code(x[t][e], qi) << (8 * e);
-          hi |= (uint32_t)(uint8_t)q8_code(x[t][4 + e], qi) << (8 * e);
-        }
-        *reinterpret_cast<uint2*>(a.q8 + (size_t)row * a.hidden + 8 * c) = make_uint2(lo, hi);
-      }
-    }
-    if (lane == 0) a.qscale[row] = amax / 127.0f;
+  switch (a.hidden) {
+    case 128: ln_global_row<128>(a, row, lane); break;
+    case 256: ln_global_row<256>(a, row, lane); break;
+    case 384: ln_global_row<384>(a, row, lane); break;
+    case 512: ln_global_row<512>(a, row, lane); break;
+    default: ln_global_row<768>(a, row, lane); break;
   }
 }
+
+// ------------------------------------------------------- fused layer tail
+
+namespace {
+
+constexpr int kTailFC = 128;  // FFN intermediate columns per chunk
+
+// Block of BM = 32 RT rows, 8 wavefronts (two per SIMD). Every MFMA takes a
+// weight fragment (32 output features, read from global memory in fragment
+// order, 1 KB per wavefront load) as its first operand and an activation
+// fragment (32 rows, from LDS) as its second, so a lane's results are
+// 4-feature groups of one row.
+//  - "down" wavefronts 0..3: wavefront d owns output features
+//    [d H / 4, (d + 1) H / 4) (CT = H / 128 column tiles) of the O and
+//    FFN-down projections over all RT row tiles;
+//  - "up" wavefronts 4..7: wavefront u owns features [32 u, 32 u + 32) of
+//    each 128-wide FFN-up chunk and computes its bias + GELU.
+// The FFN is a two-stage pipeline over the chunks: while the down wavefronts
+// multiply chunk c out of one LDS buffer, the up wavefronts fill the other
+// with chunk c + 1, so one SIMD's MFMAs overlap the other wavefront's GELU.
+// LayerNorms use all 8 wavefronts.
+//
+// LDS: region A holds the context rows (O projection), then the O output
+// (first LayerNorm), then the two GELU chunk buffers, then the FFN output
+// (second LayerNorm); region B the int8 codes of the first LayerNorm's
+// output and their row scales. Row strides are padded by 16 bytes.
+template <int RT, int H>
+struct TailLds {
+  static constexpr int BM = 32 * RT;
+  static constexpr int XS = H + 8;           // halves per X / Y row
+  static constexpr int QS = H + 16;          // bytes per Q8 row
+  static constexpr int MS = kTailFC + 8;     // halves per GELU-chunk row
+  static constexpr int FMAX = 4 * H;         // FFN widths up to 4 H
+  static_assert(2 * BM * MS <= BM * XS, "two GELU chunks must fit in region A");
+  uint16_t A[BM * XS];
+  int8_t Q8[BM * QS];
+  float rsc[BM];
+  // per-feature scales and biases: O (s, b), FFN-down (s, b), FFN-up (s, b)
+  float so[H], bo[H], s2[H], b2[H], s1[FMAX], b1[FMAX];
+};
+
+// Rows m = wave + 8 k of the block through the LayerNorm, four at a time.
+template <int RT, int H, typename RowFn>
+EOS_DEV void tail_layer_norm(int wave, int lane, const float* gamma, const float* beta, float eps,
+                             RowFn&& row_ptrs) {
+  constexpr int BM = 32 * RT, NR = BM / 8 >= 4 ? 4 : BM / 8;
+  static_assert((BM / 8) % NR == 0, "rows per wavefront");
+  LnParams<H> p;
+  ln_params<H>(gamma, beta, lane, p);
+#pragma unroll 1
+  for (int k0 = 0; k0 < BM / 8; k0 += NR) {
+    const uint16_t* yin[NR];
+    uint16_t* yout[NR];
+    int8_t* q8[NR];
+    float* qs[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) row_ptrs(wave + 8 * (k0 + r), yin[r], yout[r], q8[r], qs[r]);
+    ln_rows<H, NR>(yin, p, eps, lane, yout, q8, qs);
+  }
+}
+
+// The down and up wavefronts run separate code paths (so that neither path's
+// registers are live in the other) that meet at the same sequence of
+// NC + 8 workgroup barriers.
+template <int RT, int H, int GELU>
+EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
+  using L = TailLds<RT, H>;
+  constexpr int BM = L::BM, CT = H / 128, XS = L::XS, QS = L::QS, MS = L::MS;
+  constexpr int KSO = H / 16, KS1 = H / 32, KS2C = kTailFC / 16, PF = 4;
+  uint16_t* const X = lds.A;  // context rows, then O output / FFN output rows
+  int8_t* const Q8 = lds.Q8;
+  float* const rsc = lds.rsc;
+  uint16_t* const Mbuf0 = X;
+  uint16_t* const Mbuf1 = X + BM * MS;
+
+  const int rows = *a.rows;
+  const int m0 = blockIdx.x * BM;
+  if (m0 >= rows) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, l32 = lane & 31;
+  const int role = wave & 3;
+  const int F = a.inter, NC = F / kTailFC;
+
+  // context rows -> X (rows past the matrix clamped; never stored), all
+  // loads issued before any store; scales and biases -> LDS
+  static_assert(EOS_TAIL_THREADS == 512, "4 down + 4 up wavefronts");
+  {
+    constexpr int PER = BM * (H / 8) / EOS_TAIL_THREADS;
+    static_assert(BM * (H / 8) % EOS_TAIL_THREADS == 0, "staging split");
+    v4i st[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = tid + EOS_TAIL_THREADS * u;
+      const int r = i / (H / 8), c = i % (H / 8);
+      st[u] = *reinterpret_cast<const v4i*>(a.ctx + (size_t)min(m0 + r, a.max_rows - 1) * H + 8 * c);
+    }
+    // H / 4 float4 of each O / FFN-down vector (H / 4 <= 512 threads), F / 4
+    // of each FFN-up vector (F <= 4 H: at most 2 per thread)
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool hv = tid < H / 4;
+    const bool f0 = tid < F / 4, f1 = tid + EOS_TAIL_THREADS < F / 4;
+    const float4 v0 = hv ? reinterpret_cast<const float4*>(a.s_o)[tid] : zero4;
+    const float4 v1 = hv ? reinterpret_cast<const float4*>(a.b_o)[tid] : zero4;
+    const float4 v2 = hv ? reinterpret_cast<const float4*>(a.s_2)[tid] : zero4;
+    const float4 v3 = hv ? reinterpret_cast<const float4*>(a.b_2)[tid] : zero4;
+    const float4 s1a = f0 ? reinterpret_cast<const float4*>(a.s_1)[tid] : zero4;
+    const float4 b1a = f0 ? reinterpret_cast<const float4*>(a.b_1)[tid] : zero4;
+    const float4 s1b = f1 ? reinterpret_cast<const float4*>(a.s_1)[tid + EOS_TAIL_THREADS] : zero4;
+    const float4 b1b = f1 ? reinterpret_cast<const float4*>(a.b_1)[tid + EOS_TAIL_THREADS] : zero4;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int i = tid + EOS_TAIL_THREADS * u;
+      const int r = i / (H / 8), c = i % (H / 8);
+      *reinterpret_cast<v4i*>(&X[r * XS + 8 * c]) = st[u];
+    }
+    if (hv) {
+      reinterpret_cast<float4*>(lds.so)[tid] = v0;
+      reinterpret_cast<float4*>(lds.bo)[tid] = v1;
+      reinterpret_cast<float4*>(lds.s2)[tid] = v2;
+      reinterpret_cast<float4*>(lds.b2)[tid] = v3;
+    }
+    if (f0) {
+      reinterpret_cast<float4*>(lds.s1)[tid] = s1a;
+      reinterpret_cast<float4*>(lds.b1)[tid] = b1a;
+    }
+    if (f1) {
+      reinterpret_cast<float4*>(lds.s1)[tid + EOS_TAIL_THREADS] = s1b;
+      reinterpret_cast<float4*>(lds.b1)[tid + EOS_TAIL_THREADS] = b1b;
+    }
+  }
+  __syncthreads();  // barrier 1
+
+  // First LayerNorm (all wavefronts): f16 -> h1 (global scratch), int8
+  // codes -> Q8, scales -> rsc. Rows past the matrix are normalized too
+  // (stored only to h1, which has room for them).
+  auto layer_norm1 = [&]() {
+    tail_layer_norm<RT, H>(wave, lane, a.g1, a.be1, a.eps,
+                           [&](int m, const uint16_t*& yin, uint16_t*& yout, int8_t*& q8, float*& qs) {
+                             yin = &X[m * XS];
+                             yout = a.h1 + (size_t)min(m0 + m, a.max_rows - 1) * H;
+                             q8 = Q8 + m * QS;
+                             qs = &rsc[m];
+                           });
+  };
+  // Second LayerNorm (all wavefronts) -> the layer output rows; rows past
+  // the matrix go to the clamped last row with the values that row has.
+  auto layer_norm2 = [&]() {
+    tail_layer_norm<RT, H>(wave, lane, a.g2, a.be2, a.eps,
+                           [&](int m, const uint16_t*& yin, uint16_t*& yout, int8_t*& q8, float*& qs) {
+                             const int gr = m0 + m < rows ? m0 + m : m0;  // m0 < rows
+                             const bool live = m0 + m < rows;
+                             yin = &X[(live ? m : 0) * XS];
+                             yout = a.h + (size_t)gr * H;
+                             q8 = a.h8 + (size_t)gr * H;
+                             qs = a.hs + gr;
+                           });
+  };
+
+  if (wave < 4) {
+    // ================= down wavefront: features [nb, nb + H / 4)
+    const int nb = role * (H / 4);
+    v16f acc[RT][CT];
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int j = 0; j < CT; ++j) acc[i][j] = v16f{0};
+    const uint32_t loff = (uint32_t)lane * 16u;
+    // O projection, weight fragments PF K steps ahead. Weight addresses are
+    // a wave-uniform base plus lane * 16 bytes.
+    {
+      const char* wbase = reinterpret_cast<const char*>(a.w_o) + (size_t)(nb / 32) * KSO * 1024;
+      auto wfrag = [&](int j, int ks) {
+        return *reinterpret_cast<const v8h*>(wbase + (uint32_t)(j * KSO + ks) * 1024u + loff);
+      };
+      v8h wq[PF][CT];
+#pragma unroll
+      for (int p = 0; p < PF; ++p)
+#pragma unroll
+        for (int j = 0; j < CT; ++j) wq[p][j] = wfrag(j, p);
+#pragma unroll 1
+      for (int ks0 = 0; ks0 < KSO; ks0 += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+          const int ks = ks0 + p;
+          v8h af[CT], bf[RT];
+#pragma unroll
+          for (int j = 0; j < CT; ++j) af[j] = wq[p][j];
+          if (ks + PF < KSO) {
+#pragma unroll
+            for (int j = 0; j < CT; ++j) wq[p][j] = wfrag(j, ks + PF);
+          }
+#pragma unroll
+          for (int i = 0; i < RT; ++i)
+            bf[i] = *reinterpret_cast<const v8h*>(&X[(32 * i + l32) * XS + 16 * ks + 8 * g]);
+#pragma unroll
+          for (int i = 0; i < RT; ++i)
+#pragma unroll
+            for (int j = 0; j < CT; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j], bf[i], acc[i][j], 0, 0, 0);
+        }
+      }
+    }
+    // Epilogue as the unfused residual GEMM: v = acc * s + b (one fma),
+    // v += residual, rounded to f16. The residual rows are in X (placed there
+    // by the up wavefronts); each element is read and rewritten by one lane.
+    auto epilogue = [&](const float* sc_l, const float* bi_l) {
+#pragma unroll
+      for (int j = 0; j < CT; ++j) {
+        v4h r[RT][4];
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            r[i][q] = *reinterpret_cast<const v4h*>(&X[(32 * i + l32) * XS + nb + 32 * j + 8 * q + 4 * g]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = nb + 32 * j + 8 * q + 4 * g;
+          const float4 sc = *reinterpret_cast<const float4*>(sc_l + n);
+          const float4 bi = *reinterpret_cast<const float4*>(bi_l + n);
+#pragma unroll
+          for (int i = 0; i < RT; ++i) {
+            const int m = 32 * i + l32;
+            float v[4] = {__builtin_fmaf(acc[i][j][4 * q], sc.x, bi.x),
+                          __builtin_fmaf(acc[i][j][4 * q + 1], sc.y, bi.y),
+                          __builtin_fmaf(acc[i][j][4 * q + 2], sc.z, bi.z),
+                          __builtin_fmaf(acc[i][j][4 * q + 3], sc.w, bi.w)};
+            v4h o;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) o[t] = (_Float16)(v[t] + (float)r[i][q][t]);
+            *reinterpret_cast<v4h*>(&X[m * XS + n]) = o;
+          }
+        }
+      }
+    };
+    __syncthreads();  // barrier 2: every context read done
+    __syncthreads();  // barrier 3: the residual rows are in X
+    epilogue(lds.so, lds.bo);
+#pragma unroll
+    for (int i = 0; i < RT; ++i)
+#pragma unroll
+      for (int j = 0; j < CT; ++j) acc[i][j] = v16f{0};
+    // W2 fragments PF K steps ahead, the ring running on across chunks
+    // (primed here, so the first ones land during the first LayerNorm).
+    const int KS2 = F / 16;
+    const char* const w2base = reinterpret_cast<const char*>(a.w_2) + (size_t)(nb / 32) * KS2 * 1024;
+    auto w2frag = [&](int j, int ks) {
+      return *reinterpret_cast<const v8h*>(w2base + (uint32_t)(j * KS2 + ks) * 1024u + loff);
+    };
+    static_assert(KS2C % PF == 0, "the W2 ring slot of a K step is its index within the chunk");
+    v8h wq[PF][CT];
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+#pragma unroll
+      for (int j = 0; j < CT; ++j) wq[p][j] = w2frag(j, p);
+    __syncthreads();  // barrier 4
+    layer_norm1();
+    __syncthreads();  // barrier 5: X free, it now holds the two GELU chunk buffers
+    __syncthreads();  // barrier 6: chunk 0 written by the up wavefronts
+#pragma unroll 1
+    for (int c = 0; c < NC; ++c) {
+      // acc[i][j] += W2 rows (nb + 32 j ..)[chunk c] x the chunk's rows
+      const uint16_t* M = (c & 1) ? Mbuf1 : Mbuf0;
+      const int ks0 = c * KS2C;
+#pragma unroll
+      for (int kk = 0; kk < KS2C; ++kk) {
+        v8h af[CT], bf[RT];
+#pragma unroll
+        for (int j = 0; j < CT; ++j) af[j] = wq[kk % PF][j];
+        if (ks0 + kk + PF < KS2) {
+#pragma unroll
+          for (int j = 0; j < CT; ++j) wq[kk % PF][j] = w2frag(j, ks0 + kk + PF);
+        }
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+          bf[i] = *reinterpret_cast<const v8h*>(&M[(32 * i + l32) * MS + 16 * kk + 8 * g]);
+#pragma unroll
+        for (int i = 0; i < RT; ++i)
+#pragma unroll
+          for (int j = 0; j < CT; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j], bf[i], acc[i][j], 0, 0, 0);
+      }
+      __syncthreads();  // barriers 7 .. NC + 6: chunk c consumed, chunk c + 1 written
+    }
+    __syncthreads();  // barrier NC + 7: the first LayerNorm's output rows are in X
+    epilogue(lds.s2, lds.b2);
+    __syncthreads();  // barrier NC + 8
+    layer_norm2();
+  } else {
+    // ================= up wavefront: features [32 role, + 32) of each chunk
+    // W1 fragments of chunk c, requested a chunk ahead.
+    v4i w1f[KS1];
+    auto load_w1 = [&](int c) {
+      const char* base = reinterpret_cast<const char*>(a.w_1) +
+                         (size_t)(c * (kTailFC / 32) + role) * KS1 * 1024;
+      const uint32_t loff = (uint32_t)lane * 16u;
+#pragma unroll
+      for (int ks = 0; ks < KS1; ++ks)
+        w1f[ks] = *reinterpret_cast<const v4i*>(base + (uint32_t)ks * 1024u + loff);
+    };
+    auto up_chunk = [&](int c) {
+      const int c0 = c * kTailFC;
+      v16i up[RT];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) up[i] = v16i{0};
+#pragma unroll
+      for (int ks = 0; ks < KS1; ++ks) {
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          const v4i bf = *reinterpret_cast<const v4i*>(Q8 + (32 * i + l32) * QS + 32 * ks + 16 * g);
+          up[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w1f[ks], bf, up[i], 0, 0, 0);
+        }
+      }
+      if (c + 1 < NC) load_w1(c + 1);  // lands behind the GELU and the barrier
+      // bias + GELU: v = (float)acc * (s * rs) + b (one fma)
+      uint16_t* M = (c & 1) ? Mbuf1 : Mbuf0;
+      float rs[RT];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) rs[i] = rsc[32 * i + l32];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = 32 * role + 8 * q + 4 * g;  // within the chunk
+        const float4 sc = *reinterpret_cast<const float4*>(lds.s1 + c0 + n);
+        const float4 bi = *reinterpret_cast<const float4*>(lds.b1 + c0 + n);
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          const int m = 32 * i + l32;
+          float v[4] = {__builtin_fmaf((float)up[i][4 * q], sc.x * rs[i], bi.x),
+                        __builtin_fmaf((float)up[i][4 * q + 1], sc.y * rs[i], bi.y),
+                        __builtin_fmaf((float)up[i][4 * q + 2], sc.z * rs[i], bi.z),
+                        __builtin_fmaf((float)up[i][4 * q + 3], sc.w * rs[i], bi.w)};
+          v4h o;
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            o[t] = (_Float16)(GELU == 1 ? gelu_erf_fast(v[t]) : gelu(v[t], 2));
+          *reinterpret_cast<v4h*>(&M[m * MS + n]) = o;
+        }
+      }
+    };
+    // Residual rows for the down wavefronts' epilogues, requested while they
+    // compute (the O projection; the last FFN chunk) and then copied into X.
+    constexpr int RPER = BM * (H / 8) / 256;
+    static_assert(BM * (H / 8) % 256 == 0, "residual split");
+    const int ut = tid - 256;
+    v4i res[RPER];
+    auto load_rows = [&](const uint16_t* src) {
+#pragma unroll
+      for (int u = 0; u < RPER; ++u) {
+        const int i = ut + 256 * u;
+        const int r = i / (H / 8), c = i % (H / 8);
+        res[u] = *reinterpret_cast<const v4i*>(src + (size_t)min(m0 + r, a.max_rows - 1) * H + 8 * c);
+      }
+    };
+    auto store_rows = [&]() {
+#pragma unroll
+      for (int u = 0; u < RPER; ++u) {
+        const int i = ut + 256 * u;
+        const int r = i / (H / 8), c = i % (H / 8);
+        *reinterpret_cast<v4i*>(&X[r * XS + 8 * c]) = res[u];
+      }
+    };
+    load_rows(a.h);
+    load_w1(0);
+    __syncthreads();  // barrier 2: every context read done
+    store_rows();
+    __syncthreads();  // barrier 3
+    __syncthreads();  // barrier 4
+    layer_norm1();
+    __syncthreads();  // barrier 5
+    up_chunk(0);
+    __syncthreads();  // barrier 6
+#pragma unroll 1
+    for (int c = 0; c + 1 < NC; ++c) {
+      up_chunk(c + 1);
+      __syncthreads();  // barriers 7 .. NC + 5
+    }
+    load_rows(a.h1);  // written by the first LayerNorm before barrier 5
+    __syncthreads();  // barrier NC + 6: the last chunk consumed
+    store_rows();
+    __syncthreads();  // barrier NC + 7
+    __syncthreads();  // barrier NC + 8
+    layer_norm2();
+  }
+}
+
+}  // namespace
+
+#define EOS_TAIL_KERNEL(RT, H, G)                                                       \
+  extern "C" __global__ __launch_bounds__(EOS_TAIL_THREADS) void                          \
+      eos_enc_tail_r##RT##_h##H##_g##G(                                                    \
+      EncTailArgs a) {                                                                     \
+    __shared__ __attribute__((aligned(16))) TailLds<RT, H> lds;                           \
+    tail_body<RT, H, G>(a, lds);                                                         \
+  }
+EOS_TAIL_KERNEL(3, 384, 1)
+EOS_TAIL_KERNEL(3, 384, 2)
+EOS_TAIL_KERNEL(2, 512, 1)
+EOS_TAIL_KERNEL(2, 512, 2)
+EOS_TAIL_KERNEL(1, 768, 1)
+EOS_TAIL_KERNEL(1, 768, 2)
+#undef EOS_TAIL_KERNEL
 
 // --------------------------------------------------------------- attention
 

@@ -255,6 +255,11 @@ class Encoder:
         _lib.call("eoship_encoder_status", self.rt.handle, self.handle, C.byref(st))
         return st.value
 
+    def set_fused_tail(self, fused: bool) -> None:
+        """BERT family at hidden 384 / 512 / 768: run the layer tail as one
+        fused kernel (default) or as the unfused GEMM + LayerNorm launches."""
+        _lib.call("eoship_encoder_set_fused_tail", self.rt.handle, self.handle, C.c_int32(int(fused)))
+
     def attention_moves(self) -> int:
         """Diagnostic of the last forward: attention wavefronts that moved their
         softmax exponent reference after a sequence's first key block."""

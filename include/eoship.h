@@ -343,6 +343,13 @@ int eoship_encoder_forward_device(EosHipRuntime* rt, EosHipEncoder* enc, const i
                                   int32_t tokens, float* d_out, char** err);
 /* 0 when every id of the last forward was in range; synchronises. */
 int eoship_encoder_status(EosHipRuntime* rt, EosHipEncoder* enc, int32_t* status, char** err);
+/* Selects the BERT family's layer tail at hidden 384, 512 and 768: fused
+ * (default: O projection, residual, LayerNorm, FFN and the second LayerNorm
+ * as one kernel per row block, the intermediate kept on chip) or the unfused
+ * GEMM and LayerNorm launches. Both round at the same points. No counterpart
+ * in the reference; for comparing the two paths. */
+int eoship_encoder_set_fused_tail(EosHipRuntime* rt, EosHipEncoder* enc, int32_t fused,
+                                  char** err);
 /* Diagnostic of the last forward (synchronises): how many times a wavefront
  * of the attention kernels moved its softmax exponent reference after a
  * sequence's first key block (a score far above every earlier one, as peaked

@@ -188,3 +188,26 @@ def test_w8a8_outlier_channels(rt):
         enc = Encoder(rt, w)
         _check(enc.embed(ids, mask), _oracle(w, ids, mask))
         enc.release()
+
+
+@pytest.mark.parametrize("hidden,heads,inter,gelu", [(384, 12, 1536, 1), (384, 6, 768, 2),
+                                                      (512, 8, 2048, 1), (768, 12, 3072, 1)])
+def test_fused_tail_matches_unfused_and_oracle(rt, hidden, heads, inter, gelu):
+    """The fused layer tail (O projection through the second LayerNorm in one
+    kernel per row block) against the unfused GEMM + LayerNorm launches, which
+    round at the same points: embeddings equal to within a few f16 units, and
+    both within the contract against the oracle. Ragged lengths put partial
+    row blocks at every sequence boundary and at the end."""
+    _case(f"fused tail H={hidden} heads={heads} F={inter} gelu={gelu}")
+    w = datagen.bert_q8_weights(2, hidden, heads, inter, 3000, 256, seed=hidden + gelu,
+                                random_affine=True, gelu=gelu)
+    ids, mask, _ = datagen.encoder_batch(9, 200, 3000, 1, 200, hidden + 11, hidden + 12)
+    enc = Encoder(rt, w)
+    fused = enc.embed(ids, mask)
+    enc.set_fused_tail(False)
+    plain = enc.embed(ids, mask)
+    enc.release()
+    d = np.max(np.abs(fused - plain))
+    print(f"  fused vs unfused max abs {d:.3e}", flush=True)
+    assert d <= 2e-3
+    _check(fused, _oracle(w, ids, mask))
