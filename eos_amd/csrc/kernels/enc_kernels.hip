@@ -836,6 +836,79 @@ struct TailLds {
   float so[H], bo[H], s2[H], b2[H], s1[FMAX], b1[FMAX];
 };
 
+// O projection of row tiles [I0, I0 + N) of the block (context rows in X)
+// for the features [nb, nb + H / 4): acc[i][j] += Wo rows (nb + 32 j ..) x
+// context rows (32 (I0 + i) ..), weight fragments (fragment order, 1 KB per
+// load) PF K steps ahead in a ring whose first PF entries the caller primed.
+template <int H, int N, int I0, int PF, int XS>
+EOS_DEV void tail_o_proj(const char* wbase, uint32_t loff, const uint16_t* X, int l32, int g,
+                         v8h (&wq)[PF][H / 128], v16f (&acc)[N][H / 128]) {
+  constexpr int CT = H / 128, KSO = H / 16;
+  auto wfrag = [&](int j, int ks) {
+    return *reinterpret_cast<const v8h*>(wbase + (uint32_t)(j * KSO + ks) * 1024u + loff);
+  };
+#pragma unroll 1
+  for (int ks0 = 0; ks0 < KSO; ks0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p) {
+      const int ks = ks0 + p;
+      v8h af[CT], bf[N];
+#pragma unroll
+      for (int j = 0; j < CT; ++j) af[j] = wq[p][j];
+      if (ks + PF < KSO) {
+#pragma unroll
+        for (int j = 0; j < CT; ++j) wq[p][j] = wfrag(j, ks + PF);
+      }
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+        bf[i] = *reinterpret_cast<const v8h*>(&X[(32 * (I0 + i) + l32) * XS + 16 * ks + 8 * g]);
+#pragma unroll
+      for (int i = 0; i < N; ++i)
+#pragma unroll
+        for (int j = 0; j < CT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j], bf[i], acc[i][j], 0, 0, 0);
+    }
+  }
+}
+
+// Epilogue of row tiles [I0, I0 + N) for the features [nb, nb + H / 4), as
+// the unfused residual GEMM: v = acc * s + b (one fma), v += residual,
+// rounded to f16. The residual rows are in X; each element is read and
+// rewritten by one lane.
+template <int H, int N, int I0, int XS>
+EOS_DEV void tail_epilogue(uint16_t* X, const float* sc_l, const float* bi_l, int nb, int l32,
+                           int g, const v16f (&acc)[N][H / 128]) {
+  constexpr int CT = H / 128;
+#pragma unroll
+  for (int j = 0; j < CT; ++j) {
+    v4h r[N][4];
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        r[i][q] = *reinterpret_cast<const v4h*>(
+            &X[(32 * (I0 + i) + l32) * XS + nb + 32 * j + 8 * q + 4 * g]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = nb + 32 * j + 8 * q + 4 * g;
+      const float4 sc = *reinterpret_cast<const float4*>(sc_l + n);
+      const float4 bi = *reinterpret_cast<const float4*>(bi_l + n);
+#pragma unroll
+      for (int i = 0; i < N; ++i) {
+        const int m = 32 * (I0 + i) + l32;
+        float v[4] = {__builtin_fmaf(acc[i][j][4 * q], sc.x, bi.x),
+                      __builtin_fmaf(acc[i][j][4 * q + 1], sc.y, bi.y),
+                      __builtin_fmaf(acc[i][j][4 * q + 2], sc.z, bi.z),
+                      __builtin_fmaf(acc[i][j][4 * q + 3], sc.w, bi.w)};
+        v4h o;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t] = (_Float16)(v[t] + (float)r[i][q][t]);
+        *reinterpret_cast<v4h*>(&X[m * XS + n]) = o;
+      }
+    }
+  }
+}
+
 // Rows m = wave + 8 k of the block through the LayerNorm, four at a time.
 template <int RT, int H, typename RowFn>
 EOS_DEV void tail_layer_norm(int wave, int lane, const float* gamma, const float* beta, float eps,
@@ -878,6 +951,20 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
   const int g = lane >> 5, l32 = lane & 31;
   const int role = wave & 3;
   const int F = a.inter, NC = F / kTailFC;
+
+  // O projection row tiles: [0, RTD) on the down wavefronts, [RTD, RT) on
+  // the up wavefronts (same features).
+  constexpr int RTU = RT / 2, RTD = RT - RTU;
+  const int nb = role * (H / 4);  // O / FFN-down features of this wavefront pair
+  const char* const wo_base = reinterpret_cast<const char*>(a.w_o) + (size_t)(nb / 32) * KSO * 1024;
+  auto prime_wo = [&](v8h (&wqo)[PF][CT]) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+#pragma unroll
+      for (int j = 0; j < CT; ++j)
+        wqo[p][j] = *reinterpret_cast<const v8h*>(wo_base + (uint32_t)(j * KSO + p) * 1024u +
+                                                  (uint32_t)lane * 16u);
+  };
 
   // context rows -> X (rows past the matrix clamped; never stored), all
   // loads issued before any store; scales and biases -> LDS
@@ -956,83 +1043,22 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
 
   if (wave < 4) {
     // ================= down wavefront: features [nb, nb + H / 4)
-    const int nb = role * (H / 4);
-    v16f acc[RT][CT];
-#pragma unroll
-    for (int i = 0; i < RT; ++i)
-#pragma unroll
-      for (int j = 0; j < CT; ++j) acc[i][j] = v16f{0};
     const uint32_t loff = (uint32_t)lane * 16u;
-    // O projection, weight fragments PF K steps ahead. Weight addresses are
-    // a wave-uniform base plus lane * 16 bytes.
+    // O projection of row tiles [0, RTD) (the up wavefronts take the rest).
     {
-      const char* wbase = reinterpret_cast<const char*>(a.w_o) + (size_t)(nb / 32) * KSO * 1024;
-      auto wfrag = [&](int j, int ks) {
-        return *reinterpret_cast<const v8h*>(wbase + (uint32_t)(j * KSO + ks) * 1024u + loff);
-      };
-      v8h wq[PF][CT];
+      v16f acco[RTD][CT];
 #pragma unroll
-      for (int p = 0; p < PF; ++p)
+      for (int i = 0; i < RTD; ++i)
 #pragma unroll
-        for (int j = 0; j < CT; ++j) wq[p][j] = wfrag(j, p);
-#pragma unroll 1
-      for (int ks0 = 0; ks0 < KSO; ks0 += PF) {
-#pragma unroll
-        for (int p = 0; p < PF; ++p) {
-          const int ks = ks0 + p;
-          v8h af[CT], bf[RT];
-#pragma unroll
-          for (int j = 0; j < CT; ++j) af[j] = wq[p][j];
-          if (ks + PF < KSO) {
-#pragma unroll
-            for (int j = 0; j < CT; ++j) wq[p][j] = wfrag(j, ks + PF);
-          }
-#pragma unroll
-          for (int i = 0; i < RT; ++i)
-            bf[i] = *reinterpret_cast<const v8h*>(&X[(32 * i + l32) * XS + 16 * ks + 8 * g]);
-#pragma unroll
-          for (int i = 0; i < RT; ++i)
-#pragma unroll
-            for (int j = 0; j < CT; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j], bf[i], acc[i][j], 0, 0, 0);
-        }
-      }
+        for (int j = 0; j < CT; ++j) acco[i][j] = v16f{0};
+      v8h wqo[PF][CT];
+      prime_wo(wqo);
+      tail_o_proj<H, RTD, 0, PF, XS>(wo_base, loff, X, l32, g, wqo, acco);
+      __syncthreads();  // barrier 2: every context read done
+      __syncthreads();  // barrier 3: the residual rows are in X
+      tail_epilogue<H, RTD, 0, XS>(X, lds.so, lds.bo, nb, l32, g, acco);
     }
-    // Epilogue as the unfused residual GEMM: v = acc * s + b (one fma),
-    // v += residual, rounded to f16. The residual rows are in X (placed there
-    // by the up wavefronts); each element is read and rewritten by one lane.
-    auto epilogue = [&](const float* sc_l, const float* bi_l) {
-#pragma unroll
-      for (int j = 0; j < CT; ++j) {
-        v4h r[RT][4];
-#pragma unroll
-        for (int i = 0; i < RT; ++i)
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            r[i][q] = *reinterpret_cast<const v4h*>(&X[(32 * i + l32) * XS + nb + 32 * j + 8 * q + 4 * g]);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n = nb + 32 * j + 8 * q + 4 * g;
-          const float4 sc = *reinterpret_cast<const float4*>(sc_l + n);
-          const float4 bi = *reinterpret_cast<const float4*>(bi_l + n);
-#pragma unroll
-          for (int i = 0; i < RT; ++i) {
-            const int m = 32 * i + l32;
-            float v[4] = {__builtin_fmaf(acc[i][j][4 * q], sc.x, bi.x),
-                          __builtin_fmaf(acc[i][j][4 * q + 1], sc.y, bi.y),
-                          __builtin_fmaf(acc[i][j][4 * q + 2], sc.z, bi.z),
-                          __builtin_fmaf(acc[i][j][4 * q + 3], sc.w, bi.w)};
-            v4h o;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) o[t] = (_Float16)(v[t] + (float)r[i][q][t]);
-            *reinterpret_cast<v4h*>(&X[m * XS + n]) = o;
-          }
-        }
-      }
-    };
-    __syncthreads();  // barrier 2: every context read done
-    __syncthreads();  // barrier 3: the residual rows are in X
-    epilogue(lds.so, lds.bo);
+    v16f acc[RT][CT];
 #pragma unroll
     for (int i = 0; i < RT; ++i)
 #pragma unroll
@@ -1080,7 +1106,7 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
       __syncthreads();  // barriers 7 .. NC + 6: chunk c consumed, chunk c + 1 written
     }
     __syncthreads();  // barrier NC + 7: the first LayerNorm's output rows are in X
-    epilogue(lds.s2, lds.b2);
+    tail_epilogue<H, RT, 0, XS>(X, lds.s2, lds.b2, nb, l32, g, acc);
     __syncthreads();  // barrier NC + 8
     layer_norm2();
   } else {
@@ -1157,10 +1183,25 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
       }
     };
     load_rows(a.h);
-    load_w1(0);
-    __syncthreads();  // barrier 2: every context read done
-    store_rows();
-    __syncthreads();  // barrier 3
+    if constexpr (RTU > 0) {
+      v16f acco[RTU][CT];
+#pragma unroll
+      for (int i = 0; i < RTU; ++i)
+#pragma unroll
+        for (int j = 0; j < CT; ++j) acco[i][j] = v16f{0};
+      v8h wqo[PF][CT];
+      prime_wo(wqo);
+      tail_o_proj<H, RTU, RTD, PF, XS>(wo_base, (uint32_t)lane * 16u, X, l32, g, wqo, acco);
+      __syncthreads();  // barrier 2: every context read done
+      store_rows();
+      __syncthreads();  // barrier 3
+      tail_epilogue<H, RTU, RTD, XS>(X, lds.so, lds.bo, nb, l32, g, acco);
+    } else {
+      __syncthreads();  // barrier 2: every context read done
+      store_rows();
+      __syncthreads();  // barrier 3
+    }
+    load_w1(0);  // lands during the first LayerNorm
     __syncthreads();  // barrier 4
     layer_norm1();
     __syncthreads();  // barrier 5
