@@ -620,13 +620,14 @@ int eoship_tq_bind_corpus_opts(EosHipRuntime* rt, const EosHipTQDesc* desc, cons
       hip_err(err, "hipMemcpyAsync(codes)", e);
       return fail();
     }
-    if (rt->alloc((size_t)tq->ntiles * sizeof(float), reinterpret_cast<void**>(&tq->tile_cn), err) != 0) {
+    if (rt->alloc((size_t)tq->ntiles * 2 * sizeof(float), reinterpret_cast<void**>(&tq->tile_cn), err) != 0) {
       hipFree(dcodes);
       return fail();
     }
     TqTileNormArgs tn;
     memset(&tn, 0, sizeof(tn));
     tn.codes = static_cast<const uint8_t*>(dcodes);
+    tn.norms = tq->norms;
     tn.tile_cn = tq->tile_cn;
     tn.n = n;
     tn.d = tq->d;

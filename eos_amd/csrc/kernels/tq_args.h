@@ -44,7 +44,7 @@ struct TqScanArgs {
   int32_t* out_dots;       // dense output (optional)
   const int* gate;         // non-NULL: run only if some gate[i] != 0, i < q
   const float* lonorm;     // high-half filter: [32*nqg] ||lo||_2 per column (rounded up)
-  const float* tile_cn;    // high-half filter: [ntiles] max ||C[codes]||_2 of the tile (rounded up)
+  const float* tile_cn;    // high-half filter: [ntiles][2] max ||C[codes]||_2 of the tile (rounded up), max Norm
   long long n;             // valid vectors
   long long out_begin;     // dense: vector index of column 0
   long long out_count;     // dense: columns
@@ -141,10 +141,12 @@ struct TqRescoreArgs {
   uint32_t lut0, lut1, lut2, lut3;
 };
 
-// Per tile of 32 vectors, the largest ||C[codes]||_2 (rounded up to f32).
+// Per tile of 32 vectors, the largest ||C[codes]||_2 (rounded up to f32) and
+// the largest Norm.
 struct TqTileNormArgs {
   const uint8_t* codes;    // [n][row_bytes] reference layout
-  float* tile_cn;          // [ntiles]
+  const float* norms;      // [n]
+  float* tile_cn;          // [ntiles][2]: {max ||C[codes]||_2, max Norm}
   long long n;
   int d, bits, row_bytes;
   int cb[16];              // codebook grid values

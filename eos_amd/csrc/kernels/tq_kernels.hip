@@ -284,7 +284,8 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_pack(TqPackArgs a) {
 }
 
 // Per tile, the largest ||C[codes_v]||_2 over its vectors (exact integer
-// sums of squares, rounded up): one thread per vector, a half-wave per tile.
+// sums of squares, rounded up) and the largest Norm: one thread per vector, a
+// half-wave per tile.
 extern "C" __global__ __launch_bounds__(256) void eos_tq_tile_cnorm(TqTileNormArgs a) {
   const long long v = (long long)blockIdx.x * 256 + threadIdx.x;
   long long ss = 0;
@@ -310,13 +311,18 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_tile_cnorm(TqTileNormAr
       ss += (long long)(c * c);
     }
   }
+  float nm = v < a.n ? a.norms[v] : 0.0f;
 #pragma unroll
   for (int o = 16; o > 0; o >>= 1) {
     const long long t = __shfl_xor(ss, o);
     ss = t > ss ? t : ss;
+    nm = fmaxf(nm, __shfl_xor(nm, o));
   }
   const long long tile = v >> 5;
-  if ((threadIdx.x & 31) == 0 && tile * kTile < a.n) a.tile_cn[tile] = sqrt_up(ss);
+  if ((threadIdx.x & 31) == 0 && tile * kTile < a.n) {
+    a.tile_cn[2 * tile] = sqrt_up(ss);
+    a.tile_cn[2 * tile + 1] = nm;
+  }
 }
 
 // ----------------------------------------------------------------- encode
@@ -469,6 +475,7 @@ constexpr int kLdsSlots = 16;
 constexpr int kRingRegsHi = 176;
 constexpr int kRingRegsExact = 150;
 constexpr int kRingCap = 2;
+constexpr int kRingCapHi = 2;
 
 template <int NLOAD>
 EOS_DEV void load_tile_codes(v4i (&r)[NLOAD], const v4i* packed, long long tile, int lane) {
@@ -542,12 +549,12 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     int t;  // tile index in [0, ntiles); >= the range end: none
   };
   // Codes first, then norms: lanes 0-31 load the tile's norms; with HI, lanes
-  // 32-63 load its tile_cn.
+  // 32 and 33 load its tile_cn pair (code-norm bound, largest Norm).
   auto load_stage = [&](Stage& st, int jj) {
     const long long t = a.tile_begin + (long long)jj * a.tile_step;
     load_tile_codes<NLOAD>(st.raw, packed, t, lane);
     if constexpr (HI)
-      st.nv = lane < 32 ? a.norms[t * kTile + lane] : a.tile_cn[t];
+      st.nv = lane < 32 ? a.norms[t * kTile + lane] : a.tile_cn[2 * t + (lane & 1)];
     else
       st.nv = a.norms[t * kTile + (lane & 31)];
   };
@@ -579,30 +586,52 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
     // Epilogue. Accumulator element i of lane l is row 8(i/4) + 4(l/32) + i%4
     // (a corpus vector of the tile) and column l%32 (a query of the group).
     const long long vbase = tile * kTile;
-    // Row r's norm sits at float r of the wave's slot; lane l needs rows
-    // 8 i4 + 4 (l / 32) + {0..3}, i.e. float4 2 i4 + l / 32. LDS operations of
-    // one wave complete in order, so no barrier is needed around the slot.
-    if (lane < 32) reinterpret_cast<float*>(nstage[wave])[lane] = st.nv;
-    __builtin_amdgcn_wave_barrier();
-    float4 nrm4[4];
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) nrm4[i4] = nstage[wave][2 * i4 + half];
-    __builtin_amdgcn_wave_barrier();
-    float nrm[16];
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      nrm[4 * i4 + 0] = nrm4[i4].x;
-      nrm[4 * i4 + 1] = nrm4[i4].y;
-      nrm[4 * i4 + 2] = nrm4[i4].z;
-      nrm[4 * i4 + 3] = nrm4[i4].w;
-    }
     // Rows of this tile that are real vectors (the last tile may be partial).
     const long long rem64 = a.n - vbase;
     const int rem = rem64 >= kTile ? kTile : (int)rem64;
+    // Row r's norm sits at float r of the wave's slot; lane l needs rows
+    // 8 i4 + 4 (l / 32) + {0..3}, i.e. float4 2 i4 + l / 32. LDS operations of
+    // one wave complete in order, so no barrier is needed around the slot.
+    float nrm[16];
+    auto row_norms = [&]() {
+      if (lane < 32) reinterpret_cast<float*>(nstage[wave])[lane] = st.nv;
+      __builtin_amdgcn_wave_barrier();
+      float4 nrm4[4];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) nrm4[i4] = nstage[wave][2 * i4 + half];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        nrm[4 * i4 + 0] = nrm4[i4].x;
+        nrm[4 * i4 + 1] = nrm4[i4].y;
+        nrm[4 * i4 + 2] = nrm4[i4].z;
+        nrm[4 * i4 + 3] = nrm4[i4].w;
+      }
+    };
     if constexpr (HI) {
       const float cn = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(st.nv), 32));
+      const float nmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(st.nv), 33));
+      // Tile-level test first: with A = max_i acc_i and N = the tile's
+      // largest Norm, fl(fl(256 A + lb) N) >= every row's fl(fl(256 acc_i +
+      // lb) n_i) whenever it is >= 0 (rounding is monotone, n_i <= N), and
+      // when it is < 0 no row reaches pt > 0; pt = -inf passes every tile.
+      // Only lanes that pass evaluate their rows.
+      bool pass[NQG];
+      bool anyp = false;
 #pragma unroll
       for (int g = 0; g < NQG; ++g) {
+        int am = acc[g][0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) am = max(am, acc[g][i]);
+        const float lb = (lo_r[g] * cn) * 1.0000002f;  // >= lonorm * cn exactly
+        pass[g] = __builtin_fmaf((float)am, 256.0f, lb) * nmax >= pt_r[g];
+        anyp |= pass[g];
+      }
+      if (__ballot(anyp) == 0ull) return;
+      row_norms();
+#pragma unroll
+      for (int g = 0; g < NQG; ++g) {
+        if (!pass[g]) continue;
         const int qi = g * 32 + (lane & 31);
         const float lb = (lo_r[g] * cn) * 1.0000002f;  // >= lonorm * cn exactly
         float p[16];
@@ -636,6 +665,7 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
       }
       return;
     }
+    row_norms();
 #pragma unroll
     for (int g = 0; g < NQG; ++g) {
       const int qi = g * 32 + (lane & 31);
@@ -734,7 +764,8 @@ EOS_DEV void tq_scan_body(const TqScanArgs& a) {
   // accumulators in the 256 registers of two waves per SIMD.
   constexpr int kStageRegs = NLOAD * 4 + 1;
   constexpr int kRingFit = ((HI ? kRingRegsHi : kRingRegsExact) - NCBU * 16) / kStageRegs;
-  constexpr int R = kRingFit > kRingCap ? kRingCap : kRingFit < 2 ? 2 : kRingFit;
+  constexpr int kCap = HI ? kRingCapHi : kRingCap;
+  constexpr int R = kRingFit > kCap ? kCap : kRingFit < 2 ? 2 : kRingFit;
   Stage st[R];
   // Query fragments (HI: the high-half blocks only, block cb = 2 g of each
   // K-step) are staged in LDS once per workgroup. Loads retire in order, so
