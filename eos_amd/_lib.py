@@ -92,6 +92,62 @@ class EosHipCompactLayer(C.Structure):
     ]
 
 
+class EosHipCompactOptions(C.Structure):
+    _fields_ = [
+        ("rope", C.c_int32),
+        ("role", C.c_int32),
+        ("scaled_scores", C.c_int32),
+        ("attend_padding", C.c_int32),
+    ]
+
+
+class EosHipMllInfo(C.Structure):
+    _fields_ = [
+        ("profile", C.c_int32),
+        ("sections", C.c_int32),
+        ("strings", C.c_int64),
+        ("tensors", C.c_int64),
+        ("has_metadata", C.c_int32),
+        ("module_name", C.c_char * 128),
+        ("module_version", C.c_char * 64),
+    ]
+
+
+class EosHipMllTensor(C.Structure):
+    _fields_ = [
+        ("name", C.c_char_p),
+        ("kind", C.c_int32),
+        ("storage_dtype", C.c_int32),
+        ("rank", C.c_int32),
+        ("dims", C.c_int64 * 8),
+        ("elements", C.c_int64),
+        ("data", C.c_void_p),
+        ("bytes", C.c_uint64),
+        ("scale", C.c_float),
+    ]
+
+
+class EosHipMllPlan(C.Structure):
+    _fields_ = [
+        ("route", C.c_int32),
+        ("layers", C.c_int32),
+        ("distinct_layers", C.c_int32),
+        ("model_dim", C.c_int32),
+        ("heads", C.c_int32),
+        ("hidden_dim", C.c_int32),
+        ("vocab", C.c_int32),
+        ("max_sequence", C.c_int32),
+        ("output_dim", C.c_int32),
+        ("batched", C.c_int32),
+        ("steps", C.c_int32),
+        ("options", EosHipCompactOptions),
+        ("entry", C.c_char * 64),
+        ("token_input", C.c_char * 64),
+        ("mask_input", C.c_char * 64),
+        ("output_name", C.c_char * 64),
+    ]
+
+
 # name -> (argtypes) ; every function returns int except where noted
 _SIGNATURES = {
     "eoship_abi_version": ([], C.c_int),
@@ -187,6 +243,23 @@ _SIGNATURES = {
     "eoship_encoder_bind_compact": ([C.c_void_p, C.POINTER(EosHipCompactDesc), _I8P, C.c_float,
                                      _I8P, C.c_float, C.POINTER(EosHipCompactLayer), _I8P,
                                      C.c_float, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_encoder_bind_compact_opts": ([C.c_void_p, C.POINTER(EosHipCompactDesc),
+                                          C.POINTER(EosHipCompactOptions), _I8P, C.c_float, _I8P,
+                                          C.c_float, C.POINTER(EosHipCompactLayer), _I8P,
+                                          C.c_float, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_mll_open": ([C.c_void_p, C.c_uint64, C.POINTER(C.c_void_p), C.c_void_p], C.c_int),
+    "eoship_mll_close": ([C.c_void_p], None),
+    "eoship_mll_info": ([C.c_void_p, C.POINTER(EosHipMllInfo), C.c_void_p], C.c_int),
+    "eoship_mll_section": ([C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p),
+                            C.POINTER(C.c_uint64), C.c_void_p], C.c_int),
+    "eoship_mll_tensor": ([C.c_void_p, C.c_int64, C.c_char_p, C.POINTER(EosHipMllTensor),
+                           C.c_void_p], C.c_int),
+    "eoship_blake3": ([C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_mll_classify": ([C.c_void_p, C.c_char_p, C.POINTER(EosHipMllPlan), C.c_void_p],
+                            C.c_int),
+    "eoship_encoder_bind_mll": ([C.c_void_p, C.c_void_p, C.c_char_p, C.c_int32,
+                                 C.POINTER(C.c_void_p), C.POINTER(EosHipMllPlan), C.c_void_p],
+                                C.c_int),
     "eoship_encoder_release": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_forward": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                 C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),

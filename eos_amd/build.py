@@ -41,6 +41,7 @@ HOST_SOURCES = [
     os.path.join(CSRC, "eoship_tq.cpp"),
     os.path.join(CSRC, "eoship_encoder.cpp"),
     os.path.join(CSRC, "eoship_embed.cpp"),
+    os.path.join(CSRC, "eoship_mll.cpp"),
 ]
 
 # Packed-FP32 instructions are disabled for every device build.

@@ -73,6 +73,12 @@ struct EosHipEncoder {
   // LayerNorm as one kernel per row block (eos_enc_tail_*); otherwise, or
   // when switched off, the unfused GEMM + LayerNorm launches.
   bool fused_tail = true;
+  // Compact family: attention scores times 1/sqrt(head dim) (else plain q kT),
+  // and attention over every position of the padded input with the mask
+  // selecting only the pooled rows (else over each sequence's mask != 0
+  // positions).
+  bool scaled_scores = true;
+  bool attend_all = false;
   int odim = 0;
   float* proj = nullptr;
   std::vector<void*> owned;
@@ -229,7 +235,7 @@ struct EosHipEncoder {
     // status[0]: an id out of range; status[1]: attention reference moves.
     hipError_t e = hipMemsetAsync(status, 0, 8, rt->stream);
     if (e != hipSuccess) return hip_err(err, "hipMemsetAsync(status)", e);
-    EncPackArgs pk{d_mask, row_b, row_t, seq_off, seq_cnt, total, batch, tokens};
+    EncPackArgs pk{d_mask, row_b, row_t, seq_off, seq_cnt, total, batch, tokens, attend_all ? 1 : 0};
     if (rt->launch("eos_enc_count", dim3(batch), dim3(256), 0, &pk, err) != 0 ||
         rt->launch("eos_enc_pack", dim3(batch), dim3(256), 0, &pk, err) != 0)
       return 1;
@@ -299,8 +305,9 @@ struct EosHipEncoder {
       if (gemm(h, L.w_qkv, a8 ? L.w_qkv8 : nullptr, L.s_qkv, L.b_qkv, qkv, nullptr, 3 * H, H, 0,
                "enc_gemm_qkv", vt) != 0)
         return 1;
+      const double log2e = 1.4426950408889634;
       EncAttnArgs at{qkv, vt, ctx, seq_off, seq_cnt, batch, nh, H, tokens, vt_ld,
-                     (float)(1.4426950408889634 / std::sqrt((double)hd)), status + 1};
+                     (float)(scaled_scores ? log2e / std::sqrt((double)hd) : log2e), status + 1};
       if (rt->launch(attn_name, dim3((tokens + 127) / 128, nh, batch), dim3(256), 0, &at, err) != 0)
         return 1;
       if (tail_name != nullptr) {
@@ -322,7 +329,9 @@ struct EosHipEncoder {
         return 1;
     }
     const int nchunk = (tokens + kPoolChunk - 1) / kPoolChunk;
-    EncPoolArgs pl{h, seq_off, seq_cnt, d_out, proj, pool_part, batch, H, family, out_dim(), nchunk};
+    EncPoolArgs pl{h,     seq_off, seq_cnt,   d_out,   proj,
+                   pool_part, batch, H,     family,  out_dim(),
+                   nchunk, attend_all ? d_mask : nullptr, tokens};
     if (rt->launch("eos_enc_pool_part", dim3((unsigned)nchunk, (unsigned)batch), dim3(256), 0, &pl,
                    err) != 0)
       return 1;
@@ -332,14 +341,14 @@ struct EosHipEncoder {
 
 // Shapes the kernels support: hidden widths 128..768 (embed and LayerNorm
 // hold a row in one wavefront; every GEMM N a multiple of the 128-column
-// tile), attention head dims 32/64/128, FFN widths in multiples of 128.
+// tile), attention head dims 32/64/128/256, FFN widths in multiples of 128.
 static int check_dims(int H, int heads, int F, const char* what, char** err) {
   if (H != 128 && H != 256 && H != 384 && H != 512 && H != 768)
     return set_err(err, "%s: hidden must be 128, 256, 384, 512 or 768 (got %d)", what, H);
   if (heads <= 0 || H % heads != 0 ||
-      (H / heads != 32 && H / heads != 64 && H / heads != 128))
-    return set_err(err, "%s: head dim must be 32, 64 or 128 (hidden %d, heads %d)", what, H,
-                   heads);
+      (H / heads != 32 && H / heads != 64 && H / heads != 128 && H / heads != 256))
+    return set_err(err, "%s: head dim must be 32, 64, 128 or 256 (hidden %d, heads %d)", what,
+                   H, heads);
   if (F <= 0 || F % 128 != 0)
     return set_err(err, "%s: intermediate width must be a positive multiple of 128", what);
   return 0;
@@ -418,9 +427,27 @@ int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc
                                 const int8_t* role_embedding, float s_role,
                                 const EosHipCompactLayer* layers, const int8_t* output_projection,
                                 float s_output, EosHipEncoder** out, char** err) {
+  if (role_embedding == nullptr) return set_err(err, "eoship_encoder_bind_compact: NULL argument");
+  return eoship_encoder_bind_compact_opts(rt, desc, nullptr, token_embedding, s_token,
+                                          role_embedding, s_role, layers, output_projection,
+                                          s_output, out, err);
+}
+
+int eoship_encoder_bind_compact_opts(EosHipRuntime* rt, const EosHipCompactDesc* desc,
+                                     const EosHipCompactOptions* opts,
+                                     const int8_t* token_embedding, float s_token,
+                                     const int8_t* role_embedding, float s_role,
+                                     const EosHipCompactLayer* layers,
+                                     const int8_t* output_projection, float s_output,
+                                     EosHipEncoder** out, char** err) {
   const char* what = "eoship_encoder_bind_compact";
+  EosHipCompactOptions o{1, 1, 1, 0};
+  if (opts != nullptr) o = *opts;
+  auto bit = [](int32_t v) { return v == 0 || v == 1; };
+  if (!bit(o.rope) || !bit(o.role) || !bit(o.scaled_scores) || !bit(o.attend_padding))
+    return set_err(err, "%s: options must be 0 or 1", what);
   if (rt == nullptr || desc == nullptr || out == nullptr || token_embedding == nullptr ||
-      role_embedding == nullptr || (desc->layers > 0 && layers == nullptr))
+      (o.role && role_embedding == nullptr) || (desc->layers > 0 && layers == nullptr))
     return set_err(err, "%s: NULL argument", what);
   *out = nullptr;
   const int D = desc->model_dim, F = desc->hidden_dim, O = desc->output_dim;
@@ -432,7 +459,8 @@ int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc
     return set_err(err, "%s: output_projection must be given exactly when output_dim != model_dim",
                    what);
   auto bad_scale = [](float sc) { return !(sc >= 0.f) || std::isinf(sc); };
-  if (bad_scale(s_token) || bad_scale(s_role) || (output_projection && bad_scale(s_output)))
+  if (bad_scale(s_token) || (o.role && bad_scale(s_role)) ||
+      (output_projection && bad_scale(s_output)))
     return set_err(err, "%s: scales must be finite and >= 0", what);
   for (int l = 0; l < desc->layers; ++l) {
     const EosHipCompactLayer& s = layers[l];
@@ -446,6 +474,8 @@ int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc
   enc->rt = rt;
   enc->family = 1;
   enc->odim = O;
+  enc->scaled_scores = o.scaled_scores != 0;
+  enc->attend_all = o.attend_padding != 0;
   EosHipEncoderDesc& d = enc->desc;
   d.layers = desc->layers;
   d.hidden = D;
@@ -467,16 +497,19 @@ int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc
     return v;
   };
   const std::vector<float> tok = dequant(token_embedding, s_token, (size_t)desc->vocab * D);
-  const std::vector<float> role = dequant(role_embedding, s_role, (size_t)3 * D);
+  // Without roles the role rows are zeros: token + 0 is the token row exactly.
+  const std::vector<float> role = o.role ? dequant(role_embedding, s_role, (size_t)3 * D)
+                                         : std::vector<float>((size_t)3 * D, 0.0f);
   // RoPE table: per position, (cos, sin) of theta = pos / 10000^(c / D) for
   // each even column c, computed in f64 and rounded to f32 (ropeRows,
-  // runtime/backend/tensor_ops.go:1936-1965).
+  // runtime/backend/tensor_ops.go:1936-1965). Without RoPE, (1, 0) for every
+  // pair: the rotation x0 * 1 - x1 * 0, x0 * 0 + x1 * 1 returns the pair exactly.
   std::vector<float> rope((size_t)desc->max_sequence * D);
   for (int pos = 0; pos < desc->max_sequence; ++pos)
     for (int c = 0; c + 1 < D; c += 2) {
       const double theta = (double)pos / std::pow(10000.0, (double)c / (double)D);
-      rope[(size_t)pos * D + c] = (float)std::cos(theta);
-      rope[(size_t)pos * D + c + 1] = (float)std::sin(theta);
+      rope[(size_t)pos * D + c] = o.rope ? (float)std::cos(theta) : 1.0f;
+      rope[(size_t)pos * D + c + 1] = o.rope ? (float)std::sin(theta) : 0.0f;
     }
   const std::vector<float> ones((size_t)D, 1.0f);
   const std::vector<float> zeros((size_t)std::max(3 * D, F), 0.0f);
@@ -495,6 +528,21 @@ int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc
   }
   for (int l = 0; l < desc->layers; ++l) {
     const EosHipCompactLayer& s = layers[l];
+    // Tied layers (the same codes and scales as an earlier layer) share its
+    // device copies.
+    int tied = -1;
+    auto same = [](const EosHipCompactLayer& x, const EosHipCompactLayer& y) {
+      return x.attn_q == y.attn_q && x.s_q == y.s_q && x.attn_k == y.attn_k && x.s_k == y.s_k &&
+             x.attn_v == y.attn_v && x.s_v == y.s_v && x.attn_o == y.attn_o && x.s_o == y.s_o &&
+             x.ffn_up == y.ffn_up && x.s_up == y.s_up && x.ffn_down == y.ffn_down &&
+             x.s_down == y.s_down;
+    };
+    for (int j = 0; j < l && tied < 0; ++j)
+      if (same(layers[j], s)) tied = j;
+    if (tied >= 0) {
+      enc->layers.push_back(enc->layers[(size_t)tied]);
+      continue;
+    }
     DevLayer dl;
     const int8_t* qkv[] = {s.attn_q, s.attn_k, s.attn_v};
     const float sqkv[] = {s.s_q, s.s_k, s.s_v};

@@ -11,7 +11,7 @@
 
 #include "eoship.h"
 
-#define EOSHIP_ABI_VERSION 5
+#define EOSHIP_ABI_VERSION 6
 
 namespace eoship {
 

@@ -16,6 +16,7 @@ struct EncPackArgs {
   int32_t* seq_cnt;      // [batch]
   int32_t* total;        // [1] active rows
   int batch, tokens;
+  int all_active;        // 1: every position is packed, whatever the mask says
 };
 
 // mode 0 (BERT): token + position + type, then affine LayerNorm.
@@ -145,6 +146,11 @@ struct EncPoolArgs {
   const float* proj;       // mode 1 only, [hidden][odim] f32, or NULL
   float* part;             // [batch][nchunk][hidden] f32 partial sums
   int batch, hidden, mode, odim, nchunk;
+  // NULL, or the [batch][tokens] mask when every position was packed (row r
+  // of a sequence is its position r): only rows whose mask is non-zero are
+  // pooled, and the mean divides by their count.
+  const int32_t* mask;
+  int tokens;
 };
 
 // Tiny embed pipeline (examples/embed.eos): gather f16 table rows, multiply by

@@ -175,7 +175,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_count(EncPackArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int t = base + 256 * u;
-      v[u] = t < a.tokens ? m[t] : 0;
+      v[u] = t < a.tokens ? (a.all_active ? 1 : m[t]) : 0;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) mine += v[u] != 0 ? 1 : 0;
@@ -208,7 +208,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int t = t0 + k0 + u;
-      v[u] = (k0 + u < per && t < a.tokens) ? m[t] : 0;
+      v[u] = (k0 + u < per && t < a.tokens) ? (a.all_active ? 1 : m[t]) : 0;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) mine += v[u] != 0 ? 1 : 0;
@@ -220,7 +220,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int t = t0 + k0 + u;
-      v[u] = (k0 + u < per && t < a.tokens) ? m[t] : 0;
+      v[u] = (k0 + u < per && t < a.tokens) ? (a.all_active ? 1 : m[t]) : 0;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -1477,6 +1477,12 @@ extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
 void eos_enc_attn_hd128(EncAttnArgs a) {
   attn_body<128, 32>(a);
 }
+// Head dim 256 (the single-head compact graphs at D = 256): the O^T
+// accumulator alone is 128 registers and the Q^T fragments 64, so this one
+// keeps the one-wave-per-SIMD budget.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_attn_hd256(EncAttnArgs a) {
+  attn_body<256, 32>(a);
+}
 
 // ------------------------------------------------------------------- pool
 
@@ -1530,7 +1536,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_pool_part(EncPoolArgs 
         const float norm = sqrtf(wave_sum(q));
         scale = norm > 0.f ? norm : 1.0f;
       }
-      if (r0 + u < r_end) {
+      if (r0 + u < r_end && (a.mask == nullptr || a.mask[(size_t)b * a.tokens + r0 + u] != 0)) {
 #pragma unroll
         for (int gg = 0; gg < 2; ++gg)
 #pragma unroll
@@ -1563,13 +1569,26 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
   __shared__ float red[16];
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ int mcount[16];
   const int cnt = a.seq_cnt[b];
   const int nc = cnt > 0 ? (cnt + kPoolChunk - 1) / kPoolChunk : 0;
+  // Pooled rows: all of the sequence's rows, or those whose mask is set.
+  int pooled_rows = cnt;
+  if (a.mask != nullptr) {
+    int mine = 0;
+    for (int t = tid; t < a.tokens; t += 1024) mine += a.mask[(size_t)b * a.tokens + t] != 0 ? 1 : 0;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mine += __shfl_xor(mine, o);
+    if (lane == 0) mcount[w] = mine;
+    __syncthreads();
+    pooled_rows = 0;
+    for (int i = 0; i < 16; ++i) pooled_rows += mcount[i];
+  }
   float v = 0.f;
   if (tid < a.hidden) {
     const float* src = a.part + (size_t)b * a.nchunk * a.hidden + tid;
     for (int c = 0; c < nc; ++c) v += src[(size_t)c * a.hidden];
-    v = cnt > 0 ? v * (1.0f / (float)cnt) : 0.f;
+    v = pooled_rows > 0 ? v * (1.0f / (float)pooled_rows) : 0.f;
   }
   if (a.mode == 1) {
     if (a.proj == nullptr) {

@@ -272,7 +272,10 @@ class CompactEncoder(Encoder):
     """A compact (family (a)) embedder bound on the device; ``embed`` takes
     (tokens, attention_mask, role_ids) and returns [batch, output_dim]."""
 
-    def __init__(self, rt: Runtime, w: CompactWeights):
+    def __init__(self, rt: Runtime, w: CompactWeights, options: dict | None = None):
+        """options: graph options {rope, role, scaled_scores, attend_padding}
+        (0/1 each; None: the compactTransformerSource graph, 1/1/1/0); with
+        role 0 the role table is not read."""
         self.rt, self.w = rt, w
         D, F = w.model_dim, w.hidden_dim
         keep = []
@@ -295,7 +298,17 @@ class CompactEncoder(Encoder):
             x.ffn_down, x.s_down = i8(L.ffn_down, (F, D)), L.s_down
         vocab = int(np.asarray(w.token_embedding).shape[0])
         tok = i8(w.token_embedding, (vocab, D))
-        role = i8(w.role_embedding, (3, D))
+        opts = None
+        if options is not None:
+            full = {"rope": 1, "role": 1, "scaled_scores": 1, "attend_padding": 0}
+            unknown = set(options) - set(full)
+            if unknown:
+                raise ValueError(f"unknown compact options {sorted(unknown)}")
+            full.update({k: int(v) for k, v in options.items()})
+            opts = _lib.EosHipCompactOptions(**full)
+        role = None
+        if opts is None or opts.role:
+            role = i8(w.role_embedding, (3, D))
         proj = None
         if w.output_projection is not None:
             proj = i8(w.output_projection, (D, w.output_dim))
@@ -304,9 +317,10 @@ class CompactEncoder(Encoder):
                                       output_dim=w.output_dim)
         self.out_dim = w.output_dim
         self.handle = C.c_void_p()
-        _lib.call("eoship_encoder_bind_compact", rt.handle, C.byref(desc), tok,
-                  C.c_float(w.s_token), role, C.c_float(w.s_role), layers, proj,
-                  C.c_float(w.s_output), C.byref(self.handle))
+        _lib.call("eoship_encoder_bind_compact_opts", rt.handle, C.byref(desc),
+                  C.byref(opts) if opts is not None else None, tok, C.c_float(w.s_token), role,
+                  C.c_float(w.s_role), layers, proj, C.c_float(w.s_output),
+                  C.byref(self.handle))
         del keep
 
     def embed(self, tokens: np.ndarray, attention_mask: np.ndarray,

@@ -295,7 +295,7 @@ typedef struct EosHipEncoder EosHipEncoder;
 typedef struct {
   int32_t layers;        /* num_hidden_layers */
   int32_t hidden;        /* 128, 256, 384, 512 or 768 */
-  int32_t heads;         /* hidden / heads in {32, 64, 128} */
+  int32_t heads;         /* hidden / heads in {32, 64, 128, 256} */
   int32_t intermediate;  /* FFN width, multiple of 128 */
   int32_t vocab;         /* token table rows */
   int32_t max_positions; /* position table rows (>= tokens) */
@@ -362,9 +362,9 @@ int eoship_encoder_attention_moves(EosHipRuntime* rt, EosHipEncoder* enc, int64_
  * compactTransformerSource emits, models/default_embedding.go:419-505, with
  * the DefaultEmbeddingPackageConfig fields of :264-300). */
 typedef struct {
-  int32_t layers;        /* EncoderRepeats (each layer has its own weights) */
+  int32_t layers;        /* EncoderRepeats (layers may repeat one set of codes: tied) */
   int32_t model_dim;     /* D: 128, 256, 384, 512 or 768 */
-  int32_t heads;         /* AttentionHeads; D / heads in {32, 64, 128} */
+  int32_t heads;         /* AttentionHeads; D / heads in {32, 64, 128, 256} */
   int32_t hidden_dim;    /* FFN width H, positive multiple of 128 */
   int32_t vocab;         /* token_embedding rows */
   int32_t max_sequence;  /* longest accepted tokens (RoPE table rows) */
@@ -399,6 +399,40 @@ int eoship_encoder_bind_compact(EosHipRuntime* rt, const EosHipCompactDesc* desc
                                 const int8_t* role_embedding, float s_role,
                                 const EosHipCompactLayer* layers, const int8_t* output_projection,
                                 float s_output, EosHipEncoder** out, char** err);
+
+/* Graph options of a compact embedder, each 0 or 1. eoship_encoder_bind_compact
+ * binds with rope, role and scaled_scores 1 and attend_padding 0 (the
+ * compactTransformerSource graph). */
+typedef struct {
+  int32_t rope;            /* 1: ropeRows after the gather; 0: no rotation */
+  int32_t role;            /* 1: token + role_embedding[role id]; 0: token rows only
+                            * (role_embedding may then be NULL) */
+  int32_t scaled_scores;   /* 1: one head's q kT times 1/sqrt(D) (scaled_attention_scores,
+                            * runtime/backend/tensor_ops.go:1291-1315); 0: the plain matmul
+                            * q kT of a plan's matmul step (tensor_ops.go:1168-1249).
+                            * Several heads always scale by 1/sqrt(D / heads). */
+  int32_t attend_padding;  /* 0: each query attends the mask != 0 positions of its
+                            * sequence (maskedSoftmaxRowsF32, tensor_ops.go:1825-1865; also
+                            * what EmbeddingModel's length-grouped batches give,
+                            * runtime/embedding_model.go:689-691, 798-850); 1: every position
+                            * of the padded [batch][tokens] input is a key and a query (a
+                            * plan whose softmax step is softmaxRows, tensor_ops.go:
+                            * 1757-1788), and the mask only selects the pooled rows
+                            * (meanPoolMaskedTensor, tensor_ops.go:1644-1709); every id,
+                            * padding included, must then be in range, as gatherTensor
+                            * requires. */
+} EosHipCompactOptions;
+
+/* eoship_encoder_bind_compact with graph options (NULL: its defaults); with
+ * role 0, role_embedding may be NULL. Also the binding behind
+ * eoship_encoder_bind_mll. */
+int eoship_encoder_bind_compact_opts(EosHipRuntime* rt, const EosHipCompactDesc* desc,
+                                     const EosHipCompactOptions* opts,
+                                     const int8_t* token_embedding, float s_token,
+                                     const int8_t* role_embedding, float s_role,
+                                     const EosHipCompactLayer* layers,
+                                     const int8_t* output_projection, float s_output,
+                                     EosHipEncoder** out, char** err);
 
 /* Two-stage retrieval, second stage (the promoted serving profile
  * turboquant_ip_b4_overfetch200_fp16_rerank). eoship_f16_sidecar_device turns
@@ -441,6 +475,101 @@ int eoship_tq_fp16_rerank_device_noalloc(EosHipRuntime* rt, const float* d_queri
                                          int32_t c, int32_t k, int32_t bit_width,
                                          int32_t overfetch, const int64_t* d_id_rank,
                                          int64_t* d_ids, float* d_scores, char** err);
+
+/* ------------------------------------------------------------------------
+ * MLL packages (the reference's sealed .mll container) and plan binding.
+ * ------------------------------------------------------------------------ */
+
+/* A parsed, digest-verified package (the file bytes are copied). */
+typedef struct EosHipMll EosHipMll;
+
+/* Storage kinds of a TNSR payload. */
+#define EOSHIP_MLL_Q8 1   /* int8 codes, dequantized = code * scale */
+#define EOSHIP_MLL_Q4 2   /* offset-binary nibbles, low nibble first: (nibble - 8) * scale */
+#define EOSHIP_MLL_F32 3  /* little-endian f32 values (logical f32, or q8/q4 held as values) */
+#define EOSHIP_MLL_F16 4  /* little-endian binary16 values */
+#define EOSHIP_MLL_I32 5
+#define EOSHIP_MLL_I64 6
+
+typedef struct {
+  int32_t profile;          /* header profile byte */
+  int32_t sections;
+  int64_t strings;          /* STRG entries, the implicit "" at index 0 included */
+  int64_t tensors;
+  int32_t has_metadata;     /* an XMTA section that MLLMetadata.Validate accepts */
+  char module_name[128];
+  char module_version[64];
+} EosHipMllInfo;
+
+typedef struct {
+  const char* name;         /* valid while the package is open */
+  int32_t kind;             /* EOSHIP_MLL_* */
+  int32_t storage_dtype;    /* the TNSR entry's dtype byte */
+  int32_t rank;
+  int64_t dims[8];
+  int64_t elements;
+  const uint8_t* data;      /* payload inside the package's copy of the file */
+  uint64_t bytes;
+  float scale;              /* tensor_scales[name] (0 when absent) */
+} EosHipMllTensor;
+
+/* Reads an MLL file image: header, section directory, the BLAKE3 digest of
+ * every section body (XKBI, the offline kernel images, is skipped without
+ * reading its bytes), STRG, TNSR and the XMTA metadata (version, module name
+ * and version, artifact JSON, logical dtypes, finite non-negative
+ * tensor_scales). A packed Q8/Q4 tensor without a positive scale must hold
+ * only zero codes. Replaces DecodeMLL / ReadFile (artifact/eos/mll.go:
+ * 332-360, 404-420) and decodeWeightFileFromMLLReader + decodeTensorEntry
+ * (runtime/weight_file.go:248-415). */
+int eoship_mll_open(const uint8_t* data, uint64_t bytes, EosHipMll** out, char** err);
+void eoship_mll_close(EosHipMll* mll);
+int eoship_mll_info(const EosHipMll* mll, EosHipMllInfo* info, char** err);
+/* Body of a section by its 4-character tag (XKBI is refused). The pointer
+ * stays valid while the package is open. mll.Reader.Section. */
+int eoship_mll_section(const EosHipMll* mll, const char* tag, const uint8_t** body,
+                       uint64_t* size, char** err);
+/* A tensor by name (name != NULL) or by TNSR index. */
+int eoship_mll_tensor(const EosHipMll* mll, int64_t index, const char* name,
+                      EosHipMllTensor* out, char** err);
+/* BLAKE3 (hash mode, 32-byte digest) of a buffer: the section digest. */
+int eoship_blake3(const uint8_t* data, uint64_t bytes, uint8_t* digest32, char** err);
+
+#define EOSHIP_PLAN_COMPACT_EMBEDDER 1
+
+typedef struct {
+  int32_t route;            /* EOSHIP_PLAN_* */
+  int32_t layers;           /* encoder layers in the plan */
+  int32_t distinct_layers;  /* distinct weight sets (tied layers share one) */
+  int32_t model_dim, heads, hidden_dim, vocab, max_sequence, output_dim;
+  int32_t batched;          /* 1: inputs [B, T]; 0: [T] */
+  int32_t steps;            /* plan steps of the entry that were matched */
+  EosHipCompactOptions options;  /* the plan's graph options (attend_padding: 1
+                                  * for softmaxRows, 0 for masked_softmax) */
+  char entry[64], token_input[64], mask_input[64], output_name[64];
+} EosHipMllPlan;
+
+/* Matches an entry's step list (NULL: the embedding_manifest's batch entry)
+ * against the family-(a) encoder graph by value flow and kernel op class:
+ * gather + dequant of the token table; per layer q/k/v = x W, kT, q kT
+ * (optionally scale rsqrt_rhs_rows), softmax or masked_softmax, p v, W_o,
+ * binary_add + layernorm, W_up, gelu, W_down, binary_add + layernorm; then
+ * normalize and mean_pool(mask) returned. Anything else is reported as "not
+ * handled" with the step. In the spirit of classifyCUDAKernel
+ * (runtime/backends/cuda/native_linux.go:3783-3803) over the plan that
+ * ExecuteSymbolic runs (runtime/backend/symbolic.go:17-172). */
+int eoship_mll_classify(const EosHipMll* mll, const char* entry, EosHipMllPlan* plan, char** err);
+
+/* Classifies the entry and binds its weights (int8 codes of packed Q8, Q4
+ * unpacked, per-tensor scales; tied layers share one device copy) to the
+ * fused compact encoder; run it with eoship_encoder_embed[_device] on
+ * tokens and mask [batch][tokens]. attend_padding: -1 takes the plan's own
+ * softmax semantics (the [B, T] entry run as given, padding included); 0
+ * attends each sequence's mask != 0 positions only (EmbeddingModel's batches,
+ * which group sequences by length, runtime/embedding_model.go:689-691).
+ * plan (optional) receives the classification with the options used. */
+int eoship_encoder_bind_mll(EosHipRuntime* rt, const EosHipMll* mll, const char* entry,
+                            int32_t attend_padding, EosHipEncoder** out, EosHipMllPlan* plan,
+                            char** err);
 
 #ifdef __cplusplus
 }

@@ -229,6 +229,9 @@ def _enc():
     lib.compact_embed.argtypes = [P, C.c_int, P, C.c_int, P, C.c_int, P, C.c_int, P, P, P,
                                   C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P]
     lib.compact_embed.restype = None
+    lib.compact_embed_opts.argtypes = [P, C.c_int, P, C.c_int, P, C.c_int, P, C.c_int, P, P, P,
+                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P]
+    lib.compact_embed_opts.restype = None
     lib.gelu_tanh_inplace.argtypes = [P, C.c_long]
     lib.gelu_tanh_inplace.restype = None
     lib._enc_ready = True
@@ -346,9 +349,15 @@ def compact_single_head_attention(q, k, v, mask):
     return out
 
 
-def compact_embed(tok, role, layers, ids, mask, role_ids, heads, wout=None):
-    """Family (a) embedder. tok [V][D], role [R][D] dequantized f32; layers: list
-    of (wq, wk, wv, wo, wup, wdown) in [in, out] layout; wout [D][O] or None."""
+COMPACT_NO_ROPE, COMPACT_UNSCALED, COMPACT_ATTEND_ALL = 1, 2, 4
+
+
+def compact_embed(tok, role, layers, ids, mask, role_ids, heads, wout=None, flags=0):
+    """Family (a) embedder. tok [V][D], role [R][D] dequantized f32 (None: no
+    role rows); layers: list of (wq, wk, wv, wo, wup, wdown) in [in, out]
+    layout; wout [D][O] or None. flags: COMPACT_NO_ROPE, COMPACT_UNSCALED (one
+    head's plain q kT), COMPACT_ATTEND_ALL (softmax over every position, the
+    mask only pools)."""
     lib = _enc()
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     mask = np.ascontiguousarray(mask, dtype=np.int32)
@@ -358,13 +367,16 @@ def compact_embed(tok, role, layers, ids, mask, role_ids, heads, wout=None):
     ffn = layers[0][4].shape[1] if layers else dim
     keep = [_f32(x) for L in layers for x in L]
     ptrs = (C.c_void_p * max(len(keep), 1))(*[k.ctypes.data for k in keep])
+    if role is None:
+        role = np.zeros((1, tok.shape[1]), np.float32)
+        roles = np.zeros_like(ids)
     tok, role = _f32(tok), _f32(role)
     wo = None if wout is None else _f32(wout)
     odim = dim if wo is None else wo.shape[1]
     out = np.zeros((batch, odim), np.float32)
-    lib.compact_embed(_p(tok), tok.shape[0], _p(role), role.shape[0], ptrs, len(layers),
-                      None if wo is None else _p(wo), odim, _p(ids), _p(roles), _p(mask), batch,
-                      tokens, dim, heads, ffn, _p(out))
+    lib.compact_embed_opts(_p(tok), tok.shape[0], _p(role), role.shape[0], ptrs, len(layers),
+                           None if wo is None else _p(wo), odim, _p(ids), _p(roles), _p(mask),
+                           batch, tokens, dim, heads, ffn, int(flags), _p(out))
     return out
 
 

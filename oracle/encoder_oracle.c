@@ -305,10 +305,14 @@ void gelu_tanh_inplace(float* x, long n) {
   for (long i = 0; i < n; ++i) x[i] = tanh_gelu(x[i]);
 }
 
-/* Single-head attention of the compact graph on [batch][tokens][dim]. */
-void compact_single_head_attention(const float* q, const float* k, const float* v,
-                                   const int32_t* mask, int batch, int tokens, int dim,
-                                   float* mixed) {
+/* Single-head attention of the compact graph on [batch][tokens][dim].
+ * scaled != 0: scores times float32(1/sqrt(dim)) (scaled_attention_scores);
+ * 0: the plain q kT matmul of a plan's matmul step. A mask of all ones gives
+ * softmaxRows (tensor_ops.go:1757-1788: f32 max over every column, f64 exp
+ * and sum, f32 probabilities times float32(1/sum)). */
+static void compact_single_head_attention_s(const float* q, const float* k, const float* v,
+                                            const int32_t* mask, int batch, int tokens, int dim,
+                                            int scaled, float* mixed) {
   const float scale = (float)(1.0 / sqrt((double)dim));
 #pragma omp parallel for schedule(dynamic, 8)
   for (long job = 0; job < (long)batch * tokens; ++job) {
@@ -320,7 +324,7 @@ void compact_single_head_attention(const float* q, const float* k, const float* 
       const float* kr = k + ((size_t)b * tokens + kt) * dim;
       float sum = 0.0f;
       for (int d = 0; d < dim; ++d) sum += qr[d] * kr[d];
-      p[kt] = sum * scale;
+      p[kt] = scaled ? sum * scale : sum;
     }
     float mx = -INFINITY;
     int any = 0;
@@ -358,16 +362,33 @@ void compact_single_head_attention(const float* q, const float* k, const float* 
   }
 }
 
+void compact_single_head_attention(const float* q, const float* k, const float* v,
+                                   const int32_t* mask, int batch, int tokens, int dim,
+                                   float* mixed) {
+  compact_single_head_attention_s(q, k, v, mask, batch, tokens, dim, 1, mixed);
+}
+
 /* tok [vocab][dim], role [nrole][dim] (dequantized); layer_w: 6 pointers per
  * layer, wq wk wv wo [dim][dim], wup [dim][ffn], wdown [ffn][dim], all
- * [in][out]; wout [dim][odim] or NULL. out: [batch][wout ? odim : dim]. */
-void compact_embed(const float* tok, int vocab, const float* role, int nrole,
-                   const float* const* layer_w, int layers, const float* wout, int odim,
-                   const int32_t* ids, const int32_t* role_ids, const int32_t* mask, int batch,
-                   int tokens, int dim, int heads, int ffn, float* out) {
+ * [in][out]; wout [dim][odim] or NULL. out: [batch][wout ? odim : dim].
+ * flags: 1 = no RoPE; 2 = one head's scores unscaled (a plan's plain q kT
+ * matmul); 4 = attention over every position of the padded input
+ * (softmaxRows), the mask selecting only the pooled rows. */
+void compact_embed_opts(const float* tok, int vocab, const float* role, int nrole,
+                        const float* const* layer_w, int layers, const float* wout, int odim,
+                        const int32_t* ids, const int32_t* role_ids, const int32_t* mask,
+                        int batch, int tokens, int dim, int heads, int ffn, int flags,
+                        float* out) {
   (void)vocab;
   (void)nrole;
   const int rows = batch * tokens;
+  int32_t* ones = NULL;
+  const int32_t* amask = mask;
+  if (flags & 4) {
+    ones = (int32_t*)malloc(sizeof(int32_t) * (size_t)rows);
+    for (int r = 0; r < rows; ++r) ones[r] = 1;
+    amask = ones;
+  }
   const size_t rd = (size_t)rows * dim;
   float* x = (float*)malloc(sizeof(float) * rd);
   float* q = (float*)malloc(sizeof(float) * rd);
@@ -381,16 +402,16 @@ void compact_embed(const float* tok, int vocab, const float* role, int nrole,
     const float* re = role + (size_t)(role_ids ? role_ids[r] : 0) * dim;
     for (int c = 0; c < dim; ++c) x[(size_t)r * dim + c] = te[c] + re[c];
   }
-  rope_rows(x, rows, tokens, dim);
+  if (!(flags & 1)) rope_rows(x, rows, tokens, dim);
   for (int l = 0; l < layers; ++l) {
     const float* const* w = layer_w + (size_t)l * 6;
     matmul_f32(x, rows, dim, w[0], dim, q);
     matmul_f32(x, rows, dim, w[1], dim, k);
     matmul_f32(x, rows, dim, w[2], dim, v);
     if (heads > 1)
-      bert_attention(q, k, v, mask, batch, tokens, dim, heads, mixed);
+      bert_attention(q, k, v, amask, batch, tokens, dim, heads, mixed);
     else
-      compact_single_head_attention(q, k, v, mask, batch, tokens, dim, mixed);
+      compact_single_head_attention_s(q, k, v, amask, batch, tokens, dim, !(flags & 2), mixed);
     matmul_f32(mixed, rows, dim, w[3], dim, t);
     for (size_t i = 0; i < rd; ++i) t[i] = t[i] + x[i];
     layer_norm_rows(t, rows, dim);
@@ -416,4 +437,13 @@ void compact_embed(const float* tok, int vocab, const float* role, int nrole,
   free(mixed);
   free(t);
   free(mid);
+  free(ones);
+}
+
+void compact_embed(const float* tok, int vocab, const float* role, int nrole,
+                   const float* const* layer_w, int layers, const float* wout, int odim,
+                   const int32_t* ids, const int32_t* role_ids, const int32_t* mask, int batch,
+                   int tokens, int dim, int heads, int ffn, float* out) {
+  compact_embed_opts(tok, vocab, role, nrole, layer_w, layers, wout, odim, ids, role_ids, mask,
+                     batch, tokens, dim, heads, ffn, 0, out);
 }

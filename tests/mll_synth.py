@@ -1,0 +1,157 @@
+"""Synthetic MLL packages for the reader and plan tests: the family-(a)
+encoder plan in the shape the reference's sealed export writes
+(artifact/eos/mll.go:112-330; the shipped default embedder's XMTA artifact),
+with seeded q8 weights, and variants of its step list."""
+from __future__ import annotations
+
+import copy
+import json
+
+import numpy as np
+
+from oracle import mll_oracle
+from oracle.blake3 import blake3
+
+
+def _kernel(name, op, attrs=None):
+    body = {"kind": "reduce", "name": "result", "op": op, "inputs": ["x"], "outputs": ["result"]}
+    if attrs:
+        body["attributes"] = attrs
+    return {"name": name, "body": [body, {"kind": "return", "op": "return", "outputs": ["result"]}]}
+
+
+def encoder_artifact(layers: list[dict], masked: bool = False, scale: str | None = None,
+                     batched: bool = True) -> dict:
+    """Plan of the embedding entry: layers is a list of parameter-name dicts
+    {q, k, v, o, up, down}; masked uses masked_softmax(scores, mask); scale
+    sets the score matmul's scale attribute."""
+    entry = "embed_batch" if batched else "embed"
+    shape = ["B", "T"] if batched else ["T"]
+    steps = []
+
+    def st(kind, name, ins, outs, kernel=None, attrs=None):
+        s = {"entry": entry, "kind": kind, "name": name, "inputs": ins, "outputs": outs}
+        if kernel:
+            s["kernel"] = kernel
+        if attrs:
+            s["attributes"] = attrs
+        steps.append(s)
+
+    st("gather", "gather", ["token_embedding", "tokens"], ["hidden_q"])
+    st("dequant", "dequant", ["hidden_q"], ["hidden"])
+    deq = {}
+    for L in layers:
+        for p in L.values():
+            if p not in deq:
+                deq[p] = p + "_f"
+                st("dequant", "dequant", [p], [deq[p]])
+    x = "hidden"
+    for i, L in enumerate(layers, 1):
+        st("matmul", "matmul", [x, deq[L["q"]]], [f"q{i}"])
+        st("matmul", "matmul", [x, deq[L["k"]]], [f"k{i}"])
+        st("matmul", "matmul", [x, deq[L["v"]]], [f"v{i}"])
+        st("transpose", "transpose", [f"k{i}"], [f"kt{i}"])
+        st("matmul", "matmul", [f"q{i}", f"kt{i}"], [f"scores{i}"],
+           attrs={"scale": scale} if scale else None)
+        if masked:
+            st("launch_kernel", "masked_softmax", [f"scores{i}", "attention_mask"], [f"probs{i}"],
+               kernel="masked_softmax")
+        else:
+            st("launch_kernel", "softmax", [f"scores{i}"], [f"probs{i}"], kernel="softmax")
+        st("matmul", "matmul", [f"probs{i}", f"v{i}"], [f"mixed{i}"])
+        st("matmul", "matmul", [f"mixed{i}", deq[L["o"]]], [f"attended{i}"])
+        st("launch_kernel", "binary_add", [f"attended{i}", x], [f"res{i}"], kernel="binary_add")
+        st("launch_kernel", "layernorm", [f"res{i}"], [f"attn_hidden{i}"], kernel="layernorm")
+        st("matmul", "matmul", [f"attn_hidden{i}", deq[L["up"]]], [f"ffn{i}"])
+        st("launch_kernel", "gelu", [f"ffn{i}"], [f"act{i}"], kernel="gelu")
+        st("matmul", "matmul", [f"act{i}", deq[L["down"]]], [f"proj{i}"])
+        st("launch_kernel", "binary_add", [f"proj{i}", f"attn_hidden{i}"], [f"res2_{i}"],
+           kernel="binary_add")
+        st("launch_kernel", "layernorm", [f"res2_{i}"], [f"encoded{i}"], kernel="layernorm")
+        x = f"encoded{i}"
+    st("launch_kernel", "normalize", [x], ["normalized"], kernel="normalize")
+    st("launch_kernel", "mean_pool", ["normalized", "attention_mask"], ["result"],
+       kernel="mean_pool")
+    steps.append({"entry": entry, "kind": "return", "outputs": ["result"]})
+    params = []
+    for name in ["token_embedding"] + sorted({p for L in layers for p in L.values()}):
+        params.append({"name": name, "type": {"kind": "tensor", "tensor": {"dtype": "q8"}},
+                       "binding": "weights/" + name})
+    tens = lambda shp: {"kind": "tensor", "tensor": {"dtype": "i32", "shape": shp}}
+    kernels = [_kernel("softmax", "softmax", {"axis": "-1"}), _kernel("binary_add", "binary_add",
+               {"operator": "+"}), _kernel("layernorm", "layernorm"), _kernel("gelu", "gelu"),
+               _kernel("normalize", "normalize"), _kernel("mean_pool", "mean_pool"),
+               _kernel("masked_softmax", "masked_softmax")]
+    return {
+        "version": "manta/v0alpha1", "name": "synthetic-embedder", "params": params,
+        "entry_points": [{"name": entry, "kind": "pipeline",
+                          "inputs": [{"name": "tokens", "type": tens(shape)},
+                                     {"name": "attention_mask", "type": tens(shape)}],
+                          "outputs": [{"name": "result", "type": tens(["D"])}]}],
+        "kernels": kernels, "steps": steps,
+    }
+
+
+def weights(vocab: int, dim: int, ffn: int, names: list[str], seed: int,
+            gain: float = 1.0) -> dict:
+    """Seeded int8 codes (about N(0, 40), clipped to +-127) and per-tensor
+    scales giving weights of std gain / sqrt(fan in): name -> (codes, scale).
+    Names starting with "up" are [dim, ffn], with "down" [ffn, dim], the
+    token table [vocab, dim], the rest [dim, dim]."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for n in names:
+        if n == "token_embedding":
+            shp, fan = (vocab, dim), 1.0
+        elif n.startswith("up"):
+            shp, fan = (dim, ffn), dim
+        elif n.startswith("down"):
+            shp, fan = (ffn, dim), ffn
+        else:
+            shp, fan = (dim, dim), dim
+        codes = np.clip(np.rint(rng.normal(0.0, 40.0, size=shp)), -127, 127).astype(np.int8)
+        scale = gain / np.sqrt(fan) / 40.0 * rng.uniform(0.8, 1.2)
+        out[n] = (codes, float(np.float32(scale)))
+    return out
+
+
+def package(artifact: dict, w: dict, extra_sections=(), bad_digest=None, scales=None,
+            max_sequence: int = 256, logical=None, payloads=None) -> bytes:
+    """A sealed-profile container: STRG, TNSR (w as Q8 payloads unless
+    payloads overrides name -> (dtype code, bytes)), XMTA, plus extra
+    (tag, body, flags) sections."""
+    names = list(w)
+    strings = [""] + names
+    entries = []
+    for n in names:
+        codes, _ = w[n]
+        dt, payload = (mll_oracle.DTYPE_Q8, codes.tobytes())
+        if payloads and n in payloads:
+            dt, payload = payloads[n]
+        entries.append((strings.index(n), dt, codes.shape, payload))
+    meta = {
+        "version": "manta/mll/v0alpha1", "module_name": artifact["name"],
+        "module_version": "manta/v0alpha1", "artifact": artifact,
+        "json_files": {"embedding_manifest": {
+            "batch_entry": artifact["entry_points"][0]["name"], "token_input": "tokens",
+            "mask_input": "attention_mask", "output_name": "result",
+            "tokenizer": {"vocab_size": int(w["token_embedding"][0].shape[0]),
+                          "max_sequence": max_sequence}}},
+        "logical_tensor_dtypes": logical if logical is not None else {n: "q8" for n in names},
+        "tensor_scales": scales if scales is not None else {n: w[n][1] for n in names},
+    }
+    secs = [("HEAD", b"\0" * 16, 1), ("STRG", mll_oracle.strg_body(strings), 1),
+            ("TNSR", mll_oracle.tnsr_body(entries), 0x11),
+            ("XMTA", json.dumps(meta).encode(), 0x22)]
+    secs += list(extra_sections)
+    return mll_oracle.write(secs, blake3, bad_digest=bad_digest)
+
+
+def dequantized(w: dict) -> dict:
+    return {n: c.astype(np.float32) * np.float32(s) for n, (c, s) in w.items()}
+
+
+def mutate(artifact: dict, fn) -> dict:
+    a = copy.deepcopy(artifact)
+    fn(a)
+    return a

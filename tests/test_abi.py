@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_abi_version():
-    assert _lib.load().eoship_abi_version() == 5
+    assert _lib.load().eoship_abi_version() == 6
 
 
 def test_runtime_create_without_gpu_fails_cleanly():
