@@ -148,6 +148,36 @@ class EosHipMllPlan(C.Structure):
     ]
 
 
+class EosHipScoreSpec(C.Structure):
+    _fields_ = [
+        ("op", C.c_int32),
+        ("k", C.c_int32),
+        ("docs_q4", C.c_int32),
+        ("docs_scale", C.c_float),
+        ("batched", C.c_int32),
+    ]
+
+
+class EosHipRetrievalPlan(C.Structure):
+    _fields_ = [
+        ("op", C.c_int32),
+        ("k", C.c_int32),
+        ("batched", C.c_int32),
+        ("docs_param", C.c_int32),
+        ("has_candidate_ids", C.c_int32),
+        ("docs_q4", C.c_int32),
+        ("docs_rows", C.c_int64),
+        ("dim", C.c_int32),
+        ("n_outputs", C.c_int32),
+        ("outputs", C.c_int32 * 8),
+        ("steps", C.c_int32),
+        ("entry", C.c_char * 64),
+        ("query_input", C.c_char * 64),
+        ("docs_input", C.c_char * 64),
+        ("ids_input", C.c_char * 64),
+    ]
+
+
 # name -> (argtypes) ; every function returns int except where noted
 _SIGNATURES = {
     "eoship_abi_version": ([], C.c_int),
@@ -260,6 +290,18 @@ _SIGNATURES = {
     "eoship_encoder_bind_mll": ([C.c_void_p, C.c_void_p, C.c_char_p, C.c_int32,
                                  C.POINTER(C.c_void_p), C.POINTER(EosHipMllPlan), C.c_void_p],
                                 C.c_int),
+    "eoship_score_topk_device": ([C.c_void_p, C.POINTER(EosHipScoreSpec), C.c_void_p, C.c_int32,
+                                  C.c_int32, C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p,
+                                  C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
+                                 C.c_int),
+    "eoship_mll_classify_retrieval": ([C.c_void_p, C.c_char_p, C.POINTER(EosHipRetrievalPlan),
+                                       C.c_void_p], C.c_int),
+    "eoship_retrieval_bind_mll": ([C.c_void_p, C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p),
+                                   C.POINTER(EosHipRetrievalPlan), C.c_void_p], C.c_int),
+    "eoship_retrieval_run_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                     C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p,
+                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_retrieval_release": ([C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_release": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_forward": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                 C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),

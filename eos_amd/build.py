@@ -31,6 +31,7 @@ ARCH = "gfx950"
 DEVICE_SOURCES = [
     ("tq", os.path.join(CSRC, "kernels", "tq_kernels.hip")),
     ("enc", os.path.join(CSRC, "kernels", "enc_kernels.hip")),
+    ("ret", os.path.join(CSRC, "kernels", "ret_kernels.hip")),
 ]
 # Host translation units that hold device variables (hipcc, host + device).
 HIP_HOST_SOURCES = [
@@ -42,6 +43,7 @@ HOST_SOURCES = [
     os.path.join(CSRC, "eoship_encoder.cpp"),
     os.path.join(CSRC, "eoship_embed.cpp"),
     os.path.join(CSRC, "eoship_mll.cpp"),
+    os.path.join(CSRC, "eoship_retrieval.cpp"),
 ]
 
 # Packed-FP32 instructions are disabled for every device build.

@@ -75,8 +75,30 @@ int tq_fp16_rerank_check(const Runtime* rt, const float* d_queries, int32_t q, i
                          const float* d_cand_scores, int32_t c, int64_t* d_ids, float* d_scores,
                          const char* what, char** err);
 
+// Row scores of a retrieval plan's score step, its topk and the gathers
+// (documents as f32 values or a packed q4 tensor, exactly one non-NULL).
+int score_topk_launch(Runtime* rt, const EosHipScoreSpec& s, const float* d_queries, int32_t q,
+                      int32_t d, const float* d_docs, const uint8_t* d_docs_q4, int64_t n,
+                      const int64_t* d_candidate_ids, float* d_scores, int32_t* d_top_index,
+                      int64_t* d_top_ids, float* d_top_scores, float* d_top_docs,
+                      const char* what, char** err);
+
 }  // namespace eoship
 
 struct EosHipRuntime : eoship::Runtime {};
+
+// A retrieval plan bound from a package: the score op and topk limit, and
+// the documents when the plan reads them from a param (uploaded at bind).
+struct EosHipRetrieval {
+  EosHipRuntime* rt = nullptr;
+  EosHipScoreSpec spec{};
+  bool docs_param = false;
+  bool has_ids = false;
+  int64_t rows = 0;
+  int dim = 0;
+  float* docs_f32 = nullptr;
+  uint8_t* docs_q4 = nullptr;
+  EosHipRetrievalPlan plan{};
+};
 
 #endif  // EOSHIP_INTERNAL_H

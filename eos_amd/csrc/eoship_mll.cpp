@@ -841,7 +841,11 @@ int classify(const EosHipMll* m, const char* entry_name, PlanResult* out, char**
     std::vector<Sym> v;
     for (const std::string& x : in) v.push_back(value(x));
     if (kind == "gather") {
-      if (v.size() != 2 || v[0].kind != Sym::kParam || v[1].kind != Sym::kTokens || !no_attrs)
+      // The compiler marks the [B, T] token gather mode "shared".
+      const bool shared = attrs != nullptr && attrs->kind == Json::kObj &&
+                          attrs->obj.size() == 1 && attrs->str_or("mode", "") == "shared";
+      if (v.size() != 2 || v[0].kind != Sym::kParam || v[1].kind != Sym::kTokens ||
+          !(no_attrs || shared))
         return plan_fail(err, entry, i, "gather of something other than (param, tokens)");
       o.kind = Sym::kEmbQ;
       o.a = v[0].a;
@@ -1080,6 +1084,180 @@ std::vector<int8_t> codes_of(const EosHipMll* m, const Tensor& t) {
   return c;
 }
 
+// Retrieval plans: score step, topk, gathers, pack_candidates, return.
+int classify_retrieval(const EosHipMll* m, const char* entry_name, EosHipRetrievalPlan* out,
+                       char** err) {
+  const char* what = "eoship_mll_classify_retrieval";
+  if (!m->has_meta) return set_err(err, "%s: the package has no XMTA metadata", what);
+  const Json& art = *m->meta.get("artifact");
+  const Json* eps = art.get("entry_points");
+  const Json* ep = nullptr;
+  std::string entry = entry_name != nullptr ? entry_name : "";
+  if (eps != nullptr && eps->kind == Json::kArr) {
+    if (entry.empty() && eps->arr.size() == 1) entry = eps->arr[0].str_or("name", "");
+    for (const Json& e : eps->arr)
+      if (e.str_or("name", "") == entry) ep = &e;
+  }
+  if (ep == nullptr) return set_err(err, "%s: unknown entrypoint \"%s\"", what, entry.c_str());
+  struct In {
+    std::string name, dtype;
+    size_t rank;
+  };
+  std::vector<In> inputs;
+  if (const Json* ins = ep->get("inputs"))
+    for (const Json& in : ins->arr) {
+      const Json* ty = in.get("type");
+      const Json* tt = ty != nullptr ? ty->get("tensor") : nullptr;
+      const Json* shape = tt != nullptr ? tt->get("shape") : nullptr;
+      inputs.push_back({in.str_or("name", ""), tt != nullptr ? tt->str_or("dtype", "") : "",
+                        shape != nullptr && shape->kind == Json::kArr ? shape->arr.size() : 0});
+    }
+  auto input = [&](const std::string& n) -> const In* {
+    for (const In& i : inputs)
+      if (i.name == n) return &i;
+    return nullptr;
+  };
+  auto is_param = [&](const std::string& n) {
+    const Json* ps = art.get("params");
+    if (ps == nullptr || ps->kind != Json::kArr) return false;
+    for (const Json& p : ps->arr)
+      if (p.str_or("name", "") == n) return true;
+    return false;
+  };
+  enum Kind { kNone, kQuery, kDocs, kIds, kScores, kIdx, kTopIds, kTopScores, kTopDocs, kPack };
+  std::vector<std::pair<std::string, int>> env;
+  auto kind_of = [&](const std::string& n) {
+    for (auto& kv : env)
+      if (kv.first == n) return kv.second;
+    return (int)kNone;
+  };
+  EosHipRetrievalPlan p{};
+  std::string query, docs, ids;
+  const Json* steps = art.get("steps");
+  if (steps == nullptr || steps->kind != Json::kArr)
+    return set_err(err, "%s: the artifact has no steps", what);
+  bool returned = false, have_score = false, packed = false;
+  int nsteps = 0;
+  auto fail = [&](size_t i, const std::string& msg) {
+    return set_err(err, "%s: entry \"%s\" not handled at step %zu: %s", what, entry.c_str(), i,
+                   msg.c_str());
+  };
+  for (size_t i = 0; i < steps->arr.size(); ++i) {
+    const Json& st = steps->arr[i];
+    if (st.str_or("entry", "") != entry) continue;
+    ++nsteps;
+    if (returned) return fail(i, "steps after return");
+    const std::string kind = st.str_or("kind", "");
+    std::vector<std::string> in, outn;
+    if (const Json* a = st.get("inputs"))
+      for (const Json& x : a->arr) in.push_back(x.str);
+    if (const Json* a = st.get("outputs"))
+      for (const Json& x : a->arr) outn.push_back(x.str);
+    const Json* attrs = st.get("attributes");
+    if (kind == "return") {
+      if (outn.empty() || outn.size() > 8) return fail(i, "return of no or too many values");
+      for (const std::string& o : outn) {
+        const int k = kind_of(o);
+        static const int kMap[] = {0, 0, 0, 0, EOSHIP_RET_SCORES, EOSHIP_RET_TOP_INDEX,
+                                   EOSHIP_RET_TOP_IDS, EOSHIP_RET_TOP_SCORES, EOSHIP_RET_TOP_DOCS,
+                                   EOSHIP_RET_PACK};
+        if (kMap[k] == 0) return fail(i, "return of \"" + o + "\", not a plan result");
+        p.outputs[p.n_outputs++] = kMap[k];
+      }
+      returned = true;
+      continue;
+    }
+    if (outn.size() != 1) return fail(i, kind + " step without one output");
+    int o = kNone;
+    if (kind == "launch_kernel") {
+      const std::string cls = kernel_op(art, st.str_or("kernel", ""), nullptr);
+      const int op = cls == "dot" ? EOSHIP_SCORE_DOT
+                     : cls == "cosine" ? EOSHIP_SCORE_COSINE
+                     : cls == "l2_distance" ? EOSHIP_SCORE_L2 : 0;
+      if (op == 0) return fail(i, "kernel op class \"" + cls + "\" not handled");
+      if (have_score) return fail(i, "a second score step");
+      if (in.size() != 2) return fail(i, "score step without (query, documents)");
+      const In* qi = input(in[0]);
+      if (qi == nullptr || (qi->rank != 1 && qi->rank != 2)) return fail(i, "query is not a [D] or [Q, D] input");
+      const In* di = input(in[1]);
+      const bool dparam = di == nullptr && is_param(in[1]);
+      if (!dparam && (di == nullptr || di->rank != qi->rank + 1))
+        return fail(i, "documents are not a [N, D] or [Q, N, D] input or param");
+      if (dparam && qi->rank != 1) return fail(i, "param documents with batched queries");
+      query = in[0];
+      docs = in[1];
+      p.op = op;
+      p.batched = qi->rank == 2 ? 1 : 0;
+      p.docs_param = dparam ? 1 : 0;
+      env.emplace_back(query, (int)kQuery);
+      env.emplace_back(docs, (int)kDocs);
+      have_score = true;
+      o = kScores;
+    } else if (kind == "topk") {
+      if (in.size() != 1 || kind_of(in[0]) != kScores) return fail(i, "topk of something other than the scores");
+      const std::string* kk = attrs != nullptr ? attrs->get_str("k") : nullptr;
+      char* end = nullptr;
+      const long k = kk != nullptr ? std::strtol(kk->c_str(), &end, 10) : 0;
+      if (kk == nullptr || end == kk->c_str() || *end != 0 || k <= 0 || k > 8192)
+        return fail(i, "topk limit missing or outside 1..8192");
+      if (p.k != 0) return fail(i, "a second topk");
+      p.k = (int32_t)k;
+      o = kIdx;
+    } else if (kind == "gather") {
+      if (in.size() != 2 || kind_of(in[1]) != kIdx) return fail(i, "gather not indexed by the topk");
+      if (attrs != nullptr && attrs->kind == Json::kObj && !attrs->obj.empty()) {
+        const std::string mode = attrs->str_or("mode", "");
+        if (attrs->obj.size() != 1 || mode != "batched" || !p.batched)
+          return fail(i, "gather attributes other than the batched mode of batched plans");
+      }
+      const int src = kind_of(in[0]);
+      if (src == kScores) {
+        o = kTopScores;
+      } else if (src == kDocs) {
+        o = kTopDocs;
+      } else if (src == kNone && input(in[0]) != nullptr && input(in[0])->dtype == "i64" &&
+                 (ids.empty() || ids == in[0])) {
+        ids = in[0];
+        env.emplace_back(ids, (int)kIds);
+        o = kTopIds;
+      } else {
+        return fail(i, "gather of \"" + in[0] + "\", not the scores, documents or i64 candidate ids");
+      }
+    } else if (kind == "pack_candidates") {
+      if (in.size() != 3 || kind_of(in[0]) != kTopIds || kind_of(in[1]) != kTopScores ||
+          kind_of(in[2]) != kTopDocs)
+        return fail(i, "pack_candidates of something other than (ids, scores, docs) at the topk");
+      packed = true;
+      o = kPack;
+    } else {
+      return fail(i, "step kind \"" + kind + "\" not handled");
+    }
+    env.emplace_back(outn[0], o);
+  }
+  (void)packed;
+  if (!returned) return set_err(err, "%s: entry \"%s\" has no return step", what, entry.c_str());
+  if (!have_score) return set_err(err, "%s: entry \"%s\" has no score step", what, entry.c_str());
+  p.has_candidate_ids = ids.empty() ? 0 : 1;
+  if (p.docs_param) {
+    const Tensor* t = m->tensor(docs);
+    if (t == nullptr || t->dims.size() != 2)
+      return set_err(err, "%s: document param \"%s\" has no [N, D] payload", what, docs.c_str());
+    if (t->kind != EOSHIP_MLL_Q4 && t->kind != EOSHIP_MLL_Q8 && t->kind != EOSHIP_MLL_F32)
+      return set_err(err, "%s: document param \"%s\" is not q4, q8 or f32", what, docs.c_str());
+    if (t->dims[1] > 4096) return set_err(err, "%s: documents wider than 4096", what);
+    p.docs_rows = t->dims[0];
+    p.dim = (int32_t)t->dims[1];
+    p.docs_q4 = t->kind == EOSHIP_MLL_Q4 ? 1 : 0;
+  }
+  p.steps = nsteps;
+  copy_name(p.entry, sizeof(p.entry), entry);
+  copy_name(p.query_input, sizeof(p.query_input), query);
+  copy_name(p.docs_input, sizeof(p.docs_input), docs);
+  copy_name(p.ids_input, sizeof(p.ids_input), ids);
+  *out = p;
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1223,6 +1401,73 @@ int eoship_encoder_bind_mll(EosHipRuntime* rt, const EosHipMll* m, const char* e
     *plan = r.plan;
     plan->options = opts;
   }
+  return 0;
+}
+
+int eoship_mll_classify_retrieval(const EosHipMll* m, const char* entry,
+                                  EosHipRetrievalPlan* plan, char** err) {
+  if (m == nullptr || plan == nullptr)
+    return set_err(err, "eoship_mll_classify_retrieval: NULL argument");
+  return classify_retrieval(m, entry, plan, err);
+}
+
+int eoship_retrieval_bind_mll(EosHipRuntime* rt, const EosHipMll* m, const char* entry,
+                              EosHipRetrieval** out, EosHipRetrievalPlan* plan, char** err) {
+  const char* what = "eoship_retrieval_bind_mll";
+  if (rt == nullptr || m == nullptr || out == nullptr) return set_err(err, "%s: NULL argument", what);
+  *out = nullptr;
+  EosHipRetrievalPlan p{};
+  if (classify_retrieval(m, entry, &p, err) != 0) return 1;
+  auto* r = new EosHipRetrieval();
+  r->rt = rt;
+  r->plan = p;
+  r->spec.op = p.op;
+  r->spec.k = p.k;
+  r->spec.batched = p.batched;
+  r->has_ids = p.has_candidate_ids != 0;
+  if (p.docs_param) {
+    const Tensor* t = m->tensor(p.docs_input);
+    r->docs_param = true;
+    r->rows = p.docs_rows;
+    r->dim = p.dim;
+    const uint8_t* b = m->bytes.data() + t->off;
+    void* dev = nullptr;
+    hipError_t e = hipSuccess;
+    if (t->kind == EOSHIP_MLL_Q4) {
+      // Packed nibbles stay packed; the kernels decode (nibble - 8) * scale.
+      r->spec.docs_q4 = 1;
+      r->spec.docs_scale = t->scale > 0.f ? t->scale : 0.f;
+      if (rt->alloc(t->size, &dev, err) != 0) {
+        delete r;
+        return 1;
+      }
+      r->docs_q4 = static_cast<uint8_t*>(dev);
+      e = hipMemcpy(dev, b, t->size, hipMemcpyHostToDevice);
+    } else {
+      // q8 codes dequantized as the reference decodes them (f32 code * scale).
+      std::vector<float> v((size_t)t->elements);
+      if (t->kind == EOSHIP_MLL_Q8) {
+        const float sc = t->scale > 0.f ? t->scale : 0.f;
+        for (size_t i = 0; i < v.size(); ++i) v[i] = (float)(int8_t)b[i] * sc;
+      } else {
+        std::memcpy(v.data(), b, v.size() * 4);
+      }
+      if (rt->alloc(v.size() * 4, &dev, err) != 0) {
+        delete r;
+        return 1;
+      }
+      r->docs_f32 = static_cast<float*>(dev);
+      e = hipMemcpy(dev, v.data(), v.size() * 4, hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+      if (r->docs_f32) (void)hipFree(r->docs_f32);
+      if (r->docs_q4) (void)hipFree(r->docs_q4);
+      delete r;
+      return eoship::hip_err(err, "hipMemcpy(retrieval documents)", e);
+    }
+  }
+  *out = r;
+  if (plan != nullptr) *plan = p;
   return 0;
 }
 

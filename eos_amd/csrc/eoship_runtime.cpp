@@ -25,6 +25,8 @@ extern const unsigned char eoship_tq_co_begin[];
 extern const unsigned char eoship_tq_co_end[];
 extern const unsigned char eoship_enc_co_begin[];
 extern const unsigned char eoship_enc_co_end[];
+extern const unsigned char eoship_ret_co_begin[];
+extern const unsigned char eoship_ret_co_end[];
 }
 
 namespace eoship {
@@ -201,8 +203,9 @@ int eoship_runtime_create(int device, EosHipRuntime** out, char** err) {
     delete rt;
     return hip_err(err, "hipStreamCreateWithFlags", e);
   }
-  const unsigned char* images[2][2] = {{eoship_tq_co_begin, eoship_tq_co_end},
-                                       {eoship_enc_co_begin, eoship_enc_co_end}};
+  const unsigned char* images[3][2] = {{eoship_tq_co_begin, eoship_tq_co_end},
+                                       {eoship_enc_co_begin, eoship_enc_co_end},
+                                       {eoship_ret_co_begin, eoship_ret_co_end}};
   for (auto& im : images) {
     hipModule_t m = nullptr;
     e = im[1] > im[0] ? hipModuleLoadData(&m, im[0]) : hipErrorInvalidImage;

@@ -571,6 +571,85 @@ int eoship_encoder_bind_mll(EosHipRuntime* rt, const EosHipMll* mll, const char*
                             int32_t attend_padding, EosHipEncoder** out, EosHipMllPlan* plan,
                             char** err);
 
+/* ------------------------------------------------------------------------
+ * Retrieval plans: a dot / cosine / l2_distance score step, topk and the
+ * gathers of candidate ids, scores and document rows (runtime/retrieval.go:
+ * 51-112; examples/retrieve.eos, candidates.eos, packed_candidates.eos).
+ * ------------------------------------------------------------------------ */
+
+#define EOSHIP_SCORE_DOT 1     /* dotRows, tensor_ops.go:1967-1997: f32 sum in c order */
+#define EOSHIP_SCORE_COSINE 2  /* cosineRows, :1999-2057: f64 dot and norms, f32 result */
+#define EOSHIP_SCORE_L2 3      /* l2DistanceRows, :2059-2089: f64 sum of f32 differences */
+
+typedef struct {
+  int32_t op;          /* EOSHIP_SCORE_* */
+  int32_t k;           /* topk limit (1 <= k <= min(n, 8192)); 0: scores only */
+  int32_t docs_q4;     /* 0: documents are f32 values; 1: a packed q4 tensor */
+  float docs_scale;    /* q4: value = (nibble - 8) * docs_scale */
+  int32_t batched;     /* 1: documents [q][n][d], candidate ids [q][n] (the [Q, D] x
+                        * [Q, N, D] score layout); 0: documents [n][d] and ids [n]
+                        * shared by every query */
+} EosHipScoreSpec;
+
+/* Scores of every (query, document row) into d_scores [q][n] (bit-identical
+ * to the host ops), then, with k > 0, the top k rows per query by score
+ * descending and row index ascending (topKTensor, tensor_ops.go:2124-2193)
+ * and its gathers: d_top_index [q][k] (i32 row indices, as topk returns),
+ * d_top_ids [q][k] (candidate ids gathered at those rows; the row index when
+ * d_candidate_ids is NULL), d_top_scores [q][k], d_top_docs [q][k][d]
+ * (document values as f32). Any top output may be NULL. Queries are f32
+ * [q][d] (d <= 4096); k > n is refused as the reference refuses it. Uses
+ * the runtime workspace (q * k * 12 bytes). Enqueued on the runtime stream. */
+int eoship_score_topk_device(EosHipRuntime* rt, const EosHipScoreSpec* spec,
+                             const float* d_queries, int32_t q, int32_t d, const void* d_docs,
+                             int64_t n, const int64_t* d_candidate_ids, float* d_scores,
+                             int32_t* d_top_index, int64_t* d_top_ids, float* d_top_scores,
+                             float* d_top_docs, char** err);
+
+/* Plan outputs, in the entry's return order. */
+#define EOSHIP_RET_SCORES 1      /* [n] / [Q, n] scores */
+#define EOSHIP_RET_TOP_INDEX 2   /* topk indices (i32) */
+#define EOSHIP_RET_TOP_IDS 3     /* gather(candidate_ids, topk) (i64) */
+#define EOSHIP_RET_TOP_SCORES 4  /* gather(scores, topk) */
+#define EOSHIP_RET_TOP_DOCS 5    /* gather(docs, topk) */
+#define EOSHIP_RET_PACK 6        /* pack_candidates(ids, scores, docs) */
+
+typedef struct EosHipRetrieval EosHipRetrieval;
+
+typedef struct {
+  int32_t op;               /* EOSHIP_SCORE_* */
+  int32_t k;                /* topk limit, 0 when the plan has no topk */
+  int32_t batched;          /* 1: queries [Q, D], documents [Q, N, D] */
+  int32_t docs_param;       /* 1: documents are a param bound from the package */
+  int32_t has_candidate_ids;
+  int32_t docs_q4;          /* param documents stored as packed q4 */
+  int64_t docs_rows;        /* param documents: N */
+  int32_t dim;              /* param documents: D (0 when documents are an input) */
+  int32_t n_outputs;
+  int32_t outputs[8];       /* EOSHIP_RET_* in return order */
+  int32_t steps;
+  char entry[64], query_input[64], docs_input[64], ids_input[64];
+} EosHipRetrievalPlan;
+
+/* Matches an entry's steps: launch_kernel of op class dot / cosine /
+ * l2_distance on (query, documents), optionally topk(k) and gathers of the
+ * candidate ids, the scores and the documents at the topk indices, an
+ * optional pack_candidates, and the return. Anything else is "not handled". */
+int eoship_mll_classify_retrieval(const EosHipMll* mll, const char* entry,
+                                  EosHipRetrievalPlan* plan, char** err);
+/* Classifies the entry and uploads param documents (packed q4 stays packed). */
+int eoship_retrieval_bind_mll(EosHipRuntime* rt, const EosHipMll* mll, const char* entry,
+                              EosHipRetrieval** out, EosHipRetrievalPlan* plan, char** err);
+/* Runs a bound retrieval plan (see eoship_score_topk_device for the
+ * buffers); d_docs are f32 document values, NULL when the plan binds them
+ * (n and the width then come from the package). */
+int eoship_retrieval_run_device(EosHipRuntime* rt, EosHipRetrieval* ret, const float* d_queries,
+                                int32_t q, int32_t d, const float* d_docs, int64_t n,
+                                const int64_t* d_candidate_ids, float* d_scores,
+                                int32_t* d_top_index, int64_t* d_top_ids, float* d_top_scores,
+                                float* d_top_docs, char** err);
+int eoship_retrieval_release(EosHipRuntime* rt, EosHipRetrieval* ret, char** err);
+
 #ifdef __cplusplus
 }
 #endif

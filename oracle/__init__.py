@@ -142,6 +142,24 @@ def topk_scores(scores: np.ndarray, k: int):
     return ids, out
 
 
+SCORE_OPS = {"dot": 1, "cosine": 2, "l2_distance": 3}
+
+
+def score_rows(op, query, docs) -> np.ndarray:
+    """dotRows / cosineRows / l2DistanceRows of one query [D] against docs
+    [N, D] (retrieval_oracle.c), f32 [N]."""
+    lib = load()
+    fn = lib.ret_score_rows
+    fn.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_void_p]
+    fn.restype = None
+    q, x = _f32(query), _f32(docs)
+    n, d = x.shape
+    assert q.shape == (d,)
+    out = np.zeros(n, np.float32)
+    fn(SCORE_OPS[op] if isinstance(op, str) else int(op), _p(q), _p(x), n, d, _p(out))
+    return out
+
+
 def tq_maxsim_scores(queries, rotation, dim, bits, codebook, codebook_scale, codes, norms,
                      doc_len):
     """queries [Q, tokens, dim] -> doc scores [Q, ndocs]."""

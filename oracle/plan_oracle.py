@@ -26,6 +26,15 @@ and binds its outputs. The host ops, in the reference's precisions:
                f32 norm, rows of norm 0 unchanged
   mean_pool    meanPoolMaskedTensor (tensor_ops.go:1644-1709): f32 sum of the
                mask != 0 rows times float32(1 / count), count 0 -> zeros
+  dot, cosine, l2_distance   dotRows / cosineRows / l2DistanceRows
+               (tensor_ops.go:1967-2122) through the C restatement
+               (retrieval_oracle.c), per query for the [Q, D] x [Q, N, D] form
+  topk         topKTensor (tensor_ops.go:2124-2193): score descending, index
+               ascending; k above the row width is an error
+  gather       modes "batched" (per-row table) and "shared" as the compiler
+               marks them (compiler/compiler.go:1872-1900)
+  pack_candidates   NewCandidatePack (runtime/backend/tensor.go:105-118): the
+               (ids, scores, docs) triple
 
 One difference in summation order: matmul sums in f64 and rounds once to
 f32 where the reference runs an f32 sum in k order (relative difference
@@ -34,6 +43,8 @@ below k * 2^-24), and the f32 reductions use numpy's pairwise order.
 from __future__ import annotations
 
 import numpy as np
+
+import oracle
 
 F32 = np.float32
 
@@ -133,9 +144,27 @@ def run(artifact: dict, params: dict[str, np.ndarray], entry: str,
         if kind == "gather":
             table, idx = ins
             idx = np.asarray(idx)
-            if idx.min() < 0 or idx.max() >= table.shape[0]:
-                raise IndexError("gather index out of range")
-            y = table[idx].astype(F32)
+            mode = (st.get("attributes") or {}).get("mode", "")
+            if mode == "batched":
+                if idx.min() < 0 or idx.max() >= table.shape[1]:
+                    raise IndexError("gather index out of range")
+                y = np.stack([table[b][idx[b]] for b in range(idx.shape[0])])
+            else:
+                if idx.min() < 0 or idx.max() >= table.shape[0]:
+                    raise IndexError("gather index out of range")
+                y = table[idx]
+            if y.dtype not in (np.int32, np.int64):
+                y = y.astype(F32)
+        elif kind == "topk":
+            k = int(st["attributes"]["k"])
+            s2 = np.atleast_2d(ins[0])
+            if k <= 0 or k > s2.shape[1]:
+                raise ValueError(f"topk limit {k} out of range for row width {s2.shape[1]}")
+            y = np.stack([oracle.topk_scores(row, k)[0] for row in s2]).astype(np.int32)
+            if ins[0].ndim == 1:
+                y = y[0]
+        elif kind == "pack_candidates":
+            y = tuple(ins)
         elif kind == "dequant":
             y = ins[0].astype(F32)
         elif kind == "matmul":
@@ -159,6 +188,12 @@ def run(artifact: dict, params: dict[str, np.ndarray], entry: str,
                 y = _normalize_rows(ins[0])
             elif op == "mean_pool":
                 y = _mean_pool(ins[0], ins[1])
+            elif op in ("dot", "cosine", "l2_distance"):
+                q, docs = ins
+                if q.ndim == 1:
+                    y = oracle.score_rows(op, q, docs)
+                else:
+                    y = np.stack([oracle.score_rows(op, q[b], docs[b]) for b in range(q.shape[0])])
             else:
                 raise ValueError(f"kernel op {op} not in this interpreter")
         else:

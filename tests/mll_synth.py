@@ -155,3 +155,90 @@ def mutate(artifact: dict, fn) -> dict:
     a = copy.deepcopy(artifact)
     fn(a)
     return a
+
+
+def retrieval_artifact(form: str, op: str = "cosine", k: int = 2) -> dict:
+    """The plans the reference's compiler emits for examples/*.eos
+    (compiler/compiler.go:1767-1960): a launch_kernel of the score op class,
+    topk with its k attribute, gathers (mode "batched" for the [Q, ...]
+    forms), pack_candidates. form: score, select, rerank, retrieve
+    (documents are the param "docs"), candidates, packed, batch (documents
+    and candidate ids are inputs)."""
+    entry = form
+    batched = form == "batch"
+    steps = []
+
+    def st(kind, name, ins, outs, kernel=None, attrs=None):
+        s = {"entry": entry, "kind": kind, "name": name, "inputs": ins, "outputs": outs}
+        if kernel:
+            s["kernel"] = kernel
+        if attrs:
+            s["attributes"] = attrs
+        steps.append(s)
+
+    tens = lambda dt, shp: {"kind": "tensor", "tensor": {"dtype": dt, "shape": shp}}
+    inputs = [{"name": "query", "type": tens("f16", ["Q", "D"] if batched else ["D"])}]
+    params = []
+    if form in ("score", "select", "rerank", "retrieve"):
+        params.append({"name": "docs", "type": tens("q4", ["N", "D"]), "binding": "weights/docs"})
+    else:
+        inputs.append({"name": "docs", "type": tens("q4", ["Q", "N", "D"] if batched else ["N", "D"])})
+        inputs.append({"name": "candidate_ids", "type": tens("i64", ["Q", "N"] if batched else ["N"])})
+    gm = {"mode": "batched"} if batched else None
+    st("launch_kernel", op, ["query", "docs"], ["scores"], kernel=op)
+    rets = []
+    if form == "score":
+        rets = ["scores"]
+    else:
+        st("topk", "topk", ["scores"], ["top"], attrs={"k": str(k)})
+        if form == "select":
+            st("gather", "gather", ["scores", "top"], ["sel"], attrs=gm)
+            rets = ["sel"]
+        elif form in ("rerank", "retrieve"):
+            st("gather", "gather", ["scores", "top"], ["top_scores"])
+            rets = ["top", "top_scores"]
+            if form == "retrieve":
+                st("gather", "gather", ["docs", "top"], ["top_docs"])
+                rets.append("top_docs")
+        else:
+            st("gather", "gather", ["candidate_ids", "top"], ["top_candidate_ids"], attrs=gm)
+            st("gather", "gather", ["scores", "top"], ["top_scores"], attrs=gm)
+            st("gather", "gather", ["docs", "top"], ["top_docs"], attrs=gm)
+            if form == "packed":
+                st("pack_candidates", "pack_candidates",
+                   ["top_candidate_ids", "top_scores", "top_docs"], ["pack"])
+                rets = ["pack"]
+            else:
+                rets = ["top_candidate_ids", "top_scores", "top_docs"]
+    steps.append({"entry": entry, "kind": "return", "outputs": rets})
+    kernels = [{"name": op, "body": [{"kind": "reduce", "name": "result", "op": op,
+                                      "inputs": ["query", "docs"], "outputs": ["result"]},
+                                     {"kind": "return", "op": "return", "outputs": ["result"]}]}]
+    return {"version": "manta/v0alpha1", "name": f"retrieval-{form}", "params": params,
+            "entry_points": [{"name": entry, "kind": "pipeline", "inputs": inputs,
+                              "outputs": [{"name": r, "type": tens("f32", ["K"])} for r in rets]}],
+            "kernels": kernels, "steps": steps}
+
+
+def retrieval_package(artifact: dict, docs_codes: np.ndarray | None = None,
+                      docs_scale: float = 0.0) -> bytes:
+    """A sealed-profile container for a retrieval artifact; docs_codes
+    (int8 in -8..7, [N, D]) become the q4 param "docs" packed low nibble
+    first."""
+    strings, entries, scales, logical = [""], [], {}, {}
+    if docs_codes is not None:
+        flat = (docs_codes.reshape(-1).astype(np.int16) + 8).astype(np.uint8)
+        if flat.size % 2:
+            flat = np.concatenate([flat, np.array([8], np.uint8)])
+        packed = (flat[0::2] | (flat[1::2] << 4)).astype(np.uint8).tobytes()
+        strings.append("docs")
+        entries.append((1, 12, docs_codes.shape, packed))
+        scales["docs"] = docs_scale
+        logical["docs"] = "q4"
+    meta = {"version": "manta/mll/v0alpha1", "module_name": artifact["name"],
+            "module_version": "manta/v0alpha1", "artifact": artifact,
+            "logical_tensor_dtypes": logical, "tensor_scales": scales}
+    secs = [("HEAD", b"\0" * 16, 1), ("STRG", mll_oracle.strg_body(strings), 1),
+            ("TNSR", mll_oracle.tnsr_body(entries), 0x11),
+            ("XMTA", json.dumps(meta).encode(), 0x22)]
+    return mll_oracle.write(secs, blake3)

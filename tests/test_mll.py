@@ -276,3 +276,40 @@ def test_plan_interpreter_masked_scaled_variant():
     want = oracle.compact_embed(params["token_embedding"], None, layers, ids, mask, None, 1,
                                 flags=oracle.COMPACT_NO_ROPE)
     np.testing.assert_allclose(got, want, rtol=0, atol=2e-6)
+
+
+def test_retrieval_classifier_forms():
+    """The retrieval plans of examples/*.eos as the compiler emits them: each
+    form maps to its op, k, document source and output list."""
+    rng = np.random.default_rng(0)
+    codes = rng.integers(-8, 8, (50, 20)).astype(np.int8)
+    want = {"score": (0, True, ["scores"]), "select": (3, True, ["top_scores"]),
+            "rerank": (3, True, ["top_index", "top_scores"]),
+            "retrieve": (3, True, ["top_index", "top_scores", "top_docs"]),
+            "candidates": (3, False, ["top_ids", "top_scores", "top_docs"]),
+            "packed": (3, False, ["pack"]), "batch": (3, False, ["top_ids", "top_scores",
+                                                                "top_docs"])}
+    from eos_amd.retrieval import plan_dict
+    for form, (k, param, outs) in want.items():
+        art = mll_synth.retrieval_artifact(form, "dot", 3)
+        data = mll_synth.retrieval_package(art, codes if param else None, 0.05)
+        with MllPackage(data) as m:
+            p = _lib.EosHipRetrievalPlan()
+            _lib.call("eoship_mll_classify_retrieval", m.handle, None, C.byref(p))
+            d = plan_dict(p)
+            assert (d["op"], d["k"], d["docs_param"], d["outputs"]) == ("dot", k, param, outs), form
+            assert d["batched"] == (form == "batch")
+            if param:
+                assert (d["docs_rows"], d["dim"], d["docs_q4"]) == (50, 20, True)
+            # The encoder classifier refuses a retrieval plan.
+            with pytest.raises(EosHipError, match="not handled|no complete|inputs"):
+                m.classify(form)
+    bad = mll_synth.mutate(mll_synth.retrieval_artifact("candidates"),
+                           lambda a: a["steps"].insert(1, {"entry": "candidates", "kind": "topk",
+                                                          "name": "topk", "inputs": ["scores"],
+                                                          "outputs": ["t2"],
+                                                          "attributes": {"k": "0"}}))
+    with MllPackage(mll_synth.retrieval_package(bad)) as m:
+        with pytest.raises(EosHipError, match="topk limit"):
+            _lib.call("eoship_mll_classify_retrieval", m.handle, None,
+                      C.byref(_lib.EosHipRetrievalPlan()))
