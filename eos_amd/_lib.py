@@ -178,6 +178,18 @@ class EosHipRetrievalPlan(C.Structure):
     ]
 
 
+class EosHipTQCodes(C.Structure):
+    _fields_ = [
+        ("bits", C.c_int32),
+        ("dim", C.c_int32),
+        ("n", C.c_int64),
+        ("codes", C.c_void_p),
+        ("norms", C.c_void_p),
+        ("codebook", C.c_void_p),
+        ("rotation_t", C.c_void_p),
+    ]
+
+
 # name -> (argtypes) ; every function returns int except where noted
 _SIGNATURES = {
     "eoship_abi_version": ([], C.c_int),
@@ -302,6 +314,13 @@ _SIGNATURES = {
                                      C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p,
                                      C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_retrieval_release": ([C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_dense_rerank_device": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
+                                       C.c_int64, C.c_void_p, C.c_int32, C.c_int32, C.c_void_p,
+                                       C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_reconstruct_rerank_device": ([C.c_void_p, C.POINTER(EosHipTQCodes), C.c_void_p,
+                                             C.c_int32, C.c_void_p, C.c_int32, C.c_int32,
+                                             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
+                                            C.c_int),
     "eoship_encoder_release": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_forward": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                 C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),

@@ -1457,6 +1457,7 @@ int tq_fp16_rerank_launch(Runtime* rt, const float* d_queries, int32_t q, int32_
   a.c = c;
   a.kk = (k <= 0 || k > c) ? c : k;
   a.id_rank = reinterpret_cast<const long long*>(d_id_rank);
+  a.vec = (d % 8 == 0 && (reinterpret_cast<uintptr_t>(d_rows) & 15) == 0) ? 1 : 0;
   // shouldApplyTurboQuantFP16RerankRescue (runtime/retrieval_turboquant.go:1664-1669).
   a.rescue = (bit_width == 4 && k == 100 && overfetch == 200 && c >= 120) ? 1 : 0;
   if (rt->launch("eos_tq_rr_dots", dim3((unsigned)((c + 63) / 64), (unsigned)q), dim3(64), 0, &a,
@@ -1465,9 +1466,116 @@ int tq_fp16_rerank_launch(Runtime* rt, const float* d_queries, int32_t q, int32_
   return rt->launch("eos_tq_rr_sort", dim3((unsigned)q), dim3(256), 0, &a, err, "tq_fp16_rerank_sort");
 }
 
+// Shared checks of the dense and reconstruct reranks.
+static int rerank_sizes_check(const Runtime* rt, const float* d_queries, int32_t q, int32_t d,
+                              int64_t n, const int64_t* d_cand_ids, int32_t c, int64_t* d_ids,
+                              float* d_scores, const char* what, char** err) {
+  if (rt == nullptr) return set_err(err, "%s: NULL runtime", what);
+  if (q < 0 || c < 0 || n < 0) return set_err(err, "%s: negative size", what);
+  if (d < 1 || d > 4096) return set_err(err, "%s: dim must be in [1, 4096]", what);
+  if (c > 4096)
+    return set_err(err, "%s: at most 4096 candidates per query (got %d; the reference takes any overfetch)",
+                   what, c);
+  if (q > 65535) return set_err(err, "%s: at most 65535 queries per call", what);
+  if (n >= ((int64_t)1 << 32) - 1)
+    return set_err(err, "%s: corpus must hold fewer than 2^32 - 1 rows", what);
+  if (q == 0 || c == 0) return 0;
+  if (d_queries == nullptr || d_cand_ids == nullptr || d_ids == nullptr || d_scores == nullptr)
+    return set_err(err, "%s: NULL buffer", what);
+  return 0;
+}
+
 }  // namespace eoship
 
 extern "C" {
+
+int eoship_tq_dense_rerank_device(EosHipRuntime* rt, const float* d_queries, int32_t q, int32_t d,
+                                  const float* d_rows, int64_t n, const int64_t* d_cand_ids,
+                                  int32_t c, int32_t k, const int64_t* d_id_rank, int64_t* d_ids,
+                                  float* d_scores, char** err) {
+  const char* what = "eoship_tq_dense_rerank_device";
+  if (eoship::rerank_sizes_check(rt, d_queries, q, d, n, d_cand_ids, c, d_ids, d_scores, what,
+                                 err) != 0)
+    return 1;
+  if (q == 0 || c == 0) return 0;
+  if (d_rows == nullptr) return set_err(err, "%s: NULL rows", what);
+  void* ws = nullptr;
+  if (rt->workspace((size_t)q * (size_t)c * sizeof(float), &ws, err) != 0) return 1;
+  TqRerankArgs a;
+  memset(&a, 0, sizeof(a));
+  a.queries = d_queries;
+  a.rows_f32 = d_rows;
+  a.cand_ids = reinterpret_cast<const long long*>(d_cand_ids);
+  a.out_ids = reinterpret_cast<long long*>(d_ids);
+  a.out_scores = d_scores;
+  a.dots = static_cast<float*>(ws);
+  a.n = n;
+  a.d = d;
+  a.c = c;
+  a.kk = (k <= 0 || k > c) ? c : k;
+  a.id_rank = reinterpret_cast<const long long*>(d_id_rank);
+  a.vec = (d % 4 == 0 && (reinterpret_cast<uintptr_t>(d_rows) & 15) == 0) ? 1 : 0;
+  if (rt->launch("eos_tq_rr_dots_f32", dim3((unsigned)((c + 63) / 64), (unsigned)q), dim3(64), 0,
+                 &a, err, "tq_dense_rerank_dots") != 0)
+    return 1;
+  return rt->launch("eos_tq_rr_sort", dim3((unsigned)q), dim3(256), 0, &a, err,
+                    "tq_dense_rerank_sort");
+}
+
+int eoship_tq_reconstruct_rerank_device(EosHipRuntime* rt, const EosHipTQCodes* codes,
+                                        const float* d_queries, int32_t q,
+                                        const int64_t* d_cand_ids, int32_t c, int32_t k,
+                                        const int64_t* d_id_rank, int64_t* d_ids,
+                                        float* d_scores, char** err) {
+  const char* what = "eoship_tq_reconstruct_rerank_device";
+  if (codes == nullptr) return set_err(err, "%s: NULL codes", what);
+  const int d = codes->dim, bits = codes->bits;
+  if (bits != 1 && bits != 2 && bits != 4 && bits != 8)
+    return set_err(err, "%s: bits must be 1, 2, 4 or 8 (got %d)", what, bits);
+  if (eoship::rerank_sizes_check(rt, d_queries, q, d, codes->n, d_cand_ids, c, d_ids, d_scores,
+                                 what, err) != 0)
+    return 1;
+  if (q == 0 || c == 0) return 0;
+  if (codes->codes == nullptr || codes->norms == nullptr || codes->codebook == nullptr)
+    return set_err(err, "%s: NULL codes, norms or codebook", what);
+  // Rotated queries (f64) and the f32 scores share one workspace block.
+  const size_t rq_bytes = (size_t)q * (size_t)d * sizeof(double);
+  void* ws = nullptr;
+  if (rt->workspace(rq_bytes + (size_t)q * (size_t)c * sizeof(float), &ws, err) != 0) return 1;
+  TqReconArgs r;
+  memset(&r, 0, sizeof(r));
+  r.queries = d_queries;
+  r.rot_t = codes->rotation_t;
+  r.rq = static_cast<double*>(ws);
+  r.codes = codes->codes;
+  r.norms = codes->norms;
+  r.codebook = codes->codebook;
+  r.cand_ids = reinterpret_cast<const long long*>(d_cand_ids);
+  r.dots = reinterpret_cast<float*>(static_cast<char*>(ws) + rq_bytes);
+  r.n = codes->n;
+  r.d = d;
+  r.c = c;
+  r.bits = bits;
+  r.row_bytes = (d * bits + 7) / 8;
+  if (rt->launch("eos_tq_rr_rotate", dim3((unsigned)q), dim3(256), 0, &r, err,
+                 "tq_reconstruct_rotate") != 0 ||
+      rt->launch("eos_tq_rr_dots_recon", dim3((unsigned)((c + 63) / 64), (unsigned)q), dim3(64),
+                 0, &r, err, "tq_reconstruct_dots") != 0)
+    return 1;
+  TqRerankArgs a;
+  memset(&a, 0, sizeof(a));
+  a.cand_ids = r.cand_ids;
+  a.out_ids = reinterpret_cast<long long*>(d_ids);
+  a.out_scores = d_scores;
+  a.dots = r.dots;
+  a.n = codes->n;
+  a.d = d;
+  a.c = c;
+  a.kk = (k <= 0 || k > c) ? c : k;
+  a.id_rank = reinterpret_cast<const long long*>(d_id_rank);
+  return rt->launch("eos_tq_rr_sort", dim3((unsigned)q), dim3(256), 0, &a, err,
+                    "tq_reconstruct_sort");
+}
 
 int eoship_f16_sidecar_device(EosHipRuntime* rt, const float* d_x, int64_t count, uint16_t* d_half,
                               char** err) {

@@ -188,6 +188,23 @@ struct TqRerankArgs {
   // Optional [n]: the order of id's string ID among the corpus IDs; equal
   // rerank scores then rank by it instead of by the integer id.
   const long long* id_rank;
+  const float* rows_f32;         // [n][d] f32 rows (dense rerank) instead of rows
+  int vec;                       // rows allow whole 16-byte loads (d % 8 or 4, aligned)
+};
+
+// Reconstruct rerank: candidates' codes (reference row layout) against the
+// rotated query; writes the f32 scores into dots for eos_tq_rr_sort.
+struct TqReconArgs {
+  const float* queries;          // [q][d]
+  const float* rot_t;            // [d][d], rot_t[k*d + j] = R[j][k]; NULL = identity
+  double* rq;                    // [q][d] rotated queries (eos_tq_rr_rotate)
+  const unsigned char* codes;    // [n][row_bytes]
+  const float* norms;            // [n]
+  const float* codebook;         // [2^bits] f32 centroid values
+  const long long* cand_ids;     // [q][c]
+  float* dots;                   // [q][c]
+  long long n;
+  int d, c, bits, row_bytes;
 };
 
 #endif  // EOSHIP_TQ_ARGS_H

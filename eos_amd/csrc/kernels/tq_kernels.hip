@@ -18,6 +18,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "tq_args.h"
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -1683,63 +1685,144 @@ __device__ inline unsigned rr_desc(float s) {
   return ~u;
 }
 
-// One candidate's score: scoreValue += query[i] * halfToFloat32(half) in
-// order, each product and sum rounded to f32 (no fused multiply-add), as
-// topFP16RerankScores computes it (runtime/retrieval_turboquant.go:1646-1649).
+// First rerank kernels, one wavefront per 64 candidates of a query (grid:
+// candidate blocks x queries). The candidates' rows are staged through LDS
+// 128 columns at a time with coalesced 16-byte loads (consecutive lanes read
+// consecutive bytes of one row), then each lane sums its own candidate in
+// index order, each product and sum rounded to f32 (no fused multiply-add):
+//   f16 rows   scoreValue += query[i] * halfToFloat32(half)
+//              (topFP16RerankScores, runtime/retrieval_turboquant.go:1646-1649)
+//   f32 rows   sum += a[i] * b[i] (dotRetrievalVectors, runtime/retrieval_eval.go:
+//              1189-1199, as topDenseRerankScores calls it, :1610-1633)
 // halfToFloat32 is exact for every finite half and for the infinities, where
 // it equals the hardware conversion; a NaN row element gives a NaN score
-// either way (NaN payloads are outside the ranking contract).
-__device__ inline float rr_dot(const float* qv, const unsigned short* row, int d) {
+// either way (NaN payloads are outside the ranking contract). The f32 score
+// of candidate j of query qi goes to a.dots[qi * c + j]; candidates whose id
+// is outside [0, n) have no row and are left unscored (the sort kernel skips
+// them).
+constexpr int kRrCand = 64;
+constexpr int kRrChunk = 128;
+
+template <bool F32>
+EOS_DEV void rr_dots_staged(const TqRerankArgs& a) {
 #pragma clang fp contract(off)
+  using Elem = typename std::conditional<F32, float, unsigned short>::type;
+  constexpr int EPV = 16 / (int)sizeof(Elem);  // elements per 16-byte load
+  constexpr int LD = kRrChunk + EPV;           // row pitch in LDS (one 16-byte pad)
+  constexpr int CPR = kRrChunk / EPV;          // 16-byte loads per staged row
+  __shared__ float qv[kRrMaxDim];
+  __shared__ __attribute__((aligned(16))) Elem tile[kRrCand * LD];
+  typedef unsigned v4u __attribute__((ext_vector_type(4)));
+  const int qi = blockIdx.y, lane = threadIdx.x;
+  const int j = blockIdx.x * kRrCand + lane;
+  for (int i = lane; i < a.d; i += kRrCand) qv[i] = a.queries[(size_t)qi * a.d + i];
+  const long long myid = j < a.c ? a.cand_ids[(size_t)qi * a.c + j] : -1ll;
+  const bool valid = myid >= 0 && myid < a.n;
+  const Elem* rows = F32 ? reinterpret_cast<const Elem*>(a.rows_f32)
+                         : reinterpret_cast<const Elem*>(a.rows);
   float s = 0.0f;
-  int i = 0;
-  if ((d & 7) == 0) {
-    // 16 row loads in flight per chunk; the sum still runs in index order.
-    typedef unsigned v4u __attribute__((ext_vector_type(4)));
-    const v4u* r4 = reinterpret_cast<const v4u*>(row);
-    const int nch = d >> 3;
-    for (int c0 = 0; c0 < nch; c0 += 16) {
-      v4u buf[16];
+  for (int c0 = 0; c0 < a.d; c0 += kRrChunk) {
+    const int cols = min(kRrChunk, a.d - c0);
+    if (a.vec) {
+      // d % EPV == 0 and 16-byte aligned rows: whole 16-byte loads.
+      v4u buf[kRrCand * CPR / 64];
 #pragma unroll
-      for (int u = 0; u < 16; ++u)
-        if (c0 + u < nch) buf[u] = __builtin_nontemporal_load(r4 + c0 + u);
+      for (int u = 0; u < kRrCand * CPR / 64; ++u) {
+        const int t = lane + 64 * u, r = t / CPR, cc = t % CPR;
+        const long long id = __shfl(myid, r);
+        buf[u] = (id >= 0 && id < a.n && cc * EPV < cols)
+                     ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(
+                           rows + (size_t)id * a.d + c0 + cc * EPV))
+                     : v4u{0u, 0u, 0u, 0u};
+      }
 #pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        if (c0 + u < nch) {
-          const unsigned ws[4] = {buf[u].x, buf[u].y, buf[u].z, buf[u].w};
-          const int b = (c0 + u) * 8;
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float p0 = qv[b + 2 * t] * (float)__builtin_bit_cast(_Float16, (unsigned short)(ws[t] & 0xffffu));
-            s = s + p0;
-            const float p1 = qv[b + 2 * t + 1] * (float)__builtin_bit_cast(_Float16, (unsigned short)(ws[t] >> 16));
-            s = s + p1;
-          }
-        }
+      for (int u = 0; u < kRrCand * CPR / 64; ++u) {
+        const int t = lane + 64 * u, r = t / CPR, cc = t % CPR;
+        *reinterpret_cast<v4u*>(&tile[r * LD + cc * EPV]) = buf[u];
+      }
+    } else {
+      for (int t = lane; t < kRrCand * kRrChunk; t += 64) {
+        const int r = t / kRrChunk, cc = t % kRrChunk;
+        const long long id = __shfl(myid, r);
+        tile[r * LD + cc] = (id >= 0 && id < a.n && cc < cols) ? rows[(size_t)id * a.d + c0 + cc]
+                                                                 : (Elem)0;
       }
     }
-    i = d;
+    __syncthreads();
+    if (valid) {
+      const Elem* row = &tile[lane * LD];
+      for (int i = 0; i < cols; ++i) {
+        float x;
+        if constexpr (F32) {
+          x = row[i];
+        } else {
+          x = (float)__builtin_bit_cast(_Float16, row[i]);
+        }
+        const float p = qv[c0 + i] * x;
+        s = s + p;
+      }
+    }
+    __syncthreads();
   }
-  for (; i < d; ++i) {
-    const float p = qv[i] * ref_half_to_f32(row[i]);
-    s = s + p;
-  }
-  return s;
+  if (valid) a.dots[(size_t)qi * a.c + j] = s;
 }
 
-// First rerank kernel: one lane per (query, candidate), spread over the whole
-// device (grid: candidate blocks of 64 x queries). The f32 score of candidate
-// j of query qi goes to a.dots[qi * c + j]; candidates whose id is outside
-// [0, n) have no row and are left unscored (the sort kernel skips them).
 extern "C" __global__ __launch_bounds__(64) void eos_tq_rr_dots(TqRerankArgs a) {
-  __shared__ float qv[kRrMaxDim];
-  const int qi = blockIdx.y, j = blockIdx.x * 64 + threadIdx.x;
-  for (int i = threadIdx.x; i < a.d; i += 64) qv[i] = a.queries[(size_t)qi * a.d + i];
+  rr_dots_staged<false>(a);
+}
+extern "C" __global__ __launch_bounds__(64) void eos_tq_rr_dots_f32(TqRerankArgs a) {
+  rr_dots_staged<true>(a);
+}
+
+// Reconstruct rerank (topTurboQuantReconstructRerankScores and, on a sidecar
+// code set, topTurboQuantMixedWidthRerankScores, runtime/retrieval_turboquant.
+// go:1788-1846): the score of a candidate is the inner product of the query
+// with the dequantized vector norm * R^T c[code]. The dequantizer lives in the
+// un-vendored quantizer module; this build's contract evaluates the product
+// in the rotated frame, in f64:
+//   rq_j  = fma chain over k ascending of R[j][k] * q[k]     (eos_tq_rr_rotate)
+//   acc   = fma chain over j ascending of rq_j * codebook[code_j]
+//   score = (float)(acc * norm)
+// Codes are the reference row layout (bits in {1, 2, 4, 8}, code j in byte
+// j / (8 / bits) at bit (j % (8 / bits)) * bits).
+extern "C" __global__ __launch_bounds__(256) void eos_tq_rr_rotate(TqReconArgs a) {
+  const int qi = blockIdx.x;
+  const float* q = a.queries + (size_t)qi * a.d;
+  for (int jj = threadIdx.x; jj < a.d; jj += 256) {
+    double acc = 0.0;
+    if (a.rot_t != nullptr) {
+      for (int k = 0; k < a.d; ++k)
+        acc = __fma_rn((double)a.rot_t[(size_t)k * a.d + jj], (double)q[k], acc);
+    } else {
+      acc = (double)q[jj];
+    }
+    a.rq[(size_t)qi * a.d + jj] = acc;
+  }
+}
+
+extern "C" __global__ __launch_bounds__(64) void eos_tq_rr_dots_recon(TqReconArgs a) {
+  __shared__ double rq[kRrMaxDim];
+  __shared__ double cb[256];
+  const int qi = blockIdx.y, lane = threadIdx.x;
+  const int j = blockIdx.x * 64 + lane;
+  for (int i = lane; i < a.d; i += 64) rq[i] = a.rq[(size_t)qi * a.d + i];
+  for (int i = lane; i < (1 << a.bits); i += 64) cb[i] = (double)a.codebook[i];
   __syncthreads();
   if (j >= a.c) return;
   const long long id = a.cand_ids[(size_t)qi * a.c + j];
   if (id < 0 || id >= a.n) return;
-  a.dots[(size_t)qi * a.c + j] = rr_dot(qv, a.rows + (size_t)id * a.d, a.d);
+  const unsigned char* row = a.codes + (size_t)id * a.row_bytes;
+  const int per = 8 / a.bits;
+  const unsigned mask = (1u << a.bits) - 1u;
+  double acc = 0.0;
+  for (int b = 0; b < a.row_bytes; ++b) {
+    const unsigned byte = row[b];
+    for (int e = 0; e < per; ++e) {
+      const int jj = b * per + e;
+      if (jj < a.d) acc = __fma_rn(rq[jj], cb[(byte >> (e * a.bits)) & mask], acc);
+    }
+  }
+  a.dots[(size_t)qi * a.c + j] = __double2float_rn(acc * (double)a.norms[id]);
 }
 
 // Second rerank kernel, one workgroup per query: sorts the candidates in LDS by

@@ -472,3 +472,75 @@ def turboquant_fp16_rerank_top_k(index: "TurboQuantIndex", sidecar: F16Sidecar,
     for b in (d_q, d_cid, d_cs, d_ids, d_sc) + ((d_rank,) if d_rank is not None else ()):
         b.free()
     return ids, scores, cand
+
+
+def _rerank_out(rt, nq, c, top_k):
+    kk = c if (top_k <= 0 or top_k > c) else int(top_k)
+    return kk, DeviceBuffer(rt, max(8, nq * kk * 8)), DeviceBuffer(rt, max(4, nq * kk * 4))
+
+
+def dense_rerank_top_k(rt: Runtime, queries: np.ndarray, rows: np.ndarray,
+                       cand_ids: np.ndarray, top_k: int, id_rank: np.ndarray | None = None):
+    """topDenseRerankScores (runtime/retrieval_turboquant.go:1610-1633) for each
+    query over f32 corpus rows [n, d]: (ids int64 [Q, kk], scores float32)."""
+    q = np.ascontiguousarray(queries, np.float32)
+    cid = np.ascontiguousarray(cand_ids, np.int64)
+    nq, c = cid.shape
+    rows = np.ascontiguousarray(rows, np.float32)
+    bufs = [DeviceBuffer.from_array(rt, q), DeviceBuffer.from_array(rt, rows),
+            DeviceBuffer.from_array(rt, cid)]
+    rank = DeviceBuffer.from_array(rt, np.ascontiguousarray(id_rank, np.int64)) \
+        if id_rank is not None else None
+    kk, d_ids, d_sc = _rerank_out(rt, nq, c, top_k)
+    try:
+        _lib.call("eoship_tq_dense_rerank_device", rt.handle, bufs[0].ptr, C.c_int32(nq),
+                  C.c_int32(q.shape[1]), bufs[1].ptr, C.c_int64(rows.shape[0]), bufs[2].ptr,
+                  C.c_int32(c), C.c_int32(int(top_k)), rank.ptr if rank is not None else None,
+                  d_ids.ptr, d_sc.ptr)
+        return d_ids.download(np.int64, (nq, kk)), d_sc.download(np.float32, (nq, kk))
+    finally:
+        for b in bufs + [d_ids, d_sc] + ([rank] if rank is not None else []):
+            b.free()
+
+
+def reconstruct_rerank_top_k(rt: Runtime, queries: np.ndarray, codes: np.ndarray, bits: int,
+                             norms: np.ndarray, codebook: np.ndarray, rotation: np.ndarray | None,
+                             cand_ids: np.ndarray, top_k: int,
+                             id_rank: np.ndarray | None = None):
+    """Reconstruct rerank over a code set in the reference row layout (the
+    primary codes: topTurboQuantReconstructRerankScores; a wider sidecar set:
+    topTurboQuantMixedWidthRerankScores, runtime/retrieval_turboquant.go:
+    1788-1846). rotation is R [d, d] (None: identity), codebook the f32
+    centroids [2^bits]. Returns (ids int64 [Q, kk], scores float32)."""
+    q = np.ascontiguousarray(queries, np.float32)
+    cid = np.ascontiguousarray(cand_ids, np.int64)
+    nq, c = cid.shape
+    d = q.shape[1]
+    codes = np.ascontiguousarray(codes, np.uint8)
+    norms = np.ascontiguousarray(norms, np.float32)
+    cb = np.ascontiguousarray(codebook, np.float32)
+    if cb.shape != (1 << bits,):
+        raise ValueError(f"codebook must hold 2^{bits} values")
+    bufs = [DeviceBuffer.from_array(rt, q), DeviceBuffer.from_array(rt, codes),
+            DeviceBuffer.from_array(rt, norms), DeviceBuffer.from_array(rt, cb),
+            DeviceBuffer.from_array(rt, cid)]
+    rot = None
+    if rotation is not None:
+        rot = DeviceBuffer.from_array(rt, np.ascontiguousarray(np.asarray(rotation, np.float32).T))
+        bufs.append(rot)
+    rank = None
+    if id_rank is not None:
+        rank = DeviceBuffer.from_array(rt, np.ascontiguousarray(id_rank, np.int64))
+        bufs.append(rank)
+    spec = _lib.EosHipTQCodes(bits=bits, dim=d, n=norms.shape[0], codes=bufs[1].ptr.value,
+                              norms=bufs[2].ptr.value, codebook=bufs[3].ptr.value,
+                              rotation_t=rot.ptr.value if rot is not None else None)
+    kk, d_ids, d_sc = _rerank_out(rt, nq, c, top_k)
+    try:
+        _lib.call("eoship_tq_reconstruct_rerank_device", rt.handle, C.byref(spec), bufs[0].ptr,
+                  C.c_int32(nq), bufs[4].ptr, C.c_int32(c), C.c_int32(int(top_k)),
+                  rank.ptr if rank is not None else None, d_ids.ptr, d_sc.ptr)
+        return d_ids.download(np.int64, (nq, kk)), d_sc.download(np.float32, (nq, kk))
+    finally:
+        for b in bufs + [d_ids, d_sc]:
+            b.free()

@@ -460,6 +460,45 @@ int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int3
                                  const float* d_cand_scores, int32_t c, int32_t k,
                                  int32_t bit_width, int32_t overfetch, const int64_t* d_id_rank,
                                  int64_t* d_ids, float* d_scores, char** err);
+/* Second stage over f32 rows [n][d] (topDenseRerankScores,
+ * runtime/retrieval_turboquant.go:1610-1633): score = sum += q[i] * row[i] in
+ * index order, each product and sum rounded to f32, then (score desc, ID
+ * asc) -- the id-rank order when d_id_rank is given -- over the candidates in
+ * [0, n); others are skipped. Arguments as eoship_tq_fp16_rerank_device, with
+ * no rescue. Uses a workspace of q * c * 4 bytes. */
+int eoship_tq_dense_rerank_device(EosHipRuntime* rt, const float* d_queries, int32_t q, int32_t d,
+                                  const float* d_rows, int64_t n, const int64_t* d_cand_ids,
+                                  int32_t c, int32_t k, const int64_t* d_id_rank, int64_t* d_ids,
+                                  float* d_scores, char** err);
+
+/* A TurboQuant code set on the device in the reference row layout: the
+ * primary codes or a wider sidecar set with its own codebook. */
+typedef struct {
+  int32_t bits;               /* 1, 2, 4 or 8 bits per coordinate */
+  int32_t dim;                /* d */
+  int64_t n;                  /* vectors */
+  const uint8_t* codes;       /* [n][(d * bits + 7) / 8], code j in byte j / (8 / bits),
+                               * low bits first */
+  const float* norms;         /* [n] */
+  const float* codebook;      /* [2^bits] f32 centroid values */
+  const float* rotation_t;    /* [d][d], rotation_t[k * d + j] = R[j][k]; NULL = identity */
+} EosHipTQCodes;
+
+/* Reconstruct rerank: each candidate scored as the inner product of the query
+ * with its dequantized vector norm * R^T codebook[code], then (score desc, ID
+ * asc) as eoship_tq_dense_rerank_device. With the primary codes this replaces
+ * topTurboQuantReconstructRerankScores, with a sidecar set (e.g. 8-bit codes)
+ * topTurboQuantMixedWidthRerankScores (runtime/retrieval_turboquant.go:
+ * 1788-1846). The dequantizer is in the un-vendored quantizer module, so the
+ * product is this build's contract, evaluated in the rotated frame in f64:
+ * rq = R q (fma in k order), acc = sum_j fma(rq_j, codebook[code_j]), score =
+ * (float)(acc * norm). Uses a workspace of q * d * 8 + q * c * 4 bytes. */
+int eoship_tq_reconstruct_rerank_device(EosHipRuntime* rt, const EosHipTQCodes* codes,
+                                        const float* d_queries, int32_t q,
+                                        const int64_t* d_cand_ids, int32_t c, int32_t k,
+                                        const int64_t* d_id_rank, int64_t* d_ids,
+                                        float* d_scores, char** err);
+
 /* eoship_tq_fp16_rerank_device without any device allocation: no counterpart
  * in the reference; for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). The scores

@@ -458,3 +458,62 @@ def fp16_rerank(queries, rows, cand_ids, cand_scores, k, bit_width=0, overfetch=
                                C.c_int(c), C.c_int(int(k)), C.c_int(1 if rescue else 0),
                                ids[i].ctypes.data_as(C.c_void_p), scores[i].ctypes.data_as(C.c_void_p))
     return ids, scores
+
+
+def _rerank_finish(scores, cid, n, k, id_rank):
+    lib = load()
+    nq, c = cid.shape
+    kk = c if (k <= 0 or k > c) else k
+    ids = np.full((nq, kk), -1, np.int64)
+    out = np.zeros((nq, kk), np.float32)
+    rank = None if id_rank is None else np.ascontiguousarray(id_rank, np.int64)
+    for i in range(nq):
+        lib.oracle_rerank_order(scores[i].ctypes.data_as(C.c_void_p),
+                                cid[i].ctypes.data_as(C.c_void_p), C.c_int64(n), C.c_int(c),
+                                C.c_int(int(k)),
+                                None if rank is None else rank.ctypes.data_as(C.c_void_p),
+                                ids[i].ctypes.data_as(C.c_void_p),
+                                out[i].ctypes.data_as(C.c_void_p))
+    return ids, out
+
+
+def dense_rerank(queries, rows, cand_ids, k, id_rank=None):
+    """topDenseRerankScores per query over f32 rows: (ids [Q, kk], scores)."""
+    q = np.ascontiguousarray(queries, np.float32)
+    rows = np.ascontiguousarray(rows, np.float32)
+    cid = np.ascontiguousarray(cand_ids, np.int64)
+    nq, d = q.shape
+    c = cid.shape[1]
+    sc = np.zeros((nq, c), np.float32)
+    lib = load()
+    for i in range(nq):
+        lib.oracle_dense_scores(q[i].ctypes.data_as(C.c_void_p), C.c_int(d),
+                                rows.ctypes.data_as(C.c_void_p), C.c_int64(rows.shape[0]),
+                                cid[i].ctypes.data_as(C.c_void_p), C.c_int(c),
+                                sc[i].ctypes.data_as(C.c_void_p))
+    return _rerank_finish(sc, cid, rows.shape[0], k, id_rank)
+
+
+def reconstruct_rerank(queries, rotation, codes, bits, norms, codebook, cand_ids, k,
+                       id_rank=None):
+    """Reconstruct / mixed-width rerank per query (this build's contract, see
+    rerank_oracle.c): (ids [Q, kk], scores)."""
+    q = np.ascontiguousarray(queries, np.float32)
+    rot = None if rotation is None else np.ascontiguousarray(rotation, np.float32)
+    codes = np.ascontiguousarray(codes, np.uint8)
+    norms = np.ascontiguousarray(norms, np.float32)
+    cb = np.ascontiguousarray(codebook, np.float32)
+    cid = np.ascontiguousarray(cand_ids, np.int64)
+    nq, d = q.shape
+    c = cid.shape[1]
+    n = norms.shape[0]
+    sc = np.zeros((nq, c), np.float32)
+    lib = load()
+    for i in range(nq):
+        lib.oracle_recon_scores(q[i].ctypes.data_as(C.c_void_p), C.c_int(d),
+                                None if rot is None else rot.ctypes.data_as(C.c_void_p),
+                                codes.ctypes.data_as(C.c_void_p), C.c_int(bits),
+                                norms.ctypes.data_as(C.c_void_p), cb.ctypes.data_as(C.c_void_p),
+                                C.c_int64(n), cid[i].ctypes.data_as(C.c_void_p), C.c_int(c),
+                                sc[i].ctypes.data_as(C.c_void_p))
+    return _rerank_finish(sc, cid, n, k, id_rank)

@@ -12,6 +12,7 @@
  * multiply-add). Ids are vector indices; "ID asc/desc" compares them as
  * integers (the reference's string IDs order the same way when they are
  * fixed-width, e.g. d%03d in its rescue fixtures). */
+#include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -194,5 +195,102 @@ int oracle_fp16_rerank(const float* query, int d, const uint16_t* rows, int64_t 
     out_scores[i] = ranked[i].score;
   }
   free(ranked);
+  return topk;
+}
+
+/* ---------------------------------------------------------------------
+ * Dense and reconstruct reranks (topDenseRerankScores,
+ * topTurboQuantReconstructRerankScores, topTurboQuantMixedWidthRerankScores,
+ * retrieval_turboquant.go:1610-1633, 1788-1846): a score per candidate, the
+ * candidates outside [0, n) skipped, then the heap + sort of
+ * retrievalScoreBetter (score desc, ID asc; with id_rank, the order of the
+ * string IDs). */
+
+/* dotRetrievalVectors (retrieval_eval.go:1189-1199) against f32 rows. */
+void oracle_dense_scores(const float* query, int d, const float* rows, int64_t n,
+                         const int64_t* cand_ids, int c, float* out) {
+  for (int j = 0; j < c; ++j) {
+    const int64_t id = cand_ids[j];
+    if (id < 0 || id >= n) {
+      out[j] = 0.0f;
+      continue;
+    }
+    const float* x = rows + (size_t)id * (size_t)d;
+    float s = 0.0f;
+    for (int i = 0; i < d; ++i) s += query[i] * x[i];
+    out[j] = s;
+  }
+}
+
+/* This build's reconstruct contract: rq = R q (fma, k ascending), acc = fma
+ * chain of rq_j * codebook[code_j] (j ascending), score = (float)(acc *
+ * norm). rot is R row-major (NULL: identity); codes in the reference row
+ * layout (code j in byte j / (8 / bits), low bits first). */
+void oracle_recon_scores(const float* query, int d, const float* rot, const uint8_t* codes,
+                         int bits, const float* norms, const float* codebook, int64_t n,
+                         const int64_t* cand_ids, int c, float* out) {
+  double* rq = (double*)malloc(sizeof(double) * (size_t)d);
+  for (int jj = 0; jj < d; ++jj) {
+    double acc = 0.0;
+    if (rot != NULL) {
+      for (int k = 0; k < d; ++k) acc = fma((double)rot[(size_t)jj * d + k], (double)query[k], acc);
+    } else {
+      acc = (double)query[jj];
+    }
+    rq[jj] = acc;
+  }
+  const int per = 8 / bits, row_bytes = (d * bits + 7) / 8;
+  for (int j = 0; j < c; ++j) {
+    const int64_t id = cand_ids[j];
+    if (id < 0 || id >= n) {
+      out[j] = 0.0f;
+      continue;
+    }
+    const uint8_t* row = codes + (size_t)id * (size_t)row_bytes;
+    double acc = 0.0;
+    for (int jj = 0; jj < d; ++jj) {
+      const int code = (row[jj / per] >> ((jj % per) * bits)) & ((1 << bits) - 1);
+      acc = fma(rq[jj], (double)codebook[code], acc);
+    }
+    out[j] = (float)(acc * (double)norms[id]);
+  }
+  free(rq);
+}
+
+/* Order the scored candidates (insertion sort by score desc, tie key asc:
+ * id_rank[id] when given, else id) and keep the first kk; returns the count. */
+int oracle_rerank_order(const float* scores, const int64_t* cand_ids, int64_t n, int c, int k,
+                        const int64_t* id_rank, int64_t* out_ids, float* out_scores) {
+  int topk = (k <= 0 || k > c) ? c : k;
+  scored_t* ranked = (scored_t*)malloc((size_t)(c > 0 ? c : 1) * sizeof(scored_t));
+  int64_t* key = (int64_t*)malloc((size_t)(c > 0 ? c : 1) * sizeof(int64_t));
+  int m = 0;
+  for (int j = 0; j < c; ++j) {
+    const int64_t id = cand_ids[j];
+    if (id < 0 || id >= n) continue;
+    ranked[m].id = id;
+    ranked[m].score = scores[j];
+    key[m] = id_rank != NULL ? id_rank[id] : id;
+    ++m;
+  }
+  for (int i = 1; i < m; ++i)
+    for (int j = i; j > 0; --j) {
+      const int swap = ranked[j].score > ranked[j - 1].score ||
+                       (ranked[j].score == ranked[j - 1].score && key[j] < key[j - 1]);
+      if (!swap) break;
+      scored_t t = ranked[j];
+      ranked[j] = ranked[j - 1];
+      ranked[j - 1] = t;
+      const int64_t tk = key[j];
+      key[j] = key[j - 1];
+      key[j - 1] = tk;
+    }
+  if (topk > m) topk = m;
+  for (int i = 0; i < topk; ++i) {
+    out_ids[i] = ranked[i].id;
+    out_scores[i] = ranked[i].score;
+  }
+  free(ranked);
+  free(key);
   return topk;
 }

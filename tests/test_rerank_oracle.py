@@ -138,3 +138,72 @@ def test_rerank_brute_force_no_rescue():
         sc.sort()
         assert [j for _, j, _ in sc[:40]] == ids[i].tolist()
         assert np.array_equal(np.array([a for _, _, a in sc[:40]], np.float32), scores[i])
+
+
+def test_dense_rerank_oracle_pins():
+    """topDenseRerankScores: the sequential f32 sum (a known answer an f64 or
+    pairwise accumulator fails), brute force order (score desc, id asc),
+    skipped ids outside [0, n), and the string-ID order through id_rank."""
+    big = np.float32(2.0 ** 24)
+    rows = np.array([[big, 1.0, 1.0, -big], [1.0, 1.0, big, -big]], np.float32)
+    q = np.ones((1, 4), np.float32)
+    _, sc = oracle.dense_rerank(q, rows, np.array([[0, 1]]), 0)
+    # row 0: 2^24 + 1 -> 2^24 (rounded), + 1 -> 2^24, - 2^24 = 0; row 1: 2 + 2^24 - 2^24 = 2
+    assert sc[0].tolist() == [2.0, 0.0]
+    rng = np.random.default_rng(3)
+    rows = rng.normal(size=(300, 24)).astype(np.float32)
+    rows[7] = rows[9]
+    q = rng.normal(size=(4, 24)).astype(np.float32)
+    cid = np.stack([rng.permutation(300)[:80] for _ in range(4)]).astype(np.int64)
+    cid[:, :2] = [9, 7]
+    cid[0, 5] = 400
+    ids, sc = oracle.dense_rerank(q, rows, cid, 30)
+    for i in range(4):
+        live = [j for j in cid[i] if 0 <= j < 300]
+        s = {j: np.float32(0) for j in live}
+        for j in live:
+            acc = np.float32(0)
+            for t in range(24):
+                acc = np.float32(acc + np.float32(q[i, t] * rows[j, t]))
+            s[j] = acc
+        want = sorted(live, key=lambda j: (-s[j], j))[:30]
+        assert ids[i].tolist() == want
+        assert sc[i].tolist() == [s[j] for j in want]
+    rank = np.arange(300)[::-1].copy()
+    ids_r, _ = oracle.dense_rerank(q[:1], np.ones((300, 24), np.float32), cid[:1], 3, id_rank=rank)
+    live = [j for j in cid[0] if 0 <= j < 300]
+    assert ids_r[0].tolist() == sorted(live, key=lambda j: rank[j])[:3]
+
+
+def test_reconstruct_rerank_oracle_pins():
+    """The reconstruct contract equals the dense rerank over the explicitly
+    dequantized vectors norm * R^T codebook[code] (to f32 rounding), equals
+    the f64 estimator tq_scores_f64 with an int8-grid codebook, and with the
+    identity rotation and a one-hot query reduces to norm * codebook value."""
+    rng = np.random.default_rng(5)
+    d, bits, n = 64, 4, 200
+    rot = np.linalg.qr(rng.normal(size=(d, d)))[0].astype(np.float32)
+    codes = rng.integers(0, 256, size=(n, d * bits // 8)).astype(np.uint8)
+    norms = np.exp(0.2 * rng.normal(size=n)).astype(np.float32)
+    cbi = np.array([-127, -90, -64, -45, -30, -18, -8, -2, 2, 8, 18, 30, 45, 64, 90, 127], np.int8)
+    s_c = np.float32(0.004)
+    cb = (cbi.astype(np.float32) * s_c).astype(np.float32)
+    q = rng.normal(size=(3, d)).astype(np.float32)
+    cid = np.tile(np.arange(n, dtype=np.int64), (3, 1))
+    ids, sc = oracle.reconstruct_rerank(q, rot, codes, bits, norms, cb, cid, 0)
+    full = np.zeros((3, n), np.float32)
+    for i in range(3):
+        full[i, ids[i]] = sc[i]
+    # dequantized vectors, then plain dots
+    lo, hi = codes & 0xF, codes >> 4
+    code = np.stack([lo, hi], axis=2).reshape(n, d)
+    xhat = (norms[:, None].astype(np.float64) *
+            (cb.astype(np.float64)[code] @ rot.astype(np.float64)))
+    np.testing.assert_allclose(full, q.astype(np.float64) @ xhat.T, rtol=2e-5, atol=2e-6)
+    est = oracle.tq_scores_f64(q, rot, d, bits, cbi, s_c, codes, norms)
+    np.testing.assert_allclose(full, est, rtol=1e-6, atol=1e-7)
+    one = np.zeros((1, d), np.float32)
+    one[0, 5] = 1.0
+    ids1, sc1 = oracle.reconstruct_rerank(one, None, codes, bits, norms, cb, cid[:1], 0)
+    want = norms[ids1[0]] * cb[code[ids1[0], 5]]
+    np.testing.assert_array_equal(sc1[0], want.astype(np.float32))
