@@ -190,6 +190,18 @@ class EosHipTQCodes(C.Structure):
     ]
 
 
+class EosHipHadamardSpec(C.Structure):
+    _fields_ = [
+        ("channels", C.c_int32),
+        ("bits", C.c_int32),
+        ("perm", C.c_void_p),
+        ("signs1", C.c_void_p),
+        ("signs2", C.c_void_p),
+        ("centroids", C.c_void_p),
+        ("boundaries", C.c_void_p),
+    ]
+
+
 # name -> (argtypes) ; every function returns int except where noted
 _SIGNATURES = {
     "eoship_abi_version": ([], C.c_int),
@@ -321,6 +333,15 @@ _SIGNATURES = {
                                              C.c_int32, C.c_void_p, C.c_int32, C.c_int32,
                                              C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
                                             C.c_int),
+    "eoship_hadamard_tq_bind": ([C.c_void_p, C.POINTER(EosHipHadamardSpec), C.POINTER(C.c_void_p),
+                                 C.c_void_p], C.c_int),
+    "eoship_hadamard_tq_encode_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32,
+                                          C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
+                                          C.c_void_p], C.c_int),
+    "eoship_hadamard_tq_decode_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                          C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
+                                          C.c_void_p], C.c_int),
+    "eoship_hadamard_tq_release": ([C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_release": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_forward": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                 C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),

@@ -101,4 +101,13 @@ struct EosHipRetrieval {
   EosHipRetrievalPlan plan{};
 };
 
+// A bound Hadamard TurboQuant codec: the spec tables on the device.
+struct EosHipHadamardTQ {
+  EosHipRuntime* rt = nullptr;
+  int channels = 0, levels = 0;
+  void* tables = nullptr;
+  int32_t* perm = nullptr;
+  float *signs1 = nullptr, *signs2 = nullptr, *centroids = nullptr, *boundaries = nullptr;
+};
+
 #endif  // EOSHIP_INTERNAL_H

@@ -8,6 +8,7 @@
 //   eos_ret_gather      selected indices -> candidate ids and document rows
 #include <cmath>
 #include <cstring>
+#include <vector>
 
 #include "eoship_internal.h"
 #include "kernels/ret_args.h"
@@ -134,6 +135,134 @@ int eoship_retrieval_release(EosHipRuntime* rt, EosHipRetrieval* ret, char** err
   if (ret->docs_f32) (void)hipFree(ret->docs_f32);
   if (ret->docs_q4) (void)hipFree(ret->docs_q4);
   delete ret;
+  return 0;
+}
+
+// ------------------------------------------------ Hadamard TurboQuant codec
+
+int eoship_hadamard_tq_bind(EosHipRuntime* rt, const EosHipHadamardSpec* spec,
+                            EosHipHadamardTQ** out, char** err) {
+  const char* what = "eoship_hadamard_tq_bind";
+  if (rt == nullptr || spec == nullptr || out == nullptr) return set_err(err, "%s: NULL argument", what);
+  *out = nullptr;
+  const int c = spec->channels, bits = spec->bits;
+  if (c < 1 || c > kHqMaxChannels)
+    return set_err(err, "%s: channels must be in 1..%d (got %d)", what, kHqMaxChannels, c);
+  if (bits != 2 && bits != 4 && bits != 8)
+    return set_err(err, "%s: turboquant bits must be 2, 4, or 8", what);
+  if (!spec->perm || !spec->signs1 || !spec->signs2 || !spec->centroids || !spec->boundaries)
+    return set_err(err, "%s: NULL table", what);
+  const int levels = 1 << bits;
+  std::vector<char> seen((size_t)c, 0);
+  for (int i = 0; i < c; ++i) {
+    const int p = spec->perm[i];
+    if (p < 0 || p >= c || seen[(size_t)p]) return set_err(err, "%s: perm is not a permutation of 0..%d", what, c - 1);
+    seen[(size_t)p] = 1;
+    if (!std::isfinite(spec->signs1[i]) || !std::isfinite(spec->signs2[i]))
+      return set_err(err, "%s: signs must be finite", what);
+  }
+  for (int i = 0; i < levels; ++i)
+    if (!std::isfinite(spec->centroids[i])) return set_err(err, "%s: centroids must be finite", what);
+  for (int i = 0; i + 1 < levels; ++i) {
+    if (std::isnan(spec->boundaries[i])) return set_err(err, "%s: NaN boundary", what);
+    if (i > 0 && spec->boundaries[i] < spec->boundaries[i - 1])
+      return set_err(err, "%s: boundaries must be non-decreasing", what);
+  }
+  auto* h = new EosHipHadamardTQ();
+  h->rt = rt;
+  h->channels = c;
+  h->levels = levels;
+  const size_t tb = (size_t)c * 4 * 3 + (size_t)levels * 4 * 2;
+  void* mem = nullptr;
+  if (rt->alloc(tb, &mem, err) != 0) {
+    delete h;
+    return 1;
+  }
+  h->tables = mem;
+  char* p = static_cast<char*>(mem);
+  h->perm = reinterpret_cast<int32_t*>(p);
+  h->signs1 = reinterpret_cast<float*>(p + (size_t)c * 4);
+  h->signs2 = reinterpret_cast<float*>(p + (size_t)c * 8);
+  h->centroids = reinterpret_cast<float*>(p + (size_t)c * 12);
+  h->boundaries = h->centroids + levels;
+  struct Part {
+    void* dst;
+    const void* src;
+    size_t bytes;
+  } parts[] = {{h->perm, spec->perm, (size_t)c * 4},
+               {h->signs1, spec->signs1, (size_t)c * 4},
+               {h->signs2, spec->signs2, (size_t)c * 4},
+               {h->centroids, spec->centroids, (size_t)levels * 4},
+               {h->boundaries, spec->boundaries, (size_t)(levels - 1) * 4}};
+  for (const Part& pt : parts) {
+    const hipError_t e = hipMemcpy(pt.dst, pt.src, pt.bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(mem);
+      delete h;
+      return eoship::hip_err(err, "hipMemcpy(hadamard tables)", e);
+    }
+  }
+  *out = h;
+  return 0;
+}
+
+static int hq_launch(EosHipRuntime* rt, EosHipHadamardTQ* h, int32_t n, int32_t height,
+                     int32_t width, const char* kernel, HqArgs& a, const char* what, char** err) {
+  if (rt == nullptr || h == nullptr) return set_err(err, "%s: NULL argument", what);
+  if (h->rt != rt) return set_err(err, "%s: the codec is bound to another runtime", what);
+  if (n < 0 || height < 0 || width < 0) return set_err(err, "%s: negative shape", what);
+  const long long pixels = (long long)n * height * width;
+  if (pixels == 0) return 0;
+  if ((long long)height * width > 0x7fffffffll) return set_err(err, "%s: height * width too large", what);
+  a.perm = h->perm;
+  a.signs1 = h->signs1;
+  a.signs2 = h->signs2;
+  a.centroids = h->centroids;
+  a.boundaries = h->boundaries;
+  a.pixels = pixels;
+  a.channels = h->channels;
+  a.hw = height * width;
+  a.levels = h->levels;
+  const size_t lds = (size_t)h->channels * kHqThreads * sizeof(float);
+  return rt->launch(kernel, dim3((unsigned)((pixels + kHqThreads - 1) / kHqThreads)),
+                    dim3(kHqThreads), lds, &a, err, kernel);
+}
+
+int eoship_hadamard_tq_encode_device(EosHipRuntime* rt, EosHipHadamardTQ* h, const float* d_input,
+                                     int32_t n, int32_t height, int32_t width, uint8_t* d_coords,
+                                     uint8_t* d_norm_codes, char** err) {
+  const char* what = "eoship_hadamard_tq_encode_device";
+  if (d_input == nullptr || d_coords == nullptr || d_norm_codes == nullptr)
+    return (long long)n * height * width == 0 ? 0 : set_err(err, "%s: NULL buffer", what);
+  HqArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.input = d_input;
+  a.coords = d_coords;
+  a.norms = d_norm_codes;
+  return hq_launch(rt, h, n, height, width, "eos_hq_encode", a, what, err);
+}
+
+int eoship_hadamard_tq_decode_device(EosHipRuntime* rt, EosHipHadamardTQ* h,
+                                     const uint8_t* d_coords, const uint8_t* d_norm_codes,
+                                     int32_t n, int32_t height, int32_t width, float* d_out,
+                                     char** err) {
+  const char* what = "eoship_hadamard_tq_decode_device";
+  if (d_coords == nullptr || d_norm_codes == nullptr || d_out == nullptr)
+    return (long long)n * height * width == 0 ? 0 : set_err(err, "%s: NULL buffer", what);
+  HqArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.coords_in = d_coords;
+  a.norms_in = d_norm_codes;
+  a.out = d_out;
+  return hq_launch(rt, h, n, height, width, "eos_hq_decode", a, what, err);
+}
+
+int eoship_hadamard_tq_release(EosHipRuntime* rt, EosHipHadamardTQ* h, char** err) {
+  if (h == nullptr) return 0;
+  if (rt == nullptr || h->rt != rt) return set_err(err, "eoship_hadamard_tq_release: wrong runtime");
+  if (rt->sync(err) != 0) return 1;
+  (void)hipFree(h->tables);
+  delete h;
   return 0;
 }
 

@@ -36,4 +36,24 @@ struct RetGatherArgs {
   int d, q, k, batched;
 };
 
+// Hadamard TurboQuant codec of NCHW tensors (one vector per (n, y, x) pixel
+// over the channels): the spec tables of one rotation round.
+constexpr int kHqMaxChannels = 512;
+constexpr int kHqThreads = 64;   // pixels per workgroup, one per thread
+struct HqArgs {
+  const float* input;      // encode: [n][c][h][w]
+  const uint8_t* coords_in;  // decode: [n][c][h][w] centroid indices
+  const uint8_t* norms_in;   // decode: [n][h][w] 8-bit log norm codes
+  uint8_t* coords;         // encode out
+  uint8_t* norms;          // encode out
+  float* out;              // decode out [n][c][h][w]
+  const int32_t* perm;     // [c]
+  const float* signs1;     // [c]
+  const float* signs2;     // [c]
+  const float* centroids;  // [levels]
+  const float* boundaries; // [levels - 1]
+  long long pixels;        // n * h * w
+  int channels, hw, levels;
+};
+
 #endif

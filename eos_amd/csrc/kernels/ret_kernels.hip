@@ -116,3 +116,113 @@ extern "C" __global__ __launch_bounds__(kRetThreads) void eos_ret_gather(RetGath
     dst[c] = v;
   }
 }
+
+// ------------------------------------------------------ Hadamard TurboQuant
+
+// The Hadamard TurboQuant codec of NCHW tensors (turboquant_encode /
+// turboquant_decode steps; host runtime/backend/image_ops.go:212-300, CUDA
+// runtime/backends/cuda/native_linux.go:1812-2004). One thread per pixel
+// vector (consecutive threads read consecutive pixels of a channel, so every
+// channel load is coalesced); its working vector lives in an LDS column
+// work[i * 64 + thread]. Arithmetic, in f32 unless noted:
+//   encode  normSq = fma chain over c ascending; norm = sqrt; scale = 1/norm
+//           (1 when norm <= 1e-12); work[i] = x[perm[i]] * scale * signs1[i];
+//           normalized FWHT on power-of-two blocks from the front (largest
+//           power <= remaining), butterflies (a + b, a - b), block scale
+//           float(1/sqrt(size)); coord[perm[i]] = index of the first boundary
+//           > work[i] * signs2[i] (levels - 1 when none); norm code = the
+//           8-bit log code of quantizeQNorm (image_ops.go:759-775: f64 log,
+//           t = (log(norm) + 16) / 32, round half away from zero of t * 255)
+//   decode  work[i] = centroids[coord[perm[i]]] * signs2[i]; the same FWHT;
+//           out[perm[i]] = work[i] * signs1[i] * norm, norm =
+//           float(exp(-16 + code / 255 * 32)) in f64 (dequantizeQNorm, :777-780)
+namespace {
+
+EOS_DEV void hq_fwht_blocks(float* work, int channels, int t) {
+  int offset = 0, remaining = channels;
+  while (remaining > 0) {
+    int size = 1;
+    while ((size << 1) <= remaining) size <<= 1;
+    for (int step = 1; step < size; step <<= 1)
+      for (int i = 0; i < size; i += step << 1)
+        for (int j = i; j < i + step; ++j) {
+          const float a = work[(offset + j) * kHqThreads + t];
+          const float b = work[(offset + j + step) * kHqThreads + t];
+          work[(offset + j) * kHqThreads + t] = __fadd_rn(a, b);
+          work[(offset + j + step) * kHqThreads + t] = __fsub_rn(a, b);
+        }
+    if (size > 1) {
+      const float scale = __double2float_rn(1.0 / __dsqrt_rn((double)size));
+      for (int i = 0; i < size; ++i)
+        work[(offset + i) * kHqThreads + t] = __fmul_rn(work[(offset + i) * kHqThreads + t], scale);
+    }
+    offset += size;
+    remaining -= size;
+  }
+}
+
+EOS_DEV int hq_norm_code(float norm) {
+  if (!(norm > 0.0f)) return 0;  // <= 0 or NaN
+  if (__builtin_isinf(norm)) return 255;
+  const double t = (log((double)norm) + 16.0) / 32.0;
+  if (t <= 0.0) return 0;
+  if (t >= 1.0) return 255;
+  return (int)round(t * 255.0);
+}
+
+}  // namespace
+
+// Dynamic LDS: channels * 64 floats.
+extern "C" __global__ __launch_bounds__(kHqThreads) void eos_hq_encode(HqArgs a) {
+  extern __shared__ float work[];
+  const int t = threadIdx.x;
+  const long long pix = (long long)blockIdx.x * kHqThreads + t;
+  if (pix >= a.pixels) return;
+  const long long img = pix / a.hw, p = pix % a.hw;
+  const float* x = a.input + img * (long long)a.channels * a.hw + p;
+  float normSq = 0.0f;
+  for (int c = 0; c < a.channels; ++c) {
+    const float v = x[(long long)c * a.hw];
+    normSq = __fmaf_rn(v, v, normSq);
+  }
+  const float norm = __fsqrt_rn(normSq);
+  const float scale = norm > 1.0e-12f ? __fdiv_rn(1.0f, norm) : 1.0f;
+  for (int i = 0; i < a.channels; ++i) {
+    const float v = x[(long long)a.perm[i] * a.hw];
+    work[i * kHqThreads + t] = __fmul_rn(__fmul_rn(v, scale), a.signs1[i]);
+  }
+  hq_fwht_blocks(work, a.channels, t);
+  uint8_t* coords = a.coords + img * (long long)a.channels * a.hw + p;
+  for (int i = 0; i < a.channels; ++i) {
+    const float r = __fmul_rn(work[i * kHqThreads + t], a.signs2[i]);
+    int lo = 0, hi = a.levels - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (a.boundaries[mid] > r) hi = mid;
+      else lo = mid + 1;
+    }
+    coords[(long long)a.perm[i] * a.hw] = (uint8_t)lo;
+  }
+  a.norms[pix] = (uint8_t)hq_norm_code(norm);
+}
+
+extern "C" __global__ __launch_bounds__(kHqThreads) void eos_hq_decode(HqArgs a) {
+  extern __shared__ float work[];
+  const int t = threadIdx.x;
+  const long long pix = (long long)blockIdx.x * kHqThreads + t;
+  if (pix >= a.pixels) return;
+  const long long img = pix / a.hw, p = pix % a.hw;
+  const uint8_t* coords = a.coords_in + img * (long long)a.channels * a.hw + p;
+  for (int i = 0; i < a.channels; ++i) {
+    int idx = coords[(long long)a.perm[i] * a.hw];
+    idx = idx < a.levels ? idx : a.levels - 1;
+    work[i * kHqThreads + t] = __fmul_rn(a.centroids[idx], a.signs2[i]);
+  }
+  hq_fwht_blocks(work, a.channels, t);
+  const double tt = (double)a.norms_in[pix] / 255.0;
+  const float norm = __double2float_rn(exp(-16.0 + tt * 32.0));
+  float* out = a.out + img * (long long)a.channels * a.hw + p;
+  for (int i = 0; i < a.channels; ++i)
+    out[(long long)a.perm[i] * a.hw] =
+        __fmul_rn(__fmul_rn(work[i * kHqThreads + t], a.signs1[i]), norm);
+}

@@ -689,6 +689,46 @@ int eoship_retrieval_run_device(EosHipRuntime* rt, EosHipRetrieval* ret, const f
                                 float* d_top_docs, char** err);
 int eoship_retrieval_release(EosHipRuntime* rt, EosHipRetrieval* ret, char** err);
 
+/* ------------------------------------------------------------------------
+ * Hadamard TurboQuant codec of NCHW tensors (the turboquant_encode /
+ * turboquant_decode steps: host runtime/backend/image_ops.go:212-300, 759-790;
+ * CUDA runtime/backends/cuda/native_linux.go:1812-2004). Each (n, y, x)
+ * pixel's channel vector is rotated by one round of permutation, signs, a
+ * normalized fast Walsh-Hadamard transform on power-of-two blocks and
+ * signs, quantized to the nearest centroid, and its norm kept as an 8-bit
+ * log code over [e^-16, e^16].
+ * ------------------------------------------------------------------------ */
+
+/* The tables of one rotation round and its codebook (the quantizer module's
+ * Spec() for a seed and one round, which the caller provides). */
+typedef struct {
+  int32_t channels;          /* C, 1..512 */
+  int32_t bits;              /* 2, 4 or 8 */
+  const int32_t* perm;       /* [C] a permutation of 0..C-1 */
+  const float* signs1;       /* [C] */
+  const float* signs2;       /* [C] */
+  const float* centroids;    /* [2^bits] */
+  const float* boundaries;   /* [2^bits - 1], non-decreasing */
+} EosHipHadamardSpec;
+
+typedef struct EosHipHadamardTQ EosHipHadamardTQ;
+
+/* Validates the tables and uploads them (host pointers). */
+int eoship_hadamard_tq_bind(EosHipRuntime* rt, const EosHipHadamardSpec* spec,
+                            EosHipHadamardTQ** out, char** err);
+/* d_input f32 [n][C][height][width] -> d_coords u8 [n][C][height][width]
+ * centroid indices and d_norm_codes u8 [n][height][width] (the q_norm code
+ * of quantizeQNorm). */
+int eoship_hadamard_tq_encode_device(EosHipRuntime* rt, EosHipHadamardTQ* h, const float* d_input,
+                                     int32_t n, int32_t height, int32_t width, uint8_t* d_coords,
+                                     uint8_t* d_norm_codes, char** err);
+/* The inverse: indices above the codebook clamp to its last centroid. */
+int eoship_hadamard_tq_decode_device(EosHipRuntime* rt, EosHipHadamardTQ* h,
+                                     const uint8_t* d_coords, const uint8_t* d_norm_codes,
+                                     int32_t n, int32_t height, int32_t width, float* d_out,
+                                     char** err);
+int eoship_hadamard_tq_release(EosHipRuntime* rt, EosHipHadamardTQ* h, char** err);
+
 #ifdef __cplusplus
 }
 #endif

@@ -517,3 +517,59 @@ def reconstruct_rerank(queries, rotation, codes, bits, norms, codebook, cand_ids
                                 C.c_int64(n), cid[i].ctypes.data_as(C.c_void_p), C.c_int(c),
                                 sc[i].ctypes.data_as(C.c_void_p))
     return _rerank_finish(sc, cid, n, k, id_rank)
+
+
+# ------------------------------------------------ Hadamard TurboQuant codec
+def hq_fwht(v):
+    """Normalized FWHT on power-of-two blocks (retrieval_oracle.c)."""
+    x = np.array(v, np.float32)
+    fn = load().hq_fwht
+    fn.argtypes = [C.c_void_p, C.c_int]
+    fn.restype = None
+    fn(_p(x), x.shape[0])
+    return x
+
+
+def hq_norm_code(norm: float) -> int:
+    fn = load().hq_norm_code
+    fn.argtypes = [C.c_float]
+    fn.restype = C.c_int
+    return fn(C.c_float(norm))
+
+
+def hq_norm_value(code: int) -> float:
+    fn = load().hq_norm_value
+    fn.argtypes = [C.c_int]
+    fn.restype = C.c_float
+    return fn(int(code))
+
+
+def hq_encode(x, perm, s1, s2, boundaries, levels):
+    """x f32 [n, C, H, W] -> (coords u8 [n, C, H, W], norm codes u8 [n, H, W])."""
+    x = _f32(x)
+    n, c, h, w = x.shape
+    coords = np.zeros(x.shape, np.uint8)
+    norms = np.zeros((n, h, w), np.uint8)
+    fn = load().hq_encode
+    fn.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int] + [C.c_void_p] * 4 + [C.c_int] + \
+        [C.c_void_p] * 2
+    fn.restype = None
+    perm = np.ascontiguousarray(perm, np.int32)
+    s1, s2, b = _f32(s1), _f32(s2), _f32(boundaries)
+    fn(_p(x), n, c, h * w, _p(perm), _p(s1), _p(s2), _p(b), levels, _p(coords), _p(norms))
+    return coords, norms
+
+
+def hq_decode(coords, norms, perm, s1, s2, centroids, levels):
+    coords = np.ascontiguousarray(coords, np.uint8)
+    norms = np.ascontiguousarray(norms, np.uint8)
+    n, c, h, w = coords.shape
+    out = np.zeros(coords.shape, np.float32)
+    fn = load().hq_decode
+    fn.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_int] + [C.c_void_p] * 4 + \
+        [C.c_int, C.c_void_p]
+    fn.restype = None
+    perm = np.ascontiguousarray(perm, np.int32)
+    s1, s2, cb = _f32(s1), _f32(s2), _f32(centroids)
+    fn(_p(coords), _p(norms), n, c, h * w, _p(perm), _p(s1), _p(s2), _p(cb), levels, _p(out))
+    return out
