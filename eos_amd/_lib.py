@@ -202,6 +202,17 @@ class EosHipHadamardSpec(C.Structure):
     ]
 
 
+class EosHipTQIPSpec(C.Structure):
+    _fields_ = [
+        ("dim", C.c_int32),
+        ("bits", C.c_int32),
+        ("codebook_scale", C.c_float),
+        ("codebook", C.c_void_p),
+        ("rotation_t", C.c_void_p),
+        ("qjl_t", C.c_void_p),
+    ]
+
+
 # name -> (argtypes) ; every function returns int except where noted
 _SIGNATURES = {
     "eoship_abi_version": ([], C.c_int),
@@ -342,6 +353,13 @@ _SIGNATURES = {
                                           C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                                           C.c_void_p], C.c_int),
     "eoship_hadamard_tq_release": ([C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_ip_encode_device": ([C.c_void_p, C.POINTER(EosHipTQIPSpec), C.c_void_p, C.c_int64,
+                                    C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
+                                   C.c_int),
+    "eoship_tq_ip_scores_device": ([C.c_void_p, C.POINTER(EosHipTQIPSpec), C.c_void_p, C.c_int32,
+                                    C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
+                                    C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p],
+                                   C.c_int),
     "eoship_encoder_release": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_forward": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                 C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),

@@ -1577,6 +1577,112 @@ int eoship_tq_reconstruct_rerank_device(EosHipRuntime* rt, const EosHipTQCodes* 
                     "tq_reconstruct_sort");
 }
 
+// ------------------------------------------------------ inner-product layout
+
+static int ip_spec_check(EosHipRuntime* rt, const EosHipTQIPSpec* spec, TqIpArgs* a,
+                         const char* what, char** err) {
+  if (rt == nullptr || spec == nullptr) return set_err(err, "%s: NULL argument", what);
+  const int d = spec->dim, bits = spec->bits;
+  if (d < 1 || d > 1024) return set_err(err, "%s: dim must be in [1, 1024]", what);
+  if (bits != 1 && bits != 2 && bits != 4)
+    return set_err(err, "%s: MSE bits must be 1, 2 or 4 (got %d)", what, bits);
+  if (spec->codebook == nullptr || spec->qjl_t == nullptr)
+    return set_err(err, "%s: NULL codebook or QJL matrix", what);
+  if (!(spec->codebook_scale > 0.f) || std::isinf(spec->codebook_scale))
+    return set_err(err, "%s: codebook_scale must be finite and > 0", what);
+  memset(a, 0, sizeof(*a));
+  const int levels = 1 << bits;
+  int cmax = 0;
+  for (int v = 0; v < levels; ++v) {
+    a->cb[v] = spec->codebook[v];
+    cmax = std::max(cmax, std::abs((int)spec->codebook[v]));
+  }
+  // The MSE query grid keeps |D_mse| < 2^31 as the flat scan's does; the QJL
+  // grid |D_qjl| <= d * qmax2 < 2^31.
+  const int64_t lim = cmax == 0 ? kQmaxLimit : (int64_t)2147483647 / ((int64_t)cmax * d) - 128;
+  a->qmax = (int)std::min<int64_t>(kQmaxLimit, lim);
+  a->qmax2 = (int)std::min<int64_t>(32767, (int64_t)2147483647 / d - 1);
+  if (a->qmax < 1) return set_err(err, "%s: codebook too wide for dim %d", what, d);
+  a->rot_t = spec->rotation_t;
+  a->qjl_t = spec->qjl_t;
+  a->d = d;
+  a->bits = bits;
+  a->row_bytes = (d * bits + 7) / 8;
+  a->sign_bytes = (d + 7) / 8;
+  a->cb_scale = spec->codebook_scale;
+  return 0;
+}
+
+int eoship_tq_ip_encode_device(EosHipRuntime* rt, const EosHipTQIPSpec* spec, const float* d_x,
+                               int64_t n, uint8_t* d_codes, uint8_t* d_signs, float* d_resnorms,
+                               float* d_norms, char** err) {
+  const char* what = "eoship_tq_ip_encode_device";
+  TqIpArgs a;
+  if (ip_spec_check(rt, spec, &a, what, err) != 0) return 1;
+  if (n < 0) return set_err(err, "%s: negative n", what);
+  if (n == 0) return 0;
+  if (!d_x || !d_codes || !d_signs || !d_resnorms || !d_norms)
+    return set_err(err, "%s: NULL buffer", what);
+  a.x = d_x;
+  a.codes = d_codes;
+  a.signs = d_signs;
+  a.resnorms = d_resnorms;
+  a.norms = d_norms;
+  a.n = n;
+  return rt->launch("eos_tq_encode_ip", dim3((unsigned)((n + 7) / 8)), dim3(256), 0, &a, err,
+                    "tq_encode_ip");
+}
+
+int eoship_tq_ip_scores_device(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
+                               const float* d_queries, int32_t q, const uint8_t* d_codes,
+                               const uint8_t* d_signs, const float* d_resnorms,
+                               const float* d_norms, int64_t n, float* d_scores, int32_t k,
+                               int64_t* d_top_ids, float* d_top_scores, char** err) {
+  const char* what = "eoship_tq_ip_scores_device";
+  TqIpArgs a;
+  if (ip_spec_check(rt, spec, &a, what, err) != 0) return 1;
+  if (q < 0 || n < 0) return set_err(err, "%s: negative size", what);
+  if (n >= ((int64_t)1 << 31)) return set_err(err, "%s: n must be below 2^31", what);
+  if (k < 0 || k > 8192) return set_err(err, "%s: k must be in 0..8192", what);
+  if (k > 0 && (d_top_ids == nullptr || d_top_scores == nullptr))
+    return set_err(err, "%s: top-k outputs are NULL", what);
+  if (q == 0 || n == 0) return 0;
+  if (!d_queries || !d_codes || !d_signs || !d_resnorms || !d_norms || !d_scores)
+    return set_err(err, "%s: NULL buffer", what);
+  const size_t grid_bytes = (size_t)q * (size_t)a.d * sizeof(int);
+  void* ws = nullptr;
+  if (rt->workspace(2 * grid_bytes + (size_t)q * 8, &ws, err) != 0) return 1;
+  char* w = static_cast<char*>(ws);
+  a.queries = d_queries;
+  a.qs = reinterpret_cast<int*>(w);
+  a.ys = reinterpret_cast<int*>(w + grid_bytes);
+  a.alpha = reinterpret_cast<float*>(w + 2 * grid_bytes);
+  a.beta = a.alpha + q;
+  a.codes = const_cast<uint8_t*>(d_codes);
+  a.signs = const_cast<uint8_t*>(d_signs);
+  a.resnorms = const_cast<float*>(d_resnorms);
+  a.norms = const_cast<float*>(d_norms);
+  a.scores = d_scores;
+  a.n = n;
+  a.q = q;
+  if (rt->launch("eos_tq_ip_prepare", dim3((unsigned)q), dim3(256), 0, &a, err, "tq_ip_prepare") != 0 ||
+      rt->launch("eos_tq_ip_scores", dim3((unsigned)((n + 255) / 256), (unsigned)((q + 7) / 8)),
+                 dim3(256), 0, &a, err, "tq_ip_scores") != 0)
+    return 1;
+  if (k == 0) return 0;
+  TqSelectArgs sel;
+  memset(&sel, 0, sizeof(sel));
+  sel.rows = d_scores;
+  sel.ids = reinterpret_cast<long long*>(d_top_ids);
+  sel.scores = d_top_scores;
+  sel.n = n;
+  sel.stride = n;
+  sel.kk = (int64_t)k > n ? (int)n : k;
+  sel.mode = 1;
+  sel.nrows = q;
+  return rt->launch("eos_tq_row_select", dim3((unsigned)q), dim3(1024), 0, &sel, err, "tq_ip_topk");
+}
+
 int eoship_f16_sidecar_device(EosHipRuntime* rt, const float* d_x, int64_t count, uint16_t* d_half,
                               char** err) {
   if (rt == nullptr) return set_err(err, "eoship_f16_sidecar_device: NULL runtime");

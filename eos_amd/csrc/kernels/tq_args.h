@@ -165,6 +165,28 @@ struct TqEncodeArgs {
   int cb[16];
 };
 
+// Inner-product layout (MSE codes + QJL signs + ResNorm + Norm): encode,
+// query preparation and exhaustive scores.
+struct TqIpArgs {
+  const float* x;          // encode: [n][d]
+  const float* queries;    // prepare: [q][d]
+  const float* rot_t;      // [d][d], rot_t[k*d + j] = R[j][k]; NULL = identity
+  const float* qjl_t;      // [d][d], qjl_t[j*d + i] = S[i][j]
+  uint8_t* codes;          // [n][row_bytes] (encode out / scores in)
+  uint8_t* signs;          // [n][sign_bytes]
+  float* resnorms;         // [n]
+  float* norms;            // [n]
+  int* qs;                 // [q][d] MSE query grid
+  int* ys;                 // [q][d] QJL query grid
+  float* alpha;            // [q]
+  float* beta;             // [q]
+  float* scores;           // [q][n]
+  long long n;
+  int d, bits, row_bytes, sign_bytes, q, qmax, qmax2;
+  float cb_scale;
+  int cb[16];
+};
+
 // f16 rerank sidecar: f32 rows -> the reference's half encoding.
 struct TqHalfArgs {
   const float* x;          // [count]

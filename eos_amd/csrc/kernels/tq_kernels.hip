@@ -426,6 +426,222 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_encode_d1024(TqEncodeAr
   encode_body<16, 1024>(a);
 }
 
+// ------------------------------------------------------- inner-product layout
+
+// Build-defined inner-product layout after the published TurboQuant_prod
+// estimator (the quantizer is in the un-vendored module; byte layout of
+// runtime/turboquant_bytes.go:14-25): the MSE stage of encode_body, then a
+// 1-bit QJL sketch of the residual in the rotated frame, all in f64:
+//   r_j = u_j - nrm c_code_j;  ResNorm = (float)(sqrt(sum_j r_j^2) / nrm)
+//   sign bit i = (sum_j S[i][j] r_j >= 0), fma chains in j order
+// Eight vectors per workgroup (d <= 1024); thread t runs coordinates and
+// sketch rows t, t + 256, ... for all eight, reading R^T and S^T coalesced.
+constexpr int kIpV = 8;
+constexpr int kIpDMax = 1024;
+extern "C" __global__ __launch_bounds__(256) void eos_tq_encode_ip(TqIpArgs a) {
+  __shared__ float xs[kIpDMax * kIpV];
+  __shared__ double rs[kIpV * kIpDMax];
+  __shared__ double ncs[kIpV * 16];
+  __shared__ uint8_t cs[kIpV * kIpDMax];
+  __shared__ uint8_t sb[kIpV * kIpDMax];
+  __shared__ double nrms[kIpV];
+  const int tid = threadIdx.x;
+  const long long v0 = (long long)blockIdx.x * kIpV;
+  const int nv = (int)min((long long)kIpV, a.n - v0);
+  if (nv <= 0) return;
+  const int d = a.d, levels = 1 << a.bits;
+  for (int i = tid; i < kIpV * d; i += 256) {
+    const int v = i / d, k = i - v * d;
+    xs[k * kIpV + v] = v < nv ? a.x[(size_t)(v0 + v) * d + k] : 0.0f;
+  }
+  __syncthreads();
+  if (tid < kIpV) {
+    double ss = 0.0;
+    for (int k = 0; k < d; ++k) {
+      const double xk = (double)xs[k * kIpV + tid];
+      ss = fma(xk, xk, ss);
+    }
+    const double nrm = __builtin_sqrt(ss);
+    nrms[tid] = nrm;
+    if (tid < nv) a.norms[v0 + tid] = (float)nrm;
+    for (int l = 0; l < levels; ++l) ncs[tid * 16 + l] = nrm * ((double)a.cb_scale * (double)a.cb[l]);
+  }
+  __syncthreads();
+  for (int j = tid; j < d; j += 256) {
+    double acc[kIpV];
+#pragma unroll
+    for (int v = 0; v < kIpV; ++v) acc[v] = a.rot_t != nullptr ? 0.0 : (double)xs[j * kIpV + v];
+    if (a.rot_t != nullptr) {
+      for (int k = 0; k < d; ++k) {
+        const double r = (double)a.rot_t[(size_t)k * d + j];
+#pragma unroll
+        for (int v = 0; v < kIpV; ++v) acc[v] = fma(r, (double)xs[k * kIpV + v], acc[v]);
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < kIpV; ++v) {
+      const double u = acc[v];
+      int best = 0;
+      double bd = fabs(u - ncs[v * 16]);
+      for (int l = 1; l < levels; ++l) {
+        const double dv = fabs(u - ncs[v * 16 + l]);
+        if (dv < bd) {
+          bd = dv;
+          best = l;
+        }
+      }
+      cs[v * kIpDMax + j] = (uint8_t)best;
+      rs[v * kIpDMax + j] = u - ncs[v * 16 + best];
+    }
+  }
+  __syncthreads();
+  if (tid < nv) {
+    double rn = 0.0;
+    for (int j = 0; j < d; ++j) rn = fma(rs[tid * kIpDMax + j], rs[tid * kIpDMax + j], rn);
+    const double nrm = nrms[tid];
+    a.resnorms[v0 + tid] = nrm > 0.0 ? (float)(__builtin_sqrt(rn) / nrm) : 0.0f;
+  }
+  for (int i = tid; i < d; i += 256) {
+    double p[kIpV];
+#pragma unroll
+    for (int v = 0; v < kIpV; ++v) p[v] = 0.0;
+    for (int j = 0; j < d; ++j) {
+      const double s = (double)a.qjl_t[(size_t)j * d + i];
+#pragma unroll
+      for (int v = 0; v < kIpV; ++v) p[v] = fma(s, rs[v * kIpDMax + j], p[v]);
+    }
+#pragma unroll
+    for (int v = 0; v < kIpV; ++v) sb[v * kIpDMax + i] = p[v] >= 0.0 ? 1 : 0;
+  }
+  __syncthreads();
+  const int per = 8 / a.bits;
+  for (int i = tid; i < nv * a.row_bytes; i += 256) {
+    const int v = i / a.row_bytes, b = i - v * a.row_bytes;
+    uint32_t byte = 0;
+    for (int e = 0; e < per; ++e) {
+      const int j = b * per + e;
+      if (j < d) byte |= (uint32_t)cs[v * kIpDMax + j] << (e * a.bits);
+    }
+    a.codes[(size_t)(v0 + v) * a.row_bytes + b] = (uint8_t)byte;
+  }
+  for (int i = tid; i < nv * a.sign_bytes; i += 256) {
+    const int v = i / a.sign_bytes, b = i - v * a.sign_bytes;
+    uint32_t byte = 0;
+    for (int e = 0; e < 8; ++e) {
+      const int j = b * 8 + e;
+      if (j < d) byte |= (uint32_t)sb[v * kIpDMax + j] << e;
+    }
+    a.signs[(size_t)(v0 + v) * a.sign_bytes + b] = (uint8_t)byte;
+  }
+}
+
+// Query preparation of the inner-product layout, one workgroup per query:
+// q' = R q, the MSE grid Qs = rint(q' qmax / max|q'|) with alpha = s_q s_c (as
+// eos_tq_rotate / eos_tq_quantize), then y = S q' (fma chain in j order), the
+// QJL grid Ys = rint(y qmax2 / max|y|) and beta = (max|y| / qmax2)
+// sqrt(pi / 2) / d.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_prepare(TqIpArgs a) {
+  __shared__ double qr[kIpDMax];
+  __shared__ double yv[kIpDMax];
+  __shared__ double red[4];
+  const int qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int d = a.d;
+  const float* q = a.queries + (size_t)qi * d;
+  auto block_max = [&](double m) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmax(m, __shfl_xor(m, o));
+    if (lane == 0) red[w] = m;
+    __syncthreads();
+    const double r = fmax(fmax(red[0], red[1]), fmax(red[2], red[3]));
+    __syncthreads();
+    return r;
+  };
+  double m = 0.0;
+  for (int j = tid; j < d; j += 256) {
+    double acc = 0.0;
+    if (a.rot_t != nullptr) {
+      for (int k = 0; k < d; ++k) acc = fma((double)a.rot_t[(size_t)k * d + j], (double)q[k], acc);
+    } else {
+      acc = (double)q[j];
+    }
+    qr[j] = acc;
+    m = fmax(m, fabs(acc));
+  }
+  const double mq = block_max(m);
+  const double inv = mq > 0.0 ? (double)a.qmax / mq : 0.0;
+  m = 0.0;
+  for (int j = tid; j < d; j += 256) {
+    double v = rint(qr[j] * inv);
+    v = fmin(fmax(v, (double)-a.qmax), (double)a.qmax);
+    a.qs[(size_t)qi * d + j] = (int)v;
+    double acc = 0.0;
+    for (int k = 0; k < d; ++k) acc = fma((double)a.qjl_t[(size_t)k * d + j], qr[k], acc);
+    yv[j] = acc;
+    m = fmax(m, fabs(acc));
+  }
+  // qr is complete before any thread's y chain reads it: the chains above
+  // read qr[k] for all k, written in the first loop and ordered by the
+  // barriers of block_max.
+  const double my = block_max(m);
+  const double inv2 = my > 0.0 ? (double)a.qmax2 / my : 0.0;
+  for (int j = tid; j < d; j += 256) {
+    double v = rint(yv[j] * inv2);
+    v = fmin(fmax(v, (double)-a.qmax2), (double)a.qmax2);
+    a.ys[(size_t)qi * d + j] = (int)v;
+  }
+  if (tid == 0) {
+    a.alpha[qi] = mq > 0.0 ? (float)((mq / (double)a.qmax) * (double)a.cb_scale) : 0.0f;
+    const double half_pi = 1.5707963267948966;
+    a.beta[qi] = my > 0.0 ? (float)((my / (double)a.qmax2) * __builtin_sqrt(half_pi) / (double)d)
+                          : 0.0f;
+  }
+}
+
+// Exhaustive scores of the inner-product layout: grid (ceil(n / 256),
+// ceil(q / 8)), one vector per thread against 8 queries (their grids in
+// LDS), exact int32 dots, then the fixed f32 expression
+//   ((float)D_mse * alpha + ResNorm * ((float)D_qjl * beta)) * Norm.
+constexpr int kIpQ = 8;
+extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_scores(TqIpArgs a) {
+  __shared__ int qs[kIpQ * kIpDMax];
+  __shared__ int ys[kIpQ * kIpDMax];
+  const int tid = threadIdx.x;
+  const int q0 = blockIdx.y * kIpQ, nq = min(kIpQ, a.q - q0);
+  const int d = a.d;
+  for (int i = tid; i < kIpQ * d; i += 256) {
+    const int g = i / d, j = i - g * d;
+    qs[j * kIpQ + g] = g < nq ? a.qs[(size_t)(q0 + g) * d + j] : 0;
+    ys[j * kIpQ + g] = g < nq ? a.ys[(size_t)(q0 + g) * d + j] : 0;
+  }
+  __syncthreads();
+  const long long v = (long long)blockIdx.x * 256 + tid;
+  if (v >= a.n) return;
+  int dm[kIpQ], dq[kIpQ];
+#pragma unroll
+  for (int g = 0; g < kIpQ; ++g) dm[g] = dq[g] = 0;
+  const uint8_t* row = a.codes + (size_t)v * a.row_bytes;
+  const int mask = (1 << a.bits) - 1;
+  for (int j = 0; j < d; ++j) {
+    const int bit = j * a.bits;
+    const int c = a.cb[(row[bit >> 3] >> (bit & 7)) & mask];
+#pragma unroll
+    for (int g = 0; g < kIpQ; ++g) dm[g] += qs[j * kIpQ + g] * c;
+  }
+  const uint8_t* sg = a.signs + (size_t)v * a.sign_bytes;
+  for (int j = 0; j < d; ++j) {
+    const bool pos = (sg[j >> 3] >> (j & 7)) & 1;
+#pragma unroll
+    for (int g = 0; g < kIpQ; ++g) dq[g] += pos ? ys[j * kIpQ + g] : -ys[j * kIpQ + g];
+  }
+  const float rn = a.resnorms[v], nm = a.norms[v];
+  for (int g = 0; g < nq; ++g) {
+    const float t1 = __fmul_rn((float)dm[g], a.alpha[q0 + g]);
+    const float t2 = __fmul_rn((float)dq[g], a.beta[q0 + g]);
+    const float t3 = __fmul_rn(rn, t2);
+    a.scores[(size_t)(q0 + g) * a.n + v] = __fmul_rn(__fadd_rn(t1, t3), nm);
+  }
+}
+
 // --------------------------------------------------------------------- scan
 
 

@@ -544,3 +544,77 @@ def reconstruct_rerank_top_k(rt: Runtime, queries: np.ndarray, codes: np.ndarray
     finally:
         for b in bufs + [d_ids, d_sc]:
             b.free()
+
+
+class IPQuantizer:
+    """The inner-product layout (MSE codes + QJL signs + ResNorm + Norm) on
+    the device: ``encode`` (eoship_tq_ip_encode_device) and exhaustive
+    ``scores`` / top-k (eoship_tq_ip_scores_device). rotation R and sketch S
+    are [d, d] f32; codebook the int8 grid with its scale."""
+
+    def __init__(self, rt: Runtime, dim: int, bits: int, codebook: np.ndarray,
+                 codebook_scale: float, rotation: np.ndarray | None, sketch: np.ndarray):
+        self.rt, self.dim, self.bits = rt, int(dim), int(bits)
+        self._cb = np.ascontiguousarray(codebook, np.int8)
+        if self._cb.shape != (1 << self.bits,):
+            raise ValueError("codebook must hold 2^bits entries")
+        self._rot = None
+        if rotation is not None:
+            self._rot = DeviceBuffer.from_array(rt, np.ascontiguousarray(
+                np.asarray(rotation, np.float32).T))
+        self._qjl = DeviceBuffer.from_array(rt, np.ascontiguousarray(np.asarray(sketch, np.float32).T))
+        self.spec = _lib.EosHipTQIPSpec(self.dim, self.bits, float(codebook_scale),
+                                        self._cb.ctypes.data_as(C.c_void_p).value,
+                                        self._rot.ptr.value if self._rot is not None else None,
+                                        self._qjl.ptr.value)
+        self.row_bytes = (self.dim * self.bits + 7) // 8
+        self.sign_bytes = (self.dim + 7) // 8
+
+    def vector_bytes(self) -> int:
+        """MSE + signs + 8 bytes per vector (runtime/turboquant_bytes.go:14-25)."""
+        return self.row_bytes + self.sign_bytes + 8
+
+    def encode(self, x: np.ndarray):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.dim)
+        n = x.shape[0]
+        bufs = [DeviceBuffer.from_array(self.rt, x), DeviceBuffer(self.rt, max(1, n * self.row_bytes)),
+                DeviceBuffer(self.rt, max(1, n * self.sign_bytes)), DeviceBuffer(self.rt, max(4, n * 4)),
+                DeviceBuffer(self.rt, max(4, n * 4))]
+        try:
+            _lib.call("eoship_tq_ip_encode_device", self.rt.handle, C.byref(self.spec), bufs[0].ptr,
+                      C.c_int64(n), bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, bufs[4].ptr)
+            return (bufs[1].download(np.uint8, (n, self.row_bytes)),
+                    bufs[2].download(np.uint8, (n, self.sign_bytes)),
+                    bufs[3].download(np.float32, (n,)), bufs[4].download(np.float32, (n,)))
+        finally:
+            for b in bufs:
+                b.free()
+
+    def scores(self, queries, codes, signs, resnorms, norms, k: int = 0):
+        """scores [q, n], and with k > 0 also (top ids [q, kk], top scores)."""
+        q = np.ascontiguousarray(queries, np.float32).reshape(-1, self.dim)
+        nq, n = q.shape[0], int(np.asarray(norms).shape[0])
+        kk = min(k, n)
+        ins = [DeviceBuffer.from_array(self.rt, a) for a in (
+            q, np.ascontiguousarray(codes, np.uint8), np.ascontiguousarray(signs, np.uint8),
+            np.ascontiguousarray(resnorms, np.float32), np.ascontiguousarray(norms, np.float32))]
+        out = DeviceBuffer(self.rt, max(4, nq * n * 4))
+        tid = DeviceBuffer(self.rt, max(8, nq * kk * 8)) if k > 0 else None
+        tsc = DeviceBuffer(self.rt, max(4, nq * kk * 4)) if k > 0 else None
+        try:
+            _lib.call("eoship_tq_ip_scores_device", self.rt.handle, C.byref(self.spec), ins[0].ptr,
+                      C.c_int32(nq), ins[1].ptr, ins[2].ptr, ins[3].ptr, ins[4].ptr, C.c_int64(n),
+                      out.ptr, C.c_int32(k), tid.ptr if tid else None, tsc.ptr if tsc else None)
+            s = out.download(np.float32, (nq, n))
+            if k > 0:
+                return s, tid.download(np.int64, (nq, kk)), tsc.download(np.float32, (nq, kk))
+            return s
+        finally:
+            for b in ins + [out] + ([tid, tsc] if k > 0 else []):
+                b.free()
+
+    def release(self) -> None:
+        for b in (self._rot, self._qjl):
+            if b is not None:
+                b.free()
+        self._rot = self._qjl = None

@@ -460,6 +460,42 @@ int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int3
                                  const float* d_cand_scores, int32_t c, int32_t k,
                                  int32_t bit_width, int32_t overfetch, const int64_t* d_id_rank,
                                  int64_t* d_ids, float* d_scores, char** err);
+/* The inner-product layout (IPQuantized{MSE, Signs, ResNorm, Norm};
+ * byte accounting runtime/turboquant_bytes.go:14-25): the MSE codes of
+ * eoship_tq_encode_device plus a 1-bit QJL sketch of the residual. The
+ * quantizer is in the un-vendored module (called at runtime/
+ * retrieval_turboquant.go:700-711), so this is the build's contract after the
+ * published TurboQuant_prod estimator, in f64: r = R x - Norm c[code],
+ * ResNorm = |r| / Norm, sign bit i = (S r)_i >= 0 (packed low bit first,
+ * (d + 7) / 8 bytes). S is a d x d sketch matrix (Gaussian rows) the caller
+ * provides, like R. */
+typedef struct {
+  int32_t dim;               /* d, 1..1024 */
+  int32_t bits;              /* MSE bits: 1, 2 or 4 */
+  float codebook_scale;      /* c_v = codebook_scale * codebook[v] */
+  const int8_t* codebook;    /* host [2^bits] int8 grid */
+  const float* rotation_t;   /* device [d][d], rotation_t[k * d + j] = R[j][k]; NULL = I */
+  const float* qjl_t;        /* device [d][d], qjl_t[j * d + i] = S[i][j] */
+} EosHipTQIPSpec;
+
+/* x [n][d] -> codes [n][(d * bits + 7) / 8], signs [n][(d + 7) / 8],
+ * resnorms [n], norms [n]. */
+int eoship_tq_ip_encode_device(EosHipRuntime* rt, const EosHipTQIPSpec* spec, const float* d_x,
+                               int64_t n, uint8_t* d_codes, uint8_t* d_signs, float* d_resnorms,
+                               float* d_norms, char** err);
+/* Exhaustive scores [q][n] of the inner-product estimate
+ *   ((float)D_mse * alpha + ResNorm * ((float)D_qjl * beta)) * Norm
+ * with D_mse = sum_j Qs_j C[code_j] and D_qjl = sum_i Ys_i (2 bit_i - 1)
+ * exact int32 over int16 grids of R q and S R q (alpha = s_q s_c, beta =
+ * s_y sqrt(pi / 2) / d), then with k > 0 the top k per query by (score
+ * desc, index asc) into d_top_ids / d_top_scores [q][min(k, n)]. Uses a
+ * workspace of q * (8 d + 8) bytes. */
+int eoship_tq_ip_scores_device(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
+                               const float* d_queries, int32_t q, const uint8_t* d_codes,
+                               const uint8_t* d_signs, const float* d_resnorms,
+                               const float* d_norms, int64_t n, float* d_scores, int32_t k,
+                               int64_t* d_top_ids, float* d_top_scores, char** err);
+
 /* Second stage over f32 rows [n][d] (topDenseRerankScores,
  * runtime/retrieval_turboquant.go:1610-1633): score = sum += q[i] * row[i] in
  * index order, each product and sum rounded to f32, then (score desc, ID

@@ -573,3 +573,44 @@ def hq_decode(coords, norms, perm, s1, s2, centroids, levels):
     s1, s2, cb = _f32(s1), _f32(s2), _f32(centroids)
     fn(_p(coords), _p(norms), n, c, h * w, _p(perm), _p(s1), _p(s2), _p(cb), levels, _p(out))
     return out
+
+
+# ------------------------------------------------ inner-product layout (QJL)
+def tq_encode_ip(vectors, rotation, qjl, dim, bits, codebook, codebook_scale):
+    """(codes [n, row_bytes], signs [n, (d + 7) // 8], resnorms [n], norms [n])."""
+    x = _f32(vectors).reshape(-1, dim)
+    n = x.shape[0]
+    rot = None if rotation is None else _f32(rotation)
+    s = _f32(qjl)
+    cb = np.ascontiguousarray(codebook, np.int8)
+    codes = np.zeros((n, (dim * bits + 7) // 8), np.uint8)
+    signs = np.zeros((n, (dim + 7) // 8), np.uint8)
+    rn = np.zeros(n, np.float32)
+    nm = np.zeros(n, np.float32)
+    fn = load().tq_encode_ip
+    fn.argtypes = [C.c_void_p, C.c_int64, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                   C.c_float] + [C.c_void_p] * 4
+    fn.restype = None
+    fn(_p(x), n, _p(rot), _p(s), dim, bits, _p(cb), C.c_float(codebook_scale), _p(codes),
+       _p(signs), _p(rn), _p(nm))
+    return codes, signs, rn, nm
+
+
+def tq_ip_scores(queries, rotation, qjl, dim, bits, codebook, codebook_scale, codes, signs,
+                 resnorms, norms):
+    q = _f32(queries).reshape(-1, dim)
+    rot = None if rotation is None else _f32(rotation)
+    s = _f32(qjl)
+    cb = np.ascontiguousarray(codebook, np.int8)
+    codes = np.ascontiguousarray(codes, np.uint8)
+    signs = np.ascontiguousarray(signs, np.uint8)
+    rn, nm = _f32(resnorms), _f32(norms)
+    n = nm.shape[0]
+    out = np.zeros((q.shape[0], n), np.float32)
+    fn = load().tq_ip_scores
+    fn.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p,
+                   C.c_float] + [C.c_void_p] * 4 + [C.c_int64, C.c_void_p]
+    fn.restype = None
+    fn(_p(q), q.shape[0], _p(rot), _p(s), dim, bits, _p(cb), C.c_float(codebook_scale),
+       _p(codes), _p(signs), _p(rn), _p(nm), n, _p(out))
+    return out

@@ -441,3 +441,134 @@ void tq_encode(const float* x, int64_t n, const float* rot, int d, int bits, con
   }
   free(u);
 }
+
+/* ------------------------------------------------------------- QJL stage
+ * Build-defined inner-product layout (IPQuantized{MSE, Signs, ResNorm, Norm},
+ * runtime/turboquant_bytes.go:14-25 / turboquant_quantized_vector.go; the
+ * quantizer itself is in the un-vendored module, called at
+ * runtime/retrieval_turboquant.go:700-711), after the published
+ * TurboQuant_prod estimator: the MSE stage of tq_encode, then a 1-bit QJL
+ * sketch of the residual in the rotated frame:
+ *   r_j    = u_j - nrm * c_code_j                        (f64)
+ *   ResNorm = (float)(sqrt(sum_j r_j^2) / nrm)           (fma chain; 0 when nrm = 0)
+ *   p_i    = sum_j S[i][j] r_j                           (f64 fma chain, j ascending)
+ *   sign bit i = p_i >= 0, packed low bit first ((d + 7) / 8 bytes)
+ * Scoring: q' = R q, Qs / alpha as tq_prepare; y = S q' (f64 fma chain),
+ * Ys = rint(y * qmax2 / max|y|) with qmax2 = min(32767, (2^31 - 1) / d - 1),
+ * gamma = max|y| / qmax2, beta = (float)(gamma * sqrt(pi / 2) / d);
+ *   D_mse = sum_j Qs_j C[code_j], D_qjl = sum_i Ys_i (2 bit_i - 1)   (exact int32)
+ *   score = ((float)D_mse * alpha + ResNorm * ((float)D_qjl * beta)) * Norm
+ * (each product and sum rounded to f32 in that order). */
+int tq_qjl_qmax(int d) {
+  const long long lim = 2147483647LL / d - 1;
+  return (int)(lim < 32767 ? lim : 32767);
+}
+
+void tq_encode_ip(const float* x, int64_t n, const float* rot, const float* qjl, int d, int bits,
+                  const int8_t* cb, float cb_scale, uint8_t* codes, uint8_t* signs,
+                  float* resnorms, float* norms) {
+  const int levels = 1 << bits;
+  const int row_bytes = (d * bits + 7) / 8, sign_bytes = (d + 7) / 8;
+  tq_encode(x, n, rot, d, bits, cb, cb_scale, codes, norms);
+  double c[16];
+  for (int v = 0; v < levels; ++v) c[v] = (double)cb_scale * (double)cb[v];
+  double* u = (double*)malloc(sizeof(double) * (size_t)d);
+  double* r = (double*)malloc(sizeof(double) * (size_t)d);
+  for (int64_t i = 0; i < n; ++i) {
+    const float* xi = x + (size_t)i * d;
+    double ss = 0.0;
+    for (int k = 0; k < d; ++k) ss = fma((double)xi[k], (double)xi[k], ss);
+    const double nrm = sqrt(ss);
+    for (int j = 0; j < d; ++j) {
+      if (rot == NULL) {
+        u[j] = (double)xi[j];
+        continue;
+      }
+      double acc = 0.0;
+      for (int k = 0; k < d; ++k) acc = fma((double)rot[(size_t)j * d + k], (double)xi[k], acc);
+      u[j] = acc;
+    }
+    const uint8_t* row = codes + (size_t)i * row_bytes;
+    double rn = 0.0;
+    for (int j = 0; j < d; ++j) {
+      const int code = (row[(j * bits) >> 3] >> ((j * bits) & 7)) & (levels - 1);
+      r[j] = u[j] - nrm * c[code];
+      rn = fma(r[j], r[j], rn);
+    }
+    resnorms[i] = nrm > 0.0 ? (float)(sqrt(rn) / nrm) : 0.0f;
+    uint8_t* sg = signs + (size_t)i * sign_bytes;
+    memset(sg, 0, (size_t)sign_bytes);
+    for (int s = 0; s < d; ++s) {
+      double p = 0.0;
+      for (int j = 0; j < d; ++j) p = fma((double)qjl[(size_t)s * d + j], r[j], p);
+      if (p >= 0.0) sg[s >> 3] |= (uint8_t)(1u << (s & 7));
+    }
+  }
+  free(u);
+  free(r);
+}
+
+void tq_ip_prepare(const float* q, const float* rot, const float* qjl, int d, int qmax,
+                   float cb_scale, int16_t* qs, float* alpha, int16_t* ys, float* beta) {
+  tq_prepare(q, rot, d, qmax, cb_scale, qs, alpha);
+  double* qr = (double*)malloc(sizeof(double) * (size_t)d);
+  for (int j = 0; j < d; ++j) {
+    double acc = 0.0;
+    if (rot != NULL) {
+      for (int k = 0; k < d; ++k) acc = fma((double)rot[(size_t)j * d + k], (double)q[k], acc);
+    } else {
+      acc = (double)q[j];
+    }
+    qr[j] = acc;
+  }
+  double* y = (double*)malloc(sizeof(double) * (size_t)d);
+  double maxabs = 0.0;
+  for (int s = 0; s < d; ++s) {
+    double acc = 0.0;
+    for (int j = 0; j < d; ++j) acc = fma((double)qjl[(size_t)s * d + j], qr[j], acc);
+    y[s] = acc;
+    if (fabs(acc) > maxabs) maxabs = fabs(acc);
+  }
+  const int qmax2 = tq_qjl_qmax(d);
+  const double inv = maxabs > 0.0 ? (double)qmax2 / maxabs : 0.0;
+  for (int s = 0; s < d; ++s) {
+    double v = rint(y[s] * inv);
+    if (v > qmax2) v = qmax2;
+    if (v < -qmax2) v = -qmax2;
+    ys[s] = (int16_t)v;
+  }
+  const double half_pi = 1.5707963267948966;
+  *beta = maxabs > 0.0 ? (float)((maxabs / (double)qmax2) * sqrt(half_pi) / (double)d) : 0.0f;
+  free(qr);
+  free(y);
+}
+
+void tq_ip_scores(const float* queries, int nq, const float* rot, const float* qjl, int d,
+                  int bits, const int8_t* cb, float cb_scale, const uint8_t* codes,
+                  const uint8_t* signs, const float* resnorms, const float* norms, int64_t n,
+                  float* out) {
+  const int levels = 1 << bits;
+  const int qmax = tq_qmax(cb, levels, d);
+  const int row_bytes = (d * bits + 7) / 8, sign_bytes = (d + 7) / 8;
+  int16_t* qs = (int16_t*)malloc(sizeof(int16_t) * (size_t)d);
+  int16_t* ys = (int16_t*)malloc(sizeof(int16_t) * (size_t)d);
+  for (int q = 0; q < nq; ++q) {
+    float alpha, beta;
+    tq_ip_prepare(queries + (size_t)q * d, rot, qjl, d, qmax, cb_scale, qs, &alpha, ys, &beta);
+    for (int64_t i = 0; i < n; ++i) {
+      const uint8_t* row = codes + (size_t)i * row_bytes;
+      const uint8_t* sg = signs + (size_t)i * sign_bytes;
+      int32_t dm = 0, dq = 0;
+      for (int j = 0; j < d; ++j) {
+        dm += (int32_t)qs[j] * cb[(row[(j * bits) >> 3] >> ((j * bits) & 7)) & (levels - 1)];
+        dq += ((sg[j >> 3] >> (j & 7)) & 1) ? (int32_t)ys[j] : -(int32_t)ys[j];
+      }
+      const float t1 = (float)dm * alpha;
+      const float t2 = (float)dq * beta;
+      const float t3 = resnorms[i] * t2;
+      out[(size_t)q * n + i] = (t1 + t3) * norms[i];
+    }
+  }
+  free(qs);
+  free(ys);
+}
