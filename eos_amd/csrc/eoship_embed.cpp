@@ -27,6 +27,14 @@ struct EosHipEmbed {
     hipError_t e = hipMemsetAsync(status, 0, 4, rt->stream);
     if (e != hipSuccess) return hip_err(err, "hipMemsetAsync(status)", e);
     EmbedTinyArgs a{table, proj, d_tokens, d_out, status, n, vocab, dim, edim};
+    // 4 tokens per workgroup with the projection in LDS when it fits.
+    const size_t lds = (size_t)dim * edim * 2 + ((size_t)dim * 4 + (size_t)4 * edim) * 4;
+    if ((edim == 64 || edim == 128 || edim == 256) && dim % 8 == 0 && lds <= 150 * 1024) {
+      const char* name = edim == 64 ? "eos_embed_tiny_e64"
+                         : edim == 128 ? "eos_embed_tiny_e128" : "eos_embed_tiny_e256";
+      return rt->launch(name, dim3((unsigned)((n + 3) / 4)), dim3((unsigned)(4 * edim)), lds, &a,
+                        err);
+    }
     return rt->launch("eos_embed_tiny", dim3((unsigned)((n + 3) / 4)), dim3(256), 0, &a, err);
   }
 };

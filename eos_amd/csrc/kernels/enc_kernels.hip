@@ -1615,6 +1615,104 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
 
 // ------------------------------------------------------------- tiny embed
 
+// The same pipeline for kTinyTok tokens per workgroup when edim is 64, 128
+// or 256 and the projection fits LDS: the f16 projection is staged once per
+// workgroup (16-byte loads, several in flight per thread), the gathered rows
+// are held transposed (xs[k][token]) in f32, and each of the kTinyTok * edim
+// threads runs the k-ascending chain of one (token, output) pair (the
+// reference's order: one product, then one sum, per k); two or more
+// wavefronts per SIMD hide the LDS latency of the chains. The f64 sum of squares uses fma(v, v, ss): v * v of an f32 value is
+// exact in f64, so this is the reference's multiply-then-add bit for bit.
+// Dynamic LDS: dim * edim halves + dim * kTinyTok + kTinyTok * edim floats.
+constexpr int kTinyTok = 4;
+template <int EDIM>
+EOS_DEV void embed_tiny_lds(const EmbedTinyArgs& a) {
+  constexpr int NT = kTinyTok * EDIM;  // threads
+  extern __shared__ __attribute__((aligned(16))) unsigned char tiny_lds[];
+  uint16_t* pw = reinterpret_cast<uint16_t*>(tiny_lds);
+  float* xs = reinterpret_cast<float*>(tiny_lds + (size_t)a.dim * a.edim * 2);
+  float* ys = xs + (size_t)a.dim * kTinyTok;
+  __shared__ float nrm[kTinyTok];
+  __shared__ int toks[kTinyTok];
+  const int tid = threadIdx.x;
+  const int t0 = blockIdx.x * kTinyTok;
+  if (tid < kTinyTok) {
+    int tok = t0 + tid < a.n ? a.tokens[t0 + tid] : -1;
+    if (t0 + tid < a.n && (tok < 0 || tok >= a.vocab)) {
+      *a.status = 1;
+      tok = 0;
+    }
+    toks[tid] = tok;
+  }
+  // projection: [dim][edim] halves, 8 per 16-byte load, 8 loads of each
+  // thread in flight before any is stored (a load-store-load loop would wait
+  // one memory latency per load)
+  const int nvec = a.dim * a.edim / 8;
+  for (int base = tid; base < nvec; base += NT * 8) {
+    v4i buf[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + NT * u;
+      buf[u] = i < nvec ? reinterpret_cast<const v4i*>(a.proj)[i] : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + NT * u;
+      if (i < nvec) reinterpret_cast<v4i*>(pw)[i] = buf[u];
+    }
+  }
+  __syncthreads();
+  // the rows, 8 halves per 16-byte load (dim % 8 == 0), stored transposed
+  const int cpr = a.dim / 8, nch = kTinyTok * cpr;
+  for (int i = tid; i < nch; i += NT) {
+    const int t = i / cpr, c = i - t * cpr;
+    const int tok = toks[t];
+    const v4i raw = tok >= 0 ? *reinterpret_cast<const v4i*>(a.table + (size_t)tok * a.dim + 8 * c)
+                             : v4i{0, 0, 0, 0};
+    const v8h h = __builtin_bit_cast(v8h, raw);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xs[(8 * c + e) * kTinyTok + t] = (float)h[e];
+  }
+  __syncthreads();
+  {
+    const int e = tid % EDIM, t = tid / EDIM;
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < a.dim; ++k) {
+      const float p = xs[k * kTinyTok + t] * h2f(pw[k * EDIM + e]);
+      acc = acc + p;
+    }
+    ys[t * EDIM + e] = acc;
+  }
+  __syncthreads();
+  if (tid < kTinyTok) {
+    double ss = 0.0;
+#pragma unroll 8
+    for (int c = 0; c < EDIM; ++c) {
+      const double v = (double)ys[tid * EDIM + c];
+      ss = __builtin_fma(v, v, ss);
+    }
+    nrm[tid] = (float)sqrt(ss);
+  }
+  __syncthreads();
+  for (int i = tid; i < kTinyTok * EDIM; i += NT) {
+    const int t = i / EDIM, c = i - t * EDIM;
+    if (t0 + t >= a.n) continue;
+    const float v = ys[i], nv = nrm[t];
+    a.out[(size_t)(t0 + t) * EDIM + c] = f2h(nv == 0.0f ? v : v / nv);
+  }
+}
+
+extern "C" __global__ __launch_bounds__(kTinyTok * 64) void eos_embed_tiny_e64(EmbedTinyArgs a) {
+  embed_tiny_lds<64>(a);
+}
+extern "C" __global__ __launch_bounds__(kTinyTok * 128) void eos_embed_tiny_e128(EmbedTinyArgs a) {
+  embed_tiny_lds<128>(a);
+}
+extern "C" __global__ __launch_bounds__(kTinyTok * 256) void eos_embed_tiny_e256(EmbedTinyArgs a) {
+  embed_tiny_lds<256>(a);
+}
+
 // examples/embed.eos on one wavefront per token: gather (tensor_ops.go:
 // 938-1166), f32 matmul with k ascending and separate multiply / add
 // (matmulTensor, tensor_ops.go:1168-1249), then normalizeRows
