@@ -1663,12 +1663,15 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
         for (int h = 0; h < SPL; ++h) {
           const int s = c * SPL + h;
           if (s < KS) {
+            // The step's query fragments are read together, so their LDS
+            // latencies overlap instead of one wait per MFMA.
+            v4i bf[NCB];
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) bf[cb] = sb[(s * NCB + cb) * 64 + boff];
             const v4i af = decode_step<BITS>(raw[c], h, la);
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) {
-              const v4i bf = sb[(s * NCB + cb) * 64 + boff];
-              acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, acc[cb], 0, 0, 0);
-            }
+            for (int cb = 0; cb < NCB; ++cb)
+              acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[cb], acc[cb], 0, 0, 0);
           }
         }
       }
@@ -1707,9 +1710,12 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
 
 }  // namespace
 
+// A 256-register budget (two waves per SIMD) keeps the accumulators in
+// ordinary VGPRs: the epilogue then reads them directly instead of copying
+// each element out of the accumulation registers.
 #define EOS_TQ_MAXSIM(BITS, KS, NQG)                                                        \
-  extern "C" __global__ __launch_bounds__(kScanThreads) void eos_tq_maxsim_b##BITS##_k##KS##_g##NQG( \
-      TqMaxsimArgs a) {                                                                     \
+  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2))) \
+  void eos_tq_maxsim_b##BITS##_k##KS##_g##NQG(TqMaxsimArgs a) {                              \
     tq_maxsim_body<BITS, KS, NQG>(a);                                                       \
   }
 
