@@ -46,6 +46,10 @@ struct Runtime {
   // `label` names the launch in profiles (defaults to the kernel name).
   int launch(const char* name, dim3 grid, dim3 block, size_t lds, void* args, char** err,
              const char* label = nullptr);
+  // Workgroups of `block` threads and `lds` dynamic LDS bytes that one CU
+  // holds at once for kernel `name` (its register and LDS use); cached.
+  std::unordered_map<std::string, int> occupancy;
+  int blocks_per_cu(const char* name, int block, size_t lds, int* out, char** err);
   int alloc(size_t bytes, void** p, char** err);
   // A device workspace owned by the runtime, grown (never shrunk) on demand
   // and reused by later calls on the same stream; freed with the runtime.

@@ -97,6 +97,23 @@ int Runtime::launch(const char* name, dim3 grid, dim3 block, size_t lds, void* a
   return 0;
 }
 
+int Runtime::blocks_per_cu(const char* name, int block, size_t lds, int* out, char** err) {
+  const auto it = occupancy.find(name);
+  if (it != occupancy.end()) {
+    *out = it->second;
+    return 0;
+  }
+  hipFunction_t f = nullptr;
+  if (function(name, &f, err) != 0) return 1;
+  int n = 0;
+  const hipError_t e = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, block, lds);
+  if (e != hipSuccess) return hip_err(err, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor", e);
+  if (n < 1) n = 1;
+  occupancy.emplace(name, n);
+  *out = n;
+  return 0;
+}
+
 int Runtime::take_event(hipEvent_t* ev, char** err) {
   if (!event_pool.empty()) {
     *ev = event_pool.back();

@@ -304,8 +304,12 @@ struct EosHipTQ {
     m.lut3 = lut[3];
     char name[64];
     snprintf(name, sizeof(name), "eos_tq_maxsim_b%d_k%d_g%d", bits, ks, nqg);
+    // As many resident workgroups as the kernel's registers allow (three
+    // waves per SIMD for most variants), each wave striding over documents.
+    int per_cu = 2;
+    if (rt->blocks_per_cu(name, 256, 0, &per_cu, err) != 0) return 1;
     int64_t blocks = (ndocs + 3) / 4;
-    const int64_t maxb = (int64_t)rt->compute_units * 2;
+    const int64_t maxb = (int64_t)rt->compute_units * per_cu;
     if (blocks > maxb) blocks = maxb;
     if (blocks < 1) blocks = 1;
     return rt->launch(name, dim3((unsigned)blocks), dim3(256), 0, &m, err, "tq_maxsim");

@@ -1612,6 +1612,17 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
 
 namespace {
 
+// Token maxima of one query group over a tile's 16 rows of the lane: the
+// exact score ((float)(256 hi + lo) * alpha) * norm of each (row, token).
+EOS_DEV void maxsim_epilogue(float& mx, const v16i& hi, const v16i& lo, float al,
+                             const float (&nrm)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int dot = hi[i] * 256 + lo[i];
+    mx = fmaxf(mx, ((float)dot * al) * nrm[i]);
+  }
+}
+
 template <int BITS, int KS, int NQG>
 EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
   constexpr int NCB = 2 * NQG;
@@ -1654,27 +1665,6 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
       }
       int boff = lane;
       asm volatile("" : "+v"(boff));
-      v16i acc[NCB];
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
-#pragma unroll
-      for (int c = 0; c < NLOAD; ++c) {
-#pragma unroll
-        for (int h = 0; h < SPL; ++h) {
-          const int s = c * SPL + h;
-          if (s < KS) {
-            // The step's query fragments are read together, so their LDS
-            // latencies overlap instead of one wait per MFMA.
-            v4i bf[NCB];
-#pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) bf[cb] = sb[(s * NCB + cb) * 64 + boff];
-            const v4i af = decode_step<BITS>(raw[c], h, la);
-#pragma unroll
-            for (int cb = 0; cb < NCB; ++cb)
-              acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[cb], acc[cb], 0, 0, 0);
-          }
-        }
-      }
       float nrm[16];
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
@@ -1685,13 +1675,60 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
       }
       // The score's "+ 0.0f" (-0 -> +0) commutes with the maximum (fmaxf
       // treats the zeros as equal), so it is applied once to the token max.
+      v16i acc[NCB];
+      if constexpr (KS <= 8) {
+        // Short K: every step's code fragment is decoded once up front, then
+        // the query groups run one after another; group g's MFMAs are
+        // followed by the exact epilogue of group g - 1, which does not
+        // depend on them (and only two query fragments are live at a time).
+        v4i af[KS];
 #pragma unroll
-      for (int g = 0; g < NQG; ++g) {
+        for (int c = 0; c < NLOAD; ++c) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int dot = acc[2 * g][i] * 256 + acc[2 * g + 1][i];
-          mx[g] = fmaxf(mx[g], ((float)dot * al[g]) * nrm[i]);
+          for (int h = 0; h < SPL; ++h) {
+            const int s = c * SPL + h;
+            if (s < KS) af[s] = decode_step<BITS>(raw[c], h, la);
+          }
         }
+#pragma unroll
+        for (int g = 0; g <= NQG; ++g) {
+          if (g < NQG) {
+            acc[2 * g] = v16i{0};
+            acc[2 * g + 1] = v16i{0};
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+              const v4i bh = sb[(s * NCB + 2 * g) * 64 + boff];
+              const v4i bl = sb[(s * NCB + 2 * g + 1) * 64 + boff];
+              acc[2 * g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bh, acc[2 * g], 0, 0, 0);
+              acc[2 * g + 1] =
+                  __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bl, acc[2 * g + 1], 0, 0, 0);
+            }
+          }
+          if (g > 0) maxsim_epilogue(mx[g - 1], acc[2 * g - 2], acc[2 * g - 1], al[g - 1], nrm);
+        }
+      } else {
+        // Long K: steps outer, each step's code fragment decoded once and its
+        // query fragments read together before its MFMAs.
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
+#pragma unroll
+        for (int c = 0; c < NLOAD; ++c) {
+#pragma unroll
+          for (int h = 0; h < SPL; ++h) {
+            const int s = c * SPL + h;
+            if (s < KS) {
+              v4i bf[NCB];
+#pragma unroll
+              for (int cb = 0; cb < NCB; ++cb) bf[cb] = sb[(s * NCB + cb) * 64 + boff];
+              const v4i af = decode_step<BITS>(raw[c], h, la);
+#pragma unroll
+              for (int cb = 0; cb < NCB; ++cb)
+                acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[cb], acc[cb], 0, 0, 0);
+            }
+          }
+        }
+#pragma unroll
+        for (int g = 0; g < NQG; ++g) maxsim_epilogue(mx[g], acc[2 * g], acc[2 * g + 1], al[g], nrm);
       }
 #pragma unroll
       for (int c = 0; c < NLOAD; ++c) raw[c] = nraw[c];
@@ -1710,11 +1747,12 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
 
 }  // namespace
 
-// A 256-register budget (two waves per SIMD) keeps the accumulators in
-// ordinary VGPRs: the epilogue then reads them directly instead of copying
-// each element out of the accumulation registers.
+// A budget of three waves per SIMD (<= 168 VGPRs) keeps the accumulators in
+// ordinary VGPRs (the epilogue reads them directly instead of copying each
+// element out of the accumulation registers) and lets a third wave's VALU
+// fill the gaps of the other two.
 #define EOS_TQ_MAXSIM(BITS, KS, NQG)                                                        \
-  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(2))) \
+  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(3))) \
   void eos_tq_maxsim_b##BITS##_k##KS##_g##NQG(TqMaxsimArgs a) {                              \
     tq_maxsim_body<BITS, KS, NQG>(a);                                                       \
   }
