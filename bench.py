@@ -408,6 +408,7 @@ def maxsim_leg(rt, steps: int, cpu: bool = True) -> dict:
                      "kernel": "tq_maxsim", "avg_launch_ms": avg, "launches_per_batch": n_scan,
                      "int8_ops_per_launch": ops_per_launch, "bytes_per_launch": bytes_per_pass,
                      "hbm_gbs": hbm_gbs, "hbm_frac": hbm_gbs / HBM_PEAK_GBS},
+        "select_ms_per_batch": ms_sel,
     }
     if cpu:
         out["cpu_baseline"] = maxsim_cpu_baseline(corpus, q, doc_len, ndocs)

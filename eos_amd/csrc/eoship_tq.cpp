@@ -132,6 +132,22 @@ struct EosHipTQ {
   int64_t samp_tiles = 0;
   float* dense = nullptr;
   size_t dense_bytes = 0;
+  // MaxSim query preparation for a whole chunk of queries (every pass reads
+  // its column blocks from it): fragments [ks][ms_ncb][64][16], alpha and the
+  // f64 rotated columns of 32 * ms_ncb / 2 token columns
+  int8_t* ms_bfrag = nullptr;
+  size_t ms_bfrag_bytes = 0;
+  float* ms_alpha = nullptr;
+  size_t ms_alpha_bytes = 0;
+  double* ms_qrot = nullptr;
+  size_t ms_qrot_bytes = 0;
+  int ms_ncb = 0;
+  // chunked row selection: per-chunk top-k keys, then per row the list
+  // length and finalize status
+  unsigned long long* sel_keys = nullptr;
+  size_t sel_keys_bytes = 0;
+  uint32_t* sel_aux = nullptr;
+  size_t sel_aux_bytes = 0;
   int32_t* dense_dots = nullptr;
   size_t dense_dots_bytes = 0;
   int16_t* qs_buf = nullptr;
@@ -155,8 +171,8 @@ struct EosHipTQ {
   int* corpus_refs = nullptr;
 
   void free_all() {
-    void* scratch[] = {qrot, bfrag, alpha, tau, cand, cand_count, status,
-                       samp, dense, dense_dots, qs_buf, lonorm, io};
+    void* scratch[] = {qrot, bfrag, alpha, tau, cand, cand_count, status, samp, dense, dense_dots,
+                       qs_buf, lonorm, io, sel_keys, sel_aux, ms_bfrag, ms_alpha, ms_qrot};
     for (void* p : scratch)
       if (p) hipFree(p);
     if (corpus_refs != nullptr && --*corpus_refs > 0) return;
@@ -249,12 +265,22 @@ struct EosHipTQ {
                    int16_t* qs_out, char** err) {
     TqPrepArgs p;
     memset(&p, 0, sizeof(p));
-    p.queries = d_src;
-    p.rot_t = rot_t;
     p.bfrag = bfrag;
     p.alpha = alpha;
     p.tau = tau;
     p.cand_count = cand_count;
+    p.qrot = qrot;
+    p.lonorm = lonorm;
+    return prepare_into(&p, d_src, nsrc, nqg, group, group_live, qs_out, err);
+  }
+
+  // prepare_cols into the output buffers p already names (tau, cand_count
+  // and lonorm may be NULL).
+  int prepare_into(TqPrepArgs* pp, const float* d_src, int nsrc, int nqg, int group,
+                   int group_live, int16_t* qs_out, char** err) {
+    TqPrepArgs& p = *pp;
+    p.queries = d_src;
+    p.rot_t = rot_t;
     p.qs_out = qs_out;
     p.q = nsrc;
     p.d = d;
@@ -262,10 +288,8 @@ struct EosHipTQ {
     p.ncb = 2 * nqg;
     p.qmax = qmax;
     p.cb_scale = cb_scale;
-    p.qrot = qrot;
     p.group = group;
     p.group_live = group_live;
-    p.lonorm = lonorm;
     const unsigned cblocks = (unsigned)(32 * nqg / 8);  // 8 columns per workgroup
     if (rot_t != nullptr) {
       const unsigned jblocks = (unsigned)((d + 31) / 32);
@@ -280,18 +304,42 @@ struct EosHipTQ {
 
   int maxsim_nqg() const { return ks <= 8 ? 4 : ks <= 24 ? 2 : 1; }
 
-  // Doc scores of qp queries (tq tokens each, source rows [qp * tq][d]) for
-  // documents [doc_begin, doc_begin + ndocs) into out [qp][ndocs].
-  int maxsim_pass(const float* d_src, int qp, int tq, int doc_len, int64_t doc_begin,
-                  int64_t ndocs, float* out, char** err) {
+  // Prepares nq queries of tq tokens (source rows [nq * tq][d]) at once: query
+  // g is the 32-column group g (tokens past tq are zero columns), rounded up
+  // to whole passes of maxsim_nqg() groups.
+  int maxsim_prepare(const float* d_src, int nq, int tq, char** err) {
+    const int per = maxsim_nqg();
+    const int groups = (nq + per - 1) / per * per;
+    const size_t cols = (size_t)groups * 32;
+    if (ensure(reinterpret_cast<void**>(&ms_bfrag), &ms_bfrag_bytes, (size_t)ks * 2 * groups * 64 * 16,
+               err) != 0 ||
+        ensure(reinterpret_cast<void**>(&ms_alpha), &ms_alpha_bytes, cols * sizeof(float), err) != 0 ||
+        (rot_t != nullptr && ensure(reinterpret_cast<void**>(&ms_qrot), &ms_qrot_bytes,
+                                    cols * (size_t)d * sizeof(double), err) != 0))
+      return 1;
+    ms_ncb = 2 * groups;
+    TqPrepArgs p;
+    memset(&p, 0, sizeof(p));
+    p.bfrag = ms_bfrag;
+    p.alpha = ms_alpha;
+    p.qrot = ms_qrot;
+    return prepare_into(&p, d_src, nq * tq, groups, 32, tq, nullptr, err);
+  }
+
+  // Doc scores of the prepared queries [q0, q0 + qp) (qp <= maxsim_nqg(),
+  // q0 a multiple of it) for documents [doc_begin, doc_begin + ndocs) into
+  // out [qp][ndocs].
+  int maxsim_pass(int q0, int qp, int doc_len, int64_t doc_begin, int64_t ndocs, float* out,
+                  char** err) {
     const int nqg = maxsim_nqg();
-    if (prepare_cols(d_src, qp * tq, nqg, 32, tq, nullptr, err) != 0) return 1;
     TqMaxsimArgs m;
     memset(&m, 0, sizeof(m));
     m.packed = static_cast<const int32_t*>(packed);
     m.norms = norms;
-    m.bfrag = bfrag;
-    m.alpha = alpha;
+    m.bfrag = ms_bfrag;
+    m.alpha = ms_alpha + (size_t)q0 * 32;
+    m.frag_ncb = ms_ncb;
+    m.frag_cb0 = 2 * q0;
     m.out = out;
     m.doc_begin = doc_begin;
     m.ndocs = ndocs;
@@ -1005,6 +1053,57 @@ int maxsim_check(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, int32_t q, in
   return 0;
 }
 
+// Top kk of each of `rows` score rows [rows][n] by (score desc, index asc)
+// into ids / scores [rows][kk]. With few rows, each row is split into
+// chunks so that about one workgroup per CU selects: every chunk's exact
+// top kk (keys unique, so exactly kk or the whole chunk), then
+// eos_tq_finalize merges each row's nchunks * kk keys; with many rows (or
+// a kk too large to merge) one workgroup ranks each row.
+int rank_rows(EosHipRuntime* rt, EosHipTQ* tq, const float* d_rows, int rows, int64_t n, int kk,
+              int64_t* d_ids, float* d_scores, char** err) {
+  TqSelectArgs sel;
+  memset(&sel, 0, sizeof(sel));
+  sel.rows = d_rows;
+  sel.ids = reinterpret_cast<long long*>(d_ids);
+  sel.scores = d_scores;
+  sel.n = n;
+  sel.stride = n;
+  sel.kk = kk;
+  sel.nrows = rows;
+  int64_t chunks = std::max<int64_t>(1, rt->compute_units / rows);
+  chunks = std::min<int64_t>(chunks, kSortCap / kk);
+  chunks = std::min<int64_t>(chunks, n / std::max<int64_t>(4 * (int64_t)kk, 2048));
+  if (chunks <= 1) {
+    sel.mode = 1;
+    return rt->launch("eos_tq_row_select", dim3(rows), dim3(1024), 0, &sel, err,
+                      "tq_maxsim_select");
+  }
+  const int nch = (int)chunks;
+  if (tq->ensure(reinterpret_cast<void**>(&tq->sel_keys), &tq->sel_keys_bytes,
+                 (size_t)rows * nch * kk * sizeof(unsigned long long), err) != 0 ||
+      tq->ensure(reinterpret_cast<void**>(&tq->sel_aux), &tq->sel_aux_bytes,
+                 (size_t)rows * 2 * sizeof(uint32_t), err) != 0)
+    return 1;
+  sel.mode = 2;
+  sel.nchunks = nch;
+  sel.keys_out = tq->sel_keys;
+  sel.counts_out = tq->sel_aux;
+  if (rt->launch("eos_tq_row_select", dim3(rows, nch), dim3(1024), 0, &sel, err,
+                 "tq_maxsim_select") != 0)
+    return 1;
+  TqFinalizeArgs f;
+  memset(&f, 0, sizeof(f));
+  f.cand = tq->sel_keys;
+  f.cand_count = tq->sel_aux;
+  f.ids = reinterpret_cast<long long*>(d_ids);
+  f.scores = d_scores;
+  f.status = reinterpret_cast<int*>(tq->sel_aux + rows);
+  f.cap = nch * kk;
+  f.kk = kk;
+  f.q = rows;
+  return rt->launch("eos_tq_finalize", dim3(rows), dim3(256), 0, &f, err, "tq_maxsim_select_merge");
+}
+
 int maxsim_topk_impl(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const float* d_queries,
                      int32_t q, int32_t tq_tokens, int32_t k, int64_t* d_ids, float* d_scores,
                      char** err) {
@@ -1028,23 +1127,16 @@ int maxsim_topk_impl(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const flo
     return 1;
   for (int c0 = 0; c0 < q; c0 += chunk) {
     const int cq = std::min(chunk, q - c0);
-    for (int q0 = c0; q0 < c0 + cq; q0 += per) {
-      const int qp = std::min(per, c0 + cq - q0);
-      if (tq->maxsim_pass(d_queries + (size_t)q0 * tq_tokens * tq->d, qp, tq_tokens, doc_len, 0,
-                          ndocs, tq->dense + (size_t)(q0 - c0) * ndocs, err) != 0)
+    // One preparation for every pass of the chunk.
+    if (tq->maxsim_prepare(d_queries + (size_t)c0 * tq_tokens * tq->d, cq, tq_tokens, err) != 0)
+      return 1;
+    for (int q0 = 0; q0 < cq; q0 += per) {
+      const int qp = std::min(per, cq - q0);
+      if (tq->maxsim_pass(q0, qp, doc_len, 0, ndocs, tq->dense + (size_t)q0 * ndocs, err) != 0)
         return 1;
     }
-    TqSelectArgs sel;
-    memset(&sel, 0, sizeof(sel));
-    sel.rows = tq->dense;
-    sel.ids = reinterpret_cast<long long*>(d_ids + (size_t)c0 * kk);
-    sel.scores = d_scores + (size_t)c0 * kk;
-    sel.n = ndocs;
-    sel.stride = ndocs;
-    sel.kk = kk;
-    sel.mode = 1;
-    sel.nrows = cq;
-    if (rt->launch("eos_tq_row_select", dim3(cq), dim3(1024), 0, &sel, err, "tq_maxsim_select") != 0)
+    if (rank_rows(rt, tq, tq->dense, cq, ndocs, kk, d_ids + (size_t)c0 * kk,
+                  d_scores + (size_t)c0 * kk, err) != 0)
       return 1;
   }
   return 0;
@@ -1110,8 +1202,8 @@ int eoship_tq_maxsim_scores(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, co
     return 1;
   for (int q0 = 0; q0 < q; q0 += per) {
     const int qp = std::min(per, q - q0);
-    if (tq->maxsim_pass(dq + (size_t)q0 * tq_tokens * tq->d, qp, tq_tokens, doc_len, doc_begin,
-                        doc_count, tq->dense, err) != 0)
+    if (tq->maxsim_prepare(dq + (size_t)q0 * tq_tokens * tq->d, qp, tq_tokens, err) != 0 ||
+        tq->maxsim_pass(0, qp, doc_len, doc_begin, doc_count, tq->dense, err) != 0)
       return 1;
     e = hipMemcpyAsync(scores + (size_t)q0 * doc_count, tq->dense,
                        (size_t)qp * doc_count * sizeof(float), hipMemcpyDeviceToHost, rt->stream);

@@ -70,6 +70,13 @@ struct TqSelectArgs {
   int mode;                // 0: tau = score of the kk-th best; 1: sorted top-kk
   int nrows;
   const long long* id_map; // mode 1, optional [n]: element i is reported as id id_map[i]
+  // mode 2: each row is split into nchunks equal chunks (grid.y); a chunk's
+  // top-kk rank keys go unsorted to keys_out[(row * nchunks + chunk) * kk ..],
+  // padded with 0 (below every rank key), and chunk 0 sets counts_out[row] =
+  // nchunks * kk (the list length eos_tq_finalize merges).
+  int nchunks;
+  unsigned long long* keys_out;
+  uint32_t* counts_out;
 };
 
 struct TqFinalizeArgs {
@@ -97,6 +104,9 @@ struct TqMaxsimArgs {
   int tiles_per_doc;
   int groups;              // live query groups (<= nqg)
   uint32_t lut0, lut1, lut2, lut3;
+  // bfrag holds the fragments of every prepared query, [ks][frag_ncb][64];
+  // this pass uses column blocks [frag_cb0, frag_cb0 + 2 nqg).
+  int frag_ncb, frag_cb0;
 };
 
 // Parent (multivector) aggregation over child scores: parent p owns children

@@ -163,8 +163,8 @@ EOS_DEV void prep_quantize_column(const TqPrepArgs& a, int c, int t, Get get) {
   if (t == 0) {
     if (a.lonorm != nullptr) a.lonorm[c] = sqrt_up(lo2);
     a.alpha[c] = mx > 0.0 ? (float)((mx / (double)a.qmax) * (double)a.cb_scale) : 0.0f;
-    a.tau[c] = -__builtin_inff();
-    a.cand_count[c] = 0u;
+    if (a.tau != nullptr) a.tau[c] = -__builtin_inff();
+    if (a.cand_count != nullptr) a.cand_count[c] = 0u;
   }
 }
 
@@ -1251,37 +1251,50 @@ EOS_DEV void bitonic_sort_desc(u64* list, int npow) {
 }  // namespace
 
 // Exact radix selection of the kk-th best element of a score row by its
-// composite rank key (8 passes of 8-bit digits; keys are unique, so exactly
-// kk elements are >= the selected key). One workgroup per row.
+// composite rank key (up to 8 passes of 8-bit digits; keys are unique, so
+// exactly kk elements are >= the selected key). One workgroup per row, or
+// per (row, chunk) in mode 2.
 extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_row_select(TqSelectArgs a) {
   __shared__ uint32_t hist[256];
   __shared__ u64 sel_prefix;
   __shared__ int sel_rem;
+  __shared__ int sel_done;
   __shared__ int list_n;
   __shared__ u64 list[kSortCap];
   const int row = blockIdx.x;
   if (row >= a.nrows) return;
   if (a.mode == 1 && a.status != nullptr && a.status[row] == 0) return;
-  const float* x = a.rows + (size_t)row * a.stride;
   const int tid = threadIdx.x;
   if (a.kk <= 0 || a.n <= 0) return;
-  if (a.mode == 0 && (long long)a.kk > a.n) {
+  // Elements [c0, c0 + n) of the row: the whole row, or one chunk in mode 2.
+  long long c0 = 0, n = a.n;
+  if (a.mode == 2) {
+    const long long per = (a.n + a.nchunks - 1) / a.nchunks;
+    c0 = (long long)blockIdx.y * per;
+    n = c0 < a.n ? (a.n - c0 < per ? a.n - c0 : per) : 0ll;
+    if (blockIdx.y == 0 && tid == 0) a.counts_out[row] = (uint32_t)(a.nchunks * a.kk);
+  }
+  const float* x = a.rows + (size_t)row * a.stride + c0;
+  if (a.mode == 0 && (long long)a.kk > n) {
     if (tid == 0) a.tau[row] = -__builtin_inff();
     return;
   }
-  const int passes = a.mode == 0 ? 4 : 8;
+  // A chunk of at most kk elements is kept whole (threshold 0).
+  const int passes = a.mode == 0 ? 4 : ((long long)a.kk >= n ? 0 : 8);
   if (tid == 0) {
     sel_prefix = 0ull;
     sel_rem = a.kk;
+    sel_done = 0;
   }
-  for (int p = 0; p < passes; ++p) {
+  __syncthreads();
+  for (int p = 0; p < passes && sel_done == 0; ++p) {
     const int shift = 56 - 8 * p;
     for (int b = tid; b < 256; b += kSelThreads) hist[b] = 0u;
     __syncthreads();
     const u64 pfx = sel_prefix;
     const u64 hmask = p == 0 ? 0ull : ~((1ull << (shift + 8)) - 1ull);
-    for_each_batched<kSelThreads, 8>(x, a.n, [&](long long i, float v) {
-      const u64 c = rank_key(v, (uint32_t)i);
+    for_each_batched<kSelThreads, 8>(x, n, [&](long long i, float v) {
+      const u64 c = rank_key(v, (uint32_t)(c0 + i));
       if (((c ^ pfx) & hmask) == 0ull) atomicAdd(&hist[(c >> shift) & 255u], 1u);
     });
     __syncthreads();
@@ -1299,6 +1312,9 @@ extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_row_select(TqSe
       }
       sel_rem = rem;
       sel_prefix = pfx | ((u64)digit << shift);
+      // Selecting a set (modes 1, 2): once every element under the prefix
+      // is needed, the keys >= the prefix (lower digits 0) are exactly kk.
+      if (a.mode != 0 && hist[digit] == (uint32_t)rem) sel_done = 1;
     }
     __syncthreads();
   }
@@ -1307,20 +1323,25 @@ extern "C" __global__ __launch_bounds__(kSelThreads) void eos_tq_row_select(TqSe
     if (tid == 0) a.tau[row] = key_score((uint32_t)(thr >> 32));
     return;
   }
-  // mode 1: gather the kk elements >= thr and sort them.
+  // modes 1, 2: gather the (at most) kk elements >= thr.
   int npow = 1;
   while (npow < a.kk) npow <<= 1;
   if (tid == 0) list_n = 0;
   for (int i = tid; i < npow; i += kSelThreads) list[i] = 0ull;
   __syncthreads();
-  for_each_batched<kSelThreads, 8>(x, a.n, [&](long long i, float v) {
-    const u64 c = rank_key(v, (uint32_t)i);
+  for_each_batched<kSelThreads, 8>(x, n, [&](long long i, float v) {
+    const u64 c = rank_key(v, (uint32_t)(c0 + i));
     if (c >= thr) {
       const int pos = atomicAdd(&list_n, 1);
       if (pos < kSortCap) list[pos] = c;
     }
   });
   __syncthreads();
+  if (a.mode == 2) {
+    u64* out = a.keys_out + ((size_t)row * a.nchunks + blockIdx.y) * a.kk;
+    for (int i = tid; i < a.kk; i += kSelThreads) out[i] = list[i];
+    return;
+  }
   bitonic_sort_desc(list, npow);
   for (int i = tid; i < a.kk; i += kSelThreads) {
     const u64 c = list[i];
@@ -1628,16 +1649,39 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
   constexpr int NCB = 2 * NQG;
   constexpr int SPL = 8 / BITS;
   constexpr int NLOAD = (KS + SPL - 1) / SPL;
+  constexpr int NWV = kScanThreads / 64;
   __shared__ v4i sb[KS * NCB * 64];
+  __shared__ float4 nstage[NWV][8];
   {
-    stage_fragments<kScanThreads, KS * NCB * 64>(sb, reinterpret_cast<const v4i*>(a.bfrag));
+    // The pass's column blocks [frag_cb0, frag_cb0 + NCB) of each K step
+    // (fragments laid out [ks][frag_ncb][64] for all queries prepared).
+    constexpr int COUNT = KS * NCB * 64;
+    constexpr int PER = (COUNT + kScanThreads - 1) / kScanThreads;
+    const v4i* src = reinterpret_cast<const v4i*>(a.bfrag);
+    v4i v[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int i = threadIdx.x + r * kScanThreads;
+      const int s = i / (NCB * 64), rem = i - s * (NCB * 64);
+      if (i < COUNT) v[r] = src[((size_t)s * a.frag_ncb + a.frag_cb0) * 64 + rem];
+    }
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int i = threadIdx.x + r * kScanThreads;
+      if (i < COUNT) sb[i] = v[r];
+    }
   }
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  // Wave-uniform tile indices keep the tile addressing in scalar registers.
+  // Wave-uniform document and tile indices live in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = gridDim.x * (kScanThreads / 64);
+  const long long nw = (long long)gridDim.x * NWV;
   const int half = lane >> 5;
+  const int tpd = a.tiles_per_doc;
+  // Wave w scores documents w, w + nw, ... (no barrier follows).
+  const long long doc0 = (long long)blockIdx.x * NWV + wave;
+  if (doc0 >= a.ndocs) return;
+  const long long last_doc = doc0 + (a.ndocs - 1 - doc0) / nw * nw;
   const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
   TqScanArgs la;  // lookup tables for decode_step
   la.lut0 = a.lut0;
@@ -1647,102 +1691,136 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
   float al[NQG];
 #pragma unroll
   for (int g = 0; g < NQG; ++g) al[g] = a.alpha[g * 32 + (lane & 31)];
-  for (long long doc = blockIdx.x * (kScanThreads / 64) + wave; doc < a.ndocs; doc += nw) {
-    float mx[NQG];
-#pragma unroll
-    for (int g = 0; g < NQG; ++g) mx[g] = -__builtin_inff();
-    const long long t0 = (a.doc_begin + doc) * a.tiles_per_doc;
+  // The wave's tiles form one stream of (document, tile) steps, loaded one
+  // step ahead through two register stages that are never copied (a copy of
+  // a register still being loaded would wait for every load issued before
+  // it). Every phase issues the same loads (past the wave's last step they
+  // repeat its last tile), so each wait covers exactly the stage it needs. A
+  // stage holds the tile's codes and one norm per lane (row lane % 32).
+  struct Stage {
     v4i raw[NLOAD];
-    float4 nrm4[4];
-    load_tile_codes<NLOAD>(raw, packed, t0, lane);
-    load_tile_norms(nrm4, a.norms, t0, half);
-    for (int t = 0; t < a.tiles_per_doc; ++t) {
-      v4i nraw[NLOAD];
-      float4 nnrm4[4];
-      if (t + 1 < a.tiles_per_doc) {
-        load_tile_codes<NLOAD>(nraw, packed, t0 + t + 1, lane);
-        load_tile_norms(nnrm4, a.norms, t0 + t + 1, half);
-      }
-      int boff = lane;
-      asm volatile("" : "+v"(boff));
-      float nrm[16];
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        nrm[4 * i4 + 0] = nrm4[i4].x;
-        nrm[4 * i4 + 1] = nrm4[i4].y;
-        nrm[4 * i4 + 2] = nrm4[i4].z;
-        nrm[4 * i4 + 3] = nrm4[i4].w;
-      }
-      // The score's "+ 0.0f" (-0 -> +0) commutes with the maximum (fmaxf
-      // treats the zeros as equal), so it is applied once to the token max.
-      v16i acc[NCB];
-      if constexpr (KS <= 8) {
-        // Short K: every step's code fragment is decoded once up front, then
-        // the query groups run one after another; group g's MFMAs are
-        // followed by the exact epilogue of group g - 1, which does not
-        // depend on them (and only two query fragments are live at a time).
-        v4i af[KS];
-#pragma unroll
-        for (int c = 0; c < NLOAD; ++c) {
-#pragma unroll
-          for (int h = 0; h < SPL; ++h) {
-            const int s = c * SPL + h;
-            if (s < KS) af[s] = decode_step<BITS>(raw[c], h, la);
-          }
-        }
-#pragma unroll
-        for (int g = 0; g <= NQG; ++g) {
-          if (g < NQG) {
-            acc[2 * g] = v16i{0};
-            acc[2 * g + 1] = v16i{0};
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-              const v4i bh = sb[(s * NCB + 2 * g) * 64 + boff];
-              const v4i bl = sb[(s * NCB + 2 * g + 1) * 64 + boff];
-              acc[2 * g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bh, acc[2 * g], 0, 0, 0);
-              acc[2 * g + 1] =
-                  __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bl, acc[2 * g + 1], 0, 0, 0);
-            }
-          }
-          if (g > 0) maxsim_epilogue(mx[g - 1], acc[2 * g - 2], acc[2 * g - 1], al[g - 1], nrm);
-        }
-      } else {
-        // Long K: steps outer, each step's code fragment decoded once and its
-        // query fragments read together before its MFMAs.
-#pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
-#pragma unroll
-        for (int c = 0; c < NLOAD; ++c) {
-#pragma unroll
-          for (int h = 0; h < SPL; ++h) {
-            const int s = c * SPL + h;
-            if (s < KS) {
-              v4i bf[NCB];
-#pragma unroll
-              for (int cb = 0; cb < NCB; ++cb) bf[cb] = sb[(s * NCB + cb) * 64 + boff];
-              const v4i af = decode_step<BITS>(raw[c], h, la);
-#pragma unroll
-              for (int cb = 0; cb < NCB; ++cb)
-                acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[cb], acc[cb], 0, 0, 0);
-            }
-          }
-        }
-#pragma unroll
-        for (int g = 0; g < NQG; ++g) maxsim_epilogue(mx[g], acc[2 * g], acc[2 * g + 1], al[g], nrm);
-      }
-#pragma unroll
-      for (int c = 0; c < NLOAD; ++c) raw[c] = nraw[c];
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) nrm4[i4] = nnrm4[i4];
+    float nv;
+  };
+  long long ld_doc = doc0;
+  int ld_t = 0;
+  auto load_next = [&](Stage& st) {
+    const long long dd = ld_doc <= last_doc ? ld_doc : last_doc;
+    const int tt = ld_doc <= last_doc ? ld_t : tpd - 1;
+    const long long tile = (a.doc_begin + dd) * tpd + tt;
+    load_tile_codes<NLOAD>(st.raw, packed, tile, lane);
+    st.nv = a.norms[tile * kTile + (lane & 31)];
+    if (++ld_t == tpd) {
+      ld_t = 0;
+      ld_doc += nw;
     }
+  };
+  long long doc = doc0;
+  int t = 0;
+  float mx[NQG];
+  auto process = [&](const Stage& st) {
+    if (t == 0) {
 #pragma unroll
-    for (int g = 0; g < NQG; ++g) {
-      float v = fmaxf(mx[g], __shfl_xor(mx[g], 32)) + 0.0f;  // token max over the document
-#pragma unroll
-      for (int o = 1; o < 32; o <<= 1) v = v + __shfl_xor(v, o);
-      if (lane == 0 && g < a.groups) a.out[(size_t)g * a.out_stride + doc] = v;
+      for (int g = 0; g < NQG; ++g) mx[g] = -__builtin_inff();
     }
-  }
+    int boff = lane;
+    asm volatile("" : "+v"(boff));
+    // Row r's norm sits at float r of the wave's slot; lane l needs rows
+    // 8 i4 + 4 (l / 32) + {0..3}. LDS operations of one wave complete in
+    // order, so no barrier is needed around the slot.
+    if (lane < 32) reinterpret_cast<float*>(nstage[wave])[lane] = st.nv;
+    __builtin_amdgcn_wave_barrier();
+    float nrm[16];
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const float4 v = nstage[wave][2 * i4 + half];
+      nrm[4 * i4 + 0] = v.x;
+      nrm[4 * i4 + 1] = v.y;
+      nrm[4 * i4 + 2] = v.z;
+      nrm[4 * i4 + 3] = v.w;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // The score's "+ 0.0f" (-0 -> +0) commutes with the maximum (fmaxf
+    // treats the zeros as equal), so it is applied once to the token max.
+    v16i acc[NCB];
+    if constexpr (KS <= 8) {
+      // Short K: every step's code fragment is decoded once up front, then
+      // the query groups run one after another; group g's MFMAs are followed
+      // by the exact epilogue of group g - 1, which does not depend on them
+      // (and only two query fragments are live at a time).
+      v4i af[KS];
+#pragma unroll
+      for (int c = 0; c < NLOAD; ++c) {
+#pragma unroll
+        for (int h = 0; h < SPL; ++h) {
+          const int s = c * SPL + h;
+          if (s < KS) af[s] = decode_step<BITS>(st.raw[c], h, la);
+        }
+      }
+#pragma unroll
+      for (int g = 0; g <= NQG; ++g) {
+        if (g < NQG) {
+          acc[2 * g] = v16i{0};
+          acc[2 * g + 1] = v16i{0};
+#pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            const v4i bh = sb[(s * NCB + 2 * g) * 64 + boff];
+            const v4i bl = sb[(s * NCB + 2 * g + 1) * 64 + boff];
+            acc[2 * g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bh, acc[2 * g], 0, 0, 0);
+            acc[2 * g + 1] =
+                __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bl, acc[2 * g + 1], 0, 0, 0);
+          }
+        }
+        if (g > 0) maxsim_epilogue(mx[g - 1], acc[2 * g - 2], acc[2 * g - 1], al[g - 1], nrm);
+      }
+    } else {
+      // Long K: steps outer, each step's code fragment decoded once and its
+      // query fragments read together before its MFMAs.
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
+#pragma unroll
+      for (int c = 0; c < NLOAD; ++c) {
+#pragma unroll
+        for (int h = 0; h < SPL; ++h) {
+          const int s = c * SPL + h;
+          if (s < KS) {
+            v4i bf[NCB];
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) bf[cb] = sb[(s * NCB + cb) * 64 + boff];
+            const v4i af = decode_step<BITS>(st.raw[c], h, la);
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb)
+              acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[cb], acc[cb], 0, 0, 0);
+          }
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < NQG; ++g) maxsim_epilogue(mx[g], acc[2 * g], acc[2 * g + 1], al[g], nrm);
+    }
+    if (t == tpd - 1) {
+#pragma unroll
+      for (int g = 0; g < NQG; ++g) {
+        float v = fmaxf(mx[g], __shfl_xor(mx[g], 32)) + 0.0f;  // token max over the document
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) v = v + __shfl_xor(v, o);
+        if (lane == 0 && g < a.groups) a.out[(size_t)g * a.out_stride + doc] = v;
+      }
+    }
+    if (++t == tpd) {
+      t = 0;
+      doc += nw;
+    }
+  };
+  Stage s0, s1;
+  load_next(s0);
+  // Two phases per pass; the loop has a single exit at its end (exits between
+  // phases make the compiler's wait analysis merge the phases at the loop
+  // head and wait for the newest stage too).
+  do {
+    load_next(s1);
+    process(s0);
+    load_next(s0);
+    if (doc <= last_doc) process(s1);
+  } while (doc <= last_doc);
 }
 
 }  // namespace

@@ -81,6 +81,41 @@ def test_maxsim_matches_oracle(rt, bits, d, doc_len, ntok, nq):
 
 
 @pytest.mark.gpu
+def test_maxsim_topk_chunked_selection_with_ties(rt):
+    """Enough documents that the top-k is selected per row chunk and then
+    merged: copies of query 0's best document sit at the chunk edges (exact
+    score ties, ranked by lower document index), and k covers the chunked
+    sizes and one too large to merge (one workgroup per row)."""
+    print("[case] maxsim chunked top-k 12000 docs with planted ties", flush=True)
+    from eos_amd.turboquant import TurboQuantIndex, TurboQuantMultiVectorIndex
+    ndocs, doc_len, d, bits = 12000, 32, 64, 2
+    c = _corpus(ndocs, doc_len, d, bits, seed=41)
+    q = _tokens(3, 2, d, 43)
+    args = (c.rotation, d, bits, c.codebook, c.codebook_scale)
+    first = oracle.tq_maxsim_scores(q[:1], *args, c.codes, c.norms, doc_len)
+    best = int(np.argmax(first[0]))
+    codes = c.codes.reshape(ndocs, doc_len, -1).copy()
+    norms = c.norms.reshape(ndocs, doc_len).copy()
+    for dst in (0, 2399, 2400, 4800, 11999):
+        codes[dst], norms[dst] = codes[best], norms[best]
+    codes = codes.reshape(ndocs * doc_len, -1)
+    norms = norms.reshape(-1)
+    want = oracle.tq_maxsim_scores(q, *args, codes, norms, doc_len)
+    idx = TurboQuantIndex(rt, codes, norms, d, bits, c.codebook, c.codebook_scale, c.rotation)
+    mv = TurboQuantMultiVectorIndex(idx, doc_len)
+    for k in (1, 7, 100, 500, 2000):
+        ids, sc = mv.top_k(q, k)
+        for i in range(3):
+            order = np.lexsort((np.arange(ndocs), -want[i]))[:k]
+            np.testing.assert_array_equal(ids[i], order, err_msg=f"k={k} query {i}")
+            np.testing.assert_array_equal(sc[i], want[i][order])
+    tied = sorted({0, 2399, 2400, 4800, 11999, best})
+    ids, _ = mv.top_k(q[:1], len(tied))
+    assert ids[0].tolist() == tied
+    idx.release()
+
+
+@pytest.mark.gpu
 def test_maxsim_zero_scores_keep_the_oracle_sign(rt):
     """Documents whose vectors all have norm 0 score (D * alpha) * 0, which is
     -0 for a negative dot; the score's + 0.0f makes it +0 before the token
