@@ -109,5 +109,36 @@ def build(verbose: bool = False) -> str:
     return LIB_PATH
 
 
+ASAN_LIB_PATH = os.path.join(BUILD_DIR, "libeoship_asan.so")
+
+
+def build_sanitized(verbose: bool = False) -> str:
+    """The host shim built with AddressSanitizer and UndefinedBehaviorSanitizer
+    (host code only; the gfx950 code objects and the device-variable objects
+    of build() are linked in unchanged) into _build/libeoship_asan.so. For
+    CPU tests of the host-side parsers and argument checks, loaded by a
+    process that preloads the sanitizer runtimes."""
+    asm_path = os.path.join(BUILD_DIR, "eoship_blobs.S")
+    hip_objs = [os.path.join(BUILD_DIR, os.path.splitext(os.path.basename(src))[0] + ".o")
+                for src in HIP_HOST_SOURCES]
+    if not os.path.exists(asm_path) or not all(os.path.exists(o) for o in hip_objs):
+        build(verbose)
+    tmp = ASAN_LIB_PATH + ".tmp"
+    _run([
+        "g++", "-O1", "-g", "-std=c++17", "-fPIC", "-shared", "-fno-omit-frame-pointer",
+        "-fsanitize=address,undefined", "-fno-sanitize-recover=undefined",
+        "-Wno-unused-result", "-D__HIP_PLATFORM_AMD__",
+        "-I", os.path.join(REPO_DIR, "include"), "-I", CSRC, "-I", os.path.join(ROCM, "include"),
+        *HOST_SOURCES, *hip_objs, asm_path,
+        "-L", os.path.join(ROCM, "lib"), "-lamdhip64", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}",
+        "-o", tmp,
+    ], verbose)
+    os.replace(tmp, ASAN_LIB_PATH)
+    return ASAN_LIB_PATH
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--sanitize" in sys.argv:
+        print(build_sanitized(verbose="-v" in sys.argv))
+    else:
+        print(build(verbose="-v" in sys.argv))
