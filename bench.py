@@ -165,8 +165,8 @@ def encoder_leg(rt, steps: int, name: str = "c3", cpu: bool = True) -> dict:
         enc.embed_device(d_ids, d_mask, B, T, d_out)
     rt.sync()
     kernels = {}
-    for kname in ("eos_enc_pack", "eos_enc_embed", "enc_gemm_qkv", "eos_enc_attn", "enc_gemm_o",
-                  "enc_ln", "enc_gemm_ffn_up", "enc_gemm_ffn_down", "eos_enc_pool"):
+    for kname in ("eos_enc_pack", "eos_enc_embed", "enc_gemm_qkv", "eos_enc_attn", "enc_tail",
+                  "enc_gemm_o", "enc_ln", "enc_gemm_ffn_up", "enc_gemm_ffn_down", "eos_enc_pool"):
         n, t = rt.profile_read(kname)
         kernels[kname] = t / steps
     rt.profile(False)

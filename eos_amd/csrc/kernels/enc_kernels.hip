@@ -834,6 +834,8 @@ struct TailLds {
   float rsc[BM];
   // per-feature scales and biases: O (s, b), FFN-down (s, b), FFN-up (s, b)
   float so[H], bo[H], s2[H], b2[H], s1[FMAX], b1[FMAX];
+  // the two LayerNorms' gamma and beta
+  float lg1[H], lb1[H], lg2[H], lb2[H];
 };
 
 // O projection of row tiles [I0, I0 + N) of the block (context rows in X)
@@ -967,7 +969,8 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
   };
 
   // context rows -> X (rows past the matrix clamped; never stored), all
-  // loads issued before any store; scales and biases -> LDS
+  // loads issued before any store; scales, biases and LayerNorm parameters
+  // -> LDS
   static_assert(EOS_TAIL_THREADS == 512, "4 down + 4 up wavefronts");
   {
     constexpr int PER = BM * (H / 8) / EOS_TAIL_THREADS;
@@ -992,6 +995,10 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
     const float4 b1a = f0 ? reinterpret_cast<const float4*>(a.b_1)[tid] : zero4;
     const float4 s1b = f1 ? reinterpret_cast<const float4*>(a.s_1)[tid + EOS_TAIL_THREADS] : zero4;
     const float4 b1b = f1 ? reinterpret_cast<const float4*>(a.b_1)[tid + EOS_TAIL_THREADS] : zero4;
+    const float4 l0 = hv ? reinterpret_cast<const float4*>(a.g1)[tid] : zero4;
+    const float4 l1 = hv ? reinterpret_cast<const float4*>(a.be1)[tid] : zero4;
+    const float4 l2 = hv ? reinterpret_cast<const float4*>(a.g2)[tid] : zero4;
+    const float4 l3 = hv ? reinterpret_cast<const float4*>(a.be2)[tid] : zero4;
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int i = tid + EOS_TAIL_THREADS * u;
@@ -1003,6 +1010,10 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
       reinterpret_cast<float4*>(lds.bo)[tid] = v1;
       reinterpret_cast<float4*>(lds.s2)[tid] = v2;
       reinterpret_cast<float4*>(lds.b2)[tid] = v3;
+      reinterpret_cast<float4*>(lds.lg1)[tid] = l0;
+      reinterpret_cast<float4*>(lds.lb1)[tid] = l1;
+      reinterpret_cast<float4*>(lds.lg2)[tid] = l2;
+      reinterpret_cast<float4*>(lds.lb2)[tid] = l3;
     }
     if (f0) {
       reinterpret_cast<float4*>(lds.s1)[tid] = s1a;
@@ -1019,7 +1030,7 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
   // codes -> Q8, scales -> rsc. Rows past the matrix are normalized too
   // (stored only to h1, which has room for them).
   auto layer_norm1 = [&]() {
-    tail_layer_norm<RT, H>(wave, lane, a.g1, a.be1, a.eps,
+    tail_layer_norm<RT, H>(wave, lane, lds.lg1, lds.lb1, a.eps,
                            [&](int m, const uint16_t*& yin, uint16_t*& yout, int8_t*& q8, float*& qs) {
                              yin = &X[m * XS];
                              yout = a.h1 + (size_t)min(m0 + m, a.max_rows - 1) * H;
@@ -1030,7 +1041,7 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
   // Second LayerNorm (all wavefronts) -> the layer output rows; rows past
   // the matrix go to the clamped last row with the values that row has.
   auto layer_norm2 = [&]() {
-    tail_layer_norm<RT, H>(wave, lane, a.g2, a.be2, a.eps,
+    tail_layer_norm<RT, H>(wave, lane, lds.lg2, lds.lb2, a.eps,
                            [&](int m, const uint16_t*& yin, uint16_t*& yout, int8_t*& q8, float*& qs) {
                              const int gr = m0 + m < rows ? m0 + m : m0;  // m0 < rows
                              const bool live = m0 + m < rows;
