@@ -437,7 +437,8 @@ EOS_DEV void lgkm_wait(v8h (&f)[N]) {
 // given): A first, a lane's results lie along an output column, stored
 // transposed into vt[col - vt_col0][row].
 template <int WM, int WN, int NS, bool TR, bool I8>
-EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t* st) {
+EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t* st, float* lsc,
+                       float* lbi, float* lrs) {
   constexpr int BM = 64 * WM, BN = 64 * WN, ST = (BM + BN) * kBK;  // halves per stage
   constexpr int ESZ = I8 ? 1 : 2;  // operand bytes: a 64-byte chunk is 32 halves or 64 int8
   constexpr int NLD = WM + WN;  // 16-row loads per wavefront per chunk
@@ -523,11 +524,23 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
     lgkm_wait(f1);
     mma(f1);
   };
+  // The tile's column scales and biases (and int8 row scales) are loaded
+  // before the first chunks are requested and stored to LDS behind them, so
+  // the epilogue reads them from LDS (the loop's barriers publish them).
+  const bool ep_c = tid < BN, ep_r = I8 && tid < BM;
+  const float v_sc = ep_c ? a.wscale[n0 + tid] : 0.0f;
+  const float v_bi = ep_c ? a.bias[n0 + tid] : 0.0f;
+  const float v_rs = ep_r ? a.ascale[min(m0 + tid, a.max_rows - 1)] : 1.0f;
   // Chunks 0 .. NS - 2 are requested up front; at the step of chunk c the
   // stage of chunk c - 1 (read at the step before, ordered by this step's
   // barrier) receives chunk c + NS - 1, so NS - 1 chunks are in flight.
 #pragma unroll
   for (int c = 0; c < NS - 1; ++c) issue(st + c * ST, c);
+  if (ep_c) {
+    lsc[tid] = v_sc;
+    lbi[tid] = v_bi;
+  }
+  if (ep_r) lrs[tid] = v_rs;
   // NS chunks per pass, one stage each, stage indices static (the fragment
   // reads address stages by immediate offsets); one back-edge and no exit in
   // the body. The barrier is the bare s_barrier: a fenced one
@@ -547,40 +560,106 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
   } while (kc < nk);
   // No LDS write may land after the workgroup exits.
   wait_vmcnt<0>();
-  if constexpr (TR) {
-    // Element e of lane (l32, g) is row 8(e/4) + 4g + e%4 of the block and
-    // column l32: each group of 4 is 4 consecutive rows of one column, one
-    // 8-byte store into vt. Row groups start below rows; their tail past
-    // rows lands in vt's padding.
+  // Epilogue through LDS (every mode but the residual one): each lane writes
+  // its results into the tile in the ring's memory, then whole output rows
+  // (or, transposed, whole V^T row segments) go out as 16-byte stores, 16
+  // consecutive lanes per 256-byte row segment. Writing the MFMA layout
+  // directly scattered every store instruction over 32 rows.
+  if (TR || a.epi != 3) {
+    __syncthreads();  // every wavefront's last fragment reads are done
+    uint16_t* const tile = st;
+    constexpr int TS = TR ? BM + 8 : BN + 8;  // halves per tile row (V^T: per column)
+    static_assert((TR ? BN * TS : BM * TS) <= NS * ST, "the output tile fits the ring");
+    if constexpr (TR) {
+      // Element e of lane (l32, g) is row 8(e/4) + 4g + e%4 of the block and
+      // column l32: 4 consecutive rows of one column, one 8-byte LDS store.
 #pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int col = n0 + wn * 32 * WN + j * 32 + l32;
-      const float sc = a.wscale[col], bi = a.bias[col];
-      uint16_t* vrow = a.vt + (size_t)(col - a.vt_col0) * a.vt_ld;
+      for (int j = 0; j < WN; ++j) {
+        const int cl = wn * 32 * WN + j * 32 + l32;
+        const float sc = lsc[cl], bi = lbi[cl];
 #pragma unroll
-      for (int i = 0; i < WM; ++i) {
+        for (int i = 0; i < WM; ++i) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int row = m0 + wm * 32 * WM + i * 32 + 8 * q + 4 * g;
-          if (row < rows) {
-            // int8: the row scales of the 4 rows (row is a multiple of 4 and
-            // rows of 8, so all 4 are below rows).
-            float rs[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-            if constexpr (I8) {
-              const float4 r4 = *reinterpret_cast<const float4*>(a.ascale + row);
-              rs[0] = r4.x, rs[1] = r4.y, rs[2] = r4.z, rs[3] = r4.w;
-            }
+          for (int q = 0; q < 4; ++q) {
+            const int rl = wm * 32 * WM + i * 32 + 8 * q + 4 * g;
             v4h o;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
               if constexpr (I8)
-                o[t] = (_Float16)__builtin_fmaf((float)acc[i][j][4 * q + t], sc * rs[t], bi);
+                o[t] = (_Float16)__builtin_fmaf((float)acc[i][j][4 * q + t], sc * lrs[rl + t], bi);
               else
                 o[t] = (_Float16)__builtin_fmaf(acc[i][j][4 * q + t], sc, bi);
             }
-            *reinterpret_cast<v4h*>(vrow + row) = o;
+            *reinterpret_cast<v4h*>(&tile[cl * TS + rl]) = o;
           }
         }
+      }
+    } else {
+      // Element e of lane (l32, g) is row l32 and columns 8(e/4) + 4g ..
+      // + 3: one 8-byte LDS store per group of 4.
+      auto stage = [&](auto epi_c) {
+        constexpr int EPI = decltype(epi_c)::value;
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+          const int rl = wm * 32 * WM + i * 32 + l32;
+          const float rs = I8 ? lrs[rl] : 1.0f;
+#pragma unroll
+          for (int j = 0; j < WN; ++j) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int cl = wn * 32 * WN + j * 32 + 8 * q + 4 * g;
+              float4 sc = *reinterpret_cast<const float4*>(lsc + cl);
+              const float4 bi = *reinterpret_cast<const float4*>(lbi + cl);
+              if constexpr (I8) sc = make_float4(sc.x * rs, sc.y * rs, sc.z * rs, sc.w * rs);
+              float v[4] = {__builtin_fmaf((float)acc[i][j][4 * q], sc.x, bi.x),
+                            __builtin_fmaf((float)acc[i][j][4 * q + 1], sc.y, bi.y),
+                            __builtin_fmaf((float)acc[i][j][4 * q + 2], sc.z, bi.z),
+                            __builtin_fmaf((float)acc[i][j][4 * q + 3], sc.w, bi.w)};
+              if constexpr (EPI == 1) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) v[t] = gelu_erf_fast(v[t]);
+              } else if constexpr (EPI == 2) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) v[t] = gelu(v[t], 2);
+              }
+              v4h o;
+#pragma unroll
+              for (int t = 0; t < 4; ++t) o[t] = (_Float16)v[t];
+              *reinterpret_cast<v4h*>(&tile[rl * TS + cl]) = o;
+            }
+          }
+        }
+      };
+      switch (a.epi) {
+        case 1: stage(std::integral_constant<int, 1>{}); break;
+        case 2: stage(std::integral_constant<int, 2>{}); break;
+        default: stage(std::integral_constant<int, 0>{}); break;
+      }
+    }
+    __syncthreads();
+    if constexpr (TR) {
+      // V^T row (feature) m0 .. m0 + BM - 1 of each of the BN columns, 8 rows
+      // per lane; groups start below rows (a multiple of 8), so none passes it.
+      constexpr int R8 = BM / 8;
+#pragma unroll
+      for (int u = 0; u < BN * R8 / 256; ++u) {
+        const int idx = tid + 256 * u;
+        const int cl = idx / R8, r8 = idx % R8;
+        const int row = m0 + 8 * r8;
+        if (row < rows)
+          *reinterpret_cast<v4i*>(a.vt + (size_t)(n0 + cl - a.vt_col0) * a.vt_ld + row) =
+              *reinterpret_cast<const v4i*>(&tile[cl * TS + 8 * r8]);
+      }
+    } else {
+      constexpr int C8 = BN / 8;
+#pragma unroll
+      for (int u = 0; u < BM * C8 / 256; ++u) {
+        const int idx = tid + 256 * u;
+        const int rl = idx / C8, c8 = idx % C8;
+        const int row = m0 + rl;
+        if (row < rows)
+          *reinterpret_cast<v4i*>(a.out + (size_t)row * a.n + n0 + 8 * c8) =
+              *reinterpret_cast<const v4i*>(&tile[rl * TS + 8 * c8]);
       }
     }
     return;
@@ -630,18 +709,14 @@ EOS_DEV void gemm_tile(const EncGemmArgs& a, int m0, int n0, int rows, uint16_t*
       }
     }
   };
-  switch (a.epi) {
-    case 1: epilogue(std::integral_constant<int, 1>{}); break;
-    case 2: epilogue(std::integral_constant<int, 2>{}); break;
-    case 3: epilogue(std::integral_constant<int, 3>{}); break;
-    default: epilogue(std::integral_constant<int, 0>{}); break;
-  }
+  epilogue(std::integral_constant<int, 3>{});  // the residual epilogue (a.epi == 3)
 }
 
 template <int WM, int WN, int NS, bool I8 = false>
 EOS_DEV void gemm_body(const EncGemmArgs& a) {
   constexpr int BM = 64 * WM, BN = 64 * WN, ST = (BM + BN) * kBK;
   __shared__ __attribute__((aligned(16))) uint16_t st[NS * ST];
+  __shared__ __attribute__((aligned(16))) float lsc[BN], lbi[BN], lrs[BM];
   const int rows = *a.rows;
   // XCD-aware tile order: workgroup w runs on XCD w % 8 (round-robin
   // dispatch), so XCD x takes row blocks x, x + 8, ... and walks all column
@@ -653,9 +728,9 @@ EOS_DEV void gemm_body(const EncGemmArgs& a) {
   const int m0 = mb * BM, n0 = nb * BN;
   if (m0 >= rows) return;
   if (a.vt != nullptr && n0 >= a.vt_col0)
-    gemm_tile<WM, WN, NS, true, I8>(a, m0, n0, rows, st);
+    gemm_tile<WM, WN, NS, true, I8>(a, m0, n0, rows, st, lsc, lbi, lrs);
   else
-    gemm_tile<WM, WN, NS, false, I8>(a, m0, n0, rows, st);
+    gemm_tile<WM, WN, NS, false, I8>(a, m0, n0, rows, st, lsc, lbi, lrs);
 }
 
 }  // namespace
