@@ -1343,6 +1343,11 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   constexpr int CPT = (NCH + 255) / 256; // chunks per thread
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][KB * (HD + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * (KB + 8)];
+  // Per-wavefront output staging (head dims up to 64): the K buffers when
+  // they are large enough (free once the key loop is done), else its own.
+  constexpr bool kStageInK = 2 * KB * (HD + 8) >= 4 * 32 * (HD + 8);
+  __shared__ __attribute__((aligned(16)))
+  uint16_t ostage[(HD <= 64 && !kStageInK) ? 4 * 32 * (HD + 8) : 8];
   const int b = blockIdx.z, h = blockIdx.y;
   const int cnt = a.seq_cnt[b];
   const int q0 = blockIdx.x * (4 * QW);
@@ -1516,6 +1521,40 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     __syncthreads();
   }
   const float lsum = lrun + __shfl_xor(lrun, 32);  // before any lane leaves
+  if constexpr (HD <= 64) {
+    // The wavefront's 32 output rows go through LDS and leave as whole row
+    // segments (HD halves each) in 16-byte stores; rows of the sequence's
+    // 8-row slot past its end get zeros (no kernel writes them otherwise,
+    // and a NaN left there by a freed buffer would reach the next layer's V
+    // rows past the sequence). Storing the MFMA layout directly scattered
+    // each store over 32 rows.
+    constexpr int OS = HD + 8;  // halves per staged row
+    uint16_t* const os = (kStageInK ? &ks[0][0] : ostage) + wave * 32 * OS;
+    const float inv = (qlive && lsum > 0.f) ? 1.0f / lsum : 0.f;
+#pragma unroll
+    for (int t = 0; t < HD / 32; ++t) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        v4h v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (_Float16)(o[t][4 * q + j] * inv);
+        *reinterpret_cast<v4h*>(&os[l32 * OS + t * 32 + 8 * q + 4 * g]) = v;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    constexpr int LPR = HD / 8;       // lanes per row (16 bytes each)
+    constexpr int RPI = 64 / LPR;     // rows per store instruction
+    const int slot = (cnt + 7) & ~7;  // the sequence's rows, pad rows included
+#pragma unroll
+    for (int r0 = 0; r0 < 32; r0 += RPI) {
+      const int r = r0 + lane / LPR, c = (lane % LPR) * 8;
+      const int qr = q0 + wave * QW + r;
+      if (qr < slot)
+        *reinterpret_cast<v4i*>(a.ctx + (size_t)(off + qr) * a.hidden + h * HD + c) =
+            *reinterpret_cast<const v4i*>(&os[r * OS + c]);
+    }
+    return;
+  }
   if (!qlive) {
     // Pad rows of the sequence's 8-row slot get zeros: no kernel writes them
     // otherwise, and the memory may hold anything a freed buffer left (a NaN
