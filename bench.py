@@ -8,9 +8,15 @@ A step is one full top-k call (prepare, sample threshold, filtered scan,
 finalize) over the device-resident corpus with device-resident queries.
 
 Prints one JSON line (the driver's contract), with `roofline` for the
-dominant kernel (the filtered scan, timed per launch with hipEvents on the
-library's stream) and `cpu_baseline` (the C oracle's reference-loop port,
-single-threaded, on a bounded sample).
+dominant kernel (the filtered scan, timed per launch with HIP events that its
+own dispatches record, against 8 TB/s and against a copy kernel's measured
+rate) and `cpu_baseline` (the C oracle's reference-loop port on a bounded
+sample, single-threaded and all-core). The other BASELINE configs ride on the
+same line as sub-objects, each with its own roofline and CPU baseline:
+`tiny_c1` (tiny embed, µs per call), `two_stage_c2` (TurboQuant top-200 +
+f16 rerank top-100), `maxsim_c5` (MaxSim over 100k documents of 128 vectors,
+against the int8 MFMA peak), `encoder_c3` / `encoder_c4` (q8 BERT-style
+encoder forward, tokens/s, with a per-stage breakdown).
 """
 from __future__ import annotations
 
