@@ -207,6 +207,57 @@ def encoder_leg(rt, steps: int, name: str = "c3", cpu: bool = True) -> dict:
     }
 
 
+def tq_shard_leg(rt, n: int, queries: int, k: int, steps: int, warmup: int) -> dict:
+    """The c2 scan at one GPU's shard of an 8-GPU job (N / 8 vectors: the
+    corpus rows are the unit a multi-GPU run would split): one stream, the
+    same top-k pipeline, and the filter scan's per-launch time."""
+    from eos_amd import datagen
+    from eos_amd.runtime import DeviceBuffer
+    from eos_amd.turboquant import TurboQuantIndex
+
+    corpus = datagen.baseline_flat_corpus(n=n)
+    q = datagen.baseline_queries(queries, corpus.dim)
+    idx = TurboQuantIndex(rt, corpus.codes, corpus.norms, corpus.dim, corpus.bits, corpus.codebook,
+                          corpus.codebook_scale, corpus.rotation)
+    kk = idx.effective_k(k)
+    dq = DeviceBuffer.from_array(rt, q)
+    dids = DeviceBuffer(rt, queries * kk * 8)
+    dsc = DeviceBuffer(rt, queries * kk * 4)
+    # top_k_device: the exact fallback is gated on the device, so every
+    # timed step is final without a host round trip.
+    for _ in range(warmup):
+        idx.top_k_device(dq, queries, k, dids, dsc, with_stats=False)
+    rt.sync()
+    rt.mark(4)
+    for _ in range(steps):
+        idx.top_k_device(dq, queries, k, dids, dsc, with_stats=False)
+    rt.mark(5)
+    ms = rt.elapsed_ms(4, 5) / steps
+    rt.profile_reset()
+    rt.profile_select("tq_scan_filter")
+    rt.profile(True)
+    for _ in range(steps):
+        idx.top_k_device(dq, queries, k, dids, dsc, with_stats=False)
+    rt.sync()
+    nf, msf = rt.profile_read("tq_scan_filter")
+    rt.profile(False)
+    avg = msf / max(nf, 1)
+    bytes_per_launch = n * (corpus.dim * corpus.bits // 8 + 4)
+    for b in (dq, dids, dsc):
+        b.free()
+    idx.release()
+    return {
+        "metric": "TurboQuant vectors scored/s (one GPU's shard of an 8-GPU job)",
+        "value": queries * n / (ms / 1e3), "unit": "vectors scored/s", "ms_per_batch": ms,
+        "config": {"workload": "turboquant_flat_c2_shard8", "n": n, "dim": corpus.dim,
+                   "bits": corpus.bits, "queries": queries, "k": k, "streams": 1},
+        "roofline": {"bound": "hbm", "kernel": "tq_scan_filter", "avg_launch_ms": avg,
+                     "bytes_per_launch": bytes_per_launch,
+                     "achieved": bytes_per_launch / (avg / 1e3) / 1e9, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": bytes_per_launch / (avg / 1e3) / 1e9 / HBM_PEAK_GBS},
+    }
+
+
 def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -632,6 +683,8 @@ def main() -> int:
     ap.add_argument("--encoder-configs", default="c3,c4", help="comma list of c3, c4")
     ap.add_argument("--copy-calibration-mb", type=int, default=1024)
     ap.add_argument("--skip-tiny", action="store_true")
+    ap.add_argument("--shard-n", type=int, default=125_000,
+                    help="c2 at one GPU's shard of an 8-GPU job (0: skip)")
     ap.add_argument("--tiny-reps", type=int, default=2000)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -667,6 +720,10 @@ def main() -> int:
             out["copy_calibration"] = cal
             out["roofline"]["peak_measured"] = cal["read_plus_write_GBps"]
             out["roofline"]["frac_measured"] = out["roofline"]["achieved"] / cal["read_plus_write_GBps"]
+    if not args.skip_tq and args.shard_n > 0:
+        log(f"c2 shard ({args.shard_n} vectors)")
+        out["tq_shard8_c2"] = tq_shard_leg(rt, args.shard_n, args.queries, args.k, args.steps,
+                                           args.warmup)
     if not args.skip_tiny:
         log("tiny c1")
         out["tiny_c1"] = tiny_leg(rt, args.tiny_reps, cpu=not args.no_cpu_baseline)
