@@ -16,7 +16,10 @@ same line as sub-objects, each with its own roofline and CPU baseline:
 `tiny_c1` (tiny embed, µs per call), `two_stage_c2` (TurboQuant top-200 +
 f16 rerank top-100), `maxsim_c5` (MaxSim over 100k documents of 128 vectors,
 against the int8 MFMA peak), `encoder_c3` / `encoder_c4` (q8 BERT-style
-encoder forward, tokens/s, with a per-stage breakdown).
+encoder forward, tokens/s, with a per-stage breakdown). `mfma_ceiling` is the
+rate and shader clock a stream of independent MFMAs reaches on zero and on
+full-range random operands; the MFMA-bound legs carry their fraction of that
+clock-limited ceiling beside their fraction of the published peak.
 """
 from __future__ import annotations
 
@@ -201,7 +204,8 @@ def encoder_leg(rt, steps: int, name: str = "c3", cpu: bool = True) -> dict:
                      "peak_f16": 2500.0, "frac_f16": achieved / 2500.0,
                      "peak_int8": 5000.0, "frac_int8": achieved / 5000.0,
                      "flops_per_forward_valid": flops,
-                     "int8_share_of_gemm_flops": (3 * H * H + H * F) / (4 * H * H + 2 * H * F)},
+                     "int8_share_of_gemm_flops": (3 * H * H + H * F) / (4 * H * H + 2 * H * F),
+                     "int8_share_of_flops": 2.0 * valid * L * (3 * H * H + H * F) / flops},
         "breakdown_ms": kernels,
         "cpu_baseline": base,
     }
@@ -523,6 +527,81 @@ def copy_calibration(rt, mb: int, reps: int = 5) -> dict:
 
 
 
+def mfma_ceiling(rt, iters: int = 400) -> dict:
+    """Matrix-core rate and shader clock reached by a stream of independent
+    MFMAs (eos_amd/csrc/kernels/probe_kernels.hip, 3 waves per SIMD, no VALU
+    work) on three kinds of operand bytes: zeros, full-range random int8, and
+    random f16 drawn N(0, 1). The clock falls under the power drawn by
+    full-range operands, so the rate an int8 kernel can reach on real data
+    is this ceiling, below the published dense peak (which assumes the top
+    clock). Launch time from stream events; clock from s_memtime over
+    s_memrealtime (100 MHz) inside each wave."""
+    import ctypes as C
+    from eos_amd import _lib
+    from eos_amd.build import PROBE_PATH
+    from eos_amd.runtime import DeviceBuffer
+
+    if not os.path.exists(PROBE_PATH):
+        raise RuntimeError(f"{PROBE_PATH} is missing: run python -m eos_amd.build")
+    img = open(PROBE_PATH, "rb").read()
+    mod = C.c_void_p()
+    _lib.call("eoship_module_load", rt.handle, img, C.c_size_t(len(img)), C.byref(mod))
+    cu = rt.info()["compute_units"]
+    blocks = cu * 3
+    waves = blocks * 4
+    slots, frags = 64, 8
+    words = slots * 2 * frags * 64 * 4
+    rng = np.random.default_rng(0x5eed)
+    operands = {
+        "zeros": np.zeros(words, np.int32),
+        "random_int8": rng.integers(-2**31, 2**31, words, dtype=np.int64).astype(np.int32),
+        "random_f16": rng.standard_normal(words * 2).astype(np.float16).view(np.int32),
+    }
+
+    class Args(C.Structure):
+        _fields_ = [("operands", C.c_void_p), ("sink", C.c_void_p), ("clocks", C.c_void_p),
+                    ("iters", C.c_int)]
+
+    sink = DeviceBuffer(rt, blocks * 256 * 4)
+    clocks = DeviceBuffer(rt, waves * 16)
+    grid = (C.c_uint32 * 3)(blocks, 1, 1)
+    block = (C.c_uint32 * 3)(256, 1, 1)
+    out = {"waves_per_simd": 3, "mfma_per_wave": iters * 64}
+    try:
+        for label, kname, kind, ops in (
+                ("int8_zeros", "eos_probe_mfma_i8", "zeros", 2.0 * 32 ** 3),
+                ("int8_random", "eos_probe_mfma_i8", "random_int8", 2.0 * 32 ** 3),
+                ("f16_random", "eos_probe_mfma_f16", "random_f16", 2.0 * 32 * 32 * 16)):
+            fn = C.c_void_p()
+            _lib.call("eoship_function", mod, kname.encode(), C.byref(fn))
+            src = DeviceBuffer.from_array(rt, operands[kind])
+            args = Args(src.ptr, sink.ptr, clocks.ptr, iters)
+            params = (C.c_void_p * 1)(C.cast(C.pointer(args), C.c_void_p))
+
+            def launch():
+                _lib.call("eoship_launch", rt.handle, fn, grid, block, C.c_uint32(0), params)
+
+            for _ in range(3):
+                launch()
+            rt.sync()
+            rt.mark(8)
+            reps = 5
+            for _ in range(reps):
+                launch()
+            rt.mark(9)
+            ms = rt.elapsed_ms(8, 9) / reps
+            clk = clocks.download(np.uint64, (waves, 2)).astype(np.float64)
+            mhz = float(np.median(clk[:, 0] / (clk[:, 1] / 100.0)))
+            total = waves * iters * 64 * ops
+            out[label] = {"tops": total / (ms / 1e3) / 1e12, "clock_mhz": mhz, "ms": ms}
+            src.free()
+    finally:
+        sink.free()
+        clocks.free()
+        _lib.call("eoship_module_unload", mod)
+    return out
+
+
 def tiny_leg(rt, reps: int, cpu: bool = True) -> dict:
     """BASELINE config 1 (examples/embed.eos): f16 token_embedding [30522, 256]
     and projection [256, 128], N(0, 0.02); 128 tokens; gather -> matmul ->
@@ -686,6 +765,7 @@ def main() -> int:
     ap.add_argument("--shard-n", type=int, default=125_000,
                     help="c2 at one GPU's shard of an 8-GPU job (0: skip)")
     ap.add_argument("--tiny-reps", type=int, default=2000)
+    ap.add_argument("--skip-mfma-ceiling", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -724,6 +804,11 @@ def main() -> int:
         log(f"c2 shard ({args.shard_n} vectors)")
         out["tq_shard8_c2"] = tq_shard_leg(rt, args.shard_n, args.queries, args.k, args.steps,
                                            args.warmup)
+    ceiling = None
+    if not args.skip_mfma_ceiling and not (args.skip_encoder and args.skip_maxsim):
+        log("MFMA ceiling probe")
+        ceiling = mfma_ceiling(rt)
+        out["mfma_ceiling"] = ceiling
     if not args.skip_tiny:
         log("tiny c1")
         out["tiny_c1"] = tiny_leg(rt, args.tiny_reps, cpu=not args.no_cpu_baseline)
@@ -732,8 +817,23 @@ def main() -> int:
             log(f"encoder {name}")
             out[f"encoder_{name}"] = encoder_leg(rt, args.encoder_steps, name,
                                                  cpu=not args.no_cpu_baseline)
+            if ceiling is not None:
+                # The forward's flops split over int8 MFMAs (QKV, FFN-up) and
+                # f16 MFMAs (O, FFN-down, attention): the time each share
+                # would take at its clock-limited ceiling.
+                roof = out[f"encoder_{name}"]["roofline"]
+                sh = roof["int8_share_of_flops"]
+                ceil = 1.0 / (sh / ceiling["int8_random"]["tops"]
+                              + (1.0 - sh) / ceiling["f16_random"]["tops"])
+                roof["ceiling_mixed_random"] = ceil
+                roof["frac_of_ceiling"] = roof["achieved"] / ceil
     if not args.skip_maxsim:
         out["maxsim_c5"] = maxsim_leg(rt, args.maxsim_steps, cpu=not args.no_cpu_baseline)
+        if ceiling is not None:
+            # Against the rate full-range int8 operands allow (clock-limited).
+            roof = out["maxsim_c5"]["roofline"]
+            roof["ceiling_int8_random"] = ceiling["int8_random"]["tops"]
+            roof["frac_of_ceiling"] = roof["achieved"] / ceiling["int8_random"]["tops"]
     if not args.skip_two_stage:
         log("two-stage c2")
         out["two_stage_c2"] = two_stage_leg(rt, args.maxsim_steps * 4, args.n)

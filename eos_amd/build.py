@@ -9,6 +9,8 @@
    ``eos_amd/libeoship.so``, together with the objects hipcc builds from the
    host sources that declare device variables (the static scratch of the
    no-allocation entry points).
+4. A measurement code object (``_build/probe.hsaco``: MFMA rate and shader
+   clock against operand data) is built for bench.py and not linked in.
 
 Run ``python -m eos_amd.build`` or call :func:`build`.
 """
@@ -33,6 +35,10 @@ DEVICE_SOURCES = [
     ("enc", os.path.join(CSRC, "kernels", "enc_kernels.hip")),
     ("ret", os.path.join(CSRC, "kernels", "ret_kernels.hip")),
 ]
+# Measurement code object for bench.py (MFMA rate and shader clock against
+# operand data), built beside the library and not linked into it.
+PROBE_SOURCE = os.path.join(CSRC, "kernels", "probe_kernels.hip")
+PROBE_PATH = os.path.join(BUILD_DIR, "probe.hsaco")
 # Host translation units that hold device variables (hipcc, host + device).
 HIP_HOST_SOURCES = [
     os.path.join(CSRC, "eoship_noalloc.hip"),
@@ -75,6 +81,7 @@ def build(verbose: bool = False) -> str:
         _run([hipcc, *HIPCC_FLAGS, "--genco", "-I", os.path.join(CSRC, "kernels"), "-o", out, src],
              verbose)
         blobs.append((stem, out))
+    _run([hipcc, *HIPCC_FLAGS, "--genco", "-o", PROBE_PATH, PROBE_SOURCE], verbose)
     asm = [".section .note.GNU-stack,\"\",@progbits"]
     for stem, path in blobs:
         asm += [
