@@ -42,26 +42,48 @@ EOS_DEV float wave_sum(float v) {
   return v;
 }
 
-// Sum over the wavefront without LDS round trips: DPP adds within each row of
-// 16 lanes (quad swaps, then half-row and row mirrors, so every lane of a row
-// holds the row's sum), then the four row sums read into scalars. Uniform
-// result; a different summation order from wave_sum.
+// Sum over the wavefront without LDS or scalar round trips: DPP adds within
+// each row of 16 lanes (quad swaps, then half-row and row mirrors, so every
+// lane of a row holds the row's sum), then v_permlane16_swap (lane l gets
+// lane l ^ 16's value) and v_permlane32_swap (lane l ^ 32's) with an add
+// each. Every lane ends with (r0 + r1) + (r2 + r3) of the row sums r_i (each
+// add is commutative, so every lane computes the same value); a different
+// summation order from wave_sum.
 template <int CTRL>
 EOS_DEV float dpp_shuffled(float v) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// v (lane l) and v (lane l ^ 16) / (lane l ^ 32): the two results of a swap
+// of v with itself (odd rows against even rows, or the upper 32 lanes
+// against the lower 32; a is the even row's / lower half's value, b the
+// other's). The elements are copied out of the builtin's two-element vector
+// before the bit casts: __builtin_bit_cast applied to an element r[1]
+// directly compiles to element 0.
+EOS_DEV void swapped16(float v, float& a, float& b) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const unsigned r0 = r[0], r1 = r[1];
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+EOS_DEV void swapped32(float v, float& a, float& b) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const unsigned r0 = r[0], r1 = r[1];
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
 }
 EOS_DEV float wave_sum_dpp(float v) {
   v += dpp_shuffled<0xb1>(v);   // quad_perm [1, 0, 3, 2]
   v += dpp_shuffled<0x4e>(v);   // quad_perm [2, 3, 0, 1]
   v += dpp_shuffled<0x141>(v);  // row_half_mirror
   v += dpp_shuffled<0x140>(v);  // row_mirror
-  const int b = __builtin_bit_cast(int, v);
-  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
-  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
-  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
-  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
-  return (r0 + r1) + (r2 + r3);
+  float a, b;
+  swapped16(v, a, b);  // rows {0, 1} and {2, 3}: a is the even row's sum
+  v = a + b;
+  swapped32(v, a, b);  // a holds r0 + r1, b holds r2 + r3
+  return a + b;
 }
 
 // Maximum over the wavefront, the same pattern as wave_sum_dpp.
@@ -70,12 +92,11 @@ EOS_DEV float wave_max_dpp(float v) {
   v = fmaxf(v, dpp_shuffled<0x4e>(v));
   v = fmaxf(v, dpp_shuffled<0x141>(v));
   v = fmaxf(v, dpp_shuffled<0x140>(v));
-  const int b = __builtin_bit_cast(int, v);
-  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
-  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
-  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
-  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
-  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+  float a, b;
+  swapped16(v, a, b);
+  v = fmaxf(a, b);
+  swapped32(v, a, b);
+  return fmaxf(a, b);
 }
 
 // Symmetric per-row int8 quantization: scale = max|y| / 127 (0 for a zero
@@ -777,9 +798,10 @@ EOS_DEV void ln_params(const float* gamma, const float* beta, int lane, LnParams
 // reductions overlap. Every lane holds the column pairs 2 lane + 128 t.
 // Two-pass mean / variance in f32 (wavefront sums by DPP), then
 // out = (x - mean) * (rsq(var + eps) * gamma) + beta as one fma, rounded to
-// f16 into yout[r]. With q8[r], also the int8 codes rint(out * 127 / max|out|)
-// of the f32 result (|code| <= 127 since the reciprocal is within 1 ulp) and
-// the scale max|out| / 127 (0 for a zero row) into *qscale[r].
+// f16 into yout[r]. With q8 (given for every row or for none), also the
+// int8 codes rint(out * 127 / max|out|) of the f32 result (|code| <= 127
+// since the reciprocal is within 1 ulp) and the scale max|out| / 127 (0 for
+// a zero row) into *qscale[r].
 template <int H, int NR>
 EOS_DEV void ln_rows(const uint16_t* const (&y)[NR], const LnParams<H>& p, float eps, int lane,
                      uint16_t* const (&yout)[NR], int8_t* const (&q8)[NR],
@@ -827,18 +849,27 @@ EOS_DEV void ln_rows(const uint16_t* const (&y)[NR], const LnParams<H>& p, float
           (uint32_t)f2h(x[r][t][0]) | ((uint32_t)f2h(x[r][t][1]) << 16);
     }
   }
+  // int8 codes: callers give q8 for every row or for none. The rows'
+  // maxima are reduced together, then every code is stored, then lane 0
+  // writes the scales in one branch (per-row reductions and lane-0 branches
+  // in turn made the rows wait on each other).
+  if (q8[0] == nullptr) return;
+  float am[NR], qi[NR];
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    if (q8[r] == nullptr) continue;
-    const float am = wave_max_dpp(amax[r]);
-    const float qi = am > 0.0f ? 127.0f * __builtin_amdgcn_rcpf(am) : 0.0f;
+  for (int r = 0; r < NR; ++r) am[r] = wave_max_dpp(amax[r]);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) qi[r] = am[r] > 0.0f ? 127.0f * __builtin_amdgcn_rcpf(am[r]) : 0.0f;
+#pragma unroll
+  for (int r = 0; r < NR; ++r)
 #pragma unroll
     for (int t = 0; t < P; ++t) {
-      const uint32_t c0 = (uint32_t)(uint8_t)(int8_t)(int)rintf(x[r][t][0] * qi);
-      const uint32_t c1 = (uint32_t)(uint8_t)(int8_t)(int)rintf(x[r][t][1] * qi);
+      const uint32_t c0 = (uint32_t)(uint8_t)(int8_t)(int)rintf(x[r][t][0] * qi[r]);
+      const uint32_t c1 = (uint32_t)(uint8_t)(int8_t)(int)rintf(x[r][t][1] * qi[r]);
       *reinterpret_cast<uint16_t*>(q8[r] + 2 * lane + 128 * t) = (uint16_t)(c0 | (c1 << 8));
     }
-    if (lane == 0) *qscale[r] = am * (1.0f / 127.0f);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) *qscale[r] = am[r] * (1.0f / 127.0f);
   }
 }
 
