@@ -1170,7 +1170,12 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
         for (int j = 0; j < CT; ++j) acco[i][j] = v16f{0};
       v8h wqo[PF][CT];
       prime_wo(wqo);
+      // The down wavefront has RTD of the RT row tiles (the up wavefront on
+      // its SIMD the rest): it paces the O projection, so it runs it at a
+      // raised wave priority.
+      __builtin_amdgcn_s_setprio(2);
       tail_o_proj<H, RTD, 0, PF, XS>(wo_base, loff, X, l32, g, wqo, acco);
+      __builtin_amdgcn_s_setprio(0);
       __syncthreads();  // barrier 2: every context read done
       __syncthreads();  // barrier 3: the residual rows are in X
       tail_epilogue<H, RTD, 0, XS>(X, lds.so, lds.bo, nb, l32, g, acco);
