@@ -1746,8 +1746,19 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
   // Pooled rows: all of the sequence's rows, or those whose mask is set.
   int pooled_rows = cnt;
   if (a.mask != nullptr) {
+    // Eight mask words per thread requested at a time (one memory round trip
+    // per 8192 tokens instead of one per 1024).
     int mine = 0;
-    for (int t = tid; t < a.tokens; t += 1024) mine += a.mask[(size_t)b * a.tokens + t] != 0 ? 1 : 0;
+    for (int t0 = tid; t0 < a.tokens; t0 += 8 * 1024) {
+      int mv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int t = t0 + 1024 * i;
+        mv[i] = t < a.tokens ? a.mask[(size_t)b * a.tokens + t] : 0;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) mine += mv[i] != 0 ? 1 : 0;
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) mine += __shfl_xor(mine, o);
     if (lane == 0) mcount[w] = mine;
@@ -1757,8 +1768,19 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
   }
   float v = 0.f;
   if (tid < a.hidden) {
+    // Up to 32 chunk partials requested at a time, then added in chunk order
+    // (the same sum as one load and add per chunk, without a memory round
+    // trip per chunk).
     const float* src = a.part + (size_t)b * a.nchunk * a.hidden + tid;
-    for (int c = 0; c < nc; ++c) v += src[(size_t)c * a.hidden];
+    for (int c0 = 0; c0 < nc; c0 += 32) {
+      const int m = min(32, nc - c0);
+      float pv[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) pv[i] = i < m ? src[(size_t)(c0 + i) * a.hidden] : 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        if (i < m) v += pv[i];
+    }
     v = pooled_rows > 0 ? v * (1.0f / (float)pooled_rows) : 0.f;
   }
   if (a.mode == 1) {
