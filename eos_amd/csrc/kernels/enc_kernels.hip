@@ -190,16 +190,22 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_count(EncPackArgs a) {
   __shared__ int scr[4];
   const int b = blockIdx.x, tid = threadIdx.x;
   const int32_t* m = a.mask + (size_t)b * a.tokens;
+  // 32 mask words per thread requested at a time, from clamped positions
+  // (a load under a per-lane condition becomes a branch of its own and waits
+  // for its data before the next one is issued).
   int mine = 0;
-  for (int base = tid; base < a.tokens; base += 256 * 8) {
-    int v[8];
+  if (a.all_active) {
+    mine = tid < a.tokens ? (a.tokens - 1 - tid) / 256 + 1 : 0;
+  } else {
+    for (int b0 = 0; b0 < a.tokens; b0 += 256 * 32) {  // b0: uniform
+      const int base = b0 + tid;
+      int v[32];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int t = base + 256 * u;
-      v[u] = t < a.tokens ? (a.all_active ? 1 : m[t]) : 0;
+      for (int u = 0; u < 32; ++u)
+        if (b0 + 256 * u < a.tokens) v[u] = m[min(base + 256 * u, a.tokens - 1)];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) mine += (base + 256 * u < a.tokens && v[u] != 0) ? 1 : 0;
     }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) mine += v[u] != 0 ? 1 : 0;
   }
   int total = 0;
   (void)block_exclusive_scan256(mine, scr, &total);
@@ -223,35 +229,51 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
   const int32_t* m = a.mask + (size_t)b * a.tokens;
   const int per = (a.tokens + 255) / 256;
   const int t0 = tid * per;
-  int mine = 0;
-  for (int k0 = 0; k0 < per; k0 += 8) {
-    int v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int t = t0 + k0 + u;
-      v[u] = (k0 + u < per && t < a.tokens) ? (a.all_active ? 1 : m[t]) : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) mine += v[u] != 0 ? 1 : 0;
-  }
+  // The thread's positions in chunks of mask words (8 when a thread has at
+  // most 8, else 32), each chunk requested at once; with a single chunk the
+  // words stay in registers for the second pass instead of being read
+  // again. per is uniform, so every thread takes the same instance.
   int seq_cnt = 0;
-  int r = seq_base + block_exclusive_scan256(mine, scr, &seq_cnt);
-  for (int k0 = 0; k0 < per; k0 += 8) {
-    int v[8];
+  auto pack_body = [&](auto chunk) {
+    constexpr int kChunk = decltype(chunk)::value;
+    int v[kChunk];
+    auto load = [&](int k0) {
+      // Clamped positions, then the validity test (see eos_enc_count).
+      if (!a.all_active) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int t = t0 + k0 + u;
-      v[u] = (k0 + u < per && t < a.tokens) ? (a.all_active ? 1 : m[t]) : 0;
+        for (int u = 0; u < kChunk; ++u)
+          if (k0 + u < per) v[u] = m[min(t0 + k0 + u, a.tokens - 1)];  // uniform test
+      }
+#pragma unroll
+      for (int u = 0; u < kChunk; ++u) {
+        const int t = t0 + k0 + u;
+        const bool in = k0 + u < per && t < a.tokens;
+        v[u] = in && (a.all_active || v[u] != 0) ? 1 : 0;
+      }
+    };
+    int mine = 0;
+    for (int k0 = 0; k0 < per; k0 += kChunk) {
+      load(k0);
+#pragma unroll
+      for (int u = 0; u < kChunk; ++u) mine += v[u] != 0 ? 1 : 0;
     }
+    int r = seq_base + block_exclusive_scan256(mine, scr, &seq_cnt);
+    for (int k0 = 0; k0 < per; k0 += kChunk) {
+      if (per > kChunk) load(k0);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (v[u] != 0) {
-        a.row_b[r] = b;
-        a.row_t[r] = t0 + k0 + u;
-        ++r;
+      for (int u = 0; u < kChunk; ++u) {
+        if (v[u] != 0) {
+          a.row_b[r] = b;
+          a.row_t[r] = t0 + k0 + u;
+          ++r;
+        }
       }
     }
-  }
+  };
+  if (per <= 8)
+    pack_body(std::integral_constant<int, 8>{});
+  else
+    pack_body(std::integral_constant<int, 32>{});
   const int padded = (seq_cnt + 7) & ~7;
   if (tid < padded - seq_cnt) {
     a.row_b[seq_base + seq_cnt + tid] = b;
@@ -1752,12 +1774,9 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
     for (int t0 = tid; t0 < a.tokens; t0 += 8 * 1024) {
       int mv[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int t = t0 + 1024 * i;
-        mv[i] = t < a.tokens ? a.mask[(size_t)b * a.tokens + t] : 0;
-      }
+      for (int i = 0; i < 8; ++i) mv[i] = a.mask[(size_t)b * a.tokens + min(t0 + 1024 * i, a.tokens - 1)];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) mine += mv[i] != 0 ? 1 : 0;
+      for (int i = 0; i < 8; ++i) mine += (t0 + 1024 * i < a.tokens && mv[i] != 0) ? 1 : 0;
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) mine += __shfl_xor(mine, o);
@@ -1776,7 +1795,7 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
       const int m = min(32, nc - c0);
       float pv[32];
 #pragma unroll
-      for (int i = 0; i < 32; ++i) pv[i] = i < m ? src[(size_t)(c0 + i) * a.hidden] : 0.f;
+      for (int i = 0; i < 32; ++i) pv[i] = src[(size_t)(c0 + min(i, m - 1)) * a.hidden];
 #pragma unroll
       for (int i = 0; i < 32; ++i)
         if (i < m) v += pv[i];
