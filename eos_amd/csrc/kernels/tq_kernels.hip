@@ -124,11 +124,19 @@ EOS_DEV void prep_quantize_column(const TqPrepArgs& a, int c, int t, Get get) {
   const int src = prep_source(a, c);
   // All of the lane's values are fetched before any is used, so the loads
   // overlap instead of costing one round trip each.
+  // The loads come from clamped positions and the validity test is applied
+  // afterwards: a load under a per-lane condition compiles to a branch of its
+  // own that waits for its data before the next load is issued. (get is only
+  // called with a valid source: the callers pass a get that reads nothing
+  // when the block has no query rows.)
   double v[M];
+  const int srcc = src >= 0 ? src : 0;
+#pragma unroll
+  for (int m = 0; m < M; ++m) v[m] = get(srcc, min(t + 32 * m, a.d - 1));
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     const int j = t + 32 * m;
-    v[m] = (src >= 0 && j < a.d) ? get(src, j) : 0.0;
+    v[m] = (src >= 0 && j < a.d) ? v[m] : 0.0;
   }
   double mx = 0.0;
 #pragma unroll
@@ -190,16 +198,26 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_rotate(TqPrepArgs a) {
   {
     // Every query value of the 8 columns is loaded before any is stored, so
     // the staging costs one memory round trip.
+    // Loads from clamped positions, then the validity test (a load under a
+    // per-lane condition would be a branch of its own, waiting for its data
+    // before the next load). With no query rows nothing is loaded.
     constexpr int R = kMaxDim / 256;
     float qv[kPrepC][R];
+    if (a.q > 0) {
 #pragma unroll
-    for (int cc = 0; cc < kPrepC; ++cc) {
-      const int src = prep_source(a, c0 + cc);
+      for (int cc = 0; cc < kPrepC; ++cc) {
+        const int src = prep_source(a, c0 + cc);
+        const float* qrow = a.queries + (size_t)(src >= 0 ? src : 0) * a.d;
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int k = tid + 256 * r;
-        qv[cc][r] = (src >= 0 && k < a.d) ? a.queries[(size_t)src * a.d + k] : 0.0f;
+        for (int r = 0; r < R; ++r) qv[cc][r] = qrow[min(tid + 256 * r, a.d - 1)];
+#pragma unroll
+        for (int r = 0; r < R; ++r) qv[cc][r] = (src >= 0 && tid + 256 * r < a.d) ? qv[cc][r] : 0.0f;
       }
+    } else {
+#pragma unroll
+      for (int cc = 0; cc < kPrepC; ++cc)
+#pragma unroll
+        for (int r = 0; r < R; ++r) qv[cc][r] = 0.0f;
     }
 #pragma unroll
     for (int cc = 0; cc < kPrepC; ++cc)
@@ -213,9 +231,12 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_rotate(TqPrepArgs a) {
     const int kn = min(kPrepK, a.d - k0);
     float tmp[kPrepK * kPrepJ / 256];
 #pragma unroll
+    for (int r = 0; r < kPrepK * kPrepJ / 256; ++r)
+      tmp[r] = a.rot_t[(size_t)(k0 + min((tid >> 5) + 8 * r, kn - 1)) * a.d + min(j, a.d - 1)];
+#pragma unroll
     for (int r = 0; r < kPrepK * kPrepJ / 256; ++r) {
       const int kk = (tid >> 5) + 8 * r;
-      tmp[r] = (kk < kn && j < a.d) ? a.rot_t[(size_t)(k0 + kk) * a.d + j] : 0.0f;
+      tmp[r] = (kk < kn && j < a.d) ? tmp[r] : 0.0f;
     }
     __syncthreads();  // previous chunk consumed; qsh visible
 #pragma unroll
@@ -237,9 +258,11 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) 
   if (a.rot_t != nullptr) {
     prep_quantize_column(a, c, threadIdx.x & 31,
                          [&](int, int jx) { return a.qrot[(size_t)c * a.d + jx]; });
-  } else {
+  } else if (a.q > 0) {
     prep_quantize_column(a, c, threadIdx.x & 31,
                          [&](int src, int jx) { return (double)a.queries[(size_t)src * a.d + jx]; });
+  } else {
+    prep_quantize_column(a, c, threadIdx.x & 31, [&](int, int) { return 0.0; });
   }
 }
 
