@@ -343,6 +343,20 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
     return;
   }
   constexpr int kMaxPer = 12;  // hidden <= 768
+  // Every table value is loaded from a clamped column before any is used,
+  // then the validity test applies (loads under a per-lane condition compile
+  // to a branch each and wait for their data one after another); likewise
+  // gamma and beta.
+  float tv[kMaxPer], pv[kMaxPer], yv[kMaxPer], gv[kMaxPer], bv[kMaxPer];
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    const int c = min(lane + 64 * j, a.hidden - 1);
+    tv[j] = a.tok[(size_t)id * a.hidden + c];
+    pv[j] = a.pos[(size_t)p * a.hidden + c];
+    yv[j] = a.typ[(size_t)ty * a.hidden + c];
+    gv[j] = a.gamma[c];
+    bv[j] = a.beta[c];
+  }
   float v[kMaxPer];
   float s = 0.f;
 #pragma unroll
@@ -350,8 +364,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
     const int c = lane + 64 * j;
     v[j] = 0.f;
     if (c < a.hidden) {
-      v[j] = a.tok[(size_t)id * a.hidden + c] + a.pos[(size_t)p * a.hidden + c] +
-             a.typ[(size_t)ty * a.hidden + c];
+      v[j] = tv[j] + pv[j] + yv[j];
       s += v[j];
     }
   }
@@ -373,7 +386,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_embed(EncEmbedArgs a) 
     const int c = lane + 64 * j;
     y16[j] = (_Float16)0.0f;
     if (c < a.hidden) {
-      const float y = (v[j] - mean) * inv * a.gamma[c] + a.beta[c];
+      const float y = (v[j] - mean) * inv * gv[j] + bv[j];
       y16[j] = (_Float16)y;
       a.out[(size_t)row * a.hidden + c] = __builtin_bit_cast(uint16_t, y16[j]);
       amax = fmaxf(amax, fabsf(y));
@@ -1701,16 +1714,20 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_pool_part(EncPoolArgs 
     for (int e = 0; e < 8; ++e) s[gg][e] = 0.f;
   for (int r0 = r_begin + w * kRows; r0 < r_end; r0 += 4 * kRows) {
     v4i v[kRows][2];
+    // Loads from clamped columns, zeroed afterwards (see eos_enc_embed).
 #pragma unroll
     for (int u = 0; u < kRows; ++u) {
       const int r = min(r0 + u, r_end - 1);
       const uint16_t* row = a.h + (size_t)(off + r) * a.hidden;
 #pragma unroll
-      for (int gg = 0; gg < 2; ++gg) {
-        const int col = gg * 512 + lane * 8;
-        v[u][gg] = col < a.hidden ? *reinterpret_cast<const v4i*>(row + col) : v4i{0, 0, 0, 0};
-      }
+      for (int gg = 0; gg < 2; ++gg)
+        v[u][gg] = *reinterpret_cast<const v4i*>(row + min(gg * 512 + lane * 8, a.hidden - 8));
     }
+#pragma unroll
+    for (int u = 0; u < kRows; ++u)
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg)
+        if (gg * 512 + lane * 8 >= a.hidden) v[u][gg] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int u = 0; u < kRows; ++u) {
       float x[2][8];
