@@ -769,7 +769,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the scan would shard by corpus rows with one top-k merge; see DESIGN.md)",
+              "(the scan would shard by corpus rows, each GPU scoring its own rows, with one top-k merge)",
               file=sys.stderr)
         return 2
 
