@@ -353,6 +353,7 @@ def tq_leg(rt, args) -> dict:
         idx.top_k_device_deferred(dq, args.queries, args.k, dids, dsc, dstat.view(i * srow, srow))
     rt.sync()
     n_filter, ms_filter = rt.profile_read("tq_scan_filter")
+    filter_samples = rt.profile_samples("tq_scan_filter")
     rt.profile(False)
     # Per-kernel breakdown from a separate pass with every launch bracketed.
     rt.profile_reset()
@@ -376,13 +377,9 @@ def tq_leg(rt, args) -> dict:
         h.rt.close()
     bytes_per_launch = corpus.n * (corpus.dim * corpus.bits // 8 + 4)
     avg_filter_ms = ms_filter / max(n_filter, 1)
-    achieved = bytes_per_launch / (avg_filter_ms / 1e3) / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        try:
-            traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+    med_filter_ms = float(np.median(filter_samples)) if len(filter_samples) else avg_filter_ms
+    achieved = bytes_per_launch / (med_filter_ms / 1e3) / 1e9
+    traffic, traffic_note = traffic_figure()
     out = {
         "value": args.queries * corpus.n / (ms_per_step / 1e3),
         "ms_per_step": ms_per_step,
@@ -392,7 +389,10 @@ def tq_leg(rt, args) -> dict:
                    "batches_in_flight": args.streams, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "tq_scan_filter", "avg_launch_ms": avg_filter_ms,
+                     "traffic_source": traffic_note,
+                     "kernel": "tq_scan_filter", "median_launch_ms": med_filter_ms,
+                     "avg_launch_ms": avg_filter_ms, "launches_timed": int(n_filter),
+                     "min_launch_ms": float(np.min(filter_samples)) if len(filter_samples) else None,
                      "bytes_per_launch": bytes_per_launch},
         "breakdown_ms_per_step": breakdown,
         "fallback_queries": st.fallback_queries,
@@ -506,6 +506,82 @@ def maxsim_cpu_baseline(corpus, q, doc_len: int, ndocs: int) -> dict:
                      "sample": f"{q.shape[0]} queries split over {threads} threads ({dt_all:.2f} s)"},
         "cpu_model": _cpu_model(),
     }
+
+
+def code_object_sha256(stem: str = "tq") -> str | None:
+    """SHA-256 of a built code object (eos_amd/_build/<stem>.hsaco), the
+    identity of the kernels a counter file was captured on."""
+    import hashlib
+    from eos_amd.build import BUILD_DIR
+    path = os.path.join(BUILD_DIR, f"{stem}.hsaco")
+    if not os.path.exists(path):
+        return None
+    return hashlib.sha256(open(path, "rb").read()).hexdigest()
+
+
+def traffic_figure() -> tuple:
+    """HBM bytes per filter-scan launch from the committed counter summary,
+    only when it was captured on the code object this run loads (else None,
+    with the reason)."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None, "no counter summary"
+    try:
+        rec = json.load(open(TRAFFIC_FILE))
+    except (OSError, ValueError) as e:
+        return None, f"counter summary unreadable: {e}"
+    want = rec.get("code_object_sha256")
+    have = code_object_sha256("tq")
+    if want is None or have is None or want != have:
+        return None, (f"stale: counters captured on tq.hsaco {str(want)[:12]}, "
+                      f"this run loads {str(have)[:12]}")
+    return rec.get("hbm_bytes_per_launch"), (f"{os.path.relpath(TRAFFIC_FILE, ROOT)} "
+                                             f"(tq.hsaco {have[:12]}, commit {rec.get('commit')})")
+
+
+def read_calibration(rt, mb: int, reps: int = 5) -> dict:
+    """A read-only stream over `mb` MB (probe kernel eos_probe_read_stream:
+    16-byte non-temporal loads, 8 in flight per thread, XOR-folded into one
+    word per thread): the achievable rate of a kernel that only reads, which
+    is what the corpus scans are (>= 99.7 % of their bytes are reads)."""
+    import ctypes as C
+    from eos_amd import _lib
+    from eos_amd.build import PROBE_PATH
+    from eos_amd.runtime import DeviceBuffer
+
+    img = open(PROBE_PATH, "rb").read()
+    mod = C.c_void_p()
+    _lib.call("eoship_module_load", rt.handle, img, C.c_size_t(len(img)), C.byref(mod))
+    fn = C.c_void_p()
+    _lib.call("eoship_function", mod, b"eos_probe_read_stream", C.byref(fn))
+    nbytes = mb * 1_000_000 // 16 * 16
+    blocks = rt.info()["compute_units"] * 8
+
+    class Args(C.Structure):
+        _fields_ = [("src", C.c_void_p), ("sink", C.c_void_p), ("words", C.c_longlong)]
+
+    src = DeviceBuffer(rt, nbytes)
+    _lib.call("eoship_memset", rt.handle, src.ptr, 1, C.c_size_t(nbytes))
+    sink = DeviceBuffer(rt, blocks * 256 * 16)
+    args = Args(src.ptr, sink.ptr, nbytes // 16)
+    params = (C.c_void_p * 1)(C.cast(C.pointer(args), C.c_void_p))
+    grid = (C.c_uint32 * 3)(blocks, 1, 1)
+    block = (C.c_uint32 * 3)(256, 1, 1)
+    try:
+        for _ in range(2):
+            _lib.call("eoship_launch", rt.handle, fn, grid, block, C.c_uint32(0), params)
+        rt.sync()
+        times = []
+        for _ in range(reps):
+            rt.mark(4)
+            _lib.call("eoship_launch", rt.handle, fn, grid, block, C.c_uint32(0), params)
+            rt.mark(5)
+            times.append(rt.elapsed_ms(4, 5))
+    finally:
+        src.free()
+        sink.free()
+        _lib.call("eoship_module_unload", mod)
+    ms = float(np.median(times))
+    return {"bytes": nbytes, "ms": ms, "read_GBps": nbytes / (ms / 1e3) / 1e9}
 
 
 def copy_calibration(rt, mb: int, reps: int = 5) -> dict:
@@ -798,8 +874,18 @@ def main() -> int:
             # the vendor peak.
             cal = copy_calibration(rt, args.copy_calibration_mb)
             out["copy_calibration"] = cal
-            out["roofline"]["peak_measured"] = cal["read_plus_write_GBps"]
-            out["roofline"]["frac_measured"] = out["roofline"]["achieved"] / cal["read_plus_write_GBps"]
+            # The scan only reads: its measured peak is a read-only stream,
+            # over a buffer past the 256 MB Infinity Cache (HBM) and over
+            # the corpus's own size (which the cache can partly hold).
+            rd = read_calibration(rt, args.copy_calibration_mb)
+            rd_corpus = read_calibration(rt, out["roofline"]["bytes_per_launch"] // 1_000_000)
+            out["read_calibration"] = {"hbm": rd, "corpus_size": rd_corpus}
+            roof = out["roofline"]
+            roof["peak_measured_read_only"] = rd["read_GBps"]
+            roof["frac_measured_read_only"] = roof["achieved"] / rd["read_GBps"]
+            roof["peak_measured_read_only_corpus_size"] = rd_corpus["read_GBps"]
+            roof["peak_measured_copy"] = cal["read_plus_write_GBps"]
+            roof["frac_measured_copy"] = roof["achieved"] / cal["read_plus_write_GBps"]
     if not args.skip_tq and args.shard_n > 0:
         log(f"c2 shard ({args.shard_n} vectors)")
         out["tq_shard8_c2"] = tq_shard_leg(rt, args.shard_n, args.queries, args.k, args.steps,

@@ -145,6 +145,12 @@ class EosHipMllPlan(C.Structure):
         ("token_input", C.c_char * 64),
         ("mask_input", C.c_char * 64),
         ("output_name", C.c_char * 64),
+        ("pooling", C.c_int32),
+        ("type_vocab", C.c_int32),
+        ("weights_quantized", C.c_int32),
+        ("reserved", C.c_int32),
+        ("ln_eps", C.c_double),
+        ("type_input", C.c_char * 64),
     ]
 
 
@@ -226,6 +232,7 @@ _SIGNATURES = {
     "eoship_h2d": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
     "eoship_d2h": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
     "eoship_d2d": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "eoship_memset": ([C.c_void_p, C.c_void_p, C.c_int, C.c_size_t, C.c_void_p], C.c_int),
     "eoship_sync": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_runtime_wait": ([C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_module_load": ([C.c_void_p, C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p), C.c_void_p],
@@ -239,6 +246,8 @@ _SIGNATURES = {
     "eoship_profile_read": ([C.c_void_p, C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_double),
                              C.c_void_p], C.c_int),
     "eoship_profile_reset": ([C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_profile_samples": ([C.c_void_p, C.c_char_p, C.c_void_p, C.c_int64,
+                                C.POINTER(C.c_int64), C.c_void_p], C.c_int),
     "eoship_timer_mark": ([C.c_void_p, C.c_int, C.c_void_p], C.c_int),
     "eoship_timer_elapsed": ([C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_double), C.c_void_p],
                              C.c_int),
@@ -367,6 +376,7 @@ _SIGNATURES = {
                                        C.c_int32, C.c_int32, C.c_void_p, C.c_void_p], C.c_int),
     "eoship_encoder_status": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_int32), C.c_void_p], C.c_int),
     "eoship_encoder_set_fused_tail": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p], C.c_int),
+    "eoship_encoder_set_pooling": ([C.c_void_p, C.c_void_p, C.c_int32, C.c_void_p], C.c_int),
     "eoship_encoder_attention_moves": ([C.c_void_p, C.c_void_p, C.POINTER(C.c_int64), C.c_void_p],
                                        C.c_int),
 }

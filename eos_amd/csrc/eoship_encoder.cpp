@@ -79,6 +79,10 @@ struct EosHipEncoder {
   // positions).
   bool scaled_scores = true;
   bool attend_all = false;
+  // BERT family pooling: 0 masked mean (the default), 1 CLS (position 0's
+  // row), as bert_embedder's "pooling" attribute (bert_embedder_ops.go:
+  // 150-152, 183-196).
+  int pooling = 0;
   int odim = 0;
   float* proj = nullptr;
   std::vector<void*> owned;
@@ -98,6 +102,7 @@ struct EosHipEncoder {
   uint16_t* vt = nullptr;
   int vt_ld = 0;
   int32_t *row_b = nullptr, *row_t = nullptr, *seq_off = nullptr, *seq_cnt = nullptr;
+  int32_t* seq_q = nullptr;  // query rows per sequence (CLS pooling may add one)
   int32_t *total = nullptr, *status = nullptr;
   // host-API staging
   void* io = nullptr;
@@ -106,8 +111,8 @@ struct EosHipEncoder {
   ~EosHipEncoder() {
     for (void* p : owned)
       if (p) hipFree(p);
-    void* act[] = {h, qkv, ctx, mid, h8, hs, pool_part, vt, row_b, row_t, seq_off, seq_cnt, total,
-                   status, io};
+    void* act[] = {h,     qkv,     ctx,     mid,   h8,    hs,     pool_part, vt, row_b,
+                   row_t, seq_off, seq_cnt, seq_q, total, status, io};
     for (void* p : act)
       if (p) hipFree(p);
   }
@@ -184,8 +189,8 @@ struct EosHipEncoder {
   int ensure_activations(int batch, int tokens, char** err) {
     const size_t rows = row_capacity(batch, tokens);
     if (rows <= cap_rows && batch <= cap_batch) return 0;
-    void* act[] = {h, qkv, ctx, mid, h8, hs, pool_part, vt, row_b, row_t, seq_off, seq_cnt, total,
-                   status};
+    void* act[] = {h,     qkv,     ctx,     mid,   h8,    hs,    pool_part, vt,
+                   row_b, row_t, seq_off, seq_cnt, seq_q, total, status};
     for (void* p : act)
       if (p) hipFree(p);
     h = qkv = ctx = mid = nullptr;
@@ -193,7 +198,7 @@ struct EosHipEncoder {
     hs = nullptr;
     pool_part = nullptr;
     vt = nullptr;
-    row_b = row_t = seq_off = seq_cnt = total = status = nullptr;
+    row_b = row_t = seq_off = seq_cnt = seq_q = total = status = nullptr;
     cap_rows = 0;
     cap_batch = 0;
     const size_t H = desc.hidden, F = desc.intermediate;
@@ -211,6 +216,7 @@ struct EosHipEncoder {
         rt->alloc(rows * 4, reinterpret_cast<void**>(&row_t), err) ||
         rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_off), err) ||
         rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_cnt), err) ||
+        rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_q), err) ||
         rt->alloc(4, reinterpret_cast<void**>(&total), err) ||
         rt->alloc(8, reinterpret_cast<void**>(&status), err))
       return 1;
@@ -235,7 +241,24 @@ struct EosHipEncoder {
     // status[0]: an id out of range; status[1]: attention reference moves.
     hipError_t e = hipMemsetAsync(status, 0, 8, rt->stream);
     if (e != hipSuccess) return hip_err(err, "hipMemsetAsync(status)", e);
-    EncPackArgs pk{d_mask, row_b, row_t, seq_off, seq_cnt, total, batch, tokens, attend_all ? 1 : 0};
+    const bool cls = family == 0 && pooling == 1;
+    EncPackArgs pk{};
+    pk.mask = d_mask;
+    pk.row_b = row_b;
+    pk.row_t = row_t;
+    pk.seq_off = seq_off;
+    pk.seq_cnt = seq_cnt;
+    pk.total = total;
+    pk.batch = batch;
+    pk.tokens = tokens;
+    pk.all_active = attend_all ? 1 : 0;
+    pk.seq_q = seq_q;
+    pk.cls_row = cls ? 1 : 0;
+    pk.ids = d_ids;
+    pk.type_ids = d_types;
+    pk.vocab = desc.vocab;
+    pk.ntype = desc.type_vocab;
+    pk.status = status;
     if (rt->launch("eos_enc_count", dim3(batch), dim3(256), 0, &pk, err) != 0 ||
         rt->launch("eos_enc_pack", dim3(batch), dim3(256), 0, &pk, err) != 0)
       return 1;
@@ -306,7 +329,7 @@ struct EosHipEncoder {
                "enc_gemm_qkv", vt) != 0)
         return 1;
       const double log2e = 1.4426950408889634;
-      EncAttnArgs at{qkv, vt, ctx, seq_off, seq_cnt, batch, nh, H, tokens, vt_ld,
+      EncAttnArgs at{qkv, vt, ctx, seq_off, seq_cnt, seq_q, batch, nh, H, tokens, vt_ld,
                      (float)(scaled_scores ? log2e / std::sqrt((double)hd) : log2e), status + 1};
       if (rt->launch(attn_name, dim3((tokens + 127) / 128, nh, batch), dim3(256), 0, &at, err) != 0)
         return 1;
@@ -332,9 +355,12 @@ struct EosHipEncoder {
     EncPoolArgs pl{h,     seq_off, seq_cnt,   d_out,   proj,
                    pool_part, batch, H,     family,  out_dim(),
                    nchunk, attend_all ? d_mask : nullptr, tokens};
-    if (rt->launch("eos_enc_pool_part", dim3((unsigned)nchunk, (unsigned)batch), dim3(256), 0, &pl,
-                   err) != 0)
+    if (cls) {
+      pl.cls_seq_q = seq_q;
+    } else if (rt->launch("eos_enc_pool_part", dim3((unsigned)nchunk, (unsigned)batch), dim3(256),
+                          0, &pl, err) != 0) {
       return 1;
+    }
     return rt->launch("eos_enc_pool", dim3(batch), dim3(1024), 0, &pl, err);
   }
 };
@@ -606,6 +632,17 @@ int eoship_encoder_set_fused_tail(EosHipRuntime* rt, EosHipEncoder* enc, int32_t
                                    char** err) {
   if (rt == nullptr || enc == nullptr) return set_err(err, "eoship_encoder_set_fused_tail: NULL argument");
   enc->fused_tail = fused != 0;
+  return 0;
+}
+
+int eoship_encoder_set_pooling(EosHipRuntime* rt, EosHipEncoder* enc, int32_t pooling,
+                               char** err) {
+  if (rt == nullptr || enc == nullptr) return set_err(err, "eoship_encoder_set_pooling: NULL argument");
+  if (pooling != 0 && pooling != 1)
+    return set_err(err, "eoship_encoder_set_pooling: pooling must be 0 (masked_mean) or 1 (cls)");
+  if (pooling == 1 && enc->family != 0)
+    return set_err(err, "eoship_encoder_set_pooling: cls pooling applies to the BERT family only");
+  enc->pooling = pooling;
   return 0;
 }
 

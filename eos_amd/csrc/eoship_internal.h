@@ -39,6 +39,9 @@ struct Runtime {
   std::vector<ProfileRecord> records;
   std::vector<hipEvent_t> event_pool;  // recycled profiling events
   std::map<std::string, std::pair<int64_t, double>> totals;
+  // Every recorded launch's duration, per label, in launch order (cleared
+  // with the totals).
+  std::map<std::string, std::vector<float>> samples;
   hipEvent_t timer[kTimerSlots];
 
   int function(const char* name, hipFunction_t* out, char** err);

@@ -711,6 +711,9 @@ struct PlanResult {
   EosHipMllPlan plan{};
   std::string token_param;
   std::vector<LayerParams> layers;
+  // BERT family: the bert_embedder step's inputs (ids, mask, types, the five
+  // embedding tensors, 16 per layer in the reference's order).
+  std::vector<std::string> bert_inputs;
 };
 
 int plan_fail(char** err, const std::string& entry, size_t step, const char* fmt, const char* a = "",
@@ -721,8 +724,212 @@ int plan_fail(char** err, const std::string& entry, size_t step, const char* fmt
                  step, msg);
 }
 
-void copy_name(char* dst, size_t cap, const std::string& s) {
+// Copies a name into a fixed plan field; false when it does not fit (the
+// classifiers refuse such names, so a plan never names a truncated value).
+bool copy_name(char* dst, size_t cap, const std::string& s) {
   std::snprintf(dst, cap, "%s", s.c_str());
+  return s.size() < cap;
+}
+
+// Go's strconv.Atoi: an optional sign and decimal digits, nothing else.
+bool go_atoi(const std::string& s, long long* out) {
+  size_t i = 0;
+  if (i < s.size() && (s[i] == '+' || s[i] == '-')) ++i;
+  if (i == s.size()) return false;
+  for (size_t j = i; j < s.size(); ++j)
+    if (s[j] < '0' || s[j] > '9') return false;
+  if (s.size() - i > 18) return false;
+  *out = std::strtoll(s.c_str(), nullptr, 10);
+  return true;
+}
+
+// The bert_embedder step (one fused step of BERT embeddings, every encoder
+// layer, pooling and L2, runtime/backend/bert_embedder_ops.go:10-197; the
+// module the pretrained-BERT importer emits, runtime/pretrained_bert_importer.go:
+// 901-1009): attributes as bertEmbedderConfigFromAttrs reads them, 8 + 16 L
+// inputs (input_ids, attention_mask, token_type_ids entry inputs, then the
+// five embedding tensors and 16 tensors per layer, all params), the one
+// output returned. Shapes are those BERTEmbedderReferenceWithPooling and
+// BERTEncoderLayerReference accept, and the fused encoder's own limits.
+int classify_bert(const EosHipMll* m, const Json& art, const std::string& entry, const Json& ep,
+                  PlanResult* out, char** err) {
+  auto fail = [&](size_t step, const std::string& msg) {
+    return plan_fail(err, entry, step, "%s", msg.c_str());
+  };
+  const Json* steps = art.get("steps");
+  const Json* bstep = nullptr;
+  size_t bi = 0, nsteps = 0;
+  std::string result;
+  bool returned = false;
+  for (size_t i = 0; i < steps->arr.size(); ++i) {
+    const Json& st = steps->arr[i];
+    if (st.str_or("entry", "") != entry) continue;
+    ++nsteps;
+    const std::string kind = st.str_or("kind", "");
+    if (returned) return fail(i, "steps after return");
+    if (kind == "bert_embedder") {
+      if (bstep != nullptr) return fail(i, "a second bert_embedder step");
+      bstep = &st;
+      bi = i;
+      const Json* o = st.get("outputs");
+      if (o == nullptr || o->kind != Json::kArr || o->arr.size() != 1)
+        return fail(i, "bert_embedder step expects 1 output");
+      result = o->arr[0].str;
+    } else if (kind == "return") {
+      const Json* o = st.get("outputs");
+      if (bstep == nullptr || o == nullptr || o->kind != Json::kArr || o->arr.size() != 1 ||
+          o->arr[0].str != result)
+        return fail(i, "return of something other than the bert_embedder output");
+      returned = true;
+    } else {
+      return fail(i, "step kind \"" + kind + "\" beside a bert_embedder step");
+    }
+  }
+  if (!returned) return set_err(err, "eoship_mll_classify: entry \"%s\" has no return step", entry.c_str());
+  // Attributes (bertEmbedderConfigFromAttrs, bert_embedder_ops.go:35-77).
+  long long layers = 1, heads = 1;
+  double eps = 1e-12;
+  std::string act = "gelu", pooling = "masked_mean";
+  if (const Json* at = bstep->get("attributes")) {
+    if (at->kind != Json::kObj) return fail(bi, "attributes are not an object");
+    for (const auto& kv : at->obj) {
+      if (kv.second.kind != Json::kStr) return fail(bi, "attribute \"" + kv.first + "\" is not a string");
+      const std::string& v = kv.second.str;
+      if (v.empty()) continue;
+      if (kv.first == "num_hidden_layers") {
+        if (!go_atoi(v, &layers) || layers <= 0)
+          return fail(bi, "bert_embedder num_hidden_layers \"" + v + "\" is invalid");
+      } else if (kv.first == "num_attention_heads") {
+        if (!go_atoi(v, &heads) || heads <= 0)
+          return fail(bi, "bert_embedder num_attention_heads \"" + v + "\" is invalid");
+      } else if (kv.first == "epsilon") {
+        char* end = nullptr;
+        eps = std::strtod(v.c_str(), &end);
+        if (end == v.c_str() || *end != 0) return fail(bi, "bert_embedder epsilon \"" + v + "\" is invalid");
+        if (eps < 0) return fail(bi, "bert_embedder epsilon must be non-negative");
+        if (!std::isfinite(eps)) return fail(bi, "bert_embedder epsilon is not finite");
+      } else if (kv.first == "hidden_act") {
+        act = v;
+      } else if (kv.first == "pooling") {
+        pooling = v;
+      }
+    }
+  }
+  if (act != "gelu")
+    return fail(bi, "bert_embedder unsupported hidden_act \"" + act + "\"; only gelu is supported");
+  if (pooling != "masked_mean" && pooling != "cls")
+    return fail(bi, "bert_embedder unsupported pooling \"" + pooling +
+                        "\"; supported values are masked_mean and cls");
+  std::vector<std::string> in;
+  if (const Json* a = bstep->get("inputs"))
+    for (const Json& x : a->arr) in.push_back(x.str);
+  if (layers > 4096 || (long long)in.size() != 8 + 16 * layers) {
+    char msg[160];
+    std::snprintf(msg, sizeof(msg), "bert_embedder expects %lld tensors for %lld layers, got %zu",
+                  8 + 16 * layers, layers, in.size());
+    return fail(bi, msg);
+  }
+  // input_ids, attention_mask, token_type_ids: the entry's i32 [B, T] inputs.
+  const Json* eins = ep.get("inputs");
+  for (int k = 0; k < 3; ++k) {
+    const Json* found = nullptr;
+    if (eins != nullptr && eins->kind == Json::kArr)
+      for (const Json& e : eins->arr)
+        if (e.str_or("name", "") == in[k]) found = &e;
+    const Json* ty = found != nullptr ? found->get("type") : nullptr;
+    const Json* tt = ty != nullptr ? ty->get("tensor") : nullptr;
+    const Json* shape = tt != nullptr ? tt->get("shape") : nullptr;
+    if (tt == nullptr || tt->str_or("dtype", "") != "i32" || shape == nullptr ||
+        shape->kind != Json::kArr || shape->arr.size() != 2)
+      return fail(bi, "bert_embedder input \"" + in[k] + "\" is not an i32 [B, T] entry input");
+  }
+  // Tensors: the payload of every other input, of the shape the reference
+  // validates (validateBERTEmbeddingTables, validateBERTLayerNormParam, the
+  // per-layer checks of BERTEncoderLayerReference).
+  auto tensor = [&](const std::string& n, const Tensor** t) -> bool {
+    *t = m->tensor(n);
+    return *t != nullptr && ((*t)->kind == EOSHIP_MLL_F32 || (*t)->kind == EOSHIP_MLL_F16 ||
+                             (*t)->kind == EOSHIP_MLL_Q8 || (*t)->kind == EOSHIP_MLL_Q4);
+  };
+  const Tensor *tok = nullptr, *pos = nullptr, *typ = nullptr, *g = nullptr, *be = nullptr;
+  if (!tensor(in[3], &tok) || !tensor(in[4], &pos) || !tensor(in[5], &typ) || !tensor(in[6], &g) ||
+      !tensor(in[7], &be))
+    return fail(bi, "an embedding tensor is missing or not f32, f16, q8 or q4");
+  if (tok->dims.size() != 2 || pos->dims.size() != 2 || typ->dims.size() != 2)
+    return fail(bi, "embedding tables must be rank 2");
+  const int64_t H = tok->dims[1];
+  if (pos->dims[1] != H || typ->dims[1] != H)
+    return fail(bi, "embedding tables differ in width");
+  if (g->dims.size() != 1 || g->dims[0] != H || be->dims.size() != 1 || be->dims[0] != H)
+    return fail(bi, "embedding layernorm parameters must be [hidden]");
+  if (H % heads != 0) return fail(bi, "hidden size is not a multiple of num_attention_heads");
+  int64_t F = -1;
+  for (long long l = 0; l < layers; ++l) {
+    const std::string* w = &in[8 + 16 * l];
+    const Tensor* t[16];
+    for (int k = 0; k < 16; ++k)
+      if (!tensor(w[k], &t[k])) return fail(bi, "layer tensor \"" + w[k] + "\" is missing or not f32, f16, q8 or q4");
+    if (F < 0 && t[10]->dims.size() == 2) F = t[10]->dims[0];
+    auto is = [](const Tensor* x, int64_t a, int64_t b) {
+      return b < 0 ? (x->dims.size() == 1 && x->dims[0] == a)
+                   : (x->dims.size() == 2 && x->dims[0] == a && x->dims[1] == b);
+    };
+    const bool ok = is(t[0], H, H) && is(t[1], H, -1) && is(t[2], H, H) && is(t[3], H, -1) &&
+                    is(t[4], H, H) && is(t[5], H, -1) && is(t[6], H, H) && is(t[7], H, -1) &&
+                    is(t[8], H, -1) && is(t[9], H, -1) && is(t[10], F, H) && is(t[11], F, -1) &&
+                    is(t[12], H, F) && is(t[13], H, -1) && is(t[14], H, -1) && is(t[15], H, -1);
+    if (!ok) {
+      char msg[96];
+      std::snprintf(msg, sizeof(msg), "layer %lld tensor shapes do not match hidden %lld", l,
+                    (long long)H);
+      return fail(bi, msg);
+    }
+  }
+  // What the fused encoder binds (its kernels' shapes).
+  const int64_t hd = H / heads;
+  if ((H != 128 && H != 256 && H != 384 && H != 512 && H != 768) ||
+      (hd != 32 && hd != 64 && hd != 128 && hd != 256) || F <= 0 || F % 128 != 0 ||
+      tok->dims[0] > (1ll << 30) || pos->dims[0] > 65536 || typ->dims[0] > 65536) {
+    char msg[160];
+    std::snprintf(msg, sizeof(msg),
+                  "hidden %lld, head dim %lld, intermediate %lld outside the fused encoder "
+                  "(hidden 128/256/384/512/768, head dim 32/64/128/256, intermediate a multiple of 128)",
+                  (long long)H, (long long)hd, (long long)F);
+    return fail(bi, msg);
+  }
+  PlanResult r;
+  EosHipMllPlan& p = r.plan;
+  p.route = EOSHIP_PLAN_BERT_EMBEDDER;
+  p.layers = (int32_t)layers;
+  p.distinct_layers = (int32_t)layers;
+  p.model_dim = (int32_t)H;
+  p.heads = (int32_t)heads;
+  p.hidden_dim = (int32_t)F;
+  p.vocab = (int32_t)tok->dims[0];
+  p.max_sequence = (int32_t)pos->dims[0];
+  p.output_dim = (int32_t)H;
+  p.batched = 1;
+  p.steps = (int32_t)nsteps;
+  p.pooling = pooling == "cls" ? 1 : 0;
+  p.ln_eps = eps;
+  p.type_vocab = (int32_t)typ->dims[0];
+  bool quantize = false;
+  for (long long l = 0; l < layers; ++l)
+    for (int k : {0, 2, 4, 6, 10, 12}) {
+      const Tensor* t = m->tensor(in[8 + 16 * l + k]);
+      quantize = quantize || t->kind == EOSHIP_MLL_F32 || t->kind == EOSHIP_MLL_F16;
+    }
+  p.weights_quantized = quantize ? 1 : 0;
+  if (!copy_name(p.entry, sizeof(p.entry), entry) ||
+      !copy_name(p.token_input, sizeof(p.token_input), in[0]) ||
+      !copy_name(p.mask_input, sizeof(p.mask_input), in[1]) ||
+      !copy_name(p.type_input, sizeof(p.type_input), in[2]) ||
+      !copy_name(p.output_name, sizeof(p.output_name), result))
+    return set_err(err, "eoship_mll_classify: an entry, input or output name of %zu bytes or more",
+                   sizeof(p.entry));
+  r.bert_inputs = in;
+  *out = std::move(r);
+  return 0;
 }
 
 int classify(const EosHipMll* m, const char* entry_name, PlanResult* out, char** err) {
@@ -737,14 +944,21 @@ int classify(const EosHipMll* m, const char* entry_name, PlanResult* out, char**
     entry = man->str_or("batch_entry", "");
     if (entry.empty()) entry = man->str_or("pooled_entry", "");
   }
+  const Json* eps = art.get("entry_points");
+  if (entry.empty() && eps != nullptr && eps->kind == Json::kArr && eps->arr.size() == 1)
+    entry = eps->arr[0].str_or("name", "");
   if (entry.empty())
     return set_err(err, "eoship_mll_classify: no entry named and no embedding_manifest entry");
-  const Json* eps = art.get("entry_points");
   const Json* ep = nullptr;
   if (eps != nullptr && eps->kind == Json::kArr)
     for (const Json& e : eps->arr)
       if (e.str_or("name", "") == entry) ep = &e;
   if (ep == nullptr) return set_err(err, "eoship_mll_classify: unknown entrypoint \"%s\"", entry.c_str());
+  if (const Json* all = art.get("steps"))
+    if (all->kind == Json::kArr)
+      for (const Json& st : all->arr)
+        if (st.str_or("entry", "") == entry && st.str_or("kind", "") == "bert_embedder")
+          return classify_bert(m, art, entry, *ep, out, err);
   const Json* ins = ep->get("inputs");
   const Json* outs = ep->get("outputs");
   if (ins == nullptr || ins->kind != Json::kArr || ins->arr.size() != 2 || outs == nullptr ||
@@ -1044,7 +1258,14 @@ int classify(const EosHipMll* m, const char* entry_name, PlanResult* out, char**
   p.max_sequence = 0;
   if (man != nullptr)
     if (const Json* tk = man->get("tokenizer"))
-      if (const Json* ms = tk->get("max_sequence")) p.max_sequence = (int32_t)ms->num;
+      if (const Json* ms = tk->get("max_sequence")) {
+        // A finite integer in 1..8192 (it sizes the bind-time RoPE table).
+        const double v = ms->num;
+        if (ms->kind != Json::kNum || !(v >= 1.0 && v <= 8192.0) || v != std::floor(v))
+          return set_err(err, "eoship_mll_classify: tokenizer.max_sequence must be an integer in "
+                              "1..8192");
+        p.max_sequence = (int32_t)v;
+      }
   if (p.max_sequence <= 0) p.max_sequence = 512;
   p.output_dim = (int32_t)D;
   p.batched = batched;
@@ -1064,10 +1285,12 @@ int classify(const EosHipMll* m, const char* entry_name, PlanResult* out, char**
   p.options.role = 0;
   p.options.scaled_scores = scaled ? 1 : 0;
   p.options.attend_padding = key_masked ? 0 : 1;
-  copy_name(p.entry, sizeof(p.entry), entry);
-  copy_name(p.token_input, sizeof(p.token_input), tok_in);
-  copy_name(p.mask_input, sizeof(p.mask_input), mask_in);
-  copy_name(p.output_name, sizeof(p.output_name), result_name);
+  if (!copy_name(p.entry, sizeof(p.entry), entry) ||
+      !copy_name(p.token_input, sizeof(p.token_input), tok_in) ||
+      !copy_name(p.mask_input, sizeof(p.mask_input), mask_in) ||
+      !copy_name(p.output_name, sizeof(p.output_name), result_name))
+    return set_err(err, "eoship_mll_classify: an entry, input or output name of %zu bytes or more",
+                   sizeof(p.entry));
   *out = std::move(r);
   return 0;
 }
@@ -1250,10 +1473,12 @@ int classify_retrieval(const EosHipMll* m, const char* entry_name, EosHipRetriev
     p.docs_q4 = t->kind == EOSHIP_MLL_Q4 ? 1 : 0;
   }
   p.steps = nsteps;
-  copy_name(p.entry, sizeof(p.entry), entry);
-  copy_name(p.query_input, sizeof(p.query_input), query);
-  copy_name(p.docs_input, sizeof(p.docs_input), docs);
-  copy_name(p.ids_input, sizeof(p.ids_input), ids);
+  if (!copy_name(p.entry, sizeof(p.entry), entry) ||
+      !copy_name(p.query_input, sizeof(p.query_input), query) ||
+      !copy_name(p.docs_input, sizeof(p.docs_input), docs) ||
+      !copy_name(p.ids_input, sizeof(p.ids_input), ids))
+    return set_err(err, "%s: an entry, input or param name of %zu bytes or more", what,
+                   sizeof(p.entry));
   *out = p;
   return 0;
 }
@@ -1340,6 +1565,161 @@ int eoship_mll_classify(const EosHipMll* m, const char* entry, EosHipMllPlan* pl
   return 0;
 }
 
+}  // extern "C"
+
+namespace {
+
+float half_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, f = h & 0x3ffu;
+  uint32_t bits;
+  if (e == 0x1f) {
+    bits = sign | 0x7f800000u | (f << 13);
+  } else if (e != 0) {
+    bits = sign | ((e + 112u) << 23) | (f << 13);
+  } else if (f == 0) {
+    bits = sign;
+  } else {  // subnormal: f * 2^-24, exact in f32
+    const float v = (float)f * 5.9604644775390625e-8f;
+    std::memcpy(&bits, &v, 4);
+    bits |= sign;
+  }
+  float out;
+  std::memcpy(&out, &bits, 4);
+  return out;
+}
+
+// f32 values of a tensor as the reference decodes it (q8: code * scale, q4:
+// (nibble - 8) * scale, runtime/weight_file.go:315-351).
+std::vector<float> values_of(const EosHipMll* m, const Tensor& t) {
+  std::vector<float> v((size_t)t.elements);
+  const uint8_t* b = m->bytes.data() + t.off;
+  if (t.kind == EOSHIP_MLL_F32) {
+    std::memcpy(v.data(), b, v.size() * 4);
+  } else if (t.kind == EOSHIP_MLL_F16) {
+    for (size_t i = 0; i < v.size(); ++i) {
+      uint16_t h;
+      std::memcpy(&h, b + 2 * i, 2);
+      v[i] = half_to_float(h);
+    }
+  } else {
+    const std::vector<int8_t> c = codes_of(m, t);
+    const float sc = t.scale > 0.f ? t.scale : 0.f;
+    for (size_t i = 0; i < v.size(); ++i) v[i] = (float)c[i] * sc;
+  }
+  return v;
+}
+
+// int8 codes [rows][cols] with one scale per row: a q8/q4 payload keeps its
+// codes and per-tensor scale; f32/f16 values are quantized per row (output
+// channel): scale = max|w| / 127, code = rint(w / scale) clamped to +-127.
+void codes_per_row(const EosHipMll* m, const Tensor& t, std::vector<int8_t>* codes,
+                   std::vector<float>* scales) {
+  const int64_t rows = t.dims[0], cols = t.dims[1];
+  if (t.kind == EOSHIP_MLL_Q8 || t.kind == EOSHIP_MLL_Q4) {
+    *codes = codes_of(m, t);
+    scales->assign((size_t)rows, t.scale > 0.f ? t.scale : 0.f);
+    return;
+  }
+  const std::vector<float> v = values_of(m, t);
+  codes->assign((size_t)(rows * cols), 0);
+  scales->assign((size_t)rows, 0.f);
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* w = v.data() + r * cols;
+    float mx = 0.f;
+    for (int64_t c = 0; c < cols; ++c) mx = std::max(mx, std::fabs(w[c]));
+    const float sc = mx > 0.f ? mx / 127.0f : 0.f;
+    (*scales)[(size_t)r] = sc;
+    if (sc == 0.f) continue;
+    for (int64_t c = 0; c < cols; ++c) {
+      const float q = std::nearbyint(w[c] / sc);
+      (*codes)[(size_t)(r * cols + c)] = (int8_t)std::max(-127.f, std::min(127.f, q));
+    }
+  }
+}
+
+// Binds a classified bert_embedder plan to the fused BERT encoder.
+int bind_bert(EosHipRuntime* rt, const EosHipMll* m, const PlanResult& r, EosHipEncoder** out,
+              char** err) {
+  const EosHipMllPlan& p = r.plan;
+  const std::vector<std::string>& in = r.bert_inputs;
+  const int H = p.model_dim, F = p.hidden_dim;
+  auto vals = [&](const std::string& n) { return values_of(m, *m->tensor(n)); };
+  const std::vector<float> tok = vals(in[3]), pos = vals(in[4]), typ = vals(in[5]),
+                           eg = vals(in[6]), eb = vals(in[7]);
+  struct Layer {
+    std::vector<int8_t> qkv, o, w1, w2;
+    std::vector<float> sqkv, bqkv, so, bo, g1, b1, s1, bb1, s2, bb2, g2, b2;
+  };
+  std::vector<Layer> ls((size_t)p.layers);
+  std::vector<EosHipEncoderLayer> desc_layers((size_t)p.layers);
+  for (int l = 0; l < p.layers; ++l) {
+    const std::string* w = &in[8 + 16 * (size_t)l];
+    Layer& L = ls[(size_t)l];
+    // Q, K, V stacked into one [3H][H] projection (rows: q, then k, then v).
+    for (int part = 0; part < 3; ++part) {
+      std::vector<int8_t> c;
+      std::vector<float> sc;
+      codes_per_row(m, *m->tensor(w[2 * part]), &c, &sc);
+      L.qkv.insert(L.qkv.end(), c.begin(), c.end());
+      L.sqkv.insert(L.sqkv.end(), sc.begin(), sc.end());
+      const std::vector<float> bias = vals(w[2 * part + 1]);
+      L.bqkv.insert(L.bqkv.end(), bias.begin(), bias.end());
+    }
+    codes_per_row(m, *m->tensor(w[6]), &L.o, &L.so);
+    L.bo = vals(w[7]);
+    L.g1 = vals(w[8]);
+    L.b1 = vals(w[9]);
+    codes_per_row(m, *m->tensor(w[10]), &L.w1, &L.s1);
+    L.bb1 = vals(w[11]);
+    codes_per_row(m, *m->tensor(w[12]), &L.w2, &L.s2);
+    L.bb2 = vals(w[13]);
+    L.g2 = vals(w[14]);
+    L.b2 = vals(w[15]);
+    EosHipEncoderLayer& d = desc_layers[(size_t)l];
+    d.w_qkv = L.qkv.data();
+    d.s_qkv = L.sqkv.data();
+    d.b_qkv = L.bqkv.data();
+    d.w_o = L.o.data();
+    d.s_o = L.so.data();
+    d.b_o = L.bo.data();
+    d.ln1_gamma = L.g1.data();
+    d.ln1_beta = L.b1.data();
+    d.w_1 = L.w1.data();
+    d.s_1 = L.s1.data();
+    d.b_1 = L.bb1.data();
+    d.w_2 = L.w2.data();
+    d.s_2 = L.s2.data();
+    d.b_2 = L.bb2.data();
+    d.ln2_gamma = L.g2.data();
+    d.ln2_beta = L.b2.data();
+  }
+  (void)F;
+  EosHipEncoderDesc desc{};
+  desc.layers = p.layers;
+  desc.hidden = H;
+  desc.heads = p.heads;
+  desc.intermediate = p.hidden_dim;
+  desc.vocab = p.vocab;
+  desc.max_positions = p.max_sequence;
+  desc.type_vocab = p.type_vocab;
+  desc.ln_eps = (float)p.ln_eps;
+  desc.gelu = 1;  // hidden_act "gelu": exactGELU, the erf form
+  if (eoship_encoder_bind(rt, &desc, tok.data(), pos.data(), typ.data(), eg.data(), eb.data(),
+                          desc_layers.data(), out, err) != 0)
+    return 1;
+  if (eoship_encoder_set_pooling(rt, *out, p.pooling, err) != 0) {
+    eoship_encoder_release(*out, nullptr);
+    *out = nullptr;
+    return 1;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
 int eoship_encoder_bind_mll(EosHipRuntime* rt, const EosHipMll* m, const char* entry,
                             int32_t attend_padding, EosHipEncoder** out, EosHipMllPlan* plan,
                             char** err) {
@@ -1350,6 +1730,14 @@ int eoship_encoder_bind_mll(EosHipRuntime* rt, const EosHipMll* m, const char* e
     return set_err(err, "eoship_encoder_bind_mll: attend_padding must be -1, 0 or 1");
   PlanResult r;
   if (classify(m, entry, &r, err) != 0) return 1;
+  if (r.plan.route == EOSHIP_PLAN_BERT_EMBEDDER) {
+    if (attend_padding == 1)
+      return set_err(err, "eoship_encoder_bind_mll: attend_padding 1 applies to the compact "
+                          "family (BERT attention is masked)");
+    if (bind_bert(rt, m, r, out, err) != 0) return 1;
+    if (plan != nullptr) *plan = r.plan;
+    return 0;
+  }
   EosHipCompactOptions opts = r.plan.options;
   if (attend_padding >= 0) opts.attend_padding = attend_padding;
   EosHipCompactDesc desc{};
@@ -1427,6 +1815,10 @@ int eoship_retrieval_bind_mll(EosHipRuntime* rt, const EosHipMll* m, const char*
   r->has_ids = p.has_candidate_ids != 0;
   if (p.docs_param) {
     const Tensor* t = m->tensor(p.docs_input);
+    if (t == nullptr) {
+      delete r;
+      return set_err(err, "%s: document param \"%s\" has no payload", what, p.docs_input);
+    }
     r->docs_param = true;
     r->rows = p.docs_rows;
     r->dim = p.dim;

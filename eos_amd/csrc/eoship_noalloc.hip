@@ -7,6 +7,15 @@
 // host that name is only a stand-in for the symbol. The per-device address
 // from hipGetSymbolAddress is what kernels receive.
 //
+// Calls on one GPU share its array. They are ordered by a per-device event
+// chain: each call's stream waits for the event the previous call recorded
+// after its last kernel, then records it again after its own (under one
+// mutex, so the chain follows the order of the calls). Calls from several
+// runtimes (streams) therefore run one after another on the device instead
+// of overwriting each other's scores; nothing is allocated for it. A stream
+// under graph capture is left out of the chain (the capturing caller orders
+// its graph's replays).
+//
 // Compiled by hipcc as a host translation unit with a device variable (no
 // kernels); the kernels it launches are in the built-in code objects.
 #include <hip/hip_runtime.h>
@@ -27,6 +36,9 @@ std::mutex g_mu;
 float* g_ptr[kMaxDevices] = {};
 hipError_t g_status[kMaxDevices] = {};
 bool g_done[kMaxDevices] = {};
+// Completion of the last call on each device (created at set-up; a wait on
+// an event never recorded returns at once).
+hipEvent_t g_last[kMaxDevices] = {};
 
 }  // namespace
 
@@ -40,21 +52,40 @@ void noalloc_init(int device) {
   std::lock_guard<std::mutex> lock(g_mu);
   if (g_done[device]) return;
   void* p = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&g_last[device], hipEventDisableTiming);
   g_status[device] = e;
   g_ptr[device] = e == hipSuccess ? static_cast<float*>(p) : nullptr;
   g_done[device] = true;
 }
 
-static int noalloc_scratch(const Runtime* rt, float** out, const char* what, char** err) {
+// Runs launch(ptr) with this device's scratch, ordered after the previous
+// call on the device (see the event chain above), with g_mu held.
+template <typename F>
+static int noalloc_run(const Runtime* rt, const char* what, char** err, F launch) {
   const int dev = rt->device;
   if (dev < 0 || dev >= kMaxDevices)
     return set_err(err, "%s: device %d beyond the %d this library tracks", what, dev, kMaxDevices);
   std::lock_guard<std::mutex> lock(g_mu);
   if (!g_done[dev]) return set_err(err, "%s: scratch of device %d not resolved", what, dev);
-  if (g_status[dev] != hipSuccess) return hip_err(err, "hipGetSymbolAddress(scratch)", g_status[dev]);
-  *out = g_ptr[dev];
-  return 0;
+  if (g_status[dev] != hipSuccess)
+    return hip_err(err, "hipGetSymbolAddress(scratch) / hipEventCreate", g_status[dev]);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(rt->stream, &cap);
+  if (e != hipSuccess) return hip_err(err, "hipStreamIsCapturing", e);
+  const bool chained = cap == hipStreamCaptureStatusNone;
+  if (chained) {
+    e = hipStreamWaitEvent(rt->stream, g_last[dev], 0);
+    if (e != hipSuccess) return hip_err(err, "hipStreamWaitEvent(scratch chain)", e);
+  }
+  const int rc = launch(g_ptr[dev]);
+  if (chained) {
+    // Recorded whatever launch() returned: a later call must not wait on a
+    // stream position before kernels this call did launch.
+    e = hipEventRecord(g_last[dev], rt->stream);
+    if (e != hipSuccess && rc == 0) return hip_err(err, "hipEventRecord(scratch chain)", e);
+  }
+  return rc;
 }
 
 }  // namespace eoship
@@ -75,13 +106,13 @@ int eoship_tq_fp16_rerank_device_noalloc(EosHipRuntime* rt, const float* d_queri
   if ((size_t)q * (size_t)c > kNoAllocRerankFloats)
     return eoship::set_err(err, "%s: q * c = %lld exceeds the %zu candidates of the static scratch",
                            what, (long long)q * c, kNoAllocRerankFloats);
-  float* ptr = nullptr;
-  if (eoship::noalloc_scratch(rt, &ptr, what, err) != 0) return 1;
   // Every valid candidate's score is written by the first kernel before the
   // second reads it, so nothing is cleared between calls.
-  return eoship::tq_fp16_rerank_launch(rt, d_queries, q, d, d_rows, n, d_cand_ids, d_cand_scores,
-                                       c, k, bit_width, overfetch, d_id_rank, d_ids, d_scores, ptr,
-                                       what, err);
+  return eoship::noalloc_run(rt, what, err, [&](float* ptr) {
+    return eoship::tq_fp16_rerank_launch(rt, d_queries, q, d, d_rows, n, d_cand_ids,
+                                         d_cand_scores, c, k, bit_width, overfetch, d_id_rank,
+                                         d_ids, d_scores, ptr, what, err);
+  });
 }
 
 }  // extern "C"

@@ -168,6 +168,7 @@ int Runtime::flush_profile(char** err) {
     auto& acc = totals[r.name];
     acc.first += 1;
     acc.second += ms;
+    samples[r.name].push_back(ms);
     event_pool.push_back(r.begin);
     event_pool.push_back(r.end);
   }
@@ -302,6 +303,15 @@ int eoship_d2d(EosHipRuntime* rt, void* dst, const void* src, size_t bytes, char
   return copy(rt, dst, src, bytes, hipMemcpyDeviceToDevice, "eoship_d2d", err);
 }
 
+int eoship_memset(EosHipRuntime* rt, void* dst, int value, size_t bytes, char** err) {
+  if (rt == nullptr || (dst == nullptr && bytes != 0))
+    return set_err(err, "eoship_memset: NULL argument");
+  if (bytes == 0) return 0;
+  const hipError_t e = hipMemsetAsync(dst, value, bytes, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "eoship_memset", e);
+  return 0;
+}
+
 int eoship_sync(EosHipRuntime* rt, char** err) {
   if (rt == nullptr) return set_err(err, "eoship_sync: runtime is NULL");
   return rt->sync(err);
@@ -398,6 +408,25 @@ int eoship_profile_reset(EosHipRuntime* rt, char** err) {
   if (rt == nullptr) return set_err(err, "eoship_profile_reset: runtime is NULL");
   if (rt->flush_profile(err) != 0) return 1;
   rt->totals.clear();
+  rt->samples.clear();
+  return 0;
+}
+
+int eoship_profile_samples(EosHipRuntime* rt, const char* prefix, float* ms, int64_t cap,
+                           int64_t* count, char** err) {
+  if (rt == nullptr || count == nullptr || (cap > 0 && ms == nullptr))
+    return set_err(err, "eoship_profile_samples: NULL argument");
+  if (rt->flush_profile(err) != 0) return 1;
+  const size_t plen = prefix ? strlen(prefix) : 0;
+  int64_t n = 0;
+  for (auto& kv : rt->samples) {
+    if (plen != 0 && kv.first.compare(0, plen, prefix) != 0) continue;
+    for (float v : kv.second) {
+      if (n < cap) ms[n] = v;
+      ++n;
+    }
+  }
+  *count = n;
   return 0;
 }
 

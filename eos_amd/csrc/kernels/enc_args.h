@@ -13,10 +13,23 @@ struct EncPackArgs {
   int32_t* row_b;        // [batch*tokens]
   int32_t* row_t;        // [batch*tokens]
   int32_t* seq_off;      // [batch]
-  int32_t* seq_cnt;      // [batch]
+  int32_t* seq_cnt;      // [batch] active positions (the attention keys)
   int32_t* total;        // [1] active rows
   int batch, tokens;
   int all_active;        // 1: every position is packed, whatever the mask says
+  // Rows per sequence that carry a query (seq_cnt, plus one when cls_row is
+  // set and position 0 is masked: that position then gets a row of its own
+  // after the active ones, computed like any row but never a key, because
+  // CLS pooling reads position 0 whatever the mask says).
+  int32_t* seq_q;        // [batch]
+  int cls_row;
+  // Every position's ids are range-checked (as the reference checks the
+  // whole [B, T] input, masked positions included): status[0] = 1 on an id
+  // outside [0, vocab) or a type outside [0, ntype). ids may be NULL (no check).
+  const int32_t* ids;
+  const int32_t* type_ids;  // or NULL (all 0)
+  int vocab, ntype;
+  int32_t* status;
 };
 
 // mode 0 (BERT): token + position + type, then affine LayerNorm.
@@ -124,7 +137,8 @@ struct EncAttnArgs {
   const uint16_t* vt;      // [hidden][vt_ld] f16: V transposed (feature-major)
   uint16_t* ctx;           // [rows][hidden] f16
   const int32_t* seq_off;
-  const int32_t* seq_cnt;
+  const int32_t* seq_cnt;  // keys per sequence
+  const int32_t* seq_q;    // query rows per sequence (>= seq_cnt), or NULL (= seq_cnt)
   int batch, heads, hidden, max_len, vt_ld;
   float scale_log2;        // log2(e) / sqrt(head_dim)
   // Optional: counts (per wavefront) the exponent-reference moves after a
@@ -151,6 +165,10 @@ struct EncPoolArgs {
   // pooled, and the mean divides by their count.
   const int32_t* mask;
   int tokens;
+  // mode 0 only: non-NULL selects CLS pooling (position 0's row, then L2
+  // normalize): the sequence's first row when position 0 is active, else the
+  // query-only row after the active ones (seq_q > seq_cnt).
+  const int32_t* cls_seq_q;
 };
 
 // Tiny embed pipeline (examples/embed.eos): gather f16 table rows, multiply by

@@ -190,26 +190,41 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_count(EncPackArgs a) {
   __shared__ int scr[4];
   const int b = blockIdx.x, tid = threadIdx.x;
   const int32_t* m = a.mask + (size_t)b * a.tokens;
-  // 32 mask words per thread requested at a time, from clamped positions
-  // (a load under a per-lane condition becomes a branch of its own and waits
-  // for its data before the next one is issued).
+  const int32_t* ids = a.ids != nullptr ? a.ids + (size_t)b * a.tokens : nullptr;
+  const int32_t* tys = a.type_ids != nullptr ? a.type_ids + (size_t)b * a.tokens : nullptr;
+  // 16 mask words (and ids, types) per thread requested at a time, from
+  // clamped positions (a load under a per-lane condition becomes a branch of
+  // its own and waits for its data before the next one is issued).
   int mine = 0;
-  if (a.all_active) {
-    mine = tid < a.tokens ? (a.tokens - 1 - tid) / 256 + 1 : 0;
-  } else {
-    for (int b0 = 0; b0 < a.tokens; b0 += 256 * 32) {  // b0: uniform
-      const int base = b0 + tid;
-      int v[32];
+  bool bad = false;
+  for (int b0 = 0; b0 < a.tokens; b0 += 256 * 16) {  // b0: uniform
+    const int base = b0 + tid;
+    int v[16], iv[16], tv[16];
 #pragma unroll
-      for (int u = 0; u < 32; ++u)
-        if (b0 + 256 * u < a.tokens) v[u] = m[min(base + 256 * u, a.tokens - 1)];
+    for (int u = 0; u < 16; ++u) {
+      const int t = min(base + 256 * u, a.tokens - 1);
+      if (b0 + 256 * u < a.tokens) {
+        v[u] = a.all_active ? 1 : m[t];
+        iv[u] = ids != nullptr ? ids[t] : 0;
+        tv[u] = tys != nullptr ? tys[t] : 0;
+      }
+    }
 #pragma unroll
-      for (int u = 0; u < 32; ++u) mine += (base + 256 * u < a.tokens && v[u] != 0) ? 1 : 0;
+    for (int u = 0; u < 16; ++u) {
+      if (base + 256 * u < a.tokens) {
+        mine += v[u] != 0 ? 1 : 0;
+        bad = bad || iv[u] < 0 || iv[u] >= a.vocab || tv[u] < 0 || tv[u] >= a.ntype;
+      }
     }
   }
+  if (bad && ids != nullptr) *a.status = 1;
   int total = 0;
   (void)block_exclusive_scan256(mine, scr, &total);
-  if (tid == 0) a.seq_cnt[b] = total;
+  if (tid == 0) {
+    a.seq_cnt[b] = total;
+    if (a.seq_q != nullptr)
+      a.seq_q[b] = total + ((a.cls_row && !a.all_active && m[0] == 0) ? 1 : 0);
+  }
 }
 
 // One workgroup per sequence: rows of sequence b start at the sum of the
@@ -222,8 +237,11 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
   __shared__ int scr[4];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  // Rows of a sequence: its query rows (the active positions, plus the
+  // query-only CLS row when there is one), rounded up to a multiple of 8.
+  const int32_t* qrows = a.seq_q != nullptr ? a.seq_q : a.seq_cnt;
   int before = 0;
-  for (int i = tid; i < b; i += 256) before += (a.seq_cnt[i] + 7) & ~7;
+  for (int i = tid; i < b; i += 256) before += (qrows[i] + 7) & ~7;
   int seq_base = 0;
   (void)block_exclusive_scan256(before, scr, &seq_base);
   const int32_t* m = a.mask + (size_t)b * a.tokens;
@@ -274,10 +292,17 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
     pack_body(std::integral_constant<int, 8>{});
   else
     pack_body(std::integral_constant<int, 32>{});
-  const int padded = (seq_cnt + 7) & ~7;
-  if (tid < padded - seq_cnt) {
-    a.row_b[seq_base + seq_cnt + tid] = b;
-    a.row_t[seq_base + seq_cnt + tid] = -1;
+  // The query-only row of position 0 (CLS pooling with position 0 masked).
+  const int extra = a.seq_q != nullptr ? a.seq_q[b] - seq_cnt : 0;
+  if (extra != 0 && tid == 0) {
+    a.row_b[seq_base + seq_cnt] = b;
+    a.row_t[seq_base + seq_cnt] = 0;
+  }
+  const int used = seq_cnt + extra;
+  const int padded = (used + 7) & ~7;
+  if (tid < padded - used) {
+    a.row_b[seq_base + used + tid] = b;
+    a.row_t[seq_base + used + tid] = -1;
   }
   if (tid == 0) {
     a.seq_off[b] = seq_base;
@@ -1430,15 +1455,16 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   __shared__ __attribute__((aligned(16)))
   uint16_t ostage[(HD <= 64 && !kStageInK) ? 4 * 32 * (HD + 8) : 8];
   const int b = blockIdx.z, h = blockIdx.y;
-  const int cnt = a.seq_cnt[b];
+  const int cnt = a.seq_cnt[b];                          // keys
+  const int qcnt = a.seq_q != nullptr ? a.seq_q[b] : cnt;  // query rows (>= cnt)
   const int q0 = blockIdx.x * (4 * QW);
-  if (q0 >= cnt) return;
+  if (q0 >= qcnt) return;
   const int off = a.seq_off[b];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   const int ld = 3 * a.hidden;
   const int qi = q0 + wave * QW + l32;           // this lane's query (column)
-  const bool qlive = qi < cnt;
+  const bool qlive = qi < qcnt;
   // Q^T fragments (B operand): lane (query l32, group g) holds q[16s + 8g .. +7].
   // Q is pre-scaled by log2(e) / sqrt(hd) (in f32, rounded once to f16), so
   // the scores come out in the exp2 domain.
@@ -1471,7 +1497,9 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
       const int idx = tid + 256 * u;
       if (idx < NCH) {
         const int kr = idx / (HD / 8), c = (idx % (HD / 8)) * 8;
-        const int key = min(k0 + kr, cnt - 1);
+        // Clamped to the sequence's rows (row 0 when it has no key: then the
+        // block is never multiplied, and row 0 is its query-only row).
+        const int key = max(min(k0 + kr, cnt - 1), 0);
         kreg[u] = *reinterpret_cast<const v4i*>(a.qkv + (size_t)(off + key) * ld + a.hidden +
                                                 h * HD + c);
         const int d = idx / KC, k8 = (idx % KC) * 8;
@@ -1625,7 +1653,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     __builtin_amdgcn_wave_barrier();
     constexpr int LPR = HD / 8;       // lanes per row (16 bytes each)
     constexpr int RPI = 64 / LPR;     // rows per store instruction
-    const int slot = (cnt + 7) & ~7;  // the sequence's rows, pad rows included
+    const int slot = (qcnt + 7) & ~7;  // the sequence's rows, pad rows included
 #pragma unroll
     for (int r0 = 0; r0 < 32; r0 += RPI) {
       const int r = r0 + lane / LPR, c = (lane % LPR) * 8;
@@ -1640,7 +1668,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     // Pad rows of the sequence's 8-row slot get zeros: no kernel writes them
     // otherwise, and the memory may hold anything a freed buffer left (a NaN
     // there would reach the next layer's V rows past the sequence).
-    if (qi < ((cnt + 7) & ~7)) {
+    if (qi < ((qcnt + 7) & ~7)) {
       uint16_t* prow = a.ctx + (size_t)(off + qi) * a.hidden + h * HD;
 #pragma unroll
       for (int t = 0; t < HD / 32; ++t)
@@ -1803,7 +1831,12 @@ extern "C" __global__ __launch_bounds__(1024) void eos_enc_pool(EncPoolArgs a) {
     for (int i = 0; i < 16; ++i) pooled_rows += mcount[i];
   }
   float v = 0.f;
-  if (tid < a.hidden) {
+  if (a.cls_seq_q != nullptr) {
+    // CLS pooling (clsPoolTensor, bert_embedder_ops.go:183-196): position
+    // 0's row, then the L2 normalization below.
+    const int row = a.seq_off[b] + (a.cls_seq_q[b] > cnt ? cnt : 0);
+    if (tid < a.hidden) v = (float)__builtin_bit_cast(_Float16, a.h[(size_t)row * a.hidden + tid]);
+  } else if (tid < a.hidden) {
     // Up to 32 chunk partials requested at a time, then added in chunk order
     // (the same sum as one load and add per chunk, without a memory round
     // trip per chunk).

@@ -84,3 +84,30 @@ extern "C" __global__ __launch_bounds__(256) void eos_probe_mfma_i8(MfmaProbeArg
 extern "C" __global__ __launch_bounds__(256) void eos_probe_mfma_f16(MfmaProbeArgs a) {
   probe_body<true>(a);
 }
+
+// Read-only HBM stream: every thread reads 16-byte words at a grid stride,
+// U loads in flight at a time, and folds them into one word that it writes
+// once (so the loads are kept). The bytes read per launch are `words` x 16;
+// writes are one word per thread. This is the achievable rate of a scan that
+// only reads, the bound a corpus scan is held to beside the copy's.
+struct ReadProbeArgs {
+  const v4i* src;
+  v4i* sink;                   // [grid threads]
+  long long words;             // 16-byte words to read
+};
+
+extern "C" __global__ __launch_bounds__(256) void eos_probe_read_stream(ReadProbeArgs a) {
+  constexpr int U = 8;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  v4i acc = v4i{0, 0, 0, 0};
+  for (; i + (U - 1) * stride < a.words; i += U * stride) {
+    v4i v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(a.src + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u];
+  }
+  for (; i < a.words; i += stride) acc ^= a.src[i];
+  a.sink[(long long)blockIdx.x * blockDim.x + threadIdx.x] = acc;
+}

@@ -37,8 +37,11 @@ constexpr int kScanThreads = 256;
 // registers fit the 168 of three waves.
 constexpr int scan_threads(bool hi, int ks) { return hi && ks <= 16 ? 768 : 512; }
 
+// Order bits of a score; -0 keys as +0 (the reference compares -0 == +0 and
+// then breaks the tie by id or index).
 EOS_DEV uint32_t score_key(float s) {
   uint32_t u = __float_as_uint(s);
+  u = u == 0x80000000u ? 0u : u;
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 EOS_DEV float key_score(uint32_t k) {

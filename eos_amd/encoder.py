@@ -260,6 +260,15 @@ class Encoder:
         fused kernel (default) or as the unfused GEMM + LayerNorm launches."""
         _lib.call("eoship_encoder_set_fused_tail", self.rt.handle, self.handle, C.c_int32(int(fused)))
 
+    def set_pooling(self, pooling: str) -> None:
+        """BERT family: "masked_mean" (default) or "cls" (bert_embedder's
+        pooling attribute, runtime/backend/bert_embedder_ops.go:150-152)."""
+        modes = {"masked_mean": 0, "cls": 1}
+        if pooling not in modes:
+            raise ValueError(f"unsupported pooling {pooling!r}; supported values are masked_mean and cls")
+        _lib.call("eoship_encoder_set_pooling", self.rt.handle, self.handle,
+                  C.c_int32(modes[pooling]))
+
     def attention_moves(self) -> int:
         """Diagnostic of the last forward: attention wavefronts that moved their
         softmax exponent reference after a sequence's first key block."""

@@ -116,9 +116,12 @@ class MllPackage:
         return plan_dict(plan)
 
 
+ROUTES = {1: "compact_embedder", 2: "bert_embedder"}
+
+
 def plan_dict(p) -> dict:
-    return {
-        "route": "compact_embedder" if p.route == 1 else p.route,
+    d = {
+        "route": ROUTES.get(p.route, p.route),
         "layers": p.layers, "distinct_layers": p.distinct_layers, "model_dim": p.model_dim,
         "heads": p.heads, "hidden_dim": p.hidden_dim, "vocab": p.vocab,
         "max_sequence": p.max_sequence, "output_dim": p.output_dim, "batched": bool(p.batched),
@@ -129,12 +132,20 @@ def plan_dict(p) -> dict:
         "entry": p.entry.decode(), "token_input": p.token_input.decode(),
         "mask_input": p.mask_input.decode(), "output_name": p.output_name.decode(),
     }
+    if p.route == 2:
+        d.update({"pooling": "cls" if p.pooling == 1 else "masked_mean",
+                  "type_vocab": p.type_vocab, "ln_eps": p.ln_eps,
+                  "weights_quantized": bool(p.weights_quantized),
+                  "type_input": p.type_input.decode(), "max_positions": p.max_sequence})
+    return d
 
 
 class MllEncoder(Encoder):
     """An embedding entry of an MLL package bound to the fused encoder.
-    ``embed(tokens, mask)`` takes [batch, tokens] i32 arrays and returns
-    [batch, output_dim] f32.
+    ``embed(tokens, mask[, token_type_ids])`` takes [batch, tokens] i32 arrays
+    and returns [batch, output_dim] f32. A bert_embedder entry (route
+    "bert_embedder") runs the fused BERT encoder with the step's pooling and
+    takes token type ids (None: all 0); a compact-family entry ignores them.
 
     attend_padding: -1 runs the plan's own softmax semantics (the [B, T]
     entry as given: padding positions are keys and queries when the plan's
@@ -153,5 +164,7 @@ class MllEncoder(Encoder):
         self.plan = plan_dict(plan)
         self.out_dim = self.plan["output_dim"]
 
-    def embed(self, tokens: np.ndarray, attention_mask: np.ndarray) -> np.ndarray:
-        return super().embed(tokens, attention_mask, None)
+    def embed(self, tokens: np.ndarray, attention_mask: np.ndarray,
+              token_type_ids: np.ndarray | None = None) -> np.ndarray:
+        types = token_type_ids if self.plan["route"] == "bert_embedder" else None
+        return super().embed(tokens, attention_mask, types)

@@ -118,6 +118,16 @@ class Runtime:
         _lib.call("eoship_profile_read", self.handle, prefix.encode(), C.byref(n), C.byref(ms))
         return n.value, ms.value
 
+    def profile_samples(self, prefix: str) -> np.ndarray:
+        """Per-launch durations (ms) of the recorded launches matching prefix."""
+        n = C.c_int64()
+        _lib.call("eoship_profile_samples", self.handle, prefix.encode(), None, C.c_int64(0),
+                  C.byref(n))
+        out = np.zeros(max(n.value, 1), np.float32)
+        _lib.call("eoship_profile_samples", self.handle, prefix.encode(),
+                  out.ctypes.data_as(C.c_void_p), C.c_int64(n.value), C.byref(n))
+        return out[:n.value]
+
     def mark(self, slot: int) -> None:
         _lib.call("eoship_timer_mark", self.handle, int(slot))
 

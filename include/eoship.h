@@ -53,6 +53,8 @@ int eoship_free(EosHipRuntime* rt, void* dptr, char** err);
 int eoship_h2d(EosHipRuntime* rt, void* dst, const void* src, size_t bytes, char** err);
 int eoship_d2h(EosHipRuntime* rt, void* dst, const void* src, size_t bytes, char** err);
 int eoship_d2d(EosHipRuntime* rt, void* dst, const void* src, size_t bytes, char** err);
+/* Sets bytes of device memory to the byte value, on the runtime stream. */
+int eoship_memset(EosHipRuntime* rt, void* dst, int value, size_t bytes, char** err);
 int eoship_sync(EosHipRuntime* rt, char** err);
 /* Orders two runtimes on one device: work enqueued on rt after this call
  * starts only after all work enqueued on other so far has finished (an event
@@ -82,6 +84,12 @@ int eoship_profile_select(EosHipRuntime* rt, const char* prefix, char** err);
 int eoship_profile_read(EosHipRuntime* rt, const char* prefix, int64_t* launches, double* total_ms,
                         char** err);
 int eoship_profile_reset(EosHipRuntime* rt, char** err);
+/* The duration (ms) of each recorded launch whose label starts with prefix
+ * (labels in name order, launches in order within a label): up to cap values
+ * into ms, the number recorded into *count. For medians of per-launch times
+ * (no counterpart in the reference, whose profiler keeps totals only). */
+int eoship_profile_samples(EosHipRuntime* rt, const char* prefix, float* ms, int64_t cap,
+                           int64_t* count, char** err);
 /* Stream-level timer: records an event now; eoship_timer_elapsed gives the
  * milliseconds between two recorded marks (synchronising the second). */
 int eoship_timer_mark(EosHipRuntime* rt, int slot, char** err);
@@ -330,7 +338,8 @@ int eoship_encoder_release(EosHipEncoder* enc, char** err);
  * masked mean pool, L2 normalize -> out [batch][hidden] f32 (an encoder bound
  * with eoship_encoder_bind_compact: out [batch][output_dim]). type_ids may be
  * NULL (all 0). Fails with an error for a token, type or position id outside
- * its table (the reference rejects these, runtime/backend/tensor_ops.go:1484-1492).
+ * its table, at any position, masked ones included (the reference checks the
+ * whole input, runtime/backend/tensor_ops.go:1484-1492).
  * Replaces Program.Run of a bert_embedder plan / EmbeddingModel.EmbedBatch
  * (runtime/inference.go:57-101; runtime/embedding_model.go:669-761). */
 int eoship_encoder_forward(EosHipRuntime* rt, EosHipEncoder* enc, const int32_t* ids,
@@ -350,6 +359,14 @@ int eoship_encoder_status(EosHipRuntime* rt, EosHipEncoder* enc, int32_t* status
  * in the reference; for comparing the two paths. */
 int eoship_encoder_set_fused_tail(EosHipRuntime* rt, EosHipEncoder* enc, int32_t fused,
                                   char** err);
+/* BERT family sentence pooling, the bert_embedder step's "pooling" attribute
+ * (runtime/backend/bert_embedder_ops.go:150-152, 183-196): 0 masked_mean
+ * (the default: mean over mask != 0 positions, then L2), 1 cls (position 0's
+ * hidden state, then L2; position 0 is computed even where the mask clears
+ * it, attending to the sequence's active positions, as the reference
+ * computes every row). Refused for the compact family. */
+int eoship_encoder_set_pooling(EosHipRuntime* rt, EosHipEncoder* enc, int32_t pooling,
+                               char** err);
 /* Diagnostic of the last forward (synchronises): how many times a wavefront
  * of the attention kernels moved its softmax exponent reference after a
  * sequence's first key block (a score far above every earlier one, as peaked
@@ -541,9 +558,12 @@ int eoship_tq_reconstruct_rerank_device(EosHipRuntime* rt, const EosHipTQCodes* 
  * between its two kernels go to a static device array of 2^20 floats per GPU
  * (4 MiB, held until the process ends), so q * c must be <= 2^20 (larger is
  * refused with an error). Arguments, limits and results are those of
- * eoship_tq_fp16_rerank_device. Every call on one GPU shares that array:
- * calls that overlap on one GPU (two runtimes' streams running at once)
- * race; calls ordered on one stream do not. */
+ * eoship_tq_fp16_rerank_device. Every call on one GPU shares that array;
+ * calls from several runtimes (streams) on one GPU are ordered by a
+ * per-device event chain (each call's stream waits for the previous call's
+ * kernels), so they do not overwrite each other's scores. A stream under
+ * graph capture is left out of that chain: replays of a captured graph that
+ * overlap other calls on the same GPU race. */
 int eoship_tq_fp16_rerank_device_noalloc(EosHipRuntime* rt, const float* d_queries, int32_t q,
                                          int32_t d, const uint16_t* d_rows, int64_t n,
                                          const int64_t* d_cand_ids, const float* d_cand_scores,
@@ -610,6 +630,7 @@ int eoship_mll_tensor(const EosHipMll* mll, int64_t index, const char* name,
 int eoship_blake3(const uint8_t* data, uint64_t bytes, uint8_t* digest32, char** err);
 
 #define EOSHIP_PLAN_COMPACT_EMBEDDER 1
+#define EOSHIP_PLAN_BERT_EMBEDDER 2
 
 typedef struct {
   int32_t route;            /* EOSHIP_PLAN_* */
@@ -621,10 +642,29 @@ typedef struct {
   EosHipCompactOptions options;  /* the plan's graph options (attend_padding: 1
                                   * for softmaxRows, 0 for masked_softmax) */
   char entry[64], token_input[64], mask_input[64], output_name[64];
+  /* BERT family (route EOSHIP_PLAN_BERT_EMBEDDER) only: */
+  int32_t pooling;            /* 0 masked_mean, 1 cls */
+  int32_t type_vocab;         /* token type table rows */
+  int32_t weights_quantized;  /* 1: f32/f16 dense weights, quantized at bind to int8
+                               * per output channel (the q8 encoder); 0: q8/q4 payloads
+                               * used as stored */
+  int32_t reserved;
+  double ln_eps;              /* the step's epsilon */
+  char type_input[64];        /* token_type_ids input; max_sequence holds the
+                               * position table rows */
 } EosHipMllPlan;
 
-/* Matches an entry's step list (NULL: the embedding_manifest's batch entry)
- * against the family-(a) encoder graph by value flow and kernel op class:
+/* Matches an entry's step list (NULL: the embedding_manifest's batch entry,
+ * else the only entry point). An entry holding a bert_embedder step (the
+ * pretrained-BERT importer's module, runtime/pretrained_bert_importer.go:
+ * 901-1009) classifies as EOSHIP_PLAN_BERT_EMBEDDER when it is that step and
+ * its return: attributes read as bertEmbedderConfigFromAttrs reads them
+ * (runtime/backend/bert_embedder_ops.go:35-77: num_hidden_layers,
+ * num_attention_heads, epsilon, hidden_act "gelu", pooling masked_mean or
+ * cls), 8 + 16 L inputs (three i32 [B, T] entry inputs, then f32/f16/q8/q4
+ * tensors of the shapes the reference validates), within the fused
+ * encoder's shapes. Otherwise it is matched against the family-(a) encoder
+ * graph by value flow and kernel op class:
  * gather + dequant of the token table; per layer q/k/v = x W, kT, q kT
  * (optionally scale rsqrt_rhs_rows), softmax or masked_softmax, p v, W_o,
  * binary_add + layernorm, W_up, gelu, W_down, binary_add + layernorm; then
@@ -634,10 +674,17 @@ typedef struct {
  * ExecuteSymbolic runs (runtime/backend/symbolic.go:17-172). */
 int eoship_mll_classify(const EosHipMll* mll, const char* entry, EosHipMllPlan* plan, char** err);
 
-/* Classifies the entry and binds its weights (int8 codes of packed Q8, Q4
- * unpacked, per-tensor scales; tied layers share one device copy) to the
- * fused compact encoder; run it with eoship_encoder_embed[_device] on
- * tokens and mask [batch][tokens]. attend_padding: -1 takes the plan's own
+/* Classifies the entry and binds its weights. BERT route: the fused BERT
+ * encoder with the step's heads, epsilon, erf GELU and pooling; q8/q4 dense
+ * weights keep their codes and per-tensor scale, f32/f16 dense weights are
+ * quantized per output channel (scale max|row| / 127, codes rint(w / scale)),
+ * every other tensor is dequantized to f32; run it with
+ * eoship_encoder_forward[_device] on ids, types and mask [batch][tokens]
+ * (attend_padding must be -1 or 0: BERT attention is masked). Compact route:
+ * (int8 codes of packed Q8, Q4 unpacked, per-tensor scales; tied layers
+ * share one device copy) the fused compact encoder; run it with
+ * eoship_encoder_forward[_device] on tokens and mask [batch][tokens].
+ * attend_padding: -1 takes the plan's own
  * softmax semantics (the [B, T] entry run as given, padding included); 0
  * attends each sequence's mask != 0 positions only (EmbeddingModel's batches,
  * which group sequences by length, runtime/embedding_model.go:689-691).

@@ -230,6 +230,12 @@ def _enc():
     lib.bert_embed.argtypes = [P, C.c_int, P, C.c_int, P, C.c_int, P, P, P, C.c_int, P, P, P,
                                C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, P]
     lib.bert_embed.restype = None
+    lib.bert_embed_pool.argtypes = [P, C.c_int, P, C.c_int, P, C.c_int, P, P, P, C.c_int, P, P,
+                                    P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_double,
+                                    C.c_int, P]
+    lib.bert_embed_pool.restype = None
+    lib.bert_hidden.argtypes = lib.bert_embed.argtypes
+    lib.bert_hidden.restype = None
     lib.mean_pool_masked.argtypes = [P, P, C.c_int, C.c_int, C.c_int, P]
     lib.mean_pool_masked.restype = None
     lib.normalize_rows.argtypes = [P, C.c_int, C.c_int]
@@ -256,8 +262,10 @@ def _enc():
     return lib
 
 
-def bert_embed(tok, pos, typ, emb_gamma, emb_beta, layers, ids, mask, type_ids, heads, eps):
-    """layers: list of 16-tensor lists (reference order, f32, HF [out, in])."""
+def bert_embed(tok, pos, typ, emb_gamma, emb_beta, layers, ids, mask, type_ids, heads, eps,
+               pooling: str = "masked_mean"):
+    """layers: list of 16-tensor lists (reference order, f32, HF [out, in]).
+    pooling: "masked_mean" or "cls" (bert_embedder_ops.go:179-196)."""
     lib = _enc()
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     mask = np.ascontiguousarray(mask, dtype=np.int32)
@@ -270,10 +278,32 @@ def bert_embed(tok, pos, typ, emb_gamma, emb_beta, layers, ids, mask, type_ids, 
     tok, pos, typ = _f32(tok), _f32(pos), _f32(typ)
     g, b = _f32(emb_gamma), _f32(emb_beta)
     out = np.zeros((batch, hidden), np.float32)
-    lib.bert_embed(_p(tok), tok.shape[0], _p(pos), pos.shape[0], _p(typ), typ.shape[0], _p(g),
-                   _p(b), ptrs, len(layers), _p(ids), _p(types), _p(mask), batch, tokens, hidden,
-                   heads, inter, C.c_double(eps), _p(out))
+    mode = {"masked_mean": 0, "cls": 1}[pooling]
+    lib.bert_embed_pool(_p(tok), tok.shape[0], _p(pos), pos.shape[0], _p(typ), typ.shape[0],
+                        _p(g), _p(b), ptrs, len(layers), _p(ids), _p(types), _p(mask), batch,
+                        tokens, hidden, heads, inter, C.c_double(eps), mode, _p(out))
     return out
+
+
+def bert_hidden(tok, pos, typ, emb_gamma, emb_beta, layers, ids, mask, type_ids, heads, eps):
+    """Hidden states [batch, tokens, hidden] after every layer (the state the
+    pooling reads), every position computed."""
+    lib = _enc()
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    mask = np.ascontiguousarray(mask, dtype=np.int32)
+    types = np.zeros_like(ids) if type_ids is None else np.ascontiguousarray(type_ids, np.int32)
+    batch, tokens = ids.shape
+    hidden = tok.shape[1]
+    inter = layers[0][10].shape[0] if layers else hidden
+    keep = [_f32(x) for L in layers for x in L]
+    ptrs = (C.c_void_p * max(len(keep), 1))(*[k.ctypes.data for k in keep])
+    tok, pos, typ = _f32(tok), _f32(pos), _f32(typ)
+    g, b = _f32(emb_gamma), _f32(emb_beta)
+    h = np.zeros((batch, tokens, hidden), np.float32)
+    lib.bert_hidden(_p(tok), tok.shape[0], _p(pos), pos.shape[0], _p(typ), typ.shape[0], _p(g),
+                    _p(b), ptrs, len(layers), _p(ids), _p(types), _p(mask), batch, tokens, hidden,
+                    heads, inter, C.c_double(eps), _p(h))
+    return h
 
 
 def dense_hf(x, w, b):

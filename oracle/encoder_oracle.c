@@ -197,20 +197,50 @@ void normalize_rows(float* x, int rows, int cols) {
   }
 }
 
+/* Hidden states after the embeddings and `layers` encoder layers (the state
+ * BERTEmbedderReferenceWithPooling pools, bert_embedder_ops.go:155-178):
+ * h [batch][tokens][hidden], every position computed (masked ones too). */
+void bert_hidden(const float* tok, int vocab, const float* pos, int npos, const float* typ,
+                 int ntype, const float* emb_gamma, const float* emb_beta,
+                 const float* const* layer_w, int layers, const int32_t* ids,
+                 const int32_t* type_ids, const int32_t* mask, int batch, int tokens, int hidden,
+                 int heads, int inter, double eps, float* h) {
+  bert_embeddings(tok, vocab, pos, npos, typ, ntype, emb_gamma, emb_beta, ids, type_ids, batch,
+                  tokens, hidden, eps, h);
+  for (int l = 0; l < layers; ++l)
+    bert_layer(h, mask, batch, tokens, hidden, heads, inter, eps, layer_w + (size_t)l * 16);
+}
+
+/* Full embedder with the step's pooling (bert_embedder_ops.go:179-196):
+ * pooling 0 masked_mean (mean over mask != 0 rows, count 0 -> zeros), 1 cls
+ * (clsPoolTensor: the row of position 0 whatever the mask), then L2
+ * (normalizeRows). out: [batch][hidden]. */
+void bert_embed_pool(const float* tok, int vocab, const float* pos, int npos, const float* typ,
+                     int ntype, const float* emb_gamma, const float* emb_beta,
+                     const float* const* layer_w, int layers, const int32_t* ids,
+                     const int32_t* type_ids, const int32_t* mask, int batch, int tokens,
+                     int hidden, int heads, int inter, double eps, int pooling, float* out) {
+  float* h = (float*)malloc(sizeof(float) * (size_t)batch * tokens * hidden);
+  bert_hidden(tok, vocab, pos, npos, typ, ntype, emb_gamma, emb_beta, layer_w, layers, ids,
+              type_ids, mask, batch, tokens, hidden, heads, inter, eps, h);
+  if (pooling == 1) {
+    for (int b = 0; b < batch; ++b)
+      memcpy(out + (size_t)b * hidden, h + (size_t)b * tokens * hidden, sizeof(float) * hidden);
+  } else {
+    mean_pool_masked(h, mask, batch, tokens, hidden, out);
+  }
+  normalize_rows(out, batch, hidden);
+  free(h);
+}
+
 /* Full embedder: embeddings, `layers` encoder layers, masked mean pool, L2.
  * layer_w: layers*16 pointers. out: [batch][hidden]. */
 void bert_embed(const float* tok, int vocab, const float* pos, int npos, const float* typ,
                 int ntype, const float* emb_gamma, const float* emb_beta, const float* const* layer_w,
                 int layers, const int32_t* ids, const int32_t* type_ids, const int32_t* mask,
                 int batch, int tokens, int hidden, int heads, int inter, double eps, float* out) {
-  float* h = (float*)malloc(sizeof(float) * (size_t)batch * tokens * hidden);
-  bert_embeddings(tok, vocab, pos, npos, typ, ntype, emb_gamma, emb_beta, ids, type_ids, batch,
-                  tokens, hidden, eps, h);
-  for (int l = 0; l < layers; ++l)
-    bert_layer(h, mask, batch, tokens, hidden, heads, inter, eps, layer_w + (size_t)l * 16);
-  mean_pool_masked(h, mask, batch, tokens, hidden, out);
-  normalize_rows(out, batch, hidden);
-  free(h);
+  bert_embed_pool(tok, vocab, pos, npos, typ, ntype, emb_gamma, emb_beta, layer_w, layers, ids,
+                  type_ids, mask, batch, tokens, hidden, heads, inter, eps, 0, out);
 }
 
 /* Tiny embed (examples/embed.eos): rows = gather(table, ids); y = rows @ proj

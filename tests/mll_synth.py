@@ -10,7 +10,21 @@ import json
 import numpy as np
 
 from oracle import mll_oracle
-from oracle.blake3 import blake3
+from oracle.blake3 import blake3 as _py_blake3
+
+
+def blake3(data: bytes) -> bytes:
+    """Section digests of the synthetic packages: the library's BLAKE3 for
+    bodies past 64 KiB (the pure-Python restatement takes minutes on the
+    dense weights of a BERT package), else the Python one. Both are pinned
+    to the specification and to each other in tests/test_mll.py."""
+    if len(data) <= 65536:
+        return _py_blake3(data)
+    import ctypes as C
+    from eos_amd import _lib
+    out = (C.c_uint8 * 32)()
+    _lib.call("eoship_blake3", C.c_char_p(data), C.c_uint64(len(data)), out)
+    return bytes(out)
 
 
 def _kernel(name, op, attrs=None):
@@ -235,6 +249,110 @@ def retrieval_package(artifact: dict, docs_codes: np.ndarray | None = None,
         entries.append((1, 12, docs_codes.shape, packed))
         scales["docs"] = docs_scale
         logical["docs"] = "q4"
+    meta = {"version": "manta/mll/v0alpha1", "module_name": artifact["name"],
+            "module_version": "manta/v0alpha1", "artifact": artifact,
+            "logical_tensor_dtypes": logical, "tensor_scales": scales}
+    secs = [("HEAD", b"\0" * 16, 1), ("STRG", mll_oracle.strg_body(strings), 1),
+            ("TNSR", mll_oracle.tnsr_body(entries), 0x11),
+            ("XMTA", json.dumps(meta).encode(), 0x22)]
+    return mll_oracle.write(secs, blake3)
+
+
+BERT_LAYER_ROLES = ["attention_query_weight", "attention_query_bias", "attention_key_weight",
+                    "attention_key_bias", "attention_value_weight", "attention_value_bias",
+                    "attention_output_weight", "attention_output_bias",
+                    "attention_layernorm_weight", "attention_layernorm_bias",
+                    "intermediate_weight", "intermediate_bias", "output_weight", "output_bias",
+                    "output_layernorm_weight", "output_layernorm_bias"]
+BERT_EMB_ROLES = ["token_embeddings", "position_embeddings", "token_type_embeddings",
+                  "embedding_layernorm_weight", "embedding_layernorm_bias"]
+
+
+def bert_artifact(layers: int, heads: int, eps: float = 1e-12, pooling: str = "masked_mean",
+                  hidden_act: str = "gelu", attrs: dict | None = None) -> dict:
+    """The module the pretrained-BERT importer builds
+    (runtime/pretrained_bert_importer.go:901-1009): params for the five
+    embedding tensors and 16 per layer, entry bert_embed (input_ids,
+    attention_mask, token_type_ids -> embeddings), one bert_embedder step
+    with the config attributes, then its return. attrs overrides the
+    attribute map."""
+    names = list(BERT_EMB_ROLES)
+    for l in range(layers):
+        names += [f"encoder_layer_{l}_{r}" for r in BERT_LAYER_ROLES]
+    ids = {"kind": "tensor", "tensor": {"dtype": "i32", "shape": ["B", "T"]}}
+    a = {"epsilon": repr(float(eps)), "hidden_act": hidden_act,
+         "num_attention_heads": str(heads), "num_hidden_layers": str(layers),
+         "pooling": pooling, "normalization": "l2"}
+    if attrs is not None:
+        a = attrs
+    return {
+        "version": "manta/v0alpha1", "name": "pretrained_bert_embedder",
+        "params": [{"name": n, "type": {"kind": "tensor", "tensor": {"dtype": "f32"}},
+                    "binding": n} for n in names],
+        "entry_points": [{"name": "bert_embed", "kind": "pipeline",
+                          "inputs": [{"name": "input_ids", "type": ids},
+                                     {"name": "attention_mask", "type": ids},
+                                     {"name": "token_type_ids", "type": ids}],
+                          "outputs": [{"name": "embeddings",
+                                       "type": {"kind": "tensor",
+                                                "tensor": {"dtype": "f32", "shape": ["B", "H"]}}}]}],
+        "steps": [{"entry": "bert_embed", "kind": "bert_embedder",
+                   "name": "bert_embedder_reference",
+                   "inputs": ["input_ids", "attention_mask", "token_type_ids"] + names,
+                   "outputs": ["embeddings"], "attributes": a},
+                  {"entry": "bert_embed", "kind": "return", "name": "return_embeddings",
+                   "outputs": ["embeddings"]}],
+    }
+
+
+def bert_tensors(w) -> dict:
+    """name -> f32 array of an EncoderWeights (datagen.bert_q8_weights) in the
+    importer's roles, the dense weights dequantized (codes x per-channel
+    scale) so that their per-channel int8 quantization returns the same codes."""
+    out = {"token_embeddings": w.tok, "position_embeddings": w.pos,
+           "token_type_embeddings": w.typ, "embedding_layernorm_weight": w.emb_gamma,
+           "embedding_layernorm_bias": w.emb_beta}
+    H = w.hidden
+    for l, L in enumerate(w.layers):
+        deq = L.dequantized()   # 16 tensors in the reference order
+        q, k, v = deq[0], deq[2], deq[4]
+        vals = [q, deq[1], k, deq[3], v, deq[5]] + list(deq[6:])
+        assert q.shape == (H, H)
+        for r, x in zip(BERT_LAYER_ROLES, vals):
+            out[f"encoder_layer_{l}_{r}"] = np.asarray(x, np.float32)
+    return out
+
+
+def bert_package(artifact: dict, tensors: dict, q8: tuple = (), q4: tuple = ()) -> bytes:
+    """A sealed-profile container holding `tensors` (name -> f32 array) as
+    f32 payloads, except the names in q8 / q4, stored as the reference's
+    per-tensor packed Q8 / Q4 (packQuantizedTensorStorage,
+    runtime/mll_export.go:897-975) with their tensor_scales. The storage
+    dtype byte of an f32 payload is not fixed by any shipped package; the
+    reader goes by the logical dtype and the payload size."""
+    from eos_amd.encoder import quantize_per_tensor
+    names = list(tensors)
+    strings = [""] + names
+    entries, scales, logical = [], {}, {}
+    for n in names:
+        x = np.ascontiguousarray(tensors[n], np.float32)
+        if n in q8 or n in q4:
+            bits = 8 if n in q8 else 4
+            codes, sc = quantize_per_tensor(x, bits)
+            scales[n] = float(sc)
+            if bits == 8:
+                entries.append((strings.index(n), mll_oracle.DTYPE_Q8, x.shape, codes.tobytes()))
+                logical[n] = "q8"
+            else:
+                flat = (codes.reshape(-1).astype(np.int16) + 8).astype(np.uint8)
+                if flat.size % 2:
+                    flat = np.concatenate([flat, np.array([8], np.uint8)])
+                packed = (flat[0::2] | (flat[1::2] << 4)).astype(np.uint8).tobytes()
+                entries.append((strings.index(n), 12, x.shape, packed))
+                logical[n] = "q4"
+        else:
+            entries.append((strings.index(n), 1, x.shape, x.tobytes()))
+            logical[n] = "f32"
     meta = {"version": "manta/mll/v0alpha1", "module_name": artifact["name"],
             "module_version": "manta/v0alpha1", "artifact": artifact,
             "logical_tensor_dtypes": logical, "tensor_scales": scales}

@@ -115,17 +115,20 @@ def test_baseline_c3_full_size(rt):
 def test_baseline_c4_long_context(rt):
     """BASELINE config 4 at full size: 4 layers, hidden 512, 8 heads (hd 64),
     FFN 2048, batch 4 x 8192, lengths U[4096, 8192] (seed 10). The two
-    shortest sequences are checked against the oracle on their own valid
-    tokens (sequences are independent and padding never reaches a valid
-    token)."""
+    shortest sequences and the longest (the most key blocks, so the most
+    chances for the lazy-rescale move) are checked against the oracle on
+    their own valid tokens (sequences are independent and padding never
+    reaches a valid token)."""
     _case("c4 full size 4 x 8192")
     w = datagen.bert_q8_weights(4, 512, 8, 2048, 30522, 8192, seed=10)
     ids, mask, lens = datagen.encoder_batch(4, 8192, 30522, 4096, 8192, 11, 10)
     enc = Encoder(rt, w)
     got = enc.embed(ids, mask)
     np.testing.assert_allclose(np.linalg.norm(got, axis=1), 1.0, atol=1e-5)
-    for b in np.argsort(lens, kind="stable")[:2]:
+    order = np.argsort(lens, kind="stable")
+    for b in (*order[:2], order[-1]):
         b = int(b)
+        print(f"  sequence {b}: {int(lens[b])} tokens", flush=True)
         n = int(lens[b])
         want = _oracle(w, ids[b:b + 1, :n], np.ones((1, n), np.int32))
         _check(got[b:b + 1], want)
@@ -215,3 +218,54 @@ def test_fused_tail_matches_unfused_and_oracle(rt, hidden, heads, inter, gelu):
     print(f"  fused vs unfused max abs {d:.3e}", flush=True)
     assert d <= 2e-3
     _check(fused, _oracle(w, ids, mask))
+
+
+def test_encoder_cls_pooling(rt):
+    """CLS pooling (bert_embedder pooling "cls", bert_embedder_ops.go:183-196)
+    on the fused encoder: position 0's hidden state, normalized. Position 0
+    masked (its row is computed anyway, attending to the active positions),
+    a sequence with no active position (its CLS row attends to nothing), and
+    the unfused layer path agree with the oracle."""
+    _case("encoder CLS pooling")
+    w = datagen.bert_q8_weights(2, 512, 8, 2048, 1000, 300, seed=61, random_affine=True)
+    ids, mask, _ = datagen.encoder_batch(6, 300, 1000, 1, 300, 62, 63)
+    mask[1, 0] = 0
+    mask[2, :] = 0
+    mask[3, :5] = 0
+    mask[4, :] = 0
+    mask[4, 0] = 1                       # only position 0 active: CLS == mean
+    enc = Encoder(rt, w)
+    mean = enc.embed(ids, mask)
+    enc.set_pooling("cls")
+    got = enc.embed(ids, mask)
+    want = oracle.bert_embed(w.tok, w.pos, w.typ, w.emb_gamma, w.emb_beta,
+                             [L.dequantized() for L in w.layers], ids, mask, None, w.heads,
+                             w.ln_eps, pooling="cls")
+    _check(got, want)
+    np.testing.assert_allclose(got[4], mean[4], atol=1e-6)
+    enc.set_fused_tail(False)
+    _check(enc.embed(ids, mask), want)
+    enc.release()
+
+
+def test_encoder_rejects_out_of_range_ids_at_masked_positions(rt):
+    """The reference range-checks every input id, masked positions included
+    (BERTEmbeddingsReference, tensor_ops.go:1476-1489)."""
+    _case("encoder id validation at masked positions")
+    from eos_amd._lib import EosHipError
+    w = datagen.bert_q8_weights(1, 384, 12, 1536, 100, 64, seed=5)
+    enc = Encoder(rt, w)
+    ids = np.zeros((2, 16), np.int32)
+    mask = np.ones((2, 16), np.int32)
+    mask[1, 10:] = 0
+    ids[1, 12] = 100
+    with pytest.raises(EosHipError, match="out of range"):
+        enc.embed(ids, mask)
+    ids[1, 12] = 0
+    types = np.zeros_like(ids)
+    types[0, 15] = 2                     # type table has 2 rows
+    mask[0, 15] = 0
+    with pytest.raises(EosHipError, match="out of range"):
+        enc.embed(ids, mask, types)
+    types[0, 15] = 1
+    enc.embed(ids, mask, types)

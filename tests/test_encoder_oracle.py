@@ -134,3 +134,49 @@ def test_encoder_batch_masks():
     assert lens.min() >= 32 and lens.max() <= 512
     np.testing.assert_array_equal(mask.sum(axis=1), lens)
     assert ids.max() < 30522 and ids.min() >= 0
+
+
+def test_cls_pooling_is_position_zero_of_the_pinned_hidden_states():
+    """CLS pooling (clsPoolTensor, bert_embedder_ops.go:183-196): the golden
+    model's hidden states give the golden masked-mean embeddings through an
+    independent numpy mean + f64 L2 (which ties them to the fixture), and
+    oracle.bert_embed(pooling="cls") equals position 0 of those states,
+    normalized, whatever the mask says at position 0. A sequence whose only
+    active position is 0 pools identically both ways."""
+    t, g, cfg = _golden()
+    L = max(int(k.split(".")[2]) for k in t if k.startswith("encoder.layer.")) + 1
+    n, T = len(g["texts"]), g["max_length"]
+    ids = np.array(g["input_ids"], np.int32).reshape(n, T)
+    mask = np.array(g["attention_mask"], np.int32).reshape(n, T)
+    types = np.array(g["token_type_ids"], np.int32).reshape(n, T)
+    args = (t["embeddings.word_embeddings.weight"], t["embeddings.position_embeddings.weight"],
+            t["embeddings.token_type_embeddings.weight"], t["embeddings.LayerNorm.weight"],
+            t["embeddings.LayerNorm.bias"], _layers_from_hf(t, L))
+    heads, eps = cfg["num_attention_heads"], cfg["layer_norm_eps"]
+    h = oracle.bert_hidden(*args, ids, mask, types, heads, eps).astype(np.float64)
+    m = mask.astype(np.float64)
+    mean = (h * m[:, :, None]).sum(axis=1) / m.sum(axis=1, keepdims=True)
+    mean /= np.linalg.norm(mean, axis=1, keepdims=True)
+    np.testing.assert_allclose(mean, np.array(g["embeddings"]), atol=2e-5)
+
+    def unit(x):
+        return x / np.linalg.norm(x, axis=1, keepdims=True)
+
+    cls = oracle.bert_embed(*args, ids, mask, types, heads, eps, pooling="cls")
+    np.testing.assert_allclose(cls, unit(h[:, 0, :]), atol=2e-7)
+    assert np.max(np.abs(cls - mean)) > 1e-2        # CLS is not the mean here
+    # Position 0 masked: its row is still computed (attending to the active
+    # positions) and pooled.
+    mask2 = mask.copy()
+    mask2[1, 0] = 0
+    h2 = oracle.bert_hidden(*args, ids, mask2, types, heads, eps).astype(np.float64)
+    cls2 = oracle.bert_embed(*args, ids, mask2, types, heads, eps, pooling="cls")
+    np.testing.assert_allclose(cls2, unit(h2[:, 0, :]), atol=2e-7)
+    assert np.max(np.abs(cls2[1] - cls[1])) > 1e-4
+    np.testing.assert_array_equal(cls2[[0, 2]], cls[[0, 2]])
+    # Only position 0 active: CLS == masked mean.
+    mask3 = np.zeros_like(mask)
+    mask3[:, 0] = 1
+    a = oracle.bert_embed(*args, ids, mask3, types, heads, eps, pooling="cls")
+    b = oracle.bert_embed(*args, ids, mask3, types, heads, eps)
+    np.testing.assert_allclose(a, b, atol=1e-7)

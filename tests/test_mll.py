@@ -313,3 +313,120 @@ def test_retrieval_classifier_forms():
         with pytest.raises(EosHipError, match="topk limit"):
             _lib.call("eoship_mll_classify_retrieval", m.handle, None,
                       C.byref(_lib.EosHipRetrievalPlan()))
+
+
+def _bert(layers=2, heads=4, hidden=128, inter=256):
+    from eos_amd import datagen
+    w = datagen.bert_q8_weights(layers, hidden, heads, inter, 300, 64, seed=41,
+                                random_affine=True)
+    return w, mll_synth.bert_tensors(w)
+
+
+def test_bert_embedder_plans_classify():
+    """The pretrained-BERT importer's module (one bert_embedder step and its
+    return, runtime/pretrained_bert_importer.go:901-1009) classifies with
+    the step's configuration; f32 dense weights are marked for per-channel
+    quantization at bind, q8 payloads are used as stored."""
+    w, t = _bert()
+    art = mll_synth.bert_artifact(2, 4, eps=1e-7, pooling="cls")
+    with MllPackage(mll_synth.bert_package(art, t)) as m:
+        p = m.classify()
+    assert p["route"] == "bert_embedder" and p["entry"] == "bert_embed"
+    assert (p["layers"], p["model_dim"], p["heads"], p["hidden_dim"], p["vocab"],
+            p["max_positions"], p["type_vocab"], p["output_dim"]) == (2, 128, 4, 256, 300, 64, 2,
+                                                                      128)
+    assert p["pooling"] == "cls" and p["ln_eps"] == 1e-7 and p["weights_quantized"]
+    assert (p["token_input"], p["mask_input"], p["type_input"], p["output_name"]) == (
+        "input_ids", "attention_mask", "token_type_ids", "embeddings")
+    dense = [n for n in t if n.endswith("_weight") and "layernorm" not in n]
+    art2 = mll_synth.bert_artifact(2, 4, attrs={})      # eps, act, pooling defaulted
+    art2["steps"][0]["attributes"] = {"num_hidden_layers": "2", "num_attention_heads": "4"}
+    with MllPackage(mll_synth.bert_package(art2, t, q8=tuple(dense))) as m:
+        p = m.classify()
+    assert p["pooling"] == "masked_mean" and p["ln_eps"] == 1e-12 and not p["weights_quantized"]
+
+
+def test_bert_embedder_refusals():
+    """What bertEmbedderConfigFromAttrs and BERTEmbedderReferenceWithPooling
+    reject (runtime/backend/bert_embedder_ops.go:10-77, 101-152), and shapes
+    outside the fused encoder, are refused with the step named."""
+    w, t = _bert()
+
+    def attrs(**kv):
+        a = {"num_hidden_layers": "2", "num_attention_heads": "4", "epsilon": "1e-12",
+             "hidden_act": "gelu", "pooling": "masked_mean"}
+        a.update(kv)
+        return mll_synth.bert_artifact(2, 4, attrs=a)
+
+    cases = [
+        (attrs(hidden_act="relu"), "unsupported hidden_act \"relu\""),
+        (attrs(pooling="max"), "unsupported pooling \"max\""),
+        (attrs(num_hidden_layers="two"), "num_hidden_layers \"two\" is invalid"),
+        (attrs(num_hidden_layers="0"), "num_hidden_layers \"0\" is invalid"),
+        (attrs(num_attention_heads="-4"), "num_attention_heads \"-4\" is invalid"),
+        (attrs(epsilon="-1e-5"), "epsilon must be non-negative"),
+        (attrs(epsilon="abc"), "epsilon \"abc\" is invalid"),
+        (attrs(num_hidden_layers="3"), "expects 56 tensors for 3 layers, got 40"),
+        (attrs(num_attention_heads="3"), "not a multiple of num_attention_heads"),
+        (attrs(num_attention_heads="16"), "head dim 8"),
+        (mll_synth.mutate(attrs(), lambda a: a["steps"].insert(
+            1, {"entry": "bert_embed", "kind": "normalize", "name": "n", "inputs": ["embeddings"],
+                "outputs": ["e2"]})), "beside a bert_embedder step"),
+        (mll_synth.mutate(attrs(), lambda a: a["steps"].pop()), "no return step"),
+    ]
+    for art, msg in cases:
+        with MllPackage(mll_synth.bert_package(art, t)) as m:
+            with pytest.raises(EosHipError) as ei:
+                m.classify()
+            assert msg in str(ei.value), (msg, str(ei.value))
+    # A layer tensor of the wrong shape, and one that is missing.
+    bad = dict(t)
+    bad["encoder_layer_1_intermediate_bias"] = np.zeros(100, np.float32)
+    with MllPackage(mll_synth.bert_package(mll_synth.bert_artifact(2, 4), bad)) as m:
+        with pytest.raises(EosHipError, match="layer 1 tensor shapes"):
+            m.classify()
+    del bad["encoder_layer_1_intermediate_bias"]
+    with MllPackage(mll_synth.bert_package(mll_synth.bert_artifact(2, 4), bad)) as m:
+        with pytest.raises(EosHipError, match="missing"):
+            m.classify()
+    # The golden fixture's model (hidden 16, 4 heads) is outside the fused
+    # encoder's shapes: refused, so a caller keeps its host executor for it.
+    from safetensors.numpy import load_file
+    g = load_file(os.path.join(os.path.dirname(__file__), "golden", "bert_tiny",
+                               "model.safetensors"))
+    gt = {"token_embeddings": g["embeddings.word_embeddings.weight"],
+          "position_embeddings": g["embeddings.position_embeddings.weight"],
+          "token_type_embeddings": g["embeddings.token_type_embeddings.weight"],
+          "embedding_layernorm_weight": g["embeddings.LayerNorm.weight"],
+          "embedding_layernorm_bias": g["embeddings.LayerNorm.bias"]}
+    hf = ["attention.self.query.weight", "attention.self.query.bias", "attention.self.key.weight",
+          "attention.self.key.bias", "attention.self.value.weight", "attention.self.value.bias",
+          "attention.output.dense.weight", "attention.output.dense.bias",
+          "attention.output.LayerNorm.weight", "attention.output.LayerNorm.bias",
+          "intermediate.dense.weight", "intermediate.dense.bias", "output.dense.weight",
+          "output.dense.bias", "output.LayerNorm.weight", "output.LayerNorm.bias"]
+    for l in range(2):
+        for role, name in zip(mll_synth.BERT_LAYER_ROLES, hf):
+            gt[f"encoder_layer_{l}_{role}"] = g[f"encoder.layer.{l}.{name}"]
+    with MllPackage(mll_synth.bert_package(mll_synth.bert_artifact(2, 4), gt)) as m:
+        with pytest.raises(EosHipError, match="hidden 16, head dim 4, intermediate 32 outside"):
+            m.classify()
+
+
+def test_long_names_are_refused():
+    """Entry, input and param names of 64 bytes or more do not fit the plan's
+    fixed fields: both classifiers refuse them (no truncated name reaches a
+    bind)."""
+    long = "q" * 70
+    art = mll_synth.retrieval_artifact("candidates", "dot", 3)
+    art = json.loads(json.dumps(art).replace('"query"', f'"{long}"'))
+    with MllPackage(mll_synth.retrieval_package(art, None)) as m:
+        with pytest.raises(EosHipError, match="64 bytes or more"):
+            _lib.call("eoship_mll_classify_retrieval", m.handle, None,
+                      C.byref(_lib.EosHipRetrievalPlan()))
+    w, t = _bert()
+    art = mll_synth.bert_artifact(2, 4)
+    art = json.loads(json.dumps(art).replace('"input_ids"', '"' + "i" * 64 + '"'))
+    with MllPackage(mll_synth.bert_package(art, t)) as m:
+        with pytest.raises(EosHipError, match="64 bytes or more"):
+            m.classify()

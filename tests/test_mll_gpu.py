@@ -135,3 +135,72 @@ def test_synthetic_plans(rt, masked, scale, tied):
                            {"tokens": ids, "attention_mask": mask})["result"]
     _check(got, want)
     enc.release()
+
+
+def _bert_oracle_layers(pkg, layers, requantize):
+    """The 16 f32 tensors per layer the GPU computes with: the package's
+    values (q8 payloads: code x tensor scale), with f32 dense weights
+    quantized per output channel as the bind does."""
+    from eos_amd.encoder import quantize_per_channel
+    out = []
+    for l in range(layers):
+        row = []
+        for k, role in enumerate(mll_synth.BERT_LAYER_ROLES):
+            t = pkg.tensor(f"encoder_layer_{l}_{role}")
+            v = np.asarray(t["values"], np.float32)
+            if k in (0, 2, 4, 6, 10, 12) and t["kind"] == "f32" and requantize:
+                c, s = quantize_per_channel(v)
+                v = c.astype(np.float32) * s[:, None]
+            row.append(v)
+        out.append(row)
+    return out
+
+
+@pytest.mark.parametrize("pooling", ["masked_mean", "cls"])
+@pytest.mark.parametrize("storage", ["f32", "q8"])
+def test_bert_embedder_package(rt, pooling, storage):
+    """A bert_embedder package (the pretrained-BERT importer's module) bound
+    through eoship_encoder_bind_mll embeds within the contract of
+    oracle.bert_embed on the weights the GPU computes with (f32 dense
+    weights quantized per output channel at bind; q8 payloads as stored),
+    for both poolings; ragged lengths, token types, position 0 masked in one
+    sequence (CLS still reads it) and a sequence with no active position."""
+    import oracle
+    from eos_amd import datagen
+    _case(f"bert_embedder package {storage} {pooling}")
+    L, H, heads, F = 2, 384, 12, 1536
+    w = datagen.bert_q8_weights(L, H, heads, F, 3000, 256, seed=57, random_affine=True)
+    t = mll_synth.bert_tensors(w)
+    dense = tuple(n for n in t if n.endswith("_weight") and "layernorm" not in n
+                  and n.startswith("encoder_layer_"))
+    art = mll_synth.bert_artifact(L, heads, eps=1e-12, pooling=pooling)
+    pkg = MllPackage(mll_synth.bert_package(art, t, q8=dense if storage == "q8" else ()))
+    enc = MllEncoder(rt, pkg)
+    assert enc.plan["route"] == "bert_embedder" and enc.plan["pooling"] == pooling
+    assert enc.plan["weights_quantized"] == (storage == "f32")
+    ids, mask = _ragged(7, 200, 3000, [200, 17, 1, 120, 0, 64, 199], 58)
+    mask[3, 0] = 0                       # position 0 masked
+    mask[5, 10:20] = 0                   # a hole
+    rng = np.random.default_rng(59)
+    types = rng.integers(0, 2, ids.shape).astype(np.int32)
+    got = enc.embed(ids, mask, types)
+    layers = _bert_oracle_layers(pkg, L, requantize=True)
+    want = oracle.bert_embed(w.tok, w.pos, w.typ, w.emb_gamma, w.emb_beta, layers, ids, mask,
+                             types, heads, 1e-12, pooling=pooling)
+    if pooling == "masked_mean":
+        assert np.all(got[4] == 0) and np.all(want[4] == 0)
+    else:
+        assert np.all(np.isfinite(got)) and abs(np.linalg.norm(got[4]) - 1) < 1e-5
+    _check(got, want)
+    enc.release()
+    pkg.close()
+
+
+def test_bert_embedder_package_refuses_attend_padding(rt):
+    _case("bert_embedder package attend_padding refusal")
+    from eos_amd import datagen
+    w = datagen.bert_q8_weights(1, 128, 4, 256, 100, 32, seed=3)
+    pkg = MllPackage(mll_synth.bert_package(mll_synth.bert_artifact(1, 4), mll_synth.bert_tensors(w)))
+    with pytest.raises(EosHipError, match="attend_padding 1"):
+        MllEncoder(rt, pkg, attend_padding=1)
+    pkg.close()

@@ -111,3 +111,31 @@ def test_score_topk_large_and_errors(rt):
     assert res["top_index"][1][:2].tolist() == [7, 123_456]
     with pytest.raises(EosHipError, match="topk limit"):
         score_topk(rt, "dot", queries[:1], docs[:10], k=11)
+
+
+@pytest.mark.parametrize("op,want", [("dot", [1, 0, 1]), ("cosine", [1, 0, 0.70710677]),
+                                     ("l2_distance", [0, 1.4142135, 1])])
+def test_reference_score_known_answers(rt, op, want):
+    """The reference's score-op known answers (runtime/runtime_test.go:
+    1702-1716): query [1, 0] against docs [[1,0],[0,1],[1,1]]."""
+    _case(f"score known answers {op}")
+    q = np.asarray([[1, 0]], np.float32)
+    docs = np.asarray([[1, 0], [0, 1], [1, 1]], np.float32)
+    res = score_topk(rt, op, q, docs, k=3)
+    np.testing.assert_array_equal(res["scores"][0], np.asarray(want, np.float32))
+
+
+def test_signed_zero_ties_rank_by_index(rt):
+    """A cosine that underflows to -0 (dot -1e-30 against a norm of 1e20)
+    ties with a +0 cosine, as Go's -0 == +0 comparison makes it: the lower
+    index ranks first, whichever zero it holds."""
+    _case("signed zero ties")
+    q = np.asarray([[1, 0]], np.float32)
+    docs = np.asarray([[-1, 0], [-1e-30, 1e20], [0, 1], [0.5, 0.5], [0, 3]], np.float32)
+    want = plan_oracle.oracle.score_rows("cosine", q[0], docs)
+    assert np.signbit(want[1]) and want[1] == 0 and not np.signbit(want[2])
+    res = score_topk(rt, "cosine", q, docs, k=3)
+    np.testing.assert_array_equal(res["scores"][0], want)
+    assert res["top_index"][0].tolist() == [3, 1, 2]
+    idx, _ = plan_oracle.oracle.topk_scores(want, 3)
+    assert idx.tolist() == [3, 1, 2]

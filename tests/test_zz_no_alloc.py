@@ -78,3 +78,50 @@ def test_noalloc_rerank_refuses_more_than_its_scratch(rt):
     for b in (d_q, d_cid, d_cs, d_ids, d_sc):
         b.free()
     side.buf.free()
+
+
+def test_noalloc_rerank_two_runtimes_interleaved(rt):
+    """Two runtimes (two streams) on one GPU call the no-allocation rerank
+    back to back without a synchronisation between them: the per-device
+    event chain orders them on the shared static scratch, so each result
+    equals the allocating entry point's bit for bit."""
+    print("[case] noalloc rerank: two runtimes interleaved on one GPU", flush=True)
+    from eos_amd.runtime import Runtime
+    rng = np.random.default_rng(93)
+    n, d = 4000, 256
+    x = rng.standard_normal((n, d)).astype(np.float32)
+    rt2 = Runtime(0)
+    sides = (F16Sidecar(rt, x), F16Sidecar(rt2, x))
+    runs = []
+    for r, side, nq, c in ((rt, sides[0], 64, 200), (rt2, sides[1], 48, 160)):
+        q = rng.standard_normal((nq, d)).astype(np.float32)
+        cid, cs = _cands(rng, nq, n, c)
+        d_q = DeviceBuffer.from_array(r, q)
+        d_cid = DeviceBuffer.from_array(r, cid)
+        d_cs = DeviceBuffer.from_array(r, cs)
+        runs.append((r, side, nq, c, d_q, d_cid, d_cs, q, cid, cs))
+    rt.sync()
+    rt2.sync()
+    # Outputs allocated first, so nothing between the calls synchronises.
+    outs = [(r, DeviceBuffer(r, nq * 100 * 8), DeviceBuffer(r, nq * 100 * 4), nq)
+            for rep in range(4) for r, side, nq, *_ in runs]
+    for j, (r, d_ids, d_sc, nq) in enumerate(outs):
+        _, side, _, c, d_q, d_cid, d_cs, *_ = runs[j % 2]
+        top_fp16_rerank_scores_device(side, d_q, nq, d_cid, d_cs, c, 100, 4, c, d_ids, d_sc,
+                                      noalloc=True)
+    got = [(i.download(np.int64, (nq, 100)), s.download(np.float32, (nq, 100)))
+           for r, i, s, nq in outs]
+    for r, i, s, nq in outs:
+        i.free()
+        s.free()
+    for j, (r, side, nq, c, d_q, d_cid, d_cs, q, cid, cs) in enumerate(runs):
+        (ia, sa), _ = _both(r, side, q, cid, cs, 100, c)
+        for rep in range(4):
+            ib, sb = got[2 * rep + j]
+            assert np.array_equal(ia, ib)
+            assert np.array_equal(sa.view(np.uint32), sb.view(np.uint32))
+        for b in (d_q, d_cid, d_cs):
+            b.free()
+    for side in sides:
+        side.buf.free()
+    rt2.close()
