@@ -193,6 +193,9 @@ class EosHipTQCodes(C.Structure):
         ("norms", C.c_void_p),
         ("codebook", C.c_void_p),
         ("rotation_t", C.c_void_p),
+        ("signs", C.c_void_p),
+        ("resnorms", C.c_void_p),
+        ("qjl_t", C.c_void_p),
     ]
 
 

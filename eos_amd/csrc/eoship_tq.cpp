@@ -1626,49 +1626,61 @@ int eoship_tq_reconstruct_rerank_device(EosHipRuntime* rt, const EosHipTQCodes* 
   const char* what = "eoship_tq_reconstruct_rerank_device";
   if (codes == nullptr) return set_err(err, "%s: NULL codes", what);
   const int d = codes->dim, bits = codes->bits;
-  if (bits != 1 && bits != 2 && bits != 4 && bits != 8)
-    return set_err(err, "%s: bits must be 1, 2, 4 or 8 (got %d)", what, bits);
+  if (bits != 1 && bits != 2 && bits != 3 && bits != 4 && bits != 8)
+    return set_err(err, "%s: bits must be 1, 2, 3, 4 or 8 (got %d)", what, bits);
+  if (d > 1024) return set_err(err, "%s: dim must be in [1, 1024] (got %d)", what, d);
   if (eoship::rerank_sizes_check(rt, d_queries, q, d, codes->n, d_cand_ids, c, d_ids, d_scores,
                                  what, err) != 0)
     return 1;
   if (q == 0 || c == 0) return 0;
   if (codes->codes == nullptr || codes->norms == nullptr || codes->codebook == nullptr)
     return set_err(err, "%s: NULL codes, norms or codebook", what);
-  // Rotated queries (f64) and the f32 scores share one workspace block.
-  const size_t rq_bytes = (size_t)q * (size_t)d * sizeof(double);
+  const bool ip = codes->signs != nullptr;
+  if (ip && (codes->resnorms == nullptr || codes->qjl_t == nullptr))
+    return set_err(err, "%s: an inner-product code set needs resnorms and qjl_t", what);
+  if (!ip && (codes->resnorms != nullptr || codes->qjl_t != nullptr))
+    return set_err(err, "%s: resnorms and qjl_t without signs", what);
+  // Dequantized vectors [q][c][d] and the f32 scores share one workspace block.
+  const size_t x_bytes = (size_t)q * (size_t)c * (size_t)d * sizeof(float);
   void* ws = nullptr;
-  if (rt->workspace(rq_bytes + (size_t)q * (size_t)c * sizeof(float), &ws, err) != 0) return 1;
+  if (rt->workspace(x_bytes + (size_t)q * (size_t)c * sizeof(float), &ws, err) != 0) return 1;
   TqReconArgs r;
   memset(&r, 0, sizeof(r));
-  r.queries = d_queries;
   r.rot_t = codes->rotation_t;
-  r.rq = static_cast<double*>(ws);
   r.codes = codes->codes;
   r.norms = codes->norms;
   r.codebook = codes->codebook;
+  r.signs = codes->signs;
+  r.resnorms = codes->resnorms;
+  r.qjl_t = codes->qjl_t;
   r.cand_ids = reinterpret_cast<const long long*>(d_cand_ids);
-  r.dots = reinterpret_cast<float*>(static_cast<char*>(ws) + rq_bytes);
+  r.xhat = static_cast<float*>(ws);
   r.n = codes->n;
   r.d = d;
   r.c = c;
   r.bits = bits;
   r.row_bytes = (d * bits + 7) / 8;
-  if (rt->launch("eos_tq_rr_rotate", dim3((unsigned)q), dim3(256), 0, &r, err,
-                 "tq_reconstruct_rotate") != 0 ||
-      rt->launch("eos_tq_rr_dots_recon", dim3((unsigned)((c + 63) / 64), (unsigned)q), dim3(64),
-                 0, &r, err, "tq_reconstruct_dots") != 0)
+  if (rt->launch("eos_tq_rr_dequant", dim3((unsigned)((c + 7) / 8), (unsigned)q), dim3(256), 0, &r,
+                 err, "tq_reconstruct_dequant") != 0)
     return 1;
   TqRerankArgs a;
   memset(&a, 0, sizeof(a));
+  a.queries = d_queries;
+  a.rows_f32 = r.xhat;
+  a.rows_by_pos = 1;
   a.cand_ids = r.cand_ids;
   a.out_ids = reinterpret_cast<long long*>(d_ids);
   a.out_scores = d_scores;
-  a.dots = r.dots;
+  a.dots = reinterpret_cast<float*>(static_cast<char*>(ws) + x_bytes);
   a.n = codes->n;
   a.d = d;
   a.c = c;
   a.kk = (k <= 0 || k > c) ? c : k;
   a.id_rank = reinterpret_cast<const long long*>(d_id_rank);
+  a.vec = d % 4 == 0 ? 1 : 0;
+  if (rt->launch("eos_tq_rr_dots_f32", dim3((unsigned)((c + 63) / 64), (unsigned)q), dim3(64), 0,
+                 &a, err, "tq_reconstruct_dots") != 0)
+    return 1;
   return rt->launch("eos_tq_rr_sort", dim3((unsigned)q), dim3(256), 0, &a, err,
                     "tq_reconstruct_sort");
 }

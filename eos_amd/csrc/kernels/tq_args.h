@@ -222,19 +222,26 @@ struct TqRerankArgs {
   const long long* id_rank;
   const float* rows_f32;         // [n][d] f32 rows (dense rerank) instead of rows
   int vec;                       // rows allow whole 16-byte loads (d % 8 or 4, aligned)
+  // 1: rows_f32 holds one row per candidate position ([q][c][d], the
+  // reconstruct rerank's dequantized vectors) instead of one per id.
+  int rows_by_pos;
 };
 
-// Reconstruct rerank: candidates' codes (reference row layout) against the
-// rotated query; writes the f32 scores into dots for eos_tq_rr_sort.
+// Reconstruct rerank: each candidate's dequantized vector into xhat
+// [q][c][d] (eos_tq_rr_dequant), then the f32 dots of eos_tq_rr_dots_f32
+// (rows by position) and eos_tq_rr_sort.
 struct TqReconArgs {
-  const float* queries;          // [q][d]
   const float* rot_t;            // [d][d], rot_t[k*d + j] = R[j][k]; NULL = identity
-  double* rq;                    // [q][d] rotated queries (eos_tq_rr_rotate)
   const unsigned char* codes;    // [n][row_bytes]
   const float* norms;            // [n]
   const float* codebook;         // [2^bits] f32 centroid values
+  // Inner-product code sets (NULL otherwise): sign bits [n][(d + 7) / 8],
+  // ResNorm [n], and the sketch qjl_t[j*d + i] = S[i][j].
+  const unsigned char* signs;
+  const float* resnorms;
+  const float* qjl_t;
   const long long* cand_ids;     // [q][c]
-  float* dots;                   // [q][c]
+  float* xhat;                   // [q][c][d]
   long long n;
   int d, c, bits, row_bytes;
 };

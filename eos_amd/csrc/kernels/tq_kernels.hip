@@ -2038,6 +2038,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_f16_sidecar(TqHalfArgs 
 constexpr int kRrThreads = 256;
 constexpr int kRrMaxCand = 4096;
 constexpr int kRrMaxDim = 4096;
+constexpr int kRrMaxDqDim = 1024;  // reconstruct rerank: dimensions it dequantizes
 constexpr int kRescueTopK = 100, kRescueLo = 100, kRescueHi = 120, kRescuePromote = 5;
 
 // Order key of a score for a descending sort (-0 and +0 compare equal, as Go's
@@ -2082,6 +2083,8 @@ EOS_DEV void rr_dots_staged(const TqRerankArgs& a) {
   for (int i = lane; i < a.d; i += kRrCand) qv[i] = a.queries[(size_t)qi * a.d + i];
   const long long myid = j < a.c ? a.cand_ids[(size_t)qi * a.c + j] : -1ll;
   const bool valid = myid >= 0 && myid < a.n;
+  // Row of this candidate: its id, or its position (rows_by_pos); -1: none.
+  const long long myrow = !valid ? -1ll : (a.rows_by_pos ? (long long)qi * a.c + j : myid);
   const Elem* rows = F32 ? reinterpret_cast<const Elem*>(a.rows_f32)
                          : reinterpret_cast<const Elem*>(a.rows);
   float s = 0.0f;
@@ -2093,8 +2096,8 @@ EOS_DEV void rr_dots_staged(const TqRerankArgs& a) {
 #pragma unroll
       for (int u = 0; u < kRrCand * CPR / 64; ++u) {
         const int t = lane + 64 * u, r = t / CPR, cc = t % CPR;
-        const long long id = __shfl(myid, r);
-        buf[u] = (id >= 0 && id < a.n && cc * EPV < cols)
+        const long long id = __shfl(myrow, r);
+        buf[u] = (id >= 0 && cc * EPV < cols)
                      ? __builtin_nontemporal_load(reinterpret_cast<const v4u*>(
                            rows + (size_t)id * a.d + c0 + cc * EPV))
                      : v4u{0u, 0u, 0u, 0u};
@@ -2107,9 +2110,8 @@ EOS_DEV void rr_dots_staged(const TqRerankArgs& a) {
     } else {
       for (int t = lane; t < kRrCand * kRrChunk; t += 64) {
         const int r = t / kRrChunk, cc = t % kRrChunk;
-        const long long id = __shfl(myid, r);
-        tile[r * LD + cc] = (id >= 0 && id < a.n && cc < cols) ? rows[(size_t)id * a.d + c0 + cc]
-                                                                 : (Elem)0;
+        const long long id = __shfl(myrow, r);
+        tile[r * LD + cc] = (id >= 0 && cc < cols) ? rows[(size_t)id * a.d + c0 + cc] : (Elem)0;
       }
     }
     __syncthreads();
@@ -2140,53 +2142,97 @@ extern "C" __global__ __launch_bounds__(64) void eos_tq_rr_dots_f32(TqRerankArgs
 
 // Reconstruct rerank (topTurboQuantReconstructRerankScores and, on a sidecar
 // code set, topTurboQuantMixedWidthRerankScores, runtime/retrieval_turboquant.
-// go:1788-1846): the score of a candidate is the inner product of the query
-// with the dequantized vector norm * R^T c[code]. The dequantizer lives in the
-// un-vendored quantizer module; this build's contract evaluates the product
-// in the rotated frame, in f64:
-//   rq_j  = fma chain over k ascending of R[j][k] * q[k]     (eos_tq_rr_rotate)
-//   acc   = fma chain over j ascending of rq_j * codebook[code_j]
-//   score = (float)(acc * norm)
-// Codes are the reference row layout (bits in {1, 2, 4, 8}, code j in byte
-// j / (8 / bits) at bit (j % (8 / bits)) * bits).
-extern "C" __global__ __launch_bounds__(256) void eos_tq_rr_rotate(TqReconArgs a) {
-  const int qi = blockIdx.x;
-  const float* q = a.queries + (size_t)qi * a.d;
-  for (int jj = threadIdx.x; jj < a.d; jj += 256) {
-    double acc = 0.0;
-    if (a.rot_t != nullptr) {
-      for (int k = 0; k < a.d; ++k)
-        acc = __fma_rn((double)a.rot_t[(size_t)k * a.d + jj], (double)q[k], acc);
-    } else {
-      acc = (double)q[jj];
-    }
-    a.rq[(size_t)qi * a.d + jj] = acc;
-  }
+// go:1788-1846): the reference scores dotRetrievalVectors(query,
+// q.Dequantize(codes)). The dequantizer is in the un-vendored quantizer
+// module; this build's contract follows the published TurboQuant dequantizers
+// in f64 with one rounding per coordinate:
+//   y_j = (double)codebook[code_j]
+//         (+ coef * z_j for an inner-product set: z_j = sum over i ascending of
+//          (bit_i ? S[i][j] : -S[i][j]), coef = (sqrt(pi/2) / d) * ResNorm)
+//   x_k = (float)(Norm * acc_k), acc_k = fma chain over j ascending of
+//         R[j][k] * y_j (identity: y_k)
+// eos_tq_rr_dequant writes x for 8 candidates per workgroup into xhat; the
+// f32 index-order dots (eos_tq_rr_dots_f32 over rows by position) follow.
+// Codes are the reference row layout: code j at bits j*bits .. + bits - 1,
+// low bits first (3-bit codes may straddle two bytes).
+constexpr int kRrDqCand = 8;
+
+EOS_DEV int rr_code_at(const unsigned char* row, int j, int bits) {
+  const int bit = j * bits, byte = bit >> 3, sh = bit & 7;
+  unsigned v = (unsigned)row[byte] >> sh;
+  if (sh + bits > 8) v |= (unsigned)row[byte + 1] << (8 - sh);
+  return (int)(v & ((1u << bits) - 1u));
 }
 
-extern "C" __global__ __launch_bounds__(64) void eos_tq_rr_dots_recon(TqReconArgs a) {
-  __shared__ double rq[kRrMaxDim];
-  __shared__ double cb[256];
-  const int qi = blockIdx.y, lane = threadIdx.x;
-  const int j = blockIdx.x * 64 + lane;
-  for (int i = lane; i < a.d; i += 64) rq[i] = a.rq[(size_t)qi * a.d + i];
-  for (int i = lane; i < (1 << a.bits); i += 64) cb[i] = (double)a.codebook[i];
+extern "C" __global__ __launch_bounds__(256) void eos_tq_rr_dequant(TqReconArgs a) {
+  __shared__ double y[kRrDqCand][kRrMaxDqDim];
+  __shared__ unsigned char sg[kRrDqCand][kRrMaxDqDim / 8];
+  __shared__ long long ids[kRrDqCand];
+  __shared__ double coef[kRrDqCand];
+  const int qi = blockIdx.y, tid = threadIdx.x;
+  const int j0 = blockIdx.x * kRrDqCand;
+  if (tid < kRrDqCand) {
+    const int j = j0 + tid;
+    const long long id = j < a.c ? a.cand_ids[(size_t)qi * a.c + j] : -1ll;
+    ids[tid] = (id >= 0 && id < a.n) ? id : -1ll;
+    coef[tid] = (a.signs != nullptr && ids[tid] >= 0)
+                    ? __dmul_rn(__ddiv_rn(1.2533141373155003, (double)a.d),
+                                (double)a.resnorms[ids[tid]])
+                    : 0.0;
+  }
   __syncthreads();
-  if (j >= a.c) return;
-  const long long id = a.cand_ids[(size_t)qi * a.c + j];
-  if (id < 0 || id >= a.n) return;
-  const unsigned char* row = a.codes + (size_t)id * a.row_bytes;
-  const int per = 8 / a.bits;
-  const unsigned mask = (1u << a.bits) - 1u;
-  double acc = 0.0;
-  for (int b = 0; b < a.row_bytes; ++b) {
-    const unsigned byte = row[b];
-    for (int e = 0; e < per; ++e) {
-      const int jj = b * per + e;
-      if (jj < a.d) acc = __fma_rn(rq[jj], cb[(byte >> (e * a.bits)) & mask], acc);
+  // y = codebook values of each candidate's codes (zeros for no candidate).
+  for (int t = tid; t < kRrDqCand * a.d; t += 256) {
+    const int cc = t / a.d, j = t % a.d;
+    const long long id = ids[cc];
+    y[cc][j] = id >= 0 ? (double)a.codebook[rr_code_at(a.codes + (size_t)id * a.row_bytes, j, a.bits)]
+                       : 0.0;
+  }
+  if (a.signs != nullptr) {
+    const int sb = (a.d + 7) / 8;
+    for (int t = tid; t < kRrDqCand * sb; t += 256) {
+      const int cc = t / sb, b = t % sb;
+      sg[cc][b] = ids[cc] >= 0 ? a.signs[(size_t)ids[cc] * sb + b] : (unsigned char)0;
+    }
+    __syncthreads();
+    // z_j = S^T sign: thread j streams row j of qjl_t (S[i][j], i ascending).
+    for (int j = tid; j < a.d; j += 256) {
+      const float* srow = a.qjl_t + (size_t)j * a.d;
+      double z[kRrDqCand];
+#pragma unroll
+      for (int cc = 0; cc < kRrDqCand; ++cc) z[cc] = 0.0;
+      for (int i = 0; i < a.d; ++i) {
+        const double v = (double)srow[i];
+#pragma unroll
+        for (int cc = 0; cc < kRrDqCand; ++cc)
+          z[cc] = ((sg[cc][i >> 3] >> (i & 7)) & 1) ? __dadd_rn(z[cc], v) : __dsub_rn(z[cc], v);
+      }
+#pragma unroll
+      for (int cc = 0; cc < kRrDqCand; ++cc) y[cc][j] = __dadd_rn(y[cc][j], __dmul_rn(coef[cc], z[cc]));
     }
   }
-  a.dots[(size_t)qi * a.c + j] = __double2float_rn(acc * (double)a.norms[id]);
+  __syncthreads();
+  // x_k = Norm * (R^T y)_k: thread k streams row k of rot_t (R[j][k], j ascending).
+  for (int k = tid; k < a.d; k += 256) {
+    double acc[kRrDqCand];
+#pragma unroll
+    for (int cc = 0; cc < kRrDqCand; ++cc) acc[cc] = a.rot_t != nullptr ? 0.0 : y[cc][k];
+    if (a.rot_t != nullptr) {
+      const float* rrow = a.rot_t + (size_t)k * a.d;
+      for (int j = 0; j < a.d; ++j) {
+        const double r = (double)rrow[j];
+#pragma unroll
+        for (int cc = 0; cc < kRrDqCand; ++cc) acc[cc] = __fma_rn(r, y[cc][j], acc[cc]);
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < kRrDqCand; ++cc) {
+      const long long id = ids[cc];
+      if (id >= 0)
+        a.xhat[((size_t)qi * a.c + j0 + cc) * a.d + k] =
+            __double2float_rn(__dmul_rn((double)a.norms[id], acc[cc]));
+    }
+  }
 }
 
 // Second rerank kernel, one workgroup per query: sorts the candidates in LDS by

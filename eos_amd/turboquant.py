@@ -506,12 +506,15 @@ def dense_rerank_top_k(rt: Runtime, queries: np.ndarray, rows: np.ndarray,
 def reconstruct_rerank_top_k(rt: Runtime, queries: np.ndarray, codes: np.ndarray, bits: int,
                              norms: np.ndarray, codebook: np.ndarray, rotation: np.ndarray | None,
                              cand_ids: np.ndarray, top_k: int,
-                             id_rank: np.ndarray | None = None):
+                             id_rank: np.ndarray | None = None, signs: np.ndarray | None = None,
+                             resnorms: np.ndarray | None = None, sketch: np.ndarray | None = None):
     """Reconstruct rerank over a code set in the reference row layout (the
     primary codes: topTurboQuantReconstructRerankScores; a wider sidecar set:
     topTurboQuantMixedWidthRerankScores, runtime/retrieval_turboquant.go:
-    1788-1846). rotation is R [d, d] (None: identity), codebook the f32
-    centroids [2^bits]. Returns (ids int64 [Q, kk], scores float32)."""
+    1788-1846): each candidate dequantized (with the QJL term when signs,
+    resnorms and the sketch S [d, d] are given: an inner-product set), then
+    the f32 index-order dot. rotation is R [d, d] (None: identity), codebook
+    the f32 centroids [2^bits]. Returns (ids int64 [Q, kk], scores float32)."""
     q = np.ascontiguousarray(queries, np.float32)
     cid = np.ascontiguousarray(cand_ids, np.int64)
     nq, c = cid.shape
@@ -532,9 +535,18 @@ def reconstruct_rerank_top_k(rt: Runtime, queries: np.ndarray, codes: np.ndarray
     if id_rank is not None:
         rank = DeviceBuffer.from_array(rt, np.ascontiguousarray(id_rank, np.int64))
         bufs.append(rank)
+    ipb = [None, None, None]
+    if signs is not None:
+        ipb = [DeviceBuffer.from_array(rt, np.ascontiguousarray(signs, np.uint8)),
+               DeviceBuffer.from_array(rt, np.ascontiguousarray(resnorms, np.float32)),
+               DeviceBuffer.from_array(rt, np.ascontiguousarray(np.asarray(sketch, np.float32).T))]
+        bufs += ipb
     spec = _lib.EosHipTQCodes(bits=bits, dim=d, n=norms.shape[0], codes=bufs[1].ptr.value,
                               norms=bufs[2].ptr.value, codebook=bufs[3].ptr.value,
-                              rotation_t=rot.ptr.value if rot is not None else None)
+                              rotation_t=rot.ptr.value if rot is not None else None,
+                              signs=ipb[0].ptr.value if ipb[0] is not None else None,
+                              resnorms=ipb[1].ptr.value if ipb[1] is not None else None,
+                              qjl_t=ipb[2].ptr.value if ipb[2] is not None else None)
     kk, d_ids, d_sc = _rerank_out(rt, nq, c, top_k)
     try:
         _lib.call("eoship_tq_reconstruct_rerank_device", rt.handle, C.byref(spec), bufs[0].ptr,

@@ -525,27 +525,37 @@ int eoship_tq_dense_rerank_device(EosHipRuntime* rt, const float* d_queries, int
                                   float* d_scores, char** err);
 
 /* A TurboQuant code set on the device in the reference row layout: the
- * primary codes or a wider sidecar set with its own codebook. */
+ * primary codes or a wider sidecar set with its own codebook; with signs,
+ * resnorms and qjl_t an inner-product set (IPQuantized{MSE, Signs, ResNorm,
+ * Norm}, runtime/turboquant_bytes.go:14-25, the layout of
+ * eoship_tq_ip_encode_device). */
 typedef struct {
-  int32_t bits;               /* 1, 2, 4 or 8 bits per coordinate */
-  int32_t dim;                /* d */
+  int32_t bits;               /* 1, 2, 3, 4 or 8 bits per coordinate */
+  int32_t dim;                /* d (1..1024) */
   int64_t n;                  /* vectors */
-  const uint8_t* codes;       /* [n][(d * bits + 7) / 8], code j in byte j / (8 / bits),
-                               * low bits first */
+  const uint8_t* codes;       /* [n][(d * bits + 7) / 8], code j at bits j * bits .. + bits - 1
+                               * of the row, low bits first (3-bit codes straddle bytes) */
   const float* norms;         /* [n] */
   const float* codebook;      /* [2^bits] f32 centroid values */
   const float* rotation_t;    /* [d][d], rotation_t[k * d + j] = R[j][k]; NULL = identity */
+  const uint8_t* signs;       /* NULL, or [n][(d + 7) / 8] QJL sign bits, low bit first */
+  const float* resnorms;      /* [n] with signs: |r| / Norm */
+  const float* qjl_t;         /* [d][d] with signs: qjl_t[j * d + i] = S[i][j] */
 } EosHipTQCodes;
 
-/* Reconstruct rerank: each candidate scored as the inner product of the query
- * with its dequantized vector norm * R^T codebook[code], then (score desc, ID
- * asc) as eoship_tq_dense_rerank_device. With the primary codes this replaces
+/* Reconstruct rerank: each candidate scored as dotRetrievalVectors(query,
+ * Dequantize(codes)) -- the f32 sum += q[k] * x[k] in index order, each
+ * product and sum rounded -- then (score desc, ID asc) as
+ * eoship_tq_dense_rerank_device. With the primary codes this replaces
  * topTurboQuantReconstructRerankScores, with a sidecar set (e.g. 8-bit codes)
  * topTurboQuantMixedWidthRerankScores (runtime/retrieval_turboquant.go:
- * 1788-1846). The dequantizer is in the un-vendored quantizer module, so the
- * product is this build's contract, evaluated in the rotated frame in f64:
- * rq = R q (fma in k order), acc = sum_j fma(rq_j, codebook[code_j]), score =
- * (float)(acc * norm). Uses a workspace of q * d * 8 + q * c * 4 bytes. */
+ * 1788-1846). Dequantize is in the un-vendored quantizer module, so the
+ * dequantized vector is this build's contract after the published TurboQuant
+ * dequantizers, in f64 with one rounding per coordinate: y_j =
+ * codebook[code_j] (+ (sqrt(pi/2) / d) * ResNorm * sum_i (bit_i ? S[i][j] :
+ * -S[i][j]) for an inner-product set, the TurboQuant_prod QJL term), x_k =
+ * (float)(Norm * sum_j R[j][k] y_j) (fma chain, j ascending). Uses a
+ * workspace of q * c * (d + 1) * 4 bytes. */
 int eoship_tq_reconstruct_rerank_device(EosHipRuntime* rt, const EosHipTQCodes* codes,
                                         const float* d_queries, int32_t q,
                                         const int64_t* d_cand_ids, int32_t c, int32_t k,

@@ -525,28 +525,59 @@ def dense_rerank(queries, rows, cand_ids, k, id_rank=None):
 
 
 def reconstruct_rerank(queries, rotation, codes, bits, norms, codebook, cand_ids, k,
-                       id_rank=None):
-    """Reconstruct / mixed-width rerank per query (this build's contract, see
-    rerank_oracle.c): (ids [Q, kk], scores)."""
+                       id_rank=None, signs=None, resnorms=None, sketch=None):
+    """Reconstruct / mixed-width rerank per query (rerank_oracle.c): each
+    candidate dequantized to the original frame (with the QJL term when
+    signs, resnorms and sketch S [d, d] are given: an inner-product code
+    set), then the f32 index-order dot. (ids [Q, kk], scores)."""
     q = np.ascontiguousarray(queries, np.float32)
     rot = None if rotation is None else np.ascontiguousarray(rotation, np.float32)
     codes = np.ascontiguousarray(codes, np.uint8)
     norms = np.ascontiguousarray(norms, np.float32)
     cb = np.ascontiguousarray(codebook, np.float32)
     cid = np.ascontiguousarray(cand_ids, np.int64)
+    ip = signs is not None
+    if ip:
+        signs = np.ascontiguousarray(signs, np.uint8)
+        resnorms = np.ascontiguousarray(resnorms, np.float32)
+        sketch = np.ascontiguousarray(sketch, np.float32)
     nq, d = q.shape
     c = cid.shape[1]
     n = norms.shape[0]
     sc = np.zeros((nq, c), np.float32)
     lib = load()
+    fn = lib.oracle_recon_scores_ip
+    fn.restype = None
+    vp = lambda a: None if a is None else a.ctypes.data_as(C.c_void_p)
     for i in range(nq):
-        lib.oracle_recon_scores(q[i].ctypes.data_as(C.c_void_p), C.c_int(d),
-                                None if rot is None else rot.ctypes.data_as(C.c_void_p),
-                                codes.ctypes.data_as(C.c_void_p), C.c_int(bits),
-                                norms.ctypes.data_as(C.c_void_p), cb.ctypes.data_as(C.c_void_p),
-                                C.c_int64(n), cid[i].ctypes.data_as(C.c_void_p), C.c_int(c),
-                                sc[i].ctypes.data_as(C.c_void_p))
+        fn(vp(q[i]), C.c_int(d), vp(rot), vp(codes), C.c_int(bits), vp(norms), vp(cb),
+           vp(signs) if ip else None, vp(resnorms) if ip else None, vp(sketch) if ip else None,
+           C.c_int64(n), vp(cid[i]), C.c_int(c), vp(sc[i]))
     return _rerank_finish(sc, cid, n, k, id_rank)
+
+
+def tq_dequantize(rotation, code_row, bits, norm, codebook, sign_row=None, resnorm=0.0,
+                  sketch=None):
+    """One entry's dequantized vector (rerank_oracle.c oracle_tq_dequantize)."""
+    cb = np.ascontiguousarray(codebook, np.float32)
+    row = np.ascontiguousarray(code_row, np.uint8)
+    d = None
+    rot = None if rotation is None else np.ascontiguousarray(rotation, np.float32)
+    sk = None if sketch is None else np.ascontiguousarray(sketch, np.float32)
+    if rot is not None:
+        d = rot.shape[0]
+    elif sk is not None:
+        d = sk.shape[0]
+    else:
+        d = row.size * 8 // bits
+    out = np.zeros(d, np.float32)
+    sg = None if sign_row is None else np.ascontiguousarray(sign_row, np.uint8)
+    vp = lambda a: None if a is None else a.ctypes.data_as(C.c_void_p)
+    fn = load().oracle_tq_dequantize
+    fn.restype = None
+    fn(C.c_int(d), vp(rot), vp(row), C.c_int(bits), C.c_float(norm), vp(cb), vp(sg),
+       C.c_float(resnorm), vp(sk), vp(out))
+    return out
 
 
 # ------------------------------------------------ Hadamard TurboQuant codec

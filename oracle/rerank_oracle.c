@@ -222,39 +222,88 @@ void oracle_dense_scores(const float* query, int d, const float* rows, int64_t n
   }
 }
 
-/* This build's reconstruct contract: rq = R q (fma, k ascending), acc = fma
- * chain of rq_j * codebook[code_j] (j ascending), score = (float)(acc *
- * norm). rot is R row-major (NULL: identity); codes in the reference row
- * layout (code j in byte j / (8 / bits), low bits first). */
-void oracle_recon_scores(const float* query, int d, const float* rot, const uint8_t* codes,
-                         int bits, const float* norms, const float* codebook, int64_t n,
-                         const int64_t* cand_ids, int c, float* out) {
-  double* rq = (double*)malloc(sizeof(double) * (size_t)d);
-  for (int jj = 0; jj < d; ++jj) {
-    double acc = 0.0;
-    if (rot != NULL) {
-      for (int k = 0; k < d; ++k) acc = fma((double)rot[(size_t)jj * d + k], (double)query[k], acc);
-    } else {
-      acc = (double)query[jj];
+/* Code j of a row in the reference row layout: bits j*bits .. j*bits+bits-1
+ * of the row, low bits first (a 3-bit code may straddle two bytes). */
+static int tq_code_at(const uint8_t* row, int j, int bits) {
+  const int bit = j * bits, byte = bit >> 3, sh = bit & 7;
+  unsigned v = (unsigned)row[byte] >> sh;
+  if (sh + bits > 8) v |= (unsigned)row[byte + 1] << (8 - sh);
+  return (int)(v & ((1u << bits) - 1u));
+}
+
+/* The dequantized vector of one code-set entry, this build's contract after
+ * the published TurboQuant dequantizers (the reference calls the un-vendored
+ * module's Dequantize, runtime/retrieval_turboquant.go:1802,1833):
+ *   y_j = (double)codebook[code_j], plus, for an inner-product entry
+ *         (signs != NULL), coef * z_j with z_j = the f64 sum over i ascending
+ *         of (bit_i ? S[i][j] : -S[i][j]) and coef = (sqrt(pi/2) / d) * ResNorm
+ *         (TurboQuant_prod's sqrt(pi/2)/d * |r| * S^T sign(S r), with |r| =
+ *         ResNorm * Norm and Norm applied below);
+ *   x_k = (float)(Norm * acc_k), acc_k the f64 fma chain over j ascending of
+ *         R[j][k] * y_j (the inverse rotation R^T y; identity: acc_k = y_k).
+ * rot: R row-major (NULL: identity); sketch: S row-major. */
+void oracle_tq_dequantize(int d, const float* rot, const uint8_t* row, int bits, float norm,
+                          const float* codebook, const uint8_t* sign_row, float resnorm,
+                          const float* sketch, float* out) {
+  double* y = (double*)malloc(sizeof(double) * (size_t)d);
+  for (int j = 0; j < d; ++j) y[j] = (double)codebook[tq_code_at(row, j, bits)];
+  if (sign_row != NULL) {
+    const double coef = (1.2533141373155003 / (double)d) * (double)resnorm;
+    for (int j = 0; j < d; ++j) {
+      double z = 0.0;
+      for (int i = 0; i < d; ++i) {
+        const double s = (double)sketch[(size_t)i * d + j];
+        z = ((sign_row[i >> 3] >> (i & 7)) & 1) ? z + s : z - s;
+      }
+      y[j] = y[j] + coef * z;
     }
-    rq[jj] = acc;
   }
-  const int per = 8 / bits, row_bytes = (d * bits + 7) / 8;
+  for (int k = 0; k < d; ++k) {
+    double acc;
+    if (rot != NULL) {
+      acc = 0.0;
+      for (int j = 0; j < d; ++j) acc = fma((double)rot[(size_t)j * d + k], y[j], acc);
+    } else {
+      acc = y[k];
+    }
+    out[k] = (float)((double)norm * acc);
+  }
+  free(y);
+}
+
+/* Reconstruct / mixed-width rerank scores: each candidate's dequantized
+ * vector (above) dotted with the query as dotRetrievalVectors does
+ * (runtime/retrieval_eval.go:1189-1199: sum += a[i] * b[i] in f32, i
+ * ascending, product and sum rounded separately). signs / resnorms / sketch
+ * NULL: an MSE-only code set. Candidates outside [0, n) score 0 (skipped by
+ * the order). */
+void oracle_recon_scores_ip(const float* query, int d, const float* rot, const uint8_t* codes,
+                            int bits, const float* norms, const float* codebook,
+                            const uint8_t* signs, const float* resnorms, const float* sketch,
+                            int64_t n, const int64_t* cand_ids, int c, float* out) {
+  const size_t row_bytes = ((size_t)d * bits + 7) / 8, sign_bytes = ((size_t)d + 7) / 8;
+  float* x = (float*)malloc(sizeof(float) * (size_t)d);
   for (int j = 0; j < c; ++j) {
     const int64_t id = cand_ids[j];
     if (id < 0 || id >= n) {
       out[j] = 0.0f;
       continue;
     }
-    const uint8_t* row = codes + (size_t)id * (size_t)row_bytes;
-    double acc = 0.0;
-    for (int jj = 0; jj < d; ++jj) {
-      const int code = (row[jj / per] >> ((jj % per) * bits)) & ((1 << bits) - 1);
-      acc = fma(rq[jj], (double)codebook[code], acc);
-    }
-    out[j] = (float)(acc * (double)norms[id]);
+    oracle_tq_dequantize(d, rot, codes + (size_t)id * row_bytes, bits, norms[id], codebook,
+                         signs != NULL ? signs + (size_t)id * sign_bytes : NULL,
+                         resnorms != NULL ? resnorms[id] : 0.0f, sketch, x);
+    float s = 0.0f;
+    for (int k = 0; k < d; ++k) s += query[k] * x[k];
+    out[j] = s;
   }
-  free(rq);
+  free(x);
+}
+
+void oracle_recon_scores(const float* query, int d, const float* rot, const uint8_t* codes,
+                         int bits, const float* norms, const float* codebook, int64_t n,
+                         const int64_t* cand_ids, int c, float* out) {
+  oracle_recon_scores_ip(query, d, rot, codes, bits, norms, codebook, NULL, NULL, NULL, n,
+                         cand_ids, c, out);
 }
 
 /* Order the scored candidates (insertion sort by score desc, tie key asc:

@@ -176,10 +176,14 @@ def test_dense_rerank_oracle_pins():
 
 
 def test_reconstruct_rerank_oracle_pins():
-    """The reconstruct contract equals the dense rerank over the explicitly
-    dequantized vectors norm * R^T codebook[code] (to f32 rounding), equals
-    the f64 estimator tq_scores_f64 with an int8-grid codebook, and with the
-    identity rotation and a one-hot query reduces to norm * codebook value."""
+    """The reconstruct contract (dequantize to the original frame, then the
+    reference's f32 index-order dot): the dequantized vector equals an
+    independent numpy f64 construction norm * R^T codebook[code] to f32
+    rounding; the scores equal the f32 dots of those vectors bit for bit;
+    they track the f64 estimator tq_scores_f64 to f32 accumulation error;
+    the identity rotation and a one-hot query reduce to norm * codebook
+    value; and a slip in the row layout or the frame (R instead of R^T) is
+    caught."""
     rng = np.random.default_rng(5)
     d, bits, n = 64, 4, 200
     rot = np.linalg.qr(rng.normal(size=(d, d)))[0].astype(np.float32)
@@ -194,16 +198,96 @@ def test_reconstruct_rerank_oracle_pins():
     full = np.zeros((3, n), np.float32)
     for i in range(3):
         full[i, ids[i]] = sc[i]
-    # dequantized vectors, then plain dots
     lo, hi = codes & 0xF, codes >> 4
     code = np.stack([lo, hi], axis=2).reshape(n, d)
-    xhat = (norms[:, None].astype(np.float64) *
-            (cb.astype(np.float64)[code] @ rot.astype(np.float64)))
-    np.testing.assert_allclose(full, q.astype(np.float64) @ xhat.T, rtol=2e-5, atol=2e-6)
+    xhat64 = (norms[:, None].astype(np.float64) *
+              (cb.astype(np.float64)[code] @ rot.astype(np.float64)))
+    xhat = np.stack([oracle.tq_dequantize(rot, codes[v], bits, norms[v], cb) for v in range(n)])
+    np.testing.assert_allclose(xhat, xhat64, rtol=1e-6, atol=1e-7)
+    assert np.max(np.abs(xhat - xhat64.astype(np.float32))) <= 1.2e-7 * np.abs(xhat64).max()
+    # scores: dotRetrievalVectors over the dequantized f32 vectors
+    for i in range(3):
+        want = np.zeros(n, np.float32)
+        for k in range(d):
+            want = (want + (q[i, k] * xhat[:, k]).astype(np.float32)).astype(np.float32)
+        np.testing.assert_array_equal(full[i], want)
     est = oracle.tq_scores_f64(q, rot, d, bits, cbi, s_c, codes, norms)
-    np.testing.assert_allclose(full, est, rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(full, est, rtol=1e-5, atol=2e-6)
+    # R^T, not R: the same codes under R dequantize elsewhere
+    wrong = norms[:, None].astype(np.float64) * (cb.astype(np.float64)[code] @ rot.T.astype(np.float64))
+    assert np.max(np.abs(xhat - wrong)) > 1e-2
     one = np.zeros((1, d), np.float32)
     one[0, 5] = 1.0
     ids1, sc1 = oracle.reconstruct_rerank(one, None, codes, bits, norms, cb, cid[:1], 0)
     want = norms[ids1[0]] * cb[code[ids1[0], 5]]
     np.testing.assert_array_equal(sc1[0], want.astype(np.float32))
+
+
+def test_reconstruct_three_bit_rows_straddle_bytes():
+    """3-bit codes (the (b - 1)-bit MSE part of an inner-product set at b =
+    4) packed low bits first across byte boundaries: code j sits at bits
+    3j .. 3j + 2 of the row."""
+    d, bits = 16, 3
+    want_codes = np.arange(16) % 8
+    bitsv = np.zeros(d * bits, np.uint8)
+    for j, v in enumerate(want_codes):
+        for b in range(bits):
+            bitsv[j * bits + b] = (v >> b) & 1
+    row = np.packbits(bitsv, bitorder="little")
+    assert row.size == 6
+    cb = np.arange(8, dtype=np.float32) - 3.5
+    x = oracle.tq_dequantize(None, row, bits, 2.0, cb)
+    np.testing.assert_array_equal(x, 2.0 * cb[want_codes])
+
+
+def test_reconstruct_inner_product_set_adds_the_qjl_term():
+    """Inner-product code sets (MSE codes + QJL signs + ResNorm + Norm): the
+    dequantized vector is norm * R^T (c[code] + sqrt(pi/2)/d * ResNorm *
+    S^T sign) (TurboQuant_prod's dequantizer), built independently in numpy
+    f64 here; its inner product with a query equals the inner-product
+    estimator tq_ip_scores (the same estimator through int16 query grids, to
+    their rounding); and over many sketches it is unbiased for <q, x> where
+    the MSE part alone is biased."""
+    rng = np.random.default_rng(8)
+    d, bits = 64, 3
+    rot = np.linalg.qr(rng.normal(size=(d, d)))[0].astype(np.float32)
+    pts = np.sort(rng.normal(size=1 << bits))
+    cbi = np.clip(np.rint(pts / np.abs(pts).max() * 127), -127, 127).astype(np.int8)
+    s_c = float(np.float32(2.2 / np.sqrt(d) / 127))
+    cb = (cbi.astype(np.float32) * np.float32(s_c)).astype(np.float32)
+    x = rng.normal(size=(40, d)).astype(np.float32)
+    q = rng.normal(size=(2, d)).astype(np.float32)
+    S = rng.normal(size=(d, d)).astype(np.float32)
+    codes, signs, rn, nm = oracle.tq_encode_ip(x, rot, S, d, bits, cbi, s_c)
+    bitsv = np.unpackbits(codes, axis=1, bitorder="little")[:, :d * bits].reshape(40, d, bits)
+    code = (bitsv * (1 << np.arange(bits))).sum(2)
+    sg = np.unpackbits(signs, axis=1, bitorder="little")[:, :d].astype(np.float64) * 2 - 1
+    y = cb.astype(np.float64)[code] + (np.sqrt(np.pi / 2) / d) * rn[:, None].astype(np.float64) * (
+        sg @ S.astype(np.float64))
+    xhat64 = nm[:, None].astype(np.float64) * (y @ rot.astype(np.float64))
+    xhat = np.stack([oracle.tq_dequantize(rot, codes[v], bits, nm[v], cb, signs[v], rn[v], S)
+                     for v in range(40)])
+    np.testing.assert_allclose(xhat, xhat64, rtol=2e-6, atol=1e-6)
+    cid = np.tile(np.arange(40, dtype=np.int64), (2, 1))
+    ids, sc = oracle.reconstruct_rerank(q, rot, codes, bits, nm, cb, cid, 0, signs=signs,
+                                        resnorms=rn, sketch=S)
+    full = np.zeros((2, 40), np.float32)
+    for i in range(2):
+        full[i, ids[i]] = sc[i]
+    ip = oracle.tq_ip_scores(q, rot, S, d, bits, cbi, s_c, codes, signs, rn, nm)
+    scale = np.linalg.norm(q, axis=1)[:, None] * nm[None, :]
+    assert np.max(np.abs(full - ip) / scale) < 2e-4
+    # unbiasedness over sketches (one vector, one query)
+    xv, qv = x[0], q[0]
+    true = float(np.dot(qv.astype(np.float64), xv.astype(np.float64)))
+    ests, mses = [], []
+    for t in range(300):
+        St = np.random.default_rng(100 + t).normal(size=(d, d)).astype(np.float32)
+        c1, s1, r1, n1 = oracle.tq_encode_ip(xv[None], rot, St, d, bits, cbi, s_c)
+        xi = oracle.tq_dequantize(rot, c1[0], bits, n1[0], cb, s1[0], r1[0], St)
+        xm = oracle.tq_dequantize(rot, c1[0], bits, n1[0], cb)
+        ests.append(float(np.dot(qv, xi)))
+        mses.append(float(np.dot(qv, xm)))
+    ests = np.array(ests)
+    assert abs(ests.mean() - true) < 4 * ests.std() / np.sqrt(len(ests))
+    assert np.std(mses) < 1e-9                       # the MSE part does not move

@@ -57,7 +57,7 @@ def test_dense_rerank_string_id_order(rt):
 
 
 @pytest.mark.parametrize("bits,d,rotate", [(4, 384, True), (8, 256, True), (2, 128, False),
-                                           (1, 96, True)])
+                                           (1, 96, True), (3, 250, True)])
 def test_reconstruct_rerank(rt, bits, d, rotate):
     """Primary 4-bit codes and an 8-bit sidecar set (mixed width), with and
     without a rotation."""
@@ -75,5 +75,33 @@ def test_reconstruct_rerank(rt, bits, d, rotate):
     cid[3, :2] = [22, 21]
     ids, sc = reconstruct_rerank_top_k(rt, queries, codes, bits, norms, cb, rot, cid, k)
     wid, wsc = oracle.reconstruct_rerank(queries, rot, codes, bits, norms, cb, cid, k)
+    np.testing.assert_array_equal(ids, wid)
+    np.testing.assert_array_equal(sc, wsc)
+
+
+@pytest.mark.parametrize("bits,d", [(3, 256), (1, 384), (4, 130)])
+def test_reconstruct_rerank_inner_product_set(rt, bits, d):
+    """An inner-product code set (MSE codes + QJL signs + ResNorm + Norm, as
+    eoship_tq_ip_encode_device writes it) dequantized with the QJL term, then
+    the f32 index-order dots: ids and scores bit-exact vs the oracle."""
+    _case(f"reconstruct rerank inner-product set bits={bits} d={d}")
+    rng = np.random.default_rng(bits * 7 + d)
+    n, q, c, k = 3000, 6, 200, 50
+    rot = np.linalg.qr(rng.normal(size=(d, d)))[0].astype(np.float32)
+    S = rng.normal(size=(d, d)).astype(np.float32)
+    pts = np.sort(rng.normal(size=1 << bits))
+    cbi = np.clip(np.rint(pts / np.abs(pts).max() * 127), -127, 127).astype(np.int8)
+    s_c = float(np.float32(2.2 / np.sqrt(d) / 127))
+    x = rng.normal(size=(n, d)).astype(np.float32)
+    x[7] = x[8]
+    codes, signs, rn, nm = oracle.tq_encode_ip(x, rot, S, d, bits, cbi, s_c)
+    cb = (cbi.astype(np.float32) * np.float32(s_c)).astype(np.float32)
+    queries = rng.normal(size=(q, d)).astype(np.float32)
+    cid = _cands(rng, q, c, n)
+    cid[2, :2] = [8, 7]
+    ids, sc = reconstruct_rerank_top_k(rt, queries, codes, bits, nm, cb, rot, cid, k,
+                                       signs=signs, resnorms=rn, sketch=S)
+    wid, wsc = oracle.reconstruct_rerank(queries, rot, codes, bits, nm, cb, cid, k, signs=signs,
+                                         resnorms=rn, sketch=S)
     np.testing.assert_array_equal(ids, wid)
     np.testing.assert_array_equal(sc, wsc)
