@@ -751,33 +751,58 @@ def tiny_leg(rt, reps: int, cpu: bool = True) -> dict:
 
 
 def two_stage_leg(rt, steps: int, n: int) -> dict:
-    """Two-stage retrieval on the c2 corpus shape (the promoted serving profile
-    turboquant_ip_b4_overfetch200_fp16_rerank): TurboQuant top-200 over n x 384
-    4-bit vectors, then the f16 rerank of those 200 to the top 100 with the
-    rank-100 rescue. Document rows: seeded unit Gaussian f32 vectors converted
-    to f16 on the device at bind."""
+    """Two-stage retrieval on the c2 corpus shape as the promoted serving
+    profile turboquant_ip_b4_overfetch200_fp16_rerank runs it
+    (runtime/retrieval_turboquant.go:1500-1556): n x 384 unit Gaussian
+    documents encoded on the device into the inner-product layout at bit
+    width 4 (3-bit MSE codes + QJL sign bits + ResNorm + Norm, 200 B per
+    vector), the top 200 by the inner-product estimate, then the f16 rerank
+    of those 200 to the top 100 with the rank-100 rescue (gate fed bit width
+    4). f16 rows: the same documents, converted on the device at bind."""
     from eos_amd import datagen
     from eos_amd.runtime import DeviceBuffer
-    from eos_amd.turboquant import F16Sidecar, TurboQuantIndex, top_fp16_rerank_scores_device
+    from eos_amd.turboquant import F16Sidecar, IPQuantizer, top_fp16_rerank_scores_device
 
-    dim, bits, nq, k, over = 384, 4, 64, 100, 200
-    log("two-stage c2: generating corpus and f16 rows")
-    corpus = datagen.TurboQuantCorpus(n, dim, bits, 31, 32, 33)
+    dim, bit_width, nq, k, over = 384, 4, 64, 100, 200
+    mse_bits = bit_width - 1
+    log("two-stage c2: generating documents, IP b4 encode, f16 rows")
     rng = np.random.default_rng(35)
-    docs = rng.standard_normal((n, dim), dtype=np.float32)
-    docs /= np.linalg.norm(docs, axis=1, keepdims=True)
-    idx = TurboQuantIndex(rt, corpus.codes, corpus.norms, dim, bits, corpus.codebook,
-                          corpus.codebook_scale, corpus.rotation)
-    side = F16Sidecar(rt, docs)
-    del docs
+    rot = np.linalg.qr(rng.standard_normal((dim, dim)))[0].astype(np.float32)
+    sketch = rng.standard_normal((dim, dim)).astype(np.float32)
+    cb, s_c = datagen.turboquant_codebook(mse_bits, dim)
+    qz = IPQuantizer(rt, dim, mse_bits, cb, s_c, rot, sketch)
+    row_bytes, sign_bytes = qz.row_bytes, qz.sign_bytes
+    d_codes = DeviceBuffer(rt, n * row_bytes)
+    d_signs = DeviceBuffer(rt, n * sign_bytes)
+    d_rn = DeviceBuffer(rt, n * 4)
+    d_nm = DeviceBuffer(rt, n * 4)
+    side = F16Sidecar.allocate(rt, n, dim)
+    import ctypes as C
+    from eos_amd import _lib
+    chunk = 131072
+    for c0 in range(0, n, chunk):
+        m = min(chunk, n - c0)
+        x = rng.standard_normal((m, dim), dtype=np.float32)
+        x /= np.linalg.norm(x, axis=1, keepdims=True)
+        dx = DeviceBuffer.from_array(rt, x)
+        _lib.call("eoship_tq_ip_encode_device", rt.handle, C.byref(qz.spec), dx.ptr, C.c_int64(m),
+                  d_codes.view(c0 * row_bytes, m * row_bytes).ptr,
+                  d_signs.view(c0 * sign_bytes, m * sign_bytes).ptr,
+                  d_rn.view(c0 * 4, m * 4).ptr, d_nm.view(c0 * 4, m * 4).ptr)
+        side.fill_device(dx, c0, m)
+        rt.sync()
+        dx.free()
+    idx = qz.bind(d_codes, d_signs, d_rn, d_nm)
+    for b in (d_codes, d_signs, d_rn, d_nm):
+        b.free()
     q = datagen.baseline_queries(nq, dim, 34)
     dq = DeviceBuffer.from_array(rt, q)
     dcid, dcs = DeviceBuffer(rt, nq * over * 8), DeviceBuffer(rt, nq * over * 4)
     dids, dsc = DeviceBuffer(rt, nq * k * 8), DeviceBuffer(rt, nq * k * 4)
 
     def step():
-        idx.top_k_device(dq, nq, over, dcid, dcs, with_stats=False)
-        top_fp16_rerank_scores_device(side, dq, nq, dcid, dcs, over, k, bits, over, dids, dsc)
+        idx.top_k_device(dq, nq, over, dcid, dcs)
+        top_fp16_rerank_scores_device(side, dq, nq, dcid, dcs, over, k, bit_width, over, dids, dsc)
 
     for _ in range(3):
         step()
@@ -788,24 +813,48 @@ def two_stage_leg(rt, steps: int, n: int) -> dict:
     rt.mark(7)
     ms = rt.elapsed_ms(6, 7) / steps
     rt.profile_reset()
-    rt.profile_select("tq_fp16_rerank")
+    rt.profile_select(None)
     rt.profile(True)
     for _ in range(10):
         step()
     rt.sync()
+    kernels = {}
+    for name in ("tq_ip_prepare", "tq_ip_frag", "tq_ipscan_sample", "tq_ip_threshold",
+                 "tq_ipscan_filter", "tq_ip_finalize", "tq_ipscan_dense", "tq_ip_fallback_select",
+                 "tq_fp16_rerank_dots", "tq_fp16_rerank_sort"):
+        kernels[name] = rt.profile_read(name)[1] / 10
+    filt = rt.profile_samples("tq_ipscan_filter")
     n_rr, ms_rr = rt.profile_read("tq_fp16_rerank")
     rt.profile(False)
+    med = float(np.median(filt)) if len(filt) else 0.0
+    bytes_per_launch = n * (row_bytes + sign_bytes + 8)
+    # int8 ops of the scan: per (query, vector, dimension) a MAC in each of
+    # the four int8 passes (MSE grid high and low halves, QJL grid high and
+    # low halves against the sign bits).
+    ops = 2.0 * 4 * nq * n * dim
     avg = ms_rr / max(n_rr, 1)
     rr_bytes = nq * over * (dim * 2 + 12) + nq * dim * 4 + nq * k * 12
     out = {
-        "metric": "two-stage retrieval queries/s (TurboQuant top-200 + f16 rerank top-100)",
+        "metric": "two-stage retrieval queries/s (IP b4 top-200 + f16 rerank top-100)",
         "value": nq / (ms / 1e3),
         "unit": "queries/s",
         "ms_per_batch": ms,
         "vectors_scored_per_s": n * nq / (ms / 1e3),
-        "config": {"workload": "turboquant_two_stage_c2", "n": n, "dim": dim, "bits": bits,
-                   "queries": nq, "overfetch": over, "k": k,
-                   "profile": "turboquant_ip_b4_overfetch200_fp16_rerank"},
+        "config": {"workload": "turboquant_two_stage_c2", "n": n, "dim": dim,
+                   "bit_width": bit_width, "mse_bits": mse_bits, "queries": nq,
+                   "overfetch": over, "k": k,
+                   "profile": "turboquant_ip_b4_overfetch200_fp16_rerank",
+                   "bytes_per_vector": row_bytes + sign_bytes + 8},
+        "breakdown_ms": kernels,
+        "roofline": {"kernel": "tq_ipscan_filter", "median_launch_ms": med,
+                     "bytes_per_launch": bytes_per_launch,
+                     "hbm_gbs": bytes_per_launch / (med / 1e3) / 1e9 if med > 0 else None,
+                     "hbm_frac": bytes_per_launch / (med / 1e3) / 1e9 / HBM_PEAK_GBS if med > 0 else None,
+                     "int8_ops_per_launch": ops,
+                     "achieved": ops / (med / 1e3) / 1e12 if med > 0 else None,
+                     "peak": INT8_PEAK_TOPS, "unit": "TOP/s (int8)",
+                     "frac": ops / (med / 1e3) / 1e12 / INT8_PEAK_TOPS if med > 0 else None,
+                     "bound": "mfma"},
         "rerank": {"kernel": "tq_fp16_rerank", "bound": "latency", "avg_launch_ms": avg,
                    "launches": n_rr, "bytes_per_launch": rr_bytes,
                    "achieved_gbs": rr_bytes / (avg / 1e3) / 1e9 if avg > 0 else None},
@@ -814,6 +863,7 @@ def two_stage_leg(rt, steps: int, n: int) -> dict:
         b.free()
     side.buf.free()
     idx.release()
+    qz.release()
     return out
 
 def main() -> int:

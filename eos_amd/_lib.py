@@ -368,6 +368,12 @@ _SIGNATURES = {
     "eoship_tq_ip_encode_device": ([C.c_void_p, C.POINTER(EosHipTQIPSpec), C.c_void_p, C.c_int64,
                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p],
                                    C.c_int),
+    "eoship_tq_ip_bind_corpus": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                  C.c_void_p, C.c_int64, C.c_void_p, C.POINTER(C.c_void_p),
+                                  C.c_void_p], C.c_int),
+    "eoship_tq_ip_topk_device": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32,
+                                  C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),
+    "eoship_tq_ip_release": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_tq_ip_scores_device": ([C.c_void_p, C.POINTER(EosHipTQIPSpec), C.c_void_p, C.c_int32,
                                     C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64,
                                     C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p],

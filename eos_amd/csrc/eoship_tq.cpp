@@ -1692,8 +1692,8 @@ static int ip_spec_check(EosHipRuntime* rt, const EosHipTQIPSpec* spec, TqIpArgs
   if (rt == nullptr || spec == nullptr) return set_err(err, "%s: NULL argument", what);
   const int d = spec->dim, bits = spec->bits;
   if (d < 1 || d > 1024) return set_err(err, "%s: dim must be in [1, 1024]", what);
-  if (bits != 1 && bits != 2 && bits != 4)
-    return set_err(err, "%s: MSE bits must be 1, 2 or 4 (got %d)", what, bits);
+  if (bits != 1 && bits != 2 && bits != 3 && bits != 4)
+    return set_err(err, "%s: MSE bits must be 1, 2, 3 or 4 (got %d)", what, bits);
   if (spec->codebook == nullptr || spec->qjl_t == nullptr)
     return set_err(err, "%s: NULL codebook or QJL matrix", what);
   if (!(spec->codebook_scale > 0.f) || std::isinf(spec->codebook_scale))
@@ -1706,10 +1706,11 @@ static int ip_spec_check(EosHipRuntime* rt, const EosHipTQIPSpec* spec, TqIpArgs
     cmax = std::max(cmax, std::abs((int)spec->codebook[v]));
   }
   // The MSE query grid keeps |D_mse| < 2^31 as the flat scan's does; the QJL
-  // grid |D_qjl| <= d * qmax2 < 2^31.
+  // grid |D_qjl| <= d * qmax2 < 2^31, and both stay within the int8 high /
+  // low split (127 * 256 + 127) of the MFMA scan.
   const int64_t lim = cmax == 0 ? kQmaxLimit : (int64_t)2147483647 / ((int64_t)cmax * d) - 128;
   a->qmax = (int)std::min<int64_t>(kQmaxLimit, lim);
-  a->qmax2 = (int)std::min<int64_t>(32767, (int64_t)2147483647 / d - 1);
+  a->qmax2 = (int)std::min<int64_t>(kQmaxLimit, (int64_t)2147483647 / d - 1);
   if (a->qmax < 1) return set_err(err, "%s: codebook too wide for dim %d", what, d);
   a->rot_t = spec->rotation_t;
   a->qjl_t = spec->qjl_t;
@@ -1821,6 +1822,332 @@ int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int3
   return eoship::tq_fp16_rerank_launch(rt, d_queries, q, d, d_rows, n, d_cand_ids, d_cand_scores,
                                        c, k, bit_width, overfetch, d_id_rank, d_ids, d_scores,
                                        static_cast<float*>(ws), what, err);
+}
+
+}  // extern "C"
+
+// ---------------------------------------- inner-product first stage (top-k)
+//
+// The promoted serving profile's first stage (turboquant_ip_b4_overfetch200_
+// fp16_rerank, runtime/retrieval_turboquant.go:1500-1556): the top-k of the
+// inner-product estimate over IPQuantized documents, as
+// topTurboQuantRetrievalScoresWithStats computes it with InnerProductPrepared
+// (:1853-1887). Per batch of <= 64 queries (32 when the dimension needs more
+// than 12 K-steps): eos_tq_ip_prepare (int grids of R q and S R q),
+// eos_tq_ip_frag (MFMA fragments), a sample scan of tile maxima and
+// eos_tq_threshold, the filter scan (exact scores, keep >= tau),
+// eos_tq_finalize, and the exact fallback gated on its flags (dense scan +
+// eos_tq_row_select).
+struct EosHipTQIP {
+  EosHipRuntime* rt = nullptr;
+  int d = 0, bits = 0, ks = 0, nqg = 0, qmax = 0, qmax2 = 0;
+  int64_t n = 0, ntiles = 0;
+  float cb_scale = 0.f;
+  int cb[16] = {0};
+  uint32_t lut0 = 0, lut1 = 0;
+  const float* rot_t = nullptr;  // caller's device matrices
+  const float* qjl_t = nullptr;
+  int32_t* packed = nullptr;
+  float* norms = nullptr;
+  float* resnorms = nullptr;
+  // per-batch scratch
+  int* qs = nullptr;
+  int* ys = nullptr;
+  float* alpha = nullptr;
+  float* beta = nullptr;
+  int* ysum = nullptr;
+  int8_t* bfrag = nullptr;
+  float* tau = nullptr;
+  unsigned long long* cand = nullptr;
+  uint32_t* cand_count = nullptr;
+  int* status = nullptr;
+  float* samp = nullptr;
+  float* dense = nullptr;
+  size_t dense_bytes = 0;
+
+  int batch_cap() const { return 32 * nqg; }
+
+  ~EosHipTQIP() {
+    void* p[] = {packed, norms, resnorms, qs, ys, alpha, beta, ysum, bfrag, tau, cand, cand_count,
+                 status, samp, dense};
+    for (void* x : p)
+      if (x) (void)hipFree(x);
+  }
+
+  int scan(int mode, int qb, int64_t tile_begin, int64_t tile_step, int64_t ntl, float* out,
+           int64_t out_stride, const int* gate, char** err) {
+    if (ntl <= 0) return 0;
+    TqIpScanArgs s;
+    memset(&s, 0, sizeof(s));
+    s.packed = packed;
+    s.norms = norms;
+    s.resnorms = resnorms;
+    s.bfrag = bfrag;
+    s.alpha = alpha;
+    s.beta = beta;
+    s.ysum = ysum;
+    s.tau = tau;
+    s.cand = cand;
+    s.cand_count = cand_count;
+    s.out_scores = out;
+    s.gate = gate;
+    s.n = n;
+    s.out_begin = 0;
+    s.out_count = n;
+    s.out_stride = out_stride;
+    s.tile_begin = tile_begin;
+    s.tile_step = tile_step;
+    s.ntiles = (int)ntl;
+    s.q = qb;
+    s.cap = kCap;
+    s.mode = mode;
+    s.lut0 = lut0;
+    s.lut1 = lut1;
+    char name[48];
+    snprintf(name, sizeof(name), "eos_tq_ipscan_k%d_g%d", ks, nqg);
+    static const char* const labels[3] = {"tq_ipscan_dense", "tq_ipscan_filter", "tq_ipscan_sample"};
+    int64_t blocks = (ntl + 7) / 8;
+    if (blocks > rt->compute_units) blocks = rt->compute_units;
+    if (blocks < 1) blocks = 1;
+    return rt->launch(name, dim3((unsigned)blocks), dim3(512), 0, &s, err, labels[mode]);
+  }
+
+  int prepare(const float* d_queries, int qb, char** err) {
+    TqIpArgs a;
+    memset(&a, 0, sizeof(a));
+    a.queries = d_queries;
+    a.rot_t = rot_t;
+    a.qjl_t = qjl_t;
+    a.qs = qs;
+    a.ys = ys;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.d = d;
+    a.q = qb;
+    a.qmax = qmax;
+    a.qmax2 = qmax2;
+    a.cb_scale = cb_scale;
+    if (rt->launch("eos_tq_ip_prepare", dim3((unsigned)qb), dim3(256), 0, &a, err,
+                   "tq_ip_prepare") != 0)
+      return 1;
+    TqIpFragArgs f;
+    memset(&f, 0, sizeof(f));
+    f.qs = qs;
+    f.ys = ys;
+    f.bfrag = bfrag;
+    f.ysum = ysum;
+    f.tau = tau;
+    f.cand_count = cand_count;
+    f.q = qb;
+    f.d = d;
+    f.ks = ks;
+    f.nqg = nqg;
+    return rt->launch("eos_tq_ip_frag", dim3((unsigned)(32 * nqg)), dim3(256), 0, &f, err,
+                      "tq_ip_frag");
+  }
+
+  int topk_batch(const float* d_queries, int qb, int kk, int64_t* d_ids, float* d_scores,
+                 char** err) {
+    if (prepare(d_queries, qb, err) != 0) return 1;
+    if (n > kCap) {
+      const int64_t stride =
+          std::max<int64_t>(kSampleStride, (ntiles + kMaxSampleTiles - 1) / kMaxSampleTiles);
+      const int64_t ns = (ntiles + stride - 1) / stride;
+      int64_t nsv = 0;
+      for (int64_t j = 0; j < ns; ++j) nsv += std::min<int64_t>(kTile, n - j * stride * kTile);
+      const double target = std::min<double>(kKeepFactor * kk, kCap / 4.0);
+      int64_t r = (int64_t)std::ceil(target * (double)nsv / (double)n);
+      r = std::max<int64_t>(1, std::min<int64_t>(r, ns));
+      if (scan(2, qb, 0, stride, ns, samp, ns, nullptr, err) != 0) return 1;
+      TqSelectArgs sel;
+      memset(&sel, 0, sizeof(sel));
+      sel.rows = samp;
+      sel.tau = tau;
+      sel.n = ns;
+      sel.stride = ns;
+      sel.kk = (int)r;
+      sel.nrows = qb;
+      if (rt->launch("eos_tq_threshold", dim3(qb), dim3(256), 0, &sel, err, "tq_ip_threshold") != 0)
+        return 1;
+    }
+    if (scan(1, qb, 0, 1, ntiles, nullptr, 0, nullptr, err) != 0) return 1;
+    TqFinalizeArgs f;
+    memset(&f, 0, sizeof(f));
+    f.cand = cand;
+    f.cand_count = cand_count;
+    f.ids = reinterpret_cast<long long*>(d_ids);
+    f.scores = d_scores;
+    f.status = status;
+    f.cap = kCap;
+    f.kk = kk;
+    f.q = qb;
+    if (rt->launch("eos_tq_finalize", dim3(qb), dim3(256), 0, &f, err, "tq_ip_finalize") != 0)
+      return 1;
+    // Exact fallback, gated on the device by the finalize flags.
+    const size_t need = (size_t)qb * (size_t)n * sizeof(float);
+    if (dense_bytes < need) {
+      if (dense != nullptr) {
+        if (rt->sync(err) != 0) return 1;
+        (void)hipFree(dense);
+      }
+      dense = nullptr;
+      dense_bytes = 0;
+      if (rt->alloc(need, reinterpret_cast<void**>(&dense), err) != 0) return 1;
+      dense_bytes = need;
+    }
+    if (scan(0, qb, 0, 1, ntiles, dense, n, status, err) != 0) return 1;
+    TqSelectArgs sel;
+    memset(&sel, 0, sizeof(sel));
+    sel.rows = dense;
+    sel.status = status;
+    sel.ids = reinterpret_cast<long long*>(d_ids);
+    sel.scores = d_scores;
+    sel.n = n;
+    sel.stride = n;
+    sel.kk = kk;
+    sel.mode = 1;
+    sel.nrows = qb;
+    return rt->launch("eos_tq_row_select", dim3(qb), dim3(1024), 0, &sel, err,
+                      "tq_ip_fallback_select");
+  }
+};
+
+extern "C" {
+
+int eoship_tq_ip_bind_corpus(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
+                             const uint8_t* d_codes, const uint8_t* d_signs,
+                             const float* d_resnorms, const float* d_norms, int64_t n,
+                             const EosHipTQBindOptions* opts, EosHipTQIP** out, char** err) {
+  const char* what = "eoship_tq_ip_bind_corpus";
+  if (out == nullptr) return set_err(err, "%s: NULL output", what);
+  *out = nullptr;
+  TqIpArgs a;
+  if (ip_spec_check(rt, spec, &a, what, err) != 0) return 1;
+  if (spec->bits > 3)
+    return set_err(err, "%s: the scan takes MSE codes of 1, 2 or 3 bits (bit widths 2..4; got %d)",
+                   what, spec->bits);
+  if (n < 1 || n >= ((int64_t)1 << 31) - 64)
+    return set_err(err, "%s: n must be in [1, 2^31 - 64)", what);
+  if (!d_codes || !d_signs || !d_resnorms || !d_norms) return set_err(err, "%s: NULL buffer", what);
+  if (opts != nullptr && opts->id_rank != nullptr)
+    return set_err(err, "%s: id_rank is not supported for the inner-product layout", what);
+  int ks = 0;
+  for (int k : {4, 8, 12, 16, 24, 32})
+    if (ks == 0 && k * 32 >= spec->dim) ks = k;
+  // Norm policy of validateEosQuantizedVectorNorm (runtime/
+  // turboquant_quantized_vector.go:25-49), as the MSE bind applies it.
+  {
+    std::vector<float> hn((size_t)n);
+    hipError_t e = hipMemcpy(hn.data(), d_norms, (size_t)n * 4, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_err(err, "hipMemcpy(norms)", e);
+    for (int64_t i = 0; i < n; ++i) {
+      const float v = hn[(size_t)i];
+      if (!(v >= 0.f) || std::isinf(v))
+        return set_err(err, "%s: vector %lld has an invalid norm %g", what, (long long)i, (double)v);
+      if (v == 0.f && (opts == nullptr || opts->zero_vector_allowed == nullptr ||
+                       opts->zero_vector_allowed[i] == 0))
+        return set_err(err, "%s: vector %lld has Norm 0 and is not marked as a zero vector", what,
+                       (long long)i);
+    }
+  }
+  auto* ip = new EosHipTQIP();
+  ip->rt = rt;
+  ip->d = spec->dim;
+  ip->bits = spec->bits;
+  ip->ks = ks;
+  ip->nqg = ks <= 12 ? 2 : 1;
+  ip->qmax = a.qmax;
+  ip->qmax2 = a.qmax2;
+  ip->n = n;
+  ip->ntiles = (n + kTile - 1) / kTile;
+  ip->cb_scale = spec->codebook_scale;
+  ip->rot_t = spec->rotation_t;
+  ip->qjl_t = spec->qjl_t;
+  uint8_t t8[8] = {0};
+  for (int v = 0; v < (1 << spec->bits); ++v) {
+    ip->cb[v] = spec->codebook[v];
+    t8[v] = (uint8_t)spec->codebook[v];
+  }
+  ip->lut0 = t8[0] | (t8[1] << 8) | (t8[2] << 16) | ((uint32_t)t8[3] << 24);
+  ip->lut1 = t8[4] | (t8[5] << 8) | (t8[6] << 16) | ((uint32_t)t8[7] << 24);
+  const int cols = 32 * ip->nqg;
+  const int64_t samp_tiles =
+      std::min<int64_t>((ip->ntiles + kSampleStride - 1) / kSampleStride, kMaxSampleTiles);
+  auto fail = [&]() {
+    delete ip;
+    return 1;
+  };
+  if (rt->alloc((size_t)ip->ntiles * (ks / 2) * 64 * 16, reinterpret_cast<void**>(&ip->packed), err) ||
+      rt->alloc((size_t)ip->ntiles * kTile * 4, reinterpret_cast<void**>(&ip->norms), err) ||
+      rt->alloc((size_t)ip->ntiles * kTile * 4, reinterpret_cast<void**>(&ip->resnorms), err) ||
+      rt->alloc((size_t)cols * ip->d * 4, reinterpret_cast<void**>(&ip->qs), err) ||
+      rt->alloc((size_t)cols * ip->d * 4, reinterpret_cast<void**>(&ip->ys), err) ||
+      rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->alpha), err) ||
+      rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->beta), err) ||
+      rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->ysum), err) ||
+      rt->alloc((size_t)ks * 4 * ip->nqg * 64 * 16, reinterpret_cast<void**>(&ip->bfrag), err) ||
+      rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->tau), err) ||
+      rt->alloc((size_t)cols * kCap * 8, reinterpret_cast<void**>(&ip->cand), err) ||
+      rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->cand_count), err) ||
+      rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->status), err) ||
+      rt->alloc((size_t)cols * std::max<int64_t>(samp_tiles, 1) * 4,
+                reinterpret_cast<void**>(&ip->samp), err))
+    return fail();
+  TqIpPackArgs p;
+  memset(&p, 0, sizeof(p));
+  p.codes = d_codes;
+  p.signs = d_signs;
+  p.norms = d_norms;
+  p.resnorms = d_resnorms;
+  p.packed = ip->packed;
+  p.norms_out = ip->norms;
+  p.resnorms_out = ip->resnorms;
+  p.n = n;
+  p.ntiles = ip->ntiles;
+  p.d = ip->d;
+  p.ks = ks;
+  p.bits = ip->bits;
+  p.row_bytes = a.row_bytes;
+  p.sign_bytes = a.sign_bytes;
+  const int64_t threads = ip->ntiles * (ks / 2) * 64;
+  if (rt->launch("eos_tq_ip_pack", dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, &p, err,
+                 "tq_ip_pack") != 0 ||
+      rt->sync(err) != 0)
+    return fail();
+  *out = ip;
+  return 0;
+}
+
+int eoship_tq_ip_topk_device(EosHipRuntime* rt, EosHipTQIP* ip, const float* d_queries,
+                             int32_t q, int32_t k, int64_t* d_ids, float* d_scores, char** err) {
+  const char* what = "eoship_tq_ip_topk_device";
+  if (rt == nullptr || ip == nullptr) return set_err(err, "%s: NULL runtime or corpus", what);
+  if (ip->rt != rt) return set_err(err, "%s: corpus was bound on another runtime", what);
+  if (q < 0) return set_err(err, "%s: negative query count", what);
+  const int64_t kk64 = (k <= 0 || (int64_t)k > ip->n) ? ip->n : k;
+  if (q == 0) return 0;
+  if (kk64 > kSortCap)
+    return set_err(err, "%s: k=%lld exceeds the device top-k limit of %d", what, (long long)kk64,
+                   kSortCap);
+  if (d_queries == nullptr || d_ids == nullptr || d_scores == nullptr)
+    return set_err(err, "%s: NULL buffer", what);
+  const int kk = (int)kk64;
+  const int cap = ip->batch_cap();
+  for (int q0 = 0; q0 < q; q0 += cap) {
+    const int qb = std::min(cap, q - q0);
+    if (ip->topk_batch(d_queries + (size_t)q0 * ip->d, qb, kk, d_ids + (size_t)q0 * kk,
+                       d_scores + (size_t)q0 * kk, err) != 0)
+      return 1;
+  }
+  return 0;
+}
+
+int eoship_tq_ip_release(EosHipTQIP* ip, char** err) {
+  (void)err;
+  if (ip == nullptr) return 0;
+  (void)hipStreamSynchronize(ip->rt->stream);
+  delete ip;
+  return 0;
 }
 
 }  // extern "C"

@@ -246,4 +246,61 @@ struct TqReconArgs {
   int d, c, bits, row_bytes;
 };
 
+
+// Inner-product corpus (IPQuantized rows: MSE codes of 1..3 bits + QJL sign
+// bits + ResNorm + Norm) in the scan's tile layout: tile t, chunk c (K-steps
+// 2c and 2c + 1), lane (m + 32 g): two dwords per K-step s,
+//   L:  bit 8 b + 2 k + e = bit e of the code of fragment byte 4 k + b (e = 0, 1)
+//   HS: bit 8 b + k = bit 2 of that code; bit 8 b + 4 + k = its QJL sign bit
+// where fragment byte i of K-step s, lane group g is dimension 32 s + 16 g + i
+// of vector 32 t + m (dimensions past d, and vectors past n: code 0, sign 0).
+struct TqIpPackArgs {
+  const uint8_t* codes;    // [n][row_bytes] reference layout, low bits first
+  const uint8_t* signs;    // [n][sign_bytes]
+  const float* norms;      // [n]
+  const float* resnorms;   // [n]
+  int32_t* packed;         // [ntiles][ks / 2][64][4] dwords
+  float* norms_out;        // [ntiles * 32], zero past n
+  float* resnorms_out;     // [ntiles * 32]
+  long long n, ntiles;
+  int d, ks, bits, row_bytes, sign_bytes;
+};
+
+// Query fragments of the inner-product scan from the int grids of
+// eos_tq_ip_prepare: per K-step and 32-column group g, blocks 4 g + 0 / + 1
+// (MSE grid Qs = 256 hi + lo) and 4 g + 2 / + 3 (QJL grid Ys likewise); the
+// sum of Ys over the dimensions (D_qjl = 2 sum_{bit = 1} Ys - sum Ys); the
+// filter state of each column reset (tau = -inf, no kept candidates).
+struct TqIpFragArgs {
+  const int* qs;           // [q][d]
+  const int* ys;           // [q][d]
+  int8_t* bfrag;           // [ks][4 * nqg][64][16]
+  int* ysum;               // [32 * nqg]
+  float* tau;              // [32 * nqg]
+  uint32_t* cand_count;    // [32 * nqg]
+  int q, d, ks, nqg;
+};
+
+// Inner-product scan: exact D_mse = sum Qs_j C[code_j] and D_qjl = sum Ys_i
+// (2 bit_i - 1) on int8 MFMA, score = ((float)D_mse alpha + ResNorm
+// ((float)D_qjl beta)) Norm; modes as TqScanArgs (0 dense, 1 keep score >=
+// tau, 2 sampled tile maxima).
+struct TqIpScanArgs {
+  const int32_t* packed;
+  const float* norms;      // [ntiles * 32]
+  const float* resnorms;   // [ntiles * 32]
+  const int8_t* bfrag;     // [ks][4 * nqg][64][16]
+  const float* alpha;      // [32 * nqg]
+  const float* beta;       // [32 * nqg]
+  const int* ysum;         // [32 * nqg]
+  const float* tau;        // [32 * nqg]
+  unsigned long long* cand;  // [32 * nqg][cap]
+  uint32_t* cand_count;    // [32 * nqg]
+  float* out_scores;
+  const int* gate;
+  long long n, out_begin, out_count, out_stride, tile_begin, tile_step;
+  int ntiles, q, cap, mode;
+  uint32_t lut0, lut1;     // the 8-entry int8 codebook: bytes C[0..3], C[4..7]
+};
+
 #endif  // EOSHIP_TQ_ARGS_H

@@ -540,13 +540,14 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_encode_ip(TqIpArgs a) {
     for (int v = 0; v < kIpV; ++v) sb[v * kIpDMax + i] = p[v] >= 0.0 ? 1 : 0;
   }
   __syncthreads();
-  const int per = 8 / a.bits;
+  // Codes packed low bits first: bit t of a row is bit t % bits of code
+  // t / bits (a 3-bit code straddles two bytes where t crosses one).
   for (int i = tid; i < nv * a.row_bytes; i += 256) {
     const int v = i / a.row_bytes, b = i - v * a.row_bytes;
     uint32_t byte = 0;
-    for (int e = 0; e < per; ++e) {
-      const int j = b * per + e;
-      if (j < d) byte |= (uint32_t)cs[v * kIpDMax + j] << (e * a.bits);
+    for (int e = 0; e < 8; ++e) {
+      const int t = 8 * b + e, j = t / a.bits;
+      if (j < d) byte |= (((uint32_t)cs[v * kIpDMax + j] >> (t - j * a.bits)) & 1u) << e;
     }
     a.codes[(size_t)(v0 + v) * a.row_bytes + b] = (uint8_t)byte;
   }
@@ -648,8 +649,10 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_scores(TqIpArgs a) {
   const uint8_t* row = a.codes + (size_t)v * a.row_bytes;
   const int mask = (1 << a.bits) - 1;
   for (int j = 0; j < d; ++j) {
-    const int bit = j * a.bits;
-    const int c = a.cb[(row[bit >> 3] >> (bit & 7)) & mask];
+    const int bit = j * a.bits, sh = bit & 7;
+    unsigned cv = (unsigned)row[bit >> 3] >> sh;
+    if (sh + a.bits > 8) cv |= (unsigned)row[(bit >> 3) + 1] << (8 - sh);
+    const int c = a.cb[cv & (unsigned)mask];
 #pragma unroll
     for (int g = 0; g < kIpQ; ++g) dm[g] += qs[j * kIpQ + g] * c;
   }
@@ -1141,6 +1144,325 @@ EOS_TQ_SCAN_KS(2, 1)
 EOS_TQ_SCAN_KS(2, 2)
 EOS_TQ_SCAN(4, 32, 1)
 EOS_TQ_SCAN(2, 32, 1)
+
+// ---------------------------------------------------- inner-product scan
+
+// Repacks an inner-product corpus into the scan's tile layout (TqIpPackArgs):
+// one thread per (tile, chunk, lane), 16 bytes each; thread 0 .. 31 of a tile's
+// chunk 0 also copy the tile's norms and ResNorms (zero past n).
+extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_pack(TqIpPackArgs a) {
+  const int nl = a.ks / 2;
+  const long long o = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (o >= a.ntiles * nl * 64) return;
+  const int lane = (int)(o & 63);
+  const long long tc = o >> 6;
+  const int c = (int)(tc % nl);
+  const long long t = tc / nl;
+  const int m = lane & 31, g = lane >> 5;
+  const long long v = t * 32 + m;
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  if (v < a.n) {
+    const uint8_t* row = a.codes + (size_t)v * a.row_bytes;
+    const uint8_t* sg = a.signs + (size_t)v * a.sign_bytes;
+    for (int h = 0; h < 2; ++h) {
+      const int s = 2 * c + h;
+      uint32_t L = 0u, HS = 0u;
+      for (int i = 0; i < 16; ++i) {
+        const int j = 32 * s + 16 * g + i;
+        if (j >= a.d) break;
+        const int bit = j * a.bits, sh = bit & 7;
+        uint32_t code = (uint32_t)row[bit >> 3] >> sh;
+        if (sh + a.bits > 8) code |= (uint32_t)row[(bit >> 3) + 1] << (8 - sh);
+        code &= (1u << a.bits) - 1u;
+        const uint32_t sign = (sg[j >> 3] >> (j & 7)) & 1u;
+        const int k = i >> 2, b = i & 3;
+        L |= (code & 3u) << (8 * b + 2 * k);
+        HS |= ((code >> 2) & 1u) << (8 * b + k);
+        HS |= sign << (8 * b + 4 + k);
+      }
+      w[2 * h] = L;
+      w[2 * h + 1] = HS;
+    }
+  }
+  int32_t* dst = a.packed + (size_t)o * 4;
+  *reinterpret_cast<v4i*>(dst) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  if (c == 0 && g == 0) {
+    a.norms_out[v] = v < a.n ? a.norms[v] : 0.0f;
+    a.resnorms_out[v] = v < a.n ? a.resnorms[v] : 0.0f;
+  }
+}
+
+// Query fragments of the inner-product scan (TqIpFragArgs), one workgroup per
+// query column c (zero columns past q): Qs and Ys split as 256 hi + lo with
+// int8 halves, their sum of Ys, and the column's filter state reset.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_frag(TqIpFragArgs a) {
+  __shared__ int red[4];
+  const int c = blockIdx.x, tid = threadIdx.x;
+  const int gq = c >> 5, col = c & 31, ncb = 4 * a.nqg;
+  const bool live = c < a.q;
+  int ysum = 0;
+  for (int j = tid; j < a.ks * 32; j += 256) {
+    const int qv = (live && j < a.d) ? a.qs[(size_t)c * a.d + j] : 0;
+    const int yv = (live && j < a.d) ? a.ys[(size_t)c * a.d + j] : 0;
+    ysum += yv;
+    const int qlo = ((qv + 128) & 255) - 128, qhi = (qv - qlo) >> 8;
+    const int ylo = ((yv + 128) & 255) - 128, yhi = (yv - ylo) >> 8;
+    const int s = j >> 5, g = (j >> 4) & 1, i = j & 15;
+    const int lane = col + 32 * g;
+    int8_t* base = a.bfrag + ((size_t)(s * ncb + 4 * gq) * 64 + lane) * 16 + i;
+    base[0] = (int8_t)qhi;
+    base[64 * 16] = (int8_t)qlo;
+    base[2 * 64 * 16] = (int8_t)yhi;
+    base[3 * 64 * 16] = (int8_t)ylo;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ysum += __shfl_xor(ysum, o);
+  if ((tid & 63) == 0) red[tid >> 6] = ysum;
+  __syncthreads();
+  if (tid == 0) {
+    a.ysum[c] = red[0] + red[1] + red[2] + red[3];
+    a.tau[c] = -__builtin_inff();
+    a.cand_count[c] = 0u;
+  }
+}
+
+namespace {
+
+// 8-entry int8 lookup of the 3-bit codes and 0/1 bytes of the sign bits of
+// one K-step (dwords L, HS of the tile layout): af = C[code] per fragment
+// byte, sf = the sign bits as bytes.
+EOS_DEV void ip_decode(uint32_t L, uint32_t HS, uint32_t lut0, uint32_t lut1, v4i& af, v4i& sf) {
+  const uint32_t m2 = 0x03030303u, m1 = 0x01010101u;
+  const uint32_t c0 = (L & m2) | ((HS & m1) << 2);
+  const uint32_t c1 = ((L >> 2) & m2) | (((HS >> 1) & m1) << 2);
+  const uint32_t c2 = ((L >> 4) & m2) | (((HS >> 2) & m1) << 2);
+  const uint32_t c3 = ((L >> 6) & m2) | (((HS >> 3) & m1) << 2);
+  af.x = (int)__builtin_amdgcn_perm(lut1, lut0, c0);
+  af.y = (int)__builtin_amdgcn_perm(lut1, lut0, c1);
+  af.z = (int)__builtin_amdgcn_perm(lut1, lut0, c2);
+  af.w = (int)__builtin_amdgcn_perm(lut1, lut0, c3);
+  sf.x = (int)((HS >> 4) & m1);
+  sf.y = (int)((HS >> 5) & m1);
+  sf.z = (int)((HS >> 6) & m1);
+  sf.w = (int)((HS >> 7) & m1);
+}
+
+template <int KS, int NQG>
+EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
+  constexpr int NCB = 4 * NQG, NQ = 32 * NQG, NTH = 512, NWV = NTH / 64, NLOAD = KS / 2;
+  constexpr bool FILTER_OK = true;
+  (void)FILTER_OK;
+  __shared__ v4i sb[KS * NCB * 64];
+  __shared__ uint32_t lc_cnt[NQ];
+  __shared__ u64 lc_buf[NQ * kLdsSlots];
+  __shared__ float4 nstage[NWV][16];
+  __shared__ int tile_next;
+  if (a.gate != nullptr) {
+    bool any = false;
+    for (int i = 0; i < a.q; ++i) any |= a.gate[i] != 0;
+    if (!any) return;
+  }
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = lane >> 5;
+  const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
+  const bool filter = a.mode == 1;
+  float al_r[NQG], be_r[NQG], ta_r[NQG];
+  int ys_r[NQG];
+  bool live_r[NQG];
+#pragma unroll
+  for (int g = 0; g < NQG; ++g) {
+    const int qi = g * 32 + (lane & 31);
+    live_r[g] = qi < a.q;
+    al_r[g] = live_r[g] ? a.alpha[qi] : 0.0f;
+    be_r[g] = live_r[g] ? a.beta[qi] : 0.0f;
+    ys_r[g] = live_r[g] ? a.ysum[qi] : 0;
+    ta_r[g] = (filter && live_r[g]) ? a.tau[qi] : __builtin_inff();
+  }
+  struct Stage {
+    v4i raw[NLOAD];
+    float nv;  // lanes 0-31: the tile's Norms; lanes 32-63: its ResNorms
+    int t;
+  };
+  auto load_stage = [&](Stage& st, int jj) {
+    const long long t = a.tile_begin + (long long)jj * a.tile_step;
+    const v4i* src = packed + (size_t)t * NLOAD * 64 + lane;
+#pragma unroll
+    for (int c = 0; c < NLOAD; ++c) st.raw[c] = __builtin_nontemporal_load(src + c * 64);
+    st.nv = lane < 32 ? a.norms[t * kTile + lane] : a.resnorms[t * kTile + (lane & 31)];
+  };
+  auto process = [&](const Stage& st, int j) {
+    const long long tile = a.tile_begin + (long long)j * a.tile_step;
+    int boff = lane;
+    asm volatile("" : "+v"(boff));
+    v16i acc[NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
+#pragma unroll
+    for (int c = 0; c < NLOAD; ++c) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int s = 2 * c + h;
+        v4i af, sf;
+        ip_decode((uint32_t)(h == 0 ? st.raw[c].x : st.raw[c].z),
+                  (uint32_t)(h == 0 ? st.raw[c].y : st.raw[c].w), a.lut0, a.lut1, af, sf);
+#pragma unroll
+        for (int g = 0; g < NQG; ++g) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const v4i bf = sb[(s * NCB + 4 * g + u) * 64 + boff];
+            acc[4 * g + u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(u < 2 ? af : sf, bf,
+                                                                  acc[4 * g + u], 0, 0, 0);
+          }
+        }
+      }
+    }
+    // Epilogue: accumulator element i of lane l is row 8 (i / 4) + 4 (l / 32)
+    // + i % 4 of the tile and query column l % 32 of the group.
+    const long long vbase = tile * kTile;
+    const long long rem64 = a.n - vbase;
+    const int rem = rem64 >= kTile ? kTile : (int)rem64;
+    // The tile's Norms and ResNorms go to the wave's LDS slot; each group of
+    // four rows reads its values there (no per-row registers held across the
+    // epilogue). LDS operations of one wave complete in order.
+    reinterpret_cast<float*>(nstage[wave])[lane] = st.nv;
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int g = 0; g < NQG; ++g) {
+      if (!live_r[g]) continue;
+      const int qi = g * 32 + (lane & 31);
+      float smax = -__builtin_inff();
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const float4 n4 = nstage[wave][2 * i4 + half];
+        const float4 r4 = nstage[wave][8 + 2 * i4 + half];
+        const float nv4[4] = {n4.x, n4.y, n4.z, n4.w};
+        const float rv4[4] = {r4.x, r4.y, r4.z, r4.w};
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * i4 + e;
+          const int dm = acc[4 * g][i] * 256 + acc[4 * g + 1][i];
+          const int dq = 2 * (acc[4 * g + 2][i] * 256 + acc[4 * g + 3][i]) - ys_r[g];
+          const float t1 = (float)dm * al_r[g];
+          const float t2 = (float)dq * be_r[g];
+          const float t3 = rv4[e] * t2;
+          sc[e] = (t1 + t3) * nv4[e];
+        }
+        const int r0 = 8 * i4 + 4 * half;  // rows r0 .. r0 + 3
+        if (a.mode == 1) {
+          const float ta = ta_r[g];
+          uint32_t cnt = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cnt += (r0 + e < rem && sc[e] >= ta) ? 1u : 0u;
+          if (cnt != 0u) {
+            uint32_t pos = atomicAdd(&lc_cnt[qi], cnt);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (r0 + e < rem && sc[e] >= ta) {
+                const u64 key = rank_key(sc[e], (uint32_t)(vbase + r0 + e));
+                if (pos < (uint32_t)kLdsSlots) {
+                  lc_buf[qi * kLdsSlots + pos] = key;
+                } else {
+                  const uint32_t gpos = atomicAdd(&a.cand_count[qi], 1u);
+                  if ((int)gpos < a.cap) a.cand[(size_t)qi * a.cap + gpos] = key;
+                }
+                ++pos;
+              }
+            }
+          }
+        } else if (a.mode == 0) {
+          float* orow = a.out_scores + (size_t)qi * a.out_stride;
+          const long long c0 = vbase - a.out_begin;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const long long colx = c0 + r0 + e;
+            if (r0 + e < rem && colx >= 0 && colx < a.out_count) orow[colx] = sc[e];
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (r0 + e < rem) smax = fmaxf(smax, sc[e]);
+        }
+      }
+      if (a.mode == 2) {
+        smax = fmaxf(smax, __shfl_xor(smax, 32));
+        if (half == 0) a.out_scores[(size_t)qi * a.out_stride + j] = smax;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+  const int nt = a.ntiles;
+  const int rb = (int)((long long)blockIdx.x * nt / gridDim.x);
+  const int re = (int)((long long)(blockIdx.x + 1) * nt / gridDim.x);
+  auto cl = [&](int jj) { return jj < re ? jj : re - 1; };
+  auto claim = [&]() {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&tile_next, 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+  constexpr int R = 2;
+  Stage st[R];
+  {
+    constexpr int FCOUNT = KS * NCB * 64;
+    constexpr int FPER = (FCOUNT + NTH - 1) / NTH;
+    const v4i* fsrc = reinterpret_cast<const v4i*>(a.bfrag);
+    v4i fv[FPER];
+#pragma unroll
+    for (int r = 0; r < FPER; ++r) {
+      const int i = threadIdx.x + r * NTH;
+      if (i < FCOUNT) fv[r] = fsrc[i];
+    }
+    st[0].t = rb + wave;
+    load_stage(st[0], cl(st[0].t));
+#pragma unroll
+    for (int r = 0; r < FPER; ++r) {
+      const int i = threadIdx.x + r * NTH;
+      if (i < FCOUNT) sb[i] = fv[r];
+    }
+  }
+  if (threadIdx.x < NQ) lc_cnt[threadIdx.x] = 0u;
+  if (threadIdx.x == 0) tile_next = rb + NWV;
+  __syncthreads();
+  if (st[0].t < re) {
+    do {
+#pragma unroll
+      for (int p = 0; p < R; ++p) {
+        Stage& nx = st[(p + R - 1) % R];
+        nx.t = claim();
+        load_stage(nx, cl(nx.t));
+        if (st[p].t < re) process(st[p], st[p].t);
+      }
+    } while (st[0].t < re);
+  }
+  if (a.mode == 1) {
+    __syncthreads();
+    if (threadIdx.x < NQ && threadIdx.x < a.q) {
+      const int qi = threadIdx.x;
+      const uint32_t nk = lc_cnt[qi] < (uint32_t)kLdsSlots ? lc_cnt[qi] : (uint32_t)kLdsSlots;
+      if (nk > 0) {
+        const uint32_t base = atomicAdd(&a.cand_count[qi], nk);
+        for (uint32_t i = 0; i < nk; ++i)
+          if ((int)(base + i) < a.cap) a.cand[(size_t)qi * a.cap + base + i] = lc_buf[qi * kLdsSlots + i];
+      }
+    }
+  }
+}
+
+}  // namespace
+
+#define EOS_TQ_IPSCAN(KS, NQG)                                                            \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) \
+  void eos_tq_ipscan_k##KS##_g##NQG(TqIpScanArgs a) {                                     \
+    tq_ipscan_body<KS, NQG>(a);                                                           \
+  }
+EOS_TQ_IPSCAN(4, 2)
+EOS_TQ_IPSCAN(8, 2)
+EOS_TQ_IPSCAN(12, 2)
+EOS_TQ_IPSCAN(16, 1)
+EOS_TQ_IPSCAN(24, 1)
+EOS_TQ_IPSCAN(32, 1)
+#undef EOS_TQ_IPSCAN
 
 // ----------------------------------------------------------------- rescore
 

@@ -108,27 +108,24 @@ def turboquant_codebook(bits: int, dim: int) -> tuple[np.ndarray, float]:
 
 
 def pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
-    """[n, d] integer codes -> [n, ceil(d*bits/8)] bytes, coordinate j at bit
-    (j*bits) % 8 of byte (j*bits) // 8 (low bits first)."""
+    """[n, d] integer codes -> [n, ceil(d*bits/8)] bytes, coordinate j at bits
+    j*bits .. j*bits + bits - 1 of the row, low bits first (a 3-bit code may
+    straddle two bytes)."""
     n, d = codes.shape
     row_bytes = (d * bits + 7) // 8
-    per = 8 // bits
-    pad = row_bytes * per - d
-    c = np.concatenate([codes.astype(np.uint8), np.zeros((n, pad), np.uint8)], axis=1)
-    c = c.reshape(n, row_bytes, per)
-    out = np.zeros((n, row_bytes), np.uint8)
-    for e in range(per):
-        out |= (c[:, :, e] & ((1 << bits) - 1)) << (e * bits)
-    return out
+    c = codes.astype(np.uint8) & ((1 << bits) - 1)
+    bitsv = ((c[:, :, None] >> np.arange(bits, dtype=np.uint8)) & 1).reshape(n, d * bits)
+    pad = row_bytes * 8 - d * bits
+    bitsv = np.concatenate([bitsv, np.zeros((n, pad), np.uint8)], axis=1)
+    return np.packbits(bitsv, axis=1, bitorder="little")
 
 
 def unpack_codes(packed: np.ndarray, bits: int, d: int) -> np.ndarray:
-    per = 8 // bits
-    n, row_bytes = packed.shape
-    out = np.zeros((n, row_bytes, per), np.uint8)
-    for e in range(per):
-        out[:, :, e] = (packed >> (e * bits)) & ((1 << bits) - 1)
-    return out.reshape(n, row_bytes * per)[:, :d]
+    """Inverse of pack_codes: [n, row_bytes] -> [n, d] codes."""
+    n = packed.shape[0]
+    bitsv = np.unpackbits(np.ascontiguousarray(packed, np.uint8), axis=1, bitorder="little")
+    bitsv = bitsv[:, :d * bits].reshape(n, d, bits).astype(np.uint8)
+    return (bitsv << np.arange(bits, dtype=np.uint8)).sum(axis=2).astype(np.uint8)
 
 
 class TurboQuantCorpus:

@@ -417,6 +417,23 @@ class F16Sidecar:
                       self.buf.ptr)
             src.free()
 
+    @classmethod
+    def allocate(cls, rt: Runtime, n: int, dim: int) -> "F16Sidecar":
+        """An n x dim sidecar whose rows are filled later with fill_device."""
+        obj = cls.__new__(cls)
+        obj.rt, obj.n, obj.dim = rt, int(n), int(dim)
+        obj.buf = DeviceBuffer(rt, max(2, obj.n * obj.dim * 2))
+        return obj
+
+    def fill_device(self, d_x: DeviceBuffer, row0: int, rows: int) -> None:
+        """Rows [row0, row0 + rows) from f32 vectors already on the device."""
+        if row0 < 0 or rows < 0 or row0 + rows > self.n:
+            raise ValueError("rows outside the sidecar")
+        if rows:
+            _lib.call("eoship_f16_sidecar_device", self.rt.handle, d_x.ptr,
+                      C.c_int64(rows * self.dim),
+                      self.buf.view(row0 * self.dim * 2, rows * self.dim * 2).ptr)
+
     def halves(self) -> np.ndarray:
         return self.buf.download(np.uint16, (self.n, self.dim))
 
@@ -441,18 +458,28 @@ def top_fp16_rerank_scores_device(sidecar: F16Sidecar, d_queries: DeviceBuffer, 
     return c if (top_k <= 0 or top_k > c) else int(top_k)
 
 
-def turboquant_fp16_rerank_top_k(index: "TurboQuantIndex", sidecar: F16Sidecar,
-                                 queries: np.ndarray, top_k: int, overfetch: int):
+def turboquant_fp16_rerank_top_k(index, sidecar: F16Sidecar, queries: np.ndarray, top_k: int,
+                                 overfetch: int, bit_width: int | None = None):
     """Two-stage retrieval per query as computeTurboQuantFP16RerankRetrievalQuality
     runs it (runtime/retrieval_turboquant.go:1512-1556): top_k < 100 -> 100,
     overfetch < top_k -> top_k, TurboQuant top-overfetch candidates, then the f16
-    rerank (with the rank-100 rescue for the b4 / overfetch 200 / top 100 profile).
-    Returns (ids int64 [Q, kk], scores float32 [Q, kk], candidate ids [Q, c])."""
+    rerank (with the rank-100 rescue for the b4 / overfetch 200 / top 100
+    profile). index: an IPIndex (the reference's IPQuantized first stage; the
+    rescue gate gets its bit width, MSE bits + 1, as the reference passes the
+    IP quantizer's bitWidth) or a TurboQuantIndex over the MSE-stage layout,
+    for which bit_width must be given. Returns (ids int64 [Q, kk], scores
+    float32 [Q, kk], candidate ids [Q, c])."""
     top_k = max(int(top_k), 100)
     overfetch = max(int(overfetch), top_k)
-    if sidecar.n != index.n or sidecar.dim != index.dim:
+    is_ip = isinstance(index, IPIndex)
+    dim = index.qz.dim if is_ip else index.dim
+    if bit_width is None:
+        if not is_ip:
+            raise ValueError("bit_width is required for an MSE-layout index")
+        bit_width = index.qz.bits + 1
+    if sidecar.n != index.n or sidecar.dim != dim:
         raise ValueError("sidecar rows must match the bound corpus")
-    q = index._queries(queries)
+    q = np.ascontiguousarray(queries, np.float32).reshape(-1, dim) if is_ip else index._queries(queries)
     nq = q.shape[0]
     c = index.effective_k(overfetch)
     rt = index.rt
@@ -463,8 +490,9 @@ def turboquant_fp16_rerank_top_k(index: "TurboQuantIndex", sidecar: F16Sidecar,
     kk = c if top_k > c else top_k
     d_ids = DeviceBuffer(rt, max(8, nq * kk * 8))
     d_sc = DeviceBuffer(rt, max(4, nq * kk * 4))
-    d_rank = DeviceBuffer.from_array(rt, index.id_rank) if index.id_rank is not None else None
-    top_fp16_rerank_scores_device(sidecar, d_q, nq, d_cid, d_cs, c, top_k, index.bits, overfetch,
+    rank = None if is_ip else index.id_rank
+    d_rank = DeviceBuffer.from_array(rt, rank) if rank is not None else None
+    top_fp16_rerank_scores_device(sidecar, d_q, nq, d_cid, d_cs, c, top_k, bit_width, overfetch,
                                   d_ids, d_sc, d_rank)
     ids = d_ids.download(np.int64, (nq, kk))
     scores = d_sc.download(np.float32, (nq, kk))
@@ -625,8 +653,75 @@ class IPQuantizer:
             for b in ins + [out] + ([tid, tsc] if k > 0 else []):
                 b.free()
 
+    def bind(self, codes, signs, resnorms, norms, zero_vector_allowed=None) -> "IPIndex":
+        """Binds an encoded corpus for top-k search (eoship_tq_ip_bind_corpus):
+        host arrays or DeviceBuffers of codes [n, row_bytes], signs [n,
+        sign_bytes], resnorms and norms [n]."""
+        return IPIndex(self, codes, signs, resnorms, norms, zero_vector_allowed)
+
     def release(self) -> None:
         for b in (self._rot, self._qjl):
             if b is not None:
                 b.free()
         self._rot = self._qjl = None
+
+
+class IPIndex:
+    """An inner-product corpus bound for top-k (the promoted profile's first
+    stage): ``top_k_device`` on device queries, ``top_k`` on host arrays."""
+
+    def __init__(self, quantizer: IPQuantizer, codes, signs, resnorms, norms,
+                 zero_vector_allowed=None):
+        self.qz, self.rt = quantizer, quantizer.rt
+        tmp = []
+
+        def dev(x, dtype):
+            if isinstance(x, DeviceBuffer):
+                return x
+            b = DeviceBuffer.from_array(self.rt, np.ascontiguousarray(x, dtype))
+            tmp.append(b)
+            return b
+
+        n = int(norms.nbytes // 4) if isinstance(norms, DeviceBuffer) else int(np.asarray(norms).shape[0])
+        bufs = [dev(codes, np.uint8), dev(signs, np.uint8), dev(resnorms, np.float32),
+                dev(norms, np.float32)]
+        zv = None
+        opts = None
+        if zero_vector_allowed is not None:
+            zv = np.ascontiguousarray(zero_vector_allowed, np.uint8)
+            opts = _lib.EosHipTQBindOptions(zero_vector_allowed=zv.ctypes.data_as(C.POINTER(C.c_uint8)),
+                                            id_rank=None)
+        self.handle = C.c_void_p()
+        try:
+            _lib.call("eoship_tq_ip_bind_corpus", self.rt.handle, C.byref(quantizer.spec),
+                      bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, C.c_int64(n),
+                      C.byref(opts) if opts is not None else None, C.byref(self.handle))
+        finally:
+            for b in tmp:
+                b.free()
+        self.n = n
+
+    def effective_k(self, k: int) -> int:
+        return self.n if (k <= 0 or k > self.n) else k
+
+    def top_k_device(self, d_queries: DeviceBuffer, nq: int, k: int, d_ids: DeviceBuffer,
+                     d_scores: DeviceBuffer) -> None:
+        _lib.call("eoship_tq_ip_topk_device", self.rt.handle, self.handle, d_queries.ptr,
+                  C.c_int32(nq), C.c_int32(int(k)), d_ids.ptr, d_scores.ptr)
+
+    def top_k(self, queries: np.ndarray, k: int):
+        q = np.ascontiguousarray(queries, np.float32).reshape(-1, self.qz.dim)
+        nq, kk = q.shape[0], self.effective_k(k)
+        dq = DeviceBuffer.from_array(self.rt, q)
+        di, ds = DeviceBuffer(self.rt, max(8, nq * kk * 8)), DeviceBuffer(self.rt, max(4, nq * kk * 4))
+        try:
+            self.top_k_device(dq, nq, k, di, ds)
+            return di.download(np.int64, (nq, kk)), ds.download(np.float32, (nq, kk))
+        finally:
+            for b in (dq, di, ds):
+                b.free()
+
+    def release(self) -> None:
+        if self.handle and self.rt.handle:
+            _lib.call("eoship_tq_ip_release", self.handle)
+        self.handle = C.c_void_p()

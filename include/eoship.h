@@ -488,7 +488,7 @@ int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int3
  * provides, like R. */
 typedef struct {
   int32_t dim;               /* d, 1..1024 */
-  int32_t bits;              /* MSE bits: 1, 2 or 4 */
+  int32_t bits;              /* MSE bits: 1, 2, 3 or 4 (bit width - 1) */
   float codebook_scale;      /* c_v = codebook_scale * codebook[v] */
   const int8_t* codebook;    /* host [2^bits] int8 grid */
   const float* rotation_t;   /* device [d][d], rotation_t[k * d + j] = R[j][k]; NULL = I */
@@ -512,6 +512,31 @@ int eoship_tq_ip_scores_device(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
                                const uint8_t* d_signs, const float* d_resnorms,
                                const float* d_norms, int64_t n, float* d_scores, int32_t k,
                                int64_t* d_top_ids, float* d_top_scores, char** err);
+
+/* The promoted profile's first stage (turboquant_ip_b4_overfetch200_fp16_
+ * rerank, runtime/retrieval_turboquant.go:1500-1556): an inner-product
+ * corpus -- the codes, signs, ResNorms and Norms eoship_tq_ip_encode_device
+ * writes, MSE codes of 1, 2 or 3 bits (bit widths 2, 3, 4) -- bound for
+ * top-k search. Bind repacks it into a tile layout on the device (the
+ * caller's buffers may be freed afterwards; spec->rotation_t and qjl_t must
+ * stay valid while the corpus is bound) and applies the Norm policy of
+ * validateEosQuantizedVectorNorm (Norm < 0 or non-finite refused, Norm == 0
+ * only with opts->zero_vector_allowed; id_rank is not supported). */
+typedef struct EosHipTQIP EosHipTQIP;
+int eoship_tq_ip_bind_corpus(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
+                             const uint8_t* d_codes, const uint8_t* d_signs,
+                             const float* d_resnorms, const float* d_norms, int64_t n,
+                             const EosHipTQBindOptions* opts, EosHipTQIP** out, char** err);
+/* Top k per query of the inner-product estimate (the score
+ * eoship_tq_ip_scores_device computes; topTurboQuantRetrievalScoresWithStats
+ * over InnerProductPrepared scores, :1853-1887): ids and scores [q][kk],
+ * kk = min(k, n) (k <= 0: n, at most 8192), by score descending then index
+ * ascending. Exact whatever the data: a sample threshold prunes the scan and
+ * a device-gated exhaustive pass repairs any query it leaves short.
+ * Enqueued on the runtime stream. */
+int eoship_tq_ip_topk_device(EosHipRuntime* rt, EosHipTQIP* ip, const float* d_queries,
+                             int32_t q, int32_t k, int64_t* d_ids, float* d_scores, char** err);
+int eoship_tq_ip_release(EosHipTQIP* ip, char** err);
 
 /* Second stage over f32 rows [n][d] (topDenseRerankScores,
  * runtime/retrieval_turboquant.go:1610-1633): score = sum += q[i] * row[i] in

@@ -26,9 +26,19 @@
 
 #define QMAX_LIMIT (127 * 256 + 127)
 
+/* Code j of a row packed low bits first (coordinate j at bits j * bits ..
+ * j * bits + bits - 1; a 3-bit code may straddle two bytes). */
 static inline unsigned code_at(const uint8_t* row, int j, int bits) {
-  const int bit = j * bits;
-  return (row[bit >> 3] >> (bit & 7)) & ((1u << bits) - 1u);
+  const int bit = j * bits, sh = bit & 7;
+  unsigned v = (unsigned)row[bit >> 3] >> sh;
+  if (sh + bits > 8) v |= (unsigned)row[(bit >> 3) + 1] << (8 - sh);
+  return v & ((1u << bits) - 1u);
+}
+
+static inline void code_put(uint8_t* row, int j, int bits, unsigned code) {
+  const int bit = j * bits, sh = bit & 7;
+  row[bit >> 3] |= (uint8_t)(code << sh);
+  if (sh + bits > 8) row[(bit >> 3) + 1] |= (uint8_t)(code >> (8 - sh));
 }
 
 int tq_qmax(const int8_t* cb, int levels, int d) {
@@ -435,8 +445,7 @@ void tq_encode(const float* x, int64_t n, const float* rot, int d, int bits, con
           best = v;
         }
       }
-      const int bit = j * bits;
-      row[bit >> 3] |= (uint8_t)(best << (bit & 7));
+      code_put(row, j, bits, (unsigned)best);
     }
   }
   free(u);
@@ -459,9 +468,12 @@ void tq_encode(const float* x, int64_t n, const float* rot, int d, int bits, con
  *   D_mse = sum_j Qs_j C[code_j], D_qjl = sum_i Ys_i (2 bit_i - 1)   (exact int32)
  *   score = ((float)D_mse * alpha + ResNorm * ((float)D_qjl * beta)) * Norm
  * (each product and sum rounded to f32 in that order). */
+/* QJL query grid limit: |Ys| <= 127 * 256 + 127 (each value splits into an
+ * int8 high and low half, Ys = 256 hi + lo, for the int8 MFMA scan) and
+ * d * |Ys| < 2^31. */
 int tq_qjl_qmax(int d) {
   const long long lim = 2147483647LL / d - 1;
-  return (int)(lim < 32767 ? lim : 32767);
+  return (int)(lim < QMAX_LIMIT ? lim : QMAX_LIMIT);
 }
 
 void tq_encode_ip(const float* x, int64_t n, const float* rot, const float* qjl, int d, int bits,
@@ -491,7 +503,7 @@ void tq_encode_ip(const float* x, int64_t n, const float* rot, const float* qjl,
     const uint8_t* row = codes + (size_t)i * row_bytes;
     double rn = 0.0;
     for (int j = 0; j < d; ++j) {
-      const int code = (row[(j * bits) >> 3] >> ((j * bits) & 7)) & (levels - 1);
+      const int code = (int)code_at(row, j, bits);
       r[j] = u[j] - nrm * c[code];
       rn = fma(r[j], r[j], rn);
     }
@@ -560,7 +572,7 @@ void tq_ip_scores(const float* queries, int nq, const float* rot, const float* q
       const uint8_t* sg = signs + (size_t)i * sign_bytes;
       int32_t dm = 0, dq = 0;
       for (int j = 0; j < d; ++j) {
-        dm += (int32_t)qs[j] * cb[(row[(j * bits) >> 3] >> ((j * bits) & 7)) & (levels - 1)];
+        dm += (int32_t)qs[j] * cb[code_at(row, j, bits)];
         dq += ((sg[j >> 3] >> (j & 7)) & 1) ? (int32_t)ys[j] : -(int32_t)ys[j];
       }
       const float t1 = (float)dm * alpha;

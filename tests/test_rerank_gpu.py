@@ -104,7 +104,7 @@ def test_two_stage_end_to_end(rt, k, overfetch):
     idx = TurboQuantIndex(rt, c.codes, c.norms, c.dim, c.bits, c.codebook, c.codebook_scale,
                           c.rotation)
     side = F16Sidecar(rt, docs)
-    ids, sc, cand = turboquant_fp16_rerank_top_k(idx, side, q, k, overfetch)
+    ids, sc, cand = turboquant_fp16_rerank_top_k(idx, side, q, k, overfetch, bit_width=4)
     wc_ids, wc_sc = oracle.tq_topk(q, c.rotation, c.dim, c.bits, c.codebook, c.codebook_scale,
                                    c.codes, c.norms, overfetch)
     assert np.array_equal(cand, wc_ids)
@@ -185,3 +185,36 @@ def test_rerank_string_id_ties(rt):
     assert np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))
     plain, _ = oracle.fp16_rerank(q, side.halves(), cid, cs, 0, 4, 200)
     assert not np.array_equal(plain, ids)
+
+
+@pytest.mark.parametrize("k,overfetch", [(100, 200), (100, 250)])
+def test_two_stage_inner_product_first_stage(rt, k, overfetch):
+    """The promoted profile as the reference runs it: an inner-product (b = 4:
+    3-bit MSE + QJL) first stage over the encoded documents, top-overfetch,
+    then the f16 rerank whose rescue gate sees bit width 4: ids and scores
+    bit-exact vs the oracle's IP scores + top-k + f16 rerank."""
+    _case(f"two-stage IP b4 first stage k={k} overfetch={overfetch}")
+    from eos_amd.turboquant import IPQuantizer
+    n, d = 12000, 384
+    rng = np.random.default_rng(45)
+    docs = rng.standard_normal((n, d)).astype(np.float32)
+    docs /= np.linalg.norm(docs, axis=1, keepdims=True)
+    q = rng.standard_normal((8, d)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=1, keepdims=True)
+    rot = np.linalg.qr(rng.normal(size=(d, d)))[0].astype(np.float32)
+    S = rng.normal(size=(d, d)).astype(np.float32)
+    cb, s_c = datagen.turboquant_codebook(3, d)
+    qz = IPQuantizer(rt, d, 3, cb, s_c, rot, S)
+    codes, signs, rn, nm = qz.encode(docs)
+    idx = qz.bind(codes, signs, rn, nm)
+    side = F16Sidecar(rt, docs)
+    ids, sc, cand = turboquant_fp16_rerank_top_k(idx, side, q, k, overfetch)
+    full = oracle.tq_ip_scores(q, rot, S, d, 3, cb, s_c, codes, signs, rn, nm)
+    wc = [oracle.topk_scores(r, overfetch) for r in full]
+    wc_ids = np.stack([w[0] for w in wc])
+    wc_sc = np.stack([w[1] for w in wc])
+    assert np.array_equal(cand, wc_ids)
+    wids, wsc = oracle.fp16_rerank(q, oracle.f32_to_half(docs), wc_ids, wc_sc, k, 4, overfetch)
+    assert np.array_equal(ids, wids) and np.array_equal(sc.view(np.uint32), wsc.view(np.uint32))
+    idx.release()
+    qz.release()

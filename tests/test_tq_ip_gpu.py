@@ -16,7 +16,8 @@ def _case(name):
 
 @pytest.mark.parametrize("d,bits,n,rotate", [(384, 4, 3000, True), (256, 2, 1001, True),
                                              (128, 1, 777, False), (1000, 4, 100, True),
-                                             (37, 2, 65, True)])
+                                             (37, 2, 65, True), (384, 3, 2000, True),
+                                             (29, 3, 99, False)])
 def test_ip_layout_matches_oracle(rt, d, bits, n, rotate):
     _case(f"ip layout d={d} bits={bits} n={n} rotate={rotate}")
     rng = np.random.default_rng(d * 7 + bits)
