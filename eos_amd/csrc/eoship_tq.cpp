@@ -1687,6 +1687,22 @@ int eoship_tq_reconstruct_rerank_device(EosHipRuntime* rt, const EosHipTQCodes* 
 
 // ------------------------------------------------------ inner-product layout
 
+// Query preparation of the inner-product layout into qs / ys / alpha / beta:
+// qr = R q and y = S qr as tiled f64 matrix-vector launches (eos_tq_ip_matvec),
+// then one quantize workgroup per query (eos_tq_ip_quant).
+// qr, y: device scratch of q * d doubles each.
+static int ip_prepare_launch(EosHipRuntime* rt, const TqIpArgs& a, int q, double* qr, double* y,
+                             char** err) {
+  const dim3 grid((unsigned)((a.d + 31) / 32), (unsigned)((q + 7) / 8));
+  TqIpMatArgs m1{a.rot_t, a.queries, nullptr, qr, q, a.d};
+  TqIpMatArgs m2{a.qjl_t, nullptr, qr, y, q, a.d};
+  TqIpQuantArgs qa{qr, y, a.qs, a.ys, a.alpha, a.beta, q, a.d, a.qmax, a.qmax2, a.cb_scale};
+  if (rt->launch("eos_tq_ip_matvec", grid, dim3(256), 0, &m1, err, "tq_ip_prepare") != 0 ||
+      rt->launch("eos_tq_ip_matvec", grid, dim3(256), 0, &m2, err, "tq_ip_prepare") != 0)
+    return 1;
+  return rt->launch("eos_tq_ip_quant", dim3((unsigned)q), dim3(256), 0, &qa, err, "tq_ip_prepare");
+}
+
 static int ip_spec_check(EosHipRuntime* rt, const EosHipTQIPSpec* spec, TqIpArgs* a,
                          const char* what, char** err) {
   if (rt == nullptr || spec == nullptr) return set_err(err, "%s: NULL argument", what);
@@ -1759,9 +1775,13 @@ int eoship_tq_ip_scores_device(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
   if (!d_queries || !d_codes || !d_signs || !d_resnorms || !d_norms || !d_scores)
     return set_err(err, "%s: NULL buffer", what);
   const size_t grid_bytes = (size_t)q * (size_t)a.d * sizeof(int);
+  const size_t f64_bytes = (size_t)q * (size_t)a.d * sizeof(double);
   void* ws = nullptr;
-  if (rt->workspace(2 * grid_bytes + (size_t)q * 8, &ws, err) != 0) return 1;
+  if (rt->workspace(2 * f64_bytes + 2 * grid_bytes + (size_t)q * 8, &ws, err) != 0) return 1;
   char* w = static_cast<char*>(ws);
+  double* qr = reinterpret_cast<double*>(w);
+  double* yv = reinterpret_cast<double*>(w + f64_bytes);
+  w += 2 * f64_bytes;
   a.queries = d_queries;
   a.qs = reinterpret_cast<int*>(w);
   a.ys = reinterpret_cast<int*>(w + grid_bytes);
@@ -1774,7 +1794,7 @@ int eoship_tq_ip_scores_device(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
   a.scores = d_scores;
   a.n = n;
   a.q = q;
-  if (rt->launch("eos_tq_ip_prepare", dim3((unsigned)q), dim3(256), 0, &a, err, "tq_ip_prepare") != 0 ||
+  if (ip_prepare_launch(rt, a, q, qr, yv, err) != 0 ||
       rt->launch("eos_tq_ip_scores", dim3((unsigned)((n + 255) / 256), (unsigned)((q + 7) / 8)),
                  dim3(256), 0, &a, err, "tq_ip_scores") != 0)
     return 1;
@@ -1833,7 +1853,7 @@ int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int3
 // inner-product estimate over IPQuantized documents, as
 // topTurboQuantRetrievalScoresWithStats computes it with InnerProductPrepared
 // (:1853-1887). Per batch of <= 64 queries (32 when the dimension needs more
-// than 12 K-steps): eos_tq_ip_prepare (int grids of R q and S R q),
+// than 12 K-steps): eos_tq_ip_matvec + eos_tq_ip_quant (int grids of R q and S R q),
 // eos_tq_ip_frag (MFMA fragments), a sample scan of tile maxima and
 // eos_tq_threshold, the filter scan (exact scores, keep >= tau),
 // eos_tq_finalize, and the exact fallback gated on its flags (dense scan +
@@ -1864,12 +1884,14 @@ struct EosHipTQIP {
   float* samp = nullptr;
   float* dense = nullptr;
   size_t dense_bytes = 0;
+  double* qr = nullptr;  // [cols][d] R q
+  double* yv = nullptr;  // [cols][d] S R q
 
   int batch_cap() const { return 32 * nqg; }
 
   ~EosHipTQIP() {
-    void* p[] = {packed, norms, resnorms, qs, ys, alpha, beta, ysum, bfrag, tau, cand, cand_count,
-                 status, samp, dense};
+    void* p[] = {packed, norms, resnorms, qs,         ys,     alpha, beta, ysum, bfrag,
+                 tau,    cand,  cand_count, status, samp, dense, qr,    yv};
     for (void* x : p)
       if (x) (void)hipFree(x);
   }
@@ -1927,9 +1949,7 @@ struct EosHipTQIP {
     a.qmax = qmax;
     a.qmax2 = qmax2;
     a.cb_scale = cb_scale;
-    if (rt->launch("eos_tq_ip_prepare", dim3((unsigned)qb), dim3(256), 0, &a, err,
-                   "tq_ip_prepare") != 0)
-      return 1;
+    if (ip_prepare_launch(rt, a, qb, qr, yv, err) != 0) return 1;
     TqIpFragArgs f;
     memset(&f, 0, sizeof(f));
     f.qs = qs;
@@ -2091,7 +2111,9 @@ int eoship_tq_ip_bind_corpus(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
       rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->cand_count), err) ||
       rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->status), err) ||
       rt->alloc((size_t)cols * std::max<int64_t>(samp_tiles, 1) * 4,
-                reinterpret_cast<void**>(&ip->samp), err))
+                reinterpret_cast<void**>(&ip->samp), err) ||
+      rt->alloc((size_t)cols * ip->d * 8, reinterpret_cast<void**>(&ip->qr), err) ||
+      rt->alloc((size_t)cols * ip->d * 8, reinterpret_cast<void**>(&ip->yv), err))
     return fail();
   TqIpPackArgs p;
   memset(&p, 0, sizeof(p));

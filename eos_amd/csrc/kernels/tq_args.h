@@ -267,7 +267,7 @@ struct TqIpPackArgs {
 };
 
 // Query fragments of the inner-product scan from the int grids of
-// eos_tq_ip_prepare: per K-step and 32-column group g, blocks 4 g + 0 / + 1
+// eos_tq_ip_quant: per K-step and 32-column group g, blocks 4 g + 0 / + 1
 // (MSE grid Qs = 256 hi + lo) and 4 g + 2 / + 3 (QJL grid Ys likewise); the
 // sum of Ys over the dimensions (D_qjl = 2 sum_{bit = 1} Ys - sum Ys); the
 // filter state of each column reset (tau = -inf, no kept candidates).
@@ -301,6 +301,30 @@ struct TqIpScanArgs {
   long long n, out_begin, out_count, out_stride, tile_begin, tile_step;
   int ntiles, q, cap, mode;
   uint32_t lut0, lut1;     // the 8-entry int8 codebook: bytes C[0..3], C[4..7]
+};
+
+// out[c][j] = sum over k ascending of M[j][k] in[c][k] (one f64 fma chain per
+// (c, j)), mt[k * d + j] = M[j][k]; in is f32 (in32) or f64 (in64); mt NULL:
+// out = in. Grid (ceil(d / 32), ceil(q / 8)).
+struct TqIpMatArgs {
+  const float* mt;
+  const float* in32;
+  const double* in64;
+  double* out;
+  int q, d;
+};
+
+// Per query column c < q: Qs and alpha from qr, Ys and beta from y. One
+// workgroup per column.
+struct TqIpQuantArgs {
+  const double* qr;        // [q][d]
+  const double* y;         // [q][d]
+  int* qs;                 // [q][d]
+  int* ys;                 // [q][d]
+  float* alpha;
+  float* beta;
+  int q, d, qmax, qmax2;
+  float cb_scale;
 };
 
 #endif  // EOSHIP_TQ_ARGS_H

@@ -562,18 +562,55 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_encode_ip(TqIpArgs a) {
   }
 }
 
-// Query preparation of the inner-product layout, one workgroup per query:
-// q' = R q, the MSE grid Qs = rint(q' qmax / max|q'|) with alpha = s_q s_c (as
-// eos_tq_rotate / eos_tq_quantize), then y = S q' (fma chain in j order), the
-// QJL grid Ys = rint(y qmax2 / max|y|) and beta = (max|y| / qmax2)
-// sqrt(pi / 2) / d.
-extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_prepare(TqIpArgs a) {
-  __shared__ double qr[kIpDMax];
-  __shared__ double yv[kIpDMax];
-  __shared__ double red[4];
-  const int qi = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+// Query preparation of the inner-product layout: q' = R q and y = S q' (f64,
+// one fma chain per coordinate in k order), then eos_tq_ip_quant. These are
+// the matrix-vector products, workgroup (x, y) computing rows [32 x, 32 x +
+// 32) for the 8 columns [8 y, 8 y + 8): the columns staged in LDS as f64, the
+// matrix in 32 x 32 chunks.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_matvec(TqIpMatArgs a) {
+  __shared__ double xin[8 * kIpDMax];
+  __shared__ float ms[32 * 33];
+  const int tid = threadIdx.x, jj = tid & 31, cl = tid >> 5;
+  const int j0 = blockIdx.x * 32, c0 = blockIdx.y * 8;
   const int d = a.d;
-  const float* q = a.queries + (size_t)qi * d;
+  for (int i = tid; i < 8 * d; i += 256) {
+    const int c = i / d, k = i - c * d;
+    double v = 0.0;
+    if (c0 + c < a.q)
+      v = a.in64 != nullptr ? a.in64[(size_t)(c0 + c) * d + k] : (double)a.in32[(size_t)(c0 + c) * d + k];
+    xin[c * kIpDMax + k] = v;
+  }
+  __syncthreads();
+  const int j = j0 + jj, c = c0 + cl;
+  double acc = 0.0;
+  if (a.mt == nullptr) {
+    acc = j < d ? xin[cl * kIpDMax + j] : 0.0;
+  } else {
+    for (int k0 = 0; k0 < d; k0 += 32) {
+      // chunk rows k0 .. k0 + 31 of mt (columns j0 .. j0 + 31), zero past d
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int kk = cl + 8 * r, k = k0 + kk;
+        ms[kk * 33 + jj] = (k < d && j < d) ? a.mt[(size_t)k * d + j] : 0.0f;
+      }
+      __syncthreads();
+      const int kn = min(32, d - k0);
+      for (int kk = 0; kk < kn; ++kk)
+        acc = fma((double)ms[kk * 33 + jj], xin[cl * kIpDMax + k0 + kk], acc);
+      __syncthreads();
+    }
+  }
+  if (c < a.q && j < d) a.out[(size_t)c * d + j] = acc;
+}
+
+// Grids and scales of one query column from qr = R q and y = S qr: the MSE
+// grid Qs = rint(q' qmax / max|q'|) with alpha = (max|q'| / qmax) s_c (as
+// eos_tq_rotate / eos_tq_quantize), the QJL grid Ys = rint(y qmax2 / max|y|)
+// and beta = (max|y| / qmax2) sqrt(pi / 2) / d; both clamped to +-qmax.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_quant(TqIpQuantArgs a) {
+  __shared__ double red[4];
+  const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int d = a.d;
   auto block_max = [&](double m) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmax(m, __shfl_xor(m, o));
@@ -583,44 +620,30 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_prepare(TqIpArgs a) 
     __syncthreads();
     return r;
   };
-  double m = 0.0;
+  const double* qr = a.qr + (size_t)c * d;
+  const double* y = a.y + (size_t)c * d;
+  double m1 = 0.0, m2 = 0.0;
   for (int j = tid; j < d; j += 256) {
-    double acc = 0.0;
-    if (a.rot_t != nullptr) {
-      for (int k = 0; k < d; ++k) acc = fma((double)a.rot_t[(size_t)k * d + j], (double)q[k], acc);
-    } else {
-      acc = (double)q[j];
-    }
-    qr[j] = acc;
-    m = fmax(m, fabs(acc));
+    m1 = fmax(m1, fabs(qr[j]));
+    m2 = fmax(m2, fabs(y[j]));
   }
-  const double mq = block_max(m);
+  const double mq = block_max(m1);
+  const double my = block_max(m2);
   const double inv = mq > 0.0 ? (double)a.qmax / mq : 0.0;
-  m = 0.0;
+  const double inv2 = my > 0.0 ? (double)a.qmax2 / my : 0.0;
   for (int j = tid; j < d; j += 256) {
     double v = rint(qr[j] * inv);
     v = fmin(fmax(v, (double)-a.qmax), (double)a.qmax);
-    a.qs[(size_t)qi * d + j] = (int)v;
-    double acc = 0.0;
-    for (int k = 0; k < d; ++k) acc = fma((double)a.qjl_t[(size_t)k * d + j], qr[k], acc);
-    yv[j] = acc;
-    m = fmax(m, fabs(acc));
-  }
-  // qr is complete before any thread's y chain reads it: the chains above
-  // read qr[k] for all k, written in the first loop and ordered by the
-  // barriers of block_max.
-  const double my = block_max(m);
-  const double inv2 = my > 0.0 ? (double)a.qmax2 / my : 0.0;
-  for (int j = tid; j < d; j += 256) {
-    double v = rint(yv[j] * inv2);
-    v = fmin(fmax(v, (double)-a.qmax2), (double)a.qmax2);
-    a.ys[(size_t)qi * d + j] = (int)v;
+    a.qs[(size_t)c * d + j] = (int)v;
+    double u = rint(y[j] * inv2);
+    u = fmin(fmax(u, (double)-a.qmax2), (double)a.qmax2);
+    a.ys[(size_t)c * d + j] = (int)u;
   }
   if (tid == 0) {
-    a.alpha[qi] = mq > 0.0 ? (float)((mq / (double)a.qmax) * (double)a.cb_scale) : 0.0f;
+    a.alpha[c] = mq > 0.0 ? (float)((mq / (double)a.qmax) * (double)a.cb_scale) : 0.0f;
     const double half_pi = 1.5707963267948966;
-    a.beta[qi] = my > 0.0 ? (float)((my / (double)a.qmax2) * __builtin_sqrt(half_pi) / (double)d)
-                          : 0.0f;
+    a.beta[c] = my > 0.0 ? (float)((my / (double)a.qmax2) * __builtin_sqrt(half_pi) / (double)d)
+                         : 0.0f;
   }
 }
 
