@@ -127,6 +127,19 @@ class EosHipMllTensor(C.Structure):
     ]
 
 
+class EosHipAccounting(C.Structure):
+    _fields_ = [
+        ("kernel_launches", C.c_int64),
+        ("uploaded_bytes", C.c_int64),
+        ("downloaded_bytes", C.c_int64),
+        ("sync_count", C.c_int64),
+        ("graph_captures", C.c_int64),
+        ("graph_replays", C.c_int64),
+        ("device_execution", C.c_int32),
+        ("reserved", C.c_int32),
+    ]
+
+
 class EosHipMllPlan(C.Structure):
     _fields_ = [
         ("route", C.c_int32),
@@ -235,6 +248,8 @@ _SIGNATURES = {
     "eoship_h2d": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
     "eoship_d2h": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
     "eoship_d2d": ([C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p], C.c_int),
+    "eoship_accounting_read": ([C.c_void_p, C.POINTER(EosHipAccounting), C.c_int32, C.c_void_p],
+                               C.c_int),
     "eoship_memset": ([C.c_void_p, C.c_void_p, C.c_int, C.c_size_t, C.c_void_p], C.c_int),
     "eoship_sync": ([C.c_void_p, C.c_void_p], C.c_int),
     "eoship_runtime_wait": ([C.c_void_p, C.c_void_p, C.c_void_p], C.c_int),

@@ -61,8 +61,8 @@ int eoship_embed_bind(EosHipRuntime* rt, const uint16_t* table_f16, int32_t voca
     delete m;
     return 1;
   }
-  e = hipMemcpy(m->table, table_f16, tb, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(m->proj, proj_f16, pb, hipMemcpyHostToDevice);
+  e = rt->copy_sync(m->table, table_f16, tb, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = rt->copy_sync(m->proj, proj_f16, pb, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     delete m;
     return hip_err(err, "hipMemcpy(embed weights)", e);
@@ -74,7 +74,7 @@ int eoship_embed_bind(EosHipRuntime* rt, const uint16_t* table_f16, int32_t voca
 int eoship_embed_release(EosHipEmbed* m, char** err) {
   (void)err;
   if (m == nullptr) return 0;
-  hipStreamSynchronize(m->rt->stream);
+  (void)m->rt->sync(nullptr);
   delete m;
   return 0;
 }
@@ -106,12 +106,12 @@ int eoship_embed_run(EosHipRuntime* rt, EosHipEmbed* m, const int32_t* tokens, i
   }
   int32_t* dt = static_cast<int32_t*>(m->io);
   uint16_t* dout = reinterpret_cast<uint16_t*>(static_cast<char*>(m->io) + (((size_t)n * 4 + 15) & ~(size_t)15));
-  hipError_t e = hipMemcpyAsync(dt, tokens, (size_t)n * 4, hipMemcpyHostToDevice, rt->stream);
+  hipError_t e = rt->copy_async(dt, tokens, (size_t)n * 4, hipMemcpyHostToDevice);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(tokens)", e);
   if (m->run(dt, n, dout, err) != 0) return 1;
   int32_t st = 0;
-  e = hipMemcpyAsync(out_f16, dout, (size_t)n * m->edim * 2, hipMemcpyDeviceToHost, rt->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(&st, m->status, 4, hipMemcpyDeviceToHost, rt->stream);
+  e = rt->copy_async(out_f16, dout, (size_t)n * m->edim * 2, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = rt->copy_async(&st, m->status, 4, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(embeddings)", e);
   if (rt->sync(err) != 0) return 1;
   if (st != 0) return set_err(err, "eoship_embed_run: token id out of range [0, %d)", m->vocab);

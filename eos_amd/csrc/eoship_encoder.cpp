@@ -122,7 +122,7 @@ struct EosHipEncoder {
     void* p = nullptr;
     if (rt->alloc(count * sizeof(T), &p, err) != 0) return 1;
     owned.push_back(p);
-    hipError_t e = hipMemcpy(p, src, count * sizeof(T), hipMemcpyHostToDevice);
+    hipError_t e = rt->copy_sync(p, src, count * sizeof(T), hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_err(err, "hipMemcpy(encoder weights)", e);
     *dst = static_cast<T*>(p);
     return 0;
@@ -591,7 +591,7 @@ int eoship_encoder_bind_compact_opts(EosHipRuntime* rt, const EosHipCompactDesc*
 int eoship_encoder_release(EosHipEncoder* enc, char** err) {
   (void)err;
   if (enc == nullptr) return 0;
-  hipStreamSynchronize(enc->rt->stream);
+  (void)enc->rt->sync(nullptr);
   delete enc;
   return 0;
 }
@@ -623,7 +623,7 @@ int eoship_encoder_status(EosHipRuntime* rt, EosHipEncoder* enc, int32_t* status
     return set_err(err, "eoship_encoder_status: NULL argument");
   *status = 0;
   if (enc->status == nullptr) return 0;
-  hipError_t e = hipMemcpyAsync(status, enc->status, 4, hipMemcpyDeviceToHost, rt->stream);
+  hipError_t e = rt->copy_async(status, enc->status, 4, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
   return rt->sync(err);
 }
@@ -653,7 +653,7 @@ int eoship_encoder_attention_moves(EosHipRuntime* rt, EosHipEncoder* enc, int64_
   *moves = 0;
   if (enc->status == nullptr) return 0;
   int32_t v = 0;
-  hipError_t e = hipMemcpyAsync(&v, enc->status + 1, 4, hipMemcpyDeviceToHost, rt->stream);
+  hipError_t e = rt->copy_async(&v, enc->status + 1, 4, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(moves)", e);
   if (rt->sync(err) != 0) return 1;
   *moves = v;
@@ -680,15 +680,14 @@ int eoship_encoder_forward(EosHipRuntime* rt, EosHipEncoder* enc, const int32_t*
   int32_t* d_types = d_ids + n;
   int32_t* d_mask = d_types + n;
   float* d_out = reinterpret_cast<float*>(d_mask + n);
-  hipError_t e = hipMemcpyAsync(d_ids, ids, n * 4, hipMemcpyHostToDevice, rt->stream);
+  hipError_t e = rt->copy_async(d_ids, ids, n * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess && type_ids != nullptr)
-    e = hipMemcpyAsync(d_types, type_ids, n * 4, hipMemcpyHostToDevice, rt->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(d_mask, mask, n * 4, hipMemcpyHostToDevice, rt->stream);
+    e = rt->copy_async(d_types, type_ids, n * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = rt->copy_async(d_mask, mask, n * 4, hipMemcpyHostToDevice);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(encoder inputs)", e);
   if (enc->forward(d_ids, type_ids ? d_types : nullptr, d_mask, batch, tokens, d_out, err) != 0)
     return 1;
-  e = hipMemcpyAsync(out, d_out, (size_t)batch * enc->out_dim() * 4, hipMemcpyDeviceToHost,
-                     rt->stream);
+  e = rt->copy_async(out, d_out, (size_t)batch * enc->out_dim() * 4, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(embeddings)", e);
   int32_t st = 0;
   if (eoship_encoder_status(rt, enc, &st, err) != 0) return 1;

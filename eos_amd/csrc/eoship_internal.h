@@ -63,6 +63,26 @@ struct Runtime {
   int sync(char** err);
   int flush_profile(char** err);
   int take_event(hipEvent_t* ev, char** err);
+
+  // Execution accounting (the counters the reference's executor reports per
+  // step, runtime/backend/symbolic.go:174-216): kernel launches, bytes
+  // copied host -> device and device -> host, host synchronisations.
+  int64_t n_launches = 0, n_uploaded = 0, n_downloaded = 0, n_syncs = 0;
+  void count_copy(hipMemcpyKind kind, size_t bytes) {
+    if (kind == hipMemcpyHostToDevice) n_uploaded += (int64_t)bytes;
+    if (kind == hipMemcpyDeviceToHost) n_downloaded += (int64_t)bytes;
+  }
+  // Copies on the runtime stream, counted.
+  hipError_t copy_async(void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+    count_copy(kind, bytes);
+    return hipMemcpyAsync(dst, src, bytes, kind, stream);
+  }
+  // Blocking copies (bind-time uploads), counted as a copy and a host sync.
+  hipError_t copy_sync(void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+    count_copy(kind, bytes);
+    ++n_syncs;
+    return hipMemcpy(dst, src, bytes, kind);
+  }
 };
 
 // Two-stage rerank on a caller-chosen scratch buffer of at least

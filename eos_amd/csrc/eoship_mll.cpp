@@ -1834,7 +1834,7 @@ int eoship_retrieval_bind_mll(EosHipRuntime* rt, const EosHipMll* m, const char*
         return 1;
       }
       r->docs_q4 = static_cast<uint8_t*>(dev);
-      e = hipMemcpy(dev, b, t->size, hipMemcpyHostToDevice);
+      e = rt->copy_sync(dev, b, t->size, hipMemcpyHostToDevice);
     } else {
       // q8 codes dequantized as the reference decodes them (f32 code * scale).
       std::vector<float> v((size_t)t->elements);
@@ -1849,7 +1849,7 @@ int eoship_retrieval_bind_mll(EosHipRuntime* rt, const EosHipMll* m, const char*
         return 1;
       }
       r->docs_f32 = static_cast<float*>(dev);
-      e = hipMemcpy(dev, v.data(), v.size() * 4, hipMemcpyHostToDevice);
+      e = rt->copy_sync(dev, v.data(), v.size() * 4, hipMemcpyHostToDevice);
     }
     if (e != hipSuccess) {
       if (r->docs_f32) (void)hipFree(r->docs_f32);

@@ -195,7 +195,7 @@ int eoship_hadamard_tq_bind(EosHipRuntime* rt, const EosHipHadamardSpec* spec,
                {h->centroids, spec->centroids, (size_t)levels * 4},
                {h->boundaries, spec->boundaries, (size_t)(levels - 1) * 4}};
   for (const Part& pt : parts) {
-    const hipError_t e = hipMemcpy(pt.dst, pt.src, pt.bytes, hipMemcpyHostToDevice);
+    const hipError_t e = rt->copy_sync(pt.dst, pt.src, pt.bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
       (void)hipFree(mem);
       delete h;

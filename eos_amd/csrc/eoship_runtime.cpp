@@ -94,6 +94,7 @@ int Runtime::launch(const char* name, dim3 grid, dim3 block, size_t lds, void* a
     return hip_err(err, name, e);
   }
   if (rec) records.push_back(ProfileRecord{tag, e0, e1});
+  ++n_launches;
   return 0;
 }
 
@@ -154,6 +155,7 @@ void Runtime::release(void* p) {
 }
 
 int Runtime::sync(char** err) {
+  ++n_syncs;
   hipError_t e = hipStreamSynchronize(stream);
   if (e != hipSuccess) return hip_err(err, "hipStreamSynchronize", e);
   return 0;
@@ -287,7 +289,7 @@ static int copy(EosHipRuntime* rt, void* dst, const void* src, size_t bytes, hip
   if (rt == nullptr) return set_err(err, "%s: runtime is NULL", what);
   if (bytes == 0) return 0;
   if (dst == nullptr || src == nullptr) return set_err(err, "%s: NULL buffer", what);
-  hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, rt->stream);
+  hipError_t e = rt->copy_async(dst, src, bytes, kind);
   if (e != hipSuccess) return hip_err(err, what, e);
   if (kind != hipMemcpyDeviceToDevice) return rt->sync(err);
   return 0;
@@ -409,6 +411,18 @@ int eoship_profile_reset(EosHipRuntime* rt, char** err) {
   if (rt->flush_profile(err) != 0) return 1;
   rt->totals.clear();
   rt->samples.clear();
+  return 0;
+}
+
+int eoship_accounting_read(EosHipRuntime* rt, EosHipAccounting* out, int32_t reset, char** err) {
+  if (rt == nullptr || out == nullptr) return set_err(err, "eoship_accounting_read: NULL argument");
+  memset(out, 0, sizeof(*out));
+  out->kernel_launches = rt->n_launches;
+  out->uploaded_bytes = rt->n_uploaded;
+  out->downloaded_bytes = rt->n_downloaded;
+  out->sync_count = rt->n_syncs;
+  out->device_execution = 1;
+  if (reset) rt->n_launches = rt->n_uploaded = rt->n_downloaded = rt->n_syncs = 0;
   return 0;
 }
 

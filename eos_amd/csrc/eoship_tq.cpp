@@ -507,9 +507,9 @@ struct EosHipTQ {
   int batch_status(int qb, const int* d_status, EosHipTQStats* st, int* flagged, char** err) {
     int hstatus[kBatch];
     uint32_t hcount[kBatch];
-    hipError_t e = hipMemcpyAsync(hstatus, d_status, sizeof(int) * qb, hipMemcpyDeviceToHost, rt->stream);
+    hipError_t e = rt->copy_async(hstatus, d_status, sizeof(int) * qb, hipMemcpyDeviceToHost);
     if (e == hipSuccess && st)
-      e = hipMemcpyAsync(hcount, cand_count, sizeof(uint32_t) * qb, hipMemcpyDeviceToHost, rt->stream);
+      e = rt->copy_async(hcount, cand_count, sizeof(uint32_t) * qb, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(status)", e);
     if (rt->sync(err) != 0) return 1;
     int nf = 0;
@@ -658,7 +658,7 @@ int eoship_tq_bind_corpus_opts(EosHipRuntime* rt, const EosHipTQDesc* desc, cons
     return fail();
   }
   if (n > 0) {
-    e = hipMemcpyAsync(tq->norms, norms, (size_t)n * sizeof(float), hipMemcpyHostToDevice, rt->stream);
+    e = rt->copy_async(tq->norms, norms, (size_t)n * sizeof(float), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
       hip_err(err, "hipMemcpyAsync(norms)", e);
       return fail();
@@ -666,7 +666,7 @@ int eoship_tq_bind_corpus_opts(EosHipRuntime* rt, const EosHipTQDesc* desc, cons
     void* dcodes = nullptr;
     const size_t code_bytes = (size_t)n * tq->row_bytes;
     if (rt->alloc(code_bytes, &dcodes, err) != 0) return fail();
-    e = hipMemcpyAsync(dcodes, codes, code_bytes, hipMemcpyHostToDevice, rt->stream);
+    e = rt->copy_async(dcodes, codes, code_bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
       hipFree(dcodes);
       hip_err(err, "hipMemcpyAsync(codes)", e);
@@ -729,7 +729,10 @@ int eoship_tq_bind_corpus_opts(EosHipRuntime* rt, const EosHipTQDesc* desc, cons
       if (e == hipSuccess)
         e = hipMemcpy2DAsync(tq->codes_rm, pitch, dcodes, tq->row_bytes, tq->row_bytes, (size_t)n,
                              hipMemcpyDeviceToDevice, rt->stream);
-      if (e == hipSuccess) e = hipStreamSynchronize(rt->stream);
+      if (e == hipSuccess) {
+        ++rt->n_syncs;
+        e = hipStreamSynchronize(rt->stream);
+      }
       hipFree(dcodes);
       if (e != hipSuccess) {
         hip_err(err, "hipMemcpy2DAsync(code rows)", e);
@@ -743,7 +746,7 @@ int eoship_tq_bind_corpus_opts(EosHipRuntime* rt, const EosHipTQDesc* desc, cons
       for (int k = 0; k < tq->d; ++k) rt_host[(size_t)k * tq->d + j] = desc->rotation[(size_t)j * tq->d + k];
     if (rt->alloc(rt_host.size() * sizeof(float), reinterpret_cast<void**>(&tq->rot_t), err) != 0)
       return fail();
-    e = hipMemcpy(tq->rot_t, rt_host.data(), rt_host.size() * sizeof(float), hipMemcpyHostToDevice);
+    e = rt->copy_sync(tq->rot_t, rt_host.data(), rt_host.size() * sizeof(float), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
       hip_err(err, "hipMemcpy(rotation)", e);
       return fail();
@@ -752,8 +755,7 @@ int eoship_tq_bind_corpus_opts(EosHipRuntime* rt, const EosHipTQDesc* desc, cons
   if (!map_host.empty()) {
     if (rt->alloc(map_host.size() * sizeof(long long), reinterpret_cast<void**>(&tq->id_map), err) != 0)
       return fail();
-    e = hipMemcpy(tq->id_map, map_host.data(), map_host.size() * sizeof(long long),
-                  hipMemcpyHostToDevice);
+    e = rt->copy_sync(tq->id_map, map_host.data(), map_host.size() * sizeof(long long), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
       hip_err(err, "hipMemcpy(id_map)", e);
       return fail();
@@ -826,7 +828,7 @@ int eoship_tq_share(EosHipRuntime* rt, EosHipTQ* src, EosHipTQ** out, char** err
 int eoship_tq_release(EosHipTQ* tq, char** err) {
   (void)err;
   if (tq == nullptr) return 0;
-  hipStreamSynchronize(tq->rt->stream);
+  (void)tq->rt->sync(nullptr);
   tq->free_all();
   delete tq;
   return 0;
@@ -928,11 +930,11 @@ int eoship_tq_topk(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int32_
   float* dq = reinterpret_cast<float*>(base);
   int64_t* di = reinterpret_cast<int64_t*>(base + ((qbytes + 15) & ~(size_t)15));
   float* ds = reinterpret_cast<float*>(reinterpret_cast<char*>(di) + ibytes);
-  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  hipError_t e = rt->copy_async(dq, queries, qbytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
   if (topk_device_impl(rt, tq, dq, q, k, di, ds, stats, 2, nullptr, err) != 0) return 1;
-  e = hipMemcpyAsync(ids, di, ibytes, hipMemcpyDeviceToHost, rt->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(scores, ds, sbytes, hipMemcpyDeviceToHost, rt->stream);
+  e = rt->copy_async(ids, di, ibytes, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = rt->copy_async(scores, ds, sbytes, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(results)", e);
   return rt->sync(err);
 }
@@ -948,7 +950,7 @@ int eoship_tq_scores(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int3
   const size_t qbytes = (size_t)q * tq->d * sizeof(float);
   if (tq->ensure(&tq->io, &tq->io_bytes, qbytes, err) != 0) return 1;
   float* dq = static_cast<float*>(tq->io);
-  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  hipError_t e = rt->copy_async(dq, queries, qbytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
   const int cap = tq->batch_cap();
   if (tq->id_map != nullptr) {
@@ -961,11 +963,9 @@ int eoship_tq_scores(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int3
       const int qb = std::min(cap, q - q0);
       if (tq->prepare(dq + (size_t)q0 * tq->d, qb, nullptr, err) != 0) return 1;
       if (tq->dense_scores(qb, 0, n, dots != nullptr, err) != 0) return 1;
-      if (scores) e = hipMemcpyAsync(hs.data(), tq->dense, (size_t)qb * n * sizeof(float),
-                                     hipMemcpyDeviceToHost, rt->stream);
+      if (scores) e = rt->copy_async(hs.data(), tq->dense, (size_t)qb * n * sizeof(float), hipMemcpyDeviceToHost);
       if (e == hipSuccess && dots)
-        e = hipMemcpyAsync(hd.data(), tq->dense_dots, (size_t)qb * n * sizeof(int32_t),
-                           hipMemcpyDeviceToHost, rt->stream);
+        e = rt->copy_async(hd.data(), tq->dense_dots, (size_t)qb * n * sizeof(int32_t), hipMemcpyDeviceToHost);
       if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(scores)", e);
       if (rt->sync(err) != 0) return 1;
       for (int r = 0; r < qb; ++r)
@@ -984,13 +984,11 @@ int eoship_tq_scores(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int3
     if (tq->dense_scores(qb, begin, count, dots != nullptr, err) != 0) return 1;
     const size_t rows = (size_t)qb * count;
     if (scores) {
-      e = hipMemcpyAsync(scores + (size_t)q0 * count, tq->dense, rows * sizeof(float),
-                         hipMemcpyDeviceToHost, rt->stream);
+      e = rt->copy_async(scores + (size_t)q0 * count, tq->dense, rows * sizeof(float), hipMemcpyDeviceToHost);
       if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(scores)", e);
     }
     if (dots) {
-      e = hipMemcpyAsync(dots + (size_t)q0 * count, tq->dense_dots, rows * sizeof(int32_t),
-                         hipMemcpyDeviceToHost, rt->stream);
+      e = rt->copy_async(dots + (size_t)q0 * count, tq->dense_dots, rows * sizeof(int32_t), hipMemcpyDeviceToHost);
       if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(dots)", e);
     }
     if (rt->sync(err) != 0) return 1;
@@ -1010,20 +1008,18 @@ int eoship_tq_prepare(EosHipRuntime* rt, EosHipTQ* tq, const float* queries, int
                     err) != 0)
     return 1;
   float* dq = static_cast<float*>(tq->io);
-  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  hipError_t e = rt->copy_async(dq, queries, qbytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
   const int cap = tq->batch_cap();
   for (int q0 = 0; q0 < q; q0 += cap) {
     const int qb = std::min(cap, q - q0);
     if (tq->prepare(dq + (size_t)q0 * tq->d, qb, tq->qs_buf, err) != 0) return 1;
     if (qs) {
-      e = hipMemcpyAsync(qs + (size_t)q0 * tq->d, tq->qs_buf, (size_t)qb * tq->d * sizeof(int16_t),
-                         hipMemcpyDeviceToHost, rt->stream);
+      e = rt->copy_async(qs + (size_t)q0 * tq->d, tq->qs_buf, (size_t)qb * tq->d * sizeof(int16_t), hipMemcpyDeviceToHost);
       if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(qs)", e);
     }
     if (alpha) {
-      e = hipMemcpyAsync(alpha + q0, tq->alpha, (size_t)qb * sizeof(float), hipMemcpyDeviceToHost,
-                         rt->stream);
+      e = rt->copy_async(alpha + q0, tq->alpha, (size_t)qb * sizeof(float), hipMemcpyDeviceToHost);
       if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(alpha)", e);
     }
     if (rt->sync(err) != 0) return 1;
@@ -1172,11 +1168,11 @@ int eoship_tq_maxsim_topk(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, cons
   float* dq = reinterpret_cast<float*>(base);
   int64_t* di = reinterpret_cast<int64_t*>(base + ((qbytes + 15) & ~(size_t)15));
   float* ds = reinterpret_cast<float*>(reinterpret_cast<char*>(di) + ibytes);
-  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  hipError_t e = rt->copy_async(dq, queries, qbytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
   if (maxsim_topk_impl(rt, tq, doc_len, dq, q, tq_tokens, k, di, ds, err) != 0) return 1;
-  e = hipMemcpyAsync(ids, di, ibytes, hipMemcpyDeviceToHost, rt->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(scores, ds, sbytes, hipMemcpyDeviceToHost, rt->stream);
+  e = rt->copy_async(ids, di, ibytes, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = rt->copy_async(scores, ds, sbytes, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(results)", e);
   return rt->sync(err);
 }
@@ -1194,7 +1190,7 @@ int eoship_tq_maxsim_scores(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, co
   const size_t qbytes = (size_t)q * tq_tokens * tq->d * sizeof(float);
   if (tq->ensure(&tq->io, &tq->io_bytes, qbytes, err) != 0) return 1;
   float* dq = static_cast<float*>(tq->io);
-  hipError_t e = hipMemcpyAsync(dq, queries, qbytes, hipMemcpyHostToDevice, rt->stream);
+  hipError_t e = rt->copy_async(dq, queries, qbytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
   const int per = tq->maxsim_nqg();
   if (tq->ensure(reinterpret_cast<void**>(&tq->dense), &tq->dense_bytes,
@@ -1205,8 +1201,8 @@ int eoship_tq_maxsim_scores(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, co
     if (tq->maxsim_prepare(dq + (size_t)q0 * tq_tokens * tq->d, qp, tq_tokens, err) != 0 ||
         tq->maxsim_pass(0, qp, doc_len, doc_begin, doc_count, tq->dense, err) != 0)
       return 1;
-    e = hipMemcpyAsync(scores + (size_t)q0 * doc_count, tq->dense,
-                       (size_t)qp * doc_count * sizeof(float), hipMemcpyDeviceToHost, rt->stream);
+    e = rt->copy_async(scores + (size_t)q0 * doc_count, tq->dense,
+                       (size_t)qp * doc_count * sizeof(float), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(scores)", e);
     if (rt->sync(err) != 0) return 1;
   }
@@ -1356,8 +1352,8 @@ int eoship_tq_parents_bind(EosHipRuntime* rt, EosHipTQ* tq, const int64_t* offse
     delete P;
     return 1;
   }
-  e = hipMemcpy(P->off, offsets, ob, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(P->l1p, l1p.data(), lb, hipMemcpyHostToDevice);
+  e = rt->copy_sync(P->off, offsets, ob, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = rt->copy_sync(P->l1p, l1p.data(), lb, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     delete P;
     return hip_err(err, "hipMemcpy(parent offsets)", e);
@@ -1369,7 +1365,7 @@ int eoship_tq_parents_bind(EosHipRuntime* rt, EosHipTQ* tq, const int64_t* offse
 int eoship_tq_parents_release(EosHipTQParents* parents, char** err) {
   (void)err;
   if (parents == nullptr) return 0;
-  hipStreamSynchronize(parents->tq->rt->stream);
+  (void)parents->tq->rt->sync(nullptr);
   delete parents;
   return 0;
 }
@@ -1410,16 +1406,15 @@ int eoship_tq_parent_topk(EosHipRuntime* rt, EosHipTQParents* parents, const flo
   int64_t* db = di + rows;
   float* ds = reinterpret_cast<float*>(db + rows);
   float* dbs = ds + rows;
-  hipError_t e = hipMemcpyAsync(dq, queries, (size_t)q * d * sizeof(float), hipMemcpyHostToDevice,
-                                rt->stream);
+  hipError_t e = rt->copy_async(dq, queries, (size_t)q * d * sizeof(float), hipMemcpyHostToDevice);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(queries)", e);
   if (parent_topk_impl(rt, parents, dq, q, k, top_n, child_count_penalty, di, ds, db, dbs, err) != 0)
     return 1;
-  e = hipMemcpyAsync(parent_ids, di, rows * 8, hipMemcpyDeviceToHost, rt->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(scores, ds, rows * 4, hipMemcpyDeviceToHost, rt->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(best_child, db, rows * 8, hipMemcpyDeviceToHost, rt->stream);
+  e = rt->copy_async(parent_ids, di, rows * 8, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = rt->copy_async(scores, ds, rows * 4, hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = rt->copy_async(best_child, db, rows * 8, hipMemcpyDeviceToHost);
   if (e == hipSuccess)
-    e = hipMemcpyAsync(best_child_score, dbs, rows * 4, hipMemcpyDeviceToHost, rt->stream);
+    e = rt->copy_async(best_child_score, dbs, rows * 4, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(results)", e);
   return rt->sync(err);
 }
@@ -1493,14 +1488,12 @@ int eoship_tq_encode(EosHipRuntime* rt, EosHipTQ* tq, const float* x, int64_t n,
   float* dn = reinterpret_cast<float*>(base + xb + cb);
   for (int64_t i0 = 0; i0 < n; i0 += chunk) {
     const int64_t cnt = std::min(chunk, n - i0);
-    hipError_t e = hipMemcpyAsync(dx, x + (size_t)i0 * tq->d, (size_t)cnt * tq->d * sizeof(float),
-                                  hipMemcpyHostToDevice, rt->stream);
+    hipError_t e = rt->copy_async(dx, x + (size_t)i0 * tq->d, (size_t)cnt * tq->d * sizeof(float), hipMemcpyHostToDevice);
     if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(vectors)", e);
     if (encode_impl(rt, tq, dx, cnt, dc, dn, err) != 0) return 1;
-    e = hipMemcpyAsync(codes + (size_t)i0 * tq->row_bytes, dc, (size_t)cnt * tq->row_bytes,
-                       hipMemcpyDeviceToHost, rt->stream);
+    e = rt->copy_async(codes + (size_t)i0 * tq->row_bytes, dc, (size_t)cnt * tq->row_bytes, hipMemcpyDeviceToHost);
     if (e == hipSuccess)
-      e = hipMemcpyAsync(norms + i0, dn, (size_t)cnt * sizeof(float), hipMemcpyDeviceToHost, rt->stream);
+      e = rt->copy_async(norms + i0, dn, (size_t)cnt * sizeof(float), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_err(err, "hipMemcpyAsync(codes)", e);
     if (rt->sync(err) != 0) return 1;
   }
@@ -2058,7 +2051,7 @@ int eoship_tq_ip_bind_corpus(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
   // turboquant_quantized_vector.go:25-49), as the MSE bind applies it.
   {
     std::vector<float> hn((size_t)n);
-    hipError_t e = hipMemcpy(hn.data(), d_norms, (size_t)n * 4, hipMemcpyDeviceToHost);
+    hipError_t e = rt->copy_sync(hn.data(), d_norms, (size_t)n * 4, hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_err(err, "hipMemcpy(norms)", e);
     for (int64_t i = 0; i < n; ++i) {
       const float v = hn[(size_t)i];
@@ -2167,7 +2160,7 @@ int eoship_tq_ip_topk_device(EosHipRuntime* rt, EosHipTQIP* ip, const float* d_q
 int eoship_tq_ip_release(EosHipTQIP* ip, char** err) {
   (void)err;
   if (ip == nullptr) return 0;
-  (void)hipStreamSynchronize(ip->rt->stream);
+  (void)ip->rt->sync(nullptr);
   delete ip;
   return 0;
 }

@@ -118,6 +118,16 @@ class Runtime:
         _lib.call("eoship_profile_read", self.handle, prefix.encode(), C.byref(n), C.byref(ms))
         return n.value, ms.value
 
+    def accounting(self, reset: bool = False) -> dict:
+        """Execution accounting since creation or the last reset (the keys of
+        the reference's StepDispatchResult.Metadata / ExecutionAccounting)."""
+        a = _lib.EosHipAccounting()
+        _lib.call("eoship_accounting_read", self.handle, C.byref(a), C.c_int32(int(reset)))
+        return {"device_execution": bool(a.device_execution), "execution_mode": "hip_device",
+                "kernel_launches": a.kernel_launches, "uploaded_bytes": a.uploaded_bytes,
+                "downloaded_bytes": a.downloaded_bytes, "sync_count": a.sync_count,
+                "graph_captures": a.graph_captures, "graph_replays": a.graph_replays}
+
     def profile_samples(self, prefix: str) -> np.ndarray:
         """Per-launch durations (ms) of the recorded launches matching prefix."""
         n = C.c_int64()

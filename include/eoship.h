@@ -90,6 +90,29 @@ int eoship_profile_reset(EosHipRuntime* rt, char** err);
  * (no counterpart in the reference, whose profiler keeps totals only). */
 int eoship_profile_samples(EosHipRuntime* rt, const char* prefix, float* ms, int64_t cap,
                            int64_t* count, char** err);
+/* Execution accounting of a runtime since its creation or the last reset:
+ * the per-step counters the reference's executor reports in
+ * StepDispatchResult.Metadata and sums into ExecutionAccounting
+ * (runtime/backend/symbolic.go:174-216, backend.go:1376-1401). A caller reads
+ * it before and after a call and reports the difference for that call. Every
+ * call of this library runs on the device (device_execution = 1, no host
+ * fallback: there is no fallback_reason); graph captures and replays are
+ * always 0 (the library captures no graphs). uploaded_bytes / downloaded_bytes
+ * count the host <-> device copies the library makes (bind-time uploads,
+ * the host-API entry points' inputs and outputs, status reads); sync_count
+ * the host waits it makes. */
+typedef struct {
+  int64_t kernel_launches;
+  int64_t uploaded_bytes;
+  int64_t downloaded_bytes;
+  int64_t sync_count;
+  int64_t graph_captures;
+  int64_t graph_replays;
+  int32_t device_execution;
+  int32_t reserved;
+} EosHipAccounting;
+int eoship_accounting_read(EosHipRuntime* rt, EosHipAccounting* out, int32_t reset, char** err);
+
 /* Stream-level timer: records an event now; eoship_timer_elapsed gives the
  * milliseconds between two recorded marks (synchronising the second). */
 int eoship_timer_mark(EosHipRuntime* rt, int slot, char** err);
