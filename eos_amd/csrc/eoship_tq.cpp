@@ -1682,18 +1682,51 @@ int eoship_tq_reconstruct_rerank_device(EosHipRuntime* rt, const EosHipTQCodes* 
 
 // Query preparation of the inner-product layout into qs / ys / alpha / beta:
 // qr = R q and y = S qr as tiled f64 matrix-vector launches (eos_tq_ip_matvec),
-// then one quantize workgroup per query (eos_tq_ip_quant).
+// then one quantize workgroup per column (eos_tq_ip_quant); with `frag` the
+// quantize also writes the scan's query fragments, ysum and the filter state
+// of frag->ncols columns (qs / ys may then be NULL).
 // qr, y: device scratch of q * d doubles each.
+struct IpFragOut {
+  int8_t* bfrag;
+  int* ysum;
+  float* tau;
+  uint32_t* cand_count;
+  int ks, nqg;
+};
 static int ip_prepare_launch(EosHipRuntime* rt, const TqIpArgs& a, int q, double* qr, double* y,
-                             char** err) {
+                             const IpFragOut* frag, char** err) {
+  if (q <= 0) return 0;
   const dim3 grid((unsigned)((a.d + 31) / 32), (unsigned)((q + 7) / 8));
   TqIpMatArgs m1{a.rot_t, a.queries, nullptr, qr, q, a.d};
   TqIpMatArgs m2{a.qjl_t, nullptr, qr, y, q, a.d};
-  TqIpQuantArgs qa{qr, y, a.qs, a.ys, a.alpha, a.beta, q, a.d, a.qmax, a.qmax2, a.cb_scale};
+  TqIpQuantArgs qa;
+  memset(&qa, 0, sizeof(qa));
+  qa.qr = qr;
+  qa.y = y;
+  qa.qs = a.qs;
+  qa.ys = a.ys;
+  qa.alpha = a.alpha;
+  qa.beta = a.beta;
+  qa.q = q;
+  qa.d = a.d;
+  qa.qmax = a.qmax;
+  qa.qmax2 = a.qmax2;
+  qa.cb_scale = a.cb_scale;
+  int ncols = q;
+  if (frag != nullptr) {
+    qa.bfrag = frag->bfrag;
+    qa.ysum = frag->ysum;
+    qa.tau = frag->tau;
+    qa.cand_count = frag->cand_count;
+    qa.ks = frag->ks;
+    qa.nqg = frag->nqg;
+    ncols = 32 * frag->nqg;
+  }
   if (rt->launch("eos_tq_ip_matvec", grid, dim3(256), 0, &m1, err, "tq_ip_prepare") != 0 ||
       rt->launch("eos_tq_ip_matvec", grid, dim3(256), 0, &m2, err, "tq_ip_prepare") != 0)
     return 1;
-  return rt->launch("eos_tq_ip_quant", dim3((unsigned)q), dim3(256), 0, &qa, err, "tq_ip_prepare");
+  return rt->launch("eos_tq_ip_quant", dim3((unsigned)ncols), dim3(256), 0, &qa, err,
+                    "tq_ip_prepare");
 }
 
 static int ip_spec_check(EosHipRuntime* rt, const EosHipTQIPSpec* spec, TqIpArgs* a,
@@ -1787,7 +1820,7 @@ int eoship_tq_ip_scores_device(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
   a.scores = d_scores;
   a.n = n;
   a.q = q;
-  if (ip_prepare_launch(rt, a, q, qr, yv, err) != 0 ||
+  if (ip_prepare_launch(rt, a, q, qr, yv, nullptr, err) != 0 ||
       rt->launch("eos_tq_ip_scores", dim3((unsigned)((n + 255) / 256), (unsigned)((q + 7) / 8)),
                  dim3(256), 0, &a, err, "tq_ip_scores") != 0)
     return 1;
@@ -1846,8 +1879,8 @@ int eoship_tq_fp16_rerank_device(EosHipRuntime* rt, const float* d_queries, int3
 // inner-product estimate over IPQuantized documents, as
 // topTurboQuantRetrievalScoresWithStats computes it with InnerProductPrepared
 // (:1853-1887). Per batch of <= 64 queries (32 when the dimension needs more
-// than 12 K-steps): eos_tq_ip_matvec + eos_tq_ip_quant (int grids of R q and S R q),
-// eos_tq_ip_frag (MFMA fragments), a sample scan of tile maxima and
+// than 12 K-steps): eos_tq_ip_matvec (R q, S R q) + eos_tq_ip_quant (their int
+// grids as MFMA fragments), a sample scan of tile maxima and
 // eos_tq_threshold, the filter scan (exact scores, keep >= tau),
 // eos_tq_finalize, and the exact fallback gated on its flags (dense scan +
 // eos_tq_row_select).
@@ -1864,8 +1897,6 @@ struct EosHipTQIP {
   float* norms = nullptr;
   float* resnorms = nullptr;
   // per-batch scratch
-  int* qs = nullptr;
-  int* ys = nullptr;
   float* alpha = nullptr;
   float* beta = nullptr;
   int* ysum = nullptr;
@@ -1883,8 +1914,8 @@ struct EosHipTQIP {
   int batch_cap() const { return 32 * nqg; }
 
   ~EosHipTQIP() {
-    void* p[] = {packed, norms, resnorms, qs,         ys,     alpha, beta, ysum, bfrag,
-                 tau,    cand,  cand_count, status, samp, dense, qr,    yv};
+    void* p[] = {packed, norms,      resnorms, alpha, beta,  ysum, bfrag, tau,
+                 cand,   cand_count, status,   samp,  dense, qr,   yv};
     for (void* x : p)
       if (x) (void)hipFree(x);
   }
@@ -1933,8 +1964,6 @@ struct EosHipTQIP {
     a.queries = d_queries;
     a.rot_t = rot_t;
     a.qjl_t = qjl_t;
-    a.qs = qs;
-    a.ys = ys;
     a.alpha = alpha;
     a.beta = beta;
     a.d = d;
@@ -1942,21 +1971,8 @@ struct EosHipTQIP {
     a.qmax = qmax;
     a.qmax2 = qmax2;
     a.cb_scale = cb_scale;
-    if (ip_prepare_launch(rt, a, qb, qr, yv, err) != 0) return 1;
-    TqIpFragArgs f;
-    memset(&f, 0, sizeof(f));
-    f.qs = qs;
-    f.ys = ys;
-    f.bfrag = bfrag;
-    f.ysum = ysum;
-    f.tau = tau;
-    f.cand_count = cand_count;
-    f.q = qb;
-    f.d = d;
-    f.ks = ks;
-    f.nqg = nqg;
-    return rt->launch("eos_tq_ip_frag", dim3((unsigned)(32 * nqg)), dim3(256), 0, &f, err,
-                      "tq_ip_frag");
+    const IpFragOut f{bfrag, ysum, tau, cand_count, ks, nqg};
+    return ip_prepare_launch(rt, a, qb, qr, yv, &f, err);
   }
 
   int topk_batch(const float* d_queries, int qb, int kk, int64_t* d_ids, float* d_scores,
@@ -2093,8 +2109,6 @@ int eoship_tq_ip_bind_corpus(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
   if (rt->alloc((size_t)ip->ntiles * (ks / 2) * 64 * 16, reinterpret_cast<void**>(&ip->packed), err) ||
       rt->alloc((size_t)ip->ntiles * kTile * 4, reinterpret_cast<void**>(&ip->norms), err) ||
       rt->alloc((size_t)ip->ntiles * kTile * 4, reinterpret_cast<void**>(&ip->resnorms), err) ||
-      rt->alloc((size_t)cols * ip->d * 4, reinterpret_cast<void**>(&ip->qs), err) ||
-      rt->alloc((size_t)cols * ip->d * 4, reinterpret_cast<void**>(&ip->ys), err) ||
       rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->alpha), err) ||
       rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->beta), err) ||
       rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->ysum), err) ||

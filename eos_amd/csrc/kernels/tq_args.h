@@ -266,21 +266,6 @@ struct TqIpPackArgs {
   int d, ks, bits, row_bytes, sign_bytes;
 };
 
-// Query fragments of the inner-product scan from the int grids of
-// eos_tq_ip_quant: per K-step and 32-column group g, blocks 4 g + 0 / + 1
-// (MSE grid Qs = 256 hi + lo) and 4 g + 2 / + 3 (QJL grid Ys likewise); the
-// sum of Ys over the dimensions (D_qjl = 2 sum_{bit = 1} Ys - sum Ys); the
-// filter state of each column reset (tau = -inf, no kept candidates).
-struct TqIpFragArgs {
-  const int* qs;           // [q][d]
-  const int* ys;           // [q][d]
-  int8_t* bfrag;           // [ks][4 * nqg][64][16]
-  int* ysum;               // [32 * nqg]
-  float* tau;              // [32 * nqg]
-  uint32_t* cand_count;    // [32 * nqg]
-  int q, d, ks, nqg;
-};
-
 // Inner-product scan: exact D_mse = sum Qs_j C[code_j] and D_qjl = sum Ys_i
 // (2 bit_i - 1) on int8 MFMA, score = ((float)D_mse alpha + ResNorm
 // ((float)D_qjl beta)) Norm; modes as TqScanArgs (0 dense, 1 keep score >=
@@ -314,17 +299,25 @@ struct TqIpMatArgs {
   int q, d;
 };
 
-// Per query column c < q: Qs and alpha from qr, Ys and beta from y. One
-// workgroup per column.
+// Per query column c < ncols (the grid): Qs and alpha from qr, Ys and beta
+// from y (zero columns past q). qs / ys receive the grids when non-NULL; with
+// bfrag the scan's query fragments [ks][4 * nqg][64][16] (per 32-column
+// group g: MSE hi, MSE lo, QJL hi, QJL lo), ysum, tau (-inf) and cand_count
+// (0) of every column too.
 struct TqIpQuantArgs {
   const double* qr;        // [q][d]
   const double* y;         // [q][d]
-  int* qs;                 // [q][d]
-  int* ys;                 // [q][d]
+  int* qs;                 // [q][d] or NULL
+  int* ys;                 // [q][d] or NULL
   float* alpha;
   float* beta;
+  int8_t* bfrag;           // or NULL
+  int* ysum;               // [32 * nqg]
+  float* tau;              // [32 * nqg]
+  uint32_t* cand_count;    // [32 * nqg]
   int q, d, qmax, qmax2;
   float cb_scale;
+  int ks, nqg;
 };
 
 #endif  // EOSHIP_TQ_ARGS_H

@@ -565,39 +565,58 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_encode_ip(TqIpArgs a) {
 // Query preparation of the inner-product layout: q' = R q and y = S q' (f64,
 // one fma chain per coordinate in k order), then eos_tq_ip_quant. These are
 // the matrix-vector products, workgroup (x, y) computing rows [32 x, 32 x +
-// 32) for the 8 columns [8 y, 8 y + 8): the columns staged in LDS as f64, the
-// matrix in 32 x 32 chunks.
+// 32) for the 8 columns [8 y, 8 y + 8): the columns staged in LDS as f64 and
+// the matrix slice (rows j, all k) in chunks of kPrepK values of k, with
+// every load of a stage issued before any is stored (one memory round trip
+// per stage; d <= kPrepK takes one stage).
 extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_matvec(TqIpMatArgs a) {
   __shared__ double xin[8 * kIpDMax];
-  __shared__ float ms[32 * 33];
+  __shared__ float ms[kPrepK * kPrepJ];
   const int tid = threadIdx.x, jj = tid & 31, cl = tid >> 5;
-  const int j0 = blockIdx.x * 32, c0 = blockIdx.y * 8;
+  const int j0 = blockIdx.x * kPrepJ, c0 = blockIdx.y * 8;
   const int d = a.d;
-  for (int i = tid; i < 8 * d; i += 256) {
-    const int c = i / d, k = i - c * d;
-    double v = 0.0;
-    if (c0 + c < a.q)
-      v = a.in64 != nullptr ? a.in64[(size_t)(c0 + c) * d + k] : (double)a.in32[(size_t)(c0 + c) * d + k];
-    xin[c * kIpDMax + k] = v;
+  {
+    // Loads from clamped positions first, the validity test afterwards (a
+    // load under a per-lane condition waits for its data before the next).
+    constexpr int R = kIpDMax / 256;
+    double xv[8][R];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int src = min(c0 + c, a.q - 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const size_t o = (size_t)src * d + min(tid + 256 * r, d - 1);
+        xv[c][r] = a.in64 != nullptr ? a.in64[o] : (double)a.in32[o];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (tid + 256 * r < d) xin[c * kIpDMax + tid + 256 * r] = c0 + c < a.q ? xv[c][r] : 0.0;
   }
-  __syncthreads();
   const int j = j0 + jj, c = c0 + cl;
   double acc = 0.0;
   if (a.mt == nullptr) {
+    __syncthreads();
     acc = j < d ? xin[cl * kIpDMax + j] : 0.0;
   } else {
-    for (int k0 = 0; k0 < d; k0 += 32) {
-      // chunk rows k0 .. k0 + 31 of mt (columns j0 .. j0 + 31), zero past d
+    for (int k0 = 0; k0 < d; k0 += kPrepK) {
+      const int kn = min(kPrepK, d - k0);
+      float tmp[kPrepK * kPrepJ / 256];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int kk = cl + 8 * r, k = k0 + kk;
-        ms[kk * 33 + jj] = (k < d && j < d) ? a.mt[(size_t)k * d + j] : 0.0f;
-      }
+      for (int r = 0; r < kPrepK * kPrepJ / 256; ++r)
+        tmp[r] = a.mt[(size_t)(k0 + min(cl + 8 * r, kn - 1)) * d + min(j, d - 1)];
+#pragma unroll
+      for (int r = 0; r < kPrepK * kPrepJ / 256; ++r)
+        tmp[r] = (cl + 8 * r < kn && j < d) ? tmp[r] : 0.0f;
+      __syncthreads();  // the previous chunk consumed; xin visible
+#pragma unroll
+      for (int r = 0; r < kPrepK * kPrepJ / 256; ++r) ms[tid + 256 * r] = tmp[r];
       __syncthreads();
-      const int kn = min(32, d - k0);
-      for (int kk = 0; kk < kn; ++kk)
-        acc = fma((double)ms[kk * 33 + jj], xin[cl * kIpDMax + k0 + kk], acc);
-      __syncthreads();
+      const double* xc = xin + cl * kIpDMax + k0;
+#pragma unroll 16
+      for (int kk = 0; kk < kn; ++kk) acc = fma((double)ms[kk * kPrepJ + jj], xc[kk], acc);
     }
   }
   if (c < a.q && j < d) a.out[(size_t)c * d + j] = acc;
@@ -607,10 +626,18 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_matvec(TqIpMatArgs a
 // grid Qs = rint(q' qmax / max|q'|) with alpha = (max|q'| / qmax) s_c (as
 // eos_tq_rotate / eos_tq_quantize), the QJL grid Ys = rint(y qmax2 / max|y|)
 // and beta = (max|y| / qmax2) sqrt(pi / 2) / d; both clamped to +-qmax.
+// One workgroup per column c < ncols (columns past q are zero). The grids go
+// to qs / ys when given; with bfrag, also the scan's query fragments (per
+// K-step and 32-column group g: blocks 4 g + 0 / + 1 the MSE grid's int8
+// high / low halves Qs = 256 hi + lo, blocks 4 g + 2 / + 3 the QJL grid's),
+// the sum of Ys over the dimensions (D_qjl = 2 sum_{bit = 1} Ys - sum Ys) and
+// the column's filter state reset (tau = -inf, no kept candidates).
 extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_quant(TqIpQuantArgs a) {
   __shared__ double red[4];
+  __shared__ int ired[4];
   const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int d = a.d;
+  const bool live = c < a.q;
   auto block_max = [&](double m) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmax(m, __shfl_xor(m, o));
@@ -620,30 +647,64 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_quant(TqIpQuantArgs 
     __syncthreads();
     return r;
   };
-  const double* qr = a.qr + (size_t)c * d;
-  const double* y = a.y + (size_t)c * d;
+  const double* qr = a.qr + (size_t)(live ? c : 0) * d;
+  const double* y = a.y + (size_t)(live ? c : 0) * d;
   double m1 = 0.0, m2 = 0.0;
-  for (int j = tid; j < d; j += 256) {
-    m1 = fmax(m1, fabs(qr[j]));
-    m2 = fmax(m2, fabs(y[j]));
+  if (live) {
+    for (int j = tid; j < d; j += 256) {
+      m1 = fmax(m1, fabs(qr[j]));
+      m2 = fmax(m2, fabs(y[j]));
+    }
   }
   const double mq = block_max(m1);
   const double my = block_max(m2);
   const double inv = mq > 0.0 ? (double)a.qmax / mq : 0.0;
   const double inv2 = my > 0.0 ? (double)a.qmax2 / my : 0.0;
-  for (int j = tid; j < d; j += 256) {
-    double v = rint(qr[j] * inv);
-    v = fmin(fmax(v, (double)-a.qmax), (double)a.qmax);
-    a.qs[(size_t)c * d + j] = (int)v;
-    double u = rint(y[j] * inv2);
-    u = fmin(fmax(u, (double)-a.qmax2), (double)a.qmax2);
-    a.ys[(size_t)c * d + j] = (int)u;
+  const int dpad = a.bfrag != nullptr ? a.ks * 32 : d;
+  const int gq = c >> 5, col = c & 31, ncb = 4 * a.nqg;
+  int ysum = 0;
+  for (int j = tid; j < dpad; j += 256) {
+    int qv = 0, yv = 0;
+    if (live && j < d) {
+      double v = rint(qr[j] * inv);
+      v = fmin(fmax(v, (double)-a.qmax), (double)a.qmax);
+      qv = (int)v;
+      double u = rint(y[j] * inv2);
+      u = fmin(fmax(u, (double)-a.qmax2), (double)a.qmax2);
+      yv = (int)u;
+      if (a.qs != nullptr) a.qs[(size_t)c * d + j] = qv;
+      if (a.ys != nullptr) a.ys[(size_t)c * d + j] = yv;
+    }
+    ysum += yv;
+    if (a.bfrag != nullptr) {
+      const int qlo = ((qv + 128) & 255) - 128, qhi = (qv - qlo) >> 8;
+      const int ylo = ((yv + 128) & 255) - 128, yhi = (yv - ylo) >> 8;
+      const int s = j >> 5, g = (j >> 4) & 1, i = j & 15;
+      int8_t* base = a.bfrag + ((size_t)(s * ncb + 4 * gq) * 64 + col + 32 * g) * 16 + i;
+      base[0] = (int8_t)qhi;
+      base[64 * 16] = (int8_t)qlo;
+      base[2 * 64 * 16] = (int8_t)yhi;
+      base[3 * 64 * 16] = (int8_t)ylo;
+    }
+  }
+  if (a.bfrag != nullptr) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ysum += __shfl_xor(ysum, o);
+    if (lane == 0) ired[w] = ysum;
+    __syncthreads();
   }
   if (tid == 0) {
-    a.alpha[c] = mq > 0.0 ? (float)((mq / (double)a.qmax) * (double)a.cb_scale) : 0.0f;
-    const double half_pi = 1.5707963267948966;
-    a.beta[c] = my > 0.0 ? (float)((my / (double)a.qmax2) * __builtin_sqrt(half_pi) / (double)d)
-                         : 0.0f;
+    if (live) {
+      a.alpha[c] = mq > 0.0 ? (float)((mq / (double)a.qmax) * (double)a.cb_scale) : 0.0f;
+      const double half_pi = 1.5707963267948966;
+      a.beta[c] = my > 0.0 ? (float)((my / (double)a.qmax2) * __builtin_sqrt(half_pi) / (double)d)
+                           : 0.0f;
+    }
+    if (a.bfrag != nullptr) {
+      a.ysum[c] = ired[0] + ired[1] + ired[2] + ired[3];
+      a.tau[c] = -__builtin_inff();
+      a.cand_count[c] = 0u;
+    }
   }
 }
 
@@ -1215,40 +1276,6 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_pack(TqIpPackArgs a)
   }
 }
 
-// Query fragments of the inner-product scan (TqIpFragArgs), one workgroup per
-// query column c (zero columns past q): Qs and Ys split as 256 hi + lo with
-// int8 halves, their sum of Ys, and the column's filter state reset.
-extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_frag(TqIpFragArgs a) {
-  __shared__ int red[4];
-  const int c = blockIdx.x, tid = threadIdx.x;
-  const int gq = c >> 5, col = c & 31, ncb = 4 * a.nqg;
-  const bool live = c < a.q;
-  int ysum = 0;
-  for (int j = tid; j < a.ks * 32; j += 256) {
-    const int qv = (live && j < a.d) ? a.qs[(size_t)c * a.d + j] : 0;
-    const int yv = (live && j < a.d) ? a.ys[(size_t)c * a.d + j] : 0;
-    ysum += yv;
-    const int qlo = ((qv + 128) & 255) - 128, qhi = (qv - qlo) >> 8;
-    const int ylo = ((yv + 128) & 255) - 128, yhi = (yv - ylo) >> 8;
-    const int s = j >> 5, g = (j >> 4) & 1, i = j & 15;
-    const int lane = col + 32 * g;
-    int8_t* base = a.bfrag + ((size_t)(s * ncb + 4 * gq) * 64 + lane) * 16 + i;
-    base[0] = (int8_t)qhi;
-    base[64 * 16] = (int8_t)qlo;
-    base[2 * 64 * 16] = (int8_t)yhi;
-    base[3 * 64 * 16] = (int8_t)ylo;
-  }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ysum += __shfl_xor(ysum, o);
-  if ((tid & 63) == 0) red[tid >> 6] = ysum;
-  __syncthreads();
-  if (tid == 0) {
-    a.ysum[c] = red[0] + red[1] + red[2] + red[3];
-    a.tau[c] = -__builtin_inff();
-    a.cand_count[c] = 0u;
-  }
-}
-
 namespace {
 
 // 8-entry int8 lookup of the 3-bit codes and 0/1 bytes of the sign bits of
@@ -1273,8 +1300,6 @@ EOS_DEV void ip_decode(uint32_t L, uint32_t HS, uint32_t lut0, uint32_t lut1, v4
 template <int KS, int NQG>
 EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
   constexpr int NCB = 4 * NQG, NQ = 32 * NQG, NTH = 512, NWV = NTH / 64, NLOAD = KS / 2;
-  constexpr bool FILTER_OK = true;
-  (void)FILTER_OK;
   __shared__ v4i sb[KS * NCB * 64];
   __shared__ uint32_t lc_cnt[NQ];
   __shared__ u64 lc_buf[NQ * kLdsSlots];
