@@ -142,6 +142,11 @@ struct EosHipTQ {
   double* ms_qrot = nullptr;
   size_t ms_qrot_bytes = 0;
   int ms_ncb = 0;
+  float* ms_lonorm = nullptr;  // [token columns] ||lo||_2 (bound filter)
+  size_t ms_lonorm_bytes = 0;
+  // bound-filtered MaxSim top-k of a chunk (carved by maxsim_filtered)
+  void* ms_ws = nullptr;
+  size_t ms_ws_bytes = 0;
   // chunked row selection: per-chunk top-k keys, then per row the list
   // length and finalize status
   unsigned long long* sel_keys = nullptr;
@@ -172,7 +177,8 @@ struct EosHipTQ {
 
   void free_all() {
     void* scratch[] = {qrot, bfrag, alpha, tau, cand, cand_count, status, samp, dense, dense_dots,
-                       qs_buf, lonorm, io, sel_keys, sel_aux, ms_bfrag, ms_alpha, ms_qrot};
+                       qs_buf, lonorm, io, sel_keys, sel_aux, ms_bfrag, ms_alpha, ms_qrot,
+                       ms_lonorm, ms_ws};
     for (void* p : scratch)
       if (p) hipFree(p);
     if (corpus_refs != nullptr && --*corpus_refs > 0) return;
@@ -307,13 +313,17 @@ struct EosHipTQ {
   // Prepares nq queries of tq tokens (source rows [nq * tq][d]) at once: query
   // g is the 32-column group g (tokens past tq are zero columns), rounded up
   // to whole passes of maxsim_nqg() groups.
-  int maxsim_prepare(const float* d_src, int nq, int tq, char** err) {
+  // With `bounds` also each column's ||lo||_2 (ms_lonorm) for the high-half
+  // bound filter.
+  int maxsim_prepare(const float* d_src, int nq, int tq, char** err, bool bounds = false) {
     const int per = maxsim_nqg();
     const int groups = (nq + per - 1) / per * per;
     const size_t cols = (size_t)groups * 32;
     if (ensure(reinterpret_cast<void**>(&ms_bfrag), &ms_bfrag_bytes, (size_t)ks * 2 * groups * 64 * 16,
                err) != 0 ||
         ensure(reinterpret_cast<void**>(&ms_alpha), &ms_alpha_bytes, cols * sizeof(float), err) != 0 ||
+        (bounds && ensure(reinterpret_cast<void**>(&ms_lonorm), &ms_lonorm_bytes,
+                          cols * sizeof(float), err) != 0) ||
         (rot_t != nullptr && ensure(reinterpret_cast<void**>(&ms_qrot), &ms_qrot_bytes,
                                     cols * (size_t)d * sizeof(double), err) != 0))
       return 1;
@@ -323,7 +333,47 @@ struct EosHipTQ {
     p.bfrag = ms_bfrag;
     p.alpha = ms_alpha;
     p.qrot = ms_qrot;
+    p.lonorm = bounds ? ms_lonorm : nullptr;
     return prepare_into(&p, d_src, nq * tq, groups, 32, tq, nullptr, err);
+  }
+
+  // Arguments of a MaxSim launch over the prepared chunk's groups [g0, g0 +
+  // groups) (passes of maxsim_nqg() groups on blockIdx.y).
+  TqMaxsimArgs maxsim_args(int g0, int groups, int doc_len) const {
+    TqMaxsimArgs m;
+    memset(&m, 0, sizeof(m));
+    m.packed = static_cast<const int32_t*>(packed);
+    m.norms = norms;
+    m.bfrag = ms_bfrag;
+    m.alpha = ms_alpha + (size_t)g0 * 32;
+    m.frag_ncb = ms_ncb;
+    m.frag_cb0 = 2 * g0;
+    m.tiles_per_doc = doc_len / kTile;
+    m.groups = groups;
+    m.lut0 = lut[0];
+    m.lut1 = lut[1];
+    m.lut2 = lut[2];
+    m.lut3 = lut[3];
+    return m;
+  }
+
+  // Launches MaxSim kernel `hi` (bound filter) or exact over `docs` documents
+  // per pass, for m.groups groups in passes of maxsim_nqg().
+  int maxsim_launch(TqMaxsimArgs* m, bool hi, int64_t docs, const char* label, char** err) {
+    const int nqg = maxsim_nqg();
+    char name[64];
+    snprintf(name, sizeof(name), "eos_tq_maxsim_b%d_k%d_g%d%s", bits, ks, nqg, hi ? "_h" : "");
+    // As many resident workgroups as the kernel's registers allow (three
+    // waves per SIMD for most variants), each wave striding over documents;
+    // the passes share them.
+    int per_cu = 2;
+    if (rt->blocks_per_cu(name, 256, 0, &per_cu, err) != 0) return 1;
+    const int passes = (m->groups + nqg - 1) / nqg;
+    int64_t blocks = (docs + 3) / 4;
+    const int64_t maxb = std::max<int64_t>(1, (int64_t)rt->compute_units * per_cu / passes);
+    if (blocks > maxb) blocks = maxb;
+    if (blocks < 1) blocks = 1;
+    return rt->launch(name, dim3((unsigned)blocks, (unsigned)passes), dim3(256), 0, m, err, label);
   }
 
   // Doc scores of the prepared queries [q0, q0 + qp) (qp <= maxsim_nqg(),
@@ -331,36 +381,12 @@ struct EosHipTQ {
   // out [qp][ndocs].
   int maxsim_pass(int q0, int qp, int doc_len, int64_t doc_begin, int64_t ndocs, float* out,
                   char** err) {
-    const int nqg = maxsim_nqg();
-    TqMaxsimArgs m;
-    memset(&m, 0, sizeof(m));
-    m.packed = static_cast<const int32_t*>(packed);
-    m.norms = norms;
-    m.bfrag = ms_bfrag;
-    m.alpha = ms_alpha + (size_t)q0 * 32;
-    m.frag_ncb = ms_ncb;
-    m.frag_cb0 = 2 * q0;
+    TqMaxsimArgs m = maxsim_args(q0, qp, doc_len);
     m.out = out;
     m.doc_begin = doc_begin;
     m.ndocs = ndocs;
     m.out_stride = ndocs;
-    m.tiles_per_doc = doc_len / kTile;
-    m.groups = qp;
-    m.lut0 = lut[0];
-    m.lut1 = lut[1];
-    m.lut2 = lut[2];
-    m.lut3 = lut[3];
-    char name[64];
-    snprintf(name, sizeof(name), "eos_tq_maxsim_b%d_k%d_g%d", bits, ks, nqg);
-    // As many resident workgroups as the kernel's registers allow (three
-    // waves per SIMD for most variants), each wave striding over documents.
-    int per_cu = 2;
-    if (rt->blocks_per_cu(name, 256, 0, &per_cu, err) != 0) return 1;
-    int64_t blocks = (ndocs + 3) / 4;
-    const int64_t maxb = (int64_t)rt->compute_units * per_cu;
-    if (blocks > maxb) blocks = maxb;
-    if (blocks < 1) blocks = 1;
-    return rt->launch(name, dim3((unsigned)blocks), dim3(256), 0, &m, err, "tq_maxsim");
+    return maxsim_launch(&m, false, ndocs, "tq_maxsim", err);
   }
 
   // Exhaustive scores of all queries of the batch into dense [qb][count].
@@ -1100,6 +1126,134 @@ int rank_rows(EosHipRuntime* rt, EosHipTQ* tq, const float* d_rows, int rows, in
   return rt->launch("eos_tq_finalize", dim3(rows), dim3(256), 0, &f, err, "tq_maxsim_select_merge");
 }
 
+// Bound-filtered MaxSim top-k of one prepared chunk of cq queries (kk <=
+// kMsMaxK, ndocs >= kMsMinDocs), all passes in each launch:
+//  1. exact scores of every stride-th document (at most kMsSampleDocs), and
+//     per query tau = the r-th best of them, r chosen so that about
+//     min(3 kk, kMsCap / 8) documents of the corpus are expected above it;
+//  2. the high-half bound filter over every document: a document is listed
+//     for its pass when its score bound reaches tau of one of the pass's
+//     queries (a bound >= the exact score, so every document scoring >= tau
+//     is listed);
+//  3. exact scores of the listed documents as rank keys (0 below tau), and
+//     per query the top kk of them (eos_tq_finalize): final when at least kk
+//     listed documents score >= tau, since every unlisted one scores below;
+//  4. otherwise (too few, or the list overflowed kMsCap) the query is
+//     flagged and its row recomputed exhaustively, gated on the device.
+// Results equal the exhaustive path's: the same exact scores, ranked by
+// (score desc, document index asc).
+constexpr int kMsCap = 8192;
+constexpr int kMsSampleDocs = 2048;
+constexpr int kMsMinDocs = 16384;
+constexpr int kMsMaxK = 512;
+int maxsim_filtered(EosHipRuntime* rt, EosHipTQ* tq, int doc_len, int64_t ndocs, int cq, int kk,
+                    int64_t* d_ids, float* d_scores, char** err) {
+  const int per = tq->maxsim_nqg();
+  const int npass = (cq + per - 1) / per;
+  const int64_t stride = std::max<int64_t>(16, (ndocs + kMsSampleDocs - 1) / kMsSampleDocs);
+  const int64_t ns = (ndocs + stride - 1) / stride;
+  const double target = std::min<double>(3.0 * kk, kMsCap / 8.0);
+  int64_t r = (int64_t)std::ceil(target * (double)ns / (double)ndocs);
+  r = std::max<int64_t>(1, std::min<int64_t>(r, ns));
+  // workspace: samples [cq][ns] f32, tau [cq], list [npass][cap] u32, list
+  // counts [npass], rank keys [cq][cap] u64, key counts [cq], status [cq]
+  auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+  const size_t o_samp = 0;
+  const size_t o_tau = o_samp + al((size_t)cq * ns * 4);
+  const size_t o_list = o_tau + al((size_t)cq * 4);
+  const size_t o_lcnt = o_list + al((size_t)npass * kMsCap * 4);
+  const size_t o_cand = o_lcnt + al((size_t)npass * 4);
+  const size_t o_ccnt = o_cand + al((size_t)cq * kMsCap * 8);
+  const size_t o_stat = o_ccnt + al((size_t)cq * 4);
+  const size_t total = o_stat + al((size_t)cq * 4);
+  if (tq->ensure(&tq->ms_ws, &tq->ms_ws_bytes, total, err) != 0) return 1;
+  char* w = static_cast<char*>(tq->ms_ws);
+  float* samp = reinterpret_cast<float*>(w + o_samp);
+  float* tau = reinterpret_cast<float*>(w + o_tau);
+  uint32_t* list = reinterpret_cast<uint32_t*>(w + o_list);
+  uint32_t* lcnt = reinterpret_cast<uint32_t*>(w + o_lcnt);
+  unsigned long long* cand = reinterpret_cast<unsigned long long*>(w + o_cand);
+  uint32_t* ccnt = reinterpret_cast<uint32_t*>(w + o_ccnt);
+  int* status = reinterpret_cast<int*>(w + o_stat);
+  // 1. sample and threshold
+  TqMaxsimArgs m = tq->maxsim_args(0, cq, doc_len);
+  m.out = samp;
+  m.doc_begin = 0;
+  m.doc_stride = stride;
+  m.ndocs = ns;
+  m.out_stride = ns;
+  if (tq->maxsim_launch(&m, false, ns, "tq_maxsim_sample", err) != 0) return 1;
+  TqSelectArgs sel;
+  memset(&sel, 0, sizeof(sel));
+  sel.rows = samp;
+  sel.tau = tau;
+  sel.n = ns;
+  sel.stride = ns;
+  sel.kk = (int)r;
+  sel.nrows = cq;
+  if (rt->launch("eos_tq_threshold", dim3((unsigned)cq), dim3(256), 0, &sel, err, "tq_maxsim_threshold") != 0)
+    return 1;
+  // 2. bound filter
+  hipError_t e = hipMemsetAsync(lcnt, 0, (size_t)npass * 4, rt->stream);
+  if (e != hipSuccess) return hip_err(err, "hipMemsetAsync(list counts)", e);
+  m = tq->maxsim_args(0, cq, doc_len);
+  m.doc_begin = 0;
+  m.ndocs = ndocs;
+  m.tau = tau;
+  m.lonorm = tq->ms_lonorm;
+  m.tile_cn = tq->tile_cn;
+  m.list = list;
+  m.list_count = lcnt;
+  m.list_cap = kMsCap;
+  if (tq->maxsim_launch(&m, true, ndocs, "tq_maxsim_filter", err) != 0) return 1;
+  // 3. exact scores of the listed documents, then the top kk of each query
+  m = tq->maxsim_args(0, cq, doc_len);
+  m.ndocs = kMsCap;
+  m.doc_list = list;
+  m.list_count = lcnt;
+  m.list_cap = kMsCap;
+  m.cand = cand;
+  m.cand_count = ccnt;
+  m.tau = tau;
+  if (tq->maxsim_launch(&m, false, kMsCap, "tq_maxsim_rescore", err) != 0) return 1;
+  TqFinalizeArgs f;
+  memset(&f, 0, sizeof(f));
+  f.cand = cand;
+  f.cand_count = ccnt;
+  f.ids = reinterpret_cast<long long*>(d_ids);
+  f.scores = d_scores;
+  f.status = status;
+  f.cap = kMsCap;
+  f.kk = kk;
+  f.q = cq;
+  if (rt->launch("eos_tq_finalize", dim3((unsigned)cq), dim3(256), 0, &f, err, "tq_maxsim_finalize") != 0)
+    return 1;
+  // 4. exhaustive rows of the flagged queries (both launches return at once
+  // when none is flagged)
+  if (tq->ensure(reinterpret_cast<void**>(&tq->dense), &tq->dense_bytes,
+                 (size_t)cq * (size_t)ndocs * sizeof(float), err) != 0)
+    return 1;
+  m = tq->maxsim_args(0, cq, doc_len);
+  m.out = tq->dense;
+  m.doc_begin = 0;
+  m.ndocs = ndocs;
+  m.out_stride = ndocs;
+  m.gate = status;
+  if (tq->maxsim_launch(&m, false, ndocs, "tq_maxsim_fallback", err) != 0) return 1;
+  memset(&sel, 0, sizeof(sel));
+  sel.rows = tq->dense;
+  sel.status = status;
+  sel.ids = reinterpret_cast<long long*>(d_ids);
+  sel.scores = d_scores;
+  sel.n = ndocs;
+  sel.stride = ndocs;
+  sel.kk = kk;
+  sel.mode = 1;
+  sel.nrows = cq;
+  return rt->launch("eos_tq_row_select", dim3((unsigned)cq), dim3(1024), 0, &sel, err,
+                    "tq_maxsim_fallback_select");
+}
+
 int maxsim_topk_impl(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const float* d_queries,
                      int32_t q, int32_t tq_tokens, int32_t k, int64_t* d_ids, float* d_scores,
                      char** err) {
@@ -1111,6 +1265,20 @@ int maxsim_topk_impl(EosHipRuntime* rt, EosHipTQ* tq, int32_t doc_len, const flo
                    (long long)kk64, kSortCap);
   const int kk = (int)kk64;
   const int per = tq->maxsim_nqg();
+  if (ndocs >= kMsMinDocs && kk <= kMsMaxK) {
+    // Chunks of whole passes whose exhaustive fallback rows stay under 1 GiB.
+    const int64_t by_mem = std::max<int64_t>(1, ((int64_t)1 << 30) / (ndocs * 4));
+    const int chunk = (int)std::max<int64_t>(per, std::min<int64_t>(256, by_mem) / per * per);
+    for (int c0 = 0; c0 < q; c0 += chunk) {
+      const int cq = std::min(chunk, q - c0);
+      if (tq->maxsim_prepare(d_queries + (size_t)c0 * tq_tokens * tq->d, cq, tq_tokens, err,
+                             true) != 0 ||
+          maxsim_filtered(rt, tq, doc_len, ndocs, cq, kk, d_ids + (size_t)c0 * kk,
+                          d_scores + (size_t)c0 * kk, err) != 0)
+        return 1;
+    }
+    return 0;
+  }
   // The document scores of a chunk of queries (all of its scan passes) are
   // kept, so one select launch ranks every row of the chunk in parallel (one
   // workgroup per row; a select per pass ran only `per` workgroups at once).

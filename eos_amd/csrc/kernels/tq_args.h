@@ -96,17 +96,37 @@ struct TqMaxsimArgs {
   const int32_t* packed;
   const float* norms;
   const int8_t* bfrag;
-  const float* alpha;      // [32*nqg] per token column
+  const float* alpha;      // [32 * groups] per token column
   float* out;              // [groups][out_stride]
   long long doc_begin;     // first document
   long long ndocs;         // documents in this launch
   long long out_stride;
   int tiles_per_doc;
-  int groups;              // live query groups (<= nqg)
+  int groups;              // live query groups of the launch (all its passes)
   uint32_t lut0, lut1, lut2, lut3;
   // bfrag holds the fragments of every prepared query, [ks][frag_ncb][64];
-  // this pass uses column blocks [frag_cb0, frag_cb0 + 2 nqg).
+  // the launch uses column blocks from frag_cb0 on.
   int frag_ncb, frag_cb0;
+  // Pass p = blockIdx.y scores query groups [nqg p, nqg p + nqg) of the
+  // launch (alpha, out, tau, gate, lonorm and the doc lists offset by it).
+  // Document i of a pass is doc_begin + i * doc_stride (doc_stride 0 = 1),
+  // or, with doc_list, doc_list[p * list_cap + i] for i < min(count, cap),
+  // count = list_count[p]; in that mode the exact scores leave as rank keys
+  // cand[group][i] (0 when below tau[group]) with cand_count[group] = count.
+  long long doc_stride;
+  const uint32_t* doc_list;
+  unsigned long long* cand;
+  uint32_t* cand_count;
+  const float* tau;        // [groups]
+  const int* gate;         // or NULL: a pass runs only if a live group's gate is set
+  // High-half bound filter (the _h kernels): documents whose score bound
+  // reaches tau of some live group of the pass are appended to
+  // list[p * list_cap ..] (count list_count[p], entries past cap dropped).
+  const float* lonorm;     // [32 * groups] ||lo||_2 of each column, rounded up
+  const float* tile_cn;    // [2 * tiles] largest ||C[codes]||_2 of the tile, largest Norm
+  uint32_t* list;
+  uint32_t* list_count;
+  int list_cap;
 };
 
 // Parent (multivector) aggregation over child scores: parent p owns children

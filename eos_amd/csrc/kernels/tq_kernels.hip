@@ -2040,26 +2040,67 @@ EOS_DEV void maxsim_epilogue(float& mx, const v16i& hi, const v16i& lo, float al
   }
 }
 
-template <int BITS, int KS, int NQG>
+// High-half bound of the same maxima: with Qs = 256 hi + lo and |sum_j lo_j
+// C_j| <= lb (lonorm times the tile's largest ||C[codes]||_2, both rounded
+// up, the product bumped by 2^-22), x = fl(256 D_hi + lb) >= fl(D) (rounding
+// is monotone), and my = max_i fl(x_i n_i). For alpha, n_i >= 0 every exact
+// score fl(fl(fl(D_i) alpha) n_i) is at most max(my, 0) alpha (1 + 2^-21),
+// which the caller applies once per token.
+EOS_DEV void maxsim_bound(float& my, const v16i& hi, float lb, const float (&nrm)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) my = fmaxf(my, __builtin_fmaf((float)hi[i], 256.0f, lb) * nrm[i]);
+}
+
+// Register stages of the MaxSim tile ring: as many as fit beside the
+// accumulators in the 168 registers of three waves per SIMD.
+template <bool HI>
+constexpr int maxsim_ring(int nload) {
+  const int stage = 4 * nload + 1;
+  const int r = (HI ? 30 : 22) / stage;
+  return r < 2 ? 2 : r > 8 ? 8 : r;
+}
+
+// MaxSim of documents against NQG query groups (32 token columns each) per
+// pass; HI: the high-half bound filter (half the MFMAs) that lists the
+// documents whose score bound reaches some group's tau.
+template <int BITS, int KS, int NQG, bool HI>
 EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
   constexpr int NCB = 2 * NQG;
+  constexpr int NCBU = HI ? NQG : NCB;  // column blocks staged and used
   constexpr int SPL = 8 / BITS;
   constexpr int NLOAD = (KS + SPL - 1) / SPL;
   constexpr int NWV = kScanThreads / 64;
-  __shared__ v4i sb[KS * NCB * 64];
+  __shared__ v4i sb[KS * NCBU * 64];
   __shared__ float4 nstage[NWV][8];
+  const int goff = blockIdx.y * NQG;          // first query group of this pass
+  const int gl = min(NQG, a.groups - goff);   // its live groups
+  if (gl <= 0) return;
+  if (a.gate != nullptr) {
+    bool any = false;
+    for (int g = 0; g < gl; ++g) any |= a.gate[goff + g] != 0;
+    if (!any) return;
+  }
+  const uint32_t* dlist = a.doc_list != nullptr ? a.doc_list + (size_t)blockIdx.y * a.list_cap : nullptr;
+  long long ndocs = a.ndocs;
+  if (dlist != nullptr) {
+    const uint32_t c = a.list_count[blockIdx.y];
+    ndocs = c < (uint32_t)a.list_cap ? (long long)c : (long long)a.list_cap;
+    if (blockIdx.x == 0 && threadIdx.x < (unsigned)gl) a.cand_count[goff + threadIdx.x] = c;
+  }
   {
-    // The pass's column blocks [frag_cb0, frag_cb0 + NCB) of each K step
-    // (fragments laid out [ks][frag_ncb][64] for all queries prepared).
-    constexpr int COUNT = KS * NCB * 64;
+    // The pass's column blocks of each K step (HI: the high blocks only;
+    // fragments laid out [ks][frag_ncb][64] for all queries prepared).
+    constexpr int COUNT = KS * NCBU * 64;
     constexpr int PER = (COUNT + kScanThreads - 1) / kScanThreads;
     const v4i* src = reinterpret_cast<const v4i*>(a.bfrag);
+    const int cb0 = a.frag_cb0 + 2 * goff;
     v4i v[PER];
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
       const int i = threadIdx.x + r * kScanThreads;
-      const int s = i / (NCB * 64), rem = i - s * (NCB * 64);
-      if (i < COUNT) v[r] = src[((size_t)s * a.frag_ncb + a.frag_cb0) * 64 + rem];
+      const int s = i / (NCBU * 64), rem = i - s * (NCBU * 64);
+      const int cb = HI ? 2 * (rem >> 6) : (rem >> 6), l = rem & 63;
+      if (i < COUNT) v[r] = src[((size_t)s * a.frag_ncb + cb0 + cb) * 64 + l];
     }
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
@@ -2076,23 +2117,34 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
   const int tpd = a.tiles_per_doc;
   // Wave w scores documents w, w + nw, ... (no barrier follows).
   const long long doc0 = (long long)blockIdx.x * NWV + wave;
-  if (doc0 >= a.ndocs) return;
-  const long long last_doc = doc0 + (a.ndocs - 1 - doc0) / nw * nw;
+  if (doc0 >= ndocs) return;
+  const long long last_doc = doc0 + (ndocs - 1 - doc0) / nw * nw;
+  const long long dstride = a.doc_stride > 0 ? a.doc_stride : 1;
+  auto doc_id = [&](long long dd) -> long long {
+    return dlist != nullptr ? (long long)dlist[dd] : a.doc_begin + dd * dstride;
+  };
   const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
   TqScanArgs la;  // lookup tables for decode_step
   la.lut0 = a.lut0;
   la.lut1 = a.lut1;
   la.lut2 = a.lut2;
   la.lut3 = a.lut3;
-  float al[NQG];
+  float al[NQG], lo_r[NQG], ta_r[NQG];
 #pragma unroll
-  for (int g = 0; g < NQG; ++g) al[g] = a.alpha[g * 32 + (lane & 31)];
+  for (int g = 0; g < NQG; ++g) {
+    const int gg = min(goff + g, a.groups - 1);
+    al[g] = a.alpha[gg * 32 + (lane & 31)];
+    lo_r[g] = HI ? a.lonorm[gg * 32 + (lane & 31)] : 0.0f;
+    ta_r[g] = (HI || dlist != nullptr) ? a.tau[gg] : 0.0f;
+  }
   // The wave's tiles form one stream of (document, tile) steps, loaded one
   // step ahead through two register stages that are never copied (a copy of
   // a register still being loaded would wait for every load issued before
   // it). Every phase issues the same loads (past the wave's last step they
   // repeat its last tile), so each wait covers exactly the stage it needs. A
-  // stage holds the tile's codes and one norm per lane (row lane % 32).
+  // stage holds the tile's codes and one value per lane: the norm of row
+  // lane % 32 (lanes 0-31; all lanes without HI) and, with HI, the tile's
+  // code-norm bound and largest Norm (lanes 32 + even / odd).
   struct Stage {
     v4i raw[NLOAD];
     float nv;
@@ -2102,9 +2154,12 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
   auto load_next = [&](Stage& st) {
     const long long dd = ld_doc <= last_doc ? ld_doc : last_doc;
     const int tt = ld_doc <= last_doc ? ld_t : tpd - 1;
-    const long long tile = (a.doc_begin + dd) * tpd + tt;
+    const long long tile = doc_id(dd) * tpd + tt;
     load_tile_codes<NLOAD>(st.raw, packed, tile, lane);
-    st.nv = a.norms[tile * kTile + (lane & 31)];
+    if constexpr (HI)
+      st.nv = lane < 32 ? a.norms[tile * kTile + lane] : a.tile_cn[2 * tile + (lane & 1)];
+    else
+      st.nv = a.norms[tile * kTile + (lane & 31)];
     if (++ld_t == tpd) {
       ld_t = 0;
       ld_doc += nw;
@@ -2120,6 +2175,12 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
     }
     int boff = lane;
     asm volatile("" : "+v"(boff));
+    float lb[NQG];
+    if constexpr (HI) {
+      const float cn = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(st.nv), 32));
+#pragma unroll
+      for (int g = 0; g < NQG; ++g) lb[g] = (lo_r[g] * cn) * 1.0000002f;  // >= lonorm * cn
+    }
     // Row r's norm sits at float r of the wave's slot; lane l needs rows
     // 8 i4 + 4 (l / 32) + {0..3}. LDS operations of one wave complete in
     // order, so no barrier is needed around the slot.
@@ -2138,11 +2199,17 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
     // The score's "+ 0.0f" (-0 -> +0) commutes with the maximum (fmaxf
     // treats the zeros as equal), so it is applied once to the token max.
     v16i acc[NCB];
+    auto epi = [&](int g) {
+      if constexpr (HI)
+        maxsim_bound(mx[g], acc[g], lb[g], nrm);
+      else
+        maxsim_epilogue(mx[g], acc[2 * g], acc[2 * g + 1], al[g], nrm);
+    };
     if constexpr (KS <= 8) {
       // Short K: every step's code fragment is decoded once up front, then
       // the query groups run one after another; group g's MFMAs are followed
-      // by the exact epilogue of group g - 1, which does not depend on them
-      // (and only two query fragments are live at a time).
+      // by the epilogue of group g - 1, which does not depend on them (and
+      // only two query fragments are live at a time).
       v4i af[KS];
 #pragma unroll
       for (int c = 0; c < NLOAD; ++c) {
@@ -2155,50 +2222,80 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
 #pragma unroll
       for (int g = 0; g <= NQG; ++g) {
         if (g < NQG) {
-          acc[2 * g] = v16i{0};
-          acc[2 * g + 1] = v16i{0};
+          if constexpr (HI) {
+            acc[g] = v16i{0};
 #pragma unroll
-          for (int s = 0; s < KS; ++s) {
-            const v4i bh = sb[(s * NCB + 2 * g) * 64 + boff];
-            const v4i bl = sb[(s * NCB + 2 * g + 1) * 64 + boff];
-            acc[2 * g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bh, acc[2 * g], 0, 0, 0);
-            acc[2 * g + 1] =
-                __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bl, acc[2 * g + 1], 0, 0, 0);
+            for (int s = 0; s < KS; ++s) {
+              const v4i bh = sb[(s * NCBU + g) * 64 + boff];
+              acc[g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bh, acc[g], 0, 0, 0);
+            }
+          } else {
+            acc[2 * g] = v16i{0};
+            acc[2 * g + 1] = v16i{0};
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+              const v4i bh = sb[(s * NCBU + 2 * g) * 64 + boff];
+              const v4i bl = sb[(s * NCBU + 2 * g + 1) * 64 + boff];
+              acc[2 * g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bh, acc[2 * g], 0, 0, 0);
+              acc[2 * g + 1] =
+                  __builtin_amdgcn_mfma_i32_32x32x32_i8(af[s], bl, acc[2 * g + 1], 0, 0, 0);
+            }
           }
         }
-        if (g > 0) maxsim_epilogue(mx[g - 1], acc[2 * g - 2], acc[2 * g - 1], al[g - 1], nrm);
+        if (g > 0) epi(g - 1);
       }
     } else {
       // Long K: steps outer, each step's code fragment decoded once and its
       // query fragments read together before its MFMAs.
 #pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
+      for (int cb = 0; cb < NCBU; ++cb) acc[cb] = v16i{0};
 #pragma unroll
       for (int c = 0; c < NLOAD; ++c) {
 #pragma unroll
         for (int h = 0; h < SPL; ++h) {
           const int s = c * SPL + h;
           if (s < KS) {
-            v4i bf[NCB];
+            v4i bf[NCBU];
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb) bf[cb] = sb[(s * NCB + cb) * 64 + boff];
+            for (int cb = 0; cb < NCBU; ++cb) bf[cb] = sb[(s * NCBU + cb) * 64 + boff];
             const v4i af = decode_step<BITS>(st.raw[c], h, la);
 #pragma unroll
-            for (int cb = 0; cb < NCB; ++cb)
+            for (int cb = 0; cb < NCBU; ++cb)
               acc[cb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[cb], acc[cb], 0, 0, 0);
           }
         }
       }
 #pragma unroll
-      for (int g = 0; g < NQG; ++g) maxsim_epilogue(mx[g], acc[2 * g], acc[2 * g + 1], al[g], nrm);
+      for (int g = 0; g < NQG; ++g) epi(g);
     }
     if (t == tpd - 1) {
+      bool keep = false;
 #pragma unroll
       for (int g = 0; g < NQG; ++g) {
-        float v = fmaxf(mx[g], __shfl_xor(mx[g], 32)) + 0.0f;  // token max over the document
+        float v = fmaxf(mx[g], __shfl_xor(mx[g], 32));  // token max over the document
+        if constexpr (HI) v = (fmaxf(v, 0.0f) * al[g]) * 1.000001f;  // >= every exact token max
+        v = v + 0.0f;
 #pragma unroll
         for (int o = 1; o < 32; o <<= 1) v = v + __shfl_xor(v, o);
-        if (lane == 0 && g < a.groups) a.out[(size_t)g * a.out_stride + doc] = v;
+        if constexpr (HI) {
+          // tau <= 0 (or NaN) cannot prune: every document is listed.
+          keep |= g < gl && (v >= ta_r[g] || !(ta_r[g] > 0.0f));
+        } else if (dlist != nullptr) {
+          if (lane == 0 && g < gl) {
+            const long long id = doc_id(doc);
+            a.cand[(size_t)(goff + g) * a.list_cap + doc] =
+                v >= ta_r[g] ? rank_key(v, (uint32_t)id) : 0ull;
+          }
+        } else {
+          if (lane == 0 && g < gl) a.out[(size_t)(goff + g) * a.out_stride + doc] = v;
+        }
+      }
+      if constexpr (HI) {
+        if (lane == 0 && keep) {
+          const uint32_t pos = atomicAdd(&a.list_count[blockIdx.y], 1u);
+          if (pos < (uint32_t)a.list_cap)
+            a.list[(size_t)blockIdx.y * a.list_cap + pos] = (uint32_t)doc_id(doc);
+        }
       }
     }
     if (++t == tpd) {
@@ -2206,16 +2303,23 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
       doc += nw;
     }
   };
-  Stage s0, s1;
-  load_next(s0);
-  // Two phases per pass; the loop has a single exit at its end (exits between
-  // phases make the compiler's wait analysis merge the phases at the loop
-  // head and wait for the newest stage too).
+  // Ring of R register stages: R - 1 tiles in flight while one is
+  // processed (a tile is 16 bytes of codes and one norm per lane, so one
+  // tile ahead kept too few bytes in flight to cover the memory latency).
+  // Phase p refills the stage processed in phase p - 1, then processes stage
+  // p; the loop has a single exit at its end (exits between phases make the
+  // compiler's wait analysis merge the phases at the loop head and wait for
+  // the newest stage too).
+  constexpr int R = maxsim_ring<HI>(NLOAD);
+  Stage st[R];
+#pragma unroll
+  for (int p = 0; p < R - 1; ++p) load_next(st[p]);
   do {
-    load_next(s1);
-    process(s0);
-    load_next(s0);
-    if (doc <= last_doc) process(s1);
+#pragma unroll
+    for (int p = 0; p < R; ++p) {
+      load_next(st[(p + R - 1) % R]);
+      if (doc <= last_doc) process(st[p]);
+    }
   } while (doc <= last_doc);
 }
 
@@ -2228,7 +2332,11 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
 #define EOS_TQ_MAXSIM(BITS, KS, NQG)                                                        \
   extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(3))) \
   void eos_tq_maxsim_b##BITS##_k##KS##_g##NQG(TqMaxsimArgs a) {                              \
-    tq_maxsim_body<BITS, KS, NQG>(a);                                                       \
+    tq_maxsim_body<BITS, KS, NQG, false>(a);                                                \
+  }                                                                                          \
+  extern "C" __global__ __launch_bounds__(kScanThreads) __attribute__((amdgpu_waves_per_eu(3))) \
+  void eos_tq_maxsim_b##BITS##_k##KS##_g##NQG##_h(TqMaxsimArgs a) {                          \
+    tq_maxsim_body<BITS, KS, NQG, true>(a);                                                 \
   }
 
 EOS_TQ_MAXSIM(2, 1, 4)

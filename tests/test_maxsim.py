@@ -158,6 +158,67 @@ def test_maxsim_rejects_bad_shapes(rt):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("bits,d", [(2, 64), (4, 96)])
+def test_maxsim_bound_filter_matches_oracle(rt, bits, d):
+    """20,000 documents take the bound-filtered top-k (sampled threshold,
+    high-half bound filter, exact rescoring of the listed documents): ids and
+    scores equal the oracle's, with copies of query 0's best document planted
+    (exact ties, ranked by lower index), five queries (two passes of query
+    groups) and k from 1 to the filtered path's limit; k = 600 takes the
+    exhaustive path."""
+    print(f"[case] maxsim bound filter 20000 docs bits={bits} d={d}", flush=True)
+    from eos_amd.turboquant import TurboQuantIndex, TurboQuantMultiVectorIndex
+    ndocs, doc_len = 20000, 32
+    c = _corpus(ndocs, doc_len, d, bits, seed=53 + bits)
+    q = _tokens(5, 8, d, 57 + bits)
+    args = (c.rotation, d, bits, c.codebook, c.codebook_scale)
+    first = oracle.tq_maxsim_scores(q[:1], *args, c.codes, c.norms, doc_len)
+    best = int(np.argmax(first[0]))
+    codes = c.codes.reshape(ndocs, doc_len, -1).copy()
+    norms = c.norms.reshape(ndocs, doc_len).copy()
+    for dst in (0, 7, 9999, 10000, 19999):
+        codes[dst], norms[dst] = codes[best], norms[best]
+    codes = codes.reshape(ndocs * doc_len, -1)
+    norms = norms.reshape(-1)
+    want = oracle.tq_maxsim_scores(q, *args, codes, norms, doc_len)
+    idx = TurboQuantIndex(rt, codes, norms, d, bits, c.codebook, c.codebook_scale, c.rotation)
+    mv = TurboQuantMultiVectorIndex(idx, doc_len)
+    for k in (1, 6, 100, 512, 600):
+        ids, sc = mv.top_k(q, k)
+        for i in range(5):
+            order = np.lexsort((np.arange(ndocs), -want[i]))[:k]
+            np.testing.assert_array_equal(ids[i], order, err_msg=f"k={k} query {i}")
+            np.testing.assert_array_equal(sc[i], want[i][order])
+    idx.release()
+
+
+@pytest.mark.gpu
+def test_maxsim_bound_filter_falls_back_exactly(rt):
+    """Cases the filter cannot prune are recomputed exhaustively on the
+    device: identical documents (every document listed: the list overflows)
+    and zero query tokens (every score 0, so tau = 0 prunes nothing); the top
+    k is then documents 0 .. k-1, as the oracle ranks them."""
+    print("[case] maxsim bound filter fallback", flush=True)
+    from eos_amd.turboquant import TurboQuantIndex, TurboQuantMultiVectorIndex
+    ndocs, doc_len, d, bits = 17000, 32, 64, 2
+    c = _corpus(1, doc_len, d, bits, seed=61)
+    codes = np.tile(c.codes, (ndocs, 1))
+    norms = np.tile(c.norms, ndocs)
+    q = _tokens(4, 3, d, 62)
+    q[2] = 0.0  # a query whose every token is zero
+    args = (c.rotation, d, bits, c.codebook, c.codebook_scale)
+    want = oracle.tq_maxsim_scores(q, *args, codes[: 40 * doc_len], norms[: 40 * doc_len], doc_len)
+    idx = TurboQuantIndex(rt, codes, norms, d, bits, c.codebook, c.codebook_scale, c.rotation)
+    mv = TurboQuantMultiVectorIndex(idx, doc_len)
+    ids, sc = mv.top_k(q, 30)
+    for i in range(4):
+        np.testing.assert_array_equal(ids[i], np.arange(30), err_msg=f"query {i}")
+        np.testing.assert_array_equal(sc[i], want[i][:30])
+    assert np.all(sc[2] == 0.0)
+    idx.release()
+
+
+@pytest.mark.gpu
 def test_baseline_c5_full_size(rt):
     print("[case] c5 full size 100k x 128 x 128", flush=True)
     from eos_amd.turboquant import TurboQuantMultiVectorIndex
