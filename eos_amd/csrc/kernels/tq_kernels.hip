@@ -2060,6 +2060,42 @@ constexpr int maxsim_ring(int nload) {
   return r < 2 ? 2 : r > 8 ? 8 : r;
 }
 
+template <int CTRL>
+EOS_DEV float ms_dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// v of lane l ^ 16 / l ^ 32 through a permlane swap of v with itself (the
+// builtin's two results are copied out before the bit casts).
+EOS_DEV float ms_other16(float v, bool upper) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const unsigned r0 = r[0], r1 = r[1];
+  return __builtin_bit_cast(float, upper ? r0 : r1);
+}
+EOS_DEV void ms_halves(float v, float& lo, float& hi) {
+  const unsigned u = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const unsigned r0 = r[0], r1 = r[1];
+  lo = __builtin_bit_cast(float, r0);
+  hi = __builtin_bit_cast(float, r1);
+}
+// The token sum of a document score: the butterfly v + v[l ^ o] for o = 1,
+// 2, 4, 8, 16 over the 32 token lanes, by DPP and one permlane swap instead
+// of LDS permutes. The values are the butterfly's: after the quad steps all
+// four lanes of a quad hold the same sum, so the half-row mirror (lane 7 - i
+// of each 8) reads the value lane i ^ 4 holds, and likewise the row mirror
+// for i ^ 8; each add is commutative.
+EOS_DEV float ms_token_sum(float v, int lane) {
+  v = v + ms_dpp<0xb1>(v);   // quad_perm [1, 0, 3, 2]: lane ^ 1
+  v = v + ms_dpp<0x4e>(v);   // quad_perm [2, 3, 0, 1]: lane ^ 2
+  v = v + ms_dpp<0x141>(v);  // row_half_mirror
+  v = v + ms_dpp<0x140>(v);  // row_mirror
+  const bool odd_row = (lane & 16) != 0;
+  const float o = ms_other16(v, odd_row);
+  return odd_row ? o + v : v + o;
+}
+
 // MaxSim of documents against NQG query groups (32 token columns each) per
 // pass; HI: the high-half bound filter (half the MFMAs) that lists the
 // documents whose score bound reaches some group's tau.
@@ -2120,9 +2156,6 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
   if (doc0 >= ndocs) return;
   const long long last_doc = doc0 + (ndocs - 1 - doc0) / nw * nw;
   const long long dstride = a.doc_stride > 0 ? a.doc_stride : 1;
-  auto doc_id = [&](long long dd) -> long long {
-    return dlist != nullptr ? (long long)dlist[dd] : a.doc_begin + dd * dstride;
-  };
   const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
   TqScanArgs la;  // lookup tables for decode_step
   la.lut0 = a.lut0;
@@ -2137,32 +2170,57 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
     lo_r[g] = HI ? a.lonorm[gg * 32 + (lane & 31)] : 0.0f;
     ta_r[g] = (HI || dlist != nullptr) ? a.tau[gg] : 0.0f;
   }
-  // The wave's tiles form one stream of (document, tile) steps, loaded one
-  // step ahead through two register stages that are never copied (a copy of
-  // a register still being loaded would wait for every load issued before
-  // it). Every phase issues the same loads (past the wave's last step they
-  // repeat its last tile), so each wait covers exactly the stage it needs. A
-  // stage holds the tile's codes and one value per lane: the norm of row
-  // lane % 32 (lanes 0-31; all lanes without HI) and, with HI, the tile's
-  // code-norm bound and largest Norm (lanes 32 + even / odd).
+  // The wave's tiles form one stream of (document, tile) steps through a
+  // ring of register stages that are never copied (a copy of a register
+  // still being loaded would wait for every load issued before it). Every
+  // phase issues the same loads (past the wave's last step they repeat its
+  // last tile), so each wait covers exactly the stages it needs. A stage
+  // holds the tile's codes and one value per lane: the norm of row lane % 32
+  // (lanes 0-31; all lanes without HI) and, with HI, the tile's code-norm
+  // bound and largest Norm (lanes 32 + even / odd); and its document id.
+  // Tile indices advance by increments; a listed document's id comes from a
+  // register that holds the ids of the wave's next 64 documents (lane j:
+  // document j), refilled after every 64, so no load waits on an id.
   struct Stage {
     v4i raw[NLOAD];
     float nv;
+    long long id;
   };
-  long long ld_doc = doc0;
-  int ld_t = 0;
+  const long long wave_docs = (last_doc - doc0) / nw + 1;
+  const long long nsteps = wave_docs * tpd;
+  long long ld_k = 0;       // step of the next load
+  int ld_t = 0;             // its tile within the document
+  long long ld_j = 0;       // its document within the wave's sequence
+  uint32_t idreg = 0;
+  auto fill_ids = [&](long long j0) {
+    const long long jj = j0 + lane;
+    idreg = (dlist != nullptr && jj < wave_docs) ? dlist[doc0 + jj * nw] : 0u;
+  };
+  if (dlist != nullptr) fill_ids(0);
+  long long ld_id = dlist != nullptr
+                        ? (long long)__builtin_amdgcn_readfirstlane((int)idreg)
+                        : a.doc_begin + doc0 * dstride;
+  const long long id_step = nw * dstride;
   auto load_next = [&](Stage& st) {
-    const long long dd = ld_doc <= last_doc ? ld_doc : last_doc;
-    const int tt = ld_doc <= last_doc ? ld_t : tpd - 1;
-    const long long tile = doc_id(dd) * tpd + tt;
+    const long long tile = ld_id * tpd + ld_t;
+    st.id = ld_id;
     load_tile_codes<NLOAD>(st.raw, packed, tile, lane);
     if constexpr (HI)
       st.nv = lane < 32 ? a.norms[tile * kTile + lane] : a.tile_cn[2 * tile + (lane & 1)];
     else
       st.nv = a.norms[tile * kTile + (lane & 31)];
-    if (++ld_t == tpd) {
-      ld_t = 0;
-      ld_doc += nw;
+    if (ld_k + 1 < nsteps) {
+      ++ld_k;
+      if (++ld_t == tpd) {
+        ld_t = 0;
+        ++ld_j;
+        if (dlist != nullptr) {
+          if ((ld_j & 63) == 0) fill_ids(ld_j);
+          ld_id = (long long)(uint32_t)__builtin_amdgcn_readlane((int)idreg, (int)(ld_j & 63));
+        } else {
+          ld_id += id_step;
+        }
+      }
     }
   };
   long long doc = doc0;
@@ -2272,20 +2330,18 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
       bool keep = false;
 #pragma unroll
       for (int g = 0; g < NQG; ++g) {
-        float v = fmaxf(mx[g], __shfl_xor(mx[g], 32));  // token max over the document
+        float m0, m1;
+        ms_halves(mx[g], m0, m1);
+        float v = fmaxf(m0, m1);  // token max over the document
         if constexpr (HI) v = (fmaxf(v, 0.0f) * al[g]) * 1.000001f;  // >= every exact token max
-        v = v + 0.0f;
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) v = v + __shfl_xor(v, o);
+        v = ms_token_sum(v + 0.0f, lane);
         if constexpr (HI) {
           // tau <= 0 (or NaN) cannot prune: every document is listed.
           keep |= g < gl && (v >= ta_r[g] || !(ta_r[g] > 0.0f));
         } else if (dlist != nullptr) {
-          if (lane == 0 && g < gl) {
-            const long long id = doc_id(doc);
+          if (lane == 0 && g < gl)
             a.cand[(size_t)(goff + g) * a.list_cap + doc] =
-                v >= ta_r[g] ? rank_key(v, (uint32_t)id) : 0ull;
-          }
+                v >= ta_r[g] ? rank_key(v, (uint32_t)st.id) : 0ull;
         } else {
           if (lane == 0 && g < gl) a.out[(size_t)(goff + g) * a.out_stride + doc] = v;
         }
@@ -2294,7 +2350,7 @@ EOS_DEV void tq_maxsim_body(const TqMaxsimArgs& a) {
         if (lane == 0 && keep) {
           const uint32_t pos = atomicAdd(&a.list_count[blockIdx.y], 1u);
           if (pos < (uint32_t)a.list_cap)
-            a.list[(size_t)blockIdx.y * a.list_cap + pos] = (uint32_t)doc_id(doc);
+            a.list[(size_t)blockIdx.y * a.list_cap + pos] = (uint32_t)st.id;
         }
       }
     }
