@@ -1446,7 +1446,7 @@ EOS_TAIL_KERNEL(1, 768, 2)
 // and accumulates O^T += V^T P^T on MFMA. P^T is fed straight from the S^T
 // registers: the K order of that MFMA is the row order the S^T accumulator
 // already has, and the V^T fragment is gathered in the same order.
-template <int HD, int KB>
+template <int HD, int KB, bool FOLD = false>
 EOS_DEV void attn_body(const EncAttnArgs& a) {
   static_assert(KB == 32 || KB == 64, "keys per block");
   constexpr int KC = KB / 8;             // 8-key chunks of a V^T row per block
@@ -1490,6 +1490,12 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
 #pragma unroll
   for (int t = 0; t < HD / 32; ++t) o[t] = v16f{0};
   float mrun = -__builtin_inff(), lrun = 0.f;
+  // FOLD: the exponent reference enters the S MFMAs as their accumulator
+  // input (negm = -mrun in every element, 0 before the first block), so the
+  // scores come out already shifted and the common path subtracts nothing;
+  // sref is the reference they carry.
+  v16f negm = v16f{0};
+  float sref = 0.f;
   // K [key][HD] and V^T [HD][key] of a 32-key block are staged in LDS from
   // registers; the next block's rows are requested before the current
   // block's MFMAs (double-buffered, one barrier per block).
@@ -1548,12 +1554,12 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     v16f s[NT];
 #pragma unroll
     for (int hh = 0; hh < NT; ++hh) {
-      s[hh] = v16f{0};
 #pragma unroll
       for (int st = 0; st < HD / 16; ++st) {
         const v8h kf = *reinterpret_cast<const v8h*>(
             &ks[buf][(32 * hh + l32) * (HD + 8) + st * 16 + g * 8]);
-        s[hh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[st], s[hh], 0, 0, 0);
+        s[hh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            kf, qf[st], st == 0 ? (FOLD ? negm : v16f{0}) : s[hh], 0, 0, 0);
       }
     }
     // element e of tile hh is key k0 + 32 hh + 8(e/4) + 4g + e%4; only the
@@ -1583,20 +1589,22 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
     constexpr float kSafe = 4096.0f;
     float psum;
     v8h pf[2 * NT];
-    auto exps = [&]() {
+    auto exps = [&](float shift) {
       psum = 0.f;
 #pragma unroll
       for (int hh = 0; hh < NT; ++hh)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           // v_exp_f32 directly: masked keys give exp2(-inf) = 0.
-          const float p = __builtin_amdgcn_exp2f(s[hh][e] - mrun);
+          const float p = __builtin_amdgcn_exp2f(FOLD ? s[hh][e] : s[hh][e] - shift);
           psum += p;
           pf[2 * hh + (e >> 3)][e & 7] = (_Float16)p;
         }
     };
-    exps();
-    const bool over = !(psum <= kSafe);  // also true for inf and NaN
+    exps(mrun);
+    // FOLD: the first block always moves the reference (its scores carry
+    // none yet).
+    const bool over = !(psum <= kSafe) || (FOLD && mrun == -__builtin_inff());
     if (__ballot(over) != 0ull) {
       if (a.moves != nullptr && k0 > 0 && lane == 0) atomicAdd(a.moves, 1);
       float mloc = -__builtin_inff();
@@ -1604,6 +1612,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
       for (int hh = 0; hh < NT; ++hh)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mloc = fmaxf(mloc, s[hh][e]);
+      if (FOLD) mloc += sref;  // the block's raw maximum (or -inf)
       const float mpair = fmaxf(mloc, __shfl_xor(mloc, 32));
       // Both shuffles run with every lane active: a shuffle inside the
       // short-circuit of `over || ...` would run only in the lanes that are
@@ -1621,7 +1630,18 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
         for (int e = 0; e < 16; ++e) o[t][e] *= corr;
       }
       mrun = mnew;
-      exps();  // now every s - mrun <= 0 for the moved queries
+      if constexpr (FOLD) {
+        // Re-reference this block's scores to mnew, and the next blocks'.
+        const float d = mnew == -__builtin_inff() ? 0.f : mnew - sref;
+#pragma unroll
+        for (int hh = 0; hh < NT; ++hh)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s[hh][e] -= d;
+        sref += d;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) negm[e] = -sref;
+      }
+      exps(mrun);  // now every score - mrun <= 0 for the moved queries
     }
     lrun += psum;
     // O^T += V^T P^T. K step st covers the keys this lane's P holds for
@@ -1713,11 +1733,11 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
 // files in every key block (about 110 extra VALU moves per block at hd 64).
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void eos_enc_attn_hd32(EncAttnArgs a) {
-  attn_body<32, 32>(a);
+  attn_body<32, 32, true>(a);
 }
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void eos_enc_attn_hd64(EncAttnArgs a) {
-  attn_body<64, 64>(a);
+  attn_body<64, 64, true>(a);
 }
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void eos_enc_attn_hd128(EncAttnArgs a) {
