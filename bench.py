@@ -837,7 +837,8 @@ def two_stage_leg(rt, steps: int, n: int) -> dict:
     rt.sync()
     kernels = {}
     for name in ("tq_ip_prepare", "tq_ipscan_sample", "tq_ip_threshold",
-                 "tq_ipscan_filter", "tq_ip_finalize", "tq_ipscan_dense", "tq_ip_fallback_select",
+                 "tq_ipscan_filter", "tq_ip_rescore", "tq_ip_finalize", "tq_ipscan_dense",
+                 "tq_ip_fallback_select",
                  "tq_fp16_rerank_dots", "tq_fp16_rerank_sort"):
         kernels[name] = rt.profile_read(name)[1] / 10
     filt = rt.profile_samples("tq_ipscan_filter")

@@ -1860,6 +1860,8 @@ struct IpFragOut {
   float* tau;
   uint32_t* cand_count;
   int ks, nqg;
+  float* lonorm;
+  int* kq;
 };
 static int ip_prepare_launch(EosHipRuntime* rt, const TqIpArgs& a, int q, double* qr, double* y,
                              const IpFragOut* frag, char** err) {
@@ -1888,6 +1890,8 @@ static int ip_prepare_launch(EosHipRuntime* rt, const TqIpArgs& a, int q, double
     qa.cand_count = frag->cand_count;
     qa.ks = frag->ks;
     qa.nqg = frag->nqg;
+    qa.lonorm = frag->lonorm;
+    qa.kq = frag->kq;
     ncols = 32 * frag->nqg;
   }
   if (rt->launch("eos_tq_ip_matvec", grid, dim3(256), 0, &m1, err, "tq_ip_prepare") != 0 ||
@@ -2064,9 +2068,12 @@ struct EosHipTQIP {
   int32_t* packed = nullptr;
   float* norms = nullptr;
   float* resnorms = nullptr;
+  float* tile_cn = nullptr;  // [ntiles][4] code-norm bound per tile
   // per-batch scratch
   float* alpha = nullptr;
   float* beta = nullptr;
+  float* lonorm = nullptr;  // [cols] bound filter constants
+  int* kq = nullptr;
   int* ysum = nullptr;
   int8_t* bfrag = nullptr;
   float* tau = nullptr;
@@ -2082,15 +2089,17 @@ struct EosHipTQIP {
   int batch_cap() const { return 32 * nqg; }
 
   ~EosHipTQIP() {
-    void* p[] = {packed, norms,      resnorms, alpha, beta,  ysum, bfrag, tau,
-                 cand,   cand_count, status,   samp,  dense, qr,   yv};
+    void* p[] = {packed, norms, resnorms, alpha, beta, ysum, bfrag, tau, cand, cand_count, status,
+                 samp, dense, qr, yv, tile_cn, lonorm, kq};
     for (void* x : p)
       if (x) (void)hipFree(x);
   }
 
+  // mode 3: the high-half bound filter (mode 1 of the _h kernel).
   int scan(int mode, int qb, int64_t tile_begin, int64_t tile_step, int64_t ntl, float* out,
            int64_t out_stride, const int* gate, char** err) {
     if (ntl <= 0) return 0;
+    const bool hi = mode == 3;
     TqIpScanArgs s;
     memset(&s, 0, sizeof(s));
     s.packed = packed;
@@ -2114,12 +2123,16 @@ struct EosHipTQIP {
     s.ntiles = (int)ntl;
     s.q = qb;
     s.cap = kCap;
-    s.mode = mode;
+    s.mode = hi ? 1 : mode;
     s.lut0 = lut0;
     s.lut1 = lut1;
+    s.lonorm = lonorm;
+    s.kq = kq;
+    s.tile_cn = tile_cn;
     char name[48];
-    snprintf(name, sizeof(name), "eos_tq_ipscan_k%d_g%d", ks, nqg);
-    static const char* const labels[3] = {"tq_ipscan_dense", "tq_ipscan_filter", "tq_ipscan_sample"};
+    snprintf(name, sizeof(name), "eos_tq_ipscan_k%d_g%d%s", ks, nqg, hi ? "_h" : "");
+    static const char* const labels[4] = {"tq_ipscan_dense", "tq_ipscan_filter", "tq_ipscan_sample",
+                                          "tq_ipscan_filter"};
     int64_t blocks = (ntl + 7) / 8;
     if (blocks > rt->compute_units) blocks = rt->compute_units;
     if (blocks < 1) blocks = 1;
@@ -2139,7 +2152,7 @@ struct EosHipTQIP {
     a.qmax = qmax;
     a.qmax2 = qmax2;
     a.cb_scale = cb_scale;
-    const IpFragOut f{bfrag, ysum, tau, cand_count, ks, nqg};
+    const IpFragOut f{bfrag, ysum, tau, cand_count, ks, nqg, lonorm, kq};
     return ip_prepare_launch(rt, a, qb, qr, yv, &f, err);
   }
 
@@ -2167,7 +2180,35 @@ struct EosHipTQIP {
       if (rt->launch("eos_tq_threshold", dim3(qb), dim3(256), 0, &sel, err, "tq_ip_threshold") != 0)
         return 1;
     }
-    if (scan(1, qb, 0, 1, ntiles, nullptr, 0, nullptr, err) != 0) return 1;
+    if (n > kCap) {
+      // High-half bound filter (ids), then their exact scores.
+      if (scan(3, qb, 0, 1, ntiles, nullptr, 0, nullptr, err) != 0) return 1;
+      TqIpRescoreArgs rs;
+      memset(&rs, 0, sizeof(rs));
+      rs.packed = packed;
+      rs.norms = norms;
+      rs.resnorms = resnorms;
+      rs.bfrag = bfrag;
+      rs.nqg = nqg;
+      rs.alpha = alpha;
+      rs.beta = beta;
+      rs.ysum = ysum;
+      rs.tau = tau;
+      rs.cand = cand;
+      rs.cand_count = cand_count;
+      rs.n = n;
+      rs.q = qb;
+      rs.d = d;
+      rs.ks = ks;
+      rs.cap = kCap;
+      rs.lut0 = lut0;
+      rs.lut1 = lut1;
+      if (rt->launch("eos_tq_ip_rescore", dim3((unsigned)qb, 2 * kRescoreBlocks), dim3(256), 0, &rs,
+                     err, "tq_ip_rescore") != 0)
+        return 1;
+    } else if (scan(1, qb, 0, 1, ntiles, nullptr, 0, nullptr, err) != 0) {
+      return 1;
+    }
     TqFinalizeArgs f;
     memset(&f, 0, sizeof(f));
     f.cand = cand;
@@ -2288,7 +2329,22 @@ int eoship_tq_ip_bind_corpus(EosHipRuntime* rt, const EosHipTQIPSpec* spec,
       rt->alloc((size_t)cols * std::max<int64_t>(samp_tiles, 1) * 4,
                 reinterpret_cast<void**>(&ip->samp), err) ||
       rt->alloc((size_t)cols * ip->d * 8, reinterpret_cast<void**>(&ip->qr), err) ||
-      rt->alloc((size_t)cols * ip->d * 8, reinterpret_cast<void**>(&ip->yv), err))
+      rt->alloc((size_t)cols * ip->d * 8, reinterpret_cast<void**>(&ip->yv), err) ||
+      rt->alloc((size_t)ip->ntiles * 16, reinterpret_cast<void**>(&ip->tile_cn), err) ||
+      rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->lonorm), err) ||
+      rt->alloc((size_t)cols * 4, reinterpret_cast<void**>(&ip->kq), err))
+    return fail();
+  TqIpTileNormArgs tn;
+  memset(&tn, 0, sizeof(tn));
+  tn.codes = d_codes;
+  tn.tile_cn = ip->tile_cn;
+  tn.n = n;
+  tn.d = ip->d;
+  tn.bits = ip->bits;
+  tn.row_bytes = a.row_bytes;
+  for (int v = 0; v < (1 << spec->bits); ++v) tn.cb[v] = spec->codebook[v];
+  if (rt->launch("eos_tq_ip_tile_cnorm", dim3((unsigned)((n + 255) / 256)), dim3(256), 0, &tn, err,
+                 "tq_ip_pack") != 0)
     return fail();
   TqIpPackArgs p;
   memset(&p, 0, sizeof(p));

@@ -306,6 +306,43 @@ struct TqIpScanArgs {
   long long n, out_begin, out_count, out_stride, tile_begin, tile_step;
   int ntiles, q, cap, mode;
   uint32_t lut0, lut1;     // the 8-entry int8 codebook: bytes C[0..3], C[4..7]
+  // High-half bound filter (the _h kernels, mode 1): only the MSE and QJL
+  // grids' high int8 halves enter the MFMAs; kept rows go to cand as ids
+  // (~id) for eos_tq_ip_rescore.
+  const float* lonorm;     // [32 * nqg] ||MSE lo||_2 of each column, rounded up
+  const int* kq;           // [32 * nqg] 2 sum_i max(QJL lo_i, 0) - sum Ys
+  const float* tile_cn;    // [ntiles][4]: max ||C[codes]||_2 (rounded up), -, -, -
+};
+
+// Exact rescoring of the inner-product filter's kept ids (eos_tq_ip_rescore):
+// entry e of cand[q] (an id ~v) becomes rank_key(score, v) when the exact
+// score reaches tau[q], else 0 (finalize skips zeros). Codes and signs are
+// read from the scan's tile layout.
+struct TqIpRescoreArgs {
+  const int32_t* packed;   // [ntiles][ks / 2][64][4]
+  const float* norms;      // [ntiles * 32]
+  const float* resnorms;   // [ntiles * 32]
+  const int8_t* bfrag;     // the scan's query fragments [ks][4 nqg][64][16]
+  const float* alpha;
+  const float* beta;
+  const int* ysum;
+  const float* tau;
+  unsigned long long* cand;
+  const uint32_t* cand_count;
+  long long n;
+  int q, d, ks, nqg, cap;
+  uint32_t lut0, lut1;
+};
+
+// Per tile of the inner-product layout: {max ||C[codes]||_2 rounded up, 0, 0,
+// 0}; one thread per vector, codes from the reference rows (low bits first,
+// a code may straddle two bytes).
+struct TqIpTileNormArgs {
+  const uint8_t* codes;    // [n][row_bytes]
+  float* tile_cn;          // [ntiles][4]
+  long long n;
+  int d, bits, row_bytes;
+  int cb[8];
 };
 
 // out[c][j] = sum over k ascending of M[j][k] in[c][k] (one f64 fma chain per
@@ -338,6 +375,10 @@ struct TqIpQuantArgs {
   int q, d, qmax, qmax2;
   float cb_scale;
   int ks, nqg;
+  // bound filter inputs (frag mode, each optional): per column ||MSE lo||_2
+  // rounded up and 2 sum max(QJL lo, 0) - sum Ys
+  float* lonorm;           // [32 * nqg]
+  int* kq;                 // [32 * nqg]
 };
 
 #endif  // EOSHIP_TQ_ARGS_H

@@ -634,7 +634,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_matvec(TqIpMatArgs a
 // the column's filter state reset (tau = -inf, no kept candidates).
 extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_quant(TqIpQuantArgs a) {
   __shared__ double red[4];
-  __shared__ int ired[4];
+  __shared__ int ired[12];
   const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int d = a.d;
   const bool live = c < a.q;
@@ -662,7 +662,7 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_quant(TqIpQuantArgs 
   const double inv2 = my > 0.0 ? (double)a.qmax2 / my : 0.0;
   const int dpad = a.bfrag != nullptr ? a.ks * 32 : d;
   const int gq = c >> 5, col = c & 31, ncb = 4 * a.nqg;
-  int ysum = 0;
+  int ysum = 0, lo2 = 0, plo = 0;
   for (int j = tid; j < dpad; j += 256) {
     int qv = 0, yv = 0;
     if (live && j < d) {
@@ -679,6 +679,8 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_quant(TqIpQuantArgs 
     if (a.bfrag != nullptr) {
       const int qlo = ((qv + 128) & 255) - 128, qhi = (qv - qlo) >> 8;
       const int ylo = ((yv + 128) & 255) - 128, yhi = (yv - ylo) >> 8;
+      lo2 += qlo * qlo;
+      plo += ylo > 0 ? ylo : 0;
       const int s = j >> 5, g = (j >> 4) & 1, i = j & 15;
       int8_t* base = a.bfrag + ((size_t)(s * ncb + 4 * gq) * 64 + col + 32 * g) * 16 + i;
       base[0] = (int8_t)qhi;
@@ -689,8 +691,16 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_quant(TqIpQuantArgs 
   }
   if (a.bfrag != nullptr) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ysum += __shfl_xor(ysum, o);
-    if (lane == 0) ired[w] = ysum;
+    for (int o = 32; o >= 1; o >>= 1) {
+      ysum += __shfl_xor(ysum, o);
+      lo2 += __shfl_xor(lo2, o);
+      plo += __shfl_xor(plo, o);
+    }
+    if (lane == 0) {
+      ired[w] = ysum;
+      ired[4 + w] = lo2;
+      ired[8 + w] = plo;
+    }
     __syncthreads();
   }
   if (tid == 0) {
@@ -701,9 +711,12 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_quant(TqIpQuantArgs 
                            : 0.0f;
     }
     if (a.bfrag != nullptr) {
-      a.ysum[c] = ired[0] + ired[1] + ired[2] + ired[3];
+      const int ys_all = ired[0] + ired[1] + ired[2] + ired[3];
+      a.ysum[c] = ys_all;
       a.tau[c] = -__builtin_inff();
       a.cand_count[c] = 0u;
+      if (a.lonorm != nullptr) a.lonorm[c] = sqrt_up((long long)(ired[4] + ired[5] + ired[6] + ired[7]));
+      if (a.kq != nullptr) a.kq[c] = 2 * (ired[8] + ired[9] + ired[10] + ired[11]) - ys_all;
     }
   }
 }
@@ -1297,10 +1310,20 @@ EOS_DEV void ip_decode(uint32_t L, uint32_t HS, uint32_t lut0, uint32_t lut1, v4
   sf.w = (int)((HS >> 7) & m1);
 }
 
-template <int KS, int NQG>
+// HI (mode 1 only): the high-half bound filter. With Qs = 256 hi + lo and
+// Ys = 256 yhi + ylo, D_mse <= 256 D_mse,hi + lb (lb = ||lo||_2 times the
+// tile's largest ||C[codes]||_2, both rounded up, bumped by 2^-22) and
+// D_qjl = 2 sum_{bit=1} Ys - sum Ys <= 512 S_hi + kq (S_hi = sum_{bit=1}
+// yhi, kq = 2 sum max(ylo, 0) - sum Ys). The score's f32 expression is
+// monotone in both dots (alpha, beta, ResNorm, Norm >= 0; rounding is
+// monotone), so evaluated on the bounds it is >= the exact score: every row
+// scoring >= tau is kept, as an id for eos_tq_ip_rescore.
+template <int KS, int NQG, bool HI>
 EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
   constexpr int NCB = 4 * NQG, NQ = 32 * NQG, NTH = 512, NWV = NTH / 64, NLOAD = KS / 2;
-  __shared__ v4i sb[KS * NCB * 64];
+  constexpr int UPG = HI ? 2 : 4;  // column blocks per group in the MFMAs
+  constexpr int NCBU = UPG * NQG;
+  __shared__ v4i sb[KS * NCBU * 64];
   __shared__ uint32_t lc_cnt[NQ];
   __shared__ u64 lc_buf[NQ * kLdsSlots];
   __shared__ float4 nstage[NWV][16];
@@ -1315,7 +1338,7 @@ EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
   const int half = lane >> 5;
   const v4i* packed = reinterpret_cast<const v4i*>(a.packed);
   const bool filter = a.mode == 1;
-  float al_r[NQG], be_r[NQG], ta_r[NQG];
+  float al_r[NQG], be_r[NQG], ta_r[NQG], lo_r[NQG];
   int ys_r[NQG];
   bool live_r[NQG];
 #pragma unroll
@@ -1324,12 +1347,14 @@ EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
     live_r[g] = qi < a.q;
     al_r[g] = live_r[g] ? a.alpha[qi] : 0.0f;
     be_r[g] = live_r[g] ? a.beta[qi] : 0.0f;
-    ys_r[g] = live_r[g] ? a.ysum[qi] : 0;
+    ys_r[g] = live_r[g] ? (HI ? a.kq[qi] : a.ysum[qi]) : 0;
     ta_r[g] = (filter && live_r[g]) ? a.tau[qi] : __builtin_inff();
+    lo_r[g] = (HI && live_r[g]) ? a.lonorm[qi] : 0.0f;
   }
   struct Stage {
     v4i raw[NLOAD];
     float nv;  // lanes 0-31: the tile's Norms; lanes 32-63: its ResNorms
+    float cn;  // HI: the tile's code-norm bound
     int t;
   };
   auto load_stage = [&](Stage& st, int jj) {
@@ -1338,14 +1363,15 @@ EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
 #pragma unroll
     for (int c = 0; c < NLOAD; ++c) st.raw[c] = __builtin_nontemporal_load(src + c * 64);
     st.nv = lane < 32 ? a.norms[t * kTile + lane] : a.resnorms[t * kTile + (lane & 31)];
+    if constexpr (HI) st.cn = a.tile_cn[4 * t];
   };
   auto process = [&](const Stage& st, int j) {
     const long long tile = a.tile_begin + (long long)j * a.tile_step;
     int boff = lane;
     asm volatile("" : "+v"(boff));
-    v16i acc[NCB];
+    v16i acc[NCBU];
 #pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) acc[cb] = v16i{0};
+    for (int cb = 0; cb < NCBU; ++cb) acc[cb] = v16i{0};
 #pragma unroll
     for (int c = 0; c < NLOAD; ++c) {
 #pragma unroll
@@ -1357,10 +1383,11 @@ EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
 #pragma unroll
         for (int g = 0; g < NQG; ++g) {
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const v4i bf = sb[(s * NCB + 4 * g + u) * 64 + boff];
-            acc[4 * g + u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(u < 2 ? af : sf, bf,
-                                                                  acc[4 * g + u], 0, 0, 0);
+          for (int u = 0; u < UPG; ++u) {
+            const v4i bf = sb[(s * NCBU + UPG * g + u) * 64 + boff];
+            const bool mse = HI ? u == 0 : u < 2;
+            acc[UPG * g + u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(mse ? af : sf, bf,
+                                                                    acc[UPG * g + u], 0, 0, 0);
           }
         }
       }
@@ -1380,6 +1407,7 @@ EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
       if (!live_r[g]) continue;
       const int qi = g * 32 + (lane & 31);
       float smax = -__builtin_inff();
+      const float lb = HI ? (lo_r[g] * st.cn) * 1.0000002f : 0.0f;  // >= lonorm * cn
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const float4 n4 = nstage[wave][2 * i4 + half];
@@ -1390,10 +1418,16 @@ EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * i4 + e;
-          const int dm = acc[4 * g][i] * 256 + acc[4 * g + 1][i];
-          const int dq = 2 * (acc[4 * g + 2][i] * 256 + acc[4 * g + 3][i]) - ys_r[g];
-          const float t1 = (float)dm * al_r[g];
-          const float t2 = (float)dq * be_r[g];
+          float fdm, fdq;
+          if constexpr (HI) {
+            fdm = __builtin_fmaf((float)acc[2 * g][i], 256.0f, lb);
+            fdq = (float)(acc[2 * g + 1][i] * 512 + ys_r[g]);
+          } else {
+            fdm = (float)(acc[4 * g][i] * 256 + acc[4 * g + 1][i]);
+            fdq = (float)(2 * (acc[4 * g + 2][i] * 256 + acc[4 * g + 3][i]) - ys_r[g]);
+          }
+          const float t1 = fdm * al_r[g];
+          const float t2 = fdq * be_r[g];
           const float t3 = rv4[e] * t2;
           sc[e] = (t1 + t3) * nv4[e];
         }
@@ -1408,7 +1442,8 @@ EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               if (r0 + e < rem && sc[e] >= ta) {
-                const u64 key = rank_key(sc[e], (uint32_t)(vbase + r0 + e));
+                const u64 key = HI ? (u64)(~(uint32_t)(vbase + r0 + e))
+                                   : rank_key(sc[e], (uint32_t)(vbase + r0 + e));
                 if (pos < (uint32_t)kLdsSlots) {
                   lc_buf[qi * kLdsSlots + pos] = key;
                 } else {
@@ -1452,14 +1487,18 @@ EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
   constexpr int R = 2;
   Stage st[R];
   {
-    constexpr int FCOUNT = KS * NCB * 64;
+    // HI stages the high blocks only (block 4 g of the MSE grid, 4 g + 2 of
+    // the QJL grid).
+    constexpr int FCOUNT = KS * NCBU * 64;
     constexpr int FPER = (FCOUNT + NTH - 1) / NTH;
     const v4i* fsrc = reinterpret_cast<const v4i*>(a.bfrag);
     v4i fv[FPER];
 #pragma unroll
     for (int r = 0; r < FPER; ++r) {
       const int i = threadIdx.x + r * NTH;
-      if (i < FCOUNT) fv[r] = fsrc[i];
+      const int stp = i / (NCBU * 64), rem = i - stp * (NCBU * 64);
+      const int cb = HI ? 4 * ((rem >> 6) >> 1) + 2 * ((rem >> 6) & 1) : (rem >> 6);
+      if (i < FCOUNT) fv[r] = fsrc[((size_t)stp * NCB + cb) * 64 + (rem & 63)];
     }
     st[0].t = rb + wave;
     load_stage(st[0], cl(st[0].t));
@@ -1502,7 +1541,11 @@ EOS_DEV void tq_ipscan_body(const TqIpScanArgs& a) {
 #define EOS_TQ_IPSCAN(KS, NQG)                                                            \
   extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) \
   void eos_tq_ipscan_k##KS##_g##NQG(TqIpScanArgs a) {                                     \
-    tq_ipscan_body<KS, NQG>(a);                                                           \
+    tq_ipscan_body<KS, NQG, false>(a);                                                    \
+  }                                                                                        \
+  extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 8))) \
+  void eos_tq_ipscan_k##KS##_g##NQG##_h(TqIpScanArgs a) {                                 \
+    tq_ipscan_body<KS, NQG, true>(a);                                                     \
   }
 EOS_TQ_IPSCAN(4, 2)
 EOS_TQ_IPSCAN(8, 2)
@@ -1511,6 +1554,115 @@ EOS_TQ_IPSCAN(16, 1)
 EOS_TQ_IPSCAN(24, 1)
 EOS_TQ_IPSCAN(32, 1)
 #undef EOS_TQ_IPSCAN
+
+// Exact rescoring of the inner-product filter's kept ids (TqIpRescoreArgs):
+// grid (q, y), eight threads per candidate. The workgroup's query fragments
+// (the scan's int8 halves of both grids, fragment byte order) are staged in
+// LDS; a thread takes the (K step, lane half) units u = sub, sub + 8, ... of
+// the vector (16 dimensions each, 8 bytes of the tile layout), decodes them
+// as the scan does and accumulates the four int8 dots with v_dot4. The dots
+// are exact integers, the score the scan's f32 expression.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_rescore(TqIpRescoreArgs a) {
+  __shared__ v4i fr[32 * 2 * 4];  // [K step][lane half][MSE hi, MSE lo, QJL hi, QJL lo]
+  const int q = blockIdx.x;
+  if (q >= a.q) return;
+  const int tid = threadIdx.x, sub = tid & 7;
+  const uint32_t cnt = a.cand_count[q];
+  if (cnt > (uint32_t)a.cap) return;  // overflowed: finalize flags it
+  const uint32_t first = blockIdx.y * 32u;
+  if (first >= cnt) return;
+  const int nl = a.ks / 2, nunits = 2 * a.ks;
+  u64* list = a.cand + (size_t)q * a.cap;
+  // The first entry is requested together with the fragments (one round
+  // trip for both).
+  uint32_t lid_next = first + (uint32_t)(tid >> 3) < cnt ? rank_id(list[first + (tid >> 3)]) : 0u;
+  {
+    const int gq = q >> 5, col = q & 31, ncb = 4 * a.nqg;
+    const v4i* bf = reinterpret_cast<const v4i*>(a.bfrag);
+    for (int i = tid; i < nunits * 4; i += 256) {
+      const int u = i >> 2, blk = i & 3, st = u >> 1, g = u & 1;
+      fr[i] = bf[((size_t)st * ncb + 4 * gq + blk) * 64 + col + 32 * g];
+    }
+  }
+  __syncthreads();
+  const float al = a.alpha[q], be = a.beta[q], ta = a.tau[q];
+  const int ysum = a.ysum[q];
+  const uint2* packed = reinterpret_cast<const uint2*>(a.packed);
+  for (uint32_t base = first; base < cnt; base += 32u * gridDim.y) {
+    // Entries are rewritten in place, so a lane past the end reads no entry
+    // (it scores vector 0 and writes nothing); an id outside the corpus is
+    // dropped without reading its codes.
+    const uint32_t i = base + (uint32_t)(tid >> 3);
+    const bool in_list = i < cnt;
+    const uint32_t lid = base == first ? lid_next : (in_list ? rank_id(list[i]) : 0u);
+    const bool live = in_list && (long long)lid < a.n;
+    const uint32_t v = live ? lid : 0u;
+    const long long t = v >> 5;
+    const int m = (int)(v & 31u);
+    const float rn = a.resnorms[v], nv = a.norms[v];
+    int dm = 0, sq = 0;
+    for (int u = sub; u < nunits; u += 8) {
+      const int st = u >> 1, g = u & 1;
+      // dwords 2 (st % 2) and + 1 of the lane's 16 bytes of chunk st / 2
+      const uint2 w = packed[(((size_t)t * nl + (st >> 1)) * 64 + m + 32 * g) * 2 + (st & 1)];
+      v4i af, sf;
+      ip_decode(w.x, w.y, a.lut0, a.lut1, af, sf);
+      const v4i qh = fr[4 * u], ql = fr[4 * u + 1], yh = fr[4 * u + 2], yl = fr[4 * u + 3];
+      int dh = 0, dl = 0, sh = 0, sl = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        dh = __builtin_amdgcn_sdot4(af[k], qh[k], dh, false);
+        dl = __builtin_amdgcn_sdot4(af[k], ql[k], dl, false);
+        sh = __builtin_amdgcn_sdot4(sf[k], yh[k], sh, false);
+        sl = __builtin_amdgcn_sdot4(sf[k], yl[k], sl, false);
+      }
+      dm += dh * 256 + dl;
+      sq += sh * 256 + sl;
+    }
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+      dm += __shfl_xor(dm, o);
+      sq += __shfl_xor(sq, o);
+    }
+    const int dq = 2 * sq - ysum;
+    const float t1 = (float)dm * al;
+    const float t2 = (float)dq * be;
+    const float t3 = rn * t2;
+    const float sc = (t1 + t3) * nv;
+    if (in_list && sub == 0) list[i] = (live && sc >= ta) ? rank_key(sc, v) : 0ull;
+  }
+}
+
+// Per tile of the inner-product layout, the largest ||C[codes]||_2 over its
+// vectors (exact integer sums of squares, rounded up): one thread per
+// vector, a half-wave per tile.
+extern "C" __global__ __launch_bounds__(256) void eos_tq_ip_tile_cnorm(TqIpTileNormArgs a) {
+  const long long v = (long long)blockIdx.x * 256 + threadIdx.x;
+  long long ss = 0;
+  if (v < a.n) {
+    const uint8_t* row = a.codes + (size_t)v * a.row_bytes;
+    const uint32_t mask = (1u << a.bits) - 1u;
+    for (int j = 0; j < a.d; ++j) {
+      const int bit = j * a.bits, sh = bit & 7;
+      uint32_t code = (uint32_t)row[bit >> 3] >> sh;
+      if (sh + a.bits > 8) code |= (uint32_t)row[(bit >> 3) + 1] << (8 - sh);
+      const int c = a.cb[code & mask];
+      ss += (long long)(c * c);
+    }
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) {
+    const long long t = __shfl_xor(ss, o);
+    ss = t > ss ? t : ss;
+  }
+  const long long tile = v >> 5;
+  if ((threadIdx.x & 31) == 0 && tile * kTile < a.n) {
+    a.tile_cn[4 * tile] = sqrt_up(ss);
+    a.tile_cn[4 * tile + 1] = 0.0f;
+    a.tile_cn[4 * tile + 2] = 0.0f;
+    a.tile_cn[4 * tile + 3] = 0.0f;
+  }
+}
 
 // ----------------------------------------------------------------- rescore
 
