@@ -99,6 +99,28 @@ EOS_DEV float wave_max_dpp(float v) {
   return fmaxf(a, b);
 }
 
+// Maximum over the wavefront of non-negative values (|y|, or 0): for
+// non-negative floats the order of the bit patterns as unsigned integers is
+// the order of the values, so the steps are integer maxima (one DPP
+// instruction each, no NaN canonicalization).
+template <int CTRL>
+EOS_DEV uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+EOS_DEV float wave_max_nonneg(float f) {
+  uint32_t v = __builtin_bit_cast(uint32_t, f);
+  v = max(v, dpp_u32<0xb1>(v));
+  v = max(v, dpp_u32<0x4e>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  const unsigned a16 = r16[0], b16 = r16[1];
+  v = max(a16, b16);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  const unsigned a32 = r32[0], b32 = r32[1];
+  return __builtin_bit_cast(float, max(a32, b32));
+}
+
 // Symmetric per-row int8 quantization: scale = max|y| / 127 (0 for a zero
 // row), code = rint(y * 127 / max|y|), |code| <= 127.
 EOS_DEV float q8_inv(float amax) { return amax > 0.0f ? 127.0f / amax : 0.0f; }
@@ -906,8 +928,9 @@ EOS_DEV void ln_rows(const uint16_t* const (&y)[NR], const LnParams<H>& p, float
       x[r][t][0] = __builtin_fmaf(x[r][t][0], inv[r] * p.g[t].x, p.b[t].x);
       x[r][t][1] = __builtin_fmaf(x[r][t][1], inv[r] * p.g[t].y, p.b[t].y);
       amax[r] = fmaxf(amax[r], fmaxf(fabsf(x[r][t][0]), fabsf(x[r][t][1])));
-      *reinterpret_cast<uint32_t*>(yout[r] + 2 * lane + 128 * t) =
-          (uint32_t)f2h(x[r][t][0]) | ((uint32_t)f2h(x[r][t][1]) << 16);
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const h2 hv = {(_Float16)x[r][t][0], (_Float16)x[r][t][1]};
+      *reinterpret_cast<uint32_t*>(yout[r] + 2 * lane + 128 * t) = __builtin_bit_cast(uint32_t, hv);
     }
   }
   // int8 codes: callers give q8 for every row or for none. The rows'
@@ -917,7 +940,7 @@ EOS_DEV void ln_rows(const uint16_t* const (&y)[NR], const LnParams<H>& p, float
   if (q8[0] == nullptr) return;
   float am[NR], qi[NR];
 #pragma unroll
-  for (int r = 0; r < NR; ++r) am[r] = wave_max_dpp(amax[r]);
+  for (int r = 0; r < NR; ++r) am[r] = wave_max_nonneg(amax[r]);
 #pragma unroll
   for (int r = 0; r < NR; ++r) qi[r] = am[r] > 0.0f ? 127.0f * __builtin_amdgcn_rcpf(am[r]) : 0.0f;
   // code = rint(out * qi) by one fma: 1.5 * 2^23 + v rounds v to the
