@@ -58,6 +58,9 @@ struct DevLayer {
   uint16_t* w_of = nullptr;
   int8_t* w_1f = nullptr;
   uint16_t* w_2f = nullptr;
+  // General-shape path: int8 codes of the O and FFN-down weights.
+  int8_t* w_o8 = nullptr;
+  int8_t* w_28 = nullptr;
 };
 
 }  // namespace
@@ -73,6 +76,10 @@ struct EosHipEncoder {
   // LayerNorm as one kernel per row block (eos_enc_tail_*); otherwise, or
   // when switched off, the unfused GEMM + LayerNorm launches.
   bool fused_tail = true;
+  // BERT family at a hidden width or head dim the MFMA kernels do not take
+  // (e.g. hidden 16, head dim 4): the f32 eos_enc_gen_* kernels run every
+  // layer instead.
+  bool general = false;
   // Compact family: attention scores times 1/sqrt(head dim) (else plain q kT),
   // and attention over every position of the padded input with the mask
   // selecting only the pooled rows (else over each sequence's mask != 0
@@ -97,6 +104,9 @@ struct EosHipEncoder {
   int8_t* h8 = nullptr;
   float* hs = nullptr;
   float* pool_part = nullptr;  // [batch][chunks][hidden] pool partial sums
+  // General-shape path: f32 hidden rows, the first LayerNorm's output, q|k|v
+  // rows, attention output and FFN intermediate.
+  float *hf = nullptr, *h1f = nullptr, *qkvf = nullptr, *ctxf = nullptr, *midf = nullptr;
   // V of the QKV projection, feature-major [hidden][vt_ld] (zeroed padding
   // past the rows, so attention may read whole 16-byte key groups)
   uint16_t* vt = nullptr;
@@ -111,8 +121,9 @@ struct EosHipEncoder {
   ~EosHipEncoder() {
     for (void* p : owned)
       if (p) hipFree(p);
-    void* act[] = {h,     qkv,     ctx,     mid,   h8,    hs,     pool_part, vt, row_b,
-                   row_t, seq_off, seq_cnt, seq_q, total, status, io};
+    void* act[] = {h,     qkv,     ctx,     mid,   h8,    hs,   pool_part, vt, row_b,
+                   row_t, seq_off, seq_cnt, seq_q, total, status, io,   hf,        h1f, qkvf,
+                   ctxf,  midf};
     for (void* p : act)
       if (p) hipFree(p);
   }
@@ -189,10 +200,11 @@ struct EosHipEncoder {
   int ensure_activations(int batch, int tokens, char** err) {
     const size_t rows = row_capacity(batch, tokens);
     if (rows <= cap_rows && batch <= cap_batch) return 0;
-    void* act[] = {h,     qkv,     ctx,     mid,   h8,    hs,    pool_part, vt,
-                   row_b, row_t, seq_off, seq_cnt, seq_q, total, status};
+    void* act[] = {h,     qkv,   ctx,     mid,     h8,    hs,     pool_part, vt,  row_b, row_t,
+                   seq_off, seq_cnt, seq_q, total, status, hf,  h1f,       qkvf, ctxf, midf};
     for (void* p : act)
       if (p) hipFree(p);
+    hf = h1f = qkvf = ctxf = midf = nullptr;
     h = qkv = ctx = mid = nullptr;
     h8 = nullptr;
     hs = nullptr;
@@ -220,6 +232,13 @@ struct EosHipEncoder {
         rt->alloc(4, reinterpret_cast<void**>(&total), err) ||
         rt->alloc(8, reinterpret_cast<void**>(&status), err))
       return 1;
+    if (general &&
+        (rt->alloc(rows * H * 4, reinterpret_cast<void**>(&hf), err) ||
+         rt->alloc(rows * H * 4, reinterpret_cast<void**>(&h1f), err) ||
+         rt->alloc(rows * 3 * H * 4, reinterpret_cast<void**>(&qkvf), err) ||
+         rt->alloc(rows * H * 4, reinterpret_cast<void**>(&ctxf), err) ||
+         rt->alloc(rows * F * 4, reinterpret_cast<void**>(&midf), err)))
+      return 1;
     // At least 64 zeroed entries past the rows (attention reads whole 64-key
     // blocks); 72, so that the row stride is no multiple of 1 KiB (with +64
     // at c3 it was exactly 65 KiB and the transposed V stores of the QKV
@@ -231,6 +250,90 @@ struct EosHipEncoder {
     cap_rows = rows;
     cap_batch = batch;
     return 0;
+  }
+
+  // The general-shape forward (rows already packed): f32 activations,
+  // eos_enc_gen_* per operation, pooled from the f32 rows.
+  int forward_general(const int32_t* d_ids, const int32_t* d_types, int batch, int tokens,
+                      float* d_out, bool cls, char** err) {
+    const int H = desc.hidden, F = desc.intermediate, nh = desc.heads;
+    const int max_rows = (int)row_capacity(batch, tokens);
+    EncGenArgs g;
+    memset(&g, 0, sizeof(g));
+    g.ids = d_ids;
+    g.type_ids = d_types;
+    g.row_b = row_b;
+    g.row_t = row_t;
+    g.total = total;
+    g.status = status;
+    g.seq_off = seq_off;
+    g.seq_cnt = seq_cnt;
+    g.seq_q = seq_q;
+    g.hidden = H;
+    g.heads = nh;
+    g.tokens = tokens;
+    g.vocab = desc.vocab;
+    g.npos = desc.max_positions;
+    g.ntype = desc.type_vocab;
+    g.max_rows = max_rows;
+    g.eps = desc.ln_eps;
+    const unsigned row_blocks = (unsigned)((max_rows + 3) / 4);
+    {
+      EncGenArgs e = g;
+      e.tok = tok;
+      e.pos = pos;
+      e.typ = typ;
+      e.gamma = eg;
+      e.beta = eb;
+      e.y = hf;
+      if (rt->launch("eos_enc_gen_embed", dim3(row_blocks), dim3(256), 0, &e, err) != 0) return 1;
+    }
+    auto dense = [&](const float* x, float* y, const float* res, const int8_t* w, const float* sc,
+                     const float* b, int n, int k, int epi, const char* label) {
+      EncGenArgs d = g;
+      d.x = x;
+      d.y = y;
+      d.res = res;
+      d.w = w;
+      d.wscale = sc;
+      d.bias = b;
+      d.n = n;
+      d.k = k;
+      d.epi = epi;
+      return rt->launch("eos_enc_gen_dense", dim3((unsigned)((n + 63) / 64), row_blocks), dim3(256),
+                        0, &d, err, label);
+    };
+    auto layer_norm = [&](float* y, const float* gm, const float* bt) {
+      EncGenArgs l = g;
+      l.y = y;
+      l.gamma = gm;
+      l.beta = bt;
+      return rt->launch("eos_enc_gen_ln", dim3(row_blocks), dim3(256), 0, &l, err, "enc_ln");
+    };
+    for (const DevLayer& L : layers) {
+      EncGenArgs at = g;
+      at.x = qkvf;
+      at.y = ctxf;
+      if (dense(hf, qkvf, nullptr, L.w_qkv8, L.s_qkv, L.b_qkv, 3 * H, H, 0, "enc_gemm_qkv") != 0 ||
+          rt->launch("eos_enc_gen_attn", dim3((unsigned)((tokens + 8 + 63) / 64), nh, batch),
+                     dim3(64), 0, &at, err, "eos_enc_attn") != 0 ||
+          dense(ctxf, h1f, hf, L.w_o8, L.s_o, L.b_o, H, H, 0, "enc_gemm_o") != 0 ||
+          layer_norm(h1f, L.g1, L.be1) != 0 ||
+          dense(h1f, midf, nullptr, L.w_18, L.s_1, L.b_1, F, H, desc.gelu, "enc_gemm_ffn_up") != 0 ||
+          dense(midf, hf, h1f, L.w_28, L.s_2, L.b_2, H, F, 0, "enc_gemm_ffn_down") != 0 ||
+          layer_norm(hf, L.g2, L.be2) != 0)
+        return 1;
+    }
+    EncPoolArgs pl;
+    memset(&pl, 0, sizeof(pl));
+    pl.seq_off = seq_off;
+    pl.seq_cnt = seq_cnt;
+    pl.out = d_out;
+    pl.batch = batch;
+    pl.hidden = H;
+    pl.cls_seq_q = cls ? seq_q : nullptr;
+    pl.h32 = hf;
+    return rt->launch("eos_enc_gen_pool", dim3(batch), dim3(1024), 0, &pl, err, "eos_enc_pool");
   }
 
   int forward(const int32_t* d_ids, const int32_t* d_types, const int32_t* d_mask, int batch,
@@ -262,6 +365,7 @@ struct EosHipEncoder {
     if (rt->launch("eos_enc_count", dim3(batch), dim3(256), 0, &pk, err) != 0 ||
         rt->launch("eos_enc_pack", dim3(batch), dim3(256), 0, &pk, err) != 0)
       return 1;
+    if (general) return forward_general(d_ids, d_types, batch, tokens, d_out, cls, err);
     EncEmbedArgs em;
     memset(&em, 0, sizeof(em));
     em.ids = d_ids;
@@ -365,7 +469,14 @@ struct EosHipEncoder {
   }
 };
 
-// Shapes the kernels support: hidden widths 128..768 (embed and LayerNorm
+// Shapes the general-shape (f32) path takes: hidden a multiple of 8 up to
+// 1024, head dims up to 64, any positive FFN width up to 16384.
+static bool general_dims(int H, int heads, int F) {
+  return H >= 8 && H <= 1024 && H % 8 == 0 && heads > 0 && H % heads == 0 && H / heads <= 64 &&
+         F > 0 && F <= 16384;
+}
+
+// Shapes the MFMA kernels support: hidden widths 128..768 (embed and LayerNorm
 // hold a row in one wavefront; every GEMM N a multiple of the 128-column
 // tile), attention head dims 32/64/128/256, FFN widths in multiples of 128.
 static int check_dims(int H, int heads, int F, const char* what, char** err) {
@@ -392,7 +503,11 @@ int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const 
     return set_err(err, "eoship_encoder_bind: NULL argument");
   *out = nullptr;
   const int H = desc->hidden, F = desc->intermediate;
-  if (check_dims(H, desc->heads, F, "eoship_encoder_bind", err) != 0) return 1;
+  // Shapes outside the MFMA kernels run the general-shape path when it takes
+  // them (else the MFMA shapes' error is reported).
+  const bool general = check_dims(H, desc->heads, F, "", nullptr) != 0 &&
+                       general_dims(H, desc->heads, F);
+  if (!general && check_dims(H, desc->heads, F, "eoship_encoder_bind", err) != 0) return 1;
   if (desc->layers < 0 || desc->vocab <= 0 || desc->max_positions <= 0 || desc->type_vocab <= 0)
     return set_err(err, "eoship_encoder_bind: layers/vocab/positions/type_vocab out of range");
   if (!(desc->ln_eps >= 0.f)) return set_err(err, "eoship_encoder_bind: ln_eps must be >= 0");
@@ -401,6 +516,7 @@ int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const 
   auto* enc = new EosHipEncoder();
   enc->rt = rt;
   enc->desc = *desc;
+  enc->general = general;
   auto fail = [&]() {
     delete enc;
     return 1;
@@ -436,6 +552,9 @@ int eoship_encoder_bind(EosHipRuntime* rt, const EosHipEncoderDesc* desc, const 
         enc->upload(&d.be2, s.ln2_beta, (size_t)H, err) ||
         enc->upload(&d.w_qkv8, s.w_qkv, (size_t)3 * H * H, err) ||
         enc->upload(&d.w_18, s.w_1, (size_t)F * H, err))
+      return fail();
+    if (general && (enc->upload(&d.w_o8, s.w_o, (size_t)H * H, err) ||
+                    enc->upload(&d.w_28, s.w_2, (size_t)H * F, err)))
       return fail();
     if ((H == 384 || H == 512 || H == 768) &&
         (enc->upload_frag16(&d.w_of, s.w_o, H, H, err) ||

@@ -885,15 +885,22 @@ int classify_bert(const EosHipMll* m, const Json& art, const std::string& entry,
       return fail(bi, msg);
     }
   }
-  // What the fused encoder binds (its kernels' shapes).
+  // What the encoder binds: the MFMA kernels' shapes, or the general-shape
+  // (f32) kernels' (hidden a multiple of 8 up to 1024, head dim up to 64,
+  // intermediate up to 16384).
   const int64_t hd = H / heads;
-  if ((H != 128 && H != 256 && H != 384 && H != 512 && H != 768) ||
-      (hd != 32 && hd != 64 && hd != 128 && hd != 256) || F <= 0 || F % 128 != 0 ||
-      tok->dims[0] > (1ll << 30) || pos->dims[0] > 65536 || typ->dims[0] > 65536) {
-    char msg[160];
+  const bool mfma_shape = (H == 128 || H == 256 || H == 384 || H == 512 || H == 768) &&
+                          (hd == 32 || hd == 64 || hd == 128 || hd == 256) && F > 0 &&
+                          F % 128 == 0;
+  const bool general_shape = H >= 8 && H <= 1024 && H % 8 == 0 && hd <= 64 && F > 0 &&
+                             F <= 16384;
+  if ((!mfma_shape && !general_shape) || tok->dims[0] > (1ll << 30) || pos->dims[0] > 65536 ||
+      typ->dims[0] > 65536) {
+    char msg[200];
     std::snprintf(msg, sizeof(msg),
-                  "hidden %lld, head dim %lld, intermediate %lld outside the fused encoder "
-                  "(hidden 128/256/384/512/768, head dim 32/64/128/256, intermediate a multiple of 128)",
+                  "hidden %lld, head dim %lld, intermediate %lld outside the encoder (hidden "
+                  "128/256/384/512/768 with head dim 32/64/128/256 and intermediate a multiple of "
+                  "128, or hidden a multiple of 8 up to 1024 with head dim up to 64)",
                   (long long)H, (long long)hd, (long long)F);
     return fail(bi, msg);
   }

@@ -146,6 +146,41 @@ struct EncAttnArgs {
   int32_t* moves;
 };
 
+// General-shape BERT path (hidden widths and head dims the MFMA kernels do
+// not take): f32 activations, one launch per operation.
+//   eos_enc_gen_embed  token + position + type, affine LayerNorm -> y, h16
+//   eos_enc_gen_dense  y[m][n] = epi(sum_k x[m][k] (w[n][k] wscale[n]) + bias[n])
+//                      (+ res[m][n]); epi 0 identity, 1 erf GELU, 2 tanh GELU
+//   eos_enc_gen_ln     affine LayerNorm of y in place (and h16)
+//   eos_enc_gen_attn   softmax(q k^T / sqrt(hd)) v per (sequence, head, query)
+// Rows are the packed rows of eos_enc_pack (m < *total).
+struct EncGenArgs {
+  const int32_t* ids;
+  const int32_t* type_ids;  // or NULL
+  const int32_t* row_b;
+  const int32_t* row_t;
+  const int32_t* total;
+  const float* tok;         // [vocab][hidden]
+  const float* pos;         // [npos][hidden]
+  const float* typ;         // [ntype][hidden]
+  const float* gamma;
+  const float* beta;
+  const float* x;           // dense input [rows][k]; attention: qkv [rows][3 hidden]
+  float* y;                 // [rows][n] (LN, embed: [rows][hidden]; attention: ctx)
+  const float* res;         // dense residual [rows][n] or NULL
+  const int8_t* w;          // [n][k] int8 codes
+  const float* wscale;      // [n]
+  const float* bias;        // [n]
+  uint16_t* h16;            // embed / LN: f16 copy of the rows (pooling input) or NULL
+  int32_t* status;          // embed: 1 on an out-of-range id
+  const int32_t* seq_off;   // attention
+  const int32_t* seq_cnt;
+  const int32_t* seq_q;     // or NULL
+  int n, k, epi;
+  int hidden, heads, tokens, vocab, npos, ntype, max_rows;
+  float eps;
+};
+
 // mode 0: masked mean pool, then L2 normalize -> out [batch][hidden].
 // mode 1: L2 normalize every row, masked mean pool, then (proj != NULL)
 //   times proj [hidden][odim] -> out [batch][odim] (odim = hidden without).
@@ -169,6 +204,8 @@ struct EncPoolArgs {
   // normalize): the sequence's first row when position 0 is active, else the
   // query-only row after the active ones (seq_q > seq_cnt).
   const int32_t* cls_seq_q;
+  // eos_enc_gen_pool: the f32 rows [rows][hidden] (h is not read).
+  const float* h32;
 };
 
 // Tiny embed pipeline (examples/embed.eos): gather f16 table rows, multiply by

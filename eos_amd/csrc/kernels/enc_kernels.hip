@@ -2074,3 +2074,218 @@ extern "C" __global__ __launch_bounds__(256) void eos_embed_tiny(EmbedTinyArgs a
     a.out[(size_t)row * a.edim + e] = f2h(nv == 0.0f ? v : v / nv);
   }
 }
+
+// ---------------------------------------------------------- general shapes
+
+// BERT-family layers at shapes the MFMA kernels do not take (hidden widths
+// other than 128..768 in steps of 128, head dims other than 32..256: the
+// reference's own golden fixture has hidden 16 and head dim 4). f32
+// activations; the sums follow the reference's host path: f64 accumulation
+// from the bias in k order for the dense layers (denseHF), f64 mean and
+// variance for the LayerNorms (layerNormAffine), f64 logits, maximum, exp and
+// sum for the softmax, f32 sums over a sequence's rows in order for the mean
+// pool, f64 sum of squares for the L2 norm. Dense weights are the int8 codes
+// times their per-channel scale, as on the MFMA path.
+
+namespace {
+
+// Mean and 1 / sqrt(var + eps) (f64) of v[0..n) spread over a wavefront:
+// lane l holds v[l + 64 j], j < J.
+template <int J>
+EOS_DEV void gen_row_stats(const float (&v)[J], int n, int lane, float eps, double* mean,
+                           double* inv) {
+  double s = 0.0;
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    if (lane + 64 * j < n) s += (double)v[j];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  const double m = s / (double)n;
+  double q = 0.0;
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+    if (lane + 64 * j < n) {
+      const double c = (double)v[j] - m;
+      q += c * c;
+    }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+  *mean = m;
+  *inv = 1.0 / sqrt(q / (double)n + (double)eps);
+}
+
+constexpr int kGenMaxHidden = 1024;
+constexpr int kGenMaxHeadDim = 64;
+
+}  // namespace
+
+// One wavefront per packed row: token + position + type in f32, then the
+// affine LayerNorm; pad rows (position -1) get zeros.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gen_embed(EncGenArgs a) {
+  constexpr int J = kGenMaxHidden / 64;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= *a.total) return;
+  const int H = a.hidden;
+  float* yr = a.y + (size_t)row * H;
+  const int b = a.row_b[row], t = a.row_t[row];
+  if (t < 0) {
+    for (int c = lane; c < H; c += 64) {
+      yr[c] = 0.0f;
+      if (a.h16 != nullptr) a.h16[(size_t)row * H + c] = 0;
+    }
+    return;
+  }
+  int id = a.ids[(size_t)b * a.tokens + t];
+  int ty = a.type_ids != nullptr ? a.type_ids[(size_t)b * a.tokens + t] : 0;
+  if (id < 0 || id >= a.vocab || ty < 0 || ty >= a.ntype || t >= a.npos) {
+    if (lane == 0) *a.status = 1;
+    id = id < 0 || id >= a.vocab ? 0 : id;
+    ty = ty < 0 || ty >= a.ntype ? 0 : ty;
+  }
+  const int p = t < a.npos ? t : a.npos - 1;
+  float v[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = lane + 64 * j;
+    v[j] = c < H ? (a.tok[(size_t)id * H + c] + a.pos[(size_t)p * H + c]) + a.typ[(size_t)ty * H + c]
+                 : 0.0f;
+  }
+  double mean, inv;
+  gen_row_stats<J>(v, H, lane, a.eps, &mean, &inv);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = lane + 64 * j;
+    if (c < H) {
+      const float o = (float)(((double)v[j] - mean) * inv * (double)a.gamma[c] + (double)a.beta[c]);
+      yr[c] = o;
+      if (a.h16 != nullptr) a.h16[(size_t)row * H + c] = f2h(o);
+    }
+  }
+}
+
+// Thread (row, column): 64 columns x 4 rows per workgroup.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gen_dense(EncGenArgs a) {
+  const int col = blockIdx.x * 64 + (threadIdx.x & 63);
+  const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+  if (row >= *a.total || col >= a.n) return;
+  const float* xr = a.x + (size_t)row * a.k;
+  const int8_t* wr = a.w + (size_t)col * a.k;
+  const float sc = a.wscale[col];
+  double sum = (double)a.bias[col];
+  for (int k = 0; k < a.k; ++k) sum += (double)xr[k] * (double)((float)wr[k] * sc);
+  float o = (float)sum;
+  if (a.epi == 1) {
+    o = 0.5f * o * (1.0f + (float)erf((double)o / sqrt(2.0)));
+  } else if (a.epi == 2) {
+    const float inner = 0.7978845608f * (o + 0.044715f * (o * o * o));
+    o = 0.5f * o * (1.0f + (float)tanh((double)inner));
+  }
+  if (a.res != nullptr) o = o + a.res[(size_t)row * a.n + col];
+  a.y[(size_t)row * a.n + col] = o;
+}
+
+// One wavefront per row, in place; f16 copy into h16 when given.
+extern "C" __global__ __launch_bounds__(256) void eos_enc_gen_ln(EncGenArgs a) {
+  constexpr int J = kGenMaxHidden / 64;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= *a.total) return;
+  const int H = a.hidden;
+  float* yr = a.y + (size_t)row * H;
+  float v[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = lane + 64 * j;
+    v[j] = c < H ? yr[c] : 0.0f;
+  }
+  double mean, inv;
+  gen_row_stats<J>(v, H, lane, a.eps, &mean, &inv);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = lane + 64 * j;
+    if (c < H) {
+      const float o = (float)(((double)v[j] - mean) * inv * (double)a.gamma[c] + (double)a.beta[c]);
+      yr[c] = o;
+      if (a.h16 != nullptr) a.h16[(size_t)row * H + c] = f2h(o);
+    }
+  }
+}
+
+// Thread (query row, head) of sequence blockIdx.z: keys are the sequence's
+// active rows, in order; queries its rows up to seq_q (the CLS row included).
+// Rows of the sequence's 8-row slot past its queries get zeros.
+extern "C" __global__ __launch_bounds__(64) void eos_enc_gen_attn(EncGenArgs a) {
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int i = blockIdx.x * 64 + threadIdx.x;
+  const int cnt = a.seq_cnt[b];
+  const int qcnt = a.seq_q != nullptr ? a.seq_q[b] : cnt;
+  const int slot = (qcnt + 7) & ~7;
+  if (i >= slot) return;
+  const int off = a.seq_off[b];
+  const int H = a.hidden, hd = H / a.heads;
+  float* out = a.y + (size_t)(off + i) * H + h * hd;
+  if (i >= qcnt || cnt == 0) {
+    for (int d = 0; d < hd; ++d) out[d] = 0.0f;
+    return;
+  }
+  const int ld = 3 * H;
+  float q[kGenMaxHeadDim];
+  const float* qr = a.x + (size_t)(off + i) * ld + h * hd;
+#pragma unroll
+  for (int d = 0; d < kGenMaxHeadDim; ++d) q[d] = d < hd ? qr[d] : 0.0f;
+  const double scale = 1.0 / sqrt((double)hd);
+  auto logit = [&](int j) {
+    const float* kr = a.x + (size_t)(off + j) * ld + H + h * hd;
+    double dot = 0.0;
+#pragma unroll
+    for (int d = 0; d < kGenMaxHeadDim; ++d)
+      if (d < hd) dot += (double)q[d] * (double)kr[d];
+    return dot * scale;
+  };
+  double mx = -INFINITY;
+  for (int j = 0; j < cnt; ++j) mx = fmax(mx, logit(j));
+  double sum = 0.0;
+  for (int j = 0; j < cnt; ++j) sum += exp(logit(j) - mx);
+  float acc[kGenMaxHeadDim];
+#pragma unroll
+  for (int d = 0; d < kGenMaxHeadDim; ++d) acc[d] = 0.0f;
+  for (int j = 0; j < cnt; ++j) {
+    const double p = exp(logit(j) - mx) / sum;
+    const float* vr = a.x + (size_t)(off + j) * ld + 2 * H + h * hd;
+#pragma unroll
+    for (int d = 0; d < kGenMaxHeadDim; ++d)
+      if (d < hd) acc[d] += (float)(p * (double)vr[d]);
+  }
+  for (int d = 0; d < hd; ++d) out[d] = acc[d];
+}
+
+// One workgroup per sequence, thread c per feature: mean pool (f32 sums over
+// the sequence's active rows in order, times float32(1 / count); count 0 ->
+// zeros) or CLS (position 0's row), then L2 normalize (f64 sum of squares,
+// f32 norm, a zero row unchanged).
+extern "C" __global__ __launch_bounds__(1024) void eos_enc_gen_pool(EncPoolArgs a) {
+  __shared__ double red[16];
+  const int b = blockIdx.x, c = threadIdx.x, lane = c & 63, w = c >> 6;
+  const int off = a.seq_off[b], cnt = a.seq_cnt[b];
+  float v = 0.0f;
+  if (c < a.hidden) {
+    if (a.cls_seq_q != nullptr) {
+      const int row = off + (a.cls_seq_q[b] > cnt ? cnt : 0);
+      v = a.h32[(size_t)row * a.hidden + c];
+    } else if (cnt > 0) {
+      float s = 0.0f;
+      for (int r = 0; r < cnt; ++r) s = s + a.h32[(size_t)(off + r) * a.hidden + c];
+      v = s * (1.0f / (float)cnt);
+    }
+  }
+  double q = (double)v * (double)v;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o);
+  if (lane == 0) red[w] = q;
+  __syncthreads();
+  double ss = 0.0;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) ss += red[i];
+  const float nrm = (float)sqrt(ss);
+  if (c < a.hidden) a.out[(size_t)b * a.hidden + c] = nrm > 0.0f ? v / nrm : v;
+}

@@ -325,9 +325,11 @@ typedef struct EosHipEncoder EosHipEncoder;
  * (runtime/backend/bert_embedder_ops.go:101-197). */
 typedef struct {
   int32_t layers;        /* num_hidden_layers */
-  int32_t hidden;        /* 128, 256, 384, 512 or 768 */
-  int32_t heads;         /* hidden / heads in {32, 64, 128, 256} */
-  int32_t intermediate;  /* FFN width, multiple of 128 */
+  int32_t hidden;        /* MFMA kernels: 128, 256, 384, 512 or 768; else the
+                            general-shape f32 kernels: a multiple of 8 up to 1024 */
+  int32_t heads;         /* MFMA: hidden / heads in {32, 64, 128, 256};
+                            general-shape: hidden / heads <= 64 */
+  int32_t intermediate;  /* MFMA: a multiple of 128; general-shape: 1 .. 16384 */
   int32_t vocab;         /* token table rows */
   int32_t max_positions; /* position table rows (>= tokens) */
   int32_t type_vocab;    /* token-type table rows */

@@ -360,3 +360,27 @@ def bert_package(artifact: dict, tensors: dict, q8: tuple = (), q4: tuple = ()) 
             ("TNSR", mll_oracle.tnsr_body(entries), 0x11),
             ("XMTA", json.dumps(meta).encode(), 0x22)]
     return mll_oracle.write(secs, blake3)
+
+
+def golden_bert_tensors() -> dict:
+    """The reference's BERT golden fixture (tests/golden/bert_tiny, hidden 16,
+    4 heads, intermediate 32, 2 layers) in the importer's roles (f32)."""
+    import os
+    from safetensors.numpy import load_file
+    g = load_file(os.path.join(os.path.dirname(__file__), "golden", "bert_tiny",
+                               "model.safetensors"))
+    gt = {"token_embeddings": g["embeddings.word_embeddings.weight"],
+          "position_embeddings": g["embeddings.position_embeddings.weight"],
+          "token_type_embeddings": g["embeddings.token_type_embeddings.weight"],
+          "embedding_layernorm_weight": g["embeddings.LayerNorm.weight"],
+          "embedding_layernorm_bias": g["embeddings.LayerNorm.bias"]}
+    hf = ["attention.self.query.weight", "attention.self.query.bias", "attention.self.key.weight",
+          "attention.self.key.bias", "attention.self.value.weight", "attention.self.value.bias",
+          "attention.output.dense.weight", "attention.output.dense.bias",
+          "attention.output.LayerNorm.weight", "attention.output.LayerNorm.bias",
+          "intermediate.dense.weight", "intermediate.dense.bias", "output.dense.weight",
+          "output.dense.bias", "output.LayerNorm.weight", "output.LayerNorm.bias"]
+    for l in range(2):
+        for role, name in zip(BERT_LAYER_ROLES, hf):
+            gt[f"encoder_layer_{l}_{role}"] = g[f"encoder.layer.{l}.{name}"]
+    return gt

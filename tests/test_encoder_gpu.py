@@ -248,6 +248,39 @@ def test_encoder_cls_pooling(rt):
     enc.release()
 
 
+@pytest.mark.parametrize("hidden,heads,inter,pooling", [(16, 4, 32, "masked_mean"),
+                                                          (64, 2, 100, "cls"),
+                                                          (200, 5, 300, "masked_mean"),
+                                                          (128, 16, 256, "cls")])
+def test_encoder_general_shapes(rt, hidden, heads, inter, pooling):
+    """Shapes outside the MFMA kernels (hidden 16 / 64 / 200, head dims 4,
+    32 at hidden 64, 40 and 8) run the general-shape kernels: within f32
+    rounding of the oracle on the same dequantized weights, for both
+    poolings; ragged lengths, position 0 masked, a mask hole, a sequence
+    with no active position, token types."""
+    _case(f"encoder general shape H={hidden} heads={heads} F={inter} {pooling}")
+    w = datagen.bert_q8_weights(2, hidden, heads, inter, 500, 64, seed=hidden + heads,
+                                random_affine=True)
+    ids, mask, _ = datagen.encoder_batch(6, 64, 500, 1, 64, hidden + 7, hidden + 8)
+    mask[1, 0] = 0
+    mask[2, :] = 0
+    mask[3, 5:9] = 0
+    types = (np.arange(64)[None, :] % 2 * mask).astype(np.int32)
+    enc = Encoder(rt, w)
+    if pooling == "cls":
+        enc.set_pooling("cls")
+    got = enc.embed(ids, mask, types)
+    want = oracle.bert_embed(w.tok, w.pos, w.typ, w.emb_gamma, w.emb_beta,
+                             [L.dequantized() for L in w.layers], ids, mask, types, w.heads,
+                             w.ln_eps, pooling=pooling)
+    err = float(np.max(np.abs(got - want)))
+    print(f"  max abs {err:.3e}", flush=True)
+    assert err <= 1e-5
+    if pooling == "masked_mean":
+        assert np.all(got[2] == 0)
+    enc.release()
+
+
 def test_encoder_rejects_out_of_range_ids_at_masked_positions(rt):
     """The reference range-checks every input id, masked positions included
     (BERTEmbeddingsReference, tensor_ops.go:1476-1489)."""

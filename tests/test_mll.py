@@ -368,7 +368,6 @@ def test_bert_embedder_refusals():
         (attrs(epsilon="abc"), "epsilon \"abc\" is invalid"),
         (attrs(num_hidden_layers="3"), "expects 56 tensors for 3 layers, got 40"),
         (attrs(num_attention_heads="3"), "not a multiple of num_attention_heads"),
-        (attrs(num_attention_heads="16"), "head dim 8"),
         (mll_synth.mutate(attrs(), lambda a: a["steps"].insert(
             1, {"entry": "bert_embed", "kind": "normalize", "name": "n", "inputs": ["embeddings"],
                 "outputs": ["e2"]})), "beside a bert_embedder step"),
@@ -389,28 +388,24 @@ def test_bert_embedder_refusals():
     with MllPackage(mll_synth.bert_package(mll_synth.bert_artifact(2, 4), bad)) as m:
         with pytest.raises(EosHipError, match="missing"):
             m.classify()
-    # The golden fixture's model (hidden 16, 4 heads) is outside the fused
-    # encoder's shapes: refused, so a caller keeps its host executor for it.
-    from safetensors.numpy import load_file
-    g = load_file(os.path.join(os.path.dirname(__file__), "golden", "bert_tiny",
-                               "model.safetensors"))
-    gt = {"token_embeddings": g["embeddings.word_embeddings.weight"],
-          "position_embeddings": g["embeddings.position_embeddings.weight"],
-          "token_type_embeddings": g["embeddings.token_type_embeddings.weight"],
-          "embedding_layernorm_weight": g["embeddings.LayerNorm.weight"],
-          "embedding_layernorm_bias": g["embeddings.LayerNorm.bias"]}
-    hf = ["attention.self.query.weight", "attention.self.query.bias", "attention.self.key.weight",
-          "attention.self.key.bias", "attention.self.value.weight", "attention.self.value.bias",
-          "attention.output.dense.weight", "attention.output.dense.bias",
-          "attention.output.LayerNorm.weight", "attention.output.LayerNorm.bias",
-          "intermediate.dense.weight", "intermediate.dense.bias", "output.dense.weight",
-          "output.dense.bias", "output.LayerNorm.weight", "output.LayerNorm.bias"]
-    for l in range(2):
-        for role, name in zip(mll_synth.BERT_LAYER_ROLES, hf):
-            gt[f"encoder_layer_{l}_{role}"] = g[f"encoder.layer.{l}.{name}"]
-    with MllPackage(mll_synth.bert_package(mll_synth.bert_artifact(2, 4), gt)) as m:
-        with pytest.raises(EosHipError, match="hidden 16, head dim 4, intermediate 32 outside"):
+    # Head dim 8 (hidden 128, 16 heads) is outside the MFMA attention kernels
+    # and inside the general-shape path: it classifies.
+    with MllPackage(mll_synth.bert_package(attrs(num_attention_heads="16"), t)) as m:
+        p = m.classify()
+    assert p["route"] == "bert_embedder" and (p["model_dim"], p["heads"]) == (128, 16)
+    # A head dim above 64 at a hidden width the MFMA kernels do not take is
+    # outside both.
+    w72, t72 = _bert(heads=1, hidden=72, inter=96)
+    with MllPackage(mll_synth.bert_package(mll_synth.bert_artifact(2, 1), t72)) as m:
+        with pytest.raises(EosHipError, match="hidden 72, head dim 72, intermediate 96 outside"):
             m.classify()
+    # The golden fixture's model (hidden 16, 4 heads, intermediate 32)
+    # classifies for the general-shape path.
+    with MllPackage(mll_synth.bert_package(mll_synth.bert_artifact(2, 4),
+                                           mll_synth.golden_bert_tensors())) as m:
+        p = m.classify()
+    assert p["route"] == "bert_embedder"
+    assert (p["model_dim"], p["heads"], p["hidden_dim"], p["vocab"]) == (16, 4, 32, 17)
 
 
 def test_long_names_are_refused():

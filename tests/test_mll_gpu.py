@@ -196,6 +196,43 @@ def test_bert_embedder_package(rt, pooling, storage):
     pkg.close()
 
 
+@pytest.mark.parametrize("pooling", ["masked_mean", "cls"])
+def test_bert_embedder_golden_fixture(rt, pooling):
+    """The reference's own BERT golden fixture (hidden 16, 4 heads of dim 4,
+    intermediate 32: runtime/testdata/pretrained_bert_golden/) as a
+    bert_embedder package, bound through eoship_encoder_bind_mll (f32 dense
+    weights quantized per output channel at bind) and run by the
+    general-shape kernels: equal to oracle.bert_embed on the weights the GPU
+    computes with to f32 rounding, and within the contract of golden.json's
+    embeddings (masked mean pooling, the fixture's own)."""
+    import json
+    import oracle
+    _case(f"bert golden fixture on the GPU, {pooling}")
+    g = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "bert_tiny",
+                                    "golden.json")))
+    t = mll_synth.golden_bert_tensors()
+    pkg = MllPackage(mll_synth.bert_package(mll_synth.bert_artifact(2, 4, pooling=pooling), t))
+    enc = MllEncoder(rt, pkg)
+    assert enc.plan["route"] == "bert_embedder" and enc.plan["model_dim"] == 16
+    n, T = len(g["texts"]), g["max_length"]
+    ids = np.array(g["input_ids"], np.int32).reshape(n, T)
+    mask = np.array(g["attention_mask"], np.int32).reshape(n, T)
+    types = np.array(g["token_type_ids"], np.int32).reshape(n, T)
+    got = enc.embed(ids, mask, types)
+    layers = _bert_oracle_layers(pkg, 2, requantize=True)
+    want = oracle.bert_embed(t["token_embeddings"], t["position_embeddings"],
+                             t["token_type_embeddings"], t["embedding_layernorm_weight"],
+                             t["embedding_layernorm_bias"], layers, ids, mask, types, 4, 1e-12,
+                             pooling=pooling)
+    err = float(np.max(np.abs(got - want)))
+    print(f"  vs oracle on the bound weights: max abs {err:.3e}", flush=True)
+    assert err <= 1e-5
+    if pooling == "masked_mean":
+        _check(got, np.array(g["embeddings"], np.float32))
+    enc.release()
+    pkg.close()
+
+
 def test_bert_embedder_package_refuses_attend_padding(rt):
     _case("bert_embedder package attend_padding refusal")
     from eos_amd import datagen
