@@ -24,6 +24,14 @@
 #include "eoship_internal.h"
 #include "kernels/tq_args.h"
 
+namespace {
+// The finalize variant for k: up to 1024 the one with the small selection
+// buffer (it fits beside a running filter scan on a CU), else the full one.
+const char* finalize_kernel(int k) {
+  return k <= 1024 ? "eos_tq_finalize_k1024" : "eos_tq_finalize";
+}
+}  // namespace
+
 using eoship::hip_err;
 using eoship::set_err;
 
@@ -301,7 +309,8 @@ struct EosHipTQ {
       const unsigned jblocks = (unsigned)((d + 31) / 32);
       if (rt->launch("eos_tq_rotate", dim3(jblocks, cblocks), dim3(256), 0, &p, err) != 0) return 1;
     }
-    return rt->launch("eos_tq_quantize", dim3(cblocks), dim3(256), 0, &p, err);
+    return rt->launch(d <= 384 ? "eos_tq_quantize_m12" : "eos_tq_quantize", dim3(cblocks), dim3(256),
+                      0, &p, err, "eos_tq_quantize");
   }
 
   int prepare(const float* d_queries, int qb, int16_t* qs_out, char** err) {
@@ -487,7 +496,8 @@ struct EosHipTQ {
     f.kk = kk;
     f.q = qb;
     f.id_map = id_map;
-    if (rt->launch("eos_tq_finalize", dim3(qb), dim3(256), 0, &f, err) != 0) return 1;
+    if (rt->launch(finalize_kernel(f.kk), dim3(qb), dim3(256), 0, &f, err, "eos_tq_finalize") != 0)
+      return 1;
     if (gated) return fallback_batch(d_queries, qb, kk, d_ids, d_scores, d_status, false, err);
     return 0;
   }
@@ -1123,7 +1133,7 @@ int rank_rows(EosHipRuntime* rt, EosHipTQ* tq, const float* d_rows, int rows, in
   f.cap = nch * kk;
   f.kk = kk;
   f.q = rows;
-  return rt->launch("eos_tq_finalize", dim3(rows), dim3(256), 0, &f, err, "tq_maxsim_select_merge");
+  return rt->launch(finalize_kernel(f.kk), dim3(rows), dim3(256), 0, &f, err, "tq_maxsim_select_merge");
 }
 
 // Bound-filtered MaxSim top-k of one prepared chunk of cq queries (kk <=
@@ -1226,7 +1236,7 @@ int maxsim_filtered(EosHipRuntime* rt, EosHipTQ* tq, int doc_len, int64_t ndocs,
   f.cap = kMsCap;
   f.kk = kk;
   f.q = cq;
-  if (rt->launch("eos_tq_finalize", dim3((unsigned)cq), dim3(256), 0, &f, err, "tq_maxsim_finalize") != 0)
+  if (rt->launch(finalize_kernel(f.kk), dim3((unsigned)cq), dim3(256), 0, &f, err, "tq_maxsim_finalize") != 0)
     return 1;
   // 4. exhaustive rows of the flagged queries (both launches return at once
   // when none is flagged)
@@ -2219,7 +2229,7 @@ struct EosHipTQIP {
     f.cap = kCap;
     f.kk = kk;
     f.q = qb;
-    if (rt->launch("eos_tq_finalize", dim3(qb), dim3(256), 0, &f, err, "tq_ip_finalize") != 0)
+    if (rt->launch(finalize_kernel(f.kk), dim3(qb), dim3(256), 0, &f, err, "tq_ip_finalize") != 0)
       return 1;
     // Exact fallback, gated on the device by the finalize flags.
     const size_t need = (size_t)qb * (size_t)n * sizeof(float);

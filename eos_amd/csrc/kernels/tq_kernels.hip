@@ -121,9 +121,9 @@ EOS_DEV int prep_source(const TqPrepArgs& a, int c) {
 // max |q'|, Qs = rint(q' qmax / max|q'|) clamped, hi/lo int8 fragments,
 // alpha; resets the column's threshold and candidate count. Called by the 32
 // lanes of one half-wave (t = lane & 31), values fetched by get(j).
-template <typename Get>
+template <int M, typename Get>
 EOS_DEV void prep_quantize_column(const TqPrepArgs& a, int c, int t, Get get) {
-  constexpr int M = kMaxDim / 32;  // values per lane
+  // M values per lane: dimensions up to 32 M.
   const int src = prep_source(a, c);
   // All of the lane's values are fetched before any is used, so the loads
   // overlap instead of costing one round trip each.
@@ -181,7 +181,7 @@ EOS_DEV void prep_quantize_column(const TqPrepArgs& a, int c, int t, Get get) {
 
 constexpr int kPrepJ = 32;     // rotated coordinates per workgroup
 constexpr int kPrepC = 8;      // query columns per workgroup
-constexpr int kPrepK = 512;    // rotation rows staged in LDS per chunk
+constexpr int kPrepK = 128;    // rotation rows staged in LDS per chunk
 
 }  // namespace
 
@@ -204,29 +204,35 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_rotate(TqPrepArgs a) {
     // Loads from clamped positions, then the validity test (a load under a
     // per-lane condition would be a branch of its own, waiting for its data
     // before the next load). With no query rows nothing is loaded.
-    constexpr int R = kMaxDim / 256;
-    float qv[kPrepC][R];
-    if (a.q > 0) {
+    // Two rows of 256 values per column at a time (d <= 512: one pass), so
+    // that the staging registers stay few (the kernel then fits beside a
+    // running filter scan on a CU).
+    constexpr int R = 2;
+    for (int r0 = 0; r0 < a.d; r0 += 256 * R) {  // uniform
+      float qv[kPrepC][R];
+      if (a.q > 0) {
 #pragma unroll
-      for (int cc = 0; cc < kPrepC; ++cc) {
-        const int src = prep_source(a, c0 + cc);
-        const float* qrow = a.queries + (size_t)(src >= 0 ? src : 0) * a.d;
+        for (int cc = 0; cc < kPrepC; ++cc) {
+          const int src = prep_source(a, c0 + cc);
+          const float* qrow = a.queries + (size_t)(src >= 0 ? src : 0) * a.d;
 #pragma unroll
-        for (int r = 0; r < R; ++r) qv[cc][r] = qrow[min(tid + 256 * r, a.d - 1)];
+          for (int r = 0; r < R; ++r) qv[cc][r] = qrow[min(r0 + tid + 256 * r, a.d - 1)];
 #pragma unroll
-        for (int r = 0; r < R; ++r) qv[cc][r] = (src >= 0 && tid + 256 * r < a.d) ? qv[cc][r] : 0.0f;
+          for (int r = 0; r < R; ++r)
+            qv[cc][r] = (src >= 0 && r0 + tid + 256 * r < a.d) ? qv[cc][r] : 0.0f;
+        }
+      } else {
+#pragma unroll
+        for (int cc = 0; cc < kPrepC; ++cc)
+#pragma unroll
+          for (int r = 0; r < R; ++r) qv[cc][r] = 0.0f;
       }
-    } else {
 #pragma unroll
       for (int cc = 0; cc < kPrepC; ++cc)
 #pragma unroll
-        for (int r = 0; r < R; ++r) qv[cc][r] = 0.0f;
+        for (int r = 0; r < R; ++r)
+          if (r0 + tid + 256 * r < a.d) qsh[cc * kMaxDim + r0 + tid + 256 * r] = qv[cc][r];
     }
-#pragma unroll
-    for (int cc = 0; cc < kPrepC; ++cc)
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (tid + 256 * r < a.d) qsh[cc * kMaxDim + tid + 256 * r] = qv[cc][r];
   }
   const int j = j0 + jj;
   double acc = 0.0;
@@ -255,18 +261,32 @@ extern "C" __global__ __launch_bounds__(256) void eos_tq_rotate(TqPrepArgs a) {
 
 // Quantization of the query block, one half-wave per column: from the
 // rotated columns eos_tq_rotate wrote, or from the raw queries when the
-// corpus has no rotation.
-extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) {
+// corpus has no rotation. M values per lane (d <= 32 M): the _m12 variant
+// for d <= 384 holds 12 (it then fits beside a running filter scan on a CU).
+namespace {
+
+template <int M>
+EOS_DEV void quantize_body(const TqPrepArgs& a) {
   const int c = blockIdx.x * kPrepC + (threadIdx.x >> 5);
   if (a.rot_t != nullptr) {
-    prep_quantize_column(a, c, threadIdx.x & 31,
-                         [&](int, int jx) { return a.qrot[(size_t)c * a.d + jx]; });
+    prep_quantize_column<M>(a, c, threadIdx.x & 31,
+                            [&](int, int jx) { return a.qrot[(size_t)c * a.d + jx]; });
   } else if (a.q > 0) {
-    prep_quantize_column(a, c, threadIdx.x & 31,
-                         [&](int src, int jx) { return (double)a.queries[(size_t)src * a.d + jx]; });
+    prep_quantize_column<M>(a, c, threadIdx.x & 31, [&](int src, int jx) {
+      return (double)a.queries[(size_t)src * a.d + jx];
+    });
   } else {
-    prep_quantize_column(a, c, threadIdx.x & 31, [&](int, int) { return 0.0; });
+    prep_quantize_column<M>(a, c, threadIdx.x & 31, [&](int, int) { return 0.0; });
   }
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize(TqPrepArgs a) {
+  quantize_body<kMaxDim / 32>(a);
+}
+extern "C" __global__ __launch_bounds__(256) void eos_tq_quantize_m12(TqPrepArgs a) {
+  quantize_body<12>(a);
 }
 
 // --------------------------------------------------------------------- pack
@@ -2084,9 +2104,15 @@ extern "C" __global__ __launch_bounds__(kThrThreads) void eos_tq_threshold(TqSel
 // rank counting (or a bitonic sort when kk is large). A query whose kept set
 // is smaller than kk or overflowed is flagged (status 1 / 2) for the
 // exhaustive path; status 0 means its output row is final.
-extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFinalizeArgs a) {
+namespace {
+
+// SEL: capacity of the selected set (kSortCap, or kRankSortMax for k <= 1024:
+// 76 KB of LDS instead of 140, so that it runs beside a filter scan on the
+// same CU when batches are in flight on several streams).
+template <int SEL>
+EOS_DEV void finalize_body(const TqFinalizeArgs& a) {
   __shared__ u64 cbuf[kSortCap];
-  __shared__ u64 sel[kSortCap];
+  __shared__ u64 sel[SEL];
   __shared__ uint32_t hist[kFinThreads / 64 * 256];
   __shared__ uint32_t scr[16];
   __shared__ uint32_t sel_n;
@@ -2175,6 +2201,15 @@ extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFina
     }
   }
   if (tid == 0) a.status[row] = 0;
+}
+
+}  // namespace
+
+extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize(TqFinalizeArgs a) {
+  finalize_body<kSortCap>(a);
+}
+extern "C" __global__ __launch_bounds__(kFinThreads) void eos_tq_finalize_k1024(TqFinalizeArgs a) {
+  finalize_body<kRankSortMax>(a);
 }
 
 // ------------------------------------------------------------------ maxsim
