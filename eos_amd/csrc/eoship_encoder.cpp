@@ -435,7 +435,14 @@ struct EosHipEncoder {
       const double log2e = 1.4426950408889634;
       EncAttnArgs at{qkv, vt, ctx, seq_off, seq_cnt, seq_q, batch, nh, H, tokens, vt_ld,
                      (float)(scaled_scores ? log2e / std::sqrt((double)hd) : log2e), status + 1};
-      if (rt->launch(attn_name, dim3((tokens + 127) / 128, nh, batch), dim3(256), 0, &at, err) != 0)
+      // Head dim 64 over sequences longer than 512: 12-wavefront workgroups
+      // (384 queries each); else 4 (128 queries), which waste fewer
+      // wavefronts on short sequences.
+      const bool wide = hd == 64 && tokens > 512;
+      const int qpw = wide ? 384 : 128;
+      if (rt->launch(wide ? "eos_enc_attn_hd64_w12" : attn_name,
+                     dim3((tokens + qpw - 1) / qpw, nh, batch), dim3(wide ? 768 : 256), 0, &at,
+                     err) != 0)
         return 1;
       if (tail_name != nullptr) {
         EncTailArgs tl{ctx,    h,      mid,    h8,     hs,     L.w_of, L.s_o,    L.b_o,     L.g1,

@@ -1469,25 +1469,26 @@ EOS_TAIL_KERNEL(1, 768, 2)
 // and accumulates O^T += V^T P^T on MFMA. P^T is fed straight from the S^T
 // registers: the K order of that MFMA is the row order the S^T accumulator
 // already has, and the V^T fragment is gathered in the same order.
-template <int HD, int KB, bool FOLD = false>
+template <int HD, int KB, bool FOLD = false, int NW = 4>
 EOS_DEV void attn_body(const EncAttnArgs& a) {
   static_assert(KB == 32 || KB == 64, "keys per block");
   constexpr int KC = KB / 8;             // 8-key chunks of a V^T row per block
   constexpr int NT = KB / 32;            // 32-key S^T tiles per block
   constexpr int QW = 32;                 // queries per wavefront
   constexpr int NCH = KB * HD / 8;       // 8-half chunks of K (and of V^T) per block
-  constexpr int CPT = (NCH + 255) / 256; // chunks per thread
+  constexpr int NTHR = 64 * NW;          // threads (NW wavefronts of 32 queries)
+  constexpr int CPT = (NCH + NTHR - 1) / NTHR; // chunks per thread
   __shared__ __attribute__((aligned(16))) uint16_t ks[2][KB * (HD + 8)];
   __shared__ __attribute__((aligned(16))) uint16_t vt[2][HD * (KB + 8)];
   // Per-wavefront output staging (head dims up to 64): the K buffers when
   // they are large enough (free once the key loop is done), else its own.
-  constexpr bool kStageInK = 2 * KB * (HD + 8) >= 4 * 32 * (HD + 8);
+  constexpr bool kStageInK = 2 * KB * (HD + 8) >= NW * 32 * (HD + 8);
   __shared__ __attribute__((aligned(16)))
-  uint16_t ostage[(HD <= 64 && !kStageInK) ? 4 * 32 * (HD + 8) : 8];
+  uint16_t ostage[(HD <= 64 && !kStageInK) ? NW * 32 * (HD + 8) : 8];
   const int b = blockIdx.z, h = blockIdx.y;
   const int cnt = a.seq_cnt[b];                          // keys
   const int qcnt = a.seq_q != nullptr ? a.seq_q[b] : cnt;  // query rows (>= cnt)
-  const int q0 = blockIdx.x * (4 * QW);
+  const int q0 = blockIdx.x * (NW * QW);
   if (q0 >= qcnt) return;
   const int off = a.seq_off[b];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1531,7 +1532,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   auto kv_load = [&](int k0) {
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
-      const int idx = tid + 256 * u;
+      const int idx = tid + NTHR * u;
       if (idx < NCH) {
         const int kr = idx / (HD / 8), c = (idx % (HD / 8)) * 8;
         // Clamped to the sequence's rows (row 0 when it has no key: then the
@@ -1547,7 +1548,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   auto kv_store = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
-      const int idx = tid + 256 * u;
+      const int idx = tid + NTHR * u;
       if (idx < NCH) {
         const int kr = idx / (HD / 8), c = (idx % (HD / 8)) * 8;
         *reinterpret_cast<v4i*>(&ks[buf][kr * (HD + 8) + c]) = kreg[u];
@@ -1761,6 +1762,15 @@ void eos_enc_attn_hd32(EncAttnArgs a) {
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void eos_enc_attn_hd64(EncAttnArgs a) {
   attn_body<64, 64, true>(a);
+}
+// Head dim 64 over long sequences: twelve wavefronts (384 queries) per
+// workgroup, one workgroup per CU, so each K/V block is staged once per CU
+// for 384 queries instead of once per 128 (three 4-wavefront workgroups):
+// the loads and the wait for them were 60 % of a block's time (per-wavefront
+// phase timestamps), bound by the L1 misses a CU keeps in flight.
+extern "C" __global__ __launch_bounds__(768) __attribute__((amdgpu_waves_per_eu(3)))
+void eos_enc_attn_hd64_w12(EncAttnArgs a) {
+  attn_body<64, 64, true, 12>(a);
 }
 extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 void eos_enc_attn_hd128(EncAttnArgs a) {

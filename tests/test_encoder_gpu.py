@@ -281,6 +281,34 @@ def test_encoder_general_shapes(rt, hidden, heads, inter, pooling):
     enc.release()
 
 
+@pytest.mark.parametrize("pooling", ["masked_mean", "cls"])
+def test_attention_wide_workgroups(rt, pooling):
+    """Head dim 64 over inputs longer than 512 tokens runs 12-wavefront
+    attention workgroups (384 queries each): ragged lengths on both sides of
+    the 384-query boundaries, one and zero active tokens, position 0 masked
+    (the CLS row then follows the active rows), a mask hole; against the
+    oracle on each sequence's valid tokens."""
+    _case(f"wide attention workgroups {pooling}")
+    w = datagen.bert_q8_weights(2, 512, 8, 2048, 1000, 1100, seed=71, random_affine=True)
+    lengths = [1100, 1, 0, 385, 384, 383, 767, 769]
+    rng = np.random.default_rng(72)
+    ids = rng.integers(1, 1000, (len(lengths), 1100)).astype(np.int32)
+    mask = np.zeros_like(ids)
+    for b, n in enumerate(lengths):
+        mask[b, :n] = 1
+    mask[3, 0] = 0
+    mask[6, 100:140] = 0
+    enc = Encoder(rt, w)
+    if pooling == "cls":
+        enc.set_pooling("cls")
+    got = enc.embed(ids, mask)
+    want = oracle.bert_embed(w.tok, w.pos, w.typ, w.emb_gamma, w.emb_beta,
+                             [L.dequantized() for L in w.layers], ids, mask, None, w.heads,
+                             w.ln_eps, pooling=pooling)
+    _check(got, want)
+    enc.release()
+
+
 def test_encoder_rejects_out_of_range_ids_at_masked_positions(rt):
     """The reference range-checks every input id, masked positions included
     (BERTEmbeddingsReference, tensor_ops.go:1476-1489)."""
