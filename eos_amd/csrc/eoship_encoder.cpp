@@ -113,6 +113,7 @@ struct EosHipEncoder {
   int vt_ld = 0;
   int32_t *row_b = nullptr, *row_t = nullptr, *seq_off = nullptr, *seq_cnt = nullptr;
   int32_t* seq_q = nullptr;  // query rows per sequence (CLS pooling may add one)
+  int32_t* seq_order = nullptr;  // sequences by key count, longest first
   int32_t *total = nullptr, *status = nullptr;
   // host-API staging
   void* io = nullptr;
@@ -123,7 +124,7 @@ struct EosHipEncoder {
       if (p) hipFree(p);
     void* act[] = {h,     qkv,     ctx,     mid,   h8,    hs,   pool_part, vt, row_b,
                    row_t, seq_off, seq_cnt, seq_q, total, status, io,   hf,        h1f, qkvf,
-                   ctxf,  midf};
+                   ctxf,  midf,    seq_order};
     for (void* p : act)
       if (p) hipFree(p);
   }
@@ -201,10 +202,12 @@ struct EosHipEncoder {
     const size_t rows = row_capacity(batch, tokens);
     if (rows <= cap_rows && batch <= cap_batch) return 0;
     void* act[] = {h,     qkv,   ctx,     mid,     h8,    hs,     pool_part, vt,  row_b, row_t,
-                   seq_off, seq_cnt, seq_q, total, status, hf,  h1f,       qkvf, ctxf, midf};
+                   seq_off, seq_cnt, seq_q, total, status, hf,  h1f,       qkvf, ctxf, midf,
+                   seq_order};
     for (void* p : act)
       if (p) hipFree(p);
     hf = h1f = qkvf = ctxf = midf = nullptr;
+    seq_order = nullptr;
     h = qkv = ctx = mid = nullptr;
     h8 = nullptr;
     hs = nullptr;
@@ -229,6 +232,7 @@ struct EosHipEncoder {
         rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_off), err) ||
         rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_cnt), err) ||
         rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_q), err) ||
+        rt->alloc((size_t)batch * 4, reinterpret_cast<void**>(&seq_order), err) ||
         rt->alloc(4, reinterpret_cast<void**>(&total), err) ||
         rt->alloc(8, reinterpret_cast<void**>(&status), err))
       return 1;
@@ -362,6 +366,7 @@ struct EosHipEncoder {
     pk.vocab = desc.vocab;
     pk.ntype = desc.type_vocab;
     pk.status = status;
+    pk.order = seq_order;
     if (rt->launch("eos_enc_count", dim3(batch), dim3(256), 0, &pk, err) != 0 ||
         rt->launch("eos_enc_pack", dim3(batch), dim3(256), 0, &pk, err) != 0)
       return 1;
@@ -434,7 +439,8 @@ struct EosHipEncoder {
         return 1;
       const double log2e = 1.4426950408889634;
       EncAttnArgs at{qkv, vt, ctx, seq_off, seq_cnt, seq_q, batch, nh, H, tokens, vt_ld,
-                     (float)(scaled_scores ? log2e / std::sqrt((double)hd) : log2e), status + 1};
+                     (float)(scaled_scores ? log2e / std::sqrt((double)hd) : log2e), status + 1,
+                     seq_order};
       // Head dim 64 over sequences longer than 512: 12-wavefront workgroups
       // (384 queries each); else 4 (128 queries), which waste fewer
       // wavefronts on short sequences.

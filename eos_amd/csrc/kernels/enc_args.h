@@ -30,6 +30,10 @@ struct EncPackArgs {
   const int32_t* type_ids;  // or NULL (all 0)
   int vocab, ntype;
   int32_t* status;
+  // Optional [batch]: the sequences ordered by key count, longest first (ties
+  // by index), written by eos_enc_pack; attention dispatches its workgroups
+  // in this order, so that the longest ones start first.
+  int32_t* order;
 };
 
 // mode 0 (BERT): token + position + type, then affine LayerNorm.
@@ -144,6 +148,8 @@ struct EncAttnArgs {
   // Optional: counts (per wavefront) the exponent-reference moves after a
   // sequence's first key block, the lazy-rescale path trained models reach.
   int32_t* moves;
+  // Optional [batch]: workgroup z serves sequence order[z] (else z).
+  const int32_t* order;
 };
 
 // General-shape BERT path (hidden widths and head dims the MFMA kernels do

@@ -331,6 +331,21 @@ extern "C" __global__ __launch_bounds__(256) void eos_enc_pack(EncPackArgs a) {
     a.seq_off[b] = seq_base;
     if (b == a.batch - 1) *a.total = seq_base + padded;
   }
+  if (a.order != nullptr) {
+    // Rank of this sequence by key count, longest first, ties by index: an
+    // attention workgroup's time grows with its keys, so the long
+    // sequences' workgroups are dispatched first and the short ones fill
+    // the end.
+    const int mc = a.seq_cnt[b];
+    int ahead = 0;
+    for (int i = tid; i < a.batch; i += 256) {
+      const int c = a.seq_cnt[i];
+      ahead += (c > mc || (c == mc && i < b)) ? 1 : 0;
+    }
+    int rank = 0;
+    (void)block_exclusive_scan256(ahead, scr, &rank);
+    if (tid == 0) a.order[rank] = b;
+  }
 }
 
 // -------------------------------------------------------------- embedding
@@ -1485,7 +1500,7 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
   constexpr bool kStageInK = 2 * KB * (HD + 8) >= NW * 32 * (HD + 8);
   __shared__ __attribute__((aligned(16)))
   uint16_t ostage[(HD <= 64 && !kStageInK) ? NW * 32 * (HD + 8) : 8];
-  const int b = blockIdx.z, h = blockIdx.y;
+  const int b = a.order != nullptr ? a.order[blockIdx.z] : blockIdx.z, h = blockIdx.y;
   const int cnt = a.seq_cnt[b];                          // keys
   const int qcnt = a.seq_q != nullptr ? a.seq_q[b] : cnt;  // query rows (>= cnt)
   const int q0 = blockIdx.x * (NW * QW);
