@@ -1636,8 +1636,21 @@ EOS_DEV void attn_body(const EncAttnArgs& a) {
         for (int e = 0; e < 16; ++e) {
           // v_exp_f32 directly: masked keys give exp2(-inf) = 0.
           const float p = __builtin_amdgcn_exp2f(FOLD ? s[hh][e] : s[hh][e] - shift);
-          psum += p;
           pf[2 * hh + (e >> 3)][e & 7] = (_Float16)p;
+        }
+      // The row sum is taken over the f16 p the PV MFMAs multiply, two per
+      // v_dot2_f32_f16 against (1, 1) with f32 accumulation: half the
+      // instructions of adding the f32 p, and the weights of o / lrun sum to
+      // one exactly as rounded. A p past the f16 range gives inf (NaN stays
+      // NaN), which fails the kSafe test below like the f32 sum would.
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+      for (int j = 0; j < 2 * NT; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+          const h2 pp = {pf[j][e], pf[j][e + 1]};
+          psum = __builtin_amdgcn_fdot2(pp, ones, psum, false);
         }
     };
     exps(mrun);
