@@ -35,6 +35,17 @@ DEVICE_SOURCES = [
     ("enc", os.path.join(CSRC, "kernels", "enc_kernels.hip")),
     ("ret", os.path.join(CSRC, "kernels", "ret_kernels.hip")),
 ]
+# Extra flags per code object. The encoder kernels are built without the
+# mixed-precision FMA instructions (v_fma_mix*): the compiler folds some
+# `(half)fmaf(a, b, c)` into one of them, which rounds the exact result to
+# f16 once, and leaves others as an f32 FMA and a conversion, which round
+# twice; which epilogue element gets which form depends on its position in
+# the unrolled tile, so a row's values would depend on where the row lies in
+# the batch. Without them every element is an f32 FMA rounded to f32, then
+# to f16.
+DEVICE_FLAGS = {
+    "enc": ["-Xclang", "-target-feature", "-Xclang", "-fma-mix-insts"],
+}
 # Measurement code object for bench.py (MFMA rate and shader clock against
 # operand data), built beside the library and not linked into it.
 PROBE_SOURCE = os.path.join(CSRC, "kernels", "probe_kernels.hip")
@@ -78,8 +89,8 @@ def build(verbose: bool = False) -> str:
     blobs = []
     for stem, src in DEVICE_SOURCES:
         out = os.path.join(BUILD_DIR, f"{stem}.hsaco")
-        _run([hipcc, *HIPCC_FLAGS, "--genco", "-I", os.path.join(CSRC, "kernels"), "-o", out, src],
-             verbose)
+        _run([hipcc, *HIPCC_FLAGS, *DEVICE_FLAGS.get(stem, []), "--genco", "-I",
+              os.path.join(CSRC, "kernels"), "-o", out, src], verbose)
         blobs.append((stem, out))
     _run([hipcc, *HIPCC_FLAGS, "--genco", "-o", PROBE_PATH, PROBE_SOURCE], verbose)
     asm = [".section .note.GNU-stack,\"\",@progbits"]

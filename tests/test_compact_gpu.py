@@ -90,6 +90,36 @@ def test_stale_memory_does_not_leak_into_embeddings(rt):
     enc.release()
 
 
+def test_compact_batch_position_invariance(rt):
+    """RoPE positions restart with every sequence (the reference's
+    TestCUDARoPEBatchedRowsAreBatchPositionInvariant,
+    runtime/backends/cuda/cuda_embed_pooled_parity_linux_test.go:140-182):
+    the same sequence in every row embeds the same in each row, a permuted
+    batch gives each sequence the embedding it had, and so does a batch of
+    one, bit for bit."""
+    _case("compact batch-position invariance")
+    w = datagen.compact_q8_weights(2, 128, 1, 256, vocab=3000, max_seq=256, out_dim=64, seed=93)
+    ids, mask, _ = datagen.encoder_batch(6, 160, 3000, 1, 160, 94, 95)
+    mask[1, :] = 1
+    mask[4, 3:7] = 0
+    roles = datagen.uniform_int(96, ids.size, 0, 3).astype(np.int32).reshape(ids.shape)
+    enc = CompactEncoder(rt, w)
+    base = enc.embed(ids, mask, roles)
+    _check(base, _oracle(w, ids, mask, roles))
+    rep = enc.embed(np.repeat(ids[1:2], 5, axis=0), np.repeat(mask[1:2], 5, axis=0),
+                    np.repeat(roles[1:2], 5, axis=0))
+    perm = np.array([3, 0, 5, 1, 4, 2])
+    got = enc.embed(ids[perm], mask[perm], roles[perm])
+    one = enc.embed(ids[4:5], mask[4:5], roles[4:5])
+    d_rep = float(np.max(np.abs(rep - base[1])))
+    d_perm = float(np.max(np.abs(got - base[perm])))
+    d_one = float(np.max(np.abs(one[0] - base[4])))
+    print(f"  max diff: replicated {d_rep:.3e}  permuted {d_perm:.3e}  alone {d_one:.3e}",
+          flush=True)
+    assert d_rep == 0.0 and d_perm == 0.0 and d_one == 0.0
+    enc.release()
+
+
 def test_compact_q4_weights_and_no_roles(rt):
     _case("compact q4 weights, role ids omitted")
     w = datagen.compact_q8_weights(2, 128, 1, 256, vocab=500, max_seq=64, seed=9, bits=4)

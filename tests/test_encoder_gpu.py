@@ -54,6 +54,48 @@ def test_encoder_matches_oracle(rt, hidden, heads, inter, tokens):
     _check(got, _oracle(w, ids, mask, types))
 
 
+@pytest.mark.parametrize("hidden,heads,inter,tokens,pooling", [(384, 12, 1536, 200, "masked_mean"),
+                                                                (512, 8, 2048, 700, "cls"),
+                                                                (16, 4, 32, 40, "masked_mean")])
+def test_encoder_batch_position_invariance(rt, hidden, heads, inter, tokens, pooling):
+    """Positions restart with every sequence and nothing of a sequence's
+    neighbours reaches it (the batch-row invariance the reference checks in
+    runtime/backends/cuda/cuda_embed_pooled_parity_linux_test.go:140-182): the
+    same sequence in every row embeds the same in each row, a permuted batch
+    gives each sequence the embedding it had, and so does a batch of one, bit
+    for bit (a row's arithmetic in every kernel is independent of where the
+    row lies in the packed batch). Covers the MFMA path (hidden 384; hidden 512 over 700 tokens, the
+    12-wavefront attention workgroups, with CLS pooling) and the general-shape
+    kernels (hidden 16)."""
+    _case(f"batch-position invariance H={hidden} T={tokens} {pooling}")
+    w = datagen.bert_q8_weights(2, hidden, heads, inter, 1000, tokens, seed=hidden + 90,
+                                random_affine=True)
+    ids, mask, _ = datagen.encoder_batch(6, tokens, 1000, 1, tokens, hidden + 91, hidden + 92)
+    mask[1, :] = 1
+    mask[4, 3:7] = 0
+    types = (np.arange(tokens)[None, :] % 2 * mask).astype(np.int32)
+    enc = Encoder(rt, w)
+    if pooling == "cls":
+        enc.set_pooling("cls")
+    base = enc.embed(ids, mask, types)
+    want = oracle.bert_embed(w.tok, w.pos, w.typ, w.emb_gamma, w.emb_beta,
+                             [L.dequantized() for L in w.layers], ids, mask, types, w.heads,
+                             w.ln_eps, pooling=pooling)
+    _check(base, want)
+    rep = enc.embed(np.repeat(ids[1:2], 5, axis=0), np.repeat(mask[1:2], 5, axis=0),
+                    np.repeat(types[1:2], 5, axis=0))
+    perm = np.array([3, 0, 5, 1, 4, 2])
+    got = enc.embed(ids[perm], mask[perm], types[perm])
+    one = enc.embed(ids[4:5], mask[4:5], types[4:5])
+    d_rep = float(np.max(np.abs(rep - base[1])))
+    d_perm = float(np.max(np.abs(got - base[perm])))
+    d_one = float(np.max(np.abs(one[0] - base[4])))
+    print(f"  max diff: replicated {d_rep:.3e}  permuted {d_perm:.3e}  alone {d_one:.3e}",
+          flush=True)
+    assert d_rep == 0.0 and d_perm == 0.0 and d_one == 0.0
+    enc.release()
+
+
 def test_encoder_mask_holes_and_empty_sequence(rt):
     _case("encoder mask holes / empty")
     w = datagen.bert_q8_weights(1, 384, 12, 1536, 500, 128, seed=3, random_affine=True)
