@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized embedding-inference hot path on one MI355X.
 
-Workload (the config BASELINE's metric is quoted on):
+Workload (benchmark config c2, the config the headline metric is quoted on):
 TurboQuant flat retrieval scoring -- 1,000,000 vectors x 384 dims, 4-bit codes
 + one f32 norm each (196 B/vector), seeded rotation, 64 unit queries, top-100.
 A step is one full top-k call (prepare, sample threshold, filtered scan,
@@ -11,7 +11,7 @@ Prints one JSON line (the driver's contract), with `roofline` for the
 dominant kernel (the filtered scan, timed per launch with HIP events that its
 own dispatches record, against 8 TB/s and against a copy kernel's measured
 rate) and `cpu_baseline` (the C oracle's reference-loop port on a bounded
-sample, single-threaded and all-core). The other BASELINE configs ride on the
+sample, single-threaded and all-core). The other benchmark configs ride on the
 same line as sub-objects, each with its own roofline and CPU baseline:
 `tiny_c1` (tiny embed, µs per call), `two_stage_c2` (TurboQuant top-200 +
 f16 rerank top-100), `maxsim_c5` (MaxSim over 100k documents of 128 vectors,
@@ -143,7 +143,7 @@ def encoder_cpu_baseline(w, ids, mask, lens, name: str) -> dict:
 
 
 def encoder_leg(rt, steps: int, name: str = "c3", cpu: bool = True) -> dict:
-    """BASELINE config 3 (q8 BERT-style encoder, 6 layers, hidden 384, 12
+    """Benchmark config c3 (q8 BERT-style encoder, 6 layers, hidden 384, 12
     heads, FFN 1536, batch 64 x seq 512, lengths U[32, 512]) or config 4 (long
     context: 4 layers, hidden 512, 8 heads, FFN 2048, batch 4 x 8192, lengths
     U[4096, 8192]); inputs resident on device."""
@@ -273,7 +273,7 @@ def _cpu_model() -> str:
 
 
 def tq_leg(rt, args) -> dict:
-    """BASELINE config 2 (the bench line's workload)."""
+    """Benchmark config c2 (the bench line's workload)."""
     from eos_amd import datagen
     from eos_amd.runtime import DeviceBuffer, Runtime
     from eos_amd.turboquant import TurboQuantIndex
@@ -411,7 +411,7 @@ def tq_leg(rt, args) -> dict:
 
 
 def maxsim_leg(rt, steps: int, cpu: bool = True) -> dict:
-    """100,000 documents x 128 token vectors of dim 128,
+    """Benchmark config c5: 100,000 documents x 128 token vectors of dim 128,
     2-bit codes, lognormal(0, 0.25) norms, seeded rotation; 32 queries x 32
     unit Gaussian tokens; MaxSim top-100 documents per query."""
     from eos_amd import datagen
@@ -696,7 +696,7 @@ def mfma_ceiling(rt, iters: int = 400) -> dict:
 
 
 def tiny_leg(rt, reps: int, cpu: bool = True) -> dict:
-    """BASELINE config 1 (examples/embed.eos): f16 token_embedding [30522, 256]
+    """Benchmark config c1 (examples/embed.eos): f16 token_embedding [30522, 256]
     and projection [256, 128], N(0, 0.02); 128 tokens; gather -> matmul ->
     row L2 normalize -> f16 [128, 128]. Latency-bound: one launch per call."""
     from eos_amd import datagen

@@ -45,7 +45,7 @@ constexpr int kSortCap = 8192;      // largest k the device sort handles
 constexpr int kSampleStride = 16;     // sample every 16th tile (at least)
 constexpr int kMaxSampleTiles = 2048;  // tile maxima per query (the threshold kernel holds 4096)
 // Candidates the sample threshold aims to keep per query, as a multiple of k:
-// on the BASELINE corpus a 1/16 sample at 3 k keeps ~320 for k = 100, with the
+// on the benchmark's c2 corpus a 1/16 sample at 3 k keeps ~320 for k = 100, with the
 // fewest kept over 256 queries still ~1.8 k (fewer than k triggers the exact
 // fallback, which stays correct but costs a dense pass).
 constexpr double kKeepFactor = 3.0;

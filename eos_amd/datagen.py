@@ -1,4 +1,4 @@
-"""Seeded synthetic inputs for the BASELINE configurations.
+"""Seeded synthetic inputs for the benchmark configurations (c1-c5).
 
 Every generator is counter-based (splitmix64 over the element index), so a
 (seed, shape) pair always yields the same array on any machine and in any
@@ -129,7 +129,7 @@ def unpack_codes(packed: np.ndarray, bits: int, d: int) -> np.ndarray:
 
 
 class TurboQuantCorpus:
-    """Synthetic TurboQuant corpus of the BASELINE flat / multivector configs."""
+    """Synthetic TurboQuant corpus of the benchmark's flat / multivector configs."""
 
     def __init__(self, n: int, dim: int, bits: int, seed_codes: int, seed_norms: int,
                  seed_rot: int, norm_sigma: float = 0.25, rotation: bool = True):
@@ -149,7 +149,7 @@ class TurboQuantCorpus:
 
 
 def baseline_flat_corpus(n: int = 1_000_000, dim: int = 384) -> TurboQuantCorpus:
-    """4-bit codes (seed 3), lognormal(0, 0.25) norms (seed 4), rotation seed 5."""
+    """Benchmark config c2: 4-bit codes (seed 3), lognormal(0, 0.25) norms (seed 4), rotation seed 5."""
     return TurboQuantCorpus(n, dim, 4, seed_codes=3, seed_norms=4, seed_rot=5)
 
 

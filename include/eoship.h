@@ -120,7 +120,7 @@ int eoship_timer_elapsed(EosHipRuntime* rt, int slot_begin, int slot_end, double
 
 /* ------------------------------------------------------------- TurboQuant */
 
-/* Build-defined TurboQuant MSE-stage layout (the BASELINE corpus layout):
+/* Build-defined TurboQuant MSE-stage layout (the benchmark's c2 layout):
  * per vector, dim*bits/8 bytes of codes (coordinate j at bit (j*bits)%8 of byte
  * (j*bits)/8, low bits first, as the q4 packer of runtime/mll_export.go:950-958)
  * plus one f32 Norm. Codebook centroid v is codebook_scale * codebook[v]

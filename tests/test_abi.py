@@ -64,7 +64,7 @@ def test_turboquant_vector_bytes():
     assert turboquant_vector_bytes(384, 5) == 248
     for d, b in ((8, 1), (8, 2), (128, 2), (128, 4), (128, 8), (256, 4), (3072, 8)):
         assert turboquant_vector_bytes(d, b) == -(-d * (b - 1) // 8) + -(-d // 8) + 8
-    assert turboquant_mse_vector_bytes(384, 4) == 196     # the BASELINE c2 layout
+    assert turboquant_mse_vector_bytes(384, 4) == 196     # the benchmark's c2 layout
     assert turboquant_mse_vector_bytes(128, 2) == 36      # c5
     assert turboquant_mse_vector_bytes(40, 4) == 24
     with pytest.raises(_lib.EosHipError):

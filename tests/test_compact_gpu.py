@@ -1,6 +1,6 @@
 """GPU parity of the compact (family (a)) embedder against the CPU oracle.
 
-Bar (as for the BERT family): per sequence, cosine >=
+Bar (the benchmark's north star, as for the BERT family): per sequence, cosine >=
 0.9999 and max-abs error <= 2e-2 between the GPU embedding and
 oracle.compact_embed (oracle/encoder_oracle.c, the reference's f32 graph of
 models/default_embedding.go:484-505), both on the same dequantized per-tensor

@@ -1,6 +1,6 @@
 """GPU parity of the q8 encoder (libeoship on gfx950) against the CPU oracle.
 
-Bar: per sequence, cosine >= 0.9999 and max-abs error
+Bar (the benchmark's north star): per sequence, cosine >= 0.9999 and max-abs error
 <= 2e-2 between the GPU embedding and the oracle's, both using the same
 dequantized int8 per-channel weights; the oracle follows the reference's f32/f64
 host path (oracle/encoder_oracle.c)."""
@@ -139,7 +139,7 @@ def test_encoder_rejects_out_of_range_ids(rt):
 
 
 def test_baseline_c3_full_size(rt):
-    """BASELINE config 3 at full size: 6 layers, hidden 384, 12 heads, FFN
+    """Benchmark config c3 at full size: 6 layers, hidden 384, 12 heads, FFN
     1536, batch 64 x 512, lengths U[32, 512]; a quarter of the batch (the
     shortest and longest sequences among them) checked against the oracle
     (sequences are independent), all 64 unit-norm."""
@@ -155,7 +155,7 @@ def test_baseline_c3_full_size(rt):
 
 
 def test_baseline_c4_long_context(rt):
-    """BASELINE config 4 at full size: 4 layers, hidden 512, 8 heads (hd 64),
+    """Benchmark config c4 at full size: 4 layers, hidden 512, 8 heads (hd 64),
     FFN 2048, batch 4 x 8192, lengths U[4096, 8192] (seed 10). The two
     shortest sequences and the longest (the most key blocks, so the most
     chances for the lazy-rescale move) are checked against the oracle on

@@ -4,7 +4,7 @@ CPU: the oracle's MaxSim is pinned to the flat scorer -- with one query token
 it equals the reference child-max (per document, the best child score,
 runtime/retrieval_multivector_turboquant.go:746-783), and the token sum is
 the stated pairwise tree. GPU: document scores and top-k ids are bit-exact
-against the oracle; at BASELINE config 5 size (100k docs x 128 vectors,
+against the oracle; at benchmark config c5 size (100k docs x 128 vectors,
 d = 128, 2-bit, 32 queries x 32 tokens) the device top-k must equal the sort
 of the device's exhaustive document scores, and those equal the oracle's on a
 sampled subset of documents."""

@@ -1,7 +1,7 @@
 """GPU parity of the encoder bound from MLL packages (eoship_encoder_bind_mll)
 against the plan run step by step on the CPU (oracle/plan_oracle.py).
 
-Bar: per sequence, cosine >= 0.9999 and max-abs error
+Bar (the benchmark's north star): per sequence, cosine >= 0.9999 and max-abs error
 <= 2e-2 between the GPU embedding and the oracle's, both from the same
 dequantized q8 weights."""
 import os

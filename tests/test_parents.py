@@ -199,7 +199,7 @@ def test_parent_topk_reference_case_and_validation(rt):
 
 @pytest.mark.gpu
 def test_parent_topk_c5_shape(rt):
-    """BASELINE config 5 corpus (100k parents x 128 children, d = 128, 2-bit)
+    """Benchmark config c5 corpus (100k parents x 128 children, d = 128, 2-bit)
     with one query vector per query: "max" equals the MaxSim child max of the
     same corpus on one token, and the top5-mean rows equal the oracle's for
     two queries."""

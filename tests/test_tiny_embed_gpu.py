@@ -1,4 +1,4 @@
-"""the examples/embed.eos pipeline on the GPU against the
+"""Benchmark config c1: the examples/embed.eos pipeline on the GPU against the
 oracle (f32 matmul in k order, f64 sum of squares, f16 output) and the
 reference known answer (runtime/runtime_test.go:616-686 with the weights of
 :1911-1922). f16 results are compared in f16 units in the last place; the

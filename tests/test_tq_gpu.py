@@ -2,7 +2,7 @@
 
 Bar: prepared queries, integer code dot products, scores and top-k ids are
 bit-exact against oracle/tq_oracle.c on the same seeded inputs; at the
-BASELINE size (1M x 384, 4-bit, 64 queries, k = 100) the filtered top-k must
+benchmark size (1M x 384, 4-bit, 64 queries, k = 100) the filtered top-k must
 equal the exhaustive device scores sorted by (score desc, id asc), and the
 exhaustive scores must equal the oracle's on a sampled subset."""
 import numpy as np
@@ -383,7 +383,7 @@ def _lib_bind_bad_rank(rt, c):
 
 
 def test_baseline_c2_full_size(rt):
-    """BASELINE config 2 at full size: 1M x 384 4-bit, 64 queries, k = 100."""
+    """Benchmark config c2 at full size: 1M x 384 4-bit, 64 queries, k = 100."""
     _case("c2 full size 1M x 384")
     c = datagen.baseline_flat_corpus()
     q = datagen.baseline_queries(64, 384)
