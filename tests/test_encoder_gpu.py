@@ -62,9 +62,10 @@ def test_encoder_batch_position_invariance(rt, hidden, heads, inter, tokens, poo
     neighbours reaches it (the batch-row invariance the reference checks in
     runtime/backends/cuda/cuda_embed_pooled_parity_linux_test.go:140-182): the
     same sequence in every row embeds the same in each row, a permuted batch
-    gives each sequence the embedding it had, and so does a batch of one, bit
-    for bit (a row's arithmetic in every kernel is independent of where the
-    row lies in the packed batch). Covers the MFMA path (hidden 384; hidden 512 over 700 tokens, the
+    gives each sequence the embedding it had, and so do a batch of one and a
+    batch padded to half the width, bit for bit (a row's arithmetic in every
+    kernel is independent of where the row lies in the packed batch and of
+    the batch's width). Covers the MFMA path (hidden 384; hidden 512 over 700 tokens, the
     12-wavefront attention workgroups, with CLS pooling) and the general-shape
     kernels (hidden 16)."""
     _case(f"batch-position invariance H={hidden} T={tokens} {pooling}")
@@ -87,12 +88,20 @@ def test_encoder_batch_position_invariance(rt, hidden, heads, inter, tokens, poo
     perm = np.array([3, 0, 5, 1, 4, 2])
     got = enc.embed(ids[perm], mask[perm], types[perm])
     one = enc.embed(ids[4:5], mask[4:5], types[4:5])
+    # The sequences that fit in half the width, in a batch padded to that
+    # width (at hidden 512 the 700-token batch runs the 12-wavefront
+    # attention workgroups, the 350-token batch the 4-wavefront ones).
+    half = tokens // 2
+    short = np.array([b for b in range(6) if not mask[b, half:].any()])
+    assert short.size > 0
+    nar = enc.embed(ids[short, :half], mask[short, :half], types[short, :half])
     d_rep = float(np.max(np.abs(rep - base[1])))
     d_perm = float(np.max(np.abs(got - base[perm])))
     d_one = float(np.max(np.abs(one[0] - base[4])))
-    print(f"  max diff: replicated {d_rep:.3e}  permuted {d_perm:.3e}  alone {d_one:.3e}",
-          flush=True)
-    assert d_rep == 0.0 and d_perm == 0.0 and d_one == 0.0
+    d_nar = float(np.max(np.abs(nar - base[short])))
+    print(f"  max diff: replicated {d_rep:.3e}  permuted {d_perm:.3e}  alone {d_one:.3e}  "
+          f"narrower batch {d_nar:.3e} ({short.size} sequences)", flush=True)
+    assert d_rep == 0.0 and d_perm == 0.0 and d_one == 0.0 and d_nar == 0.0
     enc.release()
 
 
