@@ -118,6 +118,9 @@ struct EncTailArgs {
   int max_rows, inter;
   float eps;
   int gelu;                // 1 erf, 2 tanh
+  // This launch's rows: block b starts at row0 + b * (its block rows), and
+  // rows at or past min(*rows, row_cap) are left to another launch.
+  int row0, row_cap;
 };
 
 // In-place affine LayerNorm of h [rows][hidden] f16 (hidden % 8 == 0, <= 1024).

@@ -1156,8 +1156,8 @@ EOS_DEV void tail_body(const EncTailArgs& a, TailLds<RT, H>& lds) {
   uint16_t* const Mbuf0 = X;
   uint16_t* const Mbuf1 = X + BM * MS;
 
-  const int rows = *a.rows;
-  const int m0 = blockIdx.x * BM;
+  const int rows = min(*a.rows, a.row_cap);
+  const int m0 = a.row0 + (int)blockIdx.x * BM;
   if (m0 >= rows) return;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1471,6 +1471,8 @@ EOS_TAIL_KERNEL(3, 384, 1)
 EOS_TAIL_KERNEL(3, 384, 2)
 EOS_TAIL_KERNEL(2, 512, 1)
 EOS_TAIL_KERNEL(2, 512, 2)
+EOS_TAIL_KERNEL(1, 512, 1)
+EOS_TAIL_KERNEL(1, 512, 2)
 EOS_TAIL_KERNEL(1, 768, 1)
 EOS_TAIL_KERNEL(1, 768, 2)
 #undef EOS_TAIL_KERNEL

@@ -185,6 +185,34 @@ def test_baseline_c4_long_context(rt):
         _check(got[b:b + 1], want)
 
 
+def test_fused_tail_split_launch(rt):
+    """At hidden 512 the layer tail's first launch covers one 64-row block
+    per CU and a second launch takes the rows after it in 32-row blocks. A
+    batch with more packed rows than the first launch covers: the sequences
+    around the boundary row and the last one match the oracle on their own
+    valid tokens, and each embeds bit for bit as it does in a batch of one
+    (where the second launch has no rows)."""
+    first = rt.info()["compute_units"] * 64
+    nseq = first // 400 + 4
+    _case(f"fused tail split: hidden 512, {nseq} x 512 tokens, first launch {first} rows")
+    w = datagen.bert_q8_weights(2, 512, 8, 2048, 2000, 512, seed=81, random_affine=True)
+    ids, mask, lens = datagen.encoder_batch(nseq, 512, 2000, 400, 512, 82, 83)
+    rows8 = (lens.astype(np.int64) + 7) // 8 * 8
+    off = np.concatenate([[0], np.cumsum(rows8)[:-1]])
+    assert off[-1] + rows8[-1] > first
+    check = sorted({int(b) for b in np.nonzero((off < first + 600) & (off + rows8 > first - 600))[0]}
+                   | {nseq - 1})
+    enc = Encoder(rt, w)
+    got = enc.embed(ids, mask)
+    for b in check:
+        n = int(lens[b])
+        print(f"  sequence {b}: rows {int(off[b])}..{int(off[b] + n - 1)}", flush=True)
+        _check(got[b:b + 1], _oracle(w, ids[b:b + 1, :n], np.ones((1, n), np.int32)))
+        alone = enc.embed(ids[b:b + 1], mask[b:b + 1])
+        assert np.array_equal(alone, got[b:b + 1])
+    enc.release()
+
+
 def _peaked_batch(tokens, vocab, special):
     """Sequences with the planted high-scoring tokens at chosen positions:
     (ids, mask); `special` maps sequence -> [(position, token id)], every
